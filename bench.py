@@ -1,0 +1,273 @@
+"""Benchmark: tiled tt.dot on one MI355X through the tx_dot C-ABI.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only NAME]
+
+A step is one dot over synthetic inputs already resident in HBM.  The
+headline workload is BASELINE configs[1]: bf16 C = A @ B, M = N = K = 4096,
+fp32 accumulation, entries N(0,1)/sqrt(K).  `value` is its TFLOP/s (2*M*N*K
+per step over the timed region, HIP events on the launch stream).  The other
+configs are reported under "secondary": the LoopSplit K-tail and edge cases,
+int8 W8A8 decode (M = 1, 16, 64, 256; HBM-bound, timed per launch with the
+256 MB MALL flushed between launches so B streams from HBM), and the fp8
+block-scaled dot.
+
+cpu_baseline: the CPU oracle (a C restatement of the Triton interpreter's
+tiled dot, oracle/) on the host cores for the same bf16 4096^3 inputs; it
+also checks the GPU output of the timed run against that result.
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "triton-ext_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "tt.dot TFLOP/s + % MFMA/HBM roofline (bf16 4096^3; int8 W8A8 M=16)"
+PEAK_BF16 = 2516.6e12
+PEAK_I8 = 5033.2e12
+HBM = 8.0e12
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="run only the named workload(s), comma-separated")
+    return ap.parse_args()
+
+
+class Launcher:
+    """Plan once, then launch through tx_dot_launch with minimal host work."""
+
+    def __init__(self, tx, a, b, out, sa=None, sb=None, scale_mode=None, block=(0, 0, 0)):
+        import torch
+        self.tx = tx
+        self.L = tx.load()
+        sm = scale_mode if scale_mode is not None else tx.SCALE_NONE
+        self.plan = tx.plan_for(a, b, tx.tx_type(out), sm, block)
+        self.ws = tx.workspace_for(self.plan, a.device)
+        self.args = (ctypes.byref(self.plan), a.data_ptr(), b.data_ptr(), out.data_ptr(),
+                     None if sa is None else sa.data_ptr(), None if sb is None else sb.data_ptr(),
+                     None if self.ws is None else self.ws.data_ptr(),
+                     0 if self.ws is None else self.ws.numel(),
+                     torch.cuda.current_stream().cuda_stream)
+        self.keep = (a, b, out, sa, sb)
+
+    def __call__(self):
+        rc = self.L.tx_dot_launch(*self.args)
+        if rc != 0:
+            raise RuntimeError(self.L.tx_get_last_error().decode())
+
+
+def time_back_to_back(fn, steps, warmup):
+    """Average ms per launch over `steps` back-to-back launches (events on the launch stream)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def time_cold(fn, steps, warmup, flush):
+    """Median ms of single launches, each bracketed by events, with `flush` run before each."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(steps):
+        flush()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        times.append((s, e))
+    torch.cuda.synchronize()
+    ms = sorted(s.elapsed_time(e) for s, e in times)
+    return ms[len(ms) // 2], ms
+
+
+def make_flush(dev):
+    """Touch 512 MiB (2x the MALL) so the next kernel's operands come from HBM."""
+    import torch
+    buf = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+
+    def flush():
+        buf.fill_(1)
+    return flush
+
+
+def bf16_inputs(M, N, K, dev, seed):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    a = (torch.randn((M, K), generator=g, device=dev, dtype=torch.float32) / math.sqrt(K)).to(torch.bfloat16)
+    b = (torch.randn((K, N), generator=g, device=dev, dtype=torch.float32) / math.sqrt(K)).to(torch.bfloat16)
+    return a, b
+
+
+def bench_bf16(tx, dev, M, N, K, steps, warmup, seed=1):
+    import torch
+    a, b = bf16_inputs(M, N, K, dev, seed)
+    c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    run = Launcher(tx, a, b, c)
+    ms = time_back_to_back(run, steps, warmup)
+    flops = 2.0 * M * N * K
+    p = run.plan
+    return dict(workload=f"bf16 {M}x{N}x{K}", ms=ms, tflops=flops / ms / 1e9,
+                frac=flops / ms / 1e-3 / PEAK_BF16,
+                plan=dict(tile=[p.desc.block_m, p.desc.block_n, p.desc.block_k], k_split=p.k_split,
+                          k_main_steps=p.k_main_steps, k_tail=p.k_tail, m_edge=p.m_edge,
+                          n_edge=p.n_edge, intensity=round(p.intensity, 1),
+                          bound="mfma" if p.bound == tx.BOUND_MFMA else "hbm")), (a, b, c)
+
+
+def bench_w8a8(tx, dev, M, N, K, steps, warmup, flush, seed=3):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    a = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+    b = torch.randint(-127, 128, (K, N), generator=g, device=dev, dtype=torch.int8)
+    sa = torch.rand((M,), generator=g, device=dev) * 0.019 + 0.001
+    sb = torch.rand((N,), generator=g, device=dev) * 0.019 + 0.001
+    c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    run = Launcher(tx, a, b, c, sa, sb, tx.SCALE_ROWCOL)
+    med, _ = time_cold(run, steps, warmup, flush)
+    warm = time_back_to_back(run, steps, warmup)
+    nbytes = M * K + K * N + M * N * 2 + 4 * (M + N)
+    p = run.plan
+    return dict(workload=f"int8 W8A8 M={M} N={N} K={K}", ms=med, ms_warm_mall=warm,
+                gbps=nbytes / med / 1e6, frac_hbm=nbytes / med / 1e-3 / HBM,
+                tops=2.0 * M * N * K / med / 1e9,
+                plan=dict(kernel=tx.load().tx_kernel_name(p.kernel).decode(), split_k=p.split_k,
+                          grid=p.grid_x, intensity=round(p.intensity, 1),
+                          bound="mfma" if p.bound == tx.BOUND_MFMA else "hbm"))
+
+
+def bench_fp8(tx, dev, M, N, K, steps, warmup, seed=5):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    a = torch.randn((M, K), generator=g, device=dev)
+    b = torch.randn((K, N), generator=g, device=dev)
+    kb, nb = (K + 127) // 128, (N + 127) // 128
+    sa = a.view(M, kb, 128).abs().amax(dim=2) / 448.0
+    sb = b.view(kb, 128, nb, 128).abs().amax(dim=(1, 3)) / 448.0
+    qa = (a.view(M, kb, 128) / sa[:, :, None]).view(M, K).to(torch.float8_e4m3fn)
+    qb = (b.view(kb, 128, nb, 128) / sb[:, None, :, None]).view(K, N).to(torch.float8_e4m3fn)
+    c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    run = Launcher(tx, qa, qb, c, sa.contiguous(), sb.contiguous(), tx.SCALE_BLOCK128)
+    ms = time_back_to_back(run, steps, warmup)
+    flops = 2.0 * M * N * K
+    return dict(workload=f"fp8 e4m3 block-scaled {M}x{N}x{K}", ms=ms, tflops=flops / ms / 1e9,
+                frac=flops / ms / 1e-3 / PEAK_I8)
+
+
+def cpu_baseline(a, b, c, M, N, K, block):
+    """Oracle on the host cores over the full bf16 workload; also checks the GPU output."""
+    import numpy as np
+    import torch
+
+    import oracle
+    ha = a.view(torch.int16).cpu().numpy().view(np.uint16)
+    hb = b.view(torch.int16).cpu().numpy().view(np.uint16)
+    got = c.view(torch.int16).cpu().numpy().view(np.uint16)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    t0 = time.perf_counter()
+    ref = oracle.tiled_dot(ha, hb, a_type=oracle.BF16, c_type=oracle.BF16, block=block,
+                           nthreads=threads)
+    dt = time.perf_counter() - t0
+    g32, r32 = oracle.bf16_to_f32(got).astype(np.float64), oracle.bf16_to_f32(ref).astype(np.float64)
+    ok = bool((np.abs(g32 - r32) <= 1e-3 + 1e-2 * np.abs(r32)).all())
+    cpu = open("/proc/cpuinfo").read() if os.path.exists("/proc/cpuinfo") else ""
+    model = next((ln.split(":", 1)[1].strip() for ln in cpu.splitlines() if ln.startswith("model name")), "?")
+    return dict(value=2.0 * M * N * K / dt / 1e12, unit="TFLOP/s", cores=threads, kind="port",
+                sample=f"full bf16 {M}x{N}x{K} dot, {block[0]}x{block[1]}x{block[2]} tiles, "
+                       f"{dt:.2f} s on {threads} threads ({model})",
+                seconds=dt), ok
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the dot shards by N or M blocks with no exchange; see DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import triton_ext_amd as tx
+    dev = torch.device("cuda:0")
+    if not tx.load().tx_device_available():
+        print("cuda:0 is not a gfx950 device", file=sys.stderr)
+        sys.exit(3)
+    only = set(x for x in args.only.split(",") if x)
+
+    def want(name):
+        return not only or name in only
+
+    M = N = K = 4096
+    head, (a, b, c) = bench_bf16(tx, dev, M, N, K, args.steps, args.warmup)
+    print(f"# bf16 4096^3: {head['ms'] * 1e3:.1f} us/step, {head['tflops']:.1f} TFLOP/s, "
+          f"{100 * head['frac']:.1f}% of peak", file=sys.stderr, flush=True)
+    secondary = []
+    flush = make_flush(dev)
+    if want("tail"):
+        for (m, n, k) in ((4096, 4096, 4000), (4000, 4000, 4000)):
+            r, _ = bench_bf16(tx, dev, m, n, k, args.steps, args.warmup, seed=2)
+            secondary.append(r)
+            print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    if want("w8a8"):
+        for m in (1, 16, 64, 256):
+            r = bench_w8a8(tx, dev, m, 8192, 8192, max(args.steps, 20), 3, flush)
+            secondary.append(r)
+            print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us, {r['gbps']:.0f} GB/s "
+                  f"({100 * r['frac_hbm']:.1f}% HBM)", file=sys.stderr, flush=True)
+    if want("fp8"):
+        r = bench_fp8(tx, dev, 2048, 7168, 7168, args.steps, args.warmup)
+        secondary.append(r)
+        print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+
+    cpu, parity = None, None
+    if not args.no_cpu:
+        # recompute the headline output once more (the secondary runs reused no buffers)
+        Launcher(tx, a, b, c)()
+        torch.cuda.synchronize()
+        tile = head["plan"]["tile"]
+        cpu, parity = cpu_baseline(a, b, c, M, N, K, tuple(tile))
+        print(f"# cpu baseline: {cpu['value']:.3f} TFLOP/s, parity={parity}", file=sys.stderr, flush=True)
+
+    flops = 2.0 * M * N * K
+    line = {
+        "metric": METRIC, "value": round(head["tflops"], 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(head["ms"], 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (torch.randn / sqrt(K), seed 1, rounded to bf16)",
+        "config": {"workload": "bf16 dense dot C=A@B, M=N=K=4096, row-major A[M,K], B[K,N], "
+                               "fp32 accumulate, bf16 out (BASELINE configs[1])",
+                   "tile": head["plan"]["tile"], "kernel": "gemm_16bit_mfma32x32x16"},
+        "roofline": {"bound": "mfma", "achieved": round(flops / head["ms"] / 1e9, 2),
+                     "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(head["frac"], 4),
+                     "traffic": None},
+        "cpu_baseline": cpu if cpu is None else {k: v for k, v in cpu.items() if k != "seconds"},
+        "parity_vs_oracle": parity,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

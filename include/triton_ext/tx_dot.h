@@ -1,0 +1,158 @@
+/*
+ * Tiled dot on MI355X (gfx950): plan + launch C-ABI.
+ *
+ * This is the computation a Triton kernel expresses as
+ *
+ *     acc = zeros([BM, BN], fp32 | int32)
+ *     for k in range(0, K, BK):                 # scf.for over K
+ *         a = tl.load(A_blk, mask=k_idx < K, other=0)
+ *         b = tl.load(B_blk, mask=k_idx < K, other=0)
+ *         acc = tl.dot(a, b, acc)               # tt.dot
+ *     tl.store(C_blk, epilogue(acc), mask=...)
+ *
+ * (tt.dot semantics: triton/language/semantic.py:1480-1571 of triton 3.6.0;
+ * the reference's own call sites: R:pass/LoopSplit/06-fused-attention.py:63,85.)
+ *
+ * The reference has no dot implementation of its own: it ships the plugin
+ * registry (TritonExtPassInfra.h) and the LoopSplit pass, and leaves the
+ * backend directory empty (R:backend/CMakeLists.txt is 0 bytes).  These entry
+ * points are what a backend extension adds behind that registry:
+ *   tx_dot_plan_create  runs the registered passes ("arith_intensity",
+ *                       "loop_split", "mi355x_dot") over one dot: FLOP/byte
+ *                       classification and tile choice, the K-loop split into
+ *                       a full-tile main loop and a peeled masked tail
+ *                       (R:pass/LoopSplit/LoopSplit.cpp:125-197), and the
+ *                       choice of HIP kernel;
+ *   tx_dot_launch       enqueues the planned kernels on a HIP stream.
+ *
+ * All pointers are device pointers (HBM) unless stated; `stream` is a
+ * hipStream_t (NULL = the null stream).  Errors are reported by return code;
+ * tx_get_last_error() gives the message of the calling thread's last error.
+ */
+#ifndef TRITON_EXT_AMD_TX_DOT_H
+#define TRITON_EXT_AMD_TX_DOT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TX_API __attribute__((visibility("default")))
+
+typedef enum tx_dtype {
+  TX_F32 = 0,
+  TX_F16 = 1,
+  TX_BF16 = 2,
+  TX_I8 = 3,
+  TX_F8E4M3 = 4, /* OCP e4m3fn (triton fp8e4nv): bias 7, max 448 */
+  TX_I32 = 5,
+} tx_dtype;
+
+typedef enum tx_scale_mode {
+  TX_SCALE_NONE = 0,
+  /* W8A8: C[m][n] = bf16((float(acc_i32[m][n]) * sa[m]) * sb[n]) */
+  TX_SCALE_ROWCOL = 1,
+  /* fp8 block scales: for each 128-wide K block kb,
+   *   acc[m][n] += dot_f32(Aq[m][kb], Bq[kb][n]) * sa[m][kb] * sb[kb][n/128]
+   * sa is [M][ceil(K/128)], sb is [ceil(K/128)][ceil(N/128)], row-major. */
+  TX_SCALE_BLOCK128 = 2,
+} tx_scale_mode;
+
+typedef enum tx_bound {
+  TX_BOUND_UNKNOWN = 0,
+  TX_BOUND_MFMA = 1, /* arithmetic intensity above the ridge point */
+  TX_BOUND_HBM = 2,  /* below the ridge point */
+} tx_bound;
+
+typedef enum tx_status {
+  TX_OK = 0,
+  TX_ERR_INVALID = 1,     /* bad descriptor, NULL pointer, misaligned stride */
+  TX_ERR_UNSUPPORTED = 2, /* valid dot that no kernel here implements */
+  TX_ERR_HIP = 3,         /* a HIP runtime call failed */
+  TX_ERR_NO_DEVICE = 4,   /* no gfx950 device visible */
+  TX_ERR_WORKSPACE = 5,   /* workspace missing or too small */
+  TX_ERR_NO_PASS = 6,     /* a required extension pass is not registered */
+} tx_status;
+
+typedef enum tx_kernel {
+  TX_KERNEL_NONE = 0,
+  TX_KERNEL_GEMM_16BIT = 1, /* bf16/fp16 MFMA 32x32x16, LDS-staged       */
+  TX_KERNEL_GEMM_I8 = 2,    /* int8 MFMA 32x32x32, LDS-staged            */
+  TX_KERNEL_DECODE_I8 = 3,  /* int8 small-M streaming, MFMA 16x16x64     */
+  TX_KERNEL_GEMM_F8 = 4,    /* fp8 e4m3 MFMA 32x32x64, block scales      */
+} tx_kernel;
+
+/* Bit flags for tx_dot_desc.flags */
+#define TX_FLAG_NO_LOOP_SPLIT 0x1 /* run every K step masked (no peeling) */
+
+typedef struct tx_dot_desc {
+  int64_t M, N, K;
+  /* Row strides in elements of A [M,K], B [K,N], C [M,N] (all row-major);
+   * 0 means packed (K, N, N).  Row strides in bytes must be multiples of 16. */
+  int64_t lda, ldb, ldc;
+  int32_t a_type, b_type, c_type; /* tx_dtype */
+  int32_t scale_mode;             /* tx_scale_mode */
+  /* Tile sizes; 0 lets the arith_intensity pass choose. */
+  int32_t block_m, block_n, block_k;
+  int32_t flags;
+} tx_dot_desc;
+
+struct tx_dot_plan {
+  tx_dot_desc desc; /* resolved copy (strides and tiles filled in) */
+
+  /* arith_intensity pass: algorithmic work (each operand read once, C
+   * written once, scales read once) and the roofline it implies. */
+  double flops, bytes, intensity; /* FLOP, bytes, FLOP/byte */
+  double peak_flops, peak_bw;     /* MI355X peaks for this dtype, per s */
+  double ridge;                   /* peak_flops / peak_bw */
+  double roofline_us;             /* max(flops/peak, bytes/bw) in us */
+  double tile_intensity;          /* 2*BM*BN / ((BM+BN)*elt): LDS-fill AI */
+  int32_t bound;                  /* tx_bound */
+
+  /* loop_split pass: for (k = 0; k < K; k += BK) with the predicate
+   * `k > K - BK` (the step that needs a mask) split at k_split:
+   *   [0, k_split)  k_main_steps unmasked steps,
+   *   [k_split, K)  one peeled masked step of k_tail elements (0 = none). */
+  int64_t k_split;
+  int32_t k_main_steps;
+  int32_t k_tail;
+  /* Tile grid, and the extent of the last (masked) tile row / column;
+   * 0 when M (N) is a multiple of the tile. */
+  int32_t m_tiles, n_tiles;
+  int32_t m_edge, n_edge;
+
+  /* mi355x_dot pass: kernel choice and launch shape. */
+  int32_t kernel; /* tx_kernel */
+  int32_t split_k;
+  int32_t grid_x, grid_y, grid_z;
+  int32_t block_threads;
+  int64_t workspace_bytes; /* device scratch the launch needs (0 = none) */
+  int32_t passes_run;      /* number of passes the pipeline ran */
+  int32_t reserved;
+};
+
+/* Validate `desc`, run the plan pipeline and fill `plan`. */
+TX_API int tx_dot_plan_create(const tx_dot_desc *desc, tx_dot_plan *plan);
+
+/* Enqueue the planned dot on `stream`.  `scale_a`/`scale_b` are required for
+ * TX_SCALE_ROWCOL and TX_SCALE_BLOCK128 and ignored otherwise.  `workspace`
+ * must hold plan->workspace_bytes bytes when that is non-zero; its contents
+ * on entry do not matter.  Concurrent launches must not share a workspace. */
+TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A, const void *B,
+                         void *C, const float *scale_a, const float *scale_b,
+                         void *workspace, size_t workspace_bytes, void *stream);
+
+/* Message for the calling thread's last non-zero status ("" if none). */
+TX_API const char *tx_get_last_error(void);
+/* Name of a tx_kernel value ("?" if unknown). */
+TX_API const char *tx_kernel_name(int32_t kernel);
+/* 1 if a gfx950 device is visible to this process, else 0.  Never throws. */
+TX_API int tx_device_available(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRITON_EXT_AMD_TX_DOT_H */

@@ -1,0 +1,135 @@
+"""ctypes wrapper of liboracle.so -- TEST INFRASTRUCTURE ONLY.
+
+Pinned by (tests/test_oracle_cpu.py):
+  * exact integer dots vs numpy int64 matmul (int8 -> int32, bit-exact);
+  * fp dots vs numpy float64 matmul within fp32 rounding bounds, plus
+    integer-valued fp inputs where the fp32 result is exact;
+  * the Triton-interpreter golden fixtures under tests/golden/;
+  * codec checks: bf16/fp16/e4m3 round trips over all bit patterns,
+    known values (e4m3 max 448, min subnormal 2^-9), numpy's float16 RNE.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+F32, F16, BF16, I8, F8E4M3, I32 = 0, 1, 2, 3, 4, 5
+SCALE_NONE, SCALE_ROWCOL, SCALE_BLOCK128 = 0, 1, 2
+ROUND_RTZ, ROUND_RNE = 0, 1
+
+_lib = None
+
+
+def lib():
+    """Load liboracle.so (built by `make -C oracle`)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle` "
+                               "(or __graft_entry__.build())")
+        L = ctypes.CDLL(LIB_PATH)
+        i64, i32, vp = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
+        L.oracle_tiled_dot.restype = i32
+        L.oracle_tiled_dot.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64,
+                                       i32, i32, i32, i32, i32, i32, i32, i32, i64, i64, i32]
+        for name in ("or_f32_to_bf16_array",):
+            getattr(L, name).argtypes = [vp, vp, i64, i32]
+        for name in ("or_bf16_to_f32_array", "or_f32_to_f16_array", "or_f16_to_f32_array",
+                     "or_f32_to_e4m3_array", "or_e4m3_to_f32_array"):
+            getattr(L, name).argtypes = [vp, vp, i64]
+        L.or_quantize_e4m3_groups.argtypes = [vp, i64, i64, i32, i32, vp, vp]
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+_NP = {F32: np.float32, F16: np.uint16, BF16: np.uint16, I8: np.int8, F8E4M3: np.uint8,
+       I32: np.int32}
+
+
+def tiled_dot(a, b, *, a_type, c_type, block=(64, 64, 32), scale_mode=SCALE_NONE,
+              sa=None, sb=None, round_mode=ROUND_RNE, tiles=None, nthreads=0, out=None):
+    """Run the interpreter-equivalent tiled dot on the CPU.
+
+    a: [M, K] array of raw element bits (uint16 for bf16/fp16, uint8 for e4m3,
+    int8, float32); b: [K, N] likewise.  Returns C [M, N] (raw bits for
+    16-bit outputs).  `tiles=(begin, end)` runs a subset of programs (program
+    id = pid_m * tiles_n + pid_n); rows of other tiles stay as in `out`.
+    round_mode: ROUND_RTZ reproduces the interpreter's truncating fp32->bf16
+    cast, ROUND_RNE compiled Triton's rounding.
+    """
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    M, K = a.shape
+    K2, N = b.shape
+    assert K == K2, (a.shape, b.shape)
+    if out is None:
+        out = np.zeros((M, N), dtype=_NP[c_type])
+    sa_c = None if sa is None else np.ascontiguousarray(sa, dtype=np.float32)
+    sb_c = None if sb is None else np.ascontiguousarray(sb, dtype=np.float32)
+    t0, t1 = (0, -1) if tiles is None else tiles
+    bm, bn, bk = block
+    rc = lib().oracle_tiled_dot(_ptr(a), _ptr(b), _ptr(out), _ptr(sa_c), _ptr(sb_c),
+                                M, N, K, K, N, N, a_type, a_type, c_type, scale_mode,
+                                round_mode, bm, bn, bk, t0, t1, nthreads)
+    if rc != 0:
+        raise ValueError(f"oracle_tiled_dot rejected the arguments (rc={rc})")
+    return out
+
+
+def f32_to_bf16(x, round_mode=ROUND_RNE):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.uint16)
+    lib().or_f32_to_bf16_array(_ptr(x), _ptr(y), x.size, round_mode)
+    return y
+
+
+def bf16_to_f32(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    y = np.empty(h.shape, dtype=np.float32)
+    lib().or_bf16_to_f32_array(_ptr(h), _ptr(y), h.size)
+    return y
+
+
+def f32_to_f16(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.uint16)
+    lib().or_f32_to_f16_array(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def f16_to_f32(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    y = np.empty(h.shape, dtype=np.float32)
+    lib().or_f16_to_f32_array(_ptr(h), _ptr(y), h.size)
+    return y
+
+
+def f32_to_e4m3(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.uint8)
+    lib().or_f32_to_e4m3_array(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def e4m3_to_f32(q):
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    y = np.empty(q.shape, dtype=np.float32)
+    lib().or_e4m3_to_f32_array(_ptr(q), _ptr(y), q.size)
+    return y
+
+
+def quantize_e4m3_groups(x, gr, gc):
+    """Per-group e4m3 quantisation: scale = amax/448, q = RNE_sat(x/scale)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, cols = x.shape
+    q = np.empty(x.shape, dtype=np.uint8)
+    s = np.empty(((rows + gr - 1) // gr, (cols + gc - 1) // gc), dtype=np.float32)
+    lib().or_quantize_e4m3_groups(_ptr(x), rows, cols, gr, gc, _ptr(q), _ptr(s))
+    return q, s

@@ -1,0 +1,381 @@
+/*
+ * oracle/tiled_dot.c -- TEST INFRASTRUCTURE ONLY.
+ *
+ * CPU restatement of what a Triton tiled-dot kernel computes under the Triton
+ * interpreter (TRITON_INTERPRET=1, third-party triton-rocm 3.6.0, cited as
+ * T:triton/...).  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load this library, and only as the checker; the
+ * product path (libmi355x_dot.so) never calls it.
+ *
+ * The kernel being restated:
+ *
+ *   pid -> (pid_m, pid_n)                            one program per C tile
+ *   acc = zeros([BM, BN], fp32 | int32)
+ *   for k0 in range(0, K, BK):
+ *       a = tl.load(A[pid_m*BM + i, k0 + k], mask=in-bounds, other=0)
+ *       b = tl.load(B[k0 + k, pid_n*BN + j], mask=in-bounds, other=0)
+ *       acc = tl.dot(a, b, acc)        (bf16 tiles .to(fp32) first)
+ *   tl.store(C_tile, epilogue(acc), mask=in-bounds)
+ *
+ * Interpreter facts it follows:
+ *   - programs run one after another (T:runtime/interpreter.py:1353-1357);
+ *     they are independent, so a tile subset can be timed and extrapolated;
+ *   - masked loads yield `other`, default 0 (:449-455);
+ *   - tl.dot is np.matmul(a, b, dtype=acc.dtype) + acc (:630-637): one fp32
+ *     (or int32) partial product per K block, added to the accumulator.  The
+ *     partial here sums k in ascending order; BLAS may sum in another order,
+ *     so fp results agree to rounding, int32 results exactly;
+ *   - fp8 operands are widened exactly to fp16 before the matmul (:633-636),
+ *     with the generic converter (:202-263): e4m3 0x7F/0xFF decode as +-480,
+ *     not NaN (quantisation with amax/448 scales never produces them);
+ *   - bf16 <-> fp32 casts use _convert_float with rounding_mode None
+ *     (cast_impl, :461-467): widening is exact and NARROWING TRUNCATES
+ *     (round toward zero).  Compiled Triton rounds to nearest even.  Both
+ *     are offered (OR_ROUND_RTZ / OR_ROUND_RNE); fp32 -> fp16 uses numpy's
+ *     astype, i.e. round to nearest even.
+ *
+ * Epilogues (the scaled variants restate the task's configs, not a Triton
+ * builtin):
+ *   plain:      C = cast(acc)
+ *   ROWCOL:     C = bf16((float(acc_i32) * sa[m]) * sb[n])
+ *   BLOCK128:   BK == 128 and, per K block kb,
+ *               acc = acc + (dot_f32(a, b) * sa[m][kb]) * sb[kb][n/128]
+ *
+ * Build: see oracle/Makefile (-ffp-contract=off: no FMA contraction, so the
+ * epilogue arithmetic is the plain fp32 sequence written here).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+enum { OR_F32 = 0, OR_F16 = 1, OR_BF16 = 2, OR_I8 = 3, OR_F8E4M3 = 4, OR_I32 = 5 };
+enum { OR_SCALE_NONE = 0, OR_SCALE_ROWCOL = 1, OR_SCALE_BLOCK128 = 2 };
+enum { OR_ROUND_RTZ = 0, OR_ROUND_RNE = 1 };
+
+/* ---------------- element codecs ---------------- */
+
+float or_bf16_to_f32(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+uint16_t or_f32_to_bf16(float f, int mode) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) /* NaN */
+    return (uint16_t)((u >> 16) | 0x0040u);
+  if (mode == OR_ROUND_RNE)
+    u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+float or_f16_to_f32(uint16_t h) {
+  int s = h >> 15, e = (h >> 10) & 31, m = h & 1023;
+  double v;
+  if (e == 0)
+    v = ldexp((double)m, -24);
+  else if (e == 31)
+    v = m ? NAN : INFINITY;
+  else
+    v = ldexp(1.0 + m / 1024.0, e - 15);
+  return (float)(s ? -v : v);
+}
+
+/* fp32 -> fp16, round to nearest even (IEEE). */
+uint16_t or_f32_to_f16(float f) {
+  uint16_t s = signbit(f) ? 0x8000u : 0;
+  double a = fabs((double)f);
+  if (isnan(f))
+    return (uint16_t)(s | 0x7e00u);
+  if (a >= 65520.0) /* rounds past the largest finite half */
+    return (uint16_t)(s | 0x7c00u);
+  if (a < ldexp(1.0, -14)) { /* subnormal range: quantum 2^-24 */
+    double q = rint(a / ldexp(1.0, -24)); /* half-even under FE_TONEAREST */
+    return (uint16_t)(s | (uint16_t)q);   /* q == 1024 is the min normal */
+  }
+  int e;
+  frexp(a, &e); /* a = f * 2^e, f in [0.5, 1) */
+  e -= 1;       /* a in [2^e, 2^(e+1)) */
+  double q = rint(a / ldexp(1.0, e - 10)); /* 1024..2048 */
+  if (q >= 2048.0) {
+    q /= 2;
+    e += 1;
+  }
+  if (e > 15)
+    return (uint16_t)(s | 0x7c00u);
+  return (uint16_t)(s | (uint16_t)((e + 15) << 10) | ((uint16_t)q - 1024));
+}
+
+float or_e4m3_to_f32(uint8_t b) {
+  int s = b >> 7, e = (b >> 3) & 15, m = b & 7;
+  double v = e == 0 ? ldexp((double)m, -9) : ldexp(1.0 + m / 8.0, e - 7);
+  return (float)(s ? -v : v);
+}
+
+/* fp32 -> e4m3fn, round to nearest even, saturating to +-448. */
+uint8_t or_f32_to_e4m3(float f) {
+  uint8_t s = signbit(f) ? 0x80u : 0;
+  double a = fabs((double)f);
+  if (isnan(f))
+    return (uint8_t)(s | 0x7fu);
+  if (a > 448.0)
+    a = 448.0;
+  int e;
+  if (a < ldexp(1.0, -6)) { /* subnormal: quantum 2^-9 */
+    double q = rint(a / ldexp(1.0, -9));
+    return (uint8_t)(s | (uint8_t)q); /* q == 8 is the min normal 0x08 */
+  }
+  frexp(a, &e);
+  e -= 1;
+  double q = rint(a / ldexp(1.0, e - 3)); /* 8..16 */
+  if (q >= 16.0) {
+    q /= 2;
+    e += 1;
+  }
+  if (e > 8) /* cannot happen after saturation */
+    e = 8, q = 14;
+  return (uint8_t)(s | (uint8_t)((e + 7) << 3) | ((uint8_t)q - 8));
+}
+
+void or_f32_to_bf16_array(const float *x, uint16_t *y, int64_t n, int mode) {
+  for (int64_t i = 0; i < n; ++i)
+    y[i] = or_f32_to_bf16(x[i], mode);
+}
+void or_bf16_to_f32_array(const uint16_t *x, float *y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i)
+    y[i] = or_bf16_to_f32(x[i]);
+}
+void or_f32_to_f16_array(const float *x, uint16_t *y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i)
+    y[i] = or_f32_to_f16(x[i]);
+}
+void or_f16_to_f32_array(const uint16_t *x, float *y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i)
+    y[i] = or_f16_to_f32(x[i]);
+}
+void or_f32_to_e4m3_array(const float *x, uint8_t *y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i)
+    y[i] = or_f32_to_e4m3(x[i]);
+}
+void or_e4m3_to_f32_array(const uint8_t *x, float *y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i)
+    y[i] = or_e4m3_to_f32(x[i]);
+}
+
+/* ---------------- the tiled dot ---------------- */
+
+static float load_f(const uint8_t *base, int type, int64_t idx) {
+  switch (type) {
+  case OR_F32: { float v; memcpy(&v, base + 4 * idx, 4); return v; }
+  case OR_F16: { uint16_t h; memcpy(&h, base + 2 * idx, 2); return or_f16_to_f32(h); }
+  case OR_BF16: { uint16_t h; memcpy(&h, base + 2 * idx, 2); return or_bf16_to_f32(h); }
+  case OR_F8E4M3: return or_e4m3_to_f32(base[idx]);
+  default: return 0.f;
+  }
+}
+
+static int elt_size(int t) {
+  switch (t) {
+  case OR_F32: case OR_I32: return 4;
+  case OR_F16: case OR_BF16: return 2;
+  case OR_I8: case OR_F8E4M3: return 1;
+  default: return 0;
+  }
+}
+
+/*
+ * Run programs [tile_begin, tile_end) of the tiled dot (program id =
+ * pid_m * tiles_n + pid_n; tile_end < 0 means all).  Returns 0, or -1 for an
+ * unsupported combination.  Row strides are in elements.
+ */
+int oracle_tiled_dot(const void *Av, const void *Bv, void *Cv, const float *sa,
+                     const float *sb, int64_t M, int64_t N, int64_t K,
+                     int64_t lda, int64_t ldb, int64_t ldc, int a_type,
+                     int b_type, int c_type, int scale_mode, int round_mode,
+                     int BM, int BN, int BK, int64_t tile_begin,
+                     int64_t tile_end, int nthreads) {
+  const uint8_t *A = (const uint8_t *)Av, *B = (const uint8_t *)Bv;
+  uint8_t *C = (uint8_t *)Cv;
+  if (BM <= 0 || BN <= 0 || BK <= 0 || M < 0 || N < 0 || K < 0)
+    return -1;
+  if (a_type != b_type || !elt_size(a_type) || !elt_size(c_type))
+    return -1;
+  const int is_int = a_type == OR_I8;
+  if (scale_mode == OR_SCALE_BLOCK128 && BK != 128)
+    return -1;
+  if (scale_mode == OR_SCALE_ROWCOL && !is_int)
+    return -1;
+  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int64_t ntiles = tiles_m * tiles_n;
+  if (tile_end < 0 || tile_end > ntiles)
+    tile_end = ntiles;
+  if (tile_begin < 0)
+    tile_begin = 0;
+  const int64_t kblocks = (K + BK - 1) / BK;
+  const int64_t sa_ld = (K + 127) / 128, sb_ld = (N + 127) / 128;
+  int rc = 0;
+#ifdef _OPENMP
+  if (nthreads <= 0)
+    nthreads = omp_get_max_threads();
+#pragma omp parallel num_threads(nthreads)
+#endif
+  {
+    float *af = (float *)calloc((size_t)BM * BK, sizeof(float));
+    float *bf = (float *)calloc((size_t)BK * BN, sizeof(float));
+    float *part = (float *)calloc((size_t)BM * BN, sizeof(float));
+    float *acc = (float *)calloc((size_t)BM * BN, sizeof(float));
+    int32_t *ai = (int32_t *)calloc((size_t)BM * BK, sizeof(int32_t));
+    int32_t *bi = (int32_t *)calloc((size_t)BK * BN, sizeof(int32_t));
+    uint32_t *iacc = (uint32_t *)calloc((size_t)BM * BN, sizeof(uint32_t));
+    uint32_t *ipart = (uint32_t *)calloc((size_t)BM * BN, sizeof(uint32_t));
+    if (!af || !bf || !part || !acc || !ai || !bi || !iacc || !ipart) {
+#ifdef _OPENMP
+#pragma omp atomic write
+#endif
+      rc = -2;
+    } else {
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+      for (int64_t pid = tile_begin; pid < tile_end; ++pid) {
+        const int64_t m0 = (pid / tiles_n) * BM, n0 = (pid % tiles_n) * BN;
+        memset(acc, 0, sizeof(float) * BM * BN);
+        memset(iacc, 0, sizeof(uint32_t) * BM * BN);
+        for (int64_t kb = 0; kb < kblocks; ++kb) {
+          const int64_t k0 = kb * BK;
+          /* masked tile loads, other = 0 */
+          for (int i = 0; i < BM; ++i)
+            for (int k = 0; k < BK; ++k) {
+              const int ok = m0 + i < M && k0 + k < K;
+              const int64_t idx = (m0 + i) * lda + k0 + k;
+              if (is_int)
+                ai[i * BK + k] = ok ? (int32_t)((const int8_t *)A)[idx] : 0;
+              else
+                af[i * BK + k] = ok ? load_f(A, a_type, idx) : 0.f;
+            }
+          for (int k = 0; k < BK; ++k)
+            for (int j = 0; j < BN; ++j) {
+              const int ok = k0 + k < K && n0 + j < N;
+              const int64_t idx = (k0 + k) * ldb + n0 + j;
+              if (is_int)
+                bi[k * BN + j] = ok ? (int32_t)((const int8_t *)B)[idx] : 0;
+              else
+                bf[k * BN + j] = ok ? load_f(B, b_type, idx) : 0.f;
+            }
+          /* partial = a @ b, k ascending */
+          if (is_int) {
+            memset(ipart, 0, sizeof(uint32_t) * BM * BN);
+            for (int i = 0; i < BM; ++i)
+              for (int k = 0; k < BK; ++k) {
+                const uint32_t a = (uint32_t)ai[i * BK + k];
+                if (!a)
+                  continue;
+                uint32_t *pr = ipart + (size_t)i * BN;
+                const int32_t *br = bi + (size_t)k * BN;
+                for (int j = 0; j < BN; ++j)
+                  pr[j] += a * (uint32_t)br[j]; /* int32 wrap, like numpy */
+              }
+            for (int t = 0; t < BM * BN; ++t)
+              iacc[t] = ipart[t] + iacc[t];
+          } else {
+            memset(part, 0, sizeof(float) * BM * BN);
+            for (int i = 0; i < BM; ++i)
+              for (int k = 0; k < BK; ++k) {
+                const float a = af[i * BK + k];
+                float *pr = part + (size_t)i * BN;
+                const float *br = bf + (size_t)k * BN;
+                for (int j = 0; j < BN; ++j)
+                  pr[j] += a * br[j];
+              }
+            if (scale_mode == OR_SCALE_BLOCK128) {
+              for (int i = 0; i < BM; ++i) {
+                const float s_a = m0 + i < M ? sa[(m0 + i) * sa_ld + kb] : 0.f;
+                for (int j = 0; j < BN; ++j) {
+                  const float s_b = n0 + j < N ? sb[kb * sb_ld + (n0 + j) / 128] : 0.f;
+                  const float t = (part[i * BN + j] * s_a) * s_b;
+                  acc[i * BN + j] = acc[i * BN + j] + t;
+                }
+              }
+            } else {
+              for (int t = 0; t < BM * BN; ++t)
+                acc[t] = part[t] + acc[t];
+            }
+          }
+        }
+        /* epilogue + masked store */
+        for (int i = 0; i < BM; ++i) {
+          const int64_t m = m0 + i;
+          if (m >= M)
+            break;
+          for (int j = 0; j < BN; ++j) {
+            const int64_t n = n0 + j;
+            if (n >= N)
+              break;
+            const int64_t off = m * ldc + n;
+            if (is_int) {
+              const int32_t v = (int32_t)iacc[i * BN + j];
+              if (scale_mode == OR_SCALE_ROWCOL) {
+                const float f = ((float)v * sa[m]) * sb[n];
+                if (c_type == OR_BF16) {
+                  uint16_t h = or_f32_to_bf16(f, round_mode);
+                  memcpy(C + 2 * off, &h, 2);
+                } else if (c_type == OR_F32) {
+                  memcpy(C + 4 * off, &f, 4);
+                }
+              } else if (c_type == OR_I32) {
+                memcpy(C + 4 * off, &v, 4);
+              }
+            } else {
+              const float f = acc[i * BN + j];
+              if (c_type == OR_F32) {
+                memcpy(C + 4 * off, &f, 4);
+              } else if (c_type == OR_BF16) {
+                uint16_t h = or_f32_to_bf16(f, round_mode);
+                memcpy(C + 2 * off, &h, 2);
+              } else if (c_type == OR_F16) {
+                uint16_t h = or_f32_to_f16(f);
+                memcpy(C + 2 * off, &h, 2);
+              }
+            }
+          }
+        }
+      }
+    }
+    free(af); free(bf); free(part); free(acc);
+    free(ai); free(bi); free(iacc); free(ipart);
+  }
+  return rc;
+}
+
+/*
+ * fp8 block quantisation used by the C5 config: values x (fp32, row-major
+ * rows x cols) are split into gr x gc groups; each group's scale is
+ * amax / 448 (1 if the group is all zero) and q = e4m3_rne_sat(x / scale).
+ * scales is [ceil(rows/gr)][ceil(cols/gc)].
+ */
+void or_quantize_e4m3_groups(const float *x, int64_t rows, int64_t cols,
+                             int gr, int gc, uint8_t *q, float *scales) {
+  const int64_t sr = (rows + gr - 1) / gr, sc = (cols + gc - 1) / gc;
+  for (int64_t bi = 0; bi < sr; ++bi)
+    for (int64_t bj = 0; bj < sc; ++bj) {
+      float amax = 0.f;
+      for (int64_t i = bi * gr; i < rows && i < (bi + 1) * gr; ++i)
+        for (int64_t j = bj * gc; j < cols && j < (bj + 1) * gc; ++j) {
+          const float a = fabsf(x[i * cols + j]);
+          if (a > amax)
+            amax = a;
+        }
+      const float s = amax > 0.f ? amax / 448.0f : 1.0f;
+      scales[bi * sc + bj] = s;
+      for (int64_t i = bi * gr; i < rows && i < (bi + 1) * gr; ++i)
+        for (int64_t j = bj * gc; j < cols && j < (bj + 1) * gc; ++j)
+          q[i * cols + j] = or_f32_to_e4m3(x[i * cols + j] / s);
+    }
+}

@@ -1,0 +1,201 @@
+"""C-ABI surface on the CPU: exports, registry, conf files, planning errors.
+
+No kernel is launched here; launches without a gfx950 device must fail
+cleanly with TX_ERR_NO_DEVICE.
+"""
+import ctypes
+import os
+import subprocess
+
+import pytest
+
+import triton_ext_amd as tx
+from triton_ext_amd import capi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INC = os.path.join(ROOT, "include")
+CSRC = os.path.join(ROOT, "triton-ext_amd", "csrc")
+
+
+def _defined_symbols(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], check=True,
+                         capture_output=True, text=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if line.strip()}
+
+
+@pytest.mark.parametrize("lib", sorted(capi.EXPORTS))
+def test_library_exports(lib):
+    path = capi.lib_path(lib)
+    assert os.path.exists(path), f"{lib} not built"
+    syms = _defined_symbols(path)
+    missing = [s for s in capi.EXPORTS[lib] if s not in syms]
+    assert not missing, missing
+    capi.load(lib)  # and it loads
+
+
+def test_header_declarations_are_exported():
+    """Every function declared in include/triton_ext/*.h is exported by some library."""
+    import re
+    declared = set()
+    for h in os.listdir(os.path.join(INC, "triton_ext")):
+        text = open(os.path.join(INC, "triton_ext", h)).read()
+        text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", " ", text)
+        declared |= set(re.findall(r"\b((?:tx|txPassManager|txRegister|txRead|triton|TritonExt)"
+                                   r"[A-Za-z0-9_]*)\s*\(", text))
+    declared -= {"TritonExtRegisterPassFunc", "TritonExtAddPassFunc"}
+    exported = set()
+    for lib in capi.EXPORTS:
+        exported |= _defined_symbols(capi.lib_path(lib))
+    assert declared, "no declarations found"
+    assert declared <= exported, sorted(declared - exported)
+
+
+def test_self_registration_and_enumeration():
+    tx.load()
+    names = tx.enumerate_passes()
+    for n in ("loop_split", "arith_intensity", "mi355x_dot"):
+        assert names.count(n) == 1, names
+
+
+def test_registry_errors_and_duplicates():
+    L = tx.load("libTritonExtPassInfra.so")
+    assert L.tritonEnumeratePluginPasses(None, None) == capi.TP_GENERIC_FAILURE
+    assert L.tritonAddPluginPass(None, b"loop_split") == capi.TP_GENERIC_FAILURE
+    pm = L.txPassManagerCreate()
+    assert L.tritonAddPluginPass(pm, b"no_such_extension") == capi.TP_GENERIC_FAILURE
+    assert L.tritonRegisterPluginPass(b"no_such_extension") == capi.TP_GENERIC_FAILURE
+    # a Python-side extension, registered twice under one name: replaced, not duplicated
+    RUN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.POINTER(capi.DotPlan))
+    REG = ctypes.CFUNCTYPE(None)
+    ADD = ctypes.CFUNCTYPE(None, ctypes.c_void_p)
+    calls = []
+
+    def run(plan):
+        calls.append(plan.contents.desc.M)
+        return 0
+    run_c = RUN(run)
+    add_c = ADD(lambda p: L.txPassManagerAddPass(ctypes.c_void_p(p), b"py-test-pass", run_c))
+    reg_c = REG(lambda: calls.append("reg"))
+    L.TritonExtLoadPass.argtypes = [ctypes.c_char_p, REG, ADD]
+    L.txPassManagerAddPass.argtypes = [ctypes.c_void_p, ctypes.c_char_p, RUN]
+    name = ctypes.create_string_buffer(b"py_test_ext")
+    before = tx.enumerate_passes()
+    assert L.TritonExtLoadPass(name, reg_c, add_c) == capi.TP_SUCCESS
+    assert L.TritonExtLoadPass(name, reg_c, add_c) == capi.TP_SUCCESS
+    after = tx.enumerate_passes()
+    assert after.count("py_test_ext") == 1 and len(after) == len(before) + 1
+    assert L.tritonRegisterPluginPass(b"py_test_ext") == capi.TP_SUCCESS
+    assert L.tritonAddPluginPass(pm, b"py_test_ext") == capi.TP_SUCCESS
+    assert L.txPassManagerSize(pm) == 1
+    plan = capi.DotPlan()
+    plan.desc.M = 77
+    assert L.txPassManagerRun(pm, ctypes.byref(plan)) == 0
+    assert calls == ["reg", 77]
+    L.txPassManagerDestroy(pm)
+    # keep the callbacks alive for the registry's lifetime
+    test_registry_errors_and_duplicates._keep = (run_c, add_c, reg_c, name)
+
+
+def test_plugin_host_harness(tmp_path):
+    """A C host dlopen()s the extensions and drives them via dlsym only."""
+    exe = str(tmp_path / "plugin_host")
+    subprocess.run(["gcc", "-std=c11", "-O1", "-I", INC, os.path.join(ROOT, "tests", "plugin_host.c"),
+                    "-o", exe, "-ldl"], check=True)
+    r = subprocess.run([exe, capi.LIB_DIR], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stdout + r.stderr
+    out = r.stdout
+    assert "before_load count=0" in out
+    assert "after_load count=2 loop_split arith_intensity" in out
+    assert "pm size=2 tx-arith-intensity triton-loop-split" in out
+    assert "plan block=256x256x64 k_split=3968 main=62 tail=32 bound=1 passes=2" in out
+    assert "pipeline size=2 tx-arith-intensity triton-loop-split" in out
+    assert out.strip().endswith("OK")
+
+
+def test_transposes_on_host(tmp_path):
+    exe = str(tmp_path / "transpose_host")
+    subprocess.run(["g++", "-std=c++17", "-O2", "-I", CSRC, os.path.join(ROOT, "tests", "transpose_host.cpp"),
+                    "-o", exe], check=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and r.stdout.strip() == "OK", r.stdout + r.stderr
+
+
+@pytest.mark.parametrize("fname", ["triton-ext.conf", "triton_ext.conf"])
+def test_conf_reader(tmp_path, fname):
+    L = tx.load("libTritonExtPassInfra.so")
+    (tmp_path / fname).write_text("my_ext ; stable ; abc123\n")
+    name, st, hs = (ctypes.create_string_buffer(64) for _ in range(3))
+    assert L.txReadExtConf(str(tmp_path).encode(), name, 64, st, 64, hs, 64) == 0
+    assert (name.value, st.value, hs.value) == (b"my_ext", b"stable", b"abc123")
+    (tmp_path / fname).write_text("only_name")
+    assert L.txReadExtConf(str(tmp_path).encode(), name, 64, st, 64, hs, 64) == 0
+    assert (name.value, st.value, hs.value) == (b"only_name", b"experimental", b"")
+    (tmp_path / fname).write_text("  \n")
+    assert L.txReadExtConf(str(tmp_path).encode(), name, 64, st, 64, hs, 64) == 1
+    assert L.txReadExtConf(str(tmp_path / "missing").encode(), name, 64, st, 64, hs, 64) == 1
+
+
+def test_shipped_conf_files_name_the_extensions():
+    L = tx.load("libTritonExtPassInfra.so")
+    name = ctypes.create_string_buffer(64)
+    for d, expect in (("pass/loop_split", b"loop_split"), ("pass/arith_intensity", b"arith_intensity"),
+                      ("backend/mi355x", b"mi355x_dot")):
+        assert L.txReadExtConf(os.path.join(CSRC, d).encode(), name, 64, None, 0, None, 0) == 0
+        assert name.value == expect
+
+
+def _err(desc):
+    with pytest.raises(tx.TxError) as e:
+        tx.plan(desc)
+    return e.value.code
+
+
+def test_plan_validation():
+    assert _err(tx.make_desc(-1, 4, 4, tx.BF16, tx.BF16)) == tx.ERR_INVALID
+    assert _err(tx.make_desc(64, 64, 64, 42, tx.BF16)) == tx.ERR_INVALID
+    assert _err(tx.make_desc(64, 64, 60, tx.BF16, tx.BF16, lda=60)) == tx.ERR_INVALID  # 120 B rows
+    assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, lda=32)) == tx.ERR_INVALID  # short stride
+    assert _err(tx.make_desc(64, 64, 68, tx.BF16, tx.BF16, lda=72)) == tx.ERR_UNSUPPORTED  # K%8
+    assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.I32)) == tx.ERR_UNSUPPORTED
+    assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, b_type=tx.F16)) == tx.ERR_UNSUPPORTED
+    assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, block=(96, 64, 64))) == tx.ERR_UNSUPPORTED
+    assert _err(tx.make_desc(64, 64, 64, tx.F8E4M3, tx.BF16)) == tx.ERR_UNSUPPORTED  # fp8->bf16 needs scales
+    p = tx.plan(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16))
+    assert p.passes_run == 3 and p.kernel == tx.KERNEL_GEMM_16BIT
+
+
+@pytest.mark.parametrize("M,N,K,a,c,sm,kernel", [
+    (4096, 4096, 4096, tx.BF16, tx.BF16, 0, tx.KERNEL_GEMM_16BIT),
+    (512, 512, 512, tx.F16, tx.F32, 0, tx.KERNEL_GEMM_16BIT),
+    (1, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
+    (64, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
+    (256, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_GEMM_I8),
+    (300, 304, 256, tx.I8, tx.I32, 0, tx.KERNEL_GEMM_I8),
+    (2048, 7168, 7168, tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, tx.KERNEL_GEMM_F8),
+])
+def test_kernel_choice(M, N, K, a, c, sm, kernel):
+    p = tx.plan(tx.make_desc(M, N, K, a, c, scale_mode=sm))
+    assert p.kernel == kernel
+    assert p.grid_x > 0 and p.block_threads in (256, 512)
+    if kernel == tx.KERNEL_DECODE_I8 and p.split_k > 1:
+        assert p.workspace_bytes >= p.split_k * M * N * 4
+    assert (p.split_k & (p.split_k - 1)) == 0
+
+
+def test_launch_without_device_fails_cleanly():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("device present")
+    L = tx.load()
+    p = tx.plan(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16))
+    buf = ctypes.create_string_buffer(64 * 64 * 2 + 16)
+    addr = (ctypes.addressof(buf) + 15) & ~15
+    rc = L.tx_dot_launch(ctypes.byref(p), addr, addr, addr, None, None, None, 0, None)
+    assert rc == tx.ERR_NO_DEVICE
+    assert b"gfx950" in L.tx_get_last_error()
+    assert L.tx_device_available() == 0
+    # argument errors are reported before the device is touched
+    assert L.tx_dot_launch(None, addr, addr, addr, None, None, None, 0, None) == tx.ERR_INVALID
+    assert L.tx_dot_launch(ctypes.byref(p), None, addr, addr, None, None, None, 0, None) == tx.ERR_INVALID
+    assert L.tx_dot_launch(ctypes.byref(p), addr + 2, addr, addr, None, None, None, 0, None) == tx.ERR_INVALID

@@ -1,0 +1,221 @@
+"""GPU parity: libmi355x_dot.so through the tx_dot C-ABI vs the CPU oracle.
+
+Tolerances (north_star): int8 -> int32 bit-exact; fp16/bf16/fp8 with fp32
+accumulation within |d| <= 1e-3 * s + 1e-2 * |ref|, s = 1 for inputs drawn
+N(0,1)/sqrt(K) (outputs ~ 1/sqrt(K)), s = sqrt(K) for unnormalised inputs.
+The oracle sums each K block in ascending k order; the MFMA sums in its own
+order, so fp results agree to rounding, not bit for bit.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+import triton_ext_amd as tx
+from dotcase import (bits_to_f32, check_close, fp8_block_inputs, from_device, k_norm, normal_bf16,
+                     normal_f16, say, to_device, uniform_i8, uniform_scales)
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-3, 1e-2
+
+
+def run_16bit(gpu, M, N, K, kind, out_kind, block=(0, 0, 0), flags=0, seed=0, lda=None):
+    import torch
+    say(f"{kind}->{out_kind} M={M} N={N} K={K} block={block} flags={flags} lda={lda}")
+    gen = normal_bf16 if kind == "bf16" else normal_f16
+    a = gen((M, K if lda is None else lda), k_norm(K), 1 + seed)
+    b = gen((K, N), k_norm(K), 2 + seed)
+    da, db = to_device(a, gpu), to_device(b, gpu)
+    tdt = torch.bfloat16 if kind == "bf16" else torch.float16
+    da, db = da.view(tdt), db.view(tdt)
+    if lda is not None:
+        da = da[:, :K]
+    out_dt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[out_kind]
+    c = tx.dot(da, db, out_dtype=out_dt, block=block, flags=flags)
+    torch.cuda.synchronize()
+    got = from_device(c)
+    return a[:, :K].copy(), b, got
+
+
+def oracle_16bit(a, b, kind, out_kind, block, round_mode=oracle.ROUND_RNE):
+    at = oracle.BF16 if kind == "bf16" else oracle.F16
+    ct = {"f32": oracle.F32, "bf16": oracle.BF16, "f16": oracle.F16}[out_kind]
+    return oracle.tiled_dot(a, b, a_type=at, c_type=ct, block=block, round_mode=round_mode)
+
+
+def test_c1_fp16_512_block64(gpu):
+    """Config 0: fp16 512^3, BLOCK 64x64x32, fp32 C."""
+    a, b, got = run_16bit(gpu, 512, 512, 512, "f16", "f32", block=(64, 64, 32))
+    ref = oracle_16bit(a, b, "f16", "f32", (64, 64, 32))
+    err = check_close(got, ref, atol=ATOL, rtol=RTOL, what="fp16 512")
+    # exact fp64 product as a second reference: fp32 rounding only
+    exact = oracle.f16_to_f32(a).astype(np.float64) @ oracle.f16_to_f32(b).astype(np.float64)
+    assert np.abs(got - exact).max() < 1e-5
+    say(f"fp16 512 max|d|={err:.3g}")
+
+
+def test_c2_bf16_4096(gpu):
+    """Config 1: bf16 4096^3, bf16 C, the MFMA-bound headline case."""
+    M = N = K = 4096
+    a, b, got = run_16bit(gpu, M, N, K, "bf16", "bf16")
+    p = tx.plan(tx.make_desc(M, N, K, tx.BF16, tx.BF16))
+    blk = (p.desc.block_m, p.desc.block_n, p.desc.block_k)
+    ref = oracle_16bit(a, b, "bf16", "bf16", blk)
+    g, r = bits_to_f32(got, "bf16"), bits_to_f32(ref, "bf16")
+    err = check_close(g, r, atol=ATOL, rtol=RTOL, what="bf16 4096")
+    # against the interpreter's truncating cast too
+    rtz = bits_to_f32(oracle_16bit(a, b, "bf16", "bf16", blk, oracle.ROUND_RTZ), "bf16")
+    check_close(g, rtz, atol=ATOL, rtol=RTOL, what="bf16 4096 vs RTZ")
+    # most outputs are bit-identical to the oracle's RNE bf16
+    same = (got == ref).mean()
+    assert same > 0.9, same
+    say(f"bf16 4096 max|d|={err:.3g} max|d|*sqrt(K)={err * math.sqrt(K):.3g} identical={same:.4f}")
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 4000), (4000, 4000, 4000)])
+def test_c3_loop_split_tail_and_edges(gpu, M, N, K):
+    """Config 2: K-tail peeled from the main loop (K=4000 = 62*64 + 32), edge tiles."""
+    p = tx.plan(tx.make_desc(M, N, K, tx.BF16, tx.BF16))
+    assert (p.k_split, p.k_main_steps, p.k_tail) == (3968, 62, 32)
+    a, b, got = run_16bit(gpu, M, N, K, "bf16", "bf16")
+    blk = (p.desc.block_m, p.desc.block_n, p.desc.block_k)
+    ref = oracle_16bit(a, b, "bf16", "bf16", blk)
+    err = check_close(bits_to_f32(got, "bf16"), bits_to_f32(ref, "bf16"), atol=ATOL, rtol=RTOL,
+                      what=f"bf16 {M}x{N}x{K}")
+    say(f"tail {M}x{N}x{K} max|d|={err:.3g}")
+
+
+def test_loop_split_equals_all_masked(gpu):
+    """Peeling changes which loads test bounds, not the arithmetic: bit-identical."""
+    M, N, K = 1000, 1000, 1000
+    _, _, split = run_16bit(gpu, M, N, K, "bf16", "f32", block=(128, 128, 64), seed=5)
+    _, _, masked = run_16bit(gpu, M, N, K, "bf16", "f32", block=(128, 128, 64), seed=5,
+                             flags=tx.FLAG_NO_LOOP_SPLIT)
+    assert np.array_equal(split, masked)
+
+
+@pytest.mark.parametrize("M,N,K,block,kind,out", [
+    (64, 64, 32, (64, 64, 32), "f16", "f32"),
+    (1, 8, 8, (64, 64, 32), "bf16", "f32"),
+    (33, 72, 24, (64, 64, 32), "f16", "f16"),
+    (257, 264, 136, (128, 128, 64), "bf16", "bf16"),
+    (300, 520, 200, (256, 256, 64), "bf16", "f32"),
+    (128, 128, 8, (128, 128, 64), "f16", "f32"),
+])
+def test_16bit_edges(gpu, M, N, K, block, kind, out):
+    a, b, got = run_16bit(gpu, M, N, K, kind, out, block=block, seed=M)
+    ref = oracle_16bit(a, b, kind, out, block)
+    check_close(bits_to_f32(got, out), bits_to_f32(ref, out), atol=ATOL, rtol=RTOL,
+                what=f"{kind} {M}x{N}x{K}")
+
+
+def test_strided_a(gpu):
+    a, b, got = run_16bit(gpu, 200, 256, 192, "bf16", "f32", block=(128, 128, 64), lda=256)
+    ref = oracle_16bit(a, b, "bf16", "f32", (128, 128, 64))
+    check_close(got, ref, atol=ATOL, rtol=RTOL, what="strided A")
+
+
+def test_rejects_unaligned_k(gpu):
+    """K*elt must be a multiple of 16 bytes: rejected before any launch."""
+    import torch
+    say("unaligned K rejected")
+    a = torch.zeros((5, 200), dtype=torch.int8, device=gpu)
+    b = torch.zeros((200, 272), dtype=torch.int8, device=gpu)
+    with pytest.raises(tx.TxError) as e:
+        tx.dot(a, b, out_dtype=torch.int32)
+    assert e.value.code == tx.ERR_INVALID
+
+
+def test_k_zero_and_empty(gpu):
+    import torch
+    say("K=0 and empty outputs")
+    a = torch.zeros((64, 0), dtype=torch.bfloat16, device=gpu)
+    b = torch.zeros((0, 64), dtype=torch.bfloat16, device=gpu)
+    c = tx.dot(a, b, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert (c == 0).all()
+    e = tx.dot(torch.zeros((0, 64), dtype=torch.bfloat16, device=gpu),
+               torch.zeros((64, 64), dtype=torch.bfloat16, device=gpu), out_dtype=torch.float32)
+    assert e.shape == (0, 64)
+
+
+# ----------------------------------------------------------------------------- int8
+
+
+def run_w8a8(gpu, M, N, K, seed=0):
+    import torch
+    say(f"w8a8 M={M} N={N} K={K}")
+    a = uniform_i8((M, K), 1 + seed)
+    b = uniform_i8((K, N), 2 + seed)
+    sa = uniform_scales(M, 3 + seed)
+    sb = uniform_scales(N, 4 + seed)
+    c = tx.dot(to_device(a, gpu), to_device(b, gpu), scale_a=to_device(sa, gpu),
+               scale_b=to_device(sb, gpu), out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    return a, b, sa, sb, from_device(c)
+
+
+@pytest.mark.parametrize("M", [1, 16, 64, 256])
+def test_c4_w8a8_decode(gpu, M):
+    """Config 3: int8 W8A8, N=K=8192: int32 exact, so the bf16 output is bit-exact."""
+    N = K = 8192
+    a, b, sa, sb, got = run_w8a8(gpu, M, N, K)
+    ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 256, 128),
+                           scale_mode=oracle.SCALE_ROWCOL, sa=sa, sb=sb, round_mode=oracle.ROUND_RNE)
+    mism = np.flatnonzero(got != ref)
+    assert mism.size == 0, f"{mism.size} mismatches, first at {np.unravel_index(mism[0], got.shape)}"
+
+
+@pytest.mark.parametrize("M,N,K", [(5, 272, 208), (16, 256, 64), (40, 8208, 1008), (3, 16, 4160),
+                                   (64, 512, 16), (17, 4096, 2080)])
+def test_w8a8_decode_edges(gpu, M, N, K):
+    a, b, sa, sb, got = run_w8a8(gpu, M, N, K, seed=M)
+    ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 64, 64),
+                           scale_mode=oracle.SCALE_ROWCOL, sa=sa, sb=sb, round_mode=oracle.ROUND_RNE)
+    assert np.array_equal(got, ref)
+
+
+def test_w8a8_repeat_launches(gpu):
+    """The arrival counters carry over between launches: repeat, then change shape."""
+    for M, N, K in ((16, 8192, 8192), (16, 8192, 8192), (7, 4096, 2048), (16, 8192, 8192)):
+        a, b, sa, sb, got = run_w8a8(gpu, M, N, K, seed=11)
+        ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 256, 128),
+                               scale_mode=oracle.SCALE_ROWCOL, sa=sa, sb=sb)
+        assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("M,N,K,block", [(300, 304, 256, (128, 128, 128)),
+                                          (256, 512, 1000 - 1000 % 16, (256, 256, 128)),
+                                          (2, 16, 16, (128, 128, 128))])
+def test_int8_gemm_int32_exact(gpu, M, N, K, block):
+    import torch
+    say(f"int8 gemm i32 M={M} N={N} K={K} block={block}")
+    a = uniform_i8((M, K), 21)
+    b = uniform_i8((K, N), 22)
+    c = tx.dot(to_device(a, gpu), to_device(b, gpu), out_dtype=torch.int32, block=block)
+    torch.cuda.synchronize()
+    got = from_device(c)
+    exact = a.astype(np.int64) @ b.astype(np.int64)
+    assert np.array_equal(got.astype(np.int64), exact)
+
+
+# ----------------------------------------------------------------------------- fp8
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 7168, 7168), (200, 384, 640), (130, 250 + 6, 384)])
+def test_c5_fp8_block_scaled(gpu, M, N, K):
+    """Config 4: fp8 e4m3, 1x128 A-group and 128x128 B-block fp32 scales."""
+    import torch
+    say(f"fp8 block-scaled M={M} N={N} K={K}")
+    qa, qb, sa, sb = fp8_block_inputs(M, N, K, 7)
+    c = tx.dot(to_device(qa, gpu), to_device(qb, gpu), scale_a=to_device(sa, gpu),
+               scale_b=to_device(sb, gpu), out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    got = bits_to_f32(from_device(c), "bf16")
+    ref = bits_to_f32(oracle.tiled_dot(qa, qb, a_type=oracle.F8E4M3, c_type=oracle.BF16,
+                                       block=(128, 128, 128), scale_mode=oracle.SCALE_BLOCK128,
+                                       sa=sa, sb=sb), "bf16")
+    err = check_close(got, ref, atol=ATOL, rtol=RTOL, scale=math.sqrt(K), what="fp8")
+    say(f"fp8 {M}x{N}x{K} max|d|={err:.3g}")

@@ -1,0 +1,459 @@
+// mi355x_dot extension: libmi355x_dot.so.
+//
+// The backend half of the plugin: the "mi355x_dot" pass picks a gfx950 kernel
+// and launch shape for a planned dot, and the tx_dot_* C-ABI
+// (include/triton_ext/tx_dot.h) validates descriptors, runs the pass pipeline
+// (arith_intensity -> loop_split -> mi355x_dot, all through
+// tritonAddPluginPass) and launches.  The reference's backend directory is
+// empty (R:backend/CMakeLists.txt, 0 bytes); the pipeline shape follows its
+// registry (R:infra/pass/TritonExtPassInfra.cpp:19-26).
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "triton_ext/TritonExtPassInfra.h"
+#include "triton_ext/tx_dot.h"
+#include "triton_ext/tx_passes.h"
+
+#include "decode_i8.h"
+#include "gemm_tile.h"
+
+using namespace txk;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+#define TX_HIP_CHECK(expr)                                                     \
+  do {                                                                         \
+    hipError_t e_ = (expr);                                                    \
+    if (e_ != hipSuccess)                                                      \
+      return fail(TX_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_));  \
+  } while (0)
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------------------
+// Kernel table: every (operands, tile, epilogue) the backend instantiates.
+// ---------------------------------------------------------------------------
+
+typedef void (*GemmKernelFn)(GemmArgs);
+
+struct GemmConfig {
+  int op, bm, bn, bk, wm, wn, epi;
+  GemmKernelFn fn;
+  int lds_bytes;
+};
+
+#define TX_GEMM(OP, BM, BN, BK, WM, WN, EPI)                                   \
+  GemmConfig {                                                                 \
+    OP, BM, BN, BK, WM, WN, EPI, gemm_tile_kernel<OP, BM, BN, BK, WM, WN, EPI>,\
+        GemmTile<OP, BM, BN, BK, WM, WN, EPI>::LDS_BYTES                       \
+  }
+
+const GemmConfig kGemmConfigs[] = {
+    // bf16 / fp16 operands
+    TX_GEMM(OP_BF16, 256, 256, 64, 2, 2, EPI_BF16),
+    TX_GEMM(OP_BF16, 256, 256, 64, 2, 2, EPI_F32),
+    TX_GEMM(OP_BF16, 128, 128, 64, 2, 2, EPI_BF16),
+    TX_GEMM(OP_BF16, 128, 128, 64, 2, 2, EPI_F32),
+    TX_GEMM(OP_BF16, 64, 64, 32, 2, 2, EPI_BF16),
+    TX_GEMM(OP_BF16, 64, 64, 32, 2, 2, EPI_F32),
+    TX_GEMM(OP_F16, 256, 256, 64, 2, 2, EPI_F32),
+    TX_GEMM(OP_F16, 256, 256, 64, 2, 2, EPI_F16),
+    TX_GEMM(OP_F16, 128, 128, 64, 2, 2, EPI_F32),
+    TX_GEMM(OP_F16, 128, 128, 64, 2, 2, EPI_F16),
+    TX_GEMM(OP_F16, 64, 64, 32, 2, 2, EPI_F32),
+    TX_GEMM(OP_F16, 64, 64, 32, 2, 2, EPI_F16),
+    // int8 operands, int32 accumulation
+    TX_GEMM(OP_I8, 256, 256, 128, 2, 4, EPI_I32),
+    TX_GEMM(OP_I8, 256, 256, 128, 2, 4, EPI_ROWCOL_BF16),
+    TX_GEMM(OP_I8, 128, 128, 128, 2, 2, EPI_I32),
+    TX_GEMM(OP_I8, 128, 128, 128, 2, 2, EPI_ROWCOL_BF16),
+    // fp8 e4m3 operands, fp32 accumulation
+    TX_GEMM(OP_F8, 256, 256, 128, 2, 4, EPI_BLOCK128_BF16),
+    TX_GEMM(OP_F8, 256, 256, 128, 2, 4, EPI_BLOCK128_F32),
+    TX_GEMM(OP_F8, 256, 256, 128, 2, 4, EPI_F32),
+    TX_GEMM(OP_F8, 128, 128, 128, 2, 2, EPI_BLOCK128_BF16),
+    TX_GEMM(OP_F8, 128, 128, 128, 2, 2, EPI_BLOCK128_F32),
+    TX_GEMM(OP_F8, 128, 128, 128, 2, 2, EPI_F32),
+};
+constexpr int kNumGemmConfigs = sizeof(kGemmConfigs) / sizeof(kGemmConfigs[0]);
+
+typedef void (*DecodeKernelFn)(DecodeArgs);
+const DecodeKernelFn kDecodeKernels[4] = {
+    decode_i8_kernel<1, 4>, decode_i8_kernel<2, 4>, decode_i8_kernel<3, 4>,
+    decode_i8_kernel<4, 4>};
+constexpr int kDecodeWaves = 4;
+
+// Operand kind and epilogue of a descriptor (-1 if unsupported).
+void classify(const tx_dot_desc &d, int *op, int *epi) {
+  *op = -1;
+  *epi = -1;
+  if (d.a_type != d.b_type)
+    return;
+  switch (d.a_type) {
+  case TX_BF16:
+  case TX_F16:
+    if (d.scale_mode != TX_SCALE_NONE)
+      return;
+    *op = d.a_type == TX_BF16 ? OP_BF16 : OP_F16;
+    if (d.c_type == TX_F32)
+      *epi = EPI_F32;
+    else if (d.c_type == TX_BF16 && d.a_type == TX_BF16)
+      *epi = EPI_BF16;
+    else if (d.c_type == TX_F16 && d.a_type == TX_F16)
+      *epi = EPI_F16;
+    return;
+  case TX_I8:
+    *op = OP_I8;
+    if (d.scale_mode == TX_SCALE_NONE && d.c_type == TX_I32)
+      *epi = EPI_I32;
+    else if (d.scale_mode == TX_SCALE_ROWCOL && d.c_type == TX_BF16)
+      *epi = EPI_ROWCOL_BF16;
+    return;
+  case TX_F8E4M3:
+    *op = OP_F8;
+    if (d.scale_mode == TX_SCALE_BLOCK128 && d.c_type == TX_BF16)
+      *epi = EPI_BLOCK128_BF16;
+    else if (d.scale_mode == TX_SCALE_BLOCK128 && d.c_type == TX_F32)
+      *epi = EPI_BLOCK128_F32;
+    else if (d.scale_mode == TX_SCALE_NONE && d.c_type == TX_F32)
+      *epi = EPI_F32;
+    return;
+  default:
+    return;
+  }
+}
+
+int findGemmConfig(int op, int epi, int bm, int bn, int bk) {
+  for (int i = 0; i < kNumGemmConfigs; ++i) {
+    const GemmConfig &c = kGemmConfigs[i];
+    if (c.op == op && c.epi == epi && c.bm == bm && c.bn == bn && c.bk == bk)
+      return i;
+  }
+  return -1;
+}
+
+bool useDecode(const tx_dot_desc &d) {
+  return d.a_type == TX_I8 && d.scale_mode == TX_SCALE_ROWCOL && d.M <= 64;
+}
+
+// Split-K factor for the decode kernel: a power of two (<= kMaxSplit) so
+// that strips * ksplit workgroups cover the CUs about once, each with at
+// least four 64-row batches per wave.  TX_DECODE_KSPLIT overrides.
+int decodeSplit(int64_t N, int64_t K) {
+  const char *env = std::getenv("TX_DECODE_KSPLIT");
+  const int64_t strips = cdiv(N, kDecodeStripN);
+  const int64_t batches = cdiv(K, kDecodeBatchK);
+  int ks = 1;
+  if (env && *env) {
+    ks = std::atoi(env);
+  } else {
+    while (ks < (int)kMaxSplit && strips * ks < 256 &&
+           batches / (ks * 2) >= 4 * kDecodeWaves)
+      ks *= 2;
+  }
+  if (ks < 1)
+    ks = 1;
+  if (ks > (int)kMaxSplit)
+    ks = kMaxSplit;
+  while (ks & (ks - 1)) // round down to a power of two
+    ks &= ks - 1;
+  while (ks > 1 && cdiv(batches, ks) * (ks - 1) >= batches)
+    ks >>= 1; // every split must own at least one batch
+  return ks;
+}
+
+int64_t decodeWorkspace(const tx_dot_desc &d, int ksplit) {
+  if (ksplit <= 1)
+    return 0;
+  const int64_t counters = ((cdiv(d.N, kDecodeStripN) * 4 + 255) / 256) * 256;
+  return counters + (int64_t)ksplit * d.M * d.N * 4;
+}
+
+// ---------------------------------------------------------------------------
+// The "mi355x_dot" pass: kernel choice and launch shape.
+// ---------------------------------------------------------------------------
+int txMi355xDotRun(tx_dot_plan *plan) {
+  const tx_dot_desc &d = plan->desc;
+  int op, epi;
+  classify(d, &op, &epi);
+  if (op < 0 || epi < 0)
+    return fail(TX_ERR_UNSUPPORTED,
+                "no kernel for a_type=%d b_type=%d c_type=%d scale_mode=%d",
+                d.a_type, d.b_type, d.c_type, d.scale_mode);
+  if (useDecode(d)) {
+    const int ks = decodeSplit(d.N, d.K);
+    plan->kernel = TX_KERNEL_DECODE_I8;
+    plan->split_k = ks;
+    plan->grid_x = (int32_t)(cdiv(d.N, kDecodeStripN) * ks);
+    plan->grid_y = plan->grid_z = 1;
+    plan->block_threads = kDecodeWaves * 64;
+    plan->workspace_bytes = decodeWorkspace(d, ks);
+    plan->passes_run += 1;
+    return TX_OK;
+  }
+  const int ci = findGemmConfig(op, epi, d.block_m, d.block_n, d.block_k);
+  if (ci < 0)
+    return fail(TX_ERR_UNSUPPORTED, "no instantiated tile %dx%dx%d for this dtype",
+                d.block_m, d.block_n, d.block_k);
+  const GemmConfig &c = kGemmConfigs[ci];
+  plan->kernel = op == OP_I8 ? TX_KERNEL_GEMM_I8
+               : op == OP_F8 ? TX_KERNEL_GEMM_F8
+                             : TX_KERNEL_GEMM_16BIT;
+  plan->split_k = 1;
+  plan->grid_x = plan->m_tiles * plan->n_tiles;
+  plan->grid_y = plan->grid_z = 1;
+  plan->block_threads = c.wm * c.wn * 64;
+  plan->workspace_bytes = 0;
+  plan->passes_run += 1;
+  return TX_OK;
+}
+
+int validate(const tx_dot_desc *in, tx_dot_desc *d) {
+  if (!in)
+    return fail(TX_ERR_INVALID, "descriptor is NULL");
+  *d = *in;
+  if (d->M < 0 || d->N < 0 || d->K < 0)
+    return fail(TX_ERR_INVALID, "negative extent M=%lld N=%lld K=%lld",
+                (long long)d->M, (long long)d->N, (long long)d->K);
+  if (d->M > INT32_MAX || d->N > INT32_MAX || d->K > INT32_MAX)
+    return fail(TX_ERR_INVALID, "extent above 2^31-1");
+  const int32_t sa = tx_dtype_size(d->a_type), sb = tx_dtype_size(d->b_type),
+                sc = tx_dtype_size(d->c_type);
+  if (!sa || !sb || !sc)
+    return fail(TX_ERR_INVALID, "unknown dtype");
+  if (d->lda == 0) d->lda = d->K;
+  if (d->ldb == 0) d->ldb = d->N;
+  if (d->ldc == 0) d->ldc = d->N;
+  if (d->lda < d->K || d->ldb < d->N || d->ldc < d->N)
+    return fail(TX_ERR_INVALID, "row stride shorter than the row");
+  if ((d->lda * sa) % 16 || (d->ldb * sb) % 16)
+    return fail(TX_ERR_INVALID, "A/B row strides must be multiples of 16 bytes");
+  if ((d->K * sa) % 16 || (d->N * sb) % 16)
+    return fail(TX_ERR_UNSUPPORTED,
+                "K and N must be multiples of %d elements (16-byte chunks)",
+                16 / sa);
+  if (d->scale_mode < TX_SCALE_NONE || d->scale_mode > TX_SCALE_BLOCK128)
+    return fail(TX_ERR_INVALID, "unknown scale mode %d", d->scale_mode);
+  if ((d->block_m < 0) || (d->block_n < 0) || (d->block_k < 0))
+    return fail(TX_ERR_INVALID, "negative tile size");
+  return TX_OK;
+}
+
+} // namespace
+
+// ---------------------------------------------------------------------------
+// C-ABI
+// ---------------------------------------------------------------------------
+
+extern "C" TX_API const char *tx_get_last_error(void) {
+  return g_last_error.c_str();
+}
+
+extern "C" TX_API const char *tx_kernel_name(int32_t kernel) {
+  switch (kernel) {
+  case TX_KERNEL_GEMM_16BIT: return "gemm_16bit_mfma32x32x16";
+  case TX_KERNEL_GEMM_I8: return "gemm_i8_mfma32x32x32";
+  case TX_KERNEL_DECODE_I8: return "decode_i8_mfma16x16x64";
+  case TX_KERNEL_GEMM_F8: return "gemm_f8_mfma32x32x64";
+  default: return "?";
+  }
+}
+
+extern "C" TX_API int tx_device_available(void) {
+  // Per-device answer, cached: hipGetDeviceProperties is too slow to call on
+  // every launch.
+  static int cached[64];
+  static std::once_flag once[64];
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+    return 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return 0;
+  std::call_once(once[dev], [dev] {
+    hipDeviceProp_t prop;
+    cached[dev] = hipGetDeviceProperties(&prop, dev) == hipSuccess &&
+                  std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+  });
+  return cached[dev];
+}
+
+extern "C" TX_API int tx_dot_plan_create(const tx_dot_desc *desc,
+                                         tx_dot_plan *plan) {
+  g_last_error.clear();
+  if (!plan)
+    return fail(TX_ERR_INVALID, "plan is NULL");
+  tx_dot_desc d;
+  int rc = validate(desc, &d);
+  if (rc != TX_OK)
+    return rc;
+  std::memset(plan, 0, sizeof(*plan));
+  plan->desc = d;
+  TxPassManager *pm = txPassManagerCreate();
+  const char *pipeline[3] = {"arith_intensity", "loop_split", "mi355x_dot"};
+  for (const char *name : pipeline)
+    if (tritonAddPluginPass(pm, name) != TP_SUCCESS) {
+      txPassManagerDestroy(pm);
+      return fail(TX_ERR_NO_PASS, "extension pass '%s' is not registered", name);
+    }
+  rc = txPassManagerRun(pm, plan);
+  txPassManagerDestroy(pm);
+  if (rc != TX_OK && g_last_error.empty())
+    fail(rc, "plan pipeline failed with status %d", rc);
+  return rc;
+}
+
+namespace {
+
+int launchGemm(const tx_dot_plan &plan, const void *A, const void *B, void *C,
+               const float *sa, const float *sb, hipStream_t stream) {
+  const tx_dot_desc &d = plan.desc;
+  int op, epi;
+  classify(d, &op, &epi);
+  const int ci = findGemmConfig(op, epi, d.block_m, d.block_n, d.block_k);
+  if (ci < 0)
+    return fail(TX_ERR_UNSUPPORTED, "plan names a tile that is not instantiated");
+  const GemmConfig &c = kGemmConfigs[ci];
+  if (plan.grid_x != plan.m_tiles * plan.n_tiles || plan.m_tiles <= 0 ||
+      plan.n_tiles <= 0 || plan.block_threads != c.wm * c.wn * 64)
+    return fail(TX_ERR_INVALID, "plan launch shape does not match its tile");
+  static std::once_flag attr_once[kNumGemmConfigs];
+  hipError_t attr_err = hipSuccess;
+  std::call_once(attr_once[ci], [&] {
+    attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(c.fn),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   c.lds_bytes);
+  });
+  TX_HIP_CHECK(attr_err);
+
+  GemmArgs a;
+  a.A = static_cast<const uint8_t *>(A);
+  a.B = static_cast<const uint8_t *>(B);
+  a.C = C;
+  a.sa = sa;
+  a.sb = sb;
+  a.M = d.M;
+  a.N = d.N;
+  a.K = d.K;
+  a.lda = d.lda;
+  a.ldb = d.ldb;
+  a.ldc = d.ldc;
+  a.tiles_m = plan.m_tiles;
+  a.tiles_n = plan.n_tiles;
+  const int64_t masked_k = d.K - plan.k_split;
+  a.k_main_steps = plan.k_main_steps;
+  a.k_masked_steps = (int32_t)cdiv(masked_k, d.block_k);
+  const int total = a.k_main_steps + a.k_masked_steps;
+  const int km = op == OP_BF16 || op == OP_F16 ? 16 : op == OP_I8 ? 32 : 64;
+  a.last_ks = total > 0 ? (int32_t)cdiv(d.K - (int64_t)(total - 1) * d.block_k, km) : 0;
+  a.group_m = plan.m_tiles < 4 ? plan.m_tiles : 4;
+  a.sa_ld = (int32_t)cdiv(d.K, 128);
+  a.sb_ld = (int32_t)cdiv(d.N, 128);
+  hipLaunchKernelGGL(c.fn, dim3(plan.grid_x), dim3(plan.block_threads),
+                     c.lds_bytes, stream, a);
+  TX_HIP_CHECK(hipGetLastError());
+  return TX_OK;
+}
+
+int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
+                 const float *sa, const float *sb, void *ws, size_t ws_bytes,
+                 hipStream_t stream) {
+  const tx_dot_desc &d = plan.desc;
+  const int mt = (int)cdiv(d.M > 0 ? d.M : 1, 16);
+  if (mt < 1 || mt > 4)
+    return fail(TX_ERR_INVALID, "decode plan with M=%lld", (long long)d.M);
+  const int ks = plan.split_k;
+  if (ks < 1 || ks > (int)kMaxSplit || (ks & (ks - 1)))
+    return fail(TX_ERR_INVALID, "decode split %d is not a power of two <= %u", ks,
+                kMaxSplit);
+  if (plan.grid_x != cdiv(d.N, kDecodeStripN) * ks ||
+      plan.block_threads != kDecodeWaves * 64)
+    return fail(TX_ERR_INVALID, "plan launch shape does not match the decode kernel");
+  const int64_t need = decodeWorkspace(d, ks);
+  if (need > 0 && (!ws || (int64_t)ws_bytes < need))
+    return fail(TX_ERR_WORKSPACE, "decode needs %lld workspace bytes, got %zu",
+                (long long)need, ws_bytes);
+  DecodeArgs a;
+  a.A = static_cast<const int8_t *>(A);
+  a.B = static_cast<const int8_t *>(B);
+  a.C = static_cast<uint16_t *>(C);
+  a.sa = sa;
+  a.sb = sb;
+  a.M = (int32_t)d.M;
+  a.N = (int32_t)d.N;
+  a.K = (int32_t)d.K;
+  a.lda = d.lda;
+  a.ldb = d.ldb;
+  a.ldc = d.ldc;
+  a.ksplit = ks;
+  const int64_t batches = cdiv(d.K, kDecodeBatchK);
+  a.batches_per_split = (int32_t)cdiv(batches, ks);
+  a.k_main_batches = (int32_t)(plan.k_split / kDecodeBatchK);
+  const int64_t counters = ((cdiv(d.N, kDecodeStripN) * 4 + 255) / 256) * 256;
+  a.counters = static_cast<uint32_t *>(ws);
+  a.partials = need > 0 ? reinterpret_cast<int32_t *>(static_cast<uint8_t *>(ws) + counters)
+                        : nullptr;
+  hipLaunchKernelGGL(kDecodeKernels[mt - 1], dim3(plan.grid_x),
+                     dim3(plan.block_threads), 0, stream, a);
+  TX_HIP_CHECK(hipGetLastError());
+  return TX_OK;
+}
+
+} // namespace
+
+extern "C" TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A,
+                                    const void *B, void *C,
+                                    const float *scale_a, const float *scale_b,
+                                    void *workspace, size_t workspace_bytes,
+                                    void *stream) {
+  g_last_error.clear();
+  if (!plan)
+    return fail(TX_ERR_INVALID, "plan is NULL");
+  const tx_dot_desc &d = plan->desc;
+  if (d.M == 0 || d.N == 0)
+    return TX_OK; // empty output
+  if (!C || (d.K > 0 && (!A || !B)))
+    return fail(TX_ERR_INVALID, "NULL operand pointer");
+  if ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15)
+    return fail(TX_ERR_INVALID, "A and B must be 16-byte aligned");
+  if (d.scale_mode != TX_SCALE_NONE && (!scale_a || !scale_b))
+    return fail(TX_ERR_INVALID, "scaled dot needs scale_a and scale_b");
+  if (!tx_device_available())
+    return fail(TX_ERR_NO_DEVICE, "no gfx950 device visible");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (plan->kernel) {
+  case TX_KERNEL_GEMM_16BIT:
+  case TX_KERNEL_GEMM_I8:
+  case TX_KERNEL_GEMM_F8:
+    return launchGemm(*plan, A, B, C, scale_a, scale_b, s);
+  case TX_KERNEL_DECODE_I8:
+    return launchDecode(*plan, A, B, C, scale_a, scale_b, workspace,
+                        workspace_bytes, s);
+  default:
+    return fail(TX_ERR_INVALID, "plan has no kernel (kernel=%d)", plan->kernel);
+  }
+}
+
+#define TRITON_EXT_ARG "tx-mi355x-dot"
+#define TRITON_EXT_RUN txMi355xDotRun
+#include "../../infra/TritonExtPass.inc"

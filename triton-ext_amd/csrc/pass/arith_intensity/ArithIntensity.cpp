@@ -1,0 +1,159 @@
+// arith_intensity extension: libarith_intensity.so.
+//
+// The task names an "arithmetic-intensity pass" that the reference snapshot
+// does not contain, so this extension has no reference source to follow.  It
+// classifies a dot by its algorithmic work (every operand read once, the
+// output written once, scales read once) against MI355X's roofline and
+// recommends a tile from the set the mi355x_dot backend instantiates.
+//
+// MI355X public dense peaks: bf16/fp16 MFMA 2516.6 TFLOP/s (256 CUs x
+// 2.4 GHz x 4096 FLOP/clk/CU), fp8 and int8 5033.2 T(FL)OP/s, HBM3E 8 TB/s.
+
+#include "triton_ext/TritonExtPassInfra.h"
+#include "triton_ext/tx_dot.h"
+#include "triton_ext/tx_passes.h"
+
+#include <cmath>
+#include <cstdint>
+
+namespace {
+
+constexpr double kPeak16 = 2516.6e12;
+constexpr double kPeak8 = 5033.2e12;
+constexpr double kPeakF32 = 157.3e12;
+constexpr double kHbm = 8.0e12;
+constexpr int kCUs = 256;
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+struct Tile {
+  int32_t bm, bn, bk;
+  double eff; // fraction of MFMA peak a tile of this size sustains
+};
+
+// Tiles the backend instantiates, largest first.  `eff` is a planning
+// weight only: it ranks tiles by how well they amortise LDS fills.
+const Tile kTiles16[] = {{256, 256, 64, 0.85}, {128, 128, 64, 0.60},
+                         {64, 64, 32, 0.35}};
+const Tile kTiles8[] = {{256, 256, 128, 0.85}, {128, 128, 128, 0.60}};
+
+// Estimated time of a tiled dot in arbitrary units: whole waves of tiles
+// across the CUs, each tile costing BM*BN*K / eff.
+double tileCost(const Tile &t, int64_t M, int64_t N, int64_t K) {
+  int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
+  int64_t waves = cdiv(tiles, kCUs);
+  return (double)waves * t.bm * t.bn * (double)K / t.eff;
+}
+
+template <size_t N>
+Tile chooseTile(const Tile (&cands)[N], int64_t M, int64_t Nn, int64_t K) {
+  Tile best = cands[0];
+  double bestCost = tileCost(best, M, Nn, K);
+  for (size_t i = 1; i < N; ++i) {
+    double c = tileCost(cands[i], M, Nn, K);
+    if (c < bestCost) {
+      best = cands[i];
+      bestCost = c;
+    }
+  }
+  return best;
+}
+
+} // namespace
+
+extern "C" int32_t tx_dtype_size(int32_t dtype) {
+  switch (dtype) {
+  case TX_F32: return 4;
+  case TX_F16: return 2;
+  case TX_BF16: return 2;
+  case TX_I8: return 1;
+  case TX_F8E4M3: return 1;
+  case TX_I32: return 4;
+  default: return 0;
+  }
+}
+
+extern "C" double tx_mi355x_peak_flops(int32_t dtype) {
+  switch (dtype) {
+  case TX_F16:
+  case TX_BF16: return kPeak16;
+  case TX_I8:
+  case TX_F8E4M3: return kPeak8;
+  case TX_F32: return kPeakF32;
+  default: return 0.0;
+  }
+}
+
+extern "C" double tx_mi355x_peak_bw(void) { return kHbm; }
+
+extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
+  if (!d || !out)
+    return TX_ERR_INVALID;
+  *out = tx_ai_report{};
+  int32_t sa = tx_dtype_size(d->a_type), sb = tx_dtype_size(d->b_type),
+          sc = tx_dtype_size(d->c_type);
+  if (!sa || !sb || !sc || d->M < 0 || d->N < 0 || d->K < 0)
+    return TX_ERR_INVALID;
+  const double M = (double)d->M, N = (double)d->N, K = (double)d->K;
+  double scaleBytes = 0.0;
+  if (d->scale_mode == TX_SCALE_ROWCOL)
+    scaleBytes = 4.0 * (M + N);
+  else if (d->scale_mode == TX_SCALE_BLOCK128)
+    scaleBytes = 4.0 * (M * cdiv(d->K, 128) +
+                        (double)cdiv(d->K, 128) * cdiv(d->N, 128));
+  out->flops = 2.0 * M * N * K;
+  out->bytes = M * K * sa + K * N * sb + M * N * sc + scaleBytes;
+  out->intensity = out->bytes > 0 ? out->flops / out->bytes : 0.0;
+  out->peak_flops = tx_mi355x_peak_flops(d->a_type);
+  out->peak_bw = kHbm;
+  out->ridge = out->peak_flops / out->peak_bw;
+  out->bound = out->intensity > out->ridge ? TX_BOUND_MFMA : TX_BOUND_HBM;
+  double tc = out->peak_flops > 0 ? out->flops / out->peak_flops : 0.0;
+  double tm = out->bytes / out->peak_bw;
+  out->roofline_us = 1e6 * (tc > tm ? tc : tm);
+
+  Tile t{d->block_m, d->block_n, d->block_k, 1.0};
+  if (t.bm <= 0 || t.bn <= 0 || t.bk <= 0) {
+    if (sa == 2)
+      t = chooseTile(kTiles16, d->M, d->N, d->K);
+    else if (d->a_type == TX_I8 && d->M <= 64)
+      t = Tile{(int32_t)(16 * cdiv(d->M > 0 ? d->M : 1, 16)), 256, 64, 1.0};
+    else
+      t = chooseTile(kTiles8, d->M, d->N, d->K);
+  }
+  out->block_m = t.bm;
+  out->block_n = t.bn;
+  out->block_k = t.bk;
+  out->tile_intensity = 2.0 * t.bm * t.bn / ((double)(t.bm + t.bn) * sa);
+  return TX_OK;
+}
+
+namespace {
+
+// Pass body: classification and tile choice for one dot.
+int txArithIntensityRun(tx_dot_plan *plan) {
+  tx_ai_report r;
+  int rc = tx_arith_intensity(&plan->desc, &r);
+  if (rc != TX_OK)
+    return rc;
+  plan->flops = r.flops;
+  plan->bytes = r.bytes;
+  plan->intensity = r.intensity;
+  plan->peak_flops = r.peak_flops;
+  plan->peak_bw = r.peak_bw;
+  plan->ridge = r.ridge;
+  plan->roofline_us = r.roofline_us;
+  plan->tile_intensity = r.tile_intensity;
+  plan->bound = r.bound;
+  plan->desc.block_m = r.block_m;
+  plan->desc.block_n = r.block_n;
+  plan->desc.block_k = r.block_k;
+  plan->passes_run += 1;
+  return TX_OK;
+}
+
+} // namespace
+
+#define TRITON_EXT_ARG "tx-arith-intensity"
+#define TRITON_EXT_RUN txArithIntensityRun
+#include "../../infra/TritonExtPass.inc"

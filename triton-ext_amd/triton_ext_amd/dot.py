@@ -1,0 +1,100 @@
+"""`dot()` over torch device tensors, through the tx_dot C-ABI.
+
+torch provides the device memory and the current HIP stream; all arithmetic
+runs in libmi355x_dot.so's kernels.
+"""
+import ctypes
+
+from . import capi
+
+_TORCH_TYPES = {}
+_workspaces = {}
+
+
+def tx_type(t):
+    import torch
+    if not _TORCH_TYPES:
+        _TORCH_TYPES.update({torch.float32: capi.F32, torch.float16: capi.F16,
+                             torch.bfloat16: capi.BF16, torch.int8: capi.I8,
+                             torch.float8_e4m3fn: capi.F8E4M3, torch.uint8: capi.F8E4M3,
+                             torch.int32: capi.I32})
+    if t.dtype not in _TORCH_TYPES:
+        raise TypeError(f"unsupported dtype {t.dtype}")
+    return _TORCH_TYPES[t.dtype]
+
+
+def _torch_dtype(tx):
+    import torch
+    return {capi.F32: torch.float32, capi.F16: torch.float16, capi.BF16: torch.bfloat16,
+            capi.I32: torch.int32}[tx]
+
+
+def plan_for(a, b, out_dtype_tx, scale_mode=capi.SCALE_NONE, block=(0, 0, 0), flags=0):
+    if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[0]:
+        raise ValueError(f"dot of {tuple(a.shape)} and {tuple(b.shape)}")
+    if a.stride(1) != 1 or b.stride(1) != 1:
+        raise ValueError("A and B rows must be contiguous")
+    M, K = a.shape
+    N = b.shape[1]
+    # an empty operand's strides are arbitrary: describe it as packed
+    lda = a.stride(0) if M > 0 and K > 0 else 0
+    ldb = b.stride(0) if K > 0 and N > 0 else 0
+    desc = capi.make_desc(M, N, K, tx_type(a), out_dtype_tx, b_type=tx_type(b),
+                          scale_mode=scale_mode, block=block, lda=lda, ldb=ldb, flags=flags)
+    return capi.plan(desc)
+
+
+def workspace_for(p, device):
+    """A zero-initialised workspace of at least p.workspace_bytes, cached per device.
+
+    The decode kernel's arrival counters must start at zero once; after that
+    every completed launch leaves them consistent, so the buffer is reused.
+    """
+    import torch
+    if p.workspace_bytes == 0:
+        return None
+    key = str(device)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < p.workspace_bytes:
+        ws = torch.zeros(int(p.workspace_bytes), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def dot(a, b, out=None, out_dtype=None, scale_a=None, scale_b=None, scale_mode=None,
+        block=(0, 0, 0), flags=0, plan=None, workspace=None, stream=None):
+    """C = epilogue(A @ B) on the current device's stream.
+
+    scale_mode defaults to ROWCOL when int8 operands come with scales, to
+    BLOCK128 for fp8 operands with scales, else NONE.
+    """
+    import torch
+    ta = tx_type(a)
+    if scale_mode is None:
+        if scale_a is None:
+            scale_mode = capi.SCALE_NONE
+        else:
+            scale_mode = capi.SCALE_ROWCOL if ta == capi.I8 else capi.SCALE_BLOCK128
+    if out is not None:
+        c_tx = tx_type(out)
+    elif out_dtype is not None:
+        c_tx = tx_type(torch.empty(0, dtype=out_dtype))
+    else:
+        c_tx = capi.I32 if (ta == capi.I8 and scale_mode == capi.SCALE_NONE) else (
+            capi.BF16 if ta in (capi.BF16, capi.I8, capi.F8E4M3) else capi.F32)
+    p = plan if plan is not None else plan_for(a, b, c_tx, scale_mode, block, flags)
+    M, N = a.shape[0], b.shape[1]
+    if out is None:
+        out = torch.empty((M, N), dtype=_torch_dtype(c_tx), device=a.device)
+    if out.stride(1) != 1 or out.stride(0) != p.desc.ldc:
+        raise ValueError("output must be row-major with ldc == N")
+    ws = workspace if workspace is not None else workspace_for(p, a.device)
+    if stream is None:
+        stream = torch.cuda.current_stream(a.device).cuda_stream
+    L = capi.load()
+    capi.check(L.tx_dot_launch(ctypes.byref(p), a.data_ptr(), b.data_ptr(), out.data_ptr(),
+                               None if scale_a is None else scale_a.data_ptr(),
+                               None if scale_b is None else scale_b.data_ptr(),
+                               None if ws is None else ws.data_ptr(),
+                               0 if ws is None else ws.numel(), stream))
+    return out
