@@ -22,6 +22,7 @@
 #include "triton_ext/tx_passes.h"
 
 #include "decode_i8.h"
+#include "gemm16_dma.h"
 #include "gemm_tile.h"
 
 using namespace txk;
@@ -59,17 +60,36 @@ typedef void (*GemmKernelFn)(GemmArgs);
 struct GemmConfig {
   int op, bm, bn, bk, wm, wn, epi;
   GemmKernelFn fn;
-  int lds_bytes;
+  int lds_bytes; // dynamic LDS (0 for kernels with static LDS)
+  int dma;       // 1: direct-to-LDS staging + transpose reads (gemm16_dma.h)
 };
 
 #define TX_GEMM(OP, BM, BN, BK, WM, WN, EPI)                                   \
   GemmConfig {                                                                 \
     OP, BM, BN, BK, WM, WN, EPI, gemm_tile_kernel<OP, BM, BN, BK, WM, WN, EPI>,\
-        GemmTile<OP, BM, BN, BK, WM, WN, EPI>::LDS_BYTES                       \
+        GemmTile<OP, BM, BN, BK, WM, WN, EPI>::LDS_BYTES, 0                    \
   }
+#define TX_GEMM_DMA_S(OP, BM, BN, BK, WM, WN, ST, EPI)                         \
+  GemmConfig {                                                                 \
+    OP, BM, BN, BK, WM, WN, EPI,                                               \
+        gemm16_dma_kernel<OP, BM, BN, BK, WM, WN, ST, EPI>, 0, 1               \
+  }
+#define TX_GEMM_DMA(OP, BM, BN, BK, WM, WN, EPI)                               \
+  TX_GEMM_DMA_S(OP, BM, BN, BK, WM, WN, 2, EPI)
 
+// Lookup takes the first match, so a DMA variant listed before a
+// register-staged one of the same tile wins (TX_GEMM16_IMPL=regs skips DMA).
 const GemmConfig kGemmConfigs[] = {
-    // bf16 / fp16 operands
+    // bf16 / fp16 operands: direct-to-LDS staging, 8 waves (4x2) per 256x256
+    TX_GEMM_DMA(OP_BF16, 256, 256, 64, 4, 2, EPI_BF16),
+    TX_GEMM_DMA(OP_BF16, 256, 256, 64, 4, 2, EPI_F32),
+    TX_GEMM_DMA(OP_BF16, 128, 128, 64, 2, 2, EPI_BF16),
+    TX_GEMM_DMA(OP_BF16, 128, 128, 64, 2, 2, EPI_F32),
+    TX_GEMM_DMA(OP_F16, 256, 256, 64, 4, 2, EPI_F32),
+    TX_GEMM_DMA(OP_F16, 256, 256, 64, 4, 2, EPI_F16),
+    TX_GEMM_DMA(OP_F16, 128, 128, 64, 2, 2, EPI_F32),
+    TX_GEMM_DMA(OP_F16, 128, 128, 64, 2, 2, EPI_F16),
+    // register-staged fallbacks (TX_GEMM16_IMPL=regs) and the 64x64x32 tile
     TX_GEMM(OP_BF16, 256, 256, 64, 2, 2, EPI_BF16),
     TX_GEMM(OP_BF16, 256, 256, 64, 2, 2, EPI_F32),
     TX_GEMM(OP_BF16, 128, 128, 64, 2, 2, EPI_BF16),
@@ -144,8 +164,14 @@ void classify(const tx_dot_desc &d, int *op, int *epi) {
 }
 
 int findGemmConfig(int op, int epi, int bm, int bn, int bk) {
+  static const bool no_dma = [] {
+    const char *e = std::getenv("TX_GEMM16_IMPL");
+    return e && std::strcmp(e, "regs") == 0;
+  }();
   for (int i = 0; i < kNumGemmConfigs; ++i) {
     const GemmConfig &c = kGemmConfigs[i];
+    if (no_dma && c.dma)
+      continue;
     if (c.op == op && c.epi == epi && c.bm == bm && c.bn == bn && c.bk == bk)
       return i;
   }
@@ -339,11 +365,12 @@ int launchGemm(const tx_dot_plan &plan, const void *A, const void *B, void *C,
     return fail(TX_ERR_INVALID, "plan launch shape does not match its tile");
   static std::once_flag attr_once[kNumGemmConfigs];
   hipError_t attr_err = hipSuccess;
-  std::call_once(attr_once[ci], [&] {
-    attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(c.fn),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   c.lds_bytes);
-  });
+  if (c.lds_bytes > 0)
+    std::call_once(attr_once[ci], [&] {
+      attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(c.fn),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     c.lds_bytes);
+    });
   TX_HIP_CHECK(attr_err);
 
   GemmArgs a;
@@ -366,7 +393,14 @@ int launchGemm(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   const int total = a.k_main_steps + a.k_masked_steps;
   const int km = op == OP_BF16 || op == OP_F16 ? 16 : op == OP_I8 ? 32 : 64;
   a.last_ks = total > 0 ? (int32_t)cdiv(d.K - (int64_t)(total - 1) * d.block_k, km) : 0;
-  a.group_m = plan.m_tiles < 4 ? plan.m_tiles : 4;
+  if (a.last_ks > d.block_k / km)
+    a.last_ks = d.block_k / km;
+  static const int group_env = [] {
+    const char *e = std::getenv("TX_GROUP_M"); // tuning override
+    return e ? std::atoi(e) : 0;
+  }();
+  const int gm = group_env > 0 ? group_env : 4;
+  a.group_m = plan.m_tiles < gm ? plan.m_tiles : gm;
   a.sa_ld = (int32_t)cdiv(d.K, 128);
   a.sb_ld = (int32_t)cdiv(d.N, 128);
   hipLaunchKernelGGL(c.fn, dim3(plan.grid_x), dim3(plan.block_threads),

@@ -25,6 +25,8 @@
 // instantiation; interior tiles never test a bound.
 #pragma once
 
+#include <type_traits>
+
 #include "tile_common.h"
 
 namespace txk {
@@ -189,13 +191,14 @@ struct GemmTile {
     float rs = 0.f; // this thread's row scale for the staged K step
     const u32x4 zero = {0u, 0u, 0u, 0u};
 
-    auto load = [&](int kt, bool mask_k) {
+    auto load = [&](int kt, auto mask_k_tag) {
+      constexpr bool MASK_K = decltype(mask_k_tag)::value;
       const int64_t k0 = (int64_t)kt * BK;
 #pragma unroll
       for (int i = 0; i < A_LOADS; ++i) {
         const int id = tid + i * NT, row = id / NCH, ch = id % NCH;
         const int64_t gm = m0 + row, gk = k0 + (int64_t)ch * E;
-        const bool ok = (!MASK_MN || gm < p.M) && (!mask_k || gk < p.K);
+        const bool ok = (!MASK_MN || gm < p.M) && (!MASK_K || gk < p.K);
         ra[i] = ok ? *reinterpret_cast<const u32x4 *>(p.A + (gm * p.lda + gk) * ELT)
                    : zero;
       }
@@ -208,7 +211,7 @@ struct GemmTile {
 #pragma unroll
           for (int j = 0; j < E; ++j) {
             const int64_t gk = k0 + (int64_t)kb * E + j;
-            const bool ok = (!MASK_MN || gn < p.N) && (!mask_k || gk < p.K);
+            const bool ok = (!MASK_MN || gn < p.N) && (!MASK_K || gk < p.K);
             rb[i][j] = ok ? *reinterpret_cast<const u32x4 *>(p.B + (gk * p.ldb + gn) * ELT)
                           : zero;
           }
@@ -219,6 +222,8 @@ struct GemmTile {
         rs = (!MASK_MN || gm < p.M) ? p.sa[gm * p.sa_ld + kt] : 0.f;
       }
     };
+    using Unmasked = std::integral_constant<bool, false>;
+    using Masked = std::integral_constant<bool, true>;
 
     auto store = [&](int buf) {
       uint8_t *as = As + buf * A_BYTES;
@@ -247,11 +252,64 @@ struct GemmTile {
         Ss[buf * BM + tid] = rs;
     };
 
-    auto compute = [&](int buf, int nks, int kt) {
+    // One MFMA sub-step (KM elements of K) over the wave's tile.
+    auto substep = [&](const uint8_t *as, const uint8_t *bs, int ks, Acc (&dst)[FM][FN]) {
+      Frag<CPL> a[FM], b[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c)
+          a[i].v[c] = *reinterpret_cast<const u32x4 *>(
+              as + lds_off(wm * WTM + i * 32 + (lane & 31),
+                           ks * 2 * CPL + (lane >> 5) * CPL + c, NCH));
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c)
+          b[j].v[c] = *reinterpret_cast<const u32x4 *>(
+              bs + lds_off(wn * WTN + j * 32 + (lane & 31),
+                           ks * 2 * CPL + (lane >> 5) * CPL + c, NCH));
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          dst[i][j] = mfma(T(), a[i], b[j], dst[i][j]);
+    };
+
+    // Block-scale epilogue of one K step: acc += (part * sa[m][kb]) * sb[kb][n/128].
+    auto scale_add = [&](int buf, int kt, Acc (&part)[FM][FN]) {
+      const float *ss = Ss + buf * BM;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        float sr[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 s4 = *reinterpret_cast<const float4 *>(
+              ss + wm * WTM + i * 32 + 8 * q + 4 * (lane >> 5));
+          sr[4 * q + 0] = s4.x;
+          sr[4 * q + 1] = s4.y;
+          sr[4 * q + 2] = s4.z;
+          sr[4 * q + 3] = s4.w;
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int64_t nblk = (n0 + wn * WTN + j * 32) >> 7;
+          float sbv = 0.f;
+          if (!MASK_MN || nblk * 128 < p.N)
+            sbv = p.sb[(int64_t)kt * p.sb_ld + nblk];
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            acc[i][j][r] += (part[i][j][r] * sr[r]) * sbv;
+        }
+      }
+    };
+
+    // A full K step from LDS buffer `buf` (all KS sub-steps, no branches).
+    auto compute_full = [&](int buf, int kt) {
       const uint8_t *as = As + buf * A_BYTES;
       const uint8_t *bs = Bs + buf * B_BYTES;
-      Acc part[FM][FN];
-      if (SCALED) {
+      if constexpr (SCALED) {
+        Acc part[FM][FN];
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -259,84 +317,79 @@ struct GemmTile {
 #pragma unroll
             for (int r = 0; r < 16; ++r)
               part[i][j][r] = 0;
-      }
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        if (ks < nks) {
-          Frag<CPL> a[FM], b[FN];
+        for (int ks = 0; ks < KS; ++ks)
+          substep(as, bs, ks, part);
+        scale_add(buf, kt, part);
+      } else {
 #pragma unroll
-          for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int c = 0; c < CPL; ++c)
-              a[i].v[c] = *reinterpret_cast<const u32x4 *>(
-                  as + lds_off(wm * WTM + i * 32 + (lane & 31),
-                               ks * 2 * CPL + (lane >> 5) * CPL + c, NCH));
-#pragma unroll
-          for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int c = 0; c < CPL; ++c)
-              b[j].v[c] = *reinterpret_cast<const u32x4 *>(
-                  bs + lds_off(wn * WTN + j * 32 + (lane & 31),
-                               ks * 2 * CPL + (lane >> 5) * CPL + c, NCH));
-#pragma unroll
-          for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-              if (SCALED)
-                part[i][j] = mfma(T(), a[i], b[j], part[i][j]);
-              else
-                acc[i][j] = mfma(T(), a[i], b[j], acc[i][j]);
-            }
-        }
-      }
-      if (SCALED) {
-        // acc += (part * sa[m][kb]) * sb[kb][n/128]
-        const float *ss = Ss + buf * BM;
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-          float sr[16];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float4 s4 = *reinterpret_cast<const float4 *>(
-                ss + wm * WTM + i * 32 + 8 * q + 4 * (lane >> 5));
-            sr[4 * q + 0] = s4.x;
-            sr[4 * q + 1] = s4.y;
-            sr[4 * q + 2] = s4.z;
-            sr[4 * q + 3] = s4.w;
-          }
-#pragma unroll
-          for (int j = 0; j < FN; ++j) {
-            const int64_t nblk = (n0 + wn * WTN + j * 32) >> 7;
-            float sbv = 0.f;
-            if (!MASK_MN || nblk * 128 < p.N)
-              sbv = p.sb[(int64_t)kt * p.sb_ld + nblk];
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-              acc[i][j][r] += (part[i][j][r] * sr[r]) * sbv;
-          }
-        }
+        for (int ks = 0; ks < KS; ++ks)
+          substep(as, bs, ks, acc);
       }
     };
 
+    // The peeled last step: only the sub-steps that reach k < K.
+    auto compute_tail = [&](int buf, int kt, int nks) {
+      const uint8_t *as = As + buf * A_BYTES;
+      const uint8_t *bs = Bs + buf * B_BYTES;
+      if constexpr (SCALED) {
+        Acc part[FM][FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              part[i][j][r] = 0;
+        for (int ks = 0; ks < nks; ++ks)
+          substep(as, bs, ks, part);
+        scale_add(buf, kt, part);
+      } else {
+        for (int ks = 0; ks < nks; ++ks)
+          substep(as, bs, ks, acc);
+      }
+    };
+
+    // K loop in LoopSplit form: k_main_steps unmasked steps, then the masked
+    // steps (one after a split; all of them with splitting disabled), the last
+    // of which issues only last_ks sub-steps.
     const int nmain = p.k_main_steps;
     const int total = nmain + p.k_masked_steps;
-    if (total > 0) {
-      load(0, 0 >= nmain);
+    int kt = 0;
+    if (nmain > 0) {
+      load(0, Unmasked());
       store(0);
       __syncthreads();
-      for (int kt = 0; kt < total; ++kt) {
-        const int cur = kt & 1;
-        const bool has_next = kt + 1 < total;
-        if (has_next) {
-          if (kt + 1 < nmain)
-            load(kt + 1, false);
-          else
-            load(kt + 1, true);
-        }
-        compute(cur, kt == total - 1 ? p.last_ks : KS, kt);
-        if (has_next)
-          store(cur ^ 1);
+      for (; kt < nmain - 1; ++kt) { // branch-free main loop
+        load(kt + 1, Unmasked());
+        compute_full(kt & 1, kt);
+        store((kt + 1) & 1);
         __syncthreads();
+      }
+      if (total > nmain) { // last main step overlaps the first masked load
+        load(kt + 1, Masked());
+        compute_full(kt & 1, kt);
+        store((kt + 1) & 1);
+        __syncthreads();
+      } else {
+        compute_full(kt & 1, kt);
+      }
+      ++kt;
+    } else if (total > 0) {
+      load(0, Masked());
+      store(0);
+      __syncthreads();
+    }
+    for (; kt < total; ++kt) { // masked steps
+      const bool has_next = kt + 1 < total;
+      if (has_next)
+        load(kt + 1, Masked());
+      if (has_next) {
+        compute_full(kt & 1, kt);
+        store((kt + 1) & 1);
+        __syncthreads();
+      } else {
+        compute_tail(kt & 1, kt, p.last_ks);
       }
     }
 
