@@ -219,3 +219,63 @@ def test_c5_fp8_block_scaled(gpu, M, N, K):
                                        sa=sa, sb=sb), "bf16")
     err = check_close(got, ref, atol=ATOL, rtol=RTOL, scale=math.sqrt(K), what="fp8")
     say(f"fp8 {M}x{N}x{K} max|d|={err:.3g}")
+
+
+# ----------------------------------------------------------------------------- golden fixtures
+
+GOLDEN_TILE = {"f16": (64, 64, 32), "bf16": (128, 128, 64), "i8": (128, 128, 128),
+               "f8e4m3": (128, 128, 128)}
+
+
+@pytest.mark.parametrize("name", ["c1_fp16_512", "fp16_f32_edges_exact", "fp16_f16_rne_exact",
+                                  "bf16_bf16_rtz_exact", "bf16_f32_normal", "int8_i32",
+                                  "w8a8_rowcol_rtz", "fp8_block128_f32_exact",
+                                  "fp8_block128_bf16_normal"])
+def test_golden_fixture_on_gpu(gpu, name):
+    """The interpreter's fixtures through the HIP path.
+
+    Exact fixtures (every fp32 partial sum exact): the GPU output equals the
+    oracle's bit for bit, and where the interpreter truncated to bf16, the
+    GPU's fp32 accumulator truncated gives the fixture's bits.  Others: within
+    the north_star tolerance of the fixture."""
+    import os
+    import torch
+    from test_oracle_cpu import GOLDEN, OR_TYPE, fixture_output, load_fixture
+    say(f"golden {name}")
+    f = load_fixture(os.path.join(GOLDEN, name + ".npz"))
+    at, ct = str(f["a_type"]), str(f["c_type"])
+    tdt = {"f16": torch.float16, "bf16": torch.bfloat16, "i8": torch.int8,
+           "f8e4m3": torch.float8_e4m3fn}[at]
+    odt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16,
+           "i32": torch.int32}[ct]
+    view = {"f16": torch.int16, "bf16": torch.int16, "f8e4m3": torch.uint8, "i8": torch.int8}[at]
+    da = to_device(f["a"], gpu).view(view).view(tdt)
+    db = to_device(f["b"], gpu).view(view).view(tdt)
+    kw = {}
+    if "sa" in f:
+        kw = dict(scale_a=to_device(f["sa"], gpu), scale_b=to_device(f["sb"], gpu))
+    blk = GOLDEN_TILE[at] if name != "c1_fp16_512" else (64, 64, 32)
+    if name == "w8a8_rowcol_rtz":
+        blk = (0, 0, 0)  # M = 5: the decode kernel
+    c = tx.dot(da, db, out_dtype=odt, block=blk, **kw)
+    c32 = tx.dot(da, db, out_dtype=torch.float32, block=blk, **kw) if ct == "bf16" and at != "i8" \
+        else None
+    torch.cuda.synchronize()
+    got = from_device(c)
+    sm = {0: oracle.SCALE_NONE, 1: oracle.SCALE_ROWCOL, 2: oracle.SCALE_BLOCK128}[int(f["epi"])]
+    oblk = blk if blk != (0, 0, 0) else (64, 64, 64)
+    ref = oracle.tiled_dot(f["a"], f["b"], a_type=OR_TYPE[at], c_type=OR_TYPE[ct], block=oblk,
+                           scale_mode=sm, sa=f.get("sa"), sb=f.get("sb"),
+                           round_mode=oracle.ROUND_RNE)
+    if bool(f["exact"]):
+        assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} elements differ"
+        if ct == "bf16" and c32 is not None:
+            trunc = (from_device(c32).view(np.uint32) >> 16).astype(np.uint16)
+            g, w = fixture_output(f, trunc)
+            assert np.array_equal(g, w)
+        return
+    g, w = fixture_output(f, got)
+    K = int(f["K"])
+    scale = math.sqrt(K) if at == "f8e4m3" else 1.0
+    check_close(bits_to_f32(g, ct), bits_to_f32(w, ct), atol=ATOL, rtol=RTOL, scale=scale,
+                what=f"golden {name}")

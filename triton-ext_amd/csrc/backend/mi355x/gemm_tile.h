@@ -298,8 +298,12 @@ struct GemmTile {
           if (!MASK_MN || nblk * 128 < p.N)
             sbv = p.sb[(int64_t)kt * p.sb_ld + nblk];
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            acc[i][j][r] += (part[i][j][r] * sr[r]) * sbv;
+          for (int r = 0; r < 16; ++r) {
+            // No FMA contraction: the fp32 sequence acc + (part * sa) * sb,
+            // each operation rounded.
+#pragma clang fp contract(off)
+            acc[i][j][r] = acc[i][j][r] + (part[i][j][r] * sr[r]) * sbv;
+          }
         }
       }
     };

@@ -2,7 +2,7 @@
 // byte-permute transposes, bf16 rounding and the LDS swizzle.
 //
 // The transposes are __host__ __device__ so the same code is checked on the
-// CPU (tests/test_transpose_cpu.py builds a host harness).
+// CPU (tests/transpose_host.cpp is a host harness over them).
 #pragma once
 
 #include <stdint.h>
