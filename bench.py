@@ -102,12 +102,15 @@ def time_cold(fn, steps, warmup, flush):
 
 
 def make_flush(dev):
-    """Touch 512 MiB (2x the MALL) so the next kernel's operands come from HBM."""
+    """Read 512 MiB (2x the 256 MB MALL) so the next kernel's operands come from HBM.
+
+    A read, not a write: a write-flush would leave the caches full of dirty
+    lines whose write-back then competes with the timed kernel's reads."""
     import torch
-    buf = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    buf = torch.ones((512 << 20) // 4, dtype=torch.float32, device=dev)
 
     def flush():
-        buf.fill_(1)
+        buf.sum()
     return flush
 
 

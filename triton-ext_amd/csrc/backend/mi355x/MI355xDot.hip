@@ -118,10 +118,8 @@ const GemmConfig kGemmConfigs[] = {
 constexpr int kNumGemmConfigs = sizeof(kGemmConfigs) / sizeof(kGemmConfigs[0]);
 
 typedef void (*DecodeKernelFn)(DecodeArgs);
-const DecodeKernelFn kDecodeKernels[4] = {
-    decode_i8_kernel<1, 4>, decode_i8_kernel<2, 4>, decode_i8_kernel<3, 4>,
-    decode_i8_kernel<4, 4>};
-constexpr int kDecodeWaves = 4;
+const DecodeKernelFn kDecodeKernels[4] = {decode_i8_kernel<1>, decode_i8_kernel<2>,
+                                           decode_i8_kernel<3>, decode_i8_kernel<4>};
 
 // Operand kind and epilogue of a descriptor (-1 if unsupported).
 void classify(const tx_dot_desc &d, int *op, int *epi) {

@@ -2,35 +2,53 @@
 //   C[m][n] = bf16((float(sum_k A[m][k] * B[k][n]) * sa[m]) * sb[n])
 // with A int8 [M,K] (M <= 16*MT), B int8 [K,N] row-major, int32 accumulation.
 //
-// The job is a single pass over B (HBM-bound), so the kernel is built around
-// streaming B once with wide coalesced loads and keeping every CU busy:
-//  * A "batch" is 64 K-rows x 256 N-columns of B (16 KiB) for one wave.  Lane
-//    L = j + 16 g loads rows k0 + 16 g + i (i = 0..15) at columns
-//    n0 + 16 j .. +15: sixteen 16-byte loads, each wave-wide load reading
-//    four 256-byte row segments.
-//  * The lane's 16x16 byte block is transposed in registers (byte permutes),
-//    giving, for each column c, 16 K-consecutive bytes: exactly the B operand
-//    of v_mfma_i32_16x16x64_i8 for K-chunk g, with MFMA column j standing
-//    for N column n0 + 16 j + c.  One batch is 16 MFMAs per 16-row tile of A.
-//  * Waves of a workgroup take interleaved batches of the workgroup's K
-//    range; their int32 partials are summed in LDS.  Workgroups split K
-//    (ksplit ways) so that N/256 * ksplit workgroups fill the chip; each
-//    writes its int32 partial to the workspace, and the last workgroup of a
-//    column strip (atomic arrival counter) adds the partials in split order
-//    and applies the epilogue.  Integer addition is exact, so the result is
-//    bit-identical to any other summation order.
+// The job is one pass over B, so it is HBM-bound and the kernel is built to
+// stream B once with every CU keeping plenty of bytes in flight:
+//  * A workgroup owns a strip of 128 columns and a range of K (split-K);
+//    each of its 4 waves takes every 4th batch of 64 K rows (8 KiB of B).
+//  * Each wave has a private LDS ring of STAGES slots fed by
+//    global_load_lds_dwordx4 (lane l of a wave-wide load writes 16 bytes at
+//    slot + 16 l): 8 loads per batch move 64 rows x 128 bytes, 128-byte row
+//    segments, straight into LDS with no VGPR staging.  MT more loads bring
+//    the batch's A fragments in MFMA order.  B's loads are non-temporal: each
+//    byte is read once, and allocating loads would also have to write back
+//    whatever dirty lines they evict (measured: 2.7 vs 5.1 TB/s after a
+//    write-heavy kernel).  Waves never synchronise with
+//    each other inside the K loop; a wave waits for its own loads only
+//    (s_waitcnt vmcnt), STAGES - 1 batches stay in flight behind the one
+//    being used.
+//  * B rows are N-contiguous but the MFMA wants K-contiguous bytes per
+//    column.  ds_read_b64_tr_b8 does the transpose on the LDS read: within a
+//    16-lane group, lane i receives byte (i % 8) of the 8-byte words read by
+//    group lanes 2r + i/8, r = 0..7.  With group lane L reading row L/2,
+//    columns 8(L%2)..+7 of a 16-column block, lane i gets that column's 8
+//    K-consecutive bytes; two reads give the 16 bytes a lane holds for
+//    v_mfma_i32_16x16x64_i8 (lane l: column l % 16, K 16 (l/16) .. +15).
+//  * The 16-byte chunks of each LDS row are XOR-swizzled by row (chunk
+//    c ^ (row & 7)) through the choice of global address each lane loads, so
+//    the 8 rows one transposed read touches sit in 8 different chunks.
+//  * After the K loop the 4 waves' accumulators are summed through LDS.  With
+//    split-K each workgroup writes its int32 partial to the workspace and the
+//    last workgroup of a column strip (arrival counter) adds the partials in
+//    split order and applies the epilogue.  Integer addition is exact, so the
+//    result does not depend on the order.
 //  * Arrival counters are never reset: each workgroup adds kMaxSplit/ksplit,
 //    so a launch moves every counter by exactly kMaxSplit and the last
 //    arrival is the one that brings it to a multiple of kMaxSplit.  The
 //    counters must be zero once, when the workspace is created.
+//
+// K loop in LoopSplit form: batches below k_main_batches have every row
+// < K and load unmasked; the rest (the peeled tail) send rows >= K, columns
+// >= N and rows of A >= M to a zero-filled chunk (tl.load's other=0).
 #pragma once
 
-#include "gemm_tile.h"
+#include "gemm16_dma.h"
 
 namespace txk {
 
 constexpr int kDecodeBatchK = 64;
-constexpr int kDecodeStripN = 256;
+constexpr int kDecodeStripN = 128;
+constexpr int kDecodeWaves = 4;
 constexpr uint32_t kMaxSplit = 64;
 
 struct DecodeArgs {
@@ -41,115 +59,242 @@ struct DecodeArgs {
   const float *sb;
   int32_t M, N, K;
   int64_t lda, ldb, ldc;
-  int32_t ksplit;           // workgroups per column strip (power of two)
+  int32_t ksplit;            // workgroups per column strip (power of two)
   int32_t batches_per_split;
-  int32_t k_main_batches;   // batches with every K row < K (unmasked)
-  int32_t *partials;        // [ksplit][M][N] int32
-  uint32_t *counters;       // [N / 256] arrival counters
+  int32_t k_main_batches;    // batches with every K row < K (unmasked)
+  int32_t *partials;         // [ksplit][M][N] int32
+  uint32_t *counters;        // [ceil(N / 128)] arrival counters
 };
 
-__device__ __forceinline__ i32x4_t mfma_i8_16(const u32x4 &a, const u32x4 &b,
+typedef int v2i_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i_t lds_v2i;
+
+__device__ __forceinline__ i32x4_t mfma_i8_16(const i32x4_t &a, const i32x4_t &b,
                                               i32x4_t acc) {
-  return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4_t, a),
-                                               __builtin_bit_cast(i32x4_t, b),
-                                               acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
 }
 
-template <int MT, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64)
+// 32-bit LDS address of a __shared__ pointer.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+template <int MT> struct DecodeCfg {
+  // Slots per wave: 4 waves x STAGES x (8 KiB of B + MT KiB of A) <= 160 KiB.
+  static constexpr int STAGES = MT == 1 ? 4 : 3;
+  static constexpr int B_BYTES = kDecodeBatchK * kDecodeStripN; // 8 KiB
+  static constexpr int SLOT = B_BYTES + MT * 1024;
+  static constexpr int VM_PER_BATCH = 8 + MT; // direct-to-LDS loads per batch
+  static constexpr int LDS = kDecodeWaves * STAGES * SLOT;
+  static_assert(LDS <= 160 * 1024, "ring exceeds LDS");
+  static_assert((STAGES - 1) * VM_PER_BATCH <= 63, "vmcnt is 6 bits");
+};
+
+template <int MT>
+__global__ void __launch_bounds__(kDecodeWaves * 64, 1)
     decode_i8_kernel(DecodeArgs p) {
-  constexpr int MROWS = 16 * MT;
-  __shared__ int32_t red[MROWS * kDecodeStripN];
+  typedef DecodeCfg<MT> Cfg;
+  constexpr int STAGES = Cfg::STAGES;
+  constexpr int STAGE_BYTES = kDecodeWaves * Cfg::SLOT;
+  // One __shared__ array per ring stage (all waves' slots of that stage):
+  // distinct objects let the compiler's wait-count insertion tell the slot a
+  // direct-to-LDS load is filling from the slots being read.
+  __shared__ __attribute__((aligned(1024))) uint8_t st0[STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t st1[STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t st2[STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t st3[STAGES > 3 ? STAGE_BYTES : 1];
   __shared__ uint32_t last_flag;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int j = lane & 15, g = lane >> 4;
-  const int nstrips = (p.N + kDecodeStripN - 1) / kDecodeStripN;
-  // Split index varies fastest across consecutive workgroups so that a
-  // strip's splits land on different XCDs and CUs.
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int strip = blockIdx.x / p.ksplit, split = blockIdx.x % p.ksplit;
   const int64_t n0 = (int64_t)strip * kDecodeStripN;
-  const int64_t ncol = n0 + 16 * j; // this lane's 16 columns
-  const bool col_ok = ncol < p.N;
-
-  for (int i = tid; i < MROWS * kDecodeStripN; i += WAVES * 64)
-    red[i] = 0;
-
-  i32x4_t acc[MT][16];
+  const bool n_edge = n0 + kDecodeStripN > p.N;
+  uint8_t *const all_st[4] = {st0, st1, st2, st3};
+  uint8_t *slots[STAGES];
 #pragma unroll
-  for (int t = 0; t < MT; ++t)
-#pragma unroll
-    for (int c = 0; c < 16; ++c)
-      acc[t][c] = i32x4_t{0, 0, 0, 0};
+  for (int s = 0; s < STAGES; ++s)
+    slots[s] = all_st[s] + wave * Cfg::SLOT;
 
-  const u32x4 zero = {0u, 0u, 0u, 0u};
+  const int total_batches = (p.K + kDecodeBatchK - 1) / kDecodeBatchK;
   const int b_begin = split * p.batches_per_split;
   int b_end = b_begin + p.batches_per_split;
-  const int total_batches = (p.K + kDecodeBatchK - 1) / kDecodeBatchK;
   if (b_end > total_batches)
     b_end = total_batches;
+  // This wave's batches: b_begin + wave + 4 i, i < nb.
+  const int first = b_begin + wave;
+  const int nb = first < b_end ? (b_end - first + kDecodeWaves - 1) / kDecodeWaves : 0;
 
-  u32x4 rb[16];
-  u32x4 ra[MT];
-  auto load = [&](int b) {
+  // Direct-to-LDS loads of one batch into `slot`.
+  auto issue = [&](int b, uint8_t *slot) {
     const int64_t k0 = (int64_t)b * kDecodeBatchK;
-    const bool mask_k = b >= p.k_main_batches;
+    const bool mask = n_edge || b >= p.k_main_batches;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int64_t k = k0 + 16 * g + i;
-      const bool ok = col_ok && (!mask_k || k < p.K);
-      rb[i] = ok ? __builtin_nontemporal_load(
-                       reinterpret_cast<const u32x4 *>(p.B + k * p.ldb + ncol))
-                 : zero;
+    for (int i = 0; i < 8; ++i) {
+      const int row = 8 * i + (lane >> 3), pc = lane & 7;
+      const int c = pc ^ (row & 7);
+      const int64_t k = k0 + row, n = n0 + 16 * c;
+      const void *src = p.B + k * p.ldb + n;
+      if (mask && (k >= p.K || n >= p.N))
+        src = tx_zero_chunk;
+      dma16_stream(src, (lds_void *)(slot + i * 1024)); // B is read once
     }
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      const int m = t * 16 + j;
-      const int64_t k = k0 + 16 * g;
-      const bool ok = m < p.M && (!mask_k || k < p.K);
-      ra[t] = ok ? *reinterpret_cast<const u32x4 *>(p.A + m * p.lda + k) : zero;
+      const int m = 16 * t + (lane & 15);
+      const int64_t k = k0 + 16 * (lane >> 4);
+      const void *src = p.A + (int64_t)m * p.lda + k;
+      if (m >= p.M || (b >= p.k_main_batches && k >= p.K))
+        src = tx_zero_chunk;
+      dma16(src, (lds_void *)(slot + Cfg::B_BYTES + t * 1024));
     }
   };
 
-  int b = b_begin + wave;
-  if (b < b_end)
-    load(b);
-  while (b < b_end) {
-    u32x4 tb[16];
-    transpose16x16_b8(rb, tb);
-    u32x4 a[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-      a[t] = ra[t];
-    const int nb = b + WAVES;
-    if (nb < b_end)
-      load(nb); // next batch in flight during this batch's MFMAs
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-      for (int c = 0; c < 16; ++c)
-        acc[t][c] = mfma_i8_16(a[t], tb[c], acc[t][c]);
-    b = nb;
-  }
-  __syncthreads(); // red[] zeroed
-
-  // acc[t][c] register r of lane (j, g): row t*16 + 4 g + r, column 16 j + c.
+  i32x4_t acc[MT][8];
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
-    for (int c = 0; c < 16; ++c)
+    for (int j = 0; j < 8; ++j)
+      acc[t][j] = i32x4_t{0, 0, 0, 0};
+
+  // MFMAs of one batch from `slot`.  The LDS reads are inline asm blocks
+  // that end in s_waitcnt lgkmcnt(0): the compiler cannot see them as reads
+  // of memory a direct-to-LDS load may still be filling, so it adds no
+  // vmcnt(0) of its own, and the counted waits below keep STAGES - 1 batches
+  // in flight.  Each block's outputs are complete when the block ends.
+  const int G = lane >> 4, L = lane & 15;
+  // Byte offsets (within a slot) of this lane's transposed reads: rows
+  // 16 G + L/2 (+8), columns 16 j + 8 (L % 2), chunk j swizzled by row.
+  uint32_t tr_off[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int r0 = 16 * G + (L >> 1);
+    tr_off[j] = r0 * 128 + ((j ^ (r0 & 7)) << 4) + 8 * (L & 1); // row r0 + 8: +1024
+  }
+  auto consume = [&](const uint8_t *slot) {
+    const uint32_t base = lds_addr(slot);
+    i32x4_t a[MT];
+    v2i_t lo[8], hi[8];
+    // A fragments (ds_read_b128 at lane * 16) and columns 0..63.
+    if constexpr (MT == 1) {
+      asm volatile(
+          "ds_read_b128 %0, %9 offset:8192\n\t"
+          "ds_read_b64_tr_b8 %1, %10\n\tds_read_b64_tr_b8 %2, %10 offset:1024\n\t"
+          "ds_read_b64_tr_b8 %3, %11\n\tds_read_b64_tr_b8 %4, %11 offset:1024\n\t"
+          "ds_read_b64_tr_b8 %5, %12\n\tds_read_b64_tr_b8 %6, %12 offset:1024\n\t"
+          "ds_read_b64_tr_b8 %7, %13\n\tds_read_b64_tr_b8 %8, %13 offset:1024\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=v"(a[0]), "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1]), "=v"(lo[2]),
+            "=v"(hi[2]), "=v"(lo[3]), "=v"(hi[3])
+          : "v"(base + lane * 16), "v"(base + tr_off[0]), "v"(base + tr_off[1]),
+            "v"(base + tr_off[2]), "v"(base + tr_off[3])
+          : "memory");
+    } else {
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+        asm volatile("ds_read_b128 %0, %1 offset:%2\n\ts_waitcnt lgkmcnt(0)"
+                     : "=v"(a[t])
+                     : "v"(base + lane * 16), "i"(Cfg::B_BYTES + t * 1024)
+                     : "memory");
+      asm volatile(
+          "ds_read_b64_tr_b8 %0, %8\n\tds_read_b64_tr_b8 %1, %8 offset:1024\n\t"
+          "ds_read_b64_tr_b8 %2, %9\n\tds_read_b64_tr_b8 %3, %9 offset:1024\n\t"
+          "ds_read_b64_tr_b8 %4, %10\n\tds_read_b64_tr_b8 %5, %10 offset:1024\n\t"
+          "ds_read_b64_tr_b8 %6, %11\n\tds_read_b64_tr_b8 %7, %11 offset:1024\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1]), "=v"(lo[2]), "=v"(hi[2]),
+            "=v"(lo[3]), "=v"(hi[3])
+          : "v"(base + tr_off[0]), "v"(base + tr_off[1]), "v"(base + tr_off[2]),
+            "v"(base + tr_off[3])
+          : "memory");
+    }
+    // Columns 64..127.
+    asm volatile(
+        "ds_read_b64_tr_b8 %0, %8\n\tds_read_b64_tr_b8 %1, %8 offset:1024\n\t"
+        "ds_read_b64_tr_b8 %2, %9\n\tds_read_b64_tr_b8 %3, %9 offset:1024\n\t"
+        "ds_read_b64_tr_b8 %4, %10\n\tds_read_b64_tr_b8 %5, %10 offset:1024\n\t"
+        "ds_read_b64_tr_b8 %6, %11\n\tds_read_b64_tr_b8 %7, %11 offset:1024\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=v"(lo[4]), "=v"(hi[4]), "=v"(lo[5]), "=v"(hi[5]), "=v"(lo[6]), "=v"(hi[6]),
+          "=v"(lo[7]), "=v"(hi[7])
+        : "v"(base + tr_off[4]), "v"(base + tr_off[5]), "v"(base + tr_off[6]),
+          "v"(base + tr_off[7])
+        : "memory");
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const i32x4_t bf = {lo[j].x, lo[j].y, hi[j].x, hi[j].y};
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+        acc[t][j] = mfma_i8_16(a[t], bf, acc[t][j]);
+    }
+  };
+
+  // s_waitcnt vmcnt(newer * loads per batch), other counters untouched
+  // (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+  auto wait_newer = [](int newer) {
+    constexpr int V = Cfg::VM_PER_BATCH;
+    if (newer <= 0)
+      __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xf << 8));
+    else if (newer == 1)
+      __builtin_amdgcn_s_waitcnt((V & 0xf) | ((V >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+    else if (newer == 2)
+      __builtin_amdgcn_s_waitcnt(((2 * V) & 0xf) | (((2 * V) >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+    else
+      __builtin_amdgcn_s_waitcnt(((3 * V) & 0xf) | (((3 * V) >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+  };
+
+  // Prologue: STAGES - 1 batches in flight.
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < nb)
+      issue(first + kDecodeWaves * s, slots[s]);
+  // Main loop, unrolled by STAGES so slot addresses are static.
+  for (int i0 = 0; i0 < nb; i0 += STAGES) {
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s) {
+      const int i = i0 + s;
+      if (i < nb) {
+        const int in = i + STAGES - 1; // batch whose loads go out now
+        if (in < nb) {
+          // Its slot was read at step i - 1: wait for those LDS reads
+          // (lgkmcnt 0) before the new loads may overwrite it.
+          __builtin_amdgcn_s_waitcnt(0xf | (0x3 << 14) | (0x7 << 4));
+          issue(first + kDecodeWaves * in, slots[(s + STAGES - 1) % STAGES]);
+        }
+        const int newer = (nb - 1 - i) < (STAGES - 1) ? (nb - 1 - i) : (STAGES - 1);
+        wait_newer(newer);
+        consume(slots[s]);
+      }
+    }
+  }
+
+  __builtin_amdgcn_s_waitcnt(0); // every load of the loop has landed
+  // Sum the 4 waves' accumulators in LDS (stage 0 is free now) with LDS
+  // atomics.  acc[t][j] register r of lane l: row 16 t + 4 (l / 16) + r,
+  // column 16 j + l % 16.
+  constexpr int TILE = MT * 16 * kDecodeStripN; // int32 of the strip's sums
+  static_assert(TILE * 4 <= STAGE_BYTES, "reduction tile exceeds stage 0");
+  int32_t *red = reinterpret_cast<int32_t *>(st0);
+  __syncthreads();
+  for (int i = tid; i < TILE; i += kDecodeWaves * 64)
+    red[i] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        atomicAdd(&red[(t * 16 + 4 * g + r) * kDecodeStripN + 16 * j + c],
-                  acc[t][c][r]);
+        atomicAdd(&red[(16 * t + 4 * G + r) * kDecodeStripN + 16 * j + L], acc[t][j][r]);
   __syncthreads();
 
-  const int nthreads = WAVES * 64;
+  const int nthreads = kDecodeWaves * 64;
+  auto wg_sum = [&](int i) { return red[i]; };
   if (p.ksplit == 1) {
     for (int i = tid; i < p.M * kDecodeStripN; i += nthreads) {
       const int m = i / kDecodeStripN, n = i % kDecodeStripN;
       if (n0 + n < p.N) {
-        const float v = ((float)red[m * kDecodeStripN + n] * p.sa[m]) * p.sb[n0 + n];
+        const float v = ((float)wg_sum(i) * p.sa[m]) * p.sb[n0 + n];
         p.C[m * p.ldc + n0 + n] = f32_to_bf16_rne(v);
       }
     }
@@ -157,37 +302,73 @@ __global__ void __launch_bounds__(WAVES * 64)
   }
 
   // Publish this split's partial, then count arrivals for the strip.
+  // Cross-workgroup data moves only through agent-scope atomics (relaxed):
+  // on gfx950 they are coherent across the XCDs' L2s by themselves (sc1), so
+  // no fence has to write back or invalidate a whole L2 (an agent-scope
+  // release/acquire fence pair costs ~40 us here).  Ordering: every thread's
+  // stores are acknowledged (s_waitcnt vmcnt(0)) before the barrier that
+  // precedes the counter increment, and the last workgroup issues its loads
+  // only after its increment has returned.
   int32_t *mine = p.partials + (int64_t)split * p.M * p.N;
   for (int i = tid; i < p.M * kDecodeStripN; i += nthreads) {
     const int m = i / kDecodeStripN, n = i % kDecodeStripN;
     if (n0 + n < p.N)
-      mine[(int64_t)m * p.N + n0 + n] = red[m * kDecodeStripN + n];
+      __hip_atomic_store(&mine[(int64_t)m * p.N + n0 + n], wg_sum(i), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
   }
-  __threadfence();
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) {
     const uint32_t inc = kMaxSplit / (uint32_t)p.ksplit;
-    const uint32_t old = atomicAdd(&p.counters[strip], inc);
+    const uint32_t old = __hip_atomic_fetch_add(&p.counters[strip], inc, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
     last_flag = ((old + inc) % kMaxSplit) == 0;
   }
   __syncthreads();
   if (!last_flag)
     return;
-  __threadfence();
-  for (int i = tid; i < p.M * kDecodeStripN; i += nthreads) {
+  // Last arrival: add the other splits' partials to this workgroup's own sum
+  // (still in LDS), in split order, then apply the epilogue.  Loads are
+  // issued four splits at a time before any of them is used, so the gather
+  // costs one memory round trip per four splits.
+  constexpr int PER = MT * 16 * kDecodeStripN / (kDecodeWaves * 64); // elements per thread
+  int32_t sum[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e)
+    sum[e] = 0;
+  for (int q0 = 0; q0 < p.ksplit; q0 += 4) {
+    int32_t v[4][PER];
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const int q = q0 + qq;
+      const int32_t *src = p.partials + (int64_t)q * p.M * p.N;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const int i = tid + e * nthreads;
+        const int m = i / kDecodeStripN, n = i % kDecodeStripN;
+        v[qq][e] = 0;
+        if (q < p.ksplit && m < p.M && n0 + n < p.N)
+          v[qq][e] = q == split ? wg_sum(i)
+                                : __hip_atomic_load(&src[(int64_t)m * p.N + n0 + n],
+                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq)
+#pragma unroll
+      for (int e = 0; e < PER; ++e)
+        sum[e] += v[qq][e];
+  }
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const int i = tid + e * nthreads;
     const int m = i / kDecodeStripN, n = i % kDecodeStripN;
     const int64_t col = n0 + n;
-    if (col < p.N) {
-      int32_t s = 0;
-      for (int q = 0; q < p.ksplit; ++q) {
-        const int32_t *src = p.partials + (int64_t)q * p.M * p.N;
-        s += __builtin_nontemporal_load(&src[(int64_t)m * p.N + col]);
-      }
-      const float v = ((float)s * p.sa[m]) * p.sb[col];
+    if (m < p.M && col < p.N) {
+      const float v = ((float)sum[e] * p.sa[m]) * p.sb[col];
       p.C[m * p.ldc + col] = f32_to_bf16_rne(v);
     }
   }
-  (void)nstrips;
 }
 
 } // namespace txk

@@ -48,6 +48,13 @@ __device__ __forceinline__ void dma16(const void *src, lds_void *dst) {
   __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
 }
 
+// The same with the non-temporal cache policy (gfx940+ cache-policy bit NT,
+// value 2): for data read exactly once, which then neither allocates in the
+// caches nor forces write-backs of dirty lines to make room.
+__device__ __forceinline__ void dma16_stream(const void *src, lds_void *dst) {
+  __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 2);
+}
+
 __device__ __forceinline__ u32x4 tr_read_pair(const uint8_t *lds, uint32_t off0,
                                               uint32_t off1) {
   const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
