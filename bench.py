@@ -32,6 +32,10 @@ METRIC = "tt.dot TFLOP/s + % MFMA/HBM roofline (bf16 4096^3; int8 W8A8 M=16)"
 PEAK_BF16 = 2516.6e12
 PEAK_I8 = 5033.2e12
 HBM = 8.0e12
+# HBM bytes per launch of the bf16 4096^3 kernel: rocprofv3 FETCH_SIZE + WRITE_SIZE of one
+# dispatch, each scaled by the counter's reading for a 256 MiB copy (--copy-probe): FETCH x2.0,
+# WRITE x1.0 (profiles/gemm16_bf16_4096.md).
+TRAFFIC_BF16_4096 = 235.2e6
 
 
 def parse():
@@ -40,7 +44,13 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="run only the named workload(s), comma-separated")
+    ap.add_argument("--only", default="",
+                    help="secondary workloads to run, comma-separated: vendor, tail, w8a8 (or "
+                         "w8a8_1, w8a8_16, w8a8_64, w8a8_256), fp8 (default: all); the bf16 "
+                         "headline always runs")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only copy 256 MiB five times (a transfer of known size that scales the "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters), then exit")
     return ap.parse_args()
 
 
@@ -67,12 +77,28 @@ class Launcher:
             raise RuntimeError(self.L.tx_get_last_error().decode())
 
 
-def time_back_to_back(fn, steps, warmup):
-    """Average ms per launch over `steps` back-to-back launches (events on the launch stream)."""
+MIN_WARMUP_S = 0.1
+
+
+def warm(fn, warmup):
+    """`warmup` untimed launches, then more until at least MIN_WARMUP_S of GPU work has run:
+    MI355X's clocks take tens of milliseconds to settle under MFMA load (triton's do_bench
+    warms up by time for the same reason)."""
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < MIN_WARMUP_S:
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+
+
+def time_back_to_back(fn, steps, warmup):
+    """Average ms per launch over `steps` back-to-back launches (events on the launch stream)."""
+    import torch
+    warm(fn, warmup)
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
     for _ in range(steps):
@@ -85,9 +111,7 @@ def time_back_to_back(fn, steps, warmup):
 def time_cold(fn, steps, warmup, flush):
     """Median ms of single launches, each bracketed by events, with `flush` run before each."""
     import torch
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
+    warm(fn, warmup)
     times = []
     for _ in range(steps):
         flush()
@@ -137,6 +161,16 @@ def bench_bf16(tx, dev, M, N, K, steps, warmup, seed=1):
                           k_main_steps=p.k_main_steps, k_tail=p.k_tail, m_edge=p.m_edge,
                           n_edge=p.n_edge, intensity=round(p.intensity, 1),
                           bound="mfma" if p.bound == tx.BOUND_MFMA else "hbm")), (a, b, c)
+
+
+def bench_vendor_bf16(dev, M, N, K, steps, warmup, seed=1):
+    """hipBLASLt (torch.matmul) on the same workload and timing: a reference point only."""
+    import torch
+    a, b = bf16_inputs(M, N, K, dev, seed)
+    c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    ms = time_back_to_back(lambda: torch.matmul(a, b, out=c), steps, warmup)
+    return dict(workload=f"hipBLASLt (torch.matmul) bf16 {M}x{N}x{K}", ms=ms,
+                tflops=2.0 * M * N * K / ms / 1e9)
 
 
 def bench_w8a8(tx, dev, M, N, K, steps, warmup, flush, seed=3):
@@ -204,8 +238,21 @@ def cpu_baseline(a, b, c, M, N, K, block):
                 seconds=dt), ok
 
 
+def copy_probe():
+    import torch
+    x = torch.ones((256 << 20) // 4, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(5):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print("copied 5 x 256 MiB", flush=True)
+
+
 def main():
     args = parse()
+    if args.copy_probe:
+        copy_probe()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(the dot shards by N or M blocks with no exchange; see DESIGN.md).", file=sys.stderr)
@@ -227,14 +274,19 @@ def main():
     print(f"# bf16 4096^3: {head['ms'] * 1e3:.1f} us/step, {head['tflops']:.1f} TFLOP/s, "
           f"{100 * head['frac']:.1f}% of peak", file=sys.stderr, flush=True)
     secondary = []
+    if want("vendor"):
+        r = bench_vendor_bf16(dev, M, N, K, args.steps, args.warmup)
+        secondary.append(r)
+        print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
     flush = make_flush(dev)
     if want("tail"):
         for (m, n, k) in ((4096, 4096, 4000), (4000, 4000, 4000)):
             r, _ = bench_bf16(tx, dev, m, n, k, args.steps, args.warmup, seed=2)
             secondary.append(r)
             print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
-    if want("w8a8"):
-        for m in (1, 16, 64, 256):
+    w8a8_ms = [m for m in (1, 16, 64, 256) if want("w8a8") or want(f"w8a8_{m}")]
+    if w8a8_ms:
+        for m in w8a8_ms:
             r = bench_w8a8(tx, dev, m, 8192, 8192, max(args.steps, 20), 3, flush)
             secondary.append(r)
             print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us, {r['gbps']:.0f} GB/s "
@@ -261,10 +313,10 @@ def main():
         "data": "synthetic (torch.randn / sqrt(K), seed 1, rounded to bf16)",
         "config": {"workload": "bf16 dense dot C=A@B, M=N=K=4096, row-major A[M,K], B[K,N], "
                                "fp32 accumulate, bf16 out (BASELINE configs[1])",
-                   "tile": head["plan"]["tile"], "kernel": "gemm_16bit_mfma32x32x16"},
+                   "tile": head["plan"]["tile"], "kernel": "gemm16_w4_kernel<bf16, 8 waves of 128x64>"},
         "roofline": {"bound": "mfma", "achieved": round(flops / head["ms"] / 1e9, 2),
                      "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(head["frac"], 4),
-                     "traffic": None},
+                     "traffic": TRAFFIC_BF16_4096},
         "cpu_baseline": cpu if cpu is None else {k: v for k, v in cpu.items() if k != "seconds"},
         "parity_vs_oracle": parity,
         "secondary": secondary,

@@ -23,6 +23,8 @@
 
 #include "decode_i8.h"
 #include "gemm16_dma.h"
+#include "gemm16_pp.h"
+#include "gemm16_w4.h"
 #include "gemm_tile.h"
 
 using namespace txk;
@@ -61,7 +63,10 @@ struct GemmConfig {
   int op, bm, bn, bk, wm, wn, epi;
   GemmKernelFn fn;
   int lds_bytes; // dynamic LDS (0 for kernels with static LDS)
-  int dma;       // 1: direct-to-LDS staging + transpose reads (gemm16_dma.h)
+  int dma;       // 1: direct-to-LDS staging + transpose reads (gemm16_dma.h),
+                 // 2: the same staging with 4 waves of 128x128 (gemm16_w4.h),
+                 // 3: 8 waves of 128x64 (gemm16_w4.h), 4: 8-wave ping-pong
+                 // (gemm16_pp.h)
 };
 
 #define TX_GEMM(OP, BM, BN, BK, WM, WN, EPI)                                   \
@@ -77,9 +82,28 @@ struct GemmConfig {
 #define TX_GEMM_DMA(OP, BM, BN, BK, WM, WN, EPI)                               \
   TX_GEMM_DMA_S(OP, BM, BN, BK, WM, WN, 2, EPI)
 
-// Lookup takes the first match, so a DMA variant listed before a
-// register-staged one of the same tile wins (TX_GEMM16_IMPL=regs skips DMA).
+#define TX_GEMM_W4(OP, EPI)                                                    \
+  GemmConfig { OP, 256, 256, 64, 2, 2, EPI, gemm16_w4_kernel<OP, EPI, 4>, 0, 2 }
+#define TX_GEMM_W8(OP, EPI)                                                    \
+  GemmConfig { OP, 256, 256, 64, 2, 4, EPI, gemm16_w4_kernel<OP, EPI, 8>, 0, 3 }
+#define TX_GEMM_PP(OP, EPI)                                                    \
+  GemmConfig { OP, 256, 256, 64, 2, 4, EPI, gemm16_pp_kernel<OP, EPI>, 0, 4 }
+
+// Lookup takes the first match, so the 4-wave 256x256 tile wins over the
+// 8-wave one (TX_GEMM16_IMPL=dma8 skips it) and both over register staging
+// (TX_GEMM16_IMPL=regs skips every direct-to-LDS variant).
 const GemmConfig kGemmConfigs[] = {
+    // bf16 / fp16 operands, 256x256 tiles: the tuning override selects among
+    // the 4-wave, 8-wave and ping-pong variants (first match wins)
+    TX_GEMM_W8(OP_BF16, EPI_BF16),
+    TX_GEMM_W8(OP_BF16, EPI_F32),
+    TX_GEMM_W8(OP_F16, EPI_F32),
+    TX_GEMM_W8(OP_F16, EPI_F16),
+    TX_GEMM_W4(OP_BF16, EPI_BF16),
+    TX_GEMM_W4(OP_BF16, EPI_F32),
+    TX_GEMM_W4(OP_F16, EPI_F32),
+    TX_GEMM_W4(OP_F16, EPI_F16),
+    TX_GEMM_PP(OP_BF16, EPI_BF16),
     // bf16 / fp16 operands: direct-to-LDS staging, 8 waves (4x2) per 256x256
     TX_GEMM_DMA(OP_BF16, 256, 256, 64, 4, 2, EPI_BF16),
     TX_GEMM_DMA(OP_BF16, 256, 256, 64, 4, 2, EPI_F32),
@@ -162,13 +186,28 @@ void classify(const tx_dot_desc &d, int *op, int *epi) {
 }
 
 int findGemmConfig(int op, int epi, int bm, int bn, int bk) {
-  static const bool no_dma = [] {
+  // Tuning override TX_GEMM16_IMPL: "regs" (register staging), "dma8"
+  // (8-wave direct-to-LDS), "w4" (4 waves of 128x128), "pp" (ping-pong);
+  // default: 8 waves of 128x64 (fastest of these at 4096^3 on MI355X).
+  static const int want = [] {
     const char *e = std::getenv("TX_GEMM16_IMPL");
-    return e && std::strcmp(e, "regs") == 0;
+    if (!e)
+      return 3;
+    if (std::strcmp(e, "w4") == 0)
+      return 2;
+    if (std::strcmp(e, "regs") == 0)
+      return 0;
+    if (std::strcmp(e, "dma8") == 0)
+      return 1;
+    if (std::strcmp(e, "w8") == 0)
+      return 3;
+    if (std::strcmp(e, "pp") == 0)
+      return 4;
+    return 3;
   }();
   for (int i = 0; i < kNumGemmConfigs; ++i) {
     const GemmConfig &c = kGemmConfigs[i];
-    if (no_dma && c.dma)
+    if (c.dma > want || (c.dma >= 2 && c.dma != want))
       continue;
     if (c.op == op && c.epi == epi && c.bm == bm && c.bn == bn && c.bk == bk)
       return i;
@@ -270,8 +309,8 @@ int validate(const tx_dot_desc *in, tx_dot_desc *d) {
   if (d->ldc == 0) d->ldc = d->N;
   if (d->lda < d->K || d->ldb < d->N || d->ldc < d->N)
     return fail(TX_ERR_INVALID, "row stride shorter than the row");
-  if ((d->lda * sa) % 16 || (d->ldb * sb) % 16)
-    return fail(TX_ERR_INVALID, "A/B row strides must be multiples of 16 bytes");
+  if ((d->lda * sa) % 16 || (d->ldb * sb) % 16 || (d->ldc * sc) % 16)
+    return fail(TX_ERR_INVALID, "A/B/C row strides must be multiples of 16 bytes");
   if ((d->K * sa) % 16 || (d->N * sb) % 16)
     return fail(TX_ERR_UNSUPPORTED,
                 "K and N must be multiples of %d elements (16-byte chunks)",
@@ -466,8 +505,9 @@ extern "C" TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A,
     return TX_OK; // empty output
   if (!C || (d.K > 0 && (!A || !B)))
     return fail(TX_ERR_INVALID, "NULL operand pointer");
-  if ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15)
-    return fail(TX_ERR_INVALID, "A and B must be 16-byte aligned");
+  if ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) |
+       reinterpret_cast<uintptr_t>(C)) & 15)
+    return fail(TX_ERR_INVALID, "A, B and C must be 16-byte aligned");
   if (d.scale_mode != TX_SCALE_NONE && (!scale_a || !scale_b))
     return fail(TX_ERR_INVALID, "scaled dot needs scale_a and scale_b");
   if (!tx_device_available())

@@ -74,10 +74,7 @@ __device__ __forceinline__ i32x4_t mfma_i8_16(const i32x4_t &a, const i32x4_t &b
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
 }
 
-// 32-bit LDS address of a __shared__ pointer.
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
+
 
 template <int MT> struct DecodeCfg {
   // Slots per wave: 4 waves x STAGES x (8 KiB of B + MT KiB of A) <= 160 KiB.

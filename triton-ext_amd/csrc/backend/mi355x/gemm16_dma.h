@@ -55,6 +55,19 @@ __device__ __forceinline__ void dma16_stream(const void *src, lds_void *dst) {
   __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 2);
 }
 
+// 32-bit LDS address of a __shared__ pointer.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// The direct-to-LDS load as an asm statement (M0 = LDS destination, through
+// an operand constraint so the compiler sets it).  The compiler does not see
+// it as a write to LDS, so it adds no s_waitcnt vmcnt of its own before LDS
+// reads: a caller using it must wait (vmcnt) before reading what it loads.
+__device__ __forceinline__ void dma16_asm(const void *src, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+}
+
 __device__ __forceinline__ u32x4 tr_read_pair(const uint8_t *lds, uint32_t off0,
                                               uint32_t off1) {
   const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
