@@ -221,6 +221,54 @@ def test_c5_fp8_block_scaled(gpu, M, N, K):
     say(f"fp8 {M}x{N}x{K} max|d|={err:.3g}")
 
 
+@pytest.mark.parametrize("kind,out", [("i8", "rowcol"), ("f8", "f32"), ("f8", "block_f32"),
+                                      ("f8", "block_bf16")])
+@pytest.mark.parametrize("M,N,K", [(512, 512, 1024), (300, 272, 400), (16, 1024, 256)])
+@pytest.mark.parametrize("blk", [(256, 256, 128), (128, 128, 128)])
+def test_8bit_tile_epilogues(gpu, kind, out, M, N, K, blk):
+    """Each epilogue of the 8-bit tile kernels, whole and edge tiles (M, N
+    not multiples of the tile; K not a multiple of 128: a masked last step).
+    Unscaled fp8 uses full-range e4m3 values (|q| up to 448), whose running
+    sums cancel to much smaller results."""
+    import torch
+    say(f"8-bit tile {kind}/{out} M={M} N={N} K={K} block={blk}")
+    if kind == "i8":
+        a = uniform_i8((M, K), 31)
+        b = uniform_i8((K, N), 32)
+        sa = uniform_scales(M, 33)
+        sb = uniform_scales(N, 34)
+        c = tx.dot(to_device(a, gpu), to_device(b, gpu), scale_a=to_device(sa, gpu),
+                   scale_b=to_device(sb, gpu), out_dtype=torch.bfloat16, block=blk)
+        torch.cuda.synchronize()
+        ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 64, 64),
+                               scale_mode=oracle.SCALE_ROWCOL, sa=sa, sb=sb,
+                               round_mode=oracle.ROUND_RNE)
+        assert np.array_equal(from_device(c), ref)
+        return
+    qa, qb, sa, sb = fp8_block_inputs(M, N, K, 35)
+    norm = math.sqrt(K)
+    if out == "f32":
+        c = tx.dot(to_device(qa, gpu), to_device(qb, gpu), out_dtype=torch.float32, block=blk)
+        ct, sm, kw = oracle.F32, oracle.SCALE_NONE, {}
+        # Unscaled codes: normalise by the operands' RMS as well as sqrt(K).
+        rms = lambda q: float(np.sqrt(np.mean(oracle.e4m3_to_f32(q).astype(np.float64) ** 2)))
+        norm *= rms(qa) * rms(qb)
+    else:
+        odt = torch.float32 if out == "block_f32" else torch.bfloat16
+        c = tx.dot(to_device(qa, gpu), to_device(qb, gpu), scale_a=to_device(sa, gpu),
+                   scale_b=to_device(sb, gpu), out_dtype=odt, block=blk)
+        ct = oracle.F32 if out == "block_f32" else oracle.BF16
+        sm, kw = oracle.SCALE_BLOCK128, dict(sa=sa, sb=sb)
+    torch.cuda.synchronize()
+    got = from_device(c)
+    ref = oracle.tiled_dot(qa, qb, a_type=oracle.F8E4M3, c_type=ct, block=(128, 128, 128),
+                           scale_mode=sm, **kw)
+    if ct == oracle.BF16:
+        got, ref = bits_to_f32(got, "bf16"), bits_to_f32(ref, "bf16")
+    err = check_close(got, ref, atol=ATOL, rtol=RTOL, scale=norm, what=f"fp8 {out}")
+    say(f"fp8 {out} {M}x{N}x{K} max|d|={err:.3g} (normalised {err / norm:.3g})")
+
+
 # ----------------------------------------------------------------------------- golden fixtures
 
 GOLDEN_TILE = {"f16": (64, 64, 32), "bf16": (128, 128, 64), "i8": (128, 128, 128),
@@ -238,10 +286,20 @@ def test_golden_fixture_on_gpu(gpu, name):
     oracle's bit for bit, and where the interpreter truncated to bf16, the
     GPU's fp32 accumulator truncated gives the fixture's bits.  Others: within
     the north_star tolerance of the fixture."""
+    golden_on_gpu(gpu, name, None)
+
+
+@pytest.mark.parametrize("name", ["int8_i32", "fp8_block128_f32_exact", "fp8_block128_bf16_normal"])
+def test_golden_fixture_256_tile(gpu, name):
+    """The 8-bit fixtures through the 256x256x128 tile kernel (8 waves)."""
+    golden_on_gpu(gpu, name, (256, 256, 128))
+
+
+def golden_on_gpu(gpu, name, tile):
     import os
     import torch
     from test_oracle_cpu import GOLDEN, OR_TYPE, fixture_output, load_fixture
-    say(f"golden {name}")
+    say(f"golden {name} tile={tile}")
     f = load_fixture(os.path.join(GOLDEN, name + ".npz"))
     at, ct = str(f["a_type"]), str(f["c_type"])
     tdt = {"f16": torch.float16, "bf16": torch.bfloat16, "i8": torch.int8,
@@ -257,6 +315,8 @@ def test_golden_fixture_on_gpu(gpu, name):
     blk = GOLDEN_TILE[at] if name != "c1_fp16_512" else (64, 64, 32)
     if name == "w8a8_rowcol_rtz":
         blk = (0, 0, 0)  # M = 5: the decode kernel
+    if tile is not None:
+        blk = tile
     c = tx.dot(da, db, out_dtype=odt, block=blk, **kw)
     c32 = tx.dot(da, db, out_dtype=torch.float32, block=blk, **kw) if ct == "bf16" and at != "i8" \
         else None
@@ -267,6 +327,26 @@ def test_golden_fixture_on_gpu(gpu, name):
     ref = oracle.tiled_dot(f["a"], f["b"], a_type=OR_TYPE[at], c_type=OR_TYPE[ct], block=oblk,
                            scale_mode=sm, sa=f.get("sa"), sb=f.get("sb"),
                            round_mode=oracle.ROUND_RNE)
+    if bool(f["exact"]) and at == "f8e4m3" and sm == oracle.SCALE_BLOCK128 and blk[0] == 256:
+        # The 256-wide fp8 tile applies a block's scales as one fma(part,
+        # sa*sb, acc) (two roundings) where the interpreter rounds
+        # part*sa, then *sb, then the sum (three): per K block, the two
+        # differ by at most 3 units in the last place of |part*sa*sb|, and
+        # the running sums by one more of the accumulator's.
+        fa = np.abs(oracle.e4m3_to_f32(f["a"]).astype(np.float64))
+        fb = np.abs(oracle.e4m3_to_f32(f["b"]).astype(np.float64))
+        K, N = fa.shape[1], fb.shape[1]
+        nkb = (K + 127) // 128
+        S = np.zeros((fa.shape[0], N))
+        for kb in range(nkb):
+            part = fa[:, kb * 128:(kb + 1) * 128] @ fb[kb * 128:(kb + 1) * 128]
+            S += part * f["sa"][:, kb:kb + 1] * np.repeat(f["sb"][kb], 128)[:N]
+        bound = (nkb + 4) * 2.0 ** -24 * S
+        d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+        assert (d <= bound).all(), f"{np.count_nonzero(d > bound)} beyond the rounding bound"
+        say(f"golden {name}: {np.count_nonzero(d)} of {d.size} differ, max d/bound "
+            f"{(d / np.maximum(bound, 1e-300)).max():.3g}")
+        return
     if bool(f["exact"]):
         assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} elements differ"
         if ct == "bf16" and c32 is not None:

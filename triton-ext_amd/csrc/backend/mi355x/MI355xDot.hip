@@ -24,6 +24,7 @@
 #include "decode_i8.h"
 #include "gemm16_dma.h"
 #include "gemm16_pp.h"
+#include "gemm8_w4.h"
 #include "gemm16_w4.h"
 #include "gemm_tile.h"
 
@@ -66,7 +67,7 @@ struct GemmConfig {
   int dma;       // 1: direct-to-LDS staging + transpose reads (gemm16_dma.h),
                  // 2: the same staging with 4 waves of 128x128 (gemm16_w4.h),
                  // 3: 8 waves of 128x64 (gemm16_w4.h), 4: 8-wave ping-pong
-                 // (gemm16_pp.h)
+                 // (gemm16_pp.h), 5: 8-bit 256x256x128 tile (gemm8_w4.h)
 };
 
 #define TX_GEMM(OP, BM, BN, BK, WM, WN, EPI)                                   \
@@ -88,6 +89,9 @@ struct GemmConfig {
   GemmConfig { OP, 256, 256, 64, 2, 4, EPI, gemm16_w4_kernel<OP, EPI, 8>, 0, 3 }
 #define TX_GEMM_PP(OP, EPI)                                                    \
   GemmConfig { OP, 256, 256, 64, 2, 4, EPI, gemm16_pp_kernel<OP, EPI>, 0, 4 }
+
+#define TX_GEMM_8(OP, EPI)                                                     \
+  GemmConfig { OP, 256, 256, 128, 2, 4, EPI, gemm8_w4_kernel<OP, EPI>, 0, 5 }
 
 // Lookup takes the first match, so the 4-wave 256x256 tile wins over the
 // 8-wave one (TX_GEMM16_IMPL=dma8 skips it) and both over register staging
@@ -126,6 +130,12 @@ const GemmConfig kGemmConfigs[] = {
     TX_GEMM(OP_F16, 128, 128, 64, 2, 2, EPI_F16),
     TX_GEMM(OP_F16, 64, 64, 32, 2, 2, EPI_F32),
     TX_GEMM(OP_F16, 64, 64, 32, 2, 2, EPI_F16),
+    // int8 / fp8 operands, 256x256x128 tiles of 8 waves (gemm8_w4.h)
+    TX_GEMM_8(OP_I8, EPI_I32),
+    TX_GEMM_8(OP_I8, EPI_ROWCOL_BF16),
+    TX_GEMM_8(OP_F8, EPI_BLOCK128_BF16),
+    TX_GEMM_8(OP_F8, EPI_BLOCK128_F32),
+    TX_GEMM_8(OP_F8, EPI_F32),
     // int8 operands, int32 accumulation
     TX_GEMM(OP_I8, 256, 256, 128, 2, 4, EPI_I32),
     TX_GEMM(OP_I8, 256, 256, 128, 2, 4, EPI_ROWCOL_BF16),
@@ -205,9 +215,15 @@ int findGemmConfig(int op, int epi, int bm, int bn, int bk) {
       return 4;
     return 3;
   }();
+  // TX_GEMM8_IMPL=tile: the register-staged 8-bit tiles instead of gemm8_w4.
+  static const bool old8 = [] {
+    const char *e = std::getenv("TX_GEMM8_IMPL");
+    return e && std::strcmp(e, "tile") == 0;
+  }();
+  const bool is8 = op == OP_I8 || op == OP_F8;
   for (int i = 0; i < kNumGemmConfigs; ++i) {
     const GemmConfig &c = kGemmConfigs[i];
-    if (c.dma > want || (c.dma >= 2 && c.dma != want))
+    if (is8 ? (c.dma == 5 && old8) : (c.dma > want || (c.dma >= 2 && c.dma != want)))
       continue;
     if (c.op == op && c.epi == epi && c.bm == bm && c.bn == bn && c.bk == bk)
       return i;

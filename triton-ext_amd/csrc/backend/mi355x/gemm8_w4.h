@@ -1,0 +1,381 @@
+// 8-bit operand (fp8 e4m3 / int8) 256x256x128 tile kernel for gfx950, eight
+// waves of 128x64 (two per SIMD): C[M,N] = epilogue(A[M,K] . B[K,N]), all
+// row-major.  A wave's 128 fp32/int32 accumulators stay in arch VGPRs, where
+// the per-step block-scale FMA can reach them.
+//
+// One K step is 128: one scale group of the fp8 block-scaled dot, and one
+// v_mfma_f32_16x16x128_f8f6f4 (or two v_mfma_i32_16x16x64_i8) per 16x16 block.
+// A lane's operand bytes for a block are K = 32 (l/16) .. +31 (32 bytes,
+// the same permutation of K for both operands; int8 splits them into two
+// 16-byte halves for its two MFMAs).
+//
+// Staging (per step, 64 KiB plus the step's scales) is gemm16_w4.h's scheme
+// for 8-bit elements: buffer loads into LDS with per-tile lane offsets, the K
+// step in the scalar soffset and out-of-range offsets returning zeros (rows
+// of A >= M, columns of B >= N, and A's columns >= K in masked steps; B's rows
+// >= K lie past the buffer); asm statements, so the compiler keeps no LDS read
+// behind them.  LDS stage layout:
+//   A [256 rows][128 B], 16-byte chunk c of row r at c ^ ((r >> 1) & 7):
+//     the 16 rows one ds_read_b128 touches land in 16 different bank groups;
+//   B [128 rows][256 B], chunk c of row k at c ^ (k & 7): the 8 rows one
+//     ds_read_b64_tr_b8 touches land in 8 different chunks.
+//   sa [256] fp32: sa[m0 + r][kt] (block-scaled only, 4-byte buffer loads);
+//   sb [64] fp32: sb[kt][n0/128 + 0..1] (block-scaled only).
+// B is N-contiguous; ds_read_b64_tr_b8 hands each lane 8 K-consecutive bytes
+// of one column (within a 16-lane group, lane i gets byte i%8 of the words
+// read by group lanes 2r + i/8), four reads give the 32 bytes of a block.
+//
+// Operand roles are swapped (MFMA A := B columns, MFMA B := A rows): the
+// MFMA result is C^T and lane l holds C row 16 i + l%16 at the 4 consecutive
+// columns 16 j + 4 (l/16) .. +3 of block (i, j).
+//
+// Block scales: per step, part = A_blk . B_blk (a fresh MFMA), then
+// acc = fma(part, sa[m][kb] * sb[kb][n/128], acc).  sb is one value per wave
+// (a wave's 128 columns lie in one 128-column block) and sa one per lane and
+// row block, so the scale costs one FMA per output element per step.  (The
+// reference kernel's order, acc + (part * sa) * sb, rounds three times; this
+// rounds twice: the results agree to a few ulp.)
+//
+// Pipeline: two LDS stages.  A wave holds the 4 B fragments of a step (32
+// VGPRs) and streams the A fragments one row block ahead.  When the last row
+// block's A fragment is in registers every wave is done with the stage: one
+// barrier, the loads of step k+2 go into it, and each B fragment is replaced
+// by the next step's as soon as the last row block's MFMA has used it.
+#pragma once
+
+#include "gemm16_w4.h"
+
+namespace txk {
+
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+template <int OP, int EPI> struct Gemm8W4 {
+  static constexpr int BM = 256, BN = 256, BK = 128, NW = 8, WN = 4;
+  static constexpr int WTM = 128, WTN = 64, FM = WTM / 16, FN = WTN / 16;
+  static constexpr bool SCALED = EPI == EPI_BLOCK128_BF16 || EPI == EPI_BLOCK128_F32;
+  static constexpr bool INT = OP == OP_I8;
+  static constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN; // 32 KiB each
+  static constexpr int SA_OFF = A_BYTES + B_BYTES, SB_OFF = SA_OFF + BM * 4;
+  static constexpr uint32_t STAGE = SB_OFF + 256;
+  static constexpr int A_DMA = A_BYTES / 1024 / NW, B_DMA = B_BYTES / 1024 / NW; // 4, 4
+  static constexpr uint32_t kOOB = 0x80000000u;
+  static_assert(OP == OP_I8 || OP == OP_F8, "8-bit operands");
+  static_assert(STAGE % 128 == 0, "stage offsets keep address bits 0-6");
+  static_assert(2 * STAGE <= 160 * 1024, "two stages in LDS");
+
+  typedef typename std::conditional<INT, i32x4_t, f32x4_t>::type Acc;
+
+  __device__ __forceinline__ static void buffer_lds4(uint32_t voff, const i32x4_t &rsrc,
+                                                     uint32_t soff, uint32_t lds) {
+    asm volatile("buffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff),
+                 "{m0}"(lds)
+                 : "memory");
+  }
+
+  // Loads of K step kt into the stage at LDS address st (see gemm16_w4.h).
+  // Lane offsets are recomputed here rather than kept live through the K
+  // loop (registers are the scarce resource of this tile).
+  template <bool MASK_MN, bool MASK_K>
+  __device__ __forceinline__ static void issue(const GemmArgs &p, int64_t m0, int64_t n0,
+                                               const i32x4_t &ra, const i32x4_t &rb,
+                                               const i32x4_t &rsa, const i32x4_t &rsb, int kt,
+                                               uint32_t st, int wave, bool live) {
+    const int lane = threadIdx.x & 63;
+    const int k0 = kt * BK;
+    const uint32_t sa_ = (uint32_t)k0;
+    const uint32_t sb_ = (uint32_t)((int64_t)k0 * p.ldb);
+    typedef Gemm16W4<OP_BF16, EPI_F32, 4> W;
+#pragma unroll
+    for (int i = 0; i < A_DMA; ++i) {
+      const int j = wave * A_DMA + i;        // 1 KiB block: 8 rows of 128 B
+      const int row = 8 * j + (lane >> 3), pc = lane & 7;
+      const int c = pc ^ ((row >> 1) & 7);
+      const bool ok = live && (!MASK_MN || m0 + row < p.M) && (!MASK_K || k0 + 16 * c < p.K);
+      const uint32_t v = ok ? (uint32_t)(m0 + row) * (uint32_t)p.lda + 16u * c : kOOB;
+      W::buffer_lds16(v, ra, sa_, st + j * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < B_DMA; ++i) {
+      const int j = wave * B_DMA + i;        // 1 KiB block: 4 rows of 256 B
+      const int k = 4 * j + (lane >> 4), pc = lane & 15;
+      const int c = pc ^ (k & 7);
+      const bool ok = live && (!MASK_MN || n0 + 16 * c < p.N);
+      const uint32_t v = ok ? (uint32_t)k * (uint32_t)p.ldb + (uint32_t)n0 + 16u * c : kOOB;
+      W::buffer_lds16(v, rb, sb_, st + A_BYTES + j * 1024);
+    }
+    if (SCALED) {
+      if (wave < 4) { // 4 x 64 rows: sa[m0 + row][kt]
+        const int64_t gm = m0 + 64 * wave + lane;
+        const uint32_t v = (live && gm < p.M) ? (uint32_t)gm * (uint32_t)(p.sa_ld * 4) : kOOB;
+        buffer_lds4(v, rsa, (uint32_t)kt * 4, st + SA_OFF + wave * 256);
+      }
+      if (wave == 0) { // sb[kt][n0/128 + lane], lanes 0 and 1
+        const int64_t nb = (n0 >> 7) + lane;
+        const uint32_t v = (live && lane < 2 && nb < p.sb_ld) ? (uint32_t)nb * 4u : kOOB;
+        buffer_lds4(v, rsb, (uint32_t)(kt * p.sb_ld * 4), st + SB_OFF);
+      }
+    }
+  }
+
+  // Per-lane LDS addresses (stage 0) of the wave's fragments (wave at row
+  // block wm of 128 rows, column block wn of 64 columns), one register each:
+  //  * A, row block i: row wm*128 + 16 i + l%16, chunk 2 (l/16) after the
+  //    swizzle.  The swizzle term (row >> 1) & 7 = (l%16) >> 1 is the same for
+  //    every i, so block i is a + 2048 i; the lane's second chunk is ^ 16.
+  //  * B, column block j: row 32 (l/16) + (l%16)/2, chunk 4 wn + j after the
+  //    swizzle (c ^ (row & 7)); j only flips chunk bits 0-1, so block j is
+  //    b ^ (16 j).  The four transposed reads are +0, +2048, +4096, +6144.
+  struct Bases {
+    uint32_t a, b;
+  };
+  __device__ __forceinline__ static void bases(uint32_t lds0, int wm, int wn, Bases &bs) {
+    const int lane = threadIdx.x & 63;
+    const int G = lane >> 4, L = lane & 15;
+    const int row = wm * WTM + L;
+    bs.a = lds0 + row * BK + (((2 * G) ^ ((row >> 1) & 7)) << 4);
+    const int k = 32 * G + (L >> 1);
+    bs.b = lds0 + A_BYTES + k * BN + (((4 * wn) ^ (k & 7)) << 4) + 8 * (L & 1);
+  }
+
+  __device__ __forceinline__ static i32x8_t read_a(const Bases &bs, uint32_t so, int i) {
+    typedef __attribute__((address_space(3))) i32x4_t lds_i32x4;
+    const uint32_t a0 = bs.a + so + 2048 * i;
+    const i32x4_t lo = *(const lds_i32x4 *)(uintptr_t)a0;
+    const i32x4_t hi = *(const lds_i32x4 *)(uintptr_t)(a0 ^ 16u);
+    i32x8_t r;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      r[t] = lo[t];
+      r[4 + t] = hi[t];
+    }
+    return r;
+  }
+
+  __device__ __forceinline__ static i32x8_t read_b(const Bases &bs, uint32_t so, int j) {
+    typedef int v2i __attribute__((ext_vector_type(2)));
+    typedef __attribute__((address_space(3))) v2i lds_v2i_t;
+    const uint32_t b0 = (bs.b ^ (16u * j)) + so;
+    i32x8_t r;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t *)(uintptr_t)(b0 + q * 8 * BN));
+      r[2 * q] = v.x;
+      r[2 * q + 1] = v.y;
+    }
+    return r;
+  }
+
+  __device__ __forceinline__ static Acc mma(const i32x8_t &bcol, const i32x8_t &arow, Acc c) {
+    if constexpr (INT) {
+      i32x4_t b0, b1, a0, a1;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        b0[t] = bcol[t], b1[t] = bcol[4 + t], a0[t] = arow[t], a1[t] = arow[4 + t];
+      }
+      c = __builtin_amdgcn_mfma_i32_16x16x64_i8(b0, a0, c, 0, 0, 0);
+      return __builtin_amdgcn_mfma_i32_16x16x64_i8(b1, a1, c, 0, 0, 0);
+    } else {
+      // format 0 for both operands: fp8 e4m3; no hardware block scales.
+      return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bcol, arow, c, 0, 0, 0, 0, 0, 0);
+    }
+  }
+
+  // Ties a value to this point of the program: the compiler otherwise sinks
+  // the scale FMAs (pure arithmetic) to the end of the step, where every row
+  // block's partial products would be live at once.
+  __device__ __forceinline__ static void pin(Acc &v) { asm volatile("" : "+v"(v)); }
+
+  // Row block i of one step: its 4 MFMAs (and, block-scaled, its FMAs).
+  __device__ __forceinline__ static void row_block(const i32x8_t &a, const i32x8_t (&b)[FN],
+                                                   float s, Acc (&acc)[FN]) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      if constexpr (SCALED) {
+        const Acc part = mma(b[j], a, Acc{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[j][r] = __builtin_fmaf(part[r], s, acc[j][r]);
+        pin(acc[j]);
+      } else {
+        acc[j] = mma(b[j], a, acc[j]);
+      }
+    }
+  }
+
+  template <bool MASK_MN>
+  __device__ __forceinline__ static void run(const GemmArgs &p, int64_t m0, int64_t n0,
+                                             uint8_t *smem) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    Acc acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[i][j][r] = 0;
+
+    const int nmain = p.k_main_steps;
+    const int total = nmain + p.k_masked_steps;
+    const uint32_t lds0 = lds_addr(smem);
+    const i32x4_t ra = make_rsrc(p.A, (uint32_t)((p.M - 1) * p.lda + p.K));
+    const i32x4_t rb = make_rsrc(p.B, (uint32_t)((p.K - 1) * p.ldb + p.N));
+    i32x4_t rsa = {0, 0, 0, 0}, rsb = {0, 0, 0, 0};
+    if (SCALED) {
+      rsa = make_rsrc(p.sa, (uint32_t)(p.M * p.sa_ld * 4));
+      rsb = make_rsrc(p.sb, (uint32_t)(((p.K + 127) / 128) * p.sb_ld * 4));
+    }
+    Bases bs;
+    bases(lds0, wm, wn, bs);
+    auto issue_step = [&](int kt, bool live) {
+      const uint32_t st = lds0 + (kt & 1) * STAGE;
+      if (kt >= nmain)
+        issue<MASK_MN, true>(p, m0, n0, ra, rb, rsa, rsb, kt, st, wave, live);
+      else
+        issue<MASK_MN, false>(p, m0, n0, ra, rb, rsa, rsb, kt, st, wave, live);
+    };
+    auto step_barrier = [] {
+      __builtin_amdgcn_s_waitcnt(0x7 << 4); // vmcnt 0, expcnt 7, lgkmcnt 0
+      __syncthreads();
+    };
+    // Scale of row block i for the step in stage `so`: sa[row][kt] * sb[kt][nb]
+    // (sb: the 128-column block holding this wave's 64 columns).
+    typedef __attribute__((address_space(3))) float lds_f32;
+    auto scale = [&](uint32_t so, int i) {
+      if constexpr (SCALED) {
+        const float sbv = *(const lds_f32 *)(uintptr_t)(lds0 + so + SB_OFF + 4 * (wn >> 1));
+        return *(const lds_f32 *)(uintptr_t)(lds0 + so + SA_OFF +
+                                             4 * (wm * WTM + 16 * i + (lane & 15))) * sbv;
+      } else {
+        return 1.f;
+      }
+    };
+
+    if (total > 0) {
+      issue_step(0, true);
+      step_barrier();
+      if (total > 1)
+        issue_step(1, true);
+      i32x8_t b[FN];
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        b[j] = read_b(bs, 0, j);
+      float s0 = scale(0, 0);
+      i32x8_t a0;
+      // Row blocks 0 .. FM-2 of the step in stage so, with the A fragment
+      // (and scale) of the next row block read one block ahead; leaves a0/s0
+      // holding the last row block's.
+      auto first_rows = [&](uint32_t so) {
+        a0 = read_a(bs, so, 0);
+#pragma unroll
+        for (int i = 0; i < FM - 1; ++i) {
+          const i32x8_t a1 = read_a(bs, so, i + 1);
+          const float s1 = scale(so, i + 1);
+          row_block(a0, b, s0, acc[i]);
+          a0 = a1;
+          s0 = s1;
+          // Keep the prefetch one row block ahead and each block's FMAs
+          // beside its MFMAs: nothing moves across.
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      // Every step but the last: straight-line, no exit from the middle (a
+      // branch there lets the compiler sink the scale FMAs past it, holding
+      // every row block's partial products at once).
+      for (int kt = 0; kt + 1 < total; ++kt) {
+        const uint32_t so = (kt & 1) * STAGE, sn = ((kt + 1) & 1) * STAGE;
+        first_rows(so);
+        // Every read of this stage is issued; once they have returned, free it.
+        step_barrier();
+        issue_step(kt + 2, kt + 2 < total);
+        // The last row block; each B fragment is replaced by the next step's
+        // right after its last use here.
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          if constexpr (SCALED) {
+            const Acc part = mma(b[j], a0, Acc{0.f, 0.f, 0.f, 0.f});
+            b[j] = read_b(bs, sn, j);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[FM - 1][j][r] = __builtin_fmaf(part[r], s0, acc[FM - 1][j][r]);
+            pin(acc[FM - 1][j]);
+          } else {
+            acc[FM - 1][j] = mma(b[j], a0, acc[FM - 1][j]);
+            b[j] = read_b(bs, sn, j);
+          }
+        }
+        s0 = scale(sn, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      first_rows(((total - 1) & 1) * STAGE);
+      row_block(a0, b, s0, acc[FM - 1]);
+    }
+    epilogue<MASK_MN>(p, m0, n0, wm, wn, acc);
+  }
+
+  // Lane l holds, per block (i, j), C[row][col .. col+3] with
+  // row = m0 + wm*128 + 16 i + l%16 and col = n0 + wn*64 + 16 j + 4 (l/16).
+  template <bool MASK_MN>
+  __device__ __forceinline__ static void epilogue(const GemmArgs &p, int64_t m0, int64_t n0,
+                                                  int wm, int wn, const Acc (&acc)[FM][FN]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int64_t row = m0 + wm * WTM + 16 * i + (lane & 15);
+      if (MASK_MN && row >= p.M)
+        continue;
+      float sar = 1.f;
+      if (EPI == EPI_ROWCOL_BF16)
+        sar = p.sa[row];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int64_t col = n0 + wn * WTN + 16 * j + 4 * (lane >> 4);
+        if (MASK_MN && col >= p.N) // N % 16 == 0: the quad is all in or all out
+          continue;
+        const int64_t off = row * p.ldc + col;
+        const Acc &v = acc[i][j];
+        if (EPI == EPI_I32) {
+          *reinterpret_cast<i32x4_t *>(reinterpret_cast<int32_t *>(p.C) + off) = v;
+        } else if (EPI == EPI_F32 || EPI == EPI_BLOCK128_F32) {
+          *reinterpret_cast<f32x4_t *>(reinterpret_cast<float *>(p.C) + off) = v;
+        } else {
+          float f[4];
+          if (EPI == EPI_ROWCOL_BF16) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              // (float(acc) * sa[m]) * sb[n], each product rounded (the
+              // scale vectors need only 4-byte alignment)
+#pragma clang fp contract(off)
+              f[r] = ((float)v[r] * sar) * p.sb[col + r];
+            }
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              f[r] = (float)v[r];
+          }
+          uint2 w;
+          w.x = (uint32_t)f32_to_bf16_rne(f[0]) | ((uint32_t)f32_to_bf16_rne(f[1]) << 16);
+          w.y = (uint32_t)f32_to_bf16_rne(f[2]) | ((uint32_t)f32_to_bf16_rne(f[3]) << 16);
+          *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.C) + off) = w;
+        }
+      }
+    }
+  }
+};
+
+template <int OP, int EPI>
+__global__ void __launch_bounds__(512, 1) gemm8_w4_kernel(GemmArgs p) {
+  typedef Gemm8W4<OP, EPI> G;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * G::STAGE];
+  int tm, tn;
+  tile_coords(p, tm, tn);
+  const int64_t m0 = (int64_t)tm * G::BM, n0 = (int64_t)tn * G::BN;
+  if (m0 + G::BM <= p.M && n0 + G::BN <= p.N)
+    G::template run<false>(p, m0, n0, smem);
+  else
+    G::template run<true>(p, m0, n0, smem);
+}
+
+} // namespace txk

@@ -119,7 +119,7 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
     else if (d->a_type == TX_I8 && d->M <= 64)
       t = Tile{(int32_t)(16 * cdiv(d->M > 0 ? d->M : 1, 16)), 256, 64, 1.0};
     else if (d->a_type == TX_F8E4M3)
-      t = kTiles8[1]; // block-scaled fp8 keeps a second accumulator set: 128x128
+      t = kTiles8[0];
     else
       t = chooseTile(kTiles8, d->M, d->N, d->K);
   }
