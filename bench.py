@@ -313,7 +313,7 @@ def main():
         "data": "synthetic (torch.randn / sqrt(K), seed 1, rounded to bf16)",
         "config": {"workload": "bf16 dense dot C=A@B, M=N=K=4096, row-major A[M,K], B[K,N], "
                                "fp32 accumulate, bf16 out (BASELINE configs[1])",
-                   "tile": head["plan"]["tile"], "kernel": "gemm16_w4_kernel<bf16, 8 waves of 128x64>"},
+                   "tile": head["plan"]["tile"], "kernel": "gemm16_w4_kernel<bf16, 4 waves of 128x128>"},
         "roofline": {"bound": "mfma", "achieved": round(flops / head["ms"] / 1e9, 2),
                      "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(head["frac"], 4),
                      "traffic": TRAFFIC_BF16_4096},

@@ -93,9 +93,9 @@ struct GemmConfig {
 #define TX_GEMM_8(OP, EPI)                                                     \
   GemmConfig { OP, 256, 256, 128, 2, 4, EPI, gemm8_w4_kernel<OP, EPI>, 0, 5 }
 
-// Lookup takes the first match, so the 4-wave 256x256 tile wins over the
-// 8-wave one (TX_GEMM16_IMPL=dma8 skips it) and both over register staging
-// (TX_GEMM16_IMPL=regs skips every direct-to-LDS variant).
+// Lookup takes the first match among the entries the tuning override
+// allows (findGemmConfig): by default the 4-wave 256x256 tile, then the
+// direct-to-LDS and register-staged tiles of other shapes.
 const GemmConfig kGemmConfigs[] = {
     // bf16 / fp16 operands, 256x256 tiles: the tuning override selects among
     // the 4-wave, 8-wave and ping-pong variants (first match wins)
@@ -197,12 +197,12 @@ void classify(const tx_dot_desc &d, int *op, int *epi) {
 
 int findGemmConfig(int op, int epi, int bm, int bn, int bk) {
   // Tuning override TX_GEMM16_IMPL: "regs" (register staging), "dma8"
-  // (8-wave direct-to-LDS), "w4" (4 waves of 128x128), "pp" (ping-pong);
-  // default: 8 waves of 128x64 (fastest of these at 4096^3 on MI355X).
+  // (8-wave direct-to-LDS), "w8" (8 waves of 128x64), "pp" (ping-pong);
+  // default: 4 waves of 128x128 (fastest of these at 4096^3 on MI355X).
   static const int want = [] {
     const char *e = std::getenv("TX_GEMM16_IMPL");
     if (!e)
-      return 3;
+      return 2;
     if (std::strcmp(e, "w4") == 0)
       return 2;
     if (std::strcmp(e, "regs") == 0)
@@ -213,7 +213,7 @@ int findGemmConfig(int op, int epi, int bm, int bn, int bk) {
       return 3;
     if (std::strcmp(e, "pp") == 0)
       return 4;
-    return 3;
+    return 2;
   }();
   // TX_GEMM8_IMPL=tile: the register-staged 8-bit tiles instead of gemm8_w4.
   static const bool old8 = [] {

@@ -1,25 +1,20 @@
-// bf16/fp16 256x256x64 tile kernel for gfx950, four waves of 128x128:
-// C[M,N] = epilogue(A[M,K] . B[K,N]), all row-major.
+// bf16/fp16 256x256x64 tile kernel for gfx950: C[M,N] = epilogue(A[M,K] .
+// B[K,N]), all row-major.  NW = 4: four waves of 128x128 (the default);
+// NW = 8: eight waves of 128x64.
 //
-// Why four waves.  On gfx950 LDS reads are bounded by instruction issue (about
-// one wave-wide read per 4-5 clocks per CU: ds_read_b128 moves 1 KiB,
-// ds_read_b64_tr_b16 512 B), and every MFMA operand of this tile passes through
-// LDS.  A wave tile of 128x128 (4x4 blocks of 32x32) reuses each A and B
-// fragment four times: 12 LDS reads per 16 MFMAs, 192 reads per CU per K step
-// against 2048 MFMA clocks per SIMD, where eight 64x128 waves need 320.  The
-// 256 fp32 accumulators of a wave live in AGPRs; one wave per SIMD.
+// Why four waves.  The K loop is power-limited, not issue-limited: with
+// LDS reads removed the same loop runs at a clock about 15% higher.  A
+// 128x128 wave tile (4x4 blocks of 32x32) reuses each A and B fragment four
+// times, 512 LDS bytes per MFMA against 768 for 128x64, and its 256 fp32
+// accumulators live in AGPRs, one wave per SIMD.
 //
-// Staging is gemm16_dma.h's: direct-to-LDS loads (no VGPR staging) into
-// swizzled A [256][64] and B [64][256] tiles, two stages in separate
-// __shared__ arrays.  B (N-contiguous) reaches the MFMA through
-// ds_read_b64_tr_b16.
+// Staging is gemm16_dma.h's layout: direct-to-LDS buffer loads (no VGPR
+// staging) into swizzled A [256][64] and B [64][256] tiles, two stages.
+// B (N-contiguous) reaches the MFMA through ds_read_b64_tr_b16.
 //
-// Pipeline.  One wave works through the 4 sub-steps (16 of K) of a step:
-// while the 16 MFMAs of sub-step s run, the 12 LDS reads of sub-step s+1 are
-// in flight.  At the start of the last sub-step every wave has its fragments
-// in registers, so a single barrier per step (after s_waitcnt vmcnt(0), which
-// also proves the next stage has landed) frees the stage just read; the loads
-// of step k+2 then go into it while the MFMAs of step k and k+1 run.
+// Pipeline: see run().  Each sub-step (16 of K) issues its MFMAs in a fixed
+// order with the next sub-step's fragment reads and a share of the staging
+// loads between them; one barrier per step frees the stage just read.
 //
 // Operand roles are swapped (MFMA A := B columns, MFMA B := A rows), so the
 // MFMA result is C^T and lane l holds row m = l % 32 of a 32x32 block at
@@ -178,14 +173,6 @@ template <int OP, int EPI, int NW = 4> struct Gemm16W4 {
                                                  Offsets &o) {
     offsets_q<MASK_MN>(p, m0, n0, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), o);
   }
-  template <bool MASK_K>
-  __device__ __forceinline__ static void issue(const GemmArgs &p, const Offsets &o,
-                                               const i32x4_t &ra, const i32x4_t &rb, int kt,
-                                               uint32_t st, bool live = true) {
-    issue_q<MASK_K>(p, o, ra, rb, kt, st, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
-                    live);
-  }
-
   __device__ __forceinline__ static f32x16_t mma(const i16x8_t &bcol, const u32x4 &arow,
                                                  f32x16_t acc) {
     if constexpr (OP == OP_BF16)
@@ -206,17 +193,74 @@ template <int OP, int EPI, int NW = 4> struct Gemm16W4 {
         acc[i][j] = mma(f.b[j], f.a[i], acc[i][j]);
   }
 
-  // Scheduling hint for one sub-step: its MPS MFMAs with the RPS LDS reads
-  // of the next sub-step spread between them.
-  __device__ __forceinline__ static void interleave_reads() {
-#pragma unroll
-    for (int i = 0; i < MPS; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
-      if (i < RPS)
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
+  // One fragment read of sub-step ks: unit u < FM is A fragment u (one
+  // ds_read_b128), unit FM + j is B fragment j (two transposed reads).
+  __device__ __forceinline__ static void read_unit(const uint8_t *as, const uint8_t *bs, int ks,
+                                                   int wm, int wn, int u, Frags &f) {
+    const int lane = threadIdx.x & 63;
+    const int G = lane >> 4, L = lane & 15;
+    if (u < FM) {
+      const int row = wm * WTM + u * 32 + (lane & 31);
+      const int c = ks * 2 + (lane >> 5);
+      f.a[u] = *reinterpret_cast<const u32x4 *>(as + row * RA +
+                                                ((c ^ ((row ^ (row >> 3)) & (NCA - 1))) << 4));
+    } else {
+      const int j = u - FM;
+      const int n = wn * WTN + j * 32 + 16 * (G & 1) + 4 * (L & 3);
+      const int k = ks * 16 + 8 * (G >> 1) + (L >> 2), k4 = k + 4;
+      const uint32_t off0 = k * RBB + (((n >> 3) ^ (4 * (k & 3))) << 4) + (n & 7) * 2;
+      const uint32_t off1 = k4 * RBB + (((n >> 3) ^ (4 * (k4 & 3))) << 4) + (n & 7) * 2;
+      const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_i16x4 *)((__attribute__((address_space(3))) uint8_t *)bs + off0));
+      const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_i16x4 *)((__attribute__((address_space(3))) uint8_t *)bs + off1));
+      f.b[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     }
   }
 
+  // Staging loads per wave and step, issued in PARTS groups of PER spread
+  // over the step (see run()).
+  static constexpr int NDMA = Stage::A_DMA + Stage::B_DMA;
+  static constexpr int PARTS = NW == 4 ? 3 : 2;
+  static constexpr int PER = (NDMA + PARTS - 1) / PARTS;
+  static constexpr int NU = FM + FN; // read units per sub-step
+  static_assert(NU <= MPS && PER <= MPS, "one read unit and one load per MFMA at most");
+
+  // Load `idx` (0..NDMA-1) of this wave's share of step kt, into stage st.
+  template <bool MASK_K>
+  __device__ __forceinline__ static void issue_one(const GemmArgs &p, const Offsets &o,
+                                                   const i32x4_t &ra, const i32x4_t &rb, int kt,
+                                                   uint32_t st, int wave, bool live, int idx) {
+    const int k0 = kt * BK;
+    if (idx < Stage::A_DMA) {
+      uint32_t v = o.a[idx];
+      if (MASK_K && (!live || k0 + o.ak[idx] >= p.K))
+        v = kOOB;
+      buffer_lds16(v, ra, (uint32_t)k0 * 2u, st + (wave * Stage::A_DMA + idx) * 1024);
+    } else {
+      const int q = idx - Stage::A_DMA;
+      uint32_t v = o.b[q];
+      if (MASK_K && !live)
+        v = kOOB;
+      buffer_lds16(v, rb, (uint32_t)((int64_t)k0 * p.ldb * 2),
+                   st + A_BYTES + (wave * Stage::B_DMA + q) * 1024);
+    }
+  }
+
+  // Pipeline (two LDS stages; step kt in stage kt % 2).  A step's 4
+  // sub-steps each issue their MFMAs one at a time in a fixed order: after
+  // MFMA u (u < NU) read unit u of the next sub-step's fragments; after the
+  // last PER MFMAs, one staging load each.  The loads of step kt + 2 are
+  // spread over sub-step 3 of step kt and sub-steps 0 (and, four waves, 1)
+  // of step kt + 1, rather than issued in one burst: the CU's load path
+  // takes a burst of 64 KiB far slower than the MFMAs take to hide it.
+  //   sub-step 0: MFMAs ks0, read ks1, loads part 1 of step kt + 1
+  //   sub-step 1: MFMAs ks1, read ks2, loads part 2 of step kt + 1 (PARTS 3)
+  //   sub-step 2: MFMAs ks2, read ks3
+  //   barrier: s_waitcnt vmcnt(0) lgkmcnt(0) (step kt + 1 has landed, every
+  //            fragment of step kt is in registers), s_barrier (so for every
+  //            wave): stage kt % 2 is free
+  //   sub-step 3: MFMAs ks3, read ks0 of step kt + 1, loads part 0 of kt + 2
   template <bool MASK_MN>
   __device__ __forceinline__ static void run(const GemmArgs &p, int64_t m0, int64_t n0,
                                              uint8_t *smem) {
@@ -236,61 +280,66 @@ template <int OP, int EPI, int NW = 4> struct Gemm16W4 {
     const uint32_t lds0 = lds_addr(smem);
     constexpr uint32_t STAGE = A_BYTES + B_BYTES;
     auto stage_ptr = [&](int kt) { return smem + (kt & 1) * STAGE; };
+    auto stage_addr = [&](int kt) { return lds0 + (kt & 1) * STAGE; };
     const i32x4_t ra = make_rsrc(p.A, (uint32_t)(((p.M - 1) * p.lda + p.K) * 2));
     const i32x4_t rb = make_rsrc(p.B, (uint32_t)(((p.K - 1) * p.ldb + p.N) * 2));
     Offsets o;
     offsets<MASK_MN>(p, m0, n0, o);
-    // s_waitcnt vmcnt(0) lgkmcnt(0), then the workgroup barrier (with its
-    // fences, so no LDS access moves across it).
     auto step_barrier = [] {
       __builtin_amdgcn_s_waitcnt(0x7 << 4); // vmcnt 0, expcnt 7, lgkmcnt 0
       __syncthreads();
     };
+    // Loads [d0, d0 + n) of step kt (masked: the step may lie past K).
+    auto issue_range = [&](int kt, int d0, int n, auto mask_k) {
+      constexpr bool MASK_K = decltype(mask_k)::value;
+#pragma unroll
+      for (int d = 0; d < n; ++d)
+        if (d0 + d < NDMA)
+          issue_one<MASK_K>(p, o, ra, rb, kt, stage_addr(kt), wave, kt < total, d0 + d);
+    };
+    // One sub-step: the MFMAs of fc; read units of sub-step rks of stage
+    // (ras, rbs) into fn (reads); loads [d0, d0 + PER) of step dkt (d0 >= 0).
+    auto sub = [&](const Frags &fc, Frags &fn, const uint8_t *ras, int rks, bool reads, int dkt,
+                   int d0, auto mask_k) {
+      constexpr bool MASK_K = decltype(mask_k)::value;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int u = i * FN + j;
+          acc[i][j] = mma(fc.b[j], fc.a[i], acc[i][j]);
+          if (reads && u < NU)
+            read_unit(ras, ras + A_BYTES, rks, wm, wn, u, fn);
+          const int d = u - (MPS - PER);
+          if (d0 >= 0 && d >= 0 && d0 + d < NDMA)
+            issue_one<MASK_K>(p, o, ra, rb, dkt, stage_addr(dkt), wave, dkt < total, d0 + d);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+    };
 
     if (total > 0) {
-      if (nmain > 0)
-        issue<false>(p, o, ra, rb, 0, lds0);
-      else
-        issue<true>(p, o, ra, rb, 0, lds0);
+      issue_range(0, 0, NDMA, std::true_type()); // masked form: K may end in step 0
       step_barrier();
-      if (total > 1) {
-        if (nmain > 1)
-          issue<false>(p, o, ra, rb, 1, lds0 + STAGE);
-        else
-          issue<true>(p, o, ra, rb, 1, lds0 + STAGE);
-      }
+      issue_range(1, 0, PER, std::true_type());
       Frags f0, f1;
       load_frags(stage_ptr(0), stage_ptr(0) + A_BYTES, 0, wm, wn, f0);
-      // Every step but the last: straight-line, 4 full sub-steps.  The first
-      // loop's steps load step kt + 2 unmasked; the second's masked (the K
+      // Every step but the last, straight-line.  The first loop's steps
+      // load steps kt + 1 and kt + 2 unmasked; the second's masked (the K
       // tail) or dead (past the end).
       auto full_step = [&](int kt, auto mask_k) {
-        constexpr bool MASK_K = decltype(mask_k)::value;
-        const uint8_t *as = stage_ptr(kt), *bs = as + A_BYTES;
-        const uint8_t *an = stage_ptr(kt + 1), *bn = an + A_BYTES;
-        load_frags(as, bs, 1, wm, wn, f1);
-        mfmas(f0, acc);
-        interleave_reads();
-        load_frags(as, bs, 2, wm, wn, f0);
-        mfmas(f1, acc);
-        interleave_reads();
-        load_frags(as, bs, 3, wm, wn, f1);
-        mfmas(f0, acc);
-        interleave_reads();
-        // Every wave holds sub-step 3's fragments: free this stage, load
-        // step kt + 2 into it, read step kt + 1's first fragments.
+        const uint8_t *as = stage_ptr(kt), *an = stage_ptr(kt + 1);
+        sub(f0, f1, as, 1, true, kt + 1, PARTS > 1 ? PER : -1, mask_k);
+        sub(f1, f0, as, 2, true, kt + 1, PARTS > 2 ? 2 * PER : -1, mask_k);
+        sub(f0, f1, as, 3, true, 0, -1, mask_k);
         step_barrier();
-        issue<MASK_K>(p, o, ra, rb, kt + 2, lds0 + (kt & 1) * STAGE, kt + 2 < total);
-        load_frags(an, bn, 0, wm, wn, f0);
-        mfmas(f1, acc);
-        interleave_reads();
+        sub(f1, f0, an, 0, true, kt + 2, 0, mask_k);
       };
       int kt = 0;
       const int unmasked_end = nmain - 2 < total - 1 ? nmain - 2 : total - 1;
       for (; kt < unmasked_end; ++kt)
-        full_step(kt, std::integral_constant<bool, false>());
+        full_step(kt, std::false_type());
       for (; kt < total - 1; ++kt)
-        full_step(kt, std::integral_constant<bool, true>());
+        full_step(kt, std::true_type());
       // The last step (the peeled K tail when K % BK != 0): only the
       // sub-steps that reach k < K.
       const uint8_t *as = stage_ptr(kt), *bs = as + A_BYTES;
@@ -310,6 +359,9 @@ template <int OP, int EPI, int NW = 4> struct Gemm16W4 {
             mfmas(f1, acc);
         }
       }
+      // Loads of a step past the end may still be writing zeros into LDS:
+      // let them land before the workgroup can end.
+      __builtin_amdgcn_s_waitcnt(0x7 << 4);
     }
 
     epilogue_tile<MASK_MN, FM, FN, WTM, WTN>(p, m0, n0, wm, wn, acc);
