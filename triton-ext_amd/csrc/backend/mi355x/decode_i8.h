@@ -101,6 +101,8 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   __shared__ __attribute__((aligned(1024))) uint8_t st2[STAGE_BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t st3[STAGES > 3 ? STAGE_BYTES : 1];
   __shared__ uint32_t last_flag;
+  // The epilogue's scales: sb of the strip's columns, sa of the rows.
+  __shared__ float s_sb[kDecodeStripN], s_sa[16 * MT];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -240,6 +242,17 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
       __builtin_amdgcn_s_waitcnt(((3 * V) & 0xf) | (((3 * V) >> 4) << 14) | (0x7 << 4) | (0xf << 8));
   };
 
+  // Scale loads go out first, one per thread, and are parked in LDS after
+  // the K loop: the epilogue then waits on no memory round trip for them.
+  float scale_v = 0.f;
+  {
+    const int t = tid - kDecodeStripN;
+    if (tid < kDecodeStripN)
+      scale_v = p.sb[n0 + tid < p.N ? n0 + tid : 0];
+    else if (t < 16 * MT)
+      scale_v = p.sa[t < p.M ? t : 0];
+  }
+
   // Prologue: STAGES - 1 batches in flight.
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
@@ -266,6 +279,10 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   }
 
   __builtin_amdgcn_s_waitcnt(0); // every load of the loop has landed
+  if (tid < kDecodeStripN)
+    s_sb[tid] = scale_v;
+  else if (tid - kDecodeStripN < 16 * MT)
+    s_sa[tid - kDecodeStripN] = scale_v;
   // Sum the 4 waves' accumulators in LDS (stage 0 is free now) with LDS
   // atomics.  acc[t][j] register r of lane l: row 16 t + 4 (l / 16) + r,
   // column 16 j + l % 16.
@@ -287,14 +304,24 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
 
   const int nthreads = kDecodeWaves * 64;
   auto wg_sum = [&](int i) { return red[i]; };
-  if (p.ksplit == 1) {
-    for (int i = tid; i < p.M * kDecodeStripN; i += nthreads) {
+  // C = bf16((float(sum) * sa[m]) * sb[n]) for this thread's PER elements
+  // (element e: i = tid + e * nthreads), scales from LDS.
+  constexpr int PER = MT * 16 * kDecodeStripN / (kDecodeWaves * 64);
+  auto epilogue = [&](const int32_t (&sum)[PER]) {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const int i = tid + e * nthreads;
       const int m = i / kDecodeStripN, n = i % kDecodeStripN;
-      if (n0 + n < p.N) {
-        const float v = ((float)wg_sum(i) * p.sa[m]) * p.sb[n0 + n];
-        p.C[m * p.ldc + n0 + n] = f32_to_bf16_rne(v);
-      }
+      if (m < p.M && n0 + n < p.N)
+        p.C[m * p.ldc + n0 + n] = f32_to_bf16_rne(((float)sum[e] * s_sa[m]) * s_sb[n]);
     }
+  };
+  if (p.ksplit == 1) {
+    int32_t sum[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e)
+      sum[e] = wg_sum(tid + e * nthreads);
+    epilogue(sum);
     return;
   }
 
@@ -324,48 +351,49 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   __syncthreads();
   if (!last_flag)
     return;
-  // Last arrival: add the other splits' partials to this workgroup's own sum
-  // (still in LDS), in split order, then apply the epilogue.  Loads are
-  // issued four splits at a time before any of them is used, so the gather
-  // costs one memory round trip per four splits.
-  constexpr int PER = MT * 16 * kDecodeStripN / (kDecodeWaves * 64); // elements per thread
+  // Last arrival: add every split's partial (its own included, stored
+  // above) in split order, then apply the epilogue.  The loads are
+  // unconditional -- out-of-range elements read element 0 and are dropped
+  // after -- so a batch of NQ splits is issued before any value is used and
+  // the gather costs one memory round trip per batch.
   int32_t sum[PER];
-#pragma unroll
-  for (int e = 0; e < PER; ++e)
-    sum[e] = 0;
-  for (int q0 = 0; q0 < p.ksplit; q0 += 4) {
-    int32_t v[4][PER];
-#pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      const int q = q0 + qq;
-      const int32_t *src = p.partials + (int64_t)q * p.M * p.N;
-#pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        const int i = tid + e * nthreads;
-        const int m = i / kDecodeStripN, n = i % kDecodeStripN;
-        v[qq][e] = 0;
-        if (q < p.ksplit && m < p.M && n0 + n < p.N)
-          v[qq][e] = q == split ? wg_sum(i)
-                                : __hip_atomic_load(&src[(int64_t)m * p.N + n0 + n],
-                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-#pragma unroll
-    for (int qq = 0; qq < 4; ++qq)
-#pragma unroll
-      for (int e = 0; e < PER; ++e)
-        sum[e] += v[qq][e];
-  }
+  int64_t off[PER];
+  bool ok[PER];
 #pragma unroll
   for (int e = 0; e < PER; ++e) {
     const int i = tid + e * nthreads;
     const int m = i / kDecodeStripN, n = i % kDecodeStripN;
-    const int64_t col = n0 + n;
-    if (m < p.M && col < p.N) {
-      const float v = ((float)sum[e] * p.sa[m]) * p.sb[col];
-      p.C[m * p.ldc + col] = f32_to_bf16_rne(v);
-    }
+    ok[e] = m < p.M && n0 + n < p.N;
+    off[e] = ok[e] ? (int64_t)m * p.N + n0 + n : 0;
+    sum[e] = 0;
   }
+  auto gather = [&](auto nq) {
+    constexpr int NQ = decltype(nq)::value;
+    for (int q0 = 0; q0 < p.ksplit; q0 += NQ) {
+      int32_t v[NQ][PER];
+#pragma unroll
+      for (int qq = 0; qq < NQ; ++qq) {
+        const int32_t *src = p.partials + (int64_t)(q0 + qq) * p.M * p.N;
+#pragma unroll
+        for (int e = 0; e < PER; ++e)
+          v[qq][e] = __hip_atomic_load(&src[off[e]], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int qq = 0; qq < NQ; ++qq)
+#pragma unroll
+        for (int e = 0; e < PER; ++e)
+          sum[e] += ok[e] ? v[qq][e] : 0;
+    }
+  };
+  // Batches of up to 32 loads per thread (ksplit is a power of two >= 2).
+  constexpr int NQ = 32 / PER >= 4 ? 4 : (32 / PER >= 2 ? 2 : 1);
+  if (NQ >= 4 && p.ksplit >= 4)
+    gather(std::integral_constant<int, NQ>());
+  else if (NQ >= 2)
+    gather(std::integral_constant<int, 2>());
+  else
+    gather(std::integral_constant<int, 1>());
+  epilogue(sum);
 }
 
 } // namespace txk
