@@ -170,16 +170,23 @@ def test_plan_validation():
     (512, 512, 512, tx.F16, tx.F32, 0, tx.KERNEL_GEMM_16BIT),
     (1, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
     (64, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
-    (256, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_GEMM_I8),
+    (128, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
+    (256, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
+    (257, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_GEMM_I8),
     (300, 304, 256, tx.I8, tx.I32, 0, tx.KERNEL_GEMM_I8),
+    (2, 8192, 8192, tx.I8, tx.I32, 0, tx.KERNEL_GEMM_I8),
     (2048, 7168, 7168, tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, tx.KERNEL_GEMM_F8),
 ])
 def test_kernel_choice(M, N, K, a, c, sm, kernel):
     p = tx.plan(tx.make_desc(M, N, K, a, c, scale_mode=sm))
     assert p.kernel == kernel
     assert p.grid_x > 0 and p.block_threads in (256, 512)
-    if kernel == tx.KERNEL_DECODE_I8 and p.split_k > 1:
-        assert p.workspace_bytes >= p.split_k * M * N * 4
+    if kernel == tx.KERNEL_DECODE_I8:
+        # 128-column strips x row slices of 64 x K splits cover the 256 CUs
+        slices = -(-M // 64) if M > 64 else 1
+        assert p.grid_x == (N // 128) * slices * p.split_k == 256
+        if p.split_k > 1:
+            assert p.workspace_bytes >= p.split_k * M * N * 4
     assert (p.split_k & (p.split_k - 1)) == 0
 
 

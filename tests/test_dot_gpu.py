@@ -169,8 +169,11 @@ def test_c4_w8a8_decode(gpu, M):
 
 
 @pytest.mark.parametrize("M,N,K", [(5, 272, 208), (16, 256, 64), (40, 8208, 1008), (3, 16, 4160),
-                                   (64, 512, 16), (17, 4096, 2080)])
+                                   (64, 512, 16), (17, 4096, 2080), (65, 8208, 1008),
+                                   (100, 4096, 2080), (130, 272, 4160), (200, 1024, 64),
+                                   (256, 8192, 1024)])
 def test_w8a8_decode_edges(gpu, M, N, K):
+    """Decode shapes, row slices of 64 past M = 64 (M = 65 .. 256) included."""
     a, b, sa, sb, got = run_w8a8(gpu, M, N, K, seed=M)
     ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 64, 64),
                            scale_mode=oracle.SCALE_ROWCOL, sa=sa, sb=sb, round_mode=oracle.ROUND_RNE)
@@ -188,7 +191,8 @@ def test_w8a8_repeat_launches(gpu):
 
 @pytest.mark.parametrize("M,N,K,block", [(300, 304, 256, (128, 128, 128)),
                                           (256, 512, 1000 - 1000 % 16, (256, 256, 128)),
-                                          (2, 16, 16, (128, 128, 128))])
+                                          (2, 16, 16, (128, 128, 128)),
+                                          (2, 4096, 1024, (0, 0, 0)), (64, 512, 256, (0, 0, 0))])
 def test_int8_gemm_int32_exact(gpu, M, N, K, block):
     import torch
     say(f"int8 gemm i32 M={M} N={N} K={K} block={block}")

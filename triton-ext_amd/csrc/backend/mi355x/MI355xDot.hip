@@ -232,15 +232,20 @@ int findGemmConfig(int op, int epi, int bm, int bn, int bk) {
 }
 
 bool useDecode(const tx_dot_desc &d) {
-  return d.a_type == TX_I8 && d.scale_mode == TX_SCALE_ROWCOL && d.M <= 64;
+  return d.a_type == TX_I8 && d.scale_mode == TX_SCALE_ROWCOL && d.M <= kDecodeMaxM;
 }
 
+// Decode row tiling: 16 * MT rows per slice (MT <= 4), ceil(M / 64) slices
+// past 64 rows.
+int decodeMT(int64_t M) { return M > 64 ? 4 : (int)cdiv(M > 0 ? M : 1, 16); }
+int decodeSlices(int64_t M) { return M > 64 ? (int)cdiv(M, 64) : 1; }
+
 // Split-K factor for the decode kernel: a power of two (<= kMaxSplit) so
-// that strips * ksplit workgroups cover the CUs about once, each with at
-// least four 64-row batches per wave.  TX_DECODE_KSPLIT overrides.
-int decodeSplit(int64_t N, int64_t K) {
+// that slices * strips * ksplit workgroups cover the CUs about once, each
+// with at least four 64-row batches per wave.  TX_DECODE_KSPLIT overrides.
+int decodeSplit(int64_t M, int64_t N, int64_t K) {
   const char *env = std::getenv("TX_DECODE_KSPLIT");
-  const int64_t strips = cdiv(N, kDecodeStripN);
+  const int64_t strips = cdiv(N, kDecodeStripN) * decodeSlices(M);
   const int64_t batches = cdiv(K, kDecodeBatchK);
   int ks = 1;
   if (env && *env) {
@@ -261,11 +266,14 @@ int decodeSplit(int64_t N, int64_t K) {
   return ks;
 }
 
+int64_t decodeCounterBytes(const tx_dot_desc &d) {
+  return ((decodeSlices(d.M) * cdiv(d.N, kDecodeStripN) * 4 + 255) / 256) * 256;
+}
+
 int64_t decodeWorkspace(const tx_dot_desc &d, int ksplit) {
   if (ksplit <= 1)
     return 0;
-  const int64_t counters = ((cdiv(d.N, kDecodeStripN) * 4 + 255) / 256) * 256;
-  return counters + (int64_t)ksplit * d.M * d.N * 4;
+  return decodeCounterBytes(d) + (int64_t)ksplit * d.M * d.N * 4;
 }
 
 // ---------------------------------------------------------------------------
@@ -280,10 +288,10 @@ int txMi355xDotRun(tx_dot_plan *plan) {
                 "no kernel for a_type=%d b_type=%d c_type=%d scale_mode=%d",
                 d.a_type, d.b_type, d.c_type, d.scale_mode);
   if (useDecode(d)) {
-    const int ks = decodeSplit(d.N, d.K);
+    const int ks = decodeSplit(d.M, d.N, d.K);
     plan->kernel = TX_KERNEL_DECODE_I8;
     plan->split_k = ks;
-    plan->grid_x = (int32_t)(cdiv(d.N, kDecodeStripN) * ks);
+    plan->grid_x = (int32_t)(cdiv(d.N, kDecodeStripN) * ks * decodeSlices(d.M));
     plan->grid_y = plan->grid_z = 1;
     plan->block_threads = kDecodeWaves * 64;
     plan->workspace_bytes = decodeWorkspace(d, ks);
@@ -466,14 +474,15 @@ int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
                  const float *sa, const float *sb, void *ws, size_t ws_bytes,
                  hipStream_t stream) {
   const tx_dot_desc &d = plan.desc;
-  const int mt = (int)cdiv(d.M > 0 ? d.M : 1, 16);
-  if (mt < 1 || mt > 4)
+  const int mt = decodeMT(d.M);
+  if (d.M > kDecodeMaxM)
     return fail(TX_ERR_INVALID, "decode plan with M=%lld", (long long)d.M);
+  const int slices = decodeSlices(d.M);
   const int ks = plan.split_k;
   if (ks < 1 || ks > (int)kMaxSplit || (ks & (ks - 1)))
     return fail(TX_ERR_INVALID, "decode split %d is not a power of two <= %u", ks,
                 kMaxSplit);
-  if (plan.grid_x != cdiv(d.N, kDecodeStripN) * ks ||
+  if (plan.grid_x != cdiv(d.N, kDecodeStripN) * ks * slices ||
       plan.block_threads != kDecodeWaves * 64)
     return fail(TX_ERR_INVALID, "plan launch shape does not match the decode kernel");
   const int64_t need = decodeWorkspace(d, ks);
@@ -493,10 +502,11 @@ int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   a.ldb = d.ldb;
   a.ldc = d.ldc;
   a.ksplit = ks;
+  a.slices = slices;
   const int64_t batches = cdiv(d.K, kDecodeBatchK);
   a.batches_per_split = (int32_t)cdiv(batches, ks);
   a.k_main_batches = (int32_t)(plan.k_split / kDecodeBatchK);
-  const int64_t counters = ((cdiv(d.N, kDecodeStripN) * 4 + 255) / 256) * 256;
+  const int64_t counters = decodeCounterBytes(d);
   a.counters = static_cast<uint32_t *>(ws);
   a.partials = need > 0 ? reinterpret_cast<int32_t *>(static_cast<uint8_t *>(ws) + counters)
                         : nullptr;

@@ -1,16 +1,18 @@
 // int8 W8A8 small-M dot (decode shape) for gfx950:
 //   C[m][n] = bf16((float(sum_k A[m][k] * B[k][n]) * sa[m]) * sb[n])
-// with A int8 [M,K] (M <= 16*MT), B int8 [K,N] row-major, int32 accumulation.
+// with A int8 [M,K] (M <= 256), B int8 [K,N] row-major, int32 accumulation.
 //
 // The job is one pass over B, so it is HBM-bound and the kernel is built to
 // stream B once with every CU keeping plenty of bytes in flight:
-//  * A workgroup owns a strip of 128 columns and a range of K (split-K);
-//    each of its 4 waves takes every 4th batch of 64 K rows (8 KiB of B).
+//  * A workgroup owns a strip of 128 columns, a range of K (split-K) and a
+//    slice of up to 16 * MT rows (row slices of 64 past M = 64); each of its
+//    4 waves takes every 4th batch of 64 K rows (8 KiB of B).
 //  * Each wave has a private LDS ring of STAGES slots fed by
 //    global_load_lds_dwordx4 (lane l of a wave-wide load writes 16 bytes at
 //    slot + 16 l): 8 loads per batch move 64 rows x 128 bytes, 128-byte row
 //    segments, straight into LDS with no VGPR staging.  MT more loads bring
-//    the batch's A fragments in MFMA order.  B's loads are non-temporal: each
+//    the batch's A fragments straight into registers (a lane's 16 bytes of
+//    row-major A are its MFMA operand).  B's loads are non-temporal: each
 //    byte is read once, and allocating loads would also have to write back
 //    whatever dirty lines they evict (measured: 2.7 vs 5.1 TB/s after a
 //    write-heavy kernel).  Waves never synchronise with
@@ -50,6 +52,7 @@ constexpr int kDecodeBatchK = 64;
 constexpr int kDecodeStripN = 128;
 constexpr int kDecodeWaves = 4;
 constexpr uint32_t kMaxSplit = 64;
+constexpr int kDecodeMaxM = 256; // 4 row slices of 64
 
 struct DecodeArgs {
   const int8_t *A;
@@ -60,10 +63,11 @@ struct DecodeArgs {
   int32_t M, N, K;
   int64_t lda, ldb, ldc;
   int32_t ksplit;            // workgroups per column strip (power of two)
+  int32_t slices;            // row slices of 16 * MT rows (M > 16 * MT)
   int32_t batches_per_split;
   int32_t k_main_batches;    // batches with every K row < K (unmasked)
   int32_t *partials;         // [ksplit][M][N] int32
-  uint32_t *counters;        // [ceil(N / 128)] arrival counters
+  uint32_t *counters;        // [slices][ceil(N / 128)] arrival counters
 };
 
 typedef int v2i_t __attribute__((ext_vector_type(2)));
@@ -77,11 +81,11 @@ __device__ __forceinline__ i32x4_t mfma_i8_16(const i32x4_t &a, const i32x4_t &b
 
 
 template <int MT> struct DecodeCfg {
-  // Slots per wave: 4 waves x STAGES x (8 KiB of B + MT KiB of A) <= 160 KiB.
-  static constexpr int STAGES = MT == 1 ? 4 : 3;
+  // Slots per wave: 4 waves x STAGES x 8 KiB of B (A goes to registers).
+  static constexpr int STAGES = 4;
   static constexpr int B_BYTES = kDecodeBatchK * kDecodeStripN; // 8 KiB
-  static constexpr int SLOT = B_BYTES + MT * 1024;
-  static constexpr int VM_PER_BATCH = 8 + MT; // direct-to-LDS loads per batch
+  static constexpr int SLOT = B_BYTES;
+  static constexpr int VM_PER_BATCH = 8 + MT; // B loads into LDS + A loads per batch
   static constexpr int LDS = kDecodeWaves * STAGES * SLOT;
   static_assert(LDS <= 160 * 1024, "ring exceeds LDS");
   static_assert((STAGES - 1) * VM_PER_BATCH <= 63, "vmcnt is 6 bits");
@@ -106,8 +110,28 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int strip = blockIdx.x / p.ksplit, split = blockIdx.x % p.ksplit;
+  // Workgroup -> (row slice, column strip, K split).  With several slices,
+  // the slices of one (strip, split) pair go to one XCD (workgroups are
+  // dealt to the 8 XCDs round-robin) so they read its B through one L2.
+  const int strips = (p.N + kDecodeStripN - 1) / kDecodeStripN;
+  const int pairs = strips * p.ksplit;
+  int slice = 0, pair = blockIdx.x;
+  if (p.slices > 1) {
+    if (pairs % 8 == 0) {
+      const int j = blockIdx.x / 8;
+      slice = j % p.slices;
+      pair = 8 * (j / p.slices) + blockIdx.x % 8;
+    } else {
+      slice = blockIdx.x % p.slices;
+      pair = blockIdx.x / p.slices;
+    }
+  }
+  const int strip = pair / p.ksplit, split = pair % p.ksplit;
   const int64_t n0 = (int64_t)strip * kDecodeStripN;
+  // This slice's rows: row0 .. row0 + Mr - 1.
+  const int row0 = slice * 16 * MT;
+  const int Mr = p.M - row0 < 16 * MT ? p.M - row0 : 16 * MT;
+  const int8_t *const Ap = p.A + (int64_t)row0 * p.lda;
   const bool n_edge = n0 + kDecodeStripN > p.N;
   uint8_t *const all_st[4] = {st0, st1, st2, st3};
   uint8_t *slots[STAGES];
@@ -124,8 +148,10 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   const int first = b_begin + wave;
   const int nb = first < b_end ? (b_end - first + kDecodeWaves - 1) / kDecodeWaves : 0;
 
-  // Direct-to-LDS loads of one batch into `slot`.
-  auto issue = [&](int b, uint8_t *slot) {
+  // Loads of one batch: B direct to LDS into `slot`, A straight into the
+  // registers `a` (a lane's 16 bytes of A -- row 16 t + l % 16, K 16 (l / 16)
+  // .. +15 of the batch -- are exactly its MFMA operand).
+  auto issue = [&](int b, uint8_t *slot, i32x4_t (&a)[MT]) {
     const int64_t k0 = (int64_t)b * kDecodeBatchK;
     const bool mask = n_edge || b >= p.k_main_batches;
 #pragma unroll
@@ -142,10 +168,10 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
     for (int t = 0; t < MT; ++t) {
       const int m = 16 * t + (lane & 15);
       const int64_t k = k0 + 16 * (lane >> 4);
-      const void *src = p.A + (int64_t)m * p.lda + k;
-      if (m >= p.M || (b >= p.k_main_batches && k >= p.K))
+      const void *src = Ap + (int64_t)m * p.lda + k;
+      if (m >= Mr || (b >= p.k_main_batches && k >= p.K))
         src = tx_zero_chunk;
-      dma16(src, (lds_void *)(slot + Cfg::B_BYTES + t * 1024));
+      a[t] = *reinterpret_cast<const i32x4_t *>(src);
     }
   };
 
@@ -170,43 +196,21 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
     const int r0 = 16 * G + (L >> 1);
     tr_off[j] = r0 * 128 + ((j ^ (r0 & 7)) << 4) + 8 * (L & 1); // row r0 + 8: +1024
   }
-  auto consume = [&](const uint8_t *slot) {
+  auto consume = [&](const uint8_t *slot, const i32x4_t (&a)[MT]) {
     const uint32_t base = lds_addr(slot);
-    i32x4_t a[MT];
     v2i_t lo[8], hi[8];
-    // A fragments (ds_read_b128 at lane * 16) and columns 0..63.
-    if constexpr (MT == 1) {
-      asm volatile(
-          "ds_read_b128 %0, %9 offset:8192\n\t"
-          "ds_read_b64_tr_b8 %1, %10\n\tds_read_b64_tr_b8 %2, %10 offset:1024\n\t"
-          "ds_read_b64_tr_b8 %3, %11\n\tds_read_b64_tr_b8 %4, %11 offset:1024\n\t"
-          "ds_read_b64_tr_b8 %5, %12\n\tds_read_b64_tr_b8 %6, %12 offset:1024\n\t"
-          "ds_read_b64_tr_b8 %7, %13\n\tds_read_b64_tr_b8 %8, %13 offset:1024\n\t"
-          "s_waitcnt lgkmcnt(0)"
-          : "=v"(a[0]), "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1]), "=v"(lo[2]),
-            "=v"(hi[2]), "=v"(lo[3]), "=v"(hi[3])
-          : "v"(base + lane * 16), "v"(base + tr_off[0]), "v"(base + tr_off[1]),
-            "v"(base + tr_off[2]), "v"(base + tr_off[3])
-          : "memory");
-    } else {
-#pragma unroll
-      for (int t = 0; t < MT; ++t)
-        asm volatile("ds_read_b128 %0, %1 offset:%2\n\ts_waitcnt lgkmcnt(0)"
-                     : "=v"(a[t])
-                     : "v"(base + lane * 16), "i"(Cfg::B_BYTES + t * 1024)
-                     : "memory");
-      asm volatile(
-          "ds_read_b64_tr_b8 %0, %8\n\tds_read_b64_tr_b8 %1, %8 offset:1024\n\t"
-          "ds_read_b64_tr_b8 %2, %9\n\tds_read_b64_tr_b8 %3, %9 offset:1024\n\t"
-          "ds_read_b64_tr_b8 %4, %10\n\tds_read_b64_tr_b8 %5, %10 offset:1024\n\t"
-          "ds_read_b64_tr_b8 %6, %11\n\tds_read_b64_tr_b8 %7, %11 offset:1024\n\t"
-          "s_waitcnt lgkmcnt(0)"
-          : "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1]), "=v"(lo[2]), "=v"(hi[2]),
-            "=v"(lo[3]), "=v"(hi[3])
-          : "v"(base + tr_off[0]), "v"(base + tr_off[1]), "v"(base + tr_off[2]),
-            "v"(base + tr_off[3])
-          : "memory");
-    }
+    // Columns 0..63.
+    asm volatile(
+        "ds_read_b64_tr_b8 %0, %8\n\tds_read_b64_tr_b8 %1, %8 offset:1024\n\t"
+        "ds_read_b64_tr_b8 %2, %9\n\tds_read_b64_tr_b8 %3, %9 offset:1024\n\t"
+        "ds_read_b64_tr_b8 %4, %10\n\tds_read_b64_tr_b8 %5, %10 offset:1024\n\t"
+        "ds_read_b64_tr_b8 %6, %11\n\tds_read_b64_tr_b8 %7, %11 offset:1024\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1]), "=v"(lo[2]), "=v"(hi[2]),
+          "=v"(lo[3]), "=v"(hi[3])
+        : "v"(base + tr_off[0]), "v"(base + tr_off[1]), "v"(base + tr_off[2]),
+          "v"(base + tr_off[3])
+        : "memory");
     // Columns 64..127.
     asm volatile(
         "ds_read_b64_tr_b8 %0, %8\n\tds_read_b64_tr_b8 %1, %8 offset:1024\n\t"
@@ -250,14 +254,16 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
     if (tid < kDecodeStripN)
       scale_v = p.sb[n0 + tid < p.N ? n0 + tid : 0];
     else if (t < 16 * MT)
-      scale_v = p.sa[t < p.M ? t : 0];
+      scale_v = p.sa[row0 + (t < Mr ? t : 0)];
   }
 
-  // Prologue: STAGES - 1 batches in flight.
+  // Prologue: STAGES - 1 batches in flight.  Batch i uses slot and A
+  // registers i % STAGES.
+  i32x4_t a_regs[STAGES][MT];
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < nb)
-      issue(first + kDecodeWaves * s, slots[s]);
+      issue(first + kDecodeWaves * s, slots[s], a_regs[s]);
   // Main loop, unrolled by STAGES so slot addresses are static.
   for (int i0 = 0; i0 < nb; i0 += STAGES) {
 #pragma unroll
@@ -269,11 +275,12 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
           // Its slot was read at step i - 1: wait for those LDS reads
           // (lgkmcnt 0) before the new loads may overwrite it.
           __builtin_amdgcn_s_waitcnt(0xf | (0x3 << 14) | (0x7 << 4));
-          issue(first + kDecodeWaves * in, slots[(s + STAGES - 1) % STAGES]);
+          issue(first + kDecodeWaves * in, slots[(s + STAGES - 1) % STAGES],
+                a_regs[(s + STAGES - 1) % STAGES]);
         }
         const int newer = (nb - 1 - i) < (STAGES - 1) ? (nb - 1 - i) : (STAGES - 1);
         wait_newer(newer);
-        consume(slots[s]);
+        consume(slots[s], a_regs[s]);
       }
     }
   }
@@ -312,8 +319,9 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
     for (int e = 0; e < PER; ++e) {
       const int i = tid + e * nthreads;
       const int m = i / kDecodeStripN, n = i % kDecodeStripN;
-      if (m < p.M && n0 + n < p.N)
-        p.C[m * p.ldc + n0 + n] = f32_to_bf16_rne(((float)sum[e] * s_sa[m]) * s_sb[n]);
+      if (m < Mr && n0 + n < p.N)
+        p.C[(int64_t)(row0 + m) * p.ldc + n0 + n] =
+            f32_to_bf16_rne(((float)sum[e] * s_sa[m]) * s_sb[n]);
     }
   };
   if (p.ksplit == 1) {
@@ -333,8 +341,8 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   // stores are acknowledged (s_waitcnt vmcnt(0)) before the barrier that
   // precedes the counter increment, and the last workgroup issues its loads
   // only after its increment has returned.
-  int32_t *mine = p.partials + (int64_t)split * p.M * p.N;
-  for (int i = tid; i < p.M * kDecodeStripN; i += nthreads) {
+  int32_t *mine = p.partials + ((int64_t)split * p.M + row0) * p.N;
+  for (int i = tid; i < Mr * kDecodeStripN; i += nthreads) {
     const int m = i / kDecodeStripN, n = i % kDecodeStripN;
     if (n0 + n < p.N)
       __hip_atomic_store(&mine[(int64_t)m * p.N + n0 + n], wg_sum(i), __ATOMIC_RELAXED,
@@ -344,7 +352,7 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   __syncthreads();
   if (tid == 0) {
     const uint32_t inc = kMaxSplit / (uint32_t)p.ksplit;
-    const uint32_t old = __hip_atomic_fetch_add(&p.counters[strip], inc, __ATOMIC_RELAXED,
+    const uint32_t old = __hip_atomic_fetch_add(&p.counters[slice * strips + strip], inc, __ATOMIC_RELAXED,
                                                 __HIP_MEMORY_SCOPE_AGENT);
     last_flag = ((old + inc) % kMaxSplit) == 0;
   }
@@ -363,7 +371,7 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   for (int e = 0; e < PER; ++e) {
     const int i = tid + e * nthreads;
     const int m = i / kDecodeStripN, n = i % kDecodeStripN;
-    ok[e] = m < p.M && n0 + n < p.N;
+    ok[e] = m < Mr && n0 + n < p.N;
     off[e] = ok[e] ? (int64_t)m * p.N + n0 + n : 0;
     sum[e] = 0;
   }
@@ -373,7 +381,7 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
       int32_t v[NQ][PER];
 #pragma unroll
       for (int qq = 0; qq < NQ; ++qq) {
-        const int32_t *src = p.partials + (int64_t)(q0 + qq) * p.M * p.N;
+        const int32_t *src = p.partials + ((int64_t)(q0 + qq) * p.M + row0) * p.N;
 #pragma unroll
         for (int e = 0; e < PER; ++e)
           v[qq][e] = __hip_atomic_load(&src[off[e]], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
