@@ -37,10 +37,14 @@
 // rounds twice: the results agree to a few ulp.)
 //
 // Pipeline: two LDS stages.  A wave holds the 4 B fragments of a step (32
-// VGPRs) and streams the A fragments one row block ahead.  When the last row
-// block's A fragment is in registers every wave is done with the stage: one
-// barrier, the loads of step k+2 go into it, and each B fragment is replaced
-// by the next step's as soon as the last row block's MFMA has used it.
+// VGPRs) and streams the A fragments (and scales) one row block ahead.  The
+// scale FMAs of a row block run during the next row block, after its own
+// MFMAs have had that row block's worth of time to finish.  When the last
+// row block's A fragment is in registers every wave is done with the stage:
+// one barrier, the loads of step k+2 start going into it (a quarter there,
+// the rest spread over row blocks 0..2 of step k+1: a 64 KiB burst would
+// stall the load path), and each B fragment is replaced by the next step's
+// as soon as the last row block's MFMA has used it.
 #pragma once
 
 #include "gemm16_w4.h"
@@ -54,6 +58,7 @@ template <int OP, int EPI> struct Gemm8W4 {
   static constexpr int WTM = 128, WTN = 64, FM = WTM / 16, FN = WTN / 16;
   static constexpr bool SCALED = EPI == EPI_BLOCK128_BF16 || EPI == EPI_BLOCK128_F32;
   static constexpr bool INT = OP == OP_I8;
+  static constexpr bool PARTIAL = SCALED; // fresh MFMA per step, VALU scale FMA
   static constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN; // 32 KiB each
   static constexpr int SA_OFF = A_BYTES + B_BYTES, SB_OFF = SA_OFF + BM * 4;
   static constexpr uint32_t STAGE = SB_OFF + 256;
@@ -72,44 +77,48 @@ template <int OP, int EPI> struct Gemm8W4 {
                  : "memory");
   }
 
-  // Loads of K step kt into the stage at LDS address st (see gemm16_w4.h).
-  // Lane offsets are recomputed here rather than kept live through the K
-  // loop (registers are the scarce resource of this tile).
-  template <bool MASK_MN, bool MASK_K>
-  __device__ __forceinline__ static void issue(const GemmArgs &p, int64_t m0, int64_t n0,
-                                               const i32x4_t &ra, const i32x4_t &rb,
-                                               const i32x4_t &rsa, const i32x4_t &rsb, int kt,
-                                               uint32_t st, int wave, bool live) {
+  // Loads of K step kt into the stage at LDS address st (layout above),
+  // issued in four parts: PART 0 = A loads 0, 1 and the scale loads; 1 = A
+  // loads 2, 3; 2 = B loads 0, 1; 3 = B loads 2, 3 (each 1 KiB).  Buffer
+  // loads with per-lane offsets (see gemm16_w4.h): out-of-range offsets read
+  // zeros.  Offsets are recomputed per load rather than kept live through
+  // the K loop (registers are the scarce resource of this tile).
+  template <bool MASK_MN, bool MASK_K, int PART>
+  __device__ __forceinline__ static void issue_part(const GemmArgs &p, int64_t m0, int64_t n0,
+                                                    const i32x4_t &ra, const i32x4_t &rb,
+                                                    const i32x4_t &rsa, const i32x4_t &rsb,
+                                                    int kt, uint32_t st, int wave, bool live) {
     const int lane = threadIdx.x & 63;
     const int k0 = kt * BK;
-    const uint32_t sa_ = (uint32_t)k0;
-    const uint32_t sb_ = (uint32_t)((int64_t)k0 * p.ldb);
     typedef Gemm16W4<OP_BF16, EPI_F32, 4> W;
+    if (PART < 2) {
 #pragma unroll
-    for (int i = 0; i < A_DMA; ++i) {
-      const int j = wave * A_DMA + i;        // 1 KiB block: 8 rows of 128 B
-      const int row = 8 * j + (lane >> 3), pc = lane & 7;
-      const int c = pc ^ ((row >> 1) & 7);
-      const bool ok = live && (!MASK_MN || m0 + row < p.M) && (!MASK_K || k0 + 16 * c < p.K);
-      const uint32_t v = ok ? (uint32_t)(m0 + row) * (uint32_t)p.lda + 16u * c : kOOB;
-      W::buffer_lds16(v, ra, sa_, st + j * 1024);
-    }
+      for (int i = 2 * PART; i < 2 * PART + 2; ++i) {
+        const int j = wave * A_DMA + i;
+        const int row = 8 * j + (lane >> 3), pc = lane & 7;
+        const int c = pc ^ ((row >> 1) & 7);
+        const bool ok = live && (!MASK_MN || m0 + row < p.M) && (!MASK_K || k0 + 16 * c < p.K);
+        const uint32_t v = ok ? (uint32_t)(m0 + row) * (uint32_t)p.lda + 16u * c : kOOB;
+        W::buffer_lds16(v, ra, (uint32_t)k0, st + j * 1024);
+      }
+    } else {
 #pragma unroll
-    for (int i = 0; i < B_DMA; ++i) {
-      const int j = wave * B_DMA + i;        // 1 KiB block: 4 rows of 256 B
-      const int k = 4 * j + (lane >> 4), pc = lane & 15;
-      const int c = pc ^ (k & 7);
-      const bool ok = live && (!MASK_MN || n0 + 16 * c < p.N);
-      const uint32_t v = ok ? (uint32_t)k * (uint32_t)p.ldb + (uint32_t)n0 + 16u * c : kOOB;
-      W::buffer_lds16(v, rb, sb_, st + A_BYTES + j * 1024);
+      for (int i = 2 * (PART - 2); i < 2 * (PART - 2) + 2; ++i) {
+        const int j = wave * B_DMA + i;
+        const int k = 4 * j + (lane >> 4), pc = lane & 15;
+        const int c = pc ^ (k & 7);
+        const bool ok = live && (!MASK_MN || n0 + 16 * c < p.N);
+        const uint32_t v = ok ? (uint32_t)k * (uint32_t)p.ldb + (uint32_t)n0 + 16u * c : kOOB;
+        W::buffer_lds16(v, rb, (uint32_t)((int64_t)k0 * p.ldb), st + A_BYTES + j * 1024);
+      }
     }
-    if (SCALED) {
-      if (wave < 4) { // 4 x 64 rows: sa[m0 + row][kt]
+    if (SCALED && PART == 0) {
+      if (wave < 4) {
         const int64_t gm = m0 + 64 * wave + lane;
         const uint32_t v = (live && gm < p.M) ? (uint32_t)gm * (uint32_t)(p.sa_ld * 4) : kOOB;
         buffer_lds4(v, rsa, (uint32_t)kt * 4, st + SA_OFF + wave * 256);
       }
-      if (wave == 0) { // sb[kt][n0/128 + lane], lanes 0 and 1
+      if (wave == 0) {
         const int64_t nb = (n0 >> 7) + lane;
         const uint32_t v = (live && lane < 2 && nb < p.sb_ld) ? (uint32_t)nb * 4u : kOOB;
         buffer_lds4(v, rsb, (uint32_t)(kt * p.sb_ld * 4), st + SB_OFF);
@@ -185,26 +194,9 @@ template <int OP, int EPI> struct Gemm8W4 {
   // block's partial products would be live at once.
   __device__ __forceinline__ static void pin(Acc &v) { asm volatile("" : "+v"(v)); }
 
-  // Row block i of one step: its 4 MFMAs (and, block-scaled, its FMAs).
-  __device__ __forceinline__ static void row_block(const i32x8_t &a, const i32x8_t (&b)[FN],
-                                                   float s, Acc (&acc)[FN]) {
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      if constexpr (SCALED) {
-        const Acc part = mma(b[j], a, Acc{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          acc[j][r] = __builtin_fmaf(part[r], s, acc[j][r]);
-        pin(acc[j]);
-      } else {
-        acc[j] = mma(b[j], a, acc[j]);
-      }
-    }
-  }
-
   template <bool MASK_MN>
   __device__ __forceinline__ static void run(const GemmArgs &p, int64_t m0, int64_t n0,
-                                             uint8_t *smem) {
+                                              uint8_t *smem) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WN, wn = wave % WN;
@@ -216,7 +208,6 @@ template <int OP, int EPI> struct Gemm8W4 {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           acc[i][j][r] = 0;
-
     const int nmain = p.k_main_steps;
     const int total = nmain + p.k_masked_steps;
     const uint32_t lds0 = lds_addr(smem);
@@ -229,19 +220,19 @@ template <int OP, int EPI> struct Gemm8W4 {
     }
     Bases bs;
     bases(lds0, wm, wn, bs);
-    auto issue_step = [&](int kt, bool live) {
+    auto part_of = [&](int kt, auto pc) {
+      constexpr int PART = decltype(pc)::value;
       const uint32_t st = lds0 + (kt & 1) * STAGE;
+      const bool live = kt < total;
       if (kt >= nmain)
-        issue<MASK_MN, true>(p, m0, n0, ra, rb, rsa, rsb, kt, st, wave, live);
+        issue_part<MASK_MN, true, PART>(p, m0, n0, ra, rb, rsa, rsb, kt, st, wave, live);
       else
-        issue<MASK_MN, false>(p, m0, n0, ra, rb, rsa, rsb, kt, st, wave, live);
+        issue_part<MASK_MN, false, PART>(p, m0, n0, ra, rb, rsa, rsb, kt, st, wave, live);
     };
     auto step_barrier = [] {
-      __builtin_amdgcn_s_waitcnt(0x7 << 4); // vmcnt 0, expcnt 7, lgkmcnt 0
+      __builtin_amdgcn_s_waitcnt(0x7 << 4);
       __syncthreads();
     };
-    // Scale of row block i for the step in stage `so`: sa[row][kt] * sb[kt][nb]
-    // (sb: the 128-column block holding this wave's 64 columns).
     typedef __attribute__((address_space(3))) float lds_f32;
     auto scale = [&](uint32_t so, int i) {
       if constexpr (SCALED) {
@@ -252,65 +243,85 @@ template <int OP, int EPI> struct Gemm8W4 {
         return 1.f;
       }
     };
-
+    // Pending partial products (fp8) of the previous row block and its scale.
+    Acc P[FN];
+    float sp = 0.f;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      P[j] = Acc{0, 0, 0, 0};
+    auto flush = [&](Acc (&dst)[FN]) {
+      if constexpr (PARTIAL) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            dst[j][r] = __builtin_fmaf(P[j][r], sp, dst[j][r]);
+          pin(dst[j]);
+        }
+      }
+    };
     if (total > 0) {
-      issue_step(0, true);
+      part_of(0, std::integral_constant<int, 0>());
+      part_of(0, std::integral_constant<int, 1>());
+      part_of(0, std::integral_constant<int, 2>());
+      part_of(0, std::integral_constant<int, 3>());
       step_barrier();
-      if (total > 1)
-        issue_step(1, true);
+      part_of(1, std::integral_constant<int, 0>());
       i32x8_t b[FN];
 #pragma unroll
       for (int j = 0; j < FN; ++j)
         b[j] = read_b(bs, 0, j);
-      float s0 = scale(0, 0);
-      i32x8_t a0;
-      // Row blocks 0 .. FM-2 of the step in stage so, with the A fragment
-      // (and scale) of the next row block read one block ahead; leaves a0/s0
-      // holding the last row block's.
-      auto first_rows = [&](uint32_t so) {
-        a0 = read_a(bs, so, 0);
+      // One step from stage so; more: a following step exists (issue its
+      // remaining loads in row blocks 0..2, the barrier, refill b from sn).
+      auto step = [&](int kt, bool more) {
+        const uint32_t so = (kt & 1) * STAGE, sn = ((kt + 1) & 1) * STAGE;
+        i32x8_t a = read_a(bs, so, 0);
+        float sc = scale(so, 0);
 #pragma unroll
-        for (int i = 0; i < FM - 1; ++i) {
-          const i32x8_t a1 = read_a(bs, so, i + 1);
-          const float s1 = scale(so, i + 1);
-          row_block(a0, b, s0, acc[i]);
-          a0 = a1;
-          s0 = s1;
-          // Keep the prefetch one row block ahead and each block's FMAs
-          // beside its MFMAs: nothing moves across.
+        for (int i = 0; i < FM; ++i) {
+          i32x8_t an;
+          float sn_;
+          if (i + 1 < FM) {
+            an = read_a(bs, so, i + 1);
+            sn_ = scale(so, i + 1);
+          }
+          if (more && i == FM - 1) {
+            step_barrier();
+            part_of(kt + 2, std::integral_constant<int, 0>());
+          }
+          Acc Q[FN];
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            if constexpr (PARTIAL) {
+              Q[j] = mma(b[j], a, Acc{0, 0, 0, 0});
+            } else {
+              acc[i][j] = mma(b[j], a, acc[i][j]);
+            }
+            if (more && i == FM - 1)
+              b[j] = read_b(bs, sn, j);
+          }
+          if (more && i == 0) part_of(kt + 1, std::integral_constant<int, 1>());
+          if (more && i == 1) part_of(kt + 1, std::integral_constant<int, 2>());
+          if (more && i == 2) part_of(kt + 1, std::integral_constant<int, 3>());
+          // FMAs of the previous row block (the last one of the previous step
+          // for i == 0), whose MFMAs have had a row block to finish.
+          flush(acc[i == 0 ? FM - 1 : i - 1]);
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            P[j] = Q[j];
+          sp = sc;
+          if (i + 1 < FM) {
+            a = an;
+            sc = sn_;
+          }
           __builtin_amdgcn_sched_barrier(0);
         }
       };
-      // Every step but the last: straight-line, no exit from the middle (a
-      // branch there lets the compiler sink the scale FMAs past it, holding
-      // every row block's partial products at once).
-      for (int kt = 0; kt + 1 < total; ++kt) {
-        const uint32_t so = (kt & 1) * STAGE, sn = ((kt + 1) & 1) * STAGE;
-        first_rows(so);
-        // Every read of this stage is issued; once they have returned, free it.
-        step_barrier();
-        issue_step(kt + 2, kt + 2 < total);
-        // The last row block; each B fragment is replaced by the next step's
-        // right after its last use here.
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          if constexpr (SCALED) {
-            const Acc part = mma(b[j], a0, Acc{0.f, 0.f, 0.f, 0.f});
-            b[j] = read_b(bs, sn, j);
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              acc[FM - 1][j][r] = __builtin_fmaf(part[r], s0, acc[FM - 1][j][r]);
-            pin(acc[FM - 1][j]);
-          } else {
-            acc[FM - 1][j] = mma(b[j], a0, acc[FM - 1][j]);
-            b[j] = read_b(bs, sn, j);
-          }
-        }
-        s0 = scale(sn, 0);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      first_rows(((total - 1) & 1) * STAGE);
-      row_block(a0, b, s0, acc[FM - 1]);
+      for (int kt = 0; kt + 1 < total; ++kt)
+        step(kt, true);
+      step(total - 1, false);
+      flush(acc[FM - 1]);
+      __builtin_amdgcn_s_waitcnt(0x7 << 4);
     }
     epilogue<MASK_MN>(p, m0, n0, wm, wn, acc);
   }
