@@ -185,8 +185,8 @@ def test_kernel_choice(M, N, K, a, c, sm, kernel):
         # 128-column strips x row slices of 64 x K splits cover the 256 CUs
         slices = -(-M // 64) if M > 64 else 1
         assert p.grid_x == (N // 128) * slices * p.split_k == 256
-        if p.split_k > 1:
-            assert p.workspace_bytes >= p.split_k * M * N * 4
+        # a fixed 64 KiB counter region, then the [split][M][N] int32 partials
+        assert p.workspace_bytes == (65536 + p.split_k * M * N * 4 if p.split_k > 1 else 0)
     assert (p.split_k & (p.split_k - 1)) == 0
 
 

@@ -180,6 +180,17 @@ def test_w8a8_decode_edges(gpu, M, N, K):
     assert np.array_equal(got, ref)
 
 
+def test_w8a8_workspace_across_shapes(gpu):
+    """One cached workspace serves decode launches of different shapes: a launch with more row
+    slices or strips than the last must not read the last one's partials as arrival counters."""
+    for M, N, K in ((16, 8192, 8192), (128, 8192, 8192), (100, 16384, 4096), (16, 8192, 8192),
+                    (128, 8192, 8192)):
+        a, b, sa, sb, got = run_w8a8(gpu, M, N, K, seed=M + N)
+        ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 256, 128),
+                               scale_mode=oracle.SCALE_ROWCOL, sa=sa, sb=sb)
+        assert np.array_equal(got, ref), f"M={M} N={N} K={K}"
+
+
 def test_w8a8_repeat_launches(gpu):
     """The arrival counters carry over between launches: repeat, then change shape."""
     for M, N, K in ((16, 8192, 8192), (16, 8192, 8192), (7, 4096, 2048), (16, 8192, 8192)):

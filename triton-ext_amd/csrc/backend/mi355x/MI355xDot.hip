@@ -232,7 +232,8 @@ int findGemmConfig(int op, int epi, int bm, int bn, int bk) {
 }
 
 bool useDecode(const tx_dot_desc &d) {
-  return d.a_type == TX_I8 && d.scale_mode == TX_SCALE_ROWCOL && d.M <= kDecodeMaxM;
+  return d.a_type == TX_I8 && d.scale_mode == TX_SCALE_ROWCOL && d.M <= kDecodeMaxM &&
+         d.N <= (int64_t)kDecodeMaxStrips * kDecodeStripN;
 }
 
 // Decode row tiling: 16 * MT rows per slice (MT <= 4), ceil(M / 64) slices
@@ -266,9 +267,7 @@ int decodeSplit(int64_t M, int64_t N, int64_t K) {
   return ks;
 }
 
-int64_t decodeCounterBytes(const tx_dot_desc &d) {
-  return ((decodeSlices(d.M) * cdiv(d.N, kDecodeStripN) * 4 + 255) / 256) * 256;
-}
+int64_t decodeCounterBytes(const tx_dot_desc &) { return kDecodeCounterBytes; }
 
 int64_t decodeWorkspace(const tx_dot_desc &d, int ksplit) {
   if (ksplit <= 1)

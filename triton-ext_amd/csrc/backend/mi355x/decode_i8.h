@@ -53,6 +53,12 @@ constexpr int kDecodeStripN = 128;
 constexpr int kDecodeWaves = 4;
 constexpr uint32_t kMaxSplit = 64;
 constexpr int kDecodeMaxM = 256; // 4 row slices of 64
+// The workspace starts with a fixed-size counter region (one counter per
+// (row slice, column strip), for N up to kDecodeMaxStrips * 128), so the
+// counters of one shape never overlap the partials of another that used the
+// same workspace before.
+constexpr int kDecodeMaxStrips = 4096;
+constexpr int64_t kDecodeCounterBytes = (int64_t)(kDecodeMaxM / 64) * kDecodeMaxStrips * 4;
 
 struct DecodeArgs {
   const int8_t *A;
