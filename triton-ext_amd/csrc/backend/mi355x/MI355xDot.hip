@@ -236,10 +236,12 @@ bool useDecode(const tx_dot_desc &d) {
          d.N <= (int64_t)kDecodeMaxStrips * kDecodeStripN;
 }
 
-// Decode row tiling: 16 * MT rows per slice (MT <= 4), ceil(M / 64) slices
-// past 64 rows.
+// Decode row tiling: slices of 16 * MT rows (MT = ceil(M / 16) up to 4), one
+// slice up to M = 64 and slices of 64 beyond.  Slices multiply the B bytes a
+// workgroup streams (fewer splits), so they are used only once M outgrows one
+// wave's accumulators.
 int decodeMT(int64_t M) { return M > 64 ? 4 : (int)cdiv(M > 0 ? M : 1, 16); }
-int decodeSlices(int64_t M) { return M > 64 ? (int)cdiv(M, 64) : 1; }
+int decodeSlices(int64_t M) { return (int)cdiv(M > 0 ? M : 1, 16 * decodeMT(M)); }
 
 // Split-K factor for the decode kernel: a power of two (<= kMaxSplit) so
 // that slices * strips * ksplit workgroups cover the CUs about once, each

@@ -88,7 +88,7 @@ __device__ __forceinline__ i32x4_t mfma_i8_16(const i32x4_t &a, const i32x4_t &b
 
 template <int MT> struct DecodeCfg {
   // Slots per wave: 4 waves x STAGES x 8 KiB of B (A goes to registers).
-  static constexpr int STAGES = 4;
+  static constexpr int STAGES = 5;
   static constexpr int B_BYTES = kDecodeBatchK * kDecodeStripN; // 8 KiB
   static constexpr int SLOT = B_BYTES;
   static constexpr int VM_PER_BATCH = 8 + MT; // B loads into LDS + A loads per batch
@@ -109,10 +109,9 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   __shared__ __attribute__((aligned(1024))) uint8_t st0[STAGE_BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t st1[STAGE_BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t st2[STAGE_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t st3[STAGES > 3 ? STAGE_BYTES : 1];
-  __shared__ uint32_t last_flag;
-  // The epilogue's scales: sb of the strip's columns, sa of the rows.
-  __shared__ float s_sb[kDecodeStripN], s_sa[16 * MT];
+  __shared__ __attribute__((aligned(1024))) uint8_t st3[STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t st4[STAGE_BYTES];
+  static_assert(STAGES == 5, "five ring stages fill the 160 KiB of LDS");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -139,7 +138,7 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   const int Mr = p.M - row0 < 16 * MT ? p.M - row0 : 16 * MT;
   const int8_t *const Ap = p.A + (int64_t)row0 * p.lda;
   const bool n_edge = n0 + kDecodeStripN > p.N;
-  uint8_t *const all_st[4] = {st0, st1, st2, st3};
+  uint8_t *const all_st[5] = {st0, st1, st2, st3, st4};
   uint8_t *slots[STAGES];
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
@@ -248,19 +247,22 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
       __builtin_amdgcn_s_waitcnt((V & 0xf) | ((V >> 4) << 14) | (0x7 << 4) | (0xf << 8));
     else if (newer == 2)
       __builtin_amdgcn_s_waitcnt(((2 * V) & 0xf) | (((2 * V) >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-    else
+    else if (newer == 3)
       __builtin_amdgcn_s_waitcnt(((3 * V) & 0xf) | (((3 * V) >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+    else
+      __builtin_amdgcn_s_waitcnt(((4 * V) & 0xf) | (((4 * V) >> 4) << 14) | (0x7 << 4) | (0xf << 8));
   };
 
-  // Scale loads go out first, one per thread, and are parked in LDS after
-  // the K loop: the epilogue then waits on no memory round trip for them.
-  float scale_v = 0.f;
-  {
-    const int t = tid - kDecodeStripN;
-    if (tid < kDecodeStripN)
-      scale_v = p.sb[n0 + tid < p.N ? n0 + tid : 0];
-    else if (t < 16 * MT)
-      scale_v = p.sa[row0 + (t < Mr ? t : 0)];
+  // The epilogue's scales go out first and wait in registers, so the
+  // epilogue waits on no memory round trip for them.  Element e of this
+  // thread (below) is row 2 e + tid / 128, column tid % 128.
+  constexpr int PER = MT * 16 * kDecodeStripN / (kDecodeWaves * 64); // elements per thread
+  const float sbv = p.sb[n0 + tid % kDecodeStripN < p.N ? n0 + tid % kDecodeStripN : 0];
+  float sav[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const int m = 2 * e + tid / kDecodeStripN;
+    sav[e] = p.sa[row0 + (m < Mr ? m : 0)];
   }
 
   // Prologue: STAGES - 1 batches in flight.  Batch i uses slot and A
@@ -292,34 +294,41 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   }
 
   __builtin_amdgcn_s_waitcnt(0); // every load of the loop has landed
-  if (tid < kDecodeStripN)
-    s_sb[tid] = scale_v;
-  else if (tid - kDecodeStripN < 16 * MT)
-    s_sa[tid - kDecodeStripN] = scale_v;
-  // Sum the 4 waves' accumulators in LDS (stage 0 is free now) with LDS
-  // atomics.  acc[t][j] register r of lane l: row 16 t + 4 (l / 16) + r,
-  // column 16 j + l % 16.
+  // Sum the 4 waves' accumulators through LDS (the ring is free now): wave
+  // w stores its tile into stage w's array with plain stores, then every
+  // thread adds the 4 copies of its elements.  acc[t][j] register r of lane
+  // l: row m = 16 t + 4 (l / 16) + r, column n = 16 j + l % 16; element (m, n)
+  // sits at m * 128 + (n ^ (16 * ((m >> 2) & 3))), so the four 16-lane groups
+  // of one store hit different banks.
   constexpr int TILE = MT * 16 * kDecodeStripN; // int32 of the strip's sums
-  static_assert(TILE * 4 <= STAGE_BYTES, "reduction tile exceeds stage 0");
-  int32_t *red = reinterpret_cast<int32_t *>(st0);
+  static_assert(TILE * 4 <= STAGE_BYTES, "reduction tile exceeds a stage");
+  auto swz = [](int m, int n) { return m * kDecodeStripN + (n ^ (16 * ((m >> 2) & 3))); };
   __syncthreads();
-  for (int i = tid; i < TILE; i += kDecodeWaves * 64)
-    red[i] = 0;
+  {
+    uint8_t *const region = wave == 0 ? st0 : wave == 1 ? st1 : wave == 2 ? st2 : st3;
+    int32_t *mine_tile = reinterpret_cast<int32_t *>(region);
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          mine_tile[swz(16 * t + 4 * G + r, 16 * j + L)] = acc[t][j][r];
+  }
   __syncthreads();
-#pragma unroll
-  for (int t = 0; t < MT; ++t)
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        atomicAdd(&red[(16 * t + 4 * G + r) * kDecodeStripN + 16 * j + L], acc[t][j][r]);
-  __syncthreads();
-
   const int nthreads = kDecodeWaves * 64;
-  auto wg_sum = [&](int i) { return red[i]; };
+  static_assert(kDecodeWaves * 64 == 2 * kDecodeStripN, "element e: row 2 e + tid / 128");
+  // Element e of this thread: i = tid + e * nthreads, (m, n) = (i / 128, i % 128).
+  int32_t wsum[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const int i = tid + e * nthreads;
+    const int q = swz(i / kDecodeStripN, i % kDecodeStripN);
+    wsum[e] = reinterpret_cast<const int32_t *>(st0)[q] + reinterpret_cast<const int32_t *>(st1)[q] +
+              reinterpret_cast<const int32_t *>(st2)[q] + reinterpret_cast<const int32_t *>(st3)[q];
+  }
   // C = bf16((float(sum) * sa[m]) * sb[n]) for this thread's PER elements
   // (element e: i = tid + e * nthreads), scales from LDS.
-  constexpr int PER = MT * 16 * kDecodeStripN / (kDecodeWaves * 64);
   auto epilogue = [&](const int32_t (&sum)[PER]) {
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
@@ -327,15 +336,11 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
       const int m = i / kDecodeStripN, n = i % kDecodeStripN;
       if (m < Mr && n0 + n < p.N)
         p.C[(int64_t)(row0 + m) * p.ldc + n0 + n] =
-            f32_to_bf16_rne(((float)sum[e] * s_sa[m]) * s_sb[n]);
+            f32_to_bf16_rne(((float)sum[e] * sav[e]) * sbv);
     }
   };
   if (p.ksplit == 1) {
-    int32_t sum[PER];
-#pragma unroll
-    for (int e = 0; e < PER; ++e)
-      sum[e] = wg_sum(tid + e * nthreads);
-    epilogue(sum);
+    epilogue(wsum);
     return;
   }
 
@@ -348,10 +353,12 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   // precedes the counter increment, and the last workgroup issues its loads
   // only after its increment has returned.
   int32_t *mine = p.partials + ((int64_t)split * p.M + row0) * p.N;
-  for (int i = tid; i < Mr * kDecodeStripN; i += nthreads) {
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const int i = tid + e * nthreads;
     const int m = i / kDecodeStripN, n = i % kDecodeStripN;
-    if (n0 + n < p.N)
-      __hip_atomic_store(&mine[(int64_t)m * p.N + n0 + n], wg_sum(i), __ATOMIC_RELAXED,
+    if (m < Mr && n0 + n < p.N)
+      __hip_atomic_store(&mine[(int64_t)m * p.N + n0 + n], wsum[e], __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
   }
   __builtin_amdgcn_s_waitcnt(0);
@@ -360,10 +367,11 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
     const uint32_t inc = kMaxSplit / (uint32_t)p.ksplit;
     const uint32_t old = __hip_atomic_fetch_add(&p.counters[slice * strips + strip], inc, __ATOMIC_RELAXED,
                                                 __HIP_MEMORY_SCOPE_AGENT);
-    last_flag = ((old + inc) % kMaxSplit) == 0;
+    // st4 holds no reduction region: its first word carries the flag
+    *reinterpret_cast<volatile uint32_t *>(st4) = ((old + inc) % kMaxSplit) == 0;
   }
   __syncthreads();
-  if (!last_flag)
+  if (!*reinterpret_cast<volatile uint32_t *>(st4))
     return;
   // Last arrival: add every split's partial (its own included, stored
   // above) in split order, then apply the epilogue.  The loads are

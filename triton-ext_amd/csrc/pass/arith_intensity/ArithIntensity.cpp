@@ -117,7 +117,8 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
     if (sa == 2)
       t = chooseTile(kTiles16, d->M, d->N, d->K);
     else if (d->a_type == TX_I8 && d->scale_mode == TX_SCALE_ROWCOL && d->M <= 256)
-      // W8A8 decode: row slices of up to 64, 128-column strips, 64-row K batches
+      // W8A8 decode: one row slice up to M = 64, slices of 64 beyond,
+      // 128-column strips, 64-row K batches
       t = Tile{(int32_t)(d->M > 64 ? 64 : 16 * cdiv(d->M > 0 ? d->M : 1, 16)), 128, 64, 1.0};
     else if (d->a_type == TX_F8E4M3)
       t = kTiles8[0];
