@@ -117,15 +117,12 @@ const GemmConfig kGemmConfigs[] = {
     TX_GEMM_DMA(OP_F16, 256, 256, 64, 4, 2, EPI_F16),
     TX_GEMM_DMA(OP_F16, 128, 128, 64, 2, 2, EPI_F32),
     TX_GEMM_DMA(OP_F16, 128, 128, 64, 2, 2, EPI_F16),
-    // register-staged fallbacks (TX_GEMM16_IMPL=regs) and the 64x64x32 tile
-    TX_GEMM(OP_BF16, 256, 256, 64, 2, 2, EPI_BF16),
-    TX_GEMM(OP_BF16, 256, 256, 64, 2, 2, EPI_F32),
+    // register-staged tiles: the 64x64x32 tile, and 128x128 under
+    // TX_GEMM16_IMPL=regs (a 256x256 tile does not fit this scheme's registers)
     TX_GEMM(OP_BF16, 128, 128, 64, 2, 2, EPI_BF16),
     TX_GEMM(OP_BF16, 128, 128, 64, 2, 2, EPI_F32),
     TX_GEMM(OP_BF16, 64, 64, 32, 2, 2, EPI_BF16),
     TX_GEMM(OP_BF16, 64, 64, 32, 2, 2, EPI_F32),
-    TX_GEMM(OP_F16, 256, 256, 64, 2, 2, EPI_F32),
-    TX_GEMM(OP_F16, 256, 256, 64, 2, 2, EPI_F16),
     TX_GEMM(OP_F16, 128, 128, 64, 2, 2, EPI_F32),
     TX_GEMM(OP_F16, 128, 128, 64, 2, 2, EPI_F16),
     TX_GEMM(OP_F16, 64, 64, 32, 2, 2, EPI_F32),
@@ -136,15 +133,10 @@ const GemmConfig kGemmConfigs[] = {
     TX_GEMM_8(OP_F8, EPI_BLOCK128_BF16),
     TX_GEMM_8(OP_F8, EPI_BLOCK128_F32),
     TX_GEMM_8(OP_F8, EPI_F32),
-    // int8 operands, int32 accumulation
-    TX_GEMM(OP_I8, 256, 256, 128, 2, 4, EPI_I32),
-    TX_GEMM(OP_I8, 256, 256, 128, 2, 4, EPI_ROWCOL_BF16),
+    // int8 operands, int32 accumulation, 128x128x128 register-staged tiles
     TX_GEMM(OP_I8, 128, 128, 128, 2, 2, EPI_I32),
     TX_GEMM(OP_I8, 128, 128, 128, 2, 2, EPI_ROWCOL_BF16),
-    // fp8 e4m3 operands, fp32 accumulation
-    TX_GEMM(OP_F8, 256, 256, 128, 2, 4, EPI_BLOCK128_BF16),
-    TX_GEMM(OP_F8, 256, 256, 128, 2, 4, EPI_BLOCK128_F32),
-    TX_GEMM(OP_F8, 256, 256, 128, 2, 4, EPI_F32),
+    // fp8 e4m3 operands, fp32 accumulation, 128x128x128 register-staged tiles
     TX_GEMM(OP_F8, 128, 128, 128, 2, 2, EPI_BLOCK128_BF16),
     TX_GEMM(OP_F8, 128, 128, 128, 2, 2, EPI_BLOCK128_F32),
     TX_GEMM(OP_F8, 128, 128, 128, 2, 2, EPI_F32),
@@ -215,15 +207,10 @@ int findGemmConfig(int op, int epi, int bm, int bn, int bk) {
       return 4;
     return 2;
   }();
-  // TX_GEMM8_IMPL=tile: the register-staged 8-bit tiles instead of gemm8_w4.
-  static const bool old8 = [] {
-    const char *e = std::getenv("TX_GEMM8_IMPL");
-    return e && std::strcmp(e, "tile") == 0;
-  }();
   const bool is8 = op == OP_I8 || op == OP_F8;
   for (int i = 0; i < kNumGemmConfigs; ++i) {
     const GemmConfig &c = kGemmConfigs[i];
-    if (is8 ? (c.dma == 5 && old8) : (c.dma > want || (c.dma >= 2 && c.dma != want)))
+    if (!is8 && (c.dma > want || (c.dma >= 2 && c.dma != want)))
       continue;
     if (c.op == op && c.epi == epi && c.bm == bm && c.bn == bn && c.bk == bk)
       return i;
