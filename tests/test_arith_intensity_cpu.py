@@ -50,6 +50,9 @@ def test_tile_choice():
     assert (small.block_m, small.block_n, small.block_k) == (64, 64, 32)
     fixed = tx.arith_intensity(tx.make_desc(512, 512, 512, tx.F16, tx.F32, block=(128, 128, 64)))
     assert (fixed.block_m, fixed.block_n, fixed.block_k) == (128, 128, 64)
+    c5 = tx.arith_intensity(tx.make_desc(2048, 7168, 7168, tx.F8E4M3, tx.BF16,
+                                         scale_mode=tx.SCALE_BLOCK128))
+    assert (c5.block_m, c5.block_n, c5.block_k) == (256, 256, 128)
 
 
 def test_rejects_bad_desc():

@@ -239,7 +239,7 @@ def test_c5_fp8_block_scaled(gpu, M, N, K):
 @pytest.mark.parametrize("kind,out", [("i8", "rowcol"), ("f8", "f32"), ("f8", "block_f32"),
                                       ("f8", "block_bf16")])
 @pytest.mark.parametrize("M,N,K", [(512, 512, 1024), (300, 272, 400), (16, 1024, 256)])
-@pytest.mark.parametrize("blk", [(256, 256, 128), (128, 128, 128)])
+@pytest.mark.parametrize("blk", [(256, 256, 128), (256, 224, 128), (128, 128, 128)])
 def test_8bit_tile_epilogues(gpu, kind, out, M, N, K, blk):
     """Each epilogue of the 8-bit tile kernels, whole and edge tiles (M, N
     not multiples of the tile; K not a multiple of 128: a masked last step).
@@ -304,10 +304,11 @@ def test_golden_fixture_on_gpu(gpu, name):
     golden_on_gpu(gpu, name, None)
 
 
+@pytest.mark.parametrize("tile", [(256, 256, 128), (256, 224, 128)])
 @pytest.mark.parametrize("name", ["int8_i32", "fp8_block128_f32_exact", "fp8_block128_bf16_normal"])
-def test_golden_fixture_256_tile(gpu, name):
-    """The 8-bit fixtures through the 256x256x128 tile kernel (8 waves)."""
-    golden_on_gpu(gpu, name, (256, 256, 128))
+def test_golden_fixture_256_tile(gpu, name, tile):
+    """The 8-bit fixtures through the 256-row tile kernels (8 waves)."""
+    golden_on_gpu(gpu, name, tile)
 
 
 def golden_on_gpu(gpu, name, tile):
@@ -343,6 +344,7 @@ def golden_on_gpu(gpu, name, tile):
                            scale_mode=sm, sa=f.get("sa"), sb=f.get("sb"),
                            round_mode=oracle.ROUND_RNE)
     if bool(f["exact"]) and at == "f8e4m3" and sm == oracle.SCALE_BLOCK128 and blk[0] == 256:
+        # (both 256-row tiles: 256x256 and 256x224)
         # The 256-wide fp8 tile applies a block's scales as one fma(part,
         # sa*sb, acc) (two roundings) where the interpreter rounds
         # part*sa, then *sb, then the sum (three): per K block, the two

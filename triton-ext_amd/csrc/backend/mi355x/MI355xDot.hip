@@ -25,6 +25,7 @@
 #include "gemm16_dma.h"
 #include "gemm16_pp.h"
 #include "gemm8_w4.h"
+#include "gemm8_n224.h"
 #include "gemm16_w4.h"
 #include "gemm_tile.h"
 
@@ -92,6 +93,8 @@ struct GemmConfig {
 
 #define TX_GEMM_8(OP, EPI)                                                     \
   GemmConfig { OP, 256, 256, 128, 2, 4, EPI, gemm8_w4_kernel<OP, EPI>, 0, 5 }
+#define TX_GEMM_8N(OP, EPI)                                                    \
+  GemmConfig { OP, 256, 224, 128, 4, 2, EPI, gemm8_n224_kernel<OP, EPI>, 0, 5 }
 
 // Lookup takes the first match among the entries the tuning override
 // allows (findGemmConfig): by default the 4-wave 256x256 tile, then the
@@ -133,6 +136,12 @@ const GemmConfig kGemmConfigs[] = {
     TX_GEMM_8(OP_F8, EPI_BLOCK128_BF16),
     TX_GEMM_8(OP_F8, EPI_BLOCK128_F32),
     TX_GEMM_8(OP_F8, EPI_F32),
+    // the same with 256x224 tiles (gemm8_n224.h)
+    TX_GEMM_8N(OP_I8, EPI_I32),
+    TX_GEMM_8N(OP_I8, EPI_ROWCOL_BF16),
+    TX_GEMM_8N(OP_F8, EPI_BLOCK128_BF16),
+    TX_GEMM_8N(OP_F8, EPI_BLOCK128_F32),
+    TX_GEMM_8N(OP_F8, EPI_F32),
     // int8 operands, int32 accumulation, 128x128x128 register-staged tiles
     TX_GEMM(OP_I8, 128, 128, 128, 2, 2, EPI_I32),
     TX_GEMM(OP_I8, 128, 128, 128, 2, 2, EPI_ROWCOL_BF16),

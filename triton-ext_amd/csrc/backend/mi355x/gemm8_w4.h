@@ -331,18 +331,25 @@ template <int OP, int EPI> struct Gemm8W4 {
   template <bool MASK_MN>
   __device__ __forceinline__ static void epilogue(const GemmArgs &p, int64_t m0, int64_t n0,
                                                   int wm, int wn, const Acc (&acc)[FM][FN]) {
+    epilogue_t<MASK_MN, FM, FN, WTM, WTN>(p, m0, n0, wm, wn, acc);
+  }
+  // The same for a wave tile of FM_ x FN_ blocks of 16x16 (WTM_ x WTN_).
+  template <bool MASK_MN, int FM_, int FN_, int WTM_, int WTN_>
+  __device__ __forceinline__ static void epilogue_t(const GemmArgs &p, int64_t m0, int64_t n0,
+                                                    int wm, int wn,
+                                                    const Acc (&acc)[FM_][FN_]) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int64_t row = m0 + wm * WTM + 16 * i + (lane & 15);
+    for (int i = 0; i < FM_; ++i) {
+      const int64_t row = m0 + wm * WTM_ + 16 * i + (lane & 15);
       if (MASK_MN && row >= p.M)
         continue;
       float sar = 1.f;
       if (EPI == EPI_ROWCOL_BF16)
         sar = p.sa[row];
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int64_t col = n0 + wn * WTN + 16 * j + 4 * (lane >> 4);
+      for (int j = 0; j < FN_; ++j) {
+        const int64_t col = n0 + wn * WTN_ + 16 * j + 4 * (lane >> 4);
         if (MASK_MN && col >= p.N) // N % 16 == 0: the quad is all in or all out
           continue;
         const int64_t off = row * p.ldc + col;

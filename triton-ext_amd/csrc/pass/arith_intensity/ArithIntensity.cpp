@@ -35,6 +35,9 @@ struct Tile {
 // weight only: it ranks tiles by how well they amortise LDS fills.
 const Tile kTiles16[] = {{256, 256, 64, 0.85}, {128, 128, 64, 0.60},
                          {64, 64, 32, 0.35}};
+// 8-bit tiles.  (A 256x224 tile also exists for explicit requests: it fills
+// all CUs at N = 7168, but its A-resident wave layout needs 28 transposed B
+// reads per step against 16, and measured no faster than 256x256 there.)
 const Tile kTiles8[] = {{256, 256, 128, 0.85}, {128, 128, 128, 0.60}};
 
 // Estimated time of a tiled dot in arbitrary units: whole waves of tiles
@@ -121,7 +124,7 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
       // 128-column strips, 64-row K batches
       t = Tile{(int32_t)(d->M > 64 ? 64 : 16 * cdiv(d->M > 0 ? d->M : 1, 16)), 128, 64, 1.0};
     else if (d->a_type == TX_F8E4M3)
-      t = kTiles8[0];
+      t = kTiles8[0]; // the register-staged 128x128 tile is slower everywhere
     else
       t = chooseTile(kTiles8, d->M, d->N, d->K);
   }
