@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
                     help="secondary workloads to run, comma-separated: vendor, tail, w8a8 (or "
-                         "w8a8_1, w8a8_16, w8a8_64, w8a8_256), fp8 (default: all); the bf16 "
+                         "w8a8_1, w8a8_16, w8a8_64, w8a8_256), fp8, kmajor (default: all); the bf16 "
                          "headline always runs")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 256 MiB five times (a transfer of known size that scales the "
@@ -163,6 +163,20 @@ def bench_bf16(tx, dev, M, N, K, steps, warmup, seed=1):
                           bound="mfma" if p.bound == tx.BOUND_MFMA else "hbm")), (a, b, c)
 
 
+def bench_bf16_kmajor(tx, dev, M, N, K, steps, warmup, seed=1):
+    """The same dot with B stored K-major ([N, K] row-major, passed as its transpose):
+    the q @ k.T layout of attention."""
+    import torch
+    a, b = bf16_inputs(M, N, K, dev, seed)
+    bt = b.t().contiguous().t()   # same values, K-major storage
+    c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    run = Launcher(tx, a, bt, c)
+    ms = time_back_to_back(run, steps, warmup)
+    flops = 2.0 * M * N * K
+    return dict(workload=f"bf16 {M}x{N}x{K}, B K-major (q @ k.T)", ms=ms, tflops=flops / ms / 1e9,
+                frac=flops / ms / 1e-3 / PEAK_BF16)
+
+
 def bench_vendor_bf16(dev, M, N, K, steps, warmup, seed=1):
     """hipBLASLt (torch.matmul) on the same workload and timing: a reference point only."""
     import torch
@@ -276,6 +290,10 @@ def main():
     secondary = []
     if want("vendor"):
         r = bench_vendor_bf16(dev, M, N, K, args.steps, args.warmup)
+        secondary.append(r)
+        print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    if want("kmajor"):
+        r = bench_bf16_kmajor(tx, dev, M, N, K, args.steps, args.warmup)
         secondary.append(r)
         print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
     flush = make_flush(dev)

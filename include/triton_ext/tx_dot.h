@@ -78,19 +78,24 @@ typedef enum tx_status {
 
 typedef enum tx_kernel {
   TX_KERNEL_NONE = 0,
-  TX_KERNEL_GEMM_16BIT = 1, /* bf16/fp16 MFMA 32x32x16, LDS-staged       */
-  TX_KERNEL_GEMM_I8 = 2,    /* int8 MFMA 32x32x32, LDS-staged            */
-  TX_KERNEL_DECODE_I8 = 3,  /* int8 small-M streaming, MFMA 16x16x64     */
-  TX_KERNEL_GEMM_F8 = 4,    /* fp8 e4m3 MFMA 32x32x64, block scales      */
+  TX_KERNEL_GEMM_16BIT = 1, /* bf16/fp16 tile, MFMA 32x32x16, LDS-staged          */
+  TX_KERNEL_GEMM_I8 = 2,    /* int8 tile, MFMA 16x16x64 (32x32x32 small tiles)   */
+  TX_KERNEL_DECODE_I8 = 3,  /* int8 W8A8 M <= 256 streaming, MFMA 16x16x64       */
+  TX_KERNEL_GEMM_F8 = 4,    /* fp8 e4m3 tile, MFMA 16x16x128 (32x32x64 small)    */
 } tx_kernel;
 
 /* Bit flags for tx_dot_desc.flags */
 #define TX_FLAG_NO_LOOP_SPLIT 0x1 /* run every K step masked (no peeling) */
+/* B is stored K-major: [N][K] row-major with row stride ldb (0 = K), the
+ * layout of tl.dot(q, tl.trans(k)) / q @ k.T with k row-major.  Supported for
+ * bf16/fp16 operands on the 256x256x64 tile. */
+#define TX_FLAG_B_KMAJOR 0x2
 
 typedef struct tx_dot_desc {
   int64_t M, N, K;
-  /* Row strides in elements of A [M,K], B [K,N], C [M,N] (all row-major);
-   * 0 means packed (K, N, N).  Row strides in bytes must be multiples of 16. */
+  /* Row strides in elements of A [M,K], B [K,N], C [M,N] (all row-major;
+   * B [N][K] with TX_FLAG_B_KMAJOR); 0 means packed (K, N or K, N).  Row
+   * strides in bytes must be multiples of 16. */
   int64_t lda, ldb, ldc;
   int32_t a_type, b_type, c_type; /* tx_dtype */
   int32_t scale_mode;             /* tx_scale_mode */

@@ -190,6 +190,23 @@ def test_kernel_choice(M, N, K, a, c, sm, kernel):
     assert (p.split_k & (p.split_k - 1)) == 0
 
 
+def test_b_kmajor_plans():
+    """K-major B (q @ k.T): bf16/fp16 on the 256x256x64 tile, ldb defaulting to K."""
+    p = tx.plan(tx.make_desc(512, 384, 192, tx.BF16, tx.F32, flags=tx.FLAG_B_KMAJOR))
+    assert p.kernel == tx.KERNEL_GEMM_16BIT
+    assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (256, 256, 64)
+    assert p.desc.ldb == 192 and p.block_threads == 256
+    assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, ldb=32,
+                             flags=tx.FLAG_B_KMAJOR)) == tx.ERR_INVALID  # ldb < K
+    assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, block=(128, 128, 64),
+                             flags=tx.FLAG_B_KMAJOR)) == tx.ERR_UNSUPPORTED
+    for a, c, sm in ((tx.I8, tx.I32, 0), (tx.F8E4M3, tx.F32, 0),
+                     (tx.I8, tx.BF16, tx.SCALE_ROWCOL)):
+        assert _err(tx.make_desc(16, 256, 256, a, c, scale_mode=sm,
+                                 flags=tx.FLAG_B_KMAJOR)) == tx.ERR_UNSUPPORTED
+    assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, flags=0x10)) == tx.ERR_INVALID
+
+
 def test_launch_without_device_fails_cleanly():
     import torch
     if torch.cuda.is_available():

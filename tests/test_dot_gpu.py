@@ -111,6 +111,37 @@ def test_16bit_edges(gpu, M, N, K, block, kind, out):
                 what=f"{kind} {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K,kind,out", [(1024, 1024, 1024, "bf16", "bf16"),
+                                             (300, 520, 200, "bf16", "f32"),
+                                             (256, 256, 64, "f16", "f32"),
+                                             (4096, 4096, 4000, "bf16", "bf16"),
+                                             (1000, 1000, 1000, "f16", "f16")])
+def test_b_kmajor(gpu, M, N, K, kind, out):
+    """q @ k.T: B passed as the transpose of a row-major [N, K] tensor."""
+    import torch
+    say(f"K-major B {kind}->{out} M={M} N={N} K={K}")
+    gen = normal_bf16 if kind == "bf16" else normal_f16
+    a = gen((M, K), k_norm(K), M + 1)
+    bt = gen((N, K), k_norm(K), N + 2)                     # [N, K] row-major
+    tdt = torch.bfloat16 if kind == "bf16" else torch.float16
+    odt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[out]
+    da = to_device(a, gpu).view(tdt)
+    db = to_device(bt, gpu).view(tdt).t()                  # [K, N] view, K-major
+    assert db.stride() == (1, K)
+    c = tx.dot(da, db, out_dtype=odt)
+    torch.cuda.synchronize()
+    got = from_device(c)
+    at = oracle.BF16 if kind == "bf16" else oracle.F16
+    ct = {"bf16": oracle.BF16, "f16": oracle.F16, "f32": oracle.F32}[out]
+    ref = oracle.tiled_dot(a, np.ascontiguousarray(bt.T), a_type=at, c_type=ct,
+                           block=(256, 256, 64), round_mode=oracle.ROUND_RNE)
+    if out == "f32":
+        check_close(got, ref, atol=ATOL, rtol=RTOL, what="K-major B")
+    else:
+        check_close(bits_to_f32(got, out), bits_to_f32(ref, out), atol=ATOL, rtol=RTOL,
+                    what="K-major B")
+
+
 def test_strided_a(gpu):
     a, b, got = run_16bit(gpu, 200, 256, 192, "bf16", "f32", block=(128, 128, 64), lda=256)
     ref = oracle_16bit(a, b, "bf16", "f32", (128, 128, 64))
@@ -311,7 +342,14 @@ def test_golden_fixture_256_tile(gpu, name, tile):
     golden_on_gpu(gpu, name, tile)
 
 
-def golden_on_gpu(gpu, name, tile):
+@pytest.mark.parametrize("name", ["c1_fp16_512", "fp16_f32_edges_exact", "fp16_f16_rne_exact",
+                                  "bf16_bf16_rtz_exact", "bf16_f32_normal"])
+def test_golden_fixture_b_kmajor(gpu, name):
+    """The 16-bit fixtures with B stored K-major ([N, K] row-major)."""
+    golden_on_gpu(gpu, name, (256, 256, 64), b_kmajor=True)
+
+
+def golden_on_gpu(gpu, name, tile, b_kmajor=False):
     import os
     import torch
     from test_oracle_cpu import GOLDEN, OR_TYPE, fixture_output, load_fixture
@@ -324,7 +362,10 @@ def golden_on_gpu(gpu, name, tile):
            "i32": torch.int32}[ct]
     view = {"f16": torch.int16, "bf16": torch.int16, "f8e4m3": torch.uint8, "i8": torch.int8}[at]
     da = to_device(f["a"], gpu).view(view).view(tdt)
-    db = to_device(f["b"], gpu).view(view).view(tdt)
+    if b_kmajor:
+        db = to_device(np.ascontiguousarray(f["b"].T), gpu).view(view).view(tdt).t()
+    else:
+        db = to_device(f["b"], gpu).view(view).view(tdt)
     kw = {}
     if "sa" in f:
         kw = dict(scale_a=to_device(f["sa"], gpu), scale_b=to_device(f["sb"], gpu))

@@ -64,6 +64,7 @@ typedef void (*GemmKernelFn)(GemmArgs);
 struct GemmConfig {
   int op, bm, bn, bk, wm, wn, epi;
   GemmKernelFn fn;
+  int bt;        // B K-major (TX_FLAG_B_KMAJOR)
   int lds_bytes; // dynamic LDS (0 for kernels with static LDS)
   int dma;       // 1: direct-to-LDS staging + transpose reads (gemm16_dma.h),
                  // 2: the same staging with 4 waves of 128x128 (gemm16_w4.h),
@@ -74,27 +75,29 @@ struct GemmConfig {
 #define TX_GEMM(OP, BM, BN, BK, WM, WN, EPI)                                   \
   GemmConfig {                                                                 \
     OP, BM, BN, BK, WM, WN, EPI, gemm_tile_kernel<OP, BM, BN, BK, WM, WN, EPI>,\
-        GemmTile<OP, BM, BN, BK, WM, WN, EPI>::LDS_BYTES, 0                    \
+        0, GemmTile<OP, BM, BN, BK, WM, WN, EPI>::LDS_BYTES, 0                 \
   }
 #define TX_GEMM_DMA_S(OP, BM, BN, BK, WM, WN, ST, EPI)                         \
   GemmConfig {                                                                 \
     OP, BM, BN, BK, WM, WN, EPI,                                               \
-        gemm16_dma_kernel<OP, BM, BN, BK, WM, WN, ST, EPI>, 0, 1               \
+        gemm16_dma_kernel<OP, BM, BN, BK, WM, WN, ST, EPI>, 0, 0, 1            \
   }
 #define TX_GEMM_DMA(OP, BM, BN, BK, WM, WN, EPI)                               \
   TX_GEMM_DMA_S(OP, BM, BN, BK, WM, WN, 2, EPI)
 
 #define TX_GEMM_W4(OP, EPI)                                                    \
-  GemmConfig { OP, 256, 256, 64, 2, 2, EPI, gemm16_w4_kernel<OP, EPI, 4>, 0, 2 }
+  GemmConfig { OP, 256, 256, 64, 2, 2, EPI, gemm16_w4_kernel<OP, EPI, 4>, 0, 0, 2 }
+#define TX_GEMM_W4T(OP, EPI)                                                   \
+  GemmConfig { OP, 256, 256, 64, 2, 2, EPI, gemm16_w4_kernel<OP, EPI, 4, true>, 1, 0, 2 }
 #define TX_GEMM_W8(OP, EPI)                                                    \
-  GemmConfig { OP, 256, 256, 64, 2, 4, EPI, gemm16_w4_kernel<OP, EPI, 8>, 0, 3 }
+  GemmConfig { OP, 256, 256, 64, 2, 4, EPI, gemm16_w4_kernel<OP, EPI, 8>, 0, 0, 3 }
 #define TX_GEMM_PP(OP, EPI)                                                    \
-  GemmConfig { OP, 256, 256, 64, 2, 4, EPI, gemm16_pp_kernel<OP, EPI>, 0, 4 }
+  GemmConfig { OP, 256, 256, 64, 2, 4, EPI, gemm16_pp_kernel<OP, EPI>, 0, 0, 4 }
 
 #define TX_GEMM_8(OP, EPI)                                                     \
-  GemmConfig { OP, 256, 256, 128, 2, 4, EPI, gemm8_w4_kernel<OP, EPI>, 0, 5 }
+  GemmConfig { OP, 256, 256, 128, 2, 4, EPI, gemm8_w4_kernel<OP, EPI>, 0, 0, 5 }
 #define TX_GEMM_8N(OP, EPI)                                                    \
-  GemmConfig { OP, 256, 224, 128, 4, 2, EPI, gemm8_n224_kernel<OP, EPI>, 0, 5 }
+  GemmConfig { OP, 256, 224, 128, 4, 2, EPI, gemm8_n224_kernel<OP, EPI>, 0, 0, 5 }
 
 // Lookup takes the first match among the entries the tuning override
 // allows (findGemmConfig): by default the 4-wave 256x256 tile, then the
@@ -110,6 +113,11 @@ const GemmConfig kGemmConfigs[] = {
     TX_GEMM_W4(OP_BF16, EPI_F32),
     TX_GEMM_W4(OP_F16, EPI_F32),
     TX_GEMM_W4(OP_F16, EPI_F16),
+    // the same with B K-major (TX_FLAG_B_KMAJOR)
+    TX_GEMM_W4T(OP_BF16, EPI_BF16),
+    TX_GEMM_W4T(OP_BF16, EPI_F32),
+    TX_GEMM_W4T(OP_F16, EPI_F32),
+    TX_GEMM_W4T(OP_F16, EPI_F16),
     TX_GEMM_PP(OP_BF16, EPI_BF16),
     // bf16 / fp16 operands: direct-to-LDS staging, 8 waves (4x2) per 256x256
     TX_GEMM_DMA(OP_BF16, 256, 256, 64, 4, 2, EPI_BF16),
@@ -196,7 +204,7 @@ void classify(const tx_dot_desc &d, int *op, int *epi) {
   }
 }
 
-int findGemmConfig(int op, int epi, int bm, int bn, int bk) {
+int findGemmConfig(int op, int epi, int bm, int bn, int bk, bool bt) {
   // Tuning override TX_GEMM16_IMPL: "regs" (register staging), "dma8"
   // (8-wave direct-to-LDS), "w8" (8 waves of 128x64), "pp" (ping-pong);
   // default: 4 waves of 128x128 (fastest of these at 4096^3 on MI355X).
@@ -219,9 +227,11 @@ int findGemmConfig(int op, int epi, int bm, int bn, int bk) {
   const bool is8 = op == OP_I8 || op == OP_F8;
   for (int i = 0; i < kNumGemmConfigs; ++i) {
     const GemmConfig &c = kGemmConfigs[i];
-    if (!is8 && (c.dma > want || (c.dma >= 2 && c.dma != want)))
+    // (K-major B has one kernel, outside the tuning override)
+    if (!is8 && !bt && (c.dma > want || (c.dma >= 2 && c.dma != want)))
       continue;
-    if (c.op == op && c.epi == epi && c.bm == bm && c.bn == bn && c.bk == bk)
+    if (c.op == op && c.epi == epi && c.bm == bm && c.bn == bn && c.bk == bk &&
+        c.bt == (int)bt)
       return i;
   }
   return -1;
@@ -229,6 +239,7 @@ int findGemmConfig(int op, int epi, int bm, int bn, int bk) {
 
 bool useDecode(const tx_dot_desc &d) {
   return d.a_type == TX_I8 && d.scale_mode == TX_SCALE_ROWCOL && d.M <= kDecodeMaxM &&
+         !(d.flags & TX_FLAG_B_KMAJOR) &&
          d.N <= (int64_t)kDecodeMaxStrips * kDecodeStripN;
 }
 
@@ -295,7 +306,11 @@ int txMi355xDotRun(tx_dot_plan *plan) {
     plan->passes_run += 1;
     return TX_OK;
   }
-  const int ci = findGemmConfig(op, epi, d.block_m, d.block_n, d.block_k);
+  const int ci = findGemmConfig(op, epi, d.block_m, d.block_n, d.block_k,
+                                (d.flags & TX_FLAG_B_KMAJOR) != 0);
+  if (ci < 0 && (d.flags & TX_FLAG_B_KMAJOR))
+    return fail(TX_ERR_UNSUPPORTED,
+                "K-major B is implemented for bf16/fp16 on the 256x256x64 tile only");
   if (ci < 0)
     return fail(TX_ERR_UNSUPPORTED, "no instantiated tile %dx%dx%d for this dtype",
                 d.block_m, d.block_n, d.block_k);
@@ -325,11 +340,14 @@ int validate(const tx_dot_desc *in, tx_dot_desc *d) {
                 sc = tx_dtype_size(d->c_type);
   if (!sa || !sb || !sc)
     return fail(TX_ERR_INVALID, "unknown dtype");
+  const bool bt = (d->flags & TX_FLAG_B_KMAJOR) != 0;
   if (d->lda == 0) d->lda = d->K;
-  if (d->ldb == 0) d->ldb = d->N;
+  if (d->ldb == 0) d->ldb = bt ? d->K : d->N;
   if (d->ldc == 0) d->ldc = d->N;
-  if (d->lda < d->K || d->ldb < d->N || d->ldc < d->N)
+  if (d->lda < d->K || d->ldb < (bt ? d->K : d->N) || d->ldc < d->N)
     return fail(TX_ERR_INVALID, "row stride shorter than the row");
+  if (d->flags & ~(TX_FLAG_NO_LOOP_SPLIT | TX_FLAG_B_KMAJOR))
+    return fail(TX_ERR_INVALID, "unknown flags 0x%x", d->flags);
   if ((d->lda * sa) % 16 || (d->ldb * sb) % 16 || (d->ldc * sc) % 16)
     return fail(TX_ERR_INVALID, "A/B/C row strides must be multiples of 16 bytes");
   if ((d->K * sa) % 16 || (d->N * sb) % 16)
@@ -414,7 +432,8 @@ int launchGemm(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   const tx_dot_desc &d = plan.desc;
   int op, epi;
   classify(d, &op, &epi);
-  const int ci = findGemmConfig(op, epi, d.block_m, d.block_n, d.block_k);
+  const int ci = findGemmConfig(op, epi, d.block_m, d.block_n, d.block_k,
+                                (d.flags & TX_FLAG_B_KMAJOR) != 0);
   if (ci < 0)
     return fail(TX_ERR_UNSUPPORTED, "plan names a tile that is not instantiated");
   const GemmConfig &c = kGemmConfigs[ci];

@@ -45,7 +45,10 @@ __device__ __forceinline__ i32x4_t make_rsrc(const void *base, uint32_t bytes) {
   return r;
 }
 
-template <int OP, int EPI, int NW = 4> struct Gemm16W4 {
+// BT: B is stored K-major ([N][K] row-major, row stride ldb), the layout of
+// q . k^T with k row-major.  Its tile is staged exactly like A's (rows of 64
+// K values, same swizzle) and read with ds_read_b128 instead of transposes.
+template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
   static constexpr int BM = 256, BN = 256, BK = 64;
   // NW = 4: 2x2 waves of 128x128; NW = 8: 2x4 waves of 128x64.
   static constexpr int WM = 2, WN = NW / 2;
@@ -77,7 +80,24 @@ template <int OP, int EPI, int NW = 4> struct Gemm16W4 {
                                                 ((c ^ ((row ^ (row >> 3)) & (NCA - 1))) << 4));
     }
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
+    for (int j = 0; j < FN; ++j)
+      read_b_frag(bs, ks, wn, j, f);
+  }
+
+  // B fragment j of sub-step ks: lane l holds column n = l % 32 of block j,
+  // K values 8 (l / 32) .. +7 of the sub-step.  Row-major B: two transposed
+  // reads; K-major B: one 16-byte read, as for A.
+  __device__ __forceinline__ static void read_b_frag(const uint8_t *bs, int ks, int wn, int j,
+                                                     Frags &f) {
+    const int lane = threadIdx.x & 63;
+    if constexpr (BT) {
+      const int row = wn * WTN + j * 32 + (lane & 31);
+      const int c = ks * 2 + (lane >> 5);
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(
+          bs + row * RA + ((c ^ ((row ^ (row >> 3)) & (NCA - 1))) << 4));
+      f.b[j] = __builtin_bit_cast(i16x8_t, v);
+    } else {
+      const int G = lane >> 4, L = lane & 15;
       const int n = wn * WTN + j * 32 + 16 * (G & 1) + 4 * (L & 3);
       const int k = ks * 16 + 8 * (G >> 1) + (L >> 2), k4 = k + 4;
       const uint32_t off0 = k * RBB + (((n >> 3) ^ (4 * (k & 3))) << 4) + (n & 7) * 2;
@@ -108,7 +128,9 @@ template <int OP, int EPI, int NW = 4> struct Gemm16W4 {
   struct Offsets {
     uint32_t a[Stage::A_DMA]; // A: ((m0 + row) * lda + c * 8) * 2, or kOOB
     uint32_t b[Stage::B_DMA]; // B: (k * ldb + n0 + c * 8) * 2, or kOOB
+                              // (BT: ((n0 + row) * ldb + c * 8) * 2)
     int32_t ak[Stage::A_DMA]; // A: K index of the chunk within a step
+    int32_t bk[BT ? Stage::B_DMA : 1]; // BT: the same for B
   };
 
   // Offsets of the loads that staging wave `wave` (0..NW-1) issues.
@@ -129,9 +151,17 @@ template <int OP, int EPI, int NW = 4> struct Gemm16W4 {
     for (int i = 0; i < Stage::B_DMA; ++i) {
       const int j = wave * Stage::B_DMA + i;
       const int g = j * 64 + lane;
-      const int k = g / Stage::NCB, pc = g % Stage::NCB;
-      const int c = pc ^ (4 * (k & 3));
-      o.b[i] = (MASK_MN && n0 + c * 8 >= p.N) ? kOOB : (uint32_t)((k * p.ldb + n0 + c * 8) * 2);
+      if constexpr (BT) { // the A scheme over B's N rows
+        const int row = g / NCA, pc = g % NCA;
+        const int c = pc ^ ((row ^ (row >> 3)) & (NCA - 1));
+        o.bk[i] = c * 8;
+        o.b[i] = (MASK_MN && n0 + row >= p.N) ? kOOB
+                                               : (uint32_t)(((n0 + row) * p.ldb + c * 8) * 2);
+      } else {
+        const int k = g / Stage::NCB, pc = g % Stage::NCB;
+        const int c = pc ^ (4 * (k & 3));
+        o.b[i] = (MASK_MN && n0 + c * 8 >= p.N) ? kOOB : (uint32_t)((k * p.ldb + n0 + c * 8) * 2);
+      }
     }
   }
 
@@ -205,16 +235,7 @@ template <int OP, int EPI, int NW = 4> struct Gemm16W4 {
       f.a[u] = *reinterpret_cast<const u32x4 *>(as + row * RA +
                                                 ((c ^ ((row ^ (row >> 3)) & (NCA - 1))) << 4));
     } else {
-      const int j = u - FM;
-      const int n = wn * WTN + j * 32 + 16 * (G & 1) + 4 * (L & 3);
-      const int k = ks * 16 + 8 * (G >> 1) + (L >> 2), k4 = k + 4;
-      const uint32_t off0 = k * RBB + (((n >> 3) ^ (4 * (k & 3))) << 4) + (n & 7) * 2;
-      const uint32_t off1 = k4 * RBB + (((n >> 3) ^ (4 * (k4 & 3))) << 4) + (n & 7) * 2;
-      const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_i16x4 *)((__attribute__((address_space(3))) uint8_t *)bs + off0));
-      const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_i16x4 *)((__attribute__((address_space(3))) uint8_t *)bs + off1));
-      f.b[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      read_b_frag(bs, ks, wn, u - FM, f);
     }
   }
 
@@ -240,10 +261,16 @@ template <int OP, int EPI, int NW = 4> struct Gemm16W4 {
     } else {
       const int q = idx - Stage::A_DMA;
       uint32_t v = o.b[q];
-      if (MASK_K && !live)
-        v = kOOB;
-      buffer_lds16(v, rb, (uint32_t)((int64_t)k0 * p.ldb * 2),
-                   st + A_BYTES + (wave * Stage::B_DMA + q) * 1024);
+      if constexpr (BT) {
+        if (MASK_K && (!live || k0 + o.bk[q] >= p.K))
+          v = kOOB;
+        buffer_lds16(v, rb, (uint32_t)k0 * 2u, st + A_BYTES + (wave * Stage::B_DMA + q) * 1024);
+      } else {
+        if (MASK_K && !live)
+          v = kOOB;
+        buffer_lds16(v, rb, (uint32_t)((int64_t)k0 * p.ldb * 2),
+                     st + A_BYTES + (wave * Stage::B_DMA + q) * 1024);
+      }
     }
   }
 
@@ -282,7 +309,8 @@ template <int OP, int EPI, int NW = 4> struct Gemm16W4 {
     auto stage_ptr = [&](int kt) { return smem + (kt & 1) * STAGE; };
     auto stage_addr = [&](int kt) { return lds0 + (kt & 1) * STAGE; };
     const i32x4_t ra = make_rsrc(p.A, (uint32_t)(((p.M - 1) * p.lda + p.K) * 2));
-    const i32x4_t rb = make_rsrc(p.B, (uint32_t)(((p.K - 1) * p.ldb + p.N) * 2));
+    const i32x4_t rb = make_rsrc(p.B, BT ? (uint32_t)(((p.N - 1) * p.ldb + p.K) * 2)
+                                         : (uint32_t)(((p.K - 1) * p.ldb + p.N) * 2));
     Offsets o;
     offsets<MASK_MN>(p, m0, n0, o);
     auto step_barrier = [] {
@@ -413,9 +441,9 @@ template <int OP, int EPI, int NW = 4> struct Gemm16W4 {
   }
 };
 
-template <int OP, int EPI, int NW>
+template <int OP, int EPI, int NW, bool BT = false>
 __global__ void __launch_bounds__(NW * 64, 1) gemm16_w4_kernel(GemmArgs p) {
-  typedef Gemm16W4<OP, EPI, NW> G;
+  typedef Gemm16W4<OP, EPI, NW, BT> G;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * (G::A_BYTES + G::B_BYTES)];
   int tm, tn;
   tile_coords(p, tm, tn);

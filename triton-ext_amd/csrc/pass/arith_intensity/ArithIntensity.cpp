@@ -117,7 +117,9 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
 
   Tile t{d->block_m, d->block_n, d->block_k, 1.0};
   if (t.bm <= 0 || t.bn <= 0 || t.bk <= 0) {
-    if (sa == 2)
+    if (sa == 2 && (d->flags & TX_FLAG_B_KMAJOR))
+      t = kTiles16[0]; // the K-major B kernel exists for this tile only
+    else if (sa == 2)
       t = chooseTile(kTiles16, d->M, d->N, d->K);
     else if (d->a_type == TX_I8 && d->scale_mode == TX_SCALE_ROWCOL && d->M <= 256)
       // W8A8 decode: one row slice up to M = 64, slices of 64 beyond,

@@ -17,6 +17,7 @@ OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_NO_DEVICE, ERR_WORKSPACE, ERR_NO_
 # tx_kernel
 KERNEL_NONE, KERNEL_GEMM_16BIT, KERNEL_GEMM_I8, KERNEL_DECODE_I8, KERNEL_GEMM_F8 = range(5)
 FLAG_NO_LOOP_SPLIT = 0x1
+FLAG_B_KMAJOR = 0x2  # B stored [N][K] row-major (a transposed view in torch)
 # TritonPluginResult
 TP_SUCCESS, TP_GENERIC_FAILURE = 0, 1
 # tx_cmp_pred (arith::CmpIPredicate order)

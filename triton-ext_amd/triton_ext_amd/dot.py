@@ -30,15 +30,20 @@ def _torch_dtype(tx):
 
 
 def plan_for(a, b, out_dtype_tx, scale_mode=capi.SCALE_NONE, block=(0, 0, 0), flags=0):
+    """Plan C = A @ B.  B may be row-major [K,N] or a transposed view of a
+    row-major [N,K] tensor (K-major, e.g. `k.t()` in q @ k.T)."""
     if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[0]:
         raise ValueError(f"dot of {tuple(a.shape)} and {tuple(b.shape)}")
-    if a.stride(1) != 1 or b.stride(1) != 1:
-        raise ValueError("A and B rows must be contiguous")
     M, K = a.shape
     N = b.shape[1]
+    b_kmajor = b.stride(1) != 1 and b.stride(0) == 1 and K > 1
+    if a.stride(1) != 1 or (b.stride(1) != 1 and not b_kmajor):
+        raise ValueError("A rows must be contiguous, and B rows (or B's columns) too")
+    if b_kmajor:
+        flags |= capi.FLAG_B_KMAJOR
     # an empty operand's strides are arbitrary: describe it as packed
     lda = a.stride(0) if M > 0 and K > 0 else 0
-    ldb = b.stride(0) if K > 0 and N > 0 else 0
+    ldb = (b.stride(1) if b_kmajor else b.stride(0)) if K > 0 and N > 0 else 0
     desc = capi.make_desc(M, N, K, tx_type(a), out_dtype_tx, b_type=tx_type(b),
                           scale_mode=scale_mode, block=block, lda=lda, ldb=ldb, flags=flags)
     return capi.plan(desc)
