@@ -48,6 +48,13 @@ typedef enum tx_dtype {
   TX_I8 = 3,
   TX_F8E4M3 = 4, /* OCP e4m3fn (triton fp8e4nv): bias 7, max 448 */
   TX_I32 = 5,
+  TX_F8E5M2 = 6, /* OCP e5m2 (triton fp8e5): bias 15, inf and NaN codes */
+  /* OCP e2m1 (fp4), two per byte along K, element k in the low nibble of
+   * its byte when k is even (tl.dot_scaled with lhs_k_pack / rhs_k_pack):
+   * A is [M][K/2] bytes, B is [K/2][N] bytes.  Row strides stay in
+   * elements: lda counts K elements (bytes = lda / 2), ldb counts N
+   * elements of a packed row (bytes = ldb). */
+  TX_F4E2M1 = 7,
 } tx_dtype;
 
 typedef enum tx_scale_mode {
@@ -58,6 +65,16 @@ typedef enum tx_scale_mode {
    *   acc[m][n] += dot_f32(Aq[m][kb], Bq[kb][n]) * sa[m][kb] * sb[kb][n/128]
    * sa is [M][ceil(K/128)], sb is [ceil(K/128)][ceil(N/128)], row-major. */
   TX_SCALE_BLOCK128 = 2,
+  /* tl.dot_scaled microscaling (OCP MX): e8m0 scales, one per 32 K elements
+   * of each operand row (A) or column (B):
+   *   C[m][n] = sum_k (A[m][k] * 2^(sa[m][k/32] - 127)) *
+   *                   (B[k][n] * 2^(sb[n][k/32] - 127))
+   * sa is uint8 [M][K/32] and sb uint8 [N][K/32] (B's scales indexed by
+   * column first, as tl.dot_scaled's rhs_scale; not transposed), both
+   * row-major and packed, 4-byte aligned.  Scale 0xFF is NaN.  Operands
+   * e4m3 / e5m2 (either mix) or e2m1 on both sides; K % 32 == 0; C fp32 or
+   * bf16 (round to nearest even). */
+  TX_SCALE_MX32 = 3,
 } tx_scale_mode;
 
 typedef enum tx_bound {
@@ -82,6 +99,7 @@ typedef enum tx_kernel {
   TX_KERNEL_GEMM_I8 = 2,    /* int8 tile, MFMA 16x16x64 (32x32x32 small tiles)   */
   TX_KERNEL_DECODE_I8 = 3,  /* int8 W8A8 M <= 256 streaming, MFMA 16x16x64       */
   TX_KERNEL_GEMM_F8 = 4,    /* fp8 e4m3 tile, MFMA 16x16x128 (32x32x64 small)    */
+  TX_KERNEL_GEMM_MX = 5,    /* MX fp8 / fp4 tile, scaled MFMA 16x16x128 (e8m0)   */
 } tx_kernel;
 
 /* Bit flags for tx_dot_desc.flags */
@@ -142,11 +160,12 @@ struct tx_dot_plan {
 TX_API int tx_dot_plan_create(const tx_dot_desc *desc, tx_dot_plan *plan);
 
 /* Enqueue the planned dot on `stream`.  `scale_a`/`scale_b` are required for
- * TX_SCALE_ROWCOL and TX_SCALE_BLOCK128 and ignored otherwise.  `workspace`
+ * the scaled modes and ignored otherwise: fp32 arrays for TX_SCALE_ROWCOL and
+ * TX_SCALE_BLOCK128, uint8 e8m0 arrays for TX_SCALE_MX32.  `workspace`
  * must hold plan->workspace_bytes bytes when that is non-zero; its contents
  * on entry do not matter.  Concurrent launches must not share a workspace. */
 TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A, const void *B,
-                         void *C, const float *scale_a, const float *scale_b,
+                         void *C, const void *scale_a, const void *scale_b,
                          void *workspace, size_t workspace_bytes, void *stream);
 
 /* Message for the calling thread's last non-zero status ("" if none). */

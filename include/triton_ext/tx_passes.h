@@ -83,7 +83,7 @@ TX_API int tx_loop_split_k(int64_t K, int32_t bk, int64_t *k_split,
  * FLOPs = 2*M*N*K; bytes = A + B + C + scales, each read or written once;
  * ridge = peak_flops / peak_bw; bound = MFMA if intensity > ridge.
  * MI355X peaks (dense, public): bf16/fp16 2.5166 PFLOP/s, int8 and fp8
- * 5.0332 P(FL)OP/s, HBM3E 8.0 TB/s.
+ * 5.0332 P(FL)OP/s, fp4 10.0664 PFLOP/s, HBM3E 8.0 TB/s.
  * ---------------------------------------------------------------------- */
 
 typedef struct tx_ai_report {
@@ -95,8 +95,11 @@ typedef struct tx_ai_report {
   int32_t block_m, block_n, block_k; /* recommended tile */
 } tx_ai_report;
 
-/* Element size in bytes of a tx_dtype (0 for an unknown value). */
+/* Element size in bytes of a tx_dtype (0 for an unknown value and for the
+ * sub-byte TX_F4E2M1). */
 TX_API int32_t tx_dtype_size(int32_t dtype);
+/* Element size in bits of a tx_dtype (0 for an unknown value). */
+TX_API int32_t tx_dtype_bits(int32_t dtype);
 /* MI355X dense peak FLOP/s (or OP/s) for a product of `dtype` operands. */
 TX_API double tx_mi355x_peak_flops(int32_t dtype);
 /* MI355X HBM3E peak bytes/s. */

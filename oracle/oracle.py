@@ -6,7 +6,13 @@ Pinned by (tests/test_oracle_cpu.py):
     integer-valued fp inputs where the fp32 result is exact;
   * the Triton-interpreter golden fixtures under tests/golden/;
   * codec checks: bf16/fp16/e4m3 round trips over all bit patterns,
-    known values (e4m3 max 448, min subnormal 2^-9), numpy's float16 RNE.
+    known values (e4m3 max 448, min subnormal 2^-9), numpy's float16 RNE;
+  * dot_scaled (tl.dot_scaled, MX): e4m3/e5m2/e8m0 decoders vs torch's
+    float8 dtypes over all codes, e2m1 vs the OCP formula and the e4m3
+    encoding of the same values; unit scales reduce it to the tiled fp8 dot;
+    e2m1 operands equal their e4m3 re-encoding; a scale step of +1 doubles
+    exactly one group's terms; golden fixtures from the interpreter running
+    the dequantise-then-tl.dot form.
 """
 import ctypes
 import os
@@ -16,7 +22,8 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
-F32, F16, BF16, I8, F8E4M3, I32 = 0, 1, 2, 3, 4, 5
+F32, F16, BF16, I8, F8E4M3, I32, F8E5M2, F4E2M1 = 0, 1, 2, 3, 4, 5, 6, 7
+E8M0 = -1  # scale codec selector of mx_decode
 SCALE_NONE, SCALE_ROWCOL, SCALE_BLOCK128 = 0, 1, 2
 ROUND_RTZ, ROUND_RNE = 0, 1
 
@@ -41,6 +48,10 @@ def lib():
                      "or_f32_to_e4m3_array", "or_e4m3_to_f32_array"):
             getattr(L, name).argtypes = [vp, vp, i64]
         L.or_quantize_e4m3_groups.argtypes = [vp, i64, i64, i32, i32, vp, vp]
+        L.or_mx_decode_array.argtypes = [vp, vp, i64, i32]
+        L.oracle_dot_scaled.restype = i32
+        L.oracle_dot_scaled.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64,
+                                        i32, i32, i32, i32, i32]
         _lib = L
     return _lib
 
@@ -133,3 +144,37 @@ def quantize_e4m3_groups(x, gr, gc):
     s = np.empty(((rows + gr - 1) // gr, (cols + gc - 1) // gc), dtype=np.float32)
     lib().or_quantize_e4m3_groups(_ptr(x), rows, cols, gr, gc, _ptr(q), _ptr(s))
     return q, s
+
+
+def mx_decode(codes, fmt):
+    """Decode uint8 codes of F8E4M3 / F8E5M2 / F4E2M1 (low nibble) or E8M0
+    to float64 (OCP MX semantics: e4m3 S.1111.111 and e8m0 255 are NaN)."""
+    x = np.ascontiguousarray(codes, dtype=np.uint8)
+    y = np.empty(x.shape, dtype=np.float64)
+    lib().or_mx_decode_array(_ptr(x), _ptr(y), x.size, fmt)
+    return y
+
+
+def dot_scaled(a, sa, a_fmt, b, sb, b_fmt, *, K, c_type=F32, round_mode=ROUND_RNE,
+               nthreads=0):
+    """tl.dot_scaled on the CPU.
+
+    a: uint8 [M, K] codes (e2m1: [M, K/2] packed bytes); b: uint8 [K, N]
+    (e2m1: [K/2, N], packed along K); sa: uint8 [M, K/32]; sb: uint8
+    [N, K/32].  Returns fp32 [M, N] (c_type F32) or bf16 bits (BF16).
+    """
+    a = np.ascontiguousarray(a, dtype=np.uint8)
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    sa = np.ascontiguousarray(sa, dtype=np.uint8)
+    sb = np.ascontiguousarray(sb, dtype=np.uint8)
+    M, N = a.shape[0], b.shape[1]
+    assert sa.shape == (M, K // 32) and sb.shape == (N, K // 32), (sa.shape, sb.shape)
+    assert a.shape[1] == (K // 2 if a_fmt == F4E2M1 else K)
+    assert b.shape[0] == (K // 2 if b_fmt == F4E2M1 else K)
+    out = np.zeros((M, N), dtype=np.float32 if c_type == F32 else np.uint16)
+    lda = K
+    rc = lib().oracle_dot_scaled(_ptr(a), _ptr(b), _ptr(out), _ptr(sa), _ptr(sb), M, N, K,
+                                 lda, N, N, a_fmt, b_fmt, c_type, round_mode, nthreads)
+    if rc != 0:
+        raise ValueError(f"oracle_dot_scaled rejected the arguments (rc={rc})")
+    return out

@@ -41,6 +41,10 @@
  *   BLOCK128:   BK == 128 and, per K block kb,
  *               acc = acc + (dot_f32(a, b) * sa[m][kb]) * sb[kb][n/128]
  *
+ * dot_scaled (oracle_dot_scaled, below) restates tl.dot_scaled with e8m0
+ * scales (T:language/semantic.py:1611-1665, T:language/core.py:2064-2101),
+ * which the interpreter does not implement.
+ *
  * Build: see oracle/Makefile (-ffp-contract=off: no FMA contraction, so the
  * epilogue arithmetic is the plain fp32 sequence written here).
  */
@@ -53,7 +57,8 @@
 #include <omp.h>
 #endif
 
-enum { OR_F32 = 0, OR_F16 = 1, OR_BF16 = 2, OR_I8 = 3, OR_F8E4M3 = 4, OR_I32 = 5 };
+enum { OR_F32 = 0, OR_F16 = 1, OR_BF16 = 2, OR_I8 = 3, OR_F8E4M3 = 4, OR_I32 = 5,
+       OR_F8E5M2 = 6, OR_F4E2M1 = 7 };
 enum { OR_SCALE_NONE = 0, OR_SCALE_ROWCOL = 1, OR_SCALE_BLOCK128 = 2 };
 enum { OR_ROUND_RTZ = 0, OR_ROUND_RNE = 1 };
 
@@ -167,6 +172,127 @@ void or_f32_to_e4m3_array(const float *x, uint8_t *y, int64_t n) {
 void or_e4m3_to_f32_array(const uint8_t *x, float *y, int64_t n) {
   for (int64_t i = 0; i < n; ++i)
     y[i] = or_e4m3_to_f32(x[i]);
+}
+
+/* ---------------- MX element codecs (OCP Microscaling Formats v1.0) ----
+ * e4m3fn: bias 7, no inf, S.1111.111 is NaN (the MX path follows the OCP
+ *         encoding; the interpreter-facing or_e4m3_to_f32 above keeps the
+ *         interpreter's +-480 for that code);
+ * e5m2:   bias 15, exponent 31 is inf (mantissa 0) or NaN;
+ * e2m1:   bias 1, values +-{0, 0.5, 1, 1.5, 2, 3, 4, 6}, no inf or NaN;
+ * e8m0:   2^(s - 127), s = 255 is NaN (s = 0 is 2^-127). */
+double or_mx_e4m3_to_f64(uint8_t b) {
+  int s = b >> 7, e = (b >> 3) & 15, m = b & 7;
+  if (e == 15 && m == 7)
+    return NAN;
+  double v = e == 0 ? ldexp((double)m, -9) : ldexp(1.0 + m / 8.0, e - 7);
+  return s ? -v : v;
+}
+
+double or_e5m2_to_f64(uint8_t b) {
+  int s = b >> 7, e = (b >> 2) & 31, m = b & 3;
+  double v;
+  if (e == 31)
+    v = m ? NAN : INFINITY;
+  else
+    v = e == 0 ? ldexp((double)m, -16) : ldexp(1.0 + m / 4.0, e - 15);
+  return s ? -v : v;
+}
+
+double or_e2m1_to_f64(uint8_t nib) {
+  int s = (nib >> 3) & 1, e = (nib >> 1) & 3, m = nib & 1;
+  double v = e == 0 ? 0.5 * m : ldexp(1.0 + m / 2.0, e - 1);
+  return s ? -v : v;
+}
+
+double or_e8m0_to_f64(uint8_t x) { return x == 255 ? NAN : ldexp(1.0, (int)x - 127); }
+
+/* Decode n codes (one per byte; e2m1 in the low nibble) of fmt, or of e8m0
+ * for fmt == -1, to double. */
+void or_mx_decode_array(const uint8_t *x, double *y, int64_t n, int fmt) {
+  for (int64_t i = 0; i < n; ++i) {
+    switch (fmt) {
+    case OR_F8E4M3: y[i] = or_mx_e4m3_to_f64(x[i]); break;
+    case OR_F8E5M2: y[i] = or_e5m2_to_f64(x[i]); break;
+    case OR_F4E2M1: y[i] = or_e2m1_to_f64((uint8_t)(x[i] & 15)); break;
+    case -1: y[i] = or_e8m0_to_f64(x[i]); break;
+    default: y[i] = NAN;
+    }
+  }
+}
+
+/* Element (r, k) of an MX operand stored K-contiguous (A: r = m) or
+ * (packed B: r = n, read column-wise).  fp8: one byte; e2m1: the nibble of
+ * byte k/2, low nibble for even k. */
+static double mx_elem(const uint8_t *base, int fmt, int64_t byte, int k_odd) {
+  switch (fmt) {
+  case OR_F8E4M3: return or_mx_e4m3_to_f64(base[byte]);
+  case OR_F8E5M2: return or_e5m2_to_f64(base[byte]);
+  case OR_F4E2M1: return or_e2m1_to_f64((uint8_t)(k_odd ? base[byte] >> 4 : base[byte] & 15));
+  default: return NAN;
+  }
+}
+
+/*
+ * tl.dot_scaled(lhs, lhs_scale, fmt_a, rhs, rhs_scale, fmt_b, out_dtype=fp32):
+ *   C[m][n] = sum_k (A[m][k] * 2^(sa[m][k/32] - 127)) * (B[k][n] * 2^(sb[n][k/32] - 127))
+ * sa is uint8 [M][K/32], sb uint8 [N][K/32] (rhs_scale is indexed by column
+ * first, T:language/core.py:2078-2080), K % 32 == 0.  A is [M][K] (e2m1:
+ * [M][K/2] bytes, lda in elements), B is [K][N] (e2m1: [K/2][N] bytes,
+ * packed along K, ldb = bytes per packed row).  Each term is formed and
+ * summed exactly in double (e4m3/e5m2/e2m1 values times powers of two are
+ * exact; the sum of 128-term blocks of them is exact in double for the
+ * magnitudes tested) and rounded once to fp32: the exact result, against
+ * which the hardware's fixed-point group sums are judged by tolerance.
+ * c_type OR_BF16 rounds that fp32 value with round_mode.  Returns 0, or -1
+ * for an unsupported combination.
+ */
+int oracle_dot_scaled(const void *Av, const void *Bv, void *Cv, const uint8_t *sa,
+                      const uint8_t *sb, int64_t M, int64_t N, int64_t K, int64_t lda,
+                      int64_t ldb, int64_t ldc, int a_fmt, int b_fmt, int c_type,
+                      int round_mode, int nthreads) {
+  const uint8_t *A = (const uint8_t *)Av, *B = (const uint8_t *)Bv;
+  uint8_t *C = (uint8_t *)Cv;
+  if (M < 0 || N < 0 || K < 0 || K % 32)
+    return -1;
+  if ((a_fmt != OR_F8E4M3 && a_fmt != OR_F8E5M2 && a_fmt != OR_F4E2M1) ||
+      (b_fmt != OR_F8E4M3 && b_fmt != OR_F8E5M2 && b_fmt != OR_F4E2M1))
+    return -1;
+  if (c_type != OR_F32 && c_type != OR_BF16)
+    return -1;
+  const int64_t G = K / 32;
+#ifdef _OPENMP
+  if (nthreads <= 0)
+    nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)
+#endif
+  for (int64_t m = 0; m < M; ++m) {
+    double *arow = (double *)malloc(sizeof(double) * (size_t)(K > 0 ? K : 1));
+    if (!arow)
+      continue; /* left unwritten; the caller's C stays as it was */
+    for (int64_t k = 0; k < K; ++k) {
+      const int64_t byte = a_fmt == OR_F4E2M1 ? m * (lda / 2) + k / 2 : m * lda + k;
+      arow[k] = mx_elem(A, a_fmt, byte, (int)(k & 1)) * or_e8m0_to_f64(sa[m * G + k / 32]);
+    }
+    for (int64_t n = 0; n < N; ++n) {
+      double acc = 0.0;
+      for (int64_t k = 0; k < K; ++k) {
+        const int64_t byte = b_fmt == OR_F4E2M1 ? (k / 2) * ldb + n : k * ldb + n;
+        const double b = mx_elem(B, b_fmt, byte, (int)(k & 1)) * or_e8m0_to_f64(sb[n * G + k / 32]);
+        acc += arow[k] * b;
+      }
+      const float f = (float)acc;
+      const int64_t off = m * ldc + n;
+      if (c_type == OR_F32) {
+        memcpy(C + 4 * off, &f, 4);
+      } else {
+        uint16_t h = or_f32_to_bf16(f, round_mode);
+        memcpy(C + 2 * off, &h, 2);
+      }
+    }
+    free(arow);
+  }
+  return 0;
 }
 
 /* ---------------- the tiled dot ---------------- */

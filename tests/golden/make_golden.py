@@ -23,6 +23,13 @@ Interpreter facts the fixtures exercise (third-party source, read as text):
     tl.dot; fp32 -> bf16 casts truncate (cast_impl, :461-467, rounding None);
   * fp32 -> fp16 casts are numpy astype (round to nearest even).
 
+tl.dot_scaled (MX) fixtures: the interpreter has no dot_scaled, so mx_dot_kernel
+runs the form it reduces to, each operand upcast then tl.dot in fp32
+(T:language/semantic.py:1611-1665 for the operand and scale shapes): codes are
+loaded as uint8, decoded with the OCP e4m3 / e5m2 / e2m1 formulas (e2m1
+unpacked low nibble first along K), multiplied by exp2(scale - 127) per 32
+elements of K (rhs_scale indexed [n][k // 32]), and accumulated by tl.dot.
+
 "dyadic" fixtures draw small multiples of a power of two, so every product and
 partial sum is exact in fp32: the fp32 accumulator is then independent of the
 summation order, and any correct implementation must match it bit for bit.
@@ -87,6 +94,124 @@ def tiled_dot_kernel(a_ptr, b_ptr, c_ptr, sa_ptr, sb_ptr, M, N, K, sa_ld, sb_ld,
         res = acc
     tl.store(c_ptr + rm[:, None] * N + rn[None, :], res.to(OUT),
              mask=(rm[:, None] < M) & (rn[None, :] < N))
+
+
+@triton.jit
+def _mx_decode(c, FMT: tl.constexpr):
+    """OCP element value of uint8 codes (as int32): 0 e4m3, 1 e5m2, 4 e2m1."""
+    if FMT == 0:
+        e = (c >> 3) & 15
+        m = (c & 7).to(tl.float32)
+        mag = tl.where(e == 0, m * 0.001953125,
+                       (1.0 + m * 0.125) * tl.exp2((e - 7).to(tl.float32)))
+        sgn = c >> 7
+    elif FMT == 1:
+        e = (c >> 2) & 31
+        m = (c & 3).to(tl.float32)
+        mag = tl.where(e == 0, m * 0.0000152587890625,
+                       (1.0 + m * 0.25) * tl.exp2((e - 15).to(tl.float32)))
+        sgn = c >> 7
+    else:
+        e = (c >> 1) & 3
+        m = (c & 1).to(tl.float32)
+        mag = tl.where(e == 0, m * 0.5, (1.0 + m * 0.5) * tl.exp2((e - 1).to(tl.float32)))
+        sgn = (c >> 3) & 1
+    return tl.where(sgn != 0, -mag, mag)
+
+
+@triton.jit
+def mx_dot_kernel(a_ptr, b_ptr, sa_ptr, sb_ptr, c_ptr, M, N, K,
+                  BM: tl.constexpr, BN: tl.constexpr, BK: tl.constexpr,
+                  FA: tl.constexpr, FB: tl.constexpr):
+    pid_m = tl.program_id(0)
+    pid_n = tl.program_id(1)
+    rm = pid_m * BM + tl.arange(0, BM)
+    rn = pid_n * BN + tl.arange(0, BN)
+    rk = tl.arange(0, BK)
+    G = K // 32
+    acc = tl.zeros((BM, BN), dtype=tl.float32)
+    for k0 in range(0, K, BK):
+        kk = k0 + rk
+        am = (rm[:, None] < M) & (kk[None, :] < K)
+        bm = (kk[:, None] < K) & (rn[None, :] < N)
+        if FA == 4:
+            ab = tl.load(a_ptr + rm[:, None] * (K // 2) + kk[None, :] // 2, mask=am, other=0)
+            ac = (ab.to(tl.int32) >> ((kk[None, :] % 2) * 4)) & 15
+        else:
+            ac = tl.load(a_ptr + rm[:, None] * K + kk[None, :], mask=am, other=0).to(tl.int32)
+        if FB == 4:
+            bb = tl.load(b_ptr + (kk[:, None] // 2) * N + rn[None, :], mask=bm, other=0)
+            bc = (bb.to(tl.int32) >> ((kk[:, None] % 2) * 4)) & 15
+        else:
+            bc = tl.load(b_ptr + kk[:, None] * N + rn[None, :], mask=bm, other=0).to(tl.int32)
+        sa = tl.load(sa_ptr + rm[:, None] * G + kk[None, :] // 32, mask=am, other=127)
+        sb = tl.load(sb_ptr + rn[None, :] * G + kk[:, None] // 32, mask=bm, other=127)
+        a = _mx_decode(ac, FA) * tl.exp2(sa.to(tl.float32) - 127.0)
+        b = _mx_decode(bc, FB) * tl.exp2(sb.to(tl.float32) - 127.0)
+        acc = tl.dot(a, b, acc)
+    tl.store(c_ptr + rm[:, None] * N + rn[None, :], acc,
+             mask=(rm[:, None] < M) & (rn[None, :] < N))
+
+
+MX_FMT = {"e4m3": 0, "e5m2": 1, "e2m1": 4}
+
+
+def run_mx(a, sa, fa, b, sb, fb, *, K, block):
+    """Interpreter output (fp32) of tl.dot_scaled's upcast form."""
+    M, N = a.shape[0], b.shape[1]
+    c = torch.zeros((M, N), dtype=torch.float32)
+    BM, BN, BK = block
+    grid = (triton.cdiv(M, BM), triton.cdiv(N, BN))
+    mx_dot_kernel[grid](torch.from_numpy(a), torch.from_numpy(b), torch.from_numpy(sa),
+                        torch.from_numpy(sb), c, M, N, K, BM=BM, BN=BN, BK=BK,
+                        FA=MX_FMT[fa], FB=MX_FMT[fb])
+    return c.numpy()
+
+
+def save_mx(name, a, sa, fa, b, sb, fb, c, *, K, block, exact):
+    d = dict(a=a, sa=sa, b=b, sb=sb, c=c, a_fmt=fa, b_fmt=fb, K=np.int64(K),
+             M=np.int64(a.shape[0]), N=np.int64(b.shape[1]), block=np.array(block, np.int32),
+             exact=np.bool_(exact))
+    np.savez_compressed(os.path.join(HERE, name + ".npz"), **d)
+    size = os.path.getsize(os.path.join(HERE, name + ".npz"))
+    print(f"{name}: M={a.shape[0]} N={b.shape[1]} K={K} {fa} x {fb} {size / 1024:.1f} KiB",
+          flush=True)
+
+
+def mx_codes(rng, shape, fmt, exact):
+    """Codes of `fmt`; exact: small dyadic magnitudes (NaN / inf codes never)."""
+    if fmt == "e2m1":
+        return rng.integers(0, 16, size=shape, dtype=np.uint8)
+    if fmt == "e4m3":  # exponent field 5..8 (values 2^-2 .. 2^2) or any finite code
+        if exact:
+            return (rng.integers(0, 2, size=shape) << 7 | rng.integers(5, 9, size=shape) << 3
+                    | rng.integers(0, 8, size=shape)).astype(np.uint8)
+        c = rng.integers(0, 256, size=shape).astype(np.uint8)
+        return np.where((c & 0x7F) == 0x7F, c & 0xF0, c).astype(np.uint8)
+    if exact:  # e5m2, exponent field 13..16
+        return (rng.integers(0, 2, size=shape) << 7 | rng.integers(13, 17, size=shape) << 2
+                | rng.integers(0, 4, size=shape)).astype(np.uint8)
+    c = rng.integers(0, 256, size=shape).astype(np.uint8)
+    return np.where((c & 0x7C) == 0x7C, c & 0x83, c).astype(np.uint8)
+
+
+def pack_e2m1(codes, axis):
+    """Two e2m1 codes per byte along `axis`, even index in the low nibble."""
+    lo = np.take(codes, np.arange(0, codes.shape[axis], 2), axis=axis)
+    hi = np.take(codes, np.arange(1, codes.shape[axis], 2), axis=axis)
+    return (lo | (hi << 4)).astype(np.uint8)
+
+
+def mx_case(rng, name, fa, fb, M, N, K, *, exact, block):
+    ac = mx_codes(rng, (M, K), fa, exact)
+    bc = mx_codes(rng, (K, N), fb, exact)
+    lo, hi = (125, 130) if exact else (117, 138)  # exact: sums within fp32's 24 bits
+    sa = rng.integers(lo, hi, size=(M, K // 32)).astype(np.uint8)
+    sb = rng.integers(lo, hi, size=(N, K // 32)).astype(np.uint8)
+    a = pack_e2m1(ac, 1) if fa == "e2m1" else ac
+    b = pack_e2m1(bc, 0) if fb == "e2m1" else bc
+    c = run_mx(a, sa, fa, b, sb, fb, K=K, block=block)
+    save_mx(name, a, sa, fa, b, sb, fb, c, K=K, block=block, exact=exact)
 
 
 TL_OUT = {"f32": tl.float32, "bf16": tl.bfloat16, "f16": tl.float16, "i32": tl.int32}
@@ -248,6 +373,21 @@ def main():
     save("fp8_block128_bf16_normal", qa, qb,
          run(qa, qb, out="bf16", block=(32, 128, 128), epi=EPI_BLOCK128, sa=sa, sb=sb),
          block=(32, 128, 128), out="bf16", epi=EPI_BLOCK128, sa=sa, sb=sb)
+
+    # tl.dot_scaled (MX), fp32 C.  Exact: every term and partial sum fits
+    # fp32, so any summation order gives these bits.  Edges in M and N and a
+    # K that is not a multiple of the GPU's 128 (fp8) / 256 (fp4) step.
+    mx_case(rng, "mx_e4m3_e5m2_f32_exact", "e4m3", "e5m2", 40, 48, 96, exact=True,
+            block=(32, 32, 32))
+    mx_case(rng, "mx_e2m1_f32_exact", "e2m1", "e2m1", 24, 32, 160, exact=True,
+            block=(16, 32, 32))
+    mx_case(rng, "mx_e5m2_e4m3_f32_exact", "e5m2", "e4m3", 16, 64, 288, exact=True,
+            block=(16, 32, 64))
+    # full-range codes and scales 2^-10 .. 2^10: tolerance (fp32 summation order)
+    mx_case(rng, "mx_e4m3_f32_random", "e4m3", "e4m3", 32, 64, 256, exact=False,
+            block=(32, 32, 64))
+    mx_case(rng, "mx_e2m1_f32_random", "e2m1", "e2m1", 32, 48, 512, exact=False,
+            block=(32, 16, 64))
 
 
 if __name__ == "__main__":

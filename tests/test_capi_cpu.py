@@ -207,6 +207,66 @@ def test_b_kmajor_plans():
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, flags=0x10)) == tx.ERR_INVALID
 
 
+def test_mx_plans():
+    """tl.dot_scaled (TX_SCALE_MX32): fp8 / fp4 on the 256x256 tile, 128 bytes of K per step."""
+    MX = tx.SCALE_MX32
+    for a, b, c in ((tx.F8E4M3, tx.F8E4M3, tx.F32), (tx.F8E4M3, tx.F8E5M2, tx.BF16),
+                    (tx.F8E5M2, tx.F8E4M3, tx.F32), (tx.F8E5M2, tx.F8E5M2, tx.BF16)):
+        p = tx.plan(tx.make_desc(1000, 528, 4000, a, c, b_type=b, scale_mode=MX))
+        assert p.kernel == tx.KERNEL_GEMM_MX and p.block_threads == 512
+        assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (256, 256, 128)
+        assert p.k_main_steps == 4000 // 128 and p.k_tail == 4000 % 128
+        assert p.grid_x == 4 * 3
+        # algorithmic bytes: fp8 operands, one e8m0 byte per 32 K of each row
+        # and column, C once
+        assert p.bytes == 1000 * 4000 + 4000 * 528 + (1000 + 528) * 125 + \
+            1000 * 528 * (4 if c == tx.F32 else 2)
+        assert p.peak_flops == pytest.approx(5033.2e12)
+    p = tx.plan(tx.make_desc(512, 256, 1024, tx.F4E2M1, tx.F32, scale_mode=MX))
+    assert p.kernel == tx.KERNEL_GEMM_MX
+    assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (256, 256, 256)
+    assert p.desc.lda == 1024 and p.desc.ldb == 256
+    assert p.bytes == 512 * 512 + 512 * 256 + (512 + 256) * 32 + 512 * 256 * 4
+    assert p.peak_flops == pytest.approx(10066.4e12)
+    assert tx.load("libarith_intensity.so").tx_dtype_bits(tx.F4E2M1) == 4
+    assert tx.load("libarith_intensity.so").tx_dtype_size(tx.F4E2M1) == 0
+
+    def err(**kw):
+        d = dict(M=64, N=64, K=256, a_type=tx.F8E4M3, c_type=tx.F32, scale_mode=MX)
+        d.update(kw)
+        return _err(tx.make_desc(d.pop("M"), d.pop("N"), d.pop("K"), d.pop("a_type"),
+                                 d.pop("c_type"), **d))
+    assert err(K=272) == tx.ERR_UNSUPPORTED          # K % 32
+    assert err(b_type=tx.F4E2M1, K=256) == tx.ERR_UNSUPPORTED  # fp8 with fp4
+    assert err(c_type=tx.F16) == tx.ERR_UNSUPPORTED
+    assert err(a_type=tx.I8, c_type=tx.BF16) == tx.ERR_UNSUPPORTED
+    assert err(flags=tx.FLAG_B_KMAJOR) == tx.ERR_UNSUPPORTED
+    assert err(a_type=tx.F4E2M1, scale_mode=tx.SCALE_NONE) == tx.ERR_UNSUPPORTED
+    assert err(scale_mode=4) == tx.ERR_INVALID
+    assert err(a_type=tx.F4E2M1, K=256, lda=264) == tx.ERR_INVALID  # 132-byte rows
+    # the non-MX modes keep rejecting e5m2
+    assert err(a_type=tx.F8E5M2, scale_mode=tx.SCALE_NONE) == tx.ERR_UNSUPPORTED
+
+
+def test_dot_scaled_argument_checks():
+    """Host mirror of tl.dot_scaled: Triton's shape checks (no device needed)."""
+    import torch
+    a = torch.zeros(64, 128, dtype=torch.uint8)
+    b = torch.zeros(128, 32, dtype=torch.uint8)
+    sa = torch.zeros(64, 4, dtype=torch.uint8)
+    sb = torch.zeros(32, 4, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="NYI: lhs_format"):
+        tx.dot_scaled(a, sa, "e3m4", b, sb, "e4m3")
+    with pytest.raises(NotImplementedError):
+        tx.dot_scaled(a, sa, "bf16", b, sb, "e4m3")
+    with pytest.raises(ValueError, match=r"rhs_scale must be a tensor of shape \[32, 4\]"):
+        tx.dot_scaled(a, sa, "e4m3", b, sb.t().contiguous(), "e4m3")
+    with pytest.raises(ValueError, match="Reduction dimension"):
+        tx.dot_scaled(a, sa, "e2m1", b, sb, "e4m3")  # lhs packs 256, rhs 128
+    with pytest.raises(NotImplementedError):
+        tx.dot_scaled(a, sa, "e4m3", b, sb, "e4m3", acc=torch.zeros(64, 32))
+
+
 def test_launch_without_device_fails_cleanly():
     import torch
     if torch.cuda.is_available():

@@ -70,6 +70,7 @@ struct GemmConfig {
                  // 2: the same staging with 4 waves of 128x128 (gemm16_w4.h),
                  // 3: 8 waves of 128x64 (gemm16_w4.h), 4: 8-wave ping-pong
                  // (gemm16_pp.h), 5: 8-bit 256x256x128 tile (gemm8_w4.h)
+  int fmt;       // MX operand formats: MFMA code of A | code of B << 4
 };
 
 #define TX_GEMM(OP, BM, BN, BK, WM, WN, EPI)                                   \
@@ -96,6 +97,13 @@ struct GemmConfig {
 
 #define TX_GEMM_8(OP, EPI)                                                     \
   GemmConfig { OP, 256, 256, 128, 2, 4, EPI, gemm8_w4_kernel<OP, EPI>, 0, 0, 5 }
+// MX (tl.dot_scaled) tiles: MFMA format codes FA, FB (0 e4m3, 1 e5m2,
+// 4 e2m1); BK in elements (128 bytes of K per step).
+#define TX_GEMM_MX(FA, FB, BK, EPI)                                            \
+  GemmConfig {                                                                 \
+    OP_F8, 256, 256, BK, 2, 4, EPI, gemm8_w4_kernel<OP_F8, EPI, FA, FB>, 0, 0, \
+        5, (FA) | ((FB) << 4)                                                  \
+  }
 #define TX_GEMM_8N(OP, EPI)                                                    \
   GemmConfig { OP, 256, 224, 128, 4, 2, EPI, gemm8_n224_kernel<OP, EPI>, 0, 0, 5 }
 
@@ -144,6 +152,17 @@ const GemmConfig kGemmConfigs[] = {
     TX_GEMM_8(OP_F8, EPI_BLOCK128_BF16),
     TX_GEMM_8(OP_F8, EPI_BLOCK128_F32),
     TX_GEMM_8(OP_F8, EPI_F32),
+    // MX: e8m0-scaled fp8 (e4m3 / e5m2 in any mix) and fp4 (gemm8_w4.h)
+    TX_GEMM_MX(0, 0, 128, EPI_MX_F32),
+    TX_GEMM_MX(0, 0, 128, EPI_MX_BF16),
+    TX_GEMM_MX(0, 1, 128, EPI_MX_F32),
+    TX_GEMM_MX(0, 1, 128, EPI_MX_BF16),
+    TX_GEMM_MX(1, 0, 128, EPI_MX_F32),
+    TX_GEMM_MX(1, 0, 128, EPI_MX_BF16),
+    TX_GEMM_MX(1, 1, 128, EPI_MX_F32),
+    TX_GEMM_MX(1, 1, 128, EPI_MX_BF16),
+    TX_GEMM_MX(4, 4, 256, EPI_MX_F32),
+    TX_GEMM_MX(4, 4, 256, EPI_MX_BF16),
     // the same with 256x224 tiles (gemm8_n224.h)
     TX_GEMM_8N(OP_I8, EPI_I32),
     TX_GEMM_8N(OP_I8, EPI_ROWCOL_BF16),
@@ -164,10 +183,32 @@ typedef void (*DecodeKernelFn)(DecodeArgs);
 const DecodeKernelFn kDecodeKernels[4] = {decode_i8_kernel<1>, decode_i8_kernel<2>,
                                            decode_i8_kernel<3>, decode_i8_kernel<4>};
 
+// MFMA format code of an MX operand type (-1 if it has none).
+int mxFormat(int32_t t) {
+  return t == TX_F8E4M3 ? 0 : t == TX_F8E5M2 ? 1 : t == TX_F4E2M1 ? 4 : -1;
+}
+// MX format pair of a descriptor (0 for the other scale modes).
+int fmtOf(const tx_dot_desc &d) {
+  if (d.scale_mode != TX_SCALE_MX32)
+    return 0;
+  return mxFormat(d.a_type) | (mxFormat(d.b_type) << 4);
+}
+
 // Operand kind and epilogue of a descriptor (-1 if unsupported).
 void classify(const tx_dot_desc &d, int *op, int *epi) {
   *op = -1;
   *epi = -1;
+  if (d.scale_mode == TX_SCALE_MX32) {
+    const int fa = mxFormat(d.a_type), fb = mxFormat(d.b_type);
+    if (fa < 0 || fb < 0 || (fa == 4) != (fb == 4))
+      return; // fp8 with fp4 would need steps of different byte widths
+    *op = OP_F8;
+    if (d.c_type == TX_F32)
+      *epi = EPI_MX_F32;
+    else if (d.c_type == TX_BF16)
+      *epi = EPI_MX_BF16;
+    return;
+  }
   if (d.a_type != d.b_type)
     return;
   switch (d.a_type) {
@@ -204,7 +245,7 @@ void classify(const tx_dot_desc &d, int *op, int *epi) {
   }
 }
 
-int findGemmConfig(int op, int epi, int bm, int bn, int bk, bool bt) {
+int findGemmConfig(int op, int epi, int bm, int bn, int bk, bool bt, int fmt) {
   // Tuning override TX_GEMM16_IMPL: "regs" (register staging), "dma8"
   // (8-wave direct-to-LDS), "w8" (8 waves of 128x64), "pp" (ping-pong);
   // default: 4 waves of 128x128 (fastest of these at 4096^3 on MI355X).
@@ -231,7 +272,7 @@ int findGemmConfig(int op, int epi, int bm, int bn, int bk, bool bt) {
     if (!is8 && !bt && (c.dma > want || (c.dma >= 2 && c.dma != want)))
       continue;
     if (c.op == op && c.epi == epi && c.bm == bm && c.bn == bn && c.bk == bk &&
-        c.bt == (int)bt)
+        c.bt == (int)bt && c.fmt == fmt)
       return i;
   }
   return -1;
@@ -307,7 +348,7 @@ int txMi355xDotRun(tx_dot_plan *plan) {
     return TX_OK;
   }
   const int ci = findGemmConfig(op, epi, d.block_m, d.block_n, d.block_k,
-                                (d.flags & TX_FLAG_B_KMAJOR) != 0);
+                                (d.flags & TX_FLAG_B_KMAJOR) != 0, fmtOf(d));
   if (ci < 0 && (d.flags & TX_FLAG_B_KMAJOR))
     return fail(TX_ERR_UNSUPPORTED,
                 "K-major B is implemented for bf16/fp16 on the 256x256x64 tile only");
@@ -315,9 +356,10 @@ int txMi355xDotRun(tx_dot_plan *plan) {
     return fail(TX_ERR_UNSUPPORTED, "no instantiated tile %dx%dx%d for this dtype",
                 d.block_m, d.block_n, d.block_k);
   const GemmConfig &c = kGemmConfigs[ci];
-  plan->kernel = op == OP_I8 ? TX_KERNEL_GEMM_I8
-               : op == OP_F8 ? TX_KERNEL_GEMM_F8
-                             : TX_KERNEL_GEMM_16BIT;
+  plan->kernel = op == OP_I8                     ? TX_KERNEL_GEMM_I8
+               : d.scale_mode == TX_SCALE_MX32 ? TX_KERNEL_GEMM_MX
+               : op == OP_F8                   ? TX_KERNEL_GEMM_F8
+                                               : TX_KERNEL_GEMM_16BIT;
   plan->split_k = 1;
   plan->grid_x = plan->m_tiles * plan->n_tiles;
   plan->grid_y = plan->grid_z = 1;
@@ -336,11 +378,16 @@ int validate(const tx_dot_desc *in, tx_dot_desc *d) {
                 (long long)d->M, (long long)d->N, (long long)d->K);
   if (d->M > INT32_MAX || d->N > INT32_MAX || d->K > INT32_MAX)
     return fail(TX_ERR_INVALID, "extent above 2^31-1");
-  const int32_t sa = tx_dtype_size(d->a_type), sb = tx_dtype_size(d->b_type),
-                sc = tx_dtype_size(d->c_type);
-  if (!sa || !sb || !sc)
+  const int32_t ba = tx_dtype_bits(d->a_type), bb = tx_dtype_bits(d->b_type),
+                bc = tx_dtype_bits(d->c_type);
+  if (!ba || !bb || !bc || bc < 8)
     return fail(TX_ERR_INVALID, "unknown dtype");
   const bool bt = (d->flags & TX_FLAG_B_KMAJOR) != 0;
+  if (d->scale_mode < TX_SCALE_NONE || d->scale_mode > TX_SCALE_MX32)
+    return fail(TX_ERR_INVALID, "unknown scale mode %d", d->scale_mode);
+  const bool fp4 = ba == 4 || bb == 4;
+  if (fp4 && d->scale_mode != TX_SCALE_MX32)
+    return fail(TX_ERR_UNSUPPORTED, "e2m1 operands need TX_SCALE_MX32");
   if (d->lda == 0) d->lda = d->K;
   if (d->ldb == 0) d->ldb = bt ? d->K : d->N;
   if (d->ldc == 0) d->ldc = d->N;
@@ -348,14 +395,23 @@ int validate(const tx_dot_desc *in, tx_dot_desc *d) {
     return fail(TX_ERR_INVALID, "row stride shorter than the row");
   if (d->flags & ~(TX_FLAG_NO_LOOP_SPLIT | TX_FLAG_B_KMAJOR))
     return fail(TX_ERR_INVALID, "unknown flags 0x%x", d->flags);
-  if ((d->lda * sa) % 16 || (d->ldb * sb) % 16 || (d->ldc * sc) % 16)
+  // Bytes of a row of A / of B / of C.  e2m1 B is packed along K: a byte
+  // row holds N elements of two K rows.
+  const int64_t ldb_b = bb == 4 ? d->ldb : d->ldb * bb / 8;
+  if ((d->lda * ba) % 128 || ldb_b % 16 || (d->ldc * bc / 8) % 16)
     return fail(TX_ERR_INVALID, "A/B/C row strides must be multiples of 16 bytes");
-  if ((d->K * sa) % 16 || (d->N * sb) % 16)
+  if ((d->K * ba) % 128 || (bb == 4 ? d->N : d->N * bb / 8) % 16)
     return fail(TX_ERR_UNSUPPORTED,
                 "K and N must be multiples of %d elements (16-byte chunks)",
-                16 / sa);
-  if (d->scale_mode < TX_SCALE_NONE || d->scale_mode > TX_SCALE_BLOCK128)
-    return fail(TX_ERR_INVALID, "unknown scale mode %d", d->scale_mode);
+                ba == 4 ? 32 : 128 / ba);
+  if (d->scale_mode == TX_SCALE_MX32) {
+    if (d->K % 32)
+      return fail(TX_ERR_UNSUPPORTED, "MX scales need K %% 32 == 0 (one e8m0 per 32)");
+    if (bt)
+      return fail(TX_ERR_UNSUPPORTED, "MX operands take B as [K][N] (no K-major B)");
+    if ((d->M > d->N ? d->M : d->N) * (d->K / 32) >= ((int64_t)1 << 31))
+      return fail(TX_ERR_UNSUPPORTED, "MX scale arrays above 2 GiB");
+  }
   if ((d->block_m < 0) || (d->block_n < 0) || (d->block_k < 0))
     return fail(TX_ERR_INVALID, "negative tile size");
   return TX_OK;
@@ -377,6 +433,7 @@ extern "C" TX_API const char *tx_kernel_name(int32_t kernel) {
   case TX_KERNEL_GEMM_I8: return "gemm_i8_mfma32x32x32";
   case TX_KERNEL_DECODE_I8: return "decode_i8_mfma16x16x64";
   case TX_KERNEL_GEMM_F8: return "gemm_f8_mfma32x32x64";
+  case TX_KERNEL_GEMM_MX: return "gemm_mx_mfma_scale16x16x128";
   default: return "?";
   }
 }
@@ -428,12 +485,12 @@ extern "C" TX_API int tx_dot_plan_create(const tx_dot_desc *desc,
 namespace {
 
 int launchGemm(const tx_dot_plan &plan, const void *A, const void *B, void *C,
-               const float *sa, const float *sb, hipStream_t stream) {
+               const void *sa, const void *sb, hipStream_t stream) {
   const tx_dot_desc &d = plan.desc;
   int op, epi;
   classify(d, &op, &epi);
   const int ci = findGemmConfig(op, epi, d.block_m, d.block_n, d.block_k,
-                                (d.flags & TX_FLAG_B_KMAJOR) != 0);
+                                (d.flags & TX_FLAG_B_KMAJOR) != 0, fmtOf(d));
   if (ci < 0)
     return fail(TX_ERR_UNSUPPORTED, "plan names a tile that is not instantiated");
   const GemmConfig &c = kGemmConfigs[ci];
@@ -454,14 +511,20 @@ int launchGemm(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   a.A = static_cast<const uint8_t *>(A);
   a.B = static_cast<const uint8_t *>(B);
   a.C = C;
-  a.sa = sa;
-  a.sb = sb;
+  a.sa = static_cast<const float *>(sa);
+  a.sb = static_cast<const float *>(sb);
   a.M = d.M;
   a.N = d.N;
   a.K = d.K;
   a.lda = d.lda;
   a.ldb = d.ldb;
   a.ldc = d.ldc;
+  const bool mx = d.scale_mode == TX_SCALE_MX32;
+  if (mx && d.a_type == TX_F4E2M1) {
+    // the kernel steps over bytes: K and lda in bytes of A, B's packed rows
+    a.K = d.K / 2;
+    a.lda = d.lda / 2;
+  }
   a.tiles_m = plan.m_tiles;
   a.tiles_n = plan.n_tiles;
   const int64_t masked_k = d.K - plan.k_split;
@@ -478,7 +541,7 @@ int launchGemm(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   }();
   const int gm = group_env > 0 ? group_env : 4;
   a.group_m = plan.m_tiles < gm ? plan.m_tiles : gm;
-  a.sa_ld = (int32_t)cdiv(d.K, 128);
+  a.sa_ld = (int32_t)(mx ? d.K / 32 : cdiv(d.K, 128));
   a.sb_ld = (int32_t)cdiv(d.N, 128);
   hipLaunchKernelGGL(c.fn, dim3(plan.grid_x), dim3(plan.block_threads),
                      c.lds_bytes, stream, a);
@@ -487,7 +550,7 @@ int launchGemm(const tx_dot_plan &plan, const void *A, const void *B, void *C,
 }
 
 int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
-                 const float *sa, const float *sb, void *ws, size_t ws_bytes,
+                 const void *sa, const void *sb, void *ws, size_t ws_bytes,
                  hipStream_t stream) {
   const tx_dot_desc &d = plan.desc;
   const int mt = decodeMT(d.M);
@@ -509,8 +572,8 @@ int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   a.A = static_cast<const int8_t *>(A);
   a.B = static_cast<const int8_t *>(B);
   a.C = static_cast<uint16_t *>(C);
-  a.sa = sa;
-  a.sb = sb;
+  a.sa = static_cast<const float *>(sa);
+  a.sb = static_cast<const float *>(sb);
   a.M = (int32_t)d.M;
   a.N = (int32_t)d.N;
   a.K = (int32_t)d.K;
@@ -536,7 +599,7 @@ int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
 
 extern "C" TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A,
                                     const void *B, void *C,
-                                    const float *scale_a, const float *scale_b,
+                                    const void *scale_a, const void *scale_b,
                                     void *workspace, size_t workspace_bytes,
                                     void *stream) {
   g_last_error.clear();
@@ -552,6 +615,9 @@ extern "C" TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A,
     return fail(TX_ERR_INVALID, "A, B and C must be 16-byte aligned");
   if (d.scale_mode != TX_SCALE_NONE && (!scale_a || !scale_b))
     return fail(TX_ERR_INVALID, "scaled dot needs scale_a and scale_b");
+  if (d.scale_mode != TX_SCALE_NONE &&
+      ((reinterpret_cast<uintptr_t>(scale_a) | reinterpret_cast<uintptr_t>(scale_b)) & 3))
+    return fail(TX_ERR_INVALID, "scale arrays must be 4-byte aligned");
   if (!tx_device_available())
     return fail(TX_ERR_NO_DEVICE, "no gfx950 device visible");
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -559,6 +625,7 @@ extern "C" TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A,
   case TX_KERNEL_GEMM_16BIT:
   case TX_KERNEL_GEMM_I8:
   case TX_KERNEL_GEMM_F8:
+  case TX_KERNEL_GEMM_MX:
     return launchGemm(*plan, A, B, C, scale_a, scale_b, s);
   case TX_KERNEL_DECODE_I8:
     return launchDecode(*plan, A, B, C, scale_a, scale_b, workspace,

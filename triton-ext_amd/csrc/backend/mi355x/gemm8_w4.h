@@ -45,6 +45,25 @@
 // the rest spread over row blocks 0..2 of step k+1: a 64 KiB burst would
 // stall the load path), and each B fragment is replaced by the next step's
 // as soon as the last row block's MFMA has used it.
+//
+// MX (tl.dot_scaled, EPI_MX_*): e8m0 scales per 32 K elements, applied by
+// the MFMA itself (v_mfma_scale_f32_16x16x128_f8f6f4 scale operands, no VALU
+// work).  The hardware ties lane l's scale byte to row l%16 of its operand
+// and TRUE K group l/16, and a lane's operand bytes are true K 16 (l/16) ..
+// +15 and 64 + 16 (l/16) .. +15, so MX reads the fragments in that order
+// (A chunks l/16 and 4 + l/16; B rows 16 (l/16) + {0, 8, 64, 72}) instead of
+// the unscaled kernels' free permutation.  fp8 (e4m3 / e5m2, formats may
+// differ) steps over 128 elements of K; fp4 (e2m1, two per byte) over 256,
+// the same 128 bytes, as two MFMAs per block: each takes one 16-byte chunk
+// (32 elements, lane l holding true K group l/16 of its 128).
+// Scales: per step each scale row holds SG = 4 (fp8) or 8 (fp4) bytes at
+// byte offset row * (K/32) + SG kt, which need not be 4-byte aligned: the
+// row is staged as NSD dwords from that offset rounded down (4-byte buffer
+// loads into LDS), and a lane reads its byte at the row's misalignment
+// (row * K/32) % 4 plus its group.  Groups at or past K/32 (only the last
+// step can have them) read the next row's bytes and are replaced by 127 in
+// that step: their operand data is zero, and only a NaN scale (0xFF) could
+// leak into the result.
 #pragma once
 
 #include "gemm16_w4.h"
@@ -53,18 +72,36 @@ namespace txk {
 
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 
-template <int OP, int EPI> struct Gemm8W4 {
+// The fp4 form of the scaled MFMA reads 4-dword operands: the intrinsic's
+// v4i32 overload, called by its LLVM name (the clang builtin is declared for
+// 8-dword operands only).
+extern "C" __device__ f32x4_t txk_mfma_scale_16x16x128_f4(i32x4_t, i32x4_t, f32x4_t, int, int,
+                                                          int, int, int, int)
+    __asm("llvm.amdgcn.mfma.scale.f32.16x16x128.f8f6f4.v4i32.v4i32");
+
+// FA, FB: MFMA format codes of A and B for the MX epilogues (0 e4m3, 1 e5m2,
+// 4 e2m1); unused otherwise.
+template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
   static constexpr int BM = 256, BN = 256, BK = 128, NW = 8, WN = 4;
   static constexpr int WTM = 128, WTN = 64, FM = WTM / 16, FN = WTN / 16;
   static constexpr bool SCALED = EPI == EPI_BLOCK128_BF16 || EPI == EPI_BLOCK128_F32;
   static constexpr bool INT = OP == OP_I8;
   static constexpr bool PARTIAL = SCALED; // fresh MFMA per step, VALU scale FMA
+  static constexpr bool MX = EPI == EPI_MX_F32 || EPI == EPI_MX_BF16;
+  static constexpr bool F4 = MX && FA == 4;
+  static constexpr int SG = F4 ? 8 : 4;  // MX: scale groups per K step
+  static constexpr int NSD = F4 ? 4 : 2; // MX: dwords staged per scale row
+  static constexpr int RS = 4 * NSD;     // MX: LDS bytes per scale row
   static constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN; // 32 KiB each
-  static constexpr int SA_OFF = A_BYTES + B_BYTES, SB_OFF = SA_OFF + BM * 4;
-  static constexpr uint32_t STAGE = SB_OFF + 256;
+  static constexpr int SA_OFF = A_BYTES + B_BYTES;
+  static constexpr int SB_OFF = SA_OFF + (MX ? BM * RS : BM * 4);
+  static constexpr uint32_t STAGE = SB_OFF + (MX ? BN * RS : 256);
   static constexpr int A_DMA = A_BYTES / 1024 / NW, B_DMA = B_BYTES / 1024 / NW; // 4, 4
   static constexpr uint32_t kOOB = 0x80000000u;
   static_assert(OP == OP_I8 || OP == OP_F8, "8-bit operands");
+  static_assert(!MX || (OP == OP_F8 && ((FA == 4) == (FB == 4)) && FA >= 0 && FA <= 4 &&
+                        FB >= 0 && FB <= 4 && FA != 2 && FA != 3 && FB != 2 && FB != 3),
+                "MX operands: e4m3 / e5m2 in any mix, or e2m1 on both sides");
   static_assert(STAGE % 128 == 0, "stage offsets keep address bits 0-6");
   static_assert(2 * STAGE <= 160 * 1024, "two stages in LDS");
 
@@ -112,6 +149,26 @@ template <int OP, int EPI> struct Gemm8W4 {
         W::buffer_lds16(v, rb, (uint32_t)((int64_t)k0 * p.ldb), st + A_BYTES + j * 1024);
       }
     }
+    if constexpr (MX) {
+      if (PART == 0 || PART == 2) {
+        // scale rows of A (part 0) or B (part 2): lane q of the operand's
+        // 256 * NSD dwords stages dword q % NSD of row q / NSD
+        const bool isA = PART == 0;
+        const int64_t r0 = isA ? m0 : n0, rows = isA ? p.M : p.N;
+        const uint32_t dst = st + (isA ? SA_OFF : SB_OFF);
+#pragma unroll
+        for (int t = 0; t < NSD / 2; ++t) {
+          const int q = (wave * (NSD / 2) + t) * 64 + lane;
+          const int row = q / NSD, dw = q % NSD;
+          const int64_t g = r0 + row;
+          const bool ok = live && (!MASK_MN || g < rows);
+          const uint32_t v =
+              ok ? (((uint32_t)g * (uint32_t)p.sa_ld) & ~3u) + 4u * (uint32_t)dw : kOOB;
+          buffer_lds4(v, isA ? rsa : rsb, (uint32_t)(kt * SG),
+                      dst + (uint32_t)(wave * (NSD / 2) + t) * 256u);
+        }
+      }
+    }
     if (SCALED && PART == 0) {
       if (wave < 4) {
         const int64_t gm = m0 + 64 * wave + lane;
@@ -141,16 +198,51 @@ template <int OP, int EPI> struct Gemm8W4 {
     const int lane = threadIdx.x & 63;
     const int G = lane >> 4, L = lane & 15;
     const int row = wm * WTM + L;
-    bs.a = lds0 + row * BK + (((2 * G) ^ ((row >> 1) & 7)) << 4);
-    const int k = 32 * G + (L >> 1);
+    bs.a = lds0 + row * BK + (((MX ? G : 2 * G) ^ ((row >> 1) & 7)) << 4);
+    const int k = (MX ? 16 : 32) * G + (L >> 1);
     bs.b = lds0 + A_BYTES + k * BN + (((4 * wn) ^ (k & 7)) << 4) + 8 * (L & 1);
+  }
+
+  // MX: per-lane LDS addresses (stage 0) of the scale bytes of A row block 0
+  // and B column block 0 (block f is + 16 RS f: 16 f rows further, the same
+  // misalignment since 16 f (K/32) % 4 == 0).
+  __device__ __forceinline__ static void scale_bases(const GemmArgs &p, int64_t m0, int64_t n0,
+                                                     uint32_t lds0, int wm, int wn, uint32_t &xa,
+                                                     uint32_t &xb) {
+    const int lane = threadIdx.x & 63;
+    const int G = lane >> 4, L = lane & 15;
+    const uint32_t sld = (uint32_t)p.sa_ld;
+    const int ra = wm * WTM + L, cb = wn * WTN + L;
+    xa = lds0 + SA_OFF + ra * RS + (((uint32_t)(m0 + ra) * sld) & 3u) + G;
+    xb = lds0 + SB_OFF + cb * RS + (((uint32_t)(n0 + cb) * sld) & 3u) + G;
+  }
+
+  // MX: the scale operand of block f: byte 0 the lane's group (fp4: byte 1
+  // the group of the second MFMA, 4 further).
+  __device__ __forceinline__ static int read_sx(uint32_t base, uint32_t so, int f) {
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    const uint32_t a = base + so + 16 * RS * f;
+    int v = *(const lds_u8 *)(uintptr_t)a;
+    if constexpr (F4)
+      v |= (int)*(const lds_u8 *)(uintptr_t)(a + 4) << 8;
+    return v;
+  }
+  // Scale operand v of step kt with the groups at or past ng set to 127.
+  __device__ __forceinline__ static int tail_sx(int v, int kt, int ng) {
+    const int G = (threadIdx.x & 63) >> 4;
+    if (kt * SG + G >= ng)
+      v = (v & ~0xff) | 127;
+    if constexpr (F4)
+      if (kt * SG + 4 + G >= ng)
+        v = (v & 0xff) | (127 << 8);
+    return v;
   }
 
   __device__ __forceinline__ static i32x8_t read_a(const Bases &bs, uint32_t so, int i) {
     typedef __attribute__((address_space(3))) i32x4_t lds_i32x4;
     const uint32_t a0 = bs.a + so + 2048 * i;
     const i32x4_t lo = *(const lds_i32x4 *)(uintptr_t)a0;
-    const i32x4_t hi = *(const lds_i32x4 *)(uintptr_t)(a0 ^ 16u);
+    const i32x4_t hi = *(const lds_i32x4 *)(uintptr_t)(a0 ^ (MX ? 64u : 16u));
     i32x8_t r;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -167,7 +259,8 @@ template <int OP, int EPI> struct Gemm8W4 {
     i32x8_t r;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t *)(uintptr_t)(b0 + q * 8 * BN));
+      const uint32_t rows = MX ? (q & 1) * 8 + (q >> 1) * 64 : q * 8;
+      const v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t *)(uintptr_t)(b0 + rows * BN));
       r[2 * q] = v.x;
       r[2 * q + 1] = v.y;
     }
@@ -186,6 +279,24 @@ template <int OP, int EPI> struct Gemm8W4 {
     } else {
       // format 0 for both operands: fp8 e4m3; no hardware block scales.
       return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bcol, arow, c, 0, 0, 0, 0, 0, 0);
+    }
+  }
+
+  // MX: acc += (B cols * 2^(sbx - 127)) . (A rows * 2^(sxa - 127)), the
+  // scales per 32 K elements as laid out above.
+  __device__ __forceinline__ static Acc mma_mx(const i32x8_t &bcol, const i32x8_t &arow, Acc c,
+                                               int sbx, int sxa) {
+    if constexpr (F4) {
+      i32x4_t b0, b1, a0, a1;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        b0[t] = bcol[t], b1[t] = bcol[4 + t], a0[t] = arow[t], a1[t] = arow[4 + t];
+      }
+      c = txk_mfma_scale_16x16x128_f4(b0, a0, c, 4, 4, 0, sbx, 0, sxa);
+      return txk_mfma_scale_16x16x128_f4(b1, a1, c, 4, 4, 1, sbx, 1, sxa);
+    } else {
+      return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bcol, arow, c, FB, FA, 0, sbx, 0,
+                                                               sxa);
     }
   }
 
@@ -217,6 +328,15 @@ template <int OP, int EPI> struct Gemm8W4 {
     if (SCALED) {
       rsa = make_rsrc(p.sa, (uint32_t)(p.M * p.sa_ld * 4));
       rsb = make_rsrc(p.sb, (uint32_t)(((p.K + 127) / 128) * p.sb_ld * 4));
+    }
+    uint32_t xa = 0, xb = 0;
+    const int ng = p.sa_ld; // MX: scale groups per row
+    if constexpr (MX) {
+      // sizes rounded up to whole dwords: every dword read holds at least
+      // one byte of the array (its base is 4-byte aligned)
+      rsa = make_rsrc(p.sa, (uint32_t)((p.M * p.sa_ld + 3) & ~3ll));
+      rsb = make_rsrc(p.sb, (uint32_t)((p.N * p.sa_ld + 3) & ~3ll));
+      scale_bases(p, m0, n0, lds0, wm, wn, xa, xb);
     }
     Bases bs;
     bases(lds0, wm, wn, bs);
@@ -268,22 +388,39 @@ template <int OP, int EPI> struct Gemm8W4 {
       step_barrier();
       part_of(1, std::integral_constant<int, 0>());
       i32x8_t b[FN];
+      int sbx[FN]; // MX: B scale operands of the step
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
+      for (int j = 0; j < FN; ++j) {
         b[j] = read_b(bs, 0, j);
+        sbx[j] = MX ? read_sx(xb, 0, j) : 0;
+      }
       // One step from stage so; more: a following step exists (issue its
-      // remaining loads in row blocks 0..2, the barrier, refill b from sn).
-      auto step = [&](int kt, bool more) {
+      // remaining loads in row blocks 0..2, the barrier, refill b from sn);
+      // tail: the last step (MX scale groups past K/32 possible).
+      auto step = [&](int kt, bool more, auto tail) {
+        constexpr bool TAIL = MX && decltype(tail)::value;
         const uint32_t so = (kt & 1) * STAGE, sn = ((kt + 1) & 1) * STAGE;
         i32x8_t a = read_a(bs, so, 0);
         float sc = scale(so, 0);
+        int sxa = MX ? read_sx(xa, so, 0) : 0;
+        if constexpr (TAIL) {
+          sxa = tail_sx(sxa, kt, ng);
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            sbx[j] = tail_sx(sbx[j], kt, ng);
+        }
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
           i32x8_t an;
           float sn_;
+          int sxn = 0;
           if (i + 1 < FM) {
             an = read_a(bs, so, i + 1);
             sn_ = scale(so, i + 1);
+            if constexpr (MX)
+              sxn = read_sx(xa, so, i + 1);
+            if constexpr (TAIL)
+              sxn = tail_sx(sxn, kt, ng);
           }
           if (more && i == FM - 1) {
             step_barrier();
@@ -294,11 +431,17 @@ template <int OP, int EPI> struct Gemm8W4 {
           for (int j = 0; j < FN; ++j) {
             if constexpr (PARTIAL) {
               Q[j] = mma(b[j], a, Acc{0, 0, 0, 0});
+            } else if constexpr (MX) {
+              acc[i][j] = mma_mx(b[j], a, acc[i][j], sbx[j], sxa);
+              pin(acc[i][j]);
             } else {
               acc[i][j] = mma(b[j], a, acc[i][j]);
             }
-            if (more && i == FM - 1)
+            if (more && i == FM - 1) {
               b[j] = read_b(bs, sn, j);
+              if constexpr (MX)
+                sbx[j] = read_sx(xb, sn, j);
+            }
           }
           if (more && i == 0) part_of(kt + 1, std::integral_constant<int, 1>());
           if (more && i == 1) part_of(kt + 1, std::integral_constant<int, 2>());
@@ -313,13 +456,14 @@ template <int OP, int EPI> struct Gemm8W4 {
           if (i + 1 < FM) {
             a = an;
             sc = sn_;
+            sxa = sxn;
           }
           __builtin_amdgcn_sched_barrier(0);
         }
       };
       for (int kt = 0; kt + 1 < total; ++kt)
-        step(kt, true);
-      step(total - 1, false);
+        step(kt, true, std::false_type());
+      step(total - 1, false, std::true_type());
       flush(acc[FM - 1]);
       __builtin_amdgcn_s_waitcnt(0x7 << 4);
     }
@@ -356,7 +500,7 @@ template <int OP, int EPI> struct Gemm8W4 {
         const Acc &v = acc[i][j];
         if (EPI == EPI_I32) {
           *reinterpret_cast<i32x4_t *>(reinterpret_cast<int32_t *>(p.C) + off) = v;
-        } else if (EPI == EPI_F32 || EPI == EPI_BLOCK128_F32) {
+        } else if (EPI == EPI_F32 || EPI == EPI_BLOCK128_F32 || EPI == EPI_MX_F32) {
           *reinterpret_cast<f32x4_t *>(reinterpret_cast<float *>(p.C) + off) = v;
         } else {
           float f[4];
@@ -383,9 +527,9 @@ template <int OP, int EPI> struct Gemm8W4 {
   }
 };
 
-template <int OP, int EPI>
+template <int OP, int EPI, int FA = 0, int FB = 0>
 __global__ void __launch_bounds__(512, 1) gemm8_w4_kernel(GemmArgs p) {
-  typedef Gemm8W4<OP, EPI> G;
+  typedef Gemm8W4<OP, EPI, FA, FB> G;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * G::STAGE];
   int tm, tn;
   tile_coords(p, tm, tn);

@@ -47,6 +47,8 @@ enum EpiKind {
   EPI_ROWCOL_BF16 = 4,   // bf16((float(acc) * sa[m]) * sb[n])
   EPI_BLOCK128_BF16 = 5, // per-128-K-block scaled fp32 acc, RNE to bf16
   EPI_BLOCK128_F32 = 6,  // per-128-K-block scaled fp32 acc
+  EPI_MX_F32 = 7,        // e8m0 per-32-K scales applied by the MFMA, fp32 C
+  EPI_MX_BF16 = 8,       // the same, RNE to bf16
 };
 
 template <int OP> struct OpTraits;
@@ -111,8 +113,8 @@ struct GemmArgs {
   const uint8_t *A;
   const uint8_t *B;
   void *C;
-  const float *sa; // ROWCOL: [M]; BLOCK128: [M][sa_ld]
-  const float *sb; // ROWCOL: [N]; BLOCK128: [ceil(K/128)][sb_ld]
+  const float *sa; // ROWCOL: [M]; BLOCK128: [M][sa_ld]; MX: uint8 [M][sa_ld]
+  const float *sb; // ROWCOL: [N]; BLOCK128: [ceil(K/128)][sb_ld]; MX: uint8 [N][sa_ld]
   int64_t M, N, K;
   int64_t lda, ldb, ldc; // row strides in elements
   int32_t tiles_m, tiles_n;
@@ -120,7 +122,7 @@ struct GemmArgs {
   int32_t k_masked_steps; // masked K steps after them
   int32_t last_ks;        // MFMA sub-steps issued in the final K step
   int32_t group_m;        // tile rows per group in the tile order
-  int32_t sa_ld, sb_ld;
+  int32_t sa_ld, sb_ld; // MX: sa_ld = bytes per scale row = K / 32 groups
 };
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own

@@ -7,7 +7,8 @@
 // recommends a tile from the set the mi355x_dot backend instantiates.
 //
 // MI355X public dense peaks: bf16/fp16 MFMA 2516.6 TFLOP/s (256 CUs x
-// 2.4 GHz x 4096 FLOP/clk/CU), fp8 and int8 5033.2 T(FL)OP/s, HBM3E 8 TB/s.
+// 2.4 GHz x 4096 FLOP/clk/CU), fp8 and int8 5033.2 T(FL)OP/s, fp4 10066.4
+// TFLOP/s, HBM3E 8 TB/s.
 
 #include "triton_ext/TritonExtPassInfra.h"
 #include "triton_ext/tx_dot.h"
@@ -20,6 +21,7 @@ namespace {
 
 constexpr double kPeak16 = 2516.6e12;
 constexpr double kPeak8 = 5033.2e12;
+constexpr double kPeak4 = 10066.4e12;
 constexpr double kPeakF32 = 157.3e12;
 constexpr double kHbm = 8.0e12;
 constexpr int kCUs = 256;
@@ -39,6 +41,9 @@ const Tile kTiles16[] = {{256, 256, 64, 0.85}, {128, 128, 64, 0.60},
 // all CUs at N = 7168, but its A-resident wave layout needs 28 transposed B
 // reads per step against 16, and measured no faster than 256x256 there.)
 const Tile kTiles8[] = {{256, 256, 128, 0.85}, {128, 128, 128, 0.60}};
+// MX (tl.dot_scaled) tiles: one 256x256 tile of 128 bytes of K per step,
+// i.e. 128 fp8 or 256 fp4 elements.
+const Tile kTileMx8 = {256, 256, 128, 0.85}, kTileMx4 = {256, 256, 256, 0.85};
 
 // Estimated time of a tiled dot in arbitrary units: whole waves of tiles
 // across the CUs, each tile costing BM*BN*K / eff.
@@ -64,16 +69,23 @@ Tile chooseTile(const Tile (&cands)[N], int64_t M, int64_t Nn, int64_t K) {
 
 } // namespace
 
-extern "C" int32_t tx_dtype_size(int32_t dtype) {
+extern "C" int32_t tx_dtype_bits(int32_t dtype) {
   switch (dtype) {
-  case TX_F32: return 4;
-  case TX_F16: return 2;
-  case TX_BF16: return 2;
-  case TX_I8: return 1;
-  case TX_F8E4M3: return 1;
-  case TX_I32: return 4;
+  case TX_F32: return 32;
+  case TX_F16: return 16;
+  case TX_BF16: return 16;
+  case TX_I8: return 8;
+  case TX_F8E4M3: return 8;
+  case TX_I32: return 32;
+  case TX_F8E5M2: return 8;
+  case TX_F4E2M1: return 4;
   default: return 0;
   }
+}
+
+extern "C" int32_t tx_dtype_size(int32_t dtype) {
+  const int32_t b = tx_dtype_bits(dtype);
+  return b % 8 ? 0 : b / 8;
 }
 
 extern "C" double tx_mi355x_peak_flops(int32_t dtype) {
@@ -81,7 +93,9 @@ extern "C" double tx_mi355x_peak_flops(int32_t dtype) {
   case TX_F16:
   case TX_BF16: return kPeak16;
   case TX_I8:
-  case TX_F8E4M3: return kPeak8;
+  case TX_F8E4M3:
+  case TX_F8E5M2: return kPeak8;
+  case TX_F4E2M1: return kPeak4;
   case TX_F32: return kPeakF32;
   default: return 0.0;
   }
@@ -93,10 +107,11 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
   if (!d || !out)
     return TX_ERR_INVALID;
   *out = tx_ai_report{};
-  int32_t sa = tx_dtype_size(d->a_type), sb = tx_dtype_size(d->b_type),
-          sc = tx_dtype_size(d->c_type);
-  if (!sa || !sb || !sc || d->M < 0 || d->N < 0 || d->K < 0)
+  const int32_t ba = tx_dtype_bits(d->a_type), bb = tx_dtype_bits(d->b_type),
+                bc = tx_dtype_bits(d->c_type);
+  if (!ba || !bb || !bc || d->M < 0 || d->N < 0 || d->K < 0)
     return TX_ERR_INVALID;
+  const double sa = ba / 8.0, sb = bb / 8.0, sc = bc / 8.0; // bytes per element
   const double M = (double)d->M, N = (double)d->N, K = (double)d->K;
   double scaleBytes = 0.0;
   if (d->scale_mode == TX_SCALE_ROWCOL)
@@ -104,10 +119,14 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
   else if (d->scale_mode == TX_SCALE_BLOCK128)
     scaleBytes = 4.0 * (M * cdiv(d->K, 128) +
                         (double)cdiv(d->K, 128) * cdiv(d->N, 128));
+  else if (d->scale_mode == TX_SCALE_MX32)
+    scaleBytes = (M + N) * (double)cdiv(d->K, 32); // one e8m0 byte per 32 K
   out->flops = 2.0 * M * N * K;
   out->bytes = M * K * sa + K * N * sb + M * N * sc + scaleBytes;
   out->intensity = out->bytes > 0 ? out->flops / out->bytes : 0.0;
-  out->peak_flops = tx_mi355x_peak_flops(d->a_type);
+  // a mixed product runs at the rate of its wider operand
+  out->peak_flops = ba >= bb ? tx_mi355x_peak_flops(d->a_type)
+                             : tx_mi355x_peak_flops(d->b_type);
   out->peak_bw = kHbm;
   out->ridge = out->peak_flops / out->peak_bw;
   out->bound = out->intensity > out->ridge ? TX_BOUND_MFMA : TX_BOUND_HBM;
@@ -117,7 +136,9 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
 
   Tile t{d->block_m, d->block_n, d->block_k, 1.0};
   if (t.bm <= 0 || t.bn <= 0 || t.bk <= 0) {
-    if (sa == 2 && (d->flags & TX_FLAG_B_KMAJOR))
+    if (d->scale_mode == TX_SCALE_MX32)
+      t = ba == 4 ? kTileMx4 : kTileMx8;
+    else if (sa == 2 && (d->flags & TX_FLAG_B_KMAJOR))
       t = kTiles16[0]; // the K-major B kernel exists for this tile only
     else if (sa == 2)
       t = chooseTile(kTiles16, d->M, d->N, d->K);

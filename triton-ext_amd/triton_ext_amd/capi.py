@@ -6,16 +6,18 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(os.path.dirname(PKG_DIR), "lib")
 
 # tx_dtype
-F32, F16, BF16, I8, F8E4M3, I32 = 0, 1, 2, 3, 4, 5
-DTYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", I8: "i8", F8E4M3: "f8e4m3", I32: "i32"}
+F32, F16, BF16, I8, F8E4M3, I32, F8E5M2, F4E2M1 = 0, 1, 2, 3, 4, 5, 6, 7
+DTYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", I8: "i8", F8E4M3: "f8e4m3", I32: "i32",
+               F8E5M2: "f8e5m2", F4E2M1: "f4e2m1"}
 # tx_scale_mode
-SCALE_NONE, SCALE_ROWCOL, SCALE_BLOCK128 = 0, 1, 2
+SCALE_NONE, SCALE_ROWCOL, SCALE_BLOCK128, SCALE_MX32 = 0, 1, 2, 3
 # tx_bound
 BOUND_UNKNOWN, BOUND_MFMA, BOUND_HBM = 0, 1, 2
 # tx_status
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_NO_DEVICE, ERR_WORKSPACE, ERR_NO_PASS = range(7)
 # tx_kernel
-KERNEL_NONE, KERNEL_GEMM_16BIT, KERNEL_GEMM_I8, KERNEL_DECODE_I8, KERNEL_GEMM_F8 = range(5)
+(KERNEL_NONE, KERNEL_GEMM_16BIT, KERNEL_GEMM_I8, KERNEL_DECODE_I8, KERNEL_GEMM_F8,
+ KERNEL_GEMM_MX) = range(6)
 FLAG_NO_LOOP_SPLIT = 0x1
 FLAG_B_KMAJOR = 0x2  # B stored [N][K] row-major (a transposed view in torch)
 # TritonPluginResult
@@ -118,6 +120,7 @@ def load(name="libmi355x_dot.so"):
                                       ctypes.POINTER(i32)]
     elif name == "libarith_intensity.so":
         L.tx_dtype_size.argtypes = [i32]
+        L.tx_dtype_bits.argtypes = [i32]
         L.tx_mi355x_peak_flops.argtypes = [i32]
         L.tx_mi355x_peak_flops.restype = ctypes.c_double
         L.tx_mi355x_peak_bw.restype = ctypes.c_double

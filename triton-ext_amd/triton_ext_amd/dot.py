@@ -17,7 +17,7 @@ def tx_type(t):
         _TORCH_TYPES.update({torch.float32: capi.F32, torch.float16: capi.F16,
                              torch.bfloat16: capi.BF16, torch.int8: capi.I8,
                              torch.float8_e4m3fn: capi.F8E4M3, torch.uint8: capi.F8E4M3,
-                             torch.int32: capi.I32})
+                             torch.int32: capi.I32, torch.float8_e5m2: capi.F8E5M2})
     if t.dtype not in _TORCH_TYPES:
         raise TypeError(f"unsupported dtype {t.dtype}")
     return _TORCH_TYPES[t.dtype]
@@ -102,4 +102,79 @@ def dot(a, b, out=None, out_dtype=None, scale_a=None, scale_b=None, scale_mode=N
                                None if scale_b is None else scale_b.data_ptr(),
                                None if ws is None else ws.data_ptr(),
                                0 if ws is None else ws.numel(), stream))
+    return out
+
+
+_MX_FORMATS = {"e4m3": capi.F8E4M3, "e5m2": capi.F8E5M2, "e2m1": capi.F4E2M1}
+
+
+def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
+               fast_math=False, lhs_k_pack=True, rhs_k_pack=True, out_dtype=None, out=None,
+               block=(0, 0, 0), plan=None, stream=None):
+    """tl.dot_scaled over torch device tensors (T:language/core.py:2064-2101).
+
+    lhs [M, K] (e2m1: uint8 [M, K/2], two elements per byte, even K in the
+    low nibble), rhs [K, N] (e2m1: uint8 [K/2, N]); fp8 operands as
+    float8_e4m3fn / float8_e5m2 or their uint8 bits.  lhs_scale uint8
+    [M, K/32] and rhs_scale uint8 [N, K/32] hold e8m0 exponents (2^(s-127)),
+    rhs_scale indexed by column first and not transposed.  Returns fp32 (or
+    bf16 with out_dtype=torch.bfloat16) [M, N].  Checks follow
+    T:language/semantic.py:1597-1665; what this backend does not implement
+    (bf16/fp16 formats, scales of None, e2m1 mixed with fp8, packing along M
+    or N, `acc`) raises NotImplementedError.
+    """
+    import torch
+    for name, fmt in (("lhs_format", lhs_format), ("rhs_format", rhs_format)):
+        if fmt not in ("e2m1", "e4m3", "e5m2", "bf16", "fp16"):
+            raise ValueError(f"NYI: {name} {fmt}")
+        if fmt not in _MX_FORMATS:
+            raise NotImplementedError(f"{name} {fmt}: only e4m3, e5m2 and e2m1 are implemented")
+    if lhs_scale is None or rhs_scale is None:
+        raise NotImplementedError("both operands need e8m0 scales")
+    if acc is not None:
+        raise NotImplementedError("acc: accumulate into the result on the caller's side")
+    if not lhs_k_pack or not rhs_k_pack:
+        raise NotImplementedError("only K-packed e2m1 operands are implemented")
+    if lhs.dim() != 2 or rhs.dim() != 2:
+        raise ValueError(f"Both inputs must be 2D; (lhs: {tuple(lhs.shape)} vs rhs: "
+                         f"{tuple(rhs.shape)})")
+    pa = 2 if lhs_format == "e2m1" else 1
+    pb = 2 if rhs_format == "e2m1" else 1
+    M, K = lhs.shape[0], lhs.shape[1] * pa
+    N = rhs.shape[1]
+    if rhs.shape[0] * pb != K:
+        raise ValueError("Reduction dimension should pack the same number of elements; "
+                         f"(lhs: {tuple(lhs.shape)} vs rhs: {tuple(rhs.shape)})")
+    if tuple(lhs_scale.shape) != (M, K // 32):
+        raise ValueError(f"lhs_scale must be a tensor of shape [{M}, {K // 32}]. "
+                         f"Got {list(lhs_scale.shape)}")
+    if tuple(rhs_scale.shape) != (N, K // 32):
+        raise ValueError(f"rhs_scale must be a tensor of shape [{N}, {K // 32}]. "
+                         f"Got {list(rhs_scale.shape)}")
+    for t, nm in ((lhs_scale, "lhs_scale"), (rhs_scale, "rhs_scale")):
+        if t.dtype != torch.uint8 or not t.is_contiguous():
+            raise ValueError(f"{nm} must be a contiguous uint8 (e8m0) tensor")
+    if lhs.stride(1) != 1 or rhs.stride(1) != 1:
+        raise ValueError("lhs and rhs rows must be contiguous")
+    if out is not None:
+        c_tx = tx_type(out)
+    else:
+        c_tx = capi.BF16 if out_dtype == torch.bfloat16 else capi.F32
+    if plan is None:
+        lda = lhs.stride(0) * pa if M > 0 and K > 0 else 0
+        ldb = rhs.stride(0) if K > 0 and N > 0 else 0
+        desc = capi.make_desc(M, N, K, _MX_FORMATS[lhs_format], c_tx,
+                              b_type=_MX_FORMATS[rhs_format], scale_mode=capi.SCALE_MX32,
+                              block=block, lda=lda, ldb=ldb)
+        plan = capi.plan(desc)
+    if out is None:
+        out = torch.empty((M, N), dtype=_torch_dtype(c_tx), device=lhs.device)
+    if out.stride(1) != 1 or out.stride(0) != plan.desc.ldc:
+        raise ValueError("output must be row-major with ldc == N")
+    if stream is None:
+        stream = torch.cuda.current_stream(lhs.device).cuda_stream
+    L = capi.load()
+    capi.check(L.tx_dot_launch(ctypes.byref(plan), lhs.data_ptr(), rhs.data_ptr(),
+                               out.data_ptr(), lhs_scale.data_ptr(), rhs_scale.data_ptr(),
+                               None, 0, stream))
     return out
