@@ -8,8 +8,9 @@ fp32 accumulation, entries N(0,1)/sqrt(K).  `value` is its TFLOP/s (2*M*N*K
 per step over the timed region, HIP events on the launch stream).  The other
 configs are reported under "secondary": the LoopSplit K-tail and edge cases,
 int8 W8A8 decode (M = 1, 16, 64, 256; HBM-bound, timed per launch with the
-256 MB MALL flushed between launches so B streams from HBM), and the fp8
-block-scaled dot.
+256 MB MALL flushed between launches so B streams from HBM), the fp8
+block-scaled dot, and tl.dot_scaled's MX formats (mxfp8 e4m3 and mxfp4 e2m1
+with e8m0 scales per 32 K, fp32 C).
 
 cpu_baseline: the CPU oracle (a C restatement of the Triton interpreter's
 tiled dot, oracle/) on the host cores for the same bf16 4096^3 inputs; it
@@ -31,6 +32,7 @@ for p in (ROOT, os.path.join(ROOT, "triton-ext_amd")):
 METRIC = "tt.dot TFLOP/s + % MFMA/HBM roofline (bf16 4096^3; int8 W8A8 M=16)"
 PEAK_BF16 = 2516.6e12
 PEAK_I8 = 5033.2e12
+PEAK_F4 = 10066.4e12
 HBM = 8.0e12
 # HBM bytes per launch of the bf16 4096^3 kernel: rocprofv3 FETCH_SIZE + WRITE_SIZE of one
 # dispatch, each scaled by the counter's reading for a 256 MiB copy (--copy-probe): FETCH x2.0,
@@ -46,7 +48,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
                     help="secondary workloads to run, comma-separated: vendor, tail, w8a8 (or "
-                         "w8a8_1, w8a8_16, w8a8_64, w8a8_256), fp8, kmajor (default: all); the bf16 "
+                         "w8a8_1, w8a8_16, w8a8_64, w8a8_256), fp8, kmajor, mx (or mxfp8, mxfp4, "
+                         "mxfp8_4096, mxfp8_8192, mxfp4_4096, mxfp4_8192) (default: all); the bf16 "
                          "headline always runs")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 256 MiB five times (a transfer of known size that scales the "
@@ -228,6 +231,57 @@ def bench_fp8(tx, dev, M, N, K, steps, warmup, seed=5):
                 frac=flops / ms / 1e-3 / PEAK_I8)
 
 
+def mx_quantize(x, fmt):
+    """OCP MX quantisation of x [R, K] along K: per 32 elements the shared
+    exponent floor(log2(amax)) - emax (e4m3: 8, e2m1: 2), elements x / 2^e
+    rounded to the format.  Returns (uint8 codes, e2m1 packed two per byte
+    along K; uint8 e8m0 scales [R, K/32])."""
+    import torch
+    R, K = x.shape
+    g = x.view(R, K // 32, 32)
+    amax = g.abs().amax(dim=2).clamp_min(2.0 ** -100)
+    e = torch.floor(torch.log2(amax)) - (8 if fmt == "e4m3" else 2)
+    y = g / torch.exp2(e)[:, :, None]
+    scales = (e + 127).clamp(0, 254).to(torch.uint8)
+    if fmt == "e4m3":
+        return y.reshape(R, K).to(torch.float8_e4m3fn).view(torch.uint8), scales
+    vals = torch.tensor([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], device=x.device)
+    mid = (vals[1:] + vals[:-1]) / 2
+    code = torch.bucketize(y.abs().clamp_max(6.0), mid).to(torch.uint8)
+    code = (code | ((y < 0).to(torch.uint8) << 3)).reshape(R, K)
+    return (code[:, 0::2] | (code[:, 1::2] << 4)).contiguous(), scales
+
+
+def bench_mx(tx, dev, M, N, K, fmt, steps, warmup, seed=7):
+    """tl.dot_scaled(A, sa, fmt, B, sb, fmt), fp32 C: N(0,1) inputs MX-quantised."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    qa, sa = mx_quantize(torch.randn((M, K), generator=g, device=dev), fmt)
+    qbt, sb = mx_quantize(torch.randn((N, K), generator=g, device=dev), fmt)  # B^T rows
+    # B [K, N] (e2m1: [K/2, N], byte (k2, n) = codes (2 k2, n) | (2 k2 + 1, n) << 4)
+    qb = qbt.t().contiguous()
+    c = torch.empty((M, N), dtype=torch.float32, device=dev)
+    tf = tx.F8E4M3 if fmt == "e4m3" else tx.F4E2M1
+    p = tx.plan(tx.make_desc(M, N, K, tf, tx.F32, scale_mode=tx.SCALE_MX32))
+    L = tx.load()
+    args = (ctypes.byref(p), qa.data_ptr(), qb.data_ptr(), c.data_ptr(), sa.data_ptr(),
+            sb.data_ptr(), None, 0, torch.cuda.current_stream().cuda_stream)
+
+    def run():
+        rc = L.tx_dot_launch(*args)
+        if rc != 0:
+            raise RuntimeError(L.tx_get_last_error().decode())
+    ms = time_back_to_back(run, steps, warmup)
+    flops = 2.0 * M * N * K
+    peak = PEAK_I8 if fmt == "e4m3" else PEAK_F4
+    name = "mxfp8 e4m3" if fmt == "e4m3" else "mxfp4 e2m1"
+    return dict(workload=f"tl.dot_scaled {name} (e8m0 per 32) {M}x{N}x{K}, fp32 C", ms=ms,
+                tflops=flops / ms / 1e9, frac=flops / ms / 1e-3 / peak, peak_tflops=peak / 1e12,
+                plan=dict(kernel=L.tx_kernel_name(p.kernel).decode(),
+                          tile=[p.desc.block_m, p.desc.block_n, p.desc.block_k]))
+
+
 def cpu_baseline(a, b, c, M, N, K, block):
     """Oracle on the host cores over the full bf16 workload; also checks the GPU output."""
     import numpy as np
@@ -313,6 +367,15 @@ def main():
         r = bench_fp8(tx, dev, 2048, 7168, 7168, args.steps, args.warmup)
         secondary.append(r)
         print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+
+    for fmt, short in (("e4m3", "mxfp8"), ("e2m1", "mxfp4")):
+        for n in (4096, 8192):
+            if want("mx") or want(short) or want(f"{short}_{n}"):
+                r = bench_mx(tx, dev, n, n, n, fmt, args.steps, args.warmup)
+                secondary.append(r)
+                print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s "
+                      f"({100 * r['frac']:.1f}% of {r['peak_tflops']:.0f})", file=sys.stderr,
+                      flush=True)
 
     cpu, parity = None, None
     if not args.no_cpu:
