@@ -49,6 +49,9 @@ def lib():
             getattr(L, name).argtypes = [vp, vp, i64]
         L.or_quantize_e4m3_groups.argtypes = [vp, i64, i64, i32, i32, vp, vp]
         L.or_mx_decode_array.argtypes = [vp, vp, i64, i32]
+        L.oracle_attn_fwd.restype = i32
+        L.oracle_attn_fwd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i32, ctypes.c_float,
+                                      i32, i32, i32, i32, i32]
         L.oracle_dot_scaled.restype = i32
         L.oracle_dot_scaled.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64,
                                         i32, i32, i32, i32, i32]
@@ -178,3 +181,25 @@ def dot_scaled(a, sa, a_fmt, b, sb, b_fmt, *, K, c_type=F32, round_mode=ROUND_RN
     if rc != 0:
         raise ValueError(f"oracle_dot_scaled rejected the arguments (rc={rc})")
     return out
+
+
+def attn_fwd(q, k, v, *, sm_scale, causal, block=(64, 32), mode=0, nthreads=0):
+    """The fused-attention tutorial's forward on the CPU.
+
+    q, k, v: uint16 fp16 bits [Z, H, N, D] (made contiguous).  Returns
+    (o as uint16 fp16 bits [Z, H, N, D], M fp32 [Z * H, N]).  block =
+    (BLOCK_M, BLOCK_N); mode 0 the tutorial's split loop, 1 every block
+    masked, 2 mode 0 without the blocks past the diagonal.
+    """
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    Z, H, N, D = q.shape
+    assert k.shape == q.shape and v.shape == q.shape
+    o = np.zeros(q.shape, dtype=np.uint16)
+    M = np.zeros((Z * H, N), dtype=np.float32)
+    rc = lib().oracle_attn_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(M), Z, H, N, D,
+                               float(sm_scale), int(causal), block[0], block[1], mode, nthreads)
+    if rc != 0:
+        raise ValueError(f"oracle_attn_fwd rejected the arguments (rc={rc})")
+    return o, M

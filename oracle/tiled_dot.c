@@ -295,6 +295,138 @@ int oracle_dot_scaled(const void *Av, const void *Bv, void *Cv, const uint8_t *s
   return 0;
 }
 
+/* ---------------- fused attention forward ----------------
+ * The forward of the fused-attention tutorial as the interpreter runs it
+ * (R:pass/LoopSplit/06-fused-attention.py:44-93 _attn_fwd_inner, :181-239
+ * _attn_fwd): fp16 q, k, v [Z][H][N][D] packed, one program per (z*H + h,
+ * block of BM rows), K/V blocks of BN keys:
+ *   m_i = -inf, l_i = 1, acc = 0, qk_scale = fp32(sm_scale * 1.44269504)
+ *   qk = q @ k^T                         fp32, d ascending
+ *   on-band (start_n >= causal_start):   qk = fl(qk*s) + (m >= n ? 0 : -1e6);
+ *                                        m_ij = max(m_i, rowmax qk); qk -= m_ij
+ *   off-band:                            m_ij = max(m_i, fl(rowmax(qk)*s));
+ *                                        qk = fl(qk*s) - m_ij
+ *   p = exp2(qk); l_ij = rowsum p (ascending); alpha = exp2(m_i - m_ij)
+ *   l_i = l_i*alpha + l_ij; acc = acc*alpha; acc = (fp16(p) @ v) + acc
+ *   m_i = m_ij;  finally M = m_i + log2(l_i), o = fp16(acc / l_i)
+ * causal_start = start_m*BM (causal) or N.  mode (tests only) 0: the
+ * tutorial's loop over all keys, split at causal_start; 1: the same loop
+ * with every block in the masked form (no split); 2: mode 0 without the
+ * blocks wholly past the diagonal.  Returns 0, or -1 on bad arguments.
+ */
+int oracle_attn_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, uint16_t *o,
+                    float *M, int64_t Z, int64_t H, int64_t N, int D, float sm_scale,
+                    int causal, int BM, int BN, int mode, int nthreads) {
+  if (Z < 0 || H < 0 || N < 0 || D <= 0 || BM <= 0 || BN <= 0 || N % BM || N % BN)
+    return -1;
+  const float qk_scale = sm_scale * 1.44269504f;
+  const int64_t programs = Z * H * (N / BM);
+  int rc = 0;
+#ifdef _OPENMP
+  if (nthreads <= 0)
+    nthreads = omp_get_max_threads();
+#pragma omp parallel num_threads(nthreads)
+#endif
+  {
+    float *qb = (float *)malloc(sizeof(float) * (size_t)BM * D);
+    float *acc = (float *)malloc(sizeof(float) * (size_t)BM * D);
+    float *qk = (float *)malloc(sizeof(float) * (size_t)BM * BN);
+    float *pv = (float *)malloc(sizeof(float) * (size_t)BM * D);
+    float *m_i = (float *)malloc(sizeof(float) * (size_t)BM);
+    float *l_i = (float *)malloc(sizeof(float) * (size_t)BM);
+    if (!qb || !acc || !qk || !pv || !m_i || !l_i) {
+#ifdef _OPENMP
+#pragma omp atomic write
+#endif
+      rc = -2;
+    } else {
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+      for (int64_t pid = 0; pid < programs; ++pid) {
+        const int64_t hz = pid / (N / BM), start_m = pid % (N / BM);
+        const int64_t base = hz * N * D, m0 = start_m * BM;
+        for (int i = 0; i < BM; ++i) {
+          for (int d = 0; d < D; ++d) {
+            qb[i * D + d] = or_f16_to_f32(q[base + (m0 + i) * D + d]);
+            acc[i * D + d] = 0.f;
+          }
+          m_i[i] = -INFINITY;
+          l_i[i] = 1.0f;
+        }
+        const int64_t causal_start = causal ? m0 : N;
+        for (int64_t n0 = 0; n0 < N; n0 += BN) {
+          if (mode == 2 && causal && n0 >= m0 + BM)
+            break;
+          const int masked = mode == 1 || n0 >= causal_start;
+          for (int i = 0; i < BM; ++i)
+            for (int j = 0; j < BN; ++j) {
+              float t = 0.f;
+              for (int d = 0; d < D; ++d)
+                t += qb[i * D + d] * or_f16_to_f32(k[base + (n0 + j) * D + d]);
+              qk[i * BN + j] = t;
+            }
+          for (int i = 0; i < BM; ++i) {
+            float *r = qk + (size_t)i * BN;
+            float m_ij;
+            if (masked) {
+              float mx = -INFINITY;
+              for (int j = 0; j < BN; ++j) {
+                float t = r[j] * qk_scale;
+                t = t + ((!causal || m0 + i >= n0 + j) ? 0.0f : -1.0e6f);
+                r[j] = t;
+                if (t > mx)
+                  mx = t;
+              }
+              m_ij = m_i[i] > mx ? m_i[i] : mx;
+              for (int j = 0; j < BN; ++j)
+                r[j] = r[j] - m_ij;
+            } else {
+              float mx = -INFINITY;
+              for (int j = 0; j < BN; ++j)
+                if (r[j] > mx)
+                  mx = r[j];
+              const float ms = mx * qk_scale;
+              m_ij = m_i[i] > ms ? m_i[i] : ms;
+              for (int j = 0; j < BN; ++j) {
+                const float t = r[j] * qk_scale;
+                r[j] = t - m_ij;
+              }
+            }
+            float l_ij = 0.f;
+            for (int j = 0; j < BN; ++j) {
+              r[j] = exp2f(r[j]);
+              l_ij += r[j];
+            }
+            const float alpha = exp2f(m_i[i] - m_ij);
+            l_i[i] = l_i[i] * alpha + l_ij;
+            for (int d = 0; d < D; ++d)
+              acc[i * D + d] = acc[i * D + d] * alpha;
+            for (int j = 0; j < BN; ++j) /* p.to(fp16) */
+              r[j] = or_f16_to_f32(or_f32_to_f16(r[j]));
+            for (int d = 0; d < D; ++d) {
+              float t = 0.f;
+              for (int j = 0; j < BN; ++j)
+                t += r[j] * or_f16_to_f32(v[base + (n0 + j) * D + d]);
+              pv[i * D + d] = t;
+            }
+            for (int d = 0; d < D; ++d)
+              acc[i * D + d] = pv[i * D + d] + acc[i * D + d];
+            m_i[i] = m_ij;
+          }
+        }
+        for (int i = 0; i < BM; ++i) {
+          M[hz * N + m0 + i] = m_i[i] + log2f(l_i[i]);
+          for (int d = 0; d < D; ++d)
+            o[base + (m0 + i) * D + d] = or_f32_to_f16(acc[i * D + d] / l_i[i]);
+        }
+      }
+    }
+    free(qb); free(acc); free(qk); free(pv); free(m_i); free(l_i);
+  }
+  return rc;
+}
+
 /* ---------------- the tiled dot ---------------- */
 
 static float load_f(const uint8_t *base, int type, int64_t idx) {

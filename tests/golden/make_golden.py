@@ -30,6 +30,14 @@ loaded as uint8, decoded with the OCP e4m3 / e5m2 / e2m1 formulas (e2m1
 unpacked low nibble first along K), multiplied by exp2(scale - 127) per 32
 elements of K (rhs_scale indexed [n][k // 32]), and accumulated by tl.dot.
 
+attn_* fixtures: attn_fwd_kernel below follows the forward of the reference's
+fused-attention tutorial step for step (R:pass/LoopSplit/06-fused-attention.py
+:44-93 _attn_fwd_inner, :181-239 _attn_fwd) with plain pointers in place of
+block pointers: one loop over all keys with the on-band branch
+`start_n >= causal_start`, exp2 softmax with qk_scale = sm_scale * 1.44269504,
+p.to(fp16) @ v, M = m_i + log2(l_i), o = acc / l_i.  Inputs N(0, 0.5) fp16
+as in the tutorial's test_op.
+
 "dyadic" fixtures draw small multiples of a power of two, so every product and
 partial sum is exact in fp32: the fp32 accumulator is then independent of the
 summation order, and any correct implementation must match it bit for bit.
@@ -151,6 +159,67 @@ def mx_dot_kernel(a_ptr, b_ptr, sa_ptr, sb_ptr, c_ptr, M, N, K,
         acc = tl.dot(a, b, acc)
     tl.store(c_ptr + rm[:, None] * N + rn[None, :], acc,
              mask=(rm[:, None] < M) & (rn[None, :] < N))
+
+
+@triton.jit
+def attn_fwd_kernel(Q, K, V, sm_scale, M, Out, N_CTX, H,
+                    HEAD_DIM: tl.constexpr, BLOCK_M: tl.constexpr, BLOCK_N: tl.constexpr,
+                    CAUSAL: tl.constexpr):
+    start_m = tl.program_id(0)
+    off_hz = tl.program_id(1)
+    base = off_hz.to(tl.int64) * N_CTX * HEAD_DIM
+    offs_m = start_m * BLOCK_M + tl.arange(0, BLOCK_M)
+    offs_n = tl.arange(0, BLOCK_N)
+    offs_d = tl.arange(0, HEAD_DIM)
+    m_i = tl.zeros([BLOCK_M], dtype=tl.float32) - float("inf")
+    l_i = tl.zeros([BLOCK_M], dtype=tl.float32) + 1.0
+    acc = tl.zeros([BLOCK_M, HEAD_DIM], dtype=tl.float32)
+    qk_scale = sm_scale
+    qk_scale *= 1.44269504
+    q = tl.load(Q + base + offs_m[:, None] * HEAD_DIM + offs_d[None, :])
+    if CAUSAL:
+        causal_start = start_m * BLOCK_M
+    else:
+        causal_start = N_CTX
+    for start_n in range(0, N_CTX, BLOCK_N):
+        kt = tl.load(K + base + (start_n + offs_n)[None, :] * HEAD_DIM + offs_d[:, None])
+        qk = tl.dot(q, kt)
+        if start_n >= causal_start:
+            mask = offs_m[:, None] >= (start_n + offs_n[None, :])
+            qk = qk * qk_scale + tl.where(mask, 0, -1.0e6)
+            m_ij = tl.maximum(m_i, tl.max(qk, 1))
+            qk -= m_ij[:, None]
+        else:
+            m_ij = tl.maximum(m_i, tl.max(qk, 1) * qk_scale)
+            qk = qk * qk_scale - m_ij[:, None]
+        p = tl.math.exp2(qk)
+        l_ij = tl.sum(p, 1)
+        alpha = tl.math.exp2(m_i - m_ij)
+        l_i = l_i * alpha + l_ij
+        acc = acc * alpha[:, None]
+        v = tl.load(V + base + (start_n + offs_n)[:, None] * HEAD_DIM + offs_d[None, :])
+        p = p.to(tl.float16)
+        acc = tl.dot(p, v, acc)
+        m_i = m_ij
+    m_i += tl.math.log2(l_i)
+    acc = acc / l_i[:, None]
+    tl.store(M + off_hz * N_CTX + offs_m, m_i)
+    tl.store(Out + base + offs_m[:, None] * HEAD_DIM + offs_d[None, :], acc.to(tl.float16))
+
+
+def attn_case(rng, name, Z, H, N, D, causal, sm_scale, block):
+    q, k, v = (torch.from_numpy((rng.standard_normal((Z, H, N, D)) * 0.5).astype(np.float16))
+               for _ in range(3))
+    o = torch.empty_like(q)
+    M = torch.empty((Z * H, N), dtype=torch.float32)
+    BM, BN = block
+    attn_fwd_kernel[(N // BM, Z * H)](q, k, v, sm_scale, M, o, N, H, HEAD_DIM=D, BLOCK_M=BM,
+                                      BLOCK_N=BN, CAUSAL=causal)
+    d = dict(q=bits(q), k=bits(k), v=bits(v), o=bits(o), M=M.numpy(), causal=np.bool_(causal),
+             sm_scale=np.float32(sm_scale), block=np.array(block, np.int32))
+    np.savez_compressed(os.path.join(HERE, name + ".npz"), **d)
+    size = os.path.getsize(os.path.join(HERE, name + ".npz"))
+    print(f"{name}: Z={Z} H={H} N_CTX={N} D={D} causal={causal} {size / 1024:.1f} KiB", flush=True)
 
 
 MX_FMT = {"e4m3": 0, "e5m2": 1, "e2m1": 4}
@@ -388,6 +457,11 @@ def main():
             block=(32, 32, 64))
     mx_case(rng, "mx_e2m1_f32_random", "e2m1", "e2m1", 32, 48, 512, exact=False,
             block=(32, 16, 64))
+
+    # fused attention forward (the tutorial's test_op recipe, smaller): causal
+    # with the LoopSplit on-band branch, and plain
+    attn_case(rng, "attn_fwd_causal", 1, 2, 256, 64, True, 0.5, (64, 32))
+    attn_case(rng, "attn_fwd_plain", 2, 1, 128, 64, False, 1.3, (64, 32))
 
 
 if __name__ == "__main__":

@@ -1,0 +1,111 @@
+"""GPU parity of the fused attention forward (tx_attn_fwd_launch) against the
+CPU oracle and, as the tutorial's own test does, a torch reference.
+
+Bars: o within 1e-2 absolute of the reference (the tutorial's test_op,
+R:pass/LoopSplit/06-fused-attention.py:698-718) and, against the oracle,
+within 2^-8 (two fp16 ulps at |o| ~ 1: p is rounded to fp16 on both sides,
+exp2 and the summation orders differ); M (base-2 logsumexp) within 1e-4.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import triton_ext_amd as tx
+from dotcase import from_device, say, to_device
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def rand_qkv(Z, H, N, D, seed, std=0.5):
+    rng = np.random.default_rng(seed)
+    return [(rng.standard_normal((Z, H, N, D)) * std).astype(np.float16).view(np.uint16)
+            for _ in range(3)]
+
+
+def run_gpu(gpu, q, k, v, causal, sm_scale, layout="bhnd"):
+    import torch
+    ts = []
+    for x in (q, k, v):
+        t = to_device(x, gpu).view(torch.float16)
+        if layout == "bnhd":  # storage [Z, N, H, D], viewed as [Z, H, N, D]
+            t = t.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+        ts.append(t)
+    o, M = tx.attention(*ts, causal, sm_scale, return_lse=True)
+    torch.cuda.synchronize()
+    return from_device(o.contiguous().view(torch.int16)).view(np.uint16), from_device(M)
+
+
+def check(o, M, ro, rM, what, tol=2.0 ** -8):
+    go = o.view(np.float16).astype(np.float64)
+    wo = ro.view(np.float16).astype(np.float64)
+    assert np.isfinite(go).all(), f"{what}: non-finite o"
+    d = np.abs(go - wo)
+    assert d.max() <= tol, f"{what}: max |d o| {d.max():.3g} (bound {tol:.3g})"
+    dm = np.abs(M.reshape(rM.shape).astype(np.float64) - rM)
+    assert dm.max() <= 1e-4 * max(1.0, np.abs(rM).max()), f"{what}: max |d M| {dm.max():.3g}"
+    say(f"{what}: max|d o|={d.max():.3g} identical={np.mean(go == wo):.3f} max|d M|={dm.max():.3g}")
+
+
+def test_tutorial_test_op(gpu):
+    """The tutorial's test_op: (1, 2, 1024, 64), causal, N(0, 0.5) fp16,
+    sm_scale 0.5, against softmax in fp32 -> fp16 -> matmul, atol 1e-2."""
+    import torch
+    say("attn test_op (1, 2, 1024, 64) causal")
+    q, k, v = rand_qkv(1, 2, 1024, 64, seed=20)
+    o, _ = run_gpu(gpu, q, k, v, True, 0.5)
+    qt, kt, vt = (torch.from_numpy(x.view(np.float16)).float() for x in (q, k, v))
+    N = 1024
+    Mk = torch.tril(torch.ones((N, N)))
+    p = torch.matmul(qt, kt.transpose(2, 3)) * 0.5
+    p[:, :, Mk == 0] = float("-inf")
+    p = torch.softmax(p, dim=-1).half().float()
+    ref = torch.matmul(p, vt).half()
+    got = torch.from_numpy(o.view(np.float16))
+    assert torch.allclose(ref, got, atol=1e-2, rtol=0)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("Z,H,N,sm_scale,layout", [(1, 2, 256, 0.5, "bhnd"),
+                                                   (2, 3, 384, 1.3, "bhnd"),
+                                                   (1, 4, 512, 0.125, "bnhd"),
+                                                   (1, 1, 128, 0.5, "bhnd")])
+def test_attn_vs_oracle(gpu, causal, Z, H, N, sm_scale, layout):
+    say(f"attn Z={Z} H={H} N={N} causal={causal} scale={sm_scale} {layout}")
+    q, k, v = rand_qkv(Z, H, N, 64, seed=Z * 100 + H * 10 + N + causal)
+    o, M = run_gpu(gpu, q, k, v, causal, sm_scale, layout)
+    ro, rM = oracle.attn_fwd(q, k, v, sm_scale=sm_scale, causal=causal, block=(128, 64))
+    check(o, M, ro, rM, f"attn {Z}x{H}x{N} causal={causal} {layout}")
+
+
+@pytest.mark.parametrize("name", ["attn_fwd_causal", "attn_fwd_plain"])
+def test_golden_fixture_attn(gpu, name):
+    say(f"golden {name}")
+    z = np.load(os.path.join(GOLDEN, name + ".npz"), allow_pickle=False)
+    o, M = run_gpu(gpu, z["q"], z["k"], z["v"], bool(z["causal"]), float(z["sm_scale"]))
+    check(o, M, z["o"], z["M"], f"golden {name}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attn_bench_shape_sampled_heads(gpu, causal):
+    """The bench shape (4, 32, 4096, 64): every program runs; two heads are
+    checked in full against the oracle."""
+    import torch
+    say(f"attn 4x32x4096 causal={causal}")
+    Z, H, N, D = 4, 32, 4096, 64
+    g = torch.Generator(device=gpu)
+    g.manual_seed(5)
+    q, k, v = (torch.randn((Z, H, N, D), generator=g, device=gpu, dtype=torch.float16) * 0.5
+               for _ in range(3))
+    o, M = tx.attention(q, k, v, causal, 0.5, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all()
+    for (zi, hi) in ((0, 0), (3, 31)):
+        sub = [from_device(t[zi:zi + 1, hi:hi + 1].contiguous().view(torch.int16)).view(np.uint16)
+               for t in (q, k, v)]
+        ro, rM = oracle.attn_fwd(*sub, sm_scale=0.5, causal=causal, block=(128, 64))
+        got = from_device(o[zi:zi + 1, hi:hi + 1].contiguous().view(torch.int16)).view(np.uint16)
+        check(got, from_device(M[zi, hi]), ro, rM, f"attn 4x32x4096 head ({zi},{hi})")

@@ -46,7 +46,7 @@ def load_fixture(path):
 
 # tiled-dot fixtures (the tl.dot_scaled ones, mx_*, are pinned in test_mx_oracle_cpu.py)
 FIXTURES = sorted(p for p in glob.glob(os.path.join(GOLDEN, "*.npz"))
-                  if not os.path.basename(p).startswith("mx_"))
+                  if not os.path.basename(p).startswith(("mx_", "attn_")))
 
 
 def run_oracle(f, round_mode=oracle.ROUND_RTZ):

@@ -18,8 +18,11 @@
 #include <string>
 
 #include "triton_ext/TritonExtPassInfra.h"
+#include "triton_ext/tx_attn.h"
 #include "triton_ext/tx_dot.h"
 #include "triton_ext/tx_passes.h"
+
+#include "attn_fwd.h"
 
 #include "decode_i8.h"
 #include "gemm16_dma.h"
@@ -633,6 +636,117 @@ extern "C" TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A,
   default:
     return fail(TX_ERR_INVALID, "plan has no kernel (kernel=%d)", plan->kernel);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Fused attention forward (tx_attn.h)
+// ---------------------------------------------------------------------------
+
+namespace {
+
+// Packed defaults and checks of one tensor's (batch, head, row) strides.
+int attnStrides(const tx_attn_desc &d, int64_t &sz, int64_t &sh, int64_t &sm,
+                const char *name) {
+  if (sm == 0) sm = d.head_dim;
+  if (sh == 0) sh = d.N_CTX * sm;
+  if (sz == 0) sz = d.H * sh;
+  if (sm < d.head_dim || sh < 0 || sz < 0 || sm % 8 || sh % 8 || sz % 8)
+    return fail(TX_ERR_INVALID, "%s strides (%lld, %lld, %lld): rows of head_dim elements, "
+                "multiples of 8 elements", name, (long long)sz, (long long)sh, (long long)sm);
+  if (((d.N_CTX - 1) * sm + d.head_dim) * 2 >= ((int64_t)1 << 31))
+    return fail(TX_ERR_UNSUPPORTED, "%s: one head spans 2 GiB or more", name);
+  return TX_OK;
+}
+
+} // namespace
+
+extern "C" TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *plan) {
+  g_last_error.clear();
+  if (!desc || !plan)
+    return fail(TX_ERR_INVALID, "descriptor or plan is NULL");
+  tx_attn_desc d = *desc;
+  if (d.Z < 0 || d.H < 0 || d.N_CTX < 0)
+    return fail(TX_ERR_INVALID, "negative extent Z=%lld H=%lld N_CTX=%lld", (long long)d.Z,
+                (long long)d.H, (long long)d.N_CTX);
+  if (d.causal != 0 && d.causal != 1)
+    return fail(TX_ERR_INVALID, "causal must be 0 or 1");
+  if (!(d.sm_scale == d.sm_scale))
+    return fail(TX_ERR_INVALID, "sm_scale is NaN");
+  if (d.head_dim != txk::AttnFwd::D)
+    return fail(TX_ERR_UNSUPPORTED, "head_dim %d: the kernel is built for 64", d.head_dim);
+  if (d.dtype != TX_F16)
+    return fail(TX_ERR_UNSUPPORTED, "dtype %d: fp16 q/k/v/o are implemented", d.dtype);
+  if (d.block_m == 0) d.block_m = txk::AttnFwd::BM;
+  if (d.block_n == 0) d.block_n = txk::AttnFwd::BN;
+  if (d.block_m != txk::AttnFwd::BM || d.block_n != txk::AttnFwd::BN)
+    return fail(TX_ERR_UNSUPPORTED, "blocks %dx%d: 128x64 is implemented", d.block_m,
+                d.block_n);
+  if (d.N_CTX % d.block_m)
+    return fail(TX_ERR_UNSUPPORTED, "N_CTX %lld is not a multiple of %d (whole blocks only)",
+                (long long)d.N_CTX, d.block_m);
+  int rc = attnStrides(d, d.q_sz, d.q_sh, d.q_sm, "q");
+  if (rc == TX_OK) rc = attnStrides(d, d.k_sz, d.k_sh, d.k_sm, "k");
+  if (rc == TX_OK) rc = attnStrides(d, d.v_sz, d.v_sh, d.v_sm, "v");
+  if (rc == TX_OK) rc = attnStrides(d, d.o_sz, d.o_sh, d.o_sm, "o");
+  if (rc != TX_OK)
+    return rc;
+  const int64_t programs = d.Z * d.H * (d.N_CTX / d.block_m);
+  if (programs > INT32_MAX || d.N_CTX > INT32_MAX / 2 || d.Z * d.H > INT32_MAX)
+    return fail(TX_ERR_UNSUPPORTED, "grid above 2^31");
+  std::memset(plan, 0, sizeof(*plan));
+  plan->desc = d;
+  const double zh = (double)d.Z * (double)d.H, n = (double)d.N_CTX;
+  plan->flops = 4.0 * zh * n * n * d.head_dim * (d.causal ? 0.5 : 1.0);
+  plan->bytes = 4.0 * zh * n * d.head_dim * 2 + zh * n * 4;
+  plan->qk_scale = d.sm_scale * 1.44269504f; // qk_scale = sm_scale; qk_scale *= 1.44269504
+  plan->m_blocks = (int32_t)(d.N_CTX / d.block_m);
+  plan->grid_x = (int32_t)programs;
+  plan->block_threads = txk::AttnFwd::NW * 64;
+  return TX_OK;
+}
+
+extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q, const void *k,
+                                         const void *v, void *o, float *M, void *stream) {
+  g_last_error.clear();
+  if (!plan)
+    return fail(TX_ERR_INVALID, "plan is NULL");
+  const tx_attn_desc &d = plan->desc;
+  if (plan->grid_x == 0)
+    return TX_OK;
+  if (!q || !k || !v || !o || !M)
+    return fail(TX_ERR_INVALID, "NULL tensor pointer");
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+       reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o)) & 15 ||
+      reinterpret_cast<uintptr_t>(M) & 3)
+    return fail(TX_ERR_INVALID, "q, k, v, o must be 16-byte aligned and M 4-byte aligned");
+  if (plan->block_threads != txk::AttnFwd::NW * 64 || d.block_m != txk::AttnFwd::BM ||
+      d.block_n != txk::AttnFwd::BN || d.head_dim != txk::AttnFwd::D ||
+      plan->m_blocks != d.N_CTX / d.block_m || plan->grid_x != d.Z * d.H * plan->m_blocks)
+    return fail(TX_ERR_INVALID, "plan launch shape does not match the attention kernel");
+  if (!tx_device_available())
+    return fail(TX_ERR_NO_DEVICE, "no gfx950 device visible");
+  txk::AttnArgs a;
+  a.Q = static_cast<const uint16_t *>(q);
+  a.K = static_cast<const uint16_t *>(k);
+  a.V = static_cast<const uint16_t *>(v);
+  a.O = static_cast<uint16_t *>(o);
+  a.M = M;
+  a.q_sz = d.q_sz, a.q_sh = d.q_sh, a.q_sm = d.q_sm;
+  a.k_sz = d.k_sz, a.k_sh = d.k_sh, a.k_sm = d.k_sm;
+  a.v_sz = d.v_sz, a.v_sh = d.v_sh, a.v_sm = d.v_sm;
+  a.o_sz = d.o_sz, a.o_sh = d.o_sh, a.o_sm = d.o_sm;
+  a.H = (int32_t)d.H;
+  a.N_CTX = (int32_t)d.N_CTX;
+  a.qk_scale = plan->qk_scale;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (d.causal)
+    hipLaunchKernelGGL(txk::attn_fwd_kernel<true>, dim3(plan->grid_x),
+                       dim3(plan->block_threads), 0, s, a);
+  else
+    hipLaunchKernelGGL(txk::attn_fwd_kernel<false>, dim3(plan->grid_x),
+                       dim3(plan->block_threads), 0, s, a);
+  TX_HIP_CHECK(hipGetLastError());
+  return TX_OK;
 }
 
 #define TRITON_EXT_ARG "tx-mi355x-dot"

@@ -1,0 +1,282 @@
+// Fused attention forward for gfx950: the forward of the fused-attention
+// tutorial (R:pass/LoopSplit/06-fused-attention.py:44-93, :181-239), fp16
+// q/k/v/o, HEAD_DIM 64, fp32 softmax statistics and accumulator.
+//
+// A workgroup owns BM = 128 query rows of one (z, h): four waves of 32 rows.
+// Per K/V block of BN = 64 keys:
+//   S^T = K . Q^T    32x32x16 f16 MFMAs, A := K rows (LDS), B := Q rows (held
+//                    in registers for the whole loop), so lane l holds query
+//                    row m = l%32 and keys n = 8 (r/4) + 4 (l/32) + r%4 of each
+//                    32-key block: a row's statistics need one exchange with
+//                    lane l ^ 32;
+//   softmax          the tutorial's arithmetic per element (scale, mask,
+//                    running max, exp2, running sum);
+//   O^T += V^T . P^T A := V columns (LDS transpose reads), B := P straight from
+//                    the S^T registers: MFMA slot s of lane group g is key
+//                    16 c + 8 (s/4) + 4 g + s%4, so V's rows are read in that
+//                    order and no value crosses lanes.
+// Staging: K and V blocks (8 KiB each) reach LDS by direct-to-LDS buffer
+// loads, two stages, one barrier per block; the next block's loads run under
+// the current block's math.  LDS layouts (rows of 128 bytes, 16-byte chunk c
+// of row r stored at):
+//   K: c ^ ((r >> 1) & 7)   the 16 rows a ds_read_b128 pass touches hit 16
+//                           different bank groups;
+//   V: c ^ (4 ((r >> 1) & 1)) the 4 rows x 64 bytes a ds_read_b64_tr_b16
+//                           pass touches cover all 64 banks once.
+// The K/V loop runs in LoopSplit form: keys [0, causal_start) unmasked, then
+// the on-band blocks [causal_start, causal_start + BM) masked; causal_start =
+// start_m * BM, or N_CTX without the causal mask.  Blocks past the diagonal
+// are skipped (their p is exactly 0 and alpha exactly 1).
+#pragma once
+
+#include "gemm16_w4.h"
+
+namespace txk {
+
+struct AttnArgs {
+  const uint16_t *Q, *K, *V;
+  uint16_t *O;
+  float *M;
+  int64_t q_sz, q_sh, q_sm;
+  int64_t k_sz, k_sh, k_sm;
+  int64_t v_sz, v_sh, v_sm;
+  int64_t o_sz, o_sh, o_sm;
+  int32_t H, N_CTX;
+  float qk_scale;
+};
+
+struct AttnFwd {
+  static constexpr int BM = 128, BN = 64, D = 64, NW = 4;
+  static constexpr int ROW = D * 2;          // bytes per K/V row
+  static constexpr int TILE = BN * ROW;      // 8 KiB
+  static constexpr int STAGE = 2 * TILE;     // K then V
+  static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 2
+  static constexpr uint32_t kOOB = 0x80000000u;
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  typedef float f16v __attribute__((ext_vector_type(16)));
+
+  __device__ __forceinline__ static void dma16(uint32_t voff, const i32x4_t &rsrc, uint32_t soff,
+                                               uint32_t lds) {
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff),
+                 "{m0}"(lds)
+                 : "memory");
+  }
+
+  // Per-lane source byte offsets of the wave's DMA loads (relative to the
+  // block's first row): load u of wave w fills LDS rows 8 (2w + u) .. +7,
+  // lane i row 8 (2w + u) + i/8 at chunk position i%8, which holds chunk
+  // i%8 ^ swizzle(row) of the source row (V_SWZ: V's layout, else K's).
+  template <bool V_SWZ>
+  __device__ __forceinline__ static void dma_offsets(int wave, int64_t sm, uint32_t (&o)[DMA]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int u = 0; u < DMA; ++u) {
+      const int row = 8 * (DMA * wave + u) + (lane >> 3), pos = lane & 7;
+      const int c = V_SWZ ? pos ^ (4 * ((row >> 1) & 1)) : pos ^ ((row >> 1) & 7);
+      o[u] = (uint32_t)((row * sm + c * 8) * 2);
+    }
+  }
+
+  // Loads of K/V block j into the stage at LDS address st.
+  __device__ __forceinline__ static void issue(const i32x4_t &rk, const i32x4_t &rv,
+                                               const uint32_t (&ko)[DMA],
+                                               const uint32_t (&vo)[DMA], int64_t k_sm,
+                                               int64_t v_sm, int j, uint32_t st, int wave) {
+#pragma unroll
+    for (int u = 0; u < DMA; ++u)
+      dma16(ko[u], rk, (uint32_t)((int64_t)j * BN * k_sm * 2), st + (DMA * wave + u) * 1024);
+#pragma unroll
+    for (int u = 0; u < DMA; ++u)
+      dma16(vo[u], rv, (uint32_t)((int64_t)j * BN * v_sm * 2),
+            st + TILE + (DMA * wave + u) * 1024);
+  }
+
+  // K fragment (MFMA A operand) of key block b, head-dim chunk c: lane l
+  // holds key 32 b + l%32, dims 16 c + 8 (l/32) .. +7.
+  __device__ __forceinline__ static h8 read_k(uint32_t st, int b, int c) {
+    typedef __attribute__((address_space(3))) h8 lds_h8;
+    const int lane = threadIdx.x & 63;
+    const int r = 32 * b + (lane & 31), ch = (2 * c + (lane >> 5)) ^ ((r >> 1) & 7);
+    return *(const lds_h8 *)(uintptr_t)(st + r * ROW + ch * 16);
+  }
+
+  // V^T fragment (MFMA A operand) of dim block bd, key chunk c: lane l holds
+  // dim 32 bd + l%32 and keys 16 c + 4 (l/32) + {0..3} (slots 0-3) and
+  // 16 c + 8 + 4 (l/32) + {0..3} (slots 4-7), two transposed reads.
+  __device__ __forceinline__ static h8 read_v(uint32_t st, int bd, int c) {
+    const int lane = threadIdx.x & 63;
+    const int G = lane >> 4, L = lane & 15;
+    const int d = 32 * bd + 16 * (G & 1) + 4 * (L & 3);
+    const int k0 = 16 * c + 4 * (G >> 1) + (L >> 2), k1 = k0 + 8;
+    const uint32_t a0 = st + TILE + k0 * ROW + ((((d >> 3) ^ (4 * ((k0 >> 1) & 1)))) << 4) +
+                        (d & 7) * 2;
+    const uint32_t a1 = st + TILE + k1 * ROW + ((((d >> 3) ^ (4 * ((k1 >> 1) & 1)))) << 4) +
+                        (d & 7) * 2;
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(uintptr_t)a0);
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(uintptr_t)a1);
+    return __builtin_bit_cast(h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+
+  __device__ __forceinline__ static float xmax(float v) {
+    return fmaxf(v, __shfl_xor(v, 32, 64));
+  }
+  __device__ __forceinline__ static float xsum(float v) { return v + __shfl_xor(v, 32, 64); }
+
+  // One K/V block: statistics (m_i, l_i) and accumulator update for the
+  // lane's query row m.  MASK: the on-band form with keys n > m masked.
+  template <bool MASK>
+  __device__ __forceinline__ static void block(uint32_t st, int n0, int m, float qk_scale,
+                                               const h8 (&qf)[D / 16], f16v (&acc)[D / 32],
+                                               float &m_i, float &l_i) {
+    const int lane = threadIdx.x & 63, g = lane >> 5;
+    f16v s[BN / 32];
+#pragma unroll
+    for (int b = 0; b < BN / 32; ++b) {
+      s[b] = f16v{};
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c)
+        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_k(st, b, c), qf[c], s[b], 0, 0, 0);
+    }
+    float m_ij;
+    if constexpr (MASK) {
+      // qk = qk * qk_scale + where(m >= n, 0, -1e6); m_ij = max(m_i, rowmax(qk))
+      float mx = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < BN / 32; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+#pragma clang fp contract(off)
+          const int n = n0 + 32 * b + 8 * (r / 4) + 4 * g + (r % 4);
+          float t = s[b][r] * qk_scale;
+          t = t + (m >= n ? 0.0f : -1.0e6f);
+          s[b][r] = t;
+          mx = fmaxf(mx, t);
+        }
+      m_ij = fmaxf(m_i, xmax(mx));
+#pragma unroll
+      for (int b = 0; b < BN / 32; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          s[b][r] = __builtin_amdgcn_exp2f(s[b][r] - m_ij);
+    } else {
+      // m_ij = max(m_i, rowmax(qk) * qk_scale); qk = qk * qk_scale - m_ij
+      float mx = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < BN / 32; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          mx = fmaxf(mx, s[b][r]);
+      m_ij = fmaxf(m_i, xmax(mx) * qk_scale);
+#pragma unroll
+      for (int b = 0; b < BN / 32; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          s[b][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[b][r], qk_scale, -m_ij));
+    }
+    float l_ij = 0.f;
+#pragma unroll
+    for (int b = 0; b < BN / 32; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        l_ij += s[b][r];
+    l_ij = xsum(l_ij);
+    const float alpha = __builtin_amdgcn_exp2f(m_i - m_ij);
+    l_i = l_i * alpha + l_ij;
+    m_i = m_ij;
+#pragma unroll
+    for (int bd = 0; bd < D / 32; ++bd)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        acc[bd][r] *= alpha;
+    // P^T fragments: key chunk c = registers 8 (c%2) .. +7 of key block c/2
+    h8 pf[BN / 16];
+#pragma unroll
+    for (int c = 0; c < BN / 16; ++c)
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        pf[c][t] = (_Float16)s[c / 2][8 * (c % 2) + t];
+#pragma unroll
+    for (int bd = 0; bd < D / 32; ++bd)
+#pragma unroll
+      for (int c = 0; c < BN / 16; ++c)
+        acc[bd] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_v(st, bd, c), pf[c], acc[bd], 0, 0,
+                                                         0);
+  }
+};
+
+template <bool CAUSAL>
+__global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
+  typedef AttnFwd A;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * A::STAGE];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 5;
+  // Program order: the 8 XCDs take contiguous runs of programs (a head's
+  // K/V stays in one L2), and within a head the longest causal rows first.
+  const int nm = p.N_CTX / A::BM, nwg = gridDim.x, b = blockIdx.x;
+  const int t = (nwg % 8 == 0) ? (b % 8) * (nwg / 8) + b / 8 : b;
+  const int hz = t / nm, start_m = CAUSAL ? nm - 1 - t % nm : t % nm;
+  const int z = hz / p.H, h = hz % p.H;
+  const uint16_t *Qh = p.Q + z * p.q_sz + h * p.q_sh;
+  const uint16_t *Kh = p.K + z * p.k_sz + h * p.k_sh;
+  const uint16_t *Vh = p.V + z * p.v_sz + h * p.v_sh;
+  const int m = start_m * A::BM + 32 * wave + (lane & 31);
+
+  // Q rows as MFMA B operands: dims 16 c + 8 g .. +7 of row m.
+  A::h8 qf[A::D / 16];
+#pragma unroll
+  for (int c = 0; c < A::D / 16; ++c)
+    qf[c] = *reinterpret_cast<const A::h8 *>(Qh + (int64_t)m * p.q_sm + 16 * c + 8 * g);
+
+  const i32x4_t rk = make_rsrc(Kh, (uint32_t)(((int64_t)(p.N_CTX - 1) * p.k_sm + A::D) * 2));
+  const i32x4_t rv = make_rsrc(Vh, (uint32_t)(((int64_t)(p.N_CTX - 1) * p.v_sm + A::D) * 2));
+  uint32_t ko[A::DMA], vo[A::DMA];
+  A::dma_offsets<false>(wave, p.k_sm, ko);
+  A::dma_offsets<true>(wave, p.v_sm, vo);
+  const uint32_t lds0 = lds_addr(smem);
+
+  // LoopSplit form of the K/V loop (keys [0, N_CTX), predicate start_n >=
+  // causal_start): unmasked blocks [0, n_main), masked [n_main, n_end).
+  const int causal_start = CAUSAL ? start_m * A::BM : p.N_CTX;
+  const int n_main = causal_start / A::BN;
+  const int n_end = CAUSAL ? (causal_start + A::BM) / A::BN : n_main;
+
+  float m_i = -INFINITY, l_i = 1.0f;
+  A::f16v acc[A::D / 32];
+#pragma unroll
+  for (int bd = 0; bd < A::D / 32; ++bd)
+    acc[bd] = A::f16v{};
+
+  A::issue(rk, rv, ko, vo, p.k_sm, p.v_sm, 0, lds0, wave);
+  auto step = [&](int j, auto mask) {
+    __builtin_amdgcn_s_waitcnt(0x7 << 4); // vmcnt(0): this wave's loads of block j
+    __syncthreads();                      // everyone's; and stage (j+1)&1 is free
+    if (j + 1 < n_end)
+      A::issue(rk, rv, ko, vo, p.k_sm, p.v_sm, j + 1, lds0 + ((j + 1) & 1) * A::STAGE, wave);
+    A::template block<decltype(mask)::value>(lds0 + (j & 1) * A::STAGE, j * A::BN, m,
+                                             p.qk_scale, qf, acc, m_i, l_i);
+  };
+  for (int j = 0; j < n_main; ++j)
+    step(j, std::false_type());
+  for (int j = n_main; j < n_end; ++j)
+    step(j, std::true_type());
+
+  // Epilogue: M = m_i + log2(l_i); O = acc / l_i.  Lane l holds, per dim
+  // block bd and register quad q, dims 32 bd + 8 q + 4 g .. +3 of row m.
+  uint16_t *Oh = p.O + z * p.o_sz + h * p.o_sh + (int64_t)m * p.o_sm;
+#pragma unroll
+  for (int bd = 0; bd < A::D / 32; ++bd)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      A::h4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = (_Float16)(acc[bd][4 * q + e] / l_i);
+      *reinterpret_cast<A::h4 *>(Oh + 32 * bd + 8 * q + 4 * g) = o;
+    }
+  if (g == 0)
+    p.M[(int64_t)hz * p.N_CTX + m] = m_i + __builtin_log2f(l_i);
+}
+
+} // namespace txk

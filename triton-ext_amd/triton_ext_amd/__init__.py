@@ -14,4 +14,4 @@ torch is used only for device memory and streams.  There is no CPU fallback:
 if libmi355x_dot.so is missing, `load()` raises.
 """
 from .capi import *  # noqa: F401,F403
-from .dot import dot, dot_scaled, plan_for, tx_type, workspace_for  # noqa: F401
+from .dot import attention, dot, dot_scaled, plan_for, tx_type, workspace_for  # noqa: F401

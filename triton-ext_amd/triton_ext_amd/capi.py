@@ -1,4 +1,4 @@
-"""ctypes mirror of include/triton_ext/{TritonExtPassInfra,tx_dot,tx_passes}.h."""
+"""ctypes mirror of include/triton_ext/{TritonExtPassInfra,tx_dot,tx_passes,tx_attn}.h."""
 import ctypes
 import os
 
@@ -48,6 +48,20 @@ class DotPlan(ctypes.Structure):
                 ("grid_x", ctypes.c_int32), ("grid_y", ctypes.c_int32), ("grid_z", ctypes.c_int32),
                 ("block_threads", ctypes.c_int32), ("workspace_bytes", ctypes.c_int64),
                 ("passes_run", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
+class AttnDesc(ctypes.Structure):
+    _fields_ = ([("Z", ctypes.c_int64), ("H", ctypes.c_int64), ("N_CTX", ctypes.c_int64),
+                 ("head_dim", ctypes.c_int32), ("dtype", ctypes.c_int32), ("causal", ctypes.c_int32),
+                 ("sm_scale", ctypes.c_float)] +
+                [(f"{t}_{s}", ctypes.c_int64) for t in "qkvo" for s in ("sz", "sh", "sm")] +
+                [("block_m", ctypes.c_int32), ("block_n", ctypes.c_int32)])
+
+
+class AttnPlan(ctypes.Structure):
+    _fields_ = [("desc", AttnDesc), ("flops", ctypes.c_double), ("bytes", ctypes.c_double),
+                ("qk_scale", ctypes.c_float), ("m_blocks", ctypes.c_int32), ("grid_x", ctypes.c_int32),
+                ("block_threads", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 class LoopSplit(ctypes.Structure):
@@ -131,6 +145,8 @@ def load(name="libmi355x_dot.so"):
         L.tx_get_last_error.restype = ctypes.c_char_p
         L.tx_kernel_name.argtypes = [i32]
         L.tx_kernel_name.restype = ctypes.c_char_p
+        L.tx_attn_fwd_plan.argtypes = [ctypes.POINTER(AttnDesc), ctypes.POINTER(AttnPlan)]
+        L.tx_attn_fwd_launch.argtypes = [ctypes.POINTER(AttnPlan), vp, vp, vp, vp, vp, vp]
     _libs[name] = L
     return L
 
@@ -194,3 +210,18 @@ def enumerate_passes():
     if L.tritonEnumeratePluginPasses(ctypes.byref(n), arr) != TP_SUCCESS:
         raise TxError(TP_GENERIC_FAILURE, "enumerate failed")
     return [arr[i].decode() for i in range(n.value)]
+
+
+def attn_plan(Z, H, N_CTX, head_dim, causal, sm_scale, dtype=F16, strides=None, block=(0, 0)):
+    """Plan the fused attention forward.  strides: {"q": (sz, sh, sm), ...}
+    in elements (missing tensors: packed)."""
+    d = AttnDesc()
+    d.Z, d.H, d.N_CTX, d.head_dim, d.dtype = Z, H, N_CTX, head_dim, dtype
+    d.causal, d.sm_scale = int(bool(causal)), sm_scale
+    for t, st in (strides or {}).items():
+        for f, x in zip(("sz", "sh", "sm"), st):
+            setattr(d, f"{t}_{f}", x)
+    d.block_m, d.block_n = block
+    p = AttnPlan()
+    check(load().tx_attn_fwd_plan(ctypes.byref(d), ctypes.byref(p)))
+    return p

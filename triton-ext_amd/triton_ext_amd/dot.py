@@ -178,3 +178,37 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
                                out.data_ptr(), lhs_scale.data_ptr(), rhs_scale.data_ptr(),
                                None, 0, stream))
     return out
+
+
+def attention(q, k, v, causal, sm_scale, return_lse=False, plan=None, stream=None):
+    """Forward of the fused-attention tutorial's `attention(q, k, v, causal,
+    sm_scale)` (R:pass/LoopSplit/06-fused-attention.py:583-640) on the
+    MI355X kernel: q, k, v fp16 [Z, H, N_CTX, HEAD_DIM] with the head dim
+    contiguous.  Returns o (and M, the base-2 logsumexp [Z, H, N_CTX] the
+    tutorial saves for its backward, with return_lse=True).  Shape checks
+    follow the tutorial's asserts.
+    """
+    import torch
+    if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q, k, v must share one [Z, H, N_CTX, HEAD_DIM] shape: "
+                         f"{tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    HEAD_DIM = q.shape[-1]
+    if HEAD_DIM not in {16, 32, 64, 128, 256}:
+        raise ValueError(f"HEAD_DIM {HEAD_DIM} not in {{16, 32, 64, 128, 256}}")
+    for t, nm in ((q, "q"), (k, "k"), (v, "v")):
+        if t.dtype != torch.float16:
+            raise NotImplementedError(f"{nm}: fp16 is implemented, got {t.dtype}")
+        if t.stride(3) != 1:
+            raise ValueError(f"{nm}: the head dimension must be contiguous")
+    Z, H, N = q.shape[:3]
+    o = torch.empty_like(q, memory_format=torch.contiguous_format)
+    M = torch.empty((Z, H, N), device=q.device, dtype=torch.float32)
+    if plan is None:
+        st = {nm: (t.stride(0), t.stride(1), t.stride(2)) for nm, t in
+              (("q", q), ("k", k), ("v", v), ("o", o))}
+        plan = capi.attn_plan(Z, H, N, HEAD_DIM, causal, sm_scale, strides=st)
+    if stream is None:
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+    capi.check(capi.load().tx_attn_fwd_launch(ctypes.byref(plan), q.data_ptr(), k.data_ptr(),
+                                              v.data_ptr(), o.data_ptr(), M.data_ptr(), stream))
+    return (o, M) if return_lse else o
