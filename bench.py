@@ -9,8 +9,9 @@ per step over the timed region, HIP events on the launch stream).  The other
 configs are reported under "secondary": the LoopSplit K-tail and edge cases,
 int8 W8A8 decode (M = 1, 16, 64, 256; HBM-bound, timed per launch with the
 256 MB MALL flushed between launches so B streams from HBM), the fp8
-block-scaled dot, and tl.dot_scaled's MX formats (mxfp8 e4m3 and mxfp4 e2m1
-with e8m0 scales per 32 K, fp32 C).
+block-scaled dot, tl.dot_scaled's MX formats (mxfp8 e4m3 and mxfp4 e2m1
+with e8m0 scales per 32 K, fp32 C), and the fused attention forward of the
+reference's tutorial at its benchmark shape (BATCH 4, 32 heads, HEAD_DIM 64).
 
 cpu_baseline: the CPU oracle (a C restatement of the Triton interpreter's
 tiled dot, oracle/) on the host cores for the same bf16 4096^3 inputs; it
@@ -49,7 +50,9 @@ def parse():
     ap.add_argument("--only", default="",
                     help="secondary workloads to run, comma-separated: vendor, tail, w8a8 (or "
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256), fp8, kmajor, mx (or mxfp8, mxfp4, "
-                         "mxfp8_4096, mxfp8_8192, mxfp4_4096, mxfp4_8192) (default: all); the bf16 "
+                         "mxfp8_4096, mxfp8_8192, mxfp4_4096, mxfp4_8192), attn (or attn_1024, attn_4096, "
+                         "attn_16384; attn_vendor adds torch sdpa beside each) (default: all); "
+                         "the bf16 "
                          "headline always runs")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 256 MiB five times (a transfer of known size that scales the "
@@ -282,6 +285,50 @@ def bench_mx(tx, dev, M, N, K, fmt, steps, warmup, seed=7):
                           tile=[p.desc.block_m, p.desc.block_n, p.desc.block_k]))
 
 
+def bench_attn(tx, dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9):
+    """Fused attention forward, the tutorial's bench_flash_attention "fwd"
+    configuration (R:pass/LoopSplit/06-fused-attention.py:737-795): fp16
+    randn q, k, v [4, 32, N_CTX, 64], sm_scale 1.3; FLOPs 4 Z H N^2 D, halved
+    for causal."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    q, k, v = (torch.randn((Z, H, N_CTX, D), generator=g, device=dev, dtype=torch.float16)
+               for _ in range(3))
+    o = torch.empty_like(q)
+    M = torch.empty((Z, H, N_CTX), device=dev, dtype=torch.float32)
+    p = tx.attn_plan(Z, H, N_CTX, D, causal, 1.3)
+    L = tx.load()
+    args = (ctypes.byref(p), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+            M.data_ptr(), torch.cuda.current_stream().cuda_stream)
+
+    def run():
+        rc = L.tx_attn_fwd_launch(*args)
+        if rc != 0:
+            raise RuntimeError(L.tx_get_last_error().decode())
+    ms = time_back_to_back(run, steps, warmup)
+    return dict(workload=f"fused attention fwd fp16 Z={Z} H={H} N_CTX={N_CTX} D={D} "
+                         f"causal={causal}", ms=ms, tflops=p.flops / ms / 1e9,
+                frac=p.flops / ms / 1e-3 / PEAK_BF16)
+
+
+def bench_vendor_attn(dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9):
+    """torch.nn.functional.scaled_dot_product_attention on the same inputs:
+    the vendor reference (ROCm's fused attention behind torch)."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    q, k, v = (torch.randn((Z, H, N_CTX, D), generator=g, device=dev, dtype=torch.float16)
+               for _ in range(3))
+    fn = lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=causal,
+                                                                  scale=1.3)
+    ms = time_back_to_back(fn, steps, warmup)
+    flops = 4.0 * Z * H * N_CTX * N_CTX * D * (0.5 if causal else 1.0)
+    return dict(workload=f"vendor: torch sdpa fp16 Z={Z} H={H} N_CTX={N_CTX} D={D} "
+                         f"causal={causal}", ms=ms, tflops=flops / ms / 1e9,
+                frac=flops / ms / 1e-3 / PEAK_BF16)
+
+
 def cpu_baseline(a, b, c, M, N, K, block):
     """Oracle on the host cores over the full bf16 workload; also checks the GPU output."""
     import numpy as np
@@ -376,6 +423,19 @@ def main():
                 print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s "
                       f"({100 * r['frac']:.1f}% of {r['peak_tflops']:.0f})", file=sys.stderr,
                       flush=True)
+
+    for n in (1024, 4096, 16384):
+        if want("attn") or want(f"attn_{n}"):
+            for causal in (True, False):
+                r = bench_attn(tx, dev, n, causal, args.steps, args.warmup)
+                secondary.append(r)
+                print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s "
+                      f"({100 * r['frac']:.1f}% of fp16 peak)", file=sys.stderr, flush=True)
+                if want("vendor") or want("attn_vendor"):
+                    r = bench_vendor_attn(dev, n, causal, args.steps, args.warmup)
+                    secondary.append(r)
+                    print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr,
+                          flush=True)
 
     cpu, parity = None, None
     if not args.no_cpu:
