@@ -16,8 +16,8 @@
 //                    16 c + 8 (s/4) + 4 g + s%4, so V's rows are read in that
 //                    order and no value crosses lanes.
 // Staging: K and V blocks (8 KiB each) reach LDS by direct-to-LDS buffer
-// loads, two stages, one barrier per block; the next block's loads run under
-// the current block's math.  LDS layouts (rows of 128 bytes, 16-byte chunk c
+// loads into two slots each, one barrier per block; loads run a block ahead
+// under the math (the pipeline is described at the kernel).  LDS layouts (rows of 128 bytes, 16-byte chunk c
 // of row r stored at):
 //   K: c ^ ((r >> 1) & 7)   the 16 rows a ds_read_b128 pass touches hit 16
 //                           different bank groups;
@@ -49,7 +49,6 @@ struct AttnFwd {
   static constexpr int BM = 128, BN = 64, D = 64, NW = 4;
   static constexpr int ROW = D * 2;          // bytes per K/V row
   static constexpr int TILE = BN * ROW;      // 8 KiB
-  static constexpr int STAGE = 2 * TILE;     // K then V
   static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 2
   static constexpr uint32_t kOOB = 0x80000000u;
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -78,43 +77,52 @@ struct AttnFwd {
     }
   }
 
-  // Loads of K/V block j into the stage at LDS address st.
-  __device__ __forceinline__ static void issue(const i32x4_t &rk, const i32x4_t &rv,
-                                               const uint32_t (&ko)[DMA],
-                                               const uint32_t (&vo)[DMA], int64_t k_sm,
-                                               int64_t v_sm, int j, uint32_t st, int wave) {
+  // Loads of K block j into K slot `slot` (V block j into V slot `slot`).
+  __device__ __forceinline__ static void issue(const i32x4_t &rsrc, const uint32_t (&off)[DMA],
+                                               int64_t sm, int j, uint32_t slot_lds, int wave) {
 #pragma unroll
     for (int u = 0; u < DMA; ++u)
-      dma16(ko[u], rk, (uint32_t)((int64_t)j * BN * k_sm * 2), st + (DMA * wave + u) * 1024);
-#pragma unroll
-    for (int u = 0; u < DMA; ++u)
-      dma16(vo[u], rv, (uint32_t)((int64_t)j * BN * v_sm * 2),
-            st + TILE + (DMA * wave + u) * 1024);
+      dma16(off[u], rsrc, (uint32_t)((int64_t)j * BN * sm * 2), slot_lds + (DMA * wave + u) * 1024);
   }
 
-  // K fragment (MFMA A operand) of key block b, head-dim chunk c: lane l
-  // holds key 32 b + l%32, dims 16 c + 8 (l/32) .. +7.
-  __device__ __forceinline__ static h8 read_k(uint32_t st, int b, int c) {
+  // Per-lane LDS addresses (slot 0) of the fragment reads.  Every other
+  // fragment is one of these plus a constant, which the reads take as their
+  // immediate offset:
+  //   K, key block b, dim chunk c: lane l reads key 32 b + l%32, dims
+  //     16 c + 8 (l/32) .. +7 at chunk (2c + l/32) ^ ((key >> 1) & 7); the
+  //     swizzle does not depend on b, so kb[c] + 32 b ROW;
+  //   V^T, dim block bd, key chunk c: two transposed reads (keys 16 c +
+  //     4 (l/32) + (L/4) and +8 for lane group l/16 and L = l%16); the
+  //     swizzle term (key >> 1) & 1 depends on L only, so vb[bd] + 16 c ROW
+  //     (+ 8 ROW for the second read).
+  struct Bases {
+    uint32_t k[D / 16], v[D / 32];
+  };
+  __device__ __forceinline__ static void bases(uint32_t k_lds, uint32_t v_lds, Bases &bs) {
+    const int lane = threadIdx.x & 63;
+    const int G = lane >> 4, L = lane & 15, r = lane & 31;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+      bs.k[c] = k_lds + r * ROW + (((2 * c + (lane >> 5)) ^ ((r >> 1) & 7)) << 4);
+#pragma unroll
+    for (int bd = 0; bd < D / 32; ++bd) {
+      const int d = 32 * bd + 16 * (G & 1) + 4 * (L & 3);
+      const int k0 = 4 * (G >> 1) + (L >> 2);
+      bs.v[bd] = v_lds + k0 * ROW + (((d >> 3) ^ (4 * ((k0 >> 1) & 1))) << 4) + (d & 7) * 2;
+    }
+  }
+
+  template <int SLOT>
+  __device__ __forceinline__ static h8 read_k(const Bases &bs, int b, int c) {
     typedef __attribute__((address_space(3))) h8 lds_h8;
-    const int lane = threadIdx.x & 63;
-    const int r = 32 * b + (lane & 31), ch = (2 * c + (lane >> 5)) ^ ((r >> 1) & 7);
-    return *(const lds_h8 *)(uintptr_t)(st + r * ROW + ch * 16);
+    return *(const lds_h8 *)(uintptr_t)(bs.k[c] + SLOT * TILE + b * 32 * ROW);
   }
-
-  // V^T fragment (MFMA A operand) of dim block bd, key chunk c: lane l holds
-  // dim 32 bd + l%32 and keys 16 c + 4 (l/32) + {0..3} (slots 0-3) and
-  // 16 c + 8 + 4 (l/32) + {0..3} (slots 4-7), two transposed reads.
-  __device__ __forceinline__ static h8 read_v(uint32_t st, int bd, int c) {
-    const int lane = threadIdx.x & 63;
-    const int G = lane >> 4, L = lane & 15;
-    const int d = 32 * bd + 16 * (G & 1) + 4 * (L & 3);
-    const int k0 = 16 * c + 4 * (G >> 1) + (L >> 2), k1 = k0 + 8;
-    const uint32_t a0 = st + TILE + k0 * ROW + ((((d >> 3) ^ (4 * ((k0 >> 1) & 1)))) << 4) +
-                        (d & 7) * 2;
-    const uint32_t a1 = st + TILE + k1 * ROW + ((((d >> 3) ^ (4 * ((k1 >> 1) & 1)))) << 4) +
-                        (d & 7) * 2;
-    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(uintptr_t)a0);
-    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(uintptr_t)a1);
+  template <int SLOT>
+  __device__ __forceinline__ static h8 read_v(const Bases &bs, int bd, int c) {
+    const uint32_t a = bs.v[bd] + SLOT * TILE + c * 16 * ROW;
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(uintptr_t)a);
+    const i16x4_t hi =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(uintptr_t)(a + 8 * ROW));
     return __builtin_bit_cast(h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   }
 
@@ -123,21 +131,34 @@ struct AttnFwd {
   }
   __device__ __forceinline__ static float xsum(float v) { return v + __shfl_xor(v, 32, 64); }
 
-  // One K/V block: statistics (m_i, l_i) and accumulator update for the
-  // lane's query row m.  MASK: the on-band form with keys n > m masked.
-  template <bool MASK>
-  __device__ __forceinline__ static void block(uint32_t st, int n0, int m, float qk_scale,
-                                               const h8 (&qf)[D / 16], f16v (&acc)[D / 32],
-                                               float &m_i, float &l_i) {
-    const int lane = threadIdx.x & 63, g = lane >> 5;
-    f16v s[BN / 32];
+  // S^T block of the keys in K slot SLOT: lane holds query row l%32.
+  template <int SLOT>
+  __device__ __forceinline__ static void qk(const Bases &bs, const h8 (&qf)[D / 16],
+                                            f16v (&s)[BN / 32]) {
+    h8 kf[BN / 32][D / 16];
+#pragma unroll
+    for (int b = 0; b < BN / 32; ++b)
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c)
+        kf[b][c] = read_k<SLOT>(bs, b, c);
 #pragma unroll
     for (int b = 0; b < BN / 32; ++b) {
       s[b] = f16v{};
 #pragma unroll
       for (int c = 0; c < D / 16; ++c)
-        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_k(st, b, c), qf[c], s[b], 0, 0, 0);
+        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[b][c], qf[c], s[b], 0, 0, 0);
     }
+  }
+
+  // Softmax of one block (the tutorial's arithmetic) for the lane's query
+  // row m, keys n0 + 8 (r/4) + 4 g + r%4 of each 32-key block: updates m_i and
+  // l_i, rescales acc by alpha and returns P as MFMA B operands (key chunk c
+  // = registers 8 (c%2) .. +7 of key block c/2).  MASK: on-band form.
+  template <bool MASK>
+  __device__ __forceinline__ static void softmax(f16v (&s)[BN / 32], int n0, int m,
+                                                 float qk_scale, f16v (&acc)[D / 32],
+                                                 float &m_i, float &l_i, h8 (&pf)[BN / 16]) {
+    const int g = (threadIdx.x & 63) >> 5;
     float m_ij;
     if constexpr (MASK) {
       // qk = qk * qk_scale + where(m >= n, 0, -1e6); m_ij = max(m_i, rowmax(qk))
@@ -185,13 +206,6 @@ struct AttnFwd {
     l_i = l_i * alpha + l_ij;
     m_i = m_ij;
 #pragma unroll
-    for (int bd = 0; bd < D / 32; ++bd)
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        acc[bd][r] *= alpha;
-    // P^T fragments: key chunk c = registers 8 (c%2) .. +7 of key block c/2
-    h8 pf[BN / 16];
-#pragma unroll
     for (int c = 0; c < BN / 16; ++c)
 #pragma unroll
       for (int t = 0; t < 8; ++t)
@@ -199,16 +213,39 @@ struct AttnFwd {
 #pragma unroll
     for (int bd = 0; bd < D / 32; ++bd)
 #pragma unroll
+      for (int r = 0; r < 16; ++r)
+        acc[bd][r] *= alpha;
+  }
+
+  // O^T += V^T . P^T for the values in V slot SLOT.
+  template <int SLOT>
+  __device__ __forceinline__ static void pv(const Bases &bs, const h8 (&pf)[BN / 16],
+                                            f16v (&acc)[D / 32]) {
+    h8 vf[D / 32][BN / 16];
+#pragma unroll
+    for (int bd = 0; bd < D / 32; ++bd)
+#pragma unroll
       for (int c = 0; c < BN / 16; ++c)
-        acc[bd] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_v(st, bd, c), pf[c], acc[bd], 0, 0,
-                                                         0);
+        vf[bd][c] = read_v<SLOT>(bs, bd, c);
+#pragma unroll
+    for (int bd = 0; bd < D / 32; ++bd)
+#pragma unroll
+      for (int c = 0; c < BN / 16; ++c)
+        acc[bd] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[bd][c], pf[c], acc[bd], 0, 0, 0);
   }
 };
 
+// The K/V loop is software-pipelined: iteration j holds S_j in registers,
+// computes S_{j+1} (MFMA) while it turns S_j into P_j (VALU), then adds
+// P_j V_j.  K and V have two LDS slots each, K one block ahead of V:
+// iteration j first issues the loads of K_{j+2} (into K_j's slot) and
+// V_{j+1} (into V_{j-1}'s slot), and its closing barrier makes them visible.
+// Block j uses K slot j%2 and V slot j%2; the loop advances two blocks per
+// trip so that slots are constants (both segments have even trip counts).
 template <bool CAUSAL>
 __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
   typedef AttnFwd A;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * A::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[4 * A::TILE];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 5;
@@ -234,33 +271,57 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
   uint32_t ko[A::DMA], vo[A::DMA];
   A::dma_offsets<false>(wave, p.k_sm, ko);
   A::dma_offsets<true>(wave, p.v_sm, vo);
-  const uint32_t lds0 = lds_addr(smem);
+  const uint32_t k_lds = lds_addr(smem), v_lds = k_lds + 2 * A::TILE;
+  A::Bases bs;
+  A::bases(k_lds, v_lds, bs);
 
   // LoopSplit form of the K/V loop (keys [0, N_CTX), predicate start_n >=
   // causal_start): unmasked blocks [0, n_main), masked [n_main, n_end).
+  // Both counts are even (N_CTX and causal_start are multiples of 2 BN).
   const int causal_start = CAUSAL ? start_m * A::BM : p.N_CTX;
   const int n_main = causal_start / A::BN;
   const int n_end = CAUSAL ? (causal_start + A::BM) / A::BN : n_main;
 
   float m_i = -INFINITY, l_i = 1.0f;
-  A::f16v acc[A::D / 32];
+  A::f16v acc[A::D / 32], s[A::BN / 32];
 #pragma unroll
   for (int bd = 0; bd < A::D / 32; ++bd)
     acc[bd] = A::f16v{};
 
-  A::issue(rk, rv, ko, vo, p.k_sm, p.v_sm, 0, lds0, wave);
-  auto step = [&](int j, auto mask) {
-    __builtin_amdgcn_s_waitcnt(0x7 << 4); // vmcnt(0): this wave's loads of block j
-    __syncthreads();                      // everyone's; and stage (j+1)&1 is free
+  A::issue(rk, ko, p.k_sm, 0, k_lds, wave);
+  A::issue(rv, vo, p.v_sm, 0, v_lds, wave);
+  A::issue(rk, ko, p.k_sm, 1, k_lds + A::TILE, wave); // n_end >= 2
+  __builtin_amdgcn_s_waitcnt(0x7 << 4);               // vmcnt(0)
+  __syncthreads();
+  A::qk<0>(bs, qf, s);
+  __syncthreads(); // K slot 0 is refilled by iteration 0
+
+  auto iter = [&](int j, auto mask, auto slot) {
+    constexpr bool MASK = decltype(mask)::value;
+    constexpr int SL = decltype(slot)::value;
+    if (j + 2 < n_end)
+      A::issue(rk, ko, p.k_sm, j + 2, k_lds + SL * A::TILE, wave);
     if (j + 1 < n_end)
-      A::issue(rk, rv, ko, vo, p.k_sm, p.v_sm, j + 1, lds0 + ((j + 1) & 1) * A::STAGE, wave);
-    A::template block<decltype(mask)::value>(lds0 + (j & 1) * A::STAGE, j * A::BN, m,
-                                             p.qk_scale, qf, acc, m_i, l_i);
+      A::issue(rv, vo, p.v_sm, j + 1, v_lds + (1 - SL) * A::TILE, wave);
+    A::f16v sn[A::BN / 32];
+    A::qk<1 - SL>(bs, qf, sn); // S_{j+1} (a stale slot after the last block: unused)
+    A::h8 pf[A::BN / 16];
+    A::softmax<MASK>(s, j * A::BN, m, p.qk_scale, acc, m_i, l_i, pf);
+    A::pv<SL>(bs, pf, acc);
+#pragma unroll
+    for (int b2 = 0; b2 < A::BN / 32; ++b2)
+      s[b2] = sn[b2];
+    __builtin_amdgcn_s_waitcnt(0x7 << 4); // vmcnt(0): this wave's loads of K_{j+2}, V_{j+1}
+    __syncthreads();
   };
-  for (int j = 0; j < n_main; ++j)
-    step(j, std::false_type());
-  for (int j = n_main; j < n_end; ++j)
-    step(j, std::true_type());
+  for (int j = 0; j < n_main; j += 2) {
+    iter(j, std::false_type(), std::integral_constant<int, 0>());
+    iter(j + 1, std::false_type(), std::integral_constant<int, 1>());
+  }
+  for (int j = n_main; j < n_end; j += 2) {
+    iter(j, std::true_type(), std::integral_constant<int, 0>());
+    iter(j + 1, std::true_type(), std::integral_constant<int, 1>());
+  }
 
   // Epilogue: M = m_i + log2(l_i); O = acc / l_i.  Lane l holds, per dim
   // block bd and register quad q, dims 32 bd + 8 q + 4 g .. +3 of row m.
