@@ -68,7 +68,8 @@ _NP = {F32: np.float32, F16: np.uint16, BF16: np.uint16, I8: np.int8, F8E4M3: np
 
 
 def tiled_dot(a, b, *, a_type, c_type, block=(64, 64, 32), scale_mode=SCALE_NONE,
-              sa=None, sb=None, round_mode=ROUND_RNE, tiles=None, nthreads=0, out=None):
+              sa=None, sb=None, round_mode=ROUND_RNE, tiles=None, nthreads=0, out=None,
+              b_type=None):
     """Run the interpreter-equivalent tiled dot on the CPU.
 
     a: [M, K] array of raw element bits (uint16 for bf16/fp16, uint8 for e4m3,
@@ -90,7 +91,8 @@ def tiled_dot(a, b, *, a_type, c_type, block=(64, 64, 32), scale_mode=SCALE_NONE
     t0, t1 = (0, -1) if tiles is None else tiles
     bm, bn, bk = block
     rc = lib().oracle_tiled_dot(_ptr(a), _ptr(b), _ptr(out), _ptr(sa_c), _ptr(sb_c),
-                                M, N, K, K, N, N, a_type, a_type, c_type, scale_mode,
+                                M, N, K, K, N, N, a_type, a_type if b_type is None else b_type,
+                                c_type, scale_mode,
                                 round_mode, bm, bn, bk, t0, t1, nthreads)
     if rc != 0:
         raise ValueError(f"oracle_tiled_dot rejected the arguments (rc={rc})")

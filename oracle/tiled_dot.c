@@ -27,7 +27,10 @@
  *     so fp results agree to rounding, int32 results exactly;
  *   - fp8 operands are widened exactly to fp16 before the matmul (:633-636),
  *     with the generic converter (:202-263): e4m3 0x7F/0xFF decode as +-480,
- *     not NaN (quantisation with amax/448 scales never produces them);
+ *     not NaN (quantisation with amax/448 scales never produces them); e5m2
+ *     is the top byte of an fp16, so its widening is exact, inf and NaN
+ *     included.  tl.dot accepts any pair of fp8 types
+ *     (T:language/semantic.py:1484-1485);
  *   - bf16 <-> fp32 casts use _convert_float with rounding_mode None
  *     (cast_impl, :461-467): widening is exact and NARROWING TRUNCATES
  *     (round toward zero).  Compiled Triton rounds to nearest even.  Both
@@ -435,6 +438,7 @@ static float load_f(const uint8_t *base, int type, int64_t idx) {
   case OR_F16: { uint16_t h; memcpy(&h, base + 2 * idx, 2); return or_f16_to_f32(h); }
   case OR_BF16: { uint16_t h; memcpy(&h, base + 2 * idx, 2); return or_bf16_to_f32(h); }
   case OR_F8E4M3: return or_e4m3_to_f32(base[idx]);
+  case OR_F8E5M2: return or_f16_to_f32((uint16_t)(base[idx] << 8));
   default: return 0.f;
   }
 }
@@ -443,7 +447,7 @@ static int elt_size(int t) {
   switch (t) {
   case OR_F32: case OR_I32: return 4;
   case OR_F16: case OR_BF16: return 2;
-  case OR_I8: case OR_F8E4M3: return 1;
+  case OR_I8: case OR_F8E4M3: case OR_F8E5M2: return 1;
   default: return 0;
   }
 }
@@ -463,7 +467,9 @@ int oracle_tiled_dot(const void *Av, const void *Bv, void *Cv, const float *sa,
   uint8_t *C = (uint8_t *)Cv;
   if (BM <= 0 || BN <= 0 || BK <= 0 || M < 0 || N < 0 || K < 0)
     return -1;
-  if (a_type != b_type || !elt_size(a_type) || !elt_size(c_type))
+  const int fp8_pair = (a_type == OR_F8E4M3 || a_type == OR_F8E5M2) &&
+                       (b_type == OR_F8E4M3 || b_type == OR_F8E5M2);
+  if ((a_type != b_type && !fp8_pair) || !elt_size(a_type) || !elt_size(c_type))
     return -1;
   const int is_int = a_type == OR_I8;
   if (scale_mode == OR_SCALE_BLOCK128 && BK != 128)

@@ -286,16 +286,16 @@ def mx_case(rng, name, fa, fb, M, N, K, *, exact, block):
 TL_OUT = {"f32": tl.float32, "bf16": tl.bfloat16, "f16": tl.float16, "i32": tl.int32}
 TORCH_OUT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16,
              "i32": torch.int32}
-TORCH_IN = {"f16": torch.float16, "bf16": torch.bfloat16, "i8": torch.int8,
-            "f8e4m3": torch.float8_e4m3fn}
+FP8 = (torch.float8_e4m3fn, torch.float8_e5m2)
 BITS = {torch.float16: np.uint16, torch.bfloat16: np.uint16, torch.float8_e4m3fn: np.uint8,
-        torch.int8: np.int8, torch.float32: np.float32, torch.int32: np.int32}
+        torch.float8_e5m2: np.uint8, torch.int8: np.int8, torch.float32: np.float32,
+        torch.int32: np.int32}
 
 
 def bits(t):
     """Raw element bits of a CPU tensor as a numpy array."""
     view = {torch.float16: torch.int16, torch.bfloat16: torch.int16,
-            torch.float8_e4m3fn: torch.uint8}.get(t.dtype)
+            torch.float8_e4m3fn: torch.uint8, torch.float8_e5m2: torch.uint8}.get(t.dtype)
     a = (t.view(view) if view is not None else t).numpy()
     return a.view(BITS[t.dtype])
 
@@ -310,7 +310,7 @@ def run(a, b, *, out, block, epi=EPI_NONE, sa=None, sb=None):
     sa_ld = sa.shape[1] if (sa is not None and sa.dim() == 2) else 0
     sb_ld = sb.shape[1] if (sb is not None and sb.dim() == 2) else 0
     grid = (triton.cdiv(M, BM), triton.cdiv(N, BN))
-    mask = a.dtype != torch.float8_e4m3fn
+    mask = a.dtype not in FP8
     if not mask:
         assert M % BM == 0 and N % BN == 0 and K % BK == 0, "fp8 fixtures need whole tiles"
     tiled_dot_kernel[grid](a, b, c, sa_t, sb_t, M, N, K, sa_ld, sb_ld, BM=BM, BN=BN, BK=BK,
@@ -322,7 +322,8 @@ def run(a, b, *, out, block, epi=EPI_NONE, sa=None, sb=None):
 def save(name, a, b, c, *, block, out, epi=EPI_NONE, sa=None, sb=None, exact=False,
          store_inputs=True, seeds=None, tiles=None):
     """Write <name>.npz.  `tiles` keeps only those output tiles (others left out)."""
-    d = dict(a_type=str(_tname(a.dtype)), c_type=out, block=np.array(block, np.int32),
+    d = dict(a_type=str(_tname(a.dtype)), b_type=str(_tname(b.dtype)), c_type=out,
+             block=np.array(block, np.int32),
              epi=np.int32(epi), exact=np.bool_(exact), M=np.int64(a.shape[0]),
              N=np.int64(b.shape[1]), K=np.int64(a.shape[1]),
              a_sha256=hashlib.sha256(bits(a).tobytes()).hexdigest(),
@@ -348,7 +349,7 @@ def save(name, a, b, c, *, block, out, epi=EPI_NONE, sa=None, sb=None, exact=Fal
 
 def _tname(dt):
     return {torch.float16: "f16", torch.bfloat16: "bf16", torch.int8: "i8",
-            torch.float8_e4m3fn: "f8e4m3"}[dt]
+            torch.float8_e4m3fn: "f8e4m3", torch.float8_e5m2: "f8e5m2"}[dt]
 
 
 def dyadic(shape, rng, lim, denom, dtype):
@@ -462,6 +463,22 @@ def main():
     # with the LoopSplit on-band branch, and plain
     attn_case(rng, "attn_fwd_causal", 1, 2, 256, 64, True, 0.5, (64, 32))
     attn_case(rng, "attn_fwd_plain", 2, 1, 128, 64, False, 1.3, (64, 32))
+
+    # fp8 tt.dot with e5m2 operands (the tutorial's p . v with fp8e5 p,
+    # R:pass/LoopSplit/06-fused-attention.py:81-85), fp32 C.  Exact: small
+    # dyadic values (also exact in the MFMA's fixed-point group sums).
+    a = dyadic((256, 256), rng, 7, 4, torch.float8_e5m2)
+    b = dyadic((256, 256), rng, 7, 4, torch.float8_e5m2)
+    save("fp8e5_f32_exact", a, b, run(a, b, out="f32", block=(64, 64, 64)),
+         block=(64, 64, 64), out="f32", exact=True)
+    a = dyadic((128, 384), rng, 15, 8, torch.float8_e4m3fn)
+    b = dyadic((384, 256), rng, 7, 4, torch.float8_e5m2)
+    save("fp8e4e5_f32_exact", a, b, run(a, b, out="f32", block=(64, 64, 64)),
+         block=(64, 64, 64), out="f32", exact=True)
+    a = normal((64, 256), rng, 1.0, torch.float8_e5m2)
+    b = normal((256, 128), rng, 1.0, torch.float8_e5m2)
+    save("fp8e5_f32_normal", a, b, run(a, b, out="f32", block=(64, 64, 64)),
+         block=(64, 64, 64), out="f32")
 
 
 if __name__ == "__main__":

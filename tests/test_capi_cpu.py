@@ -244,8 +244,21 @@ def test_mx_plans():
     assert err(a_type=tx.F4E2M1, scale_mode=tx.SCALE_NONE) == tx.ERR_UNSUPPORTED
     assert err(scale_mode=4) == tx.ERR_INVALID
     assert err(a_type=tx.F4E2M1, K=256, lda=264) == tx.ERR_INVALID  # 132-byte rows
-    # the non-MX modes keep rejecting e5m2
-    assert err(a_type=tx.F8E5M2, scale_mode=tx.SCALE_NONE) == tx.ERR_UNSUPPORTED
+    # the fp32 block-scaled mode keeps rejecting e5m2 (e4m3 only)
+    assert err(a_type=tx.F8E5M2, scale_mode=tx.SCALE_BLOCK128) == tx.ERR_UNSUPPORTED
+
+
+def test_fp8_e5m2_plans():
+    """tt.dot over fp8 pairs with e5m2 (any mix, fp32 C): the 256x256 8-bit tile."""
+    for a, b in ((tx.F8E5M2, tx.F8E5M2), (tx.F8E4M3, tx.F8E5M2), (tx.F8E5M2, tx.F8E4M3)):
+        p = tx.plan(tx.make_desc(300, 272, 400, a, tx.F32, b_type=b))
+        assert p.kernel == tx.KERNEL_GEMM_F8
+        assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (256, 256, 128)
+        assert p.peak_flops == pytest.approx(5033.2e12)
+        assert _err(tx.make_desc(300, 272, 400, a, tx.BF16, b_type=b)) == tx.ERR_UNSUPPORTED
+        assert _err(tx.make_desc(256, 256, 256, a, tx.F32, b_type=b,
+                                 block=(128, 128, 128))) == tx.ERR_UNSUPPORTED
+    assert _err(tx.make_desc(64, 64, 128, tx.F8E5M2, tx.F32, b_type=tx.BF16)) == tx.ERR_UNSUPPORTED
 
 
 def test_dot_scaled_argument_checks():

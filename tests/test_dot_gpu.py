@@ -318,13 +318,14 @@ def test_8bit_tile_epilogues(gpu, kind, out, M, N, K, blk):
 # ----------------------------------------------------------------------------- golden fixtures
 
 GOLDEN_TILE = {"f16": (64, 64, 32), "bf16": (128, 128, 64), "i8": (128, 128, 128),
-               "f8e4m3": (128, 128, 128)}
+               "f8e4m3": (128, 128, 128), "f8e5m2": (256, 256, 128)}
 
 
 @pytest.mark.parametrize("name", ["c1_fp16_512", "fp16_f32_edges_exact", "fp16_f16_rne_exact",
                                   "bf16_bf16_rtz_exact", "bf16_f32_normal", "int8_i32",
                                   "w8a8_rowcol_rtz", "fp8_block128_f32_exact",
-                                  "fp8_block128_bf16_normal"])
+                                  "fp8_block128_bf16_normal", "fp8e5_f32_exact",
+                                  "fp8e4e5_f32_exact", "fp8e5_f32_normal"])
 def test_golden_fixture_on_gpu(gpu, name):
     """The interpreter's fixtures through the HIP path.
 
@@ -356,20 +357,22 @@ def golden_on_gpu(gpu, name, tile, b_kmajor=False):
     say(f"golden {name} tile={tile}")
     f = load_fixture(os.path.join(GOLDEN, name + ".npz"))
     at, ct = str(f["a_type"]), str(f["c_type"])
+    bt = str(f.get("b_type", at))
     tdt = {"f16": torch.float16, "bf16": torch.bfloat16, "i8": torch.int8,
-           "f8e4m3": torch.float8_e4m3fn}[at]
+           "f8e4m3": torch.float8_e4m3fn, "f8e5m2": torch.float8_e5m2}
     odt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16,
            "i32": torch.int32}[ct]
-    view = {"f16": torch.int16, "bf16": torch.int16, "f8e4m3": torch.uint8, "i8": torch.int8}[at]
-    da = to_device(f["a"], gpu).view(view).view(tdt)
+    view = {"f16": torch.int16, "bf16": torch.int16, "f8e4m3": torch.uint8, "f8e5m2": torch.uint8,
+            "i8": torch.int8}
+    da = to_device(f["a"], gpu).view(view[at]).view(tdt[at])
     if b_kmajor:
-        db = to_device(np.ascontiguousarray(f["b"].T), gpu).view(view).view(tdt).t()
+        db = to_device(np.ascontiguousarray(f["b"].T), gpu).view(view[bt]).view(tdt[bt]).t()
     else:
-        db = to_device(f["b"], gpu).view(view).view(tdt)
+        db = to_device(f["b"], gpu).view(view[bt]).view(tdt[bt])
     kw = {}
     if "sa" in f:
         kw = dict(scale_a=to_device(f["sa"], gpu), scale_b=to_device(f["sb"], gpu))
-    blk = GOLDEN_TILE[at] if name != "c1_fp16_512" else (64, 64, 32)
+    blk = GOLDEN_TILE[bt if bt == "f8e5m2" else at] if name != "c1_fp16_512" else (64, 64, 32)
     if name == "w8a8_rowcol_rtz":
         blk = (0, 0, 0)  # M = 5: the decode kernel
     if tile is not None:
@@ -383,7 +386,7 @@ def golden_on_gpu(gpu, name, tile, b_kmajor=False):
     oblk = blk if blk != (0, 0, 0) else (64, 64, 64)
     ref = oracle.tiled_dot(f["a"], f["b"], a_type=OR_TYPE[at], c_type=OR_TYPE[ct], block=oblk,
                            scale_mode=sm, sa=f.get("sa"), sb=f.get("sb"),
-                           round_mode=oracle.ROUND_RNE)
+                           round_mode=oracle.ROUND_RNE, b_type=OR_TYPE[bt])
     if bool(f["exact"]) and at == "f8e4m3" and sm == oracle.SCALE_BLOCK128 and blk[0] == 256:
         # (both 256-row tiles: 256x256 and 256x224)
         # The 256-wide fp8 tile applies a block's scales as one fma(part,
@@ -414,6 +417,42 @@ def golden_on_gpu(gpu, name, tile, b_kmajor=False):
         return
     g, w = fixture_output(f, got)
     K = int(f["K"])
-    scale = math.sqrt(K) if at == "f8e4m3" else 1.0
+    scale = math.sqrt(K) if at in ("f8e4m3", "f8e5m2") else 1.0
     check_close(bits_to_f32(g, ct), bits_to_f32(w, ct), atol=ATOL, rtol=RTOL, scale=scale,
                 what=f"golden {name}")
+
+
+@pytest.mark.parametrize("fa,fb", [("e5m2", "e5m2"), ("e4m3", "e5m2"), ("e5m2", "e4m3")])
+@pytest.mark.parametrize("M,N,K", [(512, 512, 1024), (300, 272, 400), (16, 1024, 256)])
+def test_fp8_e5m2_dot(gpu, fa, fb, M, N, K):
+    """tt.dot of fp8 operands with e5m2 on a side (the tutorial's p . v with
+    fp8e5 p), fp32 C, on the 256x256 8-bit tile: edges, a K tail, small M.
+    Finite codes across the whole range; tolerance normalised by the
+    operands' RMS (the MFMA's fixed-point group sums)."""
+    import torch
+    say(f"fp8 {fa}x{fb} M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + N + K)
+
+    def codes(shape, f):
+        c = rng.integers(0, 256, size=shape).astype(np.uint8)
+        if f == "e5m2":
+            return np.where((c & 0x7C) == 0x7C, c & 0x83, c).astype(np.uint8)
+        return np.where((c & 0x7F) == 0x7F, c & 0xF0, c).astype(np.uint8)
+    a, b = codes((M, K), fa), codes((K, N), fb)
+    tdt = {"e4m3": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}
+    otype = {"e4m3": oracle.F8E4M3, "e5m2": oracle.F8E5M2}
+    da = to_device(a, gpu).view(tdt[fa])
+    db = to_device(b, gpu).view(tdt[fb])
+    p = tx.plan_for(da, db, tx.F32)
+    assert p.kernel == tx.KERNEL_GEMM_F8
+    c = tx.dot(da, db, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    got = from_device(c)
+    ref = oracle.tiled_dot(a, b, a_type=otype[fa], b_type=otype[fb], c_type=oracle.F32,
+                           block=(256, 256, 128))
+    dec = lambda q, f: (oracle.e4m3_to_f32(q) if f == "e4m3"
+                        else oracle.f16_to_f32(q.astype(np.uint16) << 8)).astype(np.float64)
+    rms = lambda q, f: float(np.sqrt(np.mean(dec(q, f) ** 2)))
+    err = check_close(got, ref, atol=ATOL, rtol=RTOL, scale=math.sqrt(K) * rms(a, fa) * rms(b, fb),
+                      what=f"fp8 {fa}x{fb}")
+    say(f"fp8 {fa}x{fb} {M}x{N}x{K}: max|d|={err:.3g}")

@@ -24,8 +24,10 @@ GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 U32 = 2.0 ** -24  # unit roundoff of fp32
 
 OR_TYPE = {"f16": oracle.F16, "bf16": oracle.BF16, "i8": oracle.I8, "f8e4m3": oracle.F8E4M3,
-           "f32": oracle.F32, "i32": oracle.I32}
+           "f8e5m2": oracle.F8E5M2, "f32": oracle.F32, "i32": oracle.I32}
 DECODE = {"f16": oracle.f16_to_f32, "bf16": oracle.bf16_to_f32, "f8e4m3": oracle.e4m3_to_f32,
+          # e5m2 is the top byte of an fp16 (the interpreter widens it to fp16)
+          "f8e5m2": lambda x: oracle.f16_to_f32(x.astype(np.uint16) << 8),
           "i8": lambda x: x.astype(np.float32)}
 
 
@@ -54,7 +56,8 @@ def run_oracle(f, round_mode=oracle.ROUND_RTZ):
     sm = {0: oracle.SCALE_NONE, 1: oracle.SCALE_ROWCOL, 2: oracle.SCALE_BLOCK128}[int(f["epi"])]
     return oracle.tiled_dot(f["a"], f["b"], a_type=OR_TYPE[at], c_type=OR_TYPE[ct],
                             block=tuple(int(x) for x in f["block"]), scale_mode=sm,
-                            sa=f.get("sa"), sb=f.get("sb"), round_mode=round_mode)
+                            sa=f.get("sa"), sb=f.get("sb"), round_mode=round_mode,
+                            b_type=OR_TYPE[str(f.get("b_type", at))])
 
 
 def fixture_output(f, c):
@@ -76,7 +79,7 @@ def abs_product_sum(f):
     """sum_k |a[m,k]| |b[k,n]| (with block scales applied) in float64."""
     at = str(f["a_type"])
     a = np.abs(DECODE[at](f["a"]).astype(np.float64))
-    b = np.abs(DECODE[at](f["b"]).astype(np.float64))
+    b = np.abs(DECODE[str(f.get("b_type", at))](f["b"]).astype(np.float64))
     if int(f["epi"]) == 2:
         K = a.shape[1]
         sa, sb = f["sa"].astype(np.float64), f["sb"].astype(np.float64)
@@ -111,7 +114,19 @@ def test_golden_fixture(path):
 def test_fixtures_present():
     names = {os.path.basename(p)[:-4] for p in FIXTURES}
     assert {"c1_fp16_512", "fp16_f32_edges_exact", "bf16_bf16_rtz_exact", "int8_i32",
-            "w8a8_rowcol_rtz", "fp8_block128_f32_exact", "fp8_block128_bf16_normal"} <= names
+            "w8a8_rowcol_rtz", "fp8_block128_f32_exact", "fp8_block128_bf16_normal",
+            "fp8e5_f32_exact", "fp8e4e5_f32_exact", "fp8e5_f32_normal"} <= names
+
+
+def test_e5m2_widening_matches_torch():
+    """The interpreter widens fp8 to fp16; for e5m2 that is exact, so the
+    oracle's decode must equal torch's float8_e5m2 -> float for every code."""
+    import torch
+    codes = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(codes).view(torch.float8_e5m2).float().numpy()
+    got = DECODE["f8e5m2"](codes)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(got[~np.isnan(got)], ref[~np.isnan(ref)])
 
 
 def test_bf16_fixture_pins_truncation():

@@ -107,6 +107,12 @@ struct GemmConfig {
     OP_F8, 256, 256, BK, 2, 4, EPI, gemm8_w4_kernel<OP_F8, EPI, FA, FB>, 0, 0, \
         5, (FA) | ((FB) << 4)                                                  \
   }
+// Unscaled fp8 with e5m2 operands (MFMA format codes FA, FB; fp32 C).
+#define TX_GEMM_8F(FA, FB)                                                     \
+  GemmConfig {                                                                 \
+    OP_F8, 256, 256, 128, 2, 4, EPI_F32, gemm8_w4_kernel<OP_F8, EPI_F32, FA, FB>, \
+        0, 0, 5, (FA) | ((FB) << 4)                                            \
+  }
 #define TX_GEMM_8N(OP, EPI)                                                    \
   GemmConfig { OP, 256, 224, 128, 4, 2, EPI, gemm8_n224_kernel<OP, EPI>, 0, 0, 5 }
 
@@ -155,6 +161,10 @@ const GemmConfig kGemmConfigs[] = {
     TX_GEMM_8(OP_F8, EPI_BLOCK128_BF16),
     TX_GEMM_8(OP_F8, EPI_BLOCK128_F32),
     TX_GEMM_8(OP_F8, EPI_F32),
+    // fp8 tt.dot with e5m2 on either side (the tutorial's p . v with fp8e5 p)
+    TX_GEMM_8F(1, 1),
+    TX_GEMM_8F(0, 1),
+    TX_GEMM_8F(1, 0),
     // MX: e8m0-scaled fp8 (e4m3 / e5m2 in any mix) and fp4 (gemm8_w4.h)
     TX_GEMM_MX(0, 0, 128, EPI_MX_F32),
     TX_GEMM_MX(0, 0, 128, EPI_MX_BF16),
@@ -190,11 +200,13 @@ const DecodeKernelFn kDecodeKernels[4] = {decode_i8_kernel<1>, decode_i8_kernel<
 int mxFormat(int32_t t) {
   return t == TX_F8E4M3 ? 0 : t == TX_F8E5M2 ? 1 : t == TX_F4E2M1 ? 4 : -1;
 }
-// MX format pair of a descriptor (0 for the other scale modes).
+// Operand format pair of an fp8 / MX descriptor (0 otherwise, and for e4m3
+// on both sides).
 int fmtOf(const tx_dot_desc &d) {
-  if (d.scale_mode != TX_SCALE_MX32)
+  const int fa = mxFormat(d.a_type), fb = mxFormat(d.b_type);
+  if (fa < 0 || fb < 0)
     return 0;
-  return mxFormat(d.a_type) | (mxFormat(d.b_type) << 4);
+  return fa | (fb << 4);
 }
 
 // Operand kind and epilogue of a descriptor (-1 if unsupported).
@@ -210,6 +222,16 @@ void classify(const tx_dot_desc &d, int *op, int *epi) {
       *epi = EPI_MX_F32;
     else if (d.c_type == TX_BF16)
       *epi = EPI_MX_BF16;
+    return;
+  }
+  const bool fp8a = d.a_type == TX_F8E4M3 || d.a_type == TX_F8E5M2;
+  const bool fp8b = d.b_type == TX_F8E4M3 || d.b_type == TX_F8E5M2;
+  if (fp8a && fp8b && (d.a_type == TX_F8E5M2 || d.b_type == TX_F8E5M2)) {
+    // tt.dot of fp8 operands with e5m2 on a side ("all combinations of fp8
+    // x fp8 are permitted", T:language/semantic.py:1484-1485): fp32 C
+    *op = OP_F8;
+    if (d.scale_mode == TX_SCALE_NONE && d.c_type == TX_F32)
+      *epi = EPI_F32;
     return;
   }
   if (d.a_type != d.b_type)

@@ -79,8 +79,8 @@ extern "C" __device__ f32x4_t txk_mfma_scale_16x16x128_f4(i32x4_t, i32x4_t, f32x
                                                           int, int, int, int)
     __asm("llvm.amdgcn.mfma.scale.f32.16x16x128.f8f6f4.v4i32.v4i32");
 
-// FA, FB: MFMA format codes of A and B for the MX epilogues (0 e4m3, 1 e5m2,
-// 4 e2m1); unused otherwise.
+// FA, FB: MFMA format codes of A and B (0 e4m3, 1 e5m2; 4 e2m1 with the MX
+// epilogues only); the unscaled fp8 dot takes e4m3 / e5m2 in any mix.
 template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
   static constexpr int BM = 256, BN = 256, BK = 128, NW = 8, WN = 4;
   static constexpr int WTM = 128, WTN = 64, FM = WTM / 16, FN = WTN / 16;
@@ -277,8 +277,8 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
       c = __builtin_amdgcn_mfma_i32_16x16x64_i8(b0, a0, c, 0, 0, 0);
       return __builtin_amdgcn_mfma_i32_16x16x64_i8(b1, a1, c, 0, 0, 0);
     } else {
-      // format 0 for both operands: fp8 e4m3; no hardware block scales.
-      return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bcol, arow, c, 0, 0, 0, 0, 0, 0);
+      // operand formats FB (MFMA A := B columns) and FA; no hardware scales
+      return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bcol, arow, c, FB, FA, 0, 0, 0, 0);
     }
   }
 

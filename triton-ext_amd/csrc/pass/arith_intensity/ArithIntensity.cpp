@@ -146,7 +146,7 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
       // W8A8 decode: one row slice up to M = 64, slices of 64 beyond,
       // 128-column strips, 64-row K batches
       t = Tile{(int32_t)(d->M > 64 ? 64 : 16 * cdiv(d->M > 0 ? d->M : 1, 16)), 128, 64, 1.0};
-    else if (d->a_type == TX_F8E4M3)
+    else if (d->a_type == TX_F8E4M3 || d->a_type == TX_F8E5M2)
       t = kTiles8[0]; // the register-staged 128x128 tile is slower everywhere
     else
       t = chooseTile(kTiles8, d->M, d->N, d->K);
