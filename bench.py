@@ -51,7 +51,8 @@ def parse():
                     help="secondary workloads to run, comma-separated: vendor, tail, w8a8 (or "
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256), fp8, kmajor, mx (or mxfp8, mxfp4, "
                          "mxfp8_4096, mxfp8_8192, mxfp4_4096, mxfp4_8192), attn (or attn_1024, attn_4096, "
-                         "attn_16384; attn_vendor adds torch sdpa beside each) (default: all); "
+                         "attn_16384; attn_d128 for head dim 128; attn_vendor adds torch sdpa beside each) "
+                         "(default: all); "
                          "the bf16 "
                          "headline always runs")
     ap.add_argument("--copy-probe", action="store_true",
@@ -285,7 +286,7 @@ def bench_mx(tx, dev, M, N, K, fmt, steps, warmup, seed=7):
                           tile=[p.desc.block_m, p.desc.block_n, p.desc.block_k]))
 
 
-def bench_attn(tx, dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9):
+def bench_attn(tx, dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9, dtype=None):
     """Fused attention forward, the tutorial's bench_flash_attention "fwd"
     configuration (R:pass/LoopSplit/06-fused-attention.py:737-795): fp16
     randn q, k, v [4, 32, N_CTX, 64], sm_scale 1.3; FLOPs 4 Z H N^2 D, halved
@@ -293,11 +294,13 @@ def bench_attn(tx, dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9):
     import torch
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
-    q, k, v = (torch.randn((Z, H, N_CTX, D), generator=g, device=dev, dtype=torch.float16)
+    dtype = dtype or torch.float16
+    q, k, v = (torch.randn((Z, H, N_CTX, D), generator=g, device=dev, dtype=dtype)
                for _ in range(3))
     o = torch.empty_like(q)
     M = torch.empty((Z, H, N_CTX), device=dev, dtype=torch.float32)
-    p = tx.attn_plan(Z, H, N_CTX, D, causal, 1.3)
+    p = tx.attn_plan(Z, H, N_CTX, D, causal, 1.3,
+                     dtype=tx.BF16 if dtype == torch.bfloat16 else tx.F16)
     L = tx.load()
     args = (ctypes.byref(p), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
             M.data_ptr(), torch.cuda.current_stream().cuda_stream)
@@ -307,12 +310,14 @@ def bench_attn(tx, dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9):
         if rc != 0:
             raise RuntimeError(L.tx_get_last_error().decode())
     ms = time_back_to_back(run, steps, warmup)
-    return dict(workload=f"fused attention fwd fp16 Z={Z} H={H} N_CTX={N_CTX} D={D} "
+    tn = "bf16" if dtype == torch.bfloat16 else "fp16"
+    return dict(workload=f"fused attention fwd {tn} Z={Z} H={H} N_CTX={N_CTX} D={D} "
                          f"causal={causal}", ms=ms, tflops=p.flops / ms / 1e9,
                 frac=p.flops / ms / 1e-3 / PEAK_BF16)
 
 
 def bench_vendor_attn(dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9):
+    # (fp16, as the tutorial's benchmark)
     """torch.nn.functional.scaled_dot_product_attention on the same inputs:
     the vendor reference (ROCm's fused attention behind torch)."""
     import torch
@@ -436,6 +441,17 @@ def main():
                     secondary.append(r)
                     print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr,
                           flush=True)
+
+    if want("attn_d128"):  # head dim 128 (beyond the tutorial's 64)
+        for causal in (True, False):
+            r = bench_attn(tx, dev, 4096, causal, args.steps, args.warmup, Z=4, H=16, D=128)
+            secondary.append(r)
+            print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+            if want("vendor") or want("attn_vendor"):
+                r = bench_vendor_attn(dev, 4096, causal, args.steps, args.warmup, Z=4, H=16, D=128)
+                secondary.append(r)
+                print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr,
+                      flush=True)
 
     cpu, parity = None, None
     if not args.no_cpu:

@@ -26,7 +26,7 @@
  * entirely past the diagonal add exactly zero (p = 0, alpha = 1 while
  * |qk * qk_scale| < 1e6 - |m_i|) and are not run.
  *
- * q, k, v, o are [Z][H][N_CTX][HEAD_DIM] fp16 with HEAD_DIM contiguous and
+ * q, k, v, o are [Z][H][N_CTX][HEAD_DIM] fp16 or bf16 with HEAD_DIM contiguous and
  * the given element strides; M is fp32 [Z * H][N_CTX] (the tutorial's
  * logsumexp in base 2, saved for the backward).  All device pointers; errors
  * by return code and tx_get_last_error() (tx_dot.h).
@@ -42,8 +42,8 @@ extern "C" {
 
 typedef struct tx_attn_desc {
   int64_t Z, H, N_CTX;
-  int32_t head_dim; /* 64 */
-  int32_t dtype;    /* TX_F16 for q, k, v and o */
+  int32_t head_dim; /* 64 or 128 */
+  int32_t dtype;    /* TX_F16 (the tutorial's) or TX_BF16 for q, k, v and o */
   int32_t causal;   /* 0 or 1 */
   float sm_scale;
   /* element strides (batch, head, row) of q, k, v, o; 0 = packed */
@@ -65,8 +65,9 @@ typedef struct tx_attn_plan {
 } tx_attn_plan;
 
 /* Validate `desc` and fill `plan`.  TX_ERR_UNSUPPORTED unless head_dim is
- * 64, dtype TX_F16 and N_CTX a multiple of 128 (the tutorial's block
- * pointers assume whole blocks). */
+ * 64 or 128, dtype TX_F16 or TX_BF16 and N_CTX a multiple of 128 (the
+ * tutorial's block pointers assume whole blocks).  p is rounded to q's type
+ * to nearest even before p @ v, as compiled Triton does. */
 TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *plan);
 
 /* Enqueue the forward on `stream` (a hipStream_t, NULL = null stream). */

@@ -51,7 +51,7 @@ def lib():
         L.or_mx_decode_array.argtypes = [vp, vp, i64, i32]
         L.oracle_attn_fwd.restype = i32
         L.oracle_attn_fwd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i32, ctypes.c_float,
-                                      i32, i32, i32, i32, i32]
+                                      i32, i32, i32, i32, i32, i32, i32]
         L.oracle_dot_scaled.restype = i32
         L.oracle_dot_scaled.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64,
                                         i32, i32, i32, i32, i32]
@@ -185,11 +185,13 @@ def dot_scaled(a, sa, a_fmt, b, sb, b_fmt, *, K, c_type=F32, round_mode=ROUND_RN
     return out
 
 
-def attn_fwd(q, k, v, *, sm_scale, causal, block=(64, 32), mode=0, nthreads=0):
+def attn_fwd(q, k, v, *, sm_scale, causal, block=(64, 32), mode=0, dtype=F16,
+             round_mode=ROUND_RNE, nthreads=0):
     """The fused-attention tutorial's forward on the CPU.
 
-    q, k, v: uint16 fp16 bits [Z, H, N, D] (made contiguous).  Returns
-    (o as uint16 fp16 bits [Z, H, N, D], M fp32 [Z * H, N]).  block =
+    q, k, v: uint16 fp16 (or bf16, dtype=BF16) bits [Z, H, N, D] (made
+    contiguous).  Returns (o as uint16 bits of the same type [Z, H, N, D],
+    M fp32 [Z * H, N]).  block =
     (BLOCK_M, BLOCK_N); mode 0 the tutorial's split loop, 1 every block
     masked, 2 mode 0 without the blocks past the diagonal.
     """
@@ -201,7 +203,8 @@ def attn_fwd(q, k, v, *, sm_scale, causal, block=(64, 32), mode=0, nthreads=0):
     o = np.zeros(q.shape, dtype=np.uint16)
     M = np.zeros((Z * H, N), dtype=np.float32)
     rc = lib().oracle_attn_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(M), Z, H, N, D,
-                               float(sm_scale), int(causal), block[0], block[1], mode, nthreads)
+                               float(sm_scale), int(causal), block[0], block[1], mode, dtype,
+                               round_mode, nthreads)
     if rc != 0:
         raise ValueError(f"oracle_attn_fwd rejected the arguments (rc={rc})")
     return o, M

@@ -312,16 +312,23 @@ int oracle_dot_scaled(const void *Av, const void *Bv, void *Cv, const uint8_t *s
  *   p = exp2(qk); l_ij = rowsum p (ascending); alpha = exp2(m_i - m_ij)
  *   l_i = l_i*alpha + l_ij; acc = acc*alpha; acc = (fp16(p) @ v) + acc
  *   m_i = m_ij;  finally M = m_i + log2(l_i), o = fp16(acc / l_i)
- * causal_start = start_m*BM (causal) or N.  mode (tests only) 0: the
+ * causal_start = start_m*BM (causal) or N.  dtype OR_F16 (the tutorial's)
+ * or OR_BF16 for q, k, v, p and o; narrowing to bf16 uses round_mode
+ * (compiled Triton rounds to nearest even; fp16 always does).  mode (tests only) 0: the
  * tutorial's loop over all keys, split at causal_start; 1: the same loop
  * with every block in the masked form (no split); 2: mode 0 without the
  * blocks wholly past the diagonal.  Returns 0, or -1 on bad arguments.
  */
 int oracle_attn_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, uint16_t *o,
                     float *M, int64_t Z, int64_t H, int64_t N, int D, float sm_scale,
-                    int causal, int BM, int BN, int mode, int nthreads) {
-  if (Z < 0 || H < 0 || N < 0 || D <= 0 || BM <= 0 || BN <= 0 || N % BM || N % BN)
+                    int causal, int BM, int BN, int mode, int dtype, int round_mode,
+                    int nthreads) {
+  if (Z < 0 || H < 0 || N < 0 || D <= 0 || BM <= 0 || BN <= 0 || N % BM || N % BN ||
+      (dtype != OR_F16 && dtype != OR_BF16))
     return -1;
+  const int bf = dtype == OR_BF16;
+#define ATTN_LD(x) (bf ? or_bf16_to_f32(x) : or_f16_to_f32(x))
+#define ATTN_ST(f) (bf ? or_f32_to_bf16((f), round_mode) : or_f32_to_f16(f))
   const float qk_scale = sm_scale * 1.44269504f;
   const int64_t programs = Z * H * (N / BM);
   int rc = 0;
@@ -351,7 +358,7 @@ int oracle_attn_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, uin
         const int64_t base = hz * N * D, m0 = start_m * BM;
         for (int i = 0; i < BM; ++i) {
           for (int d = 0; d < D; ++d) {
-            qb[i * D + d] = or_f16_to_f32(q[base + (m0 + i) * D + d]);
+            qb[i * D + d] = ATTN_LD(q[base + (m0 + i) * D + d]);
             acc[i * D + d] = 0.f;
           }
           m_i[i] = -INFINITY;
@@ -366,7 +373,7 @@ int oracle_attn_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, uin
             for (int j = 0; j < BN; ++j) {
               float t = 0.f;
               for (int d = 0; d < D; ++d)
-                t += qb[i * D + d] * or_f16_to_f32(k[base + (n0 + j) * D + d]);
+                t += qb[i * D + d] * ATTN_LD(k[base + (n0 + j) * D + d]);
               qk[i * BN + j] = t;
             }
           for (int i = 0; i < BM; ++i) {
@@ -405,12 +412,12 @@ int oracle_attn_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, uin
             l_i[i] = l_i[i] * alpha + l_ij;
             for (int d = 0; d < D; ++d)
               acc[i * D + d] = acc[i * D + d] * alpha;
-            for (int j = 0; j < BN; ++j) /* p.to(fp16) */
-              r[j] = or_f16_to_f32(or_f32_to_f16(r[j]));
+            for (int j = 0; j < BN; ++j) /* p.to(q's type) */
+              r[j] = ATTN_LD(ATTN_ST(r[j]));
             for (int d = 0; d < D; ++d) {
               float t = 0.f;
               for (int j = 0; j < BN; ++j)
-                t += r[j] * or_f16_to_f32(v[base + (n0 + j) * D + d]);
+                t += r[j] * ATTN_LD(v[base + (n0 + j) * D + d]);
               pv[i * D + d] = t;
             }
             for (int d = 0; d < D; ++d)
@@ -421,12 +428,14 @@ int oracle_attn_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, uin
         for (int i = 0; i < BM; ++i) {
           M[hz * N + m0 + i] = m_i[i] + log2f(l_i[i]);
           for (int d = 0; d < D; ++d)
-            o[base + (m0 + i) * D + d] = or_f32_to_f16(acc[i * D + d] / l_i[i]);
+            o[base + (m0 + i) * D + d] = ATTN_ST(acc[i * D + d] / l_i[i]);
         }
       }
     }
     free(qb); free(acc); free(qk); free(pv); free(m_i); free(l_i);
   }
+#undef ATTN_LD
+#undef ATTN_ST
   return rc;
 }
 

@@ -75,6 +75,29 @@ def test_attn_oracle_vs_float64(causal, Z, H, N, block):
     assert np.abs(M - rM).max() < 1e-5 * np.abs(rM).max() + 1e-6
 
 
+@pytest.mark.parametrize("D,bf16", [(128, False), (64, True), (128, True)])
+def test_attn_oracle_dims_and_bf16(D, bf16):
+    """Head dim 128 and bf16 (p and o rounded to nearest even) against exact
+    float64 attention of the same decoded inputs."""
+    import torch
+    rng = np.random.default_rng(D + bf16)
+    x = [torch.from_numpy((rng.standard_normal((1, 2, 256, D)) * 0.5).astype(np.float32))
+         for _ in range(3)]
+    tdt = torch.bfloat16 if bf16 else torch.float16
+    bits = [t.to(tdt).view(torch.int16).numpy().view(np.uint16) for t in x]
+    qf, kf, vf = (torch.from_numpy(b.view(np.int16)).view(tdt).double().numpy() for b in bits)
+    o, M = oracle.attn_fwd(*bits, sm_scale=0.5, causal=True, block=(128, 64),
+                           dtype=oracle.BF16 if bf16 else oracle.F16)
+    got = torch.from_numpy(o.view(np.int16)).view(tdt).double().numpy()
+    N = 256
+    s = np.einsum("zhmd,zhnd->zhmn", qf, kf) * 0.5
+    s = np.where(np.tril(np.ones((N, N))) > 0, s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    ref = (p / p.sum(-1, keepdims=True)) @ vf
+    tol = 2 ** -6 if bf16 else 2 ** -9  # p and o rounded to bf16 (8 bits) or fp16 (11)
+    assert np.abs(got - ref).max() < tol, np.abs(got - ref).max()
+
+
 def test_attn_loop_split_is_exact():
     q, k, v = rand_qkv(1, 2, 512, 64, seed=3, std=1.0)
     for block in ((64, 32), (128, 64)):
@@ -118,9 +141,10 @@ def test_attn_plan():
         with pytest.raises(tx.TxError) as e:
             tx.attn_plan(**a)
         return e.value.code
-    assert err(head_dim=128) == tx.ERR_UNSUPPORTED
+    assert err(head_dim=96) == tx.ERR_UNSUPPORTED
     assert err(N_CTX=200) == tx.ERR_UNSUPPORTED
-    assert err(dtype=tx.BF16) == tx.ERR_UNSUPPORTED
+    assert err(dtype=tx.F32) == tx.ERR_UNSUPPORTED
+    assert tx.attn_plan(1, 1, 256, 128, True, 0.5, dtype=tx.BF16).desc.head_dim == 128
     assert err(block=(64, 32)) == tx.ERR_UNSUPPORTED
     assert err(Z=-1) == tx.ERR_INVALID
     assert err(sm_scale=float("nan")) == tx.ERR_INVALID

@@ -109,3 +109,37 @@ def test_attn_bench_shape_sampled_heads(gpu, causal):
         ro, rM = oracle.attn_fwd(*sub, sm_scale=0.5, causal=causal, block=(128, 64))
         got = from_device(o[zi:zi + 1, hi:hi + 1].contiguous().view(torch.int16)).view(np.uint16)
         check(got, from_device(M[zi, hi]), ro, rM, f"attn 4x32x4096 head ({zi},{hi})")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("D,bf16,Z,H,N,layout", [(128, False, 2, 3, 384, "bhnd"),
+                                                 (64, True, 2, 3, 384, "bhnd"),
+                                                 (128, True, 1, 2, 1024, "bnhd")])
+def test_attn_head_dim_128_and_bf16(gpu, causal, D, bf16, Z, H, N, layout):
+    """Head dim 128 (256-byte K/V rows, their own swizzles) and bf16 (p and
+    o rounded to nearest even) against the oracle."""
+    import torch
+    say(f"attn D={D} bf16={bf16} Z={Z} H={H} N={N} causal={causal} {layout}")
+    rng = np.random.default_rng(D * 7 + N + causal + bf16)
+    tdt = torch.bfloat16 if bf16 else torch.float16
+    bits = [torch.from_numpy((rng.standard_normal((Z, H, N, D)) * 0.5).astype(np.float32))
+            .to(tdt).view(torch.int16).numpy().view(np.uint16) for _ in range(3)]
+    ts = []
+    for b in bits:
+        t = to_device(b, gpu).view(torch.int16).view(tdt)
+        if layout == "bnhd":
+            t = t.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+        ts.append(t)
+    o, M = tx.attention(*ts, causal, 0.7, return_lse=True)
+    torch.cuda.synchronize()
+    got = from_device(o.contiguous().view(torch.int16)).view(np.uint16)
+    ro, rM = oracle.attn_fwd(*bits, sm_scale=0.7, causal=causal, block=(128, 64),
+                             dtype=oracle.BF16 if bf16 else oracle.F16)
+    dec = lambda b: torch.from_numpy(b.view(np.int16)).view(tdt).double().numpy()
+    d = np.abs(dec(got) - dec(ro))
+    tol = 2.0 ** -6 if bf16 else 2.0 ** -8
+    assert np.isfinite(dec(got)).all()
+    assert d.max() <= tol, f"max |d o| {d.max():.3g}"
+    dm = np.abs(from_device(M).reshape(rM.shape).astype(np.float64) - rM)
+    assert dm.max() <= 1e-4 * max(1.0, np.abs(rM).max()), f"max |d M| {dm.max():.3g}"
+    say(f"attn D={D} bf16={bf16}: max|d o|={d.max():.3g} identical={np.mean(got == ro):.3f}")

@@ -694,13 +694,14 @@ extern "C" TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *p
     return fail(TX_ERR_INVALID, "causal must be 0 or 1");
   if (!(d.sm_scale == d.sm_scale))
     return fail(TX_ERR_INVALID, "sm_scale is NaN");
-  if (d.head_dim != txk::AttnFwd::D)
-    return fail(TX_ERR_UNSUPPORTED, "head_dim %d: the kernel is built for 64", d.head_dim);
-  if (d.dtype != TX_F16)
-    return fail(TX_ERR_UNSUPPORTED, "dtype %d: fp16 q/k/v/o are implemented", d.dtype);
-  if (d.block_m == 0) d.block_m = txk::AttnFwd::BM;
-  if (d.block_n == 0) d.block_n = txk::AttnFwd::BN;
-  if (d.block_m != txk::AttnFwd::BM || d.block_n != txk::AttnFwd::BN)
+  typedef txk::AttnFwd<64, false> AF; // block shape (the same for every head dim)
+  if (d.head_dim != 64 && d.head_dim != 128)
+    return fail(TX_ERR_UNSUPPORTED, "head_dim %d: 64 and 128 are implemented", d.head_dim);
+  if (d.dtype != TX_F16 && d.dtype != TX_BF16)
+    return fail(TX_ERR_UNSUPPORTED, "dtype %d: fp16 and bf16 q/k/v/o are implemented", d.dtype);
+  if (d.block_m == 0) d.block_m = AF::BM;
+  if (d.block_n == 0) d.block_n = AF::BN;
+  if (d.block_m != AF::BM || d.block_n != AF::BN)
     return fail(TX_ERR_UNSUPPORTED, "blocks %dx%d: 128x64 is implemented", d.block_m,
                 d.block_n);
   if (d.N_CTX % d.block_m)
@@ -723,7 +724,7 @@ extern "C" TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *p
   plan->qk_scale = d.sm_scale * 1.44269504f; // qk_scale = sm_scale; qk_scale *= 1.44269504
   plan->m_blocks = (int32_t)(d.N_CTX / d.block_m);
   plan->grid_x = (int32_t)programs;
-  plan->block_threads = txk::AttnFwd::NW * 64;
+  plan->block_threads = AF::NW * 64;
   return TX_OK;
 }
 
@@ -741,8 +742,9 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
        reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o)) & 15 ||
       reinterpret_cast<uintptr_t>(M) & 3)
     return fail(TX_ERR_INVALID, "q, k, v, o must be 16-byte aligned and M 4-byte aligned");
-  if (plan->block_threads != txk::AttnFwd::NW * 64 || d.block_m != txk::AttnFwd::BM ||
-      d.block_n != txk::AttnFwd::BN || d.head_dim != txk::AttnFwd::D ||
+  typedef txk::AttnFwd<64, false> AF;
+  if (plan->block_threads != AF::NW * 64 || d.block_m != AF::BM || d.block_n != AF::BN ||
+      (d.head_dim != 64 && d.head_dim != 128) || (d.dtype != TX_F16 && d.dtype != TX_BF16) ||
       plan->m_blocks != d.N_CTX / d.block_m || plan->grid_x != d.Z * d.H * plan->m_blocks)
     return fail(TX_ERR_INVALID, "plan launch shape does not match the attention kernel");
   if (!tx_device_available())
@@ -761,12 +763,15 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
   a.N_CTX = (int32_t)d.N_CTX;
   a.qk_scale = plan->qk_scale;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (d.causal)
-    hipLaunchKernelGGL(txk::attn_fwd_kernel<true>, dim3(plan->grid_x),
-                       dim3(plan->block_threads), 0, s, a);
-  else
-    hipLaunchKernelGGL(txk::attn_fwd_kernel<false>, dim3(plan->grid_x),
-                       dim3(plan->block_threads), 0, s, a);
+  typedef void (*AttnFn)(txk::AttnArgs);
+  // [causal][head_dim 128][bf16]
+  static const AttnFn kAttn[2][2][2] = {
+      {{txk::attn_fwd_kernel<false, 64, false>, txk::attn_fwd_kernel<false, 64, true>},
+       {txk::attn_fwd_kernel<false, 128, false>, txk::attn_fwd_kernel<false, 128, true>}},
+      {{txk::attn_fwd_kernel<true, 64, false>, txk::attn_fwd_kernel<true, 64, true>},
+       {txk::attn_fwd_kernel<true, 128, false>, txk::attn_fwd_kernel<true, 128, true>}}};
+  const AttnFn fn = kAttn[d.causal ? 1 : 0][d.head_dim == 128][d.dtype == TX_BF16];
+  hipLaunchKernelGGL(fn, dim3(plan->grid_x), dim3(plan->block_threads), 0, s, a);
   TX_HIP_CHECK(hipGetLastError());
   return TX_OK;
 }

@@ -1,6 +1,7 @@
 // Fused attention forward for gfx950: the forward of the fused-attention
 // tutorial (R:pass/LoopSplit/06-fused-attention.py:44-93, :181-239), fp16
-// q/k/v/o, HEAD_DIM 64, fp32 softmax statistics and accumulator.
+// (the tutorial's type) or bf16 q/k/v/o, HEAD_DIM 64 or 128, fp32 softmax
+// statistics and accumulator.
 //
 // A workgroup owns BM = 128 query rows of one (z, h): four waves of 32 rows.
 // Per K/V block of BN = 64 keys:
@@ -15,14 +16,15 @@
 //                    the S^T registers: MFMA slot s of lane group g is key
 //                    16 c + 8 (s/4) + 4 g + s%4, so V's rows are read in that
 //                    order and no value crosses lanes.
-// Staging: K and V blocks (8 KiB each) reach LDS by direct-to-LDS buffer
-// loads into two slots each, one barrier per block; loads run a block ahead
-// under the math (the pipeline is described at the kernel).  LDS layouts (rows of 128 bytes, 16-byte chunk c
-// of row r stored at):
-//   K: c ^ ((r >> 1) & 7)   the 16 rows a ds_read_b128 pass touches hit 16
-//                           different bank groups;
-//   V: c ^ (4 ((r >> 1) & 1)) the 4 rows x 64 bytes a ds_read_b64_tr_b16
-//                           pass touches cover all 64 banks once.
+// Staging: K and V blocks (8 or 16 KiB each) reach LDS by direct-to-LDS
+// buffer loads into two slots each, one barrier per block; loads run a block
+// ahead under the math (the pipeline is described at the kernel).  LDS
+// layouts (rows of 2 HEAD_DIM bytes, 16-byte chunk c of row r stored at):
+//   K: c ^ ((r >> 1) & 7) (128-byte rows), c ^ (r & 15) (256-byte rows): the
+//      16 rows a ds_read_b128 pass touches hit 16 different bank groups;
+//   V: c ^ (4 ((r >> 1) & 1)) (128-byte rows), c ^ (4 (r & 3)) (256-byte
+//      rows): the 4 rows x 64 bytes a ds_read_b64_tr_b16 pass touches cover
+//      all 64 banks once.
 // The K/V loop runs in LoopSplit form: keys [0, causal_start) unmasked, then
 // the on-band blocks [causal_start, causal_start + BM) masked; causal_start =
 // start_m * BM, or N_CTX without the causal mask.  Blocks past the diagonal
@@ -45,15 +47,31 @@ struct AttnArgs {
   float qk_scale;
 };
 
-struct AttnFwd {
-  static constexpr int BM = 128, BN = 64, D = 64, NW = 4;
-  static constexpr int ROW = D * 2;          // bytes per K/V row
-  static constexpr int TILE = BN * ROW;      // 8 KiB
-  static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 2
+template <int HD, bool BF> struct AttnFwd {
+  static constexpr int BM = 128, BN = 64, D = HD, NW = 4;
+  static constexpr int ROW = D * 2;            // bytes per K/V row
+  static constexpr int TILE = BN * ROW;        // 8 / 16 KiB
+  static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 2 / 4
+  static constexpr int CPR = ROW / 16;         // 16-byte chunks per row: 8 / 16
   static constexpr uint32_t kOOB = 0x80000000u;
-  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  static_assert(D == 64 || D == 128, "head dims 64 and 128");
+  // 16-bit element vectors; BF: bf16, else fp16
+  typedef typename std::conditional<BF, __bf16, _Float16>::type elt;
+  typedef elt h8 __attribute__((ext_vector_type(8)));
+  typedef elt h4 __attribute__((ext_vector_type(4)));
   typedef float f16v __attribute__((ext_vector_type(16)));
+
+  __device__ __forceinline__ static f16v mfma(const h8 &a, const h8 &b, const f16v &c) {
+    if constexpr (BF)
+      return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    else
+      return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  // swizzles of the 16-byte chunk index (see the layouts above)
+  __device__ __forceinline__ static int kswz(int r) { return D == 64 ? (r >> 1) & 7 : r & 15; }
+  __device__ __forceinline__ static int vswz(int r) {
+    return D == 64 ? 4 * ((r >> 1) & 1) : 4 * (r & 3);
+  }
 
   __device__ __forceinline__ static void dma16(uint32_t voff, const i32x4_t &rsrc, uint32_t soff,
                                                uint32_t lds) {
@@ -63,16 +81,17 @@ struct AttnFwd {
   }
 
   // Per-lane source byte offsets of the wave's DMA loads (relative to the
-  // block's first row): load u of wave w fills LDS rows 8 (2w + u) .. +7,
-  // lane i row 8 (2w + u) + i/8 at chunk position i%8, which holds chunk
-  // i%8 ^ swizzle(row) of the source row (V_SWZ: V's layout, else K's).
+  // block's first row): load u of wave w fills 1 KiB of LDS, rows
+  // (64/CPR) (DMA w + u) .., lane i row .. + i/CPR at chunk position i%CPR,
+  // which holds chunk i%CPR ^ swizzle(row) of the source row (V_SWZ: V's
+  // layout, else K's).
   template <bool V_SWZ>
   __device__ __forceinline__ static void dma_offsets(int wave, int64_t sm, uint32_t (&o)[DMA]) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int u = 0; u < DMA; ++u) {
-      const int row = 8 * (DMA * wave + u) + (lane >> 3), pos = lane & 7;
-      const int c = V_SWZ ? pos ^ (4 * ((row >> 1) & 1)) : pos ^ ((row >> 1) & 7);
+      const int row = (64 / CPR) * (DMA * wave + u) + lane / CPR, pos = lane % CPR;
+      const int c = pos ^ (V_SWZ ? vswz(row) : kswz(row));
       o[u] = (uint32_t)((row * sm + c * 8) * 2);
     }
   }
@@ -93,8 +112,8 @@ struct AttnFwd {
   //     swizzle does not depend on b, so kb[c] + 32 b ROW;
   //   V^T, dim block bd, key chunk c: two transposed reads (keys 16 c +
   //     4 (l/32) + (L/4) and +8 for lane group l/16 and L = l%16); the
-  //     swizzle term (key >> 1) & 1 depends on L only, so vb[bd] + 16 c ROW
-  //     (+ 8 ROW for the second read).
+  //     swizzle term depends on key bits 0-1 only, which L fixes, so
+  //     vb[bd] + 16 c ROW (+ 8 ROW for the second read).
   struct Bases {
     uint32_t k[D / 16], v[D / 32];
   };
@@ -103,12 +122,12 @@ struct AttnFwd {
     const int G = lane >> 4, L = lane & 15, r = lane & 31;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c)
-      bs.k[c] = k_lds + r * ROW + (((2 * c + (lane >> 5)) ^ ((r >> 1) & 7)) << 4);
+      bs.k[c] = k_lds + r * ROW + (((2 * c + (lane >> 5)) ^ kswz(r)) << 4);
 #pragma unroll
     for (int bd = 0; bd < D / 32; ++bd) {
       const int d = 32 * bd + 16 * (G & 1) + 4 * (L & 3);
       const int k0 = 4 * (G >> 1) + (L >> 2);
-      bs.v[bd] = v_lds + k0 * ROW + (((d >> 3) ^ (4 * ((k0 >> 1) & 1))) << 4) + (d & 7) * 2;
+      bs.v[bd] = v_lds + k0 * ROW + (((d >> 3) ^ vswz(k0)) << 4) + (d & 7) * 2;
     }
   }
 
@@ -146,7 +165,7 @@ struct AttnFwd {
       s[b] = f16v{};
 #pragma unroll
       for (int c = 0; c < D / 16; ++c)
-        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[b][c], qf[c], s[b], 0, 0, 0);
+        s[b] = mfma(kf[b][c], qf[c], s[b]);
     }
   }
 
@@ -209,7 +228,7 @@ struct AttnFwd {
     for (int c = 0; c < BN / 16; ++c)
 #pragma unroll
       for (int t = 0; t < 8; ++t)
-        pf[c][t] = (_Float16)s[c / 2][8 * (c % 2) + t];
+        pf[c][t] = (elt)s[c / 2][8 * (c % 2) + t];
 #pragma unroll
     for (int bd = 0; bd < D / 32; ++bd)
 #pragma unroll
@@ -231,7 +250,7 @@ struct AttnFwd {
     for (int bd = 0; bd < D / 32; ++bd)
 #pragma unroll
       for (int c = 0; c < BN / 16; ++c)
-        acc[bd] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[bd][c], pf[c], acc[bd], 0, 0, 0);
+        acc[bd] = mfma(vf[bd][c], pf[c], acc[bd]);
   }
 };
 
@@ -242,9 +261,9 @@ struct AttnFwd {
 // V_{j+1} (into V_{j-1}'s slot), and its closing barrier makes them visible.
 // Block j uses K slot j%2 and V slot j%2; the loop advances two blocks per
 // trip so that slots are constants (both segments have even trip counts).
-template <bool CAUSAL>
+template <bool CAUSAL, int HD, bool BF>
 __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
-  typedef AttnFwd A;
+  typedef AttnFwd<HD, BF> A;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[4 * A::TILE];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -261,18 +280,18 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
   const int m = start_m * A::BM + 32 * wave + (lane & 31);
 
   // Q rows as MFMA B operands: dims 16 c + 8 g .. +7 of row m.
-  A::h8 qf[A::D / 16];
+  typename A::h8 qf[A::D / 16];
 #pragma unroll
   for (int c = 0; c < A::D / 16; ++c)
-    qf[c] = *reinterpret_cast<const A::h8 *>(Qh + (int64_t)m * p.q_sm + 16 * c + 8 * g);
+    qf[c] = *reinterpret_cast<const typename A::h8 *>(Qh + (int64_t)m * p.q_sm + 16 * c + 8 * g);
 
   const i32x4_t rk = make_rsrc(Kh, (uint32_t)(((int64_t)(p.N_CTX - 1) * p.k_sm + A::D) * 2));
   const i32x4_t rv = make_rsrc(Vh, (uint32_t)(((int64_t)(p.N_CTX - 1) * p.v_sm + A::D) * 2));
   uint32_t ko[A::DMA], vo[A::DMA];
-  A::dma_offsets<false>(wave, p.k_sm, ko);
-  A::dma_offsets<true>(wave, p.v_sm, vo);
+  A::template dma_offsets<false>(wave, p.k_sm, ko);
+  A::template dma_offsets<true>(wave, p.v_sm, vo);
   const uint32_t k_lds = lds_addr(smem), v_lds = k_lds + 2 * A::TILE;
-  A::Bases bs;
+  typename A::Bases bs;
   A::bases(k_lds, v_lds, bs);
 
   // LoopSplit form of the K/V loop (keys [0, N_CTX), predicate start_n >=
@@ -283,17 +302,17 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
   const int n_end = CAUSAL ? (causal_start + A::BM) / A::BN : n_main;
 
   float m_i = -INFINITY, l_i = 1.0f;
-  A::f16v acc[A::D / 32], s[A::BN / 32];
+  typename A::f16v acc[A::D / 32], s[A::BN / 32];
 #pragma unroll
   for (int bd = 0; bd < A::D / 32; ++bd)
-    acc[bd] = A::f16v{};
+    acc[bd] = typename A::f16v{};
 
   A::issue(rk, ko, p.k_sm, 0, k_lds, wave);
   A::issue(rv, vo, p.v_sm, 0, v_lds, wave);
   A::issue(rk, ko, p.k_sm, 1, k_lds + A::TILE, wave); // n_end >= 2
   __builtin_amdgcn_s_waitcnt(0x7 << 4);               // vmcnt(0)
   __syncthreads();
-  A::qk<0>(bs, qf, s);
+  A::template qk<0>(bs, qf, s);
   __syncthreads(); // K slot 0 is refilled by iteration 0
 
   auto iter = [&](int j, auto mask, auto slot) {
@@ -303,11 +322,11 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
       A::issue(rk, ko, p.k_sm, j + 2, k_lds + SL * A::TILE, wave);
     if (j + 1 < n_end)
       A::issue(rv, vo, p.v_sm, j + 1, v_lds + (1 - SL) * A::TILE, wave);
-    A::f16v sn[A::BN / 32];
-    A::qk<1 - SL>(bs, qf, sn); // S_{j+1} (a stale slot after the last block: unused)
-    A::h8 pf[A::BN / 16];
-    A::softmax<MASK>(s, j * A::BN, m, p.qk_scale, acc, m_i, l_i, pf);
-    A::pv<SL>(bs, pf, acc);
+    typename A::f16v sn[A::BN / 32];
+    A::template qk<1 - SL>(bs, qf, sn); // S_{j+1} (a stale slot after the last block: unused)
+    typename A::h8 pf[A::BN / 16];
+    A::template softmax<MASK>(s, j * A::BN, m, p.qk_scale, acc, m_i, l_i, pf);
+    A::template pv<SL>(bs, pf, acc);
 #pragma unroll
     for (int b2 = 0; b2 < A::BN / 32; ++b2)
       s[b2] = sn[b2];
@@ -330,11 +349,11 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
   for (int bd = 0; bd < A::D / 32; ++bd)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      A::h4 o;
+      typename A::h4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        o[e] = (_Float16)(acc[bd][4 * q + e] / l_i);
-      *reinterpret_cast<A::h4 *>(Oh + 32 * bd + 8 * q + 4 * g) = o;
+        o[e] = (typename A::elt)(acc[bd][4 * q + e] / l_i);
+      *reinterpret_cast<typename A::h4 *>(Oh + 32 * bd + 8 * q + 4 * g) = o;
     }
   if (g == 0)
     p.M[(int64_t)hz * p.N_CTX + m] = m_i + __builtin_log2f(l_i);

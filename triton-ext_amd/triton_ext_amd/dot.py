@@ -183,8 +183,8 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
 def attention(q, k, v, causal, sm_scale, return_lse=False, plan=None, stream=None):
     """Forward of the fused-attention tutorial's `attention(q, k, v, causal,
     sm_scale)` (R:pass/LoopSplit/06-fused-attention.py:583-640) on the
-    MI355X kernel: q, k, v fp16 [Z, H, N_CTX, HEAD_DIM] with the head dim
-    contiguous.  Returns o (and M, the base-2 logsumexp [Z, H, N_CTX] the
+    MI355X kernel: q, k, v fp16 (or bf16) [Z, H, N_CTX, HEAD_DIM], head dim
+    64 or 128 and contiguous.  Returns o (and M, the base-2 logsumexp [Z, H, N_CTX] the
     tutorial saves for its backward, with return_lse=True).  Shape checks
     follow the tutorial's asserts.
     """
@@ -195,9 +195,12 @@ def attention(q, k, v, causal, sm_scale, return_lse=False, plan=None, stream=Non
     HEAD_DIM = q.shape[-1]
     if HEAD_DIM not in {16, 32, 64, 128, 256}:
         raise ValueError(f"HEAD_DIM {HEAD_DIM} not in {{16, 32, 64, 128, 256}}")
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        raise NotImplementedError(f"q: fp16 and bf16 are implemented, got {q.dtype}")
+    for t, nm in ((k, "k"), (v, "v")):
+        if t.dtype != q.dtype:
+            raise ValueError(f"{nm} is {t.dtype}, q is {q.dtype}")
     for t, nm in ((q, "q"), (k, "k"), (v, "v")):
-        if t.dtype != torch.float16:
-            raise NotImplementedError(f"{nm}: fp16 is implemented, got {t.dtype}")
         if t.stride(3) != 1:
             raise ValueError(f"{nm}: the head dimension must be contiguous")
     Z, H, N = q.shape[:3]
@@ -206,7 +209,8 @@ def attention(q, k, v, causal, sm_scale, return_lse=False, plan=None, stream=Non
     if plan is None:
         st = {nm: (t.stride(0), t.stride(1), t.stride(2)) for nm, t in
               (("q", q), ("k", k), ("v", v), ("o", o))}
-        plan = capi.attn_plan(Z, H, N, HEAD_DIM, causal, sm_scale, strides=st)
+        dt = capi.BF16 if q.dtype == torch.bfloat16 else capi.F16
+        plan = capi.attn_plan(Z, H, N, HEAD_DIM, causal, sm_scale, dtype=dt, strides=st)
     if stream is None:
         stream = torch.cuda.current_stream(q.device).cuda_stream
     capi.check(capi.load().tx_attn_fwd_launch(ctypes.byref(plan), q.data_ptr(), k.data_ptr(),
