@@ -145,10 +145,19 @@ template <int HD, bool BF> struct AttnFwd {
     return __builtin_bit_cast(h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   }
 
+  // Row statistics across the lane pair (l, l ^ 32): v_permlane32_swap hands
+  // each lane both halves' values ([lo, lo] and [hi, hi]) without an LDS
+  // round trip, and both lanes form the same result.
   __device__ __forceinline__ static float xmax(float v) {
-    return fmaxf(v, __shfl_xor(v, 32, 64));
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
   }
-  __device__ __forceinline__ static float xsum(float v) { return v + __shfl_xor(v, 32, 64); }
+  __device__ __forceinline__ static float xsum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
 
   // S^T block of the keys in K slot SLOT: lane holds query row l%32.
   template <int SLOT>
