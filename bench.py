@@ -48,7 +48,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
-                    help="secondary workloads to run, comma-separated: vendor, tail, w8a8 (or "
+                    help="secondary workloads to run, comma-separated: c1, vendor, tail, w8a8 (or "
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256), fp8, kmajor, mx (or mxfp8, mxfp4, "
                          "mxfp8_4096, mxfp8_8192, mxfp4_4096, mxfp4_8192), attn (or attn_1024, attn_4096, "
                          "attn_16384; attn_d128 for head dim 128; attn_vendor adds torch sdpa beside each) "
@@ -168,6 +168,24 @@ def bench_bf16(tx, dev, M, N, K, steps, warmup, seed=1):
                           k_main_steps=p.k_main_steps, k_tail=p.k_tail, m_edge=p.m_edge,
                           n_edge=p.n_edge, intensity=round(p.intensity, 1),
                           bound="mfma" if p.bound == tx.BOUND_MFMA else "hbm")), (a, b, c)
+
+
+def bench_c1(tx, dev, steps, warmup, seed=1):
+    """BASELINE configs[0], the reference's CPU-runnable case: fp16 512^3 with
+    BLOCK 64x64x32 and fp32 C (a latency-bound launch: 64 small tiles)."""
+    import torch
+    M = N = K = 512
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    a = (torch.randn((M, K), generator=g, device=dev) / math.sqrt(K)).to(torch.float16)
+    b = (torch.randn((K, N), generator=g, device=dev) / math.sqrt(K)).to(torch.float16)
+    c = torch.empty((M, N), dtype=torch.float32, device=dev)
+    run = Launcher(tx, a, b, c, block=(64, 64, 32))
+    ms = time_back_to_back(run, max(steps, 200), warmup)
+    flops = 2.0 * M * N * K
+    return dict(workload="fp16 512x512x512, BLOCK 64x64x32, fp32 C (BASELINE configs[0])", ms=ms,
+                tflops=flops / ms / 1e9, frac=flops / ms / 1e-3 / PEAK_BF16,
+                plan=dict(tile=[64, 64, 32], grid=run.plan.grid_x))
 
 
 def bench_bf16_kmajor(tx, dev, M, N, K, steps, warmup, seed=1):
@@ -398,6 +416,11 @@ def main():
         r = bench_vendor_bf16(dev, M, N, K, args.steps, args.warmup)
         secondary.append(r)
         print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    if want("c1"):
+        r = bench_c1(tx, dev, args.steps, args.warmup)
+        secondary.append(r)
+        print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us, {r['tflops']:.1f} TFLOP/s",
+              file=sys.stderr, flush=True)
     if want("kmajor"):
         r = bench_bf16_kmajor(tx, dev, M, N, K, args.steps, args.warmup)
         secondary.append(r)
