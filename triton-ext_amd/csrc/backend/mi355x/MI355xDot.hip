@@ -564,7 +564,12 @@ int launchGemm(const tx_dot_plan &plan, const void *A, const void *B, void *C,
     const char *e = std::getenv("TX_GROUP_M"); // tuning override
     return e ? std::atoi(e) : 0;
   }();
-  const int gm = group_env > 0 ? group_env : 4;
+  // Tile rows per group of the XCD-aware tile order: 4, except 2 on the 8-bit
+  // tile once K spans 8192 bytes or more (a sweep of 1..32: mxfp8 8192^3 ran
+  // 2365 TFLOP/s at 2 against 1930 at 4; 4096^3, C5 (K = 7168) and mxfp4
+  // 8192^3 (K = 4096 bytes) were as fast or faster at 4).
+  const int64_t kbytes = d.K * tx_dtype_bits(d.a_type) / 8;
+  const int gm = group_env > 0 ? group_env : (c.dma == 5 && kbytes >= 8192 ? 2 : 4);
   a.group_m = plan.m_tiles < gm ? plan.m_tiles : gm;
   a.sa_ld = (int32_t)(mx ? d.K / 32 : cdiv(d.K, 128));
   a.sb_ld = (int32_t)cdiv(d.N, 128);
