@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
                     help="secondary workloads to run, comma-separated: c1, vendor, tail, w8a8 (or "
-                         "w8a8_1, w8a8_16, w8a8_64, w8a8_256), fp8, kmajor, mx (or mxfp8, mxfp4, "
+                         "w8a8_1, w8a8_16, w8a8_64, w8a8_256), int8, fp8, kmajor, mx (or mxfp8, mxfp4, "
                          "mxfp8_4096, mxfp8_8192, mxfp4_4096, mxfp4_8192), attn (or attn_1024, attn_4096, "
                          "attn_16384; attn_d128 for head dim 128; attn_vendor adds torch sdpa beside each) "
                          "(default: all); "
@@ -352,6 +352,21 @@ def bench_vendor_attn(dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9
                 frac=flops / ms / 1e-3 / PEAK_BF16)
 
 
+def bench_int8(tx, dev, M, N, K, steps, warmup, seed=4):
+    """int8 x int8 -> int32 tt.dot (no scales) on the 256x256x128 8-bit tile."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    a = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+    b = torch.randint(-127, 128, (K, N), generator=g, device=dev, dtype=torch.int8)
+    c = torch.empty((M, N), dtype=torch.int32, device=dev)
+    run = Launcher(tx, a, b, c)
+    ms = time_back_to_back(run, steps, warmup)
+    ops = 2.0 * M * N * K
+    return dict(workload=f"int8 {M}x{N}x{K}, int32 C", ms=ms, tops=ops / ms / 1e9,
+                frac=ops / ms / 1e-3 / PEAK_I8)
+
+
 def cpu_baseline(a, b, c, M, N, K, block):
     """Oracle on the host cores over the full bf16 workload; also checks the GPU output."""
     import numpy as np
@@ -438,6 +453,11 @@ def main():
             secondary.append(r)
             print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us, {r['gbps']:.0f} GB/s "
                   f"({100 * r['frac_hbm']:.1f}% HBM)", file=sys.stderr, flush=True)
+    if want("int8"):
+        r = bench_int8(tx, dev, 4096, 4096, 4096, args.steps, args.warmup)
+        secondary.append(r)
+        print(f"# {r['workload']}: {r['tops']:.1f} TOP/s ({100 * r['frac']:.1f}% of 5033)",
+              file=sys.stderr, flush=True)
     if want("fp8"):
         r = bench_fp8(tx, dev, 2048, 7168, 7168, args.steps, args.warmup)
         secondary.append(r)
