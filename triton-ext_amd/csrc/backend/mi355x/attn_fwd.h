@@ -333,9 +333,15 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
       A::issue(rv, vo, p.v_sm, j + 1, v_lds + (1 - SL) * A::TILE, wave);
     typename A::f16v sn[A::BN / 32];
     A::template qk<1 - SL>(bs, qf, sn); // S_{j+1} (a stale slot after the last block: unused)
-    typename A::h8 pf[A::BN / 16];
-    A::template softmax<MASK>(s, j * A::BN, m, p.qk_scale, acc, m_i, l_i, pf);
-    A::template pv<SL>(bs, pf, acc);
+    // On-band blocks whose keys all lie past this wave's 32 rows add exactly
+    // nothing (p = 0, alpha = 1, as for the blocks past the diagonal): the
+    // wave skips their softmax and P V.
+    const bool live = !MASK || j * A::BN <= start_m * A::BM + 32 * wave + 31;
+    if (live) {
+      typename A::h8 pf[A::BN / 16];
+      A::template softmax<MASK>(s, j * A::BN, m, p.qk_scale, acc, m_i, l_i, pf);
+      A::template pv<SL>(bs, pf, acc);
+    }
 #pragma unroll
     for (int b2 = 0; b2 < A::BN / 32; ++b2)
       s[b2] = sn[b2];

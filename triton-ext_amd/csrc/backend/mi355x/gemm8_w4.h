@@ -1,7 +1,8 @@
-// 8-bit operand (fp8 e4m3 / int8) 256x256x128 tile kernel for gfx950, eight
-// waves of 128x64 (two per SIMD): C[M,N] = epilogue(A[M,K] . B[K,N]), all
-// row-major.  A wave's 128 fp32/int32 accumulators stay in arch VGPRs, where
-// the per-step block-scale FMA can reach them.
+// 8-bit operand (int8; fp8 e4m3 / e5m2 in any mix; with MX scales also fp4
+// e2m1, two per byte) 256x256x128-byte tile kernel for gfx950, eight waves of
+// 128x64 (two per SIMD): C[M,N] = epilogue(A[M,K] . B[K,N]), all row-major.
+// A wave's 128 fp32/int32 accumulators stay in arch VGPRs, where the
+// per-step block-scale FMA can reach them.
 //
 // One K step is 128: one scale group of the fp8 block-scaled dot, and one
 // v_mfma_f32_16x16x128_f8f6f4 (or two v_mfma_i32_16x16x64_i8) per 16x16 block.
