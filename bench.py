@@ -51,7 +51,8 @@ def parse():
                     help="secondary workloads to run, comma-separated: c1, vendor, tail, w8a8 (or "
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256), int8, fp8, kmajor, mx (or mxfp8, mxfp4, "
                          "mxfp8_4096, mxfp8_8192, mxfp4_4096, mxfp4_8192), attn (or attn_1024, attn_4096, "
-                         "attn_16384; attn_d128 for head dim 128; attn_vendor adds torch sdpa beside each) "
+                         "attn_16384; attn_fp8 or attn_fp8_<N> for e5m2; attn_d128 for head dim 128; "
+                         "attn_vendor adds torch sdpa beside each) "
                          "(default: all); "
                          "the bf16 "
                          "headline always runs")
@@ -313,12 +314,17 @@ def bench_attn(tx, dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9, d
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     dtype = dtype or torch.float16
-    q, k, v = (torch.randn((Z, H, N_CTX, D), generator=g, device=dev, dtype=dtype)
-               for _ in range(3))
-    o = torch.empty_like(q)
+    fp8 = dtype == torch.float8_e5m2
+    # the fp8 provider (:774-779): randn fp16 cast to e5m2, v stored key-contiguous
+    q, k, v = (torch.randn((Z, H, N_CTX, D), generator=g, device=dev,
+                           dtype=torch.float16 if fp8 else dtype).to(dtype) for _ in range(3))
+    if fp8:
+        v = v.permute(0, 1, 3, 2).contiguous().permute(0, 1, 3, 2)
+    o = torch.empty_like(q, memory_format=torch.contiguous_format)
     M = torch.empty((Z, H, N_CTX), device=dev, dtype=torch.float32)
     p = tx.attn_plan(Z, H, N_CTX, D, causal, 1.3,
-                     dtype=tx.BF16 if dtype == torch.bfloat16 else tx.F16)
+                     dtype=tx.F8E5M2 if fp8 else tx.BF16 if dtype == torch.bfloat16 else tx.F16,
+                     strides={"v": (v.stride(0), v.stride(1), v.stride(3))} if fp8 else None)
     L = tx.load()
     args = (ctypes.byref(p), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
             M.data_ptr(), torch.cuda.current_stream().cuda_stream)
@@ -328,10 +334,11 @@ def bench_attn(tx, dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9, d
         if rc != 0:
             raise RuntimeError(L.tx_get_last_error().decode())
     ms = time_back_to_back(run, steps, warmup)
-    tn = "bf16" if dtype == torch.bfloat16 else "fp16"
+    tn = "fp8 e5m2" if fp8 else "bf16" if dtype == torch.bfloat16 else "fp16"
+    peak = PEAK_I8 if fp8 else PEAK_BF16  # fp8 MFMA peak = int8's 5.0 P
     return dict(workload=f"fused attention fwd {tn} Z={Z} H={H} N_CTX={N_CTX} D={D} "
                          f"causal={causal}", ms=ms, tflops=p.flops / ms / 1e9,
-                frac=p.flops / ms / 1e-3 / PEAK_BF16)
+                frac=p.flops / ms / 1e-3 / peak)
 
 
 def bench_vendor_attn(dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9):
@@ -484,6 +491,15 @@ def main():
                     secondary.append(r)
                     print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr,
                           flush=True)
+
+    for n in (1024, 4096, 16384):  # the tutorial's "triton-fp8" provider
+        if want("attn_fp8") or want(f"attn_fp8_{n}"):
+            for causal in (True, False):
+                r = bench_attn(tx, dev, n, causal, args.steps, args.warmup,
+                               dtype=torch.float8_e5m2)
+                secondary.append(r)
+                print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s "
+                      f"({100 * r['frac']:.1f}% of fp8 peak)", file=sys.stderr, flush=True)
 
     if want("attn_d128"):  # head dim 128 (beyond the tutorial's 64)
         for causal in (True, False):

@@ -30,6 +30,12 @@
  * the given element strides; M is fp32 [Z * H][N_CTX] (the tutorial's
  * logsumexp in base 2, saved for the backward).  All device pointers; errors
  * by return code and tx_get_last_error() (tx_dot.h).
+ *
+ * dtype TX_F8E5M2 is the tutorial's fp8 provider (:774-779, :81-82): q, k, o
+ * e5m2 [Z][H][N_CTX][HEAD_DIM] as above; v e5m2 stored key-contiguous, as
+ * v.permute(0, 1, 3, 2).contiguous().permute(0, 1, 3, 2) leaves it, i.e.
+ * [Z][H][HEAD_DIM][N_CTX] with v_sm the stride between head-dim rows
+ * (default N_CTX); p and o are rounded to e5m2 to nearest even.
  */
 #ifndef TRITON_EXT_AMD_TX_ATTN_H
 #define TRITON_EXT_AMD_TX_ATTN_H
@@ -43,10 +49,11 @@ extern "C" {
 typedef struct tx_attn_desc {
   int64_t Z, H, N_CTX;
   int32_t head_dim; /* 64 or 128 */
-  int32_t dtype;    /* TX_F16 (the tutorial's) or TX_BF16 for q, k, v and o */
+  int32_t dtype;    /* TX_F16 (the tutorial's), TX_BF16 or TX_F8E5M2 for q, k, v, o */
   int32_t causal;   /* 0 or 1 */
   float sm_scale;
-  /* element strides (batch, head, row) of q, k, v, o; 0 = packed */
+  /* element strides (batch, head, row) of q, k, v, o; 0 = packed; each a
+   * multiple of 16 bytes (e5m2 v: (batch, head, head-dim row)) */
   int64_t q_sz, q_sh, q_sm;
   int64_t k_sz, k_sh, k_sm;
   int64_t v_sz, v_sh, v_sm;
@@ -65,7 +72,7 @@ typedef struct tx_attn_plan {
 } tx_attn_plan;
 
 /* Validate `desc` and fill `plan`.  TX_ERR_UNSUPPORTED unless head_dim is
- * 64 or 128, dtype TX_F16 or TX_BF16 and N_CTX a multiple of 128 (the
+ * 64 or 128, dtype TX_F16, TX_BF16 or TX_F8E5M2 and N_CTX a multiple of 128 (the
  * tutorial's block pointers assume whole blocks).  p is rounded to q's type
  * to nearest even before p @ v, as compiled Triton does. */
 TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *plan);

@@ -25,7 +25,7 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 F32, F16, BF16, I8, F8E4M3, I32, F8E5M2, F4E2M1 = 0, 1, 2, 3, 4, 5, 6, 7
 E8M0 = -1  # scale codec selector of mx_decode
 SCALE_NONE, SCALE_ROWCOL, SCALE_BLOCK128 = 0, 1, 2
-ROUND_RTZ, ROUND_RNE = 0, 1
+ROUND_RTZ, ROUND_RNE, ROUND_INTERP = 0, 1, 2
 
 _lib = None
 
@@ -42,7 +42,7 @@ def lib():
         L.oracle_tiled_dot.restype = i32
         L.oracle_tiled_dot.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64,
                                        i32, i32, i32, i32, i32, i32, i32, i32, i64, i64, i32]
-        for name in ("or_f32_to_bf16_array",):
+        for name in ("or_f32_to_bf16_array", "or_f32_to_e5m2_array"):
             getattr(L, name).argtypes = [vp, vp, i64, i32]
         for name in ("or_bf16_to_f32_array", "or_f32_to_f16_array", "or_f16_to_f32_array",
                      "or_f32_to_e4m3_array", "or_e4m3_to_f32_array"):
@@ -185,22 +185,33 @@ def dot_scaled(a, sa, a_fmt, b, sb, b_fmt, *, K, c_type=F32, round_mode=ROUND_RN
     return out
 
 
+def f32_to_e5m2(x, mode=ROUND_RNE):
+    """fp32 -> e5m2 codes (uint8): ROUND_RNE is IEEE round to nearest even
+    (overflow to inf); ROUND_INTERP the interpreter's converter."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.uint8)
+    lib().or_f32_to_e5m2_array(_ptr(x), _ptr(y), x.size, mode)
+    return y
+
+
 def attn_fwd(q, k, v, *, sm_scale, causal, block=(64, 32), mode=0, dtype=F16,
              round_mode=ROUND_RNE, nthreads=0):
     """The fused-attention tutorial's forward on the CPU.
 
-    q, k, v: uint16 fp16 (or bf16, dtype=BF16) bits [Z, H, N, D] (made
-    contiguous).  Returns (o as uint16 bits of the same type [Z, H, N, D],
-    M fp32 [Z * H, N]).  block =
+    q, k, v: uint16 fp16 (or bf16, dtype=BF16) bits, or uint8 e5m2 codes
+    (dtype=F8E5M2), [Z, H, N, D] (made contiguous).  Returns (o as bits of
+    the same type [Z, H, N, D], M fp32 [Z * H, N]).  block =
     (BLOCK_M, BLOCK_N); mode 0 the tutorial's split loop, 1 every block
-    masked, 2 mode 0 without the blocks past the diagonal.
+    masked, 2 mode 0 without the blocks past the diagonal.  round_mode: bf16
+    ROUND_RTZ / ROUND_RNE, e5m2 ROUND_RNE / ROUND_INTERP (fp16 is always RNE).
     """
-    q = np.ascontiguousarray(q, dtype=np.uint16)
-    k = np.ascontiguousarray(k, dtype=np.uint16)
-    v = np.ascontiguousarray(v, dtype=np.uint16)
+    et = np.uint8 if dtype == F8E5M2 else np.uint16
+    q = np.ascontiguousarray(q, dtype=et)
+    k = np.ascontiguousarray(k, dtype=et)
+    v = np.ascontiguousarray(v, dtype=et)
     Z, H, N, D = q.shape
     assert k.shape == q.shape and v.shape == q.shape
-    o = np.zeros(q.shape, dtype=np.uint16)
+    o = np.zeros(q.shape, dtype=et)
     M = np.zeros((Z * H, N), dtype=np.float32)
     rc = lib().oracle_attn_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(M), Z, H, N, D,
                                float(sm_scale), int(causal), block[0], block[1], mode, dtype,

@@ -63,7 +63,7 @@
 enum { OR_F32 = 0, OR_F16 = 1, OR_BF16 = 2, OR_I8 = 3, OR_F8E4M3 = 4, OR_I32 = 5,
        OR_F8E5M2 = 6, OR_F4E2M1 = 7 };
 enum { OR_SCALE_NONE = 0, OR_SCALE_ROWCOL = 1, OR_SCALE_BLOCK128 = 2 };
-enum { OR_ROUND_RTZ = 0, OR_ROUND_RNE = 1 };
+enum { OR_ROUND_RTZ = 0, OR_ROUND_RNE = 1, OR_ROUND_INTERP = 2 };
 
 /* ---------------- element codecs ---------------- */
 
@@ -150,6 +150,79 @@ uint8_t or_f32_to_e4m3(float f) {
   if (e > 8) /* cannot happen after saturation */
     e = 8, q = 14;
   return (uint8_t)(s | (uint8_t)((e + 7) << 3) | ((uint8_t)q - 8));
+}
+
+/* fp32 -> e5m2, round to nearest even (IEEE, as torch's float8_e5m2 and
+ * compiled Triton's p.to(tl.float8e5)): bias 15, quantum 2^-16 below 2^-14,
+ * |x| >= 61440 (the tie above the largest finite 57344) becomes inf. */
+uint8_t or_f32_to_e5m2(float f) {
+  uint8_t s = signbit(f) ? 0x80u : 0;
+  double a = fabs((double)f);
+  if (isnan(f))
+    return (uint8_t)(s | 0x7fu);
+  if (a >= 61440.0)
+    return (uint8_t)(s | 0x7cu);
+  if (a < ldexp(1.0, -14)) { /* subnormal: quantum 2^-16 */
+    double q = rint(a / ldexp(1.0, -16));
+    return (uint8_t)(s | (uint8_t)q); /* q == 4 is the min normal 0x04 */
+  }
+  int e;
+  frexp(a, &e);
+  e -= 1;
+  double q = rint(a / ldexp(1.0, e - 2)); /* 4..8 */
+  if (q >= 8.0) {
+    q /= 2;
+    e += 1;
+  }
+  return (uint8_t)(s | (uint8_t)((e + 15) << 2) | ((uint8_t)q - 4));
+}
+
+/* fp32 -> e5m2 as the interpreter's generic converter does it with
+ * rounding_mode RTNE (T:runtime/interpreter.py:202-263, reached from
+ * p.to(tl.float8e5) through create_fp_to_fp, :479-483; the cast picks RTNE
+ * for fp downcasts, T:language/semantic.py:807-809).  Its steps:
+ *   - a subnormal fp32 input is renormalised: exponent 1 - pos, significand
+ *     shifted left by pos (pos = 23 - index of its top set bit); zero keeps
+ *     significand 0 with exponent bias_in - bias_out;
+ *   - exponent clamped to [0, 31]; significand = top 2 bits + bit 20
+ *     (round half up, not to even), and a carry to 4 is ORed into the
+ *     exponent field, not added: (1.875..2) * 2^e with e + 15 odd gives
+ *     2^e;
+ *   - exponent 0 from a normal input (|x| < 2^-14): significand >> shift |
+ *     1 << (2 - shift), shift = 113 - exponent; numpy's shifts give 0 for
+ *     counts outside [0, bits), so the leading one vanishes for shift > 2;
+ *     a subnormal fp32 input keeps its renormalised 2 bits as the code.
+ */
+uint8_t or_f32_to_e5m2_interp(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint32_t sign = u >> 31;
+  const int32_t e_in = (int32_t)((u >> 23) & 0xffu);
+  uint32_t sig = u & 0x7fffffu;
+  int32_t exp = e_in;
+  if (e_in == 0) {
+    int pos = 0;
+    for (int i = 0; i < 23; ++i)
+      if ((sig >> i) & 1u)
+        pos = 23 - i;
+    exp = sig == 0 ? 127 - 15 : 1 - pos;
+    sig = (sig << pos) & 0x7fffffu;
+  }
+  int32_t eo = exp - 127 + 15;
+  eo = eo < 0 ? 0 : (eo > 31 ? 31 : eo);
+  uint32_t so = ((sig >> 21) & 3u) + ((sig >> 20) & 1u);
+  if (eo == 0 && e_in != 0) {
+    const int shift = (1 - 15) - (e_in - 127);
+    const uint32_t hi = shift < 32 ? so >> shift : 0u;
+    const uint32_t lead = (2 - shift >= 0) ? 1u << (2 - shift) : 0u;
+    so = (hi | lead) & 0xffu;
+  }
+  return (uint8_t)(((sign << 7) | ((uint32_t)eo << 2) | so) & 0xffu);
+}
+
+void or_f32_to_e5m2_array(const float *x, uint8_t *y, int64_t n, int mode) {
+  for (int64_t i = 0; i < n; ++i)
+    y[i] = mode == 2 ? or_f32_to_e5m2_interp(x[i]) : or_f32_to_e5m2(x[i]);
 }
 
 void or_f32_to_bf16_array(const float *x, uint16_t *y, int64_t n, int mode) {
@@ -312,23 +385,48 @@ int oracle_dot_scaled(const void *Av, const void *Bv, void *Cv, const uint8_t *s
  *   p = exp2(qk); l_ij = rowsum p (ascending); alpha = exp2(m_i - m_ij)
  *   l_i = l_i*alpha + l_ij; acc = acc*alpha; acc = (fp16(p) @ v) + acc
  *   m_i = m_ij;  finally M = m_i + log2(l_i), o = fp16(acc / l_i)
- * causal_start = start_m*BM (causal) or N.  dtype OR_F16 (the tutorial's)
- * or OR_BF16 for q, k, v, p and o; narrowing to bf16 uses round_mode
- * (compiled Triton rounds to nearest even; fp16 always does).  mode (tests only) 0: the
+ * causal_start = start_m*BM (causal) or N.  dtype OR_F16 (the tutorial's),
+ * OR_BF16 or OR_F8E5M2 (the tutorial's fp8 provider, :81-82, :774-779) for
+ * q, k, v, p and o; all of them [Z][H][N][D] packed here (the tutorial's fp8
+ * v is key-contiguous in memory; the values are the same).  Narrowing:
+ * fp16 to nearest even always; bf16 by round_mode RTZ (the interpreter) or
+ * RNE (compiled Triton); e5m2 by round_mode RNE (compiled Triton, IEEE) or
+ * OR_ROUND_INTERP (the interpreter's converter, or_f32_to_e5m2_interp).
+ * fp8 operands of the dots are widened exactly to fp16 first, as the
+ * interpreter's tl.dot does (T:runtime/interpreter.py:633-637).  mode (tests only) 0: the
  * tutorial's loop over all keys, split at causal_start; 1: the same loop
  * with every block in the masked form (no split); 2: mode 0 without the
  * blocks wholly past the diagonal.  Returns 0, or -1 on bad arguments.
  */
-int oracle_attn_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, uint16_t *o,
-                    float *M, int64_t Z, int64_t H, int64_t N, int D, float sm_scale,
-                    int causal, int BM, int BN, int mode, int dtype, int round_mode,
-                    int nthreads) {
+static float attn_ld(const void *base, int64_t i, int dtype) {
+  if (dtype == OR_F8E5M2)
+    return or_f16_to_f32((uint16_t)(((const uint8_t *)base)[i] << 8));
+  const uint16_t h = ((const uint16_t *)base)[i];
+  return dtype == OR_BF16 ? or_bf16_to_f32(h) : or_f16_to_f32(h);
+}
+
+/* Store f narrowed to dtype; returns the stored value widened back. */
+static float attn_st(void *base, int64_t i, float f, int dtype, int round_mode) {
+  if (dtype == OR_F8E5M2) {
+    const uint8_t c = round_mode == OR_ROUND_INTERP ? or_f32_to_e5m2_interp(f)
+                                                    : or_f32_to_e5m2(f);
+    if (base)
+      ((uint8_t *)base)[i] = c;
+    return or_f16_to_f32((uint16_t)(c << 8));
+  }
+  const uint16_t h = dtype == OR_BF16 ? or_f32_to_bf16(f, round_mode) : or_f32_to_f16(f);
+  if (base)
+    ((uint16_t *)base)[i] = h;
+  return dtype == OR_BF16 ? or_bf16_to_f32(h) : or_f16_to_f32(h);
+}
+
+int oracle_attn_fwd(const void *q, const void *k, const void *v, void *o, float *M, int64_t Z,
+                    int64_t H, int64_t N, int D, float sm_scale, int causal, int BM, int BN,
+                    int mode, int dtype, int round_mode, int nthreads) {
   if (Z < 0 || H < 0 || N < 0 || D <= 0 || BM <= 0 || BN <= 0 || N % BM || N % BN ||
-      (dtype != OR_F16 && dtype != OR_BF16))
+      (dtype != OR_F16 && dtype != OR_BF16 && dtype != OR_F8E5M2))
     return -1;
-  const int bf = dtype == OR_BF16;
-#define ATTN_LD(x) (bf ? or_bf16_to_f32(x) : or_f16_to_f32(x))
-#define ATTN_ST(f) (bf ? or_f32_to_bf16((f), round_mode) : or_f32_to_f16(f))
+#define ATTN_LD(x, i) attn_ld((x), (i), dtype)
   const float qk_scale = sm_scale * 1.44269504f;
   const int64_t programs = Z * H * (N / BM);
   int rc = 0;
@@ -358,7 +456,7 @@ int oracle_attn_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, uin
         const int64_t base = hz * N * D, m0 = start_m * BM;
         for (int i = 0; i < BM; ++i) {
           for (int d = 0; d < D; ++d) {
-            qb[i * D + d] = ATTN_LD(q[base + (m0 + i) * D + d]);
+            qb[i * D + d] = ATTN_LD(q, base + (m0 + i) * D + d);
             acc[i * D + d] = 0.f;
           }
           m_i[i] = -INFINITY;
@@ -373,7 +471,7 @@ int oracle_attn_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, uin
             for (int j = 0; j < BN; ++j) {
               float t = 0.f;
               for (int d = 0; d < D; ++d)
-                t += qb[i * D + d] * ATTN_LD(k[base + (n0 + j) * D + d]);
+                t += qb[i * D + d] * ATTN_LD(k, base + (n0 + j) * D + d);
               qk[i * BN + j] = t;
             }
           for (int i = 0; i < BM; ++i) {
@@ -413,11 +511,11 @@ int oracle_attn_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, uin
             for (int d = 0; d < D; ++d)
               acc[i * D + d] = acc[i * D + d] * alpha;
             for (int j = 0; j < BN; ++j) /* p.to(q's type) */
-              r[j] = ATTN_LD(ATTN_ST(r[j]));
+              r[j] = attn_st(NULL, 0, r[j], dtype, round_mode);
             for (int d = 0; d < D; ++d) {
               float t = 0.f;
               for (int j = 0; j < BN; ++j)
-                t += r[j] * ATTN_LD(v[base + (n0 + j) * D + d]);
+                t += r[j] * ATTN_LD(v, base + (n0 + j) * D + d);
               pv[i * D + d] = t;
             }
             for (int d = 0; d < D; ++d)
@@ -428,14 +526,13 @@ int oracle_attn_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, uin
         for (int i = 0; i < BM; ++i) {
           M[hz * N + m0 + i] = m_i[i] + log2f(l_i[i]);
           for (int d = 0; d < D; ++d)
-            o[base + (m0 + i) * D + d] = ATTN_ST(acc[i * D + d] / l_i[i]);
+            attn_st(o, base + (m0 + i) * D + d, acc[i * D + d] / l_i[i], dtype, round_mode);
         }
       }
     }
     free(qb); free(acc); free(qk); free(pv); free(m_i); free(l_i);
   }
 #undef ATTN_LD
-#undef ATTN_ST
   return rc;
 }
 

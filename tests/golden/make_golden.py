@@ -198,18 +198,29 @@ def attn_fwd_kernel(Q, K, V, sm_scale, M, Out, N_CTX, H,
         l_i = l_i * alpha + l_ij
         acc = acc * alpha[:, None]
         v = tl.load(V + base + (start_n + offs_n)[:, None] * HEAD_DIM + offs_d[None, :])
-        p = p.to(tl.float16)
+        p = p.to(V.dtype.element_ty)  # fp16, or fp8e5 for the fp8 provider
         acc = tl.dot(p, v, acc)
         m_i = m_ij
     m_i += tl.math.log2(l_i)
     acc = acc / l_i[:, None]
     tl.store(M + off_hz * N_CTX + offs_m, m_i)
-    tl.store(Out + base + offs_m[:, None] * HEAD_DIM + offs_d[None, :], acc.to(tl.float16))
+    tl.store(Out + base + offs_m[:, None] * HEAD_DIM + offs_d[None, :],
+             acc.to(Out.dtype.element_ty))
 
 
-def attn_case(rng, name, Z, H, N, D, causal, sm_scale, block):
-    q, k, v = (torch.from_numpy((rng.standard_normal((Z, H, N, D)) * 0.5).astype(np.float16))
+@triton.jit
+def cast_e5m2_kernel(X, Y, n, BLOCK: tl.constexpr):
+    offs = tl.program_id(0) * BLOCK + tl.arange(0, BLOCK)
+    x = tl.load(X + offs, mask=offs < n)
+    tl.store(Y + offs, x.to(tl.float8e5), mask=offs < n)
+
+
+def attn_case(rng, name, Z, H, N, D, causal, sm_scale, block, fp8=False):
+    std = 1.0 if fp8 else 0.5  # the tutorial's fp8 bench: randn, then .to(float8_e5m2)
+    q, k, v = (torch.from_numpy((rng.standard_normal((Z, H, N, D)) * std).astype(np.float16))
                for _ in range(3))
+    if fp8:
+        q, k, v = (x.to(torch.float8_e5m2) for x in (q, k, v))
     o = torch.empty_like(q)
     M = torch.empty((Z * H, N), dtype=torch.float32)
     BM, BN = block
@@ -479,6 +490,38 @@ def main():
     b = normal((256, 128), rng, 1.0, torch.float8_e5m2)
     save("fp8e5_f32_normal", a, b, run(a, b, out="f32", block=(64, 64, 64)),
          block=(64, 64, 64), out="f32")
+
+    fp8_attention(np.random.default_rng(20261202))
+
+
+def e5m2_cast_inputs(rng):
+    """fp32 values for the interpreter's fp32 -> e5m2 cast: every binade from
+    fp32 subnormals to past e5m2's largest finite, with significands that hit
+    the round bit, ties, sticky bits and the carry out of the top 2 bits."""
+    sigs = [0, 1, 1 << 19, 1 << 20, (1 << 20) | 1, 1 << 21, (1 << 21) | (1 << 20), 2 << 21,
+            3 << 21, (3 << 21) | (1 << 20), (3 << 21) | (1 << 20) | 1, (2 << 21) | (1 << 20),
+            0x7FFFFF]
+    bits = []
+    for e in list(range(0, 8)) + list(range(90, 146)):
+        for m in sigs + [int(x) for x in rng.integers(0, 1 << 23, size=4)]:
+            bits.append((e << 23) | m)
+    bits = np.array(bits, dtype=np.uint32)
+    bits = np.concatenate([bits, bits | np.uint32(0x80000000)])
+    return bits.view(np.float32)
+
+
+def fp8_attention(rng):
+    """The tutorial's fp8 forward (R:pass/LoopSplit/06-fused-attention.py
+    :774-779 bench inputs, :81-82 p.to(fp8e5), :238 o in q's type): e5m2 q, k,
+    v, p and o; and the fp32 -> e5m2 cast it applies to p and o."""
+    x = e5m2_cast_inputs(rng)
+    y = torch.empty(x.size, dtype=torch.float8_e5m2)
+    cast_e5m2_kernel[(triton.cdiv(x.size, 256),)](torch.from_numpy(x), y, x.size, BLOCK=256)
+    np.savez_compressed(os.path.join(HERE, "e5m2_cast_interp.npz"), x=x,
+                        y=y.view(torch.uint8).numpy())
+    print(f"e5m2_cast_interp: {x.size} values", flush=True)
+    attn_case(rng, "attn_fwd_fp8_causal", 1, 2, 256, 64, True, 1.3, (64, 32), fp8=True)
+    attn_case(rng, "attn_fwd_fp8_plain", 1, 1, 128, 64, False, 0.5, (64, 32), fp8=True)
 
 
 if __name__ == "__main__":

@@ -11,6 +11,11 @@ fused-attention tutorial (R:pass/LoopSplit/06-fused-attention.py:44-93,
      unmasked, on-band masked) equals the loop with every block masked, bit
      for bit, and so does skipping the blocks past the diagonal (what the GPU
      kernel does).
+The fp8 provider (e5m2 q, k, v, p and o) adds two codecs for p.to(fp8e5) and
+o.to(fp8e5): round to nearest even (compiled Triton, the GPU kernel), pinned
+against torch's float8_e5m2 cast, and the interpreter's own converter, pinned
+bit for bit against the interpreter's cast (tests/golden/e5m2_cast_interp.npz);
+the attention fixtures attn_fwd_fp8_* pin the forward with the latter.
 """
 import glob
 import os
@@ -46,7 +51,14 @@ def exact_attention(q, k, v, sm_scale, causal):
     return o, lse.reshape(-1, N)
 
 
-ATTN_FIXTURES = sorted(glob.glob(os.path.join(GOLDEN, "attn_*.npz")))
+ATTN_FIXTURES = sorted(p for p in glob.glob(os.path.join(GOLDEN, "attn_*.npz"))
+                       if "_fp8_" not in p)
+FP8_FIXTURES = sorted(glob.glob(os.path.join(GOLDEN, "attn_fwd_fp8_*.npz")))
+
+
+def e5m2_values(codes):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(codes)).view(torch.float8_e5m2).double().numpy()
 
 
 @pytest.mark.parametrize("path", ATTN_FIXTURES,
@@ -62,6 +74,82 @@ def test_golden_fixture_attn(path):
     assert np.abs(go - wo).max() <= 2 ** -9, np.abs(go - wo).max()
     assert np.mean(go == wo) > 0.98
     assert np.abs(M - z["M"]).max() <= 1e-5 * np.abs(z["M"]).max() + 1e-6
+
+
+def test_e5m2_codecs():
+    """p.to(fp8e5) and o.to(fp8e5): RNE against torch over a wide sweep, the
+    interpreter's converter against the interpreter's own cast bit for bit."""
+    import torch
+    z = np.load(os.path.join(GOLDEN, "e5m2_cast_interp.npz"), allow_pickle=False)
+    x, y = z["x"], z["y"]
+    assert np.array_equal(oracle.f32_to_e5m2(x, oracle.ROUND_INTERP), y)
+    rng = np.random.default_rng(7)
+    sweep = np.concatenate([x, np.concatenate(
+        [rng.standard_normal(50000).astype(np.float32) * np.float32(s)
+         for s in (1e-6, 1e-4, 1e-2, 1.0, 1e2, 1e4)]),
+        np.arange(-70000, 70000, 0.37, dtype=np.float32)])
+    want = torch.from_numpy(sweep).to(torch.float8_e5m2).view(torch.uint8).numpy()
+    assert np.array_equal(oracle.f32_to_e5m2(sweep, oracle.ROUND_RNE), want)
+    # the two differ (half-up vs half-even, the carry ORed into the exponent):
+    # 0.4921875 = 1.96875 * 2^-2 is 0.5 to nearest and 0.25 in the interpreter
+    v = np.array([0.4921875, 0.375 + 2 ** -5], np.float32)
+    assert list(e5m2_values(oracle.f32_to_e5m2(v))) == [0.5, 0.375]
+    assert list(e5m2_values(oracle.f32_to_e5m2(v, oracle.ROUND_INTERP))) == [0.25, 0.4375]
+
+
+@pytest.mark.parametrize("path", FP8_FIXTURES, ids=[os.path.basename(p)[:-4] for p in FP8_FIXTURES])
+def test_golden_fixture_attn_fp8(path):
+    """The interpreter running the tutorial's fp8 forward (e5m2 q, k, v, p,
+    o) against the oracle with the interpreter's converter: o codes agree but
+    where a different fp32 summation order lands on the other side of a
+    rounding boundary (there the converter's carry quirk can halve a value)."""
+    z = np.load(path, allow_pickle=False)
+    o, M = oracle.attn_fwd(z["q"], z["k"], z["v"], sm_scale=float(z["sm_scale"]),
+                           causal=bool(z["causal"]), block=tuple(int(x) for x in z["block"]),
+                           dtype=oracle.F8E5M2, round_mode=oracle.ROUND_INTERP)
+    assert np.mean(o == z["o"]) > 0.99
+    a, b = e5m2_values(o), e5m2_values(z["o"])
+    m = a != b
+    assert (np.abs(a[m] - b[m]) <= 0.5 * np.maximum(np.abs(a[m]), np.abs(b[m])) + 2 ** -16).all()
+    assert np.abs(M - z["M"]).max() <= 1e-5 * np.abs(z["M"]).max() + 1e-6
+    # and with round to nearest even (the GPU kernel's rounding) the same
+    # forward moves a share of the codes
+    o_rne, M_rne = oracle.attn_fwd(z["q"], z["k"], z["v"], sm_scale=float(z["sm_scale"]),
+                                   causal=bool(z["causal"]),
+                                   block=tuple(int(x) for x in z["block"]), dtype=oracle.F8E5M2)
+    assert 0.5 < np.mean(o_rne == z["o"]) < 0.99
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attn_oracle_fp8_vs_float64(causal):
+    """e5m2 forward (round to nearest even) against float64 attention of the
+    same decoded inputs: p and o each carry e5m2's 2^-3 relative rounding."""
+    import torch
+    rng = np.random.default_rng(11 + causal)
+    codes = [torch.from_numpy(rng.standard_normal((1, 2, 256, 64)).astype(np.float16))
+             .to(torch.float8_e5m2).view(torch.uint8).numpy() for _ in range(3)]
+    qf, kf, vf = (e5m2_values(c) for c in codes)
+    o, M = oracle.attn_fwd(*codes, sm_scale=0.3, causal=causal, block=(128, 64),
+                           dtype=oracle.F8E5M2)
+    N = 256
+    s = np.einsum("zhmd,zhnd->zhmn", qf, kf) * 0.3
+    if causal:
+        s = np.where(np.tril(np.ones((N, N))) > 0, s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    ref = (p / p.sum(-1, keepdims=True)) @ vf
+    got = e5m2_values(o)
+    # |sum p eps v| / l <= 2^-3 max|v| per row, then o's own rounding
+    bound = 2 ** -3 * np.abs(vf).max(axis=(2, 3), keepdims=True) + 2 ** -3 * np.abs(ref)
+    assert (np.abs(got - ref) <= bound + 2 ** -16).all()
+    assert np.sqrt(np.mean((got - ref) ** 2)) < 0.05 * np.sqrt(np.mean(ref ** 2)) + 0.01
+    # M sums the unrounded p: base-2 logsumexp to fp32 accuracy
+    qk_scale = float(np.float32(0.3) * np.float32(1.44269504))
+    t = np.einsum("zhmd,zhnd->zhmn", qf, kf) * qk_scale
+    if causal:
+        t = np.where(np.tril(np.ones((N, N))) > 0, t, -np.inf)
+    mx = t.max(-1, keepdims=True)
+    rM = (mx[..., 0] + np.log2(np.exp2(t - mx).sum(-1))).reshape(-1, N)
+    assert np.abs(M - rM).max() < 1e-5 * np.abs(rM).max() + 1e-6
 
 
 @pytest.mark.parametrize("causal", [True, False])
@@ -96,6 +184,17 @@ def test_attn_oracle_dims_and_bf16(D, bf16):
     ref = (p / p.sum(-1, keepdims=True)) @ vf
     tol = 2 ** -6 if bf16 else 2 ** -9  # p and o rounded to bf16 (8 bits) or fp16 (11)
     assert np.abs(got - ref).max() < tol, np.abs(got - ref).max()
+
+
+def test_attn_loop_split_is_exact_fp8():
+    import torch
+    q, k, v = (torch.from_numpy(x.view(np.float16)).to(torch.float8_e5m2).view(torch.uint8)
+               .numpy() for x in rand_qkv(1, 2, 512, 64, seed=4, std=1.0))
+    kw = dict(sm_scale=1.3, causal=True, block=(128, 64), dtype=oracle.F8E5M2)
+    o0, M0 = oracle.attn_fwd(q, k, v, mode=0, **kw)
+    for mode in (1, 2):
+        o1, M1 = oracle.attn_fwd(q, k, v, mode=mode, **kw)
+        assert np.array_equal(o0, o1) and np.array_equal(M0.view(np.uint32), M1.view(np.uint32))
 
 
 def test_attn_loop_split_is_exact():
@@ -147,6 +246,13 @@ def test_attn_plan():
     assert tx.attn_plan(1, 1, 256, 128, True, 0.5, dtype=tx.BF16).desc.head_dim == 128
     assert err(block=(64, 32)) == tx.ERR_UNSUPPORTED
     assert err(Z=-1) == tx.ERR_INVALID
+    # e5m2: one byte per element, v key-contiguous ([HEAD_DIM][N_CTX] per head)
+    p8 = tx.attn_plan(4, 32, 4096, 64, False, 1.3, dtype=tx.F8E5M2)
+    assert p8.bytes == 4 * 4 * 32 * 4096 * 64 + 4 * 32 * 4096 * 4
+    assert (p8.desc.v_sm, p8.desc.v_sh) == (4096, 64 * 4096) and p8.desc.q_sm == 64
+    assert err(dtype=tx.F8E5M2, strides={"v": (0, 0, 64)}) == tx.ERR_INVALID  # dim rows < N_CTX
+    assert err(dtype=tx.F8E5M2, strides={"q": (0, 0, 72)}) == tx.ERR_INVALID  # not 16 bytes
+    assert err(dtype=tx.F8E4M3) == tx.ERR_UNSUPPORTED
     assert err(sm_scale=float("nan")) == tx.ERR_INVALID
     assert err(strides={"q": (0, 0, 60)}) == tx.ERR_INVALID
 
@@ -158,5 +264,8 @@ def test_attention_argument_checks():
         tx.attention(q[..., :48], q[..., :48], q[..., :48], True, 0.5)
     with pytest.raises(NotImplementedError):
         tx.attention(q.float(), q.float(), q.float(), True, 0.5)
+    q8 = q.to(torch.float8_e5m2)
+    with pytest.raises(ValueError, match="key-contiguous"):
+        tx.attention(q8, q8, q8, True, 0.5)
     with pytest.raises(ValueError, match="share one"):
         tx.attention(q, q[:, :1], q, True, 0.5)

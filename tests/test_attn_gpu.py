@@ -143,3 +143,108 @@ def test_attn_head_dim_128_and_bf16(gpu, causal, D, bf16, Z, H, N, layout):
     dm = np.abs(from_device(M).reshape(rM.shape).astype(np.float64) - rM)
     assert dm.max() <= 1e-4 * max(1.0, np.abs(rM).max()), f"max |d M| {dm.max():.3g}"
     say(f"attn D={D} bf16={bf16}: max|d o|={d.max():.3g} identical={np.mean(got == ro):.3f}")
+
+
+# --- fp8 e5m2 (the tutorial's fp8 provider) ---------------------------------
+
+def e5m2_qkv(Z, H, N, D, seed, std=1.0):
+    """The tutorial's fp8 bench inputs: randn fp16, then .to(float8_e5m2)."""
+    import torch
+    rng = np.random.default_rng(seed)
+    return [torch.from_numpy((rng.standard_normal((Z, H, N, D)) * std).astype(np.float16))
+            .to(torch.float8_e5m2).view(torch.uint8).numpy() for _ in range(3)]
+
+
+def run_gpu_fp8(gpu, q, k, v, causal, sm_scale):
+    """q, k head-dim contiguous; v stored key-contiguous and viewed as
+    [Z, H, N, D], as the tutorial's v.permute(0, 1, 3, 2).contiguous()
+    .permute(0, 1, 3, 2) leaves it."""
+    import torch
+    qt, kt = (to_device(x, gpu).view(torch.float8_e5m2) for x in (q, k))
+    vt = to_device(np.ascontiguousarray(v.transpose(0, 1, 3, 2)), gpu).view(torch.float8_e5m2)
+    vt = vt.permute(0, 1, 3, 2)
+    assert vt.stride(2) == 1
+    o, M = tx.attention(qt, kt, vt, causal, sm_scale, return_lse=True)
+    torch.cuda.synchronize()
+    assert o.dtype == torch.float8_e5m2
+    return o.view(torch.uint8).cpu().numpy(), from_device(M)
+
+
+def e5m2_step(x):
+    """Spacing of e5m2 values at |x| (2^-16 in the subnormal range)."""
+    a = np.maximum(np.abs(x), 2.0 ** -14)
+    return 2.0 ** (np.floor(np.log2(a)) - 2)
+
+
+def check_e5m2(o, M, ro, rM, codes, sm_scale, causal, what):
+    """Parity of e5m2 outputs.  p and o are rounded to nearest even on both
+    sides; their fp32 values differ slightly (summation order, the MFMA's
+    group sums, v_exp_f32), so a value lying at a rounding boundary can land
+    on either side.  An o code then moves one step, and a p code moves one
+    step, changing o by at most 2^-2 p_n |v_n| / l.  The bar: at least 99%
+    of o codes identical, and every difference within one e5m2 step of o
+    plus one p flip of the row's largest term, 2^-2 max_n p_n |v_n| / l
+    (float64 softmax of the decoded inputs)."""
+    import torch
+    dec = lambda c: torch.from_numpy(np.ascontiguousarray(c)).view(torch.float8_e5m2) \
+        .double().numpy()
+    a, b = dec(o), dec(ro)
+    qf, kf, vf = (dec(c) for c in codes)
+    N = qf.shape[2]
+    s = np.einsum("zhmd,zhnd->zhmn", qf, kf) * sm_scale
+    if causal:
+        s = np.where(np.tril(np.ones((N, N))) > 0, s, -np.inf)
+    P = np.exp(s - s.max(-1, keepdims=True))
+    P /= P.sum(-1, keepdims=True)
+    top = np.empty(a.shape)  # max_n p_n |v_n| / l, [Z, H, M, D], in row chunks
+    for r in range(0, N, 64):
+        top[:, :, r:r + 64] = np.max(P[:, :, r:r + 64, :, None] * np.abs(vf)[:, :, None],
+                                     axis=-2)
+    assert ((o & 0x7F) < 0x7C).all(), f"{what}: inf/NaN in o"
+    same = np.mean(o == ro)
+    assert same >= 0.99, f"{what}: only {same:.4f} of o codes identical"
+    excess = np.abs(a - b) - (e5m2_step(np.maximum(np.abs(a), np.abs(b))) + top / 4)
+    assert excess.max() <= 0, f"{what}: |d o| exceeds its bound by {excess.max():.3g} " \
+        f"(identical {same:.4f})"
+    dm = np.abs(M.reshape(rM.shape).astype(np.float64) - rM)
+    assert dm.max() <= 1e-4 * max(1.0, np.abs(rM).max()), f"{what}: max |d M| {dm.max():.3g}"
+    say(f"{what}: identical={same:.4f} max|d o|={np.abs(a - b).max():.3g} max|d M|={dm.max():.3g}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("Z,H,N,D,sm_scale", [(1, 2, 256, 64, 1.3), (2, 3, 384, 64, 0.5),
+                                              (1, 1, 128, 64, 0.3), (1, 2, 512, 128, 0.3),
+                                              (2, 1, 256, 128, 1.3)])
+def test_attn_fp8_vs_oracle(gpu, causal, Z, H, N, D, sm_scale):
+    say(f"attn fp8 Z={Z} H={H} N={N} D={D} causal={causal} scale={sm_scale}")
+    q, k, v = e5m2_qkv(Z, H, N, D, seed=Z * 100 + H * 10 + N + D + causal)
+    o, M = run_gpu_fp8(gpu, q, k, v, causal, sm_scale)
+    ro, rM = oracle.attn_fwd(q, k, v, sm_scale=sm_scale, causal=causal, block=(128, 64),
+                             dtype=oracle.F8E5M2)
+    check_e5m2(o, M, ro, rM, (q, k, v), sm_scale, causal,
+               f"attn fp8 {Z}x{H}x{N} D={D} causal={causal}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attn_fp8_bench_shape_sampled_heads(gpu, causal):
+    """The tutorial's fp8 bench shape (4, 32, 4096, 64), sm_scale 1.3: every
+    program runs; two heads are checked in full against the oracle."""
+    import torch
+    say(f"attn fp8 4x32x4096 causal={causal}")
+    Z, H, N, D = 4, 32, 4096, 64
+    g = torch.Generator(device=gpu)
+    g.manual_seed(6)
+    q, k, v = (torch.randn((Z, H, N, D), generator=g, device=gpu, dtype=torch.float16)
+               .to(torch.float8_e5m2) for _ in range(3))
+    vt = v.permute(0, 1, 3, 2).contiguous().permute(0, 1, 3, 2)
+    o, M = tx.attention(q, k, vt, causal, 1.3, return_lse=True)
+    torch.cuda.synchronize()
+    assert ((o.view(torch.uint8) & 0x7F) < 0x7C).all()
+    for (zi, hi) in ((0, 0), (3, 31)):
+        sub = [t[zi:zi + 1, hi:hi + 1].contiguous().view(torch.uint8).cpu().numpy()
+               for t in (q, k, v)]
+        ro, rM = oracle.attn_fwd(*sub, sm_scale=1.3, causal=causal, block=(128, 64),
+                                 dtype=oracle.F8E5M2)
+        got = o[zi:zi + 1, hi:hi + 1].contiguous().view(torch.uint8).cpu().numpy()
+        check_e5m2(got, from_device(M[zi, hi]), ro, rM, sub, 1.3, causal,
+                   f"attn fp8 4x32x4096 head ({zi},{hi})")

@@ -23,6 +23,7 @@
 #include "triton_ext/tx_passes.h"
 
 #include "attn_fwd.h"
+#include "attn_fwd8.h"
 
 #include "decode_i8.h"
 #include "gemm16_dma.h"
@@ -672,15 +673,19 @@ extern "C" TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A,
 namespace {
 
 // Packed defaults and checks of one tensor's (batch, head, row) strides.
+// key_major: e5m2 v, stored [HEAD_DIM][N_CTX] per head (sm = dim stride).
 int attnStrides(const tx_attn_desc &d, int64_t &sz, int64_t &sh, int64_t &sm,
-                const char *name) {
-  if (sm == 0) sm = d.head_dim;
-  if (sh == 0) sh = d.N_CTX * sm;
+                const char *name, bool key_major) {
+  const int64_t esz = d.dtype == TX_F8E5M2 ? 1 : 2, quantum = 16 / esz;
+  const int64_t rows = key_major ? d.head_dim : d.N_CTX, len = key_major ? d.N_CTX : d.head_dim;
+  if (sm == 0) sm = len;
+  if (sh == 0) sh = rows * sm;
   if (sz == 0) sz = d.H * sh;
-  if (sm < d.head_dim || sh < 0 || sz < 0 || sm % 8 || sh % 8 || sz % 8)
-    return fail(TX_ERR_INVALID, "%s strides (%lld, %lld, %lld): rows of head_dim elements, "
-                "multiples of 8 elements", name, (long long)sz, (long long)sh, (long long)sm);
-  if (((d.N_CTX - 1) * sm + d.head_dim) * 2 >= ((int64_t)1 << 31))
+  if (sm < len || sh < 0 || sz < 0 || sm % quantum || sh % quantum || sz % quantum)
+    return fail(TX_ERR_INVALID, "%s strides (%lld, %lld, %lld): rows of %s elements, "
+                "multiples of 16 bytes", name, (long long)sz, (long long)sh, (long long)sm,
+                key_major ? "N_CTX" : "head_dim");
+  if (((rows - 1) * sm + len) * esz >= ((int64_t)1 << 31))
     return fail(TX_ERR_UNSUPPORTED, "%s: one head spans 2 GiB or more", name);
   return TX_OK;
 }
@@ -702,8 +707,9 @@ extern "C" TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *p
   typedef txk::AttnFwd<64, false> AF; // block shape (the same for every head dim)
   if (d.head_dim != 64 && d.head_dim != 128)
     return fail(TX_ERR_UNSUPPORTED, "head_dim %d: 64 and 128 are implemented", d.head_dim);
-  if (d.dtype != TX_F16 && d.dtype != TX_BF16)
-    return fail(TX_ERR_UNSUPPORTED, "dtype %d: fp16 and bf16 q/k/v/o are implemented", d.dtype);
+  if (d.dtype != TX_F16 && d.dtype != TX_BF16 && d.dtype != TX_F8E5M2)
+    return fail(TX_ERR_UNSUPPORTED, "dtype %d: fp16, bf16 and fp8 e5m2 q/k/v/o are implemented",
+                d.dtype);
   if (d.block_m == 0) d.block_m = AF::BM;
   if (d.block_n == 0) d.block_n = AF::BN;
   if (d.block_m != AF::BM || d.block_n != AF::BN)
@@ -712,10 +718,11 @@ extern "C" TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *p
   if (d.N_CTX % d.block_m)
     return fail(TX_ERR_UNSUPPORTED, "N_CTX %lld is not a multiple of %d (whole blocks only)",
                 (long long)d.N_CTX, d.block_m);
-  int rc = attnStrides(d, d.q_sz, d.q_sh, d.q_sm, "q");
-  if (rc == TX_OK) rc = attnStrides(d, d.k_sz, d.k_sh, d.k_sm, "k");
-  if (rc == TX_OK) rc = attnStrides(d, d.v_sz, d.v_sh, d.v_sm, "v");
-  if (rc == TX_OK) rc = attnStrides(d, d.o_sz, d.o_sh, d.o_sm, "o");
+  const bool fp8 = d.dtype == TX_F8E5M2;
+  int rc = attnStrides(d, d.q_sz, d.q_sh, d.q_sm, "q", false);
+  if (rc == TX_OK) rc = attnStrides(d, d.k_sz, d.k_sh, d.k_sm, "k", false);
+  if (rc == TX_OK) rc = attnStrides(d, d.v_sz, d.v_sh, d.v_sm, "v", fp8);
+  if (rc == TX_OK) rc = attnStrides(d, d.o_sz, d.o_sh, d.o_sm, "o", false);
   if (rc != TX_OK)
     return rc;
   const int64_t programs = d.Z * d.H * (d.N_CTX / d.block_m);
@@ -725,7 +732,7 @@ extern "C" TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *p
   plan->desc = d;
   const double zh = (double)d.Z * (double)d.H, n = (double)d.N_CTX;
   plan->flops = 4.0 * zh * n * n * d.head_dim * (d.causal ? 0.5 : 1.0);
-  plan->bytes = 4.0 * zh * n * d.head_dim * 2 + zh * n * 4;
+  plan->bytes = 4.0 * zh * n * d.head_dim * (fp8 ? 1 : 2) + zh * n * 4;
   plan->qk_scale = d.sm_scale * 1.44269504f; // qk_scale = sm_scale; qk_scale *= 1.44269504
   plan->m_blocks = (int32_t)(d.N_CTX / d.block_m);
   plan->grid_x = (int32_t)programs;
@@ -749,16 +756,17 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
     return fail(TX_ERR_INVALID, "q, k, v, o must be 16-byte aligned and M 4-byte aligned");
   typedef txk::AttnFwd<64, false> AF;
   if (plan->block_threads != AF::NW * 64 || d.block_m != AF::BM || d.block_n != AF::BN ||
-      (d.head_dim != 64 && d.head_dim != 128) || (d.dtype != TX_F16 && d.dtype != TX_BF16) ||
+      (d.head_dim != 64 && d.head_dim != 128) ||
+      (d.dtype != TX_F16 && d.dtype != TX_BF16 && d.dtype != TX_F8E5M2) ||
       plan->m_blocks != d.N_CTX / d.block_m || plan->grid_x != d.Z * d.H * plan->m_blocks)
     return fail(TX_ERR_INVALID, "plan launch shape does not match the attention kernel");
   if (!tx_device_available())
     return fail(TX_ERR_NO_DEVICE, "no gfx950 device visible");
   txk::AttnArgs a;
-  a.Q = static_cast<const uint16_t *>(q);
-  a.K = static_cast<const uint16_t *>(k);
-  a.V = static_cast<const uint16_t *>(v);
-  a.O = static_cast<uint16_t *>(o);
+  a.Q = q;
+  a.K = k;
+  a.V = v;
+  a.O = o;
   a.M = M;
   a.q_sz = d.q_sz, a.q_sh = d.q_sh, a.q_sm = d.q_sm;
   a.k_sz = d.k_sz, a.k_sh = d.k_sh, a.k_sm = d.k_sm;
@@ -775,7 +783,13 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
        {txk::attn_fwd_kernel<false, 128, false>, txk::attn_fwd_kernel<false, 128, true>}},
       {{txk::attn_fwd_kernel<true, 64, false>, txk::attn_fwd_kernel<true, 64, true>},
        {txk::attn_fwd_kernel<true, 128, false>, txk::attn_fwd_kernel<true, 128, true>}}};
-  const AttnFn fn = kAttn[d.causal ? 1 : 0][d.head_dim == 128][d.dtype == TX_BF16];
+  // [causal][head_dim 128]
+  static const AttnFn kAttn8[2][2] = {
+      {txk::attn_fwd8_kernel<false, 64>, txk::attn_fwd8_kernel<false, 128>},
+      {txk::attn_fwd8_kernel<true, 64>, txk::attn_fwd8_kernel<true, 128>}};
+  const AttnFn fn = d.dtype == TX_F8E5M2
+                        ? kAttn8[d.causal ? 1 : 0][d.head_dim == 128]
+                        : kAttn[d.causal ? 1 : 0][d.head_dim == 128][d.dtype == TX_BF16];
   hipLaunchKernelGGL(fn, dim3(plan->grid_x), dim3(plan->block_threads), 0, s, a);
   TX_HIP_CHECK(hipGetLastError());
   return TX_OK;

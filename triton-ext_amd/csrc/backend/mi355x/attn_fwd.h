@@ -36,8 +36,8 @@
 namespace txk {
 
 struct AttnArgs {
-  const uint16_t *Q, *K, *V;
-  uint16_t *O;
+  const void *Q, *K, *V; // fp16 / bf16, or e5m2 bytes (attn_fwd8.h)
+  void *O;
   float *M;
   int64_t q_sz, q_sh, q_sm;
   int64_t k_sz, k_sh, k_sm;
@@ -48,7 +48,7 @@ struct AttnArgs {
 };
 
 template <int HD, bool BF> struct AttnFwd {
-  static constexpr int BM = 128, BN = 64, D = HD, NW = 4;
+  static constexpr int BM = 128, BN = 64, D = HD, NW = 4, ESZ = 2;
   static constexpr int ROW = D * 2;            // bytes per K/V row
   static constexpr int TILE = BN * ROW;        // 8 / 16 KiB
   static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 2 / 4
@@ -261,6 +261,59 @@ template <int HD, bool BF> struct AttnFwd {
       for (int c = 0; c < BN / 16; ++c)
         acc[bd] = mfma(vf[bd][c], pf[c], acc[bd]);
   }
+
+  // The kernel's view of this element type.
+  struct QF {
+    h8 v[D / 16];
+  };
+  typedef h8 PF[BN / 16];
+  // Q rows as MFMA B operands: dims 16 c + 8 g .. +7 of row m.
+  __device__ __forceinline__ static void load_q(const uint8_t *Qh, int64_t m, int64_t sm,
+                                                QF &qf) {
+    const int g = (threadIdx.x & 63) >> 5;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+      qf.v[c] = *reinterpret_cast<const h8 *>(Qh + (m * sm + 16 * c + 8 * g) * 2);
+  }
+  __device__ __forceinline__ static uint32_t k_bytes(int64_t n_ctx, int64_t sm) {
+    return (uint32_t)(((n_ctx - 1) * sm + D) * 2);
+  }
+  __device__ __forceinline__ static uint32_t v_bytes(int64_t n_ctx, int64_t sm) {
+    return k_bytes(n_ctx, sm);
+  }
+  __device__ __forceinline__ static void kv_offsets(int wave, int64_t k_sm, int64_t v_sm,
+                                                    uint32_t (&ko)[DMA], uint32_t (&vo)[DMA]) {
+    dma_offsets<false>(wave, k_sm, ko);
+    dma_offsets<true>(wave, v_sm, vo);
+  }
+  __device__ __forceinline__ static void issue_k(const i32x4_t &rsrc, const uint32_t (&off)[DMA],
+                                                 int64_t sm, int j, uint32_t lds, int wave) {
+    issue(rsrc, off, sm, j, lds, wave);
+  }
+  __device__ __forceinline__ static void issue_v(const i32x4_t &rsrc, const uint32_t (&off)[DMA],
+                                                 int64_t sm, int j, uint32_t lds, int wave) {
+    issue(rsrc, off, sm, j, lds, wave);
+  }
+  template <int SLOT>
+  __device__ __forceinline__ static void qk(const Bases &bs, const QF &qf, f16v (&s)[BN / 32]) {
+    qk<SLOT>(bs, qf.v, s);
+  }
+  // O = acc / l_i.  Lane l holds, per dim block bd and register quad q, dims
+  // 32 bd + 8 q + 4 g .. +3 of row m.
+  __device__ __forceinline__ static void store_o(const f16v (&acc)[D / 32], float l_i,
+                                                 uint8_t *Orow) {
+    const int g = (threadIdx.x & 63) >> 5;
+#pragma unroll
+    for (int bd = 0; bd < D / 32; ++bd)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        h4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = (elt)(acc[bd][4 * q + e] / l_i);
+        *reinterpret_cast<h4 *>(Orow + (32 * bd + 8 * q + 4 * g) * 2) = o;
+      }
+  }
 };
 
 // The K/V loop is software-pipelined: iteration j holds S_j in registers,
@@ -270,9 +323,9 @@ template <int HD, bool BF> struct AttnFwd {
 // V_{j+1} (into V_{j-1}'s slot), and its closing barrier makes them visible.
 // Block j uses K slot j%2 and V slot j%2; the loop advances two blocks per
 // trip so that slots are constants (both segments have even trip counts).
-template <bool CAUSAL, int HD, bool BF>
-__global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
-  typedef AttnFwd<HD, BF> A;
+// A: the element type's fragments (AttnFwd<HD, BF> here, AttnFwd8<HD> for
+// e5m2).
+template <bool CAUSAL, class A> __device__ __forceinline__ void attn_fwd_body(const AttnArgs &p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[4 * A::TILE];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -283,22 +336,18 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
   const int t = (nwg % 8 == 0) ? (b % 8) * (nwg / 8) + b / 8 : b;
   const int hz = t / nm, start_m = CAUSAL ? nm - 1 - t % nm : t % nm;
   const int z = hz / p.H, h = hz % p.H;
-  const uint16_t *Qh = p.Q + z * p.q_sz + h * p.q_sh;
-  const uint16_t *Kh = p.K + z * p.k_sz + h * p.k_sh;
-  const uint16_t *Vh = p.V + z * p.v_sz + h * p.v_sh;
+  const uint8_t *Qh = static_cast<const uint8_t *>(p.Q) + (z * p.q_sz + h * p.q_sh) * A::ESZ;
+  const uint8_t *Kh = static_cast<const uint8_t *>(p.K) + (z * p.k_sz + h * p.k_sh) * A::ESZ;
+  const uint8_t *Vh = static_cast<const uint8_t *>(p.V) + (z * p.v_sz + h * p.v_sh) * A::ESZ;
   const int m = start_m * A::BM + 32 * wave + (lane & 31);
 
-  // Q rows as MFMA B operands: dims 16 c + 8 g .. +7 of row m.
-  typename A::h8 qf[A::D / 16];
-#pragma unroll
-  for (int c = 0; c < A::D / 16; ++c)
-    qf[c] = *reinterpret_cast<const typename A::h8 *>(Qh + (int64_t)m * p.q_sm + 16 * c + 8 * g);
+  typename A::QF qf;
+  A::load_q(Qh, m, p.q_sm, qf);
 
-  const i32x4_t rk = make_rsrc(Kh, (uint32_t)(((int64_t)(p.N_CTX - 1) * p.k_sm + A::D) * 2));
-  const i32x4_t rv = make_rsrc(Vh, (uint32_t)(((int64_t)(p.N_CTX - 1) * p.v_sm + A::D) * 2));
+  const i32x4_t rk = make_rsrc(Kh, A::k_bytes(p.N_CTX, p.k_sm));
+  const i32x4_t rv = make_rsrc(Vh, A::v_bytes(p.N_CTX, p.v_sm));
   uint32_t ko[A::DMA], vo[A::DMA];
-  A::template dma_offsets<false>(wave, p.k_sm, ko);
-  A::template dma_offsets<true>(wave, p.v_sm, vo);
+  A::kv_offsets(wave, p.k_sm, p.v_sm, ko, vo);
   const uint32_t k_lds = lds_addr(smem), v_lds = k_lds + 2 * A::TILE;
   typename A::Bases bs;
   A::bases(k_lds, v_lds, bs);
@@ -316,10 +365,10 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
   for (int bd = 0; bd < A::D / 32; ++bd)
     acc[bd] = typename A::f16v{};
 
-  A::issue(rk, ko, p.k_sm, 0, k_lds, wave);
-  A::issue(rv, vo, p.v_sm, 0, v_lds, wave);
-  A::issue(rk, ko, p.k_sm, 1, k_lds + A::TILE, wave); // n_end >= 2
-  __builtin_amdgcn_s_waitcnt(0x7 << 4);               // vmcnt(0)
+  A::issue_k(rk, ko, p.k_sm, 0, k_lds, wave);
+  A::issue_v(rv, vo, p.v_sm, 0, v_lds, wave);
+  A::issue_k(rk, ko, p.k_sm, 1, k_lds + A::TILE, wave); // n_end >= 2
+  __builtin_amdgcn_s_waitcnt(0x7 << 4);                 // vmcnt(0)
   __syncthreads();
   A::template qk<0>(bs, qf, s);
   __syncthreads(); // K slot 0 is refilled by iteration 0
@@ -328,9 +377,9 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
     constexpr bool MASK = decltype(mask)::value;
     constexpr int SL = decltype(slot)::value;
     if (j + 2 < n_end)
-      A::issue(rk, ko, p.k_sm, j + 2, k_lds + SL * A::TILE, wave);
+      A::issue_k(rk, ko, p.k_sm, j + 2, k_lds + SL * A::TILE, wave);
     if (j + 1 < n_end)
-      A::issue(rv, vo, p.v_sm, j + 1, v_lds + (1 - SL) * A::TILE, wave);
+      A::issue_v(rv, vo, p.v_sm, j + 1, v_lds + (1 - SL) * A::TILE, wave);
     typename A::f16v sn[A::BN / 32];
     A::template qk<1 - SL>(bs, qf, sn); // S_{j+1} (a stale slot after the last block: unused)
     // On-band blocks whose keys all lie past this wave's 32 rows add exactly
@@ -338,7 +387,7 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
     // wave skips their softmax and P V.
     const bool live = !MASK || j * A::BN <= start_m * A::BM + 32 * wave + 31;
     if (live) {
-      typename A::h8 pf[A::BN / 16];
+      typename A::PF pf;
       A::template softmax<MASK>(s, j * A::BN, m, p.qk_scale, acc, m_i, l_i, pf);
       A::template pv<SL>(bs, pf, acc);
     }
@@ -357,21 +406,17 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
     iter(j + 1, std::true_type(), std::integral_constant<int, 1>());
   }
 
-  // Epilogue: M = m_i + log2(l_i); O = acc / l_i.  Lane l holds, per dim
-  // block bd and register quad q, dims 32 bd + 8 q + 4 g .. +3 of row m.
-  uint16_t *Oh = p.O + z * p.o_sz + h * p.o_sh + (int64_t)m * p.o_sm;
-#pragma unroll
-  for (int bd = 0; bd < A::D / 32; ++bd)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      typename A::h4 o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        o[e] = (typename A::elt)(acc[bd][4 * q + e] / l_i);
-      *reinterpret_cast<typename A::h4 *>(Oh + 32 * bd + 8 * q + 4 * g) = o;
-    }
+  // Epilogue: M = m_i + log2(l_i); O = acc / l_i.
+  A::store_o(acc, l_i,
+             static_cast<uint8_t *>(p.O) +
+                 (z * p.o_sz + h * p.o_sh + (int64_t)m * p.o_sm) * A::ESZ);
   if (g == 0)
     p.M[(int64_t)hz * p.N_CTX + m] = m_i + __builtin_log2f(l_i);
+}
+
+template <bool CAUSAL, int HD, bool BF>
+__global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
+  attn_fwd_body<CAUSAL, AttnFwd<HD, BF>>(p);
 }
 
 } // namespace txk

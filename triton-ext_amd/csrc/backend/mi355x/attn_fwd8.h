@@ -1,0 +1,279 @@
+// Fused attention forward for gfx950, fp8 e5m2: the tutorial's fp8 provider
+// (R:pass/LoopSplit/06-fused-attention.py:774-779: q, k, v cast to
+// float8_e5m2, v stored key-contiguous; :81-82 p.to(tl.float8e5) before
+// p @ v; :238 o in q's type), HEAD_DIM 64 or 128, fp32 statistics and
+// accumulator.  The pipeline, split and program order are attn_fwd_body's
+// (attn_fwd.h); this file holds the element type's fragments.
+//
+// Per K/V block of BN = 64 keys and wave of 32 query rows:
+//   S^T = K . Q^T    v_mfma_f32_32x32x64_f8f6f4 (e5m2 x e5m2), one per 32
+//                    keys and 64 dims.  Lane l feeds A row l%32 with key
+//                    pi(l%32), pi(8i + 4g + j) = 16g + 4i + j, so the S^T
+//                    registers r of lane l hold keys 16 (l/32) + r of each
+//                    32-key block: 16 consecutive keys per lane;
+//   P                p converted to e5m2 with v_cvt_pk_bf8_f32 (round to
+//                    nearest even), packed in key order: byte 16 b + r of
+//                    lane l is key 32 b + 16 (l/32) + r;
+//   O^T += V^T . P^T one MFMA per 32 dims: A := V^T rows (dims), whose keys
+//                    are contiguous in memory and in LDS, read as the same
+//                    two 16-key chunks (l/32 and 2 + l/32) that P holds.
+// The two dots use any K order that is the same for both operands; the
+// order above needs no transposes and no lane exchanges.
+//
+// LDS (16-byte chunk c of row r stored at c ^ swizzle(r)):
+//   K rows (keys) of HEAD_DIM bytes: 64-byte rows ((r >> 2) & 1) |
+//     ((r >> 3) & 2); 128-byte rows ((r >> 1) & 3) | ((r >> 2) & 4).  The
+//     16 keys pi(0..15) (or pi(16..31)) that one ds_read_b128 pass reads land
+//     in 16 different 16-byte bank groups;
+//   V^T rows (dims) of 64 bytes (the block's keys): (r >> 2) & 3, likewise
+//     for dims 0..15 of a pass.
+#pragma once
+
+#include "attn_fwd.h"
+
+namespace txk {
+
+template <int HD> struct AttnFwd8 {
+  static constexpr int BM = 128, BN = 64, D = HD, NW = 4, ESZ = 1;
+  static constexpr int TILE = BN * D;          // K: BN x D bytes; V^T: D x BN bytes
+  static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 1 / 2
+  static constexpr int KCPR = D / 16;          // K: 16-byte chunks per row
+  static_assert(D == 64 || D == 128, "head dims 64 and 128");
+  typedef float f16v __attribute__((ext_vector_type(16)));
+
+  __device__ __forceinline__ static f16v mfma(const i32x8_t &a, const i32x8_t &b,
+                                              const f16v &c) {
+    // formats 1, 1: e5m2 x e5m2; zero scale operands: the unscaled MFMA.
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 1, 1, 0, 0, 0, 0);
+  }
+  __device__ __forceinline__ static int kswz(int r) {
+    return D == 64 ? ((r >> 2) & 1) | ((r >> 3) & 2) : ((r >> 1) & 3) | ((r >> 2) & 4);
+  }
+  __device__ __forceinline__ static int vswz(int r) { return (r >> 2) & 3; }
+  // key of A row R of the S^T MFMA
+  __device__ __forceinline__ static int pi(int R) {
+    return 16 * ((R >> 2) & 1) + 4 * (R >> 3) + (R & 3);
+  }
+
+  // Q rows as MFMA B operands: bytes 64 c + 32 (l/32) .. +31 of row m.
+  struct QF {
+    i32x8_t v[D / 64];
+  };
+  typedef i32x8_t PF;
+
+  __device__ __forceinline__ static void load_q(const uint8_t *Qh, int64_t m, int64_t sm,
+                                                QF &qf) {
+    const int g = (threadIdx.x & 63) >> 5;
+#pragma unroll
+    for (int c = 0; c < D / 64; ++c) {
+      const i32x4_t *src = reinterpret_cast<const i32x4_t *>(Qh + m * sm + 64 * c + 32 * g);
+      const i32x4_t lo = src[0], hi = src[1];
+      qf.v[c] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+  }
+  __device__ __forceinline__ static uint32_t k_bytes(int64_t n_ctx, int64_t sm) {
+    return (uint32_t)((n_ctx - 1) * sm + D);
+  }
+  // v is [HEAD_DIM][N_CTX] per head (key-contiguous), sm the dim stride.
+  __device__ __forceinline__ static uint32_t v_bytes(int64_t n_ctx, int64_t sm) {
+    return (uint32_t)((D - 1) * sm + n_ctx);
+  }
+
+  __device__ __forceinline__ static void dma16(uint32_t voff, const i32x4_t &rsrc, uint32_t soff,
+                                               uint32_t lds) {
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff),
+                 "{m0}"(lds)
+                 : "memory");
+  }
+  // Per-lane source offsets of the wave's DMA loads: load u of wave w fills
+  // 1 KiB of LDS.  K: rows 1024/D (DMA w + u) + i/KCPR of D bytes; V^T: dim
+  // rows 16 (DMA w + u) + i/4 of 64 bytes.  Lane i's chunk position holds the
+  // source chunk (position ^ swizzle(row)).
+  __device__ __forceinline__ static void kv_offsets(int wave, int64_t k_sm, int64_t v_sm,
+                                                    uint32_t (&ko)[DMA], uint32_t (&vo)[DMA]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int u = 0; u < DMA; ++u) {
+      const int kr = (1024 / D) * (DMA * wave + u) + lane / KCPR, kp = lane % KCPR;
+      ko[u] = (uint32_t)(kr * k_sm + 16 * (kp ^ kswz(kr)));
+      const int vr = 16 * (DMA * wave + u) + lane / 4, vp = lane % 4;
+      vo[u] = (uint32_t)(vr * v_sm + 16 * (vp ^ vswz(vr)));
+    }
+  }
+  // K block j: rows j BN .. of the key-major K; V block j: bytes j BN .. of
+  // every dim row.
+  __device__ __forceinline__ static void issue_k(const i32x4_t &rsrc, const uint32_t (&off)[DMA],
+                                                 int64_t sm, int j, uint32_t lds, int wave) {
+#pragma unroll
+    for (int u = 0; u < DMA; ++u)
+      dma16(off[u], rsrc, (uint32_t)((int64_t)j * BN * sm), lds + (DMA * wave + u) * 1024);
+  }
+  __device__ __forceinline__ static void issue_v(const i32x4_t &rsrc, const uint32_t (&off)[DMA],
+                                                 int64_t, int j, uint32_t lds, int wave) {
+#pragma unroll
+    for (int u = 0; u < DMA; ++u)
+      dma16(off[u], rsrc, (uint32_t)(j * BN), lds + (DMA * wave + u) * 1024);
+  }
+
+  // Per-lane LDS addresses (slot 0) of the fragment reads; the key block b
+  // and dim block bd enter as immediate offsets (the swizzles do not depend
+  // on key bit 5 or dim bit 5):
+  //   K, dim chunk pair c, half e: key pi(l%32), chunk 4c + 2(l/32) + e;
+  //   V^T, half e: dim l%32, chunk l/32 + 2e.
+  struct Bases {
+    uint32_t k[D / 64][2], v[2];
+  };
+  __device__ __forceinline__ static void bases(uint32_t k_lds, uint32_t v_lds, Bases &bs) {
+    const int lane = threadIdx.x & 63, g = lane >> 5, r = lane & 31;
+    const int key = pi(r);
+#pragma unroll
+    for (int c = 0; c < D / 64; ++c)
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        bs.k[c][e] = k_lds + key * D + 16 * ((4 * c + 2 * g + e) ^ kswz(key));
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+      bs.v[e] = v_lds + r * BN + 16 * ((g + 2 * e) ^ vswz(r));
+  }
+
+  __device__ __forceinline__ static i32x4_t lds16(uint32_t a) {
+    typedef __attribute__((address_space(3))) i32x4_t lds_i32x4;
+    return *(const lds_i32x4 *)(uintptr_t)a;
+  }
+  template <int SLOT>
+  __device__ __forceinline__ static i32x8_t read_k(const Bases &bs, int b, int c) {
+    const uint32_t o = SLOT * TILE + b * 32 * D;
+    const i32x4_t lo = lds16(bs.k[c][0] + o), hi = lds16(bs.k[c][1] + o);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  }
+  template <int SLOT>
+  __device__ __forceinline__ static i32x8_t read_v(const Bases &bs, int bd) {
+    const uint32_t o = SLOT * TILE + bd * 32 * BN;
+    const i32x4_t lo = lds16(bs.v[0] + o), hi = lds16(bs.v[1] + o);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  }
+
+  __device__ __forceinline__ static float xmax(float v) { return AttnFwd<HD, false>::xmax(v); }
+  __device__ __forceinline__ static float xsum(float v) { return AttnFwd<HD, false>::xsum(v); }
+
+  // S^T block of the keys in K slot SLOT: lane holds query row l%32.
+  template <int SLOT>
+  __device__ __forceinline__ static void qk(const Bases &bs, const QF &qf, f16v (&s)[BN / 32]) {
+    i32x8_t kf[BN / 32][D / 64];
+#pragma unroll
+    for (int b = 0; b < BN / 32; ++b)
+#pragma unroll
+      for (int c = 0; c < D / 64; ++c)
+        kf[b][c] = read_k<SLOT>(bs, b, c);
+#pragma unroll
+    for (int b = 0; b < BN / 32; ++b) {
+      s[b] = f16v{};
+#pragma unroll
+      for (int c = 0; c < D / 64; ++c)
+        s[b] = mfma(kf[b][c], qf.v[c], s[b]);
+    }
+  }
+
+  // Softmax of one block (the tutorial's arithmetic) for the lane's query
+  // row m, keys n0 + 32 b + 16 g + r: updates m_i and l_i, rescales acc by
+  // alpha and returns P as e5m2 bytes in key order.  MASK: on-band form.
+  template <bool MASK>
+  __device__ __forceinline__ static void softmax(f16v (&s)[BN / 32], int n0, int m,
+                                                 float qk_scale, f16v (&acc)[D / 32],
+                                                 float &m_i, float &l_i, PF &pf) {
+    const int g = (threadIdx.x & 63) >> 5;
+    float m_ij;
+    if constexpr (MASK) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < BN / 32; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+#pragma clang fp contract(off)
+          const int n = n0 + 32 * b + 16 * g + r;
+          float t = s[b][r] * qk_scale;
+          t = t + (m >= n ? 0.0f : -1.0e6f);
+          s[b][r] = t;
+          mx = fmaxf(mx, t);
+        }
+      m_ij = fmaxf(m_i, xmax(mx));
+#pragma unroll
+      for (int b = 0; b < BN / 32; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          s[b][r] = __builtin_amdgcn_exp2f(s[b][r] - m_ij);
+    } else {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < BN / 32; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          mx = fmaxf(mx, s[b][r]);
+      m_ij = fmaxf(m_i, xmax(mx) * qk_scale);
+#pragma unroll
+      for (int b = 0; b < BN / 32; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          s[b][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[b][r], qk_scale, -m_ij));
+    }
+    float l_ij = 0.f;
+#pragma unroll
+    for (int b = 0; b < BN / 32; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        l_ij += s[b][r];
+    l_ij = xsum(l_ij);
+    const float alpha = __builtin_amdgcn_exp2f(m_i - m_ij);
+    l_i = l_i * alpha + l_ij;
+    m_i = m_ij;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      const int b = w / 4, r = 4 * (w % 4);
+      const int lo = __builtin_amdgcn_cvt_pk_bf8_f32(s[b][r], s[b][r + 1], 0, false);
+      pf[w] = __builtin_amdgcn_cvt_pk_bf8_f32(s[b][r + 2], s[b][r + 3], lo, true);
+    }
+#pragma unroll
+    for (int bd = 0; bd < D / 32; ++bd)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        acc[bd][r] *= alpha;
+  }
+
+  // O^T += V^T . P^T for the values in V slot SLOT.
+  template <int SLOT>
+  __device__ __forceinline__ static void pv(const Bases &bs, const PF &pf,
+                                            f16v (&acc)[D / 32]) {
+    i32x8_t vf[D / 32];
+#pragma unroll
+    for (int bd = 0; bd < D / 32; ++bd)
+      vf[bd] = read_v<SLOT>(bs, bd);
+#pragma unroll
+    for (int bd = 0; bd < D / 32; ++bd)
+      acc[bd] = mfma(vf[bd], pf, acc[bd]);
+  }
+
+  // O = e5m2(acc / l_i), round to nearest even.  Lane l holds, per dim block
+  // bd and register quad q, dims 32 bd + 8 q + 4 (l/32) .. +3 of row m: one
+  // 4-byte store each.
+  __device__ __forceinline__ static void store_o(const f16v (&acc)[D / 32], float l_i,
+                                                 uint8_t *Orow) {
+    const int g = (threadIdx.x & 63) >> 5;
+#pragma unroll
+    for (int bd = 0; bd < D / 32; ++bd)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        int w = __builtin_amdgcn_cvt_pk_bf8_f32(acc[bd][4 * q] / l_i, acc[bd][4 * q + 1] / l_i,
+                                                0, false);
+        w = __builtin_amdgcn_cvt_pk_bf8_f32(acc[bd][4 * q + 2] / l_i, acc[bd][4 * q + 3] / l_i, w,
+                                            true);
+        *reinterpret_cast<int *>(Orow + 32 * bd + 8 * q + 4 * g) = w;
+      }
+  }
+};
+
+template <bool CAUSAL, int HD>
+__global__ void __launch_bounds__(256, 2) attn_fwd8_kernel(AttnArgs p) {
+  attn_fwd_body<CAUSAL, AttnFwd8<HD>>(p);
+}
+
+} // namespace txk

@@ -214,7 +214,8 @@ def enumerate_passes():
 
 def attn_plan(Z, H, N_CTX, head_dim, causal, sm_scale, dtype=F16, strides=None, block=(0, 0)):
     """Plan the fused attention forward.  strides: {"q": (sz, sh, sm), ...}
-    in elements (missing tensors: packed)."""
+    in elements (missing tensors: packed); for dtype F8E5M2, v's are (batch,
+    head, head-dim row) of its key-contiguous storage."""
     d = AttnDesc()
     d.Z, d.H, d.N_CTX, d.head_dim, d.dtype = Z, H, N_CTX, head_dim, dtype
     d.causal, d.sm_scale = int(bool(causal)), sm_scale

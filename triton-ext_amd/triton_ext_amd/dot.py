@@ -183,8 +183,12 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
 def attention(q, k, v, causal, sm_scale, return_lse=False, plan=None, stream=None):
     """Forward of the fused-attention tutorial's `attention(q, k, v, causal,
     sm_scale)` (R:pass/LoopSplit/06-fused-attention.py:583-640) on the
-    MI355X kernel: q, k, v fp16 (or bf16) [Z, H, N_CTX, HEAD_DIM], head dim
-    64 or 128 and contiguous.  Returns o (and M, the base-2 logsumexp [Z, H, N_CTX] the
+    MI355X kernel: q, k, v [Z, H, N_CTX, HEAD_DIM], head dim 64 or 128, in
+    fp16 or bf16 (head dim contiguous), or in float8_e5m2 as the tutorial's
+    fp8 provider passes them (:774-779): q and k head-dim contiguous, v
+    key-contiguous (stride 1 along N_CTX, "when v is in float8_e5m2 it is
+    transposed", :586).  o has q's type; p is rounded to it before p @ v
+    (:81-84).  Returns o (and M, the base-2 logsumexp [Z, H, N_CTX] the
     tutorial saves for its backward, with return_lse=True).  Shape checks
     follow the tutorial's asserts.
     """
@@ -195,21 +199,27 @@ def attention(q, k, v, causal, sm_scale, return_lse=False, plan=None, stream=Non
     HEAD_DIM = q.shape[-1]
     if HEAD_DIM not in {16, 32, 64, 128, 256}:
         raise ValueError(f"HEAD_DIM {HEAD_DIM} not in {{16, 32, 64, 128, 256}}")
-    if q.dtype not in (torch.float16, torch.bfloat16):
-        raise NotImplementedError(f"q: fp16 and bf16 are implemented, got {q.dtype}")
+    fp8 = q.dtype == torch.float8_e5m2
+    if q.dtype not in (torch.float16, torch.bfloat16) and not fp8:
+        raise NotImplementedError(f"q: fp16, bf16 and float8_e5m2 are implemented, got {q.dtype}")
     for t, nm in ((k, "k"), (v, "v")):
         if t.dtype != q.dtype:
             raise ValueError(f"{nm} is {t.dtype}, q is {q.dtype}")
-    for t, nm in ((q, "q"), (k, "k"), (v, "v")):
+    for t, nm in ((q, "q"), (k, "k")) + ((() if fp8 else ((v, "v"),))):
         if t.stride(3) != 1:
             raise ValueError(f"{nm}: the head dimension must be contiguous")
+    if fp8 and v.stride(2) != 1:
+        raise ValueError("v: float8_e5m2 v must be key-contiguous (stride 1 along N_CTX), "
+                         "as v.permute(0, 1, 3, 2).contiguous().permute(0, 1, 3, 2) makes it")
     Z, H, N = q.shape[:3]
     o = torch.empty_like(q, memory_format=torch.contiguous_format)
     M = torch.empty((Z, H, N), device=q.device, dtype=torch.float32)
     if plan is None:
         st = {nm: (t.stride(0), t.stride(1), t.stride(2)) for nm, t in
               (("q", q), ("k", k), ("v", v), ("o", o))}
-        dt = capi.BF16 if q.dtype == torch.bfloat16 else capi.F16
+        if fp8:
+            st["v"] = (v.stride(0), v.stride(1), v.stride(3))  # dim rows of N_CTX keys
+        dt = capi.F8E5M2 if fp8 else capi.BF16 if q.dtype == torch.bfloat16 else capi.F16
         plan = capi.attn_plan(Z, H, N, HEAD_DIM, causal, sm_scale, dtype=dt, strides=st)
     if stream is None:
         stream = torch.cuda.current_stream(q.device).cuda_stream
