@@ -5,6 +5,7 @@ Bars: o within 1e-2 absolute of the reference (the tutorial's test_op,
 R:pass/LoopSplit/06-fused-attention.py:698-718) and, against the oracle,
 within 2^-8 (two fp16 ulps at |o| ~ 1: p is rounded to fp16 on both sides,
 exp2 and the summation orders differ); M (base-2 logsumexp) within 1e-4.
+e5m2 (the tutorial's fp8 provider): see check_e5m2.
 """
 import os
 
