@@ -501,9 +501,13 @@ def main():
                 print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s "
                       f"({100 * r['frac']:.1f}% of fp8 peak)", file=sys.stderr, flush=True)
 
-    if want("attn_d128"):  # head dim 128 (beyond the tutorial's 64)
+    if want("attn_d128"):  # head dim 128 (beyond the tutorial's 64), fp16 and e5m2
         for causal in (True, False):
             r = bench_attn(tx, dev, 4096, causal, args.steps, args.warmup, Z=4, H=16, D=128)
+            secondary.append(r)
+            print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+            r = bench_attn(tx, dev, 4096, causal, args.steps, args.warmup, Z=4, H=16, D=128,
+                           dtype=torch.float8_e5m2)
             secondary.append(r)
             print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
             if want("vendor") or want("attn_vendor"):

@@ -278,6 +278,9 @@ def test_dot_scaled_argument_checks():
         tx.dot_scaled(a, sa, "e2m1", b, sb, "e4m3")  # lhs packs 256, rhs 128
     with pytest.raises(NotImplementedError):
         tx.dot_scaled(a, sa, "e4m3", b, sb, "e4m3", acc=torch.zeros(64, 32))
+    # a scale of None is accepted (unit scales); shapes are still checked
+    with pytest.raises(ValueError, match="Reduction dimension"):
+        tx.dot_scaled(a, None, "e2m1", b, None, "e4m3")
 
 
 def test_launch_without_device_fails_cleanly():

@@ -172,3 +172,26 @@ def test_mx_4096_sampled_rows(gpu, fmt):
     ref = ref_of(cs, rows=rows)
     check_mx(got[rows], ref, cs, "f32", f"mx 4096 {fmt} sampled", rows=rows)
     assert np.isfinite(got).all()
+
+
+@pytest.mark.parametrize("fa,fb,none", [("e4m3", "e4m3", "lhs"), ("e2m1", "e2m1", "rhs"),
+                                        ("e5m2", "e4m3", "both")])
+def test_mx_scale_none(gpu, fa, fb, none):
+    """A scale of None leaves its operand unscaled (T:language/semantic.py
+    :1625-1626): bit-identical to passing e8m0 127 (2^0) for it, and within
+    the hardware bound of the oracle given those unit scales."""
+    import torch
+    say(f"dot_scaled scale None ({none}) {fa} x {fb}")
+    cs = mx_case(160, 272, 320, fa, fb, seed=31)
+    if none in ("lhs", "both"):
+        cs["sa"] = np.full_like(cs["sa"], 127)
+    if none in ("rhs", "both"):
+        cs["sb"] = np.full_like(cs["sb"], 127)
+    dev = lambda x: to_device(x, gpu)
+    c = tx.dot_scaled(dev(cs["a"]), None if none in ("lhs", "both") else dev(cs["sa"]), fa,
+                      dev(cs["b"]), None if none in ("rhs", "both") else dev(cs["sb"]), fb)
+    torch.cuda.synchronize()
+    got = from_device(c)
+    want = run_gpu(gpu, cs)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    check_mx(got, ref_of(cs), cs, "f32", f"scale None ({none})")

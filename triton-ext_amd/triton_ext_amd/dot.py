@@ -118,10 +118,11 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
     float8_e4m3fn / float8_e5m2 or their uint8 bits.  lhs_scale uint8
     [M, K/32] and rhs_scale uint8 [N, K/32] hold e8m0 exponents (2^(s-127)),
     rhs_scale indexed by column first and not transposed.  Returns fp32 (or
-    bf16 with out_dtype=torch.bfloat16) [M, N].  Checks follow
-    T:language/semantic.py:1597-1665; what this backend does not implement
-    (bf16/fp16 formats, scales of None, e2m1 mixed with fp8, packing along M
-    or N, `acc`) raises NotImplementedError.
+    bf16 with out_dtype=torch.bfloat16) [M, N].  A scale of None leaves that
+    operand unscaled (T:language/semantic.py:1625-1626): it runs as e8m0 127
+    (2^0), which is exact.  Checks follow T:language/semantic.py:1597-1665;
+    what this backend does not implement (bf16/fp16 formats, e2m1 mixed with
+    fp8, packing along M or N, `acc`) raises NotImplementedError.
     """
     import torch
     for name, fmt in (("lhs_format", lhs_format), ("rhs_format", rhs_format)):
@@ -129,8 +130,6 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
             raise ValueError(f"NYI: {name} {fmt}")
         if fmt not in _MX_FORMATS:
             raise NotImplementedError(f"{name} {fmt}: only e4m3, e5m2 and e2m1 are implemented")
-    if lhs_scale is None or rhs_scale is None:
-        raise NotImplementedError("both operands need e8m0 scales")
     if acc is not None:
         raise NotImplementedError("acc: accumulate into the result on the caller's side")
     if not lhs_k_pack or not rhs_k_pack:
@@ -145,6 +144,11 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
     if rhs.shape[0] * pb != K:
         raise ValueError("Reduction dimension should pack the same number of elements; "
                          f"(lhs: {tuple(lhs.shape)} vs rhs: {tuple(rhs.shape)})")
+    # scale None: the operand is unscaled, i.e. e8m0 127 (2^0) in every group
+    if lhs_scale is None:
+        lhs_scale = torch.full((M, K // 32), 127, dtype=torch.uint8, device=lhs.device)
+    if rhs_scale is None:
+        rhs_scale = torch.full((N, K // 32), 127, dtype=torch.uint8, device=rhs.device)
     if tuple(lhs_scale.shape) != (M, K // 32):
         raise ValueError(f"lhs_scale must be a tensor of shape [{M}, {K // 32}]. "
                          f"Got {list(lhs_scale.shape)}")
