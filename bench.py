@@ -50,7 +50,8 @@ def parse():
     ap.add_argument("--only", default="",
                     help="secondary workloads to run, comma-separated: c1, vendor, tail, w8a8 (or "
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256), int8, fp8, kmajor, mx (or mxfp8, mxfp4, "
-                         "mxfp8_4096, mxfp8_8192, mxfp4_4096, mxfp4_8192), attn (or attn_1024, attn_4096, "
+                         "mxfp8_4096, mxfp8_8192, mxfp4_4096, mxfp4_8192), mxbf16 (or mxbf16_fp4, mxbf16_fp8: "
+                         "bf16 x MX), attn (or attn_1024, attn_4096, "
                          "attn_16384; attn_fp8 or attn_fp8_<N> for e5m2; attn_d128 for head dim 128; "
                          "attn_vendor adds torch sdpa beside each) "
                          "(default: all); "
@@ -305,6 +306,37 @@ def bench_mx(tx, dev, M, N, K, fmt, steps, warmup, seed=7):
                           tile=[p.desc.block_m, p.desc.block_n, p.desc.block_k]))
 
 
+def bench_mx_bf16(tx, dev, M, N, K, fmt, steps, warmup, seed=8):
+    """tl.dot_scaled(A bf16, None, "bf16", B, sb, fmt), fp32 C: B upcast to
+    bf16 in the workspace, then the bf16 tile; both launches timed."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    a = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
+    qbt, sb = mx_quantize(torch.randn((N, K), generator=g, device=dev), fmt)
+    qb = qbt.t().contiguous()
+    c = torch.empty((M, N), dtype=torch.float32, device=dev)
+    tf = tx.F8E4M3 if fmt == "e4m3" else tx.F4E2M1
+    p = tx.plan(tx.make_desc(M, N, K, tx.BF16, tx.F32, b_type=tf, scale_mode=tx.SCALE_MX32))
+    ws = torch.empty(int(p.workspace_bytes), dtype=torch.uint8, device=dev)
+    L = tx.load()
+    args = (ctypes.byref(p), a.data_ptr(), qb.data_ptr(), c.data_ptr(), None, sb.data_ptr(),
+            ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+
+    def run():
+        rc = L.tx_dot_launch(*args)
+        if rc != 0:
+            raise RuntimeError(L.tx_get_last_error().decode())
+    ms = time_back_to_back(run, steps, warmup)
+    flops = 2.0 * M * N * K
+    name = "mxfp8 e4m3" if fmt == "e4m3" else "mxfp4 e2m1"
+    return dict(workload=f"tl.dot_scaled bf16 x {name} (upcast + bf16 tile) {M}x{N}x{K}, "
+                         f"fp32 C", ms=ms, tflops=flops / ms / 1e9,
+                frac=flops / ms / 1e-3 / PEAK_BF16,
+                plan=dict(kernel=L.tx_kernel_name(p.kernel).decode(),
+                          tile=[p.desc.block_m, p.desc.block_n, p.desc.block_k]))
+
+
 def bench_attn(tx, dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9, dtype=None):
     """Fused attention forward, the tutorial's bench_flash_attention "fwd"
     configuration (R:pass/LoopSplit/06-fused-attention.py:737-795): fp16
@@ -478,6 +510,13 @@ def main():
                 print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s "
                       f"({100 * r['frac']:.1f}% of {r['peak_tflops']:.0f})", file=sys.stderr,
                       flush=True)
+
+    for fmt, short in (("e2m1", "mxbf16_fp4"), ("e4m3", "mxbf16_fp8")):
+        if want("mxbf16") or want(short):
+            r = bench_mx_bf16(tx, dev, 4096, 4096, 4096, fmt, args.steps, args.warmup)
+            secondary.append(r)
+            print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s "
+                  f"({100 * r['frac']:.1f}% of bf16 peak)", file=sys.stderr, flush=True)
 
     for n in (1024, 4096, 16384):
         if want("attn") or want(f"attn_{n}"):

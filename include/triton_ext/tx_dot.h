@@ -73,7 +73,13 @@ typedef enum tx_scale_mode {
    * column first, as tl.dot_scaled's rhs_scale; not transposed), both
    * row-major and packed, 4-byte aligned.  Scale 0xFF is NaN.  Operands
    * e4m3 / e5m2 (either mix) or e2m1 on both sides; K % 32 == 0; C fp32 or
-   * bf16 (round to nearest even). */
+   * bf16 (round to nearest even).
+   * One operand may instead be TX_BF16 with no scale (its scale pointer is
+   * not read): the MX operand is upcast to bf16, bf16(x * 2^(s - 127)) to
+   * nearest even, and a bf16 dot with fp32 accumulation runs on it, as
+   * tl.dot_scaled specifies (T:language/core.py:2072-2076).  The upcast goes
+   * to the workspace (plan->workspace_bytes: the MX operand at 2 bytes per
+   * element). */
   TX_SCALE_MX32 = 3,
 } tx_scale_mode;
 
@@ -100,6 +106,8 @@ typedef enum tx_kernel {
   TX_KERNEL_DECODE_I8 = 3,  /* int8 W8A8 M <= 256 streaming, MFMA 16x16x64       */
   TX_KERNEL_GEMM_F8 = 4,    /* fp8 e4m3 tile, MFMA 16x16x128 (32x32x64 small)    */
   TX_KERNEL_GEMM_MX = 5,    /* MX fp8 / fp4 tile, scaled MFMA 16x16x128 (e8m0)   */
+  TX_KERNEL_GEMM_MX_BF16 = 6, /* MX x bf16: MX operand upcast to bf16 in the
+                               * workspace, then the bf16 tile              */
 } tx_kernel;
 
 /* Bit flags for tx_dot_desc.flags */

@@ -164,15 +164,17 @@ def dot_scaled(a, sa, a_fmt, b, sb, b_fmt, *, K, c_type=F32, round_mode=ROUND_RN
                nthreads=0):
     """tl.dot_scaled on the CPU.
 
-    a: uint8 [M, K] codes (e2m1: [M, K/2] packed bytes); b: uint8 [K, N]
-    (e2m1: [K/2, N], packed along K); sa: uint8 [M, K/32]; sb: uint8
-    [N, K/32].  Returns fp32 [M, N] (c_type F32) or bf16 bits (BF16).
+    a: uint8 [M, K] codes (e2m1: [M, K/2] packed bytes; a_fmt BF16: uint16
+    bf16 bits, sa None); b: uint8 [K, N] (e2m1: [K/2, N], packed along K;
+    b_fmt BF16: uint16 bits, sb None); sa: uint8 [M, K/32]; sb: uint8
+    [N, K/32].  With a bf16 side the MX side is upcast to bf16 first.
+    Returns fp32 [M, N] (c_type F32) or bf16 bits (BF16).
     """
-    a = np.ascontiguousarray(a, dtype=np.uint8)
-    b = np.ascontiguousarray(b, dtype=np.uint8)
-    sa = np.ascontiguousarray(sa, dtype=np.uint8)
-    sb = np.ascontiguousarray(sb, dtype=np.uint8)
+    a = np.ascontiguousarray(a, dtype=np.uint16 if a_fmt == BF16 else np.uint8)
+    b = np.ascontiguousarray(b, dtype=np.uint16 if b_fmt == BF16 else np.uint8)
     M, N = a.shape[0], b.shape[1]
+    sa = np.zeros((M, K // 32), np.uint8) if sa is None else np.ascontiguousarray(sa, np.uint8)
+    sb = np.zeros((N, K // 32), np.uint8) if sb is None else np.ascontiguousarray(sb, np.uint8)
     assert sa.shape == (M, K // 32) and sb.shape == (N, K // 32), (sa.shape, sb.shape)
     assert a.shape[1] == (K // 2 if a_fmt == F4E2M1 else K)
     assert b.shape[0] == (K // 2 if b_fmt == F4E2M1 else K)

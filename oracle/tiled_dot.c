@@ -320,9 +320,18 @@ static double mx_elem(const uint8_t *base, int fmt, int64_t byte, int k_odd) {
  * exact; the sum of 128-term blocks of them is exact in double for the
  * magnitudes tested) and rounded once to fp32: the exact result, against
  * which the hardware's fixed-point group sums are judged by tolerance.
- * c_type OR_BF16 rounds that fp32 value with round_mode.  Returns 0, or -1
+ * c_type OR_BF16 rounds that fp32 value with round_mode.
+ * One side may be OR_BF16 (its scale pointer is not read): tl.dot_scaled
+ * then upcasts the MX side to bf16 and runs a bf16 dot (T:language/core.py
+ * :2072-2076), so each MX element becomes bf16(x * 2^(s - 127)), rounded to
+ * nearest even through fp32 (exact except past fp32's range), and the
+ * products of bf16 values are summed exactly as above.  Returns 0, or -1
  * for an unsupported combination.
  */
+static double upcast_bf16(double v) {
+  return or_bf16_to_f32(or_f32_to_bf16((float)v, OR_ROUND_RNE));
+}
+
 int oracle_dot_scaled(const void *Av, const void *Bv, void *Cv, const uint8_t *sa,
                       const uint8_t *sb, int64_t M, int64_t N, int64_t K, int64_t lda,
                       int64_t ldb, int64_t ldc, int a_fmt, int b_fmt, int c_type,
@@ -331,8 +340,10 @@ int oracle_dot_scaled(const void *Av, const void *Bv, void *Cv, const uint8_t *s
   uint8_t *C = (uint8_t *)Cv;
   if (M < 0 || N < 0 || K < 0 || K % 32)
     return -1;
-  if ((a_fmt != OR_F8E4M3 && a_fmt != OR_F8E5M2 && a_fmt != OR_F4E2M1) ||
-      (b_fmt != OR_F8E4M3 && b_fmt != OR_F8E5M2 && b_fmt != OR_F4E2M1))
+  const int mixed = a_fmt == OR_BF16 || b_fmt == OR_BF16;
+  if ((a_fmt != OR_F8E4M3 && a_fmt != OR_F8E5M2 && a_fmt != OR_F4E2M1 && a_fmt != OR_BF16) ||
+      (b_fmt != OR_F8E4M3 && b_fmt != OR_F8E5M2 && b_fmt != OR_F4E2M1 && b_fmt != OR_BF16) ||
+      (a_fmt == OR_BF16 && b_fmt == OR_BF16))
     return -1;
   if (c_type != OR_F32 && c_type != OR_BF16)
     return -1;
@@ -347,14 +358,27 @@ int oracle_dot_scaled(const void *Av, const void *Bv, void *Cv, const uint8_t *s
     if (!arow)
       continue; /* left unwritten; the caller's C stays as it was */
     for (int64_t k = 0; k < K; ++k) {
+      if (a_fmt == OR_BF16) {
+        arow[k] = or_bf16_to_f32(((const uint16_t *)A)[m * lda + k]);
+        continue;
+      }
       const int64_t byte = a_fmt == OR_F4E2M1 ? m * (lda / 2) + k / 2 : m * lda + k;
       arow[k] = mx_elem(A, a_fmt, byte, (int)(k & 1)) * or_e8m0_to_f64(sa[m * G + k / 32]);
+      if (mixed)
+        arow[k] = upcast_bf16(arow[k]);
     }
     for (int64_t n = 0; n < N; ++n) {
       double acc = 0.0;
       for (int64_t k = 0; k < K; ++k) {
-        const int64_t byte = b_fmt == OR_F4E2M1 ? (k / 2) * ldb + n : k * ldb + n;
-        const double b = mx_elem(B, b_fmt, byte, (int)(k & 1)) * or_e8m0_to_f64(sb[n * G + k / 32]);
+        double b;
+        if (b_fmt == OR_BF16) {
+          b = or_bf16_to_f32(((const uint16_t *)B)[k * ldb + n]);
+        } else {
+          const int64_t byte = b_fmt == OR_F4E2M1 ? (k / 2) * ldb + n : k * ldb + n;
+          b = mx_elem(B, b_fmt, byte, (int)(k & 1)) * or_e8m0_to_f64(sb[n * G + k / 32]);
+          if (mixed)
+            b = upcast_bf16(b);
+        }
         acc += arow[k] * b;
       }
       const float f = (float)acc;

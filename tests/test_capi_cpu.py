@@ -246,6 +246,24 @@ def test_mx_plans():
     assert err(a_type=tx.F4E2M1, K=256, lda=264) == tx.ERR_INVALID  # 132-byte rows
     # the fp32 block-scaled mode keeps rejecting e5m2 (e4m3 only)
     assert err(a_type=tx.F8E5M2, scale_mode=tx.SCALE_BLOCK128) == tx.ERR_UNSUPPORTED
+    # MX x bf16: the MX operand upcast into the workspace, then the bf16 tile
+    for a, b in ((tx.BF16, tx.F4E2M1), (tx.BF16, tx.F8E4M3), (tx.F8E5M2, tx.BF16),
+                 (tx.F4E2M1, tx.BF16)):
+        p = tx.plan(tx.make_desc(1000, 528, 4000, a, tx.F32, b_type=b, scale_mode=MX))
+        assert p.kernel == tx.KERNEL_GEMM_MX_BF16
+        q = tx.plan(tx.make_desc(1000, 528, 4000, tx.BF16, tx.F32))  # the bf16 dot's tile
+        assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == \
+            (q.desc.block_m, q.desc.block_n, q.desc.block_k)
+        assert (p.k_main_steps, p.k_tail, p.grid_x) == (q.k_main_steps, q.k_tail, q.grid_x)
+        mx_elems = 4000 * 528 if b != tx.BF16 else 1000 * 4000
+        assert p.workspace_bytes == (mx_elems * 2 + 255) // 256 * 256
+        bits = {tx.BF16: 16, tx.F4E2M1: 4, tx.F8E4M3: 8, tx.F8E5M2: 8}
+        scale_rows = 528 if b != tx.BF16 else 1000  # only the MX side is scaled
+        assert p.bytes == 1000 * 4000 * bits[a] / 8 + 4000 * 528 * bits[b] / 8 + \
+            scale_rows * 125 + 1000 * 528 * 4
+        assert p.peak_flops == pytest.approx(2516.6e12)
+    assert err(a_type=tx.BF16, b_type=tx.BF16) == tx.ERR_UNSUPPORTED  # bf16 on both sides
+    assert err(a_type=tx.F16, b_type=tx.F4E2M1) == tx.ERR_UNSUPPORTED  # fp16 side
 
 
 def test_fp8_e5m2_plans():
@@ -271,7 +289,7 @@ def test_dot_scaled_argument_checks():
     with pytest.raises(ValueError, match="NYI: lhs_format"):
         tx.dot_scaled(a, sa, "e3m4", b, sb, "e4m3")
     with pytest.raises(NotImplementedError):
-        tx.dot_scaled(a, sa, "bf16", b, sb, "e4m3")
+        tx.dot_scaled(a, sa, "fp16", b, sb, "e4m3")
     with pytest.raises(ValueError, match=r"rhs_scale must be a tensor of shape \[32, 4\]"):
         tx.dot_scaled(a, sa, "e4m3", b, sb.t().contiguous(), "e4m3")
     with pytest.raises(ValueError, match="Reduction dimension"):
@@ -281,6 +299,16 @@ def test_dot_scaled_argument_checks():
     # a scale of None is accepted (unit scales); shapes are still checked
     with pytest.raises(ValueError, match="Reduction dimension"):
         tx.dot_scaled(a, None, "e2m1", b, None, "e4m3")
+    # bf16 operands: a torch.bfloat16 tensor and no scale; fp16 is not built
+    abf = torch.zeros(64, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="no scale"):
+        tx.dot_scaled(abf, sa, "bf16", b, sb, "e4m3")
+    with pytest.raises(ValueError, match="no scale"):
+        tx.dot_scaled(a, None, "bf16", b, sb, "e4m3")  # uint8 tensor named bf16
+    with pytest.raises(NotImplementedError):
+        tx.dot_scaled(abf.half(), None, "fp16", b, sb, "e4m3")
+    with pytest.raises(NotImplementedError):
+        tx.dot_scaled(abf, None, "bf16", abf.t().contiguous(), None, "bf16")
 
 
 def test_launch_without_device_fails_cleanly():

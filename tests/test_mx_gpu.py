@@ -195,3 +195,85 @@ def test_mx_scale_none(gpu, fa, fb, none):
     want = run_gpu(gpu, cs)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     check_mx(got, ref_of(cs), cs, "f32", f"scale None ({none})")
+
+
+# --- MX x bf16: the MX operand upcast to bf16, then the bf16 tile -----------
+
+def upcast_bf16(codes, scales, fmt, side):
+    """The MX operand as bf16 (T:language/core.py:2072-2076): decode *
+    2^(s - 127), rounded to nearest even by torch's float32 -> bfloat16.
+    side "b": codes [K, N] unpacked, scales [N, K/32]; "a": [M, K], [M, K/32]."""
+    import torch
+    v = oracle.mx_decode(codes, FMT[fmt])
+    K = codes.shape[0] if side == "b" else codes.shape[1]
+    g = np.arange(K) // 32
+    s = scales[:, g].T if side == "b" else scales[:, g]
+    x = (v * np.exp2(s.astype(np.float64) - 127)).astype(np.float32)
+    return torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def mx_bf16_case(M, N, K, side, fmt, seed):
+    import torch
+    rng = np.random.default_rng(seed)
+    bf = lambda shape: torch.from_numpy(rng.standard_normal(shape).astype(np.float32)) \
+        .to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    if side == "b":
+        a16 = bf((M, K))
+        c = codes(rng, (K, N), fmt)
+        s = rng.integers(117, 138, size=(N, K // 32)).astype(np.uint8)
+        return dict(a16=a16, b=pack(c, 0) if fmt == "e2m1" else c, codes=c, s=s,
+                    b16=upcast_bf16(c, s, fmt, "b"))
+    b16 = bf((K, N))
+    c = codes(rng, (M, K), fmt)
+    s = rng.integers(117, 138, size=(M, K // 32)).astype(np.uint8)
+    return dict(b16=b16, a=pack(c, 1) if fmt == "e2m1" else c, codes=c, s=s,
+                a16=upcast_bf16(c, s, fmt, "a"))
+
+
+@pytest.mark.parametrize("side,fmt", [("b", "e2m1"), ("b", "e4m3"), ("b", "e5m2"),
+                                      ("a", "e2m1"), ("a", "e4m3")])
+@pytest.mark.parametrize("out", ["f32", "bf16"])
+@pytest.mark.parametrize("M,N,K", [(300, 272, 416), (512, 512, 1024), (16, 1024, 256)])
+def test_mx_bf16_vs_oracle(gpu, side, fmt, out, M, N, K):
+    """dot_scaled with one bf16 operand against the oracle (upcast, then
+    exact products rounded once): |d| <= K 2^-24 sum |a b| (fp32 summation)
+    plus one bf16 ulp of |ref| for bf16 C; and bit-identical to the bf16 dot
+    of the host-upcast operand (the same tile on the same bf16 inputs), which
+    pins the upcast kernel bit for bit."""
+    import torch
+    say(f"dot_scaled MX x bf16 side={side} {fmt} {M}x{N}x{K} out={out}")
+    cs = mx_bf16_case(M, N, K, side, fmt, seed=M + N + K + len(fmt) + (side == "a"))
+    dev = lambda x, dt=None: to_device(x, gpu) if dt is None else \
+        to_device(x.view(np.int16), gpu).view(dt)
+    odt = torch.bfloat16 if out == "bf16" else torch.float32
+    if side == "b":
+        c = tx.dot_scaled(dev(cs["a16"], torch.bfloat16), None, "bf16", dev(cs["b"]),
+                          dev(cs["s"]), fmt, out_dtype=odt)
+        ref = oracle.dot_scaled(cs["a16"], None, oracle.BF16, cs["b"], cs["s"], FMT[fmt], K=K,
+                                c_type=oracle.BF16 if out == "bf16" else oracle.F32)
+    else:
+        c = tx.dot_scaled(dev(cs["a"]), dev(cs["s"]), fmt, dev(cs["b16"], torch.bfloat16), None,
+                          "bf16", out_dtype=odt)
+        ref = oracle.dot_scaled(cs["a"], cs["s"], FMT[fmt], cs["b16"], None, oracle.BF16, K=K,
+                                c_type=oracle.BF16 if out == "bf16" else oracle.F32)
+    torch.cuda.synchronize()
+    got = from_device(c)
+    # the same bf16 tile on the host-upcast operand: bit for bit
+    d16 = tx.dot(dev(cs["a16"], torch.bfloat16), dev(cs["b16"], torch.bfloat16), out_dtype=odt)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_device(d16).view(np.int16 if out == "bf16" else np.int32),
+                          got.view(np.int16 if out == "bf16" else np.int32)), \
+        "the upcast operand differs from the host's bf16 upcast"
+    g = bits_to_f32(got, "bf16") if out == "bf16" else got
+    r = bits_to_f32(ref, "bf16") if out == "bf16" else ref
+    a = np.abs(bits_to_f32(cs["a16"], "bf16").astype(np.float64))
+    b = np.abs(bits_to_f32(cs["b16"], "bf16").astype(np.float64))
+    S = a @ b
+    bound = K * 2.0 ** -24 * S + 1e-30
+    if out == "bf16":
+        bound = bound + 2.0 ** -7 * np.abs(r.astype(np.float64))
+    d = np.abs(g.astype(np.float64) - r)
+    assert np.isfinite(g).all()
+    assert (d <= bound).all(), f"worst d/bound {(d / bound).max():.3g}"
+    s = math.sqrt(K) * math.sqrt(np.mean(a ** 2)) * math.sqrt(np.mean(b ** 2))
+    check_close(g, r, atol=1e-3, rtol=1e-2, scale=s, what="MX x bf16")

@@ -219,3 +219,59 @@ def test_golden_fixture_mx(path):
     b = np.abs(oracle.mx_decode(bc, fb) * np.exp2(z["sb"][:, g].T.astype(np.float64) - 127))
     bound = (K + 1) * U32 * (a @ b) + 1e-30
     assert (np.abs(got.astype(np.float64) - want) <= bound).all()
+
+
+def _e4m3_codes(rng, shape):
+    c = rng.integers(0, 256, size=shape).astype(np.uint8)
+    return np.where((c & 0x7F) == 0x7F, c & 0xF0, c).astype(np.uint8)
+
+
+@pytest.mark.parametrize("side", ["a", "b"])
+@pytest.mark.parametrize("fmt", [oracle.F4E2M1, oracle.F8E5M2])
+def test_bf16_side_reduces_to_mx(side, fmt):
+    """tl.dot_scaled with a bf16 operand (T:language/core.py:2072-2076):
+    when the bf16 values are e4m3 values and the MX side's upcast is exact
+    (moderate scales), the result equals the all-MX dot with e4m3 codes and
+    unit scales in place of the bf16 operand, bit for bit."""
+    rng = np.random.default_rng(5 + (side == "b"))
+    M, N, K = 24, 40, 96
+    e4 = _e4m3_codes(rng, (M, K) if side == "a" else (K, N))
+    bf = torch.from_numpy(e4).view(torch.float8_e4m3fn).float().to(torch.bfloat16) \
+        .view(torch.int16).numpy().view(np.uint16)
+    rows = K if fmt != oracle.F4E2M1 else K // 2
+    if side == "a":  # A bf16, B MX
+        c = rng.integers(0, 16, size=(K, N)).astype(np.uint8) if fmt == oracle.F4E2M1 else \
+            rng.integers(0, 0x7C, size=(K, N)).astype(np.uint8)
+        b = (c[0::2] | (c[1::2] << 4)).astype(np.uint8) if fmt == oracle.F4E2M1 else c
+        assert b.shape[0] == rows
+        sb = rng.integers(117, 138, size=(N, K // 32)).astype(np.uint8)
+        got = oracle.dot_scaled(bf, None, oracle.BF16, b, sb, fmt, K=K)
+        want = oracle.dot_scaled(e4, np.full((M, K // 32), 127, np.uint8), oracle.F8E4M3,
+                                 b, sb, fmt, K=K)
+    else:  # A MX, B bf16
+        c = rng.integers(0, 16, size=(M, K)).astype(np.uint8) if fmt == oracle.F4E2M1 else \
+            rng.integers(0, 0x7C, size=(M, K)).astype(np.uint8)
+        a = (c[:, 0::2] | (c[:, 1::2] << 4)).astype(np.uint8) if fmt == oracle.F4E2M1 else c
+        sa = rng.integers(117, 138, size=(M, K // 32)).astype(np.uint8)
+        got = oracle.dot_scaled(a, sa, fmt, bf, None, oracle.BF16, K=K)
+        want = oracle.dot_scaled(a, sa, fmt, e4, np.full((N, K // 32), 127, np.uint8),
+                                 oracle.F8E4M3, K=K)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_bf16_side_upcast_rounds_to_bf16():
+    """The MX side is rounded to bf16 before the products: an e4m3 subnormal
+    7 * 2^-9 scaled by 2^-127 is 7 * 2^-136, below bf16's 2^-133 quantum, so
+    it becomes torch's bf16 of that value (2^-133); 448 * 2^127 overflows to
+    inf; scale 0xFF is NaN."""
+    K = 32
+    one = torch.tensor([1.0], dtype=torch.bfloat16).view(torch.int16).numpy().view(np.uint16)[0]
+    a = np.zeros((1, K), np.uint16)
+    a[0, 3] = one
+    b = np.zeros((K, 3), np.uint8)
+    b[3] = [0x07, 0x7E, 0x38]  # e4m3: 7 * 2^-9, 448, 1.0
+    sb = np.array([[0], [254], [255]], np.uint8)
+    c = oracle.dot_scaled(a, None, oracle.BF16, b, sb, oracle.F8E4M3, K=K)[0]
+    want0 = torch.tensor([7 * 2.0 ** -136], dtype=torch.float32).to(torch.bfloat16).float().item()
+    assert want0 == 2.0 ** -133 and c[0] == np.float32(want0)
+    assert np.isposinf(c[1]) and np.isnan(c[2])

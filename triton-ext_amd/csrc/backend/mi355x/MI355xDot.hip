@@ -24,6 +24,7 @@
 
 #include "attn_fwd.h"
 #include "attn_fwd8.h"
+#include "mx_upcast.h"
 
 #include "decode_i8.h"
 #include "gemm16_dma.h"
@@ -210,10 +211,38 @@ int fmtOf(const tx_dot_desc &d) {
   return fa | (fb << 4);
 }
 
+// tl.dot_scaled with one bf16 operand: the MX operand is upcast to bf16
+// (T:language/core.py:2072-2076) and the bf16 tile runs.  1: A is the MX
+// operand, 2: B is, 0: not this form.
+int mxUpcastSide(const tx_dot_desc &d) {
+  if (d.scale_mode != TX_SCALE_MX32)
+    return 0;
+  if (d.a_type == TX_BF16 && mxFormat(d.b_type) >= 0)
+    return 2;
+  if (d.b_type == TX_BF16 && mxFormat(d.a_type) >= 0)
+    return 1;
+  return 0;
+}
+
+// Workspace of the upcast form: the MX operand as bf16, 256-byte aligned.
+int64_t mxUpcastWorkspace(const tx_dot_desc &d) {
+  const int side = mxUpcastSide(d);
+  const int64_t elems = side == 2 ? d.K * d.N : side == 1 ? d.M * d.K : 0;
+  return (elems * 2 + 255) / 256 * 256;
+}
+
 // Operand kind and epilogue of a descriptor (-1 if unsupported).
 void classify(const tx_dot_desc &d, int *op, int *epi) {
   *op = -1;
   *epi = -1;
+  if (mxUpcastSide(d)) {
+    *op = OP_BF16; // the bf16 tile on the upcast operand
+    if (d.c_type == TX_F32)
+      *epi = EPI_F32;
+    else if (d.c_type == TX_BF16)
+      *epi = EPI_BF16;
+    return;
+  }
   if (d.scale_mode == TX_SCALE_MX32) {
     const int fa = mxFormat(d.a_type), fb = mxFormat(d.b_type);
     if (fa < 0 || fb < 0 || (fa == 4) != (fb == 4))
@@ -382,7 +411,9 @@ int txMi355xDotRun(tx_dot_plan *plan) {
     return fail(TX_ERR_UNSUPPORTED, "no instantiated tile %dx%dx%d for this dtype",
                 d.block_m, d.block_n, d.block_k);
   const GemmConfig &c = kGemmConfigs[ci];
+  const bool upcast = mxUpcastSide(d) != 0;
   plan->kernel = op == OP_I8                     ? TX_KERNEL_GEMM_I8
+               : upcast                        ? TX_KERNEL_GEMM_MX_BF16
                : d.scale_mode == TX_SCALE_MX32 ? TX_KERNEL_GEMM_MX
                : op == OP_F8                   ? TX_KERNEL_GEMM_F8
                                                : TX_KERNEL_GEMM_16BIT;
@@ -390,7 +421,7 @@ int txMi355xDotRun(tx_dot_plan *plan) {
   plan->grid_x = plan->m_tiles * plan->n_tiles;
   plan->grid_y = plan->grid_z = 1;
   plan->block_threads = c.wm * c.wn * 64;
-  plan->workspace_bytes = 0;
+  plan->workspace_bytes = upcast ? mxUpcastWorkspace(d) : 0;
   plan->passes_run += 1;
   return TX_OK;
 }
@@ -460,6 +491,7 @@ extern "C" TX_API const char *tx_kernel_name(int32_t kernel) {
   case TX_KERNEL_DECODE_I8: return "decode_i8_mfma16x16x64";
   case TX_KERNEL_GEMM_F8: return "gemm_f8_mfma32x32x64";
   case TX_KERNEL_GEMM_MX: return "gemm_mx_mfma_scale16x16x128";
+  case TX_KERNEL_GEMM_MX_BF16: return "mx_upcast_bf16+gemm_16bit_mfma32x32x16";
   default: return "?";
   }
 }
@@ -580,6 +612,66 @@ int launchGemm(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   return TX_OK;
 }
 
+// tl.dot_scaled with one bf16 operand: upcast the MX operand into the
+// workspace, then the bf16 tile on (bf16 side, upcast) -- two launches on
+// one stream.
+int launchMxUpcast(const tx_dot_plan &plan, const void *A, const void *B, void *C,
+                   const void *sa, const void *sb, void *ws, size_t ws_bytes,
+                   hipStream_t stream) {
+  const tx_dot_desc &d = plan.desc;
+  const int side = mxUpcastSide(d);
+  const int64_t need = mxUpcastWorkspace(d);
+  if (!side)
+    return fail(TX_ERR_INVALID, "plan is not an MX x bf16 dot_scaled");
+  if (!ws || (int64_t)ws_bytes < need)
+    return fail(TX_ERR_WORKSPACE, "MX x bf16 needs %lld workspace bytes, got %zu",
+                (long long)need, ws_bytes);
+  if (reinterpret_cast<uintptr_t>(ws) & 15)
+    return fail(TX_ERR_INVALID, "workspace must be 16-byte aligned");
+  const int32_t mxt = side == 2 ? d.b_type : d.a_type;
+  const int fmt = mxFormat(mxt);
+  txk::UpcastArgs u;
+  u.src = static_cast<const uint8_t *>(side == 2 ? B : A);
+  u.scale = static_cast<const uint8_t *>(side == 2 ? sb : sa);
+  u.dst = static_cast<uint16_t *>(ws);
+  u.ld_scale = d.K / 32;
+  u.fmt = fmt;
+  int64_t threads;
+  if (side == 2) {
+    u.rows = d.K;
+    u.cols = d.N;
+    u.ld_src = d.ldb; // fp8: bytes per row; e2m1: bytes per packed row
+    threads = (d.K / 8) * (d.N / (fmt == 4 ? 8 : 16)); // 8 K rows per thread
+  } else {
+    u.rows = d.M;
+    u.cols = d.K;
+    u.ld_src = fmt == 4 ? d.lda / 2 : d.lda;
+    threads = d.M * (d.K / 16);
+  }
+  typedef void (*UpFn)(txk::UpcastArgs);
+  const UpFn fn = side == 2 ? (fmt == 0 ? txk::mx_upcast_b_kernel<0>
+                               : fmt == 1 ? txk::mx_upcast_b_kernel<1>
+                                          : txk::mx_upcast_b_kernel<4>)
+                            : (fmt == 0 ? txk::mx_upcast_a_kernel<0>
+                               : fmt == 1 ? txk::mx_upcast_a_kernel<1>
+                                          : txk::mx_upcast_a_kernel<4>);
+  if (threads > 0) {
+    hipLaunchKernelGGL(fn, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0, stream, u);
+    TX_HIP_CHECK(hipGetLastError());
+  }
+  // The bf16 tile over the upcast operand.
+  tx_dot_plan g = plan;
+  g.desc.a_type = TX_BF16;
+  g.desc.b_type = TX_BF16;
+  g.desc.scale_mode = TX_SCALE_NONE;
+  if (side == 2)
+    g.desc.ldb = d.N;
+  else
+    g.desc.lda = d.K;
+  g.kernel = TX_KERNEL_GEMM_16BIT;
+  return launchGemm(g, side == 1 ? ws : A, side == 2 ? ws : B, C, nullptr, nullptr, stream);
+}
+
 int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
                  const void *sa, const void *sb, void *ws, size_t ws_bytes,
                  hipStream_t stream) {
@@ -644,10 +736,14 @@ extern "C" TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A,
   if ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) |
        reinterpret_cast<uintptr_t>(C)) & 15)
     return fail(TX_ERR_INVALID, "A, B and C must be 16-byte aligned");
-  if (d.scale_mode != TX_SCALE_NONE && (!scale_a || !scale_b))
+  // MX x bf16 (dot_scaled with one bf16 operand): only the MX side is scaled
+  const int up = mxUpcastSide(d);
+  const bool need_sa = d.scale_mode != TX_SCALE_NONE && up != 2;
+  const bool need_sb = d.scale_mode != TX_SCALE_NONE && up != 1;
+  if ((need_sa && !scale_a) || (need_sb && !scale_b))
     return fail(TX_ERR_INVALID, "scaled dot needs scale_a and scale_b");
-  if (d.scale_mode != TX_SCALE_NONE &&
-      ((reinterpret_cast<uintptr_t>(scale_a) | reinterpret_cast<uintptr_t>(scale_b)) & 3))
+  if (((need_sa ? reinterpret_cast<uintptr_t>(scale_a) : 0) |
+       (need_sb ? reinterpret_cast<uintptr_t>(scale_b) : 0)) & 3)
     return fail(TX_ERR_INVALID, "scale arrays must be 4-byte aligned");
   if (!tx_device_available())
     return fail(TX_ERR_NO_DEVICE, "no gfx950 device visible");
@@ -661,6 +757,8 @@ extern "C" TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A,
   case TX_KERNEL_DECODE_I8:
     return launchDecode(*plan, A, B, C, scale_a, scale_b, workspace,
                         workspace_bytes, s);
+  case TX_KERNEL_GEMM_MX_BF16:
+    return launchMxUpcast(*plan, A, B, C, scale_a, scale_b, workspace, workspace_bytes, s);
   default:
     return fail(TX_ERR_INVALID, "plan has no kernel (kernel=%d)", plan->kernel);
   }

@@ -119,8 +119,8 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
   else if (d->scale_mode == TX_SCALE_BLOCK128)
     scaleBytes = 4.0 * (M * cdiv(d->K, 128) +
                         (double)cdiv(d->K, 128) * cdiv(d->N, 128));
-  else if (d->scale_mode == TX_SCALE_MX32)
-    scaleBytes = (M + N) * (double)cdiv(d->K, 32); // one e8m0 byte per 32 K
+  else if (d->scale_mode == TX_SCALE_MX32) // one e8m0 byte per 32 K; a bf16 side has none
+    scaleBytes = ((ba == 16 ? 0.0 : M) + (bb == 16 ? 0.0 : N)) * (double)cdiv(d->K, 32);
   out->flops = 2.0 * M * N * K;
   out->bytes = M * K * sa + K * N * sb + M * N * sc + scaleBytes;
   out->intensity = out->bytes > 0 ? out->flops / out->bytes : 0.0;
@@ -136,7 +136,9 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
 
   Tile t{d->block_m, d->block_n, d->block_k, 1.0};
   if (t.bm <= 0 || t.bn <= 0 || t.bk <= 0) {
-    if (d->scale_mode == TX_SCALE_MX32)
+    if (d->scale_mode == TX_SCALE_MX32 && (ba == 16 || bb == 16))
+      t = chooseTile(kTiles16, d->M, d->N, d->K); // MX x bf16 runs on the bf16 tile
+    else if (d->scale_mode == TX_SCALE_MX32)
       t = ba == 4 ? kTileMx4 : kTileMx8;
     else if (sa == 2 && (d->flags & TX_FLAG_B_KMAJOR))
       t = kTiles16[0]; // the K-major B kernel exists for this tile only

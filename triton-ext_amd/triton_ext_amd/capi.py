@@ -17,7 +17,7 @@ BOUND_UNKNOWN, BOUND_MFMA, BOUND_HBM = 0, 1, 2
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_NO_DEVICE, ERR_WORKSPACE, ERR_NO_PASS = range(7)
 # tx_kernel
 (KERNEL_NONE, KERNEL_GEMM_16BIT, KERNEL_GEMM_I8, KERNEL_DECODE_I8, KERNEL_GEMM_F8,
- KERNEL_GEMM_MX) = range(6)
+ KERNEL_GEMM_MX, KERNEL_GEMM_MX_BF16) = range(7)
 FLAG_NO_LOOP_SPLIT = 0x1
 FLAG_B_KMAJOR = 0x2  # B stored [N][K] row-major (a transposed view in torch)
 # TritonPluginResult

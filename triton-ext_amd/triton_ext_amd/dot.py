@@ -120,16 +120,24 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
     rhs_scale indexed by column first and not transposed.  Returns fp32 (or
     bf16 with out_dtype=torch.bfloat16) [M, N].  A scale of None leaves that
     operand unscaled (T:language/semantic.py:1625-1626): it runs as e8m0 127
-    (2^0), which is exact.  Checks follow T:language/semantic.py:1597-1665;
-    what this backend does not implement (bf16/fp16 formats, e2m1 mixed with
-    fp8, packing along M or N, `acc`) raises NotImplementedError.
+    (2^0), which is exact.  One operand may be "bf16" (a torch.bfloat16
+    tensor, no scale): the other is upcast to bf16 and a bf16 dot runs, as
+    tl.dot_scaled specifies (T:language/core.py:2072-2076).  Checks follow
+    T:language/semantic.py:1597-1665; what this backend does not implement
+    (fp16 operands, bf16 on both sides, e2m1 mixed with fp8, packing along M
+    or N, `acc`) raises NotImplementedError.
     """
     import torch
     for name, fmt in (("lhs_format", lhs_format), ("rhs_format", rhs_format)):
         if fmt not in ("e2m1", "e4m3", "e5m2", "bf16", "fp16"):
             raise ValueError(f"NYI: {name} {fmt}")
-        if fmt not in _MX_FORMATS:
-            raise NotImplementedError(f"{name} {fmt}: only e4m3, e5m2 and e2m1 are implemented")
+        if fmt not in _MX_FORMATS and fmt != "bf16":
+            raise NotImplementedError(f"{name} {fmt}: e4m3, e5m2, e2m1 and bf16 are implemented")
+    if lhs_format == "bf16" and rhs_format == "bf16":
+        raise NotImplementedError("bf16 on both sides is tl.dot, not dot_scaled")
+    for fmt, t, sc, nm in ((lhs_format, lhs, lhs_scale, "lhs"), (rhs_format, rhs, rhs_scale, "rhs")):
+        if fmt == "bf16" and (t.dtype != torch.bfloat16 or sc is not None):
+            raise ValueError(f"{nm}: a bf16 operand is a torch.bfloat16 tensor with no scale")
     if acc is not None:
         raise NotImplementedError("acc: accumulate into the result on the caller's side")
     if not lhs_k_pack or not rhs_k_pack:
@@ -145,18 +153,19 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
         raise ValueError("Reduction dimension should pack the same number of elements; "
                          f"(lhs: {tuple(lhs.shape)} vs rhs: {tuple(rhs.shape)})")
     # scale None: the operand is unscaled, i.e. e8m0 127 (2^0) in every group
-    if lhs_scale is None:
+    # (a bf16 operand has none and reads none)
+    if lhs_scale is None and lhs_format != "bf16":
         lhs_scale = torch.full((M, K // 32), 127, dtype=torch.uint8, device=lhs.device)
-    if rhs_scale is None:
+    if rhs_scale is None and rhs_format != "bf16":
         rhs_scale = torch.full((N, K // 32), 127, dtype=torch.uint8, device=rhs.device)
-    if tuple(lhs_scale.shape) != (M, K // 32):
+    if lhs_scale is not None and tuple(lhs_scale.shape) != (M, K // 32):
         raise ValueError(f"lhs_scale must be a tensor of shape [{M}, {K // 32}]. "
                          f"Got {list(lhs_scale.shape)}")
-    if tuple(rhs_scale.shape) != (N, K // 32):
+    if rhs_scale is not None and tuple(rhs_scale.shape) != (N, K // 32):
         raise ValueError(f"rhs_scale must be a tensor of shape [{N}, {K // 32}]. "
                          f"Got {list(rhs_scale.shape)}")
     for t, nm in ((lhs_scale, "lhs_scale"), (rhs_scale, "rhs_scale")):
-        if t.dtype != torch.uint8 or not t.is_contiguous():
+        if t is not None and (t.dtype != torch.uint8 or not t.is_contiguous()):
             raise ValueError(f"{nm} must be a contiguous uint8 (e8m0) tensor")
     if lhs.stride(1) != 1 or rhs.stride(1) != 1:
         raise ValueError("lhs and rhs rows must be contiguous")
@@ -167,9 +176,9 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
     if plan is None:
         lda = lhs.stride(0) * pa if M > 0 and K > 0 else 0
         ldb = rhs.stride(0) if K > 0 and N > 0 else 0
-        desc = capi.make_desc(M, N, K, _MX_FORMATS[lhs_format], c_tx,
-                              b_type=_MX_FORMATS[rhs_format], scale_mode=capi.SCALE_MX32,
-                              block=block, lda=lda, ldb=ldb)
+        desc = capi.make_desc(M, N, K, _MX_FORMATS.get(lhs_format, capi.BF16), c_tx,
+                              b_type=_MX_FORMATS.get(rhs_format, capi.BF16),
+                              scale_mode=capi.SCALE_MX32, block=block, lda=lda, ldb=ldb)
         plan = capi.plan(desc)
     if out is None:
         out = torch.empty((M, N), dtype=_torch_dtype(c_tx), device=lhs.device)
@@ -177,11 +186,33 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
         raise ValueError("output must be row-major with ldc == N")
     if stream is None:
         stream = torch.cuda.current_stream(lhs.device).cuda_stream
+    ws = _upcast_workspace(plan, lhs.device)
     L = capi.load()
     capi.check(L.tx_dot_launch(ctypes.byref(plan), lhs.data_ptr(), rhs.data_ptr(),
-                               out.data_ptr(), lhs_scale.data_ptr(), rhs_scale.data_ptr(),
-                               None, 0, stream))
+                               out.data_ptr(),
+                               None if lhs_scale is None else lhs_scale.data_ptr(),
+                               None if rhs_scale is None else rhs_scale.data_ptr(),
+                               None if ws is None else ws.data_ptr(),
+                               0 if ws is None else ws.numel(), stream))
     return out
+
+
+_upcast_workspaces = {}
+
+
+def _upcast_workspace(p, device):
+    """Workspace of an MX x bf16 dot_scaled (the upcast operand), cached per
+    device apart from the decode kernel's (whose counters it would clobber).
+    Launches that overlap on one device race on it."""
+    import torch
+    if p.workspace_bytes == 0:
+        return None
+    key = str(device)
+    ws = _upcast_workspaces.get(key)
+    if ws is None or ws.numel() < p.workspace_bytes:
+        ws = torch.empty(int(p.workspace_bytes), dtype=torch.uint8, device=device)
+        _upcast_workspaces[key] = ws
+    return ws
 
 
 def attention(q, k, v, causal, sm_scale, return_lse=False, plan=None, stream=None):
