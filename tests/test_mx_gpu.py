@@ -277,3 +277,35 @@ def test_mx_bf16_vs_oracle(gpu, side, fmt, out, M, N, K):
     assert (d <= bound).all(), f"worst d/bound {(d / bound).max():.3g}"
     s = math.sqrt(K) * math.sqrt(np.mean(a ** 2)) * math.sqrt(np.mean(b ** 2))
     check_close(g, r, atol=1e-3, rtol=1e-2, scale=s, what="MX x bf16")
+
+
+@pytest.mark.parametrize("side,fmt", [("b", "e2m1"), ("b", "e4m3"), ("b", "e5m2"),
+                                      ("a", "e2m1"), ("a", "e4m3"), ("a", "e5m2")])
+def test_mx_bf16_scale_range_bit_identity(gpu, side, fmt):
+    """Scales across [1, 239]: the upcast's pair conversion (scale exponents
+    17..239) and its element path (the rest: subnormal bf16 results) both
+    equal the host's bf16 upcast, seen through the same bf16 tile bit for
+    bit (fp32 C)."""
+    import torch
+    say(f"dot_scaled MX x bf16 scale range side={side} {fmt}")
+    M, N, K = 128, 256, 256
+    cs = mx_bf16_case(M, N, K, side, fmt, seed=77 + len(fmt) + (side == "a"))
+    rng = np.random.default_rng(3)
+    cs["s"] = rng.integers(1, 240, size=cs["s"].shape).astype(np.uint8)
+    if side == "b":
+        cs["b16"] = upcast_bf16(cs["codes"], cs["s"], fmt, "b")
+    else:
+        cs["a16"] = upcast_bf16(cs["codes"], cs["s"], fmt, "a")
+    dev = lambda x, dt=None: to_device(x, gpu) if dt is None else \
+        to_device(x.view(np.int16), gpu).view(dt)
+    if side == "b":
+        c = tx.dot_scaled(dev(cs["a16"], torch.bfloat16), None, "bf16", dev(cs["b"]),
+                          dev(cs["s"]), fmt)
+    else:
+        c = tx.dot_scaled(dev(cs["a"]), dev(cs["s"]), fmt, dev(cs["b16"], torch.bfloat16), None,
+                          "bf16")
+    d16 = tx.dot(dev(cs["a16"], torch.bfloat16), dev(cs["b16"], torch.bfloat16),
+                 out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    got, want = from_device(c), from_device(d16)
+    assert np.array_equal(got.view(np.int32), want.view(np.int32))

@@ -641,7 +641,7 @@ int launchMxUpcast(const tx_dot_plan &plan, const void *A, const void *B, void *
     u.rows = d.K;
     u.cols = d.N;
     u.ld_src = d.ldb; // fp8: bytes per row; e2m1: bytes per packed row
-    threads = (d.K / 8) * (d.N / (fmt == 4 ? 8 : 16)); // 8 K rows per thread
+    threads = (d.K / 8) * (d.N / 16); // 16 columns x 8 K rows per thread
   } else {
     u.rows = d.M;
     u.cols = d.K;

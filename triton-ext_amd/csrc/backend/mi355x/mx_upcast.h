@@ -57,17 +57,40 @@ __device__ __forceinline__ uint16_t mx_upcast1(uint32_t c, int fmt, uint32_t s) 
   return f32_to_bf16_rne(x);
 }
 
+// Hardware pair conversion: v_cvt_scalef32_pk_bf16_{fp8,bf8,fp4} decodes
+// two elements (bytes 2w, 2w + 1 of `src`, or byte `sel`'s two e2m1 nibbles)
+// and multiplies by one fp32 scale.  Used only where the scale exponent lies
+// in [17, 239]: there every result is a normal bf16 with at most 4
+// significant bits -- exact, so the instruction's rounding never applies --
+// and a zero code stays zero.  Other scales (subnormal results, overflow,
+// 0xFF) take mx_upcast1.  Returns the two bf16 as (lo, hi) halves.
+constexpr uint32_t kHwScaleLo = 17, kHwScaleHi = 239;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+template <int FMT, int SEL>
+__device__ __forceinline__ uint32_t mx_cvt_pair(uint32_t src, float scale) {
+  bf16x2_t r;
+  if constexpr (FMT == 0)
+    r = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(src, scale, SEL != 0);
+  else if constexpr (FMT == 1)
+    r = __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(src, scale, SEL != 0);
+  else
+    r = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, scale, SEL);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
 // B side: dst[k][n] = upcast(B[k][n] * 2^(scale[n][k/32] - 127)).  A
-// thread owns COLS columns and RUN consecutive source rows inside one 32-K
-// scale group, so it loads its COLS scale bytes once: fp8 16 columns x 8
-// rows, e2m1 8 columns x 4 packed rows (8 K).  Neighbouring threads take
-// neighbouring column groups (coalesced 16- / 8-byte loads, 32- / 16-byte
-// stores per row).
+// thread owns 16 columns and the source rows of 8 consecutive K inside one
+// 32-K scale group (fp8 8 rows, e2m1 4 packed rows), so it loads its 16
+// scale bytes once.  Neighbouring threads take neighbouring column groups
+// (coalesced 16-byte loads and 32-byte row stores).  B's scales vary along a row, so the pair conversion
+// runs on K pairs of one column: fp8 bytes of rows k, k + 1 are paired by
+// v_perm_b32, e2m1 bytes hold K pairs already; results are re-paired into
+// row order by v_perm_b32.
 template <int FMT>
 __global__ void __launch_bounds__(256) mx_upcast_b_kernel(UpcastArgs p) {
-  constexpr int COLS = FMT == 4 ? 8 : 16; // columns per thread
-  constexpr int RUN = FMT == 4 ? 4 : 8;   // source rows per thread
-  constexpr int KR = FMT == 4 ? 2 : 1;    // K rows per source row
+  constexpr int COLS = 16;              // columns per thread
+  constexpr int RUN = FMT == 4 ? 4 : 8; // source rows per thread (8 K)
+  constexpr int KR = FMT == 4 ? 2 : 1;  // K rows per source row
   const int64_t groups = p.cols / COLS;
   const int64_t srows = p.rows / KR; // source rows
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -76,32 +99,90 @@ __global__ void __launch_bounds__(256) mx_upcast_b_kernel(UpcastArgs p) {
   const int64_t r0 = (t / groups) * RUN, n0 = (t % groups) * COLS;
   const int64_t kg = r0 * KR / 32; // the scale group of all RUN rows
   uint32_t sc[COLS];
+  bool hw = true;
 #pragma unroll
-  for (int i = 0; i < COLS; ++i)
+  for (int i = 0; i < COLS; ++i) {
     sc[i] = p.scale[(n0 + i) * p.ld_scale + kg];
-  uint8_t code[RUN][16];
+    hw = hw && sc[i] >= kHwScaleLo && sc[i] <= kHwScaleHi;
+  }
+  uint32_t w[RUN][COLS / 4]; // source dwords: row r, columns 4 q .. +3
 #pragma unroll
   for (int r = 0; r < RUN; ++r) {
-    const uint8_t *src = p.src + (r0 + r) * p.ld_src + n0;
-    if constexpr (FMT == 4)
-      *reinterpret_cast<uint64_t *>(code[r]) = *reinterpret_cast<const uint64_t *>(src);
-    else
-      *reinterpret_cast<u32x4 *>(code[r]) = *reinterpret_cast<const u32x4 *>(src);
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(p.src + (r0 + r) * p.ld_src + n0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      w[r][q] = v[q];
   }
+  auto store_row = [&](int64_t k, const uint32_t (&o)[COLS / 2]) {
+    uint16_t *d = p.dst + k * p.cols + n0;
+#pragma unroll
+    for (int q = 0; q < COLS / 8; ++q)
+      reinterpret_cast<u32x4 *>(d)[q] = u32x4{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
+  };
+  if (hw) {
+    float sf[COLS];
+#pragma unroll
+    for (int i = 0; i < COLS; ++i)
+      sf[i] = __builtin_amdgcn_ldexpf(1.0f, (int)sc[i] - 127);
+    if constexpr (FMT == 4) {
+      // byte i of a packed row: column n0 + i, K rows 2 r and 2 r + 1
+#pragma unroll
+      for (int r = 0; r < RUN; ++r) {
+        uint32_t lo[COLS / 2], hi[COLS / 2]; // rows 2 r and 2 r + 1, column pairs
+#pragma unroll
+        for (int c = 0; c < COLS; c += 2) {
+          const uint32_t src0 = w[r][c / 4], sel0 = c % 4;
+          const uint32_t a = sel0 == 0 ? mx_cvt_pair<4, 0>(src0, sf[c])
+                           : mx_cvt_pair<4, 2>(src0, sf[c]);
+          const uint32_t b = sel0 == 0 ? mx_cvt_pair<4, 1>(src0, sf[c + 1])
+                           : mx_cvt_pair<4, 3>(src0, sf[c + 1]);
+          // a = (k, c) | (k + 1, c) << 16, b likewise for column c + 1
+          lo[c / 2] = __builtin_amdgcn_perm(b, a, 0x05040100u); // (k, c) | (k, c + 1) << 16
+          hi[c / 2] = __builtin_amdgcn_perm(b, a, 0x07060302u); // (k + 1, c) | (k + 1, c + 1) << 16
+        }
+        store_row(2 * (r0 + r), lo);
+        store_row(2 * (r0 + r) + 1, hi);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < RUN; r += 2) {
+        uint32_t lo[COLS / 2], hi[COLS / 2];
+#pragma unroll
+        for (int c = 0; c < COLS; c += 2) {
+          // bytes (k, c), (k + 1, c), (k, c + 1), (k + 1, c + 1)
+          const uint32_t x = w[r][c / 4], y = w[r + 1][c / 4];
+          const uint32_t sh = c % 4; // byte of column c within its dword
+          const uint32_t pr = __builtin_amdgcn_perm(y, x, (sh) | ((sh + 4) << 8) |
+                                                              ((sh + 1) << 16) | ((sh + 5) << 24));
+          const uint32_t a = mx_cvt_pair<FMT, 0>(pr, sf[c]);     // (k, c), (k + 1, c)
+          const uint32_t b = mx_cvt_pair<FMT, 1>(pr, sf[c + 1]); // (k, c + 1), (k + 1, c + 1)
+          lo[c / 2] = __builtin_amdgcn_perm(b, a, 0x05040100u);
+          hi[c / 2] = __builtin_amdgcn_perm(b, a, 0x07060302u);
+        }
+        store_row(r0 + r, lo);
+        store_row(r0 + r + 1, hi);
+      }
+    }
+    return;
+  }
+  // scales outside [17, 239]: element by element
 #pragma unroll
   for (int r = 0; r < RUN; ++r) {
 #pragma unroll
     for (int h = 0; h < KR; ++h) {
-      uint16_t out[16];
+      uint32_t o[COLS / 2];
 #pragma unroll
-      for (int i = 0; i < COLS; ++i) {
-        const uint32_t c = FMT == 4 ? (h ? code[r][i] >> 4 : code[r][i] & 15) : code[r][i];
-        out[i] = mx_upcast1(c, FMT, sc[i]);
+      for (int c = 0; c < COLS; c += 2) {
+        uint32_t e[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const uint32_t byte = (w[r][(c + u) / 4] >> (8 * ((c + u) % 4))) & 0xFFu;
+          const uint32_t code = FMT == 4 ? (h ? byte >> 4 : byte & 15) : byte;
+          e[u] = mx_upcast1(code, FMT, sc[c + u]);
+        }
+        o[c / 2] = e[0] | (e[1] << 16);
       }
-      uint16_t *d = p.dst + ((r0 + r) * KR + h) * p.cols + n0;
-#pragma unroll
-      for (int q = 0; q < COLS / 8; ++q)
-        reinterpret_cast<u32x4 *>(d)[q] = *reinterpret_cast<const u32x4 *>(&out[8 * q]);
+      store_row((r0 + r) * KR + h, o);
     }
   }
 }
@@ -122,13 +203,34 @@ __global__ void __launch_bounds__(256) mx_upcast_a_kernel(UpcastArgs p) {
   else
     *reinterpret_cast<u32x4 *>(code) =
         *reinterpret_cast<const u32x4 *>(p.src + m * p.ld_src + k0);
+  uint16_t *d = p.dst + m * p.cols + k0;
+  if (s >= kHwScaleLo && s <= kHwScaleHi) {
+    // neighbouring K share the scale: pairs convert in place (see mx_cvt_pair)
+    const float sf = __builtin_amdgcn_ldexpf(1.0f, (int)s - 127);
+    uint32_t o[8];
+    const uint32_t *cw = reinterpret_cast<const uint32_t *>(code);
+#pragma unroll
+    for (int q = 0; q < (FMT == 4 ? 2 : 4); ++q) {
+      if constexpr (FMT == 4) {
+        o[4 * q] = mx_cvt_pair<4, 0>(cw[q], sf);
+        o[4 * q + 1] = mx_cvt_pair<4, 1>(cw[q], sf);
+        o[4 * q + 2] = mx_cvt_pair<4, 2>(cw[q], sf);
+        o[4 * q + 3] = mx_cvt_pair<4, 3>(cw[q], sf);
+      } else {
+        o[2 * q] = mx_cvt_pair<FMT, 0>(cw[q], sf);
+        o[2 * q + 1] = mx_cvt_pair<FMT, 1>(cw[q], sf);
+      }
+    }
+    reinterpret_cast<u32x4 *>(d)[0] = u32x4{o[0], o[1], o[2], o[3]};
+    reinterpret_cast<u32x4 *>(d)[1] = u32x4{o[4], o[5], o[6], o[7]};
+    return;
+  }
   uint16_t out[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const uint32_t c = FMT == 4 ? (i & 1 ? code[i / 2] >> 4 : code[i / 2] & 15) : code[i];
     out[i] = mx_upcast1(c, FMT, s);
   }
-  uint16_t *d = p.dst + m * p.cols + k0;
   reinterpret_cast<u32x4 *>(d)[0] = *reinterpret_cast<const u32x4 *>(&out[0]);
   reinterpret_cast<u32x4 *>(d)[1] = *reinterpret_cast<const u32x4 *>(&out[8]);
 }
