@@ -5,8 +5,9 @@
 // then reads it as its A or B.
 //
 //   element  x = decode(code) * 2^(s - 127)   (s = 255: NaN)
-//   output   bf16 round-to-nearest-even of x, computed as
-//            f32_to_bf16_rne(ldexp(decode(code), s - 127))
+//   output   bf16 round-to-nearest-even of x: for scale exponents 17..239
+//            by v_cvt_scalef32_pk_bf16_* (exact there, see mx_cvt_pair),
+//            else as f32_to_bf16_rne(ldexp(decode(code), s - 127))
 // decode: e4m3 (OCP: S.1111.111 is NaN, no inf), e5m2 (the top byte of an
 // fp16, inf and NaN included), e2m1 (+-{0, .5, 1, 1.5, 2, 3, 4, 6}).  The
 // decoded value and its power-of-two scaling are exact in fp32 except past
