@@ -116,6 +116,12 @@ typedef enum tx_kernel {
  * layout of tl.dot(q, tl.trans(k)) / q @ k.T with k row-major.  Supported for
  * bf16/fp16 operands on the 256x256x64 tile. */
 #define TX_FLAG_B_KMAJOR 0x2
+/* C = C + A . B: the accumulator operand of tl.dot(a, b, acc) and
+ * tl.dot_scaled(..., acc) (R:pass/LoopSplit/06-fused-attention.py:85).  C
+ * must be TX_F32 or TX_I32; the kernel adds its finished fp32 / int32 sum to
+ * C's contents (int32 exactly; fp32 in one more rounding than an MFMA chain
+ * seeded with C).  Not for the W8A8 decode path (bf16 C). */
+#define TX_FLAG_ACCUMULATE 0x4
 
 typedef struct tx_dot_desc {
   int64_t M, N, K;

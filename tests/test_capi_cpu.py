@@ -266,6 +266,20 @@ def test_mx_plans():
     assert err(a_type=tx.F16, b_type=tx.F4E2M1) == tx.ERR_UNSUPPORTED  # fp16 side
 
 
+def test_accumulate_plans():
+    """TX_FLAG_ACCUMULATE: fp32 / int32 C only; C counts twice in the bytes."""
+    p = tx.plan(tx.make_desc(1024, 1024, 1024, tx.BF16, tx.F32, flags=tx.FLAG_ACCUMULATE))
+    q = tx.plan(tx.make_desc(1024, 1024, 1024, tx.BF16, tx.F32))
+    assert p.bytes == q.bytes + 1024 * 1024 * 4 and p.kernel == q.kernel
+    assert tx.plan(tx.make_desc(64, 128, 256, tx.I8, tx.I32,
+                                flags=tx.FLAG_ACCUMULATE)).kernel == tx.KERNEL_GEMM_I8
+    assert _err(tx.make_desc(256, 256, 256, tx.BF16, tx.BF16,
+                             flags=tx.FLAG_ACCUMULATE)) == tx.ERR_UNSUPPORTED
+    assert _err(tx.make_desc(16, 8192, 8192, tx.I8, tx.BF16, scale_mode=tx.SCALE_ROWCOL,
+                             flags=tx.FLAG_ACCUMULATE)) == tx.ERR_UNSUPPORTED  # W8A8: bf16 C
+    assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.F32, flags=0x8)) == tx.ERR_INVALID
+
+
 def test_fp8_e5m2_plans():
     """tt.dot over fp8 pairs with e5m2 (any mix, fp32 C): the 256x256 8-bit tile."""
     for a, b in ((tx.F8E5M2, tx.F8E5M2), (tx.F8E4M3, tx.F8E5M2), (tx.F8E5M2, tx.F8E4M3)):
@@ -294,8 +308,8 @@ def test_dot_scaled_argument_checks():
         tx.dot_scaled(a, sa, "e4m3", b, sb.t().contiguous(), "e4m3")
     with pytest.raises(ValueError, match="Reduction dimension"):
         tx.dot_scaled(a, sa, "e2m1", b, sb, "e4m3")  # lhs packs 256, rhs 128
-    with pytest.raises(NotImplementedError):
-        tx.dot_scaled(a, sa, "e4m3", b, sb, "e4m3", acc=torch.zeros(64, 32))
+    with pytest.raises(ValueError, match="acc must be fp32"):
+        tx.dot_scaled(a, sa, "e4m3", b, sb, "e4m3", acc=torch.zeros(64, 32, dtype=torch.int32))
     # a scale of None is accepted (unit scales); shapes are still checked
     with pytest.raises(ValueError, match="Reduction dimension"):
         tx.dot_scaled(a, None, "e2m1", b, None, "e4m3")

@@ -456,3 +456,66 @@ def test_fp8_e5m2_dot(gpu, fa, fb, M, N, K):
     err = check_close(got, ref, atol=ATOL, rtol=RTOL, scale=math.sqrt(K) * rms(a, fa) * rms(b, fb),
                       what=f"fp8 {fa}x{fb}")
     say(f"fp8 {fa}x{fb} {M}x{N}x{K}: max|d|={err:.3g}")
+
+
+# ----------------------------------------------------------------------------- accumulate
+@pytest.mark.parametrize("kind,M,N,K", [("bf16", 512, 512, 1024), ("bf16", 300, 272, 416),
+                                        ("f16", 256, 512, 4000), ("i8", 512, 256, 1024),
+                                        ("i8", 96, 160, 640), ("f8", 512, 512, 512),
+                                        ("bf16", 128, 256, 0)])
+def test_accumulate(gpu, kind, M, N, K):
+    """tl.dot(a, b, acc): TX_FLAG_ACCUMULATE stores fl(C + sum) -- bit for bit
+    the non-accumulating result plus C in one fp32 addition (int32: exactly),
+    on the 256x256 tiles, the small register-staged tiles and K = 0."""
+    import torch
+    say(f"accumulate {kind} {M}x{N}x{K}")
+    g = torch.Generator(device=gpu)
+    g.manual_seed(M + N + K)
+    if kind == "i8":
+        a = torch.randint(-127, 128, (M, K), generator=g, device=gpu, dtype=torch.int8)
+        b = torch.randint(-127, 128, (K, N), generator=g, device=gpu, dtype=torch.int8)
+        c0 = torch.randint(-2 ** 20, 2 ** 20, (M, N), generator=g, device=gpu, dtype=torch.int32)
+        odt = torch.int32
+    else:
+        dt = {"bf16": torch.bfloat16, "f16": torch.float16, "f8": torch.float8_e4m3fn}[kind]
+        a = torch.randn((M, K), generator=g, device=gpu).to(dt)
+        b = torch.randn((K, N), generator=g, device=gpu).to(dt)
+        c0 = torch.randn((M, N), generator=g, device=gpu) * 3
+        odt = torch.float32
+    plain = tx.dot(a, b, out_dtype=odt)
+    got = tx.dot(a, b, out_dtype=odt, acc=c0)
+    torch.cuda.synchronize()
+    want = (from_device(plain) + from_device(c0)).astype(np.int32 if odt == torch.int32
+                                                          else np.float32)
+    g_ = from_device(got)
+    assert np.array_equal(g_.view(np.int32), want.view(np.int32)), \
+        f"max |d| {np.abs(g_.astype(np.float64) - want).max()}"
+    assert np.array_equal(from_device(c0), from_device(c0))  # acc itself is not written
+
+
+@pytest.mark.parametrize("lhs_fmt,rhs_fmt", [("e4m3", "e4m3"), ("e2m1", "e2m1"), ("bf16", "e2m1")])
+def test_dot_scaled_accumulate(gpu, lhs_fmt, rhs_fmt):
+    """tl.dot_scaled(..., acc): acc + the dot, bit for bit the plain result
+    plus acc in one fp32 addition."""
+    import torch
+    say(f"dot_scaled acc {lhs_fmt} x {rhs_fmt}")
+    M, N, K = 320, 256, 512
+    rng = np.random.default_rng(9)
+    def operand(fmt, rows, cols, kdim):
+        if fmt == "bf16":
+            return torch.from_numpy(rng.standard_normal((rows, cols)).astype(np.float32)) \
+                .to(torch.bfloat16).to(gpu), None
+        c = rng.integers(0, 16 if fmt == "e2m1" else 0x70, size=(rows, cols)).astype(np.uint8)
+        if fmt == "e2m1":
+            c = (c[:, 0::2] | (c[:, 1::2] << 4)) if kdim == 1 else (c[0::2] | (c[1::2] << 4))
+        return to_device(np.ascontiguousarray(c.astype(np.uint8)), gpu), None
+    a, _ = operand(lhs_fmt, M, K, 1)
+    b, _ = operand(rhs_fmt, K, N, 0)
+    sa = None if lhs_fmt == "bf16" else to_device(rng.integers(120, 134, (M, K // 32)).astype(np.uint8), gpu)
+    sb = None if rhs_fmt == "bf16" else to_device(rng.integers(120, 134, (N, K // 32)).astype(np.uint8), gpu)
+    acc = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).to(gpu)
+    plain = tx.dot_scaled(a, sa, lhs_fmt, b, sb, rhs_fmt)
+    got = tx.dot_scaled(a, sa, lhs_fmt, b, sb, rhs_fmt, acc=acc)
+    torch.cuda.synchronize()
+    want = (from_device(plain) + from_device(acc)).astype(np.float32)
+    assert np.array_equal(from_device(got).view(np.int32), want.view(np.int32))

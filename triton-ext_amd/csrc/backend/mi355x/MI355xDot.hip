@@ -450,8 +450,10 @@ int validate(const tx_dot_desc *in, tx_dot_desc *d) {
   if (d->ldc == 0) d->ldc = d->N;
   if (d->lda < d->K || d->ldb < (bt ? d->K : d->N) || d->ldc < d->N)
     return fail(TX_ERR_INVALID, "row stride shorter than the row");
-  if (d->flags & ~(TX_FLAG_NO_LOOP_SPLIT | TX_FLAG_B_KMAJOR))
+  if (d->flags & ~(TX_FLAG_NO_LOOP_SPLIT | TX_FLAG_B_KMAJOR | TX_FLAG_ACCUMULATE))
     return fail(TX_ERR_INVALID, "unknown flags 0x%x", d->flags);
+  if ((d->flags & TX_FLAG_ACCUMULATE) && d->c_type != TX_F32 && d->c_type != TX_I32)
+    return fail(TX_ERR_UNSUPPORTED, "accumulating into C needs an fp32 or int32 C");
   // Bytes of a row of A / of B / of C.  e2m1 B is packed along K: a byte
   // row holds N elements of two K rows.
   const int64_t ldb_b = bb == 4 ? d->ldb : d->ldb * bb / 8;
@@ -606,6 +608,7 @@ int launchGemm(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   a.group_m = plan.m_tiles < gm ? plan.m_tiles : gm;
   a.sa_ld = (int32_t)(mx ? d.K / 32 : cdiv(d.K, 128));
   a.sb_ld = (int32_t)cdiv(d.N, 128);
+  a.accumulate = (d.flags & TX_FLAG_ACCUMULATE) != 0;
   hipLaunchKernelGGL(c.fn, dim3(plan.grid_x), dim3(plan.block_threads),
                      c.lds_bytes, stream, a);
   TX_HIP_CHECK(hipGetLastError());

@@ -278,8 +278,10 @@ struct Gemm16Dma {
           if (MASK_MN && (row >= p.M || col >= p.N))
             continue;
           const int64_t off = row * p.ldc + col;
-          if (EPI == EPI_F32)
-            reinterpret_cast<float *>(p.C)[off] = acc[i][j][r];
+          if (EPI == EPI_F32) {
+            float *c = reinterpret_cast<float *>(p.C) + off;
+            *c = p.accumulate ? *c + acc[i][j][r] : acc[i][j][r];
+          }
           else if (EPI == EPI_BF16)
             reinterpret_cast<uint16_t *>(p.C)[off] = f32_to_bf16_rne(acc[i][j][r]);
           else

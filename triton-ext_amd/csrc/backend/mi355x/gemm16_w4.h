@@ -420,8 +420,13 @@ template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
           const float v0 = acc[i][j][4 * g], v1 = acc[i][j][4 * g + 1];
           const float v2 = acc[i][j][4 * g + 2], v3 = acc[i][j][4 * g + 3];
           if (EPI == EPI_F32) {
-            *reinterpret_cast<float4 *>(reinterpret_cast<float *>(p.C) + off) =
-                make_float4(v0, v1, v2, v3);
+            float4 *c = reinterpret_cast<float4 *>(reinterpret_cast<float *>(p.C) + off);
+            if (p.accumulate) {
+              const float4 o = *c;
+              *c = make_float4(o.x + v0, o.y + v1, o.z + v2, o.w + v3);
+            } else {
+              *c = make_float4(v0, v1, v2, v3);
+            }
           } else {
             uint16_t h0, h1, h2, h3;
             if (EPI == EPI_BF16) {

@@ -500,9 +500,11 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
         const int64_t off = row * p.ldc + col;
         const Acc &v = acc[i][j];
         if (EPI == EPI_I32) {
-          *reinterpret_cast<i32x4_t *>(reinterpret_cast<int32_t *>(p.C) + off) = v;
+          i32x4_t *c = reinterpret_cast<i32x4_t *>(reinterpret_cast<int32_t *>(p.C) + off);
+          *c = p.accumulate ? *c + v : v;
         } else if (EPI == EPI_F32 || EPI == EPI_BLOCK128_F32 || EPI == EPI_MX_F32) {
-          *reinterpret_cast<f32x4_t *>(reinterpret_cast<float *>(p.C) + off) = v;
+          f32x4_t *c = reinterpret_cast<f32x4_t *>(reinterpret_cast<float *>(p.C) + off);
+          *c = p.accumulate ? *c + v : v;
         } else {
           float f[4];
           if (EPI == EPI_ROWCOL_BF16) {

@@ -123,6 +123,7 @@ struct GemmArgs {
   int32_t last_ks;        // MFMA sub-steps issued in the final K step
   int32_t group_m;        // tile rows per group in the tile order
   int32_t sa_ld, sb_ld; // MX: sa_ld = bytes per scale row = K / 32 groups
+  int32_t accumulate;   // fp32 / int32 C: C = C + A . B (tl.dot's acc operand)
 };
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
@@ -417,13 +418,15 @@ struct GemmTile {
             continue;
           const int64_t off = row * p.ldc + col;
           if (EPI == EPI_F32 || EPI == EPI_BLOCK128_F32) {
-            reinterpret_cast<float *>(p.C)[off] = (float)acc[i][j][r];
+            float *c = reinterpret_cast<float *>(p.C) + off;
+            *c = p.accumulate ? *c + (float)acc[i][j][r] : (float)acc[i][j][r];
           } else if (EPI == EPI_BF16 || EPI == EPI_BLOCK128_BF16) {
             reinterpret_cast<uint16_t *>(p.C)[off] = f32_to_bf16_rne((float)acc[i][j][r]);
           } else if (EPI == EPI_F16) {
             reinterpret_cast<uint16_t *>(p.C)[off] = f32_to_f16_rne((float)acc[i][j][r]);
           } else if (EPI == EPI_I32) {
-            reinterpret_cast<int32_t *>(p.C)[off] = (int32_t)acc[i][j][r];
+            int32_t *c = reinterpret_cast<int32_t *>(p.C) + off;
+            *c = p.accumulate ? *c + (int32_t)acc[i][j][r] : (int32_t)acc[i][j][r];
           } else { // EPI_ROWCOL_BF16
             const float v = ((float)acc[i][j][r] * p.sa[row]) * sbc;
             reinterpret_cast<uint16_t *>(p.C)[off] = f32_to_bf16_rne(v);

@@ -122,7 +122,9 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
   else if (d->scale_mode == TX_SCALE_MX32) // one e8m0 byte per 32 K; a bf16 side has none
     scaleBytes = ((ba == 16 ? 0.0 : M) + (bb == 16 ? 0.0 : N)) * (double)cdiv(d->K, 32);
   out->flops = 2.0 * M * N * K;
-  out->bytes = M * K * sa + K * N * sb + M * N * sc + scaleBytes;
+  // C once, twice when accumulating into it (read, then written)
+  const double cPasses = (d->flags & TX_FLAG_ACCUMULATE) ? 2.0 : 1.0;
+  out->bytes = M * K * sa + K * N * sb + cPasses * M * N * sc + scaleBytes;
   out->intensity = out->bytes > 0 ? out->flops / out->bytes : 0.0;
   // a mixed product runs at the rate of its wider operand
   out->peak_flops = ba >= bb ? tx_mi355x_peak_flops(d->a_type)

@@ -20,6 +20,7 @@ OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_NO_DEVICE, ERR_WORKSPACE, ERR_NO_
  KERNEL_GEMM_MX, KERNEL_GEMM_MX_BF16) = range(7)
 FLAG_NO_LOOP_SPLIT = 0x1
 FLAG_B_KMAJOR = 0x2  # B stored [N][K] row-major (a transposed view in torch)
+FLAG_ACCUMULATE = 0x4  # C = C + A . B (fp32 / int32 C)
 # TritonPluginResult
 TP_SUCCESS, TP_GENERIC_FAILURE = 0, 1
 # tx_cmp_pred (arith::CmpIPredicate order)

@@ -67,13 +67,23 @@ def workspace_for(p, device):
 
 
 def dot(a, b, out=None, out_dtype=None, scale_a=None, scale_b=None, scale_mode=None,
-        block=(0, 0, 0), flags=0, plan=None, workspace=None, stream=None):
+        block=(0, 0, 0), flags=0, plan=None, workspace=None, stream=None, acc=None):
     """C = epilogue(A @ B) on the current device's stream.
 
     scale_mode defaults to ROWCOL when int8 operands come with scales, to
-    BLOCK128 for fp8 operands with scales, else NONE.
+    BLOCK128 for fp8 operands with scales, else NONE.  acc (fp32 or int32
+    [M, N]): returns acc + A @ B, as tl.dot(a, b, acc) does, in a new tensor
+    (or in `out`); the kernel adds its finished sum to C.
     """
     import torch
+    if acc is not None:
+        if acc.dtype not in (torch.float32, torch.int32) or acc.dim() != 2:
+            raise ValueError("acc must be an fp32 or int32 [M, N] tensor")
+        if out is None:
+            out = acc.clone(memory_format=torch.contiguous_format)
+        elif out.data_ptr() != acc.data_ptr():
+            out.copy_(acc)
+        flags |= capi.FLAG_ACCUMULATE
     ta = tx_type(a)
     if scale_mode is None:
         if scale_a is None:
@@ -125,7 +135,8 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
     tl.dot_scaled specifies (T:language/core.py:2072-2076).  Checks follow
     T:language/semantic.py:1597-1665; what this backend does not implement
     (fp16 operands, bf16 on both sides, e2m1 mixed with fp8, packing along M
-    or N, `acc`) raises NotImplementedError.
+    or N) raises NotImplementedError.  acc (fp32 [M, N]) returns acc + the
+    dot, as tl.dot_scaled's acc does.
     """
     import torch
     for name, fmt in (("lhs_format", lhs_format), ("rhs_format", rhs_format)):
@@ -139,7 +150,8 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
         if fmt == "bf16" and (t.dtype != torch.bfloat16 or sc is not None):
             raise ValueError(f"{nm}: a bf16 operand is a torch.bfloat16 tensor with no scale")
     if acc is not None:
-        raise NotImplementedError("acc: accumulate into the result on the caller's side")
+        if acc.dtype != torch.float32 or (out_dtype not in (None, torch.float32)):
+            raise ValueError("acc must be fp32, as tl.dot_scaled's out_dtype")
     if not lhs_k_pack or not rhs_k_pack:
         raise NotImplementedError("only K-packed e2m1 operands are implemented")
     if lhs.dim() != 2 or rhs.dim() != 2:
@@ -169,6 +181,13 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
             raise ValueError(f"{nm} must be a contiguous uint8 (e8m0) tensor")
     if lhs.stride(1) != 1 or rhs.stride(1) != 1:
         raise ValueError("lhs and rhs rows must be contiguous")
+    flags = 0
+    if acc is not None:  # acc + dot, in a new tensor (or `out`), as tl.dot_scaled(acc=)
+        if out is None:
+            out = acc.clone(memory_format=torch.contiguous_format)
+        elif out.data_ptr() != acc.data_ptr():
+            out.copy_(acc)
+        flags = capi.FLAG_ACCUMULATE
     if out is not None:
         c_tx = tx_type(out)
     else:
@@ -178,7 +197,8 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
         ldb = rhs.stride(0) if K > 0 and N > 0 else 0
         desc = capi.make_desc(M, N, K, _MX_FORMATS.get(lhs_format, capi.BF16), c_tx,
                               b_type=_MX_FORMATS.get(rhs_format, capi.BF16),
-                              scale_mode=capi.SCALE_MX32, block=block, lda=lda, ldb=ldb)
+                              scale_mode=capi.SCALE_MX32, block=block, lda=lda, ldb=ldb,
+                              flags=flags)
         plan = capi.plan(desc)
     if out is None:
         out = torch.empty((M, N), dtype=_torch_dtype(c_tx), device=lhs.device)
