@@ -428,17 +428,14 @@ template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
               *c = make_float4(v0, v1, v2, v3);
             }
           } else {
-            uint16_t h0, h1, h2, h3;
-            if (EPI == EPI_BF16) {
-              h0 = f32_to_bf16_rne(v0), h1 = f32_to_bf16_rne(v1);
-              h2 = f32_to_bf16_rne(v2), h3 = f32_to_bf16_rne(v3);
-            } else {
-              h0 = f32_to_f16_rne(v0), h1 = f32_to_f16_rne(v1);
-              h2 = f32_to_f16_rne(v2), h3 = f32_to_f16_rne(v3);
-            }
             uint2 w;
-            w.x = (uint32_t)h0 | ((uint32_t)h1 << 16);
-            w.y = (uint32_t)h2 | ((uint32_t)h3 << 16);
+            if (EPI == EPI_BF16) {
+              w.x = pk_bf16_rne(v0, v1);
+              w.y = pk_bf16_rne(v2, v3);
+            } else {
+              w.x = pk_f16_rne(v0, v1);
+              w.y = pk_f16_rne(v2, v3);
+            }
             *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.C) + off) = w;
           }
         }

@@ -521,8 +521,8 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
               f[r] = (float)v[r];
           }
           uint2 w;
-          w.x = (uint32_t)f32_to_bf16_rne(f[0]) | ((uint32_t)f32_to_bf16_rne(f[1]) << 16);
-          w.y = (uint32_t)f32_to_bf16_rne(f[2]) | ((uint32_t)f32_to_bf16_rne(f[3]) << 16);
+          w.x = pk_bf16_rne(f[0], f[1]);
+          w.y = pk_bf16_rne(f[2], f[3]);
           *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.C) + off) = w;
         }
       }

@@ -87,6 +87,24 @@ TX_HD uint16_t f32_to_bf16_rne(float f) {
 }
 
 #ifdef __HIPCC__
+// Two fp32 -> packed bf16 / fp16 (first in the low half), round to nearest
+// even, by the hardware conversion the compiler emits for a cast
+// (v_cvt_pk_bf16_f32 on gfx950): one instruction per pair, bit-identical
+// to f32_to_bf16_rne / f32_to_f16_rne for every non-NaN input (fp32
+// denormals are kept, not flushed).
+__device__ __forceinline__ uint32_t pk_bf16_rne(float a, float b) {
+  typedef __bf16 bf16x2_t_ __attribute__((ext_vector_type(2)));
+  const bf16x2_t_ r = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, r);
+}
+__device__ __forceinline__ uint32_t pk_f16_rne(float a, float b) {
+  typedef _Float16 f16x2_t_ __attribute__((ext_vector_type(2)));
+  const f16x2_t_ r = {(_Float16)a, (_Float16)b};
+  return __builtin_bit_cast(uint32_t, r);
+}
+#endif
+
+#ifdef __HIPCC__
 // fp32 -> fp16 bits, round to nearest even (IEEE conversion).
 __device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
   _Float16 h = (_Float16)f;
