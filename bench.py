@@ -7,8 +7,10 @@ headline workload is BASELINE configs[1]: bf16 C = A @ B, M = N = K = 4096,
 fp32 accumulation, entries N(0,1)/sqrt(K).  `value` is its TFLOP/s (2*M*N*K
 per step over the timed region, HIP events on the launch stream).  The other
 configs are reported under "secondary": the LoopSplit K-tail and edge cases,
-int8 W8A8 decode (M = 1, 16, 64, 256; HBM-bound, timed per launch with the
-256 MB MALL flushed between launches so B streams from HBM), the fp8
+int8 W8A8 decode (M = 1, 16, 64, 256; HBM-bound, each launch after a
+512 MiB read that flushes the 256 MB MALL so B streams from HBM: `ms` is a
+launch inside the stream, (flush, launch) sequences minus the flushes alone;
+`ms_isolated` a lone launch between its own events), the fp8
 block-scaled dot, tl.dot_scaled's MX formats (mxfp8 e4m3 and mxfp4 e2m1
 with e8m0 scales per 32 K, fp32 C), and the fused attention forward of the
 reference's tutorial at its benchmark shape (BATCH 4, 32 heads, HEAD_DIM 64).
@@ -134,6 +136,31 @@ def time_cold(fn, steps, warmup, flush):
     return ms[len(ms) // 2], ms
 
 
+def time_cold_in_stream(fn, flush, reps=30, rounds=5):
+    """Per-launch ms of a cold launch inside a stream: (flush, fn) x reps minus
+    flush x reps, each sequence bracketed by events, median over rounds.  The
+    launch follows another kernel, as in a decode loop, so its dispatch
+    overlaps that kernel's tail; the difference is the launch's own time."""
+    import torch
+    out = []
+    for _ in range(rounds):
+        torch.cuda.synchronize()
+        s0, e0 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s1, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        for _ in range(reps):
+            flush()
+            fn()
+        e0.record()
+        s1.record()
+        for _ in range(reps):
+            flush()
+        e1.record()
+        torch.cuda.synchronize()
+        out.append((s0.elapsed_time(e0) - s1.elapsed_time(e1)) / reps)
+    return sorted(out)[len(out) // 2]
+
+
 def make_flush(dev):
     """Read 512 MiB (2x the 256 MB MALL) so the next kernel's operands come from HBM.
 
@@ -224,12 +251,15 @@ def bench_w8a8(tx, dev, M, N, K, steps, warmup, flush, seed=3):
     sb = torch.rand((N,), generator=g, device=dev) * 0.019 + 0.001
     c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     run = Launcher(tx, a, b, c, sa, sb, tx.SCALE_ROWCOL)
-    med, _ = time_cold(run, steps, warmup, flush)
+    iso, _ = time_cold(run, steps, warmup, flush)
+    med = time_cold_in_stream(run, flush)
     warm = time_back_to_back(run, steps, warmup)
     nbytes = M * K + K * N + M * N * 2 + 4 * (M + N)
     p = run.plan
-    return dict(workload=f"int8 W8A8 M={M} N={N} K={K}", ms=med, ms_warm_mall=warm,
-                gbps=nbytes / med / 1e6, frac_hbm=nbytes / med / 1e-3 / HBM,
+    # ms: a cold launch (B from HBM) inside a stream; ms_isolated: a lone launch
+    # bracketed by its own events (adds the dispatch latency a stream hides)
+    return dict(workload=f"int8 W8A8 M={M} N={N} K={K}", ms=med, ms_isolated=iso,
+                ms_warm_mall=warm, gbps=nbytes / med / 1e6, frac_hbm=nbytes / med / 1e-3 / HBM,
                 tops=2.0 * M * N * K / med / 1e9,
                 plan=dict(kernel=tx.load().tx_kernel_name(p.kernel).decode(), split_k=p.split_k,
                           grid=p.grid_x, intensity=round(p.intensity, 1),
@@ -490,8 +520,9 @@ def main():
         for m in w8a8_ms:
             r = bench_w8a8(tx, dev, m, 8192, 8192, max(args.steps, 20), 3, flush)
             secondary.append(r)
-            print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us, {r['gbps']:.0f} GB/s "
-                  f"({100 * r['frac_hbm']:.1f}% HBM)", file=sys.stderr, flush=True)
+            print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
+                  f"({100 * r['frac_hbm']:.1f}% HBM); isolated launch "
+                  f"{r['ms_isolated'] * 1e3:.2f} us", file=sys.stderr, flush=True)
     if want("int8"):
         r = bench_int8(tx, dev, 4096, 4096, 4096, args.steps, args.warmup)
         secondary.append(r)
