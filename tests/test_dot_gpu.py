@@ -482,6 +482,7 @@ def test_accumulate(gpu, kind, M, N, K):
         b = torch.randn((K, N), generator=g, device=gpu).to(dt)
         c0 = torch.randn((M, N), generator=g, device=gpu) * 3
         odt = torch.float32
+    c0_host = from_device(c0).copy()
     plain = tx.dot(a, b, out_dtype=odt)
     got = tx.dot(a, b, out_dtype=odt, acc=c0)
     torch.cuda.synchronize()
@@ -490,7 +491,8 @@ def test_accumulate(gpu, kind, M, N, K):
     g_ = from_device(got)
     assert np.array_equal(g_.view(np.int32), want.view(np.int32)), \
         f"max |d| {np.abs(g_.astype(np.float64) - want).max()}"
-    assert np.array_equal(from_device(c0), from_device(c0))  # acc itself is not written
+    assert np.array_equal(from_device(c0).view(np.int32), c0_host.view(np.int32)), \
+        "acc itself was written"
 
 
 @pytest.mark.parametrize("lhs_fmt,rhs_fmt", [("e4m3", "e4m3"), ("e2m1", "e2m1"), ("bf16", "e2m1")])
