@@ -12,7 +12,14 @@ Pinned by (tests/test_oracle_cpu.py):
     encoding of the same values; unit scales reduce it to the tiled fp8 dot;
     e2m1 operands equal their e4m3 re-encoding; a scale step of +1 doubles
     exactly one group's terms; golden fixtures from the interpreter running
-    the dequantise-then-tl.dot form.
+    the dequantise-then-tl.dot form; with one bf16 operand, e4m3-valued bf16
+    reduces it bit for bit to the all-MX dot, and subnormal / overflow / NaN
+    scales take bf16's rounding (tests/test_mx_oracle_cpu.py);
+  * fp32 -> e5m2: round to nearest even against torch's float8_e5m2 cast
+    (1.6 M values), the interpreter's converter against the interpreter's
+    own cast bit for bit (tests/golden/e5m2_cast_interp.npz);
+  * attention (fp16, bf16, e5m2): interpreter fixtures (attn_*.npz), float64
+    attention, and the LoopSplit equivalences (tests/test_attn_cpu.py).
 """
 import ctypes
 import os
