@@ -81,6 +81,14 @@ typedef enum tx_scale_mode {
    * to the workspace (plan->workspace_bytes: the MX operand at 2 bytes per
    * element). */
   TX_SCALE_MX32 = 3,
+  /* tl.dot_scaled with e4m3 scales, one per 16 K elements (the scale size
+   * Triton takes for fp8e4nv scale tensors, T:language/semantic.py:1597-1609;
+   * NVFP4): e2m1 operands, sa uint8 e4m3 [M][K/16], sb [N][K/16], 4-byte
+   * aligned; one side may be TX_BF16 with no scale.  gfx950's scaled MFMA
+   * takes e8m0 scales only, so each e2m1 operand is upcast to bf16
+   * (x * decoded scale: exact in bf16) into the workspace and the bf16 tile
+   * runs; K % 16 == 0; C fp32 or bf16. */
+  TX_SCALE_NV16 = 4,
 } tx_scale_mode;
 
 typedef enum tx_bound {

@@ -59,9 +59,10 @@ def lib():
         L.oracle_attn_fwd.restype = i32
         L.oracle_attn_fwd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i32, ctypes.c_float,
                                       i32, i32, i32, i32, i32, i32, i32]
-        L.oracle_dot_scaled.restype = i32
-        L.oracle_dot_scaled.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64,
-                                        i32, i32, i32, i32, i32]
+        for name in ("oracle_dot_scaled", "oracle_dot_scaled_nv16"):
+            getattr(L, name).restype = i32
+            getattr(L, name).argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64,
+                                         i32, i32, i32, i32, i32]
         _lib = L
     return _lib
 
@@ -168,27 +169,30 @@ def mx_decode(codes, fmt):
 
 
 def dot_scaled(a, sa, a_fmt, b, sb, b_fmt, *, K, c_type=F32, round_mode=ROUND_RNE,
-               nthreads=0):
+               nthreads=0, nv16=False):
     """tl.dot_scaled on the CPU.
 
     a: uint8 [M, K] codes (e2m1: [M, K/2] packed bytes; a_fmt BF16: uint16
     bf16 bits, sa None); b: uint8 [K, N] (e2m1: [K/2, N], packed along K;
     b_fmt BF16: uint16 bits, sb None); sa: uint8 [M, K/32]; sb: uint8
     [N, K/32].  With a bf16 side the MX side is upcast to bf16 first.
+    nv16: e4m3 scale codes per 16 K instead ([M, K/16], [N, K/16]).
     Returns fp32 [M, N] (c_type F32) or bf16 bits (BF16).
     """
     a = np.ascontiguousarray(a, dtype=np.uint16 if a_fmt == BF16 else np.uint8)
     b = np.ascontiguousarray(b, dtype=np.uint16 if b_fmt == BF16 else np.uint8)
     M, N = a.shape[0], b.shape[1]
-    sa = np.zeros((M, K // 32), np.uint8) if sa is None else np.ascontiguousarray(sa, np.uint8)
-    sb = np.zeros((N, K // 32), np.uint8) if sb is None else np.ascontiguousarray(sb, np.uint8)
-    assert sa.shape == (M, K // 32) and sb.shape == (N, K // 32), (sa.shape, sb.shape)
+    g = 16 if nv16 else 32
+    sa = np.zeros((M, K // g), np.uint8) if sa is None else np.ascontiguousarray(sa, np.uint8)
+    sb = np.zeros((N, K // g), np.uint8) if sb is None else np.ascontiguousarray(sb, np.uint8)
+    assert sa.shape == (M, K // g) and sb.shape == (N, K // g), (sa.shape, sb.shape)
     assert a.shape[1] == (K // 2 if a_fmt == F4E2M1 else K)
     assert b.shape[0] == (K // 2 if b_fmt == F4E2M1 else K)
     out = np.zeros((M, N), dtype=np.float32 if c_type == F32 else np.uint16)
     lda = K
-    rc = lib().oracle_dot_scaled(_ptr(a), _ptr(b), _ptr(out), _ptr(sa), _ptr(sb), M, N, K,
-                                 lda, N, N, a_fmt, b_fmt, c_type, round_mode, nthreads)
+    fn = lib().oracle_dot_scaled_nv16 if nv16 else lib().oracle_dot_scaled
+    rc = fn(_ptr(a), _ptr(b), _ptr(out), _ptr(sa), _ptr(sb), M, N, K,
+            lda, N, N, a_fmt, b_fmt, c_type, round_mode, nthreads)
     if rc != 0:
         raise ValueError(f"oracle_dot_scaled rejected the arguments (rc={rc})")
     return out

@@ -332,22 +332,26 @@ static double upcast_bf16(double v) {
   return or_bf16_to_f32(or_f32_to_bf16((float)v, OR_ROUND_RNE));
 }
 
-int oracle_dot_scaled(const void *Av, const void *Bv, void *Cv, const uint8_t *sa,
-                      const uint8_t *sb, int64_t M, int64_t N, int64_t K, int64_t lda,
-                      int64_t ldb, int64_t ldc, int a_fmt, int b_fmt, int c_type,
-                      int round_mode, int nthreads) {
+static int dot_scaled_impl(const void *Av, const void *Bv, void *Cv, const uint8_t *sa,
+                           const uint8_t *sb, int64_t M, int64_t N, int64_t K, int64_t lda,
+                           int64_t ldb, int64_t ldc, int a_fmt, int b_fmt, int c_type,
+                           int round_mode, int nthreads, int nv) {
   const uint8_t *A = (const uint8_t *)Av, *B = (const uint8_t *)Bv;
   uint8_t *C = (uint8_t *)Cv;
   if (M < 0 || N < 0 || K < 0 || K % 32)
     return -1;
-  const int mixed = a_fmt == OR_BF16 || b_fmt == OR_BF16;
+  /* e4m3 scales per 16 (nv): e2m1 sides only, both upcast to bf16 */
+  const int mixed = a_fmt == OR_BF16 || b_fmt == OR_BF16 || nv;
+  if (nv && ((a_fmt != OR_F4E2M1 && a_fmt != OR_BF16) || (b_fmt != OR_F4E2M1 && b_fmt != OR_BF16)))
+    return -1;
+  const int GS = nv ? 16 : 32; /* K per scale */
   if ((a_fmt != OR_F8E4M3 && a_fmt != OR_F8E5M2 && a_fmt != OR_F4E2M1 && a_fmt != OR_BF16) ||
       (b_fmt != OR_F8E4M3 && b_fmt != OR_F8E5M2 && b_fmt != OR_F4E2M1 && b_fmt != OR_BF16) ||
       (a_fmt == OR_BF16 && b_fmt == OR_BF16))
     return -1;
   if (c_type != OR_F32 && c_type != OR_BF16)
     return -1;
-  const int64_t G = K / 32;
+  const int64_t G = K / GS;
 #ifdef _OPENMP
   if (nthreads <= 0)
     nthreads = omp_get_max_threads();
@@ -363,7 +367,9 @@ int oracle_dot_scaled(const void *Av, const void *Bv, void *Cv, const uint8_t *s
         continue;
       }
       const int64_t byte = a_fmt == OR_F4E2M1 ? m * (lda / 2) + k / 2 : m * lda + k;
-      arow[k] = mx_elem(A, a_fmt, byte, (int)(k & 1)) * or_e8m0_to_f64(sa[m * G + k / 32]);
+      const uint8_t s = sa[m * G + k / GS];
+      arow[k] = mx_elem(A, a_fmt, byte, (int)(k & 1)) *
+                (nv ? or_mx_e4m3_to_f64(s) : or_e8m0_to_f64(s));
       if (mixed)
         arow[k] = upcast_bf16(arow[k]);
     }
@@ -375,7 +381,9 @@ int oracle_dot_scaled(const void *Av, const void *Bv, void *Cv, const uint8_t *s
           b = or_bf16_to_f32(((const uint16_t *)B)[k * ldb + n]);
         } else {
           const int64_t byte = b_fmt == OR_F4E2M1 ? (k / 2) * ldb + n : k * ldb + n;
-          b = mx_elem(B, b_fmt, byte, (int)(k & 1)) * or_e8m0_to_f64(sb[n * G + k / 32]);
+          const uint8_t s = sb[n * G + k / GS];
+          b = mx_elem(B, b_fmt, byte, (int)(k & 1)) *
+              (nv ? or_mx_e4m3_to_f64(s) : or_e8m0_to_f64(s));
           if (mixed)
             b = upcast_bf16(b);
         }
@@ -393,6 +401,26 @@ int oracle_dot_scaled(const void *Av, const void *Bv, void *Cv, const uint8_t *s
     free(arow);
   }
   return 0;
+}
+
+int oracle_dot_scaled(const void *Av, const void *Bv, void *Cv, const uint8_t *sa,
+                      const uint8_t *sb, int64_t M, int64_t N, int64_t K, int64_t lda,
+                      int64_t ldb, int64_t ldc, int a_fmt, int b_fmt, int c_type,
+                      int round_mode, int nthreads) {
+  return dot_scaled_impl(Av, Bv, Cv, sa, sb, M, N, K, lda, ldb, ldc, a_fmt, b_fmt, c_type,
+                         round_mode, nthreads, 0);
+}
+
+/* The same with e4m3 scales, one per 16 K (tl.dot_scaled's fp8e4nv scale
+ * tensors, T:language/semantic.py:1597-1609): sa [M][K/16], sb [N][K/16],
+ * each element x * decode_e4m3(s), e2m1 (or bf16) operands, both upcast to
+ * bf16 -- exact for e2m1 times e4m3 -- then the products summed as above. */
+int oracle_dot_scaled_nv16(const void *Av, const void *Bv, void *Cv, const uint8_t *sa,
+                           const uint8_t *sb, int64_t M, int64_t N, int64_t K, int64_t lda,
+                           int64_t ldb, int64_t ldc, int a_fmt, int b_fmt, int c_type,
+                           int round_mode, int nthreads) {
+  return dot_scaled_impl(Av, Bv, Cv, sa, sb, M, N, K, lda, ldb, ldc, a_fmt, b_fmt, c_type,
+                         round_mode, nthreads, 1);
 }
 
 /* ---------------- fused attention forward ----------------

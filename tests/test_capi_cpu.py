@@ -242,7 +242,8 @@ def test_mx_plans():
     assert err(a_type=tx.I8, c_type=tx.BF16) == tx.ERR_UNSUPPORTED
     assert err(flags=tx.FLAG_B_KMAJOR) == tx.ERR_UNSUPPORTED
     assert err(a_type=tx.F4E2M1, scale_mode=tx.SCALE_NONE) == tx.ERR_UNSUPPORTED
-    assert err(scale_mode=4) == tx.ERR_INVALID
+    assert err(scale_mode=5) == tx.ERR_INVALID
+    assert err(scale_mode=tx.SCALE_NV16) == tx.ERR_UNSUPPORTED  # e4m3 values, e4m3 scales
     assert err(a_type=tx.F4E2M1, K=256, lda=264) == tx.ERR_INVALID  # 132-byte rows
     # the fp32 block-scaled mode keeps rejecting e5m2 (e4m3 only)
     assert err(a_type=tx.F8E5M2, scale_mode=tx.SCALE_BLOCK128) == tx.ERR_UNSUPPORTED
@@ -264,6 +265,20 @@ def test_mx_plans():
         assert p.peak_flops == pytest.approx(2516.6e12)
     assert err(a_type=tx.BF16, b_type=tx.BF16) == tx.ERR_UNSUPPORTED  # bf16 on both sides
     assert err(a_type=tx.F16, b_type=tx.F4E2M1) == tx.ERR_UNSUPPORTED  # fp16 side
+
+
+def test_nv16_plans():
+    """e4m3 scales per 16 (TX_SCALE_NV16): e2m1 sides upcast to bf16, the bf16 tile."""
+    NV = tx.SCALE_NV16
+    p = tx.plan(tx.make_desc(512, 256, 1024, tx.F4E2M1, tx.F32, b_type=tx.F4E2M1, scale_mode=NV))
+    assert p.kernel == tx.KERNEL_GEMM_MX_BF16
+    assert p.workspace_bytes == 512 * 1024 * 2 + 1024 * 256 * 2  # both operands as bf16
+    assert p.bytes == 512 * 512 + 512 * 256 + (512 + 256) * 64 + 512 * 256 * 4
+    assert p.peak_flops == pytest.approx(2516.6e12)
+    p = tx.plan(tx.make_desc(512, 256, 1024, tx.BF16, tx.F32, b_type=tx.F4E2M1, scale_mode=NV))
+    assert p.workspace_bytes == 1024 * 256 * 2
+    assert _err(tx.make_desc(64, 64, 256, tx.F8E4M3, tx.F32, scale_mode=NV)) == tx.ERR_UNSUPPORTED
+    assert _err(tx.make_desc(64, 64, 256, tx.F4E2M1, tx.F32, scale_mode=5)) == tx.ERR_INVALID
 
 
 def test_accumulate_plans():

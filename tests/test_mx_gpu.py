@@ -309,3 +309,51 @@ def test_mx_bf16_scale_range_bit_identity(gpu, side, fmt):
     torch.cuda.synchronize()
     got, want = from_device(c), from_device(d16)
     assert np.array_equal(got.view(np.int32), want.view(np.int32))
+
+
+# --- e4m3 scales per 16 K (tl.dot_scaled's fp8e4nv scales) ------------------
+
+@pytest.mark.parametrize("lhs,rhs", [("e2m1", "e2m1"), ("bf16", "e2m1"), ("e2m1", "bf16")])
+@pytest.mark.parametrize("M,N,K", [(300, 272, 416), (512, 512, 1024)])
+def test_nv16_vs_oracle(gpu, lhs, rhs, M, N, K):
+    """e2m1 operands with e4m3 scales per 16 K, upcast to bf16 (exact) and
+    run on the bf16 tile: bit for bit the bf16 dot of the host upcast, and
+    within fp32 summation error of the oracle."""
+    import torch
+    say(f"dot_scaled e4m3/16 {lhs} x {rhs} {M}x{N}x{K}")
+    rng = np.random.default_rng(M + K + len(lhs))
+    dec4 = lambda c: torch.from_numpy(np.ascontiguousarray(c)).view(torch.float8_e4m3fn) \
+        .double().numpy()
+    bf = lambda x: torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16) \
+        .view(torch.int16).numpy().view(np.uint16)
+
+    def side(fmt, rows, cols, along_k_axis):
+        if fmt == "bf16":
+            x = bf(rng.standard_normal((rows, cols)))
+            return x, None, x
+        c = rng.integers(0, 16, size=(rows, cols)).astype(np.uint8)
+        kdim = cols if along_k_axis == 1 else rows
+        other = rows if along_k_axis == 1 else cols
+        s = rng.integers(0x20, 0x50, size=(other, kdim // 16)).astype(np.uint8)
+        g = np.arange(kdim) // 16
+        v = oracle.mx_decode(c, oracle.F4E2M1) * (dec4(s)[:, g] if along_k_axis == 1
+                                                  else dec4(s)[:, g].T)
+        return pack(c, along_k_axis), s, bf(v)
+
+    a, sa, a16 = side(lhs, M, K, 1)
+    b, sb, b16 = side(rhs, K, N, 0)
+    dev = lambda x: None if x is None else to_device(x, gpu)
+    e4 = lambda x: None if x is None else dev(x).view(torch.float8_e4m3fn)
+    bfd = lambda x: dev(x.view(np.int16)).view(torch.bfloat16)
+    c = tx.dot_scaled(bfd(a) if lhs == "bf16" else dev(a), e4(sa), lhs,
+                      bfd(b) if rhs == "bf16" else dev(b), e4(sb), rhs)
+    d16 = tx.dot(bfd(a16), bfd(b16), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    got = from_device(c)
+    assert np.array_equal(got.view(np.int32), from_device(d16).view(np.int32))
+    ref = oracle.dot_scaled(a, sa, oracle.BF16 if lhs == "bf16" else oracle.F4E2M1,
+                            b, sb, oracle.BF16 if rhs == "bf16" else oracle.F4E2M1, K=K, nv16=True)
+    S = np.abs(bits_to_f32(a16, "bf16").astype(np.float64)) @ \
+        np.abs(bits_to_f32(b16, "bf16").astype(np.float64))
+    d = np.abs(got.astype(np.float64) - ref)
+    assert (d <= K * 2.0 ** -24 * S + 1e-30).all(), f"worst {(d / (K * 2.0 ** -24 * S + 1e-30)).max()}"

@@ -275,3 +275,31 @@ def test_bf16_side_upcast_rounds_to_bf16():
     want0 = torch.tensor([7 * 2.0 ** -136], dtype=torch.float32).to(torch.bfloat16).float().item()
     assert want0 == 2.0 ** -133 and c[0] == np.float32(want0)
     assert np.isposinf(c[1]) and np.isnan(c[2])
+
+
+def test_nv16_power_of_two_scales_equal_mx32():
+    """e4m3 scales per 16 K (tl.dot_scaled's fp8e4nv scale tensors): with
+    power-of-two e4m3 scales 2^k (code (k + 7) << 3), equal on both 16-halves
+    of every 32-group, the result equals the MX dot with e8m0 127 + k, bit
+    for bit (the e2m1 x e4m3 upcast is exact)."""
+    rng = np.random.default_rng(12)
+    M, N, K = 24, 40, 128
+    ac = rng.integers(0, 16, size=(M, K)).astype(np.uint8)
+    bc = rng.integers(0, 16, size=(K, N)).astype(np.uint8)
+    a = (ac[:, 0::2] | (ac[:, 1::2] << 4)).astype(np.uint8)
+    b = (bc[0::2] | (bc[1::2] << 4)).astype(np.uint8)
+    ka = rng.integers(-6, 9, size=(M, K // 32))
+    kb = rng.integers(-6, 9, size=(N, K // 32))
+    nv_a = np.repeat(((ka + 7) << 3).astype(np.uint8), 2, axis=1)
+    nv_b = np.repeat(((kb + 7) << 3).astype(np.uint8), 2, axis=1)
+    got = oracle.dot_scaled(a, nv_a, oracle.F4E2M1, b, nv_b, oracle.F4E2M1, K=K, nv16=True)
+    want = oracle.dot_scaled(a, (127 + ka).astype(np.uint8), oracle.F4E2M1, b,
+                             (127 + kb).astype(np.uint8), oracle.F4E2M1, K=K)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # a non-power-of-two scale (1.5 = code 0x3C) scales its 16 terms exactly
+    one = np.full_like(nv_a, 0x38)
+    c1 = oracle.dot_scaled(a, one, oracle.F4E2M1, b, np.full_like(nv_b, 0x38), oracle.F4E2M1,
+                           K=K, nv16=True)
+    c15 = oracle.dot_scaled(a, np.full_like(nv_a, 0x3C), oracle.F4E2M1, b,
+                            np.full_like(nv_b, 0x38), oracle.F4E2M1, K=K, nv16=True)
+    assert np.array_equal(c15, (c1.astype(np.float64) * 1.5).astype(np.float32))

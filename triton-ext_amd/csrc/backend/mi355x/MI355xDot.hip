@@ -215,6 +215,8 @@ int fmtOf(const tx_dot_desc &d) {
 // (T:language/core.py:2072-2076) and the bf16 tile runs.  1: A is the MX
 // operand, 2: B is, 0: not this form.
 int mxUpcastSide(const tx_dot_desc &d) {
+  if (d.scale_mode == TX_SCALE_NV16) // e4m3 scales: e2m1 sides upcast (3: both)
+    return (d.a_type == TX_F4E2M1 ? 1 : 0) | (d.b_type == TX_F4E2M1 ? 2 : 0);
   if (d.scale_mode != TX_SCALE_MX32)
     return 0;
   if (d.a_type == TX_BF16 && mxFormat(d.b_type) >= 0)
@@ -227,8 +229,9 @@ int mxUpcastSide(const tx_dot_desc &d) {
 // Workspace of the upcast form: the MX operand as bf16, 256-byte aligned.
 int64_t mxUpcastWorkspace(const tx_dot_desc &d) {
   const int side = mxUpcastSide(d);
-  const int64_t elems = side == 2 ? d.K * d.N : side == 1 ? d.M * d.K : 0;
-  return (elems * 2 + 255) / 256 * 256;
+  const int64_t a = (side & 1) ? (d.M * d.K * 2 + 255) / 256 * 256 : 0;
+  const int64_t b = (side & 2) ? (d.K * d.N * 2 + 255) / 256 * 256 : 0;
+  return a + b; // A's upcast first, then B's
 }
 
 // Operand kind and epilogue of a descriptor (-1 if unsupported).
@@ -402,8 +405,10 @@ int txMi355xDotRun(tx_dot_plan *plan) {
     plan->passes_run += 1;
     return TX_OK;
   }
+  // (the upcast forms run the plain bf16 tile: format pair 0)
   const int ci = findGemmConfig(op, epi, d.block_m, d.block_n, d.block_k,
-                                (d.flags & TX_FLAG_B_KMAJOR) != 0, fmtOf(d));
+                                (d.flags & TX_FLAG_B_KMAJOR) != 0,
+                                mxUpcastSide(d) ? 0 : fmtOf(d));
   if (ci < 0 && (d.flags & TX_FLAG_B_KMAJOR))
     return fail(TX_ERR_UNSUPPORTED,
                 "K-major B is implemented for bf16/fp16 on the 256x256x64 tile only");
@@ -440,11 +445,21 @@ int validate(const tx_dot_desc *in, tx_dot_desc *d) {
   if (!ba || !bb || !bc || bc < 8)
     return fail(TX_ERR_INVALID, "unknown dtype");
   const bool bt = (d->flags & TX_FLAG_B_KMAJOR) != 0;
-  if (d->scale_mode < TX_SCALE_NONE || d->scale_mode > TX_SCALE_MX32)
+  if (d->scale_mode < TX_SCALE_NONE || d->scale_mode > TX_SCALE_NV16)
     return fail(TX_ERR_INVALID, "unknown scale mode %d", d->scale_mode);
   const bool fp4 = ba == 4 || bb == 4;
-  if (fp4 && d->scale_mode != TX_SCALE_MX32)
-    return fail(TX_ERR_UNSUPPORTED, "e2m1 operands need TX_SCALE_MX32");
+  if (fp4 && d->scale_mode != TX_SCALE_MX32 && d->scale_mode != TX_SCALE_NV16)
+    return fail(TX_ERR_UNSUPPORTED, "e2m1 operands need TX_SCALE_MX32 or TX_SCALE_NV16");
+  if (d->scale_mode == TX_SCALE_NV16) {
+    const bool ok_a = d->a_type == TX_F4E2M1 || d->a_type == TX_BF16;
+    const bool ok_b = d->b_type == TX_F4E2M1 || d->b_type == TX_BF16;
+    if (!ok_a || !ok_b || (d->a_type == TX_BF16 && d->b_type == TX_BF16))
+      return fail(TX_ERR_UNSUPPORTED, "e4m3 scales per 16 take e2m1 operands (one may be bf16)");
+    if (bt)
+      return fail(TX_ERR_UNSUPPORTED, "e4m3-scaled operands take B as [K][N]");
+    if ((d->M > d->N ? d->M : d->N) * (d->K / 16) >= ((int64_t)1 << 31))
+      return fail(TX_ERR_UNSUPPORTED, "scale arrays above 2 GiB");
+  }
   if (d->lda == 0) d->lda = d->K;
   if (d->ldb == 0) d->ldb = bt ? d->K : d->N;
   if (d->ldc == 0) d->ldc = d->N;
@@ -615,64 +630,82 @@ int launchGemm(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   return TX_OK;
 }
 
-// tl.dot_scaled with one bf16 operand: upcast the MX operand into the
-// workspace, then the bf16 tile on (bf16 side, upcast) -- two launches on
-// one stream.
+// tl.dot_scaled through bf16: upcast the scaled operand(s) -- one side
+// against a bf16 operand (MX), or each e2m1 side under e4m3 scales (NV16) --
+// into the workspace (A's first, then B's), then the bf16 tile on them, all
+// launches on one stream.
 int launchMxUpcast(const tx_dot_plan &plan, const void *A, const void *B, void *C,
                    const void *sa, const void *sb, void *ws, size_t ws_bytes,
                    hipStream_t stream) {
   const tx_dot_desc &d = plan.desc;
   const int side = mxUpcastSide(d);
+  const bool nv = d.scale_mode == TX_SCALE_NV16;
   const int64_t need = mxUpcastWorkspace(d);
   if (!side)
-    return fail(TX_ERR_INVALID, "plan is not an MX x bf16 dot_scaled");
+    return fail(TX_ERR_INVALID, "plan has no operand to upcast");
   if (!ws || (int64_t)ws_bytes < need)
-    return fail(TX_ERR_WORKSPACE, "MX x bf16 needs %lld workspace bytes, got %zu",
+    return fail(TX_ERR_WORKSPACE, "the upcast needs %lld workspace bytes, got %zu",
                 (long long)need, ws_bytes);
   if (reinterpret_cast<uintptr_t>(ws) & 15)
     return fail(TX_ERR_INVALID, "workspace must be 16-byte aligned");
-  const int32_t mxt = side == 2 ? d.b_type : d.a_type;
-  const int fmt = mxFormat(mxt);
-  txk::UpcastArgs u;
-  u.src = static_cast<const uint8_t *>(side == 2 ? B : A);
-  u.scale = static_cast<const uint8_t *>(side == 2 ? sb : sa);
-  u.dst = static_cast<uint16_t *>(ws);
-  u.ld_scale = d.K / 32;
-  u.fmt = fmt;
-  int64_t threads;
-  if (side == 2) {
-    u.rows = d.K;
-    u.cols = d.N;
-    u.ld_src = d.ldb; // fp8: bytes per row; e2m1: bytes per packed row
-    threads = (d.K / 8) * (d.N / 16); // 16 columns x 8 K rows per thread
-  } else {
-    u.rows = d.M;
-    u.cols = d.K;
-    u.ld_src = fmt == 4 ? d.lda / 2 : d.lda;
-    threads = d.M * (d.K / 16);
-  }
+  uint16_t *wa = static_cast<uint16_t *>(ws);
+  uint16_t *wb = reinterpret_cast<uint16_t *>(
+      static_cast<uint8_t *>(ws) + ((side & 1) ? (d.M * d.K * 2 + 255) / 256 * 256 : 0));
   typedef void (*UpFn)(txk::UpcastArgs);
-  const UpFn fn = side == 2 ? (fmt == 0 ? txk::mx_upcast_b_kernel<0>
-                               : fmt == 1 ? txk::mx_upcast_b_kernel<1>
-                                          : txk::mx_upcast_b_kernel<4>)
-                            : (fmt == 0 ? txk::mx_upcast_a_kernel<0>
-                               : fmt == 1 ? txk::mx_upcast_a_kernel<1>
-                                          : txk::mx_upcast_a_kernel<4>);
-  if (threads > 0) {
-    hipLaunchKernelGGL(fn, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0, stream, u);
-    TX_HIP_CHECK(hipGetLastError());
+  auto upcast = [&](int one) -> int {
+    const int fmt = mxFormat(one == 2 ? d.b_type : d.a_type);
+    txk::UpcastArgs u;
+    u.src = static_cast<const uint8_t *>(one == 2 ? B : A);
+    u.scale = static_cast<const uint8_t *>(one == 2 ? sb : sa);
+    u.dst = one == 2 ? wb : wa;
+    u.ld_scale = d.K / (nv ? 16 : 32);
+    u.fmt = fmt;
+    int64_t threads;
+    UpFn fn;
+    if (one == 2) {
+      u.rows = d.K;
+      u.cols = d.N;
+      u.ld_src = d.ldb; // fp8: bytes per row; e2m1: bytes per packed row
+      threads = (d.K / 8) * (d.N / 16); // 16 columns x 8 K rows per thread
+      fn = nv ? txk::mx_upcast_b_kernel<4, true>
+              : fmt == 0 ? txk::mx_upcast_b_kernel<0> : fmt == 1 ? txk::mx_upcast_b_kernel<1>
+                                                     : txk::mx_upcast_b_kernel<4>;
+    } else {
+      u.rows = d.M;
+      u.cols = d.K;
+      u.ld_src = fmt == 4 ? d.lda / 2 : d.lda;
+      threads = d.M * (d.K / 16);
+      fn = nv ? txk::mx_upcast_a_kernel<4, true>
+              : fmt == 0 ? txk::mx_upcast_a_kernel<0> : fmt == 1 ? txk::mx_upcast_a_kernel<1>
+                                                     : txk::mx_upcast_a_kernel<4>;
+    }
+    if (threads > 0) {
+      hipLaunchKernelGGL(fn, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0, stream, u);
+      TX_HIP_CHECK(hipGetLastError());
+    }
+    return TX_OK;
+  };
+  if (side & 1) {
+    const int rc = upcast(1);
+    if (rc != TX_OK)
+      return rc;
   }
-  // The bf16 tile over the upcast operand.
+  if (side & 2) {
+    const int rc = upcast(2);
+    if (rc != TX_OK)
+      return rc;
+  }
+  // The bf16 tile over the upcast operand(s).
   tx_dot_plan g = plan;
   g.desc.a_type = TX_BF16;
   g.desc.b_type = TX_BF16;
   g.desc.scale_mode = TX_SCALE_NONE;
-  if (side == 2)
+  if (side & 2)
     g.desc.ldb = d.N;
-  else
+  if (side & 1)
     g.desc.lda = d.K;
   g.kernel = TX_KERNEL_GEMM_16BIT;
-  return launchGemm(g, side == 1 ? ws : A, side == 2 ? ws : B, C, nullptr, nullptr, stream);
+  return launchGemm(g, (side & 1) ? wa : A, (side & 2) ? wb : B, C, nullptr, nullptr, stream);
 }
 
 int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,

@@ -58,6 +58,7 @@ __device__ __forceinline__ uint16_t mx_upcast1(uint32_t c, int fmt, uint32_t s) 
   return f32_to_bf16_rne(x);
 }
 
+
 // Hardware pair conversion: v_cvt_scalef32_pk_bf16_{fp8,bf8,fp4} decodes
 // two elements (bytes 2w, 2w + 1 of `src`, or byte `sel`'s two e2m1 nibbles)
 // and multiplies by one fp32 scale.  Used only where the scale exponent lies
@@ -79,6 +80,26 @@ __device__ __forceinline__ uint32_t mx_cvt_pair(uint32_t src, float scale) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
+// Scales: e8m0 per 32 K (MX), or e4m3 per 16 K (NV: the fp8e4nv scale
+// tensors of tl.dot_scaled).  An e4m3 scale is a plain multiplier; e2m1
+// times e4m3 has at most 6 significant bits, so the bf16 product is exact.
+// The pair conversion takes only the exponent of its fp32 scale (it serves
+// e8m0's powers of two), so e4m3 scales, which carry mantissa bits, always
+// take the element path.
+template <bool NV> struct ScaleKind {
+  static constexpr int GROUP = NV ? 16 : 32;
+  // the pair conversion applies (exact products, see mx_cvt_pair)
+  __device__ __forceinline__ static bool hw(uint32_t s) {
+    return !NV && s >= kHwScaleLo && s <= kHwScaleHi;
+  }
+  __device__ __forceinline__ static float factor(uint32_t s) {
+    return NV ? mx_decode(s, 0) : __builtin_amdgcn_ldexpf(1.0f, (int)s - 127);
+  }
+  __device__ __forceinline__ static uint16_t one(uint32_t c, int fmt, uint32_t s) {
+    return NV ? f32_to_bf16_rne(mx_decode(c, fmt) * mx_decode(s, 0)) : mx_upcast1(c, fmt, s);
+  }
+};
+
 // B side: dst[k][n] = upcast(B[k][n] * 2^(scale[n][k/32] - 127)).  A
 // thread owns 16 columns and the source rows of 8 consecutive K inside one
 // 32-K scale group (fp8 8 rows, e2m1 4 packed rows), so it loads its 16
@@ -87,8 +108,9 @@ __device__ __forceinline__ uint32_t mx_cvt_pair(uint32_t src, float scale) {
 // runs on K pairs of one column: fp8 bytes of rows k, k + 1 are paired by
 // v_perm_b32, e2m1 bytes hold K pairs already; results are re-paired into
 // row order by v_perm_b32.
-template <int FMT>
+template <int FMT, bool NV = false>
 __global__ void __launch_bounds__(256) mx_upcast_b_kernel(UpcastArgs p) {
+  typedef ScaleKind<NV> SK;
   constexpr int COLS = 16;              // columns per thread
   constexpr int RUN = FMT == 4 ? 4 : 8; // source rows per thread (8 K)
   constexpr int KR = FMT == 4 ? 2 : 1;  // K rows per source row
@@ -98,13 +120,13 @@ __global__ void __launch_bounds__(256) mx_upcast_b_kernel(UpcastArgs p) {
   if (t >= (srows / RUN) * groups)
     return;
   const int64_t r0 = (t / groups) * RUN, n0 = (t % groups) * COLS;
-  const int64_t kg = r0 * KR / 32; // the scale group of all RUN rows
+  const int64_t kg = r0 * KR / SK::GROUP; // the scale group of all RUN rows
   uint32_t sc[COLS];
   bool hw = true;
 #pragma unroll
   for (int i = 0; i < COLS; ++i) {
     sc[i] = p.scale[(n0 + i) * p.ld_scale + kg];
-    hw = hw && sc[i] >= kHwScaleLo && sc[i] <= kHwScaleHi;
+    hw = hw && SK::hw(sc[i]);
   }
   uint32_t w[RUN][COLS / 4]; // source dwords: row r, columns 4 q .. +3
 #pragma unroll
@@ -124,7 +146,7 @@ __global__ void __launch_bounds__(256) mx_upcast_b_kernel(UpcastArgs p) {
     float sf[COLS];
 #pragma unroll
     for (int i = 0; i < COLS; ++i)
-      sf[i] = __builtin_amdgcn_ldexpf(1.0f, (int)sc[i] - 127);
+      sf[i] = SK::factor(sc[i]);
     if constexpr (FMT == 4) {
       // byte i of a packed row: column n0 + i, K rows 2 r and 2 r + 1
 #pragma unroll
@@ -179,7 +201,7 @@ __global__ void __launch_bounds__(256) mx_upcast_b_kernel(UpcastArgs p) {
         for (int u = 0; u < 2; ++u) {
           const uint32_t byte = (w[r][(c + u) / 4] >> (8 * ((c + u) % 4))) & 0xFFu;
           const uint32_t code = FMT == 4 ? (h ? byte >> 4 : byte & 15) : byte;
-          e[u] = mx_upcast1(code, FMT, sc[c + u]);
+          e[u] = SK::one(code, FMT, sc[c + u]);
         }
         o[c / 2] = e[0] | (e[1] << 16);
       }
@@ -189,14 +211,15 @@ __global__ void __launch_bounds__(256) mx_upcast_b_kernel(UpcastArgs p) {
 }
 
 // A side: dst[m][k] = upcast(A[m][k] * 2^(scale[m][k/32] - 127)).
-template <int FMT>
+template <int FMT, bool NV = false>
 __global__ void __launch_bounds__(256) mx_upcast_a_kernel(UpcastArgs p) {
+  typedef ScaleKind<NV> SK;
   const int64_t groups = p.cols / 16; // 16 K per thread
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= p.rows * groups)
     return;
   const int64_t m = t / groups, k0 = (t % groups) * 16;
-  const uint32_t s = p.scale[m * p.ld_scale + k0 / 32];
+  const uint32_t s = p.scale[m * p.ld_scale + k0 / SK::GROUP];
   uint8_t code[16];
   if constexpr (FMT == 4)
     *reinterpret_cast<uint64_t *>(code) =
@@ -205,9 +228,9 @@ __global__ void __launch_bounds__(256) mx_upcast_a_kernel(UpcastArgs p) {
     *reinterpret_cast<u32x4 *>(code) =
         *reinterpret_cast<const u32x4 *>(p.src + m * p.ld_src + k0);
   uint16_t *d = p.dst + m * p.cols + k0;
-  if (s >= kHwScaleLo && s <= kHwScaleHi) {
+  if (SK::hw(s)) {
     // neighbouring K share the scale: pairs convert in place (see mx_cvt_pair)
-    const float sf = __builtin_amdgcn_ldexpf(1.0f, (int)s - 127);
+    const float sf = SK::factor(s);
     uint32_t o[8];
     const uint32_t *cw = reinterpret_cast<const uint32_t *>(code);
 #pragma unroll
@@ -230,7 +253,7 @@ __global__ void __launch_bounds__(256) mx_upcast_a_kernel(UpcastArgs p) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const uint32_t c = FMT == 4 ? (i & 1 ? code[i / 2] >> 4 : code[i / 2] & 15) : code[i];
-    out[i] = mx_upcast1(c, FMT, s);
+    out[i] = SK::one(c, FMT, s);
   }
   reinterpret_cast<u32x4 *>(d)[0] = *reinterpret_cast<const u32x4 *>(&out[0]);
   reinterpret_cast<u32x4 *>(d)[1] = *reinterpret_cast<const u32x4 *>(&out[8]);

@@ -119,8 +119,10 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
   else if (d->scale_mode == TX_SCALE_BLOCK128)
     scaleBytes = 4.0 * (M * cdiv(d->K, 128) +
                         (double)cdiv(d->K, 128) * cdiv(d->N, 128));
-  else if (d->scale_mode == TX_SCALE_MX32) // one e8m0 byte per 32 K; a bf16 side has none
-    scaleBytes = ((ba == 16 ? 0.0 : M) + (bb == 16 ? 0.0 : N)) * (double)cdiv(d->K, 32);
+  else if (d->scale_mode == TX_SCALE_MX32 || d->scale_mode == TX_SCALE_NV16)
+    // one scale byte per 32 K (e8m0) or 16 K (e4m3); a bf16 side has none
+    scaleBytes = ((ba == 16 ? 0.0 : M) + (bb == 16 ? 0.0 : N)) *
+                 (double)cdiv(d->K, d->scale_mode == TX_SCALE_NV16 ? 16 : 32);
   out->flops = 2.0 * M * N * K;
   // C once, twice when accumulating into it (read, then written)
   const double cPasses = (d->flags & TX_FLAG_ACCUMULATE) ? 2.0 : 1.0;
@@ -129,6 +131,8 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
   // a mixed product runs at the rate of its wider operand
   out->peak_flops = ba >= bb ? tx_mi355x_peak_flops(d->a_type)
                              : tx_mi355x_peak_flops(d->b_type);
+  if (d->scale_mode == TX_SCALE_NV16) // e4m3 scales run on the bf16 tile
+    out->peak_flops = tx_mi355x_peak_flops(TX_BF16);
   out->peak_bw = kHbm;
   out->ridge = out->peak_flops / out->peak_bw;
   out->bound = out->intensity > out->ridge ? TX_BOUND_MFMA : TX_BOUND_HBM;
@@ -138,7 +142,8 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
 
   Tile t{d->block_m, d->block_n, d->block_k, 1.0};
   if (t.bm <= 0 || t.bn <= 0 || t.bk <= 0) {
-    if (d->scale_mode == TX_SCALE_MX32 && (ba == 16 || bb == 16))
+    if ((d->scale_mode == TX_SCALE_MX32 && (ba == 16 || bb == 16)) ||
+        d->scale_mode == TX_SCALE_NV16)
       t = chooseTile(kTiles16, d->M, d->N, d->K); // MX x bf16 runs on the bf16 tile
     else if (d->scale_mode == TX_SCALE_MX32)
       t = ba == 4 ? kTileMx4 : kTileMx8;

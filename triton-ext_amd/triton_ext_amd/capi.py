@@ -10,7 +10,7 @@ F32, F16, BF16, I8, F8E4M3, I32, F8E5M2, F4E2M1 = 0, 1, 2, 3, 4, 5, 6, 7
 DTYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", I8: "i8", F8E4M3: "f8e4m3", I32: "i32",
                F8E5M2: "f8e5m2", F4E2M1: "f4e2m1"}
 # tx_scale_mode
-SCALE_NONE, SCALE_ROWCOL, SCALE_BLOCK128, SCALE_MX32 = 0, 1, 2, 3
+SCALE_NONE, SCALE_ROWCOL, SCALE_BLOCK128, SCALE_MX32, SCALE_NV16 = 0, 1, 2, 3, 4
 # tx_bound
 BOUND_UNKNOWN, BOUND_MFMA, BOUND_HBM = 0, 1, 2
 # tx_status

@@ -136,7 +136,9 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
     T:language/semantic.py:1597-1665; what this backend does not implement
     (fp16 operands, bf16 on both sides, e2m1 mixed with fp8, packing along M
     or N) raises NotImplementedError.  acc (fp32 [M, N]) returns acc + the
-    dot, as tl.dot_scaled's acc does.
+    dot, as tl.dot_scaled's acc does.  Scales given as torch.float8_e4m3fn
+    are e4m3 multipliers per 16 K ([M, K/16], [N, K/16]; Triton's fp8e4nv
+    scales): e2m1 (or bf16) operands, run through a bf16 upcast.
     """
     import torch
     for name, fmt in (("lhs_format", lhs_format), ("rhs_format", rhs_format)):
@@ -164,21 +166,30 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
     if rhs.shape[0] * pb != K:
         raise ValueError("Reduction dimension should pack the same number of elements; "
                          f"(lhs: {tuple(lhs.shape)} vs rhs: {tuple(rhs.shape)})")
-    # scale None: the operand is unscaled, i.e. e8m0 127 (2^0) in every group
-    # (a bf16 operand has none and reads none)
+    # e4m3 scales: one per 16 K (T:language/semantic.py:1597-1609)
+    nv = any(t is not None and t.dtype == torch.float8_e4m3fn for t in (lhs_scale, rhs_scale))
+    if nv and (lhs_format not in ("e2m1", "bf16") or rhs_format not in ("e2m1", "bf16")):
+        raise NotImplementedError("e4m3 scales are implemented for e2m1 operands")
+    g = 16 if nv else 32
+    # scale None: the operand is unscaled -- e8m0 127 (2^0), or e4m3 1.0
+    # (0x38) -- in every group (a bf16 operand has none and reads none)
+    unit = 0x38 if nv else 127
     if lhs_scale is None and lhs_format != "bf16":
-        lhs_scale = torch.full((M, K // 32), 127, dtype=torch.uint8, device=lhs.device)
+        lhs_scale = torch.full((M, K // g), unit, dtype=torch.uint8, device=lhs.device)
     if rhs_scale is None and rhs_format != "bf16":
-        rhs_scale = torch.full((N, K // 32), 127, dtype=torch.uint8, device=rhs.device)
-    if lhs_scale is not None and tuple(lhs_scale.shape) != (M, K // 32):
-        raise ValueError(f"lhs_scale must be a tensor of shape [{M}, {K // 32}]. "
+        rhs_scale = torch.full((N, K // g), unit, dtype=torch.uint8, device=rhs.device)
+    if nv:
+        lhs_scale, rhs_scale = (t.view(torch.uint8) if t is not None and t.dtype != torch.uint8
+                                else t for t in (lhs_scale, rhs_scale))
+    if lhs_scale is not None and tuple(lhs_scale.shape) != (M, K // g):
+        raise ValueError(f"lhs_scale must be a tensor of shape [{M}, {K // g}]. "
                          f"Got {list(lhs_scale.shape)}")
-    if rhs_scale is not None and tuple(rhs_scale.shape) != (N, K // 32):
-        raise ValueError(f"rhs_scale must be a tensor of shape [{N}, {K // 32}]. "
+    if rhs_scale is not None and tuple(rhs_scale.shape) != (N, K // g):
+        raise ValueError(f"rhs_scale must be a tensor of shape [{N}, {K // g}]. "
                          f"Got {list(rhs_scale.shape)}")
     for t, nm in ((lhs_scale, "lhs_scale"), (rhs_scale, "rhs_scale")):
         if t is not None and (t.dtype != torch.uint8 or not t.is_contiguous()):
-            raise ValueError(f"{nm} must be a contiguous uint8 (e8m0) tensor")
+            raise ValueError(f"{nm} must be a contiguous uint8 (e8m0) or float8_e4m3fn tensor")
     if lhs.stride(1) != 1 or rhs.stride(1) != 1:
         raise ValueError("lhs and rhs rows must be contiguous")
     flags = 0
@@ -197,8 +208,8 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
         ldb = rhs.stride(0) if K > 0 and N > 0 else 0
         desc = capi.make_desc(M, N, K, _MX_FORMATS.get(lhs_format, capi.BF16), c_tx,
                               b_type=_MX_FORMATS.get(rhs_format, capi.BF16),
-                              scale_mode=capi.SCALE_MX32, block=block, lda=lda, ldb=ldb,
-                              flags=flags)
+                              scale_mode=capi.SCALE_NV16 if nv else capi.SCALE_MX32,
+                              block=block, lda=lda, ldb=ldb, flags=flags)
         plan = capi.plan(desc)
     if out is None:
         out = torch.empty((M, N), dtype=_torch_dtype(c_tx), device=lhs.device)
