@@ -74,12 +74,12 @@ class Launcher:
         self.L = tx.load()
         sm = scale_mode if scale_mode is not None else tx.SCALE_NONE
         self.plan = tx.plan_for(a, b, tx.tx_type(out), sm, block)
-        self.ws = tx.workspace_for(self.plan, a.device)
+        stream = torch.cuda.current_stream().cuda_stream
+        self.ws = tx.workspace_for(self.plan, a.device, stream)
         self.args = (ctypes.byref(self.plan), a.data_ptr(), b.data_ptr(), out.data_ptr(),
                      None if sa is None else sa.data_ptr(), None if sb is None else sb.data_ptr(),
                      None if self.ws is None else self.ws.data_ptr(),
-                     0 if self.ws is None else self.ws.numel(),
-                     torch.cuda.current_stream().cuda_stream)
+                     0 if self.ws is None else self.ws.numel(), stream)
         self.keep = (a, b, out, sa, sb)
 
     def __call__(self):

@@ -175,7 +175,9 @@ struct tx_dot_plan {
   int32_t block_threads;
   int64_t workspace_bytes; /* device scratch the launch needs (0 = none) */
   int32_t passes_run;      /* number of passes the pipeline ran */
-  int32_t reserved;
+  /* Tile rows per group of the XCD-aware tile order (tiles of one XCD walk
+   * group_m tile rows at a time); any value >= 1 gives the same result. */
+  int32_t group_m;
 };
 
 /* Validate `desc`, run the plan pipeline and fill `plan`. */
@@ -184,8 +186,11 @@ TX_API int tx_dot_plan_create(const tx_dot_desc *desc, tx_dot_plan *plan);
 /* Enqueue the planned dot on `stream`.  `scale_a`/`scale_b` are required for
  * the scaled modes and ignored otherwise: fp32 arrays for TX_SCALE_ROWCOL and
  * TX_SCALE_BLOCK128, uint8 e8m0 arrays for TX_SCALE_MX32.  `workspace`
- * must hold plan->workspace_bytes bytes when that is non-zero; its contents
- * on entry do not matter.  Concurrent launches must not share a workspace. */
+ * must hold plan->workspace_bytes bytes when that is non-zero, and be
+ * zero-filled before its first use: the W8A8 decode kernel keeps arrival
+ * counters at its start, which every completed launch leaves at zero again
+ * (the rest of the workspace needs no particular contents).  Launches that
+ * may overlap in time (different streams) must not share a workspace. */
 TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A, const void *B,
                          void *C, const void *scale_a, const void *scale_b,
                          void *workspace, size_t workspace_bytes, void *stream);

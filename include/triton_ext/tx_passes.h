@@ -104,8 +104,18 @@ TX_API int32_t tx_dtype_bits(int32_t dtype);
 TX_API double tx_mi355x_peak_flops(int32_t dtype);
 /* MI355X HBM3E peak bytes/s. */
 TX_API double tx_mi355x_peak_bw(void);
-/* Classify a dot and recommend a tile (desc->block_* if non-zero). */
+/* Classify a dot and recommend a tile (desc->block_* if non-zero).  The
+ * 256-wide tiles address A and B through 32-bit buffer offsets, so an
+ * operand spanning 2 GiB or more (tx_dot_operand_spans) gets a 128x128 tile,
+ * whose loads use 64-bit addresses. */
 TX_API int tx_arith_intensity(const tx_dot_desc *desc, tx_ai_report *out);
+/* Bytes from A's first element to one past its last, and the same for B,
+ * with desc's strides (0 = packed; B [N][K] under TX_FLAG_B_KMAJOR; e2m1
+ * packed two per byte along K).  Saturates at INT64_MAX.  TX_ERR_INVALID for
+ * a NULL argument or an unknown dtype. */
+TX_API int tx_dot_operand_spans(const tx_dot_desc *desc, int64_t *a_bytes, int64_t *b_bytes);
+/* Largest operand span (bytes, exclusive) the 32-bit-offset tiles take. */
+#define TX_SPAN32_LIMIT ((int64_t)1 << 31)
 
 #ifdef __cplusplus
 }

@@ -356,3 +356,83 @@ def test_launch_without_device_fails_cleanly():
     assert L.tx_dot_launch(None, addr, addr, addr, None, None, None, 0, None) == tx.ERR_INVALID
     assert L.tx_dot_launch(ctypes.byref(p), None, addr, addr, None, None, None, 0, None) == tx.ERR_INVALID
     assert L.tx_dot_launch(ctypes.byref(p), addr + 2, addr, addr, None, None, None, 0, None) == tx.ERR_INVALID
+
+
+def test_operand_spans_and_32bit_tiles():
+    """The 256-wide tiles address A and B through 32-bit buffer offsets.  An
+    operand spanning 2^31 bytes or more gets a 128x128 tile (64-bit
+    addresses) from the tile choice, and an explicit 256-wide tile is
+    rejected at plan time, before any launch."""
+    spans = tx.load("libarith_intensity.so").tx_dot_operand_spans
+    a, b = ctypes.c_int64(), ctypes.c_int64()
+
+    def span(desc):
+        assert spans(ctypes.byref(desc), ctypes.byref(a), ctypes.byref(b)) == tx.OK
+        return a.value, b.value
+    assert span(tx.make_desc(300, 200, 100, tx.BF16, tx.F32, lda=104, ldb=208)) == \
+        ((299 * 104 + 100) * 2, (99 * 208 + 200) * 2)
+    assert span(tx.make_desc(64, 32, 128, tx.BF16, tx.F32, flags=tx.FLAG_B_KMAJOR)) == \
+        (64 * 128 * 2, 32 * 128 * 2)
+    assert span(tx.make_desc(8, 16, 64, tx.F4E2M1, tx.F32, scale_mode=tx.SCALE_MX32)) == \
+        (8 * 64 // 2, 32 * 16)
+    assert span(tx.make_desc(0, 16, 64, tx.I8, tx.I32))[0] == 0
+    # bf16 32768 x 32768: 2 GiB each, exactly the first span the tiles cannot take
+    big = tx.make_desc(32768, 32768, 32768, tx.BF16, tx.BF16)
+    assert span(big) == (1 << 31, 1 << 31)
+    p = tx.plan(big)
+    assert (p.desc.block_m, p.desc.block_n) == (128, 128) and p.kernel == tx.KERNEL_GEMM_16BIT
+    assert _err(tx.make_desc(32768, 32768, 32768, tx.BF16, tx.BF16,
+                             block=(256, 256, 64))) == tx.ERR_UNSUPPORTED
+    assert b"32-bit" in tx.load().tx_get_last_error()
+    # just under 2 GiB each: the 256-wide tile
+    d = tx.make_desc(32767, 32760, 32768, tx.BF16, tx.BF16, ldb=32768)
+    assert span(d) == (32767 * 32768 * 2, (1 << 31) - 16)
+    p = tx.plan(d)
+    assert p.desc.block_m == 256
+    # int8 4 GiB A (the advisor's case): 128x128 register tile; explicit 256 rejected
+    p = tx.plan(tx.make_desc(131072, 4096, 32768, tx.I8, tx.I32))
+    assert (p.desc.block_m, p.desc.block_n) == (128, 128) and p.kernel == tx.KERNEL_GEMM_I8
+    assert _err(tx.make_desc(131072, 4096, 32768, tx.I8, tx.I32,
+                             block=(256, 256, 128))) == tx.ERR_UNSUPPORTED
+    # fp8 4 GiB A, block-scaled: the 128x128 fp8 tile
+    p = tx.plan(tx.make_desc(65536, 4096, 65536, tx.F8E4M3, tx.BF16,
+                             scale_mode=tx.SCALE_BLOCK128))
+    assert (p.desc.block_m, p.desc.block_n) == (128, 128)
+    # K-major B and MX have only 256-wide tiles: rejected
+    assert _err(tx.make_desc(65536, 4096, 32768, tx.BF16, tx.F32,
+                             flags=tx.FLAG_B_KMAJOR)) == tx.ERR_UNSUPPORTED
+    assert _err(tx.make_desc(65536, 256, 65536, tx.F8E4M3, tx.F32,
+                             scale_mode=tx.SCALE_MX32)) == tx.ERR_UNSUPPORTED
+    # the W8A8 decode kernel uses 64-bit addresses: B of 4 GiB plans
+    p = tx.plan(tx.make_desc(16, 65536, 65536, tx.I8, tx.BF16, scale_mode=tx.SCALE_ROWCOL))
+    assert p.kernel == tx.KERNEL_DECODE_I8
+
+
+def test_nv16_needs_whole_scale_groups():
+    """e4m3 scales per 16: K % 16 == 0, also when the other side is bf16."""
+    NV = tx.SCALE_NV16
+    for K in (24, 40, 1032):
+        assert _err(tx.make_desc(64, 64, K, tx.BF16, tx.F32, b_type=tx.F4E2M1,
+                                 scale_mode=NV)) == tx.ERR_UNSUPPORTED
+        assert b"K % 16" in tx.load().tx_get_last_error()
+    assert tx.plan(tx.make_desc(64, 64, 32, tx.BF16, tx.F32, b_type=tx.F4E2M1,
+                                scale_mode=NV)).kernel == tx.KERNEL_GEMM_MX_BF16
+
+
+def test_plan_and_acc_must_agree():
+    """dot() / dot_scaled() with a caller's plan: FLAG_ACCUMULATE set exactly
+    when acc is given (checked before anything reaches the device)."""
+    import torch
+    a = torch.zeros(64, 64, dtype=torch.bfloat16)
+    acc = torch.zeros(64, 64, dtype=torch.float32)
+    plain = tx.plan(tx.make_desc(64, 64, 64, tx.BF16, tx.F32))
+    accum = tx.plan(tx.make_desc(64, 64, 64, tx.BF16, tx.F32, flags=tx.FLAG_ACCUMULATE))
+    with pytest.raises(ValueError, match="disagree on acc"):
+        tx.dot(a, a, acc=acc, plan=plain)
+    with pytest.raises(ValueError, match="disagree on acc"):
+        tx.dot(a, a, out_dtype=torch.float32, plan=accum)
+    q = torch.zeros(64, 64, dtype=torch.uint8)
+    s = torch.full((64, 2), 127, dtype=torch.uint8)
+    mxp = tx.plan(tx.make_desc(64, 64, 64, tx.F8E4M3, tx.F32, scale_mode=tx.SCALE_MX32))
+    with pytest.raises(ValueError, match="disagree on acc"):
+        tx.dot_scaled(q, s, "e4m3", q, s, "e4m3", acc=acc, plan=mxp)

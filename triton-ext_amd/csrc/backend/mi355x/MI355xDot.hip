@@ -28,7 +28,6 @@
 
 #include "decode_i8.h"
 #include "gemm16_dma.h"
-#include "gemm16_pp.h"
 #include "gemm8_w4.h"
 #include "gemm8_n224.h"
 #include "gemm16_w4.h"
@@ -71,10 +70,11 @@ struct GemmConfig {
   GemmKernelFn fn;
   int bt;        // B K-major (TX_FLAG_B_KMAJOR)
   int lds_bytes; // dynamic LDS (0 for kernels with static LDS)
-  int dma;       // 1: direct-to-LDS staging + transpose reads (gemm16_dma.h),
-                 // 2: the same staging with 4 waves of 128x128 (gemm16_w4.h),
-                 // 3: 8 waves of 128x64 (gemm16_w4.h), 4: 8-wave ping-pong
-                 // (gemm16_pp.h), 5: 8-bit 256x256x128 tile (gemm8_w4.h)
+  int dma;       // 0: register-staged (gemm_tile.h), 1: direct-to-LDS
+                 // staging with 64-bit addresses (gemm16_dma.h), 2: 16-bit
+                 // 256x256 tile (gemm16_w4.h), 5: 8-bit 256x256x128 and
+                 // 256x224x128 tiles (gemm8_w4.h, gemm8_n224.h); 2 and 5
+                 // address A and B through 32-bit buffer offsets
   int fmt;       // MX operand formats: MFMA code of A | code of B << 4
 };
 
@@ -95,11 +95,6 @@ struct GemmConfig {
   GemmConfig { OP, 256, 256, 64, 2, 2, EPI, gemm16_w4_kernel<OP, EPI, 4>, 0, 0, 2 }
 #define TX_GEMM_W4T(OP, EPI)                                                   \
   GemmConfig { OP, 256, 256, 64, 2, 2, EPI, gemm16_w4_kernel<OP, EPI, 4, true>, 1, 0, 2 }
-#define TX_GEMM_W8(OP, EPI)                                                    \
-  GemmConfig { OP, 256, 256, 64, 2, 4, EPI, gemm16_w4_kernel<OP, EPI, 8>, 0, 0, 3 }
-#define TX_GEMM_PP(OP, EPI)                                                    \
-  GemmConfig { OP, 256, 256, 64, 2, 4, EPI, gemm16_pp_kernel<OP, EPI>, 0, 0, 4 }
-
 #define TX_GEMM_8(OP, EPI)                                                     \
   GemmConfig { OP, 256, 256, 128, 2, 4, EPI, gemm8_w4_kernel<OP, EPI>, 0, 0, 5 }
 // MX (tl.dot_scaled) tiles: MFMA format codes FA, FB (0 e4m3, 1 e5m2,
@@ -118,16 +113,10 @@ struct GemmConfig {
 #define TX_GEMM_8N(OP, EPI)                                                    \
   GemmConfig { OP, 256, 224, 128, 4, 2, EPI, gemm8_n224_kernel<OP, EPI>, 0, 0, 5 }
 
-// Lookup takes the first match among the entries the tuning override
-// allows (findGemmConfig): by default the 4-wave 256x256 tile, then the
-// direct-to-LDS and register-staged tiles of other shapes.
+// Every (operands, tile, epilogue) instantiated; findGemmConfig takes the
+// entry that matches a plan exactly.
 const GemmConfig kGemmConfigs[] = {
-    // bf16 / fp16 operands, 256x256 tiles: the tuning override selects among
-    // the 4-wave, 8-wave and ping-pong variants (first match wins)
-    TX_GEMM_W8(OP_BF16, EPI_BF16),
-    TX_GEMM_W8(OP_BF16, EPI_F32),
-    TX_GEMM_W8(OP_F16, EPI_F32),
-    TX_GEMM_W8(OP_F16, EPI_F16),
+    // bf16 / fp16 operands, 256x256x64 tiles of 4 waves
     TX_GEMM_W4(OP_BF16, EPI_BF16),
     TX_GEMM_W4(OP_BF16, EPI_F32),
     TX_GEMM_W4(OP_F16, EPI_F32),
@@ -137,24 +126,15 @@ const GemmConfig kGemmConfigs[] = {
     TX_GEMM_W4T(OP_BF16, EPI_F32),
     TX_GEMM_W4T(OP_F16, EPI_F32),
     TX_GEMM_W4T(OP_F16, EPI_F16),
-    TX_GEMM_PP(OP_BF16, EPI_BF16),
-    // bf16 / fp16 operands: direct-to-LDS staging, 8 waves (4x2) per 256x256
-    TX_GEMM_DMA(OP_BF16, 256, 256, 64, 4, 2, EPI_BF16),
-    TX_GEMM_DMA(OP_BF16, 256, 256, 64, 4, 2, EPI_F32),
+    // bf16 / fp16 operands, 128x128x64 tiles: direct-to-LDS staging, 64-bit
+    // addresses (operands spanning 2 GiB or more)
     TX_GEMM_DMA(OP_BF16, 128, 128, 64, 2, 2, EPI_BF16),
     TX_GEMM_DMA(OP_BF16, 128, 128, 64, 2, 2, EPI_F32),
-    TX_GEMM_DMA(OP_F16, 256, 256, 64, 4, 2, EPI_F32),
-    TX_GEMM_DMA(OP_F16, 256, 256, 64, 4, 2, EPI_F16),
     TX_GEMM_DMA(OP_F16, 128, 128, 64, 2, 2, EPI_F32),
     TX_GEMM_DMA(OP_F16, 128, 128, 64, 2, 2, EPI_F16),
-    // register-staged tiles: the 64x64x32 tile, and 128x128 under
-    // TX_GEMM16_IMPL=regs (a 256x256 tile does not fit this scheme's registers)
-    TX_GEMM(OP_BF16, 128, 128, 64, 2, 2, EPI_BF16),
-    TX_GEMM(OP_BF16, 128, 128, 64, 2, 2, EPI_F32),
+    // register-staged 64x64x32 tiles
     TX_GEMM(OP_BF16, 64, 64, 32, 2, 2, EPI_BF16),
     TX_GEMM(OP_BF16, 64, 64, 32, 2, 2, EPI_F32),
-    TX_GEMM(OP_F16, 128, 128, 64, 2, 2, EPI_F32),
-    TX_GEMM(OP_F16, 128, 128, 64, 2, 2, EPI_F16),
     TX_GEMM(OP_F16, 64, 64, 32, 2, 2, EPI_F32),
     TX_GEMM(OP_F16, 64, 64, 32, 2, 2, EPI_F16),
     // int8 / fp8 operands, 256x256x128 tiles of 8 waves (gemm8_w4.h)
@@ -304,31 +284,8 @@ void classify(const tx_dot_desc &d, int *op, int *epi) {
 }
 
 int findGemmConfig(int op, int epi, int bm, int bn, int bk, bool bt, int fmt) {
-  // Tuning override TX_GEMM16_IMPL: "regs" (register staging), "dma8"
-  // (8-wave direct-to-LDS), "w8" (8 waves of 128x64), "pp" (ping-pong);
-  // default: 4 waves of 128x128 (fastest of these at 4096^3 on MI355X).
-  static const int want = [] {
-    const char *e = std::getenv("TX_GEMM16_IMPL");
-    if (!e)
-      return 2;
-    if (std::strcmp(e, "w4") == 0)
-      return 2;
-    if (std::strcmp(e, "regs") == 0)
-      return 0;
-    if (std::strcmp(e, "dma8") == 0)
-      return 1;
-    if (std::strcmp(e, "w8") == 0)
-      return 3;
-    if (std::strcmp(e, "pp") == 0)
-      return 4;
-    return 2;
-  }();
-  const bool is8 = op == OP_I8 || op == OP_F8;
   for (int i = 0; i < kNumGemmConfigs; ++i) {
     const GemmConfig &c = kGemmConfigs[i];
-    // (K-major B has one kernel, outside the tuning override)
-    if (!is8 && !bt && (c.dma > want || (c.dma >= 2 && c.dma != want)))
-      continue;
     if (c.op == op && c.epi == epi && c.bm == bm && c.bn == bn && c.bk == bk &&
         c.bt == (int)bt && c.fmt == fmt)
       return i;
@@ -351,25 +308,13 @@ int decodeSlices(int64_t M) { return (int)cdiv(M > 0 ? M : 1, 16 * decodeMT(M));
 
 // Split-K factor for the decode kernel: a power of two (<= kMaxSplit) so
 // that slices * strips * ksplit workgroups cover the CUs about once, each
-// with at least four 64-row batches per wave.  TX_DECODE_KSPLIT overrides.
+// with at least four 64-row batches per wave.
 int decodeSplit(int64_t M, int64_t N, int64_t K) {
-  const char *env = std::getenv("TX_DECODE_KSPLIT");
   const int64_t strips = cdiv(N, kDecodeStripN) * decodeSlices(M);
   const int64_t batches = cdiv(K, kDecodeBatchK);
   int ks = 1;
-  if (env && *env) {
-    ks = std::atoi(env);
-  } else {
-    while (ks < (int)kMaxSplit && strips * ks < 256 &&
-           batches / (ks * 2) >= 4 * kDecodeWaves)
-      ks *= 2;
-  }
-  if (ks < 1)
-    ks = 1;
-  if (ks > (int)kMaxSplit)
-    ks = kMaxSplit;
-  while (ks & (ks - 1)) // round down to a power of two
-    ks &= ks - 1;
+  while (ks < (int)kMaxSplit && strips * ks < 256 && batches / (ks * 2) >= 4 * kDecodeWaves)
+    ks *= 2;
   while (ks > 1 && cdiv(batches, ks) * (ks - 1) >= batches)
     ks >>= 1; // every split must own at least one batch
   return ks;
@@ -417,6 +362,33 @@ int txMi355xDotRun(tx_dot_plan *plan) {
                 d.block_m, d.block_n, d.block_k);
   const GemmConfig &c = kGemmConfigs[ci];
   const bool upcast = mxUpcastSide(d) != 0;
+  if (c.dma == 2 || c.dma == 5) {
+    // These tiles address A, B and the block scales through 32-bit buffer
+    // offsets (out-of-range chunks at offset 2^31 read zeros).
+    tx_dot_desc e = d; // the operands as the tile reads them
+    if (upcast) {
+      if (mxUpcastSide(d) & 1)
+        e.a_type = TX_BF16, e.lda = d.K;
+      if (mxUpcastSide(d) & 2)
+        e.b_type = TX_BF16, e.ldb = d.N;
+    }
+    int64_t sa = 0, sb = 0;
+    tx_dot_operand_spans(&e, &sa, &sb);
+    const int64_t kb = cdiv(d.K, 128);
+    if (sa >= TX_SPAN32_LIMIT || sb >= TX_SPAN32_LIMIT ||
+        (d.scale_mode == TX_SCALE_BLOCK128 &&
+         (d.M * kb * 4 >= TX_SPAN32_LIMIT || kb * cdiv(d.N, 128) * 4 >= TX_SPAN32_LIMIT)))
+      return fail(TX_ERR_UNSUPPORTED,
+                  "the %dx%d tile addresses operands through 32-bit offsets: A spans %lld "
+                  "bytes, B %lld (limit 2^31); a 128x128 tile takes larger operands",
+                  c.bm, c.bn, (long long)sa, (long long)sb);
+  }
+  // Tile rows per group of the XCD-aware tile order: 4, except 2 on the 8-bit
+  // tile once K spans 8192 bytes or more (a sweep of 1..32: mxfp8 8192^3 ran
+  // 2365 TFLOP/s at 2 against 1930 at 4; 4096^3, C5 (K = 7168) and mxfp4
+  // 8192^3 (K = 4096 bytes) were as fast or faster at 4).
+  const int64_t kbytes = d.K * tx_dtype_bits(d.a_type) / 8;
+  plan->group_m = c.dma == 5 && kbytes >= 8192 ? 2 : 4;
   plan->kernel = op == OP_I8                     ? TX_KERNEL_GEMM_I8
                : upcast                        ? TX_KERNEL_GEMM_MX_BF16
                : d.scale_mode == TX_SCALE_MX32 ? TX_KERNEL_GEMM_MX
@@ -457,6 +429,8 @@ int validate(const tx_dot_desc *in, tx_dot_desc *d) {
       return fail(TX_ERR_UNSUPPORTED, "e4m3 scales per 16 take e2m1 operands (one may be bf16)");
     if (bt)
       return fail(TX_ERR_UNSUPPORTED, "e4m3-scaled operands take B as [K][N]");
+    if (d->K % 16)
+      return fail(TX_ERR_UNSUPPORTED, "e4m3 scales need K %% 16 == 0 (one scale per 16)");
     if ((d->M > d->N ? d->M : d->N) * (d->K / 16) >= ((int64_t)1 << 31))
       return fail(TX_ERR_UNSUPPORTED, "scale arrays above 2 GiB");
   }
@@ -610,16 +584,7 @@ int launchGemm(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   a.last_ks = total > 0 ? (int32_t)cdiv(d.K - (int64_t)(total - 1) * d.block_k, km) : 0;
   if (a.last_ks > d.block_k / km)
     a.last_ks = d.block_k / km;
-  static const int group_env = [] {
-    const char *e = std::getenv("TX_GROUP_M"); // tuning override
-    return e ? std::atoi(e) : 0;
-  }();
-  // Tile rows per group of the XCD-aware tile order: 4, except 2 on the 8-bit
-  // tile once K spans 8192 bytes or more (a sweep of 1..32: mxfp8 8192^3 ran
-  // 2365 TFLOP/s at 2 against 1930 at 4; 4096^3, C5 (K = 7168) and mxfp4
-  // 8192^3 (K = 4096 bytes) were as fast or faster at 4).
-  const int64_t kbytes = d.K * tx_dtype_bits(d.a_type) / 8;
-  const int gm = group_env > 0 ? group_env : (c.dma == 5 && kbytes >= 8192 ? 2 : 4);
+  const int gm = plan.group_m > 0 ? plan.group_m : 1;
   a.group_m = plan.m_tiles < gm ? plan.m_tiles : gm;
   a.sa_ld = (int32_t)(mx ? d.K / 32 : cdiv(d.K, 128));
   a.sb_ld = (int32_t)cdiv(d.N, 128);

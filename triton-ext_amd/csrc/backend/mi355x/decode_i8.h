@@ -34,10 +34,10 @@
 //    last workgroup of a column strip (arrival counter) adds the partials in
 //    split order and applies the epilogue.  Integer addition is exact, so the
 //    result does not depend on the order.
-//  * Arrival counters are never reset: each workgroup adds kMaxSplit/ksplit,
-//    so a launch moves every counter by exactly kMaxSplit and the last
-//    arrival is the one that brings it to a multiple of kMaxSplit.  The
-//    counters must be zero once, when the workspace is created.
+//  * Arrival counters: each workgroup of a column strip adds 1; the one that
+//    brings the counter to ksplit is the last and sets it back to zero, so a
+//    completed launch leaves every counter at zero.  The counters must be
+//    zero before the first launch on a workspace.
 //
 // K loop in LoopSplit form: batches below k_main_batches have every row
 // < K and load unmasked; the rest (the peeled tail) send rows >= K, columns
@@ -364,11 +364,13 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) {
-    const uint32_t inc = kMaxSplit / (uint32_t)p.ksplit;
-    const uint32_t old = __hip_atomic_fetch_add(&p.counters[slice * strips + strip], inc, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t *const ctr = &p.counters[slice * strips + strip];
+    const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old + 1 == (uint32_t)p.ksplit;
+    if (last) // every split has arrived: none touches the counter again
+      __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // st4 holds no reduction region: its first word carries the flag
-    *reinterpret_cast<volatile uint32_t *>(st4) = ((old + inc) % kMaxSplit) == 0;
+    *reinterpret_cast<volatile uint32_t *>(st4) = last;
   }
   __syncthreads();
   if (!*reinterpret_cast<volatile uint32_t *>(st4))

@@ -14,6 +14,7 @@
 #include "triton_ext/tx_dot.h"
 #include "triton_ext/tx_passes.h"
 
+#include <climits>
 #include <cmath>
 #include <cstdint>
 
@@ -53,11 +54,12 @@ double tileCost(const Tile &t, int64_t M, int64_t N, int64_t K) {
   return (double)waves * t.bm * t.bn * (double)K / t.eff;
 }
 
+// Cheapest candidate from index `first` on (the 256-wide tile is index 0).
 template <size_t N>
-Tile chooseTile(const Tile (&cands)[N], int64_t M, int64_t Nn, int64_t K) {
-  Tile best = cands[0];
+Tile chooseTile(const Tile (&cands)[N], int64_t M, int64_t Nn, int64_t K, size_t first = 0) {
+  Tile best = cands[first];
   double bestCost = tileCost(best, M, Nn, K);
-  for (size_t i = 1; i < N; ++i) {
+  for (size_t i = first + 1; i < N; ++i) {
     double c = tileCost(cands[i], M, Nn, K);
     if (c < bestCost) {
       best = cands[i];
@@ -103,6 +105,33 @@ extern "C" double tx_mi355x_peak_flops(int32_t dtype) {
 
 extern "C" double tx_mi355x_peak_bw(void) { return kHbm; }
 
+extern "C" int tx_dot_operand_spans(const tx_dot_desc *d, int64_t *a_bytes, int64_t *b_bytes) {
+  if (!d || !a_bytes || !b_bytes)
+    return TX_ERR_INVALID;
+  const int32_t ba = tx_dtype_bits(d->a_type), bb = tx_dtype_bits(d->b_type);
+  if (!ba || !bb)
+    return TX_ERR_INVALID;
+  const bool bt = (d->flags & TX_FLAG_B_KMAJOR) != 0;
+  const int64_t lda = d->lda ? d->lda : d->K;
+  const int64_t ldb = d->ldb ? d->ldb : (bt ? d->K : d->N);
+  // ((rows - 1) * ld + len) elements of `bits` bits, in 128-bit arithmetic
+  auto span = [](int64_t rows, int64_t ld, int64_t len, int32_t bits) -> int64_t {
+    if (rows <= 0 || len <= 0)
+      return 0;
+    const __int128 e = (__int128)(rows - 1) * ld + len;
+    const __int128 b = (e * bits + 7) / 8;
+    return b > (__int128)INT64_MAX ? INT64_MAX : (int64_t)b;
+  };
+  *a_bytes = span(d->M, lda, d->K, ba);
+  if (bt)
+    *b_bytes = span(d->N, ldb, d->K, bb);
+  else if (bb == 4) // packed rows of two K values: K / 2 rows of ldb bytes
+    *b_bytes = span((d->K + 1) / 2, ldb, d->N, 8);
+  else
+    *b_bytes = span(d->K, ldb, d->N, bb);
+  return TX_OK;
+}
+
 extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
   if (!d || !out)
     return TX_ERR_INVALID;
@@ -142,23 +171,36 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
 
   Tile t{d->block_m, d->block_n, d->block_k, 1.0};
   if (t.bm <= 0 || t.bn <= 0 || t.bk <= 0) {
-    if ((d->scale_mode == TX_SCALE_MX32 && (ba == 16 || bb == 16)) ||
-        d->scale_mode == TX_SCALE_NV16)
-      t = chooseTile(kTiles16, d->M, d->N, d->K); // MX x bf16 runs on the bf16 tile
+    // Operands as the tile reads them (an upcast MX side: packed bf16), and
+    // whether the 256-wide tiles (32-bit buffer offsets) can address them.
+    const bool upcast = (d->scale_mode == TX_SCALE_MX32 && (ba == 16 || bb == 16)) ||
+                        d->scale_mode == TX_SCALE_NV16;
+    tx_dot_desc e = *d;
+    if (upcast) {
+      if (e.a_type != TX_BF16)
+        e.a_type = TX_BF16, e.lda = 0;
+      if (e.b_type != TX_BF16)
+        e.b_type = TX_BF16, e.ldb = 0;
+    }
+    int64_t spanA = 0, spanB = 0;
+    tx_dot_operand_spans(&e, &spanA, &spanB);
+    const size_t first = spanA < TX_SPAN32_LIMIT && spanB < TX_SPAN32_LIMIT ? 0 : 1;
+    if (upcast)
+      t = chooseTile(kTiles16, d->M, d->N, d->K, first); // MX x bf16 runs on the bf16 tile
     else if (d->scale_mode == TX_SCALE_MX32)
       t = ba == 4 ? kTileMx4 : kTileMx8;
     else if (sa == 2 && (d->flags & TX_FLAG_B_KMAJOR))
       t = kTiles16[0]; // the K-major B kernel exists for this tile only
     else if (sa == 2)
-      t = chooseTile(kTiles16, d->M, d->N, d->K);
+      t = chooseTile(kTiles16, d->M, d->N, d->K, first);
     else if (d->a_type == TX_I8 && d->scale_mode == TX_SCALE_ROWCOL && d->M <= 256)
       // W8A8 decode: one row slice up to M = 64, slices of 64 beyond,
       // 128-column strips, 64-row K batches
       t = Tile{(int32_t)(d->M > 64 ? 64 : 16 * cdiv(d->M > 0 ? d->M : 1, 16)), 128, 64, 1.0};
     else if (d->a_type == TX_F8E4M3 || d->a_type == TX_F8E5M2)
-      t = kTiles8[0]; // the register-staged 128x128 tile is slower everywhere
+      t = kTiles8[first]; // the register-staged 128x128 tile is slower everywhere
     else
-      t = chooseTile(kTiles8, d->M, d->N, d->K);
+      t = chooseTile(kTiles8, d->M, d->N, d->K, first);
   }
   out->block_m = t.bm;
   out->block_n = t.bn;

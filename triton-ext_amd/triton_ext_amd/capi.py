@@ -48,7 +48,7 @@ class DotPlan(ctypes.Structure):
                 ("kernel", ctypes.c_int32), ("split_k", ctypes.c_int32),
                 ("grid_x", ctypes.c_int32), ("grid_y", ctypes.c_int32), ("grid_z", ctypes.c_int32),
                 ("block_threads", ctypes.c_int32), ("workspace_bytes", ctypes.c_int64),
-                ("passes_run", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+                ("passes_run", ctypes.c_int32), ("group_m", ctypes.c_int32)]
 
 
 class AttnDesc(ctypes.Structure):
@@ -89,8 +89,8 @@ EXPORTS = {
         "txPassManagerRun", "txRegisterPassArgument", "txPassManagerParsePipeline",
         "txReadExtConf"],
     "libloop_split.so": ["tx_loop_split_plan", "tx_loop_split_k"],
-    "libarith_intensity.so": ["tx_dtype_size", "tx_mi355x_peak_flops", "tx_mi355x_peak_bw",
-                              "tx_arith_intensity"],
+    "libarith_intensity.so": ["tx_dtype_size", "tx_dtype_bits", "tx_mi355x_peak_flops",
+                              "tx_mi355x_peak_bw", "tx_arith_intensity", "tx_dot_operand_spans"],
     "libmi355x_dot.so": ["tx_dot_plan_create", "tx_dot_launch", "tx_get_last_error",
                          "tx_kernel_name", "tx_device_available"],
 }
@@ -140,6 +140,8 @@ def load(name="libmi355x_dot.so"):
         L.tx_mi355x_peak_flops.restype = ctypes.c_double
         L.tx_mi355x_peak_bw.restype = ctypes.c_double
         L.tx_arith_intensity.argtypes = [ctypes.POINTER(DotDesc), ctypes.POINTER(AIReport)]
+        L.tx_dot_operand_spans.argtypes = [ctypes.POINTER(DotDesc), ctypes.POINTER(i64),
+                                           ctypes.POINTER(i64)]
     elif name == "libmi355x_dot.so":
         L.tx_dot_plan_create.argtypes = [ctypes.POINTER(DotDesc), ctypes.POINTER(DotPlan)]
         L.tx_dot_launch.argtypes = [ctypes.POINTER(DotPlan), vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]

@@ -49,16 +49,20 @@ def plan_for(a, b, out_dtype_tx, scale_mode=capi.SCALE_NONE, block=(0, 0, 0), fl
     return capi.plan(desc)
 
 
-def workspace_for(p, device):
-    """A zero-initialised workspace of at least p.workspace_bytes, cached per device.
+def workspace_for(p, device, stream):
+    """A zero-initialised workspace of at least p.workspace_bytes, cached per
+    (device, stream): launches on one stream run one after another, so they
+    may share it; launches on different streams may overlap and get their own.
 
-    The decode kernel's arrival counters must start at zero once; after that
-    every completed launch leaves them consistent, so the buffer is reused.
+    The decode kernel's arrival counters must start at zero; every completed
+    launch leaves them at zero again, so the buffer is reused.  A grown
+    buffer replaces the old one only after the stream has finished with it
+    (torch's caching allocator orders the free after the stream's work).
     """
     import torch
     if p.workspace_bytes == 0:
         return None
-    key = str(device)
+    key = (str(device), int(stream or 0))
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < p.workspace_bytes:
         ws = torch.zeros(int(p.workspace_bytes), dtype=torch.uint8, device=device)
@@ -98,14 +102,17 @@ def dot(a, b, out=None, out_dtype=None, scale_a=None, scale_b=None, scale_mode=N
         c_tx = capi.I32 if (ta == capi.I8 and scale_mode == capi.SCALE_NONE) else (
             capi.BF16 if ta in (capi.BF16, capi.I8, capi.F8E4M3) else capi.F32)
     p = plan if plan is not None else plan_for(a, b, c_tx, scale_mode, block, flags)
+    if bool(p.desc.flags & capi.FLAG_ACCUMULATE) != (acc is not None):
+        raise ValueError("plan and call disagree on acc: the plan's FLAG_ACCUMULATE must be "
+                         "set exactly when acc is given")
     M, N = a.shape[0], b.shape[1]
     if out is None:
         out = torch.empty((M, N), dtype=_torch_dtype(c_tx), device=a.device)
     if out.stride(1) != 1 or out.stride(0) != p.desc.ldc:
         raise ValueError("output must be row-major with ldc == N")
-    ws = workspace if workspace is not None else workspace_for(p, a.device)
     if stream is None:
         stream = torch.cuda.current_stream(a.device).cuda_stream
+    ws = workspace if workspace is not None else workspace_for(p, a.device, stream)
     L = capi.load()
     capi.check(L.tx_dot_launch(ctypes.byref(p), a.data_ptr(), b.data_ptr(), out.data_ptr(),
                                None if scale_a is None else scale_a.data_ptr(),
@@ -211,13 +218,16 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
                               scale_mode=capi.SCALE_NV16 if nv else capi.SCALE_MX32,
                               block=block, lda=lda, ldb=ldb, flags=flags)
         plan = capi.plan(desc)
+    elif bool(plan.desc.flags & capi.FLAG_ACCUMULATE) != (acc is not None):
+        raise ValueError("plan and call disagree on acc: the plan's FLAG_ACCUMULATE must be "
+                         "set exactly when acc is given")
     if out is None:
         out = torch.empty((M, N), dtype=_torch_dtype(c_tx), device=lhs.device)
     if out.stride(1) != 1 or out.stride(0) != plan.desc.ldc:
         raise ValueError("output must be row-major with ldc == N")
     if stream is None:
         stream = torch.cuda.current_stream(lhs.device).cuda_stream
-    ws = _upcast_workspace(plan, lhs.device)
+    ws = _upcast_workspace(plan, lhs.device, stream)
     L = capi.load()
     capi.check(L.tx_dot_launch(ctypes.byref(plan), lhs.data_ptr(), rhs.data_ptr(),
                                out.data_ptr(),
@@ -231,14 +241,14 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
 _upcast_workspaces = {}
 
 
-def _upcast_workspace(p, device):
+def _upcast_workspace(p, device, stream):
     """Workspace of an MX x bf16 dot_scaled (the upcast operand), cached per
-    device apart from the decode kernel's (whose counters it would clobber).
-    Launches that overlap on one device race on it."""
+    (device, stream) apart from the decode kernel's (whose counters it would
+    clobber): launches on one stream run in order, so they share it."""
     import torch
     if p.workspace_bytes == 0:
         return None
-    key = str(device)
+    key = (str(device), int(stream or 0))
     ws = _upcast_workspaces.get(key)
     if ws is None or ws.numel() < p.workspace_bytes:
         ws = torch.empty(int(p.workspace_bytes), dtype=torch.uint8, device=device)
