@@ -195,6 +195,26 @@ TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A, const void *B,
                          void *C, const void *scale_a, const void *scale_b,
                          void *workspace, size_t workspace_bytes, void *stream);
 
+/* No counterpart in the reference: a variant of tx_dot_launch for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving
+ * loops and harnesses that forbid hipMalloc).  It takes no workspace: the
+ * scratch the planned kernels need (the W8A8 decode kernel's split-K arrival
+ * counters and int32 partials, the MX operand upcast to bf16) lives in one
+ * static device array of TX_NOALLOC_SCRATCH_BYTES per GPU, held from the
+ * library's load on that GPU until the process ends, and the call allocates
+ * nothing.  A plan whose workspace does not fit (decode: more than
+ * TX_NOALLOC_SCRATCH_BYTES; upcast: more than that less the 64 KiB counter
+ * region, which the upcast never touches) returns TX_ERR_WORKSPACE.  Every
+ * call on one GPU shares that GPU's array, which keeps the last call's
+ * contents: calls that may overlap in time on one GPU (different streams)
+ * race on it.  The counters are zero when the library loads and every
+ * completed launch leaves them at zero; nothing else needs initial
+ * contents. */
+#define TX_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+TX_API int tx_dot_launch_noalloc(const tx_dot_plan *plan, const void *A, const void *B,
+                                 void *C, const void *scale_a, const void *scale_b,
+                                 void *stream);
+
 /* Message for the calling thread's last non-zero status ("" if none). */
 TX_API const char *tx_get_last_error(void);
 /* Name of a tx_kernel value ("?" if unknown). */

@@ -436,3 +436,28 @@ def test_plan_and_acc_must_agree():
     mxp = tx.plan(tx.make_desc(64, 64, 64, tx.F8E4M3, tx.F32, scale_mode=tx.SCALE_MX32))
     with pytest.raises(ValueError, match="disagree on acc"):
         tx.dot_scaled(q, s, "e4m3", q, s, "e4m3", acc=acc, plan=mxp)
+
+
+def test_noalloc_rejects_oversized_workspace():
+    """tx_dot_launch_noalloc takes no workspace: a plan needing more than the static scratch
+    holds fails with TX_ERR_WORKSPACE before the device is touched."""
+    L = tx.load()
+    buf = ctypes.create_string_buffer(4096 + 16)
+    addr = (ctypes.addressof(buf) + 15) & ~15
+    # MX x bf16 at 8192^2: the upcast B is 128 MiB
+    p = tx.plan(tx.make_desc(256, 8192, 8192, tx.BF16, tx.F32, b_type=tx.F8E4M3,
+                             scale_mode=tx.SCALE_MX32))
+    assert p.workspace_bytes > capi.NOALLOC_SCRATCH_BYTES
+    rc = L.tx_dot_launch_noalloc(ctypes.byref(p), addr, addr, addr, None, addr, None)
+    assert rc == tx.ERR_WORKSPACE and b"no-allocation scratch" in L.tx_get_last_error()
+    # decode partials beyond the scratch: M = 64, N = 131072 (4 splits x 32 MiB)
+    p = tx.plan(tx.make_desc(64, 131072, 8192, tx.I8, tx.BF16, scale_mode=tx.SCALE_ROWCOL))
+    if p.workspace_bytes > capi.NOALLOC_SCRATCH_BYTES:
+        rc = L.tx_dot_launch_noalloc(ctypes.byref(p), addr, addr, addr, addr, addr, None)
+        assert rc == tx.ERR_WORKSPACE
+    # within the scratch: argument checks pass, then no device
+    import torch
+    if not torch.cuda.is_available():
+        p = tx.plan(tx.make_desc(16, 8192, 8192, tx.I8, tx.BF16, scale_mode=tx.SCALE_ROWCOL))
+        rc = L.tx_dot_launch_noalloc(ctypes.byref(p), addr, addr, addr, addr, addr, None)
+        assert rc == tx.ERR_NO_DEVICE

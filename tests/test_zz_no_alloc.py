@@ -1,0 +1,116 @@
+"""tx_dot_launch_noalloc: the launch entry point that allocates nothing.
+
+Its kernels are tx_dot_launch's; only the workspace differs (the library's
+static per-GPU scratch array instead of the caller's buffer).  So its output
+must equal tx_dot_launch's bit for bit on the same inputs, for the kernels
+that use scratch: the W8A8 decode kernel (split-K counters and partials) and
+the MX x bf16 upcast (the bf16 operand).  Two calls in a row, the second
+smaller, check that a call does not depend on what the previous one left in
+the shared array; the decode results are also checked against the oracle
+(int32 exact, so bit-exact bf16).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+import triton_ext_amd as tx
+from dotcase import from_device, say, to_device, uniform_i8, uniform_scales
+
+pytestmark = pytest.mark.gpu
+
+
+def _launch(fn_name, plan, a, b, c, sa, sb, ws=None):
+    import torch
+    L = tx.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    ptrs = (ctypes.byref(plan), a.data_ptr(), b.data_ptr(), c.data_ptr(),
+            None if sa is None else sa.data_ptr(), None if sb is None else sb.data_ptr())
+    if fn_name == "noalloc":
+        rc = L.tx_dot_launch_noalloc(*ptrs, stream)
+    else:
+        rc = L.tx_dot_launch(*ptrs, None if ws is None else ws.data_ptr(),
+                             0 if ws is None else ws.numel(), stream)
+    assert rc == tx.OK, L.tx_get_last_error().decode()
+
+
+def _w8a8(gpu, M, N, K, seed):
+    import torch
+    say(f"noalloc W8A8 M={M} N={N} K={K} seed={seed}")
+    a = uniform_i8((M, K), seed)
+    b = uniform_i8((K, N), seed + 1)
+    sa = uniform_scales(M, seed + 2)
+    sb = uniform_scales(N, seed + 3)
+    da, db, dsa, dsb = (to_device(x, gpu) for x in (a, b, sa, sb))
+    plan = tx.plan(tx.make_desc(M, N, K, tx.I8, tx.BF16, scale_mode=tx.SCALE_ROWCOL))
+    assert plan.kernel == tx.KERNEL_DECODE_I8
+    c_ref = torch.empty((M, N), dtype=torch.bfloat16, device=gpu)
+    c_new = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
+    ws = torch.zeros(max(int(plan.workspace_bytes), 1), dtype=torch.uint8, device=gpu)
+    _launch("plain", plan, da, db, c_ref, dsa, dsb, ws)
+    _launch("noalloc", plan, da, db, c_new, dsa, dsb)
+    torch.cuda.synchronize()
+    ref, got = from_device(c_ref), from_device(c_new)
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} elements differ"
+    orc = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 256, 128),
+                           scale_mode=oracle.SCALE_ROWCOL, sa=sa, sb=sb)
+    assert np.array_equal(got, orc)
+    return plan
+
+
+def test_noalloc_w8a8_two_calls(gpu):
+    """Split-K decode, then a smaller one (fewer strips, another split) on the same scratch."""
+    p1 = _w8a8(gpu, 16, 8192, 8192, 21)
+    p2 = _w8a8(gpu, 5, 2048, 4096, 22)
+    assert p1.split_k > 1 and p2.split_k > 1 and p2.workspace_bytes < p1.workspace_bytes
+    _w8a8(gpu, 16, 8192, 8192, 23)  # and back: the counters were left at zero
+
+
+def _mx_bf16(gpu, M, N, K, seed):
+    import torch
+    say(f"noalloc MX x bf16 M={M} N={N} K={K} seed={seed}")
+    g = torch.Generator(device=gpu)
+    g.manual_seed(seed)
+    a = torch.randn((M, K), generator=g, device=gpu).to(torch.bfloat16)
+    codes = torch.randint(0, 256, (K, N), generator=g, device=gpu, dtype=torch.int32)
+    codes = codes.to(torch.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0  # no e4m3 NaN codes
+    scales = torch.randint(120, 134, (N, K // 32), generator=g, device=gpu,
+                           dtype=torch.int32).to(torch.uint8)
+    plan = tx.plan(tx.make_desc(M, N, K, tx.BF16, tx.F32, b_type=tx.F8E4M3,
+                                scale_mode=tx.SCALE_MX32))
+    assert plan.kernel == tx.KERNEL_GEMM_MX_BF16 and plan.workspace_bytes > 0
+    c_ref = torch.empty((M, N), dtype=torch.float32, device=gpu)
+    c_new = torch.full((M, N), float("nan"), dtype=torch.float32, device=gpu)
+    ws = torch.empty(int(plan.workspace_bytes), dtype=torch.uint8, device=gpu)
+    _launch("plain", plan, a, codes, c_ref, None, scales, ws)
+    _launch("noalloc", plan, a, codes, c_new, None, scales)
+    torch.cuda.synchronize()
+    assert torch.equal(c_new.view(torch.int32), c_ref.view(torch.int32))
+
+
+def test_noalloc_mx_upcast_then_decode(gpu):
+    """The upcast writes after the counter region: a decode call after it still sees its
+    counters at zero."""
+    _mx_bf16(gpu, 512, 1024, 2048, 31)
+    _mx_bf16(gpu, 256, 256, 512, 32)
+    _w8a8(gpu, 16, 8192, 8192, 33)
+
+
+def test_noalloc_workspace_free_kernels(gpu):
+    """A plan without workspace (the bf16 tile) runs through the same entry point."""
+    import torch
+    say("noalloc bf16 300x264x200")
+    g = torch.Generator(device=gpu)
+    g.manual_seed(41)
+    a = torch.randn((300, 200), generator=g, device=gpu).to(torch.bfloat16)
+    b = torch.randn((200, 264), generator=g, device=gpu).to(torch.bfloat16)
+    plan = tx.plan(tx.make_desc(300, 264, 200, tx.BF16, tx.F32))
+    assert plan.workspace_bytes == 0
+    c_ref = torch.empty((300, 264), dtype=torch.float32, device=gpu)
+    c_new = torch.empty_like(c_ref)
+    _launch("plain", plan, a, b, c_ref, None, None)
+    _launch("noalloc", plan, a, b, c_new, None, None)
+    torch.cuda.synchronize()
+    assert torch.equal(c_new, c_ref)

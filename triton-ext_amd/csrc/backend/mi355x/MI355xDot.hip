@@ -721,12 +721,43 @@ int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
 
 } // namespace
 
-extern "C" TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A,
-                                    const void *B, void *C,
-                                    const void *scale_a, const void *scale_b,
-                                    void *workspace, size_t workspace_bytes,
-                                    void *stream) {
-  g_last_error.clear();
+// Scratch of tx_dot_launch_noalloc: one array per GPU (each device holds its
+// own copy of a __device__ variable), zero when the code object loads.  Host
+// code never uses the name as an address: the device address comes from
+// hipGetSymbolAddress, once per device.  Layout: the decode kernel's counter
+// region first (kDecodeCounterBytes), then its partials; an MX upcast writes
+// after the counter region only, so it never disturbs the counters.
+__device__ __attribute__((aligned(256))) uint8_t scratch[TX_NOALLOC_SCRATCH_BYTES];
+static_assert(kDecodeCounterBytes % 256 == 0, "upcast scratch stays 256-byte aligned");
+
+namespace {
+
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[64]; // device address of `scratch`, per device ordinal
+
+// Device address of this GPU's scratch array (the current device).
+int scratchOfCurrentDevice(uint8_t **out) {
+  int dev = -1;
+  TX_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64)
+    return fail(TX_ERR_NO_DEVICE, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    TX_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p)
+      return fail(TX_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = static_cast<uint8_t *>(g_scratch_ptr[dev]);
+  return TX_OK;
+}
+
+// Checks shared by both launch entry points, then the launch itself.
+// noalloc: the workspace is this GPU's scratch array (ws is ignored).
+int launchPlanned(const tx_dot_plan *plan, const void *A, const void *B, void *C,
+                  const void *scale_a, const void *scale_b, void *workspace,
+                  size_t workspace_bytes, void *stream, bool noalloc) {
   if (!plan)
     return fail(TX_ERR_INVALID, "plan is NULL");
   const tx_dot_desc &d = plan->desc;
@@ -746,8 +777,30 @@ extern "C" TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A,
   if (((need_sa ? reinterpret_cast<uintptr_t>(scale_a) : 0) |
        (need_sb ? reinterpret_cast<uintptr_t>(scale_b) : 0)) & 3)
     return fail(TX_ERR_INVALID, "scale arrays must be 4-byte aligned");
+  if (noalloc) {
+    // The upcast operand goes after the counter region, the decode
+    // workspace (counters first) at the start.
+    const int64_t room = plan->kernel == TX_KERNEL_GEMM_MX_BF16
+                             ? (int64_t)TX_NOALLOC_SCRATCH_BYTES - kDecodeCounterBytes
+                             : (int64_t)TX_NOALLOC_SCRATCH_BYTES;
+    if (plan->workspace_bytes < 0 || plan->workspace_bytes > room)
+      return fail(TX_ERR_WORKSPACE,
+                  "the plan needs %lld bytes of workspace; the no-allocation scratch "
+                  "holds %lld for this kernel",
+                  (long long)plan->workspace_bytes, (long long)room);
+  }
   if (!tx_device_available())
     return fail(TX_ERR_NO_DEVICE, "no gfx950 device visible");
+  if (noalloc && plan->workspace_bytes > 0) {
+    uint8_t *base = nullptr;
+    const int rc = scratchOfCurrentDevice(&base);
+    if (rc != TX_OK)
+      return rc;
+    const bool up = plan->kernel == TX_KERNEL_GEMM_MX_BF16;
+    workspace = up ? base + kDecodeCounterBytes : base;
+    workspace_bytes = up ? TX_NOALLOC_SCRATCH_BYTES - kDecodeCounterBytes
+                         : TX_NOALLOC_SCRATCH_BYTES;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (plan->kernel) {
   case TX_KERNEL_GEMM_16BIT:
@@ -763,6 +816,25 @@ extern "C" TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A,
   default:
     return fail(TX_ERR_INVALID, "plan has no kernel (kernel=%d)", plan->kernel);
   }
+}
+
+} // namespace
+
+extern "C" TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A,
+                                    const void *B, void *C,
+                                    const void *scale_a, const void *scale_b,
+                                    void *workspace, size_t workspace_bytes,
+                                    void *stream) {
+  g_last_error.clear();
+  return launchPlanned(plan, A, B, C, scale_a, scale_b, workspace, workspace_bytes, stream,
+                       false);
+}
+
+extern "C" TX_API int tx_dot_launch_noalloc(const tx_dot_plan *plan, const void *A,
+                                            const void *B, void *C, const void *scale_a,
+                                            const void *scale_b, void *stream) {
+  g_last_error.clear();
+  return launchPlanned(plan, A, B, C, scale_a, scale_b, nullptr, 0, stream, true);
 }
 
 // ---------------------------------------------------------------------------

@@ -15,6 +15,8 @@ SCALE_NONE, SCALE_ROWCOL, SCALE_BLOCK128, SCALE_MX32, SCALE_NV16 = 0, 1, 2, 3, 4
 BOUND_UNKNOWN, BOUND_MFMA, BOUND_HBM = 0, 1, 2
 # tx_status
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_NO_DEVICE, ERR_WORKSPACE, ERR_NO_PASS = range(7)
+# TX_NOALLOC_SCRATCH_BYTES: the static scratch of tx_dot_launch_noalloc, per GPU
+NOALLOC_SCRATCH_BYTES = 64 << 20
 # tx_kernel
 (KERNEL_NONE, KERNEL_GEMM_16BIT, KERNEL_GEMM_I8, KERNEL_DECODE_I8, KERNEL_GEMM_F8,
  KERNEL_GEMM_MX, KERNEL_GEMM_MX_BF16) = range(7)
@@ -91,8 +93,8 @@ EXPORTS = {
     "libloop_split.so": ["tx_loop_split_plan", "tx_loop_split_k"],
     "libarith_intensity.so": ["tx_dtype_size", "tx_dtype_bits", "tx_mi355x_peak_flops",
                               "tx_mi355x_peak_bw", "tx_arith_intensity", "tx_dot_operand_spans"],
-    "libmi355x_dot.so": ["tx_dot_plan_create", "tx_dot_launch", "tx_get_last_error",
-                         "tx_kernel_name", "tx_device_available"],
+    "libmi355x_dot.so": ["tx_dot_plan_create", "tx_dot_launch", "tx_dot_launch_noalloc",
+                         "tx_get_last_error", "tx_kernel_name", "tx_device_available"],
 }
 
 _libs = {}
@@ -145,6 +147,7 @@ def load(name="libmi355x_dot.so"):
     elif name == "libmi355x_dot.so":
         L.tx_dot_plan_create.argtypes = [ctypes.POINTER(DotDesc), ctypes.POINTER(DotPlan)]
         L.tx_dot_launch.argtypes = [ctypes.POINTER(DotPlan), vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
+        L.tx_dot_launch_noalloc.argtypes = [ctypes.POINTER(DotPlan), vp, vp, vp, vp, vp, vp]
         L.tx_get_last_error.restype = ctypes.c_char_p
         L.tx_kernel_name.argtypes = [i32]
         L.tx_kernel_name.restype = ctypes.c_char_p
