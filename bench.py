@@ -41,6 +41,8 @@ HBM = 8.0e12
 # dispatch, each scaled by the counter's reading for a 256 MiB copy (--copy-probe): FETCH x2.0,
 # WRITE x1.0 (profiles/gemm16_bf16_4096.md).
 TRAFFIC_BF16_4096 = 235.2e6
+# The same for the W8A8 M=16 decode kernel (profiles/decode_i8_w8a8_m16.md).
+TRAFFIC_W8A8_M16 = 72.3e6
 
 
 def parse():
@@ -50,7 +52,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
-                    help="secondary workloads to run, comma-separated: c1, vendor, tail, w8a8 (or "
+                    help="secondary workloads to run, comma-separated: ceiling, c1, vendor, tail, w8a8 (or "
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256), int8, fp8, kmajor, mx (or mxfp8, mxfp4, "
                          "mxfp8_4096, mxfp8_8192, mxfp4_4096, mxfp4_8192), mxbf16 (or mxbf16_fp4, mxbf16_fp8: "
                          "bf16 x MX), attn (or attn_1024, attn_4096, "
@@ -436,6 +438,61 @@ def bench_int8(tx, dev, M, N, K, steps, warmup, seed=4):
                 frac=ops / ms / 1e-3 / PEAK_I8)
 
 
+def ceilings_lib():
+    """bench.py's hardware-ceiling kernels (triton-ext_amd/csrc/bench/ceilings.hip)."""
+    L = ctypes.CDLL(os.path.join(ROOT, "triton-ext_amd", "lib", "libtx_ceilings.so"))
+    vp = ctypes.c_void_p
+    L.tx_ceiling_read.argtypes = [vp, ctypes.c_size_t, ctypes.c_int, vp, vp]
+    L.tx_ceiling_mfma_bf16.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp]
+    return L
+
+
+def bench_read_ceiling(dev, nbytes, steps, flush):
+    """A plain streaming read of nbytes, timed like the W8A8 lines: cold inside a
+    stream (after the 512 MiB read that evicts the MALL) and warm back to back.
+    Variants: 16-byte loads 8 or 4 per thread (contiguous 32 / 16 KiB blocks), and
+    direct-to-LDS loads through a per-wave ring as the decode kernel streams B."""
+    import torch
+    L = ceilings_lib()
+    buf = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    rows = []
+    for variant, name in ((0, "16-byte loads x8, 32 KiB blocks"), (1, "16-byte loads x4, 16 KiB blocks"),
+                          (2, "direct-to-LDS ring, 256 workgroups")):
+        def run(v=variant):
+            if L.tx_ceiling_read(buf.data_ptr(), nbytes, v, sink.data_ptr(), stream) != 0:
+                raise RuntimeError("tx_ceiling_read failed")
+        cold = time_cold_in_stream(run, flush)
+        warm = time_back_to_back(run, steps, 3)
+        rows.append(dict(variant=name, ms=cold, gbps=nbytes / cold / 1e6, ms_warm_mall=warm))
+    best = min(rows, key=lambda r: r["ms"])
+    return dict(workload=f"HBM read ceiling: plain read of {nbytes >> 20} MiB, cold, in stream",
+                ms=best["ms"], gbps=best["gbps"], frac_hbm=best["gbps"] * 1e9 / HBM,
+                variants=rows)
+
+
+def bench_mfma_ceiling(dev, steps, warmup, seed=1):
+    """The bf16 4096^3 tile schedule's MFMAs alone: 256 workgroups x 4 waves x 64 K
+    steps x 64 v_mfma_f32_32x32x16_bf16, operands bf16 N(0,1)/64 held in registers."""
+    import torch
+    L = ceilings_lib()
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    seed_t = (torch.randn((64 * 2048 * 8,), generator=g, device=dev) / 64).to(torch.bfloat16)
+    out = torch.empty(256 * 256, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def run():
+        if L.tx_ceiling_mfma_bf16(seed_t.data_ptr(), 256, 64, out.data_ptr(), stream) != 0:
+            raise RuntimeError("tx_ceiling_mfma_bf16 failed")
+    ms = time_back_to_back(run, steps, warmup)
+    flops = 256 * 4 * 64 * 64 * 32768.0
+    return dict(workload="MFMA ceiling: the bf16 4096^3 tile schedule's 2^22 "
+                         "v_mfma_f32_32x32x16_bf16 alone (operands in registers)",
+                ms=ms, tflops=flops / ms / 1e9, frac=flops / ms / 1e-3 / PEAK_BF16)
+
+
 def cpu_baseline(a, b, c, M, N, K, block):
     """Oracle on the host cores over the full bf16 workload; also checks the GPU output."""
     import numpy as np
@@ -515,11 +572,29 @@ def main():
             r, _ = bench_bf16(tx, dev, m, n, k, args.steps, args.warmup, seed=2)
             secondary.append(r)
             print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    ceil = {}
+    if want("ceiling"):
+        r = bench_mfma_ceiling(dev, args.steps, args.warmup)
+        secondary.append(r)
+        ceil["mfma_bf16_tflops"] = round(r["tflops"], 1)
+        print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s ({100 * r['frac']:.1f}% of spec)",
+              file=sys.stderr, flush=True)
+        for nb in (64 << 20, 1 << 30):
+            r = bench_read_ceiling(dev, nb, max(args.steps, 20), flush)
+            secondary.append(r)
+            ceil[f"hbm_read_{nb >> 20}MiB_gbps"] = round(r["gbps"], 1)
+            print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us, {r['gbps']:.0f} GB/s "
+                  f"({100 * r['frac_hbm']:.1f}% of 8 TB/s); "
+                  + ", ".join(f"{v['variant']}: {v['gbps']:.0f}" for v in r["variants"]),
+                  file=sys.stderr, flush=True)
     w8a8_ms = [m for m in (1, 16, 64, 256) if want("w8a8") or want(f"w8a8_{m}")]
+    w8a8_16 = None
     if w8a8_ms:
         for m in w8a8_ms:
             r = bench_w8a8(tx, dev, m, 8192, 8192, max(args.steps, 20), 3, flush)
             secondary.append(r)
+            if m == 16:
+                w8a8_16 = r
             print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
                   f"({100 * r['frac_hbm']:.1f}% HBM); isolated launch "
                   f"{r['ms_isolated'] * 1e3:.2f} us", file=sys.stderr, flush=True)
@@ -608,6 +683,13 @@ def main():
                      "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(head["frac"], 4),
                      "traffic": TRAFFIC_BF16_4096},
         "cpu_baseline": cpu if cpu is None else {k: v for k, v in cpu.items() if k != "seconds"},
+        # the metric's second half: W8A8 decode at M=16 (N=K=8192), a cold launch inside a
+        # stream, algorithmic bytes (B, A, scales and C once) over its time
+        "roofline_w8a8_m16": None if w8a8_16 is None else {
+            "bound": "hbm", "achieved": round(w8a8_16["gbps"], 1), "peak": HBM / 1e9,
+            "unit": "GB/s", "frac": round(w8a8_16["frac_hbm"], 4), "traffic": TRAFFIC_W8A8_M16,
+            "ms": round(w8a8_16["ms"], 5)},
+        "ceilings": ceil or None,
         "parity_vs_oracle": parity,
         "secondary": secondary,
     }

@@ -325,7 +325,7 @@ int64_t decodeCounterBytes(const tx_dot_desc &) { return kDecodeCounterBytes; }
 int64_t decodeWorkspace(const tx_dot_desc &d, int ksplit) {
   if (ksplit <= 1)
     return 0;
-  return decodeCounterBytes(d) + (int64_t)ksplit * d.M * d.N * 4;
+  return decodeCounterBytes(d) + (int64_t)ksplit * d.M * ((d.N + 3) & ~3) * 4;
 }
 
 // ---------------------------------------------------------------------------

@@ -72,7 +72,7 @@ struct DecodeArgs {
   int32_t slices;            // row slices of 16 * MT rows (M > 16 * MT)
   int32_t batches_per_split;
   int32_t k_main_batches;    // batches with every K row < K (unmasked)
-  int32_t *partials;         // [ksplit][M][N] int32
+  int32_t *partials;         // [ksplit][M][N rounded up to 4] int32
   uint32_t *counters;        // [slices][ceil(N / 128)] arrival counters
 };
 
@@ -115,8 +115,13 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // Workgroup -> (row slice, column strip, K split).  With several slices,
-  // the slices of one (strip, split) pair go to one XCD (workgroups are
+  // Workgroup -> (row slice, column strip, K split).  Consecutive pairs are
+  // adjacent strips of one split: the workgroups running at once then read
+  // whole stretches of B's rows rather than every strip's 128 bytes at a
+  // fixed offset of each KiB, which loads some HBM channels far more than
+  // others (measured: the strips at offsets 384..511 of each KiB ended
+  // 3 us after the rest when a strip's splits were adjacent instead).  With
+  // several slices, the slices of one pair go to one XCD (workgroups are
   // dealt to the 8 XCDs round-robin) so they read its B through one L2.
   const int strips = (p.N + kDecodeStripN - 1) / kDecodeStripN;
   const int pairs = strips * p.ksplit;
@@ -131,7 +136,7 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
       pair = blockIdx.x / p.slices;
     }
   }
-  const int strip = pair / p.ksplit, split = pair % p.ksplit;
+  const int strip = pair % strips, split = pair / strips;
   const int64_t n0 = (int64_t)strip * kDecodeStripN;
   // This slice's rows: row0 .. row0 + Mr - 1.
   const int row0 = slice * 16 * MT;
@@ -253,16 +258,23 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
       __builtin_amdgcn_s_waitcnt(((4 * V) & 0xf) | (((4 * V) >> 4) << 14) | (0x7 << 4) | (0xf << 8));
   };
 
-  // The epilogue's scales go out first and wait in registers, so the
-  // epilogue waits on no memory round trip for them.  Element e of this
-  // thread (below) is row 2 e + tid / 128, column tid % 128.
-  constexpr int PER = MT * 16 * kDecodeStripN / (kDecodeWaves * 64); // elements per thread
-  const float sbv = p.sb[n0 + tid % kDecodeStripN < p.N ? n0 + tid % kDecodeStripN : 0];
-  float sav[PER];
+  // After the K loop each thread owns a column quad of the strip, columns
+  // cq .. cq + 3 with cq = 4 (tid % 32), in the RPT = 2 MT rows tid / 32 + 8 j
+  // (j < RPT): four consecutive int32 per row, moved as one 16-byte LDS read
+  // and as two 8-byte global accesses.  The epilogue's scales go out first
+  // and wait in registers, so the epilogue waits on no memory round trip
+  // for them.
+  constexpr int RPT = 2 * MT;
+  static_assert(RPT * 4 * kDecodeWaves * 64 == MT * 16 * kDecodeStripN, "quads cover the tile");
+  const int cq = 4 * (tid & 31), rq = tid >> 5;
+  float sbv[4], sav[RPT];
 #pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    const int m = 2 * e + tid / kDecodeStripN;
-    sav[e] = p.sa[row0 + (m < Mr ? m : 0)];
+  for (int r = 0; r < 4; ++r)
+    sbv[r] = p.sb[n0 + cq + r < p.N ? n0 + cq + r : 0];
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    const int m = rq + 8 * j;
+    sav[j] = p.sa[row0 + (m < Mr ? m : 0)];
   }
 
   // Prologue: STAGES - 1 batches in flight.  Batch i uses slot and A
@@ -296,10 +308,11 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   __builtin_amdgcn_s_waitcnt(0); // every load of the loop has landed
   // Sum the 4 waves' accumulators through LDS (the ring is free now): wave
   // w stores its tile into stage w's array with plain stores, then every
-  // thread adds the 4 copies of its elements.  acc[t][j] register r of lane
-  // l: row m = 16 t + 4 (l / 16) + r, column n = 16 j + l % 16; element (m, n)
+  // thread adds the 4 copies of its quads.  acc[t][j] register r of lane l:
+  // row m = 16 t + 4 (l / 16) + r, column n = 16 j + l % 16; element (m, n)
   // sits at m * 128 + (n ^ (16 * ((m >> 2) & 3))), so the four 16-lane groups
-  // of one store hit different banks.
+  // of one store hit different banks, and the XOR (bits 4-5 of n) keeps each
+  // column quad contiguous.
   constexpr int TILE = MT * 16 * kDecodeStripN; // int32 of the strip's sums
   static_assert(TILE * 4 <= STAGE_BYTES, "reduction tile exceeds a stage");
   auto swz = [](int m, int n) { return m * kDecodeStripN + (n ^ (16 * ((m >> 2) & 3))); };
@@ -316,27 +329,42 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
           mine_tile[swz(16 * t + 4 * G + r, 16 * j + L)] = acc[t][j][r];
   }
   __syncthreads();
-  const int nthreads = kDecodeWaves * 64;
-  static_assert(kDecodeWaves * 64 == 2 * kDecodeStripN, "element e: row 2 e + tid / 128");
-  // Element e of this thread: i = tid + e * nthreads, (m, n) = (i / 128, i % 128).
-  int32_t wsum[PER];
+  i32x4_t wsum[RPT];
 #pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    const int i = tid + e * nthreads;
-    const int q = swz(i / kDecodeStripN, i % kDecodeStripN);
-    wsum[e] = reinterpret_cast<const int32_t *>(st0)[q] + reinterpret_cast<const int32_t *>(st1)[q] +
-              reinterpret_cast<const int32_t *>(st2)[q] + reinterpret_cast<const int32_t *>(st3)[q];
+  for (int j = 0; j < RPT; ++j) {
+    const int q = swz(rq + 8 * j, cq);
+    wsum[j] = *reinterpret_cast<const i32x4_t *>(reinterpret_cast<const int32_t *>(st0) + q) +
+              *reinterpret_cast<const i32x4_t *>(reinterpret_cast<const int32_t *>(st1) + q) +
+              *reinterpret_cast<const i32x4_t *>(reinterpret_cast<const int32_t *>(st2) + q) +
+              *reinterpret_cast<const i32x4_t *>(reinterpret_cast<const int32_t *>(st3) + q);
   }
-  // C = bf16((float(sum) * sa[m]) * sb[n]) for this thread's PER elements
-  // (element e: i = tid + e * nthreads), scales from LDS.
-  auto epilogue = [&](const int32_t (&sum)[PER]) {
+  // C = bf16((float(sum) * sa[m]) * sb[n]) for this thread's quads: one
+  // 8-byte store per row (ldc and n0 + cq are multiples of 4), single
+  // elements where the quad crosses N.
+  auto epilogue = [&](const i32x4_t (&sum)[RPT]) {
 #pragma unroll
-    for (int e = 0; e < PER; ++e) {
-      const int i = tid + e * nthreads;
-      const int m = i / kDecodeStripN, n = i % kDecodeStripN;
-      if (m < Mr && n0 + n < p.N)
-        p.C[(int64_t)(row0 + m) * p.ldc + n0 + n] =
-            f32_to_bf16_rne(((float)sum[e] * sav[e]) * sbv);
+    for (int j = 0; j < RPT; ++j) {
+      const int m = rq + 8 * j;
+      if (m >= Mr)
+        continue;
+      float f[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+#pragma clang fp contract(off)
+        f[r] = ((float)sum[j][r] * sav[j]) * sbv[r];
+      }
+      uint16_t *c = p.C + (int64_t)(row0 + m) * p.ldc + n0 + cq;
+      if (n0 + cq + 4 <= p.N) {
+        uint2 w;
+        w.x = pk_bf16_rne(f[0], f[1]);
+        w.y = pk_bf16_rne(f[2], f[3]);
+        *reinterpret_cast<uint2 *>(c) = w;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n0 + cq + r < p.N)
+            c[r] = f32_to_bf16_rne(f[r]);
+      }
     }
   };
   if (p.ksplit == 1) {
@@ -344,22 +372,31 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
     return;
   }
 
-  // Publish this split's partial, then count arrivals for the strip.
-  // Cross-workgroup data moves only through agent-scope atomics (relaxed):
-  // on gfx950 they are coherent across the XCDs' L2s by themselves (sc1), so
-  // no fence has to write back or invalidate a whole L2 (an agent-scope
+  // Publish this split's partial ([split][M][np] int32, np = N rounded up
+  // to 4 so that every quad is 8-byte aligned), then count arrivals for the
+  // strip.  Cross-workgroup data moves only through agent-scope relaxed
+  // atomics, which gfx950 issues with the SC1 cache policy: stores write
+  // through the XCD's L2 to the device-coherent level and loads read from it,
+  // so no fence has to write back or invalidate a whole L2 (an agent-scope
   // release/acquire fence pair costs ~40 us here).  Ordering: every thread's
-  // stores are acknowledged (s_waitcnt vmcnt(0)) before the barrier that
+  // stores are acknowledged (s_waitcnt vmcnt(0): a store with SC1 is
+  // acknowledged once it has reached that level) before the barrier that
   // precedes the counter increment, and the last workgroup issues its loads
   // only after its increment has returned.
-  int32_t *mine = p.partials + ((int64_t)split * p.M + row0) * p.N;
+  const int64_t np = (p.N + 3) & ~3;
+  uint64_t *const mine =
+      reinterpret_cast<uint64_t *>(p.partials + ((int64_t)split * p.M + row0) * np + n0 + cq);
+  const bool quad_in = n0 + cq < p.N;
 #pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    const int i = tid + e * nthreads;
-    const int m = i / kDecodeStripN, n = i % kDecodeStripN;
-    if (m < Mr && n0 + n < p.N)
-      __hip_atomic_store(&mine[(int64_t)m * p.N + n0 + n], wsum[e], __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+  for (int j = 0; j < RPT; ++j) {
+    const int m = rq + 8 * j;
+    if (m < Mr && quad_in) {
+      uint64_t *dst = mine + (int64_t)m * (np / 2);
+      __hip_atomic_store(dst, __builtin_bit_cast(uint64_t, v2i_t{wsum[j][0], wsum[j][1]}),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(dst + 1, __builtin_bit_cast(uint64_t, v2i_t{wsum[j][2], wsum[j][3]}),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -376,41 +413,44 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   if (!*reinterpret_cast<volatile uint32_t *>(st4))
     return;
   // Last arrival: add every split's partial (its own included, stored
-  // above) in split order, then apply the epilogue.  The loads are
-  // unconditional -- out-of-range elements read element 0 and are dropped
+  // above) and apply the epilogue.  The loads are unconditional -- rows past
+  // the slice and quads past N read the slice's first quad and are dropped
   // after -- so a batch of NQ splits is issued before any value is used and
   // the gather costs one memory round trip per batch.
-  int32_t sum[PER];
-  int64_t off[PER];
-  bool ok[PER];
+  i32x4_t sum[RPT];
+  int64_t off[RPT]; // in 8-byte units from split 0's partial
 #pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    const int i = tid + e * nthreads;
-    const int m = i / kDecodeStripN, n = i % kDecodeStripN;
-    ok[e] = m < Mr && n0 + n < p.N;
-    off[e] = ok[e] ? (int64_t)m * p.N + n0 + n : 0;
-    sum[e] = 0;
+  for (int j = 0; j < RPT; ++j) {
+    const int m = rq + 8 * j;
+    off[j] = (m < Mr && quad_in) ? ((int64_t)m * np + n0 + cq) / 2 : (n0 / 2);
+    sum[j] = i32x4_t{0, 0, 0, 0};
   }
+  const uint64_t *const part0 = reinterpret_cast<const uint64_t *>(p.partials + (int64_t)row0 * np);
+  const int64_t split_stride = (int64_t)p.M * np / 2; // 8-byte units per split
   auto gather = [&](auto nq) {
     constexpr int NQ = decltype(nq)::value;
     for (int q0 = 0; q0 < p.ksplit; q0 += NQ) {
-      int32_t v[NQ][PER];
-#pragma unroll
-      for (int qq = 0; qq < NQ; ++qq) {
-        const int32_t *src = p.partials + ((int64_t)(q0 + qq) * p.M + row0) * p.N;
-#pragma unroll
-        for (int e = 0; e < PER; ++e)
-          v[qq][e] = __hip_atomic_load(&src[off[e]], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      uint64_t v[NQ][RPT][2];
 #pragma unroll
       for (int qq = 0; qq < NQ; ++qq)
 #pragma unroll
-        for (int e = 0; e < PER; ++e)
-          sum[e] += ok[e] ? v[qq][e] : 0;
+        for (int j = 0; j < RPT; ++j) {
+          const uint64_t *src = part0 + (int64_t)(q0 + qq) * split_stride + off[j];
+          v[qq][j][0] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          v[qq][j][1] = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+      for (int qq = 0; qq < NQ; ++qq)
+#pragma unroll
+        for (int j = 0; j < RPT; ++j) {
+          const v2i_t lo = __builtin_bit_cast(v2i_t, v[qq][j][0]);
+          const v2i_t hi = __builtin_bit_cast(v2i_t, v[qq][j][1]);
+          sum[j] += i32x4_t{lo.x, lo.y, hi.x, hi.y};
+        }
     }
   };
-  // Batches of up to 32 loads per thread (ksplit is a power of two >= 2).
-  constexpr int NQ = 32 / PER >= 4 ? 4 : (32 / PER >= 2 ? 2 : 1);
+  // Batches of up to 16 8-byte loads per thread (ksplit is a power of two >= 2).
+  constexpr int NQ = 8 / RPT >= 4 ? 4 : (8 / RPT >= 2 ? 2 : 1);
   if (NQ >= 4 && p.ksplit >= 4)
     gather(std::integral_constant<int, NQ>());
   else if (NQ >= 2)

@@ -1,0 +1,151 @@
+// Measured hardware ceilings for bench.py: libtx_ceilings.so.
+//
+// Not part of the dot path and not a drop-in entry point: two kernels that
+// time what one MI355X delivers at the two rooflines the dot is priced
+// against, so that the headline fractions can be read beside a ceiling the
+// same box measured.
+//   * tx_ceiling_read: a plain streaming read of a buffer (every byte once,
+//     16-byte non-temporal loads, each workgroup one contiguous block), the
+//     best case for an HBM-bound kernel such as the W8A8 decode, which reads
+//     its B operand once.
+//   * tx_ceiling_mfma_bf16: the bf16 256x256 tile kernel's MFMA work alone
+//     (the same grid, waves and v_mfma_f32_32x32x16_bf16 count per wave, on
+//     operands held in registers, no LDS and no memory traffic in the loop),
+//     the ceiling the power-limited clock leaves for the dot's MFMA stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "tx_ceilings.h"
+
+namespace {
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Read: workgroup b reads bytes [b * 4096 U, (b + 1) * 4096 U): U 16-byte
+// loads per thread, all issued before any is used.
+template <int U> __global__ void __launch_bounds__(256) read_kernel(const u32x4_t *buf, uint32_t *sink) {
+  const u32x4_t *p = buf + (size_t)blockIdx.x * 256 * U + threadIdx.x;
+  u32x4_t v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    v[u] = __builtin_nontemporal_load(p + u * 256);
+  u32x4_t x = v[0];
+#pragma unroll
+  for (int u = 1; u < U; ++u)
+    x ^= v[u];
+  // keeps the loads; no thread stores unless the xor hits this value
+  if ((x.x ^ x.y ^ x.z ^ x.w) == 0x9e3779b9u)
+    *sink = x.x;
+}
+
+// Read through LDS the way the decode kernel streams B: one wave per
+// workgroup quarter, direct-to-LDS non-temporal 16-byte loads into a ring of
+// S slots of 8 KiB, waiting only for the oldest slot.
+template <int S> __global__ void __launch_bounds__(256) read_lds_kernel(const uint8_t *buf,
+                                                                      int64_t per_wave,
+                                                                      uint32_t *sink) {
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[4][S][8192];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint8_t *p = buf + ((int64_t)blockIdx.x * 4 + wave) * per_wave;
+  const int batches = (int)(per_wave / 8192);
+  for (int b = 0; b < batches; ++b) {
+    uint8_t *slot = ring[wave][b % S];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      __builtin_amdgcn_global_load_lds(p + (int64_t)b * 8192 + i * 1024 + lane * 16,
+                                       (lds_void *)(slot + i * 1024), 16, 0, 2);
+    if (b >= S - 1) // at most S - 1 batches of 8 loads in flight beyond this one
+      __builtin_amdgcn_s_waitcnt((8 * (S - 1)) & 0xf | (((8 * (S - 1)) >> 4) << 14) |
+                                 (0x7 << 4) | (0xf << 8));
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  if (ring[wave][0][lane] == 0xA5 && ring[wave][S - 1][lane] == 0x5A)
+    *sink = lane;
+}
+
+// MFMA ceiling: 4 waves per workgroup, 16 accumulators of 32x32 per wave
+// (128x128), 4 sub-steps of 16 MFMAs per K step, operands from `seed`
+// (different per sub-step and wave) kept in registers.
+__global__ void __launch_bounds__(256, 1) mfma_bf16_kernel(const u32x4_t *seed, int ksteps,
+                                                           float *out) {
+  const int lane = threadIdx.x & 63;
+  const u32x4_t *s = seed + ((blockIdx.x * 4 + (threadIdx.x >> 6)) % 64) * 64 * 32 + lane;
+  u32x4_t a[4][4], b[4][4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[ks][i] = s[(ks * 8 + i) * 64];
+      b[ks][i] = s[(ks * 8 + 4 + i) * 64];
+    }
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        acc[i][j][r] = 0.f;
+  for (int kt = 0; kt < ksteps; ++kt) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8_t, b[ks][j]), __builtin_bit_cast(bf16x8_t, a[ks][i]),
+              acc[i][j], 0, 0, 0);
+  }
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        t += acc[i][j][r];
+  out[(size_t)blockIdx.x * 256 + threadIdx.x] = t;
+}
+
+} // namespace
+
+extern "C" int tx_ceiling_read(const void *buf, size_t bytes, int variant, void *sink,
+                               void *stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!buf || !sink || (reinterpret_cast<uintptr_t>(buf) & 15))
+    return 1;
+  if (variant == 0) { // 8 loads per thread: 32 KiB per workgroup
+    if (bytes % (4096 * 8))
+      return 1;
+    hipLaunchKernelGGL(read_kernel<8>, dim3((unsigned)(bytes / (4096 * 8))), dim3(256), 0, s,
+                       static_cast<const u32x4_t *>(buf), static_cast<uint32_t *>(sink));
+  } else if (variant == 1) { // 4 loads per thread: 16 KiB per workgroup
+    if (bytes % (4096 * 4))
+      return 1;
+    hipLaunchKernelGGL(read_kernel<4>, dim3((unsigned)(bytes / (4096 * 4))), dim3(256), 0, s,
+                       static_cast<const u32x4_t *>(buf), static_cast<uint32_t *>(sink));
+  } else if (variant == 2) { // direct-to-LDS ring, 256 workgroups of 4 waves
+    const int64_t per_wave = (int64_t)bytes / 1024;
+    if (per_wave % 8192 || per_wave <= 0)
+      return 1;
+    hipLaunchKernelGGL(read_lds_kernel<4>, dim3(256), dim3(256), 0, s,
+                       static_cast<const uint8_t *>(buf), per_wave, static_cast<uint32_t *>(sink));
+  } else {
+    return 1;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+extern "C" int tx_ceiling_mfma_bf16(const void *seed, int tiles, int ksteps, float *out,
+                                    void *stream) {
+  if (!seed || !out || tiles <= 0 || ksteps < 0 || (reinterpret_cast<uintptr_t>(seed) & 15))
+    return 1;
+  hipLaunchKernelGGL(mfma_bf16_kernel, dim3(tiles), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u32x4_t *>(seed), ksteps, out);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
