@@ -156,7 +156,13 @@ def test_plan_validation():
     assert _err(tx.make_desc(64, 64, 64, 42, tx.BF16)) == tx.ERR_INVALID
     assert _err(tx.make_desc(64, 64, 60, tx.BF16, tx.BF16, lda=60)) == tx.ERR_INVALID  # 120 B rows
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, lda=32)) == tx.ERR_INVALID  # short stride
-    assert _err(tx.make_desc(64, 64, 68, tx.BF16, tx.BF16, lda=72)) == tx.ERR_UNSUPPORTED  # K%8
+    # K and N need not fill 16-byte chunks (masked per element); row strides must
+    p = tx.plan(tx.make_desc(64, 61, 68, tx.BF16, tx.BF16, lda=72, ldb=64, ldc=64))
+    assert p.kernel == tx.KERNEL_GEMM_16BIT and p.k_tail == 68 % p.desc.block_k
+    assert _err(tx.make_desc(64, 61, 68, tx.BF16, tx.BF16, lda=72)) == tx.ERR_INVALID  # ldb 61
+    # the upcast of an MX B operand takes columns in blocks of 16
+    assert _err(tx.make_desc(64, 72, 64, tx.BF16, tx.F32, b_type=tx.F8E4M3, ldb=80,
+                             scale_mode=tx.SCALE_MX32)) == tx.ERR_UNSUPPORTED
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.I32)) == tx.ERR_UNSUPPORTED
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, b_type=tx.F16)) == tx.ERR_UNSUPPORTED
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, block=(96, 64, 64))) == tx.ERR_UNSUPPORTED

@@ -148,15 +148,20 @@ def test_strided_a(gpu):
     check_close(got, ref, atol=ATOL, rtol=RTOL, what="strided A")
 
 
-def test_rejects_unaligned_k(gpu):
-    """K*elt must be a multiple of 16 bytes: rejected before any launch."""
+def test_unaligned_row_stride(gpu):
+    """A row stride that is not a multiple of 16 bytes is rejected at plan time (the
+    kernels read 16-byte chunks); dot() copies such an operand into padded rows
+    itself, and the result stays bit-exact (int8 -> int32, K = 200)."""
     import torch
-    say("unaligned K rejected")
-    a = torch.zeros((5, 200), dtype=torch.int8, device=gpu)
-    b = torch.zeros((200, 272), dtype=torch.int8, device=gpu)
+    say("unaligned row stride")
     with pytest.raises(tx.TxError) as e:
-        tx.dot(a, b, out_dtype=torch.int32)
+        tx.plan(tx.make_desc(5, 272, 200, tx.I8, tx.I32, lda=200))
     assert e.value.code == tx.ERR_INVALID
+    a = uniform_i8((5, 200), 121)
+    b = uniform_i8((200, 272), 122)
+    c = tx.dot(to_device(a, gpu), to_device(b, gpu), out_dtype=torch.int32)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_device(c), a.astype(np.int64) @ b.astype(np.int64))
 
 
 def test_k_zero_and_empty(gpu):

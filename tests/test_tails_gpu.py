@@ -1,0 +1,265 @@
+"""GPU parity for K and N that do not fill whole 16-byte chunks.
+
+Triton's masked tl.load (T:runtime/interpreter.py:449-455) zero-fills every
+element past K and drops every column past N, whatever K and N are; the
+reference kernel's K loop has the same shape (R:pass/LoopSplit/LoopSplit.cpp
+:156-174 peels the masked step).  Here every operand lives in padded storage
+whose padding holds NaN (floating point) or random bytes (int8), with extra
+rows past M (A) and past K (B) holding the same: an element past an edge
+that reached the MFMA would turn a result into NaN or change an integer sum.
+
+Bars: int8 and W8A8 bit-exact; fp16/bf16/fp8 within the north_star tolerance
+(|d| <= 1e-3 s + 1e-2 |ref|, s as in test_dot_gpu.py).
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+import triton_ext_amd as tx
+from dotcase import (bits_to_f32, check_close, fp8_block_inputs, from_device, k_norm, normal_bf16,
+                     normal_f16, say, to_device, uniform_i8, uniform_scales)
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-3, 1e-2
+NAN16 = {"bf16": 0x7FC0, "f16": 0x7E00}
+
+
+def padded(x, fill, extra_rows=3, quantum=16):
+    """x [R, C] (numpy) inside storage [R + extra_rows, C'], the rest `fill`.
+    C' is C rounded up to whole 16-byte chunks, plus one chunk when C fills
+    its last chunk exactly, so every row has padding.  Returns (storage, C')."""
+    elt = x.dtype.itemsize
+    per = quantum // elt
+    ld = -(-x.shape[1] // per) * per
+    if ld == x.shape[1]:
+        ld += per  # padding on every row, also when C is chunk-aligned
+    st = np.full((x.shape[0] + extra_rows, ld), fill, dtype=x.dtype)
+    st[:x.shape[0], :x.shape[1]] = x
+    return st, ld
+
+
+def dev_view(st, shape, gpu, tdtype=None):
+    t = to_device(st, gpu)
+    if tdtype is not None:
+        t = t.view(tdtype)
+    return t[:shape[0], :shape[1]]
+
+
+def run16(gpu, M, N, K, kind, out_kind, block=(0, 0, 0), kmajor=False, seed=0):
+    import torch
+    say(f"tails {kind}->{out_kind} M={M} N={N} K={K} block={block} kmajor={kmajor}")
+    gen = normal_bf16 if kind == "bf16" else normal_f16
+    a = gen((M, K), k_norm(K), 51 + seed)
+    b = gen((K, N), k_norm(K), 52 + seed)
+    tdt = torch.bfloat16 if kind == "bf16" else torch.float16
+    sa, _ = padded(a, NAN16[kind])
+    da = dev_view(sa, (M, K), gpu, tdt)
+    if kmajor:  # B stored [N][K]: its rows past N and columns past K hold NaN
+        sbt, _ = padded(np.ascontiguousarray(b.T), NAN16[kind])
+        db = dev_view(sbt, (N, K), gpu, tdt).t()
+    else:
+        sb, _ = padded(b, NAN16[kind])
+        db = dev_view(sb, (K, N), gpu, tdt)
+    out_dt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[out_kind]
+    c = tx.dot(da, db, out_dtype=out_dt, block=block)
+    torch.cuda.synchronize()
+    p = tx.plan_for(da, db, tx.tx_type(c), block=block, ldc=c.stride(0))
+    blk = (p.desc.block_m, p.desc.block_n, p.desc.block_k)
+    at = oracle.BF16 if kind == "bf16" else oracle.F16
+    ct = {"f32": oracle.F32, "bf16": oracle.BF16, "f16": oracle.F16}[out_kind]
+    ref = oracle.tiled_dot(a, b, a_type=at, c_type=ct, block=blk)
+    got = from_device(c)
+    okind = "f32" if out_kind == "f32" else out_kind
+    err = check_close(bits_to_f32(got, okind), bits_to_f32(ref, okind), atol=ATOL, rtol=RTOL,
+                      what=f"{kind} {M}x{N}x{K}")
+    say(f"max|d|={err:.3g} tile={blk}")
+    return p
+
+
+@pytest.mark.parametrize("M,N,K", [(4001, 4001, 4001), (4096, 4096, 4001)])
+def test_bf16_ragged_headline_shapes(gpu, M, N, K):
+    """bf16 4001^3 and 4096 x 4096 x 4001 on the 256x256 tile: K tail of 33 (4001 = 62 * 64
+    + 33) with a chunk crossing K, and (4001^3) edge tiles whose last chunk crosses N."""
+    p = run16(gpu, M, N, K, "bf16", "bf16")
+    assert (p.desc.block_m, p.desc.block_n) == (256, 256) and p.k_tail == K % 64
+
+
+@pytest.mark.parametrize("M,N,K,kind,out,block", [
+    (300, 261, 203, "bf16", "f32", (0, 0, 0)),
+    (257, 259, 131, "f16", "f16", (0, 0, 0)),
+    (33, 17, 9, "bf16", "bf16", (0, 0, 0)),
+    (300, 261, 203, "bf16", "f32", (128, 128, 64)),
+    (129, 67, 45, "f16", "f32", (64, 64, 32)),
+    (70, 35, 1, "f16", "f16", (64, 64, 32)),
+])
+def test_16bit_ragged(gpu, M, N, K, kind, out, block):
+    run16(gpu, M, N, K, kind, out, block)
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 261, 203), (64, 50, 70)])
+def test_16bit_ragged_kmajor_b(gpu, M, N, K):
+    """K-major B (q @ k.T): B's chunk that crosses K is zeroed in registers too."""
+    run16(gpu, M, N, K, "bf16", "f32", kmajor=True)
+
+
+@pytest.mark.parametrize("M,N,K,block", [(300, 261, 203, (256, 256, 128)),
+                                         (300, 261, 203, (128, 128, 128)),
+                                         (17, 1001, 999, (0, 0, 0))])
+def test_int8_ragged(gpu, M, N, K, block):
+    """int8 -> int32, bit-exact; the padding holds random bytes."""
+    import torch
+    say(f"tails int8 M={M} N={N} K={K} block={block}")
+    a = uniform_i8((M, K), 61)
+    b = uniform_i8((K, N), 62)
+    junk = np.random.default_rng(63)
+    sa, _ = padded(a, 0)
+    sa[:, K:] = junk.integers(-128, 128, size=sa[:, K:].shape)
+    sa[M:, :] = junk.integers(-128, 128, size=sa[M:, :].shape)
+    sb, _ = padded(b, 0)
+    sb[:, N:] = junk.integers(-128, 128, size=sb[:, N:].shape)
+    sb[K:, :] = junk.integers(-128, 128, size=sb[K:, :].shape)
+    c = tx.dot(dev_view(sa, (M, K), gpu), dev_view(sb, (K, N), gpu), out_dtype=torch.int32,
+               block=block)
+    torch.cuda.synchronize()
+    ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.I32, block=(64, 64, 64))
+    assert np.array_equal(from_device(c), ref)
+
+
+def _fp8_codes(shape, seed):
+    c = np.random.default_rng(seed).integers(0, 256, size=shape).astype(np.uint8)
+    return np.where((c & 0x7F) == 0x7F, c & 0xF0, c).astype(np.uint8)  # no NaN codes
+
+
+@pytest.mark.parametrize("M,N,K,block", [(300, 263, 391, (256, 256, 128)),
+                                         (300, 263, 391, (256, 224, 128)),
+                                         (300, 263, 391, (128, 128, 128))])
+def test_fp8_ragged_unscaled(gpu, M, N, K, block):
+    """e4m3 -> fp32 with NaN codes (0x7F) in A's and B's padding: A's bytes past K must be
+    zeroed before the MFMA (NaN times B's zero rows is still NaN)."""
+    import torch
+    say(f"tails fp8 M={M} N={N} K={K} block={block}")
+    a, b = _fp8_codes((M, K), 71), _fp8_codes((K, N), 72)
+    sa, _ = padded(a, 0x7F)
+    sb, _ = padded(b, 0x7F)
+    c = tx.dot(dev_view(sa, (M, K), gpu, torch.float8_e4m3fn),
+               dev_view(sb, (K, N), gpu, torch.float8_e4m3fn), out_dtype=torch.float32,
+               block=block)
+    torch.cuda.synchronize()
+    ref = oracle.tiled_dot(a, b, a_type=oracle.F8E4M3, c_type=oracle.F32, block=(128, 128, 128))
+    fa, fb = oracle.e4m3_to_f32(a).astype(np.float64), oracle.e4m3_to_f32(b).astype(np.float64)
+    s = math.sqrt(K) * math.sqrt((fa ** 2).mean()) * math.sqrt((fb ** 2).mean())
+    check_close(from_device(c), ref, atol=ATOL, rtol=RTOL, scale=s, what="fp8 ragged")
+
+
+@pytest.mark.parametrize("M,N,K,block", [(2048, 7167, 7168, (0, 0, 0)),
+                                         (300, 263, 391, (256, 256, 128)),
+                                         (300, 263, 391, (256, 224, 128)),
+                                         (300, 263, 391, (128, 128, 128))])
+def test_fp8_block_scaled_ragged(gpu, M, N, K, block):
+    """Config 4's dot with N = 7167 (a last chunk crossing N, a partial 128-column scale
+    block), and smaller ragged shapes on each 8-bit tile."""
+    import torch
+    say(f"tails fp8 block-scaled M={M} N={N} K={K} block={block}")
+    qa, qb, sa, sb = fp8_block_inputs(M, N, K, 73)
+    pa, _ = padded(qa, 0x7F)
+    pb, _ = padded(qb, 0x7F)
+    c = tx.dot(dev_view(pa, (M, K), gpu, torch.float8_e4m3fn),
+               dev_view(pb, (K, N), gpu, torch.float8_e4m3fn),
+               scale_a=to_device(sa, gpu), scale_b=to_device(sb, gpu), out_dtype=torch.bfloat16,
+               block=block)
+    torch.cuda.synchronize()
+    ref = oracle.tiled_dot(qa, qb, a_type=oracle.F8E4M3, c_type=oracle.BF16, block=(128, 128, 128),
+                           scale_mode=oracle.SCALE_BLOCK128, sa=sa, sb=sb)
+    check_close(bits_to_f32(from_device(c), "bf16"), bits_to_f32(ref, "bf16"), atol=ATOL,
+                rtol=RTOL, scale=math.sqrt(K), what="fp8 block ragged")
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 8192, 8191), (16, 8191, 8192), (5, 1001, 999),
+                                   (100, 3001, 2049), (1, 17, 15)])
+def test_w8a8_ragged(gpu, M, N, K):
+    """W8A8 decode with K or N not a multiple of 16 (config 3's N = K = 8192 less one):
+    bit-exact."""
+    import torch
+    say(f"tails W8A8 M={M} N={N} K={K}")
+    a = uniform_i8((M, K), 81)
+    b = uniform_i8((K, N), 82)
+    sa_, sb_ = uniform_scales(M, 83), uniform_scales(N, 84)
+    junk = np.random.default_rng(85)
+    pa, _ = padded(a, 0)
+    pa[:, K:] = junk.integers(-128, 128, size=pa[:, K:].shape)
+    pb, _ = padded(b, 0)
+    pb[:, N:] = junk.integers(-128, 128, size=pb[:, N:].shape)
+    pb[K:, :] = junk.integers(-128, 128, size=pb[K:, :].shape)
+    da, db = dev_view(pa, (M, K), gpu), dev_view(pb, (K, N), gpu)
+    c = tx.new_output(M, N, torch.bfloat16, gpu)
+    p = tx.plan(tx.make_desc(M, N, K, tx.I8, tx.BF16, scale_mode=tx.SCALE_ROWCOL,
+                             lda=da.stride(0), ldb=db.stride(0), ldc=c.stride(0)))
+    assert p.kernel == tx.KERNEL_DECODE_I8
+    tx.dot(da, db, scale_a=to_device(sa_, gpu), scale_b=to_device(sb_, gpu), out=c)
+    torch.cuda.synchronize()
+    ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 256, 128),
+                           scale_mode=oracle.SCALE_ROWCOL, sa=sa_, sb=sb_)
+    got = from_device(c)
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches"
+
+
+def test_mx_ragged_n(gpu):
+    """tl.dot_scaled (e8m0 per 32) with N not a multiple of 16: the last B chunk crosses N."""
+    import torch
+    M, N, K = 200, 250, 256
+    say(f"tails mx M={M} N={N} K={K}")
+    a, b = _fp8_codes((M, K), 91), _fp8_codes((K, N), 92)
+    rng = np.random.default_rng(93)
+    sa = rng.integers(120, 134, size=(M, K // 32)).astype(np.uint8)
+    sbs = rng.integers(120, 134, size=(N, K // 32)).astype(np.uint8)
+    pb, _ = padded(b, 0x7F)
+    c = tx.dot_scaled(to_device(a, gpu), to_device(sa, gpu), "e4m3",
+                      dev_view(pb, (K, N), gpu), to_device(sbs, gpu), "e4m3")
+    torch.cuda.synchronize()
+    ref = oracle.dot_scaled(a, sa, oracle.F8E4M3, b, sbs, oracle.F8E4M3, K=K)
+    fa = oracle.e4m3_to_f32(a).astype(np.float64) * np.exp2(np.repeat(sa, 32, 1).astype(np.float64) - 127)
+    fb = oracle.e4m3_to_f32(b).astype(np.float64) * np.exp2(np.repeat(sbs, 32, 1).T.astype(np.float64) - 127)
+    s = math.sqrt(K) * math.sqrt((fa ** 2).mean()) * math.sqrt((fb ** 2).mean())
+    check_close(from_device(c), ref, atol=ATOL, rtol=RTOL, scale=s, what="mx ragged N")
+
+
+def test_accumulate_ragged_n(gpu):
+    """acc + A @ B with N = 261: the quads that cross N are added element by element."""
+    import torch
+    M, N, K = 300, 261, 203
+    say(f"tails accumulate M={M} N={N} K={K}")
+    a = normal_bf16((M, K), k_norm(K), 101)
+    b = normal_bf16((K, N), k_norm(K), 102)
+    acc = np.random.default_rng(103).standard_normal((M, N)).astype(np.float32)
+    da = to_device(a, gpu).view(torch.bfloat16)
+    db = to_device(b, gpu).view(torch.bfloat16)
+    plain = tx.dot(da, db, out_dtype=torch.float32)
+    got = tx.dot(da, db, acc=to_device(acc, gpu))
+    torch.cuda.synchronize()
+    # the result is exactly the plain result plus acc in one fp32 addition
+    want = (from_device(plain).astype(np.float32) + acc).astype(np.float32)
+    assert np.array_equal(from_device(got), want)
+
+
+def test_contiguous_unaligned_operands(gpu):
+    """dot() on contiguous [M, K] / [K, N] tensors with rows 8002 bytes apart: the binding
+    copies them into 16-byte-aligned rows; the result matches the oracle."""
+    import torch
+    M = N = K = 1001
+    say(f"tails contiguous unaligned {M}x{N}x{K}")
+    a = normal_bf16((M, K), k_norm(K), 111)
+    b = normal_bf16((K, N), k_norm(K), 112)
+    da = to_device(a, gpu).view(torch.bfloat16)
+    db = to_device(b, gpu).view(torch.bfloat16)
+    assert da.stride(0) * 2 % 16 != 0
+    c = tx.dot(da, db, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert c.shape == (M, N) and (c.stride(0) * 2) % 16 == 0
+    p = tx.plan(tx.make_desc(M, N, K, tx.BF16, tx.BF16, lda=1008, ldb=1008, ldc=1008))
+    ref = oracle.tiled_dot(a, b, a_type=oracle.BF16, c_type=oracle.BF16,
+                           block=(p.desc.block_m, p.desc.block_n, p.desc.block_k))
+    check_close(bits_to_f32(from_device(c), "bf16"), bits_to_f32(ref, "bf16"), atol=ATOL,
+                rtol=RTOL, what="contiguous unaligned")

@@ -448,10 +448,13 @@ int validate(const tx_dot_desc *in, tx_dot_desc *d) {
   const int64_t ldb_b = bb == 4 ? d->ldb : d->ldb * bb / 8;
   if ((d->lda * ba) % 128 || ldb_b % 16 || (d->ldc * bc / 8) % 16)
     return fail(TX_ERR_INVALID, "A/B/C row strides must be multiples of 16 bytes");
-  if ((d->K * ba) % 128 || (bb == 4 ? d->N : d->N * bb / 8) % 16)
-    return fail(TX_ERR_UNSUPPORTED,
-                "K and N must be multiples of %d elements (16-byte chunks)",
-                ba == 4 ? 32 : 128 / ba);
+  // K and N may be any size (tl.load's mask covers every element): the
+  // kernels load the 16-byte chunk that crosses K or N whole and zero or drop
+  // its elements past the edge.  The upcast kernels of the bf16-side
+  // dot_scaled forms take B in blocks of 16 columns.
+  if (mxUpcastSide(*d) & 2 && d->N % 16)
+    return fail(TX_ERR_UNSUPPORTED, "an upcast B operand needs N %% 16 == 0 (got N=%lld)",
+                (long long)d->N);
   if (d->scale_mode == TX_SCALE_MX32) {
     if (d->K % 32)
       return fail(TX_ERR_UNSUPPORTED, "MX scales need K %% 32 == 0 (one e8m0 per 32)");

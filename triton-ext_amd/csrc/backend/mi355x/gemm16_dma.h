@@ -14,7 +14,10 @@
 //     which touch 4 consecutive rows, land on distinct banks.
 // Lanes whose chunk lies outside the matrix (K tail, M/N edges) fetch from a
 // zero-filled device buffer instead, which is the tl.load(mask, other=0) of the
-// reference kernel.
+// reference kernel.  A chunk that crosses K or N (K and N need not fill whole
+// 16-byte chunks) is loaded whole: A's elements past K are zeroed in registers
+// in the last step, and B's columns past N only reach outputs that are not
+// stored.
 //
 // MFMA operands (v_mfma_f32_32x32x16_{bf16,f16}; lane l holds row/column
 // l % 32 and K elements 8 (l / 32) .. +7):
@@ -146,8 +149,13 @@ struct Gemm16Dma {
     }
   }
 
+  // MFMA sub-steps [0, nks) of one staged K step.  krem: K minus the step's
+  // first K index; elements at or past it (the last step only: a 16-byte
+  // chunk that crosses K is loaded whole) are zeroed in A's fragments, whose
+  // lane l holds K values 8 c .. 8 c + 7 of the step, c = 2 ks + l / 32.
+  // B's rows past K come from the zero chunk.
   __device__ __forceinline__ static void
-  compute(const uint8_t *as, const uint8_t *bs, int nks, Acc (&acc)[FM][FN]) {
+  compute(const uint8_t *as, const uint8_t *bs, int nks, Acc (&acc)[FM][FN], int64_t krem = BK) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WN, wn = wave % WN;
@@ -171,6 +179,16 @@ struct Gemm16Dma {
           const int k4 = k + 4;
           const uint32_t off1 = k4 * RBB + (((n >> 3) ^ (4 * (k4 & 3))) << 4) + (n & 7) * 2;
           b[j] = tr_read_pair(bs, off0, off1);
+        }
+        const int64_t rem = krem - (ks * 16 + 8 * (lane >> 5));
+        if (rem < 8) {
+          u32x4 m;
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+            m[w] = rem >= 2 * w + 2 ? 0xffffffffu : rem == 2 * w + 1 ? 0x0000ffffu : 0u;
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+            a[i] &= m;
         }
 #pragma unroll
         for (int i = 0; i < FM; ++i)
@@ -253,7 +271,7 @@ struct Gemm16Dma {
 #pragma unroll
       for (int s = 0; s < STAGES; ++s)
         if (s == sl)
-          compute(as[s], bs[s], p.last_ks, acc);
+          compute(as[s], bs[s], p.last_ks, acc, p.K - (int64_t)(total - 1) * BK);
     }
 
     epilogue<MASK_MN>(p, m0, n0, acc);

@@ -23,7 +23,12 @@
 //
 // K loop in LoopSplit form: k_main_steps unmasked steps, then the masked
 // ones (zero-filled past K, the tl.load(mask, other=0) of the reference
-// kernel); the last step issues only last_ks of its 4 sub-steps.
+// kernel); the last step issues only last_ks of its 4 sub-steps.  K and N
+// need not fill whole 16-byte chunks: the buffer ranges end at the chunk
+// holding an operand's last element, a chunk that crosses K is loaded whole
+// and its elements past K are zeroed in registers in the last step (B's rows
+// past K already read as zeros), and columns past N only reach accumulators
+// the epilogue does not store.
 #pragma once
 
 #include "gemm16_dma.h"
@@ -215,6 +220,28 @@ template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
                                                     0, 0, 0);
   }
 
+  // Zero the elements at K or beyond in the fragments of sub-step ks of K
+  // step kt (the last step): lane l's A fragment (and a K-major B fragment)
+  // holds K values 8 c .. 8 c + 7 of the step, c = 2 ks + l / 32.  Row-major
+  // B needs nothing: its rows past K lie beyond the buffer and read as zeros.
+  __device__ __forceinline__ static void mask_k(Frags &f, int kt, int ks, int64_t K) {
+    const int64_t rem = K - ((int64_t)kt * BK + ks * 16 + 8 * ((threadIdx.x & 63) >> 5));
+    if (rem >= 8)
+      return;
+    u32x4 m;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      m[w] = rem >= 2 * w + 2 ? 0xffffffffu : rem == 2 * w + 1 ? 0x0000ffffu : 0u;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      f.a[i] &= m;
+    if constexpr (BT) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        f.b[j] = __builtin_bit_cast(i16x8_t, __builtin_bit_cast(u32x4, f.b[j]) & m);
+    }
+  }
+
   __device__ __forceinline__ static void mfmas(const Frags &f, f32x16_t (&acc)[FM][FN]) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -308,9 +335,12 @@ template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
     constexpr uint32_t STAGE = A_BYTES + B_BYTES;
     auto stage_ptr = [&](int kt) { return smem + (kt & 1) * STAGE; };
     auto stage_addr = [&](int kt) { return lds0 + (kt & 1) * STAGE; };
-    const i32x4_t ra = make_rsrc(p.A, (uint32_t)(((p.M - 1) * p.lda + p.K) * 2));
-    const i32x4_t rb = make_rsrc(p.B, BT ? (uint32_t)(((p.N - 1) * p.ldb + p.K) * 2)
-                                         : (uint32_t)(((p.K - 1) * p.ldb + p.N) * 2));
+    // Ranges end at the 16-byte chunk holding each operand's last element
+    // (rows start 16-byte aligned, so that chunk is the row's own).
+    const int64_t K8 = (p.K + 7) & ~7ll, N8 = (p.N + 7) & ~7ll;
+    const i32x4_t ra = make_rsrc(p.A, (uint32_t)(((p.M - 1) * p.lda + K8) * 2));
+    const i32x4_t rb = make_rsrc(p.B, BT ? (uint32_t)(((p.N - 1) * p.ldb + K8) * 2)
+                                         : (uint32_t)(((p.K - 1) * p.ldb + N8) * 2));
     Offsets o;
     offsets<MASK_MN>(p, m0, n0, o);
     auto step_barrier = [] {
@@ -374,17 +404,22 @@ template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
       const int nks = p.last_ks;
       if (nks > 1)
         load_frags(as, bs, 1, wm, wn, f1);
+      mask_k(f0, kt, 0, p.K);
       mfmas(f0, acc);
       if (nks > 1) {
         if (nks > 2)
           load_frags(as, bs, 2, wm, wn, f0);
+        mask_k(f1, kt, 1, p.K);
         mfmas(f1, acc);
         if (nks > 2) {
           if (nks > 3)
             load_frags(as, bs, 3, wm, wn, f1);
+          mask_k(f0, kt, 2, p.K);
           mfmas(f0, acc);
-          if (nks > 3)
+          if (nks > 3) {
+            mask_k(f1, kt, 3, p.K);
             mfmas(f1, acc);
+          }
         }
       }
       // Loads of a step past the end may still be writing zeros into LDS:
@@ -414,11 +449,27 @@ template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int64_t col = n0 + wn * WTN_ + j * 32 + 8 * g + 4 * (lane >> 5);
-          if (MASK_MN && col >= p.N) // N % 4 == 0: the quad is all in or all out
+          if (MASK_MN && col >= p.N)
             continue;
           const int64_t off = row * p.ldc + col;
           const float v0 = acc[i][j][4 * g], v1 = acc[i][j][4 * g + 1];
           const float v2 = acc[i][j][4 * g + 2], v3 = acc[i][j][4 * g + 3];
+          if (MASK_MN && col + 4 > p.N) { // the quad crosses N: element by element
+            const float v[4] = {v0, v1, v2, v3};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              if (col + r >= p.N)
+                break;
+              if (EPI == EPI_F32) {
+                float *c = reinterpret_cast<float *>(p.C) + off + r;
+                *c = p.accumulate ? *c + v[r] : v[r];
+              } else {
+                reinterpret_cast<uint16_t *>(p.C)[off + r] =
+                    EPI == EPI_BF16 ? f32_to_bf16_rne(v[r]) : f32_to_f16_rne(v[r]);
+              }
+            }
+            continue;
+          }
           if (EPI == EPI_F32) {
             float4 *c = reinterpret_cast<float4 *>(reinterpret_cast<float *>(p.C) + off);
             if (p.accumulate) {

@@ -102,8 +102,9 @@ template <int OP, int EPI> struct Gemm8N224 {
     const int nmain = p.k_main_steps;
     const int total = nmain + p.k_masked_steps;
     const uint32_t lds0 = lds_addr(smem);
-    const i32x4_t ra = make_rsrc(p.A, (uint32_t)((p.M - 1) * p.lda + p.K));
-    const i32x4_t rb = make_rsrc(p.B, (uint32_t)((p.K - 1) * p.ldb + p.N));
+    // Ranges end at the 16-byte chunk holding each operand's last element.
+    const i32x4_t ra = make_rsrc(p.A, (uint32_t)((p.M - 1) * p.lda + ((p.K + 15) & ~15ll)));
+    const i32x4_t rb = make_rsrc(p.B, (uint32_t)((p.K - 1) * p.ldb + ((p.N + 15) & ~15ll)));
     i32x4_t rsa = {0, 0, 0, 0}, rsb = {0, 0, 0, 0};
     if (SCALED) {
       rsa = make_rsrc(p.sa, (uint32_t)(p.M * p.sa_ld * 4));
@@ -250,6 +251,11 @@ template <int OP, int EPI> struct Gemm8N224 {
       };
       for (int kt = 0; kt + 1 < total; ++kt)
         step(kt, true);
+      if constexpr (OP == OP_F8) { // fp8 K tail: A's bytes past K (W::mask_k)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          a[i] = W::mask_k(a[i], total - 1, p.K);
+      }
       step(total - 1, false);
       flush(FN - 1);
       // Loads of a step past the end may still be writing zeros into LDS.

@@ -301,6 +301,22 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
     }
   }
 
+  // fp8 K tail (a 16-byte chunk that crosses K is loaded whole; K need not
+  // fill whole chunks): zero the bytes of this lane's A fragment at K or
+  // beyond in the last step.  Byte t of the fragment is K index
+  // kt * BK + 32 (l / 16) + t (chunks 2 (l / 16) and 2 (l / 16) + 1); B's
+  // rows past K already read as zeros, and an fp8 NaN code times zero would
+  // still be NaN.  (int8 needs nothing: junk times zero is zero.)
+  __device__ __forceinline__ static i32x8_t mask_k(i32x8_t v, int kt, int64_t K) {
+    const int64_t rem = K - ((int64_t)kt * BK + 32 * ((threadIdx.x & 63) >> 4));
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      const int64_t vb = rem - 4 * w;
+      v[w] &= vb >= 4 ? -1 : vb <= 0 ? 0 : (int)((1u << (8 * vb)) - 1u);
+    }
+    return v;
+  }
+
   // Ties a value to this point of the program: the compiler otherwise sinks
   // the scale FMAs (pure arithmetic) to the end of the step, where every row
   // block's partial products would be live at once.
@@ -323,8 +339,11 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
     const int nmain = p.k_main_steps;
     const int total = nmain + p.k_masked_steps;
     const uint32_t lds0 = lds_addr(smem);
-    const i32x4_t ra = make_rsrc(p.A, (uint32_t)((p.M - 1) * p.lda + p.K));
-    const i32x4_t rb = make_rsrc(p.B, (uint32_t)((p.K - 1) * p.ldb + p.N));
+    // Ranges end at the 16-byte chunk holding each operand's last element
+    // (rows start 16-byte aligned, so that chunk is the row's own).  fp4 A:
+    // K and lda count bytes here.
+    const i32x4_t ra = make_rsrc(p.A, (uint32_t)((p.M - 1) * p.lda + ((p.K + 15) & ~15ll)));
+    const i32x4_t rb = make_rsrc(p.B, (uint32_t)((p.K - 1) * p.ldb + ((p.N + 15) & ~15ll)));
     i32x4_t rsa = {0, 0, 0, 0}, rsb = {0, 0, 0, 0};
     if (SCALED) {
       rsa = make_rsrc(p.sa, (uint32_t)(p.M * p.sa_ld * 4));
@@ -400,8 +419,11 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
       // tail: the last step (MX scale groups past K/32 possible).
       auto step = [&](int kt, bool more, auto tail) {
         constexpr bool TAIL = MX && decltype(tail)::value;
+        constexpr bool KTAIL = !INT && !MX && decltype(tail)::value;
         const uint32_t so = (kt & 1) * STAGE, sn = ((kt + 1) & 1) * STAGE;
         i32x8_t a = read_a(bs, so, 0);
+        if constexpr (KTAIL)
+          a = mask_k(a, kt, p.K);
         float sc = scale(so, 0);
         int sxa = MX ? read_sx(xa, so, 0) : 0;
         if constexpr (TAIL) {
@@ -417,6 +439,8 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
           int sxn = 0;
           if (i + 1 < FM) {
             an = read_a(bs, so, i + 1);
+            if constexpr (KTAIL)
+              an = mask_k(an, kt, p.K);
             sn_ = scale(so, i + 1);
             if constexpr (MX)
               sxn = read_sx(xa, so, i + 1);
@@ -495,10 +519,34 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
 #pragma unroll
       for (int j = 0; j < FN_; ++j) {
         const int64_t col = n0 + wn * WTN_ + 16 * j + 4 * (lane >> 4);
-        if (MASK_MN && col >= p.N) // N % 16 == 0: the quad is all in or all out
+        if (MASK_MN && col >= p.N)
           continue;
         const int64_t off = row * p.ldc + col;
         const Acc &v = acc[i][j];
+        if (MASK_MN && col + 4 > p.N) { // the quad crosses N: element by element
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if (col + r >= p.N)
+              break;
+            if (EPI == EPI_I32) {
+              int32_t *c = reinterpret_cast<int32_t *>(p.C) + off + r;
+              *c = p.accumulate ? *c + (int32_t)v[r] : (int32_t)v[r];
+            } else if (EPI == EPI_F32 || EPI == EPI_BLOCK128_F32 || EPI == EPI_MX_F32) {
+              float *c = reinterpret_cast<float *>(p.C) + off + r;
+              *c = p.accumulate ? *c + (float)v[r] : (float)v[r];
+            } else {
+              float f;
+              if (EPI == EPI_ROWCOL_BF16) {
+#pragma clang fp contract(off)
+                f = ((float)v[r] * sar) * p.sb[col + r];
+              } else {
+                f = (float)v[r];
+              }
+              reinterpret_cast<uint16_t *>(p.C)[off + r] = f32_to_bf16_rne(f);
+            }
+          }
+          continue;
+        }
         if (EPI == EPI_I32) {
           i32x4_t *c = reinterpret_cast<i32x4_t *>(reinterpret_cast<int32_t *>(p.C) + off);
           *c = p.accumulate ? *c + v : v;

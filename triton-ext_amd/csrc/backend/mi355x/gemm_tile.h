@@ -204,6 +204,16 @@ struct GemmTile {
         const bool ok = (!MASK_MN || gm < p.M) && (!MASK_K || gk < p.K);
         ra[i] = ok ? *reinterpret_cast<const u32x4 *>(p.A + (gm * p.lda + gk) * ELT)
                    : zero;
+        if (MASK_K && gk + E > p.K) {
+          // the chunk crosses K (K need not fill whole chunks): keep the
+          // bytes of elements below K (B's rows past K are zero-filled)
+          const int64_t vb = (p.K - gk) * ELT;
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+            ra[i][w] &= vb >= 4 * w + 4 ? 0xffffffffu
+                        : vb <= 4 * w   ? 0u
+                                        : (1u << (8 * (vb - 4 * w))) - 1u;
+        }
       }
 #pragma unroll
       for (int i = 0; i < B_PER; ++i) {

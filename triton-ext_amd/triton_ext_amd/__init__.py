@@ -14,4 +14,5 @@ torch is used only for device memory and streams.  There is no CPU fallback:
 if libmi355x_dot.so is missing, `load()` raises.
 """
 from .capi import *  # noqa: F401,F403
-from .dot import attention, dot, dot_scaled, plan_for, tx_type, workspace_for  # noqa: F401
+from .dot import (aligned_rows, attention, dot, dot_scaled, new_output, plan_for, tx_type,  # noqa: F401
+                  workspace_for)

@@ -4,6 +4,7 @@ torch provides the device memory and the current HIP stream; all arithmetic
 runs in libmi355x_dot.so's kernels.
 """
 import ctypes
+import math
 
 from . import capi
 
@@ -29,9 +30,60 @@ def _torch_dtype(tx):
             capi.I32: torch.int32}[tx]
 
 
-def plan_for(a, b, out_dtype_tx, scale_mode=capi.SCALE_NONE, block=(0, 0, 0), flags=0):
+def _row_pitch(cols, elt_bytes):
+    """Elements per row rounded up to a 16-byte multiple."""
+    q = 16 // math.gcd(16, elt_bytes)
+    return -(-cols // q) * q
+
+
+def new_output(M, N, dtype, device):
+    """An [M, N] tensor whose rows start 16 bytes apart as the kernels need:
+    a view of [M, N'] storage, N' = N rounded up to whole 16-byte rows."""
+    import torch
+    elt = torch.empty(0, dtype=dtype).element_size()
+    ld = _row_pitch(N, elt)
+    return torch.empty((M, ld), dtype=dtype, device=device)[:, :N]
+
+
+def _out_ldc(out):
+    """C's row stride for a plan: out's own (which must start rows 16 bytes
+    apart), or, for a single row, any 16-byte pitch (never used)."""
+    if out.dim() != 2 or (out.shape[1] > 1 and out.stride(1) != 1):
+        raise ValueError("out must be a row-major [M, N] tensor")
+    if out.shape[0] <= 1:
+        return _row_pitch(max(out.shape[1], 1), out.element_size())
+    if (out.stride(0) * out.element_size()) % 16 or out.data_ptr() % 16:
+        raise ValueError("out's rows must start 16 bytes apart on a 16-byte aligned base "
+                         "(new_output makes such a tensor)")
+    return out.stride(0)
+
+
+def aligned_rows(t):
+    """t itself when its rows (or, for a transposed view, its columns) start
+    16 bytes apart on a 16-byte aligned base, else a copy in padded storage
+    of the same layout.  The kernels read 16-byte chunks; K and N themselves
+    may be any size."""
+    import torch
+    if t.dim() != 2 or t.numel() == 0:
+        return t
+    elt = t.element_size()
+    kmajor = t.stride(1) != 1 and t.stride(0) == 1 and t.shape[1] > 1
+    ld = t.stride(1) if kmajor else t.stride(0)
+    if (ld * elt) % 16 == 0 and t.data_ptr() % 16 == 0:
+        return t
+    if kmajor:  # [N][K] storage viewed as [K][N]
+        return aligned_rows(t.t().contiguous()).t()
+    if t.stride(1) != 1:
+        t = t.contiguous()
+    buf = torch.empty((t.shape[0], _row_pitch(t.shape[1], elt)), dtype=t.dtype, device=t.device)
+    buf[:, :t.shape[1]].copy_(t)
+    return buf[:, :t.shape[1]]
+
+
+def plan_for(a, b, out_dtype_tx, scale_mode=capi.SCALE_NONE, block=(0, 0, 0), flags=0, ldc=0):
     """Plan C = A @ B.  B may be row-major [K,N] or a transposed view of a
-    row-major [N,K] tensor (K-major, e.g. `k.t()` in q @ k.T)."""
+    row-major [N,K] tensor (K-major, e.g. `k.t()` in q @ k.T).  ldc: C's row
+    stride (0: packed)."""
     if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[0]:
         raise ValueError(f"dot of {tuple(a.shape)} and {tuple(b.shape)}")
     M, K = a.shape
@@ -45,7 +97,8 @@ def plan_for(a, b, out_dtype_tx, scale_mode=capi.SCALE_NONE, block=(0, 0, 0), fl
     lda = a.stride(0) if M > 0 and K > 0 else 0
     ldb = (b.stride(1) if b_kmajor else b.stride(0)) if K > 0 and N > 0 else 0
     desc = capi.make_desc(M, N, K, tx_type(a), out_dtype_tx, b_type=tx_type(b),
-                          scale_mode=scale_mode, block=block, lda=lda, ldb=ldb, flags=flags)
+                          scale_mode=scale_mode, block=block, lda=lda, ldb=ldb, ldc=ldc,
+                          flags=flags)
     return capi.plan(desc)
 
 
@@ -78,13 +131,21 @@ def dot(a, b, out=None, out_dtype=None, scale_a=None, scale_b=None, scale_mode=N
     BLOCK128 for fp8 operands with scales, else NONE.  acc (fp32 or int32
     [M, N]): returns acc + A @ B, as tl.dot(a, b, acc) does, in a new tensor
     (or in `out`); the kernel adds its finished sum to C.
+
+    K and N may be any size.  Operands whose rows do not start 16 bytes
+    apart are copied to padded storage first (one extra pass), and a new
+    output is a view of padded storage; a given `out` must already have
+    16-byte row strides.
     """
     import torch
+    if plan is None:
+        a, b = aligned_rows(a), aligned_rows(b)
     if acc is not None:
         if acc.dtype not in (torch.float32, torch.int32) or acc.dim() != 2:
             raise ValueError("acc must be an fp32 or int32 [M, N] tensor")
         if out is None:
-            out = acc.clone(memory_format=torch.contiguous_format)
+            out = new_output(acc.shape[0], acc.shape[1], acc.dtype, acc.device)
+            out.copy_(acc)
         elif out.data_ptr() != acc.data_ptr():
             out.copy_(acc)
         flags |= capi.FLAG_ACCUMULATE
@@ -101,15 +162,16 @@ def dot(a, b, out=None, out_dtype=None, scale_a=None, scale_b=None, scale_mode=N
     else:
         c_tx = capi.I32 if (ta == capi.I8 and scale_mode == capi.SCALE_NONE) else (
             capi.BF16 if ta in (capi.BF16, capi.I8, capi.F8E4M3) else capi.F32)
-    p = plan if plan is not None else plan_for(a, b, c_tx, scale_mode, block, flags)
+    M, N = a.shape[0], b.shape[1]
+    if out is None:
+        out = new_output(M, N, _torch_dtype(c_tx), a.device)
+    ldc = _out_ldc(out)
+    p = plan if plan is not None else plan_for(a, b, c_tx, scale_mode, block, flags, ldc=ldc)
     if bool(p.desc.flags & capi.FLAG_ACCUMULATE) != (acc is not None):
         raise ValueError("plan and call disagree on acc: the plan's FLAG_ACCUMULATE must be "
                          "set exactly when acc is given")
-    M, N = a.shape[0], b.shape[1]
-    if out is None:
-        out = torch.empty((M, N), dtype=_torch_dtype(c_tx), device=a.device)
-    if out.stride(1) != 1 or out.stride(0) != p.desc.ldc:
-        raise ValueError("output must be row-major with ldc == N")
+    if M > 1 and ldc != p.desc.ldc:
+        raise ValueError(f"out's row stride {ldc} differs from the plan's ldc {p.desc.ldc}")
     if stream is None:
         stream = torch.cuda.current_stream(a.device).cuda_stream
     ws = workspace if workspace is not None else workspace_for(p, a.device, stream)
@@ -202,7 +264,8 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
     flags = 0
     if acc is not None:  # acc + dot, in a new tensor (or `out`), as tl.dot_scaled(acc=)
         if out is None:
-            out = acc.clone(memory_format=torch.contiguous_format)
+            out = new_output(acc.shape[0], acc.shape[1], acc.dtype, acc.device)
+            out.copy_(acc)
         elif out.data_ptr() != acc.data_ptr():
             out.copy_(acc)
         flags = capi.FLAG_ACCUMULATE
@@ -210,21 +273,22 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
         c_tx = tx_type(out)
     else:
         c_tx = capi.BF16 if out_dtype == torch.bfloat16 else capi.F32
+    if out is None:
+        out = new_output(M, N, _torch_dtype(c_tx), lhs.device)
+    ldc = _out_ldc(out)
     if plan is None:
         lda = lhs.stride(0) * pa if M > 0 and K > 0 else 0
         ldb = rhs.stride(0) if K > 0 and N > 0 else 0
         desc = capi.make_desc(M, N, K, _MX_FORMATS.get(lhs_format, capi.BF16), c_tx,
                               b_type=_MX_FORMATS.get(rhs_format, capi.BF16),
                               scale_mode=capi.SCALE_NV16 if nv else capi.SCALE_MX32,
-                              block=block, lda=lda, ldb=ldb, flags=flags)
+                              block=block, lda=lda, ldb=ldb, ldc=ldc, flags=flags)
         plan = capi.plan(desc)
     elif bool(plan.desc.flags & capi.FLAG_ACCUMULATE) != (acc is not None):
         raise ValueError("plan and call disagree on acc: the plan's FLAG_ACCUMULATE must be "
                          "set exactly when acc is given")
-    if out is None:
-        out = torch.empty((M, N), dtype=_torch_dtype(c_tx), device=lhs.device)
-    if out.stride(1) != 1 or out.stride(0) != plan.desc.ldc:
-        raise ValueError("output must be row-major with ldc == N")
+    if M > 1 and ldc != plan.desc.ldc:
+        raise ValueError(f"out's row stride {ldc} differs from the plan's ldc {plan.desc.ldc}")
     if stream is None:
         stream = torch.cuda.current_stream(lhs.device).cuda_stream
     ws = _upcast_workspace(plan, lhs.device, stream)
