@@ -524,7 +524,29 @@ def fp8_attention(rng):
     attn_case(rng, "attn_fwd_fp8_plain", 1, 1, 128, 64, False, 0.5, (64, 32), fp8=True)
 
 
+def e4m3_max_codes(rng):
+    """e4m3 codes 0x7F / 0xFF (S.1111.111) inside a tiled fp8 dot.  OCP e4m3fn
+    (Triton's fp8e4nv) makes them NaN; the interpreter's generic converter
+    (T:runtime/interpreter.py:202-263) decodes them as +-480.  Dyadic values
+    elsewhere (j/8, |j| <= 15), so every partial sum is exact in fp32 and the
+    fixture pins the interpreter's decode bit for bit.  Max codes sit in A
+    rows 3, 17 and 40 and in B column 9."""
+    M, N, K = 64, 64, 128
+    a = bits(dyadic((M, K), rng, 15, 8, torch.float8_e4m3fn)).copy()
+    b = bits(dyadic((K, N), rng, 15, 8, torch.float8_e4m3fn)).copy()
+    a[3, 5], a[17, 77], a[40, 127] = 0x7F, 0xFF, 0x7F
+    b[100, 9] = 0xFF
+    at = torch.from_numpy(a).view(torch.float8_e4m3fn)
+    bt = torch.from_numpy(b).view(torch.float8_e4m3fn)
+    save("fp8e4m3_maxcode_f32_exact", at, bt, run(at, bt, out="f32", block=(32, 32, 64)),
+         block=(32, 32, 64), out="f32", exact=True)
+
+
 if __name__ == "__main__":
     if not os.environ.get("TRITON_INTERPRET"):
         sys.exit("set TRITON_INTERPRET=1")
-    main()
+    if sys.argv[1:] == ["e4m3_max_codes"]:  # only this fixture
+        e4m3_max_codes(np.random.default_rng(20261203))
+    else:
+        main()
+        e4m3_max_codes(np.random.default_rng(20261203))

@@ -526,3 +526,32 @@ def test_dot_scaled_accumulate(gpu, lhs_fmt, rhs_fmt):
     torch.cuda.synchronize()
     want = (from_device(plain) + from_device(acc)).astype(np.float32)
     assert np.array_equal(from_device(got).view(np.int32), want.view(np.int32))
+
+
+def test_e4m3_max_codes_are_nan(gpu):
+    """e4m3 codes 0x7F / 0xFF.  gfx950's MFMA reads them as NaN, as OCP e4m3fn
+    (Triton's fp8e4nv, torch.float8_e4m3fn) defines them; the Triton
+    interpreter's generic converter decodes them as +-480
+    (T:runtime/interpreter.py:202-263), which the interpreter fixture and the
+    oracle reproduce.  The product keeps the hardware's reading: every output
+    whose row of A or column of B holds such a code is NaN, and every other
+    output equals the interpreter's bit for bit (the fixture is dyadic)."""
+    import os
+
+    import torch
+    from test_oracle_cpu import GOLDEN, load_fixture
+    f = load_fixture(os.path.join(GOLDEN, "fp8e4m3_maxcode_f32_exact.npz"))
+    a, b = f["a"], f["b"]
+    say("e4m3 max codes")
+    c = tx.dot(to_device(a, gpu).view(torch.float8_e4m3fn),
+               to_device(b, gpu).view(torch.float8_e4m3fn), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    got = from_device(c)
+    bad_rows = ((a & 0x7F) == 0x7F).any(axis=1)
+    bad_cols = ((b & 0x7F) == 0x7F).any(axis=0)
+    poisoned = bad_rows[:, None] | bad_cols[None, :]
+    assert bad_rows.sum() == 3 and bad_cols.sum() == 1
+    assert np.isnan(got[poisoned]).all()
+    assert np.array_equal(got[~poisoned], f["c"][~poisoned])
+    # the interpreter itself (and the oracle) read +-480: finite everywhere
+    assert np.isfinite(f["c"]).all()
