@@ -27,7 +27,9 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+# TX_ORACLE_LIB: another build of the same source (the sanitizer build,
+# oracle/_asan/liboracle.so)
+LIB_PATH = os.environ.get("TX_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 
 F32, F16, BF16, I8, F8E4M3, I32, F8E5M2, F4E2M1 = 0, 1, 2, 3, 4, 5, 6, 7
 E8M0 = -1  # scale codec selector of mx_decode

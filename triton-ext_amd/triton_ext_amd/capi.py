@@ -3,7 +3,9 @@ import ctypes
 import os
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-LIB_DIR = os.path.join(os.path.dirname(PKG_DIR), "lib")
+# TX_LIB_DIR: another build of the same libraries (the sanitizer build,
+# triton-ext_amd/lib_asan)
+LIB_DIR = os.environ.get("TX_LIB_DIR") or os.path.join(os.path.dirname(PKG_DIR), "lib")
 
 # tx_dtype
 F32, F16, BF16, I8, F8E4M3, I32, F8E5M2, F4E2M1 = 0, 1, 2, 3, 4, 5, 6, 7
