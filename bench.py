@@ -52,7 +52,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
-                    help="secondary workloads to run, comma-separated: ceiling, c1, vendor, tail, w8a8 (or "
+                    help="secondary workloads to run, comma-separated: ceiling, tiles, c1, vendor, tail, "
+                         "w8a8 (or "
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256), int8, fp8, kmajor, mx (or mxfp8, mxfp4, "
                          "mxfp8_4096, mxfp8_8192, mxfp4_4096, mxfp4_8192), mxbf16 (or mxbf16_fp4, mxbf16_fp8: "
                          "bf16 x MX), attn (or attn_1024, attn_4096, "
@@ -493,6 +494,32 @@ def bench_mfma_ceiling(dev, steps, warmup, seed=1):
                 ms=ms, tflops=flops / ms / 1e9, frac=flops / ms / 1e-3 / PEAK_BF16)
 
 
+def bench_tiles(tx, dev, steps, warmup):
+    """Every instantiated tile at one large shape per operand type: the measured
+    sustained fraction of peak behind the arith_intensity pass's tile weights."""
+    import torch
+    rows = []
+    M = N = K = 4096
+    a, b = bf16_inputs(M, N, K, dev, 11)
+    c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    for blk in ((256, 256, 64), (128, 128, 64), (64, 64, 32)):
+        ms = time_back_to_back(Launcher(tx, a, b, c, block=blk), steps, warmup)
+        rows.append(dict(workload=f"tile {blk[0]}x{blk[1]}x{blk[2]} bf16 4096^3", tile=list(blk),
+                         ms=ms, tflops=2.0 * M * N * K / ms / 1e9,
+                         frac=2.0 * M * N * K / ms / 1e-3 / PEAK_BF16))
+    g = torch.Generator(device=dev)
+    g.manual_seed(12)
+    ai = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+    bi = torch.randint(-127, 128, (K, N), generator=g, device=dev, dtype=torch.int8)
+    ci = torch.empty((M, N), dtype=torch.int32, device=dev)
+    for blk in ((256, 256, 128), (256, 224, 128), (128, 128, 128)):
+        ms = time_back_to_back(Launcher(tx, ai, bi, ci, block=blk), steps, warmup)
+        rows.append(dict(workload=f"tile {blk[0]}x{blk[1]}x{blk[2]} int8 4096^3", tile=list(blk),
+                         ms=ms, tops=2.0 * M * N * K / ms / 1e9,
+                         frac=2.0 * M * N * K / ms / 1e-3 / PEAK_I8))
+    return rows
+
+
 def cpu_baseline(a, b, c, M, N, K, block):
     """Oracle on the host cores over the full bf16 workload; also checks the GPU output."""
     import numpy as np
@@ -572,6 +599,10 @@ def main():
             r, _ = bench_bf16(tx, dev, m, n, k, args.steps, args.warmup, seed=2)
             secondary.append(r)
             print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    if want("tiles"):
+        for r in bench_tiles(tx, dev, args.steps, args.warmup):
+            secondary.append(r)
+            print(f"# {r['workload']}: {100 * r['frac']:.1f}% of peak", file=sys.stderr, flush=True)
     ceil = {}
     if want("ceiling"):
         r = bench_mfma_ceiling(dev, args.steps, args.warmup)

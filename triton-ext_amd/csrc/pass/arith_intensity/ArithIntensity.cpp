@@ -34,17 +34,22 @@ struct Tile {
   double eff; // fraction of MFMA peak a tile of this size sustains
 };
 
-// Tiles the backend instantiates, largest first.  `eff` is a planning
-// weight only: it ranks tiles by how well they amortise LDS fills.
-const Tile kTiles16[] = {{256, 256, 64, 0.85}, {128, 128, 64, 0.60},
-                         {64, 64, 32, 0.35}};
+// Tiles the backend instantiates, largest first.  `eff` is the fraction of
+// the dense MFMA peak each tile sustained at 4096^3 on one MI355X (bench.py
+// --only tiles: bf16 -> bf16 and int8 -> int32, back-to-back launches):
+// 16-bit 256x256x64 0.509, 128x128x64 0.341, 64x64x32 0.116; 8-bit
+// 256x256x128 0.463, 128x128x128 0.173.  tileCost weighs them against the
+// waves of tiles a shape needs.
+const Tile kTiles16[] = {{256, 256, 64, 0.509}, {128, 128, 64, 0.341},
+                         {64, 64, 32, 0.116}};
 // 8-bit tiles.  (A 256x224 tile also exists for explicit requests: it fills
 // all CUs at N = 7168, but its A-resident wave layout needs 28 transposed B
-// reads per step against 16, and measured no faster than 256x256 there.)
-const Tile kTiles8[] = {{256, 256, 128, 0.85}, {128, 128, 128, 0.60}};
+// reads per step against 16; it measured 0.273 at int8 4096^3 and no faster
+// than 256x256 at N = 7168.)
+const Tile kTiles8[] = {{256, 256, 128, 0.463}, {128, 128, 128, 0.173}};
 // MX (tl.dot_scaled) tiles: one 256x256 tile of 128 bytes of K per step,
 // i.e. 128 fp8 or 256 fp4 elements.
-const Tile kTileMx8 = {256, 256, 128, 0.85}, kTileMx4 = {256, 256, 256, 0.85};
+const Tile kTileMx8 = {256, 256, 128, 0.45}, kTileMx4 = {256, 256, 256, 0.33};
 
 // Estimated time of a tiled dot in arbitrary units: whole waves of tiles
 // across the CUs, each tile costing BM*BN*K / eff.
