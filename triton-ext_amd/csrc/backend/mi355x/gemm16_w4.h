@@ -427,7 +427,86 @@ template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
       __builtin_amdgcn_s_waitcnt(0x7 << 4);
     }
 
-    epilogue_tile<MASK_MN, FM, FN, WTM, WTN>(p, m0, n0, wm, wn, acc);
+    if constexpr (!MASK_MN && NW == 4)
+      epilogue_lds(p, m0, n0, wm, wn, acc, lds0);
+    else
+      epilogue_tile<MASK_MN, FM, FN, WTM, WTN>(p, m0, n0, wm, wn, acc);
+  }
+
+  // Epilogue of an interior tile through LDS (the two stages, 128 KiB, are
+  // free once every wave is past the K loop).  The accumulators' own layout
+  // writes 8-byte pieces of 32 rows per store instruction; staged as
+  // row-major C in LDS, the tile leaves in whole rows instead: each store
+  // instruction writes 1 KiB of contiguous 16-byte chunks, two 512-byte rows
+  // of bf16 / fp16 (one pass) or one 1 KiB fp32 row of a half tile (two
+  // passes of 128 rows).  Measured: the bf16 epilogue's cycles halved
+  // (20.5k -> 10.2k per wave at 4096^3).  LDS row r holds 16-byte chunk c at
+  // c ^ (r & 31), so the 32 rows one accumulator store touches, and the two
+  // rows one read covers, spread over the banks.
+  __device__ __forceinline__ static void epilogue_lds(const GemmArgs &p, int64_t m0, int64_t n0,
+                                                      int wm, int wn, const f32x16_t (&acc)[FM][FN],
+                                                      uint32_t lds0) {
+    typedef unsigned v2u __attribute__((ext_vector_type(2)));
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) v2u lds_v2u;
+    typedef __attribute__((address_space(3))) v4u lds_v4u;
+    const int lane = threadIdx.x & 63, t = threadIdx.x;
+    constexpr bool F32 = EPI == EPI_F32;
+    constexpr int ROWB = F32 ? 1024 : 512; // LDS bytes per staged row
+    constexpr int ROWS = F32 ? 128 : 256;  // rows per pass
+    constexpr int CH = ROWB / 16;          // 16-byte chunks per row
+    static_assert(ROWS * ROWB <= 2 * (A_BYTES + B_BYTES), "staged C fits the two stages");
+    static_assert(NW * 64 == 256 && BN == 256, "one 1 KiB store per wave and pass step");
+    __syncthreads(); // every wave is done reading the stages
+#pragma unroll
+    for (int pass = 0; pass < (F32 ? 2 : 1); ++pass) {
+      if (!F32 || wm == pass) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const int r = (F32 ? 0 : wm * WTM) + i * 32 + (lane & 31);
+              const int col = wn * WTN + j * 32 + 8 * g + 4 * (lane >> 5);
+              const float v[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                  acc[i][j][4 * g + 3]};
+              if constexpr (F32) {
+                const int ch = col >> 2;
+                *(lds_v4u *)(uintptr_t)(lds0 + r * ROWB + ((ch ^ (r & 31)) << 4)) =
+                    v4u{__builtin_bit_cast(unsigned, v[0]), __builtin_bit_cast(unsigned, v[1]),
+                        __builtin_bit_cast(unsigned, v[2]), __builtin_bit_cast(unsigned, v[3])};
+              } else {
+                const int ch = col >> 3;
+                const v2u w = EPI == EPI_BF16 ? v2u{pk_bf16_rne(v[0], v[1]), pk_bf16_rne(v[2], v[3])}
+                                              : v2u{pk_f16_rne(v[0], v[1]), pk_f16_rne(v[2], v[3])};
+                *(lds_v2u *)(uintptr_t)(lds0 + r * ROWB + ((ch ^ (r & 31)) << 4) + (col & 7) * 2) = w;
+              }
+            }
+      }
+      __syncthreads();
+      const int64_t row0 = m0 + pass * ROWS;
+#pragma unroll 4
+      for (int q = 0; q < ROWS * CH / 256; ++q) {
+        const int idx = q * 256 + t, r = idx / CH, ch = idx % CH;
+        const v4u v = *(const lds_v4u *)(uintptr_t)(lds0 + r * ROWB + ((ch ^ (r & 31)) << 4));
+        if constexpr (F32) {
+          v4u *c = reinterpret_cast<v4u *>(reinterpret_cast<float *>(p.C) + (row0 + r) * p.ldc +
+                                           n0 + ch * 4);
+          if (p.accumulate) {
+            typedef float v4f __attribute__((ext_vector_type(4)));
+            *c = __builtin_bit_cast(v4u, __builtin_bit_cast(v4f, *c) + __builtin_bit_cast(v4f, v));
+          } else {
+            *c = v;
+          }
+        } else {
+          *reinterpret_cast<v4u *>(reinterpret_cast<uint16_t *>(p.C) + (row0 + r) * p.ldc + n0 +
+                                   ch * 8) = v;
+        }
+      }
+      if (F32 && pass == 0)
+        __syncthreads(); // the first half is read out before the second is staged
+    }
   }
 
   // Epilogue of a wave's (FM*32) x (FN*32) sub-tile at (wm, wn): lane l
