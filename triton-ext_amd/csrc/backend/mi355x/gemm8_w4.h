@@ -492,7 +492,97 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
       flush(acc[FM - 1]);
       __builtin_amdgcn_s_waitcnt(0x7 << 4);
     }
-    epilogue<MASK_MN>(p, m0, n0, wm, wn, acc);
+    if constexpr (!MASK_MN)
+      epilogue_lds(p, m0, n0, wm, wn, acc, lds0);
+    else
+      epilogue<MASK_MN>(p, m0, n0, wm, wn, acc);
+  }
+
+  // Epilogue of an interior tile through LDS (the two stages are free once
+  // every wave is past the K loop): C is staged row-major and leaves in whole
+  // rows, each store instruction writing 1 KiB of contiguous 16-byte chunks
+  // (two 512-byte bf16 rows, or one 1 KiB row of 32-bit C per pass of 128
+  // rows), rather than the accumulators' own 32-byte pieces of 16 rows.  LDS
+  // row r holds 16-byte chunk c at c ^ (r & 31).  The values are final
+  // before staging: the row x column scales of the W8A8 epilogue are applied
+  // in registers, and accumulation into C happens on the way out.
+  __device__ __forceinline__ static void epilogue_lds(const GemmArgs &p, int64_t m0, int64_t n0,
+                                                      int wm, int wn, const Acc (&acc)[FM][FN],
+                                                      uint32_t lds0) {
+    typedef unsigned v2u __attribute__((ext_vector_type(2)));
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) v2u lds_v2u;
+    typedef __attribute__((address_space(3))) v4u lds_v4u;
+    const int lane = threadIdx.x & 63, t = threadIdx.x;
+    constexpr bool W32 = EPI == EPI_I32 || EPI == EPI_F32 || EPI == EPI_BLOCK128_F32 ||
+                         EPI == EPI_MX_F32; // 32-bit C
+    constexpr int ROWB = W32 ? 1024 : 512, ROWS = W32 ? 128 : 256, CH = ROWB / 16;
+    static_assert(ROWS * ROWB <= 2 * STAGE, "staged C fits the two stages");
+    static_assert(NW * 64 == 512 && BN == 256 && WTM == 128, "two staging passes split at wm");
+    __syncthreads(); // every wave is done reading the stages
+#pragma unroll
+    for (int pass = 0; pass < (W32 ? 2 : 1); ++pass) {
+      if (!W32 || wm == pass) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const int r = (W32 ? 0 : wm * WTM) + 16 * i + (lane & 15);
+          float sar = 1.f;
+          if (EPI == EPI_ROWCOL_BF16)
+            sar = p.sa[m0 + wm * WTM + 16 * i + (lane & 15)];
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            const int col = wn * WTN + 16 * j + 4 * (lane >> 4);
+            const Acc &v = acc[i][j];
+            if constexpr (W32) {
+              const int ch = col >> 2;
+              *(lds_v4u *)(uintptr_t)(lds0 + r * ROWB + ((ch ^ (r & 31)) << 4)) =
+                  __builtin_bit_cast(v4u, v);
+            } else {
+              float f[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                if (EPI == EPI_ROWCOL_BF16) {
+#pragma clang fp contract(off)
+                  f[q] = ((float)v[q] * sar) * p.sb[n0 + col + q];
+                } else {
+                  f[q] = (float)v[q];
+                }
+              }
+              const int ch = col >> 3;
+              *(lds_v2u *)(uintptr_t)(lds0 + r * ROWB + ((ch ^ (r & 31)) << 4) + (col & 7) * 2) =
+                  v2u{pk_bf16_rne(f[0], f[1]), pk_bf16_rne(f[2], f[3])};
+            }
+          }
+        }
+      }
+      __syncthreads();
+      const int64_t row0 = m0 + pass * ROWS;
+#pragma unroll 4
+      for (int q = 0; q < ROWS * CH / 512; ++q) {
+        const int idx = q * 512 + t, r = idx / CH, ch = idx % CH;
+        const v4u v = *(const lds_v4u *)(uintptr_t)(lds0 + r * ROWB + ((ch ^ (r & 31)) << 4));
+        if constexpr (W32) {
+          v4u *c = reinterpret_cast<v4u *>(reinterpret_cast<uint32_t *>(p.C) + (row0 + r) * p.ldc +
+                                           n0 + ch * 4);
+          if (p.accumulate) {
+            if constexpr (EPI == EPI_I32) {
+              *c = __builtin_bit_cast(v4u, __builtin_bit_cast(i32x4_t, *c) +
+                                               __builtin_bit_cast(i32x4_t, v));
+            } else {
+              *c = __builtin_bit_cast(v4u, __builtin_bit_cast(f32x4_t, *c) +
+                                               __builtin_bit_cast(f32x4_t, v));
+            }
+          } else {
+            *c = v;
+          }
+        } else {
+          *reinterpret_cast<v4u *>(reinterpret_cast<uint16_t *>(p.C) + (row0 + r) * p.ldc + n0 +
+                                   ch * 8) = v;
+        }
+      }
+      if (W32 && pass == 0)
+        __syncthreads(); // the first half is read out before the second is staged
+    }
   }
 
   // Lane l holds, per block (i, j), C[row][col .. col+3] with
