@@ -77,6 +77,7 @@ struct DecodeArgs {
 };
 
 typedef int v2i_t __attribute__((ext_vector_type(2)));
+typedef int v4i_t __attribute__((ext_vector_type(4))); // the buffer builtins' operand type
 typedef __attribute__((address_space(3))) v2i_t lds_v2i;
 
 __device__ __forceinline__ i32x4_t mfma_i8_16(const i32x4_t &a, const i32x4_t &b,
@@ -373,29 +374,35 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   }
 
   // Publish this split's partial ([split][M][np] int32, np = N rounded up
-  // to 4 so that every quad is 8-byte aligned), then count arrivals for the
-  // strip.  Cross-workgroup data moves only through agent-scope relaxed
-  // atomics, which gfx950 issues with the SC1 cache policy: stores write
-  // through the XCD's L2 to the device-coherent level and loads read from it,
-  // so no fence has to write back or invalidate a whole L2 (an agent-scope
-  // release/acquire fence pair costs ~40 us here).  Ordering: every thread's
-  // stores are acknowledged (s_waitcnt vmcnt(0): a store with SC1 is
-  // acknowledged once it has reached that level) before the barrier that
-  // precedes the counter increment, and the last workgroup issues its loads
-  // only after its increment has returned.
+  // to 4 so that every quad is 16-byte aligned), then count arrivals for the
+  // strip.  Cross-workgroup data moves only with the SC1 cache policy (what
+  // gfx950 gives agent-scope atomics; here on 16-byte buffer accesses, one
+  // per quad): stores write through the XCD's L2 to the device-coherent
+  // level and loads read from it, so no fence has to write back or
+  // invalidate a whole L2 (an agent-scope release/acquire fence pair costs
+  // ~40 us here).  Ordering: every thread's stores are acknowledged
+  // (s_waitcnt vmcnt(0): an SC1 store is acknowledged once it has reached
+  // that level) before the barrier that precedes the counter increment, and
+  // the last workgroup issues its loads only after its increment has
+  // returned.
+  constexpr int kSC1 = 16; // buffer cache-policy bits: SC1 (gfx940 family)
   const int64_t np = (p.N + 3) & ~3;
-  uint64_t *const mine =
-      reinterpret_cast<uint64_t *>(p.partials + ((int64_t)split * p.M + row0) * np + n0 + cq);
+  // A split's partial as a buffer resource: offsets stay below M * np * 4
+  // bytes (at most 512 MiB for M <= 256, N <= 524288).
+  auto part_rsrc = [&](int q) {
+    return __builtin_amdgcn_make_buffer_rsrc(p.partials + (int64_t)q * p.M * np, 0,
+                                             (int)(p.M * np * 4), 0x00020000);
+  };
   const bool quad_in = n0 + cq < p.N;
+  {
+    const auto mine = part_rsrc(split);
 #pragma unroll
-  for (int j = 0; j < RPT; ++j) {
-    const int m = rq + 8 * j;
-    if (m < Mr && quad_in) {
-      uint64_t *dst = mine + (int64_t)m * (np / 2);
-      __hip_atomic_store(dst, __builtin_bit_cast(uint64_t, v2i_t{wsum[j][0], wsum[j][1]}),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(dst + 1, __builtin_bit_cast(uint64_t, v2i_t{wsum[j][2], wsum[j][3]}),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int j = 0; j < RPT; ++j) {
+      const int m = rq + 8 * j;
+      if (m < Mr && quad_in)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(v4i_t, wsum[j]), mine,
+            (int)(((int64_t)(row0 + m) * np + n0 + cq) * 4), 0, kSC1);
     }
   }
   __builtin_amdgcn_s_waitcnt(0);
@@ -415,48 +422,36 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   // Last arrival: add every split's partial (its own included, stored
   // above) and apply the epilogue.  The loads are unconditional -- rows past
   // the slice and quads past N read the slice's first quad and are dropped
-  // after -- so a batch of NQ splits is issued before any value is used and
-  // the gather costs one memory round trip per batch.
+  // after -- and go out NQ splits at a time before any value is used, so the
+  // gather costs one memory round trip per NQ splits.
   i32x4_t sum[RPT];
-  int64_t off[RPT]; // in 8-byte units from split 0's partial
+  int off[RPT]; // byte offset within a split's partial
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     const int m = rq + 8 * j;
-    off[j] = (m < Mr && quad_in) ? ((int64_t)m * np + n0 + cq) / 2 : (n0 / 2);
+    off[j] = (int)((m < Mr && quad_in ? (int64_t)(row0 + m) * np + n0 + cq
+                                      : (int64_t)row0 * np + n0) * 4);
     sum[j] = i32x4_t{0, 0, 0, 0};
   }
-  const uint64_t *const part0 = reinterpret_cast<const uint64_t *>(p.partials + (int64_t)row0 * np);
-  const int64_t split_stride = (int64_t)p.M * np / 2; // 8-byte units per split
-  auto gather = [&](auto nq) {
-    constexpr int NQ = decltype(nq)::value;
-    for (int q0 = 0; q0 < p.ksplit; q0 += NQ) {
-      uint64_t v[NQ][RPT][2];
+  constexpr int NQ = 4; // NQ * RPT 16-byte loads in flight per thread (<= 32)
+  for (int q0 = 0; q0 < p.ksplit; q0 += NQ) {
+    v4i_t v[NQ][RPT];
 #pragma unroll
-      for (int qq = 0; qq < NQ; ++qq)
+    for (int qq = 0; qq < NQ; ++qq) {
+      if (q0 + qq < p.ksplit) {
+        const auto r = part_rsrc(q0 + qq);
 #pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-          const uint64_t *src = part0 + (int64_t)(q0 + qq) * split_stride + off[j];
-          v[qq][j][0] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          v[qq][j][1] = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-#pragma unroll
-      for (int qq = 0; qq < NQ; ++qq)
-#pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-          const v2i_t lo = __builtin_bit_cast(v2i_t, v[qq][j][0]);
-          const v2i_t hi = __builtin_bit_cast(v2i_t, v[qq][j][1]);
-          sum[j] += i32x4_t{lo.x, lo.y, hi.x, hi.y};
-        }
+        for (int j = 0; j < RPT; ++j)
+          v[qq][j] = __builtin_amdgcn_raw_buffer_load_b128(r, off[j], 0, kSC1);
+      }
     }
-  };
-  // Batches of up to 16 8-byte loads per thread (ksplit is a power of two >= 2).
-  constexpr int NQ = 8 / RPT >= 4 ? 4 : (8 / RPT >= 2 ? 2 : 1);
-  if (NQ >= 4 && p.ksplit >= 4)
-    gather(std::integral_constant<int, NQ>());
-  else if (NQ >= 2)
-    gather(std::integral_constant<int, 2>());
-  else
-    gather(std::integral_constant<int, 1>());
+#pragma unroll
+    for (int qq = 0; qq < NQ; ++qq)
+      if (q0 + qq < p.ksplit)
+#pragma unroll
+        for (int j = 0; j < RPT; ++j)
+          sum[j] += __builtin_bit_cast(i32x4_t, v[qq][j]);
+  }
   epilogue(sum);
 }
 
