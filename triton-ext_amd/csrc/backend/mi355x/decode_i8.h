@@ -31,9 +31,9 @@
 //    the 8 rows one transposed read touches sit in 8 different chunks.
 //  * After the K loop the 4 waves' accumulators are summed through LDS.  With
 //    split-K each workgroup writes its int32 partial to the workspace and the
-//    last workgroup of a column strip (arrival counter) adds the partials in
-//    split order and applies the epilogue.  Integer addition is exact, so the
-//    result does not depend on the order.
+//    last workgroup of a column strip (arrival counter) adds the others'
+//    partials to its own and applies the epilogue.  Integer addition is
+//    exact, so the result does not depend on the order.
 //  * Arrival counters: each workgroup of a column strip adds 1; the one that
 //    brings the counter to ksplit is the last and sets it back to zero, so a
 //    completed launch leaves every counter at zero.  The counters must be
@@ -419,11 +419,11 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   __syncthreads();
   if (!*reinterpret_cast<volatile uint32_t *>(st4))
     return;
-  // Last arrival: add every split's partial (its own included, stored
-  // above) and apply the epilogue.  The loads are unconditional -- rows past
-  // the slice and quads past N read the slice's first quad and are dropped
-  // after -- and go out NQ splits at a time before any value is used, so the
-  // gather costs one memory round trip per NQ splits.
+  // Last arrival: add the other splits' partials to its own (still in
+  // registers) and apply the epilogue.  The loads are unconditional -- rows
+  // past the slice and quads past N read the slice's first quad and are
+  // dropped after -- and go out NQ splits at a time before any value is used,
+  // so the gather costs one memory round trip per NQ splits.
   i32x4_t sum[RPT];
   int off[RPT]; // byte offset within a split's partial
 #pragma unroll
@@ -431,14 +431,14 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
     const int m = rq + 8 * j;
     off[j] = (int)((m < Mr && quad_in ? (int64_t)(row0 + m) * np + n0 + cq
                                       : (int64_t)row0 * np + n0) * 4);
-    sum[j] = i32x4_t{0, 0, 0, 0};
+    sum[j] = wsum[j];
   }
   constexpr int NQ = 4; // NQ * RPT 16-byte loads in flight per thread (<= 32)
   for (int q0 = 0; q0 < p.ksplit; q0 += NQ) {
     v4i_t v[NQ][RPT];
 #pragma unroll
     for (int qq = 0; qq < NQ; ++qq) {
-      if (q0 + qq < p.ksplit) {
+      if (q0 + qq < p.ksplit && q0 + qq != split) {
         const auto r = part_rsrc(q0 + qq);
 #pragma unroll
         for (int j = 0; j < RPT; ++j)
@@ -447,7 +447,7 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
     }
 #pragma unroll
     for (int qq = 0; qq < NQ; ++qq)
-      if (q0 + qq < p.ksplit)
+      if (q0 + qq < p.ksplit && q0 + qq != split)
 #pragma unroll
         for (int j = 0; j < RPT; ++j)
           sum[j] += __builtin_bit_cast(i32x4_t, v[qq][j]);
