@@ -493,11 +493,10 @@ extern "C" TX_API const char *tx_kernel_name(int32_t kernel) {
 extern "C" TX_API int tx_device_available(void) {
   // Per-device answer, cached: hipGetDeviceProperties is too slow to call on
   // every launch.
+  // hipGetDevice fails when no device is visible, so it is the only HIP
+  // call on a launch.
   static int cached[64];
   static std::once_flag once[64];
-  int n = 0;
-  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
-    return 0;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
     return 0;
