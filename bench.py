@@ -42,7 +42,7 @@ HBM = 8.0e12
 # WRITE x1.0 (profiles/gemm16_bf16_4096.md).
 TRAFFIC_BF16_4096 = 235.2e6
 # The same for the W8A8 M=16 decode kernel (profiles/decode_i8_w8a8_m16.md).
-TRAFFIC_W8A8_M16 = 72.9e6
+TRAFFIC_W8A8_M16 = 72.4e6
 
 
 def parse():
