@@ -91,6 +91,15 @@ class Launcher:
             raise RuntimeError(self.L.tx_get_last_error().decode())
 
 
+def plan_info(tx, p, **extra):
+    """What the planning passes chose for a line: kernel, tile and the
+    arith_intensity pass's FLOP/byte and bound."""
+    return dict(kernel=tx.load().tx_kernel_name(p.kernel).decode(),
+                tile=[p.desc.block_m, p.desc.block_n, p.desc.block_k],
+                intensity=round(p.intensity, 1),
+                bound="mfma" if p.bound == tx.BOUND_MFMA else "hbm", **extra)
+
+
 MIN_WARMUP_S = 0.1
 
 
@@ -196,10 +205,8 @@ def bench_bf16(tx, dev, M, N, K, steps, warmup, seed=1):
     p = run.plan
     return dict(workload=f"bf16 {M}x{N}x{K}", ms=ms, tflops=flops / ms / 1e9,
                 frac=flops / ms / 1e-3 / PEAK_BF16,
-                plan=dict(tile=[p.desc.block_m, p.desc.block_n, p.desc.block_k], k_split=p.k_split,
-                          k_main_steps=p.k_main_steps, k_tail=p.k_tail, m_edge=p.m_edge,
-                          n_edge=p.n_edge, intensity=round(p.intensity, 1),
-                          bound="mfma" if p.bound == tx.BOUND_MFMA else "hbm")), (a, b, c)
+                plan=plan_info(tx, p, k_split=p.k_split, k_main_steps=p.k_main_steps,
+                               k_tail=p.k_tail, m_edge=p.m_edge, n_edge=p.n_edge)), (a, b, c)
 
 
 def bench_c1(tx, dev, steps, warmup, seed=1):
@@ -217,7 +224,7 @@ def bench_c1(tx, dev, steps, warmup, seed=1):
     flops = 2.0 * M * N * K
     return dict(workload="fp16 512x512x512, BLOCK 64x64x32, fp32 C (BASELINE configs[0])", ms=ms,
                 tflops=flops / ms / 1e9, frac=flops / ms / 1e-3 / PEAK_BF16,
-                plan=dict(tile=[64, 64, 32], grid=run.plan.grid_x))
+                plan=plan_info(tx, run.plan, grid=run.plan.grid_x))
 
 
 def bench_bf16_kmajor(tx, dev, M, N, K, steps, warmup, seed=1):
@@ -231,7 +238,7 @@ def bench_bf16_kmajor(tx, dev, M, N, K, steps, warmup, seed=1):
     ms = time_back_to_back(run, steps, warmup)
     flops = 2.0 * M * N * K
     return dict(workload=f"bf16 {M}x{N}x{K}, B K-major (q @ k.T)", ms=ms, tflops=flops / ms / 1e9,
-                frac=flops / ms / 1e-3 / PEAK_BF16)
+                frac=flops / ms / 1e-3 / PEAK_BF16, plan=plan_info(tx, run.plan))
 
 
 def bench_vendor_bf16(dev, M, N, K, steps, warmup, seed=1):
@@ -264,9 +271,7 @@ def bench_w8a8(tx, dev, M, N, K, steps, warmup, flush, seed=3):
     return dict(workload=f"int8 W8A8 M={M} N={N} K={K}", ms=med, ms_isolated=iso,
                 ms_warm_mall=warm, gbps=nbytes / med / 1e6, frac_hbm=nbytes / med / 1e-3 / HBM,
                 tops=2.0 * M * N * K / med / 1e9,
-                plan=dict(kernel=tx.load().tx_kernel_name(p.kernel).decode(), split_k=p.split_k,
-                          grid=p.grid_x, intensity=round(p.intensity, 1),
-                          bound="mfma" if p.bound == tx.BOUND_MFMA else "hbm"))
+                plan=plan_info(tx, p, split_k=p.split_k, grid=p.grid_x))
 
 
 def bench_fp8(tx, dev, M, N, K, steps, warmup, seed=5):
@@ -285,7 +290,7 @@ def bench_fp8(tx, dev, M, N, K, steps, warmup, seed=5):
     ms = time_back_to_back(run, steps, warmup)
     flops = 2.0 * M * N * K
     return dict(workload=f"fp8 e4m3 block-scaled {M}x{N}x{K}", ms=ms, tflops=flops / ms / 1e9,
-                frac=flops / ms / 1e-3 / PEAK_I8)
+                frac=flops / ms / 1e-3 / PEAK_I8, plan=plan_info(tx, run.plan))
 
 
 def mx_quantize(x, fmt):
@@ -335,8 +340,7 @@ def bench_mx(tx, dev, M, N, K, fmt, steps, warmup, seed=7):
     name = "mxfp8 e4m3" if fmt == "e4m3" else "mxfp4 e2m1"
     return dict(workload=f"tl.dot_scaled {name} (e8m0 per 32) {M}x{N}x{K}, fp32 C", ms=ms,
                 tflops=flops / ms / 1e9, frac=flops / ms / 1e-3 / peak, peak_tflops=peak / 1e12,
-                plan=dict(kernel=L.tx_kernel_name(p.kernel).decode(),
-                          tile=[p.desc.block_m, p.desc.block_n, p.desc.block_k]))
+                plan=plan_info(tx, p))
 
 
 def bench_mx_bf16(tx, dev, M, N, K, fmt, steps, warmup, seed=8):
@@ -365,9 +369,7 @@ def bench_mx_bf16(tx, dev, M, N, K, fmt, steps, warmup, seed=8):
     name = "mxfp8 e4m3" if fmt == "e4m3" else "mxfp4 e2m1"
     return dict(workload=f"tl.dot_scaled bf16 x {name} (upcast + bf16 tile) {M}x{N}x{K}, "
                          f"fp32 C", ms=ms, tflops=flops / ms / 1e9,
-                frac=flops / ms / 1e-3 / PEAK_BF16,
-                plan=dict(kernel=L.tx_kernel_name(p.kernel).decode(),
-                          tile=[p.desc.block_m, p.desc.block_n, p.desc.block_k]))
+                frac=flops / ms / 1e-3 / PEAK_BF16, plan=plan_info(tx, p))
 
 
 def bench_attn(tx, dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9, dtype=None):
@@ -436,7 +438,7 @@ def bench_int8(tx, dev, M, N, K, steps, warmup, seed=4):
     ms = time_back_to_back(run, steps, warmup)
     ops = 2.0 * M * N * K
     return dict(workload=f"int8 {M}x{N}x{K}, int32 C", ms=ms, tops=ops / ms / 1e9,
-                frac=ops / ms / 1e-3 / PEAK_I8)
+                frac=ops / ms / 1e-3 / PEAK_I8, plan=plan_info(tx, run.plan))
 
 
 def ceilings_lib():
@@ -503,20 +505,22 @@ def bench_tiles(tx, dev, steps, warmup):
     a, b = bf16_inputs(M, N, K, dev, 11)
     c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     for blk in ((256, 256, 64), (128, 128, 64), (64, 64, 32)):
-        ms = time_back_to_back(Launcher(tx, a, b, c, block=blk), steps, warmup)
+        run = Launcher(tx, a, b, c, block=blk)
+        ms = time_back_to_back(run, steps, warmup)
         rows.append(dict(workload=f"tile {blk[0]}x{blk[1]}x{blk[2]} bf16 4096^3", tile=list(blk),
                          ms=ms, tflops=2.0 * M * N * K / ms / 1e9,
-                         frac=2.0 * M * N * K / ms / 1e-3 / PEAK_BF16))
+                         frac=2.0 * M * N * K / ms / 1e-3 / PEAK_BF16, plan=plan_info(tx, run.plan)))
     g = torch.Generator(device=dev)
     g.manual_seed(12)
     ai = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
     bi = torch.randint(-127, 128, (K, N), generator=g, device=dev, dtype=torch.int8)
     ci = torch.empty((M, N), dtype=torch.int32, device=dev)
     for blk in ((256, 256, 128), (256, 224, 128), (128, 128, 128)):
-        ms = time_back_to_back(Launcher(tx, ai, bi, ci, block=blk), steps, warmup)
+        run = Launcher(tx, ai, bi, ci, block=blk)
+        ms = time_back_to_back(run, steps, warmup)
         rows.append(dict(workload=f"tile {blk[0]}x{blk[1]}x{blk[2]} int8 4096^3", tile=list(blk),
                          ms=ms, tops=2.0 * M * N * K / ms / 1e9,
-                         frac=2.0 * M * N * K / ms / 1e-3 / PEAK_I8))
+                         frac=2.0 * M * N * K / ms / 1e-3 / PEAK_I8, plan=plan_info(tx, run.plan)))
     return rows
 
 
@@ -709,7 +713,8 @@ def main():
         "data": "synthetic (torch.randn / sqrt(K), seed 1, rounded to bf16)",
         "config": {"workload": "bf16 dense dot C=A@B, M=N=K=4096, row-major A[M,K], B[K,N], "
                                "fp32 accumulate, bf16 out (BASELINE configs[1])",
-                   "tile": head["plan"]["tile"], "kernel": "gemm16_w4_kernel<bf16, 4 waves of 128x128>"},
+                   "tile": head["plan"]["tile"], "kernel": "gemm16_w4_kernel<bf16, 4 waves of 128x128>",
+                   "intensity": head["plan"]["intensity"], "classified": head["plan"]["bound"]},
         "roofline": {"bound": "mfma", "achieved": round(flops / head["ms"] / 1e9, 2),
                      "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(head["frac"], 4),
                      "traffic": TRAFFIC_BF16_4096},
