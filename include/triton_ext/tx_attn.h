@@ -58,7 +58,13 @@ typedef struct tx_attn_desc {
   int64_t k_sz, k_sh, k_sm;
   int64_t v_sz, v_sh, v_sm;
   int64_t o_sz, o_sh, o_sm;
-  int32_t block_m, block_n; /* 0 = default (128, 64) */
+  /* BLOCK_M x BLOCK_N, one of the tutorial's autotuned configs
+   * (R:pass/LoopSplit/06-fused-attention.py:145-159): BLOCK_M 64 or 128 by
+   * BLOCK_N 32 or 64 (fp8 e5m2: BLOCK_N 64); 0 = default (128, 64).  The
+   * blocks fix the on-band split (causal_start = start_m * BLOCK_M) and the
+   * online softmax's key blocks, so they select the rounding of the result
+   * exactly as the tutorial's config does. */
+  int32_t block_m, block_n;
 } tx_attn_desc;
 
 typedef struct tx_attn_plan {
@@ -72,9 +78,10 @@ typedef struct tx_attn_plan {
 } tx_attn_plan;
 
 /* Validate `desc` and fill `plan`.  TX_ERR_UNSUPPORTED unless head_dim is
- * 64 or 128, dtype TX_F16, TX_BF16 or TX_F8E5M2 and N_CTX a multiple of 128 (the
- * tutorial's block pointers assume whole blocks).  p is rounded to q's type
- * to nearest even before p @ v, as compiled Triton does. */
+ * 64 or 128, dtype TX_F16, TX_BF16 or TX_F8E5M2, the blocks one of the
+ * implemented configs and N_CTX a multiple of BLOCK_M (the tutorial's block
+ * pointers assume whole blocks).  p is rounded to q's type to nearest even
+ * before p @ v, as compiled Triton does. */
 TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *plan);
 
 /* Enqueue the forward on `stream` (a hipStream_t, NULL = null stream). */

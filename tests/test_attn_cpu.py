@@ -244,7 +244,19 @@ def test_attn_plan():
     assert err(N_CTX=200) == tx.ERR_UNSUPPORTED
     assert err(dtype=tx.F32) == tx.ERR_UNSUPPORTED
     assert tx.attn_plan(1, 1, 256, 128, True, 0.5, dtype=tx.BF16).desc.head_dim == 128
-    assert err(block=(64, 32)) == tx.ERR_UNSUPPORTED
+    # the tutorial's autotuned blocks: BLOCK_M 64 / 128 by BLOCK_N 32 / 64, a
+    # wave per 32 query rows; N_CTX in whole BLOCK_M blocks
+    for bm, bn in ((128, 64), (128, 32), (64, 64), (64, 32)):
+        p = tx.attn_plan(1, 2, 192 if bm == 64 else 256, 64, True, 0.5, block=(bm, bn))
+        assert (p.desc.block_m, p.desc.block_n) == (bm, bn)
+        assert p.block_threads == bm // 32 * 64 and p.m_blocks == p.desc.N_CTX // bm
+        assert p.grid_x == 2 * p.m_blocks
+    assert err(N_CTX=192) == tx.ERR_UNSUPPORTED              # 128 rows per block by default
+    assert err(N_CTX=192, block=(128, 32)) == tx.ERR_UNSUPPORTED
+    for blk in ((256, 64), (64, 16), (32, 32), (128, 128)):
+        assert err(block=blk) == tx.ERR_UNSUPPORTED
+    assert err(dtype=tx.F8E5M2, block=(64, 32)) == tx.ERR_UNSUPPORTED  # fp8: BLOCK_N 64
+    assert tx.attn_plan(1, 1, 64, 64, False, 0.5, dtype=tx.F8E5M2, block=(64, 64)).grid_x == 1
     assert err(Z=-1) == tx.ERR_INVALID
     # e5m2: one byte per element, v key-contiguous ([HEAD_DIM][N_CTX] per head)
     p8 = tx.attn_plan(4, 32, 4096, 64, False, 1.3, dtype=tx.F8E5M2)

@@ -27,7 +27,7 @@ def rand_qkv(Z, H, N, D, seed, std=0.5):
             for _ in range(3)]
 
 
-def run_gpu(gpu, q, k, v, causal, sm_scale, layout="bhnd"):
+def run_gpu(gpu, q, k, v, causal, sm_scale, layout="bhnd", block=(0, 0)):
     import torch
     ts = []
     for x in (q, k, v):
@@ -35,7 +35,7 @@ def run_gpu(gpu, q, k, v, causal, sm_scale, layout="bhnd"):
         if layout == "bnhd":  # storage [Z, N, H, D], viewed as [Z, H, N, D]
             t = t.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
         ts.append(t)
-    o, M = tx.attention(*ts, causal, sm_scale, return_lse=True)
+    o, M = tx.attention(*ts, causal, sm_scale, return_lse=True, block=block)
     torch.cuda.synchronize()
     return from_device(o.contiguous().view(torch.int16)).view(np.uint16), from_device(M)
 
@@ -82,12 +82,51 @@ def test_attn_vs_oracle(gpu, causal, Z, H, N, sm_scale, layout):
     check(o, M, ro, rM, f"attn {Z}x{H}x{N} causal={causal} {layout}")
 
 
+@pytest.mark.parametrize("own_block", [False, True])
 @pytest.mark.parametrize("name", ["attn_fwd_causal", "attn_fwd_plain"])
-def test_golden_fixture_attn(gpu, name):
-    say(f"golden {name}")
+def test_golden_fixture_attn(gpu, name, own_block):
+    """The interpreter's fixtures (written with BLOCK 64 x 32) on the default
+    128 x 64 kernel and on the fixture's own block shape."""
     z = np.load(os.path.join(GOLDEN, name + ".npz"), allow_pickle=False)
-    o, M = run_gpu(gpu, z["q"], z["k"], z["v"], bool(z["causal"]), float(z["sm_scale"]))
-    check(o, M, z["o"], z["M"], f"golden {name}")
+    block = tuple(int(x) for x in z["block"]) if own_block else (0, 0)
+    say(f"golden {name} block={block}")
+    o, M = run_gpu(gpu, z["q"], z["k"], z["v"], bool(z["causal"]), float(z["sm_scale"]),
+                   block=block)
+    check(o, M, z["o"], z["M"], f"golden {name} block={block}")
+
+
+@pytest.mark.parametrize("block", [(128, 32), (64, 64), (64, 32)])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("Z,H,N,D,bf16", [(1, 2, 64, 64, False), (2, 3, 192, 64, False),
+                                          (1, 2, 320, 128, False), (1, 2, 256, 64, True),
+                                          (1, 1, 128, 128, True)])
+def test_attn_blocks_vs_oracle(gpu, block, causal, Z, H, N, D, bf16):
+    """The tutorial's other autotuned blocks (BLOCK_M 64 / 128 by BLOCK_N 32 /
+    64) against the oracle run with the same blocks.  N_CTX = 64, 192, 320
+    give odd block counts in both loop segments at BLOCK_M 64."""
+    import torch
+    if N % block[0]:
+        pytest.skip("N_CTX is not a whole number of BLOCK_M blocks")
+    say(f"attn block={block} Z={Z} H={H} N={N} D={D} bf16={bf16} causal={causal}")
+    rng = np.random.default_rng(N * 3 + D + causal + bf16 + block[0] + block[1])
+    tdt = torch.bfloat16 if bf16 else torch.float16
+    bits = [torch.from_numpy((rng.standard_normal((Z, H, N, D)) * 0.5).astype(np.float32))
+            .to(tdt).view(torch.int16).numpy().view(np.uint16) for _ in range(3)]
+    ts = [to_device(b, gpu).view(torch.int16).view(tdt) for b in bits]
+    o, M = tx.attention(*ts, causal, 0.6, return_lse=True, block=block)
+    torch.cuda.synchronize()
+    got = from_device(o.contiguous().view(torch.int16)).view(np.uint16)
+    ro, rM = oracle.attn_fwd(*bits, sm_scale=0.6, causal=causal, block=block,
+                             dtype=oracle.BF16 if bf16 else oracle.F16)
+    dec = (lambda x: oracle.bf16_to_f32(x).astype(np.float64)) if bf16 else \
+        (lambda x: x.view(np.float16).astype(np.float64))
+    d = np.abs(dec(got) - dec(ro))
+    tol = 2.0 ** -6 if bf16 else 2.0 ** -8
+    assert np.isfinite(dec(got)).all()
+    assert d.max() <= tol, f"max |d o| {d.max():.3g}"
+    dm = np.abs(from_device(M).reshape(rM.shape).astype(np.float64) - rM)
+    assert dm.max() <= 1e-4 * max(1.0, np.abs(rM).max()), f"max |d M| {dm.max():.3g}"
+    say(f"attn block={block}: max|d o|={d.max():.3g} identical={np.mean(got == ro):.3f}")
 
 
 @pytest.mark.parametrize("causal", [True, False])
@@ -156,7 +195,7 @@ def e5m2_qkv(Z, H, N, D, seed, std=1.0):
             .to(torch.float8_e5m2).view(torch.uint8).numpy() for _ in range(3)]
 
 
-def run_gpu_fp8(gpu, q, k, v, causal, sm_scale):
+def run_gpu_fp8(gpu, q, k, v, causal, sm_scale, block=(0, 0)):
     """q, k head-dim contiguous; v stored key-contiguous and viewed as
     [Z, H, N, D], as the tutorial's v.permute(0, 1, 3, 2).contiguous()
     .permute(0, 1, 3, 2) leaves it."""
@@ -165,7 +204,7 @@ def run_gpu_fp8(gpu, q, k, v, causal, sm_scale):
     vt = to_device(np.ascontiguousarray(v.transpose(0, 1, 3, 2)), gpu).view(torch.float8_e5m2)
     vt = vt.permute(0, 1, 3, 2)
     assert vt.stride(2) == 1
-    o, M = tx.attention(qt, kt, vt, causal, sm_scale, return_lse=True)
+    o, M = tx.attention(qt, kt, vt, causal, sm_scale, return_lse=True, block=block)
     torch.cuda.synchronize()
     assert o.dtype == torch.float8_e5m2
     return o.view(torch.uint8).cpu().numpy(), from_device(M)
@@ -224,6 +263,19 @@ def test_attn_fp8_vs_oracle(gpu, causal, Z, H, N, D, sm_scale):
                              dtype=oracle.F8E5M2)
     check_e5m2(o, M, ro, rM, (q, k, v), sm_scale, causal,
                f"attn fp8 {Z}x{H}x{N} D={D} causal={causal}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("Z,H,N,D", [(1, 2, 64, 64), (2, 3, 192, 64), (1, 2, 320, 128)])
+def test_attn_fp8_block_m64(gpu, causal, Z, H, N, D):
+    """fp8 e5m2 with BLOCK_M 64 (two waves), against the oracle at 64 x 64."""
+    say(f"attn fp8 block=(64, 64) Z={Z} H={H} N={N} D={D} causal={causal}")
+    q, k, v = e5m2_qkv(Z, H, N, D, seed=Z * 100 + H * 10 + N + D + causal + 7)
+    o, M = run_gpu_fp8(gpu, q, k, v, causal, 0.7, block=(64, 64))
+    ro, rM = oracle.attn_fwd(q, k, v, sm_scale=0.7, causal=causal, block=(64, 64),
+                             dtype=oracle.F8E5M2)
+    check_e5m2(o, M, ro, rM, (q, k, v), 0.7, causal,
+               f"attn fp8 block 64x64 {Z}x{H}x{N} D={D} causal={causal}")
 
 
 @pytest.mark.parametrize("causal", [True, False])

@@ -879,17 +879,18 @@ extern "C" TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *p
     return fail(TX_ERR_INVALID, "causal must be 0 or 1");
   if (!(d.sm_scale == d.sm_scale))
     return fail(TX_ERR_INVALID, "sm_scale is NaN");
-  typedef txk::AttnFwd<64, false> AF; // block shape (the same for every head dim)
   if (d.head_dim != 64 && d.head_dim != 128)
     return fail(TX_ERR_UNSUPPORTED, "head_dim %d: 64 and 128 are implemented", d.head_dim);
   if (d.dtype != TX_F16 && d.dtype != TX_BF16 && d.dtype != TX_F8E5M2)
     return fail(TX_ERR_UNSUPPORTED, "dtype %d: fp16, bf16 and fp8 e5m2 q/k/v/o are implemented",
                 d.dtype);
-  if (d.block_m == 0) d.block_m = AF::BM;
-  if (d.block_n == 0) d.block_n = AF::BN;
-  if (d.block_m != AF::BM || d.block_n != AF::BN)
-    return fail(TX_ERR_UNSUPPORTED, "blocks %dx%d: 128x64 is implemented", d.block_m,
-                d.block_n);
+  if (d.block_m == 0) d.block_m = 128;
+  if (d.block_n == 0) d.block_n = 64;
+  if ((d.block_m != 64 && d.block_m != 128) || (d.block_n != 32 && d.block_n != 64))
+    return fail(TX_ERR_UNSUPPORTED, "blocks %dx%d: BLOCK_M 64 or 128 by BLOCK_N 32 or 64 "
+                "are implemented", d.block_m, d.block_n);
+  if (d.dtype == TX_F8E5M2 && d.block_n != 64)
+    return fail(TX_ERR_UNSUPPORTED, "fp8 e5m2 attention: BLOCK_N 64 is implemented");
   if (d.N_CTX % d.block_m)
     return fail(TX_ERR_UNSUPPORTED, "N_CTX %lld is not a multiple of %d (whole blocks only)",
                 (long long)d.N_CTX, d.block_m);
@@ -911,7 +912,7 @@ extern "C" TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *p
   plan->qk_scale = d.sm_scale * 1.44269504f; // qk_scale = sm_scale; qk_scale *= 1.44269504
   plan->m_blocks = (int32_t)(d.N_CTX / d.block_m);
   plan->grid_x = (int32_t)programs;
-  plan->block_threads = AF::NW * 64;
+  plan->block_threads = d.block_m / 32 * 64; // one wave per 32 query rows
   return TX_OK;
 }
 
@@ -929,10 +930,11 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
        reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o)) & 15 ||
       reinterpret_cast<uintptr_t>(M) & 3)
     return fail(TX_ERR_INVALID, "q, k, v, o must be 16-byte aligned and M 4-byte aligned");
-  typedef txk::AttnFwd<64, false> AF;
-  if (plan->block_threads != AF::NW * 64 || d.block_m != AF::BM || d.block_n != AF::BN ||
+  const bool bm64 = d.block_m == 64, bn32 = d.block_n == 32;
+  if ((d.block_m != 64 && d.block_m != 128) || (d.block_n != 32 && d.block_n != 64) ||
+      (d.dtype == TX_F8E5M2 && bn32) || plan->block_threads != d.block_m / 32 * 64 ||
       (d.head_dim != 64 && d.head_dim != 128) ||
-      (d.dtype != TX_F16 && d.dtype != TX_BF16 && d.dtype != TX_F8E5M2) ||
+      (d.dtype != TX_F16 && d.dtype != TX_BF16 && d.dtype != TX_F8E5M2) || d.N_CTX % d.block_m ||
       plan->m_blocks != d.N_CTX / d.block_m || plan->grid_x != d.Z * d.H * plan->m_blocks)
     return fail(TX_ERR_INVALID, "plan launch shape does not match the attention kernel");
   if (!tx_device_available())
@@ -952,19 +954,25 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
   a.qk_scale = plan->qk_scale;
   hipStream_t s = static_cast<hipStream_t>(stream);
   typedef void (*AttnFn)(txk::AttnArgs);
-  // [causal][head_dim 128][bf16]
-  static const AttnFn kAttn[2][2][2] = {
-      {{txk::attn_fwd_kernel<false, 64, false>, txk::attn_fwd_kernel<false, 64, true>},
-       {txk::attn_fwd_kernel<false, 128, false>, txk::attn_fwd_kernel<false, 128, true>}},
-      {{txk::attn_fwd_kernel<true, 64, false>, txk::attn_fwd_kernel<true, 64, true>},
-       {txk::attn_fwd_kernel<true, 128, false>, txk::attn_fwd_kernel<true, 128, true>}}};
-  // [causal][head_dim 128]
-  static const AttnFn kAttn8[2][2] = {
-      {txk::attn_fwd8_kernel<false, 64>, txk::attn_fwd8_kernel<false, 128>},
-      {txk::attn_fwd8_kernel<true, 64>, txk::attn_fwd8_kernel<true, 128>}};
-  const AttnFn fn = d.dtype == TX_F8E5M2
-                        ? kAttn8[d.causal ? 1 : 0][d.head_dim == 128]
-                        : kAttn[d.causal ? 1 : 0][d.head_dim == 128][d.dtype == TX_BF16];
+#define TX_ATTN_BLOCKS(C, HD, BF)                                                          \
+  {{txk::attn_fwd_kernel<C, HD, BF, 128, 64>, txk::attn_fwd_kernel<C, HD, BF, 128, 32>},  \
+   {txk::attn_fwd_kernel<C, HD, BF, 64, 64>, txk::attn_fwd_kernel<C, HD, BF, 64, 32>}}
+  // [causal][head_dim 128][bf16][BLOCK_M 64][BLOCK_N 32]
+  static const AttnFn kAttn[2][2][2][2][2] = {
+      {{TX_ATTN_BLOCKS(false, 64, false), TX_ATTN_BLOCKS(false, 64, true)},
+       {TX_ATTN_BLOCKS(false, 128, false), TX_ATTN_BLOCKS(false, 128, true)}},
+      {{TX_ATTN_BLOCKS(true, 64, false), TX_ATTN_BLOCKS(true, 64, true)},
+       {TX_ATTN_BLOCKS(true, 128, false), TX_ATTN_BLOCKS(true, 128, true)}}};
+#undef TX_ATTN_BLOCKS
+  // [causal][head_dim 128][BLOCK_M 64]
+  static const AttnFn kAttn8[2][2][2] = {
+      {{txk::attn_fwd8_kernel<false, 64, 128>, txk::attn_fwd8_kernel<false, 64, 64>},
+       {txk::attn_fwd8_kernel<false, 128, 128>, txk::attn_fwd8_kernel<false, 128, 64>}},
+      {{txk::attn_fwd8_kernel<true, 64, 128>, txk::attn_fwd8_kernel<true, 64, 64>},
+       {txk::attn_fwd8_kernel<true, 128, 128>, txk::attn_fwd8_kernel<true, 128, 64>}}};
+  const int c = d.causal ? 1 : 0, h = d.head_dim == 128;
+  const AttnFn fn = d.dtype == TX_F8E5M2 ? kAttn8[c][h][bm64]
+                                         : kAttn[c][h][d.dtype == TX_BF16][bm64][bn32];
   hipLaunchKernelGGL(fn, dim3(plan->grid_x), dim3(plan->block_threads), 0, s, a);
   TX_HIP_CHECK(hipGetLastError());
   return TX_OK;

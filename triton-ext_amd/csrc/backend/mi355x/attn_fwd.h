@@ -3,8 +3,9 @@
 // (the tutorial's type) or bf16 q/k/v/o, HEAD_DIM 64 or 128, fp32 softmax
 // statistics and accumulator.
 //
-// A workgroup owns BM = 128 query rows of one (z, h): four waves of 32 rows.
-// Per K/V block of BN = 64 keys:
+// A workgroup owns BM query rows of one (z, h), one wave per 32 rows; BM x
+// BN is any of the tutorial's autotuned blocks (64 or 128 by 32 or 64, 128 x
+// 64 by default).  Per K/V block of BN keys:
 //   S^T = K . Q^T    32x32x16 f16 MFMAs, A := K rows (LDS), B := Q rows (held
 //                    in registers for the whole loop), so lane l holds query
 //                    row m = l%32 and keys n = 8 (r/4) + 4 (l/32) + r%4 of each
@@ -47,14 +48,18 @@ struct AttnArgs {
   float qk_scale;
 };
 
-template <int HD, bool BF> struct AttnFwd {
-  static constexpr int BM = 128, BN = 64, D = HD, NW = 4, ESZ = 2;
+// BM_ x BN_: the tutorial's autotuned block space, BLOCK_M in {64, 128} (one
+// wave per 32 query rows) and BLOCK_N in {32, 64}.
+template <int HD, bool BF, int BM_ = 128, int BN_ = 64> struct AttnFwd {
+  static constexpr int BM = BM_, BN = BN_, D = HD, NW = BM_ / 32, ESZ = 2;
   static constexpr int ROW = D * 2;            // bytes per K/V row
-  static constexpr int TILE = BN * ROW;        // 8 / 16 KiB
-  static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 2 / 4
+  static constexpr int TILE = BN * ROW;        // 4 / 8 / 16 KiB
+  static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 1 .. 8
   static constexpr int CPR = ROW / 16;         // 16-byte chunks per row: 8 / 16
   static constexpr uint32_t kOOB = 0x80000000u;
   static_assert(D == 64 || D == 128, "head dims 64 and 128");
+  static_assert((BM == 64 || BM == 128) && (BN == 32 || BN == 64), "the tutorial's blocks");
+  static_assert(DMA >= 1 && DMA * NW * 1024 == TILE, "whole 1 KiB loads per wave");
   // 16-bit element vectors; BF: bf16, else fp16
   typedef typename std::conditional<BF, __bf16, _Float16>::type elt;
   typedef elt h8 __attribute__((ext_vector_type(8)));
@@ -321,8 +326,9 @@ template <int HD, bool BF> struct AttnFwd {
 // P_j V_j.  K and V have two LDS slots each, K one block ahead of V:
 // iteration j first issues the loads of K_{j+2} (into K_j's slot) and
 // V_{j+1} (into V_{j-1}'s slot), and its closing barrier makes them visible.
-// Block j uses K slot j%2 and V slot j%2; the loop advances two blocks per
-// trip so that slots are constants (both segments have even trip counts).
+// Block j uses K slot j%2 and V slot j%2, a template constant: each segment
+// runs in pairs of iterations, with a single one first when it starts at an
+// odd block and last when it ends at one.
 // A: the element type's fragments (AttnFwd<HD, BF> here, AttnFwd8<HD> for
 // e5m2).
 template <bool CAUSAL, class A> __device__ __forceinline__ void attn_fwd_body(const AttnArgs &p) {
@@ -354,7 +360,7 @@ template <bool CAUSAL, class A> __device__ __forceinline__ void attn_fwd_body(co
 
   // LoopSplit form of the K/V loop (keys [0, N_CTX), predicate start_n >=
   // causal_start): unmasked blocks [0, n_main), masked [n_main, n_end).
-  // Both counts are even (N_CTX and causal_start are multiples of 2 BN).
+  // N_CTX and causal_start are multiples of BM, itself a multiple of BN.
   const int causal_start = CAUSAL ? start_m * A::BM : p.N_CTX;
   const int n_main = causal_start / A::BN;
   const int n_end = CAUSAL ? (causal_start + A::BM) / A::BN : n_main;
@@ -367,8 +373,9 @@ template <bool CAUSAL, class A> __device__ __forceinline__ void attn_fwd_body(co
 
   A::issue_k(rk, ko, p.k_sm, 0, k_lds, wave);
   A::issue_v(rv, vo, p.v_sm, 0, v_lds, wave);
-  A::issue_k(rk, ko, p.k_sm, 1, k_lds + A::TILE, wave); // n_end >= 2
-  __builtin_amdgcn_s_waitcnt(0x7 << 4);                 // vmcnt(0)
+  if (n_end > 1)
+    A::issue_k(rk, ko, p.k_sm, 1, k_lds + A::TILE, wave);
+  __builtin_amdgcn_s_waitcnt(0x7 << 4); // vmcnt(0)
   __syncthreads();
   A::template qk<0>(bs, qf, s);
   __syncthreads(); // K slot 0 is refilled by iteration 0
@@ -397,14 +404,20 @@ template <bool CAUSAL, class A> __device__ __forceinline__ void attn_fwd_body(co
     __builtin_amdgcn_s_waitcnt(0x7 << 4); // vmcnt(0): this wave's loads of K_{j+2}, V_{j+1}
     __syncthreads();
   };
-  for (int j = 0; j < n_main; j += 2) {
-    iter(j, std::false_type(), std::integral_constant<int, 0>());
-    iter(j + 1, std::false_type(), std::integral_constant<int, 1>());
-  }
-  for (int j = n_main; j < n_end; j += 2) {
-    iter(j, std::true_type(), std::integral_constant<int, 0>());
-    iter(j + 1, std::true_type(), std::integral_constant<int, 1>());
-  }
+  auto segment = [&](int j, int j_end, auto mask) {
+    if (j < j_end && (j & 1)) {
+      iter(j, mask, std::integral_constant<int, 1>());
+      ++j;
+    }
+    for (; j + 1 < j_end; j += 2) {
+      iter(j, mask, std::integral_constant<int, 0>());
+      iter(j + 1, mask, std::integral_constant<int, 1>());
+    }
+    if (j < j_end)
+      iter(j, mask, std::integral_constant<int, 0>());
+  };
+  segment(0, n_main, std::false_type());
+  segment(n_main, n_end, std::true_type());
 
   // Epilogue: M = m_i + log2(l_i); O = acc / l_i.
   A::store_o(acc, l_i,
@@ -414,9 +427,9 @@ template <bool CAUSAL, class A> __device__ __forceinline__ void attn_fwd_body(co
     p.M[(int64_t)hz * p.N_CTX + m] = m_i + __builtin_log2f(l_i);
 }
 
-template <bool CAUSAL, int HD, bool BF>
-__global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs p) {
-  attn_fwd_body<CAUSAL, AttnFwd<HD, BF>>(p);
+template <bool CAUSAL, int HD, bool BF, int BM = 128, int BN = 64>
+__global__ void __launch_bounds__(BM * 2, 2) attn_fwd_kernel(AttnArgs p) {
+  attn_fwd_body<CAUSAL, AttnFwd<HD, BF, BM, BN>>(p);
 }
 
 } // namespace txk

@@ -5,7 +5,7 @@
 // accumulator.  The pipeline, split and program order are attn_fwd_body's
 // (attn_fwd.h); this file holds the element type's fragments.
 //
-// Per K/V block of BN = 64 keys and wave of 32 query rows:
+// Per K/V block of BN = 64 keys and wave of 32 query rows (BM / 32 waves):
 //   S^T = K . Q^T    v_mfma_f32_32x32x64_f8f6f4 (e5m2 x e5m2), one per 32
 //                    keys and 64 dims.  Lane l feeds A row l%32 with key
 //                    pi(l%32), pi(8i + 4g + j) = 16g + 4i + j, so the S^T
@@ -33,12 +33,15 @@
 
 namespace txk {
 
-template <int HD> struct AttnFwd8 {
-  static constexpr int BM = 128, BN = 64, D = HD, NW = 4, ESZ = 1;
+// BM_: BLOCK_M 64 or 128 (one wave per 32 query rows).  BLOCK_N is 64: the
+// P V MFMA takes the block's 64 keys at once.
+template <int HD, int BM_ = 128> struct AttnFwd8 {
+  static constexpr int BM = BM_, BN = 64, D = HD, NW = BM_ / 32, ESZ = 1;
   static constexpr int TILE = BN * D;          // K: BN x D bytes; V^T: D x BN bytes
-  static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 1 / 2
+  static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 1 .. 4
   static constexpr int KCPR = D / 16;          // K: 16-byte chunks per row
   static_assert(D == 64 || D == 128, "head dims 64 and 128");
+  static_assert(BM == 64 || BM == 128, "the tutorial's BLOCK_M");
   typedef float f16v __attribute__((ext_vector_type(16)));
 
   __device__ __forceinline__ static f16v mfma(const i32x8_t &a, const i32x8_t &b,
@@ -271,9 +274,9 @@ template <int HD> struct AttnFwd8 {
   }
 };
 
-template <bool CAUSAL, int HD>
-__global__ void __launch_bounds__(256, 2) attn_fwd8_kernel(AttnArgs p) {
-  attn_fwd_body<CAUSAL, AttnFwd8<HD>>(p);
+template <bool CAUSAL, int HD, int BM = 128>
+__global__ void __launch_bounds__(BM * 2, 2) attn_fwd8_kernel(AttnArgs p) {
+  attn_fwd_body<CAUSAL, AttnFwd8<HD, BM>>(p);
 }
 
 } // namespace txk

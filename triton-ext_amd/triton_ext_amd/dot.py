@@ -320,7 +320,7 @@ def _upcast_workspace(p, device, stream):
     return ws
 
 
-def attention(q, k, v, causal, sm_scale, return_lse=False, plan=None, stream=None):
+def attention(q, k, v, causal, sm_scale, return_lse=False, plan=None, stream=None, block=(0, 0)):
     """Forward of the fused-attention tutorial's `attention(q, k, v, causal,
     sm_scale)` (R:pass/LoopSplit/06-fused-attention.py:583-640) on the
     MI355X kernel: q, k, v [Z, H, N_CTX, HEAD_DIM], head dim 64 or 128, in
@@ -330,7 +330,9 @@ def attention(q, k, v, causal, sm_scale, return_lse=False, plan=None, stream=Non
     transposed", :586).  o has q's type; p is rounded to it before p @ v
     (:81-84).  Returns o (and M, the base-2 logsumexp [Z, H, N_CTX] the
     tutorial saves for its backward, with return_lse=True).  Shape checks
-    follow the tutorial's asserts.
+    follow the tutorial's asserts.  block = (BLOCK_M, BLOCK_N), one of the
+    tutorial's autotuned configs (:145-159): BLOCK_M 64 or 128 by BLOCK_N 32
+    or 64 (fp8: 64); (0, 0) takes 128 x 64.
     """
     import torch
     if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
@@ -360,7 +362,8 @@ def attention(q, k, v, causal, sm_scale, return_lse=False, plan=None, stream=Non
         if fp8:
             st["v"] = (v.stride(0), v.stride(1), v.stride(3))  # dim rows of N_CTX keys
         dt = capi.F8E5M2 if fp8 else capi.BF16 if q.dtype == torch.bfloat16 else capi.F16
-        plan = capi.attn_plan(Z, H, N, HEAD_DIM, causal, sm_scale, dtype=dt, strides=st)
+        plan = capi.attn_plan(Z, H, N, HEAD_DIM, causal, sm_scale, dtype=dt, strides=st,
+                              block=block)
     if stream is None:
         stream = torch.cuda.current_stream(q.device).cuda_stream
     capi.check(capi.load().tx_attn_fwd_launch(ctypes.byref(plan), q.data_ptr(), k.data_ptr(),
