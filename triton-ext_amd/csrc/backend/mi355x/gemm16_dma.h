@@ -10,8 +10,9 @@
 //     pc = c ^ ((row ^ row >> 3) & (chunks - 1)), so the MFMA A reads
 //     (32 consecutive rows, one chunk, ds_read_b128) spread over all banks.
 //   B tile [BK][BN], N-contiguous rows as in global memory; physical chunk
-//     pc = c ^ (4 * (k & 3)) (BN >= 128), so the transpose reads below,
-//     which touch 4 consecutive rows, land on distinct banks.
+//     pc = c ^ (BSW * (k & 3)), BSW = 4 for rows of 16 chunks or more
+//     (BN >= 128) and 2 for BN = 64, so the transpose reads below, which
+//     touch 4 consecutive rows, land on distinct banks.
 // Lanes whose chunk lies outside the matrix (K tail, M/N edges) fetch from a
 // zero-filled device buffer instead, which is the tl.load(mask, other=0) of the
 // reference kernel.  A chunk that crosses K or N (K and N need not fill whole
@@ -93,6 +94,7 @@ struct Gemm16Dma {
   static constexpr int NW = WM * WN;
   static constexpr int RA = BK * 2, NCA = RA / 16;   // A row bytes, chunks
   static constexpr int RBB = BN * 2, NCB = RBB / 16; // B row bytes, chunks
+  static constexpr int BSW = NCB >= 16 ? 4 : 2;      // B chunk swizzle step
   static constexpr int WTM = BM / WM, WTN = BN / WN;
   static constexpr int FM = WTM / 32, FN = WTN / 32;
   static constexpr int KS = BK / 16;
@@ -113,7 +115,7 @@ struct Gemm16Dma {
   static_assert(OP == OP_BF16 || OP == OP_F16, "16-bit operands only");
   static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0,
                 "tiles must split into whole wave-wide loads");
-  static_assert(NCB >= 16 && (NCA & (NCA - 1)) == 0, "tile shape");
+  static_assert(NCB >= 8 && (NCA & (NCA - 1)) == 0, "tile shape");
   static_assert(BK % 16 == 0 && WTM % 32 == 0 && WTN % 32 == 0, "tile shape");
 
   // Issue the direct-to-LDS loads of K step kt into stage buffer (as, bs).
@@ -140,7 +142,7 @@ struct Gemm16Dma {
       const int j = wave * B_DMA + i;
       const int g = j * 64 + lane;
       const int k = g / NCB, pc = g % NCB;
-      const int c = pc ^ (4 * (k & 3));
+      const int c = pc ^ (BSW * (k & 3));
       const int64_t gk = k0 + k, gn = n0 + c * 8;
       const void *src = p.B + (gk * p.ldb + gn) * 2;
       if (MASK && (gk >= p.K || gn >= p.N))
@@ -175,9 +177,9 @@ struct Gemm16Dma {
         for (int j = 0; j < FN; ++j) {
           const int n = wn * WTN + j * 32 + 16 * (G & 1) + 4 * (L & 3);
           const int k = ks * 16 + 8 * (G >> 1) + (L >> 2);
-          const uint32_t off0 = k * RBB + (((n >> 3) ^ (4 * (k & 3))) << 4) + (n & 7) * 2;
+          const uint32_t off0 = k * RBB + (((n >> 3) ^ (BSW * (k & 3))) << 4) + (n & 7) * 2;
           const int k4 = k + 4;
-          const uint32_t off1 = k4 * RBB + (((n >> 3) ^ (4 * (k4 & 3))) << 4) + (n & 7) * 2;
+          const uint32_t off1 = k4 * RBB + (((n >> 3) ^ (BSW * (k4 & 3))) << 4) + (n & 7) * 2;
           b[j] = tr_read_pair(bs, off0, off1);
         }
         const int64_t rem = krem - (ks * 16 + 8 * (lane >> 5));
