@@ -127,7 +127,9 @@ const GemmConfig kGemmConfigs[] = {
     TX_GEMM_W4T(OP_F16, EPI_F32),
     TX_GEMM_W4T(OP_F16, EPI_F16),
     // bf16 / fp16 operands, 128x128x64 tiles: direct-to-LDS staging, 64-bit
-    // addresses (operands spanning 2 GiB or more)
+    // addresses (operands spanning 2 GiB or more); two stages, two
+    // workgroups per CU (three or four stages leave one: 32.3 -> 25.6% of
+    // peak at bf16 4096^3)
     TX_GEMM_DMA(OP_BF16, 128, 128, 64, 2, 2, EPI_BF16),
     TX_GEMM_DMA(OP_BF16, 128, 128, 64, 2, 2, EPI_F32),
     TX_GEMM_DMA(OP_F16, 128, 128, 64, 2, 2, EPI_F32),
