@@ -1,6 +1,5 @@
 // bf16/fp16 256x256x64 tile kernel for gfx950: C[M,N] = epilogue(A[M,K] .
-// B[K,N]), all row-major.  NW = 4: four waves of 128x128 (the default);
-// NW = 8: eight waves of 128x64.
+// B[K,N]), all row-major: four waves of 128x128.
 //
 // Why four waves.  The K loop is power-limited, not issue-limited: with
 // LDS reads removed the same loop runs at a clock about 15% higher.  A
@@ -55,7 +54,9 @@ __device__ __forceinline__ i32x4_t make_rsrc(const void *base, uint32_t bytes) {
 // K values, same swizzle) and read with ds_read_b128 instead of transposes.
 template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
   static constexpr int BM = 256, BN = 256, BK = 64;
-  // NW = 4: 2x2 waves of 128x128; NW = 8: 2x4 waves of 128x64.
+  // 2x2 waves of 128x128 (NW is the wave count, kept as a parameter for the
+  // staging layouts other kernels borrow from this one).
+  static_assert(NW == 4, "four waves");
   static constexpr int WM = 2, WN = NW / 2;
   static constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32, KS = BK / 16;
   static constexpr int RPS = FM + 2 * FN; // LDS reads per sub-step
@@ -269,7 +270,7 @@ template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
   // Staging loads per wave and step, issued in PARTS groups of PER spread
   // over the step (see run()).
   static constexpr int NDMA = Stage::A_DMA + Stage::B_DMA;
-  static constexpr int PARTS = NW == 4 ? 3 : 2;
+  static constexpr int PARTS = 3;
   static constexpr int PER = (NDMA + PARTS - 1) / PARTS;
   static constexpr int NU = FM + FN; // read units per sub-step
   static_assert(NU <= MPS && PER <= MPS, "one read unit and one load per MFMA at most");
@@ -427,14 +428,11 @@ template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
       __builtin_amdgcn_s_waitcnt(0x7 << 4);
     }
 
-    if constexpr (!MASK_MN && NW == 4)
-      epilogue_lds(p, m0, n0, wm, wn, acc, lds0);
-    else
-      epilogue_tile<MASK_MN, FM, FN, WTM, WTN>(p, m0, n0, wm, wn, acc);
+    epilogue_lds<MASK_MN>(p, m0, n0, wm, wn, acc, lds0);
   }
 
-  // Epilogue of an interior tile through LDS (the two stages, 128 KiB, are
-  // free once every wave is past the K loop).  The accumulators' own layout
+  // Epilogue of a tile through LDS (the two stages, 128 KiB, are free once
+  // every wave is past the K loop).  The accumulators' own layout
   // writes 8-byte pieces of 32 rows per store instruction; staged as
   // row-major C in LDS, the tile leaves in whole rows instead: each store
   // instruction writes 1 KiB of contiguous 16-byte chunks, two 512-byte rows
@@ -442,7 +440,10 @@ template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
   // passes of 128 rows).  Measured: the bf16 epilogue's cycles halved
   // (20.5k -> 10.2k per wave at 4096^3).  LDS row r holds 16-byte chunk c at
   // c ^ (r & 31), so the 32 rows one accumulator store touches, and the two
-  // rows one read covers, spread over the banks.
+  // rows one read covers, spread over the banks.  MASK_MN (tiles crossing M
+  // or N): rows past M are not stored, nor chunks past N, and the chunk that
+  // crosses N is stored element by element.
+  template <bool MASK_MN>
   __device__ __forceinline__ static void epilogue_lds(const GemmArgs &p, int64_t m0, int64_t n0,
                                                       int wm, int wn, const f32x16_t (&acc)[FM][FN],
                                                       uint32_t lds0) {
@@ -490,6 +491,33 @@ template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
       for (int q = 0; q < ROWS * CH / 256; ++q) {
         const int idx = q * 256 + t, r = idx / CH, ch = idx % CH;
         const v4u v = *(const lds_v4u *)(uintptr_t)(lds0 + r * ROWB + ((ch ^ (r & 31)) << 4));
+        if constexpr (MASK_MN) {
+          constexpr int EPC = F32 ? 4 : 8; // elements per chunk
+          const int64_t col = n0 + (int64_t)ch * EPC;
+          if (row0 + r >= p.M || col >= p.N)
+            continue;
+          if (col + EPC > p.N) { // the chunk crosses N
+            const int64_t off = (row0 + r) * p.ldc + col;
+            // The chunk's words as scalars: indexing the vector by the loop
+            // variable compiled to word 0 for every element (measured: fp32
+            // C at N = 50 got column 48's value in column 49).
+            const unsigned w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) {
+              if (col + e < p.N) {
+                if constexpr (F32) {
+                  float *c = reinterpret_cast<float *>(p.C) + off + e;
+                  const float x = __builtin_bit_cast(float, w[e]);
+                  *c = p.accumulate ? *c + x : x;
+                } else {
+                  reinterpret_cast<uint16_t *>(p.C)[off + e] =
+                      (uint16_t)(w[e / 2] >> (16 * (e & 1)));
+                }
+              }
+            }
+            continue;
+          }
+        }
         if constexpr (F32) {
           v4u *c = reinterpret_cast<v4u *>(reinterpret_cast<float *>(p.C) + (row0 + r) * p.ldc +
                                            n0 + ch * 4);
@@ -506,69 +534,6 @@ template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
       }
       if (F32 && pass == 0)
         __syncthreads(); // the first half is read out before the second is staged
-    }
-  }
-
-  // Epilogue of a wave's (FM*32) x (FN*32) sub-tile at (wm, wn): lane l
-  // holds, per 32x32 block (i, j) and register quad g, C[row][col .. col+3]
-  // with row = m0 + wm*WTM_ + 32 i + l % 32 and col = n0 + wn*WTN_ + 32 j +
-  // 8 g + 4 (l / 32).
-  template <bool MASK_MN, int FM_, int FN_, int WTM_, int WTN_>
-  __device__ __forceinline__ static void epilogue_tile(const GemmArgs &p, int64_t m0,
-                                                       int64_t n0, int wm, int wn,
-                                                       const f32x16_t (&acc)[FM_][FN_]) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int i = 0; i < FM_; ++i) {
-      const int64_t row = m0 + wm * WTM_ + i * 32 + (lane & 31);
-      if (MASK_MN && row >= p.M)
-        continue;
-#pragma unroll
-      for (int j = 0; j < FN_; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int64_t col = n0 + wn * WTN_ + j * 32 + 8 * g + 4 * (lane >> 5);
-          if (MASK_MN && col >= p.N)
-            continue;
-          const int64_t off = row * p.ldc + col;
-          const float v0 = acc[i][j][4 * g], v1 = acc[i][j][4 * g + 1];
-          const float v2 = acc[i][j][4 * g + 2], v3 = acc[i][j][4 * g + 3];
-          if (MASK_MN && col + 4 > p.N) { // the quad crosses N: element by element
-            const float v[4] = {v0, v1, v2, v3};
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              if (col + r >= p.N)
-                break;
-              if (EPI == EPI_F32) {
-                float *c = reinterpret_cast<float *>(p.C) + off + r;
-                *c = p.accumulate ? *c + v[r] : v[r];
-              } else {
-                reinterpret_cast<uint16_t *>(p.C)[off + r] =
-                    EPI == EPI_BF16 ? f32_to_bf16_rne(v[r]) : f32_to_f16_rne(v[r]);
-              }
-            }
-            continue;
-          }
-          if (EPI == EPI_F32) {
-            float4 *c = reinterpret_cast<float4 *>(reinterpret_cast<float *>(p.C) + off);
-            if (p.accumulate) {
-              const float4 o = *c;
-              *c = make_float4(o.x + v0, o.y + v1, o.z + v2, o.w + v3);
-            } else {
-              *c = make_float4(v0, v1, v2, v3);
-            }
-          } else {
-            uint2 w;
-            if (EPI == EPI_BF16) {
-              w.x = pk_bf16_rne(v0, v1);
-              w.y = pk_bf16_rne(v2, v3);
-            } else {
-              w.x = pk_f16_rne(v0, v1);
-              w.y = pk_f16_rne(v2, v3);
-            }
-            *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.C) + off) = w;
-          }
-        }
     }
   }
 };
