@@ -128,6 +128,31 @@ def test_int8_ragged(gpu, M, N, K, block):
     assert np.array_equal(from_device(c), ref)
 
 
+@pytest.mark.parametrize("N", [49, 50, 51, 53, 55])
+@pytest.mark.parametrize("out", ["f32", "bf16"])
+@pytest.mark.parametrize("kmajor", [False, True])
+def test_16bit_every_element_of_the_chunk_crossing_n(gpu, N, out, kmajor):
+    """The 256 tile's edge epilogue stores the chunk that crosses N element by element:
+    N mod 4 (fp32 C) and N mod 8 (bf16 C) take every value the chunk can leave."""
+    run16(gpu, 64, N, 70, "bf16", out, kmajor=kmajor)
+
+
+@pytest.mark.parametrize("N", [49, 50, 51])
+def test_8bit_every_element_of_the_quad_crossing_n(gpu, N):
+    """The 8-bit tile's edge epilogue: int8 -> int32 with N mod 4 = 1, 2, 3, bit-exact."""
+    import torch
+    M, K = 40, 200
+    say(f"tails int8 quad crossing N M={M} N={N} K={K}")
+    a, b = uniform_i8((M, K), 64), uniform_i8((K, N), 65)
+    sa, _ = padded(a, 0)
+    sb, _ = padded(b, 0)
+    c = tx.dot(dev_view(sa, (M, K), gpu), dev_view(sb, (K, N), gpu), out_dtype=torch.int32,
+               block=(256, 256, 128))
+    torch.cuda.synchronize()
+    ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.I32, block=(64, 64, 64))
+    assert np.array_equal(from_device(c), ref)
+
+
 def _fp8_codes(shape, seed):
     c = np.random.default_rng(seed).integers(0, 256, size=shape).astype(np.uint8)
     return np.where((c & 0x7F) == 0x7F, c & 0xF0, c).astype(np.uint8)  # no NaN codes

@@ -67,6 +67,8 @@
 // leak into the result.
 #pragma once
 
+#include <type_traits>
+
 #include "gemm16_w4.h"
 
 namespace txk {
@@ -614,23 +616,27 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
         const int64_t off = row * p.ldc + col;
         const Acc &v = acc[i][j];
         if (MASK_MN && col + 4 > p.N) { // the quad crosses N: element by element
+          // The quad as scalars: a vector indexed by an element loop that
+          // can stop early has compiled to element 0 for every element.
+          typedef std::remove_cv_t<std::remove_reference_t<decltype(v[0])>> E;
+          const E w[4] = {v[0], v[1], v[2], v[3]};
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             if (col + r >= p.N)
-              break;
+              continue;
             if (EPI == EPI_I32) {
               int32_t *c = reinterpret_cast<int32_t *>(p.C) + off + r;
-              *c = p.accumulate ? *c + (int32_t)v[r] : (int32_t)v[r];
+              *c = p.accumulate ? *c + (int32_t)w[r] : (int32_t)w[r];
             } else if (EPI == EPI_F32 || EPI == EPI_BLOCK128_F32 || EPI == EPI_MX_F32) {
               float *c = reinterpret_cast<float *>(p.C) + off + r;
-              *c = p.accumulate ? *c + (float)v[r] : (float)v[r];
+              *c = p.accumulate ? *c + (float)w[r] : (float)w[r];
             } else {
               float f;
               if (EPI == EPI_ROWCOL_BF16) {
 #pragma clang fp contract(off)
-                f = ((float)v[r] * sar) * p.sb[col + r];
+                f = ((float)w[r] * sar) * p.sb[col + r];
               } else {
-                f = (float)v[r];
+                f = (float)w[r];
               }
               reinterpret_cast<uint16_t *>(p.C)[off + r] = f32_to_bf16_rne(f);
             }
