@@ -241,6 +241,15 @@ def test_attn_plan():
             tx.attn_plan(**a)
         return e.value.code
     assert err(head_dim=96) == tx.ERR_UNSUPPORTED
+    # head dims: the tutorial's {16, 32, 64, 128, 256}; 32 .. 256 for fp16 / bf16, 64 and 128
+    # for fp8; a K block must fill one 1 KiB load per wave
+    for hd in (32, 64, 128, 256):
+        for blk in ((128, 64), (64, 64), (64, 32)) + (((128, 32),) if hd > 32 else ()):
+            assert tx.attn_plan(1, 1, 256, hd, True, 0.5, dtype=tx.BF16, block=blk).desc.head_dim == hd
+    assert err(head_dim=32, block=(128, 32)) == tx.ERR_UNSUPPORTED
+    assert err(head_dim=16) == tx.ERR_UNSUPPORTED
+    assert err(head_dim=256, dtype=tx.F8E5M2) == tx.ERR_UNSUPPORTED
+    assert err(head_dim=32, dtype=tx.F8E5M2) == tx.ERR_UNSUPPORTED
     assert err(N_CTX=200) == tx.ERR_UNSUPPORTED
     assert err(dtype=tx.F32) == tx.ERR_UNSUPPORTED
     assert tx.attn_plan(1, 1, 256, 128, True, 0.5, dtype=tx.BF16).desc.head_dim == 128

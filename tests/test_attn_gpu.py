@@ -104,6 +104,23 @@ def test_attn_blocks_vs_oracle(gpu, block, causal, Z, H, N, D, bf16):
     """The tutorial's other autotuned blocks (BLOCK_M 64 / 128 by BLOCK_N 32 /
     64) against the oracle run with the same blocks.  N_CTX = 64, 192, 320
     give odd block counts in both loop segments at BLOCK_M 64."""
+    attn_vs_oracle(gpu, block, causal, Z, H, N, D, bf16)
+
+
+@pytest.mark.parametrize("block", [(128, 64), (128, 32), (64, 64), (64, 32)])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("Z,H,N,D,bf16", [(2, 2, 256, 32, False), (1, 3, 192, 32, True),
+                                          (1, 2, 256, 256, False), (2, 1, 192, 256, True)])
+def test_attn_head_dims_32_and_256(gpu, block, causal, Z, H, N, D, bf16):
+    """Head dims 32 and 256 (64- and 512-byte K/V rows, their own swizzles; 256 reads its
+    fragments in groups) at every block shape the plan accepts."""
+    if D == 32 and block == (128, 32):
+        pytest.skip("a 2 KiB K block for four waves: rejected at plan time")
+    attn_vs_oracle(gpu, block, causal, Z, H, N, D, bf16)
+
+
+def attn_vs_oracle(gpu, block, causal, Z, H, N, D, bf16):
+    """fp16 / bf16 attention at `block` against the oracle at the same block."""
     import torch
     if N % block[0]:
         pytest.skip("N_CTX is not a whole number of BLOCK_M blocks")

@@ -851,6 +851,16 @@ extern "C" TX_API int tx_dot_launch_noalloc(const tx_dot_plan *plan, const void 
 
 namespace {
 
+// The 16-bit attention kernel for one configuration, or nullptr where a K
+// block is smaller than one 1 KiB load per wave (head dim 32 with 128 x 32
+// blocks), which the plan rejects.
+template <bool C, int HD, bool BF, int BM, int BN> constexpr void (*attnKernel())(txk::AttnArgs) {
+  if constexpr (HD * 2 * BN >= 1024 * (BM / 32))
+    return txk::attn_fwd_kernel<C, HD, BF, BM, BN>;
+  else
+    return nullptr;
+}
+
 // Packed defaults and checks of one tensor's (batch, head, row) strides.
 // key_major: e5m2 v, stored [HEAD_DIM][N_CTX] per head (sm = dim stride).
 int attnStrides(const tx_attn_desc &d, int64_t &sz, int64_t &sh, int64_t &sm,
@@ -883,11 +893,14 @@ extern "C" TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *p
     return fail(TX_ERR_INVALID, "causal must be 0 or 1");
   if (!(d.sm_scale == d.sm_scale))
     return fail(TX_ERR_INVALID, "sm_scale is NaN");
-  if (d.head_dim != 64 && d.head_dim != 128)
-    return fail(TX_ERR_UNSUPPORTED, "head_dim %d: 64 and 128 are implemented", d.head_dim);
   if (d.dtype != TX_F16 && d.dtype != TX_BF16 && d.dtype != TX_F8E5M2)
     return fail(TX_ERR_UNSUPPORTED, "dtype %d: fp16, bf16 and fp8 e5m2 q/k/v/o are implemented",
                 d.dtype);
+  if (d.dtype == TX_F8E5M2 ? d.head_dim != 64 && d.head_dim != 128
+                           : d.head_dim != 32 && d.head_dim != 64 && d.head_dim != 128 &&
+                                 d.head_dim != 256)
+    return fail(TX_ERR_UNSUPPORTED, "head_dim %d: %s are implemented", d.head_dim,
+                d.dtype == TX_F8E5M2 ? "64 and 128 (fp8)" : "32, 64, 128 and 256");
   if (d.block_m == 0) d.block_m = 128;
   if (d.block_n == 0) d.block_n = 64;
   if ((d.block_m != 64 && d.block_m != 128) || (d.block_n != 32 && d.block_n != 64))
@@ -895,6 +908,12 @@ extern "C" TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *p
                 "are implemented", d.block_m, d.block_n);
   if (d.dtype == TX_F8E5M2 && d.block_n != 64)
     return fail(TX_ERR_UNSUPPORTED, "fp8 e5m2 attention: BLOCK_N 64 is implemented");
+  // A K or V block (BLOCK_N rows of HEAD_DIM elements) is staged by whole
+  // 1 KiB loads, at least one per wave.
+  if (d.dtype != TX_F8E5M2 && (int64_t)d.block_n * d.head_dim * 2 < 1024 * (d.block_m / 32))
+    return fail(TX_ERR_UNSUPPORTED, "head_dim %d with blocks %dx%d: a K block of %d bytes for "
+                "%d waves", d.head_dim, d.block_m, d.block_n, d.block_n * d.head_dim * 2,
+                d.block_m / 32);
   if (d.N_CTX % d.block_m)
     return fail(TX_ERR_UNSUPPORTED, "N_CTX %lld is not a multiple of %d (whole blocks only)",
                 (long long)d.N_CTX, d.block_m);
@@ -937,7 +956,8 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
   const bool bm64 = d.block_m == 64, bn32 = d.block_n == 32;
   if ((d.block_m != 64 && d.block_m != 128) || (d.block_n != 32 && d.block_n != 64) ||
       (d.dtype == TX_F8E5M2 && bn32) || plan->block_threads != d.block_m / 32 * 64 ||
-      (d.head_dim != 64 && d.head_dim != 128) ||
+      (d.head_dim != 32 && d.head_dim != 64 && d.head_dim != 128 && d.head_dim != 256) ||
+      (d.dtype == TX_F8E5M2 && d.head_dim != 64 && d.head_dim != 128) ||
       (d.dtype != TX_F16 && d.dtype != TX_BF16 && d.dtype != TX_F8E5M2) || d.N_CTX % d.block_m ||
       plan->m_blocks != d.N_CTX / d.block_m || plan->grid_x != d.Z * d.H * plan->m_blocks)
     return fail(TX_ERR_INVALID, "plan launch shape does not match the attention kernel");
@@ -959,14 +979,16 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
   hipStream_t s = static_cast<hipStream_t>(stream);
   typedef void (*AttnFn)(txk::AttnArgs);
 #define TX_ATTN_BLOCKS(C, HD, BF)                                                          \
-  {{txk::attn_fwd_kernel<C, HD, BF, 128, 64>, txk::attn_fwd_kernel<C, HD, BF, 128, 32>},  \
-   {txk::attn_fwd_kernel<C, HD, BF, 64, 64>, txk::attn_fwd_kernel<C, HD, BF, 64, 32>}}
-  // [causal][head_dim 128][bf16][BLOCK_M 64][BLOCK_N 32]
-  static const AttnFn kAttn[2][2][2][2][2] = {
-      {{TX_ATTN_BLOCKS(false, 64, false), TX_ATTN_BLOCKS(false, 64, true)},
-       {TX_ATTN_BLOCKS(false, 128, false), TX_ATTN_BLOCKS(false, 128, true)}},
-      {{TX_ATTN_BLOCKS(true, 64, false), TX_ATTN_BLOCKS(true, 64, true)},
-       {TX_ATTN_BLOCKS(true, 128, false), TX_ATTN_BLOCKS(true, 128, true)}}};
+  {{attnKernel<C, HD, BF, 128, 64>(), attnKernel<C, HD, BF, 128, 32>()},                    \
+   {attnKernel<C, HD, BF, 64, 64>(), attnKernel<C, HD, BF, 64, 32>()}}
+#define TX_ATTN_DTYPES(C, HD) {TX_ATTN_BLOCKS(C, HD, false), TX_ATTN_BLOCKS(C, HD, true)}
+  // [causal][head_dim 32 / 64 / 128 / 256][bf16][BLOCK_M 64][BLOCK_N 32]
+  static const AttnFn kAttn[2][4][2][2][2] = {
+      {TX_ATTN_DTYPES(false, 32), TX_ATTN_DTYPES(false, 64), TX_ATTN_DTYPES(false, 128),
+       TX_ATTN_DTYPES(false, 256)},
+      {TX_ATTN_DTYPES(true, 32), TX_ATTN_DTYPES(true, 64), TX_ATTN_DTYPES(true, 128),
+       TX_ATTN_DTYPES(true, 256)}};
+#undef TX_ATTN_DTYPES
 #undef TX_ATTN_BLOCKS
   // [causal][head_dim 128][BLOCK_M 64]
   static const AttnFn kAttn8[2][2][2] = {
@@ -974,9 +996,12 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
        {txk::attn_fwd8_kernel<false, 128, 128>, txk::attn_fwd8_kernel<false, 128, 64>}},
       {{txk::attn_fwd8_kernel<true, 64, 128>, txk::attn_fwd8_kernel<true, 64, 64>},
        {txk::attn_fwd8_kernel<true, 128, 128>, txk::attn_fwd8_kernel<true, 128, 64>}}};
-  const int c = d.causal ? 1 : 0, h = d.head_dim == 128;
-  const AttnFn fn = d.dtype == TX_F8E5M2 ? kAttn8[c][h][bm64]
-                                         : kAttn[c][h][d.dtype == TX_BF16][bm64][bn32];
+  const int c = d.causal ? 1 : 0;
+  const int hd = d.head_dim == 32 ? 0 : d.head_dim == 64 ? 1 : d.head_dim == 128 ? 2 : 3;
+  const AttnFn fn = d.dtype == TX_F8E5M2 ? kAttn8[c][d.head_dim == 128][bm64]
+                                         : kAttn[c][hd][d.dtype == TX_BF16][bm64][bn32];
+  if (!fn)
+    return fail(TX_ERR_INVALID, "plan launch shape does not match the attention kernel");
   hipLaunchKernelGGL(fn, dim3(plan->grid_x), dim3(plan->block_threads), 0, s, a);
   TX_HIP_CHECK(hipGetLastError());
   return TX_OK;

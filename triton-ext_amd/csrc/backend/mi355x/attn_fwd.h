@@ -1,7 +1,7 @@
 // Fused attention forward for gfx950: the forward of the fused-attention
 // tutorial (R:pass/LoopSplit/06-fused-attention.py:44-93, :181-239), fp16
-// (the tutorial's type) or bf16 q/k/v/o, HEAD_DIM 64 or 128, fp32 softmax
-// statistics and accumulator.
+// (the tutorial's type) or bf16 q/k/v/o, HEAD_DIM 32, 64, 128 or 256, fp32
+// softmax statistics and accumulator.
 //
 // A workgroup owns BM query rows of one (z, h), one wave per 32 rows; BM x
 // BN is any of the tutorial's autotuned blocks (64 or 128 by 32 or 64, 128 x
@@ -17,15 +17,16 @@
 //                    the S^T registers: MFMA slot s of lane group g is key
 //                    16 c + 8 (s/4) + 4 g + s%4, so V's rows are read in that
 //                    order and no value crosses lanes.
-// Staging: K and V blocks (8 or 16 KiB each) reach LDS by direct-to-LDS
+// Staging: K and V blocks (BN x HEAD_DIM x 2 bytes each) reach LDS by direct-to-LDS
 // buffer loads into two slots each, one barrier per block; loads run a block
 // ahead under the math (the pipeline is described at the kernel).  LDS
 // layouts (rows of 2 HEAD_DIM bytes, 16-byte chunk c of row r stored at):
-//   K: c ^ ((r >> 1) & 7) (128-byte rows), c ^ (r & 15) (256-byte rows): the
-//      16 rows a ds_read_b128 pass touches hit 16 different bank groups;
-//   V: c ^ (4 ((r >> 1) & 1)) (128-byte rows), c ^ (4 (r & 3)) (256-byte
-//      rows): the 4 rows x 64 bytes a ds_read_b64_tr_b16 pass touches cover
-//      all 64 banks once.
+//   K: c ^ ((r >> 2) & 3) (64-byte rows), c ^ ((r >> 1) & 7) (128-byte
+//      rows), c ^ (r & 15) (256- and 512-byte rows): the 16 rows a
+//      ds_read_b128 pass touches hit 16 different bank groups;
+//   V: c (64-byte rows), c ^ (4 ((r >> 1) & 1)) (128-byte rows), c ^ (4 (r &
+//      3)) (256- and 512-byte rows): the 4 rows x 64 bytes a
+//      ds_read_b64_tr_b16 pass touches cover all 64 banks once.
 // The K/V loop runs in LoopSplit form: keys [0, causal_start) unmasked, then
 // the on-band blocks [causal_start, causal_start + BM) masked; causal_start =
 // start_m * BM, or N_CTX without the causal mask.  Blocks past the diagonal
@@ -57,9 +58,12 @@ template <int HD, bool BF, int BM_ = 128, int BN_ = 64> struct AttnFwd {
   static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 1 .. 8
   static constexpr int CPR = ROW / 16;         // 16-byte chunks per row: 8 / 16
   static constexpr uint32_t kOOB = 0x80000000u;
-  static_assert(D == 64 || D == 128, "head dims 64 and 128");
+  static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head dims 32 .. 256");
   static_assert((BM == 64 || BM == 128) && (BN == 32 || BN == 64), "the tutorial's blocks");
   static_assert(DMA >= 1 && DMA * NW * 1024 == TILE, "whole 1 KiB loads per wave");
+  // Fragment reads issued together in qk / pv: every one at head dims up to
+  // 128, in groups of 8 at 256 (all 32 would take 128 VGPRs).
+  static constexpr int KGRP = D / 16 < 8 ? D / 16 : 8;
   // 16-bit element vectors; BF: bf16, else fp16
   typedef typename std::conditional<BF, __bf16, _Float16>::type elt;
   typedef elt h8 __attribute__((ext_vector_type(8)));
@@ -73,9 +77,11 @@ template <int HD, bool BF, int BM_ = 128, int BN_ = 64> struct AttnFwd {
       return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
   // swizzles of the 16-byte chunk index (see the layouts above)
-  __device__ __forceinline__ static int kswz(int r) { return D == 64 ? (r >> 1) & 7 : r & 15; }
+  __device__ __forceinline__ static int kswz(int r) {
+    return D == 32 ? (r >> 2) & 3 : D == 64 ? (r >> 1) & 7 : r & 15;
+  }
   __device__ __forceinline__ static int vswz(int r) {
-    return D == 64 ? 4 * ((r >> 1) & 1) : 4 * (r & 3);
+    return D == 32 ? 0 : D == 64 ? 4 * ((r >> 1) & 1) : 4 * (r & 3);
   }
 
   __device__ __forceinline__ static void dma16(uint32_t voff, const i32x4_t &rsrc, uint32_t soff,
@@ -168,18 +174,22 @@ template <int HD, bool BF, int BM_ = 128, int BN_ = 64> struct AttnFwd {
   template <int SLOT>
   __device__ __forceinline__ static void qk(const Bases &bs, const h8 (&qf)[D / 16],
                                             f16v (&s)[BN / 32]) {
-    h8 kf[BN / 32][D / 16];
 #pragma unroll
     for (int b = 0; b < BN / 32; ++b)
-#pragma unroll
-      for (int c = 0; c < D / 16; ++c)
-        kf[b][c] = read_k<SLOT>(bs, b, c);
-#pragma unroll
-    for (int b = 0; b < BN / 32; ++b) {
       s[b] = f16v{};
 #pragma unroll
-      for (int c = 0; c < D / 16; ++c)
-        s[b] = mfma(kf[b][c], qf[c], s[b]);
+    for (int c0 = 0; c0 < D / 16; c0 += KGRP) {
+      h8 kf[BN / 32][KGRP];
+#pragma unroll
+      for (int b = 0; b < BN / 32; ++b)
+#pragma unroll
+        for (int c = 0; c < KGRP; ++c)
+          kf[b][c] = read_k<SLOT>(bs, b, c0 + c);
+#pragma unroll
+      for (int b = 0; b < BN / 32; ++b)
+#pragma unroll
+        for (int c = 0; c < KGRP; ++c)
+          s[b] = mfma(kf[b][c], qf[c0 + c], s[b]);
     }
   }
 
@@ -254,17 +264,21 @@ template <int HD, bool BF, int BM_ = 128, int BN_ = 64> struct AttnFwd {
   template <int SLOT>
   __device__ __forceinline__ static void pv(const Bases &bs, const h8 (&pf)[BN / 16],
                                             f16v (&acc)[D / 32]) {
-    h8 vf[D / 32][BN / 16];
+    constexpr int VGRP = D / 32 < 4 ? D / 32 : 4; // dim blocks read together
 #pragma unroll
-    for (int bd = 0; bd < D / 32; ++bd)
+    for (int b0 = 0; b0 < D / 32; b0 += VGRP) {
+      h8 vf[VGRP][BN / 16];
 #pragma unroll
-      for (int c = 0; c < BN / 16; ++c)
-        vf[bd][c] = read_v<SLOT>(bs, bd, c);
+      for (int bd = 0; bd < VGRP; ++bd)
 #pragma unroll
-    for (int bd = 0; bd < D / 32; ++bd)
+        for (int c = 0; c < BN / 16; ++c)
+          vf[bd][c] = read_v<SLOT>(bs, b0 + bd, c);
 #pragma unroll
-      for (int c = 0; c < BN / 16; ++c)
-        acc[bd] = mfma(vf[bd][c], pf[c], acc[bd]);
+      for (int bd = 0; bd < VGRP; ++bd)
+#pragma unroll
+        for (int c = 0; c < BN / 16; ++c)
+          acc[b0 + bd] = mfma(vf[bd][c], pf[c], acc[b0 + bd]);
+    }
   }
 
   // The kernel's view of this element type.
@@ -428,7 +442,7 @@ template <bool CAUSAL, class A> __device__ __forceinline__ void attn_fwd_body(co
 }
 
 template <bool CAUSAL, int HD, bool BF, int BM = 128, int BN = 64>
-__global__ void __launch_bounds__(BM * 2, 2) attn_fwd_kernel(AttnArgs p) {
+__global__ void __launch_bounds__(BM * 2, HD >= 256 ? 1 : 2) attn_fwd_kernel(AttnArgs p) {
   attn_fwd_body<CAUSAL, AttnFwd<HD, BF, BM, BN>>(p);
 }
 
