@@ -323,8 +323,9 @@ def _upcast_workspace(p, device, stream):
 def attention(q, k, v, causal, sm_scale, return_lse=False, plan=None, stream=None, block=(0, 0)):
     """Forward of the fused-attention tutorial's `attention(q, k, v, causal,
     sm_scale)` (R:pass/LoopSplit/06-fused-attention.py:583-640) on the
-    MI355X kernel: q, k, v [Z, H, N_CTX, HEAD_DIM], head dim 64 or 128, in
-    fp16 or bf16 (head dim contiguous), or in float8_e5m2 as the tutorial's
+    MI355X kernel: q, k, v [Z, H, N_CTX, HEAD_DIM], head dim 32, 64, 128 or
+    256 in fp16 or bf16 (head dim contiguous), or 64 or 128 in
+    float8_e5m2 as the tutorial's
     fp8 provider passes them (:774-779): q and k head-dim contiguous, v
     key-contiguous (stride 1 along N_CTX, "when v is in float8_e5m2 it is
     transposed", :586).  o has q's type; p is rounded to it before p @ v
