@@ -1,0 +1,259 @@
+"""Seeded shape sweep: every kernel family against the oracle at shapes drawn
+from a fixed generator (edges near multiples of 16..256, tiny dims, and
+uniform ones), with operands in padded storage whose padding holds NaN
+(floating point) or random bytes (int8), so an element read past an edge
+changes a result.
+
+The targeted tests name the corners one by one; this sweep crosses them
+(dtype x epilogue x tile x K-major x ragged M/N/K; attention head dim x
+block x causal x dtype) at shapes nobody picked.
+Bars as elsewhere: int8 and W8A8 bit-exact; fp16/bf16/fp8 within the
+north_star tolerance (|d| <= 1e-3 s + 1e-2 |ref|); MX within the scaled
+MFMA's rigorous bound (test_mx_gpu.check_mx) and, on codes whose 32-product
+group sums are exact in the MFMA, within the fp32 running sum's rounding;
+attention as
+test_attn_gpu.py (o within 2^-8 fp16 / 2^-6 bf16 of the oracle at the same
+block, M within 1e-4; e5m2 by check_e5m2).
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+import triton_ext_amd as tx
+from dotcase import (bits_to_f32, check_close, fp8_block_inputs, from_device, say, to_device,
+                     uniform_i8, uniform_scales)
+from test_attn_gpu import attn_vs_oracle, check_e5m2, e5m2_qkv, run_gpu_fp8
+from test_mx_gpu import check_mx, ref_of, run_gpu
+from test_tails_gpu import dev_view, padded, run16
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-3, 1e-2
+SEED = 20261202
+
+
+def _dim(rng, hi):
+    r = rng.random()
+    if r < 0.2:
+        return int(rng.integers(1, 20))
+    if r < 0.6:
+        q = int(rng.choice([16, 32, 64, 128, 256]))
+        base = q * int(rng.integers(1, max(2, hi // q)))
+        return int(min(hi, max(1, base + int(rng.integers(-3, 4)))))
+    return int(rng.integers(1, hi + 1))
+
+
+def _cases():
+    rng = np.random.default_rng(SEED)
+    out = []
+    for i in range(90):
+        kind = str(rng.choice(["bf16", "f16"]))
+        o = str(rng.choice(["f32", kind]))
+        kmajor = bool(rng.random() < 0.3)
+        blocks = [(0, 0, 0), (256, 256, 64)] if kmajor else \
+            [(0, 0, 0), (256, 256, 64), (128, 128, 64), (64, 64, 32)]
+        blk = blocks[int(rng.integers(len(blocks)))]
+        out.append(("16bit", i, dict(M=_dim(rng, 700), N=_dim(rng, 700), K=_dim(rng, 700),
+                                     kind=kind, out=o, block=blk, kmajor=kmajor)))
+    tiles8 = [(0, 0, 0), (256, 256, 128), (256, 224, 128), (128, 128, 128)]
+    for i in range(36):
+        out.append(("i8_i32", i, dict(M=_dim(rng, 700), N=_dim(rng, 700), K=_dim(rng, 900),
+                                      block=tiles8[i % 4])))
+    for i in range(48):
+        # even cases: decode (M <= 256); odd: the 8-bit tiles' row x column epilogue (M > 256)
+        M = int(rng.integers(1, 257)) if i % 2 == 0 else int(rng.integers(257, 701))
+        blk = (0, 0, 0) if i % 2 == 0 else tiles8[(i // 2) % 4]
+        out.append(("w8a8", i, dict(M=M, N=_dim(rng, 3000), K=_dim(rng, 3000), block=blk)))
+    for i in range(24):
+        fa, fb = [("e4m3", "e4m3"), ("e5m2", "e5m2"), ("e4m3", "e5m2"), ("e5m2", "e4m3")][i % 4]
+        blk = (0, 0, 0) if "e5m2" in (fa, fb) else tiles8[(i // 4) % 3 + 1]
+        out.append(("fp8", i, dict(M=_dim(rng, 600), N=_dim(rng, 600), K=_dim(rng, 900),
+                                   fa=fa, fb=fb, block=blk)))
+    for i in range(36):
+        o = str(rng.choice(["bf16", "f32"]))
+        out.append(("fp8_block", i, dict(M=_dim(rng, 600), N=_dim(rng, 600), K=_dim(rng, 900),
+                                         out=o, block=tiles8[i % 4])))
+    for i in range(36):
+        fa, fb = [("e2m1", "e2m1"), ("e4m3", "e4m3"), ("e5m2", "e4m3"), ("e4m3", "e5m2"),
+                  ("e5m2", "e5m2"), ("e2m1", "e2m1")][i % 6]
+        out.append(("mx", i, dict(M=_dim(rng, 600), N=_dim(rng, 600),
+                                  K=32 * int(rng.integers(1, 24)), fa=fa, fb=fb,
+                                  out=str(rng.choice(["f32", "bf16"])))))
+    for i in range(24):
+        D = [32, 64, 128, 256][i % 4]
+        blocks = [(128, 64), (64, 64), (64, 32)] + ([(128, 32)] if D > 32 else [])
+        bm, bn = blocks[int(rng.integers(len(blocks)))]
+        out.append(("attn", i, dict(Z=int(rng.integers(1, 3)), H=int(rng.integers(1, 4)),
+                                    N=bm * int(rng.integers(1, 6)), D=D, bf16=bool(i % 3 == 1),
+                                    causal=bool(rng.random() < 0.5), block=(bm, bn))))
+    for i in range(8):
+        bm = [128, 64][i % 2]
+        out.append(("attn_fp8", i, dict(Z=int(rng.integers(1, 3)), H=int(rng.integers(1, 3)),
+                                        N=bm * int(rng.integers(1, 5)), D=[64, 128][(i // 2) % 2],
+                                        causal=bool(rng.random() < 0.5),
+                                        scale=float(rng.choice([0.3, 0.7, 1.3])),
+                                        block=(bm, 64))))
+    return out
+
+
+CASES = _cases()
+
+
+def _junk_padded(x, seed):
+    """x inside padded storage whose padding (columns and extra rows) is random bytes."""
+    st, _ = padded(x, 0)
+    junk = np.random.default_rng(seed)
+    R, C = x.shape
+    st[:, C:] = junk.integers(-128, 128, size=st[:, C:].shape)
+    st[R:, :] = junk.integers(-128, 128, size=st[R:, :].shape)
+    return st
+
+
+def _codes(rng, shape, fmt):
+    c = rng.integers(0, 256, size=shape).astype(np.uint8)
+    if fmt == "e5m2":
+        return np.where((c & 0x7C) == 0x7C, c & 0x83, c).astype(np.uint8)
+    return np.where((c & 0x7F) == 0x7F, c & 0xF0, c).astype(np.uint8)
+
+
+def _run_i8_i32(gpu, seed, M, N, K, block):
+    import torch
+    a, b = uniform_i8((M, K), seed), uniform_i8((K, N), seed + 1)
+    c = tx.dot(dev_view(_junk_padded(a, seed + 2), (M, K), gpu),
+               dev_view(_junk_padded(b, seed + 3), (K, N), gpu), out_dtype=torch.int32,
+               block=block)
+    torch.cuda.synchronize()
+    exact = a.astype(np.int64) @ b.astype(np.int64)
+    got = from_device(c).astype(np.int64)
+    assert np.array_equal(got, exact), f"{np.count_nonzero(got != exact)} mismatches"
+
+
+def _run_w8a8(gpu, seed, M, N, K, block):
+    import torch
+    a, b = uniform_i8((M, K), seed), uniform_i8((K, N), seed + 1)
+    sa, sb = uniform_scales(M, seed + 2), uniform_scales(N, seed + 3)
+    c = tx.dot(dev_view(_junk_padded(a, seed + 4), (M, K), gpu),
+               dev_view(_junk_padded(b, seed + 5), (K, N), gpu), scale_a=to_device(sa, gpu),
+               scale_b=to_device(sb, gpu), out_dtype=torch.bfloat16, block=block)
+    torch.cuda.synchronize()
+    ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 64, 64),
+                           scale_mode=oracle.SCALE_ROWCOL, sa=sa, sb=sb)
+    got = from_device(c)
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches"
+
+
+def _run_fp8(gpu, seed, M, N, K, fa, fb, block):
+    import torch
+    rng = np.random.default_rng(seed)
+    a, b = _codes(rng, (M, K), fa), _codes(rng, (K, N), fb)
+    nan = {"e4m3": 0x7F, "e5m2": 0x7F}  # NaN codes in both formats
+    tdt = {"e4m3": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}
+    otype = {"e4m3": oracle.F8E4M3, "e5m2": oracle.F8E5M2}
+    pa, _ = padded(a, nan[fa])
+    pb, _ = padded(b, nan[fb])
+    c = tx.dot(dev_view(pa, (M, K), gpu, tdt[fa]), dev_view(pb, (K, N), gpu, tdt[fb]),
+               out_dtype=torch.float32, block=block)
+    torch.cuda.synchronize()
+    ref = oracle.tiled_dot(a, b, a_type=otype[fa], b_type=otype[fb], c_type=oracle.F32,
+                           block=(128, 128, 128))
+    dec = lambda q, f: (oracle.e4m3_to_f32(q) if f == "e4m3"
+                        else oracle.f16_to_f32(q.astype(np.uint16) << 8)).astype(np.float64)
+    rms = lambda q, f: float(np.sqrt(np.mean(dec(q, f) ** 2)))
+    s = math.sqrt(K) * rms(a, fa) * rms(b, fb)
+    check_close(from_device(c), ref, atol=ATOL, rtol=RTOL, scale=s, what="fp8 sweep")
+
+
+def _run_fp8_block(gpu, seed, M, N, K, out, block):
+    import torch
+    qa, qb, sa, sb = fp8_block_inputs(M, N, K, seed)
+    pa, _ = padded(qa, 0x7F)
+    pb, _ = padded(qb, 0x7F)
+    odt = torch.bfloat16 if out == "bf16" else torch.float32
+    c = tx.dot(dev_view(pa, (M, K), gpu, torch.float8_e4m3fn),
+               dev_view(pb, (K, N), gpu, torch.float8_e4m3fn), scale_a=to_device(sa, gpu),
+               scale_b=to_device(sb, gpu), out_dtype=odt, block=block)
+    torch.cuda.synchronize()
+    ct = oracle.BF16 if out == "bf16" else oracle.F32
+    ref = oracle.tiled_dot(qa, qb, a_type=oracle.F8E4M3, c_type=ct, block=(128, 128, 128),
+                           scale_mode=oracle.SCALE_BLOCK128, sa=sa, sb=sb)
+    got = from_device(c)
+    if out == "bf16":
+        got, ref = bits_to_f32(got, "bf16"), bits_to_f32(ref, "bf16")
+    check_close(got, ref, atol=ATOL, rtol=RTOL, scale=math.sqrt(K), what="fp8 block sweep")
+
+
+def _mx_codes_narrow(rng, shape, fmt):
+    """Codes whose products all lie within the scaled MFMA's exact range: the MFMA sums a
+    lane's 32 products in fixed point about 14 bits below the largest, so products spanning
+    fewer bits (e2m1: 2^-2..36; e4m3 / e5m2 with exponents 2^-1..2^1: 8- or 6-bit products
+    within 2^-8..2^4) sum exactly, and the GPU differs from the oracle only by the fp32
+    rounding of the running sum.  Zeros are mixed in."""
+    if fmt == "e2m1":
+        return rng.integers(0, 16, size=shape, dtype=np.uint8)
+    sign = rng.integers(0, 2, size=shape).astype(np.uint8) << 7
+    if fmt == "e4m3":  # exponent field 6..8 (bias 7), 3 mantissa bits
+        c = sign | (rng.integers(6, 9, size=shape).astype(np.uint8) << 3) | \
+            rng.integers(0, 8, size=shape).astype(np.uint8)
+    else:  # e5m2: exponent field 14..16 (bias 15), 2 mantissa bits
+        c = sign | (rng.integers(14, 17, size=shape).astype(np.uint8) << 2) | \
+            rng.integers(0, 4, size=shape).astype(np.uint8)
+    return np.where(rng.random(shape) < 0.05, 0, c).astype(np.uint8)
+
+
+def _run_mx(gpu, seed, M, N, K, fa, fb, out):
+    """MX with exact group sums: the tight bound (K/32 + 4) 2^-24 sum|a b| (the fp32 running
+    sum; one bf16 ulp more for bf16 C) on top of check_mx's bars.  A wrong element in any
+    product (an index or scale-byte error) exceeds it."""
+    from test_mx_gpu import deq_abs, pack
+    rng = np.random.default_rng(seed)
+    ac, bc = _mx_codes_narrow(rng, (M, K), fa), _mx_codes_narrow(rng, (K, N), fb)
+    sa = rng.integers(117, 138, size=(M, K // 32)).astype(np.uint8)
+    sb = rng.integers(117, 138, size=(N, K // 32)).astype(np.uint8)
+    cs = dict(a=pack(ac, 1) if fa == "e2m1" else ac, sa=sa, b=pack(bc, 0) if fb == "e2m1" else bc,
+              sb=sb, ac=ac, bc=bc, fa=fa, fb=fb, K=K)
+    got, ref = run_gpu(gpu, cs, out), ref_of(cs, out)
+    check_mx(got, ref, cs, out, f"mx sweep {fa}x{fb} {M}x{N}x{K}")
+    g = bits_to_f32(got, "bf16") if out == "bf16" else got
+    r = bits_to_f32(ref, "bf16") if out == "bf16" else ref
+    a, b = deq_abs(cs)
+    tight = (K / 32 + 4) * 2.0 ** -24 * (a @ b) + 1e-30
+    if out == "bf16":
+        tight = tight + 2.0 ** -7 * np.abs(r.astype(np.float64))
+    d = np.abs(g.astype(np.float64) - r)
+    assert (d <= tight).all(), (f"mx exact-group sweep: {np.count_nonzero(d > tight)} of {d.size} "
+                                f"beyond the fp32 bound, worst d/bound {(d / tight).max():.3g}")
+
+
+@pytest.mark.parametrize("family,i,case", CASES,
+                         ids=[f"{f}-{i}-" + "-".join(
+                             f"{k}{'x'.join(map(str, v)) if k == 'block' else v}"
+                             for k, v in c.items()) for f, i, c in CASES])
+def test_sweep(gpu, family, i, case):
+    say(f"sweep {family} #{i} {case}")
+    seed = SEED % 1000 + 17 * i
+    c = case
+    if family == "16bit":
+        run16(gpu, c["M"], c["N"], c["K"], c["kind"], c["out"], c["block"], c["kmajor"],
+              seed=seed)
+    elif family == "i8_i32":
+        _run_i8_i32(gpu, seed, c["M"], c["N"], c["K"], c["block"])
+    elif family == "w8a8":
+        _run_w8a8(gpu, seed, c["M"], c["N"], c["K"], c["block"])
+    elif family == "fp8":
+        _run_fp8(gpu, seed, c["M"], c["N"], c["K"], c["fa"], c["fb"], c["block"])
+    elif family == "fp8_block":
+        _run_fp8_block(gpu, seed, c["M"], c["N"], c["K"], c["out"], c["block"])
+    elif family == "mx":
+        _run_mx(gpu, seed, c["M"], c["N"], c["K"], c["fa"], c["fb"], c["out"])
+    elif family == "attn":
+        attn_vs_oracle(gpu, c["block"], c["causal"], c["Z"], c["H"], c["N"], c["D"], c["bf16"])
+    elif family == "attn_fp8":
+        q, k, v = e5m2_qkv(c["Z"], c["H"], c["N"], c["D"], seed=seed)
+        o, M = run_gpu_fp8(gpu, q, k, v, c["causal"], c["scale"], block=c["block"])
+        ro, rM = oracle.attn_fwd(q, k, v, sm_scale=c["scale"], causal=c["causal"],
+                                 block=c["block"], dtype=oracle.F8E5M2)
+        check_e5m2(o, M, ro, rM, (q, k, v), c["scale"], c["causal"], f"attn fp8 sweep {c}")
+    else:
+        raise AssertionError(family)

@@ -207,7 +207,9 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
     or N) raises NotImplementedError.  acc (fp32 [M, N]) returns acc + the
     dot, as tl.dot_scaled's acc does.  Scales given as torch.float8_e4m3fn
     are e4m3 multipliers per 16 K ([M, K/16], [N, K/16]; Triton's fp8e4nv
-    scales): e2m1 (or bf16) operands, run through a bf16 upcast.
+    scales): e2m1 (or bf16) operands, run through a bf16 upcast.  As in
+    dot(), operands whose rows do not start 16 bytes apart are copied to
+    padded storage first.
     """
     import torch
     for name, fmt in (("lhs_format", lhs_format), ("rhs_format", rhs_format)):
@@ -261,6 +263,8 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
             raise ValueError(f"{nm} must be a contiguous uint8 (e8m0) or float8_e4m3fn tensor")
     if lhs.stride(1) != 1 or rhs.stride(1) != 1:
         raise ValueError("lhs and rhs rows must be contiguous")
+    if plan is None:
+        lhs, rhs = aligned_rows(lhs), aligned_rows(rhs)
     flags = 0
     if acc is not None:  # acc + dot, in a new tensor (or `out`), as tl.dot_scaled(acc=)
         if out is None:
