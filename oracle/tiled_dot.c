@@ -338,7 +338,7 @@ static int dot_scaled_impl(const void *Av, const void *Bv, void *Cv, const uint8
                            int round_mode, int nthreads, int nv) {
   const uint8_t *A = (const uint8_t *)Av, *B = (const uint8_t *)Bv;
   uint8_t *C = (uint8_t *)Cv;
-  if (M < 0 || N < 0 || K < 0 || K % 32)
+  if (M < 0 || N < 0 || K < 0 || K % (nv ? 16 : 32))
     return -1;
   /* e4m3 scales per 16 (nv): e2m1 sides only, both upcast to bf16 */
   const int mixed = a_fmt == OR_BF16 || b_fmt == OR_BF16 || nv;
@@ -412,7 +412,7 @@ int oracle_dot_scaled(const void *Av, const void *Bv, void *Cv, const uint8_t *s
 }
 
 /* The same with e4m3 scales, one per 16 K (tl.dot_scaled's fp8e4nv scale
- * tensors, T:language/semantic.py:1597-1609): sa [M][K/16], sb [N][K/16],
+ * tensors, T:language/semantic.py:1597-1609), K % 16 == 0: sa [M][K/16], sb [N][K/16],
  * each element x * decode_e4m3(s), e2m1 (or bf16) operands, both upcast to
  * bf16 -- exact for e2m1 times e4m3 -- then the products summed as above. */
 int oracle_dot_scaled_nv16(const void *Av, const void *Bv, void *Cv, const uint8_t *sa,

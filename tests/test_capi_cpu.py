@@ -160,9 +160,10 @@ def test_plan_validation():
     p = tx.plan(tx.make_desc(64, 61, 68, tx.BF16, tx.BF16, lda=72, ldb=64, ldc=64))
     assert p.kernel == tx.KERNEL_GEMM_16BIT and p.k_tail == 68 % p.desc.block_k
     assert _err(tx.make_desc(64, 61, 68, tx.BF16, tx.BF16, lda=72)) == tx.ERR_INVALID  # ldb 61
-    # the upcast of an MX B operand takes columns in blocks of 16
-    assert _err(tx.make_desc(64, 72, 64, tx.BF16, tx.F32, b_type=tx.F8E4M3, ldb=80,
-                             scale_mode=tx.SCALE_MX32)) == tx.ERR_UNSUPPORTED
+    # an upcast MX B operand may have any N: its bf16 rows are N rounded up to 16 columns
+    p = tx.plan(tx.make_desc(64, 72, 64, tx.BF16, tx.F32, b_type=tx.F8E4M3, ldb=80,
+                             scale_mode=tx.SCALE_MX32))
+    assert p.kernel == tx.KERNEL_GEMM_MX_BF16 and p.workspace_bytes == 64 * 80 * 2
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.I32)) == tx.ERR_UNSUPPORTED
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, b_type=tx.F16)) == tx.ERR_UNSUPPORTED
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, block=(96, 64, 64))) == tx.ERR_UNSUPPORTED

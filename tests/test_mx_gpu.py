@@ -233,7 +233,8 @@ def mx_bf16_case(M, N, K, side, fmt, seed):
 @pytest.mark.parametrize("side,fmt", [("b", "e2m1"), ("b", "e4m3"), ("b", "e5m2"),
                                       ("a", "e2m1"), ("a", "e4m3")])
 @pytest.mark.parametrize("out", ["f32", "bf16"])
-@pytest.mark.parametrize("M,N,K", [(300, 272, 416), (512, 512, 1024), (16, 1024, 256)])
+@pytest.mark.parametrize("M,N,K", [(300, 272, 416), (512, 512, 1024), (16, 1024, 256),
+                                   (64, 250, 256)])
 def test_mx_bf16_vs_oracle(gpu, side, fmt, out, M, N, K):
     """dot_scaled with one bf16 operand against the oracle (upcast, then
     exact products rounded once): |d| <= K 2^-24 sum |a b| (fp32 summation)
@@ -314,7 +315,7 @@ def test_mx_bf16_scale_range_bit_identity(gpu, side, fmt):
 # --- e4m3 scales per 16 K (tl.dot_scaled's fp8e4nv scales) ------------------
 
 @pytest.mark.parametrize("lhs,rhs", [("e2m1", "e2m1"), ("bf16", "e2m1"), ("e2m1", "bf16")])
-@pytest.mark.parametrize("M,N,K", [(300, 272, 416), (512, 512, 1024)])
+@pytest.mark.parametrize("M,N,K", [(300, 272, 416), (512, 512, 1024), (40, 250, 48)])
 def test_nv16_vs_oracle(gpu, lhs, rhs, M, N, K):
     """e2m1 operands with e4m3 scales per 16 K, upcast to bf16 (exact) and
     run on the bf16 tile: bit for bit the bf16 dot of the host upcast, and

@@ -303,3 +303,26 @@ def test_nv16_power_of_two_scales_equal_mx32():
     c15 = oracle.dot_scaled(a, np.full_like(nv_a, 0x3C), oracle.F4E2M1, b,
                             np.full_like(nv_b, 0x38), oracle.F4E2M1, K=K, nv16=True)
     assert np.array_equal(c15, (c1.astype(np.float64) * 1.5).astype(np.float32))
+
+
+@pytest.mark.parametrize("K", [16, 48, 80])
+def test_nv16_k_a_multiple_of_16(K):
+    """e4m3 scales per 16 need K % 16 == 0 only (an odd number of 16-groups included):
+    the oracle equals a float64 brute force of decode(e2m1) * decode(e4m3 scale) per 16,
+    summed and rounded once to fp32, bit for bit."""
+    import torch
+    rng = np.random.default_rng(K)
+    M, N = 5, 7
+    ac = rng.integers(0, 16, size=(M, K)).astype(np.uint8)
+    bc = rng.integers(0, 16, size=(K, N)).astype(np.uint8)
+    a = (ac[:, 0::2] | (ac[:, 1::2] << 4)).astype(np.uint8)
+    b = (bc[0::2] | (bc[1::2] << 4)).astype(np.uint8)
+    sa = rng.integers(0x20, 0x50, size=(M, K // 16)).astype(np.uint8)
+    sb = rng.integers(0x20, 0x50, size=(N, K // 16)).astype(np.uint8)
+    got = oracle.dot_scaled(a, sa, oracle.F4E2M1, b, sb, oracle.F4E2M1, K=K, nv16=True)
+    dec4 = lambda c: torch.from_numpy(c).view(torch.float8_e4m3fn).double().numpy()
+    g = np.arange(K) // 16
+    fa = oracle.mx_decode(ac, oracle.F4E2M1) * dec4(sa)[:, g]
+    fb = oracle.mx_decode(bc, oracle.F4E2M1) * dec4(sb)[:, g].T
+    want = (fa @ fb).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

@@ -25,6 +25,7 @@ import triton_ext_amd as tx
 from dotcase import (bits_to_f32, check_close, fp8_block_inputs, from_device, say, to_device,
                      uniform_i8, uniform_scales)
 from test_attn_gpu import attn_vs_oracle, check_e5m2, e5m2_qkv, run_gpu_fp8
+import test_mx_gpu
 from test_mx_gpu import check_mx, ref_of, run_gpu
 from test_tails_gpu import dev_view, padded, run16
 
@@ -81,6 +82,16 @@ def _cases():
         out.append(("mx", i, dict(M=_dim(rng, 600), N=_dim(rng, 600),
                                   K=32 * int(rng.integers(1, 24)), fa=fa, fb=fb,
                                   out=str(rng.choice(["f32", "bf16"])))))
+    for i in range(12):
+        side, fmt = [("b", "e2m1"), ("b", "e4m3"), ("b", "e5m2"), ("a", "e2m1"), ("a", "e4m3"),
+                     ("a", "e5m2")][i % 6]
+        out.append(("mx_bf16", i, dict(M=_dim(rng, 600), N=_dim(rng, 600),
+                                       K=32 * int(rng.integers(1, 24)), side=side, fmt=fmt,
+                                       out=str(rng.choice(["f32", "bf16"])))))
+    for i in range(9):
+        lhs, rhs = [("e2m1", "e2m1"), ("bf16", "e2m1"), ("e2m1", "bf16")][i % 3]
+        out.append(("nv16", i, dict(M=_dim(rng, 600), N=_dim(rng, 600),
+                                    K=16 * int(rng.integers(1, 48)), lhs=lhs, rhs=rhs)))
     for i in range(24):
         D = [32, 64, 128, 256][i % 4]
         blocks = [(128, 64), (64, 64), (64, 32)] + ([(128, 32)] if D > 32 else [])
@@ -247,6 +258,10 @@ def test_sweep(gpu, family, i, case):
         _run_fp8_block(gpu, seed, c["M"], c["N"], c["K"], c["out"], c["block"])
     elif family == "mx":
         _run_mx(gpu, seed, c["M"], c["N"], c["K"], c["fa"], c["fb"], c["out"])
+    elif family == "mx_bf16":  # the upcast path, bit for bit against the host upcast
+        test_mx_gpu.test_mx_bf16_vs_oracle(gpu, c["side"], c["fmt"], c["out"], c["M"], c["N"], c["K"])
+    elif family == "nv16":
+        test_mx_gpu.test_nv16_vs_oracle(gpu, c["lhs"], c["rhs"], c["M"], c["N"], c["K"])
     elif family == "attn":
         attn_vs_oracle(gpu, c["block"], c["causal"], c["Z"], c["H"], c["N"], c["D"], c["bf16"])
     elif family == "attn_fp8":

@@ -210,11 +210,14 @@ int mxUpcastSide(const tx_dot_desc &d) {
   return 0;
 }
 
-// Workspace of the upcast form: the MX operand as bf16, 256-byte aligned.
+// Workspace of the upcast form: the MX operand as bf16, 256-byte aligned;
+// an upcast B's rows hold N rounded up to 16 columns (16-byte aligned rows
+// for the bf16 tile, zeros past N).
+int64_t mxUpcastLdB(const tx_dot_desc &d) { return cdiv(d.N, 16) * 16; }
 int64_t mxUpcastWorkspace(const tx_dot_desc &d) {
   const int side = mxUpcastSide(d);
   const int64_t a = (side & 1) ? (d.M * d.K * 2 + 255) / 256 * 256 : 0;
-  const int64_t b = (side & 2) ? (d.K * d.N * 2 + 255) / 256 * 256 : 0;
+  const int64_t b = (side & 2) ? (d.K * mxUpcastLdB(d) * 2 + 255) / 256 * 256 : 0;
   return a + b; // A's upcast first, then B's
 }
 
@@ -454,11 +457,7 @@ int validate(const tx_dot_desc *in, tx_dot_desc *d) {
     return fail(TX_ERR_INVALID, "A/B/C row strides must be multiples of 16 bytes");
   // K and N may be any size (tl.load's mask covers every element): the
   // kernels load the 16-byte chunk that crosses K or N whole and zero or drop
-  // its elements past the edge.  The upcast kernels of the bf16-side
-  // dot_scaled forms take B in blocks of 16 columns.
-  if (mxUpcastSide(*d) & 2 && d->N % 16)
-    return fail(TX_ERR_UNSUPPORTED, "an upcast B operand needs N %% 16 == 0 (got N=%lld)",
-                (long long)d->N);
+  // its elements past the edge.
   if (d->scale_mode == TX_SCALE_MX32) {
     if (d->K % 32)
       return fail(TX_ERR_UNSUPPORTED, "MX scales need K %% 32 == 0 (one e8m0 per 32)");
@@ -631,6 +630,7 @@ int launchMxUpcast(const tx_dot_plan &plan, const void *A, const void *B, void *
     u.src = static_cast<const uint8_t *>(one == 2 ? B : A);
     u.scale = static_cast<const uint8_t *>(one == 2 ? sb : sa);
     u.dst = one == 2 ? wb : wa;
+    u.ld_dst = one == 2 ? mxUpcastLdB(d) : d.K;
     u.ld_scale = d.K / (nv ? 16 : 32);
     u.fmt = fmt;
     int64_t threads;
@@ -639,7 +639,7 @@ int launchMxUpcast(const tx_dot_plan &plan, const void *A, const void *B, void *
       u.rows = d.K;
       u.cols = d.N;
       u.ld_src = d.ldb; // fp8: bytes per row; e2m1: bytes per packed row
-      threads = (d.K / 8) * (d.N / 16); // 16 columns x 8 K rows per thread
+      threads = (d.K / 8) * cdiv(d.N, 16); // 16 columns x 8 K rows per thread
       fn = nv ? txk::mx_upcast_b_kernel<4, true>
               : fmt == 0 ? txk::mx_upcast_b_kernel<0> : fmt == 1 ? txk::mx_upcast_b_kernel<1>
                                                      : txk::mx_upcast_b_kernel<4>;
@@ -674,7 +674,7 @@ int launchMxUpcast(const tx_dot_plan &plan, const void *A, const void *B, void *
   g.desc.b_type = TX_BF16;
   g.desc.scale_mode = TX_SCALE_NONE;
   if (side & 2)
-    g.desc.ldb = d.N;
+    g.desc.ldb = mxUpcastLdB(d);
   if (side & 1)
     g.desc.lda = d.K;
   g.kernel = TX_KERNEL_GEMM_16BIT;

@@ -16,7 +16,10 @@
 // Layouts (elements row-major, e2m1 packed two per byte along K, even K in
 // the low nibble):
 //   B side: src [K][N] (e2m1: [K/2][N] bytes, ld = bytes per packed row),
-//           scales [N][K/32]; dst bf16 [K][N], ld N.
+//           scales [N][K/32]; dst bf16 [K][N], ld N rounded up to 16.  A
+//           thread takes 16 columns; in the group that crosses N it reads
+//           only the bytes and scales of columns < N and writes zeros past
+//           N (the bf16 tile drops those columns).
 //   A side: src [M][K] (e2m1: [M][K/2] bytes), scales [M][K/32]; dst bf16
 //           [M][K], ld K.  A thread takes 16 K of one row (one scale).
 // The job is streaming (read codes, write 2 bytes per element): HBM-bound,
@@ -32,8 +35,9 @@ struct UpcastArgs {
   const uint8_t *scale;
   uint16_t *dst;
   int64_t rows, cols; // of the dst (B side: K x N; A side: M x K)
+  int64_t ld_dst;     // dst elements per row (B side: N rounded up to 16; A side: K)
   int64_t ld_src;     // bytes per src row (e2m1 B: per packed row)
-  int64_t ld_scale;   // K / 32
+  int64_t ld_scale;   // K / 32 (K / 16 for e4m3 scales)
   int32_t fmt;        // 0 e4m3, 1 e5m2, 4 e2m1 (MFMA format codes)
 };
 
@@ -114,33 +118,56 @@ __global__ void __launch_bounds__(256) mx_upcast_b_kernel(UpcastArgs p) {
   constexpr int COLS = 16;              // columns per thread
   constexpr int RUN = FMT == 4 ? 4 : 8; // source rows per thread (8 K)
   constexpr int KR = FMT == 4 ? 2 : 1;  // K rows per source row
-  const int64_t groups = p.cols / COLS;
+  const int64_t groups = (p.cols + COLS - 1) / COLS;
   const int64_t srows = p.rows / KR; // source rows
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (srows / RUN) * groups)
     return;
   const int64_t r0 = (t / groups) * RUN, n0 = (t % groups) * COLS;
   const int64_t kg = r0 * KR / SK::GROUP; // the scale group of all RUN rows
+  // valid columns of this group: COLS except in the group that crosses N
+  const int ncol = p.cols - n0 < COLS ? (int)(p.cols - n0) : COLS;
   uint32_t sc[COLS];
   bool hw = true;
 #pragma unroll
   for (int i = 0; i < COLS; ++i) {
-    sc[i] = p.scale[(n0 + i) * p.ld_scale + kg];
+    sc[i] = p.scale[(n0 + (i < ncol ? i : 0)) * p.ld_scale + kg];
     hw = hw && SK::hw(sc[i]);
   }
   uint32_t w[RUN][COLS / 4]; // source dwords: row r, columns 4 q .. +3
+  if (ncol == COLS) {
 #pragma unroll
-  for (int r = 0; r < RUN; ++r) {
-    const u32x4 v = *reinterpret_cast<const u32x4 *>(p.src + (r0 + r) * p.ld_src + n0);
+    for (int r = 0; r < RUN; ++r) {
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(p.src + (r0 + r) * p.ld_src + n0);
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      w[r][q] = v[q];
+      for (int q = 0; q < 4; ++q)
+        w[r][q] = v[q];
+    }
+  } else { // the bytes of columns < N only (the row may end at N)
+#pragma unroll
+    for (int r = 0; r < RUN; ++r)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t x = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          if (4 * q + b < ncol)
+            x |= (uint32_t)p.src[(r0 + r) * p.ld_src + n0 + 4 * q + b] << (8 * b);
+        w[r][q] = x;
+      }
   }
+  // bf16 pair words of columns >= N (in the crossing group) become zero
+  uint32_t keep[COLS / 2];
+#pragma unroll
+  for (int c = 0; c < COLS; c += 2)
+    keep[c / 2] = (c < ncol ? 0xFFFFu : 0u) | (c + 1 < ncol ? 0xFFFF0000u : 0u);
   auto store_row = [&](int64_t k, const uint32_t (&o)[COLS / 2]) {
-    uint16_t *d = p.dst + k * p.cols + n0;
+    uint16_t *d = p.dst + k * p.ld_dst + n0;
 #pragma unroll
     for (int q = 0; q < COLS / 8; ++q)
-      reinterpret_cast<u32x4 *>(d)[q] = u32x4{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
+      reinterpret_cast<u32x4 *>(d)[q] =
+          u32x4{o[4 * q] & keep[4 * q], o[4 * q + 1] & keep[4 * q + 1],
+                o[4 * q + 2] & keep[4 * q + 2], o[4 * q + 3] & keep[4 * q + 3]};
   };
   if (hw) {
     float sf[COLS];
@@ -227,7 +254,7 @@ __global__ void __launch_bounds__(256) mx_upcast_a_kernel(UpcastArgs p) {
   else
     *reinterpret_cast<u32x4 *>(code) =
         *reinterpret_cast<const u32x4 *>(p.src + m * p.ld_src + k0);
-  uint16_t *d = p.dst + m * p.cols + k0;
+  uint16_t *d = p.dst + m * p.ld_dst + k0;
   if (SK::hw(s)) {
     // neighbouring K share the scale: pairs convert in place (see mx_cvt_pair)
     const float sf = SK::factor(s);
