@@ -25,6 +25,7 @@ import triton_ext_amd as tx
 from dotcase import (bits_to_f32, check_close, fp8_block_inputs, from_device, say, to_device,
                      uniform_i8, uniform_scales)
 from test_attn_gpu import attn_vs_oracle, check_e5m2, e5m2_qkv, run_gpu_fp8
+import test_dot_gpu
 import test_mx_gpu
 from test_mx_gpu import check_mx, ref_of, run_gpu
 from test_tails_gpu import dev_view, padded, run16
@@ -92,6 +93,26 @@ def _cases():
         lhs, rhs = [("e2m1", "e2m1"), ("bf16", "e2m1"), ("e2m1", "bf16")][i % 3]
         out.append(("nv16", i, dict(M=_dim(rng, 600), N=_dim(rng, 600),
                                     K=16 * int(rng.integers(1, 48)), lhs=lhs, rhs=rhs)))
+    # larger grids: tile counts that are not multiples of the 8 XCDs, long K loops
+    big = lambda: int(rng.integers(700, 3001))
+    for i in range(6):
+        kind = ["bf16", "f16"][i % 2]
+        out.append(("16bit", 100 + i, dict(M=big(), N=big(), K=big(), kind=kind,
+                                           out=["f32", kind][(i // 2) % 2], block=(0, 0, 0),
+                                           kmajor=i % 3 == 2)))
+    for i in range(4):
+        out.append(("i8_i32", 100 + i, dict(M=big(), N=big(), K=big(), block=tiles8[i % 4])))
+    for i in range(4):
+        out.append(("fp8_block", 100 + i, dict(M=big(), N=big(), K=big(), out="bf16",
+                                               block=tiles8[i % 4])))
+    for i in range(4):
+        out.append(("w8a8", 100 + i, dict(M=int(rng.integers(1, 257)),
+                                          N=int(rng.integers(3000, 9001)),
+                                          K=int(rng.integers(3000, 9001)), block=(0, 0, 0))))
+    # tl.dot(a, b, acc): the plain result plus acc in one addition, bit for bit
+    for i in range(8):
+        out.append(("acc", i, dict(kind=["bf16", "f16", "i8", "f8"][i % 4], M=_dim(rng, 700),
+                                   N=_dim(rng, 700), K=_dim(rng, 700))))
     for i in range(24):
         D = [32, 64, 128, 256][i % 4]
         blocks = [(128, 64), (64, 64), (64, 32)] + ([(128, 32)] if D > 32 else [])
@@ -106,6 +127,10 @@ def _cases():
                                         causal=bool(rng.random() < 0.5),
                                         scale=float(rng.choice([0.3, 0.7, 1.3])),
                                         block=(bm, 64))))
+    for i in range(4):
+        out.append(("attn", 100 + i, dict(Z=1, H=2, N=128 * int(rng.integers(6, 17)),
+                                          D=[64, 128][i % 2], bf16=i >= 2, causal=i % 2 == 0,
+                                          block=(128, 64))))
     return out
 
 
@@ -136,7 +161,8 @@ def _run_i8_i32(gpu, seed, M, N, K, block):
                dev_view(_junk_padded(b, seed + 3), (K, N), gpu), out_dtype=torch.int32,
                block=block)
     torch.cuda.synchronize()
-    exact = a.astype(np.int64) @ b.astype(np.int64)
+    # float64 products and sums are exact here (|sum| <= 127^2 K < 2^53), and BLAS-fast
+    exact = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.int64)
     got = from_device(c).astype(np.int64)
     assert np.array_equal(got, exact), f"{np.count_nonzero(got != exact)} mismatches"
 
@@ -262,6 +288,8 @@ def test_sweep(gpu, family, i, case):
         test_mx_gpu.test_mx_bf16_vs_oracle(gpu, c["side"], c["fmt"], c["out"], c["M"], c["N"], c["K"])
     elif family == "nv16":
         test_mx_gpu.test_nv16_vs_oracle(gpu, c["lhs"], c["rhs"], c["M"], c["N"], c["K"])
+    elif family == "acc":
+        test_dot_gpu.test_accumulate(gpu, c["kind"], c["M"], c["N"], c["K"])
     elif family == "attn":
         attn_vs_oracle(gpu, c["block"], c["causal"], c["Z"], c["H"], c["N"], c["D"], c["bf16"])
     elif family == "attn_fp8":
