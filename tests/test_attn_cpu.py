@@ -241,13 +241,16 @@ def test_attn_plan():
             tx.attn_plan(**a)
         return e.value.code
     assert err(head_dim=96) == tx.ERR_UNSUPPORTED
-    # head dims: the tutorial's {16, 32, 64, 128, 256}; 32 .. 256 for fp16 / bf16, 64 and 128
-    # for fp8; a K block must fill one 1 KiB load per wave
-    for hd in (32, 64, 128, 256):
+    # head dims: the tutorial's {16, 32, 64, 128, 256} for fp16 / bf16, 64 and 128 for fp8; a
+    # K block (head dim 16 staged as 32) must fill one 1 KiB load per wave
+    for hd in (16, 32, 64, 128, 256):
         for blk in ((128, 64), (64, 64), (64, 32)) + (((128, 32),) if hd > 32 else ()):
             assert tx.attn_plan(1, 1, 256, hd, True, 0.5, dtype=tx.BF16, block=blk).desc.head_dim == hd
     assert err(head_dim=32, block=(128, 32)) == tx.ERR_UNSUPPORTED
-    assert err(head_dim=16) == tx.ERR_UNSUPPORTED
+    assert err(head_dim=16, block=(128, 32)) == tx.ERR_UNSUPPORTED
+    assert tx.attn_plan(1, 1, 256, 16, False, 0.5).flops == 4 * 256 ** 2 * 16
+    assert err(head_dim=8) == tx.ERR_UNSUPPORTED
+    assert err(head_dim=16, dtype=tx.F8E5M2) == tx.ERR_UNSUPPORTED
     assert err(head_dim=256, dtype=tx.F8E5M2) == tx.ERR_UNSUPPORTED
     assert err(head_dim=32, dtype=tx.F8E5M2) == tx.ERR_UNSUPPORTED
     assert err(N_CTX=200) == tx.ERR_UNSUPPORTED
@@ -290,3 +293,15 @@ def test_attention_argument_checks():
         tx.attention(q8, q8, q8, True, 0.5)
     with pytest.raises(ValueError, match="share one"):
         tx.attention(q, q[:, :1], q, True, 0.5)
+
+
+def test_attention_signature_is_the_tutorials():
+    """attention(q, k, v, causal, sm_scale, USE_TMA=True) as the tutorial's
+    _attention.forward (R:pass/LoopSplit/06-fused-attention.py:583): a sixth
+    positional argument is USE_TMA, and this build's extras are keyword-only."""
+    import inspect
+    ps = list(inspect.signature(tx.attention).parameters.values())
+    assert [p.name for p in ps[:6]] == ["q", "k", "v", "causal", "sm_scale", "USE_TMA"]
+    assert ps[5].default is True
+    assert all(p.kind == p.KEYWORD_ONLY for p in ps[6:])
+    assert {p.name for p in ps[6:]} == {"return_lse", "plan", "stream", "block"}

@@ -67,6 +67,12 @@ def test_tutorial_test_op(gpu):
     ref = torch.matmul(p, vt).half()
     got = torch.from_numpy(o.view(np.float16))
     assert torch.allclose(ref, got, atol=1e-2, rtol=0)
+    # the tutorial's positional USE_TMA: one tensor back, the same bits
+    qd, kd, vd = (to_device(x, gpu).view(torch.float16) for x in (q, k, v))
+    o2 = tx.attention(qd, kd, vd, True, 0.5, True)
+    torch.cuda.synchronize()
+    assert isinstance(o2, torch.Tensor)
+    assert np.array_equal(from_device(o2.view(torch.int16)).view(np.uint16), o)
 
 
 @pytest.mark.parametrize("causal", [True, False])
@@ -110,11 +116,13 @@ def test_attn_blocks_vs_oracle(gpu, block, causal, Z, H, N, D, bf16):
 @pytest.mark.parametrize("block", [(128, 64), (128, 32), (64, 64), (64, 32)])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("Z,H,N,D,bf16", [(2, 2, 256, 32, False), (1, 3, 192, 32, True),
-                                          (1, 2, 256, 256, False), (2, 1, 192, 256, True)])
-def test_attn_head_dims_32_and_256(gpu, block, causal, Z, H, N, D, bf16):
+                                          (1, 2, 256, 256, False), (2, 1, 192, 256, True),
+                                          (2, 2, 256, 16, False), (1, 3, 192, 16, True)])
+def test_attn_head_dims_16_32_and_256(gpu, block, causal, Z, H, N, D, bf16):
     """Head dims 32 and 256 (64- and 512-byte K/V rows, their own swizzles; 256 reads its
-    fragments in groups) at every block shape the plan accepts."""
-    if D == 32 and block == (128, 32):
+    fragments in groups), and 16 (staged as 32 with zero dims past 16, O's not stored), at
+    every block shape the plan accepts."""
+    if D <= 32 and block == (128, 32):
         pytest.skip("a 2 KiB K block for four waves: rejected at plan time")
     attn_vs_oracle(gpu, block, causal, Z, H, N, D, bf16)
 

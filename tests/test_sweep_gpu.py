@@ -113,8 +113,8 @@ def _cases():
     for i in range(8):
         out.append(("acc", i, dict(kind=["bf16", "f16", "i8", "f8"][i % 4], M=_dim(rng, 700),
                                    N=_dim(rng, 700), K=_dim(rng, 700))))
-    for i in range(24):
-        D = [32, 64, 128, 256][i % 4]
+    for i in range(30):
+        D = [16, 32, 64, 128, 256][i % 5]
         blocks = [(128, 64), (64, 64), (64, 32)] + ([(128, 32)] if D > 32 else [])
         bm, bn = blocks[int(rng.integers(len(blocks)))]
         out.append(("attn", i, dict(Z=int(rng.integers(1, 3)), H=int(rng.integers(1, 4)),

@@ -852,10 +852,10 @@ extern "C" TX_API int tx_dot_launch_noalloc(const tx_dot_plan *plan, const void 
 namespace {
 
 // The 16-bit attention kernel for one configuration, or nullptr where a K
-// block is smaller than one 1 KiB load per wave (head dim 32 with 128 x 32
-// blocks), which the plan rejects.
+// block is smaller than one 1 KiB load per wave (head dims 16 and 32, whose
+// blocks are staged as 32, with 128 x 32 blocks), which the plan rejects.
 template <bool C, int HD, bool BF, int BM, int BN> constexpr void (*attnKernel())(txk::AttnArgs) {
-  if constexpr (HD * 2 * BN >= 1024 * (BM / 32))
+  if constexpr ((HD < 32 ? 32 : HD) * 2 * BN >= 1024 * (BM / 32))
     return txk::attn_fwd_kernel<C, HD, BF, BM, BN>;
   else
     return nullptr;
@@ -897,10 +897,10 @@ extern "C" TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *p
     return fail(TX_ERR_UNSUPPORTED, "dtype %d: fp16, bf16 and fp8 e5m2 q/k/v/o are implemented",
                 d.dtype);
   if (d.dtype == TX_F8E5M2 ? d.head_dim != 64 && d.head_dim != 128
-                           : d.head_dim != 32 && d.head_dim != 64 && d.head_dim != 128 &&
-                                 d.head_dim != 256)
+                           : d.head_dim != 16 && d.head_dim != 32 && d.head_dim != 64 &&
+                                 d.head_dim != 128 && d.head_dim != 256)
     return fail(TX_ERR_UNSUPPORTED, "head_dim %d: %s are implemented", d.head_dim,
-                d.dtype == TX_F8E5M2 ? "64 and 128 (fp8)" : "32, 64, 128 and 256");
+                d.dtype == TX_F8E5M2 ? "64 and 128 (fp8)" : "16, 32, 64, 128 and 256");
   if (d.block_m == 0) d.block_m = 128;
   if (d.block_n == 0) d.block_n = 64;
   if ((d.block_m != 64 && d.block_m != 128) || (d.block_n != 32 && d.block_n != 64))
@@ -908,11 +908,12 @@ extern "C" TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *p
                 "are implemented", d.block_m, d.block_n);
   if (d.dtype == TX_F8E5M2 && d.block_n != 64)
     return fail(TX_ERR_UNSUPPORTED, "fp8 e5m2 attention: BLOCK_N 64 is implemented");
-  // A K or V block (BLOCK_N rows of HEAD_DIM elements) is staged by whole
-  // 1 KiB loads, at least one per wave.
-  if (d.dtype != TX_F8E5M2 && (int64_t)d.block_n * d.head_dim * 2 < 1024 * (d.block_m / 32))
+  // A K or V block (BLOCK_N rows of HEAD_DIM elements; head dim 16 staged as
+  // 32) is staged by whole 1 KiB loads, at least one per wave.
+  const int staged_dim = d.head_dim < 32 ? 32 : d.head_dim;
+  if (d.dtype != TX_F8E5M2 && (int64_t)d.block_n * staged_dim * 2 < 1024 * (d.block_m / 32))
     return fail(TX_ERR_UNSUPPORTED, "head_dim %d with blocks %dx%d: a K block of %d bytes for "
-                "%d waves", d.head_dim, d.block_m, d.block_n, d.block_n * d.head_dim * 2,
+                "%d waves", d.head_dim, d.block_m, d.block_n, d.block_n * staged_dim * 2,
                 d.block_m / 32);
   if (d.N_CTX % d.block_m)
     return fail(TX_ERR_UNSUPPORTED, "N_CTX %lld is not a multiple of %d (whole blocks only)",
@@ -956,7 +957,8 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
   const bool bm64 = d.block_m == 64, bn32 = d.block_n == 32;
   if ((d.block_m != 64 && d.block_m != 128) || (d.block_n != 32 && d.block_n != 64) ||
       (d.dtype == TX_F8E5M2 && bn32) || plan->block_threads != d.block_m / 32 * 64 ||
-      (d.head_dim != 32 && d.head_dim != 64 && d.head_dim != 128 && d.head_dim != 256) ||
+      (d.head_dim != 16 && d.head_dim != 32 && d.head_dim != 64 && d.head_dim != 128 &&
+       d.head_dim != 256) ||
       (d.dtype == TX_F8E5M2 && d.head_dim != 64 && d.head_dim != 128) ||
       (d.dtype != TX_F16 && d.dtype != TX_BF16 && d.dtype != TX_F8E5M2) || d.N_CTX % d.block_m ||
       plan->m_blocks != d.N_CTX / d.block_m || plan->grid_x != d.Z * d.H * plan->m_blocks)
@@ -982,12 +984,12 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
   {{attnKernel<C, HD, BF, 128, 64>(), attnKernel<C, HD, BF, 128, 32>()},                    \
    {attnKernel<C, HD, BF, 64, 64>(), attnKernel<C, HD, BF, 64, 32>()}}
 #define TX_ATTN_DTYPES(C, HD) {TX_ATTN_BLOCKS(C, HD, false), TX_ATTN_BLOCKS(C, HD, true)}
-  // [causal][head_dim 32 / 64 / 128 / 256][bf16][BLOCK_M 64][BLOCK_N 32]
-  static const AttnFn kAttn[2][4][2][2][2] = {
-      {TX_ATTN_DTYPES(false, 32), TX_ATTN_DTYPES(false, 64), TX_ATTN_DTYPES(false, 128),
-       TX_ATTN_DTYPES(false, 256)},
-      {TX_ATTN_DTYPES(true, 32), TX_ATTN_DTYPES(true, 64), TX_ATTN_DTYPES(true, 128),
-       TX_ATTN_DTYPES(true, 256)}};
+  // [causal][head_dim 16 / 32 / 64 / 128 / 256][bf16][BLOCK_M 64][BLOCK_N 32]
+  static const AttnFn kAttn[2][5][2][2][2] = {
+      {TX_ATTN_DTYPES(false, 16), TX_ATTN_DTYPES(false, 32), TX_ATTN_DTYPES(false, 64),
+       TX_ATTN_DTYPES(false, 128), TX_ATTN_DTYPES(false, 256)},
+      {TX_ATTN_DTYPES(true, 16), TX_ATTN_DTYPES(true, 32), TX_ATTN_DTYPES(true, 64),
+       TX_ATTN_DTYPES(true, 128), TX_ATTN_DTYPES(true, 256)}};
 #undef TX_ATTN_DTYPES
 #undef TX_ATTN_BLOCKS
   // [causal][head_dim 128][BLOCK_M 64]
@@ -997,7 +999,11 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
       {{txk::attn_fwd8_kernel<true, 64, 128>, txk::attn_fwd8_kernel<true, 64, 64>},
        {txk::attn_fwd8_kernel<true, 128, 128>, txk::attn_fwd8_kernel<true, 128, 64>}}};
   const int c = d.causal ? 1 : 0;
-  const int hd = d.head_dim == 32 ? 0 : d.head_dim == 64 ? 1 : d.head_dim == 128 ? 2 : 3;
+  const int hd = d.head_dim == 16    ? 0
+                 : d.head_dim == 32  ? 1
+                 : d.head_dim == 64  ? 2
+                 : d.head_dim == 128 ? 3
+                                     : 4;
   const AttnFn fn = d.dtype == TX_F8E5M2 ? kAttn8[c][d.head_dim == 128][bm64]
                                          : kAttn[c][hd][d.dtype == TX_BF16][bm64][bn32];
   if (!fn)

@@ -1,7 +1,10 @@
 // Fused attention forward for gfx950: the forward of the fused-attention
 // tutorial (R:pass/LoopSplit/06-fused-attention.py:44-93, :181-239), fp16
-// (the tutorial's type) or bf16 q/k/v/o, HEAD_DIM 32, 64, 128 or 256, fp32
-// softmax statistics and accumulator.
+// (the tutorial's type) or bf16 q/k/v/o, HEAD_DIM 16, 32, 64, 128 or 256,
+// fp32 softmax statistics and accumulator.  HEAD_DIM 16 runs in the layout
+// of 32: its K/V chunks past dim 16 load as zeros (out-of-range buffer
+// offsets), Q's dims past 16 are zero and O's are not stored, so S and P V
+// are unchanged.
 //
 // A workgroup owns BM query rows of one (z, h), one wave per 32 rows; BM x
 // BN is any of the tutorial's autotuned blocks (64 or 128 by 32 or 64, 128 x
@@ -52,13 +55,16 @@ struct AttnArgs {
 // BM_ x BN_: the tutorial's autotuned block space, BLOCK_M in {64, 128} (one
 // wave per 32 query rows) and BLOCK_N in {32, 64}.
 template <int HD, bool BF, int BM_ = 128, int BN_ = 64> struct AttnFwd {
-  static constexpr int BM = BM_, BN = BN_, D = HD, NW = BM_ / 32, ESZ = 2;
+  // D: the head dim of the layout (32 for HEAD_DIM 16); DR: the real one
+  static constexpr int BM = BM_, BN = BN_, D = HD < 32 ? 32 : HD, DR = HD, NW = BM_ / 32,
+                       ESZ = 2;
   static constexpr int ROW = D * 2;            // bytes per K/V row
   static constexpr int TILE = BN * ROW;        // 4 / 8 / 16 KiB
   static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 1 .. 8
   static constexpr int CPR = ROW / 16;         // 16-byte chunks per row: 8 / 16
   static constexpr uint32_t kOOB = 0x80000000u;
-  static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head dims 32 .. 256");
+  static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head dims 16 .. 256");
+  static_assert(DR == D || (DR == 16 && D == 32), "head dim 16 in the layout of 32");
   static_assert((BM == 64 || BM == 128) && (BN == 32 || BN == 64), "the tutorial's blocks");
   static_assert(DMA >= 1 && DMA * NW * 1024 == TILE, "whole 1 KiB loads per wave");
   // Fragment reads issued together in qk / pv: every one at head dims up to
@@ -95,7 +101,7 @@ template <int HD, bool BF, int BM_ = 128, int BN_ = 64> struct AttnFwd {
   // block's first row): load u of wave w fills 1 KiB of LDS, rows
   // (64/CPR) (DMA w + u) .., lane i row .. + i/CPR at chunk position i%CPR,
   // which holds chunk i%CPR ^ swizzle(row) of the source row (V_SWZ: V's
-  // layout, else K's).
+  // layout, else K's).  Chunks past the real head dim take kOOB (zeros).
   template <bool V_SWZ>
   __device__ __forceinline__ static void dma_offsets(int wave, int64_t sm, uint32_t (&o)[DMA]) {
     const int lane = threadIdx.x & 63;
@@ -103,7 +109,7 @@ template <int HD, bool BF, int BM_ = 128, int BN_ = 64> struct AttnFwd {
     for (int u = 0; u < DMA; ++u) {
       const int row = (64 / CPR) * (DMA * wave + u) + lane / CPR, pos = lane % CPR;
       const int c = pos ^ (V_SWZ ? vswz(row) : kswz(row));
-      o[u] = (uint32_t)((row * sm + c * 8) * 2);
+      o[u] = 8 * c >= DR ? kOOB : (uint32_t)((row * sm + c * 8) * 2);
     }
   }
 
@@ -292,10 +298,12 @@ template <int HD, bool BF, int BM_ = 128, int BN_ = 64> struct AttnFwd {
     const int g = (threadIdx.x & 63) >> 5;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c)
-      qf.v[c] = *reinterpret_cast<const h8 *>(Qh + (m * sm + 16 * c + 8 * g) * 2);
+      qf.v[c] = 16 * c + 8 * g < DR
+                    ? *reinterpret_cast<const h8 *>(Qh + (m * sm + 16 * c + 8 * g) * 2)
+                    : h8{};
   }
   __device__ __forceinline__ static uint32_t k_bytes(int64_t n_ctx, int64_t sm) {
-    return (uint32_t)(((n_ctx - 1) * sm + D) * 2);
+    return (uint32_t)(((n_ctx - 1) * sm + DR) * 2);
   }
   __device__ __forceinline__ static uint32_t v_bytes(int64_t n_ctx, int64_t sm) {
     return k_bytes(n_ctx, sm);
@@ -326,6 +334,8 @@ template <int HD, bool BF, int BM_ = 128, int BN_ = 64> struct AttnFwd {
     for (int bd = 0; bd < D / 32; ++bd)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
+        if (32 * bd + 8 * q >= DR) // the layout's dims past the real head dim
+          continue;
         h4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e)

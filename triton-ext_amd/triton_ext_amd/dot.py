@@ -324,11 +324,12 @@ def _upcast_workspace(p, device, stream):
     return ws
 
 
-def attention(q, k, v, causal, sm_scale, return_lse=False, plan=None, stream=None, block=(0, 0)):
+def attention(q, k, v, causal, sm_scale, USE_TMA=True, *, return_lse=False, plan=None,
+              stream=None, block=(0, 0)):
     """Forward of the fused-attention tutorial's `attention(q, k, v, causal,
-    sm_scale)` (R:pass/LoopSplit/06-fused-attention.py:583-640) on the
-    MI355X kernel: q, k, v [Z, H, N_CTX, HEAD_DIM], head dim 32, 64, 128 or
-    256 in fp16 or bf16 (head dim contiguous), or 64 or 128 in
+    sm_scale, USE_TMA=True)` (R:pass/LoopSplit/06-fused-attention.py:583-640) on the
+    MI355X kernel: q, k, v [Z, H, N_CTX, HEAD_DIM], head dim 16, 32, 64, 128
+    or 256 in fp16 or bf16 (head dim contiguous), or 64 or 128 in
     float8_e5m2 as the tutorial's
     fp8 provider passes them (:774-779): q and k head-dim contiguous, v
     key-contiguous (stride 1 along N_CTX, "when v is in float8_e5m2 it is
@@ -337,7 +338,10 @@ def attention(q, k, v, causal, sm_scale, return_lse=False, plan=None, stream=Non
     tutorial saves for its backward, with return_lse=True).  Shape checks
     follow the tutorial's asserts.  block = (BLOCK_M, BLOCK_N), one of the
     tutorial's autotuned configs (:145-159): BLOCK_M 64 or 128 by BLOCK_N 32
-    or 64 (fp8: 64); (0, 0) takes 128 x 64.
+    or 64 (fp8: 64); (0, 0) takes 128 x 64.  USE_TMA is accepted for the
+    tutorial's signature and has no effect (gfx950 has no tensor memory
+    accelerator; the tutorial's HIP path takes the pointer kernel too).
+    return_lse, plan, stream and block are keyword-only.
     """
     import torch
     if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
