@@ -475,14 +475,18 @@ def bench_read_ceiling(dev, nbytes, steps, flush):
                 variants=rows)
 
 
-def bench_mfma_ceiling(dev, steps, warmup, seed=1):
+def bench_mfma_ceiling(dev, steps, warmup, seed=1, zeros=False):
     """The bf16 4096^3 tile schedule's MFMAs alone: 256 workgroups x 4 waves x 64 K
-    steps x 64 v_mfma_f32_32x32x16_bf16, operands bf16 N(0,1)/64 held in registers."""
+    steps x 64 v_mfma_f32_32x32x16_bf16, operands bf16 N(0,1)/64 (the headline's
+    input distribution) held in registers.  zeros=True: all-zero operands, which toggle
+    no operand bits -- the MFMA's power, and with it the clock, depends on them."""
     import torch
     L = ceilings_lib()
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     seed_t = (torch.randn((64 * 2048 * 8,), generator=g, device=dev) / 64).to(torch.bfloat16)
+    if zeros:
+        seed_t.zero_()
     out = torch.empty(256 * 256, dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
 
@@ -492,7 +496,8 @@ def bench_mfma_ceiling(dev, steps, warmup, seed=1):
     ms = time_back_to_back(run, steps, warmup)
     flops = 256 * 4 * 64 * 64 * 32768.0
     return dict(workload="MFMA ceiling: the bf16 4096^3 tile schedule's 2^22 "
-                         "v_mfma_f32_32x32x16_bf16 alone (operands in registers)",
+                         "v_mfma_f32_32x32x16_bf16 alone (operands in registers"
+                         + (", all zero)" if zeros else ", N(0,1)/64)"),
                 ms=ms, tflops=flops / ms / 1e9, frac=flops / ms / 1e-3 / PEAK_BF16)
 
 
@@ -609,11 +614,13 @@ def main():
             print(f"# {r['workload']}: {100 * r['frac']:.1f}% of peak", file=sys.stderr, flush=True)
     ceil = {}
     if want("ceiling"):
-        r = bench_mfma_ceiling(dev, args.steps, args.warmup)
-        secondary.append(r)
-        ceil["mfma_bf16_tflops"] = round(r["tflops"], 1)
-        print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s ({100 * r['frac']:.1f}% of spec)",
-              file=sys.stderr, flush=True)
+        for zeros in (False, True):
+            r = bench_mfma_ceiling(dev, args.steps, args.warmup, zeros=zeros)
+            secondary.append(r)
+            ceil["mfma_bf16_zero_operands_tflops" if zeros else "mfma_bf16_tflops"] = \
+                round(r["tflops"], 1)
+            print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s ({100 * r['frac']:.1f}% of spec)",
+                  file=sys.stderr, flush=True)
         for nb in (64 << 20, 1 << 30):
             r = bench_read_ceiling(dev, nb, max(args.steps, 20), flush)
             secondary.append(r)
