@@ -447,6 +447,7 @@ def ceilings_lib():
     vp = ctypes.c_void_p
     L.tx_ceiling_read.argtypes = [vp, ctypes.c_size_t, ctypes.c_int, vp, vp]
     L.tx_ceiling_mfma_bf16.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp]
+    L.tx_ceiling_mfma_fp8.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp]
     return L
 
 
@@ -499,6 +500,33 @@ def bench_mfma_ceiling(dev, steps, warmup, seed=1, zeros=False):
                          "v_mfma_f32_32x32x16_bf16 alone (operands in registers"
                          + (", all zero)" if zeros else ", N(0,1)/64)"),
                 ms=ms, tflops=flops / ms / 1e9, frac=flops / ms / 1e-3 / PEAK_BF16)
+
+
+def bench_mfma_ceiling_fp8(dev, steps, warmup, seed=2, zeros=False):
+    """The fp8 C5 tile schedule's MFMAs alone: 224 workgroups (C5's 8 x 28 tiles) x 8
+    waves x 56 K steps x 32 v_mfma_f32_16x16x128_f8f6f4, e4m3 operands held in registers:
+    codes of N(0,1) * 100 (saturated at 448, no NaN codes), spread over the e4m3 range
+    as C5's amax/448-quantised values are; zeros=True: all-zero operands."""
+    import torch
+    L = ceilings_lib()
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    vals = (torch.randn((64 * 12 * 64 * 32,), generator=g, device=dev) * 100).clamp(-448, 448)
+    seed_t = vals.to(torch.float8_e4m3fn).view(torch.uint8)
+    if zeros:
+        seed_t.zero_()
+    out = torch.empty(224 * 512, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def run():
+        if L.tx_ceiling_mfma_fp8(seed_t.data_ptr(), 224, 56, out.data_ptr(), stream) != 0:
+            raise RuntimeError("tx_ceiling_mfma_fp8 failed")
+    ms = time_back_to_back(run, steps, warmup)
+    flops = 224 * 8 * 56 * 32 * 65536.0
+    return dict(workload="fp8 MFMA ceiling: the C5 tile schedule's v_mfma_f32_16x16x128_f8f6f4 "
+                         "alone (224 workgroups, operands in registers"
+                         + (", all zero)" if zeros else ", e4m3 of N(0,1)*100)"),
+                ms=ms, tflops=flops / ms / 1e9, frac=flops / ms / 1e-3 / PEAK_I8)
 
 
 def bench_tiles(tx, dev, steps, warmup):
@@ -618,6 +646,13 @@ def main():
             r = bench_mfma_ceiling(dev, args.steps, args.warmup, zeros=zeros)
             secondary.append(r)
             ceil["mfma_bf16_zero_operands_tflops" if zeros else "mfma_bf16_tflops"] = \
+                round(r["tflops"], 1)
+            print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s ({100 * r['frac']:.1f}% of spec)",
+                  file=sys.stderr, flush=True)
+        for zeros in (False, True):
+            r = bench_mfma_ceiling_fp8(dev, args.steps, args.warmup, zeros=zeros)
+            secondary.append(r)
+            ceil["mfma_fp8_zero_operands_tflops" if zeros else "mfma_fp8_tflops"] = \
                 round(r["tflops"], 1)
             print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s ({100 * r['frac']:.1f}% of spec)",
                   file=sys.stderr, flush=True)

@@ -12,6 +12,8 @@
 //     (the same grid, waves and v_mfma_f32_32x32x16_bf16 count per wave, on
 //     operands held in registers, no LDS and no memory traffic in the loop),
 //     the ceiling the power-limited clock leaves for the dot's MFMA stream.
+//   * tx_ceiling_mfma_fp8: the same for the 8-bit 256x256x128 tile (8 waves
+//     of 8 x 4 blocks of v_mfma_f32_16x16x128_f8f6f4 per K step, e4m3).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -23,6 +25,8 @@ namespace {
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 // Read: workgroup b reads bytes [b * 4096 U, (b + 1) * 4096 U): U 16-byte
@@ -114,6 +118,43 @@ __global__ void __launch_bounds__(256, 1) mfma_bf16_kernel(const u32x4_t *seed, 
 
 } // namespace
 
+// fp8 MFMA ceiling: 8 waves per workgroup, 8 x 4 accumulators of 16x16 per
+// wave (128x64), one v_mfma_f32_16x16x128_f8f6f4 (e4m3 x e4m3, unit scales)
+// per block and K step, operands from `seed` kept in registers.
+__global__ void __launch_bounds__(512, 1) mfma_fp8_kernel(const i32x8_t *seed, int ksteps,
+                                                          float *out) {
+  const int lane = threadIdx.x & 63;
+  const i32x8_t *s = seed + ((blockIdx.x * 8 + (threadIdx.x >> 6)) % 64) * 12 * 64 + lane;
+  i32x8_t a[8], b[4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    a[i] = s[i * 64];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    b[j] = s[(8 + j) * 64];
+  f32x4_t acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int kt = 0; kt < ksteps; ++kt) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b[j], a[i], acc[i][j], 0, 0,
+                                                                      0, 0, 0, 0);
+  }
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      t += acc[i][j][0] + acc[i][j][1] + acc[i][j][2] + acc[i][j][3];
+  out[(size_t)blockIdx.x * 512 + threadIdx.x] = t;
+}
+
 extern "C" int tx_ceiling_read(const void *buf, size_t bytes, int variant, void *sink,
                                void *stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -147,5 +188,14 @@ extern "C" int tx_ceiling_mfma_bf16(const void *seed, int tiles, int ksteps, flo
     return 1;
   hipLaunchKernelGGL(mfma_bf16_kernel, dim3(tiles), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<const u32x4_t *>(seed), ksteps, out);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+extern "C" int tx_ceiling_mfma_fp8(const void *seed, int tiles, int ksteps, float *out,
+                                   void *stream) {
+  if (!seed || !out || tiles <= 0 || ksteps < 0 || (reinterpret_cast<uintptr_t>(seed) & 31))
+    return 1;
+  hipLaunchKernelGGL(mfma_fp8_kernel, dim3(tiles), dim3(512), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const i32x8_t *>(seed), ksteps, out);
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }

@@ -1,6 +1,6 @@
 /* Hardware-ceiling kernels timed by bench.py (libtx_ceilings.so).  Not part
  * of the dot path: they measure what one MI355X delivers for a plain HBM
- * read and for the bf16 tile's MFMA stream alone.  Return 0 on success, 1
+ * read and for the bf16 and 8-bit tiles' MFMA streams alone.  Return 0 on success, 1
  * for bad arguments, 3 if the launch failed. */
 #ifndef TRITON_EXT_AMD_TX_CEILINGS_H
 #define TRITON_EXT_AMD_TX_CEILINGS_H
@@ -28,6 +28,14 @@ __attribute__((visibility("default"))) int tx_ceiling_read(const void *buf, size
 __attribute__((visibility("default"))) int tx_ceiling_mfma_bf16(const void *seed, int tiles,
                                                                 int ksteps, float *out,
                                                                 void *stream);
+
+/* `tiles` workgroups of 8 waves, each running `ksteps` x 32 MFMAs
+ * v_mfma_f32_16x16x128_f8f6f4 (e4m3) per wave on operands read once from
+ * `seed` (64 x 12 x 64 32-byte values, 32-byte aligned), then one fp32 per
+ * thread to `out` [tiles * 512].  FLOPs = tiles * 8 * ksteps * 32 * 65536. */
+__attribute__((visibility("default"))) int tx_ceiling_mfma_fp8(const void *seed, int tiles,
+                                                               int ksteps, float *out,
+                                                               void *stream);
 
 #ifdef __cplusplus
 }
