@@ -313,6 +313,14 @@ bool useDecode(const tx_dot_desc &d) {
 int decodeMT(int64_t M) { return M > 64 ? 4 : (int)cdiv(M > 0 ? M : 1, 16); }
 int decodeSlices(int64_t M) { return (int)cdiv(M > 0 ? M : 1, 16 * decodeMT(M)); }
 
+// The decode kernel's tile as the arith_intensity pass names it: a row slice
+// (16 MT rows) x a 128-column strip x 64-row K batches.  A caller's explicit
+// block other than this runs the tile it names (or is refused).
+bool decodeTile(const tx_dot_desc &d) {
+  return d.block_m == 16 * decodeMT(d.M) && d.block_n == kDecodeStripN &&
+         d.block_k == kDecodeBatchK;
+}
+
 // Split-K factor for the decode kernel: a power of two (<= kMaxSplit) so
 // that slices * strips * ksplit workgroups cover the CUs about once, each
 // with at least four 64-row batches per wave.
@@ -335,6 +343,39 @@ int64_t decodeWorkspace(const tx_dot_desc &d, int ksplit) {
   return decodeCounterBytes(d) + (int64_t)ksplit * d.M * ((d.N + 3) & ~3) * 4;
 }
 
+// The 32-bit-offset tiles (gemm16_w4.h, gemm8_w4.h, gemm8_n224.h) address A,
+// B and the block scales through buffer offsets: each must span less than
+// 2^31 bytes (out-of-range chunks, at offset 2^31, read zeros).
+int checkSpans32(const tx_dot_desc &d, const GemmConfig &c) {
+  if (c.dma != 2 && c.dma != 5)
+    return TX_OK;
+  tx_dot_desc e = d; // the operands as the tile reads them
+  if (mxUpcastSide(d) & 1)
+    e.a_type = TX_BF16, e.lda = d.K;
+  if (mxUpcastSide(d) & 2)
+    e.b_type = TX_BF16, e.ldb = mxUpcastLdB(d);
+  int64_t sa = 0, sb = 0;
+  tx_dot_operand_spans(&e, &sa, &sb);
+  const int64_t kb = cdiv(d.K, 128);
+  if (sa >= TX_SPAN32_LIMIT || sb >= TX_SPAN32_LIMIT ||
+      (d.scale_mode == TX_SCALE_BLOCK128 &&
+       (d.M * kb * 4 >= TX_SPAN32_LIMIT || kb * cdiv(d.N, 128) * 4 >= TX_SPAN32_LIMIT)))
+    return fail(TX_ERR_UNSUPPORTED,
+                "the %dx%d tile addresses operands through 32-bit offsets: A spans %lld "
+                "bytes, B %lld (limit 2^31); a 128x128 tile takes larger operands",
+                c.bm, c.bn, (long long)sa, (long long)sb);
+  return TX_OK;
+}
+
+// The GEMM-tile kernel id of a descriptor of operand kind `op`.
+int32_t gemmKernelOf(const tx_dot_desc &d, int op) {
+  return op == OP_I8                     ? TX_KERNEL_GEMM_I8
+         : mxUpcastSide(d)             ? TX_KERNEL_GEMM_MX_BF16
+         : d.scale_mode == TX_SCALE_MX32 ? TX_KERNEL_GEMM_MX
+         : op == OP_F8                   ? TX_KERNEL_GEMM_F8
+                                         : TX_KERNEL_GEMM_16BIT;
+}
+
 // ---------------------------------------------------------------------------
 // The "mi355x_dot" pass: kernel choice and launch shape.
 // ---------------------------------------------------------------------------
@@ -346,7 +387,7 @@ int txMi355xDotRun(tx_dot_plan *plan) {
     return fail(TX_ERR_UNSUPPORTED,
                 "no kernel for a_type=%d b_type=%d c_type=%d scale_mode=%d",
                 d.a_type, d.b_type, d.c_type, d.scale_mode);
-  if (useDecode(d)) {
+  if (useDecode(d) && decodeTile(d)) {
     const int ks = decodeSplit(d.M, d.N, d.K);
     plan->kernel = TX_KERNEL_DECODE_I8;
     plan->split_k = ks;
@@ -369,38 +410,19 @@ int txMi355xDotRun(tx_dot_plan *plan) {
                 d.block_m, d.block_n, d.block_k);
   const GemmConfig &c = kGemmConfigs[ci];
   const bool upcast = mxUpcastSide(d) != 0;
-  if (c.dma == 2 || c.dma == 5) {
-    // These tiles address A, B and the block scales through 32-bit buffer
-    // offsets (out-of-range chunks at offset 2^31 read zeros).
-    tx_dot_desc e = d; // the operands as the tile reads them
-    if (upcast) {
-      if (mxUpcastSide(d) & 1)
-        e.a_type = TX_BF16, e.lda = d.K;
-      if (mxUpcastSide(d) & 2)
-        e.b_type = TX_BF16, e.ldb = d.N;
-    }
-    int64_t sa = 0, sb = 0;
-    tx_dot_operand_spans(&e, &sa, &sb);
-    const int64_t kb = cdiv(d.K, 128);
-    if (sa >= TX_SPAN32_LIMIT || sb >= TX_SPAN32_LIMIT ||
-        (d.scale_mode == TX_SCALE_BLOCK128 &&
-         (d.M * kb * 4 >= TX_SPAN32_LIMIT || kb * cdiv(d.N, 128) * 4 >= TX_SPAN32_LIMIT)))
-      return fail(TX_ERR_UNSUPPORTED,
-                  "the %dx%d tile addresses operands through 32-bit offsets: A spans %lld "
-                  "bytes, B %lld (limit 2^31); a 128x128 tile takes larger operands",
-                  c.bm, c.bn, (long long)sa, (long long)sb);
-  }
+  const int src = checkSpans32(d, c);
+  if (src != TX_OK)
+    return src;
+  if ((int64_t)plan->m_tiles * plan->n_tiles > INT32_MAX)
+    return fail(TX_ERR_UNSUPPORTED, "a grid of %lld tiles (above 2^31)",
+                (long long)plan->m_tiles * plan->n_tiles);
   // Tile rows per group of the XCD-aware tile order: 4, except 2 on the 8-bit
   // tile once K spans 8192 bytes or more (a sweep of 1..32: mxfp8 8192^3 ran
   // 2365 TFLOP/s at 2 against 1930 at 4; 4096^3, C5 (K = 7168) and mxfp4
   // 8192^3 (K = 4096 bytes) were as fast or faster at 4).
   const int64_t kbytes = d.K * tx_dtype_bits(d.a_type) / 8;
   plan->group_m = c.dma == 5 && kbytes >= 8192 ? 2 : 4;
-  plan->kernel = op == OP_I8                     ? TX_KERNEL_GEMM_I8
-               : upcast                        ? TX_KERNEL_GEMM_MX_BF16
-               : d.scale_mode == TX_SCALE_MX32 ? TX_KERNEL_GEMM_MX
-               : op == OP_F8                   ? TX_KERNEL_GEMM_F8
-                                               : TX_KERNEL_GEMM_16BIT;
+  plan->kernel = gemmKernelOf(d, op);
   plan->split_k = 1;
   plan->grid_x = plan->m_tiles * plan->n_tiles;
   plan->grid_y = plan->grid_z = 1;
@@ -763,6 +785,62 @@ int scratchOfCurrentDevice(uint8_t **out) {
 
 // Checks shared by both launch entry points, then the launch itself.
 // noalloc: the workspace is this GPU's scratch array (ws is ignored).
+// A plan comes back from the caller at launch.  The fields the kernels trust
+// (the loop split, the tile grid, the kernel, its launch shape and workspace)
+// must still follow from the plan's descriptor, itself one that validate()
+// leaves unchanged, so that a plan edited or built by hand is rejected here,
+// before any HIP call, rather than launched with shapes its kernel does not
+// assume.  Host arithmetic only: the pass pipeline is not rerun.
+int checkPlan(const tx_dot_plan &p) {
+  const tx_dot_desc &d = p.desc;
+  tx_dot_desc v;
+  const int vrc = validate(&d, &v);
+  if (vrc != TX_OK)
+    return vrc;
+  static_assert(sizeof(tx_dot_desc) == 6 * 8 + 8 * 4, "tx_dot_desc has no padding");
+  if (std::memcmp(&v, &d, sizeof v) != 0)
+    return fail(TX_ERR_INVALID, "the plan's descriptor is not a resolved one (strides left 0)");
+  if (d.block_m <= 0 || d.block_n <= 0 || d.block_k <= 0)
+    return fail(TX_ERR_INVALID, "the plan has no tile size");
+  int64_t ks = 0;
+  int32_t km = 0, kt = (int32_t)d.K;
+  if (!(d.flags & TX_FLAG_NO_LOOP_SPLIT) && tx_loop_split_k(d.K, d.block_k, &ks, &km, &kt) != TX_OK)
+    return fail(TX_ERR_INVALID, "no loop split for K=%lld, BK=%d", (long long)d.K, d.block_k);
+  if (p.k_split != ks || p.k_main_steps != km || p.k_tail != kt ||
+      p.m_tiles != cdiv(d.M, d.block_m) || p.n_tiles != cdiv(d.N, d.block_n) ||
+      p.m_edge != d.M % d.block_m || p.n_edge != d.N % d.block_n || p.grid_y != 1 ||
+      p.grid_z != 1)
+    return fail(TX_ERR_INVALID, "the plan's loop split or tile grid does not follow from its "
+                "descriptor");
+  int op, epi;
+  classify(d, &op, &epi);
+  if (op < 0 || epi < 0)
+    return fail(TX_ERR_UNSUPPORTED, "no kernel for the plan's operand types");
+  if (p.kernel == TX_KERNEL_DECODE_I8) {
+    const int sk = p.split_k;
+    if (!useDecode(d) || !decodeTile(d) || sk < 1 || sk > (int)kMaxSplit ||
+        (sk & (sk - 1)) || p.grid_x != cdiv(d.N, kDecodeStripN) * sk * decodeSlices(d.M) ||
+        p.block_threads != kDecodeWaves * 64 || p.workspace_bytes != decodeWorkspace(d, sk))
+      return fail(TX_ERR_INVALID, "the plan's decode launch does not follow from its descriptor");
+    return TX_OK;
+  }
+  const bool upcast = mxUpcastSide(d) != 0;
+  const int ci = findGemmConfig(op, epi, d.block_m, d.block_n, d.block_k,
+                                (d.flags & TX_FLAG_B_KMAJOR) != 0, upcast ? 0 : fmtOf(d));
+  if (ci < 0)
+    return fail(TX_ERR_UNSUPPORTED, "the plan names a tile that is not instantiated");
+  const GemmConfig &c = kGemmConfigs[ci];
+  const int src = checkSpans32(d, c);
+  if (src != TX_OK)
+    return src;
+  if (p.kernel != gemmKernelOf(d, op) || p.split_k != 1 ||
+      p.grid_x != (int64_t)p.m_tiles * p.n_tiles || p.block_threads != c.wm * c.wn * 64 ||
+      p.workspace_bytes != (upcast ? mxUpcastWorkspace(d) : 0))
+    return fail(TX_ERR_INVALID, "the plan's kernel or launch shape does not follow from its "
+                "descriptor");
+  return TX_OK;
+}
+
 int launchPlanned(const tx_dot_plan *plan, const void *A, const void *B, void *C,
                   const void *scale_a, const void *scale_b, void *workspace,
                   size_t workspace_bytes, void *stream, bool noalloc) {
@@ -785,6 +863,9 @@ int launchPlanned(const tx_dot_plan *plan, const void *A, const void *B, void *C
   if (((need_sa ? reinterpret_cast<uintptr_t>(scale_a) : 0) |
        (need_sb ? reinterpret_cast<uintptr_t>(scale_b) : 0)) & 3)
     return fail(TX_ERR_INVALID, "scale arrays must be 4-byte aligned");
+  const int prc = checkPlan(*plan);
+  if (prc != TX_OK)
+    return prc;
   if (noalloc) {
     // The upcast operand goes after the counter region, the decode
     // workspace (counters first) at the start.
@@ -950,6 +1031,23 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
     return TX_OK;
   if (!q || !k || !v || !o || !M)
     return fail(TX_ERR_INVALID, "NULL tensor pointer");
+  {
+    // The plan comes back from the caller: planning its descriptor again
+    // (host arithmetic) must give this plan, field for field, so that an
+    // edited plan (strides, blocks, grid) never reaches the kernel.
+    tx_attn_plan again;
+    const int rc = tx_attn_fwd_plan(&d, &again);
+    if (rc != TX_OK)
+      return rc;
+    // (field by field: the struct's tail padding carries no meaning)
+    static_assert(sizeof(tx_attn_desc) == 3 * 8 + 4 * 4 + 12 * 8 + 2 * 4,
+                  "tx_attn_desc has no padding");
+    if (std::memcmp(&again.desc, &plan->desc, sizeof again.desc) != 0 ||
+        again.flops != plan->flops || again.bytes != plan->bytes ||
+        again.qk_scale != plan->qk_scale || again.m_blocks != plan->m_blocks ||
+        again.grid_x != plan->grid_x || again.block_threads != plan->block_threads)
+      return fail(TX_ERR_INVALID, "the plan does not follow from its descriptor");
+  }
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
        reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o)) & 15 ||
       reinterpret_cast<uintptr_t>(M) & 3)

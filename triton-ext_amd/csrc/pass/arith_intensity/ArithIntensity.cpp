@@ -198,9 +198,11 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
       t = kTiles16[0]; // the K-major B kernel exists for this tile only
     else if (sa == 2)
       t = chooseTile(kTiles16, d->M, d->N, d->K, first);
-    else if (d->a_type == TX_I8 && d->scale_mode == TX_SCALE_ROWCOL && d->M <= 256)
-      // W8A8 decode: one row slice up to M = 64, slices of 64 beyond,
-      // 128-column strips, 64-row K batches
+    else if (d->a_type == TX_I8 && d->scale_mode == TX_SCALE_ROWCOL && d->M <= 256 &&
+             d->N <= (int64_t)4096 * 128)
+      // W8A8 decode (M <= 256, N up to its 4096 column strips): one row
+      // slice up to M = 64, slices of 64 beyond, 128-column strips, 64-row
+      // K batches
       t = Tile{(int32_t)(d->M > 64 ? 64 : 16 * cdiv(d->M > 0 ? d->M : 1, 16)), 128, 64, 1.0};
     else if (d->a_type == TX_F8E4M3 || d->a_type == TX_F8E5M2)
       t = kTiles8[first]; // the register-staged 128x128 tile is slower everywhere
