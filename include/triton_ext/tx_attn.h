@@ -48,7 +48,7 @@ extern "C" {
 
 typedef struct tx_attn_desc {
   int64_t Z, H, N_CTX;
-  int32_t head_dim; /* 16, 32, 64, 128 or 256 (fp8 e5m2: 64 or 128) */
+  int32_t head_dim; /* 16, 32, 64, 128 or 256 */
   int32_t dtype;    /* TX_F16 (the tutorial's), TX_BF16 or TX_F8E5M2 for q, k, v, o */
   int32_t causal;   /* 0 or 1 */
   float sm_scale;
@@ -78,10 +78,10 @@ typedef struct tx_attn_plan {
 } tx_attn_plan;
 
 /* Validate `desc` and fill `plan`.  TX_ERR_UNSUPPORTED unless dtype is
- * TX_F16, TX_BF16 (head_dim 16, 32, 64, 128 or 256) or TX_F8E5M2 (64 or 128),
- * the blocks one of the implemented configs (a K block, BLOCK_N x head_dim
- * elements, head_dim 16 staged as 32, must fill one 1 KiB load per wave:
- * head_dims 16 and 32 reject 128 x 32)
+ * TX_F16, TX_BF16 or TX_F8E5M2 with head_dim 16, 32, 64, 128 or 256, the
+ * blocks one of the implemented configs (an fp16/bf16 K block, BLOCK_N x
+ * head_dim elements, head_dim 16 staged as 32, must fill one 1 KiB load per
+ * wave: head_dims 16 and 32 reject 128 x 32)
  * and N_CTX a multiple of BLOCK_M (the tutorial's block pointers assume whole
  * blocks).  p is rounded to q's type to nearest even before p @ v, as
  * compiled Triton does. */

@@ -241,7 +241,7 @@ def test_attn_plan():
             tx.attn_plan(**a)
         return e.value.code
     assert err(head_dim=96) == tx.ERR_UNSUPPORTED
-    # head dims: the tutorial's {16, 32, 64, 128, 256} for fp16 / bf16, 64 and 128 for fp8; a
+    # head dims: the tutorial's {16, 32, 64, 128, 256} for fp16, bf16 and fp8; an fp16 / bf16
     # K block (head dim 16 staged as 32) must fill one 1 KiB load per wave
     for hd in (16, 32, 64, 128, 256):
         for blk in ((128, 64), (64, 64), (64, 32)) + (((128, 32),) if hd > 32 else ()):
@@ -250,9 +250,14 @@ def test_attn_plan():
     assert err(head_dim=16, block=(128, 32)) == tx.ERR_UNSUPPORTED
     assert tx.attn_plan(1, 1, 256, 16, False, 0.5).flops == 4 * 256 ** 2 * 16
     assert err(head_dim=8) == tx.ERR_UNSUPPORTED
-    assert err(head_dim=16, dtype=tx.F8E5M2) == tx.ERR_UNSUPPORTED
-    assert err(head_dim=256, dtype=tx.F8E5M2) == tx.ERR_UNSUPPORTED
-    assert err(head_dim=32, dtype=tx.F8E5M2) == tx.ERR_UNSUPPORTED
+    for hd in (16, 32, 64, 128, 256):  # fp8 stages head dims 16 and 32 as 64
+        for blk in ((128, 64), (64, 64)):
+            p8 = tx.attn_plan(1, 2, 128, hd, False, 0.5, dtype=tx.F8E5M2, block=blk)
+            assert p8.desc.q_sm == hd and p8.desc.v_sm == 128 and p8.desc.v_sh == hd * 128
+            assert p8.flops == 4 * 2 * 128 ** 2 * hd
+    assert err(head_dim=8, dtype=tx.F8E5M2) == tx.ERR_UNSUPPORTED
+    assert err(head_dim=48, dtype=tx.F8E5M2) == tx.ERR_UNSUPPORTED
+    assert err(head_dim=16, dtype=tx.F8E5M2, strides={"q": (0, 0, 8)}) == tx.ERR_INVALID
     assert err(N_CTX=200) == tx.ERR_UNSUPPORTED
     assert err(dtype=tx.F32) == tx.ERR_UNSUPPORTED
     assert tx.attn_plan(1, 1, 256, 128, True, 0.5, dtype=tx.BF16).desc.head_dim == 128

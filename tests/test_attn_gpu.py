@@ -304,6 +304,24 @@ def test_attn_fp8_block_m64(gpu, causal, Z, H, N, D):
 
 
 @pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("Z,H,N,D,block", [(1, 2, 256, 16, (128, 64)), (2, 1, 192, 16, (64, 64)),
+                                           (1, 2, 384, 32, (128, 64)), (1, 3, 128, 32, (64, 64)),
+                                           (1, 2, 256, 256, (128, 64)),
+                                           (2, 1, 192, 256, (64, 64))])
+def test_attn_fp8_head_dims_16_32_and_256(gpu, causal, Z, H, N, D, block):
+    """The tutorial's other fp8 head dims: 16 and 32 run in the layout of 64
+    (K chunks and V^T rows past the head dim read as zeros), 256 in 256-byte
+    K rows."""
+    say(f"attn fp8 D={D} block={block} Z={Z} H={H} N={N} causal={causal}")
+    q, k, v = e5m2_qkv(Z, H, N, D, seed=Z * 100 + H * 10 + N + D + causal + 11)
+    o, M = run_gpu_fp8(gpu, q, k, v, causal, 0.6, block=block)
+    ro, rM = oracle.attn_fwd(q, k, v, sm_scale=0.6, causal=causal, block=block,
+                             dtype=oracle.F8E5M2)
+    check_e5m2(o, M, ro, rM, (q, k, v), 0.6, causal,
+               f"attn fp8 D={D} block={block} {Z}x{H}x{N} causal={causal}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
 def test_attn_fp8_bench_shape_sampled_heads(gpu, causal):
     """The tutorial's fp8 bench shape (4, 32, 4096, 64), sm_scale 1.3: every
     program runs; two heads are checked in full against the oracle."""

@@ -120,10 +120,11 @@ def _cases():
         out.append(("attn", i, dict(Z=int(rng.integers(1, 3)), H=int(rng.integers(1, 4)),
                                     N=bm * int(rng.integers(1, 6)), D=D, bf16=bool(i % 3 == 1),
                                     causal=bool(rng.random() < 0.5), block=(bm, bn))))
-    for i in range(8):
+    for i in range(10):
         bm = [128, 64][i % 2]
         out.append(("attn_fp8", i, dict(Z=int(rng.integers(1, 3)), H=int(rng.integers(1, 3)),
-                                        N=bm * int(rng.integers(1, 5)), D=[64, 128][(i // 2) % 2],
+                                        N=bm * int(rng.integers(1, 5)),
+                                        D=[16, 32, 64, 128, 256][(i // 2) % 5],
                                         causal=bool(rng.random() < 0.5),
                                         scale=float(rng.choice([0.3, 0.7, 1.3])),
                                         block=(bm, 64))))

@@ -977,11 +977,10 @@ extern "C" TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *p
   if (d.dtype != TX_F16 && d.dtype != TX_BF16 && d.dtype != TX_F8E5M2)
     return fail(TX_ERR_UNSUPPORTED, "dtype %d: fp16, bf16 and fp8 e5m2 q/k/v/o are implemented",
                 d.dtype);
-  if (d.dtype == TX_F8E5M2 ? d.head_dim != 64 && d.head_dim != 128
-                           : d.head_dim != 16 && d.head_dim != 32 && d.head_dim != 64 &&
-                                 d.head_dim != 128 && d.head_dim != 256)
-    return fail(TX_ERR_UNSUPPORTED, "head_dim %d: %s are implemented", d.head_dim,
-                d.dtype == TX_F8E5M2 ? "64 and 128 (fp8)" : "16, 32, 64, 128 and 256");
+  if (d.head_dim != 16 && d.head_dim != 32 && d.head_dim != 64 && d.head_dim != 128 &&
+      d.head_dim != 256)
+    return fail(TX_ERR_UNSUPPORTED, "head_dim %d: 16, 32, 64, 128 and 256 are implemented",
+                d.head_dim);
   if (d.block_m == 0) d.block_m = 128;
   if (d.block_n == 0) d.block_n = 64;
   if ((d.block_m != 64 && d.block_m != 128) || (d.block_n != 32 && d.block_n != 64))
@@ -1057,7 +1056,6 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
       (d.dtype == TX_F8E5M2 && bn32) || plan->block_threads != d.block_m / 32 * 64 ||
       (d.head_dim != 16 && d.head_dim != 32 && d.head_dim != 64 && d.head_dim != 128 &&
        d.head_dim != 256) ||
-      (d.dtype == TX_F8E5M2 && d.head_dim != 64 && d.head_dim != 128) ||
       (d.dtype != TX_F16 && d.dtype != TX_BF16 && d.dtype != TX_F8E5M2) || d.N_CTX % d.block_m ||
       plan->m_blocks != d.N_CTX / d.block_m || plan->grid_x != d.Z * d.H * plan->m_blocks)
     return fail(TX_ERR_INVALID, "plan launch shape does not match the attention kernel");
@@ -1090,19 +1088,21 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
        TX_ATTN_DTYPES(true, 128), TX_ATTN_DTYPES(true, 256)}};
 #undef TX_ATTN_DTYPES
 #undef TX_ATTN_BLOCKS
-  // [causal][head_dim 128][BLOCK_M 64]
-  static const AttnFn kAttn8[2][2][2] = {
-      {{txk::attn_fwd8_kernel<false, 64, 128>, txk::attn_fwd8_kernel<false, 64, 64>},
-       {txk::attn_fwd8_kernel<false, 128, 128>, txk::attn_fwd8_kernel<false, 128, 64>}},
-      {{txk::attn_fwd8_kernel<true, 64, 128>, txk::attn_fwd8_kernel<true, 64, 64>},
-       {txk::attn_fwd8_kernel<true, 128, 128>, txk::attn_fwd8_kernel<true, 128, 64>}}};
+  // [causal][head_dim 16 / 32 / 64 / 128 / 256][BLOCK_M 64]
+#define TX_ATTN8_BLOCKS(C, HD) {txk::attn_fwd8_kernel<C, HD, 128>, txk::attn_fwd8_kernel<C, HD, 64>}
+  static const AttnFn kAttn8[2][5][2] = {
+      {TX_ATTN8_BLOCKS(false, 16), TX_ATTN8_BLOCKS(false, 32), TX_ATTN8_BLOCKS(false, 64),
+       TX_ATTN8_BLOCKS(false, 128), TX_ATTN8_BLOCKS(false, 256)},
+      {TX_ATTN8_BLOCKS(true, 16), TX_ATTN8_BLOCKS(true, 32), TX_ATTN8_BLOCKS(true, 64),
+       TX_ATTN8_BLOCKS(true, 128), TX_ATTN8_BLOCKS(true, 256)}};
+#undef TX_ATTN8_BLOCKS
   const int c = d.causal ? 1 : 0;
   const int hd = d.head_dim == 16    ? 0
                  : d.head_dim == 32  ? 1
                  : d.head_dim == 64  ? 2
                  : d.head_dim == 128 ? 3
                                      : 4;
-  const AttnFn fn = d.dtype == TX_F8E5M2 ? kAttn8[c][d.head_dim == 128][bm64]
+  const AttnFn fn = d.dtype == TX_F8E5M2 ? kAttn8[c][hd][bm64]
                                          : kAttn[c][hd][d.dtype == TX_BF16][bm64][bn32];
   if (!fn)
     return fail(TX_ERR_INVALID, "plan launch shape does not match the attention kernel");

@@ -1,8 +1,11 @@
 // Fused attention forward for gfx950, fp8 e5m2: the tutorial's fp8 provider
 // (R:pass/LoopSplit/06-fused-attention.py:774-779: q, k, v cast to
 // float8_e5m2, v stored key-contiguous; :81-82 p.to(tl.float8e5) before
-// p @ v; :238 o in q's type), HEAD_DIM 64 or 128, fp32 statistics and
-// accumulator.  The pipeline, split and program order are attn_fwd_body's
+// p @ v; :238 o in q's type), HEAD_DIM 16, 32, 64, 128 or 256, fp32
+// statistics and accumulator.  HEAD_DIM 16 and 32 run in the layout of 64
+// (one S^T MFMA takes 64 dims): K's chunks and V^T's dim rows past the real
+// head dim load as zeros (out-of-range buffer offsets), Q's bytes past it are
+// zero and O's are not stored.  The pipeline, split and program order are attn_fwd_body's
 // (attn_fwd.h); this file holds the element type's fragments.
 //
 // Per K/V block of BN = 64 keys and wave of 32 query rows (BM / 32 waves):
@@ -22,9 +25,10 @@
 //
 // LDS (16-byte chunk c of row r stored at c ^ swizzle(r)):
 //   K rows (keys) of HEAD_DIM bytes: 64-byte rows ((r >> 2) & 1) |
-//     ((r >> 3) & 2); 128-byte rows ((r >> 1) & 3) | ((r >> 2) & 4).  The
-//     16 keys pi(0..15) (or pi(16..31)) that one ds_read_b128 pass reads land
-//     in 16 different 16-byte bank groups;
+//     ((r >> 3) & 2); 128-byte rows ((r >> 1) & 3) | ((r >> 2) & 4);
+//     256-byte rows (r & 7) | ((r >> 1) & 8).  The 16 keys pi(0..15) (or
+//     pi(16..31)) that one ds_read_b128 pass reads land in 16 different
+//     16-byte bank groups;
 //   V^T rows (dims) of 64 bytes (the block's keys): (r >> 2) & 3, likewise
 //     for dims 0..15 of a pass.
 #pragma once
@@ -36,11 +40,15 @@ namespace txk {
 // BM_: BLOCK_M 64 or 128 (one wave per 32 query rows).  BLOCK_N is 64: the
 // P V MFMA takes the block's 64 keys at once.
 template <int HD, int BM_ = 128> struct AttnFwd8 {
-  static constexpr int BM = BM_, BN = 64, D = HD, NW = BM_ / 32, ESZ = 1;
+  // D: the head dim of the layout (64 for HEAD_DIM 16 and 32); DR: the real one
+  static constexpr int BM = BM_, BN = 64, D = HD < 64 ? 64 : HD, DR = HD, NW = BM_ / 32,
+                       ESZ = 1;
   static constexpr int TILE = BN * D;          // K: BN x D bytes; V^T: D x BN bytes
-  static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 1 .. 4
+  static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 1 .. 8
   static constexpr int KCPR = D / 16;          // K: 16-byte chunks per row
-  static_assert(D == 64 || D == 128, "head dims 64 and 128");
+  static constexpr uint32_t kOOB = 0x80000000u;
+  static_assert(D == 64 || D == 128 || D == 256, "head dims 16 .. 256");
+  static_assert(DR == D || (D == 64 && (DR == 16 || DR == 32)), "16 and 32 in the layout of 64");
   static_assert(BM == 64 || BM == 128, "the tutorial's BLOCK_M");
   typedef float f16v __attribute__((ext_vector_type(16)));
 
@@ -50,7 +58,9 @@ template <int HD, int BM_ = 128> struct AttnFwd8 {
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 1, 1, 0, 0, 0, 0);
   }
   __device__ __forceinline__ static int kswz(int r) {
-    return D == 64 ? ((r >> 2) & 1) | ((r >> 3) & 2) : ((r >> 1) & 3) | ((r >> 2) & 4);
+    return D == 64    ? ((r >> 2) & 1) | ((r >> 3) & 2)
+           : D == 128 ? ((r >> 1) & 3) | ((r >> 2) & 4)
+                      : (r & 7) | ((r >> 1) & 8);
   }
   __device__ __forceinline__ static int vswz(int r) { return (r >> 2) & 3; }
   // key of A row R of the S^T MFMA
@@ -69,17 +79,19 @@ template <int HD, int BM_ = 128> struct AttnFwd8 {
     const int g = (threadIdx.x & 63) >> 5;
 #pragma unroll
     for (int c = 0; c < D / 64; ++c) {
-      const i32x4_t *src = reinterpret_cast<const i32x4_t *>(Qh + m * sm + 64 * c + 32 * g);
-      const i32x4_t lo = src[0], hi = src[1];
+      const int b0 = 64 * c + 32 * g; // the lane's first byte of the row
+      const i32x4_t *src = reinterpret_cast<const i32x4_t *>(Qh + m * sm + b0);
+      const i32x4_t lo = b0 < DR ? src[0] : i32x4_t{0, 0, 0, 0};
+      const i32x4_t hi = b0 + 16 < DR ? src[1] : i32x4_t{0, 0, 0, 0};
       qf.v[c] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     }
   }
   __device__ __forceinline__ static uint32_t k_bytes(int64_t n_ctx, int64_t sm) {
-    return (uint32_t)((n_ctx - 1) * sm + D);
+    return (uint32_t)((n_ctx - 1) * sm + DR);
   }
   // v is [HEAD_DIM][N_CTX] per head (key-contiguous), sm the dim stride.
   __device__ __forceinline__ static uint32_t v_bytes(int64_t n_ctx, int64_t sm) {
-    return (uint32_t)((D - 1) * sm + n_ctx);
+    return (uint32_t)((DR - 1) * sm + n_ctx);
   }
 
   __device__ __forceinline__ static void dma16(uint32_t voff, const i32x4_t &rsrc, uint32_t soff,
@@ -91,16 +103,18 @@ template <int HD, int BM_ = 128> struct AttnFwd8 {
   // Per-lane source offsets of the wave's DMA loads: load u of wave w fills
   // 1 KiB of LDS.  K: rows 1024/D (DMA w + u) + i/KCPR of D bytes; V^T: dim
   // rows 16 (DMA w + u) + i/4 of 64 bytes.  Lane i's chunk position holds the
-  // source chunk (position ^ swizzle(row)).
+  // source chunk (position ^ swizzle(row)).  K chunks and V^T dim rows past
+  // the real head dim take kOOB (zeros).
   __device__ __forceinline__ static void kv_offsets(int wave, int64_t k_sm, int64_t v_sm,
                                                     uint32_t (&ko)[DMA], uint32_t (&vo)[DMA]) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int u = 0; u < DMA; ++u) {
       const int kr = (1024 / D) * (DMA * wave + u) + lane / KCPR, kp = lane % KCPR;
-      ko[u] = (uint32_t)(kr * k_sm + 16 * (kp ^ kswz(kr)));
+      const int kc = kp ^ kswz(kr);
+      ko[u] = 16 * kc >= DR ? kOOB : (uint32_t)(kr * k_sm + 16 * kc);
       const int vr = 16 * (DMA * wave + u) + lane / 4, vp = lane % 4;
-      vo[u] = (uint32_t)(vr * v_sm + 16 * (vp ^ vswz(vr)));
+      vo[u] = vr >= DR ? kOOB : (uint32_t)(vr * v_sm + 16 * (vp ^ vswz(vr)));
     }
   }
   // K block j: rows j BN .. of the key-major K; V block j: bytes j BN .. of
@@ -265,6 +279,8 @@ template <int HD, int BM_ = 128> struct AttnFwd8 {
     for (int bd = 0; bd < D / 32; ++bd)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
+        if (32 * bd + 8 * q >= DR) // the layout's dims past the real head dim
+          continue;
         int w = __builtin_amdgcn_cvt_pk_bf8_f32(acc[bd][4 * q] / l_i, acc[bd][4 * q + 1] / l_i,
                                                 0, false);
         w = __builtin_amdgcn_cvt_pk_bf8_f32(acc[bd][4 * q + 2] / l_i, acc[bd][4 * q + 3] / l_i, w,
@@ -275,7 +291,7 @@ template <int HD, int BM_ = 128> struct AttnFwd8 {
 };
 
 template <bool CAUSAL, int HD, int BM = 128>
-__global__ void __launch_bounds__(BM * 2, 2) attn_fwd8_kernel(AttnArgs p) {
+__global__ void __launch_bounds__(BM * 2, HD >= 256 ? 1 : 2) attn_fwd8_kernel(AttnArgs p) {
   attn_fwd_body<CAUSAL, AttnFwd8<HD, BM>>(p);
 }
 

@@ -329,9 +329,8 @@ def attention(q, k, v, causal, sm_scale, USE_TMA=True, *, return_lse=False, plan
     """Forward of the fused-attention tutorial's `attention(q, k, v, causal,
     sm_scale, USE_TMA=True)` (R:pass/LoopSplit/06-fused-attention.py:583-640) on the
     MI355X kernel: q, k, v [Z, H, N_CTX, HEAD_DIM], head dim 16, 32, 64, 128
-    or 256 in fp16 or bf16 (head dim contiguous), or 64 or 128 in
-    float8_e5m2 as the tutorial's
-    fp8 provider passes them (:774-779): q and k head-dim contiguous, v
+    or 256, in fp16 or bf16 (head dim contiguous) or in float8_e5m2 as the
+    tutorial's fp8 provider passes them (:774-779): q and k head-dim contiguous, v
     key-contiguous (stride 1 along N_CTX, "when v is in float8_e5m2 it is
     transposed", :586).  o has q's type; p is rounded to it before p @ v
     (:81-84).  Returns o (and M, the base-2 logsumexp [Z, H, N_CTX] the
