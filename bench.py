@@ -251,7 +251,7 @@ def bench_vendor_bf16(dev, M, N, K, steps, warmup, seed=1):
                 tflops=2.0 * M * N * K / ms / 1e9)
 
 
-def bench_w8a8(tx, dev, M, N, K, steps, warmup, flush, seed=3):
+def bench_w8a8(tx, dev, M, N, K, steps, warmup, flush, seed=3, block=(0, 0, 0)):
     import torch
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
@@ -260,7 +260,7 @@ def bench_w8a8(tx, dev, M, N, K, steps, warmup, flush, seed=3):
     sa = torch.rand((M,), generator=g, device=dev) * 0.019 + 0.001
     sb = torch.rand((N,), generator=g, device=dev) * 0.019 + 0.001
     c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    run = Launcher(tx, a, b, c, sa, sb, tx.SCALE_ROWCOL)
+    run = Launcher(tx, a, b, c, sa, sb, tx.SCALE_ROWCOL, block)
     iso, _ = time_cold(run, steps, warmup, flush)
     med = time_cold_in_stream(run, flush)
     warm = time_back_to_back(run, steps, warmup)

@@ -180,15 +180,15 @@ def test_k_zero_and_empty(gpu):
 # ----------------------------------------------------------------------------- int8
 
 
-def run_w8a8(gpu, M, N, K, seed=0):
+def run_w8a8(gpu, M, N, K, seed=0, block=(0, 0, 0)):
     import torch
-    say(f"w8a8 M={M} N={N} K={K}")
+    say(f"w8a8 M={M} N={N} K={K} block={block}")
     a = uniform_i8((M, K), 1 + seed)
     b = uniform_i8((K, N), 2 + seed)
     sa = uniform_scales(M, 3 + seed)
     sb = uniform_scales(N, 4 + seed)
     c = tx.dot(to_device(a, gpu), to_device(b, gpu), scale_a=to_device(sa, gpu),
-               scale_b=to_device(sb, gpu), out_dtype=torch.bfloat16)
+               scale_b=to_device(sb, gpu), out_dtype=torch.bfloat16, block=block)
     torch.cuda.synchronize()
     return a, b, sa, sb, from_device(c)
 
@@ -214,6 +214,35 @@ def test_w8a8_decode_edges(gpu, M, N, K):
     ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 64, 64),
                            scale_mode=oracle.SCALE_ROWCOL, sa=sa, sb=sb, round_mode=oracle.ROUND_RNE)
     assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("M,N,K,bm", [(256, 8192, 8192, 256), (256, 8192, 8192, 128),
+                                      (192, 4096, 8192, 128), (128, 8192, 8192, 128),
+                                      (65, 8208, 1008, 128), (100, 4096, 2080, 256),
+                                      (130, 272, 4160, 256), (200, 1024, 64, 256),
+                                      (255, 1000, 2000, 256), (192, 8200, 8190, 256),
+                                      (129, 16, 16, 128)])
+def test_w8a8_row_kernel(gpu, M, N, K, bm):
+    """The row-parallel decode tile (block_m 128 / 256 past M = 64: every wave takes
+    every K batch of its strip, B staged once per slice in a shared ring), split-K included:
+    bit-exact, ragged M, N and K included."""
+    a, b, sa, sb, got = run_w8a8(gpu, M, N, K, seed=M + bm, block=(bm, 128, 128))
+    ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 64, 64),
+                           scale_mode=oracle.SCALE_ROWCOL, sa=sa, sb=sb, round_mode=oracle.ROUND_RNE)
+    mism = np.flatnonzero(got != ref)
+    assert mism.size == 0, f"{mism.size} mismatches, first at {np.unravel_index(mism[0], got.shape)}"
+
+
+def test_w8a8_row_kernel_shares_workspace(gpu):
+    """Row-kernel and sliced launches of different shapes on one cached workspace: the counters
+    each leaves at zero serve the next."""
+    for M, N, K, bm in ((256, 8192, 8192, 256), (16, 8192, 8192, 0), (128, 8192, 8192, 128),
+                        (256, 8192, 8192, 64), (256, 4096, 8192, 256)):
+        a, b, sa, sb, got = run_w8a8(gpu, M, N, K, seed=M + N + bm,
+                                     block=(bm, 128, 128 if bm > 64 else 64) if bm else (0, 0, 0))
+        ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 256, 128),
+                               scale_mode=oracle.SCALE_ROWCOL, sa=sa, sb=sb)
+        assert np.array_equal(got, ref), f"M={M} N={N} K={K} block_m={bm}"
 
 
 def test_w8a8_workspace_across_shapes(gpu):

@@ -27,6 +27,7 @@
 #include "mx_upcast.h"
 
 #include "decode_i8.h"
+#include "decode_rows_i8.h"
 #include "gemm16_dma.h"
 #include "gemm8_w4.h"
 #include "gemm8_n224.h"
@@ -181,6 +182,11 @@ constexpr int kNumGemmConfigs = sizeof(kGemmConfigs) / sizeof(kGemmConfigs[0]);
 typedef void (*DecodeKernelFn)(DecodeArgs);
 const DecodeKernelFn kDecodeKernels[4] = {decode_i8_kernel<1>, decode_i8_kernel<2>,
                                            decode_i8_kernel<3>, decode_i8_kernel<4>};
+// The row-parallel decode kernel by 16-row blocks per wave (MT = 2, 4): rings
+// of 4 and 3 slots of 32 and 48 KiB (a 128-row batch: B's 16 KiB and the
+// waves' A).
+const DecodeKernelFn kDecodeRowsKernels[2] = {decode_rows_i8_kernel<2, 4>,
+                                              decode_rows_i8_kernel<4, 3>};
 
 // MFMA format code of an MX operand type (-1 if it has none).
 int mxFormat(int32_t t) {
@@ -311,24 +317,39 @@ bool useDecode(const tx_dot_desc &d) {
 // workgroup streams (fewer splits), so they are used only once M outgrows one
 // wave's accumulators.
 int decodeMT(int64_t M) { return M > 64 ? 4 : (int)cdiv(M > 0 ? M : 1, 16); }
-int decodeSlices(int64_t M) { return (int)cdiv(M > 0 ? M : 1, 16 * decodeMT(M)); }
+
+// The row-parallel decode kernel (decode_rows_i8.h), named by block_m 128 or
+// 256 past M = 64 (and 128-row K batches, block_k 128): a workgroup of 4
+// waves x 16 MT rows (MT = block_m / 64) takes every K batch of its strip,
+// so a slice of block_m rows streams B once.
+bool decodeRows(const tx_dot_desc &d) {
+  return d.M > 64 && (d.block_m == 128 || d.block_m == 256);
+}
+int decodeSlices(const tx_dot_desc &d) {
+  const int64_t M = d.M > 0 ? d.M : 1;
+  return (int)cdiv(M, decodeRows(d) ? d.block_m : 16 * decodeMT(M));
+}
 
 // The decode kernel's tile as the arith_intensity pass names it: a row slice
 // (16 MT rows) x a 128-column strip x 64-row K batches.  A caller's explicit
 // block other than this runs the tile it names (or is refused).
 bool decodeTile(const tx_dot_desc &d) {
-  return d.block_m == 16 * decodeMT(d.M) && d.block_n == kDecodeStripN &&
-         d.block_k == kDecodeBatchK;
+  return d.block_n == kDecodeStripN &&
+         (decodeRows(d) ? d.block_k == kRowsBatchK
+                        : d.block_m == 16 * decodeMT(d.M) && d.block_k == kDecodeBatchK);
 }
 
 // Split-K factor for the decode kernel: a power of two (<= kMaxSplit) so
 // that slices * strips * ksplit workgroups cover the CUs about once, each
 // with at least four 64-row batches per wave.
-int decodeSplit(int64_t M, int64_t N, int64_t K) {
-  const int64_t strips = cdiv(N, kDecodeStripN) * decodeSlices(M);
-  const int64_t batches = cdiv(K, kDecodeBatchK);
+int decodeSplit(const tx_dot_desc &d) {
+  const int64_t strips = cdiv(d.N, kDecodeStripN) * decodeSlices(d);
+  const int64_t batches = cdiv(d.K, d.block_k);
+  // the K-interleaved kernel deals a split's 64-row batches to its 4 waves;
+  // the row kernel's waves each take all of its 128-row batches
+  const int64_t min_batches = decodeRows(d) ? 8 : 4 * kDecodeWaves;
   int ks = 1;
-  while (ks < (int)kMaxSplit && strips * ks < 256 && batches / (ks * 2) >= 4 * kDecodeWaves)
+  while (ks < (int)kMaxSplit && strips * ks < 256 && batches / (ks * 2) >= min_batches)
     ks *= 2;
   while (ks > 1 && cdiv(batches, ks) * (ks - 1) >= batches)
     ks >>= 1; // every split must own at least one batch
@@ -340,6 +361,10 @@ int64_t decodeCounterBytes(const tx_dot_desc &) { return kDecodeCounterBytes; }
 int64_t decodeWorkspace(const tx_dot_desc &d, int ksplit) {
   if (ksplit <= 1)
     return 0;
+  if (decodeRows(d)) // partials in lane order, per slice and strip
+    return decodeCounterBytes(d) +
+           ksplit * decode_rows_split_bytes(decodeSlices(d), (int)cdiv(d.N, kDecodeStripN),
+                                            d.block_m / 64);
   return decodeCounterBytes(d) + (int64_t)ksplit * d.M * ((d.N + 3) & ~3) * 4;
 }
 
@@ -388,10 +413,10 @@ int txMi355xDotRun(tx_dot_plan *plan) {
                 "no kernel for a_type=%d b_type=%d c_type=%d scale_mode=%d",
                 d.a_type, d.b_type, d.c_type, d.scale_mode);
   if (useDecode(d) && decodeTile(d)) {
-    const int ks = decodeSplit(d.M, d.N, d.K);
+    const int ks = decodeSplit(d);
     plan->kernel = TX_KERNEL_DECODE_I8;
     plan->split_k = ks;
-    plan->grid_x = (int32_t)(cdiv(d.N, kDecodeStripN) * ks * decodeSlices(d.M));
+    plan->grid_x = (int32_t)(cdiv(d.N, kDecodeStripN) * ks * decodeSlices(d));
     plan->grid_y = plan->grid_z = 1;
     plan->block_threads = kDecodeWaves * 64;
     plan->workspace_bytes = decodeWorkspace(d, ks);
@@ -710,7 +735,7 @@ int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   const int mt = decodeMT(d.M);
   if (d.M > kDecodeMaxM)
     return fail(TX_ERR_INVALID, "decode plan with M=%lld", (long long)d.M);
-  const int slices = decodeSlices(d.M);
+  const int slices = decodeSlices(d);
   const int ks = plan.split_k;
   if (ks < 1 || ks > (int)kMaxSplit || (ks & (ks - 1)))
     return fail(TX_ERR_INVALID, "decode split %d is not a power of two <= %u", ks,
@@ -736,14 +761,16 @@ int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   a.ldc = d.ldc;
   a.ksplit = ks;
   a.slices = slices;
-  const int64_t batches = cdiv(d.K, kDecodeBatchK);
+  const int64_t batches = cdiv(d.K, d.block_k); // the tile's K batch: 64 or 128 rows
   a.batches_per_split = (int32_t)cdiv(batches, ks);
-  a.k_main_batches = (int32_t)(plan.k_split / kDecodeBatchK);
+  a.k_main_batches = (int32_t)(plan.k_split / d.block_k);
   const int64_t counters = decodeCounterBytes(d);
   a.counters = static_cast<uint32_t *>(ws);
   a.partials = need > 0 ? reinterpret_cast<int32_t *>(static_cast<uint8_t *>(ws) + counters)
                         : nullptr;
-  hipLaunchKernelGGL(kDecodeKernels[mt - 1], dim3(plan.grid_x),
+  const DecodeKernelFn fn =
+      decodeRows(d) ? kDecodeRowsKernels[d.block_m / 128 - 1] : kDecodeKernels[mt - 1];
+  hipLaunchKernelGGL(fn, dim3(plan.grid_x),
                      dim3(plan.block_threads), 0, stream, a);
   TX_HIP_CHECK(hipGetLastError());
   return TX_OK;
@@ -819,7 +846,7 @@ int checkPlan(const tx_dot_plan &p) {
   if (p.kernel == TX_KERNEL_DECODE_I8) {
     const int sk = p.split_k;
     if (!useDecode(d) || !decodeTile(d) || sk < 1 || sk > (int)kMaxSplit ||
-        (sk & (sk - 1)) || p.grid_x != cdiv(d.N, kDecodeStripN) * sk * decodeSlices(d.M) ||
+        (sk & (sk - 1)) || p.grid_x != cdiv(d.N, kDecodeStripN) * sk * decodeSlices(d) ||
         p.block_threads != kDecodeWaves * 64 || p.workspace_bytes != decodeWorkspace(d, sk))
       return fail(TX_ERR_INVALID, "the plan's decode launch does not follow from its descriptor");
     return TX_OK;

@@ -7,12 +7,13 @@
 //  * A workgroup owns a strip of 128 columns, a range of K (split-K) and a
 //    slice of up to 16 * MT rows (row slices of 64 past M = 64); each of its
 //    4 waves takes every 4th batch of 64 K rows (8 KiB of B).
-//  * Each wave has a private LDS ring of STAGES slots fed by
-//    global_load_lds_dwordx4 (lane l of a wave-wide load writes 16 bytes at
-//    slot + 16 l): 8 loads per batch move 64 rows x 128 bytes, 128-byte row
-//    segments, straight into LDS with no VGPR staging.  MT more loads bring
-//    the batch's A fragments straight into registers (a lane's 16 bytes of
-//    row-major A are its MFMA operand).  B's loads are non-temporal: each
+//  * Each wave has a private LDS ring of STAGES slots (4, or 3 past
+//    M = 32) fed by global_load_lds_dwordx4 (lane l of a wave-wide load
+//    writes 16 bytes at slot + 16 l): 8 loads per batch move 64 rows x 128
+//    bytes, 128-byte row segments, straight into LDS with no VGPR staging.
+//    MT more loads bring the batch's A fragments into the slot, each lane
+//    fetching its own MFMA operand (16 bytes of row-major A) to where it
+//    reads it back.  B's loads are non-temporal: each
 //    byte is read once, and allocating loads would also have to write back
 //    whatever dirty lines they evict (measured: 2.7 vs 5.1 TB/s after a
 //    write-heavy kernel).  Waves never synchronise with
@@ -85,16 +86,129 @@ __device__ __forceinline__ i32x4_t mfma_i8_16(const i32x4_t &a, const i32x4_t &b
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
 }
 
+// v_mfma_i32_32x32x32_i8: measured at 4.5 POP/s on the chip (4 waves per CU,
+// 4 accumulators each) against 1.6 for v_mfma_i32_16x16x64_i8 (8 per wave),
+// so the decode kernels take their int8 products 32 x 32 at a time.
+__device__ __forceinline__ i32x16_t mfma_i8_32(const i32x4_t &a, const i32x4_t &b,
+                                               i32x16_t acc) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc, 0, 0, 0);
+}
 
+// Operands of the 32x32x32 MFMA in a decode ring slot.
+//
+// B: a batch of 64 rows (K) x 128 bytes (columns), 16-byte chunk c of row r
+// at c ^ (r & 7).  For K step ks (rows 32 ks .. +31) lane l takes column
+// 32 cb + l%32, rows 32 ks + 16 (l/32) .. +15: the 16-lane group g = l/16
+// holds columns 16 (g%2) .. +15 of block cb and rows 16 (g/2) .. +15 of the
+// step, read as two ds_read_b64_tr_b8 of 8 rows (group lane L reads row
+// 16 (g/2) + L/2, +8 for the second, bytes 8 (L%2) .. +7 of chunk
+// 2 cb + g%2).  Within a group the 8 rows sit in 8 different chunks.  Step
+// 1 is 32 rows (4 KiB) further with the same swizzle.
+__device__ __forceinline__ uint32_t tr32_off(int lane, int cb) {
+  const int g = lane >> 4, L = lane & 15;
+  const int row = 16 * (g >> 1) + (L >> 1);
+  return row * 128 + (((2 * cb + (g & 1)) ^ (row & 7)) << 4) + 8 * (L & 1);
+}
+//
+// A: R32 blocks of 32 rows; the wave's A of a batch lies in the slot as
+// 16-row loads of 1 KiB, lane l' of load t holding row 16 t + l'%16, K bytes
+// 16 (l'/16) .. +15 at 16 l'.  Lane l's operand for row block rb and step
+// ks -- row 32 rb + l%32, K bytes 32 ks + 16 (l/32) .. +15 -- is lane
+// (l%16) + 16 (2 ks + l/32) of load 2 rb + (l/16)%2: at a32_off(l) +
+// 2048 rb + 512 ks.  16 lanes read 256 contiguous bytes.
+__device__ __forceinline__ uint32_t a32_off(int lane) {
+  return ((lane >> 4) & 1) * 1024 + 16 * (lane & 15) + 256 * (lane >> 5);
+}
+
+// One asm block: the A operands (both K steps, R32 row blocks) and step 0's
+// B fragments, waiting for them before it ends; then step 1's B fragments.
+template <int R32>
+__device__ __forceinline__ void lds_read_a32_b0(uint32_t a_addr, uint32_t b_base,
+                                                const uint32_t (&off)[4], i32x4_t (&a)[R32][2],
+                                                v2i_t (&lo)[4], v2i_t (&hi)[4]) {
+  static_assert(R32 == 1 || R32 == 2, "32 or 64 rows");
+  if constexpr (R32 == 1)
+    asm volatile("ds_read_b64_tr_b8 %0, %10\n\tds_read_b64_tr_b8 %1, %10 offset:1024\n\t"
+                 "ds_read_b64_tr_b8 %2, %11\n\tds_read_b64_tr_b8 %3, %11 offset:1024\n\t"
+                 "ds_read_b64_tr_b8 %4, %12\n\tds_read_b64_tr_b8 %5, %12 offset:1024\n\t"
+                 "ds_read_b64_tr_b8 %6, %13\n\tds_read_b64_tr_b8 %7, %13 offset:1024\n\t"
+                 "ds_read_b128 %8, %14\n\tds_read_b128 %9, %14 offset:512\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1]), "=v"(lo[2]), "=v"(hi[2]),
+                   "=v"(lo[3]), "=v"(hi[3]), "=v"(a[0][0]), "=v"(a[0][1])
+                 : "v"(b_base + off[0]), "v"(b_base + off[1]), "v"(b_base + off[2]),
+                   "v"(b_base + off[3]), "v"(a_addr)
+                 : "memory");
+  else
+    asm volatile("ds_read_b64_tr_b8 %0, %12\n\tds_read_b64_tr_b8 %1, %12 offset:1024\n\t"
+                 "ds_read_b64_tr_b8 %2, %13\n\tds_read_b64_tr_b8 %3, %13 offset:1024\n\t"
+                 "ds_read_b64_tr_b8 %4, %14\n\tds_read_b64_tr_b8 %5, %14 offset:1024\n\t"
+                 "ds_read_b64_tr_b8 %6, %15\n\tds_read_b64_tr_b8 %7, %15 offset:1024\n\t"
+                 "ds_read_b128 %8, %16\n\tds_read_b128 %9, %16 offset:512\n\t"
+                 "ds_read_b128 %10, %16 offset:2048\n\tds_read_b128 %11, %16 offset:2560\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1]), "=v"(lo[2]), "=v"(hi[2]),
+                   "=v"(lo[3]), "=v"(hi[3]), "=v"(a[0][0]), "=v"(a[0][1]), "=v"(a[1][0]),
+                   "=v"(a[1][1])
+                 : "v"(b_base + off[0]), "v"(b_base + off[1]), "v"(b_base + off[2]),
+                   "v"(b_base + off[3]), "v"(a_addr)
+                 : "memory");
+}
+__device__ __forceinline__ void lds_read_b1(uint32_t b_base, const uint32_t (&off)[4],
+                                            v2i_t (&lo)[4], v2i_t (&hi)[4]) {
+  asm volatile("ds_read_b64_tr_b8 %0, %8 offset:4096\n\tds_read_b64_tr_b8 %1, %8 offset:5120\n\t"
+               "ds_read_b64_tr_b8 %2, %9 offset:4096\n\tds_read_b64_tr_b8 %3, %9 offset:5120\n\t"
+               "ds_read_b64_tr_b8 %4, %10 offset:4096\n\tds_read_b64_tr_b8 %5, %10 offset:5120\n\t"
+               "ds_read_b64_tr_b8 %6, %11 offset:4096\n\tds_read_b64_tr_b8 %7, %11 offset:5120\n\t"
+               "s_waitcnt lgkmcnt(0)"
+               : "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1]), "=v"(lo[2]), "=v"(hi[2]),
+                 "=v"(lo[3]), "=v"(hi[3])
+               : "v"(b_base + off[0]), "v"(b_base + off[1]), "v"(b_base + off[2]),
+                 "v"(b_base + off[3])
+               : "memory");
+}
+
+
+
+// s_waitcnt vmcnt(C), the other counters untouched (gfx9 encoding: vmcnt
+// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int C> __device__ __forceinline__ void wait_vmcnt() {
+  static_assert(C >= 0 && C <= 63, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((C & 0xf) | ((C >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// ds_read_b128 of MT consecutive KiB at `addr` (a lane's 16 bytes each),
+// waiting for them in the same asm block: the compiler sees the values
+// defined only once they are in the registers.
+template <int MT>
+__device__ __forceinline__ void lds_read_a(uint32_t addr, i32x4_t (&a)[MT]) {
+  if constexpr (MT == 1)
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(a[0]) : "v"(addr) : "memory");
+  else if constexpr (MT == 2)
+    asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:1024\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=v"(a[0]), "=v"(a[1]) : "v"(addr) : "memory");
+  else if constexpr (MT == 3)
+    asm volatile("ds_read_b128 %0, %3\n\tds_read_b128 %1, %3 offset:1024\n\t"
+                 "ds_read_b128 %2, %3 offset:2048\n\ts_waitcnt lgkmcnt(0)"
+                 : "=v"(a[0]), "=v"(a[1]), "=v"(a[2]) : "v"(addr) : "memory");
+  else
+    asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:1024\n\t"
+                 "ds_read_b128 %2, %4 offset:2048\n\tds_read_b128 %3, %4 offset:3072\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=v"(a[0]), "=v"(a[1]), "=v"(a[2]), "=v"(a[3]) : "v"(addr) : "memory");
+}
 
 template <int MT> struct DecodeCfg {
-  // Slots per wave: 4 waves x STAGES x 8 KiB of B (A goes to registers).
-  static constexpr int STAGES = 5;
+  // One slot per wave and ring stage: B's 8 KiB batch, then the wave's A
+  // rows of that batch (MT KiB); as many stages as fit 160 KiB (4 for
+  // MT <= 2, 3 beyond).
   static constexpr int B_BYTES = kDecodeBatchK * kDecodeStripN; // 8 KiB
-  static constexpr int SLOT = B_BYTES;
-  static constexpr int VM_PER_BATCH = 8 + MT; // B loads into LDS + A loads per batch
-  static constexpr int LDS = kDecodeWaves * STAGES * SLOT;
-  static_assert(LDS <= 160 * 1024, "ring exceeds LDS");
+  static constexpr int SLOT = B_BYTES + MT * 1024;
+  static constexpr int STAGE_BYTES = kDecodeWaves * SLOT;
+  static constexpr int STAGES = 160 * 1024 / STAGE_BYTES;
+  static constexpr int VM_PER_BATCH = 8 + MT; // B and A loads into LDS per batch
+  static_assert(STAGES >= 3, "at least two batches in flight behind the one in use");
   static_assert((STAGES - 1) * VM_PER_BATCH <= 63, "vmcnt is 6 bits");
 };
 
@@ -103,16 +217,8 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
     decode_i8_kernel(DecodeArgs p) {
   typedef DecodeCfg<MT> Cfg;
   constexpr int STAGES = Cfg::STAGES;
-  constexpr int STAGE_BYTES = kDecodeWaves * Cfg::SLOT;
-  // One __shared__ array per ring stage (all waves' slots of that stage):
-  // distinct objects let the compiler's wait-count insertion tell the slot a
-  // direct-to-LDS load is filling from the slots being read.
-  __shared__ __attribute__((aligned(1024))) uint8_t st0[STAGE_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t st1[STAGE_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t st2[STAGE_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t st3[STAGE_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t st4[STAGE_BYTES];
-  static_assert(STAGES == 5, "five ring stages fill the 160 KiB of LDS");
+  constexpr int STAGE_BYTES = Cfg::STAGE_BYTES;
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[STAGES * STAGE_BYTES];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -144,11 +250,10 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   const int Mr = p.M - row0 < 16 * MT ? p.M - row0 : 16 * MT;
   const int8_t *const Ap = p.A + (int64_t)row0 * p.lda;
   const bool n_edge = n0 + kDecodeStripN > p.N;
-  uint8_t *const all_st[5] = {st0, st1, st2, st3, st4};
   uint8_t *slots[STAGES];
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
-    slots[s] = all_st[s] + wave * Cfg::SLOT;
+    slots[s] = ring + s * STAGE_BYTES + wave * Cfg::SLOT;
 
   const int total_batches = (p.K + kDecodeBatchK - 1) / kDecodeBatchK;
   const int b_begin = split * p.batches_per_split;
@@ -159,30 +264,38 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   const int first = b_begin + wave;
   const int nb = first < b_end ? (b_end - first + kDecodeWaves - 1) / kDecodeWaves : 0;
 
-  // Loads of one batch: B direct to LDS into `slot`, A straight into the
-  // registers `a` (a lane's 16 bytes of A -- row 16 t + l % 16, K 16 (l / 16)
-  // .. +15 of the batch -- are exactly its MFMA operand).
-  auto issue = [&](int b, uint8_t *slot, i32x4_t (&a)[MT]) {
+  // Loads of this wave's batch i (split batch first + 4 i) into `slot`, all
+  // direct to LDS: B's 8 KiB, then the A rows, lane l of A load t fetching
+  // row 16 t + l%16, K bytes 16 (l/16) .. +15 (its own MFMA operand) to
+  // B_BYTES + t KiB + 16 l, where the lane reads it back.  No loaded VGPR
+  // is live across the loop: with direct-to-LDS loads pending, the compiler
+  // can only wait for a loaded register with vmcnt(0) (it counts the two
+  // kinds of load as events that may complete out of order), which drained
+  // the ring once a round when A went to registers.  For i >= nb every load
+  // reads the zero chunk instead, so each step issues the same loads.
+  auto issue = [&](int i, uint8_t *slot) {
+    const bool live = i < nb;
+    const int b = first + kDecodeWaves * i;
     const int64_t k0 = (int64_t)b * kDecodeBatchK;
-    const bool mask = n_edge || b >= p.k_main_batches;
+    const bool mask = !live || n_edge || b >= p.k_main_batches;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = 8 * i + (lane >> 3), pc = lane & 7;
+    for (int q = 0; q < 8; ++q) {
+      const int row = 8 * q + (lane >> 3), pc = lane & 7;
       const int c = pc ^ (row & 7);
       const int64_t k = k0 + row, n = n0 + 16 * c;
       const void *src = p.B + k * p.ldb + n;
-      if (mask && (k >= p.K || n >= p.N))
+      if (mask && (!live || k >= p.K || n >= p.N))
         src = tx_zero_chunk;
-      dma16_stream(src, (lds_void *)(slot + i * 1024)); // B is read once
+      dma16_stream(src, (lds_void *)(slot + q * 1024)); // B is read once
     }
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
       const int m = 16 * t + (lane & 15);
       const int64_t k = k0 + 16 * (lane >> 4);
       const void *src = Ap + (int64_t)m * p.lda + k;
-      if (m >= Mr || (b >= p.k_main_batches && k >= p.K))
+      if (!live || m >= Mr || (b >= p.k_main_batches && k >= p.K))
         src = tx_zero_chunk;
-      a[t] = *reinterpret_cast<const i32x4_t *>(src);
+      dma16(src, (lds_void *)(slot + Cfg::B_BYTES + t * 1024)); // A: re-read by other strips
     }
   };
 
@@ -207,8 +320,10 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
     const int r0 = 16 * G + (L >> 1);
     tr_off[j] = r0 * 128 + ((j ^ (r0 & 7)) << 4) + 8 * (L & 1); // row r0 + 8: +1024
   }
-  auto consume = [&](const uint8_t *slot, const i32x4_t (&a)[MT]) {
+  auto consume = [&](const uint8_t *slot) {
     const uint32_t base = lds_addr(slot);
+    i32x4_t a[MT];
+    lds_read_a<MT>(base + Cfg::B_BYTES + 16 * lane, a);
     v2i_t lo[8], hi[8];
     // Columns 0..63.
     asm volatile(
@@ -243,22 +358,6 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
     }
   };
 
-  // s_waitcnt vmcnt(newer * loads per batch), other counters untouched
-  // (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
-  auto wait_newer = [](int newer) {
-    constexpr int V = Cfg::VM_PER_BATCH;
-    if (newer <= 0)
-      __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xf << 8));
-    else if (newer == 1)
-      __builtin_amdgcn_s_waitcnt((V & 0xf) | ((V >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-    else if (newer == 2)
-      __builtin_amdgcn_s_waitcnt(((2 * V) & 0xf) | (((2 * V) >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-    else if (newer == 3)
-      __builtin_amdgcn_s_waitcnt(((3 * V) & 0xf) | (((3 * V) >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-    else
-      __builtin_amdgcn_s_waitcnt(((4 * V) & 0xf) | (((4 * V) >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-  };
-
   // After the K loop each thread owns a column quad of the strip, columns
   // cq .. cq + 3 with cq = 4 (tid % 32), in the RPT = 2 MT rows tid / 32 + 8 j
   // (j < RPT): four consecutive int32 per row, moved as one 16-byte LDS read
@@ -278,49 +377,44 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
     sav[j] = p.sa[row0 + (m < Mr ? m : 0)];
   }
 
-  // Prologue: STAGES - 1 batches in flight.  Batch i uses slot and A
-  // registers i % STAGES.
-  i32x4_t a_regs[STAGES][MT];
+  // Prologue: STAGES - 1 batches in flight; batch i uses slot i % STAGES.
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
-    if (s < nb)
-      issue(first + kDecodeWaves * s, slots[s], a_regs[s]);
-  // Main loop, unrolled by STAGES so slot addresses are static.
-  for (int i0 = 0; i0 < nb; i0 += STAGES) {
+    issue(s, slots[s]);
+  // Main loop, unrolled by STAGES so slot addresses are static; the loop is
+  // left at the first batch past nb (never skipping a step and going round).
+  for (int i0 = 0;; i0 += STAGES) {
 #pragma unroll
     for (int s = 0; s < STAGES; ++s) {
       const int i = i0 + s;
-      if (i < nb) {
-        const int in = i + STAGES - 1; // batch whose loads go out now
-        if (in < nb) {
-          // Its slot was read at step i - 1: wait for those LDS reads
-          // (lgkmcnt 0) before the new loads may overwrite it.
-          __builtin_amdgcn_s_waitcnt(0xf | (0x3 << 14) | (0x7 << 4));
-          issue(first + kDecodeWaves * in, slots[(s + STAGES - 1) % STAGES],
-                a_regs[(s + STAGES - 1) % STAGES]);
-        }
-        const int newer = (nb - 1 - i) < (STAGES - 1) ? (nb - 1 - i) : (STAGES - 1);
-        wait_newer(newer);
-        consume(slots[s], a_regs[s]);
-      }
+      if (i >= nb)
+        goto k_loop_done;
+      // Batch i + STAGES - 1 goes into the slot read at step i - 1: wait for
+      // those LDS reads (lgkmcnt 0) before the new loads may overwrite it.
+      __builtin_amdgcn_s_waitcnt(0xf | (0x3 << 14) | (0x7 << 4));
+      issue(i + STAGES - 1, slots[(s + STAGES - 1) % STAGES]);
+      wait_vmcnt<(STAGES - 1) * Cfg::VM_PER_BATCH>(); // batch i landed, later ones need not
+      consume(slots[s]);
     }
   }
-
+k_loop_done:
   __builtin_amdgcn_s_waitcnt(0); // every load of the loop has landed
   // Sum the 4 waves' accumulators through LDS (the ring is free now): wave
-  // w stores its tile into stage w's array with plain stores, then every
+  // w stores its tile into region w of the ring with plain stores, then every
   // thread adds the 4 copies of its quads.  acc[t][j] register r of lane l:
   // row m = 16 t + 4 (l / 16) + r, column n = 16 j + l % 16; element (m, n)
   // sits at m * 128 + (n ^ (16 * ((m >> 2) & 3))), so the four 16-lane groups
   // of one store hit different banks, and the XOR (bits 4-5 of n) keeps each
   // column quad contiguous.
   constexpr int TILE = MT * 16 * kDecodeStripN; // int32 of the strip's sums
-  static_assert(TILE * 4 <= STAGE_BYTES, "reduction tile exceeds a stage");
+  // wave w's copy at ring + w * TILE * 4 bytes; the flag word after the four
+  static_assert(4 * TILE * 4 + 4 <= STAGES * STAGE_BYTES, "reduction tiles exceed the ring");
+  int32_t *const red = reinterpret_cast<int32_t *>(ring);
+  uint32_t *const flag = reinterpret_cast<uint32_t *>(ring + 4 * TILE * 4);
   auto swz = [](int m, int n) { return m * kDecodeStripN + (n ^ (16 * ((m >> 2) & 3))); };
   __syncthreads();
   {
-    uint8_t *const region = wave == 0 ? st0 : wave == 1 ? st1 : wave == 2 ? st2 : st3;
-    int32_t *mine_tile = reinterpret_cast<int32_t *>(region);
+    int32_t *mine_tile = red + wave * TILE;
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
@@ -334,10 +428,10 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     const int q = swz(rq + 8 * j, cq);
-    wsum[j] = *reinterpret_cast<const i32x4_t *>(reinterpret_cast<const int32_t *>(st0) + q) +
-              *reinterpret_cast<const i32x4_t *>(reinterpret_cast<const int32_t *>(st1) + q) +
-              *reinterpret_cast<const i32x4_t *>(reinterpret_cast<const int32_t *>(st2) + q) +
-              *reinterpret_cast<const i32x4_t *>(reinterpret_cast<const int32_t *>(st3) + q);
+    wsum[j] = *reinterpret_cast<const i32x4_t *>(red + q) +
+              *reinterpret_cast<const i32x4_t *>(red + TILE + q) +
+              *reinterpret_cast<const i32x4_t *>(red + 2 * TILE + q) +
+              *reinterpret_cast<const i32x4_t *>(red + 3 * TILE + q);
   }
   // C = bf16((float(sum) * sa[m]) * sb[n]) for this thread's quads: one
   // 8-byte store per row (ldc and n0 + cq are multiples of 4), single
@@ -413,11 +507,10 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
     const bool last = old + 1 == (uint32_t)p.ksplit;
     if (last) // every split has arrived: none touches the counter again
       __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // st4 holds no reduction region: its first word carries the flag
-    *reinterpret_cast<volatile uint32_t *>(st4) = last;
+    *reinterpret_cast<volatile uint32_t *>(flag) = last; // past the reduction tiles
   }
   __syncthreads();
-  if (!*reinterpret_cast<volatile uint32_t *>(st4))
+  if (!*reinterpret_cast<volatile uint32_t *>(flag))
     return;
   // Last arrival: add the other splits' partials to its own (still in
   // registers) and apply the epilogue.  The loads are unconditional -- rows
