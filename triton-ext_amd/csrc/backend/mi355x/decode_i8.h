@@ -88,87 +88,26 @@ __device__ __forceinline__ i32x4_t mfma_i8_16(const i32x4_t &a, const i32x4_t &b
 
 // v_mfma_i32_32x32x32_i8: measured at 4.5 POP/s on the chip (4 waves per CU,
 // 4 accumulators each) against 1.6 for v_mfma_i32_16x16x64_i8 (8 per wave),
-// so the decode kernels take their int8 products 32 x 32 at a time.
+// so the row decode kernel takes its int8 products 32 x 32 at a time.
 __device__ __forceinline__ i32x16_t mfma_i8_32(const i32x4_t &a, const i32x4_t &b,
                                                i32x16_t acc) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc, 0, 0, 0);
 }
 
-// Operands of the 32x32x32 MFMA in a decode ring slot.
-//
-// B: a batch of 64 rows (K) x 128 bytes (columns), 16-byte chunk c of row r
+// B operands of the 32x32x32 MFMA in a decode ring slot: a batch of 64 or
+// more rows (K) x 128 bytes (columns), 16-byte chunk c of row r
 // at c ^ (r & 7).  For K step ks (rows 32 ks .. +31) lane l takes column
 // 32 cb + l%32, rows 32 ks + 16 (l/32) .. +15: the 16-lane group g = l/16
 // holds columns 16 (g%2) .. +15 of block cb and rows 16 (g/2) .. +15 of the
 // step, read as two ds_read_b64_tr_b8 of 8 rows (group lane L reads row
 // 16 (g/2) + L/2, +8 for the second, bytes 8 (L%2) .. +7 of chunk
-// 2 cb + g%2).  Within a group the 8 rows sit in 8 different chunks.  Step
-// 1 is 32 rows (4 KiB) further with the same swizzle.
+// 2 cb + g%2).  Within a group the 8 rows sit in 8 different chunks.  Each
+// further step is 32 rows (4 KiB) on, with the same swizzle.
 __device__ __forceinline__ uint32_t tr32_off(int lane, int cb) {
   const int g = lane >> 4, L = lane & 15;
   const int row = 16 * (g >> 1) + (L >> 1);
   return row * 128 + (((2 * cb + (g & 1)) ^ (row & 7)) << 4) + 8 * (L & 1);
 }
-//
-// A: R32 blocks of 32 rows; the wave's A of a batch lies in the slot as
-// 16-row loads of 1 KiB, lane l' of load t holding row 16 t + l'%16, K bytes
-// 16 (l'/16) .. +15 at 16 l'.  Lane l's operand for row block rb and step
-// ks -- row 32 rb + l%32, K bytes 32 ks + 16 (l/32) .. +15 -- is lane
-// (l%16) + 16 (2 ks + l/32) of load 2 rb + (l/16)%2: at a32_off(l) +
-// 2048 rb + 512 ks.  16 lanes read 256 contiguous bytes.
-__device__ __forceinline__ uint32_t a32_off(int lane) {
-  return ((lane >> 4) & 1) * 1024 + 16 * (lane & 15) + 256 * (lane >> 5);
-}
-
-// One asm block: the A operands (both K steps, R32 row blocks) and step 0's
-// B fragments, waiting for them before it ends; then step 1's B fragments.
-template <int R32>
-__device__ __forceinline__ void lds_read_a32_b0(uint32_t a_addr, uint32_t b_base,
-                                                const uint32_t (&off)[4], i32x4_t (&a)[R32][2],
-                                                v2i_t (&lo)[4], v2i_t (&hi)[4]) {
-  static_assert(R32 == 1 || R32 == 2, "32 or 64 rows");
-  if constexpr (R32 == 1)
-    asm volatile("ds_read_b64_tr_b8 %0, %10\n\tds_read_b64_tr_b8 %1, %10 offset:1024\n\t"
-                 "ds_read_b64_tr_b8 %2, %11\n\tds_read_b64_tr_b8 %3, %11 offset:1024\n\t"
-                 "ds_read_b64_tr_b8 %4, %12\n\tds_read_b64_tr_b8 %5, %12 offset:1024\n\t"
-                 "ds_read_b64_tr_b8 %6, %13\n\tds_read_b64_tr_b8 %7, %13 offset:1024\n\t"
-                 "ds_read_b128 %8, %14\n\tds_read_b128 %9, %14 offset:512\n\t"
-                 "s_waitcnt lgkmcnt(0)"
-                 : "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1]), "=v"(lo[2]), "=v"(hi[2]),
-                   "=v"(lo[3]), "=v"(hi[3]), "=v"(a[0][0]), "=v"(a[0][1])
-                 : "v"(b_base + off[0]), "v"(b_base + off[1]), "v"(b_base + off[2]),
-                   "v"(b_base + off[3]), "v"(a_addr)
-                 : "memory");
-  else
-    asm volatile("ds_read_b64_tr_b8 %0, %12\n\tds_read_b64_tr_b8 %1, %12 offset:1024\n\t"
-                 "ds_read_b64_tr_b8 %2, %13\n\tds_read_b64_tr_b8 %3, %13 offset:1024\n\t"
-                 "ds_read_b64_tr_b8 %4, %14\n\tds_read_b64_tr_b8 %5, %14 offset:1024\n\t"
-                 "ds_read_b64_tr_b8 %6, %15\n\tds_read_b64_tr_b8 %7, %15 offset:1024\n\t"
-                 "ds_read_b128 %8, %16\n\tds_read_b128 %9, %16 offset:512\n\t"
-                 "ds_read_b128 %10, %16 offset:2048\n\tds_read_b128 %11, %16 offset:2560\n\t"
-                 "s_waitcnt lgkmcnt(0)"
-                 : "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1]), "=v"(lo[2]), "=v"(hi[2]),
-                   "=v"(lo[3]), "=v"(hi[3]), "=v"(a[0][0]), "=v"(a[0][1]), "=v"(a[1][0]),
-                   "=v"(a[1][1])
-                 : "v"(b_base + off[0]), "v"(b_base + off[1]), "v"(b_base + off[2]),
-                   "v"(b_base + off[3]), "v"(a_addr)
-                 : "memory");
-}
-__device__ __forceinline__ void lds_read_b1(uint32_t b_base, const uint32_t (&off)[4],
-                                            v2i_t (&lo)[4], v2i_t (&hi)[4]) {
-  asm volatile("ds_read_b64_tr_b8 %0, %8 offset:4096\n\tds_read_b64_tr_b8 %1, %8 offset:5120\n\t"
-               "ds_read_b64_tr_b8 %2, %9 offset:4096\n\tds_read_b64_tr_b8 %3, %9 offset:5120\n\t"
-               "ds_read_b64_tr_b8 %4, %10 offset:4096\n\tds_read_b64_tr_b8 %5, %10 offset:5120\n\t"
-               "ds_read_b64_tr_b8 %6, %11 offset:4096\n\tds_read_b64_tr_b8 %7, %11 offset:5120\n\t"
-               "s_waitcnt lgkmcnt(0)"
-               : "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1]), "=v"(lo[2]), "=v"(hi[2]),
-                 "=v"(lo[3]), "=v"(hi[3])
-               : "v"(b_base + off[0]), "v"(b_base + off[1]), "v"(b_base + off[2]),
-                 "v"(b_base + off[3])
-               : "memory");
-}
-
-
 
 // s_waitcnt vmcnt(C), the other counters untouched (gfx9 encoding: vmcnt
 // bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
