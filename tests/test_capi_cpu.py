@@ -189,15 +189,16 @@ def test_kernel_choice(M, N, K, a, c, sm, kernel):
     assert p.kernel == kernel
     assert p.grid_x > 0 and p.block_threads in (256, 512)
     if kernel == tx.KERNEL_DECODE_I8:
-        # 128-column strips x row slices (one up to M = 64, of 128 rows past it) x K
-        # splits cover the 256 CUs; past M = 64 the K batches are 128 rows
-        slices = -(-M // 128) if M > 64 else 1
+        # 128-column strips x row slices (one up to M = 48, of 64 rows up to 128, of 128
+        # past it) x K splits cover the 256 CUs; past M = 48 the K batches are 128 rows
+        bm = 128 if M > 128 else 64 if M > 48 else 16 * -(-M // 16)
         assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == \
-            ((128, 128, 128) if M > 64 else (16 * -(-M // 16), 128, 64))
+            (bm, 128, 128 if M > 48 else 64)
+        slices = -(-M // bm)
         assert p.grid_x == (N // 128) * slices * p.split_k == 256
         # a fixed 64 KiB counter region, then the int32 partials: [split][M][N] up to
-        # M = 64, [split][slice][strip][128 rows x 128 columns] past it
-        rows = M if M <= 64 else slices * 128
+        # M = 48, [split][slice][strip][block_m rows x 128 columns] past it
+        rows = M if M <= 48 else slices * bm
         assert p.workspace_bytes == (65536 + p.split_k * rows * N * 4 if p.split_k > 1 else 0)
     assert (p.split_k & (p.split_k - 1)) == 0
 

@@ -221,10 +221,12 @@ def test_w8a8_decode_edges(gpu, M, N, K):
                                       (65, 8208, 1008, 128), (100, 4096, 2080, 256),
                                       (130, 272, 4160, 256), (200, 1024, 64, 256),
                                       (255, 1000, 2000, 256), (192, 8200, 8190, 256),
-                                      (129, 16, 16, 128)])
+                                      (129, 16, 16, 128), (64, 8192, 8192, 64),
+                                      (16, 8192, 8192, 64), (40, 4096, 2080, 64),
+                                      (130, 272, 4160, 64), (1, 8200, 1000, 64)])
 def test_w8a8_row_kernel(gpu, M, N, K, bm):
-    """The row-parallel decode tile (block_m 128 / 256 past M = 64: every wave takes
-    every K batch of its strip, B staged once per slice in a shared ring), split-K included:
+    """The row-parallel decode tile (block (64 | 128 | 256, 128, 128): every wave takes every
+    128-row K batch of its strip, B staged once per slice in a shared ring), split-K included:
     bit-exact, ragged M, N and K included."""
     a, b, sa, sb, got = run_w8a8(gpu, M, N, K, seed=M + bm, block=(bm, 128, 128))
     ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 64, 64),

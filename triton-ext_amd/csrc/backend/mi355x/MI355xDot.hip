@@ -182,11 +182,12 @@ constexpr int kNumGemmConfigs = sizeof(kGemmConfigs) / sizeof(kGemmConfigs[0]);
 typedef void (*DecodeKernelFn)(DecodeArgs);
 const DecodeKernelFn kDecodeKernels[4] = {decode_i8_kernel<1>, decode_i8_kernel<2>,
                                            decode_i8_kernel<3>, decode_i8_kernel<4>};
-// The row-parallel decode kernel by 16-row blocks per wave (MT = 2, 4): rings
-// of 4 and 3 slots of 32 and 48 KiB (a 128-row batch: B's 16 KiB and the
-// waves' A).
-const DecodeKernelFn kDecodeRowsKernels[2] = {decode_rows_i8_kernel<2, 4>,
-                                              decode_rows_i8_kernel<4, 3>};
+// The row-parallel decode kernel by slice height (64, 128, 256 rows): rings
+// of 6, 4 and 3 slots of 24, 32 and 48 KiB (a 128-row batch: B's 16 KiB and
+// the slice's A).
+const DecodeKernelFn kDecodeRowsKernels[3] = {decode_rows_i8_kernel<64, 6>,
+                                              decode_rows_i8_kernel<128, 4>,
+                                              decode_rows_i8_kernel<256, 3>};
 
 // MFMA format code of an MX operand type (-1 if it has none).
 int mxFormat(int32_t t) {
@@ -318,12 +319,13 @@ bool useDecode(const tx_dot_desc &d) {
 // wave's accumulators.
 int decodeMT(int64_t M) { return M > 64 ? 4 : (int)cdiv(M > 0 ? M : 1, 16); }
 
-// The row-parallel decode kernel (decode_rows_i8.h), named by block_m 128 or
-// 256 past M = 64 (and 128-row K batches, block_k 128): a workgroup of 4
-// waves x 16 MT rows (MT = block_m / 64) takes every K batch of its strip,
-// so a slice of block_m rows streams B once.
+// The row-parallel decode kernel (decode_rows_i8.h), named by a block of 64,
+// 128 or 256 rows with 128-row K batches (block_k 128): the 4 waves of a
+// workgroup split a slice of block_m rows by 128 columns between them and all
+// take every K batch of the strip, so a slice streams B once.
 bool decodeRows(const tx_dot_desc &d) {
-  return d.M > 64 && (d.block_m == 128 || d.block_m == 256);
+  return d.block_k == kRowsBatchK &&
+         (d.block_m == 64 || d.block_m == 128 || d.block_m == 256);
 }
 int decodeSlices(const tx_dot_desc &d) {
   const int64_t M = d.M > 0 ? d.M : 1;
@@ -335,8 +337,7 @@ int decodeSlices(const tx_dot_desc &d) {
 // block other than this runs the tile it names (or is refused).
 bool decodeTile(const tx_dot_desc &d) {
   return d.block_n == kDecodeStripN &&
-         (decodeRows(d) ? d.block_k == kRowsBatchK
-                        : d.block_m == 16 * decodeMT(d.M) && d.block_k == kDecodeBatchK);
+         (decodeRows(d) || (d.block_m == 16 * decodeMT(d.M) && d.block_k == kDecodeBatchK));
 }
 
 // Split-K factor for the decode kernel: a power of two (<= kMaxSplit) so
@@ -364,7 +365,7 @@ int64_t decodeWorkspace(const tx_dot_desc &d, int ksplit) {
   if (decodeRows(d)) // partials in lane order, per slice and strip
     return decodeCounterBytes(d) +
            ksplit * decode_rows_split_bytes(decodeSlices(d), (int)cdiv(d.N, kDecodeStripN),
-                                            d.block_m / 64);
+                                            d.block_m);
   return decodeCounterBytes(d) + (int64_t)ksplit * d.M * ((d.N + 3) & ~3) * 4;
 }
 
@@ -769,7 +770,7 @@ int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   a.partials = need > 0 ? reinterpret_cast<int32_t *>(static_cast<uint8_t *>(ws) + counters)
                         : nullptr;
   const DecodeKernelFn fn =
-      decodeRows(d) ? kDecodeRowsKernels[d.block_m / 128 - 1] : kDecodeKernels[mt - 1];
+      decodeRows(d) ? kDecodeRowsKernels[d.block_m == 64 ? 0 : d.block_m / 128] : kDecodeKernels[mt - 1];
   hipLaunchKernelGGL(fn, dim3(plan.grid_x),
                      dim3(plan.block_threads), 0, stream, a);
   TX_HIP_CHECK(hipGetLastError());

@@ -5,9 +5,10 @@
 //
 // decode_i8.h gives each workgroup a row slice of at most 64 rows, so past
 // M = 64 every 128-column strip of B is streamed once per slice, and its 4
-// waves split K.  Here a workgroup owns a slice of 64 MT rows (MT = 2 or 4;
-// one slice covers M when 64 MT >= M), a strip of 128 columns and a range of
-// K (split-K); each of its 4 waves owns 16 MT rows of the slice and takes
+// waves split K.  Here a workgroup owns a slice of 64, 128 or 256 rows (one
+// slice covers M when it is as tall), a strip of 128 columns and a range of
+// K (split-K); its 4 waves each own a block of the slice's outputs (32 or 64
+// rows by all 128 columns, or at 64 rows 32 rows by 64 columns) and all take
 // every batch of 128 K rows:
 //  * B's batches go through one LDS ring shared by the 4 waves: each wave
 //    issues 4 of a batch's 16 direct-to-LDS loads (global_load_lds_dwordx4,
@@ -15,18 +16,19 @@
 //    s_barrier per batch makes the whole batch visible; that barrier also
 //    tells every wave that the slot read one batch earlier is free, and the
 //    loads of the batch S - 1 ahead go into it.  B is read once per slice.
-//  * A goes through the same slots: the wave's 16 MT rows x 128 bytes of
-//    the batch, each load 8 whole 128-byte lines (loads of 16 rows x 64
+//  * A goes through the same slots: the slice's rows x 128 bytes of the
+//    batch, a quarter loaded by each wave, each load 8 whole 128-byte lines (loads of 16 rows x 64
 //    bytes, half lines, measured 2.8 times slower per byte), stored
 //    row-major with 16-byte chunk c of row r at c ^ ((r >> 1) & 7), so the
 //    16 rows one ds_read_b128 quarter-wave reads sit in 16 bank groups.
 //  * B's LDS layout and transposed reads are decode_i8.h's (128-byte rows,
 //    chunk c of row r at c ^ (r & 7), ds_read_b64_tr_b8 pairs).
-//  * Products 32 x 32 x 32 at a time (v_mfma_i32_32x32x32_i8), four K steps
-//    a batch, with the MFMA roles swapped (MFMA A := B columns, MFMA B := A
-//    rows), so the result is C^T: lane l holds C row 32 rb + l%32 of the
-//    wave's rows at the 4 consecutive columns 32 cb + 8 q + 4 (l/32) .. +3 of
-//    the strip.  No cross-wave reduction: the waves own disjoint rows.
+//  * Products 32 x 32 x 32 at a time (v_mfma_i32_32x32x32_i8: at one wave
+//    per SIMD it runs at 4.3 POP/s on the chip, v_mfma_i32_16x16x64_i8 at
+//    1.6), four K steps a batch, with the MFMA roles swapped (MFMA A := B
+//    columns, MFMA B := A rows), so the result is C^T: lane l holds C row
+//    32 rb + l%32 of the wave's rows at the 4 consecutive columns
+//    32 cb + 8 q + 4 (l/32) .. +3 of its column blocks.  No cross-wave reduction: the waves own disjoint outputs.
 //  * The epilogue's scales are staged in LDS by 4-byte direct loads that go
 //    out before the first batch.
 //  * Split-K: decode_i8.h's exchange (SC1 stores of the int32 partial, an
@@ -46,24 +48,28 @@
 
 namespace txk {
 
-// The row kernel's partials per split: [slices][strips][4 waves][MT][8] blocks
-// of 64 lanes x 16 bytes.
-__host__ __device__ constexpr int64_t decode_rows_split_bytes(int slices, int strips, int mt) {
-  return (int64_t)slices * strips * kDecodeWaves * mt * 8 * 1024;
+// The row kernel's partials per split: every slice (sr rows) and strip, its
+// sr x 128 int32 sums in lane order.
+__host__ __device__ constexpr int64_t decode_rows_split_bytes(int slices, int strips, int sr) {
+  return (int64_t)slices * strips * sr * kDecodeStripN * 4;
 }
 
 constexpr int kRowsBatchK = 128; // K rows per batch: A's rows are whole 128-byte lines
 
-// MT: 16-row blocks per wave (a slice is 64 MT rows); S: ring slots, each
-// one batch: B's 16 KiB, then the 4 waves' A rows (2 MT KiB each).
-template <int MT, int S> struct DecodeRowsCfg {
+// SR: rows a slice (64, 128 or 256); S: ring slots, each one batch: B's
+// 16 KiB, then the slice's A rows (SR x 128 bytes).  The 4 waves cover the
+// slice as WR row groups of WROWS rows by WC column groups: 4 x 1 waves of
+// 32 or 64 rows and all 128 columns past 64 rows, 2 x 2 waves of 32 rows and
+// 64 columns at 64 (a 32 x 32 MFMA block needs 32 rows).
+template <int SR, int S> struct DecodeRowsCfg {
+  static constexpr int WC = SR == 64 ? 2 : 1, WR = kDecodeWaves / WC, WROWS = SR / WR;
+  static constexpr int R32 = WROWS / 32, NCB = 4 / WC; // 32 x 32 blocks a wave
   static constexpr int A_OFF = kRowsBatchK * kDecodeStripN; // 16 KiB of B
-  static constexpr int A_WAVE = 16 * MT * kRowsBatchK;      // a wave's A rows
-  static constexpr int SLOT = A_OFF + kDecodeWaves * A_WAVE;
-  static constexpr int B_LOADS = A_OFF / 1024 / kDecodeWaves; // per wave and batch
-  static constexpr int A_LOADS = A_WAVE / 1024;
+  static constexpr int SLOT = A_OFF + SR * kRowsBatchK;
+  static constexpr int B_LOADS = A_OFF / 1024 / kDecodeWaves;          // per wave and batch
+  static constexpr int A_LOADS = SR * kRowsBatchK / 1024 / kDecodeWaves; // SR / 4 rows a wave
   static constexpr int VPB = B_LOADS + A_LOADS;
-  static_assert(MT == 2 || MT == 4, "32-row MFMA blocks: 128 or 256 rows a slice");
+  static_assert(SR == 64 || SR == 128 || SR == 256, "slices of 64, 128 or 256 rows");
   static_assert(S >= 3 && S * SLOT <= 158 * 1024, "ring (and the scales) fit LDS");
   static_assert((S - 2) * VPB <= 63, "vmcnt is 6 bits");
 };
@@ -87,6 +93,13 @@ template <int MT, int S> struct DecodeRowsCfg {
                : TX_ROWS_OUT8, "=v"(a[0])                                                  \
                : TX_ROWS_IN4, "v"(a_addr)                                                  \
                : "memory")
+#define TX_ROWS_H1(O0, O1)                                                                 \
+  asm volatile("ds_read_b64_tr_b8 %0, %5 offset:" #O0 "\n\tds_read_b64_tr_b8 %1, %5 offset:" #O1 \
+               "\n\tds_read_b64_tr_b8 %2, %6 offset:" #O0 "\n\tds_read_b64_tr_b8 %3, %6 offset:" #O1 \
+               "\n\tds_read_b128 %4, %7\n\ts_waitcnt lgkmcnt(0)"                              \
+               : "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1]), "=v"(a[0])           \
+               : "v"(b + off[0]), "v"(b + off[1]), "v"(a_addr)                             \
+               : "memory")
 #define TX_ROWS_K2(O0, O1)                                                                 \
   asm volatile(TX_ROWS_TR(O0, O1, 10, 11, 12, 13)                                          \
                "ds_read_b128 %8, %14\n\tds_read_b128 %9, %14 offset:4096\n\t"               \
@@ -94,12 +107,18 @@ template <int MT, int S> struct DecodeRowsCfg {
                : TX_ROWS_OUT8, "=v"(a[0]), "=v"(a[1])                                      \
                : TX_ROWS_IN4, "v"(a_addr)                                                  \
                : "memory")
-template <int R32, int KS>
-__device__ __forceinline__ void rows_read_k32(uint32_t b, const uint32_t (&off)[4],
-                                              uint32_t a_addr, v2i_t (&lo)[4], v2i_t (&hi)[4],
-                                              i32x4_t (&a)[R32]) {
-  static_assert(R32 == 1 || R32 == 2, "32 or 64 rows a wave");
-  if constexpr (R32 == 1) {
+template <int R32, int NCB, int KS>
+__device__ __forceinline__ void rows_read_k32(uint32_t b, const uint32_t (&off)[NCB],
+                                              uint32_t a_addr, v2i_t (&lo)[NCB],
+                                              v2i_t (&hi)[NCB], i32x4_t (&a)[R32]) {
+  static_assert((R32 == 1 || R32 == 2) && (NCB == 4 || (NCB == 2 && R32 == 1)),
+                "32 or 64 rows by 128 columns, or 32 rows by 64 columns, a wave");
+  if constexpr (NCB == 2) {
+    if constexpr (KS == 0) TX_ROWS_H1(0, 1024);
+    else if constexpr (KS == 1) TX_ROWS_H1(4096, 5120);
+    else if constexpr (KS == 2) TX_ROWS_H1(8192, 9216);
+    else TX_ROWS_H1(12288, 13312);
+  } else if constexpr (R32 == 1) {
     if constexpr (KS == 0) TX_ROWS_K1(0, 1024);
     else if constexpr (KS == 1) TX_ROWS_K1(4096, 5120);
     else if constexpr (KS == 2) TX_ROWS_K1(8192, 9216);
@@ -112,19 +131,21 @@ __device__ __forceinline__ void rows_read_k32(uint32_t b, const uint32_t (&off)[
   }
 }
 #undef TX_ROWS_K2
+#undef TX_ROWS_H1
 #undef TX_ROWS_K1
 #undef TX_ROWS_IN4
 #undef TX_ROWS_OUT8
 #undef TX_ROWS_TR
 
-template <int MT, int S>
+template <int SR, int S>
 __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_rows_i8_kernel(DecodeArgs p) {
-  typedef DecodeRowsCfg<MT, S> Cfg;
-  constexpr int SLOT = Cfg::SLOT;
+  typedef DecodeRowsCfg<SR, S> Cfg;
+  constexpr int SLOT = Cfg::SLOT, WC = Cfg::WC, WROWS = Cfg::WROWS, R32 = Cfg::R32,
+                NCB = Cfg::NCB;
   __shared__ __attribute__((aligned(1024))) uint8_t ring[S * SLOT];
   __shared__ uint32_t last_flag;
   // The epilogue's scales: sb of the strip's 128 columns, then 64 sa values
-  // per wave (its 16 MT rows first).
+  // per wave (its WROWS rows first).
   __shared__ __attribute__((aligned(16))) float scl[kDecodeStripN + 64 * kDecodeWaves];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -148,10 +169,13 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_rows_i8_kernel(De
   }
   const int strip = pair % strips, split = pair / strips;
   const int64_t n0 = (int64_t)strip * kDecodeStripN;
-  // This wave's rows: row0 .. row0 + Mr - 1 (Mr <= 0: none).
-  const int row0 = slice * 64 * MT + wave * 16 * MT;
-  const int Mr = p.M - row0 < 16 * MT ? p.M - row0 : 16 * MT;
-  const int8_t *const Ap = p.A + (int64_t)row0 * p.lda;
+  // This wave's row group rw and column group cw; its rows row0 .. row0 +
+  // Mr - 1 (Mr <= 0: none) and column blocks NCB cw .. of the strip.
+  const int rw = wave / WC, cw = wave % WC;
+  const int srow0 = slice * SR, row0 = srow0 + rw * WROWS;
+  const int Mr = p.M - row0 < WROWS ? p.M - row0 : WROWS;
+  const int Ms = p.M - srow0; // rows of the slice (> 0)
+  const int8_t *const Ap = p.A + (int64_t)srow0 * p.lda;
   const bool n_edge = n0 + kDecodeStripN > p.N;
 
   const int total_batches = (p.K + kRowsBatchK - 1) / kRowsBatchK;
@@ -162,9 +186,10 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_rows_i8_kernel(De
   const int nb = b_end > b_begin ? b_end - b_begin : 0; // the same for every wave
 
   // Loads of the split's batch i into `slot`: this wave's 4 of B's 16 KiB
-  // (rows 32 wave .. +31 of the batch) and its own A rows, 2 MT KiB at
-  // A_OFF + wave A_WAVE: load u holds rows 8 u .. +7, lane l' fetching chunk
-  // (l' % 8) ^ ((r >> 1) & 7) of row r = 8 u + l'/8 to r * 128 + 16 (l' % 8).
+  // (rows 32 wave .. +31 of the batch) and a quarter of the slice's A rows
+  // (rows SR/4 wave ..): A load u of the wave holds slice rows r = SR/4 wave
+  // + 8 u .. +7, lane l' fetching chunk (l' % 8) ^ ((r >> 1) & 7) of row
+  // r + l'/8 to A_OFF + r * 128 + 16 (l' % 8).
   // No loaded VGPR is live across the loop: with the direct-to-LDS loads
   // pending, the compiler can only wait for a loaded register with vmcnt(0)
   // (it counts the two kinds of load as events that may complete out of
@@ -188,52 +213,51 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_rows_i8_kernel(De
     }
 #pragma unroll
     for (int u = 0; u < Cfg::A_LOADS; ++u) {
-      const int r = 8 * u + (lane >> 3);
+      const int r = (SR / 4) * wave + 8 * u + (lane >> 3);
       const int c = (lane & 7) ^ ((r >> 1) & 7);
       const int64_t k = k0 + 16 * c;
       const void *src = Ap + (int64_t)r * p.lda + k;
-      if (!live || r >= Mr || (b >= p.k_main_batches && k >= p.K))
+      if (!live || r >= Ms || (b >= p.k_main_batches && k >= p.K))
         src = tx_zero_chunk;
-      dma16(src, (lds_void *)(slot + Cfg::A_OFF + wave * Cfg::A_WAVE + u * 1024)); // A: re-read by every strip
+      dma16(src, (lds_void *)(slot + Cfg::A_OFF + (Cfg::A_LOADS * wave + u) * 1024)); // A: re-read by every strip
     }
   };
 
   // acc[rb][cb]: the 32 x 32 block of rows 32 rb .. of the wave's rows and
-  // columns 32 cb .. of the strip, as C^T (MFMA A := B columns, MFMA B :=
-  // A rows): lane l holds row 32 rb + l%32 at columns 32 cb + 8 q + 4 (l/32)
-  // .. +3 in registers 4 q .. 4 q + 3.
-  constexpr int R32 = MT / 2;
-  i32x16_t acc[R32][4];
+  // columns 32 (NCB cw + cb) .. of the strip, as C^T (MFMA A := B columns,
+  // MFMA B := A rows): lane l holds row 32 rb + l%32 at columns
+  // 32 (NCB cw + cb) + 8 q + 4 (l/32) .. +3 in registers 4 q .. 4 q + 3.
+  i32x16_t acc[R32][NCB];
 #pragma unroll
   for (int rb = 0; rb < R32; ++rb)
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+    for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         acc[rb][cb][r] = 0;
 
-  // MFMAs of one batch from `slot`: four K steps of 32, each R32 x 4
+  // MFMAs of one batch from `slot`: four K steps of 32, each R32 x NCB
   // v_mfma_i32_32x32x32_i8.  Lane l's A operand for step ks and row block rb
-  // -- row 32 rb + l%32, chunk 2 ks + l/32 -- sits at a_k[ks] + 4 KiB rb.
-  uint32_t tr_off[4], a_k[4];
+  // -- slice row WROWS rw + 32 rb + l%32, chunk 2 ks + l/32 -- sits at
+  // a_k[ks] + 4 KiB rb (WROWS rw is a multiple of 32: the swizzle is l%32's).
+  uint32_t tr_off[NCB], a_k[4];
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb)
-    tr_off[cb] = tr32_off(lane, cb);
+  for (int cb = 0; cb < NCB; ++cb)
+    tr_off[cb] = tr32_off(lane, NCB * cw + cb);
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     const int r = lane & 31;
-    a_k[ks] = Cfg::A_OFF + wave * Cfg::A_WAVE + r * 128 +
-              16 * ((2 * ks + (lane >> 5)) ^ ((r >> 1) & 7));
+    a_k[ks] = Cfg::A_OFF + (WROWS * rw + r) * 128 + 16 * ((2 * ks + (lane >> 5)) ^ ((r >> 1) & 7));
   }
   auto consume = [&](const uint8_t *slot) {
     const uint32_t base = lds_addr(slot);
     auto step = [&](auto ks_c) {
       constexpr int KS = decltype(ks_c)::value;
       i32x4_t a[R32];
-      v2i_t lo[4], hi[4];
-      rows_read_k32<R32, KS>(base, tr_off, base + a_k[KS], lo, hi, a);
+      v2i_t lo[NCB], hi[NCB];
+      rows_read_k32<R32, NCB, KS>(base, tr_off, base + a_k[KS], lo, hi, a);
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) {
+      for (int cb = 0; cb < NCB; ++cb) {
         const i32x4_t bf = {lo[cb].x, lo[cb].y, hi[cb].x, hi[cb].y};
 #pragma unroll
         for (int rb = 0; rb < R32; ++rb)
@@ -252,7 +276,7 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_rows_i8_kernel(De
   // element 0 (their results are not stored).
   {
     const int m = row0 + lane;
-    __builtin_amdgcn_global_load_lds(p.sa + (lane < 16 * MT && m < p.M ? m : 0),
+    __builtin_amdgcn_global_load_lds(p.sa + (lane < WROWS && m < p.M ? m : 0),
                                      (lds_void *)(scl + kDecodeStripN + 64 * wave), 4, 0, 0);
     if (wave < 2) {
       const int64_t n = n0 + 64 * wave + lane;
@@ -289,17 +313,18 @@ k_loop_done:
   // row0 + 32 rb + l%32, columns n0 + 32 cb + 8 q + 4 (l/32) .. +3 (one
   // 8-byte store; single elements where the quad crosses N).
   const int rl = lane & 31, ch = lane >> 5;
-  auto epilogue = [&](const i32x16_t (&sum)[R32][4]) {
+  auto epilogue = [&](const i32x16_t (&sum)[R32][NCB]) {
     float sav[R32];
 #pragma unroll
     for (int rb = 0; rb < R32; ++rb)
       sav[rb] = scl[kDecodeStripN + 64 * wave + 32 * rb + rl];
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+    for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int64_t col = n0 + 32 * cb + 8 * q + 4 * ch;
-        const float4 sb4 = *reinterpret_cast<const float4 *>(scl + 32 * cb + 8 * q + 4 * ch);
+        const int cs = 32 * (NCB * cw + cb) + 8 * q + 4 * ch; // column in the strip
+        const int64_t col = n0 + cs;
+        const float4 sb4 = *reinterpret_cast<const float4 *>(scl + cs);
         const float sbv[4] = {sb4.x, sb4.y, sb4.z, sb4.w};
 #pragma unroll
         for (int rb = 0; rb < R32; ++rb) {
@@ -340,22 +365,22 @@ k_loop_done:
   // A partial block (rb, cb) is 4 KiB: register quad q of every lane at
   // 1 KiB q + 16 l.
   constexpr int kSC1 = 16;
-  const int64_t split_bytes = decode_rows_split_bytes(p.slices, strips, MT);
+  const int64_t split_bytes = decode_rows_split_bytes(p.slices, strips, SR);
   auto part_rsrc = [&](int q) {
     return __builtin_amdgcn_make_buffer_rsrc(
         reinterpret_cast<uint8_t *>(p.partials) + (int64_t)q * split_bytes, 0, (int)split_bytes,
         0x00020000);
   };
-  const int blk0 = ((slice * strips + strip) * kDecodeWaves + wave) * R32 * 4;
+  const int blk0 = ((slice * strips + strip) * kDecodeWaves + wave) * R32 * NCB;
   auto part_off = [&](int rb, int cb, int q) {
-    return ((blk0 + 4 * rb + cb) << 12) + (q << 10) + 16 * lane;
+    return ((blk0 + NCB * rb + cb) << 12) + (q << 10) + 16 * lane;
   };
   {
     const auto mine = part_rsrc(split);
 #pragma unroll
     for (int rb = 0; rb < R32; ++rb)
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb)
+      for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const i32x4_t v = {acc[rb][cb][4 * q], acc[rb][cb][4 * q + 1], acc[rb][cb][4 * q + 2],
@@ -378,29 +403,39 @@ k_loop_done:
   __syncthreads();
   if (!*reinterpret_cast<volatile uint32_t *>(&last_flag))
     return;
-  // Last arrival: add the other splits' partials to its own, one split's
-  // 16 R32 loads in flight at a time.
-  for (int qs = 0; qs < p.ksplit; ++qs) {
-    if (qs == split)
-      continue;
-    const auto r = part_rsrc(qs);
-    v4i_t v[R32][4][4];
+  // Last arrival: add the other splits' partials to its own, NQS splits'
+  // loads (32 per lane) in flight per round trip.
+  constexpr int NQS = 32 / (R32 * NCB * 4);
+  for (int q0 = 0; q0 < p.ksplit; q0 += NQS) {
+    v4i_t v[NQS][R32][NCB][4];
 #pragma unroll
-    for (int rb = 0; rb < R32; ++rb)
+    for (int qq = 0; qq < NQS; ++qq) {
+      if (q0 + qq >= p.ksplit || q0 + qq == split)
+        continue;
+      const auto r = part_rsrc(q0 + qq);
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb)
+      for (int rb = 0; rb < R32; ++rb)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          v[rb][cb][q] = __builtin_amdgcn_raw_buffer_load_b128(r, part_off(rb, cb, q), 0, kSC1);
+        for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
-    for (int rb = 0; rb < R32; ++rb)
+          for (int q = 0; q < 4; ++q)
+            v[qq][rb][cb][q] =
+                __builtin_amdgcn_raw_buffer_load_b128(r, part_off(rb, cb, q), 0, kSC1);
+    }
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb)
+    for (int qq = 0; qq < NQS; ++qq) {
+      if (q0 + qq >= p.ksplit || q0 + qq == split)
+        continue;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+      for (int rb = 0; rb < R32; ++rb)
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            acc[rb][cb][4 * q + r] += v[rb][cb][q][r];
+        for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[rb][cb][4 * q + r] += v[qq][rb][cb][q][r];
+    }
   }
   epilogue(acc);
 }

@@ -201,13 +201,15 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
     else if (d->a_type == TX_I8 && d->scale_mode == TX_SCALE_ROWCOL && d->M <= 256 &&
              d->N <= (int64_t)4096 * 128)
       // W8A8 decode (M <= 256, N up to its 4096 column strips), 128-column
-      // strips: up to M = 64 one row slice and 64-row K batches split among
-      // the waves; beyond, slices of 128 rows (one wave per 32) and 128-row
-      // K batches that every wave takes (measured at N = K = 8192: M = 128
-      // 30.2-31.0 us against 33.7-33.9 for slices of 64, M = 256 42.5-42.6
-      // against 48.7-49.2)
-      t = d->M > 64 ? Tile{128, 128, 128, 1.0}
-                    : Tile{(int32_t)(16 * cdiv(d->M > 0 ? d->M : 1, 16)), 128, 64, 1.0};
+      // strips.  Up to M = 48 one row slice and 64-row K batches split among
+      // the waves; beyond, row slices whose waves all take every 128-row K
+      // batch: of 64 rows up to M = 128, of 128 past it.  Measured at
+      // N = K = 8192, in us: M = 32 20.1 / 22.1-22.7 (slices of 64), 48 22.0 /
+      // 22.2-22.5, 64 25.2 / 22.3-22.9, 96 29.4 (64) / 31.2-32.0 (128), 128
+      // 29.6 / 30.5, 192 53.5 / 43.7-44.8, 256 44.8 / 42.6.
+      t = d->M > 128 ? Tile{128, 128, 128, 1.0}
+          : d->M > 48 ? Tile{64, 128, 128, 1.0}
+                      : Tile{(int32_t)(16 * cdiv(d->M > 0 ? d->M : 1, 16)), 128, 64, 1.0};
     else if (d->a_type == TX_F8E4M3 || d->a_type == TX_F8E5M2)
       t = kTiles8[first]; // the register-staged 128x128 tile is slower everywhere
     else
