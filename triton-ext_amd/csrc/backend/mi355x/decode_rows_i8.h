@@ -403,40 +403,45 @@ k_loop_done:
   __syncthreads();
   if (!*reinterpret_cast<volatile uint32_t *>(&last_flag))
     return;
-  // Last arrival: add the other splits' partials to its own, NQS splits'
-  // loads (32 per lane) in flight per round trip.
-  constexpr int NQS = 32 / (R32 * NCB * 4);
-  for (int q0 = 0; q0 < p.ksplit; q0 += NQS) {
-    v4i_t v[NQS][R32][NCB][4];
+  // Last arrival: add the other splits' partials to its own, 16 or 32 loads
+  // per lane in flight per round trip: NQS splits' whole blocks while a wave
+  // holds 32 rows; a row block of one split at a time at 64 rows (32 loads
+  // there would spill registers).
+  constexpr int RBG = R32 == 2 ? 1 : R32;                // row blocks per round trip
+  constexpr int NQS = R32 == 2 ? 1 : 32 / (R32 * NCB * 4); // splits per round trip
+  for (int q0 = 0; q0 < p.ksplit; q0 += NQS)
 #pragma unroll
-    for (int qq = 0; qq < NQS; ++qq) {
-      if (q0 + qq >= p.ksplit || q0 + qq == split)
-        continue;
-      const auto r = part_rsrc(q0 + qq);
+    for (int rb0 = 0; rb0 < R32; rb0 += RBG) {
+      v4i_t v[NQS][RBG][NCB][4];
 #pragma unroll
-      for (int rb = 0; rb < R32; ++rb)
+      for (int qq = 0; qq < NQS; ++qq) {
+        if (q0 + qq >= p.ksplit || q0 + qq == split)
+          continue;
+        const auto r = part_rsrc(q0 + qq);
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb)
+        for (int rb = 0; rb < RBG; ++rb)
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            v[qq][rb][cb][q] =
-                __builtin_amdgcn_raw_buffer_load_b128(r, part_off(rb, cb, q), 0, kSC1);
+          for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              v[qq][rb][cb][q] =
+                  __builtin_amdgcn_raw_buffer_load_b128(r, part_off(rb0 + rb, cb, q), 0, kSC1);
+      }
+#pragma unroll
+      for (int qq = 0; qq < NQS; ++qq) {
+        if (q0 + qq >= p.ksplit || q0 + qq == split)
+          continue;
+#pragma unroll
+        for (int rb = 0; rb < RBG; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                acc[rb0 + rb][cb][4 * q + r] += v[qq][rb][cb][q][r];
+      }
     }
-#pragma unroll
-    for (int qq = 0; qq < NQS; ++qq) {
-      if (q0 + qq >= p.ksplit || q0 + qq == split)
-        continue;
-#pragma unroll
-      for (int rb = 0; rb < R32; ++rb)
-#pragma unroll
-        for (int cb = 0; cb < NCB; ++cb)
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              acc[rb][cb][4 * q + r] += v[qq][rb][cb][q][r];
-    }
-  }
   epilogue(acc);
 }
 
