@@ -179,7 +179,9 @@ def test_plan_validation():
     (64, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
     (128, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
     (256, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
-    (257, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_GEMM_I8),
+    (257, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
+    (512, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
+    (513, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_GEMM_I8),
     (300, 304, 256, tx.I8, tx.I32, 0, tx.KERNEL_GEMM_I8),
     (2, 8192, 8192, tx.I8, tx.I32, 0, tx.KERNEL_GEMM_I8),
     (2048, 7168, 7168, tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, tx.KERNEL_GEMM_F8),
@@ -191,7 +193,7 @@ def test_kernel_choice(M, N, K, a, c, sm, kernel):
     if kernel == tx.KERNEL_DECODE_I8:
         # 128-column strips x row slices (one up to M = 48, of 64 rows up to 128, of 128
         # past it) x K splits cover the 256 CUs; past M = 48 the K batches are 128 rows
-        bm = 128 if M > 128 else 64 if M > 48 else 16 * -(-M // 16)
+        bm = 256 if M > 256 else 128 if M > 128 else 64 if M > 48 else 16 * -(-M // 16)
         assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == \
             (bm, 128, 128 if M > 48 else 64)
         slices = -(-M // bm)

@@ -207,9 +207,10 @@ def test_c4_w8a8_decode(gpu, M):
 @pytest.mark.parametrize("M,N,K", [(5, 272, 208), (16, 256, 64), (40, 8208, 1008), (3, 16, 4160),
                                    (64, 512, 16), (17, 4096, 2080), (65, 8208, 1008),
                                    (100, 4096, 2080), (130, 272, 4160), (200, 1024, 64),
-                                   (256, 8192, 1024)])
+                                   (256, 8192, 1024), (300, 1024, 1040), (512, 8192, 2048)])
 def test_w8a8_decode_edges(gpu, M, N, K):
-    """Decode shapes, row slices of 64 past M = 64 (M = 65 .. 256) included."""
+    """Decode shapes at the planner's tiles: waves splitting K up to M = 48, the row kernel's
+    slices of 64, 128 and 256 rows beyond (M = 49 .. 512)."""
     a, b, sa, sb, got = run_w8a8(gpu, M, N, K, seed=M)
     ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 64, 64),
                            scale_mode=oracle.SCALE_ROWCOL, sa=sa, sb=sb, round_mode=oracle.ROUND_RNE)
@@ -223,7 +224,9 @@ def test_w8a8_decode_edges(gpu, M, N, K):
                                       (255, 1000, 2000, 256), (192, 8200, 8190, 256),
                                       (129, 16, 16, 128), (64, 8192, 8192, 64),
                                       (16, 8192, 8192, 64), (40, 4096, 2080, 64),
-                                      (130, 272, 4160, 64), (1, 8200, 1000, 64)])
+                                      (130, 272, 4160, 64), (1, 8200, 1000, 64),
+                                      (384, 4096, 2048, 256), (300, 1000, 3000, 256),
+                                      (700, 8192, 512, 256), (1024, 2048, 1024, 64)])
 def test_w8a8_row_kernel(gpu, M, N, K, bm):
     """The row-parallel decode tile (block (64 | 128 | 256, 128, 128): every wave takes every
     128-row K batch of its strip, B staged once per slice in a shared ring), split-K included:

@@ -307,12 +307,6 @@ int findGemmConfig(int op, int epi, int bm, int bn, int bk, bool bt, int fmt) {
   return -1;
 }
 
-bool useDecode(const tx_dot_desc &d) {
-  return d.a_type == TX_I8 && d.scale_mode == TX_SCALE_ROWCOL && d.M <= kDecodeMaxM &&
-         !(d.flags & TX_FLAG_B_KMAJOR) &&
-         d.N <= (int64_t)kDecodeMaxStrips * kDecodeStripN;
-}
-
 // Decode row tiling: slices of 16 * MT rows (MT = ceil(M / 16) up to 4), one
 // slice up to M = 64 and slices of 64 beyond.  Slices multiply the B bytes a
 // workgroup streams (fewer splits), so they are used only once M outgrows one
@@ -324,12 +318,24 @@ int decodeMT(int64_t M) { return M > 64 ? 4 : (int)cdiv(M > 0 ? M : 1, 16); }
 // workgroup split a slice of block_m rows by 128 columns between them and all
 // take every K batch of the strip, so a slice streams B once.
 bool decodeRows(const tx_dot_desc &d) {
+  // past M = 256, 128 x 128 x 128 names the register-staged 8-bit tile
   return d.block_k == kRowsBatchK &&
-         (d.block_m == 64 || d.block_m == 128 || d.block_m == 256);
+         (d.block_m == 64 || d.block_m == 256 || (d.block_m == 128 && d.M <= kDecodeMaxM));
 }
 int decodeSlices(const tx_dot_desc &d) {
   const int64_t M = d.M > 0 ? d.M : 1;
   return (int)cdiv(M, decodeRows(d) ? d.block_m : 16 * decodeMT(M));
+}
+
+// W8A8 shapes a decode kernel takes: M <= 256 (the row kernel, named by its
+// block, up to 1024), N up to 4096 strips, and one arrival counter of the
+// fixed region per (slice, strip).
+bool useDecode(const tx_dot_desc &d) {
+  if (d.a_type != TX_I8 || d.scale_mode != TX_SCALE_ROWCOL || (d.flags & TX_FLAG_B_KMAJOR) ||
+      d.N > (int64_t)kDecodeMaxStrips * kDecodeStripN ||
+      d.M > (decodeRows(d) ? kDecodeRowsMaxM : kDecodeMaxM))
+    return false;
+  return (int64_t)decodeSlices(d) * cdiv(d.N, kDecodeStripN) * 4 <= kDecodeCounterBytes;
 }
 
 // The decode kernel's tile as the arith_intensity pass names it: a row slice
@@ -734,7 +740,7 @@ int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
                  hipStream_t stream) {
   const tx_dot_desc &d = plan.desc;
   const int mt = decodeMT(d.M);
-  if (d.M > kDecodeMaxM)
+  if (!useDecode(d))
     return fail(TX_ERR_INVALID, "decode plan with M=%lld", (long long)d.M);
   const int slices = decodeSlices(d);
   const int ks = plan.split_k;

@@ -55,6 +55,7 @@ __host__ __device__ constexpr int64_t decode_rows_split_bytes(int slices, int st
 }
 
 constexpr int kRowsBatchK = 128; // K rows per batch: A's rows are whole 128-byte lines
+constexpr int kDecodeRowsMaxM = 1024; // row slices of one launch: up to 16 of 64 rows
 
 // SR: rows a slice (64, 128 or 256); S: ring slots, each one batch: B's
 // 16 KiB, then the slice's A rows (SR x 128 bytes).  The 4 waves cover the

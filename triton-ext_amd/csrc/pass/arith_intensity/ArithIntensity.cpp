@@ -198,6 +198,13 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
       t = kTiles16[0]; // the K-major B kernel exists for this tile only
     else if (sa == 2)
       t = chooseTile(kTiles16, d->M, d->N, d->K, first);
+    else if (d->a_type == TX_I8 && d->scale_mode == TX_SCALE_ROWCOL && d->M > 256 &&
+             d->M <= 512 && d->N <= (int64_t)4096 * 128 && !(d->flags & TX_FLAG_B_KMAJOR))
+      // W8A8 past the decode sizes, up to M = 512: the row-parallel decode
+      // kernel's slices of 256 rows (measured at N = K = 8192: M = 384 62.3 us,
+      // 512 63.8, against 98.0 and 99.3 on the 8-bit tiles; at 768 113.2
+      // against 110.4, so larger M stays on the tiles)
+      t = Tile{256, 128, 128, 1.0};
     else if (d->a_type == TX_I8 && d->scale_mode == TX_SCALE_ROWCOL && d->M <= 256 &&
              d->N <= (int64_t)4096 * 128)
       // W8A8 decode (M <= 256, N up to its 4096 column strips), 128-column
