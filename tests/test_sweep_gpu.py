@@ -64,7 +64,8 @@ def _cases():
         out.append(("i8_i32", i, dict(M=_dim(rng, 700), N=_dim(rng, 700), K=_dim(rng, 900),
                                       block=tiles8[i % 4])))
     for i in range(48):
-        # even cases: decode (M <= 256); odd: the 8-bit tiles' row x column epilogue (M > 256)
+        # even cases: decode (M <= 256); odd (M > 256): the 8-bit tiles' row x column epilogue
+        # at explicit blocks, the planner's choice at (0, 0, 0) (the row decode kernel to 512)
         M = int(rng.integers(1, 257)) if i % 2 == 0 else int(rng.integers(257, 701))
         blk = (0, 0, 0) if i % 2 == 0 else tiles8[(i // 2) % 4]
         out.append(("w8a8", i, dict(M=M, N=_dim(rng, 3000), K=_dim(rng, 3000), block=blk)))
