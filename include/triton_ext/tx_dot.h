@@ -111,7 +111,8 @@ typedef enum tx_kernel {
   TX_KERNEL_NONE = 0,
   TX_KERNEL_GEMM_16BIT = 1, /* bf16/fp16 tile, MFMA 32x32x16, LDS-staged          */
   TX_KERNEL_GEMM_I8 = 2,    /* int8 tile, MFMA 16x16x64 (32x32x32 small tiles)   */
-  TX_KERNEL_DECODE_I8 = 3,  /* int8 W8A8 M <= 256 streaming, MFMA 16x16x64       */
+  TX_KERNEL_DECODE_I8 = 3,  /* int8 W8A8 decode shapes, MFMA 16x16x64 (M <= 48)
+                             * or 32x32x32 (row slices, M <= 1024)            */
   TX_KERNEL_GEMM_F8 = 4,    /* fp8 e4m3 tile, MFMA 16x16x128 (32x32x64 small)    */
   TX_KERNEL_GEMM_MX = 5,    /* MX fp8 / fp4 tile, scaled MFMA 16x16x128 (e8m0)   */
   TX_KERNEL_GEMM_MX_BF16 = 6, /* MX x bf16: MX operand upcast to bf16 in the

@@ -541,7 +541,8 @@ extern "C" TX_API const char *tx_kernel_name(int32_t kernel) {
   // 8-bit: the 256-wide tiles use the 16x16 MFMAs, the register-staged
   // smaller tiles the 32x32 ones.
   case TX_KERNEL_GEMM_I8: return "gemm_i8_mfma16x16x64|32x32x32";
-  case TX_KERNEL_DECODE_I8: return "decode_i8_mfma16x16x64";
+  // decode: the K-split kernel uses the 16x16 MFMAs, the row-slice kernel the 32x32 ones.
+  case TX_KERNEL_DECODE_I8: return "decode_i8_mfma16x16x64|32x32x32";
   case TX_KERNEL_GEMM_F8: return "gemm_f8_mfma16x16x128|32x32x64_f8f6f4";
   case TX_KERNEL_GEMM_MX: return "gemm_mx_mfma_scale16x16x128";
   case TX_KERNEL_GEMM_MX_BF16: return "mx_upcast_bf16+gemm_16bit_mfma32x32x16";
