@@ -67,6 +67,16 @@ def test_noalloc_w8a8_two_calls(gpu):
     _w8a8(gpu, 16, 8192, 8192, 23)  # and back: the counters were left at zero
 
 
+def test_noalloc_row_kernel_between_split_calls(gpu):
+    """The row-slice decode kernel (64- and 128-row slices, split-K) on the same scratch as the
+    K-split kernel: each leaves the shared counters at zero for the next."""
+    p1 = _w8a8(gpu, 256, 2048, 4096, 51)
+    p2 = _w8a8(gpu, 100, 4096, 2048, 52)
+    assert (p1.desc.block_m, p1.desc.block_k) == (128, 128) and p1.split_k > 1
+    assert (p2.desc.block_m, p2.desc.block_k) == (64, 128) and p2.split_k > 1
+    _w8a8(gpu, 16, 8192, 8192, 53)
+
+
 def _mx_bf16(gpu, M, N, K, seed):
     import torch
     say(f"noalloc MX x bf16 M={M} N={N} K={K} seed={seed}")
