@@ -372,11 +372,12 @@ def bench_mx_bf16(tx, dev, M, N, K, fmt, steps, warmup, seed=8):
                 frac=flops / ms / 1e-3 / PEAK_BF16, plan=plan_info(tx, p))
 
 
-def bench_attn(tx, dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9, dtype=None):
+def bench_attn(tx, dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9, dtype=None,
+               block=(0, 0)):
     """Fused attention forward, the tutorial's bench_flash_attention "fwd"
     configuration (R:pass/LoopSplit/06-fused-attention.py:737-795): fp16
     randn q, k, v [4, 32, N_CTX, 64], sm_scale 1.3; FLOPs 4 Z H N^2 D, halved
-    for causal."""
+    for causal.  block: (BLOCK_M, BLOCK_N), (0, 0) for the default."""
     import torch
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
@@ -391,7 +392,8 @@ def bench_attn(tx, dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9, d
     M = torch.empty((Z, H, N_CTX), device=dev, dtype=torch.float32)
     p = tx.attn_plan(Z, H, N_CTX, D, causal, 1.3,
                      dtype=tx.F8E5M2 if fp8 else tx.BF16 if dtype == torch.bfloat16 else tx.F16,
-                     strides={"v": (v.stride(0), v.stride(1), v.stride(3))} if fp8 else None)
+                     strides={"v": (v.stride(0), v.stride(1), v.stride(3))} if fp8 else None,
+                     block=block)
     L = tx.load()
     args = (ctypes.byref(p), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
             M.data_ptr(), torch.cuda.current_stream().cuda_stream)
@@ -403,8 +405,9 @@ def bench_attn(tx, dev, N_CTX, causal, steps, warmup, Z=4, H=32, D=64, seed=9, d
     ms = time_back_to_back(run, steps, warmup)
     tn = "fp8 e5m2" if fp8 else "bf16" if dtype == torch.bfloat16 else "fp16"
     peak = PEAK_I8 if fp8 else PEAK_BF16  # fp8 MFMA peak = int8's 5.0 P
+    blk = "" if block == (0, 0) else f" block={block[0]}x{block[1]}"
     return dict(workload=f"fused attention fwd {tn} Z={Z} H={H} N_CTX={N_CTX} D={D} "
-                         f"causal={causal}", ms=ms, tflops=p.flops / ms / 1e9,
+                         f"causal={causal}{blk}", ms=ms, tflops=p.flops / ms / 1e9,
                 frac=p.flops / ms / 1e-3 / peak)
 
 

@@ -60,7 +60,8 @@ typedef struct tx_attn_desc {
   int64_t o_sz, o_sh, o_sm;
   /* BLOCK_M x BLOCK_N, one of the tutorial's autotuned configs
    * (R:pass/LoopSplit/06-fused-attention.py:145-159): BLOCK_M 64 or 128 by
-   * BLOCK_N 32 or 64 (fp8 e5m2: BLOCK_N 64); 0 = default (128, 64).  The
+   * BLOCK_N 32 or 64 (not 128 x 32 at head dims below 64, or below 128
+   * for fp8 e5m2); 0 = default (128, 64).  The
    * blocks fix the on-band split (causal_start = start_m * BLOCK_M) and the
    * online softmax's key blocks, so they select the rounding of the result
    * exactly as the tutorial's config does. */

@@ -272,7 +272,13 @@ def test_attn_plan():
     assert err(N_CTX=192, block=(128, 32)) == tx.ERR_UNSUPPORTED
     for blk in ((256, 64), (64, 16), (32, 32), (128, 128)):
         assert err(block=blk) == tx.ERR_UNSUPPORTED
-    assert err(dtype=tx.F8E5M2, block=(64, 32)) == tx.ERR_UNSUPPORTED  # fp8: BLOCK_N 64
+    # fp8 stages head dims below 64 as 64 (one byte per element): a 128 x 32
+    # block's 2 KiB K block is less than one 1 KiB load for each of 4 waves
+    for hd, blk in ((64, (64, 32)), (16, (64, 32)), (128, (128, 32)), (256, (128, 32))):
+        p8 = tx.attn_plan(1, 2, 256, hd, True, 0.5, dtype=tx.F8E5M2, block=blk)
+        assert (p8.desc.block_m, p8.desc.block_n) == blk and p8.block_threads == blk[0] // 32 * 64
+    for hd in (16, 32, 64):
+        assert err(head_dim=hd, dtype=tx.F8E5M2, block=(128, 32)) == tx.ERR_UNSUPPORTED
     assert tx.attn_plan(1, 1, 64, 64, False, 0.5, dtype=tx.F8E5M2, block=(64, 64)).grid_x == 1
     assert err(Z=-1) == tx.ERR_INVALID
     # e5m2: one byte per element, v key-contiguous ([HEAD_DIM][N_CTX] per head)

@@ -322,6 +322,25 @@ def test_attn_fp8_head_dims_16_32_and_256(gpu, causal, Z, H, N, D, block):
 
 
 @pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("Z,H,N,D,block", [(1, 2, 64, 64, (64, 32)), (2, 3, 192, 64, (64, 32)),
+                                           (1, 2, 256, 16, (64, 32)), (1, 3, 192, 32, (64, 32)),
+                                           (1, 2, 320, 128, (64, 32)), (2, 1, 256, 128, (128, 32)),
+                                           (1, 2, 384, 256, (128, 32)), (2, 1, 192, 256, (64, 32))])
+def test_attn_fp8_block_n32(gpu, causal, Z, H, N, D, block):
+    """fp8 e5m2 with BLOCK_N 32: one 32-key block per S^T MFMA and half of
+    each P V MFMA (the other half of P and V^T zero bytes in registers),
+    against the oracle at the same blocks.  N_CTX = 64, 192, 320 give odd
+    block counts at BLOCK_M 64; head dims 16 and 32 run in the layout of 64."""
+    say(f"attn fp8 block={block} Z={Z} H={H} N={N} D={D} causal={causal}")
+    q, k, v = e5m2_qkv(Z, H, N, D, seed=Z * 100 + H * 10 + N + D + causal + 13)
+    o, M = run_gpu_fp8(gpu, q, k, v, causal, 0.8, block=block)
+    ro, rM = oracle.attn_fwd(q, k, v, sm_scale=0.8, causal=causal, block=block,
+                             dtype=oracle.F8E5M2)
+    check_e5m2(o, M, ro, rM, (q, k, v), 0.8, causal,
+               f"attn fp8 block={block} {Z}x{H}x{N} D={D} causal={causal}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
 def test_attn_fp8_bench_shape_sampled_heads(gpu, causal):
     """The tutorial's fp8 bench shape (4, 32, 4096, 64), sm_scale 1.3: every
     program runs; two heads are checked in full against the oracle."""

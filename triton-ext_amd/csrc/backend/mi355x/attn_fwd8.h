@@ -8,7 +8,8 @@
 // zero and O's are not stored.  The pipeline, split and program order are attn_fwd_body's
 // (attn_fwd.h); this file holds the element type's fragments.
 //
-// Per K/V block of BN = 64 keys and wave of 32 query rows (BM / 32 waves):
+// Per K/V block of BN = 64 (or 32) keys and wave of 32 query rows (BM / 32
+// waves):
 //   S^T = K . Q^T    v_mfma_f32_32x32x64_f8f6f4 (e5m2 x e5m2), one per 32
 //                    keys and 64 dims.  Lane l feeds A row l%32 with key
 //                    pi(l%32), pi(8i + 4g + j) = 16g + 4i + j, so the S^T
@@ -20,6 +21,9 @@
 //   O^T += V^T . P^T one MFMA per 32 dims: A := V^T rows (dims), whose keys
 //                    are contiguous in memory and in LDS, read as the same
 //                    two 16-key chunks (l/32 and 2 + l/32) that P holds.
+//                    With BN = 32 the block has only chunk l/32: the other
+//                    half of both operands is zero bytes in registers, so
+//                    the MFMA adds exactly the block's 32 products.
 // The two dots use any K order that is the same for both operands; the
 // order above needs no transposes and no lane exchanges.
 //
@@ -29,27 +33,29 @@
 //     256-byte rows (r & 7) | ((r >> 1) & 8).  The 16 keys pi(0..15) (or
 //     pi(16..31)) that one ds_read_b128 pass reads land in 16 different
 //     16-byte bank groups;
-//   V^T rows (dims) of 64 bytes (the block's keys): (r >> 2) & 3, likewise
-//     for dims 0..15 of a pass.
+//   V^T rows (dims) of BN bytes (the block's keys): (r >> 2) & 3 for 64-byte
+//     rows, (r >> 3) & 1 for 32-byte rows, likewise for dims 0..15 of a pass.
 #pragma once
 
 #include "attn_fwd.h"
 
 namespace txk {
 
-// BM_: BLOCK_M 64 or 128 (one wave per 32 query rows).  BLOCK_N is 64: the
-// P V MFMA takes the block's 64 keys at once.
-template <int HD, int BM_ = 128> struct AttnFwd8 {
+// BM_ x BN_: BLOCK_M 64 or 128 (one wave per 32 query rows) by BLOCK_N 64 or
+// 32.  The P V MFMA takes 64 keys at once; a block of 32 fills half of it.
+template <int HD, int BM_ = 128, int BN_ = 64> struct AttnFwd8 {
   // D: the head dim of the layout (64 for HEAD_DIM 16 and 32); DR: the real one
-  static constexpr int BM = BM_, BN = 64, D = HD < 64 ? 64 : HD, DR = HD, NW = BM_ / 32,
+  static constexpr int BM = BM_, BN = BN_, D = HD < 64 ? 64 : HD, DR = HD, NW = BM_ / 32,
                        ESZ = 1;
   static constexpr int TILE = BN * D;          // K: BN x D bytes; V^T: D x BN bytes
   static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 1 .. 8
   static constexpr int KCPR = D / 16;          // K: 16-byte chunks per row
+  static constexpr int VCPR = BN / 16;         // V^T: 16-byte chunks per dim row
   static constexpr uint32_t kOOB = 0x80000000u;
   static_assert(D == 64 || D == 128 || D == 256, "head dims 16 .. 256");
   static_assert(DR == D || (D == 64 && (DR == 16 || DR == 32)), "16 and 32 in the layout of 64");
-  static_assert(BM == 64 || BM == 128, "the tutorial's BLOCK_M");
+  static_assert((BM == 64 || BM == 128) && (BN == 32 || BN == 64), "the tutorial's blocks");
+  static_assert(DMA >= 1 && DMA * NW * 1024 == TILE, "whole 1 KiB loads per wave");
   typedef float f16v __attribute__((ext_vector_type(16)));
 
   __device__ __forceinline__ static f16v mfma(const i32x8_t &a, const i32x8_t &b,
@@ -62,7 +68,9 @@ template <int HD, int BM_ = 128> struct AttnFwd8 {
            : D == 128 ? ((r >> 1) & 3) | ((r >> 2) & 4)
                       : (r & 7) | ((r >> 1) & 8);
   }
-  __device__ __forceinline__ static int vswz(int r) { return (r >> 2) & 3; }
+  __device__ __forceinline__ static int vswz(int r) {
+    return BN == 64 ? (r >> 2) & 3 : (r >> 3) & 1;
+  }
   // key of A row R of the S^T MFMA
   __device__ __forceinline__ static int pi(int R) {
     return 16 * ((R >> 2) & 1) + 4 * (R >> 3) + (R & 3);
@@ -102,7 +110,7 @@ template <int HD, int BM_ = 128> struct AttnFwd8 {
   }
   // Per-lane source offsets of the wave's DMA loads: load u of wave w fills
   // 1 KiB of LDS.  K: rows 1024/D (DMA w + u) + i/KCPR of D bytes; V^T: dim
-  // rows 16 (DMA w + u) + i/4 of 64 bytes.  Lane i's chunk position holds the
+  // rows 1024/BN (DMA w + u) + i/VCPR of BN bytes.  Lane i's chunk position holds the
   // source chunk (position ^ swizzle(row)).  K chunks and V^T dim rows past
   // the real head dim take kOOB (zeros).
   __device__ __forceinline__ static void kv_offsets(int wave, int64_t k_sm, int64_t v_sm,
@@ -113,7 +121,7 @@ template <int HD, int BM_ = 128> struct AttnFwd8 {
       const int kr = (1024 / D) * (DMA * wave + u) + lane / KCPR, kp = lane % KCPR;
       const int kc = kp ^ kswz(kr);
       ko[u] = 16 * kc >= DR ? kOOB : (uint32_t)(kr * k_sm + 16 * kc);
-      const int vr = 16 * (DMA * wave + u) + lane / 4, vp = lane % 4;
+      const int vr = (1024 / BN) * (DMA * wave + u) + lane / VCPR, vp = lane % VCPR;
       vo[u] = vr >= DR ? kOOB : (uint32_t)(vr * v_sm + 16 * (vp ^ vswz(vr)));
     }
   }
@@ -138,7 +146,7 @@ template <int HD, int BM_ = 128> struct AttnFwd8 {
   //   K, dim chunk pair c, half e: key pi(l%32), chunk 4c + 2(l/32) + e;
   //   V^T, half e: dim l%32, chunk l/32 + 2e.
   struct Bases {
-    uint32_t k[D / 64][2], v[2];
+    uint32_t k[D / 64][2], v[BN / 32];
   };
   __device__ __forceinline__ static void bases(uint32_t k_lds, uint32_t v_lds, Bases &bs) {
     const int lane = threadIdx.x & 63, g = lane >> 5, r = lane & 31;
@@ -149,7 +157,7 @@ template <int HD, int BM_ = 128> struct AttnFwd8 {
       for (int e = 0; e < 2; ++e)
         bs.k[c][e] = k_lds + key * D + 16 * ((4 * c + 2 * g + e) ^ kswz(key));
 #pragma unroll
-    for (int e = 0; e < 2; ++e)
+    for (int e = 0; e < BN / 32; ++e)
       bs.v[e] = v_lds + r * BN + 16 * ((g + 2 * e) ^ vswz(r));
   }
 
@@ -166,7 +174,8 @@ template <int HD, int BM_ = 128> struct AttnFwd8 {
   template <int SLOT>
   __device__ __forceinline__ static i32x8_t read_v(const Bases &bs, int bd) {
     const uint32_t o = SLOT * TILE + bd * 32 * BN;
-    const i32x4_t lo = lds16(bs.v[0] + o), hi = lds16(bs.v[1] + o);
+    const i32x4_t lo = lds16(bs.v[0] + o);
+    const i32x4_t hi = BN == 64 ? lds16(bs.v[BN / 32 - 1] + o) : i32x4_t{0, 0, 0, 0};
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   }
 
@@ -246,6 +255,10 @@ template <int HD, int BM_ = 128> struct AttnFwd8 {
 #pragma unroll
     for (int w = 0; w < 8; ++w) {
       const int b = w / 4, r = 4 * (w % 4);
+      if (b >= BN / 32) { // the MFMA's keys past a block of 32
+        pf[w] = 0;
+        continue;
+      }
       const int lo = __builtin_amdgcn_cvt_pk_bf8_f32(s[b][r], s[b][r + 1], 0, false);
       pf[w] = __builtin_amdgcn_cvt_pk_bf8_f32(s[b][r + 2], s[b][r + 3], lo, true);
     }
@@ -290,9 +303,9 @@ template <int HD, int BM_ = 128> struct AttnFwd8 {
   }
 };
 
-template <bool CAUSAL, int HD, int BM = 128>
+template <bool CAUSAL, int HD, int BM = 128, int BN = 64>
 __global__ void __launch_bounds__(BM * 2, HD >= 256 ? 1 : 2) attn_fwd8_kernel(AttnArgs p) {
-  attn_fwd_body<CAUSAL, AttnFwd8<HD, BM>>(p);
+  attn_fwd_body<CAUSAL, AttnFwd8<HD, BM, BN>>(p);
 }
 
 } // namespace txk

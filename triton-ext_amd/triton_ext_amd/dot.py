@@ -337,7 +337,8 @@ def attention(q, k, v, causal, sm_scale, USE_TMA=True, *, return_lse=False, plan
     tutorial saves for its backward, with return_lse=True).  Shape checks
     follow the tutorial's asserts.  block = (BLOCK_M, BLOCK_N), one of the
     tutorial's autotuned configs (:145-159): BLOCK_M 64 or 128 by BLOCK_N 32
-    or 64 (fp8: 64); (0, 0) takes 128 x 64.  USE_TMA is accepted for the
+    or 64 (not 128 x 32 at head dims below 64, or below 128 in fp8); (0, 0)
+    takes 128 x 64.  USE_TMA is accepted for the
     tutorial's signature and has no effect (gfx950 has no tensor memory
     accelerator; the tutorial's HIP path takes the pointer kernel too).
     return_lse, plan, stream and block are keyword-only.
