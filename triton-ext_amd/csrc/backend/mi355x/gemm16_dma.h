@@ -135,7 +135,7 @@ struct Gemm16Dma {
       const void *src = p.A + (gm * p.lda + gk) * 2;
       if (MASK && (gm >= p.M || gk >= p.K))
         src = tx_zero_chunk;
-      dma16_asm(src, lds_addr(as + j * 1024));
+      dma16(src, (lds_void *)(as + j * 1024));
     }
 #pragma unroll
     for (int i = 0; i < B_DMA; ++i) {
@@ -147,7 +147,7 @@ struct Gemm16Dma {
       const void *src = p.B + (gk * p.ldb + gn) * 2;
       if (MASK && (gk >= p.K || gn >= p.N))
         src = tx_zero_chunk;
-      dma16_asm(src, lds_addr(bs + j * 1024));
+      dma16(src, (lds_void *)(bs + j * 1024));
     }
   }
 
@@ -232,11 +232,7 @@ struct Gemm16Dma {
     };
     // Wait until this wave's loads for step kt have landed -- the loads of
     // the `newer` steps issued after it may stay in flight -- then barrier so
-    // every wave's loads for step kt are visible.  A plain s_barrier, not
-    // __syncthreads(): the latter's workgroup fence waits for vmcnt(0), which
-    // would drain every step in flight.  The barrier also orders this step's
-    // refill after every wave's reads of the buffer it overwrites (those
-    // reads fed the previous step's MFMAs, so they have returned).
+    // every wave's loads for step kt are visible.
     auto step_barrier = [](int newer) {
       if (newer <= 0)
         vmcnt_wait<0>();
@@ -246,7 +242,7 @@ struct Gemm16Dma {
         vmcnt_wait<2 * DMA_PER_STEP>();
       else
         vmcnt_wait<3 * DMA_PER_STEP>();
-      asm volatile("s_barrier" ::: "memory");
+      __syncthreads();
     };
     if (total > 0) {
       // Prologue: fill STAGES-1 buffers.

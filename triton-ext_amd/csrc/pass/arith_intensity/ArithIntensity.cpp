@@ -37,11 +37,11 @@ struct Tile {
 // Tiles the backend instantiates, largest first.  `eff` is the fraction of
 // the dense MFMA peak each tile sustained at 4096^3 on one MI355X (bench.py
 // --only tiles: bf16 -> bf16 and int8 -> int32, back-to-back launches):
-// 16-bit 256x256x64 0.509, 128x128x64 0.348, 64x64x32 0.202; 8-bit
+// 16-bit 256x256x64 0.509, 128x128x64 0.341, 64x64x32 0.187; 8-bit
 // 256x256x128 0.463, 128x128x128 0.173.  tileCost weighs them against the
 // waves of tiles a shape needs.
-const Tile kTiles16[] = {{256, 256, 64, 0.509}, {128, 128, 64, 0.348},
-                         {64, 64, 32, 0.202}};
+const Tile kTiles16[] = {{256, 256, 64, 0.509}, {128, 128, 64, 0.341},
+                         {64, 64, 32, 0.187}};
 // 8-bit tiles.  (A 256x224 tile also exists for explicit requests: it fills
 // all CUs at N = 7168, but its A-resident wave layout needs 28 transposed B
 // reads per step against 16; it measured 0.273 at int8 4096^3 and no faster
