@@ -601,7 +601,8 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the dot shards by N or M blocks with no exchange; see DESIGN.md).", file=sys.stderr)
+              "(a dot would shard by blocks of N or M columns/rows, one per GPU, with no "
+              "exchange between them).", file=sys.stderr)
         sys.exit(2)
     import torch
 

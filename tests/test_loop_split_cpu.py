@@ -74,9 +74,10 @@ def test_lit_cases_structure():
     Each loop is `scf.for %iv = 0 to %n step S` with `if (iv P %mid)
     {addf} else {subf}`.  The checks require: first loop subf (predicate
     false), second loop addf (true) for sgt/sge; the reverse for slt/sle.
-    Split points are checked against the iteration values directly (the
-    reference's own sge/sle/step10 arithmetic is off by one iteration or
-    one step)."""
+    Split points are checked against the iteration values directly: the
+    reference's arithmetic (R:pass/LoopSplit/LoopSplit.cpp:156-174) splits
+    sgt/sge one iteration early at step 1 and overshoots by one step when
+    (mid - lo) % step == 0, so its midp is not the oracle here."""
     n, mid = 40, 13
     for pred, first_true in ((tx.CMP_SGT, False), (tx.CMP_SGE, False),
                              (tx.CMP_SLT, True), (tx.CMP_SLE, True)):
