@@ -54,7 +54,8 @@ def parse():
     ap.add_argument("--only", default="",
                     help="secondary workloads to run, comma-separated: ceiling, tiles, c1, vendor, tail, "
                          "w8a8 (or "
-                         "w8a8_1, w8a8_16, w8a8_64, w8a8_256), int8, fp8, kmajor, mx (or mxfp8, mxfp4, "
+                         "w8a8_1, w8a8_16, w8a8_64, w8a8_256; w8a8 also runs i32_16, the unscaled "
+                         "int8 -> int32 decode at M=16), int8, fp8, kmajor, mx (or mxfp8, mxfp4, "
                          "mxfp8_4096, mxfp8_8192, mxfp4_4096, mxfp4_8192), mxbf16 (or mxbf16_fp4, mxbf16_fp8: "
                          "bf16 x MX), attn (or attn_1024, attn_4096, "
                          "attn_16384; attn_fp8 or attn_fp8_<N> for e5m2; attn_d128 for head dim 128; "
@@ -270,6 +271,26 @@ def bench_w8a8(tx, dev, M, N, K, steps, warmup, flush, seed=3, block=(0, 0, 0)):
     # bracketed by its own events (adds the dispatch latency a stream hides)
     return dict(workload=f"int8 W8A8 M={M} N={N} K={K}", ms=med, ms_isolated=iso,
                 ms_warm_mall=warm, gbps=nbytes / med / 1e6, frac_hbm=nbytes / med / 1e-3 / HBM,
+                tops=2.0 * M * N * K / med / 1e9,
+                plan=plan_info(tx, p, split_k=p.split_k, grid=p.grid_x))
+
+
+def bench_decode_i32(tx, dev, M, N, K, steps, warmup, flush, seed=3):
+    """int8 x int8 -> int32 tt.dot of decode shape (no scales): the W8A8 decode kernel with
+    its int32 epilogue, timed like the W8A8 lines (cold, B from HBM)."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    a = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+    b = torch.randint(-127, 128, (K, N), generator=g, device=dev, dtype=torch.int8)
+    c = torch.empty((M, N), dtype=torch.int32, device=dev)
+    run = Launcher(tx, a, b, c)
+    iso, _ = time_cold(run, steps, warmup, flush)
+    med = time_cold_in_stream(run, flush)
+    nbytes = M * K + K * N + M * N * 4
+    p = run.plan
+    return dict(workload=f"int8 -> int32 (no scales) M={M} N={N} K={K}", ms=med, ms_isolated=iso,
+                gbps=nbytes / med / 1e6, frac_hbm=nbytes / med / 1e-3 / HBM,
                 tops=2.0 * M * N * K / med / 1e9,
                 plan=plan_info(tx, p, split_k=p.split_k, grid=p.grid_x))
 
@@ -679,6 +700,11 @@ def main():
             print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
                   f"({100 * r['frac_hbm']:.1f}% HBM); isolated launch "
                   f"{r['ms_isolated'] * 1e3:.2f} us", file=sys.stderr, flush=True)
+    if want("w8a8") or want("i32_16"):
+        r = bench_decode_i32(tx, dev, 16, 8192, 8192, max(args.steps, 20), 3, flush)
+        secondary.append(r)
+        print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
+              f"({100 * r['frac_hbm']:.1f}% HBM)", file=sys.stderr, flush=True)
     if want("int8"):
         r = bench_int8(tx, dev, 4096, 4096, 4096, args.steps, args.warmup)
         secondary.append(r)

@@ -188,10 +188,13 @@ TX_API int tx_dot_plan_create(const tx_dot_desc *desc, tx_dot_plan *plan);
  * the scaled modes and ignored otherwise: fp32 arrays for TX_SCALE_ROWCOL and
  * TX_SCALE_BLOCK128, uint8 e8m0 arrays for TX_SCALE_MX32.  `workspace`
  * must hold plan->workspace_bytes bytes when that is non-zero, and be
- * zero-filled before its first use: the W8A8 decode kernel keeps arrival
- * counters at its start, which every completed launch leaves at zero again
- * (the rest of the workspace needs no particular contents).  Launches that
- * may overlap in time (different streams) must not share a workspace. */
+ * zero-filled before its first use: every workspace starts with a 64 KiB
+ * region of the W8A8 decode kernel's arrival counters, which every completed
+ * decode launch leaves at zero again and no other kernel writes (the MX
+ * upcast of TX_KERNEL_GEMM_MX_BF16 plans goes after it).  So one workspace,
+ * zeroed once, serves every plan in turn; the rest of it needs no particular
+ * contents.  Launches that may overlap in time (different streams) must not
+ * share a workspace. */
 TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A, const void *B,
                          void *C, const void *scale_a, const void *scale_b,
                          void *workspace, size_t workspace_bytes, void *stream);

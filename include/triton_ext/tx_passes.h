@@ -116,6 +116,10 @@ TX_API int tx_arith_intensity(const tx_dot_desc *desc, tx_ai_report *out);
 TX_API int tx_dot_operand_spans(const tx_dot_desc *desc, int64_t *a_bytes, int64_t *b_bytes);
 /* Largest operand span (bytes, exclusive) the 32-bit-offset tiles take. */
 #define TX_SPAN32_LIMIT ((int64_t)1 << 31)
+/* Row stride (elements) of a B operand that tl.dot_scaled with one bf16 side
+ * upcasts to bf16 in the workspace: N rounded up to 16 columns, so every row
+ * starts 16-byte aligned for the bf16 tile.  (An upcast A is packed: K.) */
+#define TX_MX_UPCAST_LD(n) ((((int64_t)(n)) + 15) / 16 * 16)
 
 #ifdef __cplusplus
 }

@@ -15,6 +15,8 @@ from triton_ext_amd import capi
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 INC = os.path.join(ROOT, "include")
 CSRC = os.path.join(ROOT, "triton-ext_amd", "csrc")
+# every workspace starts with the decode kernel's 64 KiB arrival-counter region
+COUNTERS = 64 << 10
 
 
 def _defined_symbols(path):
@@ -163,7 +165,7 @@ def test_plan_validation():
     # an upcast MX B operand may have any N: its bf16 rows are N rounded up to 16 columns
     p = tx.plan(tx.make_desc(64, 72, 64, tx.BF16, tx.F32, b_type=tx.F8E4M3, ldb=80,
                              scale_mode=tx.SCALE_MX32))
-    assert p.kernel == tx.KERNEL_GEMM_MX_BF16 and p.workspace_bytes == 64 * 80 * 2
+    assert p.kernel == tx.KERNEL_GEMM_MX_BF16 and p.workspace_bytes == COUNTERS + 64 * 80 * 2
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.I32)) == tx.ERR_UNSUPPORTED
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, b_type=tx.F16)) == tx.ERR_UNSUPPORTED
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, block=(96, 64, 64))) == tx.ERR_UNSUPPORTED
@@ -182,8 +184,13 @@ def test_plan_validation():
     (257, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
     (512, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
     (513, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_GEMM_I8),
-    (300, 304, 256, tx.I8, tx.I32, 0, tx.KERNEL_GEMM_I8),
-    (2, 8192, 8192, tx.I8, tx.I32, 0, tx.KERNEL_GEMM_I8),
+    # plain int8 -> int32 of decode shape: the decode kernels' int32 epilogue
+    (300, 304, 256, tx.I8, tx.I32, 0, tx.KERNEL_DECODE_I8),
+    (2, 8192, 8192, tx.I8, tx.I32, 0, tx.KERNEL_DECODE_I8),
+    (16, 8192, 8192, tx.I8, tx.I32, 0, tx.KERNEL_DECODE_I8),
+    (256, 8192, 8192, tx.I8, tx.I32, 0, tx.KERNEL_DECODE_I8),
+    (513, 8192, 8192, tx.I8, tx.I32, 0, tx.KERNEL_GEMM_I8),
+    (4096, 4096, 4096, tx.I8, tx.I32, 0, tx.KERNEL_GEMM_I8),
     (2048, 7168, 7168, tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, tx.KERNEL_GEMM_F8),
 ])
 def test_kernel_choice(M, N, K, a, c, sm, kernel):
@@ -197,11 +204,14 @@ def test_kernel_choice(M, N, K, a, c, sm, kernel):
         assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == \
             (bm, 128, 128 if M > 48 else 64)
         slices = -(-M // bm)
-        assert p.grid_x == (N // 128) * slices * p.split_k == 256
+        assert p.grid_x == -(-N // 128) * slices * p.split_k
+        if N == 8192:  # the decode shapes fill the 256 CUs
+            assert p.grid_x == 256
         # a fixed 64 KiB counter region, then the int32 partials: [split][M][N] up to
         # M = 48, [split][slice][strip][block_m rows x 128 columns] past it
         rows = M if M <= 48 else slices * bm
-        assert p.workspace_bytes == (65536 + p.split_k * rows * N * 4 if p.split_k > 1 else 0)
+        cols = -(-N // 4) * 4 if M <= 48 else -(-N // 128) * 128
+        assert p.workspace_bytes == (65536 + p.split_k * rows * cols * 4 if p.split_k > 1 else 0)
     assert (p.split_k & (p.split_k - 1)) == 0
 
 
@@ -272,7 +282,7 @@ def test_mx_plans():
             (q.desc.block_m, q.desc.block_n, q.desc.block_k)
         assert (p.k_main_steps, p.k_tail, p.grid_x) == (q.k_main_steps, q.k_tail, q.grid_x)
         mx_elems = 4000 * 528 if b != tx.BF16 else 1000 * 4000
-        assert p.workspace_bytes == (mx_elems * 2 + 255) // 256 * 256
+        assert p.workspace_bytes == COUNTERS + (mx_elems * 2 + 255) // 256 * 256
         bits = {tx.BF16: 16, tx.F4E2M1: 4, tx.F8E4M3: 8, tx.F8E5M2: 8}
         scale_rows = 528 if b != tx.BF16 else 1000  # only the MX side is scaled
         assert p.bytes == 1000 * 4000 * bits[a] / 8 + 4000 * 528 * bits[b] / 8 + \
@@ -287,11 +297,11 @@ def test_nv16_plans():
     NV = tx.SCALE_NV16
     p = tx.plan(tx.make_desc(512, 256, 1024, tx.F4E2M1, tx.F32, b_type=tx.F4E2M1, scale_mode=NV))
     assert p.kernel == tx.KERNEL_GEMM_MX_BF16
-    assert p.workspace_bytes == 512 * 1024 * 2 + 1024 * 256 * 2  # both operands as bf16
+    assert p.workspace_bytes == COUNTERS + 512 * 1024 * 2 + 1024 * 256 * 2  # both as bf16
     assert p.bytes == 512 * 512 + 512 * 256 + (512 + 256) * 64 + 512 * 256 * 4
     assert p.peak_flops == pytest.approx(2516.6e12)
     p = tx.plan(tx.make_desc(512, 256, 1024, tx.BF16, tx.F32, b_type=tx.F4E2M1, scale_mode=NV))
-    assert p.workspace_bytes == 1024 * 256 * 2
+    assert p.workspace_bytes == COUNTERS + 1024 * 256 * 2
     assert _err(tx.make_desc(64, 64, 256, tx.F8E4M3, tx.F32, scale_mode=NV)) == tx.ERR_UNSUPPORTED
     assert _err(tx.make_desc(64, 64, 256, tx.F4E2M1, tx.F32, scale_mode=5)) == tx.ERR_INVALID
 
@@ -301,7 +311,10 @@ def test_accumulate_plans():
     p = tx.plan(tx.make_desc(1024, 1024, 1024, tx.BF16, tx.F32, flags=tx.FLAG_ACCUMULATE))
     q = tx.plan(tx.make_desc(1024, 1024, 1024, tx.BF16, tx.F32))
     assert p.bytes == q.bytes + 1024 * 1024 * 4 and p.kernel == q.kernel
+    # int32 C accumulates on the decode kernels too (M <= 512) and on the 8-bit tiles
     assert tx.plan(tx.make_desc(64, 128, 256, tx.I8, tx.I32,
+                                flags=tx.FLAG_ACCUMULATE)).kernel == tx.KERNEL_DECODE_I8
+    assert tx.plan(tx.make_desc(1024, 128, 256, tx.I8, tx.I32,
                                 flags=tx.FLAG_ACCUMULATE)).kernel == tx.KERNEL_GEMM_I8
     assert _err(tx.make_desc(256, 256, 256, tx.BF16, tx.BF16,
                              flags=tx.FLAG_ACCUMULATE)) == tx.ERR_UNSUPPORTED

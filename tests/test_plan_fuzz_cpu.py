@@ -224,6 +224,22 @@ def test_tampered_dot_plans_are_refused_at_launch(shape):
             f"{name}: launch answered {rc} ({L.tx_get_last_error()})"
 
 
+def test_upcast_b_span_uses_the_upcast_row_stride():
+    """MX x bf16 with ragged N near 2 GiB: the planner prices the upcast B at its real row
+    stride (N rounded up to 16 columns, the stride the launch uses), so it picks a tile
+    whose 32-bit offsets reach it -- the 128x128 tile here -- instead of a 256-wide tile
+    that plan creation then refuses."""
+    M, N, K = 3840, 3841, 278464
+    p = tx.plan(tx.make_desc(M, N, K, tx.BF16, tx.F32, b_type=tx.F8E4M3, ldb=3856, ldc=3844,
+                             scale_mode=tx.SCALE_MX32))
+    assert p.kernel == tx.KERNEL_GEMM_MX_BF16
+    assert (p.desc.block_m, p.desc.block_n) == (128, 128)
+    # the upcast B: K rows of N rounded up to 16 bf16 columns, at or past 2^31 bytes
+    assert (K - 1) * ((N + 15) // 16 * 16) * 2 + N * 2 >= 1 << 31
+    if _no_device():  # the launch's own checks accept it (dummy pointers: never on a GPU)
+        assert _launch(p) == tx.ERR_NO_DEVICE, capi.load().tx_get_last_error()
+
+
 def test_attention_planner_fuzz_and_tampering():
     L = capi.load()
     rng = np.random.default_rng(SEED + 1)

@@ -219,13 +219,18 @@ int mxUpcastSide(const tx_dot_desc &d) {
 
 // Workspace of the upcast form: the MX operand as bf16, 256-byte aligned;
 // an upcast B's rows hold N rounded up to 16 columns (16-byte aligned rows
-// for the bf16 tile, zeros past N).
-int64_t mxUpcastLdB(const tx_dot_desc &d) { return cdiv(d.N, 16) * 16; }
-int64_t mxUpcastWorkspace(const tx_dot_desc &d) {
+// for the bf16 tile, zeros past N).  The upcast starts after the decode
+// kernel's counter region (kDecodeCounterBytes), which it never writes, so
+// one workspace serves both kernels in any order.
+int64_t mxUpcastLdB(const tx_dot_desc &d) { return TX_MX_UPCAST_LD(d.N); }
+int64_t mxUpcastOperandBytes(const tx_dot_desc &d) {
   const int side = mxUpcastSide(d);
   const int64_t a = (side & 1) ? (d.M * d.K * 2 + 255) / 256 * 256 : 0;
   const int64_t b = (side & 2) ? (d.K * mxUpcastLdB(d) * 2 + 255) / 256 * 256 : 0;
   return a + b; // A's upcast first, then B's
+}
+int64_t mxUpcastWorkspace(const tx_dot_desc &d) {
+  return mxUpcastSide(d) ? kDecodeCounterBytes + mxUpcastOperandBytes(d) : 0;
 }
 
 // Operand kind and epilogue of a descriptor (-1 if unsupported).
@@ -327,11 +332,17 @@ int decodeSlices(const tx_dot_desc &d) {
   return (int)cdiv(M, decodeRows(d) ? d.block_m : 16 * decodeMT(M));
 }
 
-// W8A8 shapes a decode kernel takes: M <= 256 (the row kernel, named by its
-// block, up to 1024), N up to 4096 strips, and one arrival counter of the
-// fixed region per (slice, strip).
+// Shapes a decode kernel takes: W8A8 (row x column scales, bf16 C) or a
+// plain int8 -> int32 dot (no scales, int32 C, optionally accumulating);
+// M <= 256 (the row kernel, named by its block, up to 1024), N up to 4096
+// strips, and one arrival counter of the fixed region per (slice, strip).
+bool decodeEpilogue(const tx_dot_desc &d) {
+  return d.a_type == TX_I8 && d.b_type == TX_I8 &&
+         ((d.scale_mode == TX_SCALE_ROWCOL && d.c_type == TX_BF16) ||
+          (d.scale_mode == TX_SCALE_NONE && d.c_type == TX_I32));
+}
 bool useDecode(const tx_dot_desc &d) {
-  if (d.a_type != TX_I8 || d.scale_mode != TX_SCALE_ROWCOL || (d.flags & TX_FLAG_B_KMAJOR) ||
+  if (!decodeEpilogue(d) || (d.flags & TX_FLAG_B_KMAJOR) ||
       d.N > (int64_t)kDecodeMaxStrips * kDecodeStripN ||
       d.M > (decodeRows(d) ? kDecodeRowsMaxM : kDecodeMaxM))
     return false;
@@ -675,9 +686,11 @@ int launchMxUpcast(const tx_dot_plan &plan, const void *A, const void *B, void *
                 (long long)need, ws_bytes);
   if (reinterpret_cast<uintptr_t>(ws) & 15)
     return fail(TX_ERR_INVALID, "workspace must be 16-byte aligned");
-  uint16_t *wa = static_cast<uint16_t *>(ws);
+  // past the decode counters, which stay untouched
+  uint8_t *const up = static_cast<uint8_t *>(ws) + kDecodeCounterBytes;
+  uint16_t *wa = reinterpret_cast<uint16_t *>(up);
   uint16_t *wb = reinterpret_cast<uint16_t *>(
-      static_cast<uint8_t *>(ws) + ((side & 1) ? (d.M * d.K * 2 + 255) / 256 * 256 : 0));
+      up + ((side & 1) ? (d.M * d.K * 2 + 255) / 256 * 256 : 0));
   typedef void (*UpFn)(txk::UpcastArgs);
   auto upcast = [&](int one) -> int {
     const int fmt = mxFormat(one == 2 ? d.b_type : d.a_type);
@@ -758,7 +771,10 @@ int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   DecodeArgs a;
   a.A = static_cast<const int8_t *>(A);
   a.B = static_cast<const int8_t *>(B);
-  a.C = static_cast<uint16_t *>(C);
+  const bool i32 = d.c_type == TX_I32;
+  a.C = i32 ? nullptr : static_cast<uint16_t *>(C);
+  a.Ci = i32 ? static_cast<int32_t *>(C) : nullptr;
+  a.acc_c = i32 && (d.flags & TX_FLAG_ACCUMULATE) != 0;
   a.sa = static_cast<const float *>(sa);
   a.sb = static_cast<const float *>(sb);
   a.M = (int32_t)d.M;
@@ -791,7 +807,8 @@ int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
 // code never uses the name as an address: the device address comes from
 // hipGetSymbolAddress, once per device.  Layout: the decode kernel's counter
 // region first (kDecodeCounterBytes), then its partials; an MX upcast writes
-// after the counter region only, so it never disturbs the counters.
+// after the counter region only (as in every workspace), so it never disturbs
+// the counters.
 __device__ __attribute__((aligned(256))) uint8_t scratch[TX_NOALLOC_SCRATCH_BYTES];
 static_assert(kDecodeCounterBytes % 256 == 0, "upcast scratch stays 256-byte aligned");
 
@@ -901,18 +918,11 @@ int launchPlanned(const tx_dot_plan *plan, const void *A, const void *B, void *C
   const int prc = checkPlan(*plan);
   if (prc != TX_OK)
     return prc;
-  if (noalloc) {
-    // The upcast operand goes after the counter region, the decode
-    // workspace (counters first) at the start.
-    const int64_t room = plan->kernel == TX_KERNEL_GEMM_MX_BF16
-                             ? (int64_t)TX_NOALLOC_SCRATCH_BYTES - kDecodeCounterBytes
-                             : (int64_t)TX_NOALLOC_SCRATCH_BYTES;
-    if (plan->workspace_bytes < 0 || plan->workspace_bytes > room)
-      return fail(TX_ERR_WORKSPACE,
-                  "the plan needs %lld bytes of workspace; the no-allocation scratch "
-                  "holds %lld for this kernel",
-                  (long long)plan->workspace_bytes, (long long)room);
-  }
+  if (noalloc && (plan->workspace_bytes < 0 ||
+                  plan->workspace_bytes > (int64_t)TX_NOALLOC_SCRATCH_BYTES))
+    return fail(TX_ERR_WORKSPACE,
+                "the plan needs %lld bytes of workspace; the no-allocation scratch holds %lld",
+                (long long)plan->workspace_bytes, (long long)TX_NOALLOC_SCRATCH_BYTES);
   if (!tx_device_available())
     return fail(TX_ERR_NO_DEVICE, "no gfx950 device visible");
   if (noalloc && plan->workspace_bytes > 0) {
@@ -920,10 +930,8 @@ int launchPlanned(const tx_dot_plan *plan, const void *A, const void *B, void *C
     const int rc = scratchOfCurrentDevice(&base);
     if (rc != TX_OK)
       return rc;
-    const bool up = plan->kernel == TX_KERNEL_GEMM_MX_BF16;
-    workspace = up ? base + kDecodeCounterBytes : base;
-    workspace_bytes = up ? TX_NOALLOC_SCRATCH_BYTES - kDecodeCounterBytes
-                         : TX_NOALLOC_SCRATCH_BYTES;
+    workspace = base;
+    workspace_bytes = TX_NOALLOC_SCRATCH_BYTES;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (plan->kernel) {

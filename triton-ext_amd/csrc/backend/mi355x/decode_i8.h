@@ -1,6 +1,8 @@
 // int8 W8A8 small-M dot (decode shape) for gfx950:
 //   C[m][n] = bf16((float(sum_k A[m][k] * B[k][n]) * sa[m]) * sb[n])
-// with A int8 [M,K] (M <= 256), B int8 [K,N] row-major, int32 accumulation.
+// with A int8 [M,K] (M <= 256), B int8 [K,N] row-major, int32 accumulation;
+// or, with no scales, the int32 sums themselves (a plain int8 -> int32
+// tt.dot of decode shape: C = sum, or C += sum for tl.dot's acc).
 //
 // The job is one pass over B, so it is HBM-bound and the kernel is built to
 // stream B once with every CU keeping plenty of bytes in flight:
@@ -64,7 +66,9 @@ constexpr int64_t kDecodeCounterBytes = (int64_t)(kDecodeMaxM / 64) * kDecodeMax
 struct DecodeArgs {
   const int8_t *A;
   const int8_t *B;
-  uint16_t *C;
+  uint16_t *C;       // bf16 C of the W8A8 epilogue (when Ci is null)
+  int32_t *Ci;       // int32 C of a plain int8 -> int32 dot (no scales), or null
+  int32_t acc_c;     // with Ci: add the sums to C's contents (tl.dot's acc)
   const float *sa;
   const float *sb;
   int32_t M, N, K;
@@ -136,6 +140,28 @@ __device__ __forceinline__ void lds_read_a(uint32_t addr, i32x4_t (&a)[MT]) {
                  "ds_read_b128 %2, %4 offset:2048\n\tds_read_b128 %3, %4 offset:3072\n\t"
                  "s_waitcnt lgkmcnt(0)"
                  : "=v"(a[0]), "=v"(a[1]), "=v"(a[2]), "=v"(a[3]) : "v"(addr) : "memory");
+}
+
+// The int32 epilogue of one column quad of row m (columns n .. n + 3, n a
+// multiple of 4; row strides are multiples of 4 elements, so the quad is
+// 16-byte aligned): C = sum, or C += sum under acc_c; elements past N are
+// not touched.
+__device__ __forceinline__ void decode_store_i32(const DecodeArgs &p, int64_t m, bool row_in,
+                                                 int64_t n, const i32x4_t &sum) {
+  if (!row_in || n >= p.N)
+    return;
+  int32_t *c = p.Ci + m * p.ldc + n;
+  if (n + 4 <= p.N) {
+    i32x4_t v = sum;
+    if (p.acc_c)
+      v += *reinterpret_cast<const i32x4_t *>(c);
+    *reinterpret_cast<i32x4_t *>(c) = v;
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (n + r < p.N)
+        c[r] = p.acc_c ? c[r] + sum[r] : sum[r];
+  }
 }
 
 template <int MT> struct DecodeCfg {
@@ -306,14 +332,19 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
   constexpr int RPT = 2 * MT;
   static_assert(RPT * 4 * kDecodeWaves * 64 == MT * 16 * kDecodeStripN, "quads cover the tile");
   const int cq = 4 * (tid & 31), rq = tid >> 5;
-  float sbv[4], sav[RPT];
+  float sbv[4] = {0.f, 0.f, 0.f, 0.f}, sav[RPT];
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-    sbv[r] = p.sb[n0 + cq + r < p.N ? n0 + cq + r : 0];
+  for (int j = 0; j < RPT; ++j)
+    sav[j] = 0.f;
+  if (!p.Ci) { // the W8A8 epilogue's scales (an int32 C has none)
 #pragma unroll
-  for (int j = 0; j < RPT; ++j) {
-    const int m = rq + 8 * j;
-    sav[j] = p.sa[row0 + (m < Mr ? m : 0)];
+    for (int r = 0; r < 4; ++r)
+      sbv[r] = p.sb[n0 + cq + r < p.N ? n0 + cq + r : 0];
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      const int m = rq + 8 * j;
+      sav[j] = p.sa[row0 + (m < Mr ? m : 0)];
+    }
   }
 
   // Prologue: STAGES - 1 batches in flight; batch i uses slot i % STAGES.
@@ -374,8 +405,15 @@ k_loop_done:
   }
   // C = bf16((float(sum) * sa[m]) * sb[n]) for this thread's quads: one
   // 8-byte store per row (ldc and n0 + cq are multiples of 4), single
-  // elements where the quad crosses N.
+  // elements where the quad crosses N.  An int32 C takes the sums (plus C's
+  // contents under acc_c) as one 16-byte access per row.
   auto epilogue = [&](const i32x4_t (&sum)[RPT]) {
+    if (p.Ci) {
+#pragma unroll
+      for (int j = 0; j < RPT; ++j)
+        decode_store_i32(p, row0 + rq + 8 * j, rq + 8 * j < Mr, n0 + cq, sum[j]);
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < RPT; ++j) {
       const int m = rq + 8 * j;

@@ -1,7 +1,8 @@
 // int8 W8A8 dot for taller decode shapes (64 < M <= 256) on gfx950:
 //   C[m][n] = bf16((float(sum_k A[m][k] * B[k][n]) * sa[m]) * sb[n])
-// with A int8 [M,K], B int8 [K,N] row-major, int32 accumulation: the same
-// job and result as decode_i8.h, with the work split the other way.
+// with A int8 [M,K], B int8 [K,N] row-major, int32 accumulation (or the
+// int32 sums themselves for an unscaled int8 -> int32 dot): the same job and
+// result as decode_i8.h, with the work split the other way.
 //
 // decode_i8.h gives each workgroup a row slice of at most 64 rows, so past
 // M = 64 every 128-column strip of B is streamed once per slice, and its 4
@@ -275,7 +276,7 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_rows_i8_kernel(De
   // the first batch's wait covers them: each wave its rows' sa, waves 0 and
   // 1 a half of the strip's sb each.  Rows past M and columns past N read
   // element 0 (their results are not stored).
-  {
+  if (!p.Ci) { // an int32 C has no scales
     const int m = row0 + lane;
     __builtin_amdgcn_global_load_lds(p.sa + (lane < WROWS && m < p.M ? m : 0),
                                      (lds_void *)(scl + kDecodeStripN + 64 * wave), 4, 0, 0);
@@ -315,6 +316,21 @@ k_loop_done:
   // 8-byte store; single elements where the quad crosses N).
   const int rl = lane & 31, ch = lane >> 5;
   auto epilogue = [&](const i32x16_t (&sum)[R32][NCB]) {
+    if (p.Ci) { // int32 C: the sums (C += sum under acc_c), one 16-byte access a quad
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int rb = 0; rb < R32; ++rb) {
+            const int m = 32 * rb + rl;
+            const i32x4_t v = {sum[rb][cb][4 * q], sum[rb][cb][4 * q + 1],
+                               sum[rb][cb][4 * q + 2], sum[rb][cb][4 * q + 3]};
+            decode_store_i32(p, row0 + m, m < Mr,
+                             n0 + 32 * (NCB * cw + cb) + 8 * q + 4 * ch, v);
+          }
+      return;
+    }
     float sav[R32];
 #pragma unroll
     for (int rb = 0; rb < R32; ++rb)

@@ -185,10 +185,18 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
       if (e.a_type != TX_BF16)
         e.a_type = TX_BF16, e.lda = 0;
       if (e.b_type != TX_BF16)
-        e.b_type = TX_BF16, e.ldb = 0;
+        e.b_type = TX_BF16, e.ldb = TX_MX_UPCAST_LD(d->N);
     }
     int64_t spanA = 0, spanB = 0;
     tx_dot_operand_spans(&e, &spanA, &spanB);
+    // The decode kernels' epilogues: W8A8 (row x column scales, bf16 C) and
+    // the plain int8 -> int32 dot (no scales, int32 C), B row-major, N up to
+    // their 4096 column strips.  Both stream B once with split-K.
+    const bool decode =
+        d->a_type == TX_I8 && d->b_type == TX_I8 && !(d->flags & TX_FLAG_B_KMAJOR) &&
+        d->N <= (int64_t)4096 * 128 &&
+        ((d->scale_mode == TX_SCALE_ROWCOL && d->c_type == TX_BF16) ||
+         (d->scale_mode == TX_SCALE_NONE && d->c_type == TX_I32));
     const size_t first = spanA < TX_SPAN32_LIMIT && spanB < TX_SPAN32_LIMIT ? 0 : 1;
     if (upcast)
       t = chooseTile(kTiles16, d->M, d->N, d->K, first); // MX x bf16 runs on the bf16 tile
@@ -198,15 +206,13 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
       t = kTiles16[0]; // the K-major B kernel exists for this tile only
     else if (sa == 2)
       t = chooseTile(kTiles16, d->M, d->N, d->K, first);
-    else if (d->a_type == TX_I8 && d->scale_mode == TX_SCALE_ROWCOL && d->M > 256 &&
-             d->M <= 512 && d->N <= (int64_t)4096 * 128 && !(d->flags & TX_FLAG_B_KMAJOR))
+    else if (decode && d->M > 256 && d->M <= 512)
       // W8A8 past the decode sizes, up to M = 512: the row-parallel decode
       // kernel's slices of 256 rows (measured at N = K = 8192: M = 384 62.3 us,
       // 512 63.8, against 98.0 and 99.3 on the 8-bit tiles; at 768 113.2
       // against 110.4, so larger M stays on the tiles)
       t = Tile{256, 128, 128, 1.0};
-    else if (d->a_type == TX_I8 && d->scale_mode == TX_SCALE_ROWCOL && d->M <= 256 &&
-             d->N <= (int64_t)4096 * 128)
+    else if (decode && d->M <= 256)
       // W8A8 decode (M <= 256, N up to its 4096 column strips), 128-column
       // strips.  Up to M = 48 one row slice and 64-row K batches split among
       // the waves; beyond, row slices whose waves all take every 128-row K

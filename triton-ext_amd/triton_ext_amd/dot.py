@@ -107,10 +107,13 @@ def workspace_for(p, device, stream):
     (device, stream): launches on one stream run one after another, so they
     may share it; launches on different streams may overlap and get their own.
 
-    The decode kernel's arrival counters must start at zero; every completed
-    launch leaves them at zero again, so the buffer is reused.  A grown
-    buffer replaces the old one only after the stream has finished with it
-    (torch's caching allocator orders the free after the stream's work).
+    Every plan's workspace starts with the decode kernel's arrival counters,
+    which must start at zero and which every completed launch leaves at zero
+    (the MX upcast writes only after them), so one buffer serves every plan.
+    The buffer is allocated and zero-filled on `stream` itself, so the fill
+    runs before any launch enqueued there after it, and torch's caching
+    allocator orders the release of a buffer that grew too small after that
+    stream's queued work.
     """
     import torch
     if p.workspace_bytes == 0:
@@ -118,7 +121,10 @@ def workspace_for(p, device, stream):
     key = (str(device), int(stream or 0))
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < p.workspace_bytes:
-        ws = torch.zeros(int(p.workspace_bytes), dtype=torch.uint8, device=device)
+        s = (torch.cuda.ExternalStream(int(stream), device=device) if stream
+             else torch.cuda.default_stream(device))
+        with torch.cuda.device(device), torch.cuda.stream(s):
+            ws = torch.zeros(int(p.workspace_bytes), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
 
@@ -295,7 +301,7 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
         raise ValueError(f"out's row stride {ldc} differs from the plan's ldc {plan.desc.ldc}")
     if stream is None:
         stream = torch.cuda.current_stream(lhs.device).cuda_stream
-    ws = _upcast_workspace(plan, lhs.device, stream)
+    ws = workspace_for(plan, lhs.device, stream)
     L = capi.load()
     capi.check(L.tx_dot_launch(ctypes.byref(plan), lhs.data_ptr(), rhs.data_ptr(),
                                out.data_ptr(),
@@ -304,24 +310,6 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
                                None if ws is None else ws.data_ptr(),
                                0 if ws is None else ws.numel(), stream))
     return out
-
-
-_upcast_workspaces = {}
-
-
-def _upcast_workspace(p, device, stream):
-    """Workspace of an MX x bf16 dot_scaled (the upcast operand), cached per
-    (device, stream) apart from the decode kernel's (whose counters it would
-    clobber): launches on one stream run in order, so they share it."""
-    import torch
-    if p.workspace_bytes == 0:
-        return None
-    key = (str(device), int(stream or 0))
-    ws = _upcast_workspaces.get(key)
-    if ws is None or ws.numel() < p.workspace_bytes:
-        ws = torch.empty(int(p.workspace_bytes), dtype=torch.uint8, device=device)
-        _upcast_workspaces[key] = ws
-    return ws
 
 
 def attention(q, k, v, causal, sm_scale, USE_TMA=True, *, return_lse=False, plan=None,
