@@ -80,10 +80,8 @@ typedef struct tx_attn_plan {
 
 /* Validate `desc` and fill `plan`.  TX_ERR_UNSUPPORTED unless dtype is
  * TX_F16, TX_BF16 or TX_F8E5M2 with head_dim 16, 32, 64, 128 or 256, the
- * blocks one of the implemented configs (an fp16/bf16 K block, BLOCK_N x
- * head_dim elements, head_dim 16 staged as 32, must fill one 1 KiB load per
- * wave: head_dims 16 and 32 reject 128 x 32)
- * and N_CTX a multiple of BLOCK_M (the tutorial's block pointers assume whole
+ * blocks one of the implemented configs (BLOCK_M 64 or 128 by BLOCK_N 32 or
+ * 64, at every head_dim) and N_CTX a multiple of BLOCK_M (the tutorial's block pointers assume whole
  * blocks).  p is rounded to q's type to nearest even before p @ v, as
  * compiled Triton does. */
 TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *plan);

@@ -241,13 +241,11 @@ def test_attn_plan():
             tx.attn_plan(**a)
         return e.value.code
     assert err(head_dim=96) == tx.ERR_UNSUPPORTED
-    # head dims: the tutorial's {16, 32, 64, 128, 256} for fp16, bf16 and fp8; an fp16 / bf16
-    # K block (head dim 16 staged as 32) must fill one 1 KiB load per wave
+    # head dims: the tutorial's {16, 32, 64, 128, 256} for fp16, bf16 and fp8, at every
+    # block (head dims 16 and 32 at 128 x 32: a 2 KiB K block that two of the four waves load)
     for hd in (16, 32, 64, 128, 256):
-        for blk in ((128, 64), (64, 64), (64, 32)) + (((128, 32),) if hd > 32 else ()):
+        for blk in ((128, 64), (64, 64), (64, 32), (128, 32)):
             assert tx.attn_plan(1, 1, 256, hd, True, 0.5, dtype=tx.BF16, block=blk).desc.head_dim == hd
-    assert err(head_dim=32, block=(128, 32)) == tx.ERR_UNSUPPORTED
-    assert err(head_dim=16, block=(128, 32)) == tx.ERR_UNSUPPORTED
     assert tx.attn_plan(1, 1, 256, 16, False, 0.5).flops == 4 * 256 ** 2 * 16
     assert err(head_dim=8) == tx.ERR_UNSUPPORTED
     for hd in (16, 32, 64, 128, 256):  # fp8 stages head dims 16 and 32 as 64
@@ -272,13 +270,12 @@ def test_attn_plan():
     assert err(N_CTX=192, block=(128, 32)) == tx.ERR_UNSUPPORTED
     for blk in ((256, 64), (64, 16), (32, 32), (128, 128)):
         assert err(block=blk) == tx.ERR_UNSUPPORTED
-    # fp8 stages head dims below 64 as 64 (one byte per element): a 128 x 32
-    # block's 2 KiB K block is less than one 1 KiB load for each of 4 waves
-    for hd, blk in ((64, (64, 32)), (16, (64, 32)), (128, (128, 32)), (256, (128, 32))):
+    # fp8 stages head dims below 64 as 64 (one byte per element); at 128 x 32
+    # their 2 KiB K block is loaded by two of the four waves
+    for hd, blk in ((64, (64, 32)), (16, (64, 32)), (128, (128, 32)), (256, (128, 32)),
+                    (16, (128, 32)), (32, (128, 32)), (64, (128, 32))):
         p8 = tx.attn_plan(1, 2, 256, hd, True, 0.5, dtype=tx.F8E5M2, block=blk)
         assert (p8.desc.block_m, p8.desc.block_n) == blk and p8.block_threads == blk[0] // 32 * 64
-    for hd in (16, 32, 64):
-        assert err(head_dim=hd, dtype=tx.F8E5M2, block=(128, 32)) == tx.ERR_UNSUPPORTED
     assert tx.attn_plan(1, 1, 64, 64, False, 0.5, dtype=tx.F8E5M2, block=(64, 64)).grid_x == 1
     assert err(Z=-1) == tx.ERR_INVALID
     # e5m2: one byte per element, v key-contiguous ([HEAD_DIM][N_CTX] per head)

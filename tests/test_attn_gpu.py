@@ -121,9 +121,8 @@ def test_attn_blocks_vs_oracle(gpu, block, causal, Z, H, N, D, bf16):
 def test_attn_head_dims_16_32_and_256(gpu, block, causal, Z, H, N, D, bf16):
     """Head dims 32 and 256 (64- and 512-byte K/V rows, their own swizzles; 256 reads its
     fragments in groups), and 16 (staged as 32 with zero dims past 16, O's not stored), at
-    every block shape the plan accepts."""
-    if D <= 32 and block == (128, 32):
-        pytest.skip("a 2 KiB K block for four waves: rejected at plan time")
+    every block shape; at 128 x 32, head dims 16 and 32 give a 2 KiB K block that waves
+    0 and 1 load for all four."""
     attn_vs_oracle(gpu, block, causal, Z, H, N, D, bf16)
 
 
@@ -325,12 +324,16 @@ def test_attn_fp8_head_dims_16_32_and_256(gpu, causal, Z, H, N, D, block):
 @pytest.mark.parametrize("Z,H,N,D,block", [(1, 2, 64, 64, (64, 32)), (2, 3, 192, 64, (64, 32)),
                                            (1, 2, 256, 16, (64, 32)), (1, 3, 192, 32, (64, 32)),
                                            (1, 2, 320, 128, (64, 32)), (2, 1, 256, 128, (128, 32)),
-                                           (1, 2, 384, 256, (128, 32)), (2, 1, 192, 256, (64, 32))])
+                                           (1, 2, 384, 256, (128, 32)), (2, 1, 192, 256, (64, 32)),
+                                           (1, 2, 256, 16, (128, 32)), (2, 1, 384, 32, (128, 32)),
+                                           (1, 3, 256, 64, (128, 32))])
 def test_attn_fp8_block_n32(gpu, causal, Z, H, N, D, block):
     """fp8 e5m2 with BLOCK_N 32: one 32-key block per S^T MFMA and half of
     each P V MFMA (the other half of P and V^T zero bytes in registers),
     against the oracle at the same blocks.  N_CTX = 64, 192, 320 give odd
-    block counts at BLOCK_M 64; head dims 16 and 32 run in the layout of 64."""
+    block counts at BLOCK_M 64; head dims 16 and 32 run in the layout of 64, and
+    with 64 at 128 x 32 their 2 KiB K and V^T blocks are loaded by two of the
+    four waves."""
     say(f"attn fp8 block={block} Z={Z} H={H} N={N} D={D} causal={causal}")
     q, k, v = e5m2_qkv(Z, H, N, D, seed=Z * 100 + H * 10 + N + D + causal + 13)
     o, M = run_gpu_fp8(gpu, q, k, v, causal, 0.8, block=block)

@@ -116,7 +116,7 @@ def _cases():
                                    N=_dim(rng, 700), K=_dim(rng, 700))))
     for i in range(30):
         D = [16, 32, 64, 128, 256][i % 5]
-        blocks = [(128, 64), (64, 64), (64, 32)] + ([(128, 32)] if D > 32 else [])
+        blocks = [(128, 64), (64, 64), (64, 32), (128, 32)]
         bm, bn = blocks[int(rng.integers(len(blocks)))]
         out.append(("attn", i, dict(Z=int(rng.integers(1, 3)), H=int(rng.integers(1, 4)),
                                     N=bm * int(rng.integers(1, 6)), D=D, bf16=bool(i % 3 == 1),

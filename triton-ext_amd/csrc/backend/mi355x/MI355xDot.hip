@@ -975,25 +975,6 @@ extern "C" TX_API int tx_dot_launch_noalloc(const tx_dot_plan *plan, const void 
 
 namespace {
 
-// The 16-bit attention kernel for one configuration, or nullptr where a K
-// block is smaller than one 1 KiB load per wave (head dims 16 and 32, whose
-// blocks are staged as 32, with 128 x 32 blocks), which the plan rejects.
-template <bool C, int HD, bool BF, int BM, int BN> constexpr void (*attnKernel())(txk::AttnArgs) {
-  if constexpr ((HD < 32 ? 32 : HD) * 2 * BN >= 1024 * (BM / 32))
-    return txk::attn_fwd_kernel<C, HD, BF, BM, BN>;
-  else
-    return nullptr;
-}
-
-// The same for fp8 e5m2, whose blocks stage head dims below 64 as 64 (1 byte
-// per element): nullptr for 128 x 32 blocks at those head dims.
-template <bool C, int HD, int BM, int BN> constexpr void (*attn8Kernel())(txk::AttnArgs) {
-  if constexpr ((HD < 64 ? 64 : HD) * BN >= 1024 * (BM / 32))
-    return txk::attn_fwd8_kernel<C, HD, BM, BN>;
-  else
-    return nullptr;
-}
-
 // Packed defaults and checks of one tensor's (batch, head, row) strides.
 // key_major: e5m2 v, stored [HEAD_DIM][N_CTX] per head (sm = dim stride).
 int attnStrides(const tx_attn_desc &d, int64_t &sz, int64_t &sh, int64_t &sm,
@@ -1038,15 +1019,6 @@ extern "C" TX_API int tx_attn_fwd_plan(const tx_attn_desc *desc, tx_attn_plan *p
   if ((d.block_m != 64 && d.block_m != 128) || (d.block_n != 32 && d.block_n != 64))
     return fail(TX_ERR_UNSUPPORTED, "blocks %dx%d: BLOCK_M 64 or 128 by BLOCK_N 32 or 64 "
                 "are implemented", d.block_m, d.block_n);
-  // A K or V block (BLOCK_N rows of HEAD_DIM elements; head dims below 32
-  // staged as 32, fp8 head dims below 64 as 64) is staged by whole 1 KiB
-  // loads, at least one per wave.
-  const int esz = d.dtype == TX_F8E5M2 ? 1 : 2, min_dim = d.dtype == TX_F8E5M2 ? 64 : 32;
-  const int staged_dim = d.head_dim < min_dim ? min_dim : d.head_dim;
-  if ((int64_t)d.block_n * staged_dim * esz < 1024 * (d.block_m / 32))
-    return fail(TX_ERR_UNSUPPORTED, "head_dim %d with blocks %dx%d: a K block of %d bytes for "
-                "%d waves", d.head_dim, d.block_m, d.block_n, d.block_n * staged_dim * esz,
-                d.block_m / 32);
   if (d.N_CTX % d.block_m)
     return fail(TX_ERR_UNSUPPORTED, "N_CTX %lld is not a multiple of %d (whole blocks only)",
                 (long long)d.N_CTX, d.block_m);
@@ -1129,8 +1101,8 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
   hipStream_t s = static_cast<hipStream_t>(stream);
   typedef void (*AttnFn)(txk::AttnArgs);
 #define TX_ATTN_BLOCKS(C, HD, BF)                                                          \
-  {{attnKernel<C, HD, BF, 128, 64>(), attnKernel<C, HD, BF, 128, 32>()},                    \
-   {attnKernel<C, HD, BF, 64, 64>(), attnKernel<C, HD, BF, 64, 32>()}}
+  {{txk::attn_fwd_kernel<C, HD, BF, 128, 64>, txk::attn_fwd_kernel<C, HD, BF, 128, 32>},    \
+   {txk::attn_fwd_kernel<C, HD, BF, 64, 64>, txk::attn_fwd_kernel<C, HD, BF, 64, 32>}}
 #define TX_ATTN_DTYPES(C, HD) {TX_ATTN_BLOCKS(C, HD, false), TX_ATTN_BLOCKS(C, HD, true)}
   // [causal][head_dim 16 / 32 / 64 / 128 / 256][bf16][BLOCK_M 64][BLOCK_N 32]
   static const AttnFn kAttn[2][5][2][2][2] = {
@@ -1142,8 +1114,8 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
 #undef TX_ATTN_BLOCKS
   // [causal][head_dim 16 / 32 / 64 / 128 / 256][BLOCK_M 64][BLOCK_N 32]
 #define TX_ATTN8_BLOCKS(C, HD)                                                             \
-  {{attn8Kernel<C, HD, 128, 64>(), attn8Kernel<C, HD, 128, 32>()},                          \
-   {attn8Kernel<C, HD, 64, 64>(), attn8Kernel<C, HD, 64, 32>()}}
+  {{txk::attn_fwd8_kernel<C, HD, 128, 64>, txk::attn_fwd8_kernel<C, HD, 128, 32>},          \
+   {txk::attn_fwd8_kernel<C, HD, 64, 64>, txk::attn_fwd8_kernel<C, HD, 64, 32>}}
   static const AttnFn kAttn8[2][5][2][2] = {
       {TX_ATTN8_BLOCKS(false, 16), TX_ATTN8_BLOCKS(false, 32), TX_ATTN8_BLOCKS(false, 64),
        TX_ATTN8_BLOCKS(false, 128), TX_ATTN8_BLOCKS(false, 256)},
@@ -1158,8 +1130,6 @@ extern "C" TX_API int tx_attn_fwd_launch(const tx_attn_plan *plan, const void *q
                                      : 4;
   const AttnFn fn = d.dtype == TX_F8E5M2 ? kAttn8[c][hd][bm64][bn32]
                                          : kAttn[c][hd][d.dtype == TX_BF16][bm64][bn32];
-  if (!fn)
-    return fail(TX_ERR_INVALID, "plan launch shape does not match the attention kernel");
   hipLaunchKernelGGL(fn, dim3(plan->grid_x), dim3(plan->block_threads), 0, s, a);
   TX_HIP_CHECK(hipGetLastError());
   return TX_OK;

@@ -59,14 +59,19 @@ template <int HD, bool BF, int BM_ = 128, int BN_ = 64> struct AttnFwd {
   static constexpr int BM = BM_, BN = BN_, D = HD < 32 ? 32 : HD, DR = HD, NW = BM_ / 32,
                        ESZ = 2;
   static constexpr int ROW = D * 2;            // bytes per K/V row
-  static constexpr int TILE = BN * ROW;        // 4 / 8 / 16 KiB
-  static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 1 .. 8
+  static constexpr int TILE = BN * ROW;        // 2 .. 32 KiB
+  // LW: the waves that stage a K/V block, all of them unless the block holds
+  // fewer 1 KiB loads than there are waves (2 KiB for 4 waves at head dims
+  // 16 and 32 with 128 x 32 blocks: waves 0 and 1 load, 2 and 3 only wait
+  // at the barriers that publish every block).
+  static constexpr int LW = TILE / 1024 < NW ? TILE / 1024 : NW;
+  static constexpr int DMA = TILE / 1024 / LW; // 16-byte loads per lane per tile: 1 .. 8
   static constexpr int CPR = ROW / 16;         // 16-byte chunks per row: 8 / 16
   static constexpr uint32_t kOOB = 0x80000000u;
   static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head dims 16 .. 256");
   static_assert(DR == D || (DR == 16 && D == 32), "head dim 16 in the layout of 32");
   static_assert((BM == 64 || BM == 128) && (BN == 32 || BN == 64), "the tutorial's blocks");
-  static_assert(DMA >= 1 && DMA * NW * 1024 == TILE, "whole 1 KiB loads per wave");
+  static_assert(LW >= 1 && DMA >= 1 && DMA * LW * 1024 == TILE, "whole 1 KiB loads per wave");
   // Fragment reads issued together in qk / pv: every one at head dims up to
   // 128, in groups of 8 at 256 (all 32 would take 128 VGPRs).
   static constexpr int KGRP = D / 16 < 8 ? D / 16 : 8;
@@ -113,9 +118,12 @@ template <int HD, bool BF, int BM_ = 128, int BN_ = 64> struct AttnFwd {
     }
   }
 
-  // Loads of K block j into K slot `slot` (V block j into V slot `slot`).
+  // Loads of K block j into K slot `slot` (V block j into V slot `slot`);
+  // none from waves past LW (`wave` is wave-uniform).
   __device__ __forceinline__ static void issue(const i32x4_t &rsrc, const uint32_t (&off)[DMA],
                                                int64_t sm, int j, uint32_t slot_lds, int wave) {
+    if (LW < NW && wave >= LW)
+      return;
 #pragma unroll
     for (int u = 0; u < DMA; ++u)
       dma16(off[u], rsrc, (uint32_t)((int64_t)j * BN * sm * 2), slot_lds + (DMA * wave + u) * 1024);

@@ -48,14 +48,19 @@ template <int HD, int BM_ = 128, int BN_ = 64> struct AttnFwd8 {
   static constexpr int BM = BM_, BN = BN_, D = HD < 64 ? 64 : HD, DR = HD, NW = BM_ / 32,
                        ESZ = 1;
   static constexpr int TILE = BN * D;          // K: BN x D bytes; V^T: D x BN bytes
-  static constexpr int DMA = TILE / 1024 / NW; // 16-byte loads per lane per tile: 1 .. 8
+  // LW: the waves that stage a K/V block, all of them unless the block holds
+  // fewer 1 KiB loads than there are waves (2 KiB for 4 waves at head dims
+  // 16 and 32 with 128 x 32 blocks: waves 0 and 1 load, 2 and 3 only wait
+  // at the barriers that publish every block).
+  static constexpr int LW = TILE / 1024 < NW ? TILE / 1024 : NW;
+  static constexpr int DMA = TILE / 1024 / LW; // 16-byte loads per lane per tile: 1 .. 8
   static constexpr int KCPR = D / 16;          // K: 16-byte chunks per row
   static constexpr int VCPR = BN / 16;         // V^T: 16-byte chunks per dim row
   static constexpr uint32_t kOOB = 0x80000000u;
   static_assert(D == 64 || D == 128 || D == 256, "head dims 16 .. 256");
   static_assert(DR == D || (D == 64 && (DR == 16 || DR == 32)), "16 and 32 in the layout of 64");
   static_assert((BM == 64 || BM == 128) && (BN == 32 || BN == 64), "the tutorial's blocks");
-  static_assert(DMA >= 1 && DMA * NW * 1024 == TILE, "whole 1 KiB loads per wave");
+  static_assert(LW >= 1 && DMA >= 1 && DMA * LW * 1024 == TILE, "whole 1 KiB loads per wave");
   typedef float f16v __attribute__((ext_vector_type(16)));
 
   __device__ __forceinline__ static f16v mfma(const i32x8_t &a, const i32x8_t &b,
@@ -127,14 +132,19 @@ template <int HD, int BM_ = 128, int BN_ = 64> struct AttnFwd8 {
   }
   // K block j: rows j BN .. of the key-major K; V block j: bytes j BN .. of
   // every dim row.
+  // Neither issues from waves past LW (`wave` is wave-uniform).
   __device__ __forceinline__ static void issue_k(const i32x4_t &rsrc, const uint32_t (&off)[DMA],
                                                  int64_t sm, int j, uint32_t lds, int wave) {
+    if (LW < NW && wave >= LW)
+      return;
 #pragma unroll
     for (int u = 0; u < DMA; ++u)
       dma16(off[u], rsrc, (uint32_t)((int64_t)j * BN * sm), lds + (DMA * wave + u) * 1024);
   }
   __device__ __forceinline__ static void issue_v(const i32x4_t &rsrc, const uint32_t (&off)[DMA],
                                                  int64_t, int j, uint32_t lds, int wave) {
+    if (LW < NW && wave >= LW)
+      return;
 #pragma unroll
     for (int u = 0; u < DMA; ++u)
       dma16(off[u], rsrc, (uint32_t)(j * BN), lds + (DMA * wave + u) * 1024);
