@@ -52,7 +52,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
-                    help="secondary workloads to run, comma-separated: ceiling, tiles, c1, vendor, tail, "
+                    help="secondary workloads to run, comma-separated: ceiling, phases (where a "
+                         "headline launch's time goes), tiles, c1, vendor, tail, "
                          "w8a8 (or "
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256; w8a8 also runs i32_16, the unscaled "
                          "int8 -> int32 decode at M=16), int8, fp8, kmajor, mx (or mxfp8, mxfp4, "
@@ -207,7 +208,8 @@ def bench_bf16(tx, dev, M, N, K, steps, warmup, seed=1):
     return dict(workload=f"bf16 {M}x{N}x{K}", ms=ms, tflops=flops / ms / 1e9,
                 frac=flops / ms / 1e-3 / PEAK_BF16,
                 plan=plan_info(tx, p, k_split=p.k_split, k_main_steps=p.k_main_steps,
-                               k_tail=p.k_tail, m_edge=p.m_edge, n_edge=p.n_edge)), (a, b, c)
+                               k_tail=p.k_tail, m_edge=p.m_edge, n_edge=p.n_edge,
+                               group_m=p.group_m)), (a, b, c)
 
 
 def bench_c1(tx, dev, steps, warmup, seed=1):
@@ -472,6 +474,9 @@ def ceilings_lib():
     L.tx_ceiling_read.argtypes = [vp, ctypes.c_size_t, ctypes.c_int, vp, vp]
     L.tx_ceiling_mfma_bf16.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp]
     L.tx_ceiling_mfma_fp8.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp]
+    L.tx_ceiling_mfma_bf16_stamped.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp, vp]
+    L.tx_phases_bf16_setup.argtypes = [vp, ctypes.c_int]
+    L.tx_phases_bf16.argtypes = [vp, vp, vp] + [ctypes.c_int] * 5 + [vp]
     return L
 
 
@@ -524,6 +529,98 @@ def bench_mfma_ceiling(dev, steps, warmup, seed=1, zeros=False):
                          "v_mfma_f32_32x32x16_bf16 alone (operands in registers"
                          + (", all zero)" if zeros else ", N(0,1)/64)"),
                 ms=ms, tflops=flops / ms / 1e9, frac=flops / ms / 1e-3 / PEAK_BF16)
+
+
+def bench_phases(dev, a, b, c, group_m, steps, warmup, seed=1):
+    """Where one launch of the headline kernel goes.  libtx_ceilings.so builds
+    gemm16_w4_kernel with its phase stamps on (per wave: the wall clock and the shader
+    clock at entry, step 0 landed, K loop done, epilogue issued, stores acknowledged).
+    The stamped kernel is timed back to back like the headline; the stamps of its last
+    launch give each phase's share of the launch period in wave-time (one wave per SIMD
+    here), the K loop's shader clock and its MFMA busy (2048 MFMA cycles per K step and
+    wave against the loop's shader cycles).  A second pass stamps one K step at a time
+    (its MFMA phase, its wait for loads and LDS reads, its barrier, in shader cycles),
+    and the MFMA-only ceiling loop is stamped the same way for its clock and busy."""
+    import numpy as np
+    import torch
+    L = ceilings_lib()
+    M, K = a.shape
+    N = b.shape[1]
+    tm, tn, ks = M // 256, N // 256, K // 64
+    waves = tm * tn * 4
+    st = torch.zeros(waves * 16, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch(n):
+        if L.tx_phases_bf16(a.data_ptr(), b.data_ptr(), c.data_ptr(), tm, tn, ks, group_m, n,
+                            stream) != 0:
+            raise RuntimeError("tx_phases_bf16 failed")
+
+    def stamps(probe):
+        if L.tx_phases_bf16_setup(st.data_ptr(), probe) != 0:
+            raise RuntimeError("tx_phases_bf16_setup failed")
+
+    stamps(-1)
+    ms = time_back_to_back(lambda: launch(1), steps, warmup)  # the last launch's stamps remain
+    w = st.view(waves, 16).cpu().numpy().astype(np.int64)
+    rt, sc = w[:, 0:5], w[:, 8:13]                 # wall clock (10 ns), shader clock
+    r0, r4 = rt[:, 0].min(), rt[:, 4].max()
+    T = ms * 1e3                                   # us per launch
+    us = lambda x: x / 100.0
+    loop_us = us(rt[:, 2] - rt[:, 1])
+    loop_cyc = (sc[:, 2] - sc[:, 1]).astype(np.float64)
+    mfma_cyc = 2048.0 * ks
+    mfma_us = loop_us * mfma_cyc / loop_cyc
+    share = lambda x: round(float(np.sum(x)) / (waves * T), 4)
+    phases = {
+        "mfma_in_loop": share(mfma_us), "loop_other": share(loop_us - mfma_us),
+        "before_entry": share(us(rt[:, 0] - r0)), "prologue": share(us(rt[:, 1] - rt[:, 0])),
+        "epilogue": share(us(rt[:, 3] - rt[:, 2])), "store_drain": share(us(rt[:, 4] - rt[:, 3])),
+        "after_own_end": share(us(r4 - rt[:, 4])),
+        "between_launches": round(1.0 - us(r4 - r0) / T, 4)}
+    mean = lambda x: round(float(np.mean(x)), 2)
+    xcc = (w[:, 5] >> 32) & 7
+    xcd_end = {int(x): mean(us(rt[xcc == x, 4] - r0)) for x in range(8) if np.any(xcc == x)}
+    out = dict(
+        workload="phases of the bf16 4096^3 tile, stamped build (libtx_ceilings.so)",
+        ms_stamped=ms, tflops_stamped=2.0 * M * N * K / ms / 1e9, wave_time=phases,
+        us_mean={"prologue": mean(us(rt[:, 1] - rt[:, 0])), "k_loop": mean(loop_us),
+                 "epilogue": mean(us(rt[:, 3] - rt[:, 2])),
+                 "store_drain": mean(us(rt[:, 4] - rt[:, 3])),
+                 "span": round(us(r4 - r0), 2), "launch": round(T, 2)},
+        loop_ghz=round(float(np.mean(loop_cyc / (loop_us * 1e3))), 3),
+        epilogue_ghz=round(float(np.mean((sc[:, 4] - sc[:, 2]) / (us(rt[:, 4] - rt[:, 2]) * 1e3))), 3),
+        loop_mfma_busy=round(float(np.mean(mfma_cyc / loop_cyc)), 4),
+        xcd_mean_end_us=xcd_end)
+    steps_probed = {}
+    for s_ in (2, ks // 4, ks // 2, 3 * ks // 4, ks - 3):
+        stamps(s_)
+        launch(20)
+        torch.cuda.synchronize()
+        v = st.view(waves, 16).cpu().numpy().astype(np.int64)
+        steps_probed[s_] = {"mfma_phase": mean(v[:, 13] - v[:, 7]),
+                            "load_and_lds_wait": mean(v[:, 14] - v[:, 13]),
+                            "barrier": mean(v[:, 15] - v[:, 14])}
+    stamps(-1)
+    out["step_cycles"] = steps_probed
+    # the MFMA-only loop, stamped the same way
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    seed_t = (torch.randn((64 * 2048 * 8,), generator=g, device=dev) / 64).to(torch.bfloat16)
+    cst = torch.zeros(1024 * 4, dtype=torch.int64, device=dev)
+    cout = torch.empty(256 * 256, dtype=torch.float32, device=dev)
+
+    def ceil():
+        if L.tx_ceiling_mfma_bf16_stamped(seed_t.data_ptr(), 256, 64, cout.data_ptr(),
+                                          cst.data_ptr(), stream) != 0:
+            raise RuntimeError("tx_ceiling_mfma_bf16_stamped failed")
+    cms = time_back_to_back(ceil, steps, warmup)
+    cw = cst.view(1024, 4).cpu().numpy().astype(np.int64)
+    c_us = us(cw[:, 1] - cw[:, 0])
+    c_cyc = (cw[:, 3] - cw[:, 2]).astype(np.float64)
+    out["ceiling"] = {"ms": cms, "loop_ghz": round(float(np.mean(c_cyc / (c_us * 1e3))), 3),
+                      "loop_mfma_busy": round(float(np.mean(2048.0 * 64 / c_cyc)), 4)}
+    return out
 
 
 def bench_mfma_ceiling_fp8(dev, steps, warmup, seed=2, zeros=False):
@@ -665,6 +762,20 @@ def main():
         for r in bench_tiles(tx, dev, args.steps, args.warmup):
             secondary.append(r)
             print(f"# {r['workload']}: {100 * r['frac']:.1f}% of peak", file=sys.stderr, flush=True)
+    if want("phases"):
+        r = bench_phases(dev, a, b, c, head["plan"]["group_m"], args.steps, args.warmup)
+        secondary.append(r)
+        f = r["wave_time"]
+        print(f"# {r['workload']}: {r['ms_stamped'] * 1e3:.1f} us/launch; wave-time: MFMA in loop "
+              f"{100 * f['mfma_in_loop']:.1f}%, loop other {100 * f['loop_other']:.1f}%, prologue "
+              f"{100 * f['prologue']:.1f}%, epilogue {100 * f['epilogue']:.1f}% + drain "
+              f"{100 * f['store_drain']:.1f}%, skew {100 * (f['before_entry'] + f['after_own_end']):.1f}%, "
+              f"between launches {100 * f['between_launches']:.1f}%; loop {r['loop_ghz']:.2f} GHz, "
+              f"{100 * r['loop_mfma_busy']:.1f}% MFMA busy (ceiling loop {r['ceiling']['loop_ghz']:.2f} GHz, "
+              f"{100 * r['ceiling']['loop_mfma_busy']:.1f}%); per step (cycles) "
+              + ", ".join(f"{k}: {v['mfma_phase']:.0f}+{v['load_and_lds_wait']:.0f}+{v['barrier']:.0f}"
+                          for k, v in r["step_cycles"].items()),
+              file=sys.stderr, flush=True)
     ceil = {}
     if want("ceiling"):
         for zeros in (False, True):

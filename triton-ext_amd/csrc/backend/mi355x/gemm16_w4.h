@@ -32,6 +32,19 @@
 
 #include "gemm16_dma.h"
 
+// Phase stamps: empty in the library.  A measurement build defines them
+// before including this header (bench.py's libtx_ceilings.so) to time a
+// tile's phases per wave:
+//   TX_PHASE_STAMP(i): i = 0 at entry, 1 once step 0 has landed, 2 after the
+//     K loop, 3 after the epilogue's stores are issued, 4 after
+//     TX_PHASE_DRAIN() (their acknowledgement);
+//   TX_PHASE_STEP_BARRIER(kt, barrier): the barrier of main-loop step kt.
+#ifndef TX_PHASE_STAMP
+#define TX_PHASE_STAMP(i) ((void)0)
+#define TX_PHASE_DRAIN() ((void)0)
+#define TX_PHASE_STEP_BARRIER(kt, barrier) barrier()
+#endif
+
 namespace txk {
 
 typedef short i16x8_t __attribute__((ext_vector_type(8)));
@@ -321,6 +334,7 @@ template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
                                              uint8_t *smem) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WN, wn = wave % WN;
+    TX_PHASE_STAMP(0);
     f32x16_t acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -379,6 +393,7 @@ template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
     if (total > 0) {
       issue_range(0, 0, NDMA, std::true_type()); // masked form: K may end in step 0
       step_barrier();
+      TX_PHASE_STAMP(1);
       issue_range(1, 0, PER, std::true_type());
       Frags f0, f1;
       load_frags(stage_ptr(0), stage_ptr(0) + A_BYTES, 0, wm, wn, f0);
@@ -390,7 +405,7 @@ template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
         sub(f0, f1, as, 1, true, kt + 1, PARTS > 1 ? PER : -1, mask_k);
         sub(f1, f0, as, 2, true, kt + 1, PARTS > 2 ? 2 * PER : -1, mask_k);
         sub(f0, f1, as, 3, true, 0, -1, mask_k);
-        step_barrier();
+        TX_PHASE_STEP_BARRIER(kt, step_barrier);
         sub(f1, f0, an, 0, true, kt + 2, 0, mask_k);
       };
       int kt = 0;
@@ -427,8 +442,12 @@ template <int OP, int EPI, int NW = 4, bool BT = false> struct Gemm16W4 {
       // let them land before the workgroup can end.
       __builtin_amdgcn_s_waitcnt(0x7 << 4);
     }
+    TX_PHASE_STAMP(2);
 
     epilogue_lds<MASK_MN>(p, m0, n0, wm, wn, acc, lds0);
+    TX_PHASE_STAMP(3);
+    TX_PHASE_DRAIN();
+    TX_PHASE_STAMP(4);
   }
 
   // Epilogue of a tile through LDS (the two stages, 128 KiB, are free once

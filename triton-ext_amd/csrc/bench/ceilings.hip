@@ -14,11 +14,71 @@
 //     the ceiling the power-limited clock leaves for the dot's MFMA stream.
 //   * tx_ceiling_mfma_fp8: the same for the 8-bit 256x256x128 tile (8 waves
 //     of 8 x 4 blocks of v_mfma_f32_16x16x128_f8f6f4 per K step, e4m3).
+//   * tx_phases_bf16: the bf16 256x256 tile kernel itself, built here with
+//     its phase stamps on (s_memrealtime, a 100 MHz wall clock, and
+//     s_memtime, the shader clock, per wave at entry, step 0 landed, K loop
+//     done, epilogue issued, stores acknowledged; optionally around one
+//     step's barrier), so that bench.py can say where a launch's time goes.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 
 #include "tx_ceilings.h"
+
+// Stamp buffer and the step whose barrier is stamped (-1: none), set per
+// call of tx_phases_bf16.  A wave's 16 words: [0..4] wall clock at stamps
+// 0..4, [5] XCC_ID << 32 | HW_ID, [6] workgroup id, [7] shader clock after
+// the barrier of step g_phase_step - 1, [8..12] shader clock at stamps 0..4,
+// [13..15] shader clock before step g_phase_step's wait, after it, after
+// its barrier.
+// __constant__: loop-invariant to the compiler, so the step test in the K
+// loop is no reload after every barrier.
+__constant__ uint64_t *g_phase_buf;
+__constant__ int g_phase_step;
+
+#define TX_PHASE_WORDS(wave) (g_phase_buf + ((int64_t)blockIdx.x * 4 + (wave)) * 16)
+#define TX_PHASE_STAMP(i)                                                                      \
+  do {                                                                                         \
+    const uint64_t rt_ = __builtin_amdgcn_s_memrealtime();                                     \
+    const uint64_t mt_ = __builtin_amdgcn_s_memtime();                                         \
+    if ((threadIdx.x & 63) == 0) {                                                             \
+      uint64_t *w_ = TX_PHASE_WORDS(threadIdx.x >> 6);                                         \
+      w_[i] = rt_;                                                                             \
+      w_[8 + (i)] = mt_;                                                                       \
+      if ((i) == 0) {                                                                          \
+        uint32_t x_, h_;                                                                       \
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x_));                      \
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(h_));                       \
+        w_[5] = ((uint64_t)x_ << 32) | h_;                                                     \
+        w_[6] = blockIdx.x;                                                                    \
+      }                                                                                        \
+    }                                                                                          \
+  } while (0)
+#define TX_PHASE_DRAIN() __builtin_amdgcn_s_waitcnt(0x7 << 4) // vmcnt(0): stores acknowledged
+#define TX_PHASE_STEP_BARRIER(kt, barrier)                                                     \
+  do {                                                                                         \
+    if ((kt) == g_phase_step) {                                                                \
+      const uint64_t a_ = __builtin_amdgcn_s_memtime();                                        \
+      __builtin_amdgcn_s_waitcnt(0x7 << 4);                                                    \
+      const uint64_t b_ = __builtin_amdgcn_s_memtime();                                        \
+      __syncthreads();                                                                         \
+      const uint64_t c_ = __builtin_amdgcn_s_memtime();                                        \
+      if ((threadIdx.x & 63) == 0) {                                                           \
+        uint64_t *w_ = TX_PHASE_WORDS(threadIdx.x >> 6);                                       \
+        w_[13] = a_;                                                                           \
+        w_[14] = b_;                                                                           \
+        w_[15] = c_;                                                                           \
+      }                                                                                        \
+    } else {                                                                                   \
+      barrier();                                                                               \
+      if ((kt) + 1 == g_phase_step) {                                                          \
+        const uint64_t t_ = __builtin_amdgcn_s_memtime();                                      \
+        if ((threadIdx.x & 63) == 0)                                                           \
+          TX_PHASE_WORDS(threadIdx.x >> 6)[7] = t_;                                            \
+      }                                                                                        \
+    }                                                                                          \
+  } while (0)
+#include "backend/mi355x/gemm16_w4.h"
 
 namespace {
 
@@ -73,9 +133,12 @@ template <int S> __global__ void __launch_bounds__(256) read_lds_kernel(const ui
 
 // MFMA ceiling: 4 waves per workgroup, 16 accumulators of 32x32 per wave
 // (128x128), 4 sub-steps of 16 MFMAs per K step, operands from `seed`
-// (different per sub-step and wave) kept in registers.
+// (different per sub-step and wave) kept in registers.  STAMP: per wave,
+// the wall clock and the shader clock before and after the loop into st (a
+// separate instantiation: the stamps' registers would otherwise spill).
+template <bool STAMP>
 __global__ void __launch_bounds__(256, 1) mfma_bf16_kernel(const u32x4_t *seed, int ksteps,
-                                                           float *out) {
+                                                           float *out, uint64_t *st) {
   const int lane = threadIdx.x & 63;
   const u32x4_t *s = seed + ((blockIdx.x * 4 + (threadIdx.x >> 6)) % 64) * 64 * 32 + lane;
   u32x4_t a[4][4], b[4][4];
@@ -94,6 +157,12 @@ __global__ void __launch_bounds__(256, 1) mfma_bf16_kernel(const u32x4_t *seed, 
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         acc[i][j][r] = 0.f;
+  uint64_t r0 = 0, m0 = 0;
+  if constexpr (STAMP) {
+    __builtin_amdgcn_s_waitcnt(0);
+    r0 = __builtin_amdgcn_s_memrealtime();
+    m0 = __builtin_amdgcn_s_memtime();
+  }
   for (int kt = 0; kt < ksteps; ++kt) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
@@ -113,7 +182,26 @@ __global__ void __launch_bounds__(256, 1) mfma_bf16_kernel(const u32x4_t *seed, 
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         t += acc[i][j][r];
+  if constexpr (STAMP) {
+    const uint64_t r1 = __builtin_amdgcn_s_memrealtime(), m1 = __builtin_amdgcn_s_memtime();
+    if (lane == 0) {
+      uint64_t *w = st + ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;
+      w[0] = r0;
+      w[1] = r1;
+      w[2] = m0;
+      w[3] = m1;
+    }
+  }
   out[(size_t)blockIdx.x * 256 + threadIdx.x] = t;
+}
+
+// The bf16 256x256 tile with its phase stamps (the macros above).
+__global__ void __launch_bounds__(256, 1) phases_bf16_kernel(txk::GemmArgs p) {
+  typedef txk::Gemm16W4<txk::OP_BF16, txk::EPI_BF16, 4, false> G;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * (G::A_BYTES + G::B_BYTES)];
+  int tm, tn;
+  txk::tile_coords(p, tm, tn);
+  G::template run<false>(p, (int64_t)tm * G::BM, (int64_t)tn * G::BN, smem);
 }
 
 } // namespace
@@ -186,8 +274,57 @@ extern "C" int tx_ceiling_mfma_bf16(const void *seed, int tiles, int ksteps, flo
                                     void *stream) {
   if (!seed || !out || tiles <= 0 || ksteps < 0 || (reinterpret_cast<uintptr_t>(seed) & 15))
     return 1;
-  hipLaunchKernelGGL(mfma_bf16_kernel, dim3(tiles), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const u32x4_t *>(seed), ksteps, out);
+  hipLaunchKernelGGL(mfma_bf16_kernel<false>, dim3(tiles), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const u32x4_t *>(seed), ksteps,
+                     out, nullptr);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+extern "C" int tx_ceiling_mfma_bf16_stamped(const void *seed, int tiles, int ksteps, float *out,
+                                            uint64_t *stamps, void *stream) {
+  if (!seed || !out || !stamps || tiles <= 0 || ksteps < 0 ||
+      (reinterpret_cast<uintptr_t>(seed) & 15))
+    return 1;
+  hipLaunchKernelGGL(mfma_bf16_kernel<true>, dim3(tiles), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const u32x4_t *>(seed), ksteps,
+                     out, stamps);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+extern "C" int tx_phases_bf16_setup(uint64_t *stamps, int probe_step) {
+  if (!stamps)
+    return 1;
+  if (hipMemcpyToSymbol(HIP_SYMBOL(g_phase_buf), &stamps, sizeof(stamps)) != hipSuccess ||
+      hipMemcpyToSymbol(HIP_SYMBOL(g_phase_step), &probe_step, sizeof(probe_step)) != hipSuccess ||
+      hipDeviceSynchronize() != hipSuccess)
+    return 3;
+  return 0;
+}
+
+extern "C" int tx_phases_bf16(const void *A, const void *B, void *C, int tiles_m, int tiles_n,
+                              int ksteps, int group_m, int launches, void *stream) {
+  if (!A || !B || !C || tiles_m <= 0 || tiles_n <= 0 || ksteps < 2 || group_m <= 0 ||
+      launches <= 0 || (int64_t)tiles_m * tiles_n > 65536 || (int64_t)ksteps * 64 > 65536)
+    return 1;
+  txk::GemmArgs a{};
+  a.A = static_cast<const uint8_t *>(A);
+  a.B = static_cast<const uint8_t *>(B);
+  a.C = C;
+  a.M = (int64_t)tiles_m * 256;
+  a.N = (int64_t)tiles_n * 256;
+  a.K = (int64_t)ksteps * 64;
+  a.lda = a.K;
+  a.ldb = a.N;
+  a.ldc = a.N;
+  a.tiles_m = tiles_m;
+  a.tiles_n = tiles_n;
+  a.k_main_steps = ksteps;
+  a.k_masked_steps = 0;
+  a.last_ks = 4;
+  a.group_m = group_m < tiles_m ? group_m : tiles_m;
+  for (int i = 0; i < launches; ++i)
+    hipLaunchKernelGGL(phases_bf16_kernel, dim3(tiles_m * tiles_n), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), a);
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 

@@ -6,6 +6,7 @@
 #define TRITON_EXT_AMD_TX_CEILINGS_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -28,6 +29,35 @@ __attribute__((visibility("default"))) int tx_ceiling_read(const void *buf, size
 __attribute__((visibility("default"))) int tx_ceiling_mfma_bf16(const void *seed, int tiles,
                                                                 int ksteps, float *out,
                                                                 void *stream);
+
+/* tx_ceiling_mfma_bf16 with, per wave w, the wall clock (s_memrealtime,
+ * 100 MHz) and the shader clock (s_memtime) before and after its MFMA loop
+ * in stamps[4 w .. 4 w + 3]: r0, r1, m0, m1. */
+__attribute__((visibility("default"))) int tx_ceiling_mfma_bf16_stamped(const void *seed,
+                                                                        int tiles, int ksteps,
+                                                                        float *out,
+                                                                        uint64_t *stamps,
+                                                                        void *stream);
+
+/* Where the stamps of tx_phases_bf16 go: 16 words per wave (tiles_m *
+ * tiles_n * 4 waves), written by every launch, so the last one's remain:
+ * [0..4] the wall clock (s_memrealtime, 100 MHz) at entry, step 0 landed, K
+ * loop done, epilogue issued, stores acknowledged; [5] XCC_ID << 32 |
+ * HW_ID; [6] workgroup; [8..12] the shader clock (s_memtime) at the same
+ * five points; with probe_step s in [1, ksteps - 2]: [7] the shader clock
+ * after step s - 1's barrier, [13..15] before step s's wait for its loads,
+ * after it, after its barrier (probe_step -1: none).  Synchronous. */
+__attribute__((visibility("default"))) int tx_phases_bf16_setup(uint64_t *stamps,
+                                                                int probe_step);
+
+/* `launches` back-to-back launches of the bf16 256x256 tile kernel (the
+ * library's gemm16_w4_kernel, built here with its phase stamps) on
+ * C = A . B, all row-major and packed: M = 256 tiles_m, N = 256 tiles_n,
+ * K = 64 ksteps, tiles ordered in groups of group_m tile rows. */
+__attribute__((visibility("default"))) int tx_phases_bf16(const void *A, const void *B, void *C,
+                                                          int tiles_m, int tiles_n, int ksteps,
+                                                          int group_m, int launches,
+                                                          void *stream);
 
 /* `tiles` workgroups of 8 waves, each running `ksteps` x 32 MFMAs
  * v_mfma_f32_16x16x128_f8f6f4 (e4m3) per wave on operands read once from
