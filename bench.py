@@ -56,7 +56,9 @@ def parse():
                          "headline launch's time goes), tiles, c1, vendor, tail, "
                          "w8a8 (or "
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256; w8a8 also runs i32_16, the unscaled "
-                         "int8 -> int32 decode at M=16), int8, fp8, kmajor, mx (or mxfp8, mxfp4, "
+                         "int8 -> int32 decode at M=16), bf16_decode (or bf16_decode_1, _16, _64: "
+                         "bf16 at N = K = 8192 on the 16-bit decode kernel), int8, fp8, kmajor, "
+                         "mx (or mxfp8, mxfp4, "
                          "mxfp8_4096, mxfp8_8192, mxfp4_4096, mxfp4_8192), mxbf16 (or mxbf16_fp4, mxbf16_fp8: "
                          "bf16 x MX), attn (or attn_1024, attn_4096, "
                          "attn_16384; attn_fp8 or attn_fp8_<N> for e5m2; attn_d128 for head dim 128; "
@@ -294,6 +296,24 @@ def bench_decode_i32(tx, dev, M, N, K, steps, warmup, flush, seed=3):
     return dict(workload=f"int8 -> int32 (no scales) M={M} N={N} K={K}", ms=med, ms_isolated=iso,
                 gbps=nbytes / med / 1e6, frac_hbm=nbytes / med / 1e-3 / HBM,
                 tops=2.0 * M * N * K / med / 1e9,
+                plan=plan_info(tx, p, split_k=p.split_k, grid=p.grid_x))
+
+
+def bench_decode16(tx, dev, M, N, K, steps, warmup, flush, seed=3):
+    """bf16 x bf16 -> bf16 tt.dot of decode shape: the 16-bit decode kernel (B streamed
+    once), timed like the W8A8 lines (cold, B from HBM); algorithmic bytes A, B and C once."""
+    import torch
+    a, b = bf16_inputs(M, N, K, dev, seed)
+    c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    run = Launcher(tx, a, b, c)
+    iso, _ = time_cold(run, steps, warmup, flush)
+    med = time_cold_in_stream(run, flush)
+    warm = time_back_to_back(run, steps, warmup)
+    nbytes = 2 * (M * K + K * N + M * N)
+    p = run.plan
+    return dict(workload=f"bf16 decode M={M} N={N} K={K}", ms=med, ms_isolated=iso,
+                ms_warm_mall=warm, gbps=nbytes / med / 1e6, frac_hbm=nbytes / med / 1e-3 / HBM,
+                tflops=2.0 * M * N * K / med / 1e9,
                 plan=plan_info(tx, p, split_k=p.split_k, grid=p.grid_x))
 
 
@@ -816,6 +836,13 @@ def main():
         secondary.append(r)
         print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
               f"({100 * r['frac_hbm']:.1f}% HBM)", file=sys.stderr, flush=True)
+    for m in (1, 16, 64):
+        if want("bf16_decode") or want(f"bf16_decode_{m}"):
+            r = bench_decode16(tx, dev, m, 8192, 8192, max(args.steps, 20), 3, flush)
+            secondary.append(r)
+            print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
+                  f"({100 * r['frac_hbm']:.1f}% HBM); isolated launch "
+                  f"{r['ms_isolated'] * 1e3:.2f} us", file=sys.stderr, flush=True)
     if want("int8"):
         r = bench_int8(tx, dev, 4096, 4096, 4096, args.steps, args.warmup)
         secondary.append(r)

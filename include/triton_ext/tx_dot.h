@@ -117,6 +117,8 @@ typedef enum tx_kernel {
   TX_KERNEL_GEMM_MX = 5,    /* MX fp8 / fp4 tile, scaled MFMA 16x16x128 (e8m0)   */
   TX_KERNEL_GEMM_MX_BF16 = 6, /* MX x bf16: MX operand upcast to bf16 in the
                                * workspace, then the bf16 tile              */
+  TX_KERNEL_DECODE_16BIT = 7, /* bf16/fp16 decode shapes (M <= 64, no scales):
+                               * B streamed once, MFMA 16x16x32              */
 } tx_kernel;
 
 /* Bit flags for tx_dot_desc.flags */

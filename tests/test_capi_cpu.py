@@ -159,9 +159,9 @@ def test_plan_validation():
     assert _err(tx.make_desc(64, 64, 60, tx.BF16, tx.BF16, lda=60)) == tx.ERR_INVALID  # 120 B rows
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, lda=32)) == tx.ERR_INVALID  # short stride
     # K and N need not fill 16-byte chunks (masked per element); row strides must
-    p = tx.plan(tx.make_desc(64, 61, 68, tx.BF16, tx.BF16, lda=72, ldb=64, ldc=64))
+    p = tx.plan(tx.make_desc(128, 61, 68, tx.BF16, tx.BF16, lda=72, ldb=64, ldc=64))
     assert p.kernel == tx.KERNEL_GEMM_16BIT and p.k_tail == 68 % p.desc.block_k
-    assert _err(tx.make_desc(64, 61, 68, tx.BF16, tx.BF16, lda=72)) == tx.ERR_INVALID  # ldb 61
+    assert _err(tx.make_desc(128, 61, 68, tx.BF16, tx.BF16, lda=72)) == tx.ERR_INVALID  # ldb 61
     # an upcast MX B operand may have any N: its bf16 rows are N rounded up to 16 columns
     p = tx.plan(tx.make_desc(64, 72, 64, tx.BF16, tx.F32, b_type=tx.F8E4M3, ldb=80,
                              scale_mode=tx.SCALE_MX32))
@@ -170,7 +170,7 @@ def test_plan_validation():
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, b_type=tx.F16)) == tx.ERR_UNSUPPORTED
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, block=(96, 64, 64))) == tx.ERR_UNSUPPORTED
     assert _err(tx.make_desc(64, 64, 64, tx.F8E4M3, tx.BF16)) == tx.ERR_UNSUPPORTED  # fp8->bf16 needs scales
-    p = tx.plan(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16))
+    p = tx.plan(tx.make_desc(128, 64, 64, tx.BF16, tx.BF16))
     assert p.passes_run == 3 and p.kernel == tx.KERNEL_GEMM_16BIT
 
 
@@ -192,6 +192,12 @@ def test_plan_validation():
     (513, 8192, 8192, tx.I8, tx.I32, 0, tx.KERNEL_GEMM_I8),
     (4096, 4096, 4096, tx.I8, tx.I32, 0, tx.KERNEL_GEMM_I8),
     (2048, 7168, 7168, tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, tx.KERNEL_GEMM_F8),
+    # bf16 / fp16 of decode shape (M <= 64): the 16-bit decode kernel
+    (1, 8192, 8192, tx.BF16, tx.BF16, 0, tx.KERNEL_DECODE_16BIT),
+    (16, 8192, 8192, tx.BF16, tx.F32, 0, tx.KERNEL_DECODE_16BIT),
+    (64, 4096, 4096, tx.F16, tx.F16, 0, tx.KERNEL_DECODE_16BIT),
+    (33, 28672, 8192, tx.F16, tx.F32, 0, tx.KERNEL_DECODE_16BIT),
+    (65, 8192, 8192, tx.BF16, tx.BF16, 0, tx.KERNEL_GEMM_16BIT),
 ])
 def test_kernel_choice(M, N, K, a, c, sm, kernel):
     p = tx.plan(tx.make_desc(M, N, K, a, c, scale_mode=sm))
@@ -212,7 +218,46 @@ def test_kernel_choice(M, N, K, a, c, sm, kernel):
         rows = M if M <= 48 else slices * bm
         cols = -(-N // 4) * 4 if M <= 48 else -(-N // 128) * 128
         assert p.workspace_bytes == (65536 + p.split_k * rows * cols * 4 if p.split_k > 1 else 0)
+    if kernel == tx.KERNEL_DECODE_16BIT:
+        # the slice of 16 ceil(M / 16) rows x 64-column strips x 128-row K batches;
+        # strips x splits cover the 256 CUs (no split once the strips alone do)
+        sr = 16 * -(-M // 16)
+        assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (sr, 64, 128)
+        strips = -(-N // 64)
+        assert p.grid_x == strips * p.split_k and p.block_threads == 256
+        assert p.split_k == 1 if strips >= 256 else strips * p.split_k >= 256
+        # the 64 KiB counter region, then fp32 partials: [split][strip][sr x 64]
+        assert p.workspace_bytes == (65536 + p.split_k * strips * sr * 64 * 4
+                                     if p.split_k > 1 else 0)
     assert (p.split_k & (p.split_k - 1)) == 0
+
+
+def test_decode16_plans():
+    """The 16-bit decode kernel: which descriptors take it, its explicit block, split-K."""
+    D16 = tx.KERNEL_DECODE_16BIT
+    # K-major B, mixed operand types, scales, int32 C: not this kernel
+    assert tx.plan(tx.make_desc(16, 4096, 4096, tx.BF16, tx.BF16,
+                                flags=tx.FLAG_B_KMAJOR)).kernel == tx.KERNEL_GEMM_16BIT
+    assert _err(tx.make_desc(16, 4096, 4096, tx.BF16, tx.F16)) == tx.ERR_UNSUPPORTED
+    # an explicit GEMM tile at decode shape runs that tile; the decode block at M > 64 is refused
+    assert tx.plan(tx.make_desc(16, 4096, 4096, tx.BF16, tx.BF16,
+                                block=(64, 64, 32))).kernel == tx.KERNEL_GEMM_16BIT
+    assert tx.plan(tx.make_desc(16, 4096, 4096, tx.BF16, tx.BF16,
+                                block=(16, 64, 128))).kernel == D16
+    assert _err(tx.make_desc(80, 4096, 4096, tx.BF16, tx.BF16,
+                             block=(80, 64, 128))) == tx.ERR_UNSUPPORTED
+    # tl.dot(a, b, acc) with an fp32 acc
+    p = tx.plan(tx.make_desc(8, 1000, 3000, tx.BF16, tx.F32, flags=tx.FLAG_ACCUMULATE))
+    assert p.kernel == D16 and p.split_k == 4 and p.grid_x == 16 * 4
+    # K = 0 and a K that fills no whole batch: one split
+    for K in (0, 100):
+        p = tx.plan(tx.make_desc(4, 4096, K, tx.F16, tx.F16, lda=-(-K // 8) * 8))
+        assert p.kernel == D16 and p.split_k == 1 and p.workspace_bytes == 0
+    # split-K: every split owns at least 4 batches of 128 K rows
+    p = tx.plan(tx.make_desc(16, 1024, 8192, tx.BF16, tx.BF16))
+    assert p.split_k == 16 and p.grid_x == 256
+    p = tx.plan(tx.make_desc(16, 1024, 2048, tx.BF16, tx.BF16))
+    assert p.split_k == 4
 
 
 def test_b_kmajor_plans():

@@ -1,0 +1,170 @@
+"""The 16-bit decode kernel (decode16.h) against the oracle.
+
+bf16 / fp16 dots with M <= 64 stream B once on the decode kernel: 64-column
+strips, 128-row K batches, split-K with the fp32 partials summed in split
+order.  Parity is the north_star's fp bar: |d| <= 1e-3 + 1e-2 |ref| for inputs
+N(0,1)/sqrt(K), against the oracle at the plan's block; fp32 C is also held to
+the exact (float64) product within fp32 summation error.  Sums of fp32
+partials depend on order, so the kernel fixes it: two launches give the same
+bits.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import triton_ext_amd as tx
+from dotcase import bits_to_f32, check_close, from_device, k_norm, normal_bf16, normal_f16, say, \
+    to_device
+from test_dot_gpu import ATOL, RTOL, oracle_16bit
+
+pytestmark = pytest.mark.gpu
+
+TORCH_DT = {"bf16": "bfloat16", "f16": "float16", "f32": "float32"}
+
+
+def operands(M, N, K, kind, seed):
+    gen = normal_bf16 if kind == "bf16" else normal_f16
+    return gen((M, K), k_norm(K), 10 + seed), gen((K, N), k_norm(K), 20 + seed)
+
+
+def run(gpu, a, b, kind, out_kind, acc=None):
+    import torch
+    tdt = getattr(torch, TORCH_DT[kind])
+    da, db = to_device(a, gpu).view(tdt), to_device(b, gpu).view(tdt)
+    c = tx.dot(da, db, out_dtype=getattr(torch, TORCH_DT[out_kind]),
+               acc=None if acc is None else to_device(acc, gpu))
+    torch.cuda.synchronize()
+    return from_device(c)
+
+
+def as_f32(x, kind):
+    return x if kind == "f32" else bits_to_f32(x, kind)
+
+
+def plan_of(M, N, K, kind, out_kind, flags=0):
+    t = tx.BF16 if kind == "bf16" else tx.F16
+    c = {"bf16": tx.BF16, "f16": tx.F16, "f32": tx.F32}[out_kind]
+    up = lambda x: -(-x // 8) * 8
+    return tx.plan(tx.make_desc(M, N, K, t, c, lda=up(K), ldb=up(N), ldc=up(N), flags=flags))
+
+
+def exact(a, b, kind):
+    f = oracle.bf16_to_f32 if kind == "bf16" else oracle.f16_to_f32
+    return f(a).astype(np.float64) @ f(b).astype(np.float64)
+
+
+@pytest.mark.parametrize("M,N,K,kind,out_kind", [
+    (1, 8192, 8192, "bf16", "bf16"), (16, 8192, 8192, "bf16", "f32"),
+    (64, 4096, 4096, "f16", "f16"), (48, 2048, 8192, "bf16", "bf16"),
+    (16, 28672, 1024, "bf16", "bf16"),
+    # ragged: K and N that fill no 16-byte chunk, slices of 16 .. 64 rows, one split
+    (33, 4100, 2050, "bf16", "bf16"), (7, 1000, 3000, "f16", "f32"), (3, 24, 64, "bf16", "f32"),
+    (64, 61, 300, "f16", "f16"), (17, 130, 129, "bf16", "f32"), (50, 520, 127, "f16", "f32"),
+])
+def test_decode16_vs_oracle(gpu, M, N, K, kind, out_kind):
+    say(f"decode16 {kind}->{out_kind} M={M} N={N} K={K}")
+    p = plan_of(M, N, K, kind, out_kind)
+    assert p.kernel == tx.KERNEL_DECODE_16BIT
+    a, b = operands(M, N, K, kind, M + K)
+    got = as_f32(run(gpu, a, b, kind, out_kind), out_kind)
+    ref = as_f32(oracle_16bit(a, b, kind, out_kind, (p.desc.block_m, p.desc.block_n,
+                                                       p.desc.block_k)), out_kind)
+    err = check_close(got, ref, atol=ATOL, rtol=RTOL, what=f"decode16 {M}x{N}x{K}")
+    if out_kind == "f32":  # fp32 summation error only: K products of |x| <~ 4/sqrt(K) each
+        assert np.abs(got - exact(a, b, kind)).max() < 1e-5
+    say(f"decode16 {M}x{N}x{K} split {p.split_k}: max|d|={err:.3g}")
+
+
+def test_decode16_k_zero(gpu):
+    """K = 0: C = 0 (no batch is loaded)."""
+    import torch
+    for kind, out_kind in (("bf16", "bf16"), ("f16", "f32")):
+        tdt = getattr(torch, TORCH_DT[kind])
+        a = torch.empty((5, 0), dtype=tdt, device=gpu)
+        b = torch.empty((0, 304), dtype=tdt, device=gpu)
+        c = tx.dot(a, b, out_dtype=getattr(torch, TORCH_DT[out_kind]))
+        torch.cuda.synchronize()
+        assert not from_device(c).any()
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 8192, 8192), (5, 777, 1000)])
+def test_decode16_accumulate(gpu, M, N, K):
+    """tl.dot(a, b, acc) with an fp32 acc: C = acc + A @ B."""
+    say(f"decode16 acc M={M} N={N} K={K}")
+    assert plan_of(M, N, K, "bf16", "f32", tx.FLAG_ACCUMULATE).kernel == tx.KERNEL_DECODE_16BIT
+    a, b = operands(M, N, K, "bf16", 3)
+    acc = np.random.default_rng(4).standard_normal((M, N)).astype(np.float32)
+    got = run(gpu, a, b, "bf16", "f32", acc=acc)
+    ref = exact(a, b, "bf16") + acc
+    assert np.abs(got - ref).max() < 1e-5
+
+
+def test_decode16_inf_nan_padding(gpu):
+    """Operands in storage whose row padding (past K in A, past N in B) and extra rows of
+    B hold Inf and NaN: the chunks that cross K or N are loaded whole, and the
+    elements past K must be zeroed (Inf * 0 = NaN) while those past N are never stored."""
+    import torch
+    M, N, K = 20, 1001, 1003
+    say(f"decode16 Inf/NaN padding M={M} N={N} K={K}")
+    a, b = operands(M, N, K, "bf16", 7)
+    inf_bits, nan_bits = 0x7F80, 0x7FC0
+    A = np.full((M, K + 13), inf_bits, dtype=np.uint16)
+    A[:, K + 1::2] = nan_bits
+    A[:, :K] = a
+    B = np.full((K + 3, N + 7), nan_bits, dtype=np.uint16)
+    B[:K, :N] = b
+    da = to_device(A, gpu).view(torch.bfloat16)
+    db = to_device(B, gpu).view(torch.bfloat16)
+    c = tx.dot(da[:, :K], db[:K, :N], out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    got = from_device(c)
+    assert np.isfinite(got).all()
+    assert np.abs(got - exact(a, b, "bf16")).max() < 1e-5
+
+
+def test_decode16_deterministic(gpu):
+    """Split-K partials are summed in split order: the same bits on every launch."""
+    import torch
+    M, N, K = 16, 1024, 8192
+    p = plan_of(M, N, K, "bf16", "f32")
+    assert p.split_k == 16
+    a, b = operands(M, N, K, "bf16", 9)
+    da, db = to_device(a, gpu).view(torch.bfloat16), to_device(b, gpu).view(torch.bfloat16)
+    outs = []
+    for _ in range(4):
+        c = tx.dot(da, db, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        outs.append(from_device(c))
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+
+
+def test_decode16_after_w8a8_on_one_workspace(gpu):
+    """The decode kernels share the workspace's counter region (every launch leaves its
+    counters at zero): W8A8 split-K, then decode16 split-K, twice, on one buffer through
+    tx_dot_launch."""
+    import torch
+    from test_workspace_gpu import _launch, _w8a8_case
+    stream = torch.cuda.current_stream().cuda_stream
+    M, N, K = 16, 4096, 4096
+    pd = tx.plan(tx.make_desc(M, N, K, tx.I8, tx.BF16, scale_mode=tx.SCALE_ROWCOL))
+    p16 = tx.plan(tx.make_desc(M, N, K, tx.BF16, tx.F32))
+    assert pd.kernel == tx.KERNEL_DECODE_I8 and p16.kernel == tx.KERNEL_DECODE_16BIT
+    assert pd.split_k > 1 and p16.split_k > 1
+    ws = torch.zeros(max(int(pd.workspace_bytes), int(p16.workspace_bytes)), dtype=torch.uint8,
+                     device=gpu)
+    a8, b8, sa, sb, want8 = _w8a8_case(M, N, K, 81)
+    d8 = [to_device(x, gpu) for x in (a8, b8, sa, sb)]
+    a, b = operands(M, N, K, "bf16", 5)
+    da, db = to_device(a, gpu).view(torch.bfloat16), to_device(b, gpu).view(torch.bfloat16)
+    want16 = exact(a, b, "bf16")
+    for rep in range(2):
+        say(f"shared workspace: W8A8 then decode16 {M}x{N}x{K} (rep {rep})")
+        c8 = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
+        _launch(pd, d8[0], d8[1], c8, d8[2], d8[3], ws, stream)
+        c16 = torch.full((M, N), float("nan"), dtype=torch.float32, device=gpu)
+        _launch(p16, da, db, c16, None, None, ws, stream)
+        torch.cuda.synchronize()
+        assert np.array_equal(from_device(c8), want8)
+        assert np.abs(from_device(c16) - want16).max() < 1e-5
+    assert not from_device(ws[:65536]).any()  # every arrival counter back at zero

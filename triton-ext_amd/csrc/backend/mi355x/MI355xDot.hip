@@ -26,6 +26,7 @@
 #include "attn_fwd8.h"
 #include "mx_upcast.h"
 
+#include "decode16.h"
 #include "decode_i8.h"
 #include "decode_rows_i8.h"
 #include "gemm16_dma.h"
@@ -188,6 +189,13 @@ const DecodeKernelFn kDecodeKernels[4] = {decode_i8_kernel<1>, decode_i8_kernel<
 const DecodeKernelFn kDecodeRowsKernels[3] = {decode_rows_i8_kernel<64, 6>,
                                               decode_rows_i8_kernel<128, 4>,
                                               decode_rows_i8_kernel<256, 3>};
+// The 16-bit decode kernel by [fp16 / bf16][slice of 16, 32, 48, 64 rows].
+typedef void (*Decode16KernelFn)(Decode16Args);
+const Decode16KernelFn kDecode16Kernels[2][4] = {
+    {decode16_kernel<16, false>, decode16_kernel<32, false>, decode16_kernel<48, false>,
+     decode16_kernel<64, false>},
+    {decode16_kernel<16, true>, decode16_kernel<32, true>, decode16_kernel<48, true>,
+     decode16_kernel<64, true>}};
 
 // MFMA format code of an MX operand type (-1 if it has none).
 int mxFormat(int32_t t) {
@@ -386,6 +394,44 @@ int64_t decodeWorkspace(const tx_dot_desc &d, int ksplit) {
   return decodeCounterBytes(d) + (int64_t)ksplit * d.M * ((d.N + 3) & ~3) * 4;
 }
 
+// The 16-bit decode kernel (decode16.h): both operands bf16 or both fp16,
+// no scales, C in their type or fp32 (accumulating only into fp32, which
+// validate() enforces), B row-major, M <= 64 (one slice), one arrival
+// counter of the fixed region per 64-column strip.
+int decode16Rows(const tx_dot_desc &d) { return (int)(16 * cdiv(d.M > 0 ? d.M : 1, 16)); }
+bool useDecode16(const tx_dot_desc &d) {
+  return (d.a_type == TX_BF16 || d.a_type == TX_F16) && d.b_type == d.a_type &&
+         d.scale_mode == TX_SCALE_NONE && (d.c_type == d.a_type || d.c_type == TX_F32) &&
+         !(d.flags & TX_FLAG_B_KMAJOR) && d.M <= kDec16MaxM &&
+         cdiv(d.N, kDec16StripN) <= kDec16MaxStrips;
+}
+// Its tile as the arith_intensity pass names it: the slice (16 ceil(M / 16)
+// rows) x a 64-column strip x 128-row K batches.  (No 16-bit GEMM tile has
+// block_k 128.)
+bool decode16Tile(const tx_dot_desc &d) {
+  return d.block_m == decode16Rows(d) && d.block_n == kDec16StripN &&
+         d.block_k == kDec16BatchK;
+}
+// Split-K factor: a power of two (<= kMaxSplit) so that strips x splits
+// workgroups cover the CUs about once, each split with at least 4 batches
+// of 128 K rows, and every split owning one batch at least.
+int decode16Split(const tx_dot_desc &d) {
+  const int64_t strips = cdiv(d.N, kDec16StripN);
+  const int64_t batches = cdiv(d.K, kDec16BatchK);
+  int ks = 1;
+  while (ks < (int)kMaxSplit && strips * ks < 256 && batches / (ks * 2) >= 4)
+    ks *= 2;
+  while (ks > 1 && cdiv(batches, ks) * (ks - 1) >= batches)
+    ks >>= 1;
+  return ks;
+}
+int64_t decode16Workspace(const tx_dot_desc &d, int ksplit) {
+  if (ksplit <= 1)
+    return 0;
+  return kDecodeCounterBytes +
+         ksplit * decode16_split_bytes(cdiv(d.N, kDec16StripN), decode16Rows(d));
+}
+
 // The 32-bit-offset tiles (gemm16_w4.h, gemm8_w4.h, gemm8_n224.h) address A,
 // B and the block scales through buffer offsets: each must span less than
 // 2^31 bytes (out-of-range chunks, at offset 2^31, read zeros).
@@ -430,6 +476,17 @@ int txMi355xDotRun(tx_dot_plan *plan) {
     return fail(TX_ERR_UNSUPPORTED,
                 "no kernel for a_type=%d b_type=%d c_type=%d scale_mode=%d",
                 d.a_type, d.b_type, d.c_type, d.scale_mode);
+  if (useDecode16(d) && decode16Tile(d)) {
+    const int ks = decode16Split(d);
+    plan->kernel = TX_KERNEL_DECODE_16BIT;
+    plan->split_k = ks;
+    plan->grid_x = (int32_t)(cdiv(d.N, kDec16StripN) * ks);
+    plan->grid_y = plan->grid_z = 1;
+    plan->block_threads = kDecodeWaves * 64;
+    plan->workspace_bytes = decode16Workspace(d, ks);
+    plan->passes_run += 1;
+    return TX_OK;
+  }
   if (useDecode(d) && decodeTile(d)) {
     const int ks = decodeSplit(d);
     plan->kernel = TX_KERNEL_DECODE_I8;
@@ -557,6 +614,7 @@ extern "C" TX_API const char *tx_kernel_name(int32_t kernel) {
   case TX_KERNEL_GEMM_F8: return "gemm_f8_mfma16x16x128|32x32x64_f8f6f4";
   case TX_KERNEL_GEMM_MX: return "gemm_mx_mfma_scale16x16x128";
   case TX_KERNEL_GEMM_MX_BF16: return "mx_upcast_bf16+gemm_16bit_mfma32x32x16";
+  case TX_KERNEL_DECODE_16BIT: return "decode_16bit_mfma16x16x32";
   default: return "?";
   }
 }
@@ -800,6 +858,39 @@ int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   return TX_OK;
 }
 
+int launchDecode16(const tx_dot_plan &plan, const void *A, const void *B, void *C, void *ws,
+                   size_t ws_bytes, hipStream_t stream) {
+  const tx_dot_desc &d = plan.desc;
+  const int ks = plan.split_k;
+  const int64_t need = decode16Workspace(d, ks);
+  if (need > 0 && (!ws || (int64_t)ws_bytes < need))
+    return fail(TX_ERR_WORKSPACE, "decode needs %lld workspace bytes, got %zu",
+                (long long)need, ws_bytes);
+  Decode16Args a;
+  a.A = static_cast<const uint16_t *>(A);
+  a.B = static_cast<const uint16_t *>(B);
+  a.C = C;
+  a.c_f32 = d.c_type == TX_F32;
+  a.acc_c = (d.flags & TX_FLAG_ACCUMULATE) != 0;
+  a.M = (int32_t)d.M;
+  a.N = (int32_t)d.N;
+  a.K = (int32_t)d.K;
+  a.lda = d.lda;
+  a.ldb = d.ldb;
+  a.ldc = d.ldc;
+  a.ksplit = ks;
+  a.batches_per_split = (int32_t)cdiv(cdiv(d.K, kDec16BatchK), ks);
+  a.k_main_batches = (int32_t)(plan.k_split / kDec16BatchK);
+  a.counters = static_cast<uint32_t *>(ws);
+  a.partials = need > 0 ? reinterpret_cast<float *>(static_cast<uint8_t *>(ws) +
+                                                    kDecodeCounterBytes)
+                        : nullptr;
+  const Decode16KernelFn fn = kDecode16Kernels[d.a_type == TX_BF16][decode16Rows(d) / 16 - 1];
+  hipLaunchKernelGGL(fn, dim3(plan.grid_x), dim3(plan.block_threads), 0, stream, a);
+  TX_HIP_CHECK(hipGetLastError());
+  return TX_OK;
+}
+
 } // namespace
 
 // Scratch of tx_dot_launch_noalloc: one array per GPU (each device holds its
@@ -868,6 +959,14 @@ int checkPlan(const tx_dot_plan &p) {
   classify(d, &op, &epi);
   if (op < 0 || epi < 0)
     return fail(TX_ERR_UNSUPPORTED, "no kernel for the plan's operand types");
+  if (p.kernel == TX_KERNEL_DECODE_16BIT) {
+    const int sk = p.split_k;
+    if (!useDecode16(d) || !decode16Tile(d) || sk < 1 || sk > (int)kMaxSplit ||
+        (sk & (sk - 1)) || p.grid_x != cdiv(d.N, kDec16StripN) * sk ||
+        p.block_threads != kDecodeWaves * 64 || p.workspace_bytes != decode16Workspace(d, sk))
+      return fail(TX_ERR_INVALID, "the plan's decode launch does not follow from its descriptor");
+    return TX_OK;
+  }
   if (p.kernel == TX_KERNEL_DECODE_I8) {
     const int sk = p.split_k;
     if (!useDecode(d) || !decodeTile(d) || sk < 1 || sk > (int)kMaxSplit ||
@@ -943,6 +1042,8 @@ int launchPlanned(const tx_dot_plan *plan, const void *A, const void *B, void *C
   case TX_KERNEL_DECODE_I8:
     return launchDecode(*plan, A, B, C, scale_a, scale_b, workspace,
                         workspace_bytes, s);
+  case TX_KERNEL_DECODE_16BIT:
+    return launchDecode16(*plan, A, B, C, workspace, workspace_bytes, s);
   case TX_KERNEL_GEMM_MX_BF16:
     return launchMxUpcast(*plan, A, B, C, scale_a, scale_b, workspace, workspace_bytes, s);
   default:

@@ -1,0 +1,413 @@
+// bf16 / fp16 small-M dot (decode shape) for gfx950:
+//   C[m][n] = sum_k A[m][k] * B[k][n]
+// with A [M,K] (M <= 64) and B [K,N] row-major, both bf16 or both fp16,
+// fp32 accumulation, and C in the operands' type (rounded to nearest even)
+// or in fp32 (C = sum, or C += sum for tl.dot's acc).
+//
+// A dot with a few rows of A reads all of B once and does 2 M FLOPs per
+// element of B, so it is HBM-bound; the GEMM tiles would leave most of a
+// 64-row tile empty and cover N with a handful of workgroups.  Here a
+// workgroup owns a strip of 64 columns (128-byte rows of B), the slice of
+// SR = 16 ceil(M / 16) rows and a range of K (split-K), so strips x splits
+// workgroups stream B once between them:
+//  * B's batches of 128 K rows (16 KiB) go through one LDS ring shared by the
+//    4 waves: each wave issues 4 of a batch's 16 direct-to-LDS loads
+//    (non-temporal: each byte is read once), waits for its own loads
+//    (s_waitcnt vmcnt) and one s_barrier per batch makes the whole batch
+//    visible.  The same barrier tells every wave that the slot read one batch
+//    earlier is free; the batch S - 1 ahead is loaded into it.
+//  * A's rows of the batch (SR x 256 bytes) go into the same slot, a quarter
+//    loaded by each wave, each load 4 whole rows; 16-byte chunk c of row r
+//    sits at c ^ (r & 15), so the 16 rows one quarter-wave reads with
+//    ds_read_b128 fall in 16 bank groups.
+//  * B rows are N-contiguous and the MFMA wants K-contiguous elements per
+//    column: ds_read_b64_tr_b16 transposes on the LDS read (within a 16-lane
+//    group, lane L reads row L / 4, columns 4 (L % 4) .. +3 of a 16-column
+//    block; lane i receives column i's 4 K-consecutive elements).  B's
+//    16-byte chunk c of row r sits at c ^ (r & 7).
+//  * Wave w owns columns 16 w .. 16 w + 15 of the strip for every row of the
+//    slice, so every wave has MFMA work at any M:
+//    v_mfma_f32_16x16x32_{bf16,f16} with the roles swapped (MFMA A := B
+//    columns, MFMA B := A rows), so lane l holds row 16 t + l % 16 at the 4
+//    consecutive columns 16 w + 4 (l / 16) .. +3.  No cross-wave reduction:
+//    the waves own disjoint outputs.
+//  * Split-K: decode_i8.h's exchange (SC1 stores of the fp32 partial, an
+//    arrival counter per strip that the last arrival resets; the last
+//    arrival gathers).  Partials are kept in lane order, 1 KiB per (wave,
+//    row tile).  fp32 addition depends on order, so the last arrival adds
+//    the splits' partials in split order 0, 1, .. (its own from registers at
+//    its place): the result does not depend on which split arrives last.
+//
+// K loop in LoopSplit form: batches below k_main_batches load unmasked; the
+// rest send B rows >= K, B chunks at or past N and A rows >= M to the
+// zero-filled chunk.  An A chunk that crosses K is loaded whole and its
+// elements past K are zeroed in registers (they would meet B's zero rows,
+// but a row's padding may hold Inf or NaN, and Inf * 0 is NaN).
+#pragma once
+
+#include <type_traits>
+
+#include "decode_i8.h"
+
+namespace txk {
+
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+constexpr int kDec16StripN = 64;                                   // columns: 128-byte rows
+constexpr int kDec16BatchK = 128;                                  // K rows a batch
+constexpr int kDec16MaxM = 64;                                     // one slice of 64 rows
+constexpr int64_t kDec16MaxStrips = kDecodeCounterBytes / 4;       // one counter per strip
+
+struct Decode16Args {
+  const uint16_t *A;
+  const uint16_t *B;
+  void *C;
+  int32_t c_f32; // C is fp32 (else the operands' 16-bit type)
+  int32_t acc_c; // fp32 C: add the sums to C's contents (tl.dot's acc)
+  int32_t M, N, K;
+  int64_t lda, ldb, ldc; // row strides in elements
+  int32_t ksplit;
+  int32_t batches_per_split;
+  int32_t k_main_batches; // batches with every K row < K (unmasked)
+  float *partials;        // [ksplit][strips][4 waves][SR / 16][64 lanes][4] fp32
+  uint32_t *counters;     // [strips] arrival counters
+};
+
+// Bytes of one split's partials: every strip's SR x 64 fp32 sums.
+__host__ __device__ constexpr int64_t decode16_split_bytes(int64_t strips, int sr) {
+  return strips * sr * kDec16StripN * 4;
+}
+
+template <int SR> struct Decode16Cfg {
+  static constexpr int T = SR / 16;                         // 16-row tiles
+  static constexpr int A_OFF = kDec16BatchK * 128;          // B's 16 KiB first
+  static constexpr int SLOT = A_OFF + SR * kDec16BatchK * 2; // then SR rows of 256 bytes
+  static constexpr int S = 158 * 1024 / SLOT > 8 ? 8 : 158 * 1024 / SLOT;
+  static constexpr int B_LOADS = A_OFF / 1024 / kDecodeWaves;                  // 4
+  static constexpr int A_LOADS = SR * kDec16BatchK * 2 / 1024 / kDecodeWaves; // SR / 16
+  static constexpr int VPB = B_LOADS + A_LOADS;
+  static_assert(SR == 16 || SR == 32 || SR == 48 || SR == 64, "slices of 16 .. 64 rows");
+  static_assert(S >= 3 && (S - 2) * VPB <= 63, "ring depth; vmcnt is 6 bits");
+};
+
+// Operands of two K steps (32 rows each, KS and KS + 1) of a batch: the
+// wave's B fragments (two transposed reads a step, at `blo` / `bhi` and
+// +4 KiB for the second step) and its T A fragments (ds_read_b128 at `a0` /
+// `a1`, +4 KiB per 16-row tile), waiting for them before the block ends.
+#define TX_D16_TR                                                                           \
+  "ds_read_b64_tr_b16 %0, %[blo]\n\tds_read_b64_tr_b16 %1, %[bhi]\n\t"                      \
+  "ds_read_b64_tr_b16 %2, %[blo] offset:4096\n\tds_read_b64_tr_b16 %3, %[bhi] offset:4096\n\t"
+#define TX_D16_OUT "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1])
+#define TX_D16_IN [blo] "v"(blo), [bhi] "v"(bhi), [a0] "v"(a0), [a1] "v"(a1)
+template <int T>
+__device__ __forceinline__ void dec16_read_pair(uint32_t blo, uint32_t bhi, uint32_t a0,
+                                                uint32_t a1, v2i_t (&lo)[2], v2i_t (&hi)[2],
+                                                i32x4_t (&a)[2][T]) {
+  if constexpr (T == 1)
+    asm volatile(TX_D16_TR "ds_read_b128 %4, %[a0]\n\tds_read_b128 %5, %[a1]\n\t"
+                           "s_waitcnt lgkmcnt(0)"
+                 : TX_D16_OUT, "=v"(a[0][0]), "=v"(a[1][0])
+                 : TX_D16_IN
+                 : "memory");
+  else if constexpr (T == 2)
+    asm volatile(TX_D16_TR "ds_read_b128 %4, %[a0]\n\tds_read_b128 %5, %[a0] offset:4096\n\t"
+                           "ds_read_b128 %6, %[a1]\n\tds_read_b128 %7, %[a1] offset:4096\n\t"
+                           "s_waitcnt lgkmcnt(0)"
+                 : TX_D16_OUT, "=v"(a[0][0]), "=v"(a[0][1]), "=v"(a[1][0]), "=v"(a[1][1])
+                 : TX_D16_IN
+                 : "memory");
+  else if constexpr (T == 3)
+    asm volatile(TX_D16_TR "ds_read_b128 %4, %[a0]\n\tds_read_b128 %5, %[a0] offset:4096\n\t"
+                           "ds_read_b128 %6, %[a0] offset:8192\n\t"
+                           "ds_read_b128 %7, %[a1]\n\tds_read_b128 %8, %[a1] offset:4096\n\t"
+                           "ds_read_b128 %9, %[a1] offset:8192\n\t"
+                           "s_waitcnt lgkmcnt(0)"
+                 : TX_D16_OUT, "=v"(a[0][0]), "=v"(a[0][1]), "=v"(a[0][2]), "=v"(a[1][0]),
+                   "=v"(a[1][1]), "=v"(a[1][2])
+                 : TX_D16_IN
+                 : "memory");
+  else
+    asm volatile(TX_D16_TR "ds_read_b128 %4, %[a0]\n\tds_read_b128 %5, %[a0] offset:4096\n\t"
+                           "ds_read_b128 %6, %[a0] offset:8192\n\t"
+                           "ds_read_b128 %7, %[a0] offset:12288\n\t"
+                           "ds_read_b128 %8, %[a1]\n\tds_read_b128 %9, %[a1] offset:4096\n\t"
+                           "ds_read_b128 %10, %[a1] offset:8192\n\t"
+                           "ds_read_b128 %11, %[a1] offset:12288\n\t"
+                           "s_waitcnt lgkmcnt(0)"
+                 : TX_D16_OUT, "=v"(a[0][0]), "=v"(a[0][1]), "=v"(a[0][2]), "=v"(a[0][3]),
+                   "=v"(a[1][0]), "=v"(a[1][1]), "=v"(a[1][2]), "=v"(a[1][3])
+                 : TX_D16_IN
+                 : "memory");
+}
+#undef TX_D16_IN
+#undef TX_D16_OUT
+#undef TX_D16_TR
+
+template <bool BF>
+__device__ __forceinline__ f32x4_t mfma16x16x32(const i32x4_t &a, const i32x4_t &b,
+                                                const f32x4_t &c) {
+  if constexpr (BF) {
+    typedef __bf16 v8_t __attribute__((ext_vector_type(8)));
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8_t, a),
+                                                   __builtin_bit_cast(v8_t, b), c, 0, 0, 0);
+  } else {
+    typedef _Float16 v8_t __attribute__((ext_vector_type(8)));
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8_t, a),
+                                                  __builtin_bit_cast(v8_t, b), c, 0, 0, 0);
+  }
+}
+
+// Zero the 16-bit elements of a fragment at K index `k` .. k + 7 that lie at
+// or past K (the chunk that crosses K, in the tail batch).
+__device__ __forceinline__ i32x4_t dec16_mask_k(const i32x4_t &v, int64_t k, int64_t K) {
+  const int w[4] = {v[0], v[1], v[2], v[3]};
+  int o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = k + 2 * i < K ? 0xffffu : 0u;
+    const uint32_t hi = k + 2 * i + 1 < K ? 0xffff0000u : 0u;
+    o[i] = (int)((uint32_t)w[i] & (lo | hi));
+  }
+  return i32x4_t{o[0], o[1], o[2], o[3]};
+}
+
+template <int SR, bool BF>
+__global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode16_kernel(Decode16Args p) {
+  typedef Decode16Cfg<SR> Cfg;
+  constexpr int S = Cfg::S, SLOT = Cfg::SLOT, T = Cfg::T;
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[S * SLOT];
+  __shared__ uint32_t last_flag;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = lane >> 4, L = lane & 15;
+  // Workgroup -> (strip, split): consecutive workgroups are adjacent strips
+  // of one split, so the workgroups running at once read whole stretches of
+  // B's rows.
+  const int strips = (p.N + kDec16StripN - 1) / kDec16StripN;
+  const int strip = blockIdx.x % strips, split = blockIdx.x / strips;
+  const int64_t n0 = (int64_t)strip * kDec16StripN;
+  const bool n_edge = n0 + kDec16StripN > p.N;
+
+  const int total_batches = (p.K + kDec16BatchK - 1) / kDec16BatchK;
+  const int b_begin = split * p.batches_per_split;
+  int b_end = b_begin + p.batches_per_split;
+  if (b_end > total_batches)
+    b_end = total_batches;
+  const int nb = b_end > b_begin ? b_end - b_begin : 0; // the same for every wave
+
+  // Loads of the split's batch i into `slot`: B rows 32 wave .. +31 of the
+  // batch (load u: rows 8 q .. 8 q + 7, q = 4 wave + u, lane l' fetching
+  // chunk (l' % 8) ^ (row & 7) of row 8 q + l' / 8) and A rows 4 q .. 4 q + 3
+  // (q = A_LOADS wave + u, lane l' fetching chunk (l' % 16) ^ (row & 15) of
+  // row 4 q + l' / 16).  No loaded VGPR is live across the loop (with
+  // direct-to-LDS loads pending the compiler could only wait for one with
+  // vmcnt(0)).  For i >= nb every load reads the zero chunk, so each step
+  // issues the same loads.
+  auto issue = [&](int i, uint8_t *slot) {
+    const bool live = i < nb;
+    const int b = b_begin + i;
+    const int64_t k0 = (int64_t)b * kDec16BatchK;
+    const bool mask = !live || n_edge || b >= p.k_main_batches;
+#pragma unroll
+    for (int u = 0; u < Cfg::B_LOADS; ++u) {
+      const int q = Cfg::B_LOADS * wave + u;
+      const int row = 8 * q + (lane >> 3);
+      const int c = (lane & 7) ^ (row & 7);
+      const int64_t k = k0 + row, n = n0 + 8 * c;
+      const void *src = p.B + k * p.ldb + n;
+      if (mask && (!live || k >= p.K || n >= p.N))
+        src = tx_zero_chunk;
+      dma16_stream(src, (lds_void *)(slot + q * 1024)); // B is read once
+    }
+#pragma unroll
+    for (int u = 0; u < Cfg::A_LOADS; ++u) {
+      const int q = Cfg::A_LOADS * wave + u;
+      const int r = 4 * q + (lane >> 4);
+      const int c = (lane & 15) ^ (r & 15);
+      const int64_t k = k0 + 8 * c;
+      const void *src = p.A + (int64_t)r * p.lda + k;
+      if (!live || r >= p.M || (b >= p.k_main_batches && k >= p.K))
+        src = tx_zero_chunk;
+      dma16(src, (lds_void *)(slot + Cfg::A_OFF + q * 1024)); // A: re-read by every strip
+    }
+  };
+
+  f32x4_t acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+    acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // Per-lane LDS offsets within a slot.  B, K step ks: rows 32 ks + 8 G +
+  // L / 4 (lo) and +4 (hi), columns 16 wave + 4 (L % 4) .. +3, i.e. chunk
+  // 2 wave + (L % 4) / 2, byte 8 (L % 2); the swizzle takes row & 7, which
+  // is L / 4 for lo and L / 4 + 4 for hi in every step, so a step is +4 KiB.
+  // A, step ks, tile t: row 16 t + L, chunk (4 ks + G) ^ L: +4 KiB per tile.
+  const int cb = 2 * wave + ((L & 3) >> 1);
+  const uint32_t b_lo = (L >> 2) * 128 + ((cb ^ (L >> 2)) << 4) + 8 * (L & 1) + 8 * G * 128;
+  const uint32_t b_hi = b_lo + 4 * 128 - ((cb ^ (L >> 2)) << 4) + ((cb ^ ((L >> 2) + 4)) << 4);
+  uint32_t a_k[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    a_k[ks] = Cfg::A_OFF + L * 256 + (((4 * ks + G) ^ L) << 4);
+
+  auto consume = [&](const uint8_t *slot, int i) {
+    const uint32_t base = lds_addr(slot);
+    const bool tail = b_begin + i >= p.k_main_batches;
+    const int64_t k0 = (int64_t)(b_begin + i) * kDec16BatchK;
+#pragma unroll
+    for (int pr = 0; pr < 2; ++pr) {
+      v2i_t lo[2], hi[2];
+      i32x4_t a[2][T];
+      dec16_read_pair<T>(base + b_lo + pr * 8192, base + b_hi + pr * 8192,
+                         base + a_k[2 * pr], base + a_k[2 * pr + 1], lo, hi, a);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const i32x4_t bf = {lo[h].x, lo[h].y, hi[h].x, hi[h].y};
+        if (tail) {
+          const int64_t k = k0 + 32 * (2 * pr + h) + 8 * G;
+#pragma unroll
+          for (int t = 0; t < T; ++t)
+            a[h][t] = dec16_mask_k(a[h][t], k, p.K);
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+          acc[t] = mfma16x16x32<BF>(bf, a[h][t], acc[t]);
+      }
+    }
+  };
+
+  // Prologue: S - 1 batches in flight; batch i uses slot i % S.
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    issue(s, ring + s * SLOT);
+  // Main loop, unrolled by S so slot addresses are static; left at the first
+  // batch past nb.  At batch i: wait for this wave's loads of batch i (the
+  // S - 2 batches after it stay in flight), barrier (every wave's loads of
+  // batch i have landed and every wave has read batch i - 1's slot), issue
+  // batch i + S - 1 into that slot, then the MFMAs of batch i.
+  for (int i0 = 0;; i0 += S) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int i = i0 + s;
+      if (i >= nb)
+        goto k_loop_done;
+      wait_vmcnt<(S - 2) * Cfg::VPB>();
+      asm volatile("s_barrier" ::: "memory");
+      issue(i + S - 1, ring + ((s + S - 1) % S) * SLOT);
+      consume(ring + s * SLOT, i);
+    }
+  }
+k_loop_done:
+  __builtin_amdgcn_s_waitcnt(0); // the zero-chunk loads past nb have landed
+
+  // C for this lane: row 16 t + L, columns n0 + 16 wave + 4 G .. +3 (one
+  // 8-byte store in 16-bit C, 16 bytes in fp32; single elements where the
+  // quad crosses N).
+  const int64_t col = n0 + 16 * wave + 4 * G;
+  auto epilogue = [&](const f32x4_t (&sum)[T]) {
+    if (col >= p.N)
+      return;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int m = 16 * t + L;
+      if (m >= p.M)
+        continue;
+      const float f[4] = {sum[t][0], sum[t][1], sum[t][2], sum[t][3]};
+      if (p.c_f32) {
+        float *c = static_cast<float *>(p.C) + (int64_t)m * p.ldc + col;
+        if (col + 4 <= p.N) {
+          f32x4_t v = sum[t];
+          if (p.acc_c)
+            v += *reinterpret_cast<const f32x4_t *>(c);
+          *reinterpret_cast<f32x4_t *>(c) = v;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (col + r < p.N)
+              c[r] = p.acc_c ? c[r] + f[r] : f[r];
+        }
+      } else {
+        uint16_t *c = static_cast<uint16_t *>(p.C) + (int64_t)m * p.ldc + col;
+        if (col + 4 <= p.N) {
+          uint2 w;
+          w.x = BF ? pk_bf16_rne(f[0], f[1]) : pk_f16_rne(f[0], f[1]);
+          w.y = BF ? pk_bf16_rne(f[2], f[3]) : pk_f16_rne(f[2], f[3]);
+          *reinterpret_cast<uint2 *>(c) = w;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (col + r < p.N)
+              c[r] = BF ? f32_to_bf16_rne(f[r]) : f32_to_f16_rne(f[r]);
+        }
+      }
+    }
+  };
+  if (p.ksplit == 1) {
+    epilogue(acc);
+    return;
+  }
+
+  // Publish this split's partial, count arrivals for the strip, and let the
+  // last arrival gather: decode_i8.h's protocol and SC1 cache policy (data
+  // crosses workgroups only through the device-coherent level; every store
+  // is acknowledged before the barrier that precedes the counter increment;
+  // the last workgroup loads only after its increment has returned).
+  constexpr int kSC1 = 16;
+  const int64_t split_bytes = decode16_split_bytes(strips, SR);
+  auto part_rsrc = [&](int q) {
+    return __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<uint8_t *>(p.partials) + (int64_t)q * split_bytes, 0, (int)split_bytes,
+        0x00020000);
+  };
+  const int blk0 = (strip * kDecodeWaves + wave) * T; // 1 KiB blocks, in lane order
+  {
+    const auto mine = part_rsrc(split);
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i_t, acc[t]), mine,
+                                             ((blk0 + t) << 10) + 16 * lane, 0, kSC1);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t *const ctr = &p.counters[strip];
+    const uint32_t old =
+        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old + 1 == (uint32_t)p.ksplit;
+    if (last) // every split has arrived: none touches the counter again
+      __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *reinterpret_cast<volatile uint32_t *>(&last_flag) = last;
+  }
+  __syncthreads();
+  if (!*reinterpret_cast<volatile uint32_t *>(&last_flag))
+    return;
+  // Last arrival: sum = partial 0 + partial 1 + .. in split order, its own
+  // from registers; NQ splits' loads in flight before any is used.
+  f32x4_t sum[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+    sum[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  constexpr int NQ = 4;
+  for (int q0 = 0; q0 < p.ksplit; q0 += NQ) {
+    v4i_t v[NQ][T];
+#pragma unroll
+    for (int qq = 0; qq < NQ; ++qq)
+      if (q0 + qq < p.ksplit && q0 + qq != split) {
+        const auto r = part_rsrc(q0 + qq);
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+          v[qq][t] = __builtin_amdgcn_raw_buffer_load_b128(r, ((blk0 + t) << 10) + 16 * lane, 0,
+                                                           kSC1);
+      }
+#pragma unroll
+    for (int qq = 0; qq < NQ; ++qq)
+      if (q0 + qq < p.ksplit)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+          sum[t] += q0 + qq == split ? acc[t] : __builtin_bit_cast(f32x4_t, v[qq][t]);
+  }
+  epilogue(sum);
+}
+
+} // namespace txk

@@ -197,11 +197,20 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
         d->N <= (int64_t)4096 * 128 &&
         ((d->scale_mode == TX_SCALE_ROWCOL && d->c_type == TX_BF16) ||
          (d->scale_mode == TX_SCALE_NONE && d->c_type == TX_I32));
+    // The 16-bit decode kernel: both operands bf16 or both fp16, no scales,
+    // C in their type or fp32, B row-major, M <= 64, N up to its 16384
+    // strips of 64 columns.  It streams B once with split-K.
+    const bool decode16 =
+        (d->a_type == TX_BF16 || d->a_type == TX_F16) && d->b_type == d->a_type &&
+        d->scale_mode == TX_SCALE_NONE && (d->c_type == d->a_type || d->c_type == TX_F32) &&
+        !(d->flags & TX_FLAG_B_KMAJOR) && d->M <= 64 && d->N <= (int64_t)16384 * 64;
     const size_t first = spanA < TX_SPAN32_LIMIT && spanB < TX_SPAN32_LIMIT ? 0 : 1;
     if (upcast)
       t = chooseTile(kTiles16, d->M, d->N, d->K, first); // MX x bf16 runs on the bf16 tile
     else if (d->scale_mode == TX_SCALE_MX32)
       t = ba == 4 ? kTileMx4 : kTileMx8;
+    else if (decode16)
+      t = Tile{(int32_t)(16 * cdiv(d->M > 0 ? d->M : 1, 16)), 64, 128, 1.0};
     else if (sa == 2 && (d->flags & TX_FLAG_B_KMAJOR))
       t = kTiles16[0]; // the K-major B kernel exists for this tile only
     else if (sa == 2)
