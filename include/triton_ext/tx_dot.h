@@ -204,8 +204,9 @@ TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A, const void *B,
 /* No counterpart in the reference: a variant of tx_dot_launch for callers
  * that cannot allocate device memory (code under HIP graph capture, serving
  * loops and harnesses that forbid hipMalloc).  It takes no workspace: the
- * scratch the planned kernels need (the W8A8 decode kernel's split-K arrival
- * counters and int32 partials, the MX operand upcast to bf16) lives in one
+ * scratch the planned kernels need (the decode kernels' split-K arrival
+ * counters and their int32 or fp32 partials, the MX operand upcast to bf16)
+ * lives in one
  * static device array of TX_NOALLOC_SCRATCH_BYTES per GPU, held from the
  * library's load on that GPU until the process ends, and the call allocates
  * nothing.  A plan whose workspace does not fit (decode: more than

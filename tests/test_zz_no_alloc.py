@@ -3,8 +3,8 @@
 Its kernels are tx_dot_launch's; only the workspace differs (the library's
 static per-GPU scratch array instead of the caller's buffer).  So its output
 must equal tx_dot_launch's bit for bit on the same inputs, for the kernels
-that use scratch: the W8A8 decode kernel (split-K counters and partials) and
-the MX x bf16 upcast (the bf16 operand).  Two calls in a row, the second
+that use scratch: the decode kernels (split-K counters and partials: W8A8
+int32, 16-bit fp32) and the MX x bf16 upcast (the bf16 operand).  Two calls in a row, the second
 smaller, check that a call does not depend on what the previous one left in
 the shared array; the decode results are also checked against the oracle
 (int32 exact, so bit-exact bf16).
@@ -106,6 +106,37 @@ def test_noalloc_mx_upcast_then_decode(gpu):
     _mx_bf16(gpu, 512, 1024, 2048, 31)
     _mx_bf16(gpu, 256, 256, 512, 32)
     _w8a8(gpu, 16, 8192, 8192, 33)
+
+
+def _decode16(gpu, M, N, K, seed):
+    import torch
+    say(f"noalloc bf16 decode M={M} N={N} K={K} seed={seed}")
+    g = torch.Generator(device=gpu)
+    g.manual_seed(seed)
+    a = (torch.randn((M, K), generator=g, device=gpu) / K ** 0.5).to(torch.bfloat16)
+    b = (torch.randn((K, N), generator=g, device=gpu) / K ** 0.5).to(torch.bfloat16)
+    plan = tx.plan(tx.make_desc(M, N, K, tx.BF16, tx.F32))
+    assert plan.kernel == tx.KERNEL_DECODE_16BIT and plan.workspace_bytes > 0
+    c_ref = torch.empty((M, N), dtype=torch.float32, device=gpu)
+    c_new = torch.full((M, N), float("nan"), dtype=torch.float32, device=gpu)
+    ws = torch.zeros(int(plan.workspace_bytes), dtype=torch.uint8, device=gpu)
+    _launch("plain", plan, a, b, c_ref, None, None, ws)
+    _launch("noalloc", plan, a, b, c_new, None, None)
+    torch.cuda.synchronize()
+    assert torch.equal(c_new.view(torch.int32), c_ref.view(torch.int32))
+    return plan
+
+
+def test_noalloc_decode16_between_w8a8_calls(gpu):
+    """The 16-bit decode kernel's fp32 partials and per-strip counters on the same scratch as
+    the W8A8 decode: two decode16 calls (the second smaller), each after a W8A8 call, and a
+    W8A8 call after them, all bit-equal to tx_dot_launch on a fresh workspace."""
+    _w8a8(gpu, 16, 8192, 8192, 61)
+    p1 = _decode16(gpu, 16, 8192, 8192, 62)
+    _w8a8(gpu, 5, 2048, 4096, 63)
+    p2 = _decode16(gpu, 3, 1024, 2048, 64)
+    assert p1.split_k > 1 and p2.split_k > 1 and p2.workspace_bytes < p1.workspace_bytes
+    _w8a8(gpu, 16, 8192, 8192, 65)
 
 
 def test_noalloc_workspace_free_kernels(gpu):
