@@ -57,7 +57,9 @@ def parse():
                          "w8a8 (or "
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256; w8a8 also runs i32_16, the unscaled "
                          "int8 -> int32 decode at M=16), bf16_decode (or bf16_decode_1, _16, _64: "
-                         "bf16 at N = K = 8192 on the 16-bit decode kernel), int8, fp8, kmajor, "
+                         "bf16 at N = K = 8192 on the 16-bit decode kernel), fp8_decode (or "
+                         "fp8_decode_1, _16, _64: block-scaled e4m3 at N = K = 7168 on the fp8 "
+                         "decode kernel), int8, fp8, kmajor, "
                          "mx (or mxfp8, mxfp4, "
                          "mxfp8_4096, mxfp8_8192, mxfp4_4096, mxfp4_8192), mxbf16 (or mxbf16_fp4, mxbf16_fp8: "
                          "bf16 x MX), attn (or attn_1024, attn_4096, "
@@ -314,6 +316,41 @@ def bench_decode16(tx, dev, M, N, K, steps, warmup, flush, seed=3):
     return dict(workload=f"bf16 decode M={M} N={N} K={K}", ms=med, ms_isolated=iso,
                 ms_warm_mall=warm, gbps=nbytes / med / 1e6, frac_hbm=nbytes / med / 1e-3 / HBM,
                 tflops=2.0 * M * N * K / med / 1e9,
+                plan=plan_info(tx, p, split_k=p.split_k, grid=p.grid_x))
+
+
+def fp8_block_inputs_dev(M, N, K, dev, seed):
+    """C5's inputs on the device: N(0,1) values quantised to e4m3 per 1 x 128 group of A and
+    128 x 128 block of B, fp32 scales."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    a = torch.randn((M, K), generator=g, device=dev)
+    b = torch.randn((K, N), generator=g, device=dev)
+    kb, nb = (K + 127) // 128, (N + 127) // 128
+    sa = a.view(M, kb, 128).abs().amax(dim=2) / 448.0
+    sb = b.view(kb, 128, nb, 128).abs().amax(dim=(1, 3)) / 448.0
+    qa = (a.view(M, kb, 128) / sa[:, :, None]).view(M, K).to(torch.float8_e4m3fn)
+    qb = (b.view(kb, 128, nb, 128) / sb[:, None, :, None]).view(K, N).to(torch.float8_e4m3fn)
+    return qa, qb, sa.contiguous(), sb.contiguous()
+
+
+def bench_decode_f8(tx, dev, M, N, K, steps, warmup, flush, seed=5):
+    """fp8 e4m3 block-scaled dot of decode shape (C5's form at small M): the fp8 decode
+    kernel, timed like the W8A8 lines (cold, B from HBM); algorithmic bytes A, B, the scales
+    and C (bf16) once."""
+    import torch
+    qa, qb, sa, sb = fp8_block_inputs_dev(M, N, K, dev, seed)
+    c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    run = Launcher(tx, qa, qb, c, sa, sb, tx.SCALE_BLOCK128)
+    iso, _ = time_cold(run, steps, warmup, flush)
+    med = time_cold_in_stream(run, flush)
+    warm = time_back_to_back(run, steps, warmup)
+    nbytes = M * K + K * N + 2 * M * N + 4 * (sa.numel() + sb.numel())
+    p = run.plan
+    return dict(workload=f"fp8 e4m3 block-scaled decode M={M} N={N} K={K}", ms=med,
+                ms_isolated=iso, ms_warm_mall=warm, gbps=nbytes / med / 1e6,
+                frac_hbm=nbytes / med / 1e-3 / HBM, tflops=2.0 * M * N * K / med / 1e9,
                 plan=plan_info(tx, p, split_k=p.split_k, grid=p.grid_x))
 
 
@@ -836,6 +873,13 @@ def main():
         secondary.append(r)
         print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
               f"({100 * r['frac_hbm']:.1f}% HBM)", file=sys.stderr, flush=True)
+    for m in (1, 16, 64):
+        if want("fp8_decode") or want(f"fp8_decode_{m}"):
+            r = bench_decode_f8(tx, dev, m, 7168, 7168, max(args.steps, 20), 3, flush)
+            secondary.append(r)
+            print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
+                  f"({100 * r['frac_hbm']:.1f}% HBM); isolated launch "
+                  f"{r['ms_isolated'] * 1e3:.2f} us", file=sys.stderr, flush=True)
     for m in (1, 16, 64):
         if want("bf16_decode") or want(f"bf16_decode_{m}"):
             r = bench_decode16(tx, dev, m, 8192, 8192, max(args.steps, 20), 3, flush)

@@ -119,6 +119,8 @@ typedef enum tx_kernel {
                                * workspace, then the bf16 tile              */
   TX_KERNEL_DECODE_16BIT = 7, /* bf16/fp16 decode shapes (M <= 64, no scales):
                                * B streamed once, MFMA 16x16x32              */
+  TX_KERNEL_DECODE_F8 = 8,    /* fp8 decode shapes (M <= 64, unscaled or 128-block
+                               * scales): B streamed once, MFMA 16x16x128    */
 } tx_kernel;
 
 /* Bit flags for tx_dot_desc.flags */

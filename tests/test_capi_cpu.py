@@ -198,6 +198,11 @@ def test_plan_validation():
     (64, 4096, 4096, tx.F16, tx.F16, 0, tx.KERNEL_DECODE_16BIT),
     (33, 28672, 8192, tx.F16, tx.F32, 0, tx.KERNEL_DECODE_16BIT),
     (65, 8192, 8192, tx.BF16, tx.BF16, 0, tx.KERNEL_GEMM_16BIT),
+    # fp8 of decode shape: the fp8 decode kernel, unscaled (fp32 C) or block-scaled
+    (16, 7168, 7168, tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, tx.KERNEL_DECODE_F8),
+    (1, 8192, 8192, tx.F8E4M3, tx.F32, 0, tx.KERNEL_DECODE_F8),
+    (64, 4096, 4096, tx.F8E5M2, tx.F32, 0, tx.KERNEL_DECODE_F8),
+    (65, 7168, 7168, tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, tx.KERNEL_GEMM_F8),
 ])
 def test_kernel_choice(M, N, K, a, c, sm, kernel):
     p = tx.plan(tx.make_desc(M, N, K, a, c, scale_mode=sm))
@@ -218,18 +223,52 @@ def test_kernel_choice(M, N, K, a, c, sm, kernel):
         rows = M if M <= 48 else slices * bm
         cols = -(-N // 4) * 4 if M <= 48 else -(-N // 128) * 128
         assert p.workspace_bytes == (65536 + p.split_k * rows * cols * 4 if p.split_k > 1 else 0)
+    if kernel == tx.KERNEL_DECODE_F8:
+        # the slice x 128-column strips x 128-row K batches; fp32 partials [split][strip][sr x 128]
+        sr = 16 * -(-M // 16)
+        assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (sr, 128, 128)
+        strips = -(-N // 128)
+        assert p.grid_x == strips * p.split_k <= max(strips, 256) and p.block_threads == 256
+        assert p.split_k == 1 if 2 * strips > 256 else 2 * strips * p.split_k > 256
+        assert p.workspace_bytes == (65536 + p.split_k * strips * sr * 128 * 4
+                                     if p.split_k > 1 else 0)
     if kernel == tx.KERNEL_DECODE_16BIT:
         # the slice of 16 ceil(M / 16) rows x 64-column strips x 128-row K batches;
-        # strips x splits cover the 256 CUs (no split once the strips alone do)
+        # strips x splits workgroups, at most one a CU (no split once the strips alone fill them)
         sr = 16 * -(-M // 16)
         assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (sr, 64, 128)
         strips = -(-N // 64)
-        assert p.grid_x == strips * p.split_k and p.block_threads == 256
-        assert p.split_k == 1 if strips >= 256 else strips * p.split_k >= 256
+        # (the largest split that keeps one workgroup a CU)
+        assert p.grid_x == strips * p.split_k <= max(strips, 256) and p.block_threads == 256
+        assert p.split_k == 1 if 2 * strips > 256 else 2 * strips * p.split_k > 256
         # the 64 KiB counter region, then fp32 partials: [split][strip][sr x 64]
         assert p.workspace_bytes == (65536 + p.split_k * strips * sr * 64 * 4
                                      if p.split_k > 1 else 0)
     assert (p.split_k & (p.split_k - 1)) == 0
+
+
+def test_decode_f8_plans():
+    """The fp8 decode kernel: unscaled fp8 (any e4m3 / e5m2 mix) to fp32, e4m3 with 128-block
+    scales to bf16 / fp32; K-major fp8 B is refused as on the tiles."""
+    DF8 = tx.KERNEL_DECODE_F8
+    for a, b in ((tx.F8E4M3, tx.F8E4M3), (tx.F8E4M3, tx.F8E5M2), (tx.F8E5M2, tx.F8E4M3),
+                 (tx.F8E5M2, tx.F8E5M2)):
+        assert tx.plan(tx.make_desc(16, 4096, 4096, a, tx.F32, b_type=b)).kernel == DF8
+    for c in (tx.BF16, tx.F32):
+        assert tx.plan(tx.make_desc(8, 4096, 4096, tx.F8E4M3, c,
+                                    scale_mode=tx.SCALE_BLOCK128)).kernel == DF8
+    assert tx.plan(tx.make_desc(16, 4096, 4096, tx.F8E4M3, tx.F32, flags=tx.FLAG_ACCUMULATE,
+                                scale_mode=tx.SCALE_BLOCK128)).kernel == DF8
+    assert _err(tx.make_desc(16, 4096, 4096, tx.F8E4M3, tx.F32,
+                             flags=tx.FLAG_B_KMAJOR)) == tx.ERR_UNSUPPORTED
+    # an explicit 8-bit tile at decode shape runs that tile
+    assert tx.plan(tx.make_desc(16, 4096, 4096, tx.F8E4M3, tx.F32,
+                                block=(256, 256, 128))).kernel == tx.KERNEL_GEMM_F8
+    # split-K: at least 4 batches of 128 K rows a split
+    p = tx.plan(tx.make_desc(16, 7168, 7168, tx.F8E4M3, tx.BF16, scale_mode=tx.SCALE_BLOCK128))
+    assert p.split_k == 4 and p.grid_x == 56 * 4  # 224 workgroups: 448 would take two rounds
+    p = tx.plan(tx.make_desc(3, 1000, 300, tx.F8E4M3, tx.F32, lda=304, ldb=1008))
+    assert p.split_k == 1 and p.workspace_bytes == 0 and p.grid_x == 8
 
 
 def test_decode16_plans():

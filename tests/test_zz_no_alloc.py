@@ -139,6 +139,28 @@ def test_noalloc_decode16_between_w8a8_calls(gpu):
     _w8a8(gpu, 16, 8192, 8192, 65)
 
 
+def test_noalloc_decode_f8(gpu):
+    """The fp8 decode kernel (block-scaled, split-K) on the shared scratch, between W8A8
+    calls, bit-equal to tx_dot_launch on a fresh workspace."""
+    import torch
+    from dotcase import fp8_block_inputs
+    _w8a8(gpu, 16, 8192, 8192, 71)
+    for M, N, K, seed in ((16, 7168, 7168, 72), (4, 1024, 2048, 73)):
+        say(f"noalloc fp8 decode M={M} N={N} K={K}")
+        qa, qb, sa, sb = fp8_block_inputs(M, N, K, seed)
+        da, db, dsa, dsb = (to_device(x, gpu) for x in (qa, qb, sa, sb))
+        plan = tx.plan(tx.make_desc(M, N, K, tx.F8E4M3, tx.BF16, scale_mode=tx.SCALE_BLOCK128))
+        assert plan.kernel == tx.KERNEL_DECODE_F8 and plan.split_k > 1
+        c_ref = torch.empty((M, N), dtype=torch.bfloat16, device=gpu)
+        c_new = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
+        ws = torch.zeros(int(plan.workspace_bytes), dtype=torch.uint8, device=gpu)
+        _launch("plain", plan, da, db, c_ref, dsa, dsb, ws)
+        _launch("noalloc", plan, da, db, c_new, dsa, dsb)
+        torch.cuda.synchronize()
+        assert torch.equal(c_new.view(torch.int16), c_ref.view(torch.int16))
+    _w8a8(gpu, 16, 8192, 8192, 74)
+
+
 def test_noalloc_workspace_free_kernels(gpu):
     """A plan without workspace (the bf16 tile) runs through the same entry point."""
     import torch

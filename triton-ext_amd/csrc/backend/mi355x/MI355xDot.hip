@@ -27,6 +27,7 @@
 #include "mx_upcast.h"
 
 #include "decode16.h"
+#include "decode_f8.h"
 #include "decode_i8.h"
 #include "decode_rows_i8.h"
 #include "gemm16_dma.h"
@@ -189,6 +190,17 @@ const DecodeKernelFn kDecodeKernels[4] = {decode_i8_kernel<1>, decode_i8_kernel<
 const DecodeKernelFn kDecodeRowsKernels[3] = {decode_rows_i8_kernel<64, 6>,
                                               decode_rows_i8_kernel<128, 4>,
                                               decode_rows_i8_kernel<256, 3>};
+// The fp8 decode kernel: unscaled by [A e4m3 / e5m2][B e4m3 / e5m2][slice of
+// 16, 32, 48, 64 rows], block-scaled (e4m3) by slice.
+typedef void (*DecodeF8KernelFn)(DecodeF8Args);
+#define TX_DF8_SLICES(SC, FA, FB)                                                          \
+  {decode_f8_kernel<16, SC, FA, FB>, decode_f8_kernel<32, SC, FA, FB>,                     \
+   decode_f8_kernel<48, SC, FA, FB>, decode_f8_kernel<64, SC, FA, FB>}
+const DecodeF8KernelFn kDecodeF8Kernels[2][2][4] = {
+    {TX_DF8_SLICES(false, 0, 0), TX_DF8_SLICES(false, 0, 1)},
+    {TX_DF8_SLICES(false, 1, 0), TX_DF8_SLICES(false, 1, 1)}};
+const DecodeF8KernelFn kDecodeF8ScaledKernels[4] = TX_DF8_SLICES(true, 0, 0);
+#undef TX_DF8_SLICES
 // The 16-bit decode kernel by [fp16 / bf16][slice of 16, 32, 48, 64 rows].
 typedef void (*Decode16KernelFn)(Decode16Args);
 const Decode16KernelFn kDecode16Kernels[2][4] = {
@@ -412,14 +424,15 @@ bool decode16Tile(const tx_dot_desc &d) {
   return d.block_m == decode16Rows(d) && d.block_n == kDec16StripN &&
          d.block_k == kDec16BatchK;
 }
-// Split-K factor: a power of two (<= kMaxSplit) so that strips x splits
-// workgroups cover the CUs about once, each split with at least 4 batches
-// of 128 K rows, and every split owning one batch at least.
+// Split-K factor: the largest power of two (<= kMaxSplit) with strips x
+// splits workgroups at most one per CU (one fits a CU's LDS; a second round
+// would run behind the first), each split with at least 4 batches of 128 K
+// rows, and every split owning one batch at least.
 int decode16Split(const tx_dot_desc &d) {
   const int64_t strips = cdiv(d.N, kDec16StripN);
   const int64_t batches = cdiv(d.K, kDec16BatchK);
   int ks = 1;
-  while (ks < (int)kMaxSplit && strips * ks < 256 && batches / (ks * 2) >= 4)
+  while (ks < (int)kMaxSplit && strips * ks * 2 <= 256 && batches / (ks * 2) >= 4)
     ks *= 2;
   while (ks > 1 && cdiv(batches, ks) * (ks - 1) >= batches)
     ks >>= 1;
@@ -430,6 +443,42 @@ int64_t decode16Workspace(const tx_dot_desc &d, int ksplit) {
     return 0;
   return kDecodeCounterBytes +
          ksplit * decode16_split_bytes(cdiv(d.N, kDec16StripN), decode16Rows(d));
+}
+
+// The fp8 decode kernel (decode_f8.h): fp8 x fp8 (e4m3 / e5m2 in any mix)
+// with fp32 C, or e4m3 x e4m3 with 128-block scales and bf16 / fp32 C; B
+// row-major, M <= 64, one arrival counter per 128-column strip.
+bool useDecodeF8(const tx_dot_desc &d) {
+  const bool fa = d.a_type == TX_F8E4M3 || d.a_type == TX_F8E5M2;
+  const bool fb = d.b_type == TX_F8E4M3 || d.b_type == TX_F8E5M2;
+  if (!fa || !fb || (d.flags & TX_FLAG_B_KMAJOR) || d.M > kDec8MaxM ||
+      cdiv(d.N, kDec8StripN) > kDec16MaxStrips)
+    return false;
+  if (d.scale_mode == TX_SCALE_NONE)
+    return d.c_type == TX_F32;
+  return d.scale_mode == TX_SCALE_BLOCK128 && d.a_type == TX_F8E4M3 &&
+         d.b_type == TX_F8E4M3 && (d.c_type == TX_BF16 || d.c_type == TX_F32);
+}
+// Its tile: the slice (16 ceil(M / 16) rows) x a 128-column strip x 128-row
+// K batches (no 8-bit GEMM tile is narrower than 128 rows).
+bool decodeF8Tile(const tx_dot_desc &d) {
+  return d.block_m == decode16Rows(d) && d.block_n == kDec8StripN && d.block_k == kDec8BatchK;
+}
+int decodeF8Split(const tx_dot_desc &d) { // decode16Split's rule
+  const int64_t strips = cdiv(d.N, kDec8StripN);
+  const int64_t batches = cdiv(d.K, kDec8BatchK);
+  int ks = 1;
+  while (ks < (int)kMaxSplit && strips * ks * 2 <= 256 && batches / (ks * 2) >= 4)
+    ks *= 2;
+  while (ks > 1 && cdiv(batches, ks) * (ks - 1) >= batches)
+    ks >>= 1;
+  return ks;
+}
+int64_t decodeF8Workspace(const tx_dot_desc &d, int ksplit) {
+  if (ksplit <= 1)
+    return 0;
+  return kDecodeCounterBytes +
+         ksplit * decode_f8_split_bytes(cdiv(d.N, kDec8StripN), decode16Rows(d));
 }
 
 // The 32-bit-offset tiles (gemm16_w4.h, gemm8_w4.h, gemm8_n224.h) address A,
@@ -476,6 +525,17 @@ int txMi355xDotRun(tx_dot_plan *plan) {
     return fail(TX_ERR_UNSUPPORTED,
                 "no kernel for a_type=%d b_type=%d c_type=%d scale_mode=%d",
                 d.a_type, d.b_type, d.c_type, d.scale_mode);
+  if (useDecodeF8(d) && decodeF8Tile(d)) {
+    const int ks = decodeF8Split(d);
+    plan->kernel = TX_KERNEL_DECODE_F8;
+    plan->split_k = ks;
+    plan->grid_x = (int32_t)(cdiv(d.N, kDec8StripN) * ks);
+    plan->grid_y = plan->grid_z = 1;
+    plan->block_threads = kDecodeWaves * 64;
+    plan->workspace_bytes = decodeF8Workspace(d, ks);
+    plan->passes_run += 1;
+    return TX_OK;
+  }
   if (useDecode16(d) && decode16Tile(d)) {
     const int ks = decode16Split(d);
     plan->kernel = TX_KERNEL_DECODE_16BIT;
@@ -615,6 +675,7 @@ extern "C" TX_API const char *tx_kernel_name(int32_t kernel) {
   case TX_KERNEL_GEMM_MX: return "gemm_mx_mfma_scale16x16x128";
   case TX_KERNEL_GEMM_MX_BF16: return "mx_upcast_bf16+gemm_16bit_mfma32x32x16";
   case TX_KERNEL_DECODE_16BIT: return "decode_16bit_mfma16x16x32";
+  case TX_KERNEL_DECODE_F8: return "decode_f8_mfma16x16x128_f8f6f4";
   default: return "?";
   }
 }
@@ -891,6 +952,48 @@ int launchDecode16(const tx_dot_plan &plan, const void *A, const void *B, void *
   return TX_OK;
 }
 
+int launchDecodeF8(const tx_dot_plan &plan, const void *A, const void *B, void *C,
+                   const void *sa, const void *sb, void *ws, size_t ws_bytes,
+                   hipStream_t stream) {
+  const tx_dot_desc &d = plan.desc;
+  const int ks = plan.split_k;
+  const int64_t need = decodeF8Workspace(d, ks);
+  if (need > 0 && (!ws || (int64_t)ws_bytes < need))
+    return fail(TX_ERR_WORKSPACE, "decode needs %lld workspace bytes, got %zu",
+                (long long)need, ws_bytes);
+  const bool scaled = d.scale_mode == TX_SCALE_BLOCK128;
+  DecodeF8Args a;
+  a.A = static_cast<const uint8_t *>(A);
+  a.B = static_cast<const uint8_t *>(B);
+  a.C = C;
+  a.sa = static_cast<const float *>(sa);
+  a.sb = static_cast<const float *>(sb);
+  a.c_f32 = d.c_type == TX_F32;
+  a.acc_c = (d.flags & TX_FLAG_ACCUMULATE) != 0;
+  a.M = (int32_t)d.M;
+  a.N = (int32_t)d.N;
+  a.K = (int32_t)d.K;
+  a.lda = d.lda;
+  a.ldb = d.ldb;
+  a.ldc = d.ldc;
+  a.sa_ld = (int32_t)cdiv(d.K, 128);
+  a.sb_ld = (int32_t)cdiv(d.N, 128);
+  a.ksplit = ks;
+  a.batches_per_split = (int32_t)cdiv(cdiv(d.K, kDec8BatchK), ks);
+  a.k_main_batches = (int32_t)(plan.k_split / kDec8BatchK);
+  a.counters = static_cast<uint32_t *>(ws);
+  a.partials = need > 0 ? reinterpret_cast<float *>(static_cast<uint8_t *>(ws) +
+                                                    kDecodeCounterBytes)
+                        : nullptr;
+  const int si = decode16Rows(d) / 16 - 1;
+  const DecodeF8KernelFn fn =
+      scaled ? kDecodeF8ScaledKernels[si]
+             : kDecodeF8Kernels[d.a_type == TX_F8E5M2][d.b_type == TX_F8E5M2][si];
+  hipLaunchKernelGGL(fn, dim3(plan.grid_x), dim3(plan.block_threads), 0, stream, a);
+  TX_HIP_CHECK(hipGetLastError());
+  return TX_OK;
+}
+
 } // namespace
 
 // Scratch of tx_dot_launch_noalloc: one array per GPU (each device holds its
@@ -959,6 +1062,14 @@ int checkPlan(const tx_dot_plan &p) {
   classify(d, &op, &epi);
   if (op < 0 || epi < 0)
     return fail(TX_ERR_UNSUPPORTED, "no kernel for the plan's operand types");
+  if (p.kernel == TX_KERNEL_DECODE_F8) {
+    const int sk = p.split_k;
+    if (!useDecodeF8(d) || !decodeF8Tile(d) || sk < 1 || sk > (int)kMaxSplit ||
+        (sk & (sk - 1)) || p.grid_x != cdiv(d.N, kDec8StripN) * sk ||
+        p.block_threads != kDecodeWaves * 64 || p.workspace_bytes != decodeF8Workspace(d, sk))
+      return fail(TX_ERR_INVALID, "the plan's decode launch does not follow from its descriptor");
+    return TX_OK;
+  }
   if (p.kernel == TX_KERNEL_DECODE_16BIT) {
     const int sk = p.split_k;
     if (!useDecode16(d) || !decode16Tile(d) || sk < 1 || sk > (int)kMaxSplit ||
@@ -1044,6 +1155,8 @@ int launchPlanned(const tx_dot_plan *plan, const void *A, const void *B, void *C
                         workspace_bytes, s);
   case TX_KERNEL_DECODE_16BIT:
     return launchDecode16(*plan, A, B, C, workspace, workspace_bytes, s);
+  case TX_KERNEL_DECODE_F8:
+    return launchDecodeF8(*plan, A, B, C, scale_a, scale_b, workspace, workspace_bytes, s);
   case TX_KERNEL_GEMM_MX_BF16:
     return launchMxUpcast(*plan, A, B, C, scale_a, scale_b, workspace, workspace_bytes, s);
   default:

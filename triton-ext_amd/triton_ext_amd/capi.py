@@ -21,7 +21,7 @@ OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_NO_DEVICE, ERR_WORKSPACE, ERR_NO_
 NOALLOC_SCRATCH_BYTES = 64 << 20
 # tx_kernel
 (KERNEL_NONE, KERNEL_GEMM_16BIT, KERNEL_GEMM_I8, KERNEL_DECODE_I8, KERNEL_GEMM_F8,
- KERNEL_GEMM_MX, KERNEL_GEMM_MX_BF16, KERNEL_DECODE_16BIT) = range(8)
+ KERNEL_GEMM_MX, KERNEL_GEMM_MX_BF16, KERNEL_DECODE_16BIT, KERNEL_DECODE_F8) = range(9)
 FLAG_NO_LOOP_SPLIT = 0x1
 FLAG_B_KMAJOR = 0x2  # B stored [N][K] row-major (a transposed view in torch)
 FLAG_ACCUMULATE = 0x4  # C = C + A . B (fp32 / int32 C)
