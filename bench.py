@@ -534,6 +534,9 @@ def ceilings_lib():
     L.tx_ceiling_mfma_bf16_stamped.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp, vp]
     L.tx_phases_bf16_setup.argtypes = [vp, ctypes.c_int]
     L.tx_phases_bf16.argtypes = [vp, vp, vp] + [ctypes.c_int] * 5 + [vp]
+    L.tx_phases_8bit.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp] + [ctypes.c_int] * 5 + [vp]
+    L.tx_ceiling_mfma_fp8_stamped.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp, vp]
+    L.tx_ceiling_operand_stream_8bit.argtypes = [vp, vp] + [ctypes.c_int] * 5 + [vp]
     return L
 
 
@@ -588,6 +591,43 @@ def bench_mfma_ceiling(dev, steps, warmup, seed=1, zeros=False):
                 ms=ms, tflops=flops / ms / 1e9, frac=flops / ms / 1e-3 / PEAK_BF16)
 
 
+def phase_summary(w, ms, mfma_cyc):
+    """Wave-time by phase from the stamps of a launch (16 words per wave: the wall clock at
+    entry, step 0 landed, K loop done, epilogue issued, stores acknowledged, then XCC id,
+    workgroup, and the shader clock at the same points), ms the launch period; mfma_cyc
+    the MFMA cycles of one wave's K loop."""
+    import numpy as np
+    waves = w.shape[0]
+    rt, sc = w[:, 0:5], w[:, 8:13]                 # wall clock (10 ns), shader clock
+    r0, r4 = rt[:, 0].min(), rt[:, 4].max()
+    T = ms * 1e3                                   # us per launch
+    us = lambda x: x / 100.0
+    loop_us = us(rt[:, 2] - rt[:, 1])
+    loop_cyc = (sc[:, 2] - sc[:, 1]).astype(np.float64)
+    mfma_us = loop_us * mfma_cyc / loop_cyc
+    share = lambda x: round(float(np.sum(x)) / (waves * T), 4)
+    mean = lambda x: round(float(np.mean(x)), 2)
+    xcc = (w[:, 5] >> 32) & 7
+    return dict(
+        wave_time={
+            "mfma_in_loop": share(mfma_us), "loop_other": share(loop_us - mfma_us),
+            "before_entry": share(us(rt[:, 0] - r0)), "prologue": share(us(rt[:, 1] - rt[:, 0])),
+            "epilogue": share(us(rt[:, 3] - rt[:, 2])),
+            "store_drain": share(us(rt[:, 4] - rt[:, 3])),
+            "after_own_end": share(us(r4 - rt[:, 4])),
+            "between_launches": round(1.0 - us(r4 - r0) / T, 4)},
+        us_mean={"prologue": mean(us(rt[:, 1] - rt[:, 0])), "k_loop": mean(loop_us),
+                 "epilogue": mean(us(rt[:, 3] - rt[:, 2])),
+                 "store_drain": mean(us(rt[:, 4] - rt[:, 3])),
+                 "span": round(us(r4 - r0), 2), "launch": round(T, 2)},
+        loop_ghz=round(float(np.mean(loop_cyc / (loop_us * 1e3))), 3),
+        epilogue_ghz=round(float(np.mean((sc[:, 4] - sc[:, 2]) /
+                                         (us(rt[:, 4] - rt[:, 2]) * 1e3))), 3),
+        loop_mfma_busy=round(float(np.mean(mfma_cyc / loop_cyc)), 4),
+        xcd_mean_end_us={int(x): mean(us(rt[xcc == x, 4] - r0)) for x in range(8)
+                         if np.any(xcc == x)})
+
+
 def bench_phases(dev, a, b, c, group_m, steps, warmup, seed=1):
     """Where one launch of the headline kernel goes.  libtx_ceilings.so builds
     gemm16_w4_kernel with its phase stamps on (per wave: the wall clock and the shader
@@ -619,36 +659,11 @@ def bench_phases(dev, a, b, c, group_m, steps, warmup, seed=1):
 
     stamps(-1)
     ms = time_back_to_back(lambda: launch(1), steps, warmup)  # the last launch's stamps remain
-    w = st.view(waves, 16).cpu().numpy().astype(np.int64)
-    rt, sc = w[:, 0:5], w[:, 8:13]                 # wall clock (10 ns), shader clock
-    r0, r4 = rt[:, 0].min(), rt[:, 4].max()
-    T = ms * 1e3                                   # us per launch
-    us = lambda x: x / 100.0
-    loop_us = us(rt[:, 2] - rt[:, 1])
-    loop_cyc = (sc[:, 2] - sc[:, 1]).astype(np.float64)
-    mfma_cyc = 2048.0 * ks
-    mfma_us = loop_us * mfma_cyc / loop_cyc
-    share = lambda x: round(float(np.sum(x)) / (waves * T), 4)
-    phases = {
-        "mfma_in_loop": share(mfma_us), "loop_other": share(loop_us - mfma_us),
-        "before_entry": share(us(rt[:, 0] - r0)), "prologue": share(us(rt[:, 1] - rt[:, 0])),
-        "epilogue": share(us(rt[:, 3] - rt[:, 2])), "store_drain": share(us(rt[:, 4] - rt[:, 3])),
-        "after_own_end": share(us(r4 - rt[:, 4])),
-        "between_launches": round(1.0 - us(r4 - r0) / T, 4)}
+    out = dict(workload="phases of the bf16 4096^3 tile, stamped build (libtx_ceilings.so)",
+               ms_stamped=ms, tflops_stamped=2.0 * M * N * K / ms / 1e9)
+    out.update(phase_summary(st.view(waves, 16).cpu().numpy().astype(np.int64), ms,
+                             2048.0 * ks))
     mean = lambda x: round(float(np.mean(x)), 2)
-    xcc = (w[:, 5] >> 32) & 7
-    xcd_end = {int(x): mean(us(rt[xcc == x, 4] - r0)) for x in range(8) if np.any(xcc == x)}
-    out = dict(
-        workload="phases of the bf16 4096^3 tile, stamped build (libtx_ceilings.so)",
-        ms_stamped=ms, tflops_stamped=2.0 * M * N * K / ms / 1e9, wave_time=phases,
-        us_mean={"prologue": mean(us(rt[:, 1] - rt[:, 0])), "k_loop": mean(loop_us),
-                 "epilogue": mean(us(rt[:, 3] - rt[:, 2])),
-                 "store_drain": mean(us(rt[:, 4] - rt[:, 3])),
-                 "span": round(us(r4 - r0), 2), "launch": round(T, 2)},
-        loop_ghz=round(float(np.mean(loop_cyc / (loop_us * 1e3))), 3),
-        epilogue_ghz=round(float(np.mean((sc[:, 4] - sc[:, 2]) / (us(rt[:, 4] - rt[:, 2]) * 1e3))), 3),
-        loop_mfma_busy=round(float(np.mean(mfma_cyc / loop_cyc)), 4),
-        xcd_mean_end_us=xcd_end)
     steps_probed = {}
     for s_ in (2, ks // 4, ks // 2, 3 * ks // 4, ks - 3):
         stamps(s_)
@@ -673,10 +688,113 @@ def bench_phases(dev, a, b, c, group_m, steps, warmup, seed=1):
             raise RuntimeError("tx_ceiling_mfma_bf16_stamped failed")
     cms = time_back_to_back(ceil, steps, warmup)
     cw = cst.view(1024, 4).cpu().numpy().astype(np.int64)
-    c_us = us(cw[:, 1] - cw[:, 0])
+    c_us = (cw[:, 1] - cw[:, 0]) / 100.0
     c_cyc = (cw[:, 3] - cw[:, 2]).astype(np.float64)
     out["ceiling"] = {"ms": cms, "loop_ghz": round(float(np.mean(c_cyc / (c_us * 1e3))), 3),
                       "loop_mfma_busy": round(float(np.mean(2048.0 * 64 / c_cyc)), 4)}
+    return out
+
+
+def bench_phases8(dev, steps, warmup, seed=5):
+    """Where a launch of the 8-bit 256x256x128 tile goes, for C5 (fp8 block-scaled
+    2048x7168x7168, bf16 C) and int8 4096^3 (int32 C): libtx_ceilings.so builds
+    gemm8_w4_kernel with its phase stamps on, as bench_phases does for the bf16 tile.  A
+    wave runs 8 x 4 blocks a step, one v_mfma_f32_16x16x128_f8f6f4 (fp8) or two
+    v_mfma_i32_16x16x64_i8 (int8) each: 1024 MFMA cycles a step, two waves a SIMD.  The
+    C5 schedule's MFMA-only ceiling loop is stamped alike for its clock and busy."""
+    import numpy as np
+    import torch
+    L = ceilings_lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    out = []
+    for kind, (M, N, K) in ((0, (2048, 7168, 7168)), (1, (4096, 4096, 4096))):
+        if kind == 0:
+            a, b, sa, sb = fp8_block_inputs_dev(M, N, K, dev, seed)
+            c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            name = "fp8 block-scaled (C5)"
+        else:
+            g = torch.Generator(device=dev)
+            g.manual_seed(seed)
+            a = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+            b = torch.randint(-127, 128, (K, N), generator=g, device=dev, dtype=torch.int8)
+            sa = sb = None
+            c = torch.empty((M, N), dtype=torch.int32, device=dev)
+            name = "int8 -> int32"
+        tm, tn, ks = M // 256, N // 256, K // 128
+        waves = tm * tn * 8
+        st = torch.zeros(waves * 16, dtype=torch.int64, device=dev)
+        if L.tx_phases_bf16_setup(st.data_ptr(), -1) != 0:
+            raise RuntimeError("tx_phases_bf16_setup failed")
+
+        def launch():
+            if L.tx_phases_8bit(kind, a.data_ptr(), b.data_ptr(), c.data_ptr(),
+                                None if sa is None else sa.data_ptr(),
+                                None if sb is None else sb.data_ptr(), tm, tn, ks, 4, 1,
+                                stream) != 0:
+                raise RuntimeError("tx_phases_8bit failed")
+        ms = time_back_to_back(launch, steps, warmup)
+        r = dict(workload=f"phases of the 8-bit 256x256x128 tile, {name} {M}x{N}x{K}, stamped build",
+                 ms_stamped=ms, tflops_stamped=2.0 * M * N * K / ms / 1e9)
+        w = st.view(waves, 16).cpu().numpy().astype(np.int64)
+        r.update(phase_summary(w, ms, 1024.0 * ks))
+        del r["loop_mfma_busy"]  # a wave's share means little with two waves on a SIMD
+        # The two waves of a SIMD (same XCC, SE, SH, CU and SIMD id in HW_ID): both waves'
+        # MFMA cycles over the union of their K loops, on the CU's shader clock.
+        h = w[:, 5]
+        key = (((h >> 32) & 7) << 16) | (((h >> 13) & 7) << 12) | (((h >> 12) & 1) << 11) | \
+              (((h >> 8) & 15) << 4) | ((h >> 4) & 3)
+        busy = []
+        for k in np.unique(key):
+            sel = w[key == k]
+            span = float(sel[:, 10].max() - sel[:, 9].min())
+            busy.append(1024.0 * ks * len(sel) / span)
+        r["simd_mfma_busy_in_loop"] = round(float(np.mean(busy)), 4)
+        r["waves_per_simd"] = round(waves / len(busy), 2)
+        # single K steps: the MFMA phase (a step's 32 blocks), the wait for the next
+        # step's loads and the LDS reads, the barrier; shader cycles, mean over waves
+        mean = lambda x: round(float(np.mean(x)), 2)
+        probed = {}
+        for s_ in (2, ks // 2, ks - 3):
+            if L.tx_phases_bf16_setup(st.data_ptr(), s_) != 0:
+                raise RuntimeError("tx_phases_bf16_setup failed")
+            for _ in range(20):
+                launch()
+            torch.cuda.synchronize()
+            v = st.view(waves, 16).cpu().numpy().astype(np.int64)
+            probed[s_] = {"mfma_phase": mean(v[:, 13] - v[:, 7]),
+                          "load_and_lds_wait": mean(v[:, 14] - v[:, 13]),
+                          "barrier": mean(v[:, 15] - v[:, 14])}
+        if L.tx_phases_bf16_setup(st.data_ptr(), -1) != 0:
+            raise RuntimeError("tx_phases_bf16_setup failed")
+        r["step_cycles"] = probed
+
+        # the tile's A and B loads alone (its load code, order and step barrier)
+        def stream_only():
+            if L.tx_ceiling_operand_stream_8bit(a.data_ptr(), b.data_ptr(), tm, tn, ks, 4, 1,
+                                                stream) != 0:
+                raise RuntimeError("tx_ceiling_operand_stream_8bit failed")
+        sms = time_back_to_back(stream_only, steps, warmup)
+        r["operand_stream"] = {"ms": sms, "gb_per_s_per_cu": round(ks * 65536 / sms / 1e6, 1)}
+        out.append(r)
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    vals = (torch.randn((64 * 12 * 64 * 32,), generator=g, device=dev) * 100).clamp(-448, 448)
+    seed_t = vals.to(torch.float8_e4m3fn).view(torch.uint8)
+    cout = torch.empty(224 * 512, dtype=torch.float32, device=dev)
+    cst = torch.zeros(224 * 8 * 4, dtype=torch.int64, device=dev)
+
+    def ceil():
+        if L.tx_ceiling_mfma_fp8_stamped(seed_t.data_ptr(), 224, 56, cout.data_ptr(),
+                                         cst.data_ptr(), stream) != 0:
+            raise RuntimeError("tx_ceiling_mfma_fp8_stamped failed")
+    cms = time_back_to_back(ceil, steps, warmup)
+    cw = cst.view(224, 8, 4).cpu().numpy().astype(np.int64)
+    c_us = (cw[:, :, 1] - cw[:, :, 0]) / 100.0
+    c_cyc = (cw[:, :, 3] - cw[:, :, 2]).astype(np.float64)
+    # waves w and w + 4 of a workgroup share SIMD w: the union of their loops
+    span = np.maximum(cw[:, :4, 3], cw[:, 4:, 3]) - np.minimum(cw[:, :4, 2], cw[:, 4:, 2])
+    out[0]["ceiling"] = {"ms": cms, "loop_ghz": round(float(np.mean(c_cyc / (c_us * 1e3))), 3),
+                         "simd_mfma_busy_in_loop": round(float(np.mean(2 * 1024.0 * 56 / span)), 4)}
     return out
 
 
@@ -833,6 +951,26 @@ def main():
               + ", ".join(f"{k}: {v['mfma_phase']:.0f}+{v['load_and_lds_wait']:.0f}+{v['barrier']:.0f}"
                           for k, v in r["step_cycles"].items()),
               file=sys.stderr, flush=True)
+    if "phases8" in only:
+        for r in bench_phases8(dev, args.steps, args.warmup):
+            secondary.append(r)
+            f = r["wave_time"]
+            print(f"# {r['workload']}: {r['ms_stamped'] * 1e3:.1f} us/launch "
+                  f"({r['tflops_stamped']:.0f} T/s); wave-time: MFMA in loop "
+                  f"{100 * f['mfma_in_loop']:.1f}%, loop other {100 * f['loop_other']:.1f}%, "
+                  f"prologue {100 * f['prologue']:.1f}%, epilogue {100 * f['epilogue']:.1f}% + "
+                  f"drain {100 * f['store_drain']:.1f}%, skew "
+                  f"{100 * (f['before_entry'] + f['after_own_end']):.1f}%, between launches "
+                  f"{100 * f['between_launches']:.1f}%; loop {r['loop_ghz']:.2f} GHz, SIMD "
+                  f"{100 * r['simd_mfma_busy_in_loop']:.1f}% MFMA busy"
+                  + (f" (ceiling loop {r['ceiling']['loop_ghz']:.2f} GHz, "
+                     f"{100 * r['ceiling']['simd_mfma_busy_in_loop']:.1f}%)" if "ceiling" in r else "")
+                  + "; per step (cycles) "
+                  + ", ".join(f"{k}: {v['mfma_phase']:.0f}+{v['load_and_lds_wait']:.0f}+{v['barrier']:.0f}"
+                              for k, v in r["step_cycles"].items())
+                  + f"; A and B loads alone {r['operand_stream']['ms'] * 1e3:.1f} us "
+                  f"({r['operand_stream']['gb_per_s_per_cu']:.1f} GB/s per CU)",
+                  file=sys.stderr, flush=True)
     ceil = {}
     if want("ceiling"):
         for zeros in (False, True):

@@ -34,7 +34,7 @@
 
 // Phase stamps: empty in the library.  A measurement build defines them
 // before including this header (bench.py's libtx_ceilings.so) to time a
-// tile's phases per wave:
+// tile's phases per wave (gemm8_w4.h takes the same hooks):
 //   TX_PHASE_STAMP(i): i = 0 at entry, 1 once step 0 has landed, 2 after the
 //     K loop, 3 after the epilogue's stores are issued, 4 after
 //     TX_PHASE_DRAIN() (their acknowledgement);

@@ -330,6 +330,7 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WN, wn = wave % WN;
+    TX_PHASE_STAMP(0);
     Acc acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -408,6 +409,7 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
       part_of(0, std::integral_constant<int, 2>());
       part_of(0, std::integral_constant<int, 3>());
       step_barrier();
+      TX_PHASE_STAMP(1);
       part_of(1, std::integral_constant<int, 0>());
       i32x8_t b[FN];
       int sbx[FN]; // MX: B scale operands of the step
@@ -450,7 +452,7 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
               sxn = tail_sx(sxn, kt, ng);
           }
           if (more && i == FM - 1) {
-            step_barrier();
+            TX_PHASE_STEP_BARRIER(kt, step_barrier);
             part_of(kt + 2, std::integral_constant<int, 0>());
           }
           Acc Q[FN];
@@ -494,10 +496,14 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
       flush(acc[FM - 1]);
       __builtin_amdgcn_s_waitcnt(0x7 << 4);
     }
+    TX_PHASE_STAMP(2);
     if constexpr (!MASK_MN)
       epilogue_lds(p, m0, n0, wm, wn, acc, lds0);
     else
       epilogue<MASK_MN>(p, m0, n0, wm, wn, acc);
+    TX_PHASE_STAMP(3);
+    TX_PHASE_DRAIN();
+    TX_PHASE_STAMP(4);
   }
 
   // Epilogue of an interior tile through LDS (the two stages are free once

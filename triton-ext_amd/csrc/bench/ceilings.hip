@@ -14,11 +14,13 @@
 //     the ceiling the power-limited clock leaves for the dot's MFMA stream.
 //   * tx_ceiling_mfma_fp8: the same for the 8-bit 256x256x128 tile (8 waves
 //     of 8 x 4 blocks of v_mfma_f32_16x16x128_f8f6f4 per K step, e4m3).
-//   * tx_phases_bf16: the bf16 256x256 tile kernel itself, built here with
-//     its phase stamps on (s_memrealtime, a 100 MHz wall clock, and
-//     s_memtime, the shader clock, per wave at entry, step 0 landed, K loop
-//     done, epilogue issued, stores acknowledged; optionally around one
-//     step's barrier), so that bench.py can say where a launch's time goes.
+//   * tx_phases_bf16 / tx_phases_8bit: the bf16 256x256 tile kernel and the
+//     8-bit 256x256x128 tile kernel (fp8 block-scaled, int8 -> int32)
+//     themselves, built here with their phase stamps on (s_memrealtime, a
+//     100 MHz wall clock, and s_memtime, the shader clock, per wave at
+//     entry, step 0 landed, K loop done, epilogue issued, stores
+//     acknowledged; optionally around one step's barrier), so that bench.py
+//     can say where a launch's time goes.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -36,7 +38,8 @@
 __constant__ uint64_t *g_phase_buf;
 __constant__ int g_phase_step;
 
-#define TX_PHASE_WORDS(wave) (g_phase_buf + ((int64_t)blockIdx.x * 4 + (wave)) * 16)
+#define TX_PHASE_WORDS(wave)                                                               \
+  (g_phase_buf + ((int64_t)blockIdx.x * (blockDim.x >> 6) + (wave)) * 16)
 #define TX_PHASE_STAMP(i)                                                                      \
   do {                                                                                         \
     const uint64_t rt_ = __builtin_amdgcn_s_memrealtime();                                     \
@@ -78,7 +81,7 @@ __constant__ int g_phase_step;
       }                                                                                        \
     }                                                                                          \
   } while (0)
-#include "backend/mi355x/gemm16_w4.h"
+#include "backend/mi355x/gemm8_w4.h"
 
 namespace {
 
@@ -209,8 +212,9 @@ __global__ void __launch_bounds__(256, 1) phases_bf16_kernel(txk::GemmArgs p) {
 // fp8 MFMA ceiling: 8 waves per workgroup, 8 x 4 accumulators of 16x16 per
 // wave (128x64), one v_mfma_f32_16x16x128_f8f6f4 (e4m3 x e4m3, unit scales)
 // per block and K step, operands from `seed` kept in registers.
+template <bool STAMP>
 __global__ void __launch_bounds__(512, 1) mfma_fp8_kernel(const i32x8_t *seed, int ksteps,
-                                                          float *out) {
+                                                          float *out, uint64_t *st) {
   const int lane = threadIdx.x & 63;
   const i32x8_t *s = seed + ((blockIdx.x * 8 + (threadIdx.x >> 6)) % 64) * 12 * 64 + lane;
   i32x8_t a[8], b[4];
@@ -226,6 +230,12 @@ __global__ void __launch_bounds__(512, 1) mfma_fp8_kernel(const i32x8_t *seed, i
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  uint64_t r0 = 0, m0 = 0;
+  if constexpr (STAMP) {
+    __builtin_amdgcn_s_waitcnt(0);
+    r0 = __builtin_amdgcn_s_memrealtime();
+    m0 = __builtin_amdgcn_s_memtime();
+  }
   for (int kt = 0; kt < ksteps; ++kt) {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
@@ -240,7 +250,58 @@ __global__ void __launch_bounds__(512, 1) mfma_fp8_kernel(const i32x8_t *seed, i
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       t += acc[i][j][0] + acc[i][j][1] + acc[i][j][2] + acc[i][j][3];
+  if constexpr (STAMP) {
+    const uint64_t r1 = __builtin_amdgcn_s_memrealtime(), m1 = __builtin_amdgcn_s_memtime();
+    if (lane == 0) {
+      uint64_t *w = st + ((int64_t)blockIdx.x * 8 + (threadIdx.x >> 6)) * 4;
+      w[0] = r0;
+      w[1] = r1;
+      w[2] = m0;
+      w[3] = m1;
+    }
+  }
   out[(size_t)blockIdx.x * 512 + threadIdx.x] = t;
+}
+
+// The 8-bit tile with its phase stamps: fp8 block-scaled (bf16 C), or int8
+// with int32 C.
+template <int OP, int EPI>
+__global__ void __launch_bounds__(512, 1) phases_8bit_kernel(txk::GemmArgs p) {
+  typedef txk::Gemm8W4<OP, EPI> G;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * G::STAGE];
+  int tm, tn;
+  txk::tile_coords(p, tm, tn);
+  G::template run<false>(p, (int64_t)tm * G::BM, (int64_t)tn * G::BN, smem);
+}
+
+// The 8-bit tile's operand stream alone: each K step's 64 KiB of A and B
+// loads (the tile's own lane offsets and tile order) into two LDS stages,
+// nothing reading them.  Step kt's loads go out once step kt-1's have landed
+// (vmcnt: one step in flight behind the newest, as in the tile), then every
+// wave meets at the barrier.  The stage contents are never read, so a stage
+// refilled while an older load into it is in flight changes nothing timed.
+__global__ void __launch_bounds__(512, 1) operand_stream_8bit_kernel(txk::GemmArgs p) {
+  typedef txk::Gemm8W4<txk::OP_I8, txk::EPI_I32> G;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * G::STAGE];
+  int tm, tn;
+  txk::tile_coords(p, tm, tn);
+  const int64_t m0 = (int64_t)tm * G::BM, n0 = (int64_t)tn * G::BN;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t lds0 = txk::lds_addr(smem);
+  const txk::i32x4_t ra = txk::make_rsrc(p.A, (uint32_t)((p.M - 1) * p.lda + p.K));
+  const txk::i32x4_t rb = txk::make_rsrc(p.B, (uint32_t)((p.K - 1) * p.ldb + p.N));
+  const txk::i32x4_t z = {0, 0, 0, 0};
+  for (int kt = 0; kt < p.k_main_steps; ++kt) {
+    const uint32_t st = lds0 + (kt & 1) * G::STAGE;
+    G::template issue_part<false, false, 0>(p, m0, n0, ra, rb, z, z, kt, st, wave, true);
+    G::template issue_part<false, false, 1>(p, m0, n0, ra, rb, z, z, kt, st, wave, true);
+    G::template issue_part<false, false, 2>(p, m0, n0, ra, rb, z, z, kt, st, wave, true);
+    G::template issue_part<false, false, 3>(p, m0, n0, ra, rb, z, z, kt, st, wave, true);
+    // 8 loads a wave a step: vmcnt(8) leaves only this step's in flight
+    __builtin_amdgcn_s_waitcnt((8 & 15) | (7 << 4) | (15 << 8));
+    __syncthreads();
+  }
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
 }
 
 extern "C" int tx_ceiling_read(const void *buf, size_t bytes, int variant, void *sink,
@@ -332,7 +393,79 @@ extern "C" int tx_ceiling_mfma_fp8(const void *seed, int tiles, int ksteps, floa
                                    void *stream) {
   if (!seed || !out || tiles <= 0 || ksteps < 0 || (reinterpret_cast<uintptr_t>(seed) & 31))
     return 1;
-  hipLaunchKernelGGL(mfma_fp8_kernel, dim3(tiles), dim3(512), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const i32x8_t *>(seed), ksteps, out);
+  hipLaunchKernelGGL(mfma_fp8_kernel<false>, dim3(tiles), dim3(512), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const i32x8_t *>(seed), ksteps,
+                     out, nullptr);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+extern "C" int tx_ceiling_mfma_fp8_stamped(const void *seed, int tiles, int ksteps, float *out,
+                                           uint64_t *stamps, void *stream) {
+  if (!seed || !out || !stamps || tiles <= 0 || ksteps < 0 ||
+      (reinterpret_cast<uintptr_t>(seed) & 31))
+    return 1;
+  hipLaunchKernelGGL(mfma_fp8_kernel<true>, dim3(tiles), dim3(512), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const i32x8_t *>(seed), ksteps,
+                     out, stamps);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+extern "C" int tx_phases_8bit(int kind, const void *A, const void *B, void *C, const void *sa,
+                              const void *sb, int tiles_m, int tiles_n, int ksteps, int group_m,
+                              int launches, void *stream) {
+  if (!A || !B || !C || (kind != 0 && kind != 1) || (kind == 0 && (!sa || !sb)) ||
+      tiles_m <= 0 || tiles_n <= 0 || ksteps < 2 || group_m <= 0 || launches <= 0 ||
+      (int64_t)tiles_m * tiles_n > 65536 || (int64_t)ksteps * 128 > 65536)
+    return 1;
+  txk::GemmArgs a{};
+  a.A = static_cast<const uint8_t *>(A);
+  a.B = static_cast<const uint8_t *>(B);
+  a.C = C;
+  a.sa = static_cast<const float *>(sa);
+  a.sb = static_cast<const float *>(sb);
+  a.M = (int64_t)tiles_m * 256;
+  a.N = (int64_t)tiles_n * 256;
+  a.K = (int64_t)ksteps * 128;
+  a.lda = a.K;
+  a.ldb = a.N;
+  a.ldc = a.N;
+  a.tiles_m = tiles_m;
+  a.tiles_n = tiles_n;
+  a.k_main_steps = ksteps;
+  a.k_masked_steps = 0;
+  a.last_ks = 1;
+  a.group_m = group_m < tiles_m ? group_m : tiles_m;
+  a.sa_ld = ksteps;            // sa [M][K / 128]
+  a.sb_ld = tiles_n * 2;       // sb [K / 128][N / 128]
+  auto fn = kind == 0 ? phases_8bit_kernel<txk::OP_F8, txk::EPI_BLOCK128_BF16>
+                      : phases_8bit_kernel<txk::OP_I8, txk::EPI_I32>;
+  for (int i = 0; i < launches; ++i)
+    hipLaunchKernelGGL(fn, dim3(tiles_m * tiles_n), dim3(512), 0,
+                       static_cast<hipStream_t>(stream), a);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+extern "C" int tx_ceiling_operand_stream_8bit(const void *A, const void *B, int tiles_m,
+                                              int tiles_n, int ksteps, int group_m, int launches,
+                                              void *stream) {
+  if (!A || !B || tiles_m <= 0 || tiles_n <= 0 || ksteps <= 0 || group_m <= 0 || launches <= 0 ||
+      (int64_t)tiles_m * tiles_n > 65536 || (int64_t)ksteps * 128 > 65536)
+    return 1;
+  txk::GemmArgs a{};
+  a.A = static_cast<const uint8_t *>(A);
+  a.B = static_cast<const uint8_t *>(B);
+  a.M = (int64_t)tiles_m * 256;
+  a.N = (int64_t)tiles_n * 256;
+  a.K = (int64_t)ksteps * 128;
+  a.lda = a.K;
+  a.ldb = a.N;
+  a.ldc = a.N;
+  a.tiles_m = tiles_m;
+  a.tiles_n = tiles_n;
+  a.k_main_steps = ksteps;
+  a.group_m = group_m < tiles_m ? group_m : tiles_m;
+  for (int i = 0; i < launches; ++i)
+    hipLaunchKernelGGL(operand_stream_8bit_kernel, dim3(tiles_m * tiles_n), dim3(512), 0,
+                       static_cast<hipStream_t>(stream), a);
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }

@@ -39,8 +39,9 @@ __attribute__((visibility("default"))) int tx_ceiling_mfma_bf16_stamped(const vo
                                                                         uint64_t *stamps,
                                                                         void *stream);
 
-/* Where the stamps of tx_phases_bf16 go: 16 words per wave (tiles_m *
- * tiles_n * 4 waves), written by every launch, so the last one's remain:
+/* Where the stamps of tx_phases_bf16 (and tx_phases_8bit) go: 16 words per
+ * wave (tiles_m * tiles_n * 4 waves; 8 for the 8-bit tile), written by
+ * every launch, so the last one's remain:
  * [0..4] the wall clock (s_memrealtime, 100 MHz) at entry, step 0 landed, K
  * loop done, epilogue issued, stores acknowledged; [5] XCC_ID << 32 |
  * HW_ID; [6] workgroup; [8..12] the shader clock (s_memtime) at the same
@@ -58,6 +59,37 @@ __attribute__((visibility("default"))) int tx_phases_bf16(const void *A, const v
                                                           int tiles_m, int tiles_n, int ksteps,
                                                           int group_m, int launches,
                                                           void *stream);
+
+/* `launches` back-to-back launches of the 8-bit 256x256x128 tile kernel
+ * (the library's gemm8_w4_kernel, built here with its phase stamps): kind 0
+ * fp8 e4m3 with 128-block scales (sa [M][K/128], sb [K/128][N/128] fp32) and
+ * bf16 C, kind 1 int8 with int32 C (no scales); all row-major and packed,
+ * M = 256 tiles_m, N = 256 tiles_n, K = 128 ksteps.  Stamps as for
+ * tx_phases_bf16, 8 waves a workgroup, through tx_phases_bf16_setup. */
+__attribute__((visibility("default"))) int tx_phases_8bit(int kind, const void *A, const void *B,
+                                                          void *C, const void *sa,
+                                                          const void *sb, int tiles_m,
+                                                          int tiles_n, int ksteps, int group_m,
+                                                          int launches, void *stream);
+
+/* tx_ceiling_mfma_fp8 with the stamps of tx_ceiling_mfma_bf16_stamped, 8
+ * waves a workgroup. */
+__attribute__((visibility("default"))) int tx_ceiling_mfma_fp8_stamped(const void *seed,
+                                                                       int tiles, int ksteps,
+                                                                       float *out,
+                                                                       uint64_t *stamps,
+                                                                       void *stream);
+
+/* The 8-bit 256x256x128 tile's operand loads alone: `launches` launches of
+ * tiles_m x tiles_n workgroups of 8 waves, each loading its tile's A
+ * [256][128] and B [128][256] bytes of every K step into LDS through the
+ * tile's own load code and order (one step in flight behind the newest, a
+ * barrier a step), no MFMAs, nothing read back.  A [256 tiles_m][128 ksteps]
+ * and B [128 ksteps][256 tiles_n] row-major, 8-bit.  0 launched; 1 bad
+ * argument; 3 launch error. */
+__attribute__((visibility("default"))) int tx_ceiling_operand_stream_8bit(
+    const void *A, const void *B, int tiles_m, int tiles_n, int ksteps, int group_m, int launches,
+    void *stream);
 
 /* `tiles` workgroups of 8 waves, each running `ksteps` x 32 MFMAs
  * v_mfma_f32_16x16x128_f8f6f4 (e4m3) per wave on operands read once from
