@@ -697,18 +697,31 @@ def bench_phases(dev, a, b, c, group_m, steps, warmup, seed=1):
 
 def bench_phases8(dev, steps, warmup, seed=5):
     """Where a launch of the 8-bit 256x256x128 tile goes, for C5 (fp8 block-scaled
-    2048x7168x7168, bf16 C) and int8 4096^3 (int32 C): libtx_ceilings.so builds
-    gemm8_w4_kernel with its phase stamps on, as bench_phases does for the bf16 tile.  A
-    wave runs 8 x 4 blocks a step, one v_mfma_f32_16x16x128_f8f6f4 (fp8) or two
-    v_mfma_i32_16x16x64_i8 (int8) each: 1024 MFMA cycles a step, two waves a SIMD.  The
-    C5 schedule's MFMA-only ceiling loop is stamped alike for its clock and busy."""
+    2048x7168x7168, bf16 C), int8 4096^3 (int32 C) and MX e4m3 / e2m1 4096^3 (fp32 C):
+    libtx_ceilings.so builds gemm8_w4_kernel with its phase stamps on, as bench_phases
+    does for the bf16 tile.  A wave runs 8 x 4 blocks a step (128 bytes of K), one
+    v_mfma_f32_16x16x128_f8f6f4 (fp8), two v_mfma_i32_16x16x64_i8 (int8) or two
+    e2m1 v_mfma_scale_f32_16x16x128_f8f6f4 each: 1024 MFMA cycles a step, two waves a
+    SIMD.  The C5 schedule's MFMA-only ceiling loop is stamped alike for its clock and
+    busy."""
     import numpy as np
     import torch
     L = ceilings_lib()
     stream = torch.cuda.current_stream().cuda_stream
     out = []
-    for kind, (M, N, K) in ((0, (2048, 7168, 7168)), (1, (4096, 4096, 4096))):
-        if kind == 0:
+    for kind, (M, N, K) in ((0, (2048, 7168, 7168)), (1, (4096, 4096, 4096)),
+                            (2, (4096, 4096, 4096)), (3, (4096, 4096, 4096))):
+        kb = K // 2 if kind == 3 else K  # bytes of K (e2m1: two per byte)
+        if kind >= 2:
+            fmt = "e4m3" if kind == 2 else "e2m1"
+            g = torch.Generator(device=dev)
+            g.manual_seed(seed)
+            a, sa = mx_quantize(torch.randn((M, K), generator=g, device=dev), fmt)
+            qbt, sb = mx_quantize(torch.randn((N, K), generator=g, device=dev), fmt)
+            b = qbt.t().contiguous()
+            c = torch.empty((M, N), dtype=torch.float32, device=dev)
+            name = f"MX {fmt} (e8m0 per 32, fp32 C)"
+        elif kind == 0:
             a, b, sa, sb = fp8_block_inputs_dev(M, N, K, dev, seed)
             c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
             name = "fp8 block-scaled (C5)"
@@ -720,7 +733,7 @@ def bench_phases8(dev, steps, warmup, seed=5):
             sa = sb = None
             c = torch.empty((M, N), dtype=torch.int32, device=dev)
             name = "int8 -> int32"
-        tm, tn, ks = M // 256, N // 256, K // 128
+        tm, tn, ks = M // 256, N // 256, kb // 128
         waves = tm * tn * 8
         st = torch.zeros(waves * 16, dtype=torch.int64, device=dev)
         if L.tx_phases_bf16_setup(st.data_ptr(), -1) != 0:

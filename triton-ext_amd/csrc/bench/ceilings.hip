@@ -263,11 +263,11 @@ __global__ void __launch_bounds__(512, 1) mfma_fp8_kernel(const i32x8_t *seed, i
   out[(size_t)blockIdx.x * 512 + threadIdx.x] = t;
 }
 
-// The 8-bit tile with its phase stamps: fp8 block-scaled (bf16 C), or int8
-// with int32 C.
-template <int OP, int EPI>
+// The 8-bit tile with its phase stamps: fp8 block-scaled (bf16 C), int8
+// with int32 C, or MX (e8m0 per 32) e4m3 or e2m1 with fp32 C.
+template <int OP, int EPI, int FA = 0, int FB = 0>
 __global__ void __launch_bounds__(512, 1) phases_8bit_kernel(txk::GemmArgs p) {
-  typedef txk::Gemm8W4<OP, EPI> G;
+  typedef txk::Gemm8W4<OP, EPI, FA, FB> G;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * G::STAGE];
   int tm, tn;
   txk::tile_coords(p, tm, tn);
@@ -413,7 +413,7 @@ extern "C" int tx_ceiling_mfma_fp8_stamped(const void *seed, int tiles, int kste
 extern "C" int tx_phases_8bit(int kind, const void *A, const void *B, void *C, const void *sa,
                               const void *sb, int tiles_m, int tiles_n, int ksteps, int group_m,
                               int launches, void *stream) {
-  if (!A || !B || !C || (kind != 0 && kind != 1) || (kind == 0 && (!sa || !sb)) ||
+  if (!A || !B || !C || kind < 0 || kind > 3 || (kind != 1 && (!sa || !sb)) ||
       tiles_m <= 0 || tiles_n <= 0 || ksteps < 2 || group_m <= 0 || launches <= 0 ||
       (int64_t)tiles_m * tiles_n > 65536 || (int64_t)ksteps * 128 > 65536)
     return 1;
@@ -437,8 +437,12 @@ extern "C" int tx_phases_8bit(int kind, const void *A, const void *B, void *C, c
   a.group_m = group_m < tiles_m ? group_m : tiles_m;
   a.sa_ld = ksteps;            // sa [M][K / 128]
   a.sb_ld = tiles_n * 2;       // sb [K / 128][N / 128]
-  auto fn = kind == 0 ? phases_8bit_kernel<txk::OP_F8, txk::EPI_BLOCK128_BF16>
-                      : phases_8bit_kernel<txk::OP_I8, txk::EPI_I32>;
+  if (kind >= 2)               // MX: e8m0 bytes [M][K / 32], [N][K / 32] (fp4: 256 a step)
+    a.sa_ld = ksteps * (kind == 3 ? 8 : 4);
+  auto fn = kind == 0   ? phases_8bit_kernel<txk::OP_F8, txk::EPI_BLOCK128_BF16>
+            : kind == 1 ? phases_8bit_kernel<txk::OP_I8, txk::EPI_I32>
+            : kind == 2 ? phases_8bit_kernel<txk::OP_F8, txk::EPI_MX_F32>
+                        : phases_8bit_kernel<txk::OP_F8, txk::EPI_MX_F32, 4, 4>;
   for (int i = 0; i < launches; ++i)
     hipLaunchKernelGGL(fn, dim3(tiles_m * tiles_n), dim3(512), 0,
                        static_cast<hipStream_t>(stream), a);

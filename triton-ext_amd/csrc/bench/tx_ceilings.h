@@ -63,8 +63,10 @@ __attribute__((visibility("default"))) int tx_phases_bf16(const void *A, const v
 /* `launches` back-to-back launches of the 8-bit 256x256x128 tile kernel
  * (the library's gemm8_w4_kernel, built here with its phase stamps): kind 0
  * fp8 e4m3 with 128-block scales (sa [M][K/128], sb [K/128][N/128] fp32) and
- * bf16 C, kind 1 int8 with int32 C (no scales); all row-major and packed,
- * M = 256 tiles_m, N = 256 tiles_n, K = 128 ksteps.  Stamps as for
+ * bf16 C, kind 1 int8 with int32 C (no scales), kind 2 MX e4m3 and kind 3
+ * MX e2m1 (two per byte) with e8m0 scales per 32 elements (sa [M][K/32],
+ * sb [N][K/32] bytes) and fp32 C; all row-major and packed, M = 256
+ * tiles_m, N = 256 tiles_n, K = 128 ksteps bytes.  Stamps as for
  * tx_phases_bf16, 8 waves a workgroup, through tx_phases_bf16_setup. */
 __attribute__((visibility("default"))) int tx_phases_8bit(int kind, const void *A, const void *B,
                                                           void *C, const void *sa,
