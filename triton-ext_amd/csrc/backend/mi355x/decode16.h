@@ -94,10 +94,12 @@ template <int SR> struct Decode16Cfg {
 // wave's B fragments (two transposed reads a step, at `blo` / `bhi` and
 // +4 KiB for the second step) and its T A fragments (ds_read_b128 at `a0` /
 // `a1`, +4 KiB per 16-row tile), waiting for them before the block ends.
+// Outputs are early-clobber: a read lands while later reads of the block
+// still use their address registers.
 #define TX_D16_TR                                                                           \
   "ds_read_b64_tr_b16 %0, %[blo]\n\tds_read_b64_tr_b16 %1, %[bhi]\n\t"                      \
   "ds_read_b64_tr_b16 %2, %[blo] offset:4096\n\tds_read_b64_tr_b16 %3, %[bhi] offset:4096\n\t"
-#define TX_D16_OUT "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1])
+#define TX_D16_OUT "=&v"(lo[0]), "=&v"(hi[0]), "=&v"(lo[1]), "=&v"(hi[1])
 #define TX_D16_IN [blo] "v"(blo), [bhi] "v"(bhi), [a0] "v"(a0), [a1] "v"(a1)
 template <int T>
 __device__ __forceinline__ void dec16_read_pair(uint32_t blo, uint32_t bhi, uint32_t a0,
@@ -106,14 +108,14 @@ __device__ __forceinline__ void dec16_read_pair(uint32_t blo, uint32_t bhi, uint
   if constexpr (T == 1)
     asm volatile(TX_D16_TR "ds_read_b128 %4, %[a0]\n\tds_read_b128 %5, %[a1]\n\t"
                            "s_waitcnt lgkmcnt(0)"
-                 : TX_D16_OUT, "=v"(a[0][0]), "=v"(a[1][0])
+                 : TX_D16_OUT, "=&v"(a[0][0]), "=&v"(a[1][0])
                  : TX_D16_IN
                  : "memory");
   else if constexpr (T == 2)
     asm volatile(TX_D16_TR "ds_read_b128 %4, %[a0]\n\tds_read_b128 %5, %[a0] offset:4096\n\t"
                            "ds_read_b128 %6, %[a1]\n\tds_read_b128 %7, %[a1] offset:4096\n\t"
                            "s_waitcnt lgkmcnt(0)"
-                 : TX_D16_OUT, "=v"(a[0][0]), "=v"(a[0][1]), "=v"(a[1][0]), "=v"(a[1][1])
+                 : TX_D16_OUT, "=&v"(a[0][0]), "=&v"(a[0][1]), "=&v"(a[1][0]), "=&v"(a[1][1])
                  : TX_D16_IN
                  : "memory");
   else if constexpr (T == 3)
@@ -122,8 +124,8 @@ __device__ __forceinline__ void dec16_read_pair(uint32_t blo, uint32_t bhi, uint
                            "ds_read_b128 %7, %[a1]\n\tds_read_b128 %8, %[a1] offset:4096\n\t"
                            "ds_read_b128 %9, %[a1] offset:8192\n\t"
                            "s_waitcnt lgkmcnt(0)"
-                 : TX_D16_OUT, "=v"(a[0][0]), "=v"(a[0][1]), "=v"(a[0][2]), "=v"(a[1][0]),
-                   "=v"(a[1][1]), "=v"(a[1][2])
+                 : TX_D16_OUT, "=&v"(a[0][0]), "=&v"(a[0][1]), "=&v"(a[0][2]), "=&v"(a[1][0]),
+                   "=&v"(a[1][1]), "=&v"(a[1][2])
                  : TX_D16_IN
                  : "memory");
   else
@@ -134,8 +136,8 @@ __device__ __forceinline__ void dec16_read_pair(uint32_t blo, uint32_t bhi, uint
                            "ds_read_b128 %10, %[a1] offset:8192\n\t"
                            "ds_read_b128 %11, %[a1] offset:12288\n\t"
                            "s_waitcnt lgkmcnt(0)"
-                 : TX_D16_OUT, "=v"(a[0][0]), "=v"(a[0][1]), "=v"(a[0][2]), "=v"(a[0][3]),
-                   "=v"(a[1][0]), "=v"(a[1][1]), "=v"(a[1][2]), "=v"(a[1][3])
+                 : TX_D16_OUT, "=&v"(a[0][0]), "=&v"(a[0][1]), "=&v"(a[0][2]), "=&v"(a[0][3]),
+                   "=&v"(a[1][0]), "=&v"(a[1][1]), "=&v"(a[1][2]), "=&v"(a[1][3])
                  : TX_D16_IN
                  : "memory");
 }

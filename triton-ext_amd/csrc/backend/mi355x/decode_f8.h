@@ -97,15 +97,16 @@ template <int SR, bool SCALED> struct DecodeF8Cfg {
 // The wave's operands of one batch: the two column blocks' B fragments (four
 // transposed reads each, at b0 / b1 + 1 KiB q) and the T row tiles' A
 // fragments (two 16-byte reads each, at a0 and a0 ^ 16, +2 KiB per tile),
-// waiting for them before the block ends.
+// waiting for them before the block ends.  Outputs are early-clobber: a
+// read lands while later reads of the block still use their address registers.
 #define TX_D8_TR                                                                           \
   "ds_read_b64_tr_b8 %0, %[b0]\n\tds_read_b64_tr_b8 %1, %[b0] offset:1024\n\t"             \
   "ds_read_b64_tr_b8 %2, %[b0] offset:2048\n\tds_read_b64_tr_b8 %3, %[b0] offset:3072\n\t" \
   "ds_read_b64_tr_b8 %4, %[b1]\n\tds_read_b64_tr_b8 %5, %[b1] offset:1024\n\t"             \
   "ds_read_b64_tr_b8 %6, %[b1] offset:2048\n\tds_read_b64_tr_b8 %7, %[b1] offset:3072\n\t"
 #define TX_D8_OUT                                                                         \
-  "=v"(bq[0][0]), "=v"(bq[0][1]), "=v"(bq[0][2]), "=v"(bq[0][3]), "=v"(bq[1][0]),        \
-      "=v"(bq[1][1]), "=v"(bq[1][2]), "=v"(bq[1][3])
+  "=&v"(bq[0][0]), "=&v"(bq[0][1]), "=&v"(bq[0][2]), "=&v"(bq[0][3]), "=&v"(bq[1][0]),        \
+      "=&v"(bq[1][1]), "=&v"(bq[1][2]), "=&v"(bq[1][3])
 #define TX_D8_IN [b0] "v"(b0), [b1] "v"(b1), [a0] "v"(a0), [a1] "v"(a1)
 template <int T>
 __device__ __forceinline__ void dec8_read(uint32_t b0, uint32_t b1, uint32_t a0, uint32_t a1,
@@ -113,14 +114,14 @@ __device__ __forceinline__ void dec8_read(uint32_t b0, uint32_t b1, uint32_t a0,
   if constexpr (T == 1)
     asm volatile(TX_D8_TR "ds_read_b128 %8, %[a0]\n\tds_read_b128 %9, %[a1]\n\t"
                           "s_waitcnt lgkmcnt(0)"
-                 : TX_D8_OUT, "=v"(a[0][0]), "=v"(a[0][1])
+                 : TX_D8_OUT, "=&v"(a[0][0]), "=&v"(a[0][1])
                  : TX_D8_IN
                  : "memory");
   else if constexpr (T == 2)
     asm volatile(TX_D8_TR "ds_read_b128 %8, %[a0]\n\tds_read_b128 %9, %[a1]\n\t"
                           "ds_read_b128 %10, %[a0] offset:2048\n\tds_read_b128 %11, %[a1] offset:2048\n\t"
                           "s_waitcnt lgkmcnt(0)"
-                 : TX_D8_OUT, "=v"(a[0][0]), "=v"(a[0][1]), "=v"(a[1][0]), "=v"(a[1][1])
+                 : TX_D8_OUT, "=&v"(a[0][0]), "=&v"(a[0][1]), "=&v"(a[1][0]), "=&v"(a[1][1])
                  : TX_D8_IN
                  : "memory");
   else if constexpr (T == 3)
@@ -128,8 +129,8 @@ __device__ __forceinline__ void dec8_read(uint32_t b0, uint32_t b1, uint32_t a0,
                           "ds_read_b128 %10, %[a0] offset:2048\n\tds_read_b128 %11, %[a1] offset:2048\n\t"
                           "ds_read_b128 %12, %[a0] offset:4096\n\tds_read_b128 %13, %[a1] offset:4096\n\t"
                           "s_waitcnt lgkmcnt(0)"
-                 : TX_D8_OUT, "=v"(a[0][0]), "=v"(a[0][1]), "=v"(a[1][0]), "=v"(a[1][1]),
-                   "=v"(a[2][0]), "=v"(a[2][1])
+                 : TX_D8_OUT, "=&v"(a[0][0]), "=&v"(a[0][1]), "=&v"(a[1][0]), "=&v"(a[1][1]),
+                   "=&v"(a[2][0]), "=&v"(a[2][1])
                  : TX_D8_IN
                  : "memory");
   else
@@ -138,8 +139,8 @@ __device__ __forceinline__ void dec8_read(uint32_t b0, uint32_t b1, uint32_t a0,
                           "ds_read_b128 %12, %[a0] offset:4096\n\tds_read_b128 %13, %[a1] offset:4096\n\t"
                           "ds_read_b128 %14, %[a0] offset:6144\n\tds_read_b128 %15, %[a1] offset:6144\n\t"
                           "s_waitcnt lgkmcnt(0)"
-                 : TX_D8_OUT, "=v"(a[0][0]), "=v"(a[0][1]), "=v"(a[1][0]), "=v"(a[1][1]),
-                   "=v"(a[2][0]), "=v"(a[2][1]), "=v"(a[3][0]), "=v"(a[3][1])
+                 : TX_D8_OUT, "=&v"(a[0][0]), "=&v"(a[0][1]), "=&v"(a[1][0]), "=&v"(a[1][1]),
+                   "=&v"(a[2][0]), "=&v"(a[2][1]), "=&v"(a[3][0]), "=&v"(a[3][1])
                  : TX_D8_IN
                  : "memory");
 }
@@ -275,12 +276,12 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_f8_kernel(DecodeF
     if constexpr (SCALED) {
       const uint32_t sb_addr = base + Cfg::SCL_OFF + 256;
       float v;
-      asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(sb_addr) : "memory");
+      asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(sb_addr) : "memory");
       s_col = v;
 #pragma unroll
       for (int t = 0; t < T; ++t) {
         const uint32_t sa_addr = base + Cfg::SCL_OFF + 4 * (16 * t + L);
-        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(sa_addr) : "memory");
+        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(sa_addr) : "memory");
         s_row[t] = v * s_col;
       }
     }

@@ -122,24 +122,26 @@ template <int C> __device__ __forceinline__ void wait_vmcnt() {
 
 // ds_read_b128 of MT consecutive KiB at `addr` (a lane's 16 bytes each),
 // waiting for them in the same asm block: the compiler sees the values
-// defined only once they are in the registers.
+// defined only once they are in the registers.  Outputs are early-clobber
+// ("=&v"): a read's data lands while later reads of the block still use
+// their address registers, so no output may share a register with an input.
 template <int MT>
 __device__ __forceinline__ void lds_read_a(uint32_t addr, i32x4_t (&a)[MT]) {
   if constexpr (MT == 1)
-    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(a[0]) : "v"(addr) : "memory");
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(a[0]) : "v"(addr) : "memory");
   else if constexpr (MT == 2)
     asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:1024\n\t"
                  "s_waitcnt lgkmcnt(0)"
-                 : "=v"(a[0]), "=v"(a[1]) : "v"(addr) : "memory");
+                 : "=&v"(a[0]), "=&v"(a[1]) : "v"(addr) : "memory");
   else if constexpr (MT == 3)
     asm volatile("ds_read_b128 %0, %3\n\tds_read_b128 %1, %3 offset:1024\n\t"
                  "ds_read_b128 %2, %3 offset:2048\n\ts_waitcnt lgkmcnt(0)"
-                 : "=v"(a[0]), "=v"(a[1]), "=v"(a[2]) : "v"(addr) : "memory");
+                 : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]) : "v"(addr) : "memory");
   else
     asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:1024\n\t"
                  "ds_read_b128 %2, %4 offset:2048\n\tds_read_b128 %3, %4 offset:3072\n\t"
                  "s_waitcnt lgkmcnt(0)"
-                 : "=v"(a[0]), "=v"(a[1]), "=v"(a[2]), "=v"(a[3]) : "v"(addr) : "memory");
+                 : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3]) : "v"(addr) : "memory");
 }
 
 // The int32 epilogue of one column quad of row m (columns n .. n + 3, n a
@@ -297,8 +299,8 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
         "ds_read_b64_tr_b8 %4, %10\n\tds_read_b64_tr_b8 %5, %10 offset:1024\n\t"
         "ds_read_b64_tr_b8 %6, %11\n\tds_read_b64_tr_b8 %7, %11 offset:1024\n\t"
         "s_waitcnt lgkmcnt(0)"
-        : "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1]), "=v"(lo[2]), "=v"(hi[2]),
-          "=v"(lo[3]), "=v"(hi[3])
+        : "=&v"(lo[0]), "=&v"(hi[0]), "=&v"(lo[1]), "=&v"(hi[1]), "=&v"(lo[2]), "=&v"(hi[2]),
+          "=&v"(lo[3]), "=&v"(hi[3])
         : "v"(base + tr_off[0]), "v"(base + tr_off[1]), "v"(base + tr_off[2]),
           "v"(base + tr_off[3])
         : "memory");
@@ -309,8 +311,8 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1)
         "ds_read_b64_tr_b8 %4, %10\n\tds_read_b64_tr_b8 %5, %10 offset:1024\n\t"
         "ds_read_b64_tr_b8 %6, %11\n\tds_read_b64_tr_b8 %7, %11 offset:1024\n\t"
         "s_waitcnt lgkmcnt(0)"
-        : "=v"(lo[4]), "=v"(hi[4]), "=v"(lo[5]), "=v"(hi[5]), "=v"(lo[6]), "=v"(hi[6]),
-          "=v"(lo[7]), "=v"(hi[7])
+        : "=&v"(lo[4]), "=&v"(hi[4]), "=&v"(lo[5]), "=&v"(hi[5]), "=&v"(lo[6]), "=&v"(hi[6]),
+          "=&v"(lo[7]), "=&v"(hi[7])
         : "v"(base + tr_off[4]), "v"(base + tr_off[5]), "v"(base + tr_off[6]),
           "v"(base + tr_off[7])
         : "memory");

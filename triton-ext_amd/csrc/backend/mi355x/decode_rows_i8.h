@@ -79,7 +79,8 @@ template <int SR, int S> struct DecodeRowsCfg {
 // One K step (32 rows, KS of the batch's 4) of operands: the 4 column
 // blocks' B fragments (decode_i8.h's tr32_off layout, 4 KiB a step) and the
 // wave's R32 A row blocks (a_addr, +4 KiB per 32 rows), waiting for them
-// before the asm block ends.
+// before the asm block ends.  Outputs are early-clobber: a read lands while
+// later reads of the block still use their address registers.
 #define TX_ROWS_TR(O0, O1, A, B, C, D)                                                      \
   "ds_read_b64_tr_b8 %0, %" #A " offset:" #O0 "\n\tds_read_b64_tr_b8 %1, %" #A " offset:" #O1   \
   "\n\tds_read_b64_tr_b8 %2, %" #B " offset:" #O0 "\n\tds_read_b64_tr_b8 %3, %" #B             \
@@ -87,26 +88,26 @@ template <int SR, int S> struct DecodeRowsCfg {
   "\n\tds_read_b64_tr_b8 %5, %" #C " offset:" #O1 "\n\tds_read_b64_tr_b8 %6, %" #D             \
   " offset:" #O0 "\n\tds_read_b64_tr_b8 %7, %" #D " offset:" #O1 "\n\t"
 #define TX_ROWS_OUT8                                                                       \
-  "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1]), "=v"(lo[2]), "=v"(hi[2]), "=v"(lo[3]),   \
-      "=v"(hi[3])
+  "=&v"(lo[0]), "=&v"(hi[0]), "=&v"(lo[1]), "=&v"(hi[1]), "=&v"(lo[2]), "=&v"(hi[2]), "=&v"(lo[3]),   \
+      "=&v"(hi[3])
 #define TX_ROWS_IN4 "v"(b + off[0]), "v"(b + off[1]), "v"(b + off[2]), "v"(b + off[3])
 #define TX_ROWS_K1(O0, O1)                                                                 \
   asm volatile(TX_ROWS_TR(O0, O1, 9, 10, 11, 12) "ds_read_b128 %8, %13\n\ts_waitcnt lgkmcnt(0)"  \
-               : TX_ROWS_OUT8, "=v"(a[0])                                                  \
+               : TX_ROWS_OUT8, "=&v"(a[0])                                                  \
                : TX_ROWS_IN4, "v"(a_addr)                                                  \
                : "memory")
 #define TX_ROWS_H1(O0, O1)                                                                 \
   asm volatile("ds_read_b64_tr_b8 %0, %5 offset:" #O0 "\n\tds_read_b64_tr_b8 %1, %5 offset:" #O1 \
                "\n\tds_read_b64_tr_b8 %2, %6 offset:" #O0 "\n\tds_read_b64_tr_b8 %3, %6 offset:" #O1 \
                "\n\tds_read_b128 %4, %7\n\ts_waitcnt lgkmcnt(0)"                              \
-               : "=v"(lo[0]), "=v"(hi[0]), "=v"(lo[1]), "=v"(hi[1]), "=v"(a[0])           \
+               : "=&v"(lo[0]), "=&v"(hi[0]), "=&v"(lo[1]), "=&v"(hi[1]), "=&v"(a[0])           \
                : "v"(b + off[0]), "v"(b + off[1]), "v"(a_addr)                             \
                : "memory")
 #define TX_ROWS_K2(O0, O1)                                                                 \
   asm volatile(TX_ROWS_TR(O0, O1, 10, 11, 12, 13)                                          \
                "ds_read_b128 %8, %14\n\tds_read_b128 %9, %14 offset:4096\n\t"               \
                "s_waitcnt lgkmcnt(0)"                                                      \
-               : TX_ROWS_OUT8, "=v"(a[0]), "=v"(a[1])                                      \
+               : TX_ROWS_OUT8, "=&v"(a[0]), "=&v"(a[1])                                      \
                : TX_ROWS_IN4, "v"(a_addr)                                                  \
                : "memory")
 template <int R32, int NCB, int KS>
