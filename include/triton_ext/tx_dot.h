@@ -140,7 +140,10 @@ typedef struct tx_dot_desc {
   int64_t M, N, K;
   /* Row strides in elements of A [M,K], B [K,N], C [M,N] (all row-major;
    * B [N][K] with TX_FLAG_B_KMAJOR); 0 means packed (K, N or K, N).  Row
-   * strides in bytes must be multiples of 16. */
+   * strides in bytes must be multiples of 16.  The kernels load 16-byte
+   * chunks: a row's last chunk is read whole, up to 15 bytes past its last
+   * element (never past that element's 4 KiB page, since rows and chunks
+   * start 16-byte aligned); the bytes past K or N do not reach the result. */
   int64_t lda, ldb, ldc;
   int32_t a_type, b_type, c_type; /* tx_dtype */
   int32_t scale_mode;             /* tx_scale_mode */
