@@ -288,3 +288,36 @@ def test_contiguous_unaligned_operands(gpu):
                            block=(p.desc.block_m, p.desc.block_n, p.desc.block_k))
     check_close(bits_to_f32(from_device(c), "bf16"), bits_to_f32(ref, "bf16"), atol=ATOL,
                 rtol=RTOL, what="contiguous unaligned")
+
+
+@pytest.mark.parametrize("M,N", [(5, 220), (64, 3)])
+def test_16bit_k1_kmajor_b(gpu, M, N):
+    """K = 1 with B a transposed view (q @ k.T with one head dim): the single row of B has
+    elements ldk apart, which is the K-major layout; the stride of a size-1 dimension says
+    nothing about the layout."""
+    run16(gpu, M, N, 1, "bf16", "f32", kmajor=True)
+
+
+@pytest.mark.parametrize("out", ["i32", "bf16"])
+def test_single_column_b_from_a_transposed_row(gpu, out):
+    """N = 1 with B = x.t() for x [1, K]: a single column whose column stride is K; it is
+    row-major whatever that stride is (int8 and bf16 both take it)."""
+    import torch
+    M, K = 40, 300
+    say(f"tails single-column B {out}")
+    if out == "i32":
+        a, x = uniform_i8((M, K), 71), uniform_i8((1, K), 72)
+        c = tx.dot(to_device(a, gpu), to_device(x, gpu).t(), out_dtype=torch.int32)
+        torch.cuda.synchronize()
+        ref = oracle.tiled_dot(a, np.ascontiguousarray(x.T), a_type=oracle.I8, c_type=oracle.I32,
+                               block=(64, 64, 64))
+        assert np.array_equal(from_device(c), ref)
+    else:
+        a, x = normal_bf16((M, K), k_norm(K), 73), normal_bf16((1, K), k_norm(K), 74)
+        c = tx.dot(to_device(a, gpu).view(torch.bfloat16), to_device(x, gpu).view(torch.bfloat16).t(),
+                   out_dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        ref = oracle.tiled_dot(a, np.ascontiguousarray(x.T), a_type=oracle.BF16, c_type=oracle.BF16,
+                               block=(64, 64, 32))
+        check_close(bits_to_f32(from_device(c), "bf16"), bits_to_f32(ref, "bf16"), atol=ATOL,
+                    rtol=RTOL, what="single-column B")

@@ -58,22 +58,45 @@ def _out_ldc(out):
     return out.stride(0)
 
 
-def aligned_rows(t):
-    """t itself when its rows (or, for a transposed view, its columns) start
-    16 bytes apart on a 16-byte aligned base, else a copy in padded storage
-    of the same layout.  The kernels read 16-byte chunks; K and N themselves
-    may be any size."""
+def _layout(t, col_ok=True):
+    """How a 2-D view lies in memory: ("row", row stride) when its rows are
+    contiguous, ("col", column stride) when its columns are (a transposed
+    view of row-major storage; only if col_ok), else (None, 0).  The stride
+    of a dimension of size 1 says nothing about the layout: a single row
+    whose elements lie apart is a transposed view, and a single column is
+    row-major, or, when col_ok and its elements are adjacent, a transposed
+    view (as a K-major B it then needs no copy)."""
+    R, C = t.shape
+    s0, s1 = t.stride()
+    if col_ok and C <= 1 < R and s0 == 1 and s1 != 1:
+        return "col", s1
+    if C <= 1 or s1 == 1:
+        return "row", s0
+    if col_ok and (R <= 1 or s0 == 1):
+        return "col", s1
+    return None, 0
+
+
+def _b_col_ok(b):
+    """B may be K-major (a transposed view): 16-bit operands only."""
+    return b.element_size() == 2
+
+
+def aligned_rows(t, col_ok=True):
+    """t itself when its rows (or, for a transposed view and col_ok, its
+    columns) start 16 bytes apart on a 16-byte aligned base, else a copy in
+    padded storage of the same layout (row-major when not col_ok).  The
+    kernels read 16-byte chunks; K and N themselves may be any size."""
     import torch
     if t.dim() != 2 or t.numel() == 0:
         return t
     elt = t.element_size()
-    kmajor = t.stride(1) != 1 and t.stride(0) == 1 and t.shape[1] > 1
-    ld = t.stride(1) if kmajor else t.stride(0)
-    if (ld * elt) % 16 == 0 and t.data_ptr() % 16 == 0:
+    kind, ld = _layout(t, col_ok)
+    if kind is not None and (ld * elt) % 16 == 0 and t.data_ptr() % 16 == 0:
         return t
-    if kmajor:  # [N][K] storage viewed as [K][N]
+    if kind == "col":  # [N][K] storage viewed as [K][N]
         return aligned_rows(t.t().contiguous()).t()
-    if t.stride(1) != 1:
+    if kind is None or t.stride(1) != 1:
         t = t.contiguous()
     buf = torch.empty((t.shape[0], _row_pitch(t.shape[1], elt)), dtype=t.dtype, device=t.device)
     buf[:, :t.shape[1]].copy_(t)
@@ -88,14 +111,16 @@ def plan_for(a, b, out_dtype_tx, scale_mode=capi.SCALE_NONE, block=(0, 0, 0), fl
         raise ValueError(f"dot of {tuple(a.shape)} and {tuple(b.shape)}")
     M, K = a.shape
     N = b.shape[1]
-    b_kmajor = b.stride(1) != 1 and b.stride(0) == 1 and K > 1
-    if a.stride(1) != 1 or (b.stride(1) != 1 and not b_kmajor):
+    a_kind, a_ld = _layout(a, col_ok=False)
+    b_kind, b_ld = _layout(b, col_ok=_b_col_ok(b))
+    if a_kind != "row" or b_kind is None:
         raise ValueError("A rows must be contiguous, and B rows (or B's columns) too")
+    b_kmajor = b_kind == "col"
     if b_kmajor:
         flags |= capi.FLAG_B_KMAJOR
     # an empty operand's strides are arbitrary: describe it as packed
-    lda = a.stride(0) if M > 0 and K > 0 else 0
-    ldb = (b.stride(1) if b_kmajor else b.stride(0)) if K > 0 and N > 0 else 0
+    lda = a_ld if M > 0 and K > 0 else 0
+    ldb = b_ld if K > 0 and N > 0 else 0
     desc = capi.make_desc(M, N, K, tx_type(a), out_dtype_tx, b_type=tx_type(b),
                           scale_mode=scale_mode, block=block, lda=lda, ldb=ldb, ldc=ldc,
                           flags=flags)
@@ -139,13 +164,14 @@ def dot(a, b, out=None, out_dtype=None, scale_a=None, scale_b=None, scale_mode=N
     (or in `out`); the kernel adds its finished sum to C.
 
     K and N may be any size.  Operands whose rows do not start 16 bytes
-    apart are copied to padded storage first (one extra pass), and a new
-    output is a view of padded storage; a given `out` must already have
-    16-byte row strides.
+    apart are copied to padded storage first (one extra pass), as is a
+    transposed view of A, or of an 8-bit B (only a 16-bit B runs K-major), in
+    row-major form; a new output is a view of padded storage; a given `out`
+    must already have 16-byte row strides.
     """
     import torch
     if plan is None:
-        a, b = aligned_rows(a), aligned_rows(b)
+        a, b = aligned_rows(a, col_ok=False), aligned_rows(b, col_ok=_b_col_ok(b))
     if acc is not None:
         if acc.dtype not in (torch.float32, torch.int32) or acc.dim() != 2:
             raise ValueError("acc must be an fp32 or int32 [M, N] tensor")
@@ -267,10 +293,10 @@ def dot_scaled(lhs, lhs_scale, lhs_format, rhs, rhs_scale, rhs_format, acc=None,
     for t, nm in ((lhs_scale, "lhs_scale"), (rhs_scale, "rhs_scale")):
         if t is not None and (t.dtype != torch.uint8 or not t.is_contiguous()):
             raise ValueError(f"{nm} must be a contiguous uint8 (e8m0) or float8_e4m3fn tensor")
-    if lhs.stride(1) != 1 or rhs.stride(1) != 1:
+    if _layout(lhs, False)[0] != "row" or _layout(rhs, False)[0] != "row":
         raise ValueError("lhs and rhs rows must be contiguous")
     if plan is None:
-        lhs, rhs = aligned_rows(lhs), aligned_rows(rhs)
+        lhs, rhs = aligned_rows(lhs, col_ok=False), aligned_rows(rhs, col_ok=False)
     flags = 0
     if acc is not None:  # acc + dot, in a new tensor (or `out`), as tl.dot_scaled(acc=)
         if out is None:
