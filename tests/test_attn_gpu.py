@@ -245,10 +245,12 @@ def check_e5m2(o, M, ro, rM, codes, sm_scale, causal, what):
     sides; their fp32 values differ slightly (summation order, the MFMA's
     group sums, v_exp_f32), so a value lying at a rounding boundary can land
     on either side.  An o code then moves one step, and a p code moves one
-    step, changing o by at most 2^-2 p_n |v_n| / l.  The bar: at least 99%
-    of o codes identical, and every difference within one e5m2 step of o
-    plus one p flip of the row's largest term, 2^-2 max_n p_n |v_n| / l
-    (float64 softmax of the decoded inputs)."""
+    step, changing o by at most 2^-2 p_n |v_n| / l.  The bar: every
+    difference within one e5m2 step of o plus one p flip of the row's largest
+    term, 2^-2 max_n p_n |v_n| / l (float64 softmax of the decoded inputs),
+    and at least 99% of o codes identical, less one row of D codes: a single
+    p flip moves o in every column of its row, which on a one-head 64-row
+    output is 1.6% of the codes at D = 32."""
     import torch
     dec = lambda c: torch.from_numpy(np.ascontiguousarray(c)).view(torch.float8_e5m2) \
         .double().numpy()
@@ -266,7 +268,7 @@ def check_e5m2(o, M, ro, rM, codes, sm_scale, causal, what):
                                      axis=-2)
     assert ((o & 0x7F) < 0x7C).all(), f"{what}: inf/NaN in o"
     same = np.mean(o == ro)
-    assert same >= 0.99, f"{what}: only {same:.4f} of o codes identical"
+    assert same >= 0.99 - o.shape[-1] / o.size, f"{what}: only {same:.4f} of o codes identical"
     excess = np.abs(a - b) - (e5m2_step(np.maximum(np.abs(a), np.abs(b))) + top / 4)
     assert excess.max() <= 0, f"{what}: |d o| exceeds its bound by {excess.max():.3g} " \
         f"(identical {same:.4f})"
