@@ -53,13 +53,14 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
                     help="secondary workloads to run, comma-separated: ceiling, phases (where a "
-                         "headline launch's time goes), tiles, c1, vendor, tail, "
+                         "headline launch's time goes), tiles, c1, vendor (vendor8: hipBLASLt's 8-bit GEMMs "
+                         "only), tail, "
                          "w8a8 (or "
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256; w8a8 also runs i32_16, the unscaled "
                          "int8 -> int32 decode at M=16), bf16_decode (or bf16_decode_1, _16, _64: "
                          "bf16 at N = K = 8192 on the 16-bit decode kernel), fp8_decode (or "
                          "fp8_decode_1, _16, _64: block-scaled e4m3 at N = K = 7168 on the fp8 "
-                         "decode kernel), int8, fp8, kmajor, "
+                         "decode kernel), int8, fp8 (fp8u: the unscaled 4096^3 line only), kmajor, "
                          "mx (or mxfp8, mxfp4, "
                          "mxfp8_4096, mxfp8_8192, mxfp4_4096, mxfp4_8192), mxbf16 (or mxbf16_fp4, mxbf16_fp8: "
                          "bf16 x MX), attn (or attn_1024, attn_4096, "
@@ -258,6 +259,36 @@ def bench_vendor_bf16(dev, M, N, K, steps, warmup, seed=1):
                 tflops=2.0 * M * N * K / ms / 1e9)
 
 
+def bench_vendor_8bit(dev, steps, warmup, seed=1):
+    """hipBLASLt's 8-bit GEMMs at 4096^3, a reference point only: torch._scaled_mm on
+    e4m3 (B K-contiguous, as it requires; one tensor-wide scale) with fp32 C -- the type
+    an fp8 x fp8 tt.dot yields -- and with bf16 C, and torch._int_mm (int32 C)."""
+    import torch
+    M = N = K = 4096
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    a = torch.randn((M, K), generator=g, device=dev).to(torch.float8_e4m3fn)
+    bt = torch.randn((N, K), generator=g, device=dev).to(torch.float8_e4m3fn)
+    ai = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+    bi = torch.randint(-127, 128, (K, N), generator=g, device=dev, dtype=torch.int8)
+    one = torch.ones((), device=dev)
+    out = []
+    for name, fn in (
+            ("fp8 e4m3, fp32 C", lambda: torch._scaled_mm(a, bt.t(), scale_a=one, scale_b=one,
+                                                           out_dtype=torch.float32)),
+            ("fp8 e4m3, bf16 C", lambda: torch._scaled_mm(a, bt.t(), scale_a=one, scale_b=one,
+                                                           out_dtype=torch.bfloat16)),
+            ("int8, int32 C", lambda: torch._int_mm(ai, bi))):
+        try:
+            ms = time_back_to_back(fn, steps, warmup)
+        except Exception as e:  # a torch build without the op: no vendor line, no failure
+            print(f"# hipBLASLt {name}: not available ({type(e).__name__})", file=sys.stderr)
+            continue
+        out.append(dict(workload=f"hipBLASLt {name} {M}x{N}x{K}", ms=ms,
+                        tflops=2.0 * M * N * K / ms / 1e9))
+    return out
+
+
 def bench_w8a8(tx, dev, M, N, K, steps, warmup, flush, seed=3, block=(0, 0, 0)):
     import torch
     g = torch.Generator(device=dev)
@@ -370,6 +401,22 @@ def bench_fp8(tx, dev, M, N, K, steps, warmup, seed=5):
     ms = time_back_to_back(run, steps, warmup)
     flops = 2.0 * M * N * K
     return dict(workload=f"fp8 e4m3 block-scaled {M}x{N}x{K}", ms=ms, tflops=flops / ms / 1e9,
+                frac=flops / ms / 1e-3 / PEAK_I8, plan=plan_info(tx, run.plan))
+
+
+def bench_fp8_unscaled(tx, dev, M, N, K, steps, warmup, seed=1):
+    """fp8 e4m3 x e4m3 tt.dot with fp32 C (what the dot yields), B row-major: the
+    256x256x128 tile, beside hipBLASLt's line of the same shape."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    a = torch.randn((M, K), generator=g, device=dev).to(torch.float8_e4m3fn)
+    b = torch.randn((K, N), generator=g, device=dev).to(torch.float8_e4m3fn)
+    c = torch.empty((M, N), dtype=torch.float32, device=dev)
+    run = Launcher(tx, a, b, c)
+    ms = time_back_to_back(run, steps, warmup)
+    flops = 2.0 * M * N * K
+    return dict(workload=f"fp8 e4m3 {M}x{N}x{K}, fp32 C", ms=ms, tflops=flops / ms / 1e9,
                 frac=flops / ms / 1e-3 / PEAK_I8, plan=plan_info(tx, run.plan))
 
 
@@ -931,6 +978,10 @@ def main():
         r = bench_vendor_bf16(dev, M, N, K, args.steps, args.warmup)
         secondary.append(r)
         print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    if want("vendor") or want("vendor8"):
+        for r in bench_vendor_8bit(dev, args.steps, args.warmup):
+            secondary.append(r)
+            print(f"# {r['workload']}: {r['tflops']:.1f} T/s", file=sys.stderr, flush=True)
     if want("c1"):
         r = bench_c1(tx, dev, args.steps, args.warmup)
         secondary.append(r)
@@ -1047,6 +1098,11 @@ def main():
         r = bench_fp8(tx, dev, 2048, 7168, 7168, args.steps, args.warmup)
         secondary.append(r)
         print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    if want("fp8") or want("fp8u"):
+        r = bench_fp8_unscaled(tx, dev, 4096, 4096, 4096, args.steps, args.warmup)
+        secondary.append(r)
+        print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s ({100 * r['frac']:.1f}% of 5033)",
+              file=sys.stderr, flush=True)
 
     for fmt, short in (("e4m3", "mxfp8"), ("e2m1", "mxfp4")):
         for n in (4096, 8192):
