@@ -54,7 +54,7 @@ def parse():
     ap.add_argument("--only", default="",
                     help="secondary workloads to run, comma-separated: ceiling, phases (where a "
                          "headline launch's time goes), tiles, c1, vendor (vendor8: hipBLASLt's 8-bit GEMMs "
-                         "only), tail, "
+                         "only; vendor_decode: its decode shapes only), tail, "
                          "w8a8 (or "
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256; w8a8 also runs i32_16, the unscaled "
                          "int8 -> int32 decode at M=16), bf16_decode (or bf16_decode_1, _16, _64: "
@@ -402,6 +402,33 @@ def bench_fp8(tx, dev, M, N, K, steps, warmup, seed=5):
     flops = 2.0 * M * N * K
     return dict(workload=f"fp8 e4m3 block-scaled {M}x{N}x{K}", ms=ms, tflops=flops / ms / 1e9,
                 frac=flops / ms / 1e-3 / PEAK_I8, plan=plan_info(tx, run.plan))
+
+
+def bench_vendor_decode(dev, flush, seed=1):
+    """hipBLASLt on decode shapes at N = K = 8192, cold inside a stream like the decode
+    lines, a reference point only: bf16 torch.matmul at M = 16 (bf16 C), and
+    torch._int_mm (int32 C) at M = 32, the smallest M it takes above 16."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    N = K = 8192
+    out = []
+    a = torch.randn((16, K), generator=g, device=dev).to(torch.bfloat16)
+    b = torch.randn((K, N), generator=g, device=dev).to(torch.bfloat16)
+    c = torch.empty((16, N), dtype=torch.bfloat16, device=dev)
+    ms = time_cold_in_stream(lambda: torch.matmul(a, b, out=c), flush)
+    out.append(dict(workload=f"hipBLASLt (torch.matmul) bf16 M=16 N={N} K={K}", ms=ms,
+                    gbps=(2 * 16 * K + 2 * K * N + 2 * 16 * N) / ms / 1e6))
+    del b
+    ai = torch.randint(-127, 128, (32, K), generator=g, device=dev, dtype=torch.int8)
+    bi = torch.randint(-127, 128, (K, N), generator=g, device=dev, dtype=torch.int8)
+    try:
+        ms = time_cold_in_stream(lambda: torch._int_mm(ai, bi), flush)
+        out.append(dict(workload=f"hipBLASLt (torch._int_mm) int8 M=32 N={N} K={K}, int32 C",
+                        ms=ms, gbps=(32 * K + K * N + 4 * 32 * N) / ms / 1e6))
+    except Exception as e:  # a torch build without the op: no vendor line, no failure
+        print(f"# torch._int_mm: not available ({type(e).__name__})", file=sys.stderr)
+    return out
 
 
 def bench_fp8_unscaled(tx, dev, M, N, K, steps, warmup, seed=1):
@@ -1082,6 +1109,11 @@ def main():
             print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
                   f"({100 * r['frac_hbm']:.1f}% HBM); isolated launch "
                   f"{r['ms_isolated'] * 1e3:.2f} us", file=sys.stderr, flush=True)
+    if want("vendor") or want("vendor_decode"):
+        for r in bench_vendor_decode(dev, flush):
+            secondary.append(r)
+            print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s",
+                  file=sys.stderr, flush=True)
     for m in (1, 16, 64):
         if want("bf16_decode") or want(f"bf16_decode_{m}"):
             r = bench_decode16(tx, dev, m, 8192, 8192, max(args.steps, 20), 3, flush)
