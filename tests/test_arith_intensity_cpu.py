@@ -34,7 +34,8 @@ def test_closed_form(M, N, K, a, c, sm, flops, nbytes, bound):
 
 
 def test_baseline_roofline_times():
-    """Roofline times quoted for the configs."""
+    """Roofline times of the benchmark configs at the MI355X peaks (bf16 4096^3 at
+    2516.6 TFLOP/s, W8A8 M=16 and fp8 C5 at 8 TB/s and 5033 TFLOP/s respectively)."""
     cases = [((4096, 4096, 4096, tx.BF16, tx.BF16, 0), 54.6),
              ((16, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL), 8.44),
              ((2048, 7168, 7168, tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128), 41.8)]
