@@ -259,8 +259,9 @@ def test_decode_f8_plans():
                                     scale_mode=tx.SCALE_BLOCK128)).kernel == DF8
     assert tx.plan(tx.make_desc(16, 4096, 4096, tx.F8E4M3, tx.F32, flags=tx.FLAG_ACCUMULATE,
                                 scale_mode=tx.SCALE_BLOCK128)).kernel == DF8
-    assert _err(tx.make_desc(16, 4096, 4096, tx.F8E4M3, tx.F32,
-                             flags=tx.FLAG_B_KMAJOR)) == tx.ERR_UNSUPPORTED
+    # K-major B: not this kernel, the 256x256x128 tile
+    p = tx.plan(tx.make_desc(16, 4096, 4096, tx.F8E4M3, tx.F32, flags=tx.FLAG_B_KMAJOR))
+    assert p.kernel == tx.KERNEL_GEMM_F8 and (p.desc.block_m, p.desc.block_k) == (256, 128)
     # an explicit 8-bit tile at decode shape runs that tile
     assert tx.plan(tx.make_desc(16, 4096, 4096, tx.F8E4M3, tx.F32,
                                 block=(256, 256, 128))).kernel == tx.KERNEL_GEMM_F8
@@ -300,7 +301,8 @@ def test_decode16_plans():
 
 
 def test_b_kmajor_plans():
-    """K-major B (q @ k.T): bf16/fp16 on the 256x256x64 tile, ldb defaulting to K."""
+    """K-major B (q @ k.T): bf16/fp16 on the 256x256x64 tile, int8 -> int32 and unscaled
+    fp8 on the 256x256x128 tile; ldb defaulting to K."""
     p = tx.plan(tx.make_desc(512, 384, 192, tx.BF16, tx.F32, flags=tx.FLAG_B_KMAJOR))
     assert p.kernel == tx.KERNEL_GEMM_16BIT
     assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (256, 256, 64)
@@ -309,9 +311,21 @@ def test_b_kmajor_plans():
                              flags=tx.FLAG_B_KMAJOR)) == tx.ERR_INVALID  # ldb < K
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, block=(128, 128, 64),
                              flags=tx.FLAG_B_KMAJOR)) == tx.ERR_UNSUPPORTED
-    for a, c, sm in ((tx.I8, tx.I32, 0), (tx.F8E4M3, tx.F32, 0),
-                     (tx.I8, tx.BF16, tx.SCALE_ROWCOL)):
-        assert _err(tx.make_desc(16, 256, 256, a, c, scale_mode=sm,
+    for a, b, c, kern in ((tx.I8, tx.I8, tx.I32, tx.KERNEL_GEMM_I8),
+                          (tx.F8E4M3, tx.F8E4M3, tx.F32, tx.KERNEL_GEMM_F8),
+                          (tx.F8E5M2, tx.F8E4M3, tx.F32, tx.KERNEL_GEMM_F8),
+                          (tx.F8E4M3, tx.F8E5M2, tx.F32, tx.KERNEL_GEMM_F8),
+                          (tx.F8E5M2, tx.F8E5M2, tx.F32, tx.KERNEL_GEMM_F8)):
+        p = tx.plan(tx.make_desc(16, 300, 200, a, c, b_type=b, lda=208, ldb=208,
+                                 flags=tx.FLAG_B_KMAJOR))
+        assert p.kernel == kern and p.desc.ldb == 208
+        assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (256, 256, 128)
+    # scaled 8-bit dots and other 8-bit tiles have no K-major form
+    for a, c, sm, blk in ((tx.I8, tx.BF16, tx.SCALE_ROWCOL, (0, 0, 0)),
+                          (tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, (0, 0, 0)),
+                          (tx.I8, tx.I32, 0, (128, 128, 128)),
+                          (tx.I8, tx.I32, 0, (256, 224, 128))):
+        assert _err(tx.make_desc(16, 256, 256, a, c, scale_mode=sm, block=blk,
                                  flags=tx.FLAG_B_KMAJOR)) == tx.ERR_UNSUPPORTED
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, flags=0x10)) == tx.ERR_INVALID
 

@@ -300,8 +300,9 @@ def test_16bit_k1_kmajor_b(gpu, M, N):
 
 @pytest.mark.parametrize("out", ["i32", "bf16"])
 def test_single_column_b_from_a_transposed_row(gpu, out):
-    """N = 1 with B = x.t() for x [1, K]: a single column whose column stride is K; it is
-    row-major whatever that stride is (int8 and bf16 both take it)."""
+    """N = 1 with B = x.t() for x [1, K]: a single column whose column stride is K.  Its
+    elements are adjacent, so an int32 or bf16 dot runs it K-major (after a copy into
+    16-byte rows here, K = 300 not being a multiple of 16 bytes)."""
     import torch
     M, K = 40, 300
     say(f"tails single-column B {out}")
@@ -321,3 +322,108 @@ def test_single_column_b_from_a_transposed_row(gpu, out):
                                block=(64, 64, 32))
         check_close(bits_to_f32(from_device(c), "bf16"), bits_to_f32(ref, "bf16"), atol=ATOL,
                     rtol=RTOL, what="single-column B")
+
+
+def _codes8(rng, shape, f):
+    """Finite fp8 codes over the whole range (no NaN / Inf)."""
+    c = rng.integers(0, 256, size=shape).astype(np.uint8)
+    if f == "e5m2":
+        return np.where((c & 0x7C) == 0x7C, c & 0x83, c).astype(np.uint8)
+    return np.where((c & 0x7F) == 0x7F, c & 0xF0, c).astype(np.uint8)
+
+
+def _kmajor_b(b, fill, gpu, tdtype=None, junk=None):
+    """B [K, N] as a transposed view of [N][K'] storage: columns past K and rows past N hold
+    `fill`, or random bytes from `junk`."""
+    N, K = b.shape[1], b.shape[0]
+    st, _ = padded(np.ascontiguousarray(b.T), fill)
+    if junk is not None:
+        st[:, K:] = junk.integers(-128, 128, size=st[:, K:].shape)
+        st[N:, :] = junk.integers(-128, 128, size=st[N:, :].shape)
+    return dev_view(st, (N, K), gpu, tdtype).t()
+
+
+def _assert_kmajor_plan(da, db, c, kernel):
+    p = tx.plan_for(da, db, tx.tx_type(c), ldc=c.stride(0))
+    assert p.desc.flags & tx.FLAG_B_KMAJOR and p.kernel == kernel
+    assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (256, 256, 128)
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 263, 391), (40, 50, 200), (17, 1001, 999),
+                                   (5, 220, 1), (512, 512, 1024), (64, 3, 129)])
+def test_int8_ragged_kmajor_b(gpu, M, N, K):
+    """int8 -> int32 with B a transposed view (q @ k.T): B's padding columns past K and rows
+    past N hold random bytes, as do A's.  The chunk that crosses K is loaded whole on both
+    sides, so both are zeroed past K (junk times junk is not zero).  Bit-exact."""
+    import torch
+    say(f"tails int8 K-major B M={M} N={N} K={K}")
+    a, b = uniform_i8((M, K), 81), uniform_i8((K, N), 82)
+    junk = np.random.default_rng(83)
+    sa, _ = padded(a, 0)
+    sa[:, K:] = junk.integers(-128, 128, size=sa[:, K:].shape)
+    sa[M:, :] = junk.integers(-128, 128, size=sa[M:, :].shape)
+    da = dev_view(sa, (M, K), gpu)
+    db = _kmajor_b(b, 0, gpu, junk=junk)
+    c = tx.dot(da, db, out_dtype=torch.int32)
+    torch.cuda.synchronize()
+    _assert_kmajor_plan(da, db, c, tx.KERNEL_GEMM_I8)
+    ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.I32, block=(64, 64, 64))
+    assert np.array_equal(from_device(c), ref)
+
+
+@pytest.mark.parametrize("fa,fb", [("e4m3", "e4m3"), ("e4m3", "e5m2"), ("e5m2", "e4m3"),
+                                   ("e5m2", "e5m2")])
+@pytest.mark.parametrize("M,N,K", [(300, 263, 391), (16, 1024, 256), (130, 77, 1)])
+def test_fp8_ragged_kmajor_b(gpu, fa, fb, M, N, K):
+    """Unscaled fp8 -> fp32 with B a transposed view, NaN codes (0x7F, NaN in e4m3 and
+    e5m2) in both operands' padding; e4m3 / e5m2 in every mix.  Against the oracle, and
+    bit for bit against the same dot with B row-major (the K-major fragment holds the
+    same K indices in the same bytes)."""
+    import torch
+    say(f"tails fp8 K-major B {fa}x{fb} M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + N + K)
+    a, b = _codes8(rng, (M, K), fa), _codes8(rng, (K, N), fb)
+    tdt = {"e4m3": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}
+    otype = {"e4m3": oracle.F8E4M3, "e5m2": oracle.F8E5M2}
+    sa, _ = padded(a, 0x7F)
+    da = dev_view(sa, (M, K), gpu, tdt[fa])
+    db = _kmajor_b(b, 0x7F, gpu, tdt[fb])
+    c = tx.dot(da, db, out_dtype=torch.float32)
+    sb, _ = padded(b, 0x7F)
+    c_row = tx.dot(da, dev_view(sb, (K, N), gpu, tdt[fb]), out_dtype=torch.float32,
+                   block=(256, 256, 128))
+    torch.cuda.synchronize()
+    _assert_kmajor_plan(da, db, c, tx.KERNEL_GEMM_F8)
+    got = from_device(c)
+    ref = oracle.tiled_dot(a, b, a_type=otype[fa], b_type=otype[fb], c_type=oracle.F32,
+                           block=(256, 256, 128))
+    dec = lambda q, f: (oracle.e4m3_to_f32(q) if f == "e4m3"
+                        else oracle.f16_to_f32(q.astype(np.uint16) << 8)).astype(np.float64)
+    rms = lambda q, f: float(np.sqrt(np.mean(dec(q, f) ** 2)))
+    check_close(got, ref, atol=ATOL, rtol=RTOL, scale=math.sqrt(K) * rms(a, fa) * rms(b, fb),
+                what=f"fp8 K-major {fa}x{fb}")
+    assert np.array_equal(got.view(np.uint32), from_device(c_row).view(np.uint32))
+
+
+@pytest.mark.parametrize("kind", ["i8", "e4m3"])
+def test_8bit_kmajor_b_full_size(gpu, kind):
+    """4096 x 4096 x 4096 (the int8 headline shape) with B = k.t(): bit for bit the dot
+    with B row-major, whose parity the oracle pins at the smaller sizes."""
+    import torch
+    M = N = K = 4096
+    say(f"tails 8-bit K-major B full size {kind}")
+    g = torch.Generator(device=gpu)
+    g.manual_seed(91)
+    if kind == "i8":
+        a = torch.randint(-128, 128, (M, K), generator=g, device=gpu, dtype=torch.int8)
+        k = torch.randint(-128, 128, (N, K), generator=g, device=gpu, dtype=torch.int8)
+        odt, kern = torch.int32, tx.KERNEL_GEMM_I8
+    else:
+        a = torch.randn((M, K), generator=g, device=gpu).to(torch.float8_e4m3fn)
+        k = torch.randn((N, K), generator=g, device=gpu).to(torch.float8_e4m3fn)
+        odt, kern = torch.float32, tx.KERNEL_GEMM_F8
+    c = tx.dot(a, k.t(), out_dtype=odt)
+    c_row = tx.dot(a, k.t().contiguous(), out_dtype=odt, block=(256, 256, 128))
+    torch.cuda.synchronize()
+    _assert_kmajor_plan(a, k.t(), c, kern)
+    assert torch.equal(c.view(torch.int32), c_row.view(torch.int32))

@@ -113,6 +113,14 @@ struct GemmConfig {
     OP_F8, 256, 256, 128, 2, 4, EPI_F32, gemm8_w4_kernel<OP_F8, EPI_F32, FA, FB>, \
         0, 0, 5, (FA) | ((FB) << 4)                                            \
   }
+// The same with B K-major (TX_FLAG_B_KMAJOR): int8 -> int32 and unscaled fp8.
+#define TX_GEMM_8T(OP, EPI)                                                    \
+  GemmConfig { OP, 256, 256, 128, 2, 4, EPI, gemm8_w4_kernel<OP, EPI, 0, 0, true>, 1, 0, 5 }
+#define TX_GEMM_8FT(FA, FB)                                                    \
+  GemmConfig {                                                                 \
+    OP_F8, 256, 256, 128, 2, 4, EPI_F32, gemm8_w4_kernel<OP_F8, EPI_F32, FA, FB, true>, \
+        1, 0, 5, (FA) | ((FB) << 4)                                            \
+  }
 #define TX_GEMM_8N(OP, EPI)                                                    \
   GemmConfig { OP, 256, 224, 128, 4, 2, EPI, gemm8_n224_kernel<OP, EPI>, 0, 0, 5 }
 
@@ -154,6 +162,12 @@ const GemmConfig kGemmConfigs[] = {
     TX_GEMM_8F(1, 1),
     TX_GEMM_8F(0, 1),
     TX_GEMM_8F(1, 0),
+    // the same with B K-major (q . k^T): int8 -> int32, fp8 -> fp32
+    TX_GEMM_8T(OP_I8, EPI_I32),
+    TX_GEMM_8T(OP_F8, EPI_F32),
+    TX_GEMM_8FT(1, 1),
+    TX_GEMM_8FT(0, 1),
+    TX_GEMM_8FT(1, 0),
     // MX: e8m0-scaled fp8 (e4m3 / e5m2 in any mix) and fp4 (gemm8_w4.h)
     TX_GEMM_MX(0, 0, 128, EPI_MX_F32),
     TX_GEMM_MX(0, 0, 128, EPI_MX_BF16),
@@ -564,7 +578,8 @@ int txMi355xDotRun(tx_dot_plan *plan) {
                                 mxUpcastSide(d) ? 0 : fmtOf(d));
   if (ci < 0 && (d.flags & TX_FLAG_B_KMAJOR))
     return fail(TX_ERR_UNSUPPORTED,
-                "K-major B is implemented for bf16/fp16 on the 256x256x64 tile only");
+                "K-major B is implemented on the 256x256 tiles for bf16/fp16, int8 -> int32 "
+                "and unscaled fp8 only");
   if (ci < 0)
     return fail(TX_ERR_UNSUPPORTED, "no instantiated tile %dx%dx%d for this dtype",
                 d.block_m, d.block_n, d.block_k);

@@ -84,7 +84,12 @@ extern "C" __device__ f32x4_t txk_mfma_scale_16x16x128_f4(i32x4_t, i32x4_t, f32x
 
 // FA, FB: MFMA format codes of A and B (0 e4m3, 1 e5m2; 4 e2m1 with the MX
 // epilogues only); the unscaled fp8 dot takes e4m3 / e5m2 in any mix.
-template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
+// BT: B is stored K-major ([N][K] row-major, row stride ldb), the layout of
+// q . k^T with k row-major (int8 -> int32 and unscaled fp8 only).  Its tile is
+// staged exactly like A's ([256 columns][128 K bytes], the same swizzle) and
+// read with ds_read_b128: lane l gets column l%16's K bytes 32 (l/16) .. +31,
+// the same permutation of K as A's fragment.
+template <int OP, int EPI, int FA = 0, int FB = 0, bool BT = false> struct Gemm8W4 {
   static constexpr int BM = 256, BN = 256, BK = 128, NW = 8, WN = 4;
   static constexpr int WTM = 128, WTN = 64, FM = WTM / 16, FN = WTN / 16;
   static constexpr bool SCALED = EPI == EPI_BLOCK128_BF16 || EPI == EPI_BLOCK128_F32;
@@ -105,6 +110,7 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
   static_assert(!MX || (OP == OP_F8 && ((FA == 4) == (FB == 4)) && FA >= 0 && FA <= 4 &&
                         FB >= 0 && FB <= 4 && FA != 2 && FA != 3 && FB != 2 && FB != 3),
                 "MX operands: e4m3 / e5m2 in any mix, or e2m1 on both sides");
+  static_assert(!BT || EPI == EPI_I32 || EPI == EPI_F32, "K-major B: int32 / fp32 C, no scales");
   static_assert(STAGE % 128 == 0, "stage offsets keep address bits 0-6");
   static_assert(2 * STAGE <= 160 * 1024, "two stages in LDS");
 
@@ -145,11 +151,19 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
 #pragma unroll
       for (int i = 2 * (PART - 2); i < 2 * (PART - 2) + 2; ++i) {
         const int j = wave * B_DMA + i;
-        const int k = 4 * j + (lane >> 4), pc = lane & 15;
-        const int c = pc ^ (k & 7);
-        const bool ok = live && (!MASK_MN || n0 + 16 * c < p.N);
-        const uint32_t v = ok ? (uint32_t)k * (uint32_t)p.ldb + (uint32_t)n0 + 16u * c : kOOB;
-        W::buffer_lds16(v, rb, (uint32_t)((int64_t)k0 * p.ldb), st + A_BYTES + j * 1024);
+        if constexpr (BT) { // A's staging: column n0 + row, 16-byte K chunk c
+          const int row = 8 * j + (lane >> 3), pc = lane & 7;
+          const int c = pc ^ ((row >> 1) & 7);
+          const bool ok = live && (!MASK_MN || n0 + row < p.N) && (!MASK_K || k0 + 16 * c < p.K);
+          const uint32_t v = ok ? (uint32_t)(n0 + row) * (uint32_t)p.ldb + 16u * c : kOOB;
+          W::buffer_lds16(v, rb, (uint32_t)k0, st + A_BYTES + j * 1024);
+        } else {
+          const int k = 4 * j + (lane >> 4), pc = lane & 15;
+          const int c = pc ^ (k & 7);
+          const bool ok = live && (!MASK_MN || n0 + 16 * c < p.N);
+          const uint32_t v = ok ? (uint32_t)k * (uint32_t)p.ldb + (uint32_t)n0 + 16u * c : kOOB;
+          W::buffer_lds16(v, rb, (uint32_t)((int64_t)k0 * p.ldb), st + A_BYTES + j * 1024);
+        }
       }
     }
     if constexpr (MX) {
@@ -202,8 +216,13 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
     const int G = lane >> 4, L = lane & 15;
     const int row = wm * WTM + L;
     bs.a = lds0 + row * BK + (((MX ? G : 2 * G) ^ ((row >> 1) & 7)) << 4);
-    const int k = (MX ? 16 : 32) * G + (L >> 1);
-    bs.b = lds0 + A_BYTES + k * BN + (((4 * wn) ^ (k & 7)) << 4) + 8 * (L & 1);
+    if constexpr (BT) { // like A: column wn*64 + 16 j + l%16, chunk 2 (l/16)
+      const int col = wn * WTN + L;
+      bs.b = lds0 + A_BYTES + col * BK + (((2 * G) ^ ((col >> 1) & 7)) << 4);
+    } else {
+      const int k = (MX ? 16 : 32) * G + (L >> 1);
+      bs.b = lds0 + A_BYTES + k * BN + (((4 * wn) ^ (k & 7)) << 4) + 8 * (L & 1);
+    }
   }
 
   // MX: per-lane LDS addresses (stage 0) of the scale bytes of A row block 0
@@ -256,6 +275,11 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
   }
 
   __device__ __forceinline__ static i32x8_t read_b(const Bases &bs, uint32_t so, int j) {
+    if constexpr (BT) { // column block j: 16 columns further, +2048
+      Bases c = bs;
+      c.a = bs.b;
+      return read_a(c, so, j);
+    }
     typedef int v2i __attribute__((ext_vector_type(2)));
     typedef __attribute__((address_space(3))) v2i lds_v2i_t;
     const uint32_t b0 = (bs.b ^ (16u * j)) + so;
@@ -308,7 +332,8 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
   // beyond in the last step.  Byte t of the fragment is K index
   // kt * BK + 32 (l / 16) + t (chunks 2 (l / 16) and 2 (l / 16) + 1); B's
   // rows past K already read as zeros, and an fp8 NaN code times zero would
-  // still be NaN.  (int8 needs nothing: junk times zero is zero.)
+  // still be NaN.  (int8 needs nothing: junk times zero is zero.)  A K-major
+  // B fragment has the same byte layout and is zeroed alike, for int8 too.
   __device__ __forceinline__ static i32x8_t mask_k(i32x8_t v, int kt, int64_t K) {
     const int64_t rem = K - ((int64_t)kt * BK + 32 * ((threadIdx.x & 63) >> 4));
 #pragma unroll
@@ -346,7 +371,8 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
     // (rows start 16-byte aligned, so that chunk is the row's own).  fp4 A:
     // K and lda count bytes here.
     const i32x4_t ra = make_rsrc(p.A, (uint32_t)((p.M - 1) * p.lda + ((p.K + 15) & ~15ll)));
-    const i32x4_t rb = make_rsrc(p.B, (uint32_t)((p.K - 1) * p.ldb + ((p.N + 15) & ~15ll)));
+    const i32x4_t rb = BT ? make_rsrc(p.B, (uint32_t)((p.N - 1) * p.ldb + ((p.K + 15) & ~15ll)))
+                          : make_rsrc(p.B, (uint32_t)((p.K - 1) * p.ldb + ((p.N + 15) & ~15ll)));
     i32x4_t rsa = {0, 0, 0, 0}, rsb = {0, 0, 0, 0};
     if (SCALED) {
       rsa = make_rsrc(p.sa, (uint32_t)(p.M * p.sa_ld * 4));
@@ -423,11 +449,18 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
       // tail: the last step (MX scale groups past K/32 possible).
       auto step = [&](int kt, bool more, auto tail) {
         constexpr bool TAIL = MX && decltype(tail)::value;
-        constexpr bool KTAIL = !INT && !MX && decltype(tail)::value;
+        // K-major B's chunk that crosses K is loaded whole too: both operands'
+        // bytes past K are zeroed then (int8 included: junk times junk is not 0)
+        constexpr bool KTAIL = ((!INT && !MX) || BT) && decltype(tail)::value;
         const uint32_t so = (kt & 1) * STAGE, sn = ((kt + 1) & 1) * STAGE;
         i32x8_t a = read_a(bs, so, 0);
         if constexpr (KTAIL)
           a = mask_k(a, kt, p.K);
+        if constexpr (KTAIL && BT) {
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            b[j] = mask_k(b[j], kt, p.K);
+        }
         float sc = scale(so, 0);
         int sxa = MX ? read_sx(xa, so, 0) : 0;
         if constexpr (TAIL) {
@@ -680,9 +713,9 @@ template <int OP, int EPI, int FA = 0, int FB = 0> struct Gemm8W4 {
   }
 };
 
-template <int OP, int EPI, int FA = 0, int FB = 0>
+template <int OP, int EPI, int FA = 0, int FB = 0, bool BT = false>
 __global__ void __launch_bounds__(512, 1) gemm8_w4_kernel(GemmArgs p) {
-  typedef Gemm8W4<OP, EPI, FA, FB> G;
+  typedef Gemm8W4<OP, EPI, FA, FB, BT> G;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * G::STAGE];
   int tm, tn;
   tile_coords(p, tm, tn);

@@ -245,6 +245,8 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
       t = d->M > 128 ? Tile{128, 128, 128, 1.0}
           : d->M > 48 ? Tile{64, 128, 128, 1.0}
                       : Tile{(int32_t)(16 * cdiv(d->M > 0 ? d->M : 1, 16)), 128, 64, 1.0};
+    else if (d->flags & TX_FLAG_B_KMAJOR)
+      t = kTiles8[0]; // the K-major B kernels exist for this tile only
     else if (d->a_type == TX_F8E4M3 || d->a_type == TX_F8E5M2)
       t = kTiles8[first]; // the register-staged 128x128 tile is slower everywhere
     else

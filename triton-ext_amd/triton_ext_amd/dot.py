@@ -77,9 +77,19 @@ def _layout(t, col_ok=True):
     return None, 0
 
 
-def _b_col_ok(b):
-    """B may be K-major (a transposed view): 16-bit operands only."""
-    return b.element_size() == 2
+# The one tile per operand width that has a K-major B form.
+_KMAJOR_TILE = {2: (256, 256, 64), 1: (256, 256, 128)}
+
+
+def _b_col_ok(b, unscaled=True, block=(0, 0, 0)):
+    """B may be K-major (a transposed view): 16-bit operands, and 8-bit ones in an
+    unscaled dot (int8 -> int32, fp8 -> fp32), when the planner picks the tile
+    (block (0, 0, 0)) or the block asked for is the one tile with that form;
+    otherwise a transposed B is copied row-major."""
+    tile = _KMAJOR_TILE.get(b.element_size())
+    if tile is None or (b.element_size() == 1 and not unscaled):
+        return False
+    return tuple(block) in ((0, 0, 0), tile)
 
 
 def aligned_rows(t, col_ok=True):
@@ -112,7 +122,10 @@ def plan_for(a, b, out_dtype_tx, scale_mode=capi.SCALE_NONE, block=(0, 0, 0), fl
     M, K = a.shape
     N = b.shape[1]
     a_kind, a_ld = _layout(a, col_ok=False)
-    b_kind, b_ld = _layout(b, col_ok=_b_col_ok(b))
+    b_kind, b_ld = _layout(b, col_ok=_b_col_ok(b, scale_mode == capi.SCALE_NONE, block))
+    if a_kind == "row" and b_kind is None and _layout(b)[0] == "col":
+        raise ValueError("B is a transposed view: K-major B runs on the 256x256 tile of a "
+                         "16-bit or unscaled 8-bit dot only; copy it row-major")
     if a_kind != "row" or b_kind is None:
         raise ValueError("A rows must be contiguous, and B rows (or B's columns) too")
     b_kmajor = b_kind == "col"
@@ -165,13 +178,16 @@ def dot(a, b, out=None, out_dtype=None, scale_a=None, scale_b=None, scale_mode=N
 
     K and N may be any size.  Operands whose rows do not start 16 bytes
     apart are copied to padded storage first (one extra pass), as is a
-    transposed view of A, or of an 8-bit B (only a 16-bit B runs K-major), in
-    row-major form; a new output is a view of padded storage; a given `out`
-    must already have 16-byte row strides.
+    transposed view of A, or of an 8-bit B in a scaled dot, in row-major form
+    (a 16-bit B, and an 8-bit B of an unscaled int8 or fp8 dot, run K-major on
+    the 256x256 tile, unless `block` names another tile: then B is copied too);
+    a new output is a view of padded storage; a given `out` must already have
+    16-byte row strides.
     """
     import torch
     if plan is None:
-        a, b = aligned_rows(a, col_ok=False), aligned_rows(b, col_ok=_b_col_ok(b))
+        unscaled = scale_a is None and scale_b is None and scale_mode in (None, capi.SCALE_NONE)
+        a, b = aligned_rows(a, col_ok=False), aligned_rows(b, col_ok=_b_col_ok(b, unscaled, block))
     if acc is not None:
         if acc.dtype not in (torch.float32, torch.int32) or acc.dim() != 2:
             raise ValueError("acc must be an fp32 or int32 [M, N] tensor")
