@@ -60,7 +60,8 @@ def parse():
                          "int8 -> int32 decode at M=16), bf16_decode (or bf16_decode_1, _16, _64: "
                          "bf16 at N = K = 8192 on the 16-bit decode kernel), fp8_decode (or "
                          "fp8_decode_1, _16, _64: block-scaled e4m3 at N = K = 7168 on the fp8 "
-                         "decode kernel), int8, fp8 (fp8u: the unscaled 4096^3 line only), kmajor, "
+                         "decode kernel), int8, fp8 (fp8u: the unscaled 4096^3 line only), kmajor (bf16 "
+                         "4096^3, int8 and fp8 4096^3 with B K-major), "
                          "mx (or mxfp8, mxfp4, "
                          "mxfp8_4096, mxfp8_8192, mxfp4_4096, mxfp4_8192), mxbf16 (or mxbf16_fp4, mxbf16_fp8: "
                          "bf16 x MX), attn (or attn_1024, attn_4096, "
@@ -247,6 +248,30 @@ def bench_bf16_kmajor(tx, dev, M, N, K, steps, warmup, seed=1):
     flops = 2.0 * M * N * K
     return dict(workload=f"bf16 {M}x{N}x{K}, B K-major (q @ k.T)", ms=ms, tflops=flops / ms / 1e9,
                 frac=flops / ms / 1e-3 / PEAK_BF16, plan=plan_info(tx, run.plan))
+
+
+def bench_8bit_kmajor(tx, dev, kind, M, N, K, steps, warmup, seed=1):
+    """int8 -> int32 or unscaled fp8 e4m3 -> fp32 with B stored K-major ([N, K] row-major,
+    passed as its transpose), on the 256x256x128 tile."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    if kind == "int8":
+        a = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+        k = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+        c = torch.empty((M, N), dtype=torch.int32, device=dev)
+        what = f"int8 {M}x{N}x{K}, int32 C"
+    else:
+        a = torch.randn((M, K), generator=g, device=dev).to(torch.float8_e4m3fn)
+        k = torch.randn((N, K), generator=g, device=dev).to(torch.float8_e4m3fn)
+        c = torch.empty((M, N), dtype=torch.float32, device=dev)
+        what = f"fp8 e4m3 {M}x{N}x{K}, fp32 C"
+    run = Launcher(tx, a, k.t(), c)
+    assert run.plan.desc.flags & tx.FLAG_B_KMAJOR
+    ms = time_back_to_back(run, steps, warmup)
+    ops = 2.0 * M * N * K
+    return dict(workload=f"{what}, B K-major (q @ k.T)", ms=ms, tops=ops / ms / 1e9,
+                frac=ops / ms / 1e-3 / PEAK_I8, plan=plan_info(tx, run.plan))
 
 
 def bench_vendor_bf16(dev, M, N, K, steps, warmup, seed=1):
@@ -1018,6 +1043,11 @@ def main():
         r = bench_bf16_kmajor(tx, dev, M, N, K, args.steps, args.warmup)
         secondary.append(r)
         print(f"# {r['workload']}: {r['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+        for kind in ("int8", "fp8"):
+            r = bench_8bit_kmajor(tx, dev, kind, 4096, 4096, 4096, args.steps, args.warmup)
+            secondary.append(r)
+            print(f"# {r['workload']}: {r['ms'] * 1e3:.1f} us, {r['tops']:.1f} T/s",
+                  file=sys.stderr, flush=True)
     flush = make_flush(dev)
     if want("tail"):
         for (m, n, k) in ((4096, 4096, 4000), (4000, 4000, 4000)):

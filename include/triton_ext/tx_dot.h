@@ -127,7 +127,8 @@ typedef enum tx_kernel {
 #define TX_FLAG_NO_LOOP_SPLIT 0x1 /* run every K step masked (no peeling) */
 /* B is stored K-major: [N][K] row-major with row stride ldb (0 = K), the
  * layout of tl.dot(q, tl.trans(k)) / q @ k.T with k row-major.  Supported for
- * bf16/fp16 operands on the 256x256x64 tile. */
+ * bf16/fp16 operands on the 256x256x64 tile, and for int8 -> int32 and
+ * unscaled fp8 -> fp32 on the 256x256x128 tile. */
 #define TX_FLAG_B_KMAJOR 0x2
 /* C = C + A . B: the accumulator operand of tl.dot(a, b, acc) and
  * tl.dot_scaled(..., acc) (R:pass/LoopSplit/06-fused-attention.py:85).  C
