@@ -58,7 +58,8 @@ def parse():
                          "w8a8 (or "
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256; w8a8 also runs i32_16, the unscaled "
                          "int8 -> int32 decode at M=16), bf16_decode (or bf16_decode_1, _16, _64: "
-                         "bf16 at N = K = 8192 on the 16-bit decode kernel), fp8_decode (or "
+                         "bf16 at N = K = 8192 on the 16-bit decode kernel; bf16_decode_kmajor, "
+                         "or _1, _16, _64: the same with B K-major), fp8_decode (or "
                          "fp8_decode_1, _16, _64: block-scaled e4m3 at N = K = 7168 on the fp8 "
                          "decode kernel), int8, fp8 (fp8u: the unscaled 4096^3 line only), kmajor (bf16 "
                          "4096^3, int8 and fp8 4096^3 with B K-major), "
@@ -357,19 +358,24 @@ def bench_decode_i32(tx, dev, M, N, K, steps, warmup, flush, seed=3):
                 plan=plan_info(tx, p, split_k=p.split_k, grid=p.grid_x))
 
 
-def bench_decode16(tx, dev, M, N, K, steps, warmup, flush, seed=3):
+def bench_decode16(tx, dev, M, N, K, steps, warmup, flush, seed=3, kmajor=False):
     """bf16 x bf16 -> bf16 tt.dot of decode shape: the 16-bit decode kernel (B streamed
-    once), timed like the W8A8 lines (cold, B from HBM); algorithmic bytes A, B and C once."""
+    once), timed like the W8A8 lines (cold, B from HBM); algorithmic bytes A, B and C once.
+    kmajor: B stored [N][K] and passed as its transpose (q @ k.T; a weight kept [out][in])."""
     import torch
     a, b = bf16_inputs(M, N, K, dev, seed)
+    if kmajor:
+        b = b.t().contiguous().t()   # same values, K-major storage
     c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     run = Launcher(tx, a, b, c)
+    assert bool(run.plan.desc.flags & tx.FLAG_B_KMAJOR) == kmajor
     iso, _ = time_cold(run, steps, warmup, flush)
     med = time_cold_in_stream(run, flush)
     warm = time_back_to_back(run, steps, warmup)
     nbytes = 2 * (M * K + K * N + M * N)
     p = run.plan
-    return dict(workload=f"bf16 decode M={M} N={N} K={K}", ms=med, ms_isolated=iso,
+    return dict(workload=f"bf16 decode M={M} N={N} K={K}" + (", B K-major" if kmajor else ""),
+                ms=med, ms_isolated=iso,
                 ms_warm_mall=warm, gbps=nbytes / med / 1e6, frac_hbm=nbytes / med / 1e-3 / HBM,
                 tflops=2.0 * M * N * K / med / 1e9,
                 plan=plan_info(tx, p, split_k=p.split_k, grid=p.grid_x))
@@ -1144,9 +1150,10 @@ def main():
             secondary.append(r)
             print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s",
                   file=sys.stderr, flush=True)
-    for m in (1, 16, 64):
-        if want("bf16_decode") or want(f"bf16_decode_{m}"):
-            r = bench_decode16(tx, dev, m, 8192, 8192, max(args.steps, 20), 3, flush)
+    for m, km in ((1, False), (16, False), (64, False), (1, True), (16, True), (64, True)):
+        name = "bf16_decode_kmajor" if km else "bf16_decode"
+        if want(name) or want(f"{name}_{m}"):
+            r = bench_decode16(tx, dev, m, 8192, 8192, max(args.steps, 20), 3, flush, kmajor=km)
             secondary.append(r)
             print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
                   f"({100 * r['frac_hbm']:.1f}% HBM); isolated launch "

@@ -275,9 +275,13 @@ def test_decode_f8_plans():
 def test_decode16_plans():
     """The 16-bit decode kernel: which descriptors take it, its explicit block, split-K."""
     D16 = tx.KERNEL_DECODE_16BIT
-    # K-major B, mixed operand types, scales, int32 C: not this kernel
-    assert tx.plan(tx.make_desc(16, 4096, 4096, tx.BF16, tx.BF16,
-                                flags=tx.FLAG_B_KMAJOR)).kernel == tx.KERNEL_GEMM_16BIT
+    # K-major B (q @ k.T at decode, or a weight kept [N][K]) too, ldb defaulting to K
+    p = tx.plan(tx.make_desc(16, 4096, 4000, tx.BF16, tx.BF16, lda=4000,
+                             flags=tx.FLAG_B_KMAJOR))
+    assert p.kernel == D16 and p.desc.ldb == 4000 and (p.desc.block_m, p.desc.block_k) == (16, 128)
+    assert tx.plan(tx.make_desc(64, 300, 72, tx.F16, tx.F32, ldb=80,
+                                flags=tx.FLAG_B_KMAJOR | tx.FLAG_ACCUMULATE)).kernel == D16
+    # mixed operand types: not this kernel
     assert _err(tx.make_desc(16, 4096, 4096, tx.BF16, tx.F16)) == tx.ERR_UNSUPPORTED
     # an explicit GEMM tile at decode shape runs that tile; the decode block at M > 64 is refused
     assert tx.plan(tx.make_desc(16, 4096, 4096, tx.BF16, tx.BF16,

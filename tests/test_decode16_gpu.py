@@ -168,3 +168,63 @@ def test_decode16_after_w8a8_on_one_workspace(gpu):
         assert np.array_equal(from_device(c8), want8)
         assert np.abs(from_device(c16) - want16).max() < 1e-5
     assert not from_device(ws[:65536]).any()  # every arrival counter back at zero
+
+
+@pytest.mark.parametrize("M,N,K,kind,out_kind", [
+    (16, 8192, 8192, "bf16", "f32"), (1, 4096, 4096, "f16", "f16"), (64, 1024, 2048, "bf16", "bf16"),
+    (33, 4100, 2050, "bf16", "bf16"), (7, 1000, 3000, "f16", "f32"), (17, 130, 129, "bf16", "f32"),
+    (50, 520, 127, "f16", "f32"), (5, 61, 1, "bf16", "f32")])
+def test_decode16_kmajor_b(gpu, M, N, K, kind, out_kind):
+    """B K-major (q @ k.T at decode; a weight kept [N][K]): B stored [N][K'] whose columns
+    past K and rows past N hold NaN (A's padding holds Inf), so the chunk that crosses K
+    must be zeroed on both sides.  Against the oracle, and against the same dot with B
+    row-major: bit for bit with one batch a split (each lane's fragment holds the same K
+    indices), else within fp32 summation order (each strip starts at its own batch)."""
+    import torch
+    say(f"decode16 K-major B {kind}->{out_kind} M={M} N={N} K={K}")
+    tdt = getattr(torch, TORCH_DT[kind])
+    odt = getattr(torch, TORCH_DT[out_kind])
+    a, b = operands(M, N, K, kind, 5 * M + K)
+    up = lambda x: -(-x // 8) * 8 + 8
+    A = np.full((M, up(K)), 0x7F80 if kind == "bf16" else 0x7C00, dtype=np.uint16)
+    A[:, :K] = a
+    Bt = np.full((N + 3, up(K)), 0x7FC0 if kind == "bf16" else 0x7E00, dtype=np.uint16)
+    Bt[:N, :K] = b.T
+    da = to_device(A, gpu).view(tdt)[:, :K]
+    db = to_device(Bt, gpu).view(tdt)[:N, :K].t()
+    c = tx.dot(da, db, out_dtype=odt)
+    p = tx.plan_for(da, db, tx.tx_type(c), ldc=c.stride(0))
+    assert p.kernel == tx.KERNEL_DECODE_16BIT and p.desc.flags & tx.FLAG_B_KMAJOR
+    c_row = tx.dot(da, to_device(b, gpu).view(tdt), out_dtype=odt)
+    torch.cuda.synchronize()
+    got = from_device(c)
+    if -(-K // 128) <= p.split_k:  # at most one batch a split: the row-major order
+        assert np.array_equal(got.view(np.uint8), from_device(c_row).view(np.uint8))
+    ref = as_f32(oracle_16bit(a, b, kind, out_kind, (p.desc.block_m, p.desc.block_n,
+                                                       p.desc.block_k)), out_kind)
+    check_close(as_f32(got, out_kind), ref, atol=ATOL, rtol=RTOL, what=f"decode16 K-major")
+    if out_kind == "f32":
+        assert np.abs(got - exact(a, b, kind)).max() < 1e-5
+
+
+def test_decode16_kmajor_b_accumulate_deterministic(gpu):
+    """K-major B with an fp32 acc and split-K 16: C = acc + A @ B, the same bits on every
+    launch."""
+    import torch
+    M, N, K = 16, 1024, 8192
+    say(f"decode16 K-major B acc M={M} N={N} K={K}")
+    a, b = operands(M, N, K, "bf16", 11)
+    da = to_device(a, gpu).view(torch.bfloat16)
+    db = to_device(np.ascontiguousarray(b.T), gpu).view(torch.bfloat16).t()
+    acc = np.random.default_rng(12).standard_normal((M, N)).astype(np.float32)
+    dacc = to_device(acc, gpu)
+    p = tx.plan_for(da, db, tx.F32, flags=tx.FLAG_ACCUMULATE)
+    assert p.kernel == tx.KERNEL_DECODE_16BIT and p.split_k == 16
+    outs = []
+    for _ in range(3):
+        c = tx.dot(da, db, acc=dacc)
+        torch.cuda.synchronize()
+        outs.append(from_device(c))
+    assert np.abs(outs[0] - (exact(a, b, "bf16") + acc)).max() < 1e-5
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))

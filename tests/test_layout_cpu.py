@@ -55,31 +55,34 @@ def test_plan_8bit_transposed_b():
     scaled one (W8A8: no K-major form) it is copied row-major."""
     bt = _t((64, 304), "int8")[:, :300].t()      # [300][64] view, columns 304 bytes apart
     a = txdot.aligned_rows(_t((16, 300), "int8"), col_ok=False)
-    b = txdot.aligned_rows(bt, col_ok=txdot._b_col_ok(bt, True))
+    assert txdot._b_kmajor_ok(a, bt, tx.I32, tx.SCALE_NONE, (0, 0, 0), 0)
+    b = txdot.aligned_rows(bt, col_ok=True)
     assert b is bt
     p = txdot.plan_for(a, b, tx.I32)
     assert p.desc.flags & tx.FLAG_B_KMAJOR and p.desc.ldb == 304
-    b = txdot.aligned_rows(bt, col_ok=txdot._b_col_ok(bt, False))
+    assert not txdot._b_kmajor_ok(a, bt, tx.BF16, tx.SCALE_ROWCOL, (0, 0, 0), 0)
+    b = txdot.aligned_rows(bt, col_ok=False)
     assert b.stride(1) == 1 and b.shape == (300, 64)
     p = txdot.plan_for(a, b, tx.BF16, tx.SCALE_ROWCOL)
     assert not p.desc.flags & tx.FLAG_B_KMAJOR
 
 
-@pytest.mark.parametrize("dtype_name,txt,tile,other", [
-    ("int8", tx.I32, (256, 256, 128), (128, 128, 128)),
-    ("bfloat16", tx.F32, (256, 256, 64), (128, 128, 64))])
-def test_transposed_b_with_an_explicit_block(dtype_name, txt, tile, other):
-    """K-major B only where the tile has that form: the planner's own choice or that tile
-    asked for by name; another block copies B row-major (dot) or is refused (plan_for)."""
+@pytest.mark.parametrize("dtype_name,txt,M,tile,other", [
+    ("int8", tx.I32, 16, (256, 256, 128), (128, 128, 128)),
+    ("bfloat16", tx.F32, 16, (16, 64, 128), (128, 128, 64)),
+    ("bfloat16", tx.F32, 100, (256, 256, 64), (64, 64, 32))])
+def test_transposed_b_with_an_explicit_block(dtype_name, txt, M, tile, other):
+    """K-major B where the tile has that form: the planner's own choice, or that tile asked
+    for by name; another block copies B row-major (dot) or is refused (plan_for)."""
     bt = _t((64, 304), dtype_name)[:, :300].t()
-    a = txdot.aligned_rows(_t((16, 300), dtype_name), col_ok=False)
+    a = txdot.aligned_rows(_t((M, 300), dtype_name), col_ok=False)
     for blk in ((0, 0, 0), tile):
-        assert txdot._b_col_ok(bt, True, blk)
+        assert txdot._b_kmajor_ok(a, bt, txt, tx.SCALE_NONE, blk, 0)
         p = txdot.plan_for(a, bt, txt, block=blk)
         assert p.desc.flags & tx.FLAG_B_KMAJOR and (p.desc.block_m, p.desc.block_n,
                                                     p.desc.block_k) == tile
-    assert not txdot._b_col_ok(bt, True, other)
-    b = txdot.aligned_rows(bt, col_ok=txdot._b_col_ok(bt, True, other))
+    assert not txdot._b_kmajor_ok(a, bt, txt, tx.SCALE_NONE, other, 0)
+    b = txdot.aligned_rows(bt, col_ok=False)
     assert b.stride(1) == 1
     assert not txdot.plan_for(a, b, txt, block=other).desc.flags & tx.FLAG_B_KMAJOR
     with pytest.raises(ValueError, match="transposed view"):

@@ -135,6 +135,16 @@ def _cases():
         out.append(("attn", 100 + i, dict(Z=1, H=2, N=128 * int(rng.integers(6, 17)),
                                           D=[64, 128][i % 2], bf16=i >= 2, causal=i % 2 == 0,
                                           block=(128, 64))))
+    # K-major B (q @ k.T) in 8-bit dots: the planner's choice and the 256 tile named
+    for i in range(16):
+        out.append(("i8_i32", 200 + i, dict(M=_dim(rng, 700), N=_dim(rng, 700), K=_dim(rng, 900),
+                                            block=[(0, 0, 0), (256, 256, 128)][i % 2],
+                                            kmajor=True)))
+    for i in range(16):
+        fa, fb = [("e4m3", "e4m3"), ("e5m2", "e5m2"), ("e4m3", "e5m2"), ("e5m2", "e4m3")][i % 4]
+        out.append(("fp8", 200 + i, dict(M=_dim(rng, 600), N=_dim(rng, 600), K=_dim(rng, 900),
+                                         fa=fa, fb=fb, block=[(0, 0, 0), (256, 256, 128)][i // 8],
+                                         kmajor=True)))
     return out
 
 
@@ -158,11 +168,14 @@ def _codes(rng, shape, fmt):
     return np.where((c & 0x7F) == 0x7F, c & 0xF0, c).astype(np.uint8)
 
 
-def _run_i8_i32(gpu, seed, M, N, K, block):
+def _run_i8_i32(gpu, seed, M, N, K, block, kmajor=False):
     import torch
     a, b = uniform_i8((M, K), seed), uniform_i8((K, N), seed + 1)
-    c = tx.dot(dev_view(_junk_padded(a, seed + 2), (M, K), gpu),
-               dev_view(_junk_padded(b, seed + 3), (K, N), gpu), out_dtype=torch.int32,
+    if kmajor:  # B a transposed view of junk-padded [N][K'] storage
+        db = dev_view(_junk_padded(np.ascontiguousarray(b.T), seed + 3), (N, K), gpu).t()
+    else:
+        db = dev_view(_junk_padded(b, seed + 3), (K, N), gpu)
+    c = tx.dot(dev_view(_junk_padded(a, seed + 2), (M, K), gpu), db, out_dtype=torch.int32,
                block=block)
     torch.cuda.synchronize()
     # float64 products and sums are exact here (|sum| <= 127^2 K < 2^53), and BLAS-fast
@@ -185,7 +198,7 @@ def _run_w8a8(gpu, seed, M, N, K, block):
     assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches"
 
 
-def _run_fp8(gpu, seed, M, N, K, fa, fb, block):
+def _run_fp8(gpu, seed, M, N, K, fa, fb, block, kmajor=False):
     import torch
     rng = np.random.default_rng(seed)
     a, b = _codes(rng, (M, K), fa), _codes(rng, (K, N), fb)
@@ -193,9 +206,13 @@ def _run_fp8(gpu, seed, M, N, K, fa, fb, block):
     tdt = {"e4m3": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}
     otype = {"e4m3": oracle.F8E4M3, "e5m2": oracle.F8E5M2}
     pa, _ = padded(a, nan[fa])
-    pb, _ = padded(b, nan[fb])
-    c = tx.dot(dev_view(pa, (M, K), gpu, tdt[fa]), dev_view(pb, (K, N), gpu, tdt[fb]),
-               out_dtype=torch.float32, block=block)
+    if kmajor:  # B a transposed view of NaN-padded [N][K'] storage
+        pb, _ = padded(np.ascontiguousarray(b.T), nan[fb])
+        db = dev_view(pb, (N, K), gpu, tdt[fb]).t()
+    else:
+        pb, _ = padded(b, nan[fb])
+        db = dev_view(pb, (K, N), gpu, tdt[fb])
+    c = tx.dot(dev_view(pa, (M, K), gpu, tdt[fa]), db, out_dtype=torch.float32, block=block)
     torch.cuda.synchronize()
     ref = oracle.tiled_dot(a, b, a_type=otype[fa], b_type=otype[fb], c_type=oracle.F32,
                            block=(128, 128, 128))
@@ -279,11 +296,12 @@ def test_sweep(gpu, family, i, case):
         run16(gpu, c["M"], c["N"], c["K"], c["kind"], c["out"], c["block"], c["kmajor"],
               seed=seed)
     elif family == "i8_i32":
-        _run_i8_i32(gpu, seed, c["M"], c["N"], c["K"], c["block"])
+        _run_i8_i32(gpu, seed, c["M"], c["N"], c["K"], c["block"], c.get("kmajor", False))
     elif family == "w8a8":
         _run_w8a8(gpu, seed, c["M"], c["N"], c["K"], c["block"])
     elif family == "fp8":
-        _run_fp8(gpu, seed, c["M"], c["N"], c["K"], c["fa"], c["fb"], c["block"])
+        _run_fp8(gpu, seed, c["M"], c["N"], c["K"], c["fa"], c["fb"], c["block"],
+                 c.get("kmajor", False))
     elif family == "fp8_block":
         _run_fp8_block(gpu, seed, c["M"], c["N"], c["K"], c["out"], c["block"])
     elif family == "mx":

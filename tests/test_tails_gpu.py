@@ -99,10 +99,14 @@ def test_16bit_ragged(gpu, M, N, K, kind, out, block):
     run16(gpu, M, N, K, kind, out, block)
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 261, 203), (64, 50, 70)])
-def test_16bit_ragged_kmajor_b(gpu, M, N, K):
-    """K-major B (q @ k.T): B's chunk that crosses K is zeroed in registers too."""
-    run16(gpu, M, N, K, "bf16", "f32", kmajor=True)
+@pytest.mark.parametrize("M,N,K,block", [(300, 261, 203, (0, 0, 0)), (64, 50, 70, (256, 256, 64)),
+                                         (64, 50, 70, (0, 0, 0))])
+def test_16bit_ragged_kmajor_b(gpu, M, N, K, block):
+    """K-major B (q @ k.T): B's chunk that crosses K is zeroed in registers too, on the
+    256 tile and (M <= 64, the planner's choice) the decode kernel."""
+    p = run16(gpu, M, N, K, "bf16", "f32", block=block, kmajor=True)
+    assert p.kernel == (tx.KERNEL_DECODE_16BIT if M <= 64 and block == (0, 0, 0)
+                        else tx.KERNEL_GEMM_16BIT)
 
 
 @pytest.mark.parametrize("M,N,K,block", [(300, 261, 203, (256, 256, 128)),
@@ -133,8 +137,10 @@ def test_int8_ragged(gpu, M, N, K, block):
 @pytest.mark.parametrize("kmajor", [False, True])
 def test_16bit_every_element_of_the_chunk_crossing_n(gpu, N, out, kmajor):
     """The 256 tile's edge epilogue stores the chunk that crosses N element by element:
-    N mod 4 (fp32 C) and N mod 8 (bf16 C) take every value the chunk can leave."""
-    run16(gpu, 64, N, 70, "bf16", out, kmajor=kmajor)
+    N mod 4 (fp32 C) and N mod 8 (bf16 C) take every value the chunk can leave.  (M = 64
+    would take the decode kernel: the tile is named.)"""
+    p = run16(gpu, 64, N, 70, "bf16", out, block=(256, 256, 64), kmajor=kmajor)
+    assert p.kernel == tx.KERNEL_GEMM_16BIT
 
 
 @pytest.mark.parametrize("N", [49, 50, 51])
@@ -290,12 +296,14 @@ def test_contiguous_unaligned_operands(gpu):
                 rtol=RTOL, what="contiguous unaligned")
 
 
-@pytest.mark.parametrize("M,N", [(5, 220), (64, 3)])
-def test_16bit_k1_kmajor_b(gpu, M, N):
+@pytest.mark.parametrize("M,N,block", [(5, 220, (0, 0, 0)), (64, 3, (0, 0, 0)),
+                                       (5, 220, (256, 256, 64))])
+def test_16bit_k1_kmajor_b(gpu, M, N, block):
     """K = 1 with B a transposed view (q @ k.T with one head dim): the single row of B has
     elements ldk apart, which is the K-major layout; the stride of a size-1 dimension says
-    nothing about the layout."""
-    run16(gpu, M, N, 1, "bf16", "f32", kmajor=True)
+    nothing about the layout.  The decode kernel (the planner's choice) and the 256 tile."""
+    p = run16(gpu, M, N, 1, "bf16", "f32", block=block, kmajor=True)
+    assert p.desc.flags & tx.FLAG_B_KMAJOR
 
 
 @pytest.mark.parametrize("out", ["i32", "bf16"])

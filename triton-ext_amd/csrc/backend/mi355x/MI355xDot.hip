@@ -217,11 +217,16 @@ const DecodeF8KernelFn kDecodeF8ScaledKernels[4] = TX_DF8_SLICES(true, 0, 0);
 #undef TX_DF8_SLICES
 // The 16-bit decode kernel by [fp16 / bf16][slice of 16, 32, 48, 64 rows].
 typedef void (*Decode16KernelFn)(Decode16Args);
-const Decode16KernelFn kDecode16Kernels[2][4] = {
-    {decode16_kernel<16, false>, decode16_kernel<32, false>, decode16_kernel<48, false>,
-     decode16_kernel<64, false>},
-    {decode16_kernel<16, true>, decode16_kernel<32, true>, decode16_kernel<48, true>,
-     decode16_kernel<64, true>}};
+// [B K-major][bf16][slice rows / 16 - 1]
+const Decode16KernelFn kDecode16Kernels[2][2][4] = {
+    {{decode16_kernel<16, false>, decode16_kernel<32, false>, decode16_kernel<48, false>,
+      decode16_kernel<64, false>},
+     {decode16_kernel<16, true>, decode16_kernel<32, true>, decode16_kernel<48, true>,
+      decode16_kernel<64, true>}},
+    {{decode16_kernel<16, false, true>, decode16_kernel<32, false, true>,
+      decode16_kernel<48, false, true>, decode16_kernel<64, false, true>},
+     {decode16_kernel<16, true, true>, decode16_kernel<32, true, true>,
+      decode16_kernel<48, true, true>, decode16_kernel<64, true, true>}}};
 
 // MFMA format code of an MX operand type (-1 if it has none).
 int mxFormat(int32_t t) {
@@ -422,14 +427,13 @@ int64_t decodeWorkspace(const tx_dot_desc &d, int ksplit) {
 
 // The 16-bit decode kernel (decode16.h): both operands bf16 or both fp16,
 // no scales, C in their type or fp32 (accumulating only into fp32, which
-// validate() enforces), B row-major, M <= 64 (one slice), one arrival
-// counter of the fixed region per 64-column strip.
+// validate() enforces), B row-major or K-major, M <= 64 (one slice), one
+// arrival counter of the fixed region per 64-column strip.
 int decode16Rows(const tx_dot_desc &d) { return (int)(16 * cdiv(d.M > 0 ? d.M : 1, 16)); }
 bool useDecode16(const tx_dot_desc &d) {
   return (d.a_type == TX_BF16 || d.a_type == TX_F16) && d.b_type == d.a_type &&
          d.scale_mode == TX_SCALE_NONE && (d.c_type == d.a_type || d.c_type == TX_F32) &&
-         !(d.flags & TX_FLAG_B_KMAJOR) && d.M <= kDec16MaxM &&
-         cdiv(d.N, kDec16StripN) <= kDec16MaxStrips;
+         d.M <= kDec16MaxM && cdiv(d.N, kDec16StripN) <= kDec16MaxStrips;
 }
 // Its tile as the arith_intensity pass names it: the slice (16 ceil(M / 16)
 // rows) x a 64-column strip x 128-row K batches.  (No 16-bit GEMM tile has
@@ -961,7 +965,8 @@ int launchDecode16(const tx_dot_plan &plan, const void *A, const void *B, void *
   a.partials = need > 0 ? reinterpret_cast<float *>(static_cast<uint8_t *>(ws) +
                                                     kDecodeCounterBytes)
                         : nullptr;
-  const Decode16KernelFn fn = kDecode16Kernels[d.a_type == TX_BF16][decode16Rows(d) / 16 - 1];
+  const Decode16KernelFn fn = kDecode16Kernels[(d.flags & TX_FLAG_B_KMAJOR) != 0]
+                                               [d.a_type == TX_BF16][decode16Rows(d) / 16 - 1];
   hipLaunchKernelGGL(fn, dim3(plan.grid_x), dim3(plan.block_threads), 0, stream, a);
   TX_HIP_CHECK(hipGetLastError());
   return TX_OK;

@@ -43,6 +43,17 @@
 // zero-filled chunk.  An A chunk that crosses K is loaded whole and its
 // elements past K are zeroed in registers (they would meet B's zero rows,
 // but a row's padding may hold Inf or NaN, and Inf * 0 is NaN).
+//
+// BT: B stored K-major ([N][K] row-major, row stride ldb; q . k^T with k
+// row-major, or a weight kept [out][in]).  A strip is then 64 rows of that
+// storage, staged like A's rows (256 bytes of a batch each, chunk c of row r
+// at c ^ (r & 15)), and the wave's fragment of columns 16 w .. 16 w + 15 is
+// read with ds_read_b128 like an A tile: lane l gets column 16 w + l % 16 at
+// K 8 (l / 16) .. +7 of the step, the K indices of the A fragment it meets.
+// B's chunk that crosses K is loaded whole too, and zeroed in registers like
+// A's.  Each strip starts its split's batches at its own batch (strip mod the
+// split's batch count), so its fp32 sums can differ from the row-major form's
+// in the last bits.
 #pragma once
 
 #include <type_traits>
@@ -145,6 +156,48 @@ __device__ __forceinline__ void dec16_read_pair(uint32_t blo, uint32_t bhi, uint
 #undef TX_D16_OUT
 #undef TX_D16_TR
 
+// The same with B K-major: two K steps' B fragments (ds_read_b128 at `b0` /
+// `b1`) and the T A fragments of each.
+#define TX_D16K_T(t, off)                                                                  \
+  "ds_read_b128 %[x0" #t "], %[a0] offset:" #off "\n\tds_read_b128 %[x1" #t "], %[a1] offset:" #off \
+  "\n\t"
+#define TX_D16K_O(t) [x0##t] "=&v"(a[0][t]), [x1##t] "=&v"(a[1][t])
+#define TX_D16K_HEAD "ds_read_b128 %[y0], %[b0]\n\tds_read_b128 %[y1], %[b1]\n\t"
+#define TX_D16K_BO [y0] "=&v"(bq[0]), [y1] "=&v"(bq[1])
+#define TX_D16K_IN [b0] "v"(b0), [b1] "v"(b1), [a0] "v"(a0), [a1] "v"(a1)
+template <int T>
+__device__ __forceinline__ void dec16_read_pair_kmajor(uint32_t b0, uint32_t b1, uint32_t a0,
+                                                       uint32_t a1, i32x4_t (&bq)[2],
+                                                       i32x4_t (&a)[2][T]) {
+  if constexpr (T == 1)
+    asm volatile(TX_D16K_HEAD TX_D16K_T(0, 0) "s_waitcnt lgkmcnt(0)"
+                 : TX_D16K_BO, TX_D16K_O(0)
+                 : TX_D16K_IN
+                 : "memory");
+  else if constexpr (T == 2)
+    asm volatile(TX_D16K_HEAD TX_D16K_T(0, 0) TX_D16K_T(1, 4096) "s_waitcnt lgkmcnt(0)"
+                 : TX_D16K_BO, TX_D16K_O(0), TX_D16K_O(1)
+                 : TX_D16K_IN
+                 : "memory");
+  else if constexpr (T == 3)
+    asm volatile(TX_D16K_HEAD TX_D16K_T(0, 0) TX_D16K_T(1, 4096) TX_D16K_T(2, 8192)
+                 "s_waitcnt lgkmcnt(0)"
+                 : TX_D16K_BO, TX_D16K_O(0), TX_D16K_O(1), TX_D16K_O(2)
+                 : TX_D16K_IN
+                 : "memory");
+  else
+    asm volatile(TX_D16K_HEAD TX_D16K_T(0, 0) TX_D16K_T(1, 4096) TX_D16K_T(2, 8192)
+                 TX_D16K_T(3, 12288) "s_waitcnt lgkmcnt(0)"
+                 : TX_D16K_BO, TX_D16K_O(0), TX_D16K_O(1), TX_D16K_O(2), TX_D16K_O(3)
+                 : TX_D16K_IN
+                 : "memory");
+}
+#undef TX_D16K_IN
+#undef TX_D16K_BO
+#undef TX_D16K_HEAD
+#undef TX_D16K_O
+#undef TX_D16K_T
+
 template <bool BF>
 __device__ __forceinline__ f32x4_t mfma16x16x32(const i32x4_t &a, const i32x4_t &b,
                                                 const f32x4_t &c) {
@@ -173,7 +226,7 @@ __device__ __forceinline__ i32x4_t dec16_mask_k(const i32x4_t &v, int64_t k, int
   return i32x4_t{o[0], o[1], o[2], o[3]};
 }
 
-template <int SR, bool BF>
+template <int SR, bool BF, bool BT = false>
 __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode16_kernel(Decode16Args p) {
   typedef Decode16Cfg<SR> Cfg;
   constexpr int S = Cfg::S, SLOT = Cfg::SLOT, T = Cfg::T;
@@ -197,29 +250,50 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode16_kernel(Decode16
   if (b_end > total_batches)
     b_end = total_batches;
   const int nb = b_end > b_begin ? b_end - b_begin : 0; // the same for every wave
+  // K-major B: each strip walks its split's batches from its own starting
+  // batch (strip mod nb), so the workgroups running at once read rows of B's
+  // storage at different K offsets, not all at one offset of rows ldb apart.
+  const int rot = BT && nb > 0 ? strip % nb : 0;
+  auto batch = [&](int i) { // the split's i-th batch to run (i < nb)
+    if constexpr (!BT)
+      return b_begin + i;
+    const int j = i + rot;
+    return b_begin + (j >= nb ? j - nb : j);
+  };
 
   // Loads of the split's batch i into `slot`: B rows 32 wave .. +31 of the
   // batch (load u: rows 8 q .. 8 q + 7, q = 4 wave + u, lane l' fetching
-  // chunk (l' % 8) ^ (row & 7) of row 8 q + l' / 8) and A rows 4 q .. 4 q + 3
-  // (q = A_LOADS wave + u, lane l' fetching chunk (l' % 16) ^ (row & 15) of
-  // row 4 q + l' / 16).  No loaded VGPR is live across the loop (with
+  // chunk (l' % 8) ^ (row & 7) of row 8 q + l' / 8; K-major B: storage rows
+  // n0 + 4 q .. +3, lane l' fetching chunk (l' % 16) ^ (row & 15) of row
+  // 4 q + l' / 16, as for A) and A rows 4 q .. 4 q + 3 (q = A_LOADS wave + u,
+  // lane l' fetching chunk (l' % 16) ^ (row & 15) of row 4 q + l' / 16).  No loaded VGPR is live across the loop (with
   // direct-to-LDS loads pending the compiler could only wait for one with
   // vmcnt(0)).  For i >= nb every load reads the zero chunk, so each step
   // issues the same loads.
   auto issue = [&](int i, uint8_t *slot) {
     const bool live = i < nb;
-    const int b = b_begin + i;
+    const int b = live ? batch(i) : b_begin + i;
     const int64_t k0 = (int64_t)b * kDec16BatchK;
     const bool mask = !live || n_edge || b >= p.k_main_batches;
 #pragma unroll
     for (int u = 0; u < Cfg::B_LOADS; ++u) {
       const int q = Cfg::B_LOADS * wave + u;
-      const int row = 8 * q + (lane >> 3);
-      const int c = (lane & 7) ^ (row & 7);
-      const int64_t k = k0 + row, n = n0 + 8 * c;
-      const void *src = p.B + k * p.ldb + n;
-      if (mask && (!live || k >= p.K || n >= p.N))
-        src = tx_zero_chunk;
+      const void *src;
+      if constexpr (BT) {
+        const int r = 4 * q + (lane >> 4);
+        const int c = (lane & 15) ^ (r & 15);
+        const int64_t n = n0 + r, k = k0 + 8 * c;
+        src = p.B + n * p.ldb + k;
+        if (mask && (!live || n >= p.N || k >= p.K))
+          src = tx_zero_chunk;
+      } else {
+        const int row = 8 * q + (lane >> 3);
+        const int c = (lane & 7) ^ (row & 7);
+        const int64_t k = k0 + row, n = n0 + 8 * c;
+        src = p.B + k * p.ldb + n;
+        if (mask && (!live || k >= p.K || n >= p.N))
+          src = tx_zero_chunk;
+      }
       dma16_stream(src, (lds_void *)(slot + q * 1024)); // B is read once
     }
 #pragma unroll
@@ -248,29 +322,44 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode16_kernel(Decode16
   const int cb = 2 * wave + ((L & 3) >> 1);
   const uint32_t b_lo = (L >> 2) * 128 + ((cb ^ (L >> 2)) << 4) + 8 * (L & 1) + 8 * G * 128;
   const uint32_t b_hi = b_lo + 4 * 128 - ((cb ^ (L >> 2)) << 4) + ((cb ^ ((L >> 2) + 4)) << 4);
-  uint32_t a_k[4];
+  // K-major B, step ks: storage row 16 wave + L, chunk (4 ks + G) ^ L.
+  uint32_t a_k[4], bk_k[4];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
+  for (int ks = 0; ks < 4; ++ks) {
     a_k[ks] = Cfg::A_OFF + L * 256 + (((4 * ks + G) ^ L) << 4);
+    bk_k[ks] = (16 * wave + L) * 256 + (((4 * ks + G) ^ L) << 4);
+  }
 
   auto consume = [&](const uint8_t *slot, int i) {
     const uint32_t base = lds_addr(slot);
-    const bool tail = b_begin + i >= p.k_main_batches;
-    const int64_t k0 = (int64_t)(b_begin + i) * kDec16BatchK;
+    const int b = batch(i);
+    const bool tail = b >= p.k_main_batches;
+    const int64_t k0 = (int64_t)b * kDec16BatchK;
 #pragma unroll
     for (int pr = 0; pr < 2; ++pr) {
-      v2i_t lo[2], hi[2];
+      i32x4_t bq[2];
       i32x4_t a[2][T];
-      dec16_read_pair<T>(base + b_lo + pr * 8192, base + b_hi + pr * 8192,
-                         base + a_k[2 * pr], base + a_k[2 * pr + 1], lo, hi, a);
+      if constexpr (BT) {
+        dec16_read_pair_kmajor<T>(base + bk_k[2 * pr], base + bk_k[2 * pr + 1],
+                                  base + a_k[2 * pr], base + a_k[2 * pr + 1], bq, a);
+      } else {
+        v2i_t lo[2], hi[2];
+        dec16_read_pair<T>(base + b_lo + pr * 8192, base + b_hi + pr * 8192,
+                           base + a_k[2 * pr], base + a_k[2 * pr + 1], lo, hi, a);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          bq[h] = i32x4_t{lo[h].x, lo[h].y, hi[h].x, hi[h].y};
+      }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const i32x4_t bf = {lo[h].x, lo[h].y, hi[h].x, hi[h].y};
+        i32x4_t bf = bq[h];
         if (tail) {
           const int64_t k = k0 + 32 * (2 * pr + h) + 8 * G;
 #pragma unroll
           for (int t = 0; t < T; ++t)
             a[h][t] = dec16_mask_k(a[h][t], k, p.K);
+          if constexpr (BT)
+            bf = dec16_mask_k(bf, k, p.K);
         }
 #pragma unroll
         for (int t = 0; t < T; ++t)

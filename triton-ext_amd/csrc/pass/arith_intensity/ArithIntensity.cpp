@@ -198,12 +198,12 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
         ((d->scale_mode == TX_SCALE_ROWCOL && d->c_type == TX_BF16) ||
          (d->scale_mode == TX_SCALE_NONE && d->c_type == TX_I32));
     // The 16-bit decode kernel: both operands bf16 or both fp16, no scales,
-    // C in their type or fp32, B row-major, M <= 64, N up to its 16384
-    // strips of 64 columns.  It streams B once with split-K.
+    // C in their type or fp32, B row-major or K-major, M <= 64, N up to its
+    // 16384 strips of 64 columns.  It streams B once with split-K.
     const bool decode16 =
         (d->a_type == TX_BF16 || d->a_type == TX_F16) && d->b_type == d->a_type &&
         d->scale_mode == TX_SCALE_NONE && (d->c_type == d->a_type || d->c_type == TX_F32) &&
-        !(d->flags & TX_FLAG_B_KMAJOR) && d->M <= 64 && d->N <= (int64_t)16384 * 64;
+        d->M <= 64 && d->N <= (int64_t)16384 * 64;
     // The fp8 decode kernel: fp8 x fp8 with fp32 C, or e4m3 x e4m3 with
     // 128-block scales and bf16 / fp32 C; B row-major, M <= 64, N up to its
     // 16384 strips of 128 columns.

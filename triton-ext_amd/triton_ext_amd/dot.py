@@ -77,19 +77,30 @@ def _layout(t, col_ok=True):
     return None, 0
 
 
-# The one tile per operand width that has a K-major B form.
-_KMAJOR_TILE = {2: (256, 256, 64), 1: (256, 256, 128)}
-
-
-def _b_col_ok(b, unscaled=True, block=(0, 0, 0)):
+def _b_col_ok(b, unscaled=True):
     """B may be K-major (a transposed view): 16-bit operands, and 8-bit ones in an
-    unscaled dot (int8 -> int32, fp8 -> fp32), when the planner picks the tile
-    (block (0, 0, 0)) or the block asked for is the one tile with that form;
-    otherwise a transposed B is copied row-major."""
-    tile = _KMAJOR_TILE.get(b.element_size())
-    if tile is None or (b.element_size() == 1 and not unscaled):
-        return False
-    return tuple(block) in ((0, 0, 0), tile)
+    unscaled dot (int8 -> int32, fp8 -> fp32)."""
+    return b.element_size() == 2 or (b.element_size() == 1 and unscaled)
+
+
+def _kmajor_plans(a, b, c_tx, scale_mode, block, flags):
+    """Whether the planner takes this dot with B K-major: always with its own
+    tile choice (block (0, 0, 0)), and for a block asked for when that tile has
+    a K-major form (asked of the planner, on 16-byte strides)."""
+    if tuple(block) == (0, 0, 0):
+        return True
+    M, K = a.shape
+    N = b.shape[1]
+    d = capi.make_desc(M, N, K, tx_type(a), c_tx, b_type=tx_type(b), scale_mode=scale_mode,
+                       block=block, lda=_row_pitch(K, 1), ldb=_row_pitch(K, 1),
+                       ldc=_row_pitch(N, 1), flags=flags | capi.FLAG_B_KMAJOR)
+    p = capi.DotPlan()
+    return capi.load().tx_dot_plan_create(ctypes.byref(d), ctypes.byref(p)) == capi.OK
+
+
+def _b_kmajor_ok(a, b, c_tx, scale_mode, block, flags):
+    return (a.dim() == 2 and b.dim() == 2 and _b_col_ok(b, scale_mode == capi.SCALE_NONE)
+            and _kmajor_plans(a, b, c_tx, scale_mode, block, flags))
 
 
 def aligned_rows(t, col_ok=True):
@@ -122,10 +133,10 @@ def plan_for(a, b, out_dtype_tx, scale_mode=capi.SCALE_NONE, block=(0, 0, 0), fl
     M, K = a.shape
     N = b.shape[1]
     a_kind, a_ld = _layout(a, col_ok=False)
-    b_kind, b_ld = _layout(b, col_ok=_b_col_ok(b, scale_mode == capi.SCALE_NONE, block))
+    b_kind, b_ld = _layout(b, col_ok=_b_kmajor_ok(a, b, out_dtype_tx, scale_mode, block, flags))
     if a_kind == "row" and b_kind is None and _layout(b)[0] == "col":
-        raise ValueError("B is a transposed view: K-major B runs on the 256x256 tile of a "
-                         "16-bit or unscaled 8-bit dot only; copy it row-major")
+        raise ValueError("B is a transposed view, and this dot has no K-major form (16-bit, "
+                         "or unscaled 8-bit, on a tile with that form); copy it row-major")
     if a_kind != "row" or b_kind is None:
         raise ValueError("A rows must be contiguous, and B rows (or B's columns) too")
     b_kmajor = b_kind == "col"
@@ -179,24 +190,12 @@ def dot(a, b, out=None, out_dtype=None, scale_a=None, scale_b=None, scale_mode=N
     K and N may be any size.  Operands whose rows do not start 16 bytes
     apart are copied to padded storage first (one extra pass), as is a
     transposed view of A, or of an 8-bit B in a scaled dot, in row-major form
-    (a 16-bit B, and an 8-bit B of an unscaled int8 or fp8 dot, run K-major on
-    the 256x256 tile, unless `block` names another tile: then B is copied too);
-    a new output is a view of padded storage; a given `out` must already have
+    (a 16-bit B, and an 8-bit B of an unscaled int8 or fp8 dot, run K-major,
+    unless `block` names a tile without that form: then B is copied too); a
+    new output is a view of padded storage; a given `out` must already have
     16-byte row strides.
     """
     import torch
-    if plan is None:
-        unscaled = scale_a is None and scale_b is None and scale_mode in (None, capi.SCALE_NONE)
-        a, b = aligned_rows(a, col_ok=False), aligned_rows(b, col_ok=_b_col_ok(b, unscaled, block))
-    if acc is not None:
-        if acc.dtype not in (torch.float32, torch.int32) or acc.dim() != 2:
-            raise ValueError("acc must be an fp32 or int32 [M, N] tensor")
-        if out is None:
-            out = new_output(acc.shape[0], acc.shape[1], acc.dtype, acc.device)
-            out.copy_(acc)
-        elif out.data_ptr() != acc.data_ptr():
-            out.copy_(acc)
-        flags |= capi.FLAG_ACCUMULATE
     ta = tx_type(a)
     if scale_mode is None:
         if scale_a is None:
@@ -205,11 +204,26 @@ def dot(a, b, out=None, out_dtype=None, scale_a=None, scale_b=None, scale_mode=N
             scale_mode = capi.SCALE_ROWCOL if ta == capi.I8 else capi.SCALE_BLOCK128
     if out is not None:
         c_tx = tx_type(out)
+    elif acc is not None and acc.dtype in (torch.float32, torch.int32):
+        c_tx = tx_type(acc)  # the new output is a copy of acc
     elif out_dtype is not None:
         c_tx = tx_type(torch.empty(0, dtype=out_dtype))
     else:
         c_tx = capi.I32 if (ta == capi.I8 and scale_mode == capi.SCALE_NONE) else (
             capi.BF16 if ta in (capi.BF16, capi.I8, capi.F8E4M3) else capi.F32)
+    if acc is not None:
+        flags |= capi.FLAG_ACCUMULATE
+    if plan is None:
+        a = aligned_rows(a, col_ok=False)
+        b = aligned_rows(b, col_ok=_b_kmajor_ok(a, b, c_tx, scale_mode, block, flags))
+    if acc is not None:
+        if acc.dtype not in (torch.float32, torch.int32) or acc.dim() != 2:
+            raise ValueError("acc must be an fp32 or int32 [M, N] tensor")
+        if out is None:
+            out = new_output(acc.shape[0], acc.shape[1], acc.dtype, acc.device)
+            out.copy_(acc)
+        elif out.data_ptr() != acc.data_ptr():
+            out.copy_(acc)
     M, N = a.shape[0], b.shape[1]
     if out is None:
         out = new_output(M, N, _torch_dtype(c_tx), a.device)
