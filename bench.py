@@ -57,7 +57,8 @@ def parse():
                          "only; vendor_decode: its decode shapes only), tail, "
                          "w8a8 (or "
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256; w8a8 also runs i32_16, the unscaled "
-                         "int8 -> int32 decode at M=16), bf16_decode (or bf16_decode_1, _16, _64: "
+                         "int8 -> int32 decode at M=16, and i32_16_kmajor, the same with B "
+                         "K-major), bf16_decode (or bf16_decode_1, _16, _64: "
                          "bf16 at N = K = 8192 on the 16-bit decode kernel; bf16_decode_kmajor, "
                          "or _1, _16, _64: the same with B K-major), fp8_decode (or "
                          "fp8_decode_1, _16, _64: block-scaled e4m3 at N = K = 7168 on the fp8 "
@@ -338,21 +339,26 @@ def bench_w8a8(tx, dev, M, N, K, steps, warmup, flush, seed=3, block=(0, 0, 0)):
                 plan=plan_info(tx, p, split_k=p.split_k, grid=p.grid_x))
 
 
-def bench_decode_i32(tx, dev, M, N, K, steps, warmup, flush, seed=3):
+def bench_decode_i32(tx, dev, M, N, K, steps, warmup, flush, seed=3, kmajor=False):
     """int8 x int8 -> int32 tt.dot of decode shape (no scales): the W8A8 decode kernel with
-    its int32 epilogue, timed like the W8A8 lines (cold, B from HBM)."""
+    its int32 epilogue, timed like the W8A8 lines (cold, B from HBM).  kmajor: B stored
+    [N][K] and passed as its transpose (the 8-bit decode kernel's int8 form)."""
     import torch
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     a = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
     b = torch.randint(-127, 128, (K, N), generator=g, device=dev, dtype=torch.int8)
+    if kmajor:
+        b = b.t().contiguous().t()   # same values, K-major storage
     c = torch.empty((M, N), dtype=torch.int32, device=dev)
     run = Launcher(tx, a, b, c)
+    assert bool(run.plan.desc.flags & tx.FLAG_B_KMAJOR) == kmajor
     iso, _ = time_cold(run, steps, warmup, flush)
     med = time_cold_in_stream(run, flush)
     nbytes = M * K + K * N + M * N * 4
     p = run.plan
-    return dict(workload=f"int8 -> int32 (no scales) M={M} N={N} K={K}", ms=med, ms_isolated=iso,
+    return dict(workload=f"int8 -> int32 (no scales) M={M} N={N} K={K}" +
+                (", B K-major" if kmajor else ""), ms=med, ms_isolated=iso,
                 gbps=nbytes / med / 1e6, frac_hbm=nbytes / med / 1e-3 / HBM,
                 tops=2.0 * M * N * K / med / 1e9,
                 plan=plan_info(tx, p, split_k=p.split_k, grid=p.grid_x))
@@ -1133,11 +1139,12 @@ def main():
             print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
                   f"({100 * r['frac_hbm']:.1f}% HBM); isolated launch "
                   f"{r['ms_isolated'] * 1e3:.2f} us", file=sys.stderr, flush=True)
-    if want("w8a8") or want("i32_16"):
-        r = bench_decode_i32(tx, dev, 16, 8192, 8192, max(args.steps, 20), 3, flush)
-        secondary.append(r)
-        print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
-              f"({100 * r['frac_hbm']:.1f}% HBM)", file=sys.stderr, flush=True)
+    for km in (False, True):
+        if want("w8a8") or want("i32_16_kmajor" if km else "i32_16"):
+            r = bench_decode_i32(tx, dev, 16, 8192, 8192, max(args.steps, 20), 3, flush, kmajor=km)
+            secondary.append(r)
+            print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
+                  f"({100 * r['frac_hbm']:.1f}% HBM)", file=sys.stderr, flush=True)
     for m in (1, 16, 64):
         if want("fp8_decode") or want(f"fp8_decode_{m}"):
             r = bench_decode_f8(tx, dev, m, 7168, 7168, max(args.steps, 20), 3, flush)

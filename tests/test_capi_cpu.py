@@ -259,9 +259,11 @@ def test_decode_f8_plans():
                                     scale_mode=tx.SCALE_BLOCK128)).kernel == DF8
     assert tx.plan(tx.make_desc(16, 4096, 4096, tx.F8E4M3, tx.F32, flags=tx.FLAG_ACCUMULATE,
                                 scale_mode=tx.SCALE_BLOCK128)).kernel == DF8
-    # K-major B: not this kernel, the 256x256x128 tile
+    # K-major B (unscaled): this kernel too; with block scales, no K-major form
     p = tx.plan(tx.make_desc(16, 4096, 4096, tx.F8E4M3, tx.F32, flags=tx.FLAG_B_KMAJOR))
-    assert p.kernel == tx.KERNEL_GEMM_F8 and (p.desc.block_m, p.desc.block_k) == (256, 128)
+    assert p.kernel == DF8 and (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (16, 128, 128)
+    assert _err(tx.make_desc(16, 4096, 4096, tx.F8E4M3, tx.BF16, scale_mode=tx.SCALE_BLOCK128,
+                             flags=tx.FLAG_B_KMAJOR)) == tx.ERR_UNSUPPORTED
     # an explicit 8-bit tile at decode shape runs that tile
     assert tx.plan(tx.make_desc(16, 4096, 4096, tx.F8E4M3, tx.F32,
                                 block=(256, 256, 128))).kernel == tx.KERNEL_GEMM_F8
@@ -306,7 +308,7 @@ def test_decode16_plans():
 
 def test_b_kmajor_plans():
     """K-major B (q @ k.T): bf16/fp16 on the 256x256x64 tile, int8 -> int32 and unscaled
-    fp8 on the 256x256x128 tile; ldb defaulting to K."""
+    fp8 on the 256x256x128 tile, and at M <= 64 on the decode kernels; ldb defaulting to K."""
     p = tx.plan(tx.make_desc(512, 384, 192, tx.BF16, tx.F32, flags=tx.FLAG_B_KMAJOR))
     assert p.kernel == tx.KERNEL_GEMM_16BIT
     assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (256, 256, 64)
@@ -320,10 +322,20 @@ def test_b_kmajor_plans():
                           (tx.F8E5M2, tx.F8E4M3, tx.F32, tx.KERNEL_GEMM_F8),
                           (tx.F8E4M3, tx.F8E5M2, tx.F32, tx.KERNEL_GEMM_F8),
                           (tx.F8E5M2, tx.F8E5M2, tx.F32, tx.KERNEL_GEMM_F8)):
-        p = tx.plan(tx.make_desc(16, 300, 200, a, c, b_type=b, lda=208, ldb=208,
+        p = tx.plan(tx.make_desc(100, 300, 200, a, c, b_type=b, lda=208, ldb=208,
                                  flags=tx.FLAG_B_KMAJOR))
         assert p.kernel == kern and p.desc.ldb == 208
         assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (256, 256, 128)
+        # M <= 64: the 8-bit decode kernel, or the 256 tile by name
+        p = tx.plan(tx.make_desc(16, 300, 200, a, c, b_type=b, lda=208, ldb=208,
+                                 flags=tx.FLAG_B_KMAJOR))
+        assert p.kernel == tx.KERNEL_DECODE_F8 and p.desc.ldb == 208
+        assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (16, 128, 128)
+        assert tx.plan(tx.make_desc(16, 300, 200, a, c, b_type=b, lda=208, ldb=208,
+                                    block=(256, 256, 128), flags=tx.FLAG_B_KMAJOR)).kernel == kern
+    # W8A8 (row x column scales): no K-major decode form
+    assert _err(tx.make_desc(16, 256, 256, tx.I8, tx.BF16, scale_mode=tx.SCALE_ROWCOL,
+                             block=(16, 128, 128), flags=tx.FLAG_B_KMAJOR)) == tx.ERR_UNSUPPORTED
     # scaled 8-bit dots and other 8-bit tiles have no K-major form
     for a, c, sm, blk in ((tx.I8, tx.BF16, tx.SCALE_ROWCOL, (0, 0, 0)),
                           (tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, (0, 0, 0)),

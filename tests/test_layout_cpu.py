@@ -68,7 +68,8 @@ def test_plan_8bit_transposed_b():
 
 
 @pytest.mark.parametrize("dtype_name,txt,M,tile,other", [
-    ("int8", tx.I32, 16, (256, 256, 128), (128, 128, 128)),
+    ("int8", tx.I32, 16, (16, 128, 128), (128, 128, 128)),
+    ("int8", tx.I32, 100, (256, 256, 128), (128, 128, 128)),
     ("bfloat16", tx.F32, 16, (16, 64, 128), (128, 128, 64)),
     ("bfloat16", tx.F32, 100, (256, 256, 64), (64, 64, 32))])
 def test_transposed_b_with_an_explicit_block(dtype_name, txt, M, tile, other):

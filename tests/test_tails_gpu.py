@@ -351,20 +351,32 @@ def _kmajor_b(b, fill, gpu, tdtype=None, junk=None):
     return dev_view(st, (N, K), gpu, tdtype).t()
 
 
-def _assert_kmajor_plan(da, db, c, kernel):
-    p = tx.plan_for(da, db, tx.tx_type(c), ldc=c.stride(0))
-    assert p.desc.flags & tx.FLAG_B_KMAJOR and p.kernel == kernel
-    assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (256, 256, 128)
+def _assert_kmajor_plan(da, db, c, kernel, block=(0, 0, 0)):
+    """The plan is K-major on the 256x256x128 tile (`kernel`), or at M <= 64 with the
+    planner's choice on the 8-bit decode kernel; returns it."""
+    p = tx.plan_for(da, db, tx.tx_type(c), block=block, ldc=c.stride(0))
+    assert p.desc.flags & tx.FLAG_B_KMAJOR
+    if da.shape[0] <= 64 and block == (0, 0, 0):
+        assert p.kernel == tx.KERNEL_DECODE_F8 and (p.desc.block_n, p.desc.block_k) == (128, 128)
+    else:
+        assert p.kernel == kernel
+        assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (256, 256, 128)
+    return p
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 263, 391), (40, 50, 200), (17, 1001, 999),
-                                   (5, 220, 1), (512, 512, 1024), (64, 3, 129)])
-def test_int8_ragged_kmajor_b(gpu, M, N, K):
+@pytest.mark.parametrize("M,N,K,block", [
+    (300, 263, 391, (0, 0, 0)), (512, 512, 1024, (0, 0, 0)),
+    (40, 50, 200, (0, 0, 0)), (17, 1001, 999, (0, 0, 0)), (5, 220, 1, (0, 0, 0)),
+    (64, 3, 129, (0, 0, 0)), (16, 4096, 4096, (0, 0, 0)), (33, 300, 4001, (0, 0, 0)),
+    (40, 50, 200, (256, 256, 128)), (17, 1001, 999, (256, 256, 128)),
+    (5, 220, 1, (256, 256, 128)), (64, 3, 129, (256, 256, 128))])
+def test_int8_ragged_kmajor_b(gpu, M, N, K, block):
     """int8 -> int32 with B a transposed view (q @ k.T): B's padding columns past K and rows
     past N hold random bytes, as do A's.  The chunk that crosses K is loaded whole on both
-    sides, so both are zeroed past K (junk times junk is not zero).  Bit-exact."""
+    sides, so both are zeroed past K (junk times junk is not zero).  Bit-exact, on the
+    256x256x128 tile and (M <= 64) the 8-bit decode kernel."""
     import torch
-    say(f"tails int8 K-major B M={M} N={N} K={K}")
+    say(f"tails int8 K-major B M={M} N={N} K={K} block={block}")
     a, b = uniform_i8((M, K), 81), uniform_i8((K, N), 82)
     junk = np.random.default_rng(83)
     sa, _ = padded(a, 0)
@@ -372,23 +384,27 @@ def test_int8_ragged_kmajor_b(gpu, M, N, K):
     sa[M:, :] = junk.integers(-128, 128, size=sa[M:, :].shape)
     da = dev_view(sa, (M, K), gpu)
     db = _kmajor_b(b, 0, gpu, junk=junk)
-    c = tx.dot(da, db, out_dtype=torch.int32)
+    c = tx.dot(da, db, out_dtype=torch.int32, block=block)
     torch.cuda.synchronize()
-    _assert_kmajor_plan(da, db, c, tx.KERNEL_GEMM_I8)
+    _assert_kmajor_plan(da, db, c, tx.KERNEL_GEMM_I8, block)
     ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.I32, block=(64, 64, 64))
     assert np.array_equal(from_device(c), ref)
 
 
 @pytest.mark.parametrize("fa,fb", [("e4m3", "e4m3"), ("e4m3", "e5m2"), ("e5m2", "e4m3"),
                                    ("e5m2", "e5m2")])
-@pytest.mark.parametrize("M,N,K", [(300, 263, 391), (16, 1024, 256), (130, 77, 1)])
-def test_fp8_ragged_kmajor_b(gpu, fa, fb, M, N, K):
+@pytest.mark.parametrize("M,N,K,block", [(300, 263, 391, (0, 0, 0)), (130, 77, 1, (0, 0, 0)),
+                                         (16, 1024, 256, (256, 256, 128)),
+                                         (16, 1024, 256, (0, 0, 0)), (33, 777, 1001, (0, 0, 0)),
+                                         (1, 4096, 4096, (0, 0, 0))])
+def test_fp8_ragged_kmajor_b(gpu, fa, fb, M, N, K, block):
     """Unscaled fp8 -> fp32 with B a transposed view, NaN codes (0x7F, NaN in e4m3 and
-    e5m2) in both operands' padding; e4m3 / e5m2 in every mix.  Against the oracle, and
-    bit for bit against the same dot with B row-major (the K-major fragment holds the
-    same K indices in the same bytes)."""
+    e5m2) in both operands' padding; e4m3 / e5m2 in every mix.  Against the oracle; on the
+    256 tile also bit for bit against the same dot with B row-major (the K-major fragment
+    holds the same K indices in the same bytes).  M <= 64 with the planner's choice runs
+    the 8-bit decode kernel."""
     import torch
-    say(f"tails fp8 K-major B {fa}x{fb} M={M} N={N} K={K}")
+    say(f"tails fp8 K-major B {fa}x{fb} M={M} N={N} K={K} block={block}")
     rng = np.random.default_rng(M + N + K)
     a, b = _codes8(rng, (M, K), fa), _codes8(rng, (K, N), fb)
     tdt = {"e4m3": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}
@@ -396,12 +412,12 @@ def test_fp8_ragged_kmajor_b(gpu, fa, fb, M, N, K):
     sa, _ = padded(a, 0x7F)
     da = dev_view(sa, (M, K), gpu, tdt[fa])
     db = _kmajor_b(b, 0x7F, gpu, tdt[fb])
-    c = tx.dot(da, db, out_dtype=torch.float32)
+    c = tx.dot(da, db, out_dtype=torch.float32, block=block)
     sb, _ = padded(b, 0x7F)
     c_row = tx.dot(da, dev_view(sb, (K, N), gpu, tdt[fb]), out_dtype=torch.float32,
                    block=(256, 256, 128))
     torch.cuda.synchronize()
-    _assert_kmajor_plan(da, db, c, tx.KERNEL_GEMM_F8)
+    p = _assert_kmajor_plan(da, db, c, tx.KERNEL_GEMM_F8, block)
     got = from_device(c)
     ref = oracle.tiled_dot(a, b, a_type=otype[fa], b_type=otype[fb], c_type=oracle.F32,
                            block=(256, 256, 128))
@@ -410,7 +426,8 @@ def test_fp8_ragged_kmajor_b(gpu, fa, fb, M, N, K):
     rms = lambda q, f: float(np.sqrt(np.mean(dec(q, f) ** 2)))
     check_close(got, ref, atol=ATOL, rtol=RTOL, scale=math.sqrt(K) * rms(a, fa) * rms(b, fb),
                 what=f"fp8 K-major {fa}x{fb}")
-    assert np.array_equal(got.view(np.uint32), from_device(c_row).view(np.uint32))
+    if p.kernel == tx.KERNEL_GEMM_F8:
+        assert np.array_equal(got.view(np.uint32), from_device(c_row).view(np.uint32))
 
 
 @pytest.mark.parametrize("kind", ["i8", "e4m3"])
@@ -435,3 +452,43 @@ def test_8bit_kmajor_b_full_size(gpu, kind):
     torch.cuda.synchronize()
     _assert_kmajor_plan(a, k.t(), c, kern)
     assert torch.equal(c.view(torch.int32), c_row.view(torch.int32))
+
+
+@pytest.mark.parametrize("kind", ["i8", "e4m3"])
+def test_8bit_kmajor_decode_accumulate(gpu, kind):
+    """tl.dot(a, k.T, acc) at decode shape on the 8-bit decode kernel, split-K: C = acc +
+    A @ B (int32 exactly; fp32 within summation error), the same bits on every launch."""
+    import torch
+    M, N, K = 16, 1024, 8192
+    say(f"tails 8-bit K-major decode acc {kind}")
+    rng = np.random.default_rng(97)
+    if kind == "i8":
+        a, b = uniform_i8((M, K), 95), uniform_i8((K, N), 96)
+        acc = rng.integers(-2 ** 20, 2 ** 20, size=(M, N)).astype(np.int32)
+        da, tdt = to_device(a, gpu), None
+        exact = (a.astype(np.int64) @ b.astype(np.int64) + acc).astype(np.int64)
+    else:
+        a, b = _codes8(rng, (M, K), "e4m3"), _codes8(rng, (K, N), "e4m3")
+        acc = rng.standard_normal((M, N)).astype(np.float32)
+        tdt = torch.float8_e4m3fn
+        da = to_device(a, gpu).view(tdt)
+        fa = oracle.e4m3_to_f32(a).astype(np.float64)
+        fb = oracle.e4m3_to_f32(b).astype(np.float64)
+        exact = fa @ fb + acc
+    db = to_device(np.ascontiguousarray(b.T), gpu)
+    db = (db if tdt is None else db.view(tdt)).t()
+    dacc = to_device(acc, gpu)
+    outs = []
+    for _ in range(3):
+        c = tx.dot(da, db, acc=dacc)
+        torch.cuda.synchronize()
+        outs.append(from_device(c))
+    p = tx.plan_for(da, db, tx.tx_type(c), flags=tx.FLAG_ACCUMULATE)
+    assert p.kernel == tx.KERNEL_DECODE_F8 and p.split_k > 1 and p.desc.flags & tx.FLAG_B_KMAJOR
+    if kind == "i8":
+        assert np.array_equal(outs[0].astype(np.int64), exact)
+    else:
+        s = math.sqrt(K) * math.sqrt((fa ** 2).mean()) * math.sqrt((fb ** 2).mean())
+        check_close(outs[0], exact, atol=ATOL, rtol=RTOL, scale=s, what="fp8 K-major acc")
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))

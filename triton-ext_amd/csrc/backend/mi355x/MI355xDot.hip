@@ -204,16 +204,20 @@ const DecodeKernelFn kDecodeKernels[4] = {decode_i8_kernel<1>, decode_i8_kernel<
 const DecodeKernelFn kDecodeRowsKernels[3] = {decode_rows_i8_kernel<64, 6>,
                                               decode_rows_i8_kernel<128, 4>,
                                               decode_rows_i8_kernel<256, 3>};
-// The fp8 decode kernel: unscaled by [A e4m3 / e5m2][B e4m3 / e5m2][slice of
-// 16, 32, 48, 64 rows], block-scaled (e4m3) by slice.
+// The 8-bit ring decode kernel: unscaled fp8 by [B K-major][A e4m3 / e5m2]
+// [B e4m3 / e5m2][slice of 16, 32, 48, 64 rows], block-scaled (e4m3) by
+// slice, int8 -> int32 with B K-major by slice.
 typedef void (*DecodeF8KernelFn)(DecodeF8Args);
-#define TX_DF8_SLICES(SC, FA, FB)                                                          \
-  {decode_f8_kernel<16, SC, FA, FB>, decode_f8_kernel<32, SC, FA, FB>,                     \
-   decode_f8_kernel<48, SC, FA, FB>, decode_f8_kernel<64, SC, FA, FB>}
-const DecodeF8KernelFn kDecodeF8Kernels[2][2][4] = {
-    {TX_DF8_SLICES(false, 0, 0), TX_DF8_SLICES(false, 0, 1)},
-    {TX_DF8_SLICES(false, 1, 0), TX_DF8_SLICES(false, 1, 1)}};
-const DecodeF8KernelFn kDecodeF8ScaledKernels[4] = TX_DF8_SLICES(true, 0, 0);
+#define TX_DF8_SLICES(SC, FA, FB, BT, I8)                                                  \
+  {decode_f8_kernel<16, SC, FA, FB, BT, I8>, decode_f8_kernel<32, SC, FA, FB, BT, I8>,     \
+   decode_f8_kernel<48, SC, FA, FB, BT, I8>, decode_f8_kernel<64, SC, FA, FB, BT, I8>}
+const DecodeF8KernelFn kDecodeF8Kernels[2][2][2][4] = {
+    {{TX_DF8_SLICES(false, 0, 0, false, false), TX_DF8_SLICES(false, 0, 1, false, false)},
+     {TX_DF8_SLICES(false, 1, 0, false, false), TX_DF8_SLICES(false, 1, 1, false, false)}},
+    {{TX_DF8_SLICES(false, 0, 0, true, false), TX_DF8_SLICES(false, 0, 1, true, false)},
+     {TX_DF8_SLICES(false, 1, 0, true, false), TX_DF8_SLICES(false, 1, 1, true, false)}}};
+const DecodeF8KernelFn kDecodeF8ScaledKernels[4] = TX_DF8_SLICES(true, 0, 0, false, false);
+const DecodeF8KernelFn kDecodeI8KmajorKernels[4] = TX_DF8_SLICES(false, 0, 0, true, true);
 #undef TX_DF8_SLICES
 // The 16-bit decode kernel by [fp16 / bf16][slice of 16, 32, 48, 64 rows].
 typedef void (*Decode16KernelFn)(Decode16Args);
@@ -463,18 +467,23 @@ int64_t decode16Workspace(const tx_dot_desc &d, int ksplit) {
          ksplit * decode16_split_bytes(cdiv(d.N, kDec16StripN), decode16Rows(d));
 }
 
-// The fp8 decode kernel (decode_f8.h): fp8 x fp8 (e4m3 / e5m2 in any mix)
-// with fp32 C, or e4m3 x e4m3 with 128-block scales and bf16 / fp32 C; B
-// row-major, M <= 64, one arrival counter per 128-column strip.
+// The 8-bit ring decode kernel (decode_f8.h): fp8 x fp8 (e4m3 / e5m2 in any
+// mix) with fp32 C, B row-major or K-major; e4m3 x e4m3 with 128-block scales
+// and bf16 / fp32 C, B row-major; int8 -> int32 with B K-major (row-major int8
+// runs decode_i8.h); M <= 64, one arrival counter per 128-column strip.
 bool useDecodeF8(const tx_dot_desc &d) {
   const bool fa = d.a_type == TX_F8E4M3 || d.a_type == TX_F8E5M2;
   const bool fb = d.b_type == TX_F8E4M3 || d.b_type == TX_F8E5M2;
-  if (!fa || !fb || (d.flags & TX_FLAG_B_KMAJOR) || d.M > kDec8MaxM ||
-      cdiv(d.N, kDec8StripN) > kDec16MaxStrips)
+  const bool kmajor = (d.flags & TX_FLAG_B_KMAJOR) != 0;
+  if (d.M > kDec8MaxM || cdiv(d.N, kDec8StripN) > kDec16MaxStrips)
+    return false;
+  if (d.a_type == TX_I8 && d.b_type == TX_I8)
+    return kmajor && d.scale_mode == TX_SCALE_NONE && d.c_type == TX_I32;
+  if (!fa || !fb)
     return false;
   if (d.scale_mode == TX_SCALE_NONE)
     return d.c_type == TX_F32;
-  return d.scale_mode == TX_SCALE_BLOCK128 && d.a_type == TX_F8E4M3 &&
+  return !kmajor && d.scale_mode == TX_SCALE_BLOCK128 && d.a_type == TX_F8E4M3 &&
          d.b_type == TX_F8E4M3 && (d.c_type == TX_BF16 || d.c_type == TX_F32);
 }
 // Its tile: the slice (16 ceil(M / 16) rows) x a 128-column strip x 128-row
@@ -694,7 +703,7 @@ extern "C" TX_API const char *tx_kernel_name(int32_t kernel) {
   case TX_KERNEL_GEMM_MX: return "gemm_mx_mfma_scale16x16x128";
   case TX_KERNEL_GEMM_MX_BF16: return "mx_upcast_bf16+gemm_16bit_mfma32x32x16";
   case TX_KERNEL_DECODE_16BIT: return "decode_16bit_mfma16x16x32";
-  case TX_KERNEL_DECODE_F8: return "decode_f8_mfma16x16x128_f8f6f4";
+  case TX_KERNEL_DECODE_F8: return "decode_8bit_mfma16x16x128_f8f6f4|16x16x64_i8";
   default: return "?";
   }
 }
@@ -1006,9 +1015,11 @@ int launchDecodeF8(const tx_dot_plan &plan, const void *A, const void *B, void *
                                                     kDecodeCounterBytes)
                         : nullptr;
   const int si = decode16Rows(d) / 16 - 1;
+  const bool kmajor = (d.flags & TX_FLAG_B_KMAJOR) != 0;
   const DecodeF8KernelFn fn =
-      scaled ? kDecodeF8ScaledKernels[si]
-             : kDecodeF8Kernels[d.a_type == TX_F8E5M2][d.b_type == TX_F8E5M2][si];
+      d.a_type == TX_I8 ? kDecodeI8KmajorKernels[si]
+      : scaled          ? kDecodeF8ScaledKernels[si]
+                        : kDecodeF8Kernels[kmajor][d.a_type == TX_F8E5M2][d.b_type == TX_F8E5M2][si];
   hipLaunchKernelGGL(fn, dim3(plan.grid_x), dim3(plan.block_threads), 0, stream, a);
   TX_HIP_CHECK(hipGetLastError());
   return TX_OK;

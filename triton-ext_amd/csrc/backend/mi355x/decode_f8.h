@@ -48,6 +48,19 @@
 // zero-filled chunk.  An A chunk that crosses K is loaded whole and its bytes
 // past K are zeroed in registers (an fp8 NaN code in the padding times B's
 // zero rows would be NaN).
+//
+// BT: B stored K-major ([N][K] row-major, row stride ldb: q . k^T with k
+// row-major, or a weight kept [out][in]).  The strip's 128 rows of that
+// storage are staged like A's rows (128 bytes of a batch each, chunk c at
+// c ^ ((row >> 1) & 7)) and a column block's fragment is read like an A tile
+// (ds_read_b128 of chunks 2 G and 2 G + 1), so a lane holds the same K bytes
+// of B as of A.  B's chunk that crosses K is loaded whole and zeroed in
+// registers like A's.  Each strip starts its split's batches at its own batch
+// (strip mod the split's batch count), so the workgroups running at once read
+// B's rows at different K offsets.  I8 (with BT only): int8 x int8 -> int32,
+// C = sum or C += sum; per 16 x 16 block and batch two
+// v_mfma_i32_16x16x64_i8 on the same fragments (K bytes 32 G .. +15, then
+// +16 .. +31 of each lane), int32 partials, exact in any order.
 #pragma once
 
 #include <type_traits>
@@ -148,6 +161,53 @@ __device__ __forceinline__ void dec8_read(uint32_t b0, uint32_t b1, uint32_t a0,
 #undef TX_D8_OUT
 #undef TX_D8_TR
 
+// The same with B K-major: each column block's fragment is two 16-byte reads
+// (at b0 / b1 and their ^ 16, chunks 2 G and 2 G + 1), like A's, which are
+// at a0 and a0 ^ 16, +2 KiB per tile.
+#define TX_D8K_T(t, off)                                                                   \
+  "ds_read_b128 %[x0" #t "], %[a0] offset:" #off "\n\tds_read_b128 %[x1" #t "], %[a1] offset:" #off \
+  "\n\t"
+#define TX_D8K_O(t) [x0##t] "=&v"(a[t][0]), [x1##t] "=&v"(a[t][1])
+#define TX_D8K_HEAD                                                                        \
+  "ds_read_b128 %[y00], %[b0]\n\tds_read_b128 %[y01], %[b0x]\n\t"                           \
+  "ds_read_b128 %[y10], %[b1]\n\tds_read_b128 %[y11], %[b1x]\n\t"
+#define TX_D8K_BO                                                                          \
+  [y00] "=&v"(bk[0][0]), [y01] "=&v"(bk[0][1]), [y10] "=&v"(bk[1][0]), [y11] "=&v"(bk[1][1])
+#define TX_D8K_IN                                                                          \
+  [b0] "v"(b0), [b0x] "v"(b0 ^ 16u), [b1] "v"(b1), [b1x] "v"(b1 ^ 16u), [a0] "v"(a0),         \
+      [a1] "v"(a0 ^ 16u)
+template <int T>
+__device__ __forceinline__ void dec8_read_kmajor(uint32_t b0, uint32_t b1, uint32_t a0,
+                                                 i32x4_t (&bk)[2][2], i32x4_t (&a)[T][2]) {
+  if constexpr (T == 1)
+    asm volatile(TX_D8K_HEAD TX_D8K_T(0, 0) "s_waitcnt lgkmcnt(0)"
+                 : TX_D8K_BO, TX_D8K_O(0)
+                 : TX_D8K_IN
+                 : "memory");
+  else if constexpr (T == 2)
+    asm volatile(TX_D8K_HEAD TX_D8K_T(0, 0) TX_D8K_T(1, 2048) "s_waitcnt lgkmcnt(0)"
+                 : TX_D8K_BO, TX_D8K_O(0), TX_D8K_O(1)
+                 : TX_D8K_IN
+                 : "memory");
+  else if constexpr (T == 3)
+    asm volatile(TX_D8K_HEAD TX_D8K_T(0, 0) TX_D8K_T(1, 2048) TX_D8K_T(2, 4096)
+                 "s_waitcnt lgkmcnt(0)"
+                 : TX_D8K_BO, TX_D8K_O(0), TX_D8K_O(1), TX_D8K_O(2)
+                 : TX_D8K_IN
+                 : "memory");
+  else
+    asm volatile(TX_D8K_HEAD TX_D8K_T(0, 0) TX_D8K_T(1, 2048) TX_D8K_T(2, 4096)
+                 TX_D8K_T(3, 6144) "s_waitcnt lgkmcnt(0)"
+                 : TX_D8K_BO, TX_D8K_O(0), TX_D8K_O(1), TX_D8K_O(2), TX_D8K_O(3)
+                 : TX_D8K_IN
+                 : "memory");
+}
+#undef TX_D8K_IN
+#undef TX_D8K_BO
+#undef TX_D8K_HEAD
+#undef TX_D8K_O
+#undef TX_D8K_T
+
 // Zero the bytes of a 16-byte fragment at K index k .. k + 15 that lie at or
 // past K.
 __device__ __forceinline__ i32x4_t dec8_mask_k(const i32x4_t &v, int64_t k, int64_t K) {
@@ -164,13 +224,15 @@ __device__ __forceinline__ i32x4_t dec8_mask_k(const i32x4_t &v, int64_t k, int6
 }
 
 // FA, FB: the MFMA format codes of A and B (0 e4m3, 1 e5m2); SCALED takes
-// e4m3 x e4m3 with block scales.
-template <int SR, bool SCALED, int FA = 0, int FB = 0>
+// e4m3 x e4m3 with block scales.  BT: B K-major; I8: int8 -> int32 (BT only).
+template <int SR, bool SCALED, int FA = 0, int FB = 0, bool BT = false, bool I8 = false>
 __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_f8_kernel(DecodeF8Args p) {
   static_assert(!SCALED || (FA == 0 && FB == 0), "block scales take e4m3 operands");
+  static_assert(!BT || !SCALED, "K-major B: unscaled dots");
+  static_assert(!I8 || (BT && FA == 0 && FB == 0), "int8: the K-major form");
   typedef DecodeF8Cfg<SR, SCALED> Cfg;
   constexpr int S = Cfg::S, SLOT = Cfg::SLOT, T = Cfg::T;
-  typedef f32x4_t Acc;
+  typedef std::conditional_t<I8, i32x4_t, f32x4_t> Acc;
   __shared__ __attribute__((aligned(1024))) uint8_t ring[S * SLOT];
   __shared__ uint32_t last_flag;
 
@@ -188,28 +250,45 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_f8_kernel(DecodeF
   if (b_end > total_batches)
     b_end = total_batches;
   const int nb = b_end > b_begin ? b_end - b_begin : 0;
+  const int rot = BT && nb > 0 ? strip % nb : 0; // K-major B: the strip's first batch
+  auto batch = [&](int i) { // the split's i-th batch to run (i < nb)
+    if constexpr (!BT)
+      return b_begin + i;
+    const int j = i + rot;
+    return b_begin + (j >= nb ? j - nb : j);
+  };
 
   // Loads of the split's batch i into `slot`: B rows 32 wave .. +31 (load u:
   // rows 8 q .. +7, q = 4 wave + u, lane l' fetching chunk (l' % 8) ^ (row &
-  // 7) of row 8 q + l' / 8), A rows 8 q .. +7 (q = A_LOADS wave + u, lane l'
-  // fetching chunk (l' % 8) ^ ((row >> 1) & 7)), and with block scales wave
-  // 0's sa[row][kb] (lane = row) and wave 1's sb[kb][strip] (every lane).
-  // For i >= nb every load reads the zero chunk, so each step issues the same
-  // loads.
+  // 7) of row 8 q + l' / 8; K-major B: storage rows n0 + 8 q .. +7, lane l'
+  // fetching chunk (l' % 8) ^ ((row >> 1) & 7), as for A), A rows 8 q .. +7
+  // (q = A_LOADS wave + u, lane l' fetching chunk (l' % 8) ^ ((row >> 1) &
+  // 7)), and with block scales wave 0's sa[row][kb] (lane = row) and wave 1's
+  // sb[kb][strip] (every lane).  For i >= nb every load reads the zero chunk,
+  // so each step issues the same loads.
   auto issue = [&](int i, uint8_t *slot) {
     const bool live = i < nb;
-    const int b = b_begin + i;
+    const int b = live ? batch(i) : b_begin + i;
     const int64_t k0 = (int64_t)b * kDec8BatchK;
     const bool mask = !live || n_edge || b >= p.k_main_batches;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int q = 4 * wave + u;
       const int row = 8 * q + (lane >> 3);
-      const int c = (lane & 7) ^ (row & 7);
-      const int64_t k = k0 + row, n = n0 + 16 * c;
-      const void *src = p.B + k * p.ldb + n;
-      if (mask && (!live || k >= p.K || n >= p.N))
-        src = tx_zero_chunk;
+      const void *src;
+      if constexpr (BT) {
+        const int c = (lane & 7) ^ ((row >> 1) & 7);
+        const int64_t n = n0 + row, k = k0 + 16 * c;
+        src = p.B + n * p.ldb + k;
+        if (mask && (!live || n >= p.N || k >= p.K))
+          src = tx_zero_chunk;
+      } else {
+        const int c = (lane & 7) ^ (row & 7);
+        const int64_t k = k0 + row, n = n0 + 16 * c;
+        src = p.B + k * p.ldb + n;
+        if (mask && (!live || k >= p.K || n >= p.N))
+          src = tx_zero_chunk;
+      }
       dma16_stream(src, (lds_void *)(slot + q * 1024)); // B is read once
     }
 #pragma unroll
@@ -245,31 +324,44 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_f8_kernel(DecodeF
   // read q: row 32 G + 8 q + L / 2 (row & 7 = L / 2), chunk j, byte 8 (L % 2):
   // +1 KiB per read.  A, tile t: row 16 t + L ((row >> 1) & 7 = L / 2),
   // chunks 2 G and 2 G + 1 (the second at the first ^ 16): +2 KiB per tile.
+  // K-major B, block j: storage row 16 j + L, chunks 2 G and 2 G + 1, like A.
   uint32_t b_off[2];
 #pragma unroll
   for (int jj = 0; jj < 2; ++jj) {
     const int j = 2 * wave + jj;
-    b_off[jj] = (32 * G + (L >> 1)) * 128 + ((j ^ (L >> 1)) << 4) + 8 * (L & 1);
+    b_off[jj] = BT ? (16 * j + L) * 128 + (((2 * G) ^ (L >> 1)) << 4)
+                   : (32 * G + (L >> 1)) * 128 + ((j ^ (L >> 1)) << 4) + 8 * (L & 1);
   }
   const uint32_t a_off = Cfg::A_OFF + L * 128 + (((2 * G) ^ (L >> 1)) << 4);
 
   // operand formats FB (MFMA A := B columns) and FA; no hardware scales
-  auto mma = [&](const i32x8_t &bcol, const i32x8_t &arow, Acc c) -> Acc {
+  auto mma = [&](const i32x8_t &bcol, const i32x8_t &arow, f32x4_t c) -> f32x4_t {
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bcol, arow, c, FB, FA, 0, 0, 0, 0);
   };
 
   auto consume = [&](const uint8_t *slot, int i) {
     const uint32_t base = lds_addr(slot);
+    i32x4_t bk[2][2]; // column block jj's fragment (K-major B): chunks 2 G, 2 G + 1
     v2i_t bq[2][4];
     i32x4_t a[T][2];
-    dec8_read<T>(base + b_off[0], base + b_off[1], base + a_off, (base + a_off) ^ 16u, bq, a);
-    const int b = b_begin + i;
-    if (b >= p.k_main_batches) { // the K tail: bytes of A at or past K
+    if constexpr (BT)
+      dec8_read_kmajor<T>(base + b_off[0], base + b_off[1], base + a_off, bk, a);
+    else
+      dec8_read<T>(base + b_off[0], base + b_off[1], base + a_off, (base + a_off) ^ 16u, bq, a);
+    const int b = batch(i);
+    if (b >= p.k_main_batches) { // the K tail: bytes of A (and K-major B) at or past K
       const int64_t k = (int64_t)b * kDec8BatchK + 32 * G;
 #pragma unroll
       for (int t = 0; t < T; ++t) {
         a[t][0] = dec8_mask_k(a[t][0], k, p.K);
         a[t][1] = dec8_mask_k(a[t][1], k + 16, p.K);
+      }
+      if constexpr (BT) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          bk[jj][0] = dec8_mask_k(bk[jj][0], k, p.K);
+          bk[jj][1] = dec8_mask_k(bk[jj][1], k + 16, p.K);
+        }
       }
     }
     float s_row[T], s_col = 0.f;
@@ -287,19 +379,30 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_f8_kernel(DecodeF
     }
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
-      const i32x8_t bcol = {bq[jj][0].x, bq[jj][0].y, bq[jj][1].x, bq[jj][1].y,
-                            bq[jj][2].x, bq[jj][2].y, bq[jj][3].x, bq[jj][3].y};
+      if constexpr (I8) { // two K steps of 64: bytes 32 G .. +15, then +16 .. +31
 #pragma unroll
-      for (int t = 0; t < T; ++t) {
-        const i32x8_t arow = {a[t][0][0], a[t][0][1], a[t][0][2], a[t][0][3],
-                              a[t][1][0], a[t][1][1], a[t][1][2], a[t][1][3]};
-        if constexpr (SCALED) {
-          const Acc part = mma(bcol, arow, Acc{0, 0, 0, 0});
+        for (int t = 0; t < T; ++t) {
+          acc[t][jj] = mfma_i8_16(bk[jj][0], a[t][0], acc[t][jj]);
+          acc[t][jj] = mfma_i8_16(bk[jj][1], a[t][1], acc[t][jj]);
+        }
+      } else {
+        const i32x8_t bcol =
+            BT ? i32x8_t{bk[jj][0][0], bk[jj][0][1], bk[jj][0][2], bk[jj][0][3], bk[jj][1][0],
+                         bk[jj][1][1], bk[jj][1][2], bk[jj][1][3]}
+               : i32x8_t{bq[jj][0].x, bq[jj][0].y, bq[jj][1].x, bq[jj][1].y,
+                         bq[jj][2].x, bq[jj][2].y, bq[jj][3].x, bq[jj][3].y};
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            acc[t][jj][r] = __builtin_fmaf(part[r], s_row[t], acc[t][jj][r]);
-        } else {
-          acc[t][jj] = mma(bcol, arow, acc[t][jj]);
+        for (int t = 0; t < T; ++t) {
+          const i32x8_t arow = {a[t][0][0], a[t][0][1], a[t][0][2], a[t][0][3],
+                                a[t][1][0], a[t][1][1], a[t][1][2], a[t][1][3]};
+          if constexpr (SCALED) {
+            const f32x4_t part = mma(bcol, arow, f32x4_t{0, 0, 0, 0});
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[t][jj][r] = __builtin_fmaf(part[r], s_row[t], acc[t][jj][r]);
+          } else {
+            acc[t][jj] = mma(bcol, arow, acc[t][jj]);
+          }
         }
       }
     }
@@ -339,8 +442,20 @@ k_loop_done:
         const int m = 16 * t + L;
         if (m >= p.M)
           continue;
-        const float f[4] = {sum[t][jj][0], sum[t][jj][1], sum[t][jj][2], sum[t][jj][3]};
-        if (p.c_f32) { // fp32 C
+        if constexpr (I8) { // int32 C
+          int32_t *c = static_cast<int32_t *>(p.C) + (int64_t)m * p.ldc + col;
+          if (whole) {
+            i32x4_t v = sum[t][jj];
+            if (p.acc_c)
+              v += *reinterpret_cast<const i32x4_t *>(c);
+            *reinterpret_cast<i32x4_t *>(c) = v;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (col + r < p.N)
+                c[r] = p.acc_c ? c[r] + sum[t][jj][r] : sum[t][jj][r];
+          }
+        } else if (p.c_f32) { // fp32 C
           float *c = static_cast<float *>(p.C) + (int64_t)m * p.ldc + col;
           if (whole) {
             f32x4_t v = sum[t][jj];
@@ -351,9 +466,10 @@ k_loop_done:
 #pragma unroll
             for (int r = 0; r < 4; ++r)
               if (col + r < p.N)
-                c[r] = p.acc_c ? c[r] + f[r] : f[r];
+                c[r] = p.acc_c ? c[r] + sum[t][jj][r] : sum[t][jj][r];
           }
         } else { // bf16 C, rounded to nearest even
+          const float f[4] = {sum[t][jj][0], sum[t][jj][1], sum[t][jj][2], sum[t][jj][3]};
           uint16_t *c = static_cast<uint16_t *>(p.C) + (int64_t)m * p.ldc + col;
           if (whole) {
             uint2 w;
