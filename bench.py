@@ -58,7 +58,8 @@ def parse():
                          "w8a8 (or "
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256; w8a8 also runs i32_16, the unscaled "
                          "int8 -> int32 decode at M=16, and i32_16_kmajor, the same with B "
-                         "K-major), bf16_decode (or bf16_decode_1, _16, _64: "
+                         "K-major), w8a8_kmajor (or w8a8_kmajor_1, _16, _64: W8A8 with the "
+                         "weight kept [N][K]), bf16_decode (or bf16_decode_1, _16, _64: "
                          "bf16 at N = K = 8192 on the 16-bit decode kernel; bf16_decode_kmajor, "
                          "or _1, _16, _64: the same with B K-major), fp8_decode (or "
                          "fp8_decode_1, _16, _64: block-scaled e4m3 at N = K = 7168 on the fp8 "
@@ -316,16 +317,21 @@ def bench_vendor_8bit(dev, steps, warmup, seed=1):
     return out
 
 
-def bench_w8a8(tx, dev, M, N, K, steps, warmup, flush, seed=3, block=(0, 0, 0)):
+def bench_w8a8(tx, dev, M, N, K, steps, warmup, flush, seed=3, block=(0, 0, 0), kmajor=False):
+    """W8A8 of decode shape, B row-major (config 3); kmajor: the weight kept [N][K] and
+    passed as its transpose."""
     import torch
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     a = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
     b = torch.randint(-127, 128, (K, N), generator=g, device=dev, dtype=torch.int8)
+    if kmajor:
+        b = b.t().contiguous().t()   # same values, K-major storage
     sa = torch.rand((M,), generator=g, device=dev) * 0.019 + 0.001
     sb = torch.rand((N,), generator=g, device=dev) * 0.019 + 0.001
     c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     run = Launcher(tx, a, b, c, sa, sb, tx.SCALE_ROWCOL, block)
+    assert bool(run.plan.desc.flags & tx.FLAG_B_KMAJOR) == kmajor
     iso, _ = time_cold(run, steps, warmup, flush)
     med = time_cold_in_stream(run, flush)
     warm = time_back_to_back(run, steps, warmup)
@@ -333,7 +339,8 @@ def bench_w8a8(tx, dev, M, N, K, steps, warmup, flush, seed=3, block=(0, 0, 0)):
     p = run.plan
     # ms: a cold launch (B from HBM) inside a stream; ms_isolated: a lone launch
     # bracketed by its own events (adds the dispatch latency a stream hides)
-    return dict(workload=f"int8 W8A8 M={M} N={N} K={K}", ms=med, ms_isolated=iso,
+    return dict(workload=f"int8 W8A8 M={M} N={N} K={K}" + (", B K-major" if kmajor else ""),
+                ms=med, ms_isolated=iso,
                 ms_warm_mall=warm, gbps=nbytes / med / 1e6, frac_hbm=nbytes / med / 1e-3 / HBM,
                 tops=2.0 * M * N * K / med / 1e9,
                 plan=plan_info(tx, p, split_k=p.split_k, grid=p.grid_x))
@@ -1136,6 +1143,13 @@ def main():
             secondary.append(r)
             if m == 16:
                 w8a8_16 = r
+            print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
+                  f"({100 * r['frac_hbm']:.1f}% HBM); isolated launch "
+                  f"{r['ms_isolated'] * 1e3:.2f} us", file=sys.stderr, flush=True)
+    for m in (1, 16, 64):
+        if want("w8a8_kmajor") or want(f"w8a8_kmajor_{m}"):
+            r = bench_w8a8(tx, dev, m, 8192, 8192, max(args.steps, 20), 3, flush, kmajor=True)
+            secondary.append(r)
             print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
                   f"({100 * r['frac_hbm']:.1f}% HBM); isolated launch "
                   f"{r['ms_isolated'] * 1e3:.2f} us", file=sys.stderr, flush=True)

@@ -259,11 +259,12 @@ def test_decode_f8_plans():
                                     scale_mode=tx.SCALE_BLOCK128)).kernel == DF8
     assert tx.plan(tx.make_desc(16, 4096, 4096, tx.F8E4M3, tx.F32, flags=tx.FLAG_ACCUMULATE,
                                 scale_mode=tx.SCALE_BLOCK128)).kernel == DF8
-    # K-major B (unscaled): this kernel too; with block scales, no K-major form
-    p = tx.plan(tx.make_desc(16, 4096, 4096, tx.F8E4M3, tx.F32, flags=tx.FLAG_B_KMAJOR))
-    assert p.kernel == DF8 and (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (16, 128, 128)
-    assert _err(tx.make_desc(16, 4096, 4096, tx.F8E4M3, tx.BF16, scale_mode=tx.SCALE_BLOCK128,
-                             flags=tx.FLAG_B_KMAJOR)) == tx.ERR_UNSUPPORTED
+    # K-major B (a weight kept [N][K]): this kernel too, unscaled and block-scaled
+    for c, sm in ((tx.F32, 0), (tx.BF16, tx.SCALE_BLOCK128)):
+        p = tx.plan(tx.make_desc(16, 4096, 4096, tx.F8E4M3, c, scale_mode=sm,
+                                 flags=tx.FLAG_B_KMAJOR))
+        assert p.kernel == DF8 and (p.desc.block_m, p.desc.block_n, p.desc.block_k) == \
+            (16, 128, 128)
     # an explicit 8-bit tile at decode shape runs that tile
     assert tx.plan(tx.make_desc(16, 4096, 4096, tx.F8E4M3, tx.F32,
                                 block=(256, 256, 128))).kernel == tx.KERNEL_GEMM_F8
@@ -333,12 +334,18 @@ def test_b_kmajor_plans():
         assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (16, 128, 128)
         assert tx.plan(tx.make_desc(16, 300, 200, a, c, b_type=b, lda=208, ldb=208,
                                     block=(256, 256, 128), flags=tx.FLAG_B_KMAJOR)).kernel == kern
-    # W8A8 (row x column scales): no K-major decode form
-    assert _err(tx.make_desc(16, 256, 256, tx.I8, tx.BF16, scale_mode=tx.SCALE_ROWCOL,
-                             block=(16, 128, 128), flags=tx.FLAG_B_KMAJOR)) == tx.ERR_UNSUPPORTED
-    # scaled 8-bit dots and other 8-bit tiles have no K-major form
-    for a, c, sm, blk in ((tx.I8, tx.BF16, tx.SCALE_ROWCOL, (0, 0, 0)),
-                          (tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, (0, 0, 0)),
+    # W8A8 and block-scaled fp8 (weights kept [N][K]): the decode kernel at M <= 64, the
+    # 256 tile beyond
+    for a, c, sm, kern in ((tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_GEMM_I8),
+                           (tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, tx.KERNEL_GEMM_F8),
+                           (tx.F8E4M3, tx.F32, tx.SCALE_BLOCK128, tx.KERNEL_GEMM_F8)):
+        for M, want, blk in ((16, tx.KERNEL_DECODE_F8, (16, 128, 128)),
+                             (300, kern, (256, 256, 128))):
+            p = tx.plan(tx.make_desc(M, 512, 512, a, c, scale_mode=sm, flags=tx.FLAG_B_KMAJOR))
+            assert p.kernel == want and (p.desc.block_m, p.desc.block_n, p.desc.block_k) == blk
+    # the other 8-bit tiles have no K-major form
+    for a, c, sm, blk in ((tx.I8, tx.BF16, tx.SCALE_ROWCOL, (128, 128, 128)),
+                          (tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, (256, 224, 128)),
                           (tx.I8, tx.I32, 0, (128, 128, 128)),
                           (tx.I8, tx.I32, 0, (256, 224, 128))):
         assert _err(tx.make_desc(16, 256, 256, a, c, scale_mode=sm, block=blk,

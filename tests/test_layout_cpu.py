@@ -51,19 +51,19 @@ def test_plan_single_column_b(dtype_name, txt):
 
 
 def test_plan_8bit_transposed_b():
-    """An int8 B given as a transposed view runs K-major in an unscaled dot (int32 C); in a
-    scaled one (W8A8: no K-major form) it is copied row-major."""
+    """An int8 B given as a transposed view (a weight kept [N][K]) runs K-major, unscaled
+    (int32 C) or W8A8; with a block that has no K-major form it is copied row-major."""
     bt = _t((64, 304), "int8")[:, :300].t()      # [300][64] view, columns 304 bytes apart
     a = txdot.aligned_rows(_t((16, 300), "int8"), col_ok=False)
-    assert txdot._b_kmajor_ok(a, bt, tx.I32, tx.SCALE_NONE, (0, 0, 0), 0)
-    b = txdot.aligned_rows(bt, col_ok=True)
-    assert b is bt
-    p = txdot.plan_for(a, b, tx.I32)
-    assert p.desc.flags & tx.FLAG_B_KMAJOR and p.desc.ldb == 304
-    assert not txdot._b_kmajor_ok(a, bt, tx.BF16, tx.SCALE_ROWCOL, (0, 0, 0), 0)
+    for c, sm in ((tx.I32, tx.SCALE_NONE), (tx.BF16, tx.SCALE_ROWCOL)):
+        assert txdot._b_kmajor_ok(a, bt, c, sm, (0, 0, 0), 0)
+        assert txdot.aligned_rows(bt, col_ok=True) is bt
+        p = txdot.plan_for(a, bt, c, sm)
+        assert p.desc.flags & tx.FLAG_B_KMAJOR and p.desc.ldb == 304
+    assert not txdot._b_kmajor_ok(a, bt, tx.BF16, tx.SCALE_ROWCOL, (128, 128, 128), 0)
     b = txdot.aligned_rows(bt, col_ok=False)
     assert b.stride(1) == 1 and b.shape == (300, 64)
-    p = txdot.plan_for(a, b, tx.BF16, tx.SCALE_ROWCOL)
+    p = txdot.plan_for(a, b, tx.BF16, tx.SCALE_ROWCOL, block=(128, 128, 128))
     assert not p.desc.flags & tx.FLAG_B_KMAJOR
 
 

@@ -492,3 +492,63 @@ def test_8bit_kmajor_decode_accumulate(gpu, kind):
         check_close(outs[0], exact, atol=ATOL, rtol=RTOL, scale=s, what="fp8 K-major acc")
     for o in outs[1:]:
         assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+
+
+@pytest.mark.parametrize("M,N,K,block", [
+    (16, 8192, 8192, (0, 0, 0)), (1, 4096, 4096, (0, 0, 0)), (64, 1001, 999, (0, 0, 0)),
+    (5, 300, 200, (0, 0, 0)), (17, 1001, 999, (256, 256, 128)), (300, 263, 391, (0, 0, 0))])
+def test_w8a8_kmajor_b(gpu, M, N, K, block):
+    """W8A8 with the weight kept [N][K] (B a transposed view of junk-padded storage): the
+    8-bit decode kernel's int8 form at M <= 64, the 256x256x128 tile beyond or by name.
+    Bit-exact against the oracle (the same int32 sums and fp32 epilogue order)."""
+    import torch
+    say(f"tails W8A8 K-major B M={M} N={N} K={K} block={block}")
+    a, b = uniform_i8((M, K), 101), uniform_i8((K, N), 102)
+    sa_, sb_ = uniform_scales(M, 103), uniform_scales(N, 104)
+    junk = np.random.default_rng(105)
+    pa, _ = padded(a, 0)
+    pa[:, K:] = junk.integers(-128, 128, size=pa[:, K:].shape)
+    da = dev_view(pa, (M, K), gpu)
+    db = _kmajor_b(b, 0, gpu, junk=junk)
+    c = tx.dot(da, db, scale_a=to_device(sa_, gpu), scale_b=to_device(sb_, gpu),
+               out_dtype=torch.bfloat16, block=block)
+    torch.cuda.synchronize()
+    p = tx.plan_for(da, db, tx.BF16, tx.SCALE_ROWCOL, block, ldc=c.stride(0))
+    assert p.desc.flags & tx.FLAG_B_KMAJOR
+    assert p.kernel == (tx.KERNEL_DECODE_F8 if M <= 64 and block == (0, 0, 0)
+                        else tx.KERNEL_GEMM_I8)
+    ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 64, 64),
+                           scale_mode=oracle.SCALE_ROWCOL, sa=sa_, sb=sb_)
+    got = from_device(c)
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatches"
+
+
+@pytest.mark.parametrize("M,N,K,out,block", [
+    (16, 7168, 7168, "bf16", (0, 0, 0)), (1, 2048, 4096, "f32", (0, 0, 0)),
+    (40, 1000, 1100, "bf16", (0, 0, 0)), (40, 1000, 1100, "f32", (256, 256, 128)),
+    (300, 263, 391, "bf16", (0, 0, 0))])
+def test_fp8_block_scaled_kmajor_b(gpu, M, N, K, out, block):
+    """The block-scaled fp8 dot (config 4's form) with the weight kept [N][K], NaN codes in
+    both operands' padding: the decode kernel at M <= 64, the 256 tile beyond or by name;
+    against the oracle."""
+    import torch
+    say(f"tails fp8 block-scaled K-major B M={M} N={N} K={K} out={out} block={block}")
+    qa, qb, sa, sb = fp8_block_inputs(M, N, K, 107)
+    pa, _ = padded(qa, 0x7F)
+    da = dev_view(pa, (M, K), gpu, torch.float8_e4m3fn)
+    db = _kmajor_b(qb, 0x7F, gpu, torch.float8_e4m3fn)
+    odt = torch.bfloat16 if out == "bf16" else torch.float32
+    c = tx.dot(da, db, scale_a=to_device(sa, gpu), scale_b=to_device(sb, gpu), out_dtype=odt,
+               block=block)
+    torch.cuda.synchronize()
+    p = tx.plan_for(da, db, tx.tx_type(c), tx.SCALE_BLOCK128, block, ldc=c.stride(0))
+    assert p.desc.flags & tx.FLAG_B_KMAJOR
+    assert p.kernel == (tx.KERNEL_DECODE_F8 if M <= 64 and block == (0, 0, 0)
+                        else tx.KERNEL_GEMM_F8)
+    ct = oracle.BF16 if out == "bf16" else oracle.F32
+    ref = oracle.tiled_dot(qa, qb, a_type=oracle.F8E4M3, c_type=ct, block=(128, 128, 128),
+                           scale_mode=oracle.SCALE_BLOCK128, sa=sa, sb=sb)
+    got = from_device(c)
+    if out == "bf16":
+        got, ref = bits_to_f32(got, "bf16"), bits_to_f32(ref, "bf16")
+    check_close(got, ref, atol=ATOL, rtol=RTOL, scale=math.sqrt(K), what="fp8 block K-major")

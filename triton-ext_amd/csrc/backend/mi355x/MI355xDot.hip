@@ -113,7 +113,7 @@ struct GemmConfig {
     OP_F8, 256, 256, 128, 2, 4, EPI_F32, gemm8_w4_kernel<OP_F8, EPI_F32, FA, FB>, \
         0, 0, 5, (FA) | ((FB) << 4)                                            \
   }
-// The same with B K-major (TX_FLAG_B_KMAJOR): int8 -> int32 and unscaled fp8.
+// The same with B K-major (TX_FLAG_B_KMAJOR): every 8-bit epilogue but MX's.
 #define TX_GEMM_8T(OP, EPI)                                                    \
   GemmConfig { OP, 256, 256, 128, 2, 4, EPI, gemm8_w4_kernel<OP, EPI, 0, 0, true>, 1, 0, 5 }
 #define TX_GEMM_8FT(FA, FB)                                                    \
@@ -162,8 +162,11 @@ const GemmConfig kGemmConfigs[] = {
     TX_GEMM_8F(1, 1),
     TX_GEMM_8F(0, 1),
     TX_GEMM_8F(1, 0),
-    // the same with B K-major (q . k^T): int8 -> int32, fp8 -> fp32
+    // the same with B K-major (q . k^T, or weights kept [out][in])
     TX_GEMM_8T(OP_I8, EPI_I32),
+    TX_GEMM_8T(OP_I8, EPI_ROWCOL_BF16),
+    TX_GEMM_8T(OP_F8, EPI_BLOCK128_BF16),
+    TX_GEMM_8T(OP_F8, EPI_BLOCK128_F32),
     TX_GEMM_8T(OP_F8, EPI_F32),
     TX_GEMM_8FT(1, 1),
     TX_GEMM_8FT(0, 1),
@@ -206,7 +209,7 @@ const DecodeKernelFn kDecodeRowsKernels[3] = {decode_rows_i8_kernel<64, 6>,
                                               decode_rows_i8_kernel<256, 3>};
 // The 8-bit ring decode kernel: unscaled fp8 by [B K-major][A e4m3 / e5m2]
 // [B e4m3 / e5m2][slice of 16, 32, 48, 64 rows], block-scaled (e4m3) by
-// slice, int8 -> int32 with B K-major by slice.
+// [B K-major][slice], int8 with B K-major (int32 C or W8A8) by slice.
 typedef void (*DecodeF8KernelFn)(DecodeF8Args);
 #define TX_DF8_SLICES(SC, FA, FB, BT, I8)                                                  \
   {decode_f8_kernel<16, SC, FA, FB, BT, I8>, decode_f8_kernel<32, SC, FA, FB, BT, I8>,     \
@@ -216,7 +219,8 @@ const DecodeF8KernelFn kDecodeF8Kernels[2][2][2][4] = {
      {TX_DF8_SLICES(false, 1, 0, false, false), TX_DF8_SLICES(false, 1, 1, false, false)}},
     {{TX_DF8_SLICES(false, 0, 0, true, false), TX_DF8_SLICES(false, 0, 1, true, false)},
      {TX_DF8_SLICES(false, 1, 0, true, false), TX_DF8_SLICES(false, 1, 1, true, false)}}};
-const DecodeF8KernelFn kDecodeF8ScaledKernels[4] = TX_DF8_SLICES(true, 0, 0, false, false);
+const DecodeF8KernelFn kDecodeF8ScaledKernels[2][4] = {TX_DF8_SLICES(true, 0, 0, false, false),
+                                                       TX_DF8_SLICES(true, 0, 0, true, false)};
 const DecodeF8KernelFn kDecodeI8KmajorKernels[4] = TX_DF8_SLICES(false, 0, 0, true, true);
 #undef TX_DF8_SLICES
 // The 16-bit decode kernel by [fp16 / bf16][slice of 16, 32, 48, 64 rows].
@@ -467,10 +471,10 @@ int64_t decode16Workspace(const tx_dot_desc &d, int ksplit) {
          ksplit * decode16_split_bytes(cdiv(d.N, kDec16StripN), decode16Rows(d));
 }
 
-// The 8-bit ring decode kernel (decode_f8.h): fp8 x fp8 (e4m3 / e5m2 in any
-// mix) with fp32 C, B row-major or K-major; e4m3 x e4m3 with 128-block scales
-// and bf16 / fp32 C, B row-major; int8 -> int32 with B K-major (row-major int8
-// runs decode_i8.h); M <= 64, one arrival counter per 128-column strip.
+// The 8-bit ring decode kernel (decode_f8.h), B row-major or K-major: fp8 x
+// fp8 (e4m3 / e5m2 in any mix) with fp32 C; e4m3 x e4m3 with 128-block scales
+// and bf16 / fp32 C; with B K-major also int8 -> int32 and W8A8 (row-major
+// int8 runs decode_i8.h); M <= 64, one arrival counter per 128-column strip.
 bool useDecodeF8(const tx_dot_desc &d) {
   const bool fa = d.a_type == TX_F8E4M3 || d.a_type == TX_F8E5M2;
   const bool fb = d.b_type == TX_F8E4M3 || d.b_type == TX_F8E5M2;
@@ -478,12 +482,13 @@ bool useDecodeF8(const tx_dot_desc &d) {
   if (d.M > kDec8MaxM || cdiv(d.N, kDec8StripN) > kDec16MaxStrips)
     return false;
   if (d.a_type == TX_I8 && d.b_type == TX_I8)
-    return kmajor && d.scale_mode == TX_SCALE_NONE && d.c_type == TX_I32;
+    return kmajor && ((d.scale_mode == TX_SCALE_NONE && d.c_type == TX_I32) ||
+                      (d.scale_mode == TX_SCALE_ROWCOL && d.c_type == TX_BF16));
   if (!fa || !fb)
     return false;
   if (d.scale_mode == TX_SCALE_NONE)
     return d.c_type == TX_F32;
-  return !kmajor && d.scale_mode == TX_SCALE_BLOCK128 && d.a_type == TX_F8E4M3 &&
+  return d.scale_mode == TX_SCALE_BLOCK128 && d.a_type == TX_F8E4M3 &&
          d.b_type == TX_F8E4M3 && (d.c_type == TX_BF16 || d.c_type == TX_F32);
 }
 // Its tile: the slice (16 ceil(M / 16) rows) x a 128-column strip x 128-row
@@ -591,8 +596,8 @@ int txMi355xDotRun(tx_dot_plan *plan) {
                                 mxUpcastSide(d) ? 0 : fmtOf(d));
   if (ci < 0 && (d.flags & TX_FLAG_B_KMAJOR))
     return fail(TX_ERR_UNSUPPORTED,
-                "K-major B is implemented on the 256x256 tiles for bf16/fp16, int8 -> int32 "
-                "and unscaled fp8 only");
+                "K-major B is implemented on the 256x256 tiles and the decode kernels "
+                "(not for MX operands)");
   if (ci < 0)
     return fail(TX_ERR_UNSUPPORTED, "no instantiated tile %dx%dx%d for this dtype",
                 d.block_m, d.block_n, d.block_k);
@@ -995,10 +1000,11 @@ int launchDecodeF8(const tx_dot_plan &plan, const void *A, const void *B, void *
   a.A = static_cast<const uint8_t *>(A);
   a.B = static_cast<const uint8_t *>(B);
   a.C = C;
-  a.sa = static_cast<const float *>(sa);
-  a.sb = static_cast<const float *>(sb);
+  a.sa = d.scale_mode == TX_SCALE_NONE ? nullptr : static_cast<const float *>(sa);
+  a.sb = d.scale_mode == TX_SCALE_NONE ? nullptr : static_cast<const float *>(sb);
   a.c_f32 = d.c_type == TX_F32;
   a.acc_c = (d.flags & TX_FLAG_ACCUMULATE) != 0;
+  a.rowcol = d.scale_mode == TX_SCALE_ROWCOL;
   a.M = (int32_t)d.M;
   a.N = (int32_t)d.N;
   a.K = (int32_t)d.K;
@@ -1018,7 +1024,7 @@ int launchDecodeF8(const tx_dot_plan &plan, const void *A, const void *B, void *
   const bool kmajor = (d.flags & TX_FLAG_B_KMAJOR) != 0;
   const DecodeF8KernelFn fn =
       d.a_type == TX_I8 ? kDecodeI8KmajorKernels[si]
-      : scaled          ? kDecodeF8ScaledKernels[si]
+      : scaled          ? kDecodeF8ScaledKernels[kmajor][si]
                         : kDecodeF8Kernels[kmajor][d.a_type == TX_F8E5M2][d.b_type == TX_F8E5M2][si];
   hipLaunchKernelGGL(fn, dim3(plan.grid_x), dim3(plan.block_threads), 0, stream, a);
   TX_HIP_CHECK(hipGetLastError());

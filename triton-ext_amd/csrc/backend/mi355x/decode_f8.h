@@ -57,8 +57,9 @@
 // of B as of A.  B's chunk that crosses K is loaded whole and zeroed in
 // registers like A's.  Each strip starts its split's batches at its own batch
 // (strip mod the split's batch count), so the workgroups running at once read
-// B's rows at different K offsets.  I8 (with BT only): int8 x int8 -> int32,
-// C = sum or C += sum; per 16 x 16 block and batch two
+// B's rows at different K offsets.  I8 (with BT only): int8 x int8, int32
+// sums, C = sum or C += sum, or the W8A8 epilogue (rowcol: row x column
+// scales, bf16 C, as decode_i8.h rounds it); per 16 x 16 block and batch two
 // v_mfma_i32_16x16x64_i8 on the same fragments (K bytes 32 G .. +15, then
 // +16 .. +31 of each lane), int32 partials, exact in any order.
 #pragma once
@@ -80,7 +81,8 @@ struct DecodeF8Args {
   const float *sa;   // SCALED: [M][sa_ld]
   const float *sb;   // SCALED: [ceil(K / 128)][sb_ld]
   int32_t c_f32;     // fp32 C (else bf16)
-  int32_t acc_c;     // fp32 C: add the sums to C's contents (tl.dot's acc)
+  int32_t acc_c;     // fp32 / int32 C: add the sums to C's contents (tl.dot's acc)
+  int32_t rowcol;    // I8: W8A8, C = bf16((float(sum) * sa[m]) * sb[n]) (else int32 C)
   int32_t M, N, K;
   int64_t lda, ldb, ldc;
   int32_t sa_ld, sb_ld;
@@ -228,7 +230,6 @@ __device__ __forceinline__ i32x4_t dec8_mask_k(const i32x4_t &v, int64_t k, int6
 template <int SR, bool SCALED, int FA = 0, int FB = 0, bool BT = false, bool I8 = false>
 __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_f8_kernel(DecodeF8Args p) {
   static_assert(!SCALED || (FA == 0 && FB == 0), "block scales take e4m3 operands");
-  static_assert(!BT || !SCALED, "K-major B: unscaled dots");
   static_assert(!I8 || (BT && FA == 0 && FB == 0), "int8: the K-major form");
   typedef DecodeF8Cfg<SR, SCALED> Cfg;
   constexpr int S = Cfg::S, SLOT = Cfg::SLOT, T = Cfg::T;
@@ -442,18 +443,40 @@ k_loop_done:
         const int m = 16 * t + L;
         if (m >= p.M)
           continue;
-        if constexpr (I8) { // int32 C
-          int32_t *c = static_cast<int32_t *>(p.C) + (int64_t)m * p.ldc + col;
-          if (whole) {
-            i32x4_t v = sum[t][jj];
-            if (p.acc_c)
-              v += *reinterpret_cast<const i32x4_t *>(c);
-            *reinterpret_cast<i32x4_t *>(c) = v;
-          } else {
+        if constexpr (I8) {
+          if (p.rowcol) { // W8A8: bf16((float(sum) * sa[m]) * sb[n]), nearest even
+            const float sam = p.sa[m];
+            float f[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              if (col + r < p.N)
-                c[r] = p.acc_c ? c[r] + sum[t][jj][r] : sum[t][jj][r];
+            for (int r = 0; r < 4; ++r) {
+#pragma clang fp contract(off)
+              f[r] = ((float)sum[t][jj][r] * sam) * p.sb[col + r < p.N ? col + r : 0];
+            }
+            uint16_t *c = static_cast<uint16_t *>(p.C) + (int64_t)m * p.ldc + col;
+            if (whole) {
+              uint2 w;
+              w.x = pk_bf16_rne(f[0], f[1]);
+              w.y = pk_bf16_rne(f[2], f[3]);
+              *reinterpret_cast<uint2 *>(c) = w;
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (col + r < p.N)
+                  c[r] = f32_to_bf16_rne(f[r]);
+            }
+          } else { // int32 C
+            int32_t *c = static_cast<int32_t *>(p.C) + (int64_t)m * p.ldc + col;
+            if (whole) {
+              i32x4_t v = sum[t][jj];
+              if (p.acc_c)
+                v += *reinterpret_cast<const i32x4_t *>(c);
+              *reinterpret_cast<i32x4_t *>(c) = v;
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (col + r < p.N)
+                  c[r] = p.acc_c ? c[r] + sum[t][jj][r] : sum[t][jj][r];
+            }
           }
         } else if (p.c_f32) { // fp32 C
           float *c = static_cast<float *>(p.C) + (int64_t)m * p.ldc + col;

@@ -85,7 +85,8 @@ extern "C" __device__ f32x4_t txk_mfma_scale_16x16x128_f4(i32x4_t, i32x4_t, f32x
 // FA, FB: MFMA format codes of A and B (0 e4m3, 1 e5m2; 4 e2m1 with the MX
 // epilogues only); the unscaled fp8 dot takes e4m3 / e5m2 in any mix.
 // BT: B is stored K-major ([N][K] row-major, row stride ldb), the layout of
-// q . k^T with k row-major (int8 -> int32 and unscaled fp8 only).  Its tile is
+// q . k^T with k row-major or of a weight kept [out][in] (every epilogue but
+// MX's; the scales do not depend on B's layout).  Its tile is
 // staged exactly like A's ([256 columns][128 K bytes], the same swizzle) and
 // read with ds_read_b128: lane l gets column l%16's K bytes 32 (l/16) .. +31,
 // the same permutation of K as A's fragment.
@@ -110,7 +111,7 @@ template <int OP, int EPI, int FA = 0, int FB = 0, bool BT = false> struct Gemm8
   static_assert(!MX || (OP == OP_F8 && ((FA == 4) == (FB == 4)) && FA >= 0 && FA <= 4 &&
                         FB >= 0 && FB <= 4 && FA != 2 && FA != 3 && FB != 2 && FB != 3),
                 "MX operands: e4m3 / e5m2 in any mix, or e2m1 on both sides");
-  static_assert(!BT || EPI == EPI_I32 || EPI == EPI_F32, "K-major B: int32 / fp32 C, no scales");
+  static_assert(!BT || !MX, "K-major B: not the MX forms");
   static_assert(STAGE % 128 == 0, "stage offsets keep address bits 0-6");
   static_assert(2 * STAGE <= 160 * 1024, "two stages in LDS");
 

@@ -204,21 +204,21 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
         (d->a_type == TX_BF16 || d->a_type == TX_F16) && d->b_type == d->a_type &&
         d->scale_mode == TX_SCALE_NONE && (d->c_type == d->a_type || d->c_type == TX_F32) &&
         d->M <= 64 && d->N <= (int64_t)16384 * 64;
-    // The 8-bit ring decode kernel: fp8 x fp8 with fp32 C (B row-major or
-    // K-major), e4m3 x e4m3 with 128-block scales and bf16 / fp32 C (B
-    // row-major), int8 -> int32 with B K-major; M <= 64, N up to its 16384
-    // strips of 128 columns.
+    // The 8-bit ring decode kernel, B row-major or K-major: fp8 x fp8 with
+    // fp32 C, e4m3 x e4m3 with 128-block scales and bf16 / fp32 C; with B
+    // K-major also int8 -> int32 and W8A8; M <= 64, N up to its 16384 strips
+    // of 128 columns.
     const bool fp8a = d->a_type == TX_F8E4M3 || d->a_type == TX_F8E5M2;
     const bool fp8b = d->b_type == TX_F8E4M3 || d->b_type == TX_F8E5M2;
     const bool kmajor = (d->flags & TX_FLAG_B_KMAJOR) != 0;
     const bool decode_f8 =
         d->M <= 64 && d->N <= (int64_t)16384 * 128 &&
         ((fp8a && fp8b && d->scale_mode == TX_SCALE_NONE && d->c_type == TX_F32) ||
-         (fp8a && fp8b && !kmajor && d->scale_mode == TX_SCALE_BLOCK128 &&
-          d->a_type == TX_F8E4M3 && d->b_type == TX_F8E4M3 &&
-          (d->c_type == TX_BF16 || d->c_type == TX_F32)) ||
+         (d->scale_mode == TX_SCALE_BLOCK128 && d->a_type == TX_F8E4M3 &&
+          d->b_type == TX_F8E4M3 && (d->c_type == TX_BF16 || d->c_type == TX_F32)) ||
          (kmajor && d->a_type == TX_I8 && d->b_type == TX_I8 &&
-          d->scale_mode == TX_SCALE_NONE && d->c_type == TX_I32));
+          ((d->scale_mode == TX_SCALE_NONE && d->c_type == TX_I32) ||
+           (d->scale_mode == TX_SCALE_ROWCOL && d->c_type == TX_BF16))));
     const size_t first = spanA < TX_SPAN32_LIMIT && spanB < TX_SPAN32_LIMIT ? 0 : 1;
     if (upcast)
       t = chooseTile(kTiles16, d->M, d->N, d->K, first); // MX x bf16 runs on the bf16 tile

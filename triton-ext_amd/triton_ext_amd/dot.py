@@ -77,10 +77,10 @@ def _layout(t, col_ok=True):
     return None, 0
 
 
-def _b_col_ok(b, unscaled=True):
-    """B may be K-major (a transposed view): 16-bit operands, and 8-bit ones in an
-    unscaled dot (int8 -> int32, fp8 -> fp32)."""
-    return b.element_size() == 2 or (b.element_size() == 1 and unscaled)
+def _b_col_ok(b):
+    """B may be K-major (a transposed view): 16-bit and 8-bit operands (every
+    epilogue of dot(); tl.dot_scaled's MX operands take B as [K][N])."""
+    return b.element_size() in (1, 2)
 
 
 def _kmajor_plans(a, b, c_tx, scale_mode, block, flags):
@@ -99,7 +99,7 @@ def _kmajor_plans(a, b, c_tx, scale_mode, block, flags):
 
 
 def _b_kmajor_ok(a, b, c_tx, scale_mode, block, flags):
-    return (a.dim() == 2 and b.dim() == 2 and _b_col_ok(b, scale_mode == capi.SCALE_NONE)
+    return (a.dim() == 2 and b.dim() == 2 and _b_col_ok(b)
             and _kmajor_plans(a, b, c_tx, scale_mode, block, flags))
 
 
@@ -135,8 +135,8 @@ def plan_for(a, b, out_dtype_tx, scale_mode=capi.SCALE_NONE, block=(0, 0, 0), fl
     a_kind, a_ld = _layout(a, col_ok=False)
     b_kind, b_ld = _layout(b, col_ok=_b_kmajor_ok(a, b, out_dtype_tx, scale_mode, block, flags))
     if a_kind == "row" and b_kind is None and _layout(b)[0] == "col":
-        raise ValueError("B is a transposed view, and this dot has no K-major form (16-bit, "
-                         "or unscaled 8-bit, on a tile with that form); copy it row-major")
+        raise ValueError("B is a transposed view, and the tile asked for has no K-major "
+                         "form; copy it row-major")
     if a_kind != "row" or b_kind is None:
         raise ValueError("A rows must be contiguous, and B rows (or B's columns) too")
     b_kmajor = b_kind == "col"
@@ -189,8 +189,7 @@ def dot(a, b, out=None, out_dtype=None, scale_a=None, scale_b=None, scale_mode=N
 
     K and N may be any size.  Operands whose rows do not start 16 bytes
     apart are copied to padded storage first (one extra pass), as is a
-    transposed view of A, or of an 8-bit B in a scaled dot, in row-major form
-    (a 16-bit B, and an 8-bit B of an unscaled int8 or fp8 dot, run K-major,
+    transposed view of A in row-major form (a transposed B runs K-major,
     unless `block` names a tile without that form: then B is copied too); a
     new output is a view of padded storage; a given `out` must already have
     16-byte row strides.
