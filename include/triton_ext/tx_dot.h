@@ -120,17 +120,18 @@ typedef enum tx_kernel {
   TX_KERNEL_DECODE_16BIT = 7, /* bf16/fp16 decode shapes (M <= 64, no scales):
                                * B streamed once, MFMA 16x16x32              */
   TX_KERNEL_DECODE_F8 = 8,    /* 8-bit decode shapes (M <= 64): fp8 unscaled or
-                               * with 128-block scales, and int8 -> int32 with
-                               * B K-major; B streamed once, MFMA 16x16x128
-                               * (int8: 16x16x64)                            */
+                               * with 128-block scales, and int8 (int32 C or
+                               * W8A8) with B K-major; B streamed once, MFMA
+                               * 16x16x128 (int8: 16x16x64)                  */
 } tx_kernel;
 
 /* Bit flags for tx_dot_desc.flags */
 #define TX_FLAG_NO_LOOP_SPLIT 0x1 /* run every K step masked (no peeling) */
 /* B is stored K-major: [N][K] row-major with row stride ldb (0 = K), the
- * layout of tl.dot(q, tl.trans(k)) / q @ k.T with k row-major.  Supported for
- * bf16/fp16 operands on the 256x256x64 tile and the 16-bit decode kernel, and
- * for int8 -> int32 and unscaled fp8 -> fp32 on the 256x256x128 tile and the
+ * layout of tl.dot(q, tl.trans(k)) / q @ k.T with k row-major, and of a
+ * weight kept [out][in].  Supported for bf16/fp16 operands on the 256x256x64
+ * tile and the 16-bit decode kernel, and for every 8-bit dot but MX (int8 ->
+ * int32, W8A8, unscaled and block-scaled fp8) on the 256x256x128 tile and the
  * 8-bit decode kernel (M <= 64). */
 #define TX_FLAG_B_KMAJOR 0x2
 /* C = C + A . B: the accumulator operand of tl.dot(a, b, acc) and
