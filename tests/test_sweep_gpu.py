@@ -145,6 +145,16 @@ def _cases():
         out.append(("fp8", 200 + i, dict(M=_dim(rng, 600), N=_dim(rng, 600), K=_dim(rng, 900),
                                          fa=fa, fb=fb, block=[(0, 0, 0), (256, 256, 128)][i // 8],
                                          kmajor=True)))
+    # K-major B in the scaled 8-bit dots (weights kept [N][K])
+    for i in range(12):
+        M = int(rng.integers(1, 65)) if i % 2 == 0 else int(rng.integers(65, 600))
+        out.append(("w8a8", 200 + i, dict(M=M, N=_dim(rng, 3000), K=_dim(rng, 3000),
+                                          block=(0, 0, 0), kmajor=True)))
+    for i in range(12):
+        M = int(rng.integers(1, 65)) if i % 2 == 0 else int(rng.integers(65, 600))
+        out.append(("fp8_block", 200 + i, dict(M=M, N=_dim(rng, 600), K=_dim(rng, 900),
+                                               out=str(rng.choice(["bf16", "f32"])),
+                                               block=(0, 0, 0), kmajor=True)))
     return out
 
 
@@ -184,12 +194,15 @@ def _run_i8_i32(gpu, seed, M, N, K, block, kmajor=False):
     assert np.array_equal(got, exact), f"{np.count_nonzero(got != exact)} mismatches"
 
 
-def _run_w8a8(gpu, seed, M, N, K, block):
+def _run_w8a8(gpu, seed, M, N, K, block, kmajor=False):
     import torch
     a, b = uniform_i8((M, K), seed), uniform_i8((K, N), seed + 1)
     sa, sb = uniform_scales(M, seed + 2), uniform_scales(N, seed + 3)
-    c = tx.dot(dev_view(_junk_padded(a, seed + 4), (M, K), gpu),
-               dev_view(_junk_padded(b, seed + 5), (K, N), gpu), scale_a=to_device(sa, gpu),
+    if kmajor:  # the weight kept [N][K]: B a transposed view of junk-padded storage
+        db = dev_view(_junk_padded(np.ascontiguousarray(b.T), seed + 5), (N, K), gpu).t()
+    else:
+        db = dev_view(_junk_padded(b, seed + 5), (K, N), gpu)
+    c = tx.dot(dev_view(_junk_padded(a, seed + 4), (M, K), gpu), db, scale_a=to_device(sa, gpu),
                scale_b=to_device(sb, gpu), out_dtype=torch.bfloat16, block=block)
     torch.cuda.synchronize()
     ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 64, 64),
@@ -223,14 +236,18 @@ def _run_fp8(gpu, seed, M, N, K, fa, fb, block, kmajor=False):
     check_close(from_device(c), ref, atol=ATOL, rtol=RTOL, scale=s, what="fp8 sweep")
 
 
-def _run_fp8_block(gpu, seed, M, N, K, out, block):
+def _run_fp8_block(gpu, seed, M, N, K, out, block, kmajor=False):
     import torch
     qa, qb, sa, sb = fp8_block_inputs(M, N, K, seed)
     pa, _ = padded(qa, 0x7F)
-    pb, _ = padded(qb, 0x7F)
+    if kmajor:  # the weight kept [N][K]
+        pb, _ = padded(np.ascontiguousarray(qb.T), 0x7F)
+        db = dev_view(pb, (N, K), gpu, torch.float8_e4m3fn).t()
+    else:
+        pb, _ = padded(qb, 0x7F)
+        db = dev_view(pb, (K, N), gpu, torch.float8_e4m3fn)
     odt = torch.bfloat16 if out == "bf16" else torch.float32
-    c = tx.dot(dev_view(pa, (M, K), gpu, torch.float8_e4m3fn),
-               dev_view(pb, (K, N), gpu, torch.float8_e4m3fn), scale_a=to_device(sa, gpu),
+    c = tx.dot(dev_view(pa, (M, K), gpu, torch.float8_e4m3fn), db, scale_a=to_device(sa, gpu),
                scale_b=to_device(sb, gpu), out_dtype=odt, block=block)
     torch.cuda.synchronize()
     ct = oracle.BF16 if out == "bf16" else oracle.F32
@@ -298,12 +315,13 @@ def test_sweep(gpu, family, i, case):
     elif family == "i8_i32":
         _run_i8_i32(gpu, seed, c["M"], c["N"], c["K"], c["block"], c.get("kmajor", False))
     elif family == "w8a8":
-        _run_w8a8(gpu, seed, c["M"], c["N"], c["K"], c["block"])
+        _run_w8a8(gpu, seed, c["M"], c["N"], c["K"], c["block"], c.get("kmajor", False))
     elif family == "fp8":
         _run_fp8(gpu, seed, c["M"], c["N"], c["K"], c["fa"], c["fb"], c["block"],
                  c.get("kmajor", False))
     elif family == "fp8_block":
-        _run_fp8_block(gpu, seed, c["M"], c["N"], c["K"], c["out"], c["block"])
+        _run_fp8_block(gpu, seed, c["M"], c["N"], c["K"], c["out"], c["block"],
+                       c.get("kmajor", False))
     elif family == "mx":
         _run_mx(gpu, seed, c["M"], c["N"], c["K"], c["fa"], c["fb"], c["out"])
     elif family == "mx_bf16":  # the upcast path, bit for bit against the host upcast
