@@ -378,15 +378,18 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_f8_kernel(DecodeF
         s_row[t] = v * s_col;
       }
     }
+    if constexpr (I8) { // two K steps of 64: bytes 32 G .. +15, then +16 .. +31; a step's
+                        // 2 T products are independent of each other
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      if constexpr (I8) { // two K steps of 64: bytes 32 G .. +15, then +16 .. +31
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-          acc[t][jj] = mfma_i8_16(bk[jj][0], a[t][0], acc[t][jj]);
-          acc[t][jj] = mfma_i8_16(bk[jj][1], a[t][1], acc[t][jj]);
-        }
-      } else {
+        for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+          for (int t = 0; t < T; ++t)
+            acc[t][jj] = mfma_i8_16(bk[jj][h], a[t][h], acc[t][jj]);
+    } else {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
         const i32x8_t bcol =
             BT ? i32x8_t{bk[jj][0][0], bk[jj][0][1], bk[jj][0][2], bk[jj][0][3], bk[jj][1][0],
                          bk[jj][1][1], bk[jj][1][2], bk[jj][1][3]}
