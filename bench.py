@@ -58,7 +58,7 @@ def parse():
                          "w8a8 (or "
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256; w8a8 also runs i32_16, the unscaled "
                          "int8 -> int32 decode at M=16, and i32_16_kmajor, the same with B "
-                         "K-major), w8a8_kmajor (or w8a8_kmajor_1, _16, _64: W8A8 with the "
+                         "K-major), w8a8_kmajor (or w8a8_kmajor_1, _16, _64, _256: W8A8 with the "
                          "weight kept [N][K]), bf16_decode (or bf16_decode_1, _16, _64: "
                          "bf16 at N = K = 8192 on the 16-bit decode kernel; bf16_decode_kmajor, "
                          "or _1, _16, _64: the same with B K-major), fp8_decode (or "
@@ -1146,7 +1146,7 @@ def main():
             print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
                   f"({100 * r['frac_hbm']:.1f}% HBM); isolated launch "
                   f"{r['ms_isolated'] * 1e3:.2f} us", file=sys.stderr, flush=True)
-    for m in (1, 16, 64):
+    for m in (1, 16, 64, 256):
         if want("w8a8_kmajor") or want(f"w8a8_kmajor_{m}"):
             r = bench_w8a8(tx, dev, m, 8192, 8192, max(args.steps, 20), 3, flush, kmajor=True)
             secondary.append(r)

@@ -309,7 +309,8 @@ def test_decode16_plans():
 
 def test_b_kmajor_plans():
     """K-major B (q @ k.T): bf16/fp16 on the 256x256x64 tile, int8 -> int32 and unscaled
-    fp8 on the 256x256x128 tile, and at M <= 64 on the decode kernels; ldb defaulting to K."""
+    fp8 on the 256x256x128 tile, and at decode shapes on the decode kernels; ldb defaulting
+    to K."""
     p = tx.plan(tx.make_desc(512, 384, 192, tx.BF16, tx.F32, flags=tx.FLAG_B_KMAJOR))
     assert p.kernel == tx.KERNEL_GEMM_16BIT
     assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (256, 256, 64)
@@ -323,7 +324,7 @@ def test_b_kmajor_plans():
                           (tx.F8E5M2, tx.F8E4M3, tx.F32, tx.KERNEL_GEMM_F8),
                           (tx.F8E4M3, tx.F8E5M2, tx.F32, tx.KERNEL_GEMM_F8),
                           (tx.F8E5M2, tx.F8E5M2, tx.F32, tx.KERNEL_GEMM_F8)):
-        p = tx.plan(tx.make_desc(100, 300, 200, a, c, b_type=b, lda=208, ldb=208,
+        p = tx.plan(tx.make_desc(600, 300, 200, a, c, b_type=b, lda=208, ldb=208,
                                  flags=tx.FLAG_B_KMAJOR))
         assert p.kernel == kern and p.desc.ldb == 208
         assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (256, 256, 128)
@@ -334,21 +335,31 @@ def test_b_kmajor_plans():
         assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (16, 128, 128)
         assert tx.plan(tx.make_desc(16, 300, 200, a, c, b_type=b, lda=208, ldb=208,
                                     block=(256, 256, 128), flags=tx.FLAG_B_KMAJOR)).kernel == kern
-    # W8A8 and block-scaled fp8 (weights kept [N][K]): the decode kernel at M <= 64, the
-    # 256 tile beyond
+    # W8A8 and block-scaled fp8 (weights kept [N][K]): the 8-bit decode kernel at M <= 64;
+    # int8 (W8A8, int32) on the row kernel to M = 512; the 256 tile beyond
     for a, c, sm, kern in ((tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_GEMM_I8),
+                           (tx.I8, tx.I32, 0, tx.KERNEL_GEMM_I8),
                            (tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, tx.KERNEL_GEMM_F8),
                            (tx.F8E4M3, tx.F32, tx.SCALE_BLOCK128, tx.KERNEL_GEMM_F8)):
+        i8 = a == tx.I8
         for M, want, blk in ((16, tx.KERNEL_DECODE_F8, (16, 128, 128)),
-                             (300, kern, (256, 256, 128))):
+                             (100, tx.KERNEL_DECODE_I8 if i8 else kern,
+                              (64, 128, 128) if i8 else (256, 256, 128)),
+                             (300, tx.KERNEL_DECODE_I8 if i8 else kern,
+                              (256, 128, 128) if i8 else (256, 256, 128)),
+                             (600, kern, (256, 256, 128))):
             p = tx.plan(tx.make_desc(M, 512, 512, a, c, scale_mode=sm, flags=tx.FLAG_B_KMAJOR))
             assert p.kernel == want and (p.desc.block_m, p.desc.block_n, p.desc.block_k) == blk
-    # the other 8-bit tiles have no K-major form
-    for a, c, sm, blk in ((tx.I8, tx.BF16, tx.SCALE_ROWCOL, (128, 128, 128)),
-                          (tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, (256, 224, 128)),
-                          (tx.I8, tx.I32, 0, (128, 128, 128)),
-                          (tx.I8, tx.I32, 0, (256, 224, 128))):
-        assert _err(tx.make_desc(16, 256, 256, a, c, scale_mode=sm, block=blk,
+    # the K-interleaved int8 decode kernel (decode_i8.h) has no K-major form
+    assert _err(tx.make_desc(100, 512, 512, tx.I8, tx.BF16, scale_mode=tx.SCALE_ROWCOL,
+                             block=(64, 128, 64), flags=tx.FLAG_B_KMAJOR)) == tx.ERR_UNSUPPORTED
+    # the other 8-bit tiles (256 x 224; register-staged 128 x 128, which 128 x 128 x 128
+    # names past M = 256) have no K-major form
+    for M, a, c, sm, blk in ((300, tx.I8, tx.BF16, tx.SCALE_ROWCOL, (128, 128, 128)),
+                             (16, tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, (256, 224, 128)),
+                             (300, tx.I8, tx.I32, 0, (128, 128, 128)),
+                             (16, tx.I8, tx.I32, 0, (256, 224, 128))):
+        assert _err(tx.make_desc(M, 256, 256, a, c, scale_mode=sm, block=blk,
                                  flags=tx.FLAG_B_KMAJOR)) == tx.ERR_UNSUPPORTED
     assert _err(tx.make_desc(64, 64, 64, tx.BF16, tx.BF16, flags=0x10)) == tx.ERR_INVALID
 

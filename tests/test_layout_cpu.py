@@ -60,16 +60,16 @@ def test_plan_8bit_transposed_b():
         assert txdot.aligned_rows(bt, col_ok=True) is bt
         p = txdot.plan_for(a, bt, c, sm)
         assert p.desc.flags & tx.FLAG_B_KMAJOR and p.desc.ldb == 304
-    assert not txdot._b_kmajor_ok(a, bt, tx.BF16, tx.SCALE_ROWCOL, (128, 128, 128), 0)
+    assert not txdot._b_kmajor_ok(a, bt, tx.BF16, tx.SCALE_ROWCOL, (256, 224, 128), 0)
     b = txdot.aligned_rows(bt, col_ok=False)
     assert b.stride(1) == 1 and b.shape == (300, 64)
-    p = txdot.plan_for(a, b, tx.BF16, tx.SCALE_ROWCOL, block=(128, 128, 128))
+    p = txdot.plan_for(a, b, tx.BF16, tx.SCALE_ROWCOL, block=(256, 224, 128))
     assert not p.desc.flags & tx.FLAG_B_KMAJOR
 
 
 @pytest.mark.parametrize("dtype_name,txt,M,tile,other", [
-    ("int8", tx.I32, 16, (16, 128, 128), (128, 128, 128)),
-    ("int8", tx.I32, 100, (256, 256, 128), (128, 128, 128)),
+    ("int8", tx.I32, 16, (16, 128, 128), (256, 224, 128)),
+    ("int8", tx.I32, 600, (256, 256, 128), (256, 224, 128)),
     ("bfloat16", tx.F32, 16, (16, 64, 128), (128, 128, 64)),
     ("bfloat16", tx.F32, 100, (256, 256, 64), (64, 64, 32))])
 def test_transposed_b_with_an_explicit_block(dtype_name, txt, M, tile, other):

@@ -351,15 +351,25 @@ def _kmajor_b(b, fill, gpu, tdtype=None, junk=None):
     return dev_view(st, (N, K), gpu, tdtype).t()
 
 
-def _assert_kmajor_plan(da, db, c, kernel, block=(0, 0, 0)):
-    """The plan is K-major on the 256x256x128 tile (`kernel`), or at M <= 64 with the
-    planner's choice on the 8-bit decode kernel; returns it."""
-    p = tx.plan_for(da, db, tx.tx_type(c), block=block, ldc=c.stride(0))
+def _kmajor_kernel(M, kernel, block, i8):
+    """The kernel a K-major 8-bit plan takes: with the planner's choice the 8-bit decode
+    kernel at M <= 64 (int8: M <= 48) and for int8 the row decode kernel beyond, to
+    M = 512; else the 256x256x128 tile (`kernel`)."""
+    if block != (0, 0, 0):
+        return kernel
+    if M <= (48 if i8 else 64):
+        return tx.KERNEL_DECODE_F8
+    return tx.KERNEL_DECODE_I8 if i8 and M <= 512 else kernel
+
+
+def _assert_kmajor_plan(da, db, c, kernel, block=(0, 0, 0), scale_mode=0):
+    """The plan is K-major, on the kernel _kmajor_kernel names; returns it."""
+    p = tx.plan_for(da, db, tx.tx_type(c), scale_mode, block=block, ldc=c.stride(0))
     assert p.desc.flags & tx.FLAG_B_KMAJOR
-    if da.shape[0] <= 64 and block == (0, 0, 0):
-        assert p.kernel == tx.KERNEL_DECODE_F8 and (p.desc.block_n, p.desc.block_k) == (128, 128)
-    else:
-        assert p.kernel == kernel
+    want = _kmajor_kernel(da.shape[0], kernel, block, da.element_size() == 1 and
+                          kernel == tx.KERNEL_GEMM_I8)
+    assert p.kernel == want
+    if want == kernel:
         assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (256, 256, 128)
     return p
 
@@ -369,12 +379,14 @@ def _assert_kmajor_plan(da, db, c, kernel, block=(0, 0, 0)):
     (40, 50, 200, (0, 0, 0)), (17, 1001, 999, (0, 0, 0)), (5, 220, 1, (0, 0, 0)),
     (64, 3, 129, (0, 0, 0)), (16, 4096, 4096, (0, 0, 0)), (33, 300, 4001, (0, 0, 0)),
     (40, 50, 200, (256, 256, 128)), (17, 1001, 999, (256, 256, 128)),
-    (5, 220, 1, (256, 256, 128)), (64, 3, 129, (256, 256, 128))])
+    (5, 220, 1, (256, 256, 128)), (64, 3, 129, (256, 256, 128)),
+    (300, 263, 391, (256, 256, 128)), (129, 8192, 4096, (0, 0, 0))])
 def test_int8_ragged_kmajor_b(gpu, M, N, K, block):
     """int8 -> int32 with B a transposed view (q @ k.T): B's padding columns past K and rows
     past N hold random bytes, as do A's.  The chunk that crosses K is loaded whole on both
     sides, so both are zeroed past K (junk times junk is not zero).  Bit-exact, on the
-    256x256x128 tile and (M <= 64) the 8-bit decode kernel."""
+    256x256x128 tile and, with the planner's choice, the 8-bit decode kernel (M <= 48) and
+    the row decode kernel (48 < M <= 512)."""
     import torch
     say(f"tails int8 K-major B M={M} N={N} K={K} block={block}")
     a, b = uniform_i8((M, K), 81), uniform_i8((K, N), 82)
@@ -454,13 +466,14 @@ def test_8bit_kmajor_b_full_size(gpu, kind):
     assert torch.equal(c.view(torch.int32), c_row.view(torch.int32))
 
 
-@pytest.mark.parametrize("kind", ["i8", "e4m3"])
-def test_8bit_kmajor_decode_accumulate(gpu, kind):
-    """tl.dot(a, k.T, acc) at decode shape on the 8-bit decode kernel, split-K: C = acc +
-    A @ B (int32 exactly; fp32 within summation error), the same bits on every launch."""
+@pytest.mark.parametrize("kind,M", [("i8", 16), ("e4m3", 16), ("i8", 100)])
+def test_8bit_kmajor_decode_accumulate(gpu, kind, M):
+    """tl.dot(a, k.T, acc) at decode shape on the 8-bit decode kernel (M = 16) and the row
+    decode kernel (int8, M = 100), split-K: C = acc + A @ B (int32 exactly; fp32 within
+    summation error), the same bits on every launch."""
     import torch
-    M, N, K = 16, 1024, 8192
-    say(f"tails 8-bit K-major decode acc {kind}")
+    N, K = 1024, 8192
+    say(f"tails 8-bit K-major decode acc {kind} M={M}")
     rng = np.random.default_rng(97)
     if kind == "i8":
         a, b = uniform_i8((M, K), 95), uniform_i8((K, N), 96)
@@ -484,7 +497,8 @@ def test_8bit_kmajor_decode_accumulate(gpu, kind):
         torch.cuda.synchronize()
         outs.append(from_device(c))
     p = tx.plan_for(da, db, tx.tx_type(c), flags=tx.FLAG_ACCUMULATE)
-    assert p.kernel == tx.KERNEL_DECODE_F8 and p.split_k > 1 and p.desc.flags & tx.FLAG_B_KMAJOR
+    assert p.kernel == (tx.KERNEL_DECODE_F8 if M <= 64 else tx.KERNEL_DECODE_I8)
+    assert p.split_k > 1 and p.desc.flags & tx.FLAG_B_KMAJOR
     if kind == "i8":
         assert np.array_equal(outs[0].astype(np.int64), exact)
     else:
@@ -496,11 +510,14 @@ def test_8bit_kmajor_decode_accumulate(gpu, kind):
 
 @pytest.mark.parametrize("M,N,K,block", [
     (16, 8192, 8192, (0, 0, 0)), (1, 4096, 4096, (0, 0, 0)), (64, 1001, 999, (0, 0, 0)),
-    (5, 300, 200, (0, 0, 0)), (17, 1001, 999, (256, 256, 128)), (300, 263, 391, (0, 0, 0))])
+    (5, 300, 200, (0, 0, 0)), (17, 1001, 999, (256, 256, 128)), (300, 263, 391, (0, 0, 0)),
+    (256, 8192, 8192, (0, 0, 0)), (100, 4100, 2049, (0, 0, 0)), (200, 1001, 999, (0, 0, 0)),
+    (65, 130, 129, (0, 0, 0)), (700, 300, 200, (0, 0, 0)), (100, 300, 200, (256, 256, 128))])
 def test_w8a8_kmajor_b(gpu, M, N, K, block):
     """W8A8 with the weight kept [N][K] (B a transposed view of junk-padded storage): the
-    8-bit decode kernel's int8 form at M <= 64, the 256x256x128 tile beyond or by name.
-    Bit-exact against the oracle (the same int32 sums and fp32 epilogue order)."""
+    8-bit decode kernel's int8 form at M <= 48, the row decode kernel to M = 512 (slices of
+    64, 128, 256 rows), the 256x256x128 tile beyond or by name.  Bit-exact against the
+    oracle (the same int32 sums and fp32 epilogue order)."""
     import torch
     say(f"tails W8A8 K-major B M={M} N={N} K={K} block={block}")
     a, b = uniform_i8((M, K), 101), uniform_i8((K, N), 102)
@@ -513,10 +530,7 @@ def test_w8a8_kmajor_b(gpu, M, N, K, block):
     c = tx.dot(da, db, scale_a=to_device(sa_, gpu), scale_b=to_device(sb_, gpu),
                out_dtype=torch.bfloat16, block=block)
     torch.cuda.synchronize()
-    p = tx.plan_for(da, db, tx.BF16, tx.SCALE_ROWCOL, block, ldc=c.stride(0))
-    assert p.desc.flags & tx.FLAG_B_KMAJOR
-    assert p.kernel == (tx.KERNEL_DECODE_F8 if M <= 64 and block == (0, 0, 0)
-                        else tx.KERNEL_GEMM_I8)
+    _assert_kmajor_plan(da, db, c, tx.KERNEL_GEMM_I8, block, tx.SCALE_ROWCOL)
     ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 64, 64),
                            scale_mode=oracle.SCALE_ROWCOL, sa=sa_, sb=sb_)
     got = from_device(c)
@@ -541,10 +555,7 @@ def test_fp8_block_scaled_kmajor_b(gpu, M, N, K, out, block):
     c = tx.dot(da, db, scale_a=to_device(sa, gpu), scale_b=to_device(sb, gpu), out_dtype=odt,
                block=block)
     torch.cuda.synchronize()
-    p = tx.plan_for(da, db, tx.tx_type(c), tx.SCALE_BLOCK128, block, ldc=c.stride(0))
-    assert p.desc.flags & tx.FLAG_B_KMAJOR
-    assert p.kernel == (tx.KERNEL_DECODE_F8 if M <= 64 and block == (0, 0, 0)
-                        else tx.KERNEL_GEMM_F8)
+    _assert_kmajor_plan(da, db, c, tx.KERNEL_GEMM_F8, block, tx.SCALE_BLOCK128)
     ct = oracle.BF16 if out == "bf16" else oracle.F32
     ref = oracle.tiled_dot(qa, qb, a_type=oracle.F8E4M3, c_type=ct, block=(128, 128, 128),
                            scale_mode=oracle.SCALE_BLOCK128, sa=sa, sb=sb)

@@ -204,9 +204,11 @@ const DecodeKernelFn kDecodeKernels[4] = {decode_i8_kernel<1>, decode_i8_kernel<
 // The row-parallel decode kernel by slice height (64, 128, 256 rows): rings
 // of 6, 4 and 3 slots of 24, 32 and 48 KiB (a 128-row batch: B's 16 KiB and
 // the slice's A).
-const DecodeKernelFn kDecodeRowsKernels[3] = {decode_rows_i8_kernel<64, 6>,
-                                              decode_rows_i8_kernel<128, 4>,
-                                              decode_rows_i8_kernel<256, 3>};
+// [B K-major][slice of 64, 128, 256 rows]
+const DecodeKernelFn kDecodeRowsKernels[2][3] = {
+    {decode_rows_i8_kernel<64, 6>, decode_rows_i8_kernel<128, 4>, decode_rows_i8_kernel<256, 3>},
+    {decode_rows_i8_kernel<64, 6, true>, decode_rows_i8_kernel<128, 4, true>,
+     decode_rows_i8_kernel<256, 3, true>}};
 // The 8-bit ring decode kernel: unscaled fp8 by [B K-major][A e4m3 / e5m2]
 // [B e4m3 / e5m2][slice of 16, 32, 48, 64 rows], block-scaled (e4m3) by
 // [B K-major][slice], int8 with B K-major (int32 C or W8A8) by slice.
@@ -389,7 +391,8 @@ bool decodeEpilogue(const tx_dot_desc &d) {
           (d.scale_mode == TX_SCALE_NONE && d.c_type == TX_I32));
 }
 bool useDecode(const tx_dot_desc &d) {
-  if (!decodeEpilogue(d) || (d.flags & TX_FLAG_B_KMAJOR) ||
+  // K-major B: the row kernel only (decode_rows_i8.h's BT form)
+  if (!decodeEpilogue(d) || ((d.flags & TX_FLAG_B_KMAJOR) && !decodeRows(d)) ||
       d.N > (int64_t)kDecodeMaxStrips * kDecodeStripN ||
       d.M > (decodeRows(d) ? kDecodeRowsMaxM : kDecodeMaxM))
     return false;
@@ -473,8 +476,9 @@ int64_t decode16Workspace(const tx_dot_desc &d, int ksplit) {
 
 // The 8-bit ring decode kernel (decode_f8.h), B row-major or K-major: fp8 x
 // fp8 (e4m3 / e5m2 in any mix) with fp32 C; e4m3 x e4m3 with 128-block scales
-// and bf16 / fp32 C; with B K-major also int8 -> int32 and W8A8 (row-major
-// int8 runs decode_i8.h); M <= 64, one arrival counter per 128-column strip.
+// and bf16 / fp32 C; with B K-major also int8 -> int32 and W8A8 at M <= 48
+// (past it the row kernel's K-major form; row-major int8 runs decode_i8.h);
+// M <= 64, one arrival counter per 128-column strip.
 bool useDecodeF8(const tx_dot_desc &d) {
   const bool fa = d.a_type == TX_F8E4M3 || d.a_type == TX_F8E5M2;
   const bool fb = d.b_type == TX_F8E4M3 || d.b_type == TX_F8E5M2;
@@ -482,8 +486,9 @@ bool useDecodeF8(const tx_dot_desc &d) {
   if (d.M > kDec8MaxM || cdiv(d.N, kDec8StripN) > kDec16MaxStrips)
     return false;
   if (d.a_type == TX_I8 && d.b_type == TX_I8)
-    return kmajor && ((d.scale_mode == TX_SCALE_NONE && d.c_type == TX_I32) ||
-                      (d.scale_mode == TX_SCALE_ROWCOL && d.c_type == TX_BF16));
+    return kmajor && d.M <= 48 &&
+           ((d.scale_mode == TX_SCALE_NONE && d.c_type == TX_I32) ||
+            (d.scale_mode == TX_SCALE_ROWCOL && d.c_type == TX_BF16));
   if (!fa || !fb)
     return false;
   if (d.scale_mode == TX_SCALE_NONE)
@@ -945,7 +950,9 @@ int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   a.partials = need > 0 ? reinterpret_cast<int32_t *>(static_cast<uint8_t *>(ws) + counters)
                         : nullptr;
   const DecodeKernelFn fn =
-      decodeRows(d) ? kDecodeRowsKernels[d.block_m == 64 ? 0 : d.block_m / 128] : kDecodeKernels[mt - 1];
+      decodeRows(d) ? kDecodeRowsKernels[(d.flags & TX_FLAG_B_KMAJOR) != 0]
+                                        [d.block_m == 64 ? 0 : d.block_m / 128]
+                    : kDecodeKernels[mt - 1];
   hipLaunchKernelGGL(fn, dim3(plan.grid_x),
                      dim3(plan.block_threads), 0, stream, a);
   TX_HIP_CHECK(hipGetLastError());

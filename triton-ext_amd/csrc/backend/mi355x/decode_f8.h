@@ -210,21 +210,6 @@ __device__ __forceinline__ void dec8_read_kmajor(uint32_t b0, uint32_t b1, uint3
 #undef TX_D8K_O
 #undef TX_D8K_T
 
-// Zero the bytes of a 16-byte fragment at K index k .. k + 15 that lie at or
-// past K.
-__device__ __forceinline__ i32x4_t dec8_mask_k(const i32x4_t &v, int64_t k, int64_t K) {
-  int o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    uint32_t m = 0;
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-      m |= (k + 4 * i + b < K ? 0xffu : 0u) << (8 * b);
-    o[i] = (int)((uint32_t)v[i] & m);
-  }
-  return i32x4_t{o[0], o[1], o[2], o[3]};
-}
-
 // FA, FB: the MFMA format codes of A and B (0 e4m3, 1 e5m2); SCALED takes
 // e4m3 x e4m3 with block scales.  BT: B K-major; I8: int8 -> int32 (BT only).
 template <int SR, bool SCALED, int FA = 0, int FB = 0, bool BT = false, bool I8 = false>

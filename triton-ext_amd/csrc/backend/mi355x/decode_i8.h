@@ -166,6 +166,21 @@ __device__ __forceinline__ void decode_store_i32(const DecodeArgs &p, int64_t m,
   }
 }
 
+// Zero the bytes of a 16-byte fragment at K index k .. k + 15 that lie at or
+// past K.
+__device__ __forceinline__ i32x4_t dec8_mask_k(const i32x4_t &v, int64_t k, int64_t K) {
+  int o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      m |= (k + 4 * i + b < K ? 0xffu : 0u) << (8 * b);
+    o[i] = (int)((uint32_t)v[i] & m);
+  }
+  return i32x4_t{o[0], o[1], o[2], o[3]};
+}
+
 template <int MT> struct DecodeCfg {
   // One slot per wave and ring stage: B's 8 KiB batch, then the wave's A
   // rows of that batch (MT KiB); as many stages as fit 160 KiB (4 for

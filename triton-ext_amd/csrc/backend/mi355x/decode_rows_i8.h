@@ -41,6 +41,17 @@
 // K loop in LoopSplit form as in decode_i8.h (for 128-row batches):
 // batches below k_main_batches load unmasked; the rest send rows >= K,
 // columns >= N and rows of A >= M to the zero-filled chunk.
+//
+// BT: B stored K-major ([N][K] row-major, row stride ldb: a W8A8 weight kept
+// [out][in]).  The strip's 128 storage rows are staged like A's rows (128
+// bytes of a batch each, chunk c of row r at c ^ ((r >> 1) & 7)) and a column
+// block's operand is read like an A row block (ds_read_b128: lane l gets
+// column 32 cb + l%32 at K bytes 32 ks + 16 (l/32) .. +15, the bytes of the A
+// operand it meets).  B's chunk that crosses K is loaded whole too, so in the
+// tail batch its bytes past K are zeroed in registers (A's junk past K then
+// meets zeros).  Each strip starts its split's batches at its own batch
+// (strip mod the batch count), so the workgroups running at once read B's
+// rows at different K offsets.
 #pragma once
 
 #include <type_traits>
@@ -140,7 +151,44 @@ __device__ __forceinline__ void rows_read_k32(uint32_t b, const uint32_t (&off)[
 #undef TX_ROWS_OUT8
 #undef TX_ROWS_TR
 
-template <int SR, int S>
+// The same K step with B K-major: the NCB column blocks' operands with
+// ds_read_b128 at `bk` (+4 KiB per block) and the R32 A row blocks at `ak`
+// (+4 KiB per 32 rows).
+#define TX_RK_B(i, off) "ds_read_b128 %[y" #i "], %[bk] offset:" #off "\n\t"
+#define TX_RK_A(i, off) "ds_read_b128 %[x" #i "], %[ak] offset:" #off "\n\t"
+#define TX_RK_BO(i) [y##i] "=&v"(b[i])
+#define TX_RK_AO(i) [x##i] "=&v"(a[i])
+#define TX_RK_IN [bk] "v"(bk), [ak] "v"(ak)
+template <int R32, int NCB>
+__device__ __forceinline__ void rows_read_k32_kmajor(uint32_t bk, uint32_t ak, i32x4_t (&b)[NCB],
+                                                     i32x4_t (&a)[R32]) {
+  static_assert((R32 == 1 || R32 == 2) && (NCB == 4 || (NCB == 2 && R32 == 1)),
+                "32 or 64 rows by 128 columns, or 32 rows by 64 columns, a wave");
+  if constexpr (NCB == 2)
+    asm volatile(TX_RK_B(0, 0) TX_RK_B(1, 4096) TX_RK_A(0, 0) "s_waitcnt lgkmcnt(0)"
+                 : TX_RK_BO(0), TX_RK_BO(1), TX_RK_AO(0)
+                 : TX_RK_IN
+                 : "memory");
+  else if constexpr (R32 == 1)
+    asm volatile(TX_RK_B(0, 0) TX_RK_B(1, 4096) TX_RK_B(2, 8192) TX_RK_B(3, 12288)
+                 TX_RK_A(0, 0) "s_waitcnt lgkmcnt(0)"
+                 : TX_RK_BO(0), TX_RK_BO(1), TX_RK_BO(2), TX_RK_BO(3), TX_RK_AO(0)
+                 : TX_RK_IN
+                 : "memory");
+  else
+    asm volatile(TX_RK_B(0, 0) TX_RK_B(1, 4096) TX_RK_B(2, 8192) TX_RK_B(3, 12288)
+                 TX_RK_A(0, 0) TX_RK_A(1, 4096) "s_waitcnt lgkmcnt(0)"
+                 : TX_RK_BO(0), TX_RK_BO(1), TX_RK_BO(2), TX_RK_BO(3), TX_RK_AO(0), TX_RK_AO(1)
+                 : TX_RK_IN
+                 : "memory");
+}
+#undef TX_RK_IN
+#undef TX_RK_AO
+#undef TX_RK_BO
+#undef TX_RK_A
+#undef TX_RK_B
+
+template <int SR, int S, bool BT = false>
 __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_rows_i8_kernel(DecodeArgs p) {
   typedef DecodeRowsCfg<SR, S> Cfg;
   constexpr int SLOT = Cfg::SLOT, WC = Cfg::WC, WROWS = Cfg::WROWS, R32 = Cfg::R32,
@@ -187,6 +235,13 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_rows_i8_kernel(De
   if (b_end > total_batches)
     b_end = total_batches;
   const int nb = b_end > b_begin ? b_end - b_begin : 0; // the same for every wave
+  const int rot = BT && nb > 0 ? strip % nb : 0; // K-major B: the strip's first batch
+  auto batch = [&](int i) { // the split's i-th batch to run (i < nb)
+    if constexpr (!BT)
+      return b_begin + i;
+    const int j = i + rot;
+    return b_begin + (j >= nb ? j - nb : j);
+  };
 
   // Loads of the split's batch i into `slot`: this wave's 4 of B's 16 KiB
   // (rows 32 wave .. +31 of the batch) and a quarter of the slice's A rows
@@ -200,18 +255,27 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_rows_i8_kernel(De
   // load reads the zero chunk instead, so each step issues the same loads.
   auto issue = [&](int i, uint8_t *slot) {
     const bool live = i < nb;
-    const int b = b_begin + i;
+    const int b = live ? batch(i) : b_begin + i;
     const int64_t k0 = (int64_t)b * kRowsBatchK;
     const bool mask = !live || n_edge || b >= p.k_main_batches;
 #pragma unroll
     for (int u = 0; u < Cfg::B_LOADS; ++u) {
       const int q = Cfg::B_LOADS * wave + u; // 1 KiB part q of the batch
       const int row = 8 * q + (lane >> 3), pc = lane & 7;
-      const int c = pc ^ (row & 7);
-      const int64_t k = k0 + row, n = n0 + 16 * c;
-      const void *src = p.B + k * p.ldb + n;
-      if (mask && (!live || k >= p.K || n >= p.N))
-        src = tx_zero_chunk;
+      const void *src;
+      if constexpr (BT) { // storage row n0 + row, chunk pc ^ ((row >> 1) & 7), as A's
+        const int c = pc ^ ((row >> 1) & 7);
+        const int64_t n = n0 + row, k = k0 + 16 * c;
+        src = p.B + n * p.ldb + k;
+        if (mask && (!live || n >= p.N || k >= p.K))
+          src = tx_zero_chunk;
+      } else {
+        const int c = pc ^ (row & 7);
+        const int64_t k = k0 + row, n = n0 + 16 * c;
+        src = p.B + k * p.ldb + n;
+        if (mask && (!live || k >= p.K || n >= p.N))
+          src = tx_zero_chunk;
+      }
       dma16_stream(src, (lds_void *)(slot + q * 1024)); // B is read once per slice
     }
 #pragma unroll
@@ -243,28 +307,46 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_rows_i8_kernel(De
   // v_mfma_i32_32x32x32_i8.  Lane l's A operand for step ks and row block rb
   // -- slice row WROWS rw + 32 rb + l%32, chunk 2 ks + l/32 -- sits at
   // a_k[ks] + 4 KiB rb (WROWS rw is a multiple of 32: the swizzle is l%32's).
-  uint32_t tr_off[NCB], a_k[4];
+  // K-major B, step ks: storage row 32 NCB cw + l%32 (+4 KiB per block),
+  // chunk 2 ks + l/32, swizzled like A's.
+  uint32_t tr_off[NCB], a_k[4], bk_k[4];
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb)
     tr_off[cb] = tr32_off(lane, NCB * cw + cb);
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     const int r = lane & 31;
-    a_k[ks] = Cfg::A_OFF + (WROWS * rw + r) * 128 + 16 * ((2 * ks + (lane >> 5)) ^ ((r >> 1) & 7));
+    const uint32_t ch = 16 * ((2 * ks + (lane >> 5)) ^ ((r >> 1) & 7));
+    a_k[ks] = Cfg::A_OFF + (WROWS * rw + r) * 128 + ch;
+    bk_k[ks] = (32 * NCB * cw + r) * 128 + ch;
   }
-  auto consume = [&](const uint8_t *slot) {
+  auto consume = [&](const uint8_t *slot, int i) {
     const uint32_t base = lds_addr(slot);
+    const bool tail = BT && batch(i) >= p.k_main_batches;
     auto step = [&](auto ks_c) {
       constexpr int KS = decltype(ks_c)::value;
       i32x4_t a[R32];
-      v2i_t lo[NCB], hi[NCB];
-      rows_read_k32<R32, NCB, KS>(base, tr_off, base + a_k[KS], lo, hi, a);
+      i32x4_t bf[NCB];
+      if constexpr (BT) {
+        rows_read_k32_kmajor<R32, NCB>(base + bk_k[KS], base + a_k[KS], bf, a);
+        if (tail) { // the K tail: B's bytes at or past K
+          const int64_t k = (int64_t)batch(i) * kRowsBatchK + 32 * KS + 16 * (lane >> 5);
+#pragma unroll
+          for (int cb = 0; cb < NCB; ++cb)
+            bf[cb] = dec8_mask_k(bf[cb], k, p.K);
+        }
+      } else {
+        v2i_t lo[NCB], hi[NCB];
+        rows_read_k32<R32, NCB, KS>(base, tr_off, base + a_k[KS], lo, hi, a);
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb)
+          bf[cb] = i32x4_t{lo[cb].x, lo[cb].y, hi[cb].x, hi[cb].y};
+      }
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
-        const i32x4_t bf = {lo[cb].x, lo[cb].y, hi[cb].x, hi[cb].y};
 #pragma unroll
         for (int rb = 0; rb < R32; ++rb)
-          acc[rb][cb] = mfma_i8_32(bf, a[rb], acc[rb][cb]);
+          acc[rb][cb] = mfma_i8_32(bf[cb], a[rb], acc[rb][cb]);
       }
     };
     step(std::integral_constant<int, 0>());
@@ -306,7 +388,7 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode_rows_i8_kernel(De
       wait_vmcnt<(S - 2) * Cfg::VPB>();
       asm volatile("s_barrier" ::: "memory");
       issue(i + S - 1, ring + ((s + S - 1) % S) * SLOT);
-      consume(ring + s * SLOT);
+      consume(ring + s * SLOT, i);
     }
   }
 k_loop_done:

@@ -190,11 +190,13 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
     int64_t spanA = 0, spanB = 0;
     tx_dot_operand_spans(&e, &spanA, &spanB);
     // The decode kernels' epilogues: W8A8 (row x column scales, bf16 C) and
-    // the plain int8 -> int32 dot (no scales, int32 C), B row-major, N up to
-    // their 4096 column strips.  Both stream B once with split-K.
+    // the plain int8 -> int32 dot (no scales, int32 C), N up to their 4096
+    // column strips; B row-major, or K-major on the row kernel (M > 48: the
+    // 8-bit ring decode kernel takes K-major B below that).  Both stream B
+    // once with split-K.
     const bool decode =
-        d->a_type == TX_I8 && d->b_type == TX_I8 && !(d->flags & TX_FLAG_B_KMAJOR) &&
-        d->N <= (int64_t)4096 * 128 &&
+        d->a_type == TX_I8 && d->b_type == TX_I8 &&
+        (!(d->flags & TX_FLAG_B_KMAJOR) || d->M > 48) && d->N <= (int64_t)4096 * 128 &&
         ((d->scale_mode == TX_SCALE_ROWCOL && d->c_type == TX_BF16) ||
          (d->scale_mode == TX_SCALE_NONE && d->c_type == TX_I32));
     // The 16-bit decode kernel: both operands bf16 or both fp16, no scales,
@@ -205,9 +207,10 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
         d->scale_mode == TX_SCALE_NONE && (d->c_type == d->a_type || d->c_type == TX_F32) &&
         d->M <= 64 && d->N <= (int64_t)16384 * 64;
     // The 8-bit ring decode kernel, B row-major or K-major: fp8 x fp8 with
-    // fp32 C, e4m3 x e4m3 with 128-block scales and bf16 / fp32 C; with B
-    // K-major also int8 -> int32 and W8A8; M <= 64, N up to its 16384 strips
-    // of 128 columns.
+    // fp32 C, e4m3 x e4m3 with 128-block scales and bf16 / fp32 C, M <= 64;
+    // with B K-major also int8 -> int32 and W8A8, M <= 48 (the row kernel's
+    // 32 x 32 x 32 products take M = 64: W8A8 22.4 against 26.8 us at
+    // N = K = 8192); N up to its 16384 strips of 128 columns.
     const bool fp8a = d->a_type == TX_F8E4M3 || d->a_type == TX_F8E5M2;
     const bool fp8b = d->b_type == TX_F8E4M3 || d->b_type == TX_F8E5M2;
     const bool kmajor = (d->flags & TX_FLAG_B_KMAJOR) != 0;
@@ -216,7 +219,7 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
         ((fp8a && fp8b && d->scale_mode == TX_SCALE_NONE && d->c_type == TX_F32) ||
          (d->scale_mode == TX_SCALE_BLOCK128 && d->a_type == TX_F8E4M3 &&
           d->b_type == TX_F8E4M3 && (d->c_type == TX_BF16 || d->c_type == TX_F32)) ||
-         (kmajor && d->a_type == TX_I8 && d->b_type == TX_I8 &&
+         (kmajor && d->a_type == TX_I8 && d->b_type == TX_I8 && d->M <= 48 &&
           ((d->scale_mode == TX_SCALE_NONE && d->c_type == TX_I32) ||
            (d->scale_mode == TX_SCALE_ROWCOL && d->c_type == TX_BF16))));
     const size_t first = spanA < TX_SPAN32_LIMIT && spanB < TX_SPAN32_LIMIT ? 0 : 1;
@@ -250,7 +253,7 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
           : d->M > 48 ? Tile{64, 128, 128, 1.0}
                       : Tile{(int32_t)(16 * cdiv(d->M > 0 ? d->M : 1, 16)), 128, 64, 1.0};
     else if (d->flags & TX_FLAG_B_KMAJOR)
-      t = kTiles8[0]; // the K-major B kernels exist for this tile only
+      t = kTiles8[0]; // of the 8-bit tiles only this one has a K-major B form
     else if (d->a_type == TX_F8E4M3 || d->a_type == TX_F8E5M2)
       t = kTiles8[first]; // the register-staged 128x128 tile is slower everywhere
     else
