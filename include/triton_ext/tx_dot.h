@@ -112,7 +112,8 @@ typedef enum tx_kernel {
   TX_KERNEL_GEMM_16BIT = 1, /* bf16/fp16 tile, MFMA 32x32x16, LDS-staged          */
   TX_KERNEL_GEMM_I8 = 2,    /* int8 tile, MFMA 16x16x64 (32x32x32 small tiles)   */
   TX_KERNEL_DECODE_I8 = 3,  /* int8 W8A8 decode shapes, MFMA 16x16x64 (M <= 48)
-                             * or 32x32x32 (row slices, M <= 1024)            */
+                             * or 32x32x32 (row slices, M <= 1024; these also
+                             * with B K-major)                                */
   TX_KERNEL_GEMM_F8 = 4,    /* fp8 e4m3 tile, MFMA 16x16x128 (32x32x64 small)    */
   TX_KERNEL_GEMM_MX = 5,    /* MX fp8 / fp4 tile, scaled MFMA 16x16x128 (e8m0)   */
   TX_KERNEL_GEMM_MX_BF16 = 6, /* MX x bf16: MX operand upcast to bf16 in the
@@ -121,8 +122,8 @@ typedef enum tx_kernel {
                                * B streamed once, MFMA 16x16x32              */
   TX_KERNEL_DECODE_F8 = 8,    /* 8-bit decode shapes (M <= 64): fp8 unscaled or
                                * with 128-block scales, and int8 (int32 C or
-                               * W8A8) with B K-major; B streamed once, MFMA
-                               * 16x16x128 (int8: 16x16x64)                  */
+                               * W8A8, M <= 48) with B K-major; B streamed
+                               * once, MFMA 16x16x128 (int8: 16x16x64)       */
 } tx_kernel;
 
 /* Bit flags for tx_dot_desc.flags */
@@ -131,8 +132,9 @@ typedef enum tx_kernel {
  * layout of tl.dot(q, tl.trans(k)) / q @ k.T with k row-major, and of a
  * weight kept [out][in].  Supported for bf16/fp16 operands on the 256x256x64
  * tile and the 16-bit decode kernel, and for every 8-bit dot but MX (int8 ->
- * int32, W8A8, unscaled and block-scaled fp8) on the 256x256x128 tile and the
- * 8-bit decode kernel (M <= 64). */
+ * int32, W8A8, unscaled and block-scaled fp8) on the 256x256x128 tile, the
+ * 8-bit decode kernel (M <= 64; int8 M <= 48) and, for int8, the row decode
+ * kernel (its 64 / 128 / 256-row slices). */
 #define TX_FLAG_B_KMAJOR 0x2
 /* C = C + A . B: the accumulator operand of tl.dot(a, b, acc) and
  * tl.dot_scaled(..., acc) (R:pass/LoopSplit/06-fused-attention.py:85).  C
