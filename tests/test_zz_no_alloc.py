@@ -161,6 +161,40 @@ def test_noalloc_decode_f8(gpu):
     _w8a8(gpu, 16, 8192, 8192, 74)
 
 
+def test_noalloc_kmajor_w8a8(gpu):
+    """W8A8 with the weight kept [N][K] (B K-major) on the shared scratch: the 8-bit decode
+    kernel's int8 form (M = 16) and the row kernel's K-major form (M = 100), larger call
+    first, bit-equal to tx_dot_launch on a fresh workspace and to the oracle."""
+    import torch
+    for M, N, K, seed in ((100, 8192, 8192, 81), (16, 4096, 4096, 82), (16, 1000, 3000, 83)):
+        say(f"noalloc W8A8 K-major M={M} N={N} K={K}")
+        a, b = uniform_i8((M, K), seed), uniform_i8((K, N), seed + 1)
+        sa, sb = uniform_scales(M, seed + 2), uniform_scales(N, seed + 3)
+        lda = -(-K // 16) * 16
+        pa = np.zeros((M, lda), dtype=np.int8)
+        pa[:, :K] = a
+        pbt = np.zeros((N, lda), dtype=np.int8)
+        pbt[:, :K] = b.T
+        da, dbt, dsa, dsb = (to_device(x, gpu) for x in (pa, pbt, sa, sb))
+        plan = tx.plan(tx.make_desc(M, N, K, tx.I8, tx.BF16, scale_mode=tx.SCALE_ROWCOL,
+                                    lda=lda, ldb=lda, ldc=-(-N // 8) * 8,
+                                    flags=tx.FLAG_B_KMAJOR))
+        assert plan.kernel == (tx.KERNEL_DECODE_I8 if M > 48 else tx.KERNEL_DECODE_F8)
+        assert plan.split_k > 1
+        ldc = plan.desc.ldc
+        c_ref = torch.empty((M, ldc), dtype=torch.bfloat16, device=gpu)
+        c_new = torch.full((M, ldc), float("nan"), dtype=torch.bfloat16, device=gpu)
+        ws = torch.zeros(int(plan.workspace_bytes), dtype=torch.uint8, device=gpu)
+        _launch("plain", plan, da, dbt, c_ref, dsa, dsb, ws)
+        _launch("noalloc", plan, da, dbt, c_new, dsa, dsb)
+        torch.cuda.synchronize()
+        ref, got = from_device(c_ref)[:, :N], from_device(c_new)[:, :N]
+        assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} elements differ"
+        orc = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 256, 128),
+                               scale_mode=oracle.SCALE_ROWCOL, sa=sa, sb=sb)
+        assert np.array_equal(got, orc)
+
+
 def test_noalloc_workspace_free_kernels(gpu):
     """A plan without workspace (the bf16 tile) runs through the same entry point."""
     import torch
