@@ -116,6 +116,13 @@ TX_API int tx_arith_intensity(const tx_dot_desc *desc, tx_ai_report *out);
 TX_API int tx_dot_operand_spans(const tx_dot_desc *desc, int64_t *a_bytes, int64_t *b_bytes);
 /* Largest operand span (bytes, exclusive) the 32-bit-offset tiles take. */
 #define TX_SPAN32_LIMIT ((int64_t)1 << 31)
+/* Split-K factor of a dot on the 256x256 tiles: with fewer than half as many
+ * tiles as the 256 CUs, K is cut into S ranges of whole K steps, the
+ * workgroups (tile, range) store fp32 / int32 partial sums, and a second
+ * kernel adds them in range order and applies the epilogue.  S is the
+ * largest power of two up to 16 with tiles * S <= 256 and at least 8 K steps
+ * a range; 1 (no split) otherwise. */
+TX_API int32_t tx_gemm_split_k(int64_t tiles, int64_t ksteps);
 /* Row stride (elements) of a B operand that tl.dot_scaled with one bf16 side
  * upcasts to bf16 in the workspace: N rounded up to 16 columns, so every row
  * starts 16-byte aligned for the bf16 tile.  (An upcast A is packed: K.) */

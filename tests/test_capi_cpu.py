@@ -413,8 +413,11 @@ def test_mx_plans():
         assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == \
             (q.desc.block_m, q.desc.block_n, q.desc.block_k)
         assert (p.k_main_steps, p.k_tail, p.grid_x) == (q.k_main_steps, q.k_tail, q.grid_x)
+        assert (p.split_k, p.grid_y) == (q.split_k, q.grid_y) and q.split_k > 1
         mx_elems = 4000 * 528 if b != tx.BF16 else 1000 * 4000
-        assert p.workspace_bytes == COUNTERS + (mx_elems * 2 + 255) // 256 * 256
+        # the upcast operand, then (after it) the bf16 dot's split-K partials
+        assert p.workspace_bytes == COUNTERS + (mx_elems * 2 + 255) // 256 * 256 + \
+            q.workspace_bytes - COUNTERS
         bits = {tx.BF16: 16, tx.F4E2M1: 4, tx.F8E4M3: 8, tx.F8E5M2: 8}
         scale_rows = 528 if b != tx.BF16 else 1000  # only the MX side is scaled
         assert p.bytes == 1000 * 4000 * bits[a] / 8 + 4000 * 528 * bits[b] / 8 + \
@@ -429,11 +432,14 @@ def test_nv16_plans():
     NV = tx.SCALE_NV16
     p = tx.plan(tx.make_desc(512, 256, 1024, tx.F4E2M1, tx.F32, b_type=tx.F4E2M1, scale_mode=NV))
     assert p.kernel == tx.KERNEL_GEMM_MX_BF16
-    assert p.workspace_bytes == COUNTERS + 512 * 1024 * 2 + 1024 * 256 * 2  # both as bf16
+    q = tx.plan(tx.make_desc(512, 256, 1024, tx.BF16, tx.F32))  # the bf16 dot it runs
+    assert (p.split_k, p.grid_x, p.grid_y) == (q.split_k, q.grid_x, q.grid_y)
+    partials = q.workspace_bytes - COUNTERS if q.split_k > 1 else 0
+    assert p.workspace_bytes == COUNTERS + 512 * 1024 * 2 + 1024 * 256 * 2 + partials  # as bf16
     assert p.bytes == 512 * 512 + 512 * 256 + (512 + 256) * 64 + 512 * 256 * 4
     assert p.peak_flops == pytest.approx(2516.6e12)
     p = tx.plan(tx.make_desc(512, 256, 1024, tx.BF16, tx.F32, b_type=tx.F4E2M1, scale_mode=NV))
-    assert p.workspace_bytes == COUNTERS + 1024 * 256 * 2
+    assert p.workspace_bytes == COUNTERS + 1024 * 256 * 2 + partials
     assert _err(tx.make_desc(64, 64, 256, tx.F8E4M3, tx.F32, scale_mode=NV)) == tx.ERR_UNSUPPORTED
     assert _err(tx.make_desc(64, 64, 256, tx.F4E2M1, tx.F32, scale_mode=5)) == tx.ERR_INVALID
 

@@ -32,6 +32,7 @@
 #include "decode_rows_i8.h"
 #include "gemm16_dma.h"
 #include "gemm8_w4.h"
+#include "splitk_reduce.h"
 #include "gemm8_n224.h"
 #include "gemm16_w4.h"
 #include "gemm_tile.h"
@@ -518,6 +519,51 @@ int64_t decodeF8Workspace(const tx_dot_desc &d, int ksplit) {
          ksplit * decode_f8_split_bytes(cdiv(d.N, kDec8StripN), decode16Rows(d));
 }
 
+// Split-K on the 256x256 tiles (tx_gemm_split_k): every epilogue but MX's
+// (and not for a plan that masks every K step).  The tile kernel stores
+// range z's 32-bit sums with its fp32 / int32 epilogue (128-block fp8: the
+// scaled fp32 one) into the workspace past the decode counters, [split_k][M]
+// [ldp] with ldp = N rounded up to 4; splitk_reduce.h adds them and applies
+// the dot's own epilogue.
+int64_t splitLdp(const tx_dot_desc &d) { return (d.N + 3) & ~3ll; }
+int partialEpi(const tx_dot_desc &d, int op) {
+  if (op == OP_I8)
+    return EPI_I32;
+  if (op == OP_F8 && d.scale_mode == TX_SCALE_BLOCK128)
+    return EPI_BLOCK128_F32;
+  return EPI_F32;
+}
+// d: the dot the tile runs (for the MX x bf16 upcast, its bf16 dot: bfDot).
+int gemmSplit(const tx_dot_desc &d, int op, int64_t tiles) {
+  if (d.block_m != 256 || d.block_n != 256 || d.scale_mode == TX_SCALE_MX32 ||
+      d.scale_mode == TX_SCALE_NV16 || (d.flags & TX_FLAG_NO_LOOP_SPLIT) ||
+      findGemmConfig(op, partialEpi(d, op), d.block_m, d.block_n, d.block_k,
+                     (d.flags & TX_FLAG_B_KMAJOR) != 0, fmtOf(d)) < 0)
+    return 1;
+  return tx_gemm_split_k(tiles, cdiv(d.K, d.block_k));
+}
+int64_t gemmSplitWorkspace(const tx_dot_desc &d, int split) {
+  return split > 1 ? kDecodeCounterBytes + (int64_t)split * d.M * splitLdp(d) * 4 : 0;
+}
+// The bf16 dot a tl.dot_scaled with an upcast operand runs on the upcast
+// operands (the same tile, split-K and epilogue as that bf16 dot).
+tx_dot_desc bfDot(const tx_dot_desc &d) {
+  tx_dot_desc e = d;
+  if (mxUpcastSide(d)) {
+    e.a_type = TX_BF16;
+    e.b_type = TX_BF16;
+    e.scale_mode = TX_SCALE_NONE;
+  }
+  return e;
+}
+// Workspace of a tile plan: the upcast operands (after the counter region),
+// then the split-K partials (the same offset from the end of the upcast).
+int64_t gemmWorkspace(const tx_dot_desc &d, int split) {
+  const int64_t up = mxUpcastWorkspace(d);
+  const int64_t sk = gemmSplitWorkspace(d, split);
+  return up > 0 && sk > 0 ? up + sk - kDecodeCounterBytes : up + sk;
+}
+
 // The 32-bit-offset tiles (gemm16_w4.h, gemm8_w4.h, gemm8_n224.h) address A,
 // B and the block scales through buffer offsets: each must span less than
 // 2^31 bytes (out-of-range chunks, at offset 2^31, read zeros).
@@ -621,11 +667,12 @@ int txMi355xDotRun(tx_dot_plan *plan) {
   const int64_t kbytes = d.K * tx_dtype_bits(d.a_type) / 8;
   plan->group_m = c.dma == 5 && kbytes >= 8192 ? 2 : 4;
   plan->kernel = gemmKernelOf(d, op);
-  plan->split_k = 1;
+  plan->split_k = gemmSplit(bfDot(d), op, (int64_t)plan->m_tiles * plan->n_tiles);
   plan->grid_x = plan->m_tiles * plan->n_tiles;
-  plan->grid_y = plan->grid_z = 1;
+  plan->grid_y = plan->split_k;
+  plan->grid_z = 1;
   plan->block_threads = c.wm * c.wn * 64;
-  plan->workspace_bytes = upcast ? mxUpcastWorkspace(d) : 0;
+  plan->workspace_bytes = gemmWorkspace(d, plan->split_k);
   plan->passes_run += 1;
   return TX_OK;
 }
@@ -764,18 +811,27 @@ extern "C" TX_API int tx_dot_plan_create(const tx_dot_desc *desc,
 namespace {
 
 int launchGemm(const tx_dot_plan &plan, const void *A, const void *B, void *C,
-               const void *sa, const void *sb, hipStream_t stream) {
+               const void *sa, const void *sb, void *ws, size_t ws_bytes, hipStream_t stream) {
   const tx_dot_desc &d = plan.desc;
   int op, epi;
   classify(d, &op, &epi);
-  const int ci = findGemmConfig(op, epi, d.block_m, d.block_n, d.block_k,
-                                (d.flags & TX_FLAG_B_KMAJOR) != 0, fmtOf(d));
+  const int split = plan.split_k > 1 ? plan.split_k : 1;
+  // split-K: the tile kernel with the 32-bit partial epilogue, then the reduction
+  const int ci = findGemmConfig(op, split > 1 ? partialEpi(d, op) : epi, d.block_m, d.block_n,
+                                d.block_k, (d.flags & TX_FLAG_B_KMAJOR) != 0, fmtOf(d));
   if (ci < 0)
     return fail(TX_ERR_UNSUPPORTED, "plan names a tile that is not instantiated");
   const GemmConfig &c = kGemmConfigs[ci];
   if (plan.grid_x != plan.m_tiles * plan.n_tiles || plan.m_tiles <= 0 ||
-      plan.n_tiles <= 0 || plan.block_threads != c.wm * c.wn * 64)
+      plan.n_tiles <= 0 || plan.block_threads != c.wm * c.wn * 64 ||
+      plan.grid_y != split)
     return fail(TX_ERR_INVALID, "plan launch shape does not match its tile");
+  const int64_t need = gemmSplitWorkspace(d, split);
+  if (need > 0 && (!ws || (int64_t)ws_bytes < need))
+    return fail(TX_ERR_WORKSPACE, "split-K needs %lld workspace bytes, got %zu", (long long)need,
+                ws_bytes);
+  if (need > 0 && (reinterpret_cast<uintptr_t>(ws) & 15))
+    return fail(TX_ERR_INVALID, "workspace must be 16-byte aligned");
   static std::once_flag attr_once[kNumGemmConfigs];
   hipError_t attr_err = hipSuccess;
   if (c.lds_bytes > 0)
@@ -819,9 +875,47 @@ int launchGemm(const tx_dot_plan &plan, const void *A, const void *B, void *C,
   a.sa_ld = (int32_t)(mx ? d.K / 32 : cdiv(d.K, 128));
   a.sb_ld = (int32_t)cdiv(d.N, 128);
   a.accumulate = (d.flags & TX_FLAG_ACCUMULATE) != 0;
-  hipLaunchKernelGGL(c.fn, dim3(plan.grid_x), dim3(plan.block_threads),
-                     c.lds_bytes, stream, a);
+  if (split == 1) {
+    hipLaunchKernelGGL(c.fn, dim3(plan.grid_x), dim3(plan.block_threads),
+                       c.lds_bytes, stream, a);
+    TX_HIP_CHECK(hipGetLastError());
+    return TX_OK;
+  }
+  // Ranges 0 .. split - 2 of split_steps whole K steps each; the last range
+  // the rest, with the dot's own peeled tail (the K-loop fields, shifted).
+  uint8_t *const part = static_cast<uint8_t *>(ws) + kDecodeCounterBytes;
+  const int ksteps = (int)cdiv(d.K, d.block_k);
+  a.split_k = split;
+  a.split_steps = ksteps / split;
+  a.k_main_steps -= (split - 1) * a.split_steps;
+  a.C = part;
+  a.ldc = splitLdp(d);
+  a.accumulate = 0;
+  hipLaunchKernelGGL(c.fn, dim3(plan.grid_x, split), dim3(plan.block_threads), c.lds_bytes,
+                     stream, a);
   TX_HIP_CHECK(hipGetLastError());
+  txk::SplitReduceArgs r;
+  r.part = part;
+  r.C = C;
+  r.sa = static_cast<const float *>(sa);
+  r.sb = static_cast<const float *>(sb);
+  r.ldc = d.ldc;
+  r.ldp = splitLdp(d);
+  r.M = (int32_t)d.M;
+  r.N = (int32_t)d.N;
+  r.split_k = split;
+  r.kind = d.c_type == TX_F32   ? txk::SPLIT_F32
+           : d.c_type == TX_I32 ? txk::SPLIT_I32
+           : d.c_type == TX_F16 ? txk::SPLIT_F16
+           : d.scale_mode == TX_SCALE_ROWCOL ? txk::SPLIT_ROWCOL
+                                             : txk::SPLIT_BF16;
+  r.acc = (d.flags & TX_FLAG_ACCUMULATE) != 0;
+  const int64_t quads = d.M * cdiv(d.N, 4);
+  if (quads > 0) {
+    hipLaunchKernelGGL(txk::splitk_reduce_kernel, dim3((unsigned)cdiv(quads, 256)), dim3(256), 0,
+                       stream, r);
+    TX_HIP_CHECK(hipGetLastError());
+  }
   return TX_OK;
 }
 
@@ -903,7 +997,11 @@ int launchMxUpcast(const tx_dot_plan &plan, const void *A, const void *B, void *
   if (side & 1)
     g.desc.lda = d.K;
   g.kernel = TX_KERNEL_GEMM_16BIT;
-  return launchGemm(g, (side & 1) ? wa : A, (side & 2) ? wb : B, C, nullptr, nullptr, stream);
+  // split-K partials after the upcast operands (launchGemm skips a counter
+  // region's worth from the workspace it is given)
+  const int64_t up_bytes = need - kDecodeCounterBytes;
+  return launchGemm(g, (side & 1) ? wa : A, (side & 2) ? wb : B, C, nullptr, nullptr,
+                    static_cast<uint8_t *>(ws) + up_bytes, ws_bytes - (size_t)up_bytes, stream);
 }
 
 int launchDecode(const tx_dot_plan &plan, const void *A, const void *B, void *C,
@@ -1098,8 +1196,10 @@ int checkPlan(const tx_dot_plan &p) {
     return fail(TX_ERR_INVALID, "no loop split for K=%lld, BK=%d", (long long)d.K, d.block_k);
   if (p.k_split != ks || p.k_main_steps != km || p.k_tail != kt ||
       p.m_tiles != cdiv(d.M, d.block_m) || p.n_tiles != cdiv(d.N, d.block_n) ||
-      p.m_edge != d.M % d.block_m || p.n_edge != d.N % d.block_n || p.grid_y != 1 ||
-      p.grid_z != 1)
+      p.m_edge != d.M % d.block_m || p.n_edge != d.N % d.block_n || p.grid_z != 1 ||
+      (p.grid_y != 1 && p.kernel != TX_KERNEL_GEMM_16BIT && p.kernel != TX_KERNEL_GEMM_I8 &&
+       p.kernel != TX_KERNEL_GEMM_F8 && p.kernel != TX_KERNEL_GEMM_MX_BF16))
+    // (the tiles' split-K ranges, checked below)
     return fail(TX_ERR_INVALID, "the plan's loop split or tile grid does not follow from its "
                 "descriptor");
   int op, epi;
@@ -1139,9 +1239,10 @@ int checkPlan(const tx_dot_plan &p) {
   const int src = checkSpans32(d, c);
   if (src != TX_OK)
     return src;
-  if (p.kernel != gemmKernelOf(d, op) || p.split_k != 1 ||
+  const int split = gemmSplit(bfDot(d), op, (int64_t)p.m_tiles * p.n_tiles);
+  if (p.kernel != gemmKernelOf(d, op) || p.split_k != split || p.grid_y != split ||
       p.grid_x != (int64_t)p.m_tiles * p.n_tiles || p.block_threads != c.wm * c.wn * 64 ||
-      p.workspace_bytes != (upcast ? mxUpcastWorkspace(d) : 0))
+      p.workspace_bytes != gemmWorkspace(d, split))
     return fail(TX_ERR_INVALID, "the plan's kernel or launch shape does not follow from its "
                 "descriptor");
   return TX_OK;
@@ -1193,7 +1294,7 @@ int launchPlanned(const tx_dot_plan *plan, const void *A, const void *B, void *C
   case TX_KERNEL_GEMM_I8:
   case TX_KERNEL_GEMM_F8:
   case TX_KERNEL_GEMM_MX:
-    return launchGemm(*plan, A, B, C, scale_a, scale_b, s);
+    return launchGemm(*plan, A, B, C, scale_a, scale_b, workspace, workspace_bytes, s);
   case TX_KERNEL_DECODE_I8:
     return launchDecode(*plan, A, B, C, scale_a, scale_b, workspace,
                         workspace_bytes, s);

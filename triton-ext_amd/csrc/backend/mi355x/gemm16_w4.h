@@ -563,11 +563,12 @@ __global__ void __launch_bounds__(NW * 64, 1) gemm16_w4_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * (G::A_BYTES + G::B_BYTES)];
   int tm, tn;
   tile_coords(p, tm, tn);
+  const GemmArgs q = split_k_args<G::BK, G::BK / 16, 2, BT, false>(p);
   const int64_t m0 = (int64_t)tm * G::BM, n0 = (int64_t)tn * G::BN;
-  if (m0 + G::BM <= p.M && n0 + G::BN <= p.N)
-    G::template run<false>(p, m0, n0, smem);
+  if (m0 + G::BM <= q.M && n0 + G::BN <= q.N)
+    G::template run<false>(q, m0, n0, smem);
   else
-    G::template run<true>(p, m0, n0, smem);
+    G::template run<true>(q, m0, n0, smem);
 }
 
 } // namespace txk

@@ -720,11 +720,12 @@ __global__ void __launch_bounds__(512, 1) gemm8_w4_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * G::STAGE];
   int tm, tn;
   tile_coords(p, tm, tn);
+  const GemmArgs q = split_k_args<G::BK, 1, 1, BT, G::SCALED>(p);
   const int64_t m0 = (int64_t)tm * G::BM, n0 = (int64_t)tn * G::BN;
-  if (m0 + G::BM <= p.M && n0 + G::BN <= p.N)
-    G::template run<false>(p, m0, n0, smem);
+  if (m0 + G::BM <= q.M && n0 + G::BN <= q.N)
+    G::template run<false>(q, m0, n0, smem);
   else
-    G::template run<true>(p, m0, n0, smem);
+    G::template run<true>(q, m0, n0, smem);
 }
 
 } // namespace txk

@@ -124,7 +124,43 @@ struct GemmArgs {
   int32_t group_m;        // tile rows per group in the tile order
   int32_t sa_ld, sb_ld; // MX: sa_ld = bytes per scale row = K / 32 groups
   int32_t accumulate;   // fp32 / int32 C: C = C + A . B (tl.dot's acc operand)
+  // Split-K (the 256x256 tiles): split_k > 1 launches split_k workgroups per
+  // tile (blockIdx.y); range z runs K steps [z split_steps, (z + 1)
+  // split_steps) of its tile, the last range the rest, which the K-loop
+  // fields above describe, and stores its 32-bit sums at C + z M ldc.
+  int32_t split_k = 1;
+  int32_t split_steps = 0;
 };
+
+// The arguments of this workgroup's K range under split-K: A, B and the
+// 128-block scales advanced to the range's first K step, C to its partial,
+// and K with the loop fields of a range of whole steps (every range but the
+// last).  BK: K elements a step (bytes for 8-bit); FULL_KS: MFMA sub-steps
+// of a whole step; ELT: bytes an element; BT: B K-major; BLOCK: 128-block
+// scales (BK is then 128: a step is one scale block).
+template <int BK, int FULL_KS, int ELT, bool BT, bool BLOCK>
+__device__ __forceinline__ GemmArgs split_k_args(const GemmArgs &p) {
+  GemmArgs q = p;
+  if (p.split_k <= 1)
+    return q;
+  const int z = blockIdx.y;
+  const int64_t k0 = (int64_t)z * p.split_steps * BK;
+  q.A = p.A + k0 * ELT;
+  q.B = p.B + (BT ? k0 * ELT : k0 * p.ldb * ELT);
+  q.C = static_cast<uint8_t *>(p.C) + (int64_t)z * p.M * p.ldc * 4;
+  if (BLOCK) {
+    q.sa = p.sa + k0 / 128;
+    q.sb = p.sb + (k0 / 128) * p.sb_ld;
+  }
+  q.K = p.K - k0;
+  if (z < p.split_k - 1) {
+    q.K = (int64_t)p.split_steps * BK;
+    q.k_main_steps = p.split_steps;
+    q.k_masked_steps = 0;
+    q.last_ks = FULL_KS;
+  }
+  return q;
+}
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
 // L2), so workgroup b runs on XCD b % 8.  Renumber so that each XCD gets a

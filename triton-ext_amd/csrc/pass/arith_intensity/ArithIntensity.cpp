@@ -31,7 +31,8 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 struct Tile {
   int32_t bm, bn, bk;
-  double eff; // fraction of MFMA peak a tile of this size sustains
+  double eff;  // fraction of MFMA peak a tile of this size sustains
+  int occ = 1; // workgroups per CU that eff needs (latency hidden by each other)
 };
 
 // Tiles the backend instantiates, largest first.  `eff` is the fraction of
@@ -40,32 +41,44 @@ struct Tile {
 // 16-bit 256x256x64 0.509, 128x128x64 0.341, 64x64x32 0.187; 8-bit
 // 256x256x128 0.463, 128x128x128 0.173.  tileCost weighs them against the
 // waves of tiles a shape needs.
-const Tile kTiles16[] = {{256, 256, 64, 0.509}, {128, 128, 64, 0.341},
-                         {64, 64, 32, 0.187}};
+// With fewer workgroups than occ per CU a tile runs at the rate of occ per
+// CU all the same (measured at M = 128 / 512, N = K = 8192: 64x64x32 190 us,
+// 128x128x64 154 us, where eff alone predicts 36 and 80).
+const Tile kTiles16[] = {{256, 256, 64, 0.509, 1}, {128, 128, 64, 0.341, 2},
+                         {64, 64, 32, 0.187, 4}};
 // 8-bit tiles.  (A 256x224 tile also exists for explicit requests: it fills
 // all CUs at N = 7168, but its A-resident wave layout needs 28 transposed B
 // reads per step against 16; it measured 0.273 at int8 4096^3 and no faster
 // than 256x256 at N = 7168.)
-const Tile kTiles8[] = {{256, 256, 128, 0.463}, {128, 128, 128, 0.173}};
+const Tile kTiles8[] = {{256, 256, 128, 0.463, 1}, {128, 128, 128, 0.173, 2}};
 // MX (tl.dot_scaled) tiles: one 256x256 tile of 128 bytes of K per step,
 // i.e. 128 fp8 or 256 fp4 elements.
 const Tile kTileMx8 = {256, 256, 128, 0.45}, kTileMx4 = {256, 256, 256, 0.33};
 
-// Estimated time of a tiled dot in arbitrary units: whole waves of tiles
-// across the CUs, each tile costing BM*BN*K / eff.
-double tileCost(const Tile &t, int64_t M, int64_t N, int64_t K) {
-  int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
-  int64_t waves = cdiv(tiles, kCUs);
-  return (double)waves * t.bm * t.bn * (double)K / t.eff;
+// Estimated time of a tiled dot in MAC-units of one CU: whole waves of
+// occ workgroups a CU, each a tile over its K range costing BM*BN*K / eff.  The 256x256 tiles split K when they leave most CUs idle
+// (tx_gemm_split_k): the ranges run as more workgroups, and their fp32
+// partials, written and read back (8 S M N bytes), add their HBM time and a
+// second launch at `cu_macs` (a CU's peak MAC rate).
+double tileCost(const Tile &t, int64_t M, int64_t N, int64_t K, double cu_macs) {
+  const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
+  const int64_t ksteps = cdiv(K, t.bk);
+  const int32_t s = t.bm == 256 && t.bn == 256 ? tx_gemm_split_k(tiles, ksteps) : 1;
+  const int64_t waves = cdiv(tiles * s, (int64_t)kCUs * t.occ) * t.occ;
+  double c = (double)waves * t.bm * t.bn * (double)cdiv(ksteps, s) * t.bk / t.eff;
+  if (s > 1)
+    c += (8.0 * s * (double)M * (double)N / kHbm + 4e-6) * cu_macs;
+  return c;
 }
 
 // Cheapest candidate from index `first` on (the 256-wide tile is index 0).
 template <size_t N>
-Tile chooseTile(const Tile (&cands)[N], int64_t M, int64_t Nn, int64_t K, size_t first = 0) {
+Tile chooseTile(const Tile (&cands)[N], int64_t M, int64_t Nn, int64_t K, double cu_macs,
+                size_t first = 0) {
   Tile best = cands[first];
-  double bestCost = tileCost(best, M, Nn, K);
+  double bestCost = tileCost(best, M, Nn, K, cu_macs);
   for (size_t i = first + 1; i < N; ++i) {
-    double c = tileCost(cands[i], M, Nn, K);
+    double c = tileCost(cands[i], M, Nn, K, cu_macs);
     if (c < bestCost) {
       best = cands[i];
       bestCost = c;
@@ -75,6 +88,13 @@ Tile chooseTile(const Tile (&cands)[N], int64_t M, int64_t Nn, int64_t K, size_t
 }
 
 } // namespace
+
+extern "C" int32_t tx_gemm_split_k(int64_t tiles, int64_t ksteps) {
+  int32_t s = 1;
+  while (s < 16 && tiles * s * 2 <= kCUs && ksteps / (s * 2) >= 8)
+    s *= 2;
+  return s;
+}
 
 extern "C" int32_t tx_dtype_bits(int32_t dtype) {
   switch (dtype) {
@@ -224,7 +244,7 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
            (d->scale_mode == TX_SCALE_ROWCOL && d->c_type == TX_BF16))));
     const size_t first = spanA < TX_SPAN32_LIMIT && spanB < TX_SPAN32_LIMIT ? 0 : 1;
     if (upcast)
-      t = chooseTile(kTiles16, d->M, d->N, d->K, first); // MX x bf16 runs on the bf16 tile
+      t = chooseTile(kTiles16, d->M, d->N, d->K, kPeak16 / 2 / kCUs, first); // MX x bf16: bf16 tile
     else if (d->scale_mode == TX_SCALE_MX32)
       t = ba == 4 ? kTileMx4 : kTileMx8;
     else if (decode_f8)
@@ -234,7 +254,7 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
     else if (sa == 2 && (d->flags & TX_FLAG_B_KMAJOR))
       t = kTiles16[0]; // the K-major B kernel exists for this tile only
     else if (sa == 2)
-      t = chooseTile(kTiles16, d->M, d->N, d->K, first);
+      t = chooseTile(kTiles16, d->M, d->N, d->K, kPeak16 / 2 / kCUs, first);
     else if (decode && d->M > 256 && d->M <= 512)
       // W8A8 past the decode sizes, up to M = 512: the row-parallel decode
       // kernel's slices of 256 rows (measured at N = K = 8192: M = 384 62.3 us,
@@ -257,7 +277,7 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
     else if (d->a_type == TX_F8E4M3 || d->a_type == TX_F8E5M2)
       t = kTiles8[first]; // the register-staged 128x128 tile is slower everywhere
     else
-      t = chooseTile(kTiles8, d->M, d->N, d->K, first);
+      t = chooseTile(kTiles8, d->M, d->N, d->K, kPeak8 / 2 / kCUs, first);
   }
   out->block_m = t.bm;
   out->block_n = t.bn;
