@@ -61,7 +61,8 @@ def parse():
                          "K-major), w8a8_kmajor (or w8a8_kmajor_1, _16, _64, _256: W8A8 with the "
                          "weight kept [N][K]), bf16_decode (or bf16_decode_1, _16, _64: "
                          "bf16 at N = K = 8192 on the 16-bit decode kernel; bf16_decode_kmajor, "
-                         "or _1, _16, _64: the same with B K-major), fp8_decode (or "
+                         "or _1, _16, _64: the same with B K-major), mid_m (or mid_m_bf16_128, _256, "
+                         "_512, mid_m_fp8_256: a few hundred rows on the split-K tiles), fp8_decode (or "
                          "fp8_decode_1, _16, _64: block-scaled e4m3 at N = K = 7168 on the fp8 "
                          "decode kernel), int8, fp8 (fp8u: the unscaled 4096^3 line only), kmajor (bf16 "
                          "4096^3, int8 and fp8 4096^3 with B K-major), "
@@ -392,6 +393,31 @@ def bench_decode16(tx, dev, M, N, K, steps, warmup, flush, seed=3, kmajor=False)
                 ms_warm_mall=warm, gbps=nbytes / med / 1e6, frac_hbm=nbytes / med / 1e-3 / HBM,
                 tflops=2.0 * M * N * K / med / 1e9,
                 plan=plan_info(tx, p, split_k=p.split_k, grid=p.grid_x))
+
+
+def bench_mid_m(tx, dev, kind, M, N, K, flush, seed=7):
+    """Dots of a few hundred rows (a batch past the decode kernels), cold in a stream: the
+    256x256 tiles with split-K (kind "bf16": bf16 C; "fp8": e4m3 with 128-block scales, bf16
+    C), beside hipBLASLt's bf16 (torch.matmul) on the same shapes and timing."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    if kind == "bf16":
+        a, b = bf16_inputs(M, N, K, dev, seed)
+        run = Launcher(tx, a, b, c)
+        vendor = time_cold_in_stream(lambda: torch.matmul(a, b, out=c), flush)
+        what = f"bf16 M={M} N={N} K={K}"
+    else:
+        qa, qb, sa, sb = fp8_block_inputs_dev(M, N, K, dev, seed)
+        run = Launcher(tx, qa, qb, c, sa, sb, tx.SCALE_BLOCK128)
+        vendor = None
+        what = f"fp8 e4m3 block-scaled M={M} N={N} K={K}"
+    ms = time_cold_in_stream(run, flush)
+    p = run.plan
+    return dict(workload=what + ", split-K", ms=ms, tflops=2.0 * M * N * K / ms / 1e9,
+                ms_vendor=vendor,
+                plan=plan_info(tx, p, split_k=p.split_k, grid=[p.grid_x, p.grid_y]))
 
 
 def fp8_block_inputs_dev(M, N, K, dev, seed):
@@ -1179,6 +1205,14 @@ def main():
             print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
                   f"({100 * r['frac_hbm']:.1f}% HBM); isolated launch "
                   f"{r['ms_isolated'] * 1e3:.2f} us", file=sys.stderr, flush=True)
+    for kind, m, n in (("bf16", 128, 8192), ("bf16", 256, 8192), ("bf16", 512, 8192),
+                       ("fp8", 256, 7168)):
+        if want("mid_m") or want(f"mid_m_{kind}_{m}"):
+            r = bench_mid_m(tx, dev, kind, m, n, n, flush)
+            secondary.append(r)
+            v = f"; hipBLASLt {r['ms_vendor'] * 1e3:.1f} us" if r["ms_vendor"] else ""
+            print(f"# {r['workload']} (split {r['plan']['split_k']}): {r['ms'] * 1e3:.1f} us in "
+                  f"stream, {r['tflops']:.0f} TFLOP/s{v}", file=sys.stderr, flush=True)
     if want("int8"):
         r = bench_int8(tx, dev, 4096, 4096, 4096, args.steps, args.warmup)
         secondary.append(r)
