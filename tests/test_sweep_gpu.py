@@ -145,6 +145,27 @@ def _cases():
         out.append(("fp8", 200 + i, dict(M=_dim(rng, 600), N=_dim(rng, 600), K=_dim(rng, 900),
                                          fa=fa, fb=fb, block=[(0, 0, 0), (256, 256, 128)][i // 8],
                                          kmajor=True)))
+    # a few hundred rows with long K: the 256x256 tiles' split-K (ranges of whole steps,
+    # the K tail in the last range), every dtype and layout
+    for i in range(24):
+        M = int(rng.integers(65, 700))
+        N = int(rng.integers(1, 1200))
+        K = int(rng.integers(2048, 9000))
+        if i % 4 == 0:
+            kind = str(rng.choice(["bf16", "f16"]))
+            out.append(("16bit", 300 + i, dict(M=M, N=N, K=K, kind=kind,
+                                               out=str(rng.choice(["f32", kind])),
+                                               block=(0, 0, 0), kmajor=bool(i % 8 == 4))))
+        elif i % 4 == 1:
+            out.append(("i8_i32", 300 + i, dict(M=M + 450, N=N, K=K, block=(0, 0, 0),
+                                                kmajor=bool(i % 8 == 5))))
+        elif i % 4 == 2:
+            out.append(("fp8_block", 300 + i, dict(M=M, N=N, K=K, out=str(rng.choice(["bf16", "f32"])),
+                                                   block=(0, 0, 0), kmajor=bool(i % 8 == 6))))
+        else:
+            fa, fb = [("e4m3", "e4m3"), ("e5m2", "e4m3")][(i // 4) % 2]
+            out.append(("fp8", 300 + i, dict(M=M, N=N, K=K, fa=fa, fb=fb, block=(0, 0, 0),
+                                             kmajor=bool(i % 8 == 7))))
     # K-major B in the scaled 8-bit dots (weights kept [N][K])
     for i in range(12):
         M = int(rng.integers(1, 65)) if i % 2 == 0 else int(rng.integers(65, 600))
