@@ -455,7 +455,9 @@ def bench_decode_f8(tx, dev, M, N, K, steps, warmup, flush, seed=5):
                 plan=plan_info(tx, p, split_k=p.split_k, grid=p.grid_x))
 
 
-def bench_fp8(tx, dev, M, N, K, steps, warmup, seed=5):
+def bench_fp8(tx, dev, M, N, K, steps, warmup, seed=5, kmajor=False):
+    """Config 4's block-scaled fp8 dot; kmajor: the weight kept [N][K] (B passed as its
+    transpose), the layout a model's linear layer stores."""
     import torch
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
@@ -466,11 +468,15 @@ def bench_fp8(tx, dev, M, N, K, steps, warmup, seed=5):
     sb = b.view(kb, 128, nb, 128).abs().amax(dim=(1, 3)) / 448.0
     qa = (a.view(M, kb, 128) / sa[:, :, None]).view(M, K).to(torch.float8_e4m3fn)
     qb = (b.view(kb, 128, nb, 128) / sb[:, None, :, None]).view(K, N).to(torch.float8_e4m3fn)
+    if kmajor:
+        qb = qb.t().contiguous().t()   # same values, K-major storage
     c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     run = Launcher(tx, qa, qb, c, sa.contiguous(), sb.contiguous(), tx.SCALE_BLOCK128)
+    assert bool(run.plan.desc.flags & tx.FLAG_B_KMAJOR) == kmajor
     ms = time_back_to_back(run, steps, warmup)
     flops = 2.0 * M * N * K
-    return dict(workload=f"fp8 e4m3 block-scaled {M}x{N}x{K}", ms=ms, tflops=flops / ms / 1e9,
+    return dict(workload=f"fp8 e4m3 block-scaled {M}x{N}x{K}" + (", B K-major" if kmajor else ""),
+                ms=ms, tflops=flops / ms / 1e9,
                 frac=flops / ms / 1e-3 / PEAK_I8, plan=plan_info(tx, run.plan))
 
 
@@ -1093,6 +1099,10 @@ def main():
             secondary.append(r)
             print(f"# {r['workload']}: {r['ms'] * 1e3:.1f} us, {r['tops']:.1f} T/s",
                   file=sys.stderr, flush=True)
+        r = bench_fp8(tx, dev, 2048, 7168, 7168, args.steps, args.warmup, kmajor=True)
+        secondary.append(r)
+        print(f"# {r['workload']}: {r['ms'] * 1e3:.1f} us, {r['tflops']:.1f} TFLOP/s",
+              file=sys.stderr, flush=True)
     flush = make_flush(dev)
     if want("tail"):
         for (m, n, k) in ((4096, 4096, 4000), (4000, 4000, 4000)):
