@@ -217,13 +217,15 @@ TX_API int tx_dot_launch(const tx_dot_plan *plan, const void *A, const void *B,
  * that cannot allocate device memory (code under HIP graph capture, serving
  * loops and harnesses that forbid hipMalloc).  It takes no workspace: the
  * scratch the planned kernels need (the decode kernels' split-K arrival
- * counters and their int32 or fp32 partials, the MX operand upcast to bf16)
- * lives in one
+ * counters and their int32 or fp32 partials, the MX operand upcast to bf16,
+ * the tiles' split-K partials) lives in one
  * static device array of TX_NOALLOC_SCRATCH_BYTES per GPU, held from the
  * library's load on that GPU until the process ends, and the call allocates
- * nothing.  A plan whose workspace does not fit (decode: more than
- * TX_NOALLOC_SCRATCH_BYTES; upcast: more than that less the 64 KiB counter
- * region, which the upcast never touches) returns TX_ERR_WORKSPACE.  Every
+ * nothing.  A split-K tile plan whose partials do not fit runs unsplit (the
+ * same dot: one K range a tile, fp32 sums in another order).  Any other plan
+ * whose workspace does not fit (decode: more than TX_NOALLOC_SCRATCH_BYTES;
+ * upcast: more than that less the 64 KiB counter region, which the upcast
+ * never touches) returns TX_ERR_WORKSPACE.  Every
  * call on one GPU shares that GPU's array, which keeps the last call's
  * contents: calls that may overlap in time on one GPU (different streams)
  * race on it.  The counters are zero when the library loads and every

@@ -195,6 +195,36 @@ def test_noalloc_kmajor_w8a8(gpu):
         assert np.array_equal(got, orc)
 
 
+def test_noalloc_split_k_tiles(gpu):
+    """Split-K on the 256x256 tiles through the shared scratch: partials that fit run split
+    (bit-equal to tx_dot_launch with a workspace); partials beyond the scratch (bf16
+    M = 256, N = K = 8192: 64 MiB) run unsplit, within fp32 summation error of the exact
+    product.  Then a W8A8 decode call on the same scratch."""
+    import torch
+    from dotcase import k_norm, normal_bf16
+    for M, N, K, fits in ((200, 1000, 4096, True), (256, 8192, 8192, False)):
+        say(f"noalloc split-K bf16 M={M} N={N} K={K}")
+        a, b = normal_bf16((M, K), k_norm(K), M), normal_bf16((K, N), k_norm(K), N)
+        da, db = to_device(a, gpu).view(torch.bfloat16), to_device(b, gpu).view(torch.bfloat16)
+        plan = tx.plan(tx.make_desc(M, N, K, tx.BF16, tx.F32, ldc=-(-N // 4) * 4))
+        assert plan.kernel == tx.KERNEL_GEMM_16BIT and plan.split_k > 1
+        assert (plan.workspace_bytes <= tx.NOALLOC_SCRATCH_BYTES) == fits
+        ldc = plan.desc.ldc
+        c_ref = torch.empty((M, ldc), dtype=torch.float32, device=gpu)
+        c_new = torch.full((M, ldc), float("nan"), dtype=torch.float32, device=gpu)
+        ws = torch.empty(int(plan.workspace_bytes), dtype=torch.uint8, device=gpu)
+        ws[:65536].zero_()
+        _launch("plain", plan, da, db, c_ref, None, None, ws)
+        _launch("noalloc", plan, da, db, c_new, None, None)
+        torch.cuda.synchronize()
+        ref, got = from_device(c_ref)[:, :N], from_device(c_new)[:, :N]
+        if fits:
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+        exact = oracle.bf16_to_f32(a).astype(np.float64) @ oracle.bf16_to_f32(b).astype(np.float64)
+        assert np.abs(got - exact).max() < 1e-5
+    _w8a8(gpu, 16, 4096, 4096, 91)
+
+
 def test_noalloc_workspace_free_kernels(gpu):
     """A plan without workspace (the bf16 tile) runs through the same entry point."""
     import torch

@@ -1273,6 +1273,19 @@ int launchPlanned(const tx_dot_plan *plan, const void *A, const void *B, void *C
   const int prc = checkPlan(*plan);
   if (prc != TX_OK)
     return prc;
+  // No allocation: a split-K tile plan whose partials do not fit the scratch
+  // runs unsplit (the same dot, one K range a tile).
+  tx_dot_plan unsplit;
+  if (noalloc && plan->split_k > 1 && plan->grid_y == plan->split_k &&
+      plan->workspace_bytes > (int64_t)TX_NOALLOC_SCRATCH_BYTES &&
+      (plan->kernel == TX_KERNEL_GEMM_16BIT || plan->kernel == TX_KERNEL_GEMM_I8 ||
+       plan->kernel == TX_KERNEL_GEMM_F8 || plan->kernel == TX_KERNEL_GEMM_MX_BF16)) {
+    unsplit = *plan;
+    unsplit.split_k = 1;
+    unsplit.grid_y = 1;
+    unsplit.workspace_bytes = gemmWorkspace(plan->desc, 1);
+    plan = &unsplit;
+  }
   if (noalloc && (plan->workspace_bytes < 0 ||
                   plan->workspace_bytes > (int64_t)TX_NOALLOC_SCRATCH_BYTES))
     return fail(TX_ERR_WORKSPACE,
