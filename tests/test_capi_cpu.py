@@ -181,11 +181,13 @@ def test_plan_validation():
     (64, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
     (128, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
     (256, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
-    (257, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
-    (512, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_DECODE_I8),
+    # past M = 256 the 8-bit tiles with split-K
+    (257, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_GEMM_I8),
+    (512, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_GEMM_I8),
     (513, 8192, 8192, tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_GEMM_I8),
     # plain int8 -> int32 of decode shape: the decode kernels' int32 epilogue
-    (300, 304, 256, tx.I8, tx.I32, 0, tx.KERNEL_DECODE_I8),
+    (200, 304, 256, tx.I8, tx.I32, 0, tx.KERNEL_DECODE_I8),
+    (300, 304, 256, tx.I8, tx.I32, 0, tx.KERNEL_GEMM_I8),
     (2, 8192, 8192, tx.I8, tx.I32, 0, tx.KERNEL_DECODE_I8),
     (16, 8192, 8192, tx.I8, tx.I32, 0, tx.KERNEL_DECODE_I8),
     (256, 8192, 8192, tx.I8, tx.I32, 0, tx.KERNEL_DECODE_I8),
@@ -336,7 +338,7 @@ def test_b_kmajor_plans():
         assert tx.plan(tx.make_desc(16, 300, 200, a, c, b_type=b, lda=208, ldb=208,
                                     block=(256, 256, 128), flags=tx.FLAG_B_KMAJOR)).kernel == kern
     # W8A8 and block-scaled fp8 (weights kept [N][K]): the 8-bit decode kernel at M <= 64;
-    # int8 (W8A8, int32) on the row kernel to M = 512; the 256 tile beyond
+    # int8 (W8A8, int32) on the row kernel to M = 256; the 256 tile beyond
     for a, c, sm, kern in ((tx.I8, tx.BF16, tx.SCALE_ROWCOL, tx.KERNEL_GEMM_I8),
                            (tx.I8, tx.I32, 0, tx.KERNEL_GEMM_I8),
                            (tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, tx.KERNEL_GEMM_F8),
@@ -345,9 +347,9 @@ def test_b_kmajor_plans():
         for M, want, blk in ((16, tx.KERNEL_DECODE_F8, (16, 128, 128)),
                              (100, tx.KERNEL_DECODE_I8 if i8 else kern,
                               (64, 128, 128) if i8 else (256, 256, 128)),
-                             (300, tx.KERNEL_DECODE_I8 if i8 else kern,
-                              (256, 128, 128) if i8 else (256, 256, 128)),
-                             (600, kern, (256, 256, 128))):
+                             (200, tx.KERNEL_DECODE_I8 if i8 else kern,
+                              (128, 128, 128) if i8 else (256, 256, 128)),
+                             (300, kern, (256, 256, 128)), (600, kern, (256, 256, 128))):
             p = tx.plan(tx.make_desc(M, 512, 512, a, c, scale_mode=sm, flags=tx.FLAG_B_KMAJOR))
             assert p.kernel == want and (p.desc.block_m, p.desc.block_n, p.desc.block_k) == blk
     # the K-interleaved int8 decode kernel (decode_i8.h) has no K-major form

@@ -61,7 +61,7 @@ def test_decode_int32_sums_exact(gpu, M):
 
 
 @pytest.mark.parametrize("M,N,K", [(16, 8191, 8191), (5, 1000, 4001), (48, 4100, 2000),
-                                   (100, 4100, 2000), (200, 260, 1000), (300, 304, 256),
+                                   (100, 4100, 2000), (200, 260, 1000), (250, 304, 256),
                                    (1, 24, 64), (3, 128, 1)])
 def test_decode_int32_ragged(gpu, M, N, K):
     """Ragged K and N (the masked K tail, the column quad that crosses N), both

@@ -210,7 +210,8 @@ def test_c4_w8a8_decode(gpu, M):
                                    (256, 8192, 1024), (300, 1024, 1040), (512, 8192, 2048)])
 def test_w8a8_decode_edges(gpu, M, N, K):
     """Decode shapes at the planner's tiles: waves splitting K up to M = 48, the row kernel's
-    slices of 64, 128 and 256 rows beyond (M = 49 .. 512)."""
+    slices of 64 and 128 rows beyond (M = 49 .. 256), the 256x256x128 tile with split-K past
+    it."""
     a, b, sa, sb, got = run_w8a8(gpu, M, N, K, seed=M)
     ref = oracle.tiled_dot(a, b, a_type=oracle.I8, c_type=oracle.BF16, block=(64, 64, 64),
                            scale_mode=oracle.SCALE_ROWCOL, sa=sa, sb=sb, round_mode=oracle.ROUND_RNE)

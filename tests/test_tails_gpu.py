@@ -354,12 +354,12 @@ def _kmajor_b(b, fill, gpu, tdtype=None, junk=None):
 def _kmajor_kernel(M, kernel, block, i8):
     """The kernel a K-major 8-bit plan takes: with the planner's choice the 8-bit decode
     kernel at M <= 64 (int8: M <= 48) and for int8 the row decode kernel beyond, to
-    M = 512; else the 256x256x128 tile (`kernel`)."""
+    M = 256; else the 256x256x128 tile (`kernel`)."""
     if block != (0, 0, 0):
         return kernel
     if M <= (48 if i8 else 64):
         return tx.KERNEL_DECODE_F8
-    return tx.KERNEL_DECODE_I8 if i8 and M <= 512 else kernel
+    return tx.KERNEL_DECODE_I8 if i8 and M <= 256 else kernel
 
 
 def _assert_kmajor_plan(da, db, c, kernel, block=(0, 0, 0), scale_mode=0):
@@ -386,7 +386,7 @@ def test_int8_ragged_kmajor_b(gpu, M, N, K, block):
     past N hold random bytes, as do A's.  The chunk that crosses K is loaded whole on both
     sides, so both are zeroed past K (junk times junk is not zero).  Bit-exact, on the
     256x256x128 tile and, with the planner's choice, the 8-bit decode kernel (M <= 48) and
-    the row decode kernel (48 < M <= 512)."""
+    the row decode kernel (48 < M <= 256)."""
     import torch
     say(f"tails int8 K-major B M={M} N={N} K={K} block={block}")
     a, b = uniform_i8((M, K), 81), uniform_i8((K, N), 82)
@@ -515,8 +515,8 @@ def test_8bit_kmajor_decode_accumulate(gpu, kind, M):
     (65, 130, 129, (0, 0, 0)), (700, 300, 200, (0, 0, 0)), (100, 300, 200, (256, 256, 128))])
 def test_w8a8_kmajor_b(gpu, M, N, K, block):
     """W8A8 with the weight kept [N][K] (B a transposed view of junk-padded storage): the
-    8-bit decode kernel's int8 form at M <= 48, the row decode kernel to M = 512 (slices of
-    64, 128, 256 rows), the 256x256x128 tile beyond or by name.  Bit-exact against the
+    8-bit decode kernel's int8 form at M <= 48, the row decode kernel to M = 256 (slices of
+    64 and 128 rows), the 256x256x128 tile (split-K) beyond or by name.  Bit-exact against the
     oracle (the same int32 sums and fp32 epilogue order)."""
     import torch
     say(f"tails W8A8 K-major B M={M} N={N} K={K} block={block}")

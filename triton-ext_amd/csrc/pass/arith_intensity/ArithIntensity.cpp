@@ -255,14 +255,10 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
       t = kTiles16[0]; // the K-major B kernel exists for this tile only
     else if (sa == 2)
       t = chooseTile(kTiles16, d->M, d->N, d->K, kPeak16 / 2 / kCUs, first);
-    else if (decode && d->M > 256 && d->M <= 512)
-      // W8A8 past the decode sizes, up to M = 512: the row-parallel decode
-      // kernel's slices of 256 rows (measured at N = K = 8192: M = 384 62.3 us,
-      // 512 63.8, against 98.0 and 99.3 on the 8-bit tiles; at 768 113.2
-      // against 110.4, so larger M stays on the tiles)
-      t = Tile{256, 128, 128, 1.0};
     else if (decode && d->M <= 256)
-      // W8A8 decode (M <= 256, N up to its 4096 column strips), 128-column
+      // W8A8 decode (M <= 256, N up to its 4096 column strips; past it the
+      // 8-bit tiles with split-K: at N = K = 8192 M = 384 57.5 us, 512 63.9,
+      // against 76.0 and 78.7 for the row kernel's slices of 256), 128-column
       // strips.  Up to M = 48 one row slice and 64-row K batches split among
       // the waves; beyond, row slices whose waves all take every 128-row K
       // batch: of 64 rows up to M = 128, of 128 past it.  Measured at
