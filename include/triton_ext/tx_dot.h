@@ -118,7 +118,7 @@ typedef enum tx_kernel {
   TX_KERNEL_GEMM_MX = 5,    /* MX fp8 / fp4 tile, scaled MFMA 16x16x128 (e8m0)   */
   TX_KERNEL_GEMM_MX_BF16 = 6, /* MX x bf16: MX operand upcast to bf16 in the
                                * workspace, then the bf16 tile              */
-  TX_KERNEL_DECODE_16BIT = 7, /* bf16/fp16 decode shapes (M <= 64, no scales):
+  TX_KERNEL_DECODE_16BIT = 7, /* bf16/fp16 decode shapes (M <= 96, no scales):
                                * B streamed once, MFMA 16x16x32              */
   TX_KERNEL_DECODE_F8 = 8,    /* 8-bit decode shapes (M <= 64): fp8 unscaled or
                                * with 128-block scales, and int8 (int32 C or

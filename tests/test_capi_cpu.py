@@ -194,12 +194,14 @@ def test_plan_validation():
     (513, 8192, 8192, tx.I8, tx.I32, 0, tx.KERNEL_GEMM_I8),
     (4096, 4096, 4096, tx.I8, tx.I32, 0, tx.KERNEL_GEMM_I8),
     (2048, 7168, 7168, tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, tx.KERNEL_GEMM_F8),
-    # bf16 / fp16 of decode shape (M <= 64): the 16-bit decode kernel
+    # bf16 / fp16 of decode shape (M <= 96): the 16-bit decode kernel
     (1, 8192, 8192, tx.BF16, tx.BF16, 0, tx.KERNEL_DECODE_16BIT),
     (16, 8192, 8192, tx.BF16, tx.F32, 0, tx.KERNEL_DECODE_16BIT),
     (64, 4096, 4096, tx.F16, tx.F16, 0, tx.KERNEL_DECODE_16BIT),
     (33, 28672, 8192, tx.F16, tx.F32, 0, tx.KERNEL_DECODE_16BIT),
-    (65, 8192, 8192, tx.BF16, tx.BF16, 0, tx.KERNEL_GEMM_16BIT),
+    (80, 8192, 8192, tx.BF16, tx.BF16, 0, tx.KERNEL_DECODE_16BIT),
+    (96, 4096, 4096, tx.F16, tx.F32, 0, tx.KERNEL_DECODE_16BIT),
+    (97, 8192, 8192, tx.BF16, tx.BF16, 0, tx.KERNEL_GEMM_16BIT),
     # fp8 of decode shape: the fp8 decode kernel, unscaled (fp32 C) or block-scaled
     (16, 7168, 7168, tx.F8E4M3, tx.BF16, tx.SCALE_BLOCK128, tx.KERNEL_DECODE_F8),
     (1, 8192, 8192, tx.F8E4M3, tx.F32, 0, tx.KERNEL_DECODE_F8),
@@ -288,13 +290,15 @@ def test_decode16_plans():
                                 flags=tx.FLAG_B_KMAJOR | tx.FLAG_ACCUMULATE)).kernel == D16
     # mixed operand types: not this kernel
     assert _err(tx.make_desc(16, 4096, 4096, tx.BF16, tx.F16)) == tx.ERR_UNSUPPORTED
-    # an explicit GEMM tile at decode shape runs that tile; the decode block at M > 64 is refused
+    # an explicit GEMM tile at decode shape runs that tile; the decode block at M > 96 is refused
     assert tx.plan(tx.make_desc(16, 4096, 4096, tx.BF16, tx.BF16,
                                 block=(64, 64, 32))).kernel == tx.KERNEL_GEMM_16BIT
     assert tx.plan(tx.make_desc(16, 4096, 4096, tx.BF16, tx.BF16,
                                 block=(16, 64, 128))).kernel == D16
-    assert _err(tx.make_desc(80, 4096, 4096, tx.BF16, tx.BF16,
-                             block=(80, 64, 128))) == tx.ERR_UNSUPPORTED
+    assert tx.plan(tx.make_desc(80, 4096, 4096, tx.BF16, tx.BF16,
+                                block=(80, 64, 128))).kernel == D16
+    assert _err(tx.make_desc(112, 4096, 4096, tx.BF16, tx.BF16,
+                             block=(112, 64, 128))) == tx.ERR_UNSUPPORTED
     # tl.dot(a, b, acc) with an fp32 acc
     p = tx.plan(tx.make_desc(8, 1000, 3000, tx.BF16, tx.F32, flags=tx.FLAG_ACCUMULATE))
     assert p.kernel == D16 and p.split_k == 4 and p.grid_x == 16 * 4

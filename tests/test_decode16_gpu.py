@@ -1,6 +1,6 @@
 """The 16-bit decode kernel (decode16.h) against the oracle.
 
-bf16 / fp16 dots with M <= 64 stream B once on the decode kernel: 64-column
+bf16 / fp16 dots with M <= 96 stream B once on the decode kernel: 64-column
 strips, 128-row K batches, split-K with the fp32 partials summed in split
 order.  Parity is the north_star's fp bar: |d| <= 1e-3 + 1e-2 |ref| for inputs
 N(0,1)/sqrt(K), against the oracle at the plan's block; fp32 C is also held to
@@ -60,6 +60,9 @@ def exact(a, b, kind):
     # ragged: K and N that fill no 16-byte chunk, slices of 16 .. 64 rows, one split
     (33, 4100, 2050, "bf16", "bf16"), (7, 1000, 3000, "f16", "f32"), (3, 24, 64, "bf16", "f32"),
     (64, 61, 300, "f16", "f16"), (17, 130, 129, "bf16", "f32"), (50, 520, 127, "f16", "f32"),
+    # slices of 80 and 96 rows
+    (80, 8192, 8192, "bf16", "bf16"), (96, 4096, 4096, "f16", "f32"),
+    (90, 1000, 3000, "bf16", "f32"), (70, 61, 300, "f16", "f16"),
 ])
 def test_decode16_vs_oracle(gpu, M, N, K, kind, out_kind):
     say(f"decode16 {kind}->{out_kind} M={M} N={N} K={K}")
@@ -173,7 +176,8 @@ def test_decode16_after_w8a8_on_one_workspace(gpu):
 @pytest.mark.parametrize("M,N,K,kind,out_kind", [
     (16, 8192, 8192, "bf16", "f32"), (1, 4096, 4096, "f16", "f16"), (64, 1024, 2048, "bf16", "bf16"),
     (33, 4100, 2050, "bf16", "bf16"), (7, 1000, 3000, "f16", "f32"), (17, 130, 129, "bf16", "f32"),
-    (50, 520, 127, "f16", "f32"), (5, 61, 1, "bf16", "f32")])
+    (50, 520, 127, "f16", "f32"), (5, 61, 1, "bf16", "f32"), (96, 1024, 2048, "bf16", "bf16"),
+    (75, 520, 127, "f16", "f32")])
 def test_decode16_kmajor_b(gpu, M, N, K, kind, out_kind):
     """B K-major (q @ k.T at decode; a weight kept [N][K]): B stored [N][K'] whose columns
     past K and rows past N hold NaN (A's padding holds Inf), so the chunk that crosses K

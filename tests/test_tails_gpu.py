@@ -100,12 +100,12 @@ def test_16bit_ragged(gpu, M, N, K, kind, out, block):
 
 
 @pytest.mark.parametrize("M,N,K,block", [(300, 261, 203, (0, 0, 0)), (64, 50, 70, (256, 256, 64)),
-                                         (64, 50, 70, (0, 0, 0))])
+                                         (64, 50, 70, (0, 0, 0)), (90, 50, 70, (0, 0, 0))])
 def test_16bit_ragged_kmajor_b(gpu, M, N, K, block):
     """K-major B (q @ k.T): B's chunk that crosses K is zeroed in registers too, on the
-    256 tile and (M <= 64, the planner's choice) the decode kernel."""
+    256 tile and (M <= 96, the planner's choice) the decode kernel."""
     p = run16(gpu, M, N, K, "bf16", "f32", block=block, kmajor=True)
-    assert p.kernel == (tx.KERNEL_DECODE_16BIT if M <= 64 and block == (0, 0, 0)
+    assert p.kernel == (tx.KERNEL_DECODE_16BIT if M <= 96 and block == (0, 0, 0)
                         else tx.KERNEL_GEMM_16BIT)
 
 

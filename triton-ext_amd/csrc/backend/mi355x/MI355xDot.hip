@@ -226,18 +226,16 @@ const DecodeF8KernelFn kDecodeF8ScaledKernels[2][4] = {TX_DF8_SLICES(true, 0, 0,
                                                        TX_DF8_SLICES(true, 0, 0, true, false)};
 const DecodeF8KernelFn kDecodeI8KmajorKernels[4] = TX_DF8_SLICES(false, 0, 0, true, true);
 #undef TX_DF8_SLICES
-// The 16-bit decode kernel by [fp16 / bf16][slice of 16, 32, 48, 64 rows].
+// The 16-bit decode kernel by [B K-major][bf16][slice rows / 16 - 1], slices
+// of 16 .. 96 rows.
 typedef void (*Decode16KernelFn)(Decode16Args);
-// [B K-major][bf16][slice rows / 16 - 1]
-const Decode16KernelFn kDecode16Kernels[2][2][4] = {
-    {{decode16_kernel<16, false>, decode16_kernel<32, false>, decode16_kernel<48, false>,
-      decode16_kernel<64, false>},
-     {decode16_kernel<16, true>, decode16_kernel<32, true>, decode16_kernel<48, true>,
-      decode16_kernel<64, true>}},
-    {{decode16_kernel<16, false, true>, decode16_kernel<32, false, true>,
-      decode16_kernel<48, false, true>, decode16_kernel<64, false, true>},
-     {decode16_kernel<16, true, true>, decode16_kernel<32, true, true>,
-      decode16_kernel<48, true, true>, decode16_kernel<64, true, true>}}};
+#define TX_D16_SLICES(BF, BT)                                                                  \
+  {decode16_kernel<16, BF, BT>, decode16_kernel<32, BF, BT>, decode16_kernel<48, BF, BT>,      \
+   decode16_kernel<64, BF, BT>, decode16_kernel<80, BF, BT>, decode16_kernel<96, BF, BT>}
+const Decode16KernelFn kDecode16Kernels[2][2][kDec16MaxM / 16] = {
+    {TX_D16_SLICES(false, false), TX_D16_SLICES(true, false)},
+    {TX_D16_SLICES(false, true), TX_D16_SLICES(true, true)}};
+#undef TX_D16_SLICES
 
 // MFMA format code of an MX operand type (-1 if it has none).
 int mxFormat(int32_t t) {
@@ -439,7 +437,7 @@ int64_t decodeWorkspace(const tx_dot_desc &d, int ksplit) {
 
 // The 16-bit decode kernel (decode16.h): both operands bf16 or both fp16,
 // no scales, C in their type or fp32 (accumulating only into fp32, which
-// validate() enforces), B row-major or K-major, M <= 64 (one slice), one
+// validate() enforces), B row-major or K-major, M <= 96 (one slice), one
 // arrival counter of the fixed region per 64-column strip.
 int decode16Rows(const tx_dot_desc &d) { return (int)(16 * cdiv(d.M > 0 ? d.M : 1, 16)); }
 bool useDecode16(const tx_dot_desc &d) {

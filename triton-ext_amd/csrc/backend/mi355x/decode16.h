@@ -1,6 +1,6 @@
 // bf16 / fp16 small-M dot (decode shape) for gfx950:
 //   C[m][n] = sum_k A[m][k] * B[k][n]
-// with A [M,K] (M <= 64) and B [K,N] row-major, both bf16 or both fp16,
+// with A [M,K] (M <= 96) and B [K,N] row-major, both bf16 or both fp16,
 // fp32 accumulation, and C in the operands' type (rounded to nearest even)
 // or in fp32 (C = sum, or C += sum for tl.dot's acc).
 //
@@ -26,7 +26,8 @@
 //    block; lane i receives column i's 4 K-consecutive elements).  B's
 //    16-byte chunk c of row r sits at c ^ (r & 7).
 //  * Wave w owns columns 16 w .. 16 w + 15 of the strip for every row of the
-//    slice, so every wave has MFMA work at any M:
+//    slice (slices past 64 rows read tiles 4 .. T - 1 in a second block of
+//    LDS reads), so every wave has MFMA work at any M:
 //    v_mfma_f32_16x16x32_{bf16,f16} with the roles swapped (MFMA A := B
 //    columns, MFMA B := A rows), so lane l holds row 16 t + l % 16 at the 4
 //    consecutive columns 16 w + 4 (l / 16) .. +3.  No cross-wave reduction:
@@ -66,7 +67,7 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 
 constexpr int kDec16StripN = 64;                                   // columns: 128-byte rows
 constexpr int kDec16BatchK = 128;                                  // K rows a batch
-constexpr int kDec16MaxM = 64;                                     // one slice of 64 rows
+constexpr int kDec16MaxM = 96;                                     // one slice of 96 rows
 constexpr int64_t kDec16MaxStrips = kDecodeCounterBytes / 4;       // one counter per strip
 
 struct Decode16Args {
@@ -97,7 +98,7 @@ template <int SR> struct Decode16Cfg {
   static constexpr int B_LOADS = A_OFF / 1024 / kDecodeWaves;                  // 4
   static constexpr int A_LOADS = SR * kDec16BatchK * 2 / 1024 / kDecodeWaves; // SR / 16
   static constexpr int VPB = B_LOADS + A_LOADS;
-  static_assert(SR == 16 || SR == 32 || SR == 48 || SR == 64, "slices of 16 .. 64 rows");
+  static_assert(SR % 16 == 0 && SR >= 16 && SR <= kDec16MaxM, "slices of 16 .. 96 rows");
   static_assert(S >= 3 && (S - 2) * VPB <= 63, "ring depth; vmcnt is 6 bits");
 };
 
@@ -197,6 +198,39 @@ __device__ __forceinline__ void dec16_read_pair_kmajor(uint32_t b0, uint32_t b1,
 #undef TX_D16K_HEAD
 #undef TX_D16K_O
 #undef TX_D16K_T
+
+// The A fragments of row tiles 4 .. 4 + N - 1 of two K steps (slices past 64
+// rows): ds_read_b128 at a0 / a1 + 16 KiB, +4 KiB per tile.
+#define TX_D16M_T(t, off)                                                                  \
+  "ds_read_b128 %[p0" #t "], %[a0] offset:" #off "\n\tds_read_b128 %[p1" #t "], %[a1] offset:" #off \
+  "\n\t"
+#define TX_D16M_O(t) [p0##t] "=&v"(x[0][t]), [p1##t] "=&v"(x[1][t])
+#define TX_D16M_IN [a0] "v"(a0), [a1] "v"(a1)
+template <int N>
+__device__ __forceinline__ void dec16_read_more(uint32_t a0, uint32_t a1, i32x4_t (&x)[2][N]) {
+  if constexpr (N == 1)
+    asm volatile(TX_D16M_T(0, 16384) "s_waitcnt lgkmcnt(0)" : TX_D16M_O(0) : TX_D16M_IN : "memory");
+  else if constexpr (N == 2)
+    asm volatile(TX_D16M_T(0, 16384) TX_D16M_T(1, 20480) "s_waitcnt lgkmcnt(0)"
+                 : TX_D16M_O(0), TX_D16M_O(1)
+                 : TX_D16M_IN
+                 : "memory");
+  else if constexpr (N == 3)
+    asm volatile(TX_D16M_T(0, 16384) TX_D16M_T(1, 20480) TX_D16M_T(2, 24576)
+                 "s_waitcnt lgkmcnt(0)"
+                 : TX_D16M_O(0), TX_D16M_O(1), TX_D16M_O(2)
+                 : TX_D16M_IN
+                 : "memory");
+  else
+    asm volatile(TX_D16M_T(0, 16384) TX_D16M_T(1, 20480) TX_D16M_T(2, 24576)
+                 TX_D16M_T(3, 28672) "s_waitcnt lgkmcnt(0)"
+                 : TX_D16M_O(0), TX_D16M_O(1), TX_D16M_O(2), TX_D16M_O(3)
+                 : TX_D16M_IN
+                 : "memory");
+}
+#undef TX_D16M_IN
+#undef TX_D16M_O
+#undef TX_D16M_T
 
 template <bool BF>
 __device__ __forceinline__ f32x4_t mfma16x16x32(const i32x4_t &a, const i32x4_t &b,
@@ -337,18 +371,34 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode16_kernel(Decode16
     const int64_t k0 = (int64_t)b * kDec16BatchK;
 #pragma unroll
     for (int pr = 0; pr < 2; ++pr) {
+      constexpr int T4 = T < 4 ? T : 4; // tiles the first read block brings
       i32x4_t bq[2];
-      i32x4_t a[2][T];
+      i32x4_t a4[2][T4];
       if constexpr (BT) {
-        dec16_read_pair_kmajor<T>(base + bk_k[2 * pr], base + bk_k[2 * pr + 1],
-                                  base + a_k[2 * pr], base + a_k[2 * pr + 1], bq, a);
+        dec16_read_pair_kmajor<T4>(base + bk_k[2 * pr], base + bk_k[2 * pr + 1],
+                                   base + a_k[2 * pr], base + a_k[2 * pr + 1], bq, a4);
       } else {
         v2i_t lo[2], hi[2];
-        dec16_read_pair<T>(base + b_lo + pr * 8192, base + b_hi + pr * 8192,
-                           base + a_k[2 * pr], base + a_k[2 * pr + 1], lo, hi, a);
+        dec16_read_pair<T4>(base + b_lo + pr * 8192, base + b_hi + pr * 8192,
+                            base + a_k[2 * pr], base + a_k[2 * pr + 1], lo, hi, a4);
 #pragma unroll
         for (int h = 0; h < 2; ++h)
           bq[h] = i32x4_t{lo[h].x, lo[h].y, hi[h].x, hi[h].y};
+      }
+      i32x4_t a[2][T];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int t = 0; t < T4; ++t)
+          a[h][t] = a4[h][t];
+      if constexpr (T > 4) { // slices past 64 rows: tiles 4 .. T - 1
+        i32x4_t am[2][T - 4];
+        dec16_read_more<T - 4>(base + a_k[2 * pr], base + a_k[2 * pr + 1], am);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int t = 4; t < T; ++t)
+            a[h][t] = am[h][t - 4];
       }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {

@@ -220,12 +220,15 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
         ((d->scale_mode == TX_SCALE_ROWCOL && d->c_type == TX_BF16) ||
          (d->scale_mode == TX_SCALE_NONE && d->c_type == TX_I32));
     // The 16-bit decode kernel: both operands bf16 or both fp16, no scales,
-    // C in their type or fp32, B row-major or K-major, M <= 64, N up to its
-    // 16384 strips of 64 columns.  It streams B once with split-K.
+    // C in their type or fp32, B row-major or K-major, M <= 96, N up to its
+    // 16384 strips of 64 columns.  It streams B once with split-K.  Each wave
+    // reads every row of the slice from LDS, so its time grows with M: at
+    // N = K = 8192 bf16, M = 80 / 96 / 112 / 128 44.1 / 48.6 / 53.9 / 57.6 us
+    // against the 256 tile with split-K's 51.9 / 51.9 / 54.1 / 56.6.
     const bool decode16 =
         (d->a_type == TX_BF16 || d->a_type == TX_F16) && d->b_type == d->a_type &&
         d->scale_mode == TX_SCALE_NONE && (d->c_type == d->a_type || d->c_type == TX_F32) &&
-        d->M <= 64 && d->N <= (int64_t)16384 * 64;
+        d->M <= 96 && d->N <= (int64_t)16384 * 64;
     // The 8-bit ring decode kernel, B row-major or K-major: fp8 x fp8 with
     // fp32 C, e4m3 x e4m3 with 128-block scales and bf16 / fp32 C, M <= 64;
     // with B K-major also int8 -> int32 and W8A8, M <= 48 (the row kernel's
