@@ -59,9 +59,9 @@ def parse():
                          "w8a8_1, w8a8_16, w8a8_64, w8a8_256; w8a8 also runs i32_16, the unscaled "
                          "int8 -> int32 decode at M=16, and i32_16_kmajor, the same with B "
                          "K-major), w8a8_kmajor (or w8a8_kmajor_1, _16, _64, _256: W8A8 with the "
-                         "weight kept [N][K]), bf16_decode (or bf16_decode_1, _16, _64: "
+                         "weight kept [N][K]), bf16_decode (or bf16_decode_1, _16, _64, _96: "
                          "bf16 at N = K = 8192 on the 16-bit decode kernel; bf16_decode_kmajor, "
-                         "or _1, _16, _64: the same with B K-major), mid_m (or mid_m_bf16_128, _256, "
+                         "or _1, _16, _64, _96: the same with B K-major), mid_m (or mid_m_bf16_128, _256, "
                          "_512, mid_m_fp8_256: a few hundred rows on the split-K tiles), fp8_decode (or "
                          "fp8_decode_1, _16, _64: block-scaled e4m3 at N = K = 7168 on the fp8 "
                          "decode kernel), int8, fp8 (fp8u: the unscaled 4096^3 line only), kmajor (bf16 "
@@ -1207,7 +1207,8 @@ def main():
             secondary.append(r)
             print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s",
                   file=sys.stderr, flush=True)
-    for m, km in ((1, False), (16, False), (64, False), (1, True), (16, True), (64, True)):
+    for m, km in ((1, False), (16, False), (64, False), (96, False), (1, True), (16, True),
+                  (64, True), (96, True)):
         name = "bf16_decode_kmajor" if km else "bf16_decode"
         if want(name) or want(f"{name}_{m}"):
             r = bench_decode16(tx, dev, m, 8192, 8192, max(args.steps, 20), 3, flush, kmajor=km)
