@@ -237,16 +237,18 @@ def test_kernel_choice(M, N, K, a, c, sm, kernel):
         assert p.workspace_bytes == (65536 + p.split_k * strips * sr * 128 * 4
                                      if p.split_k > 1 else 0)
     if kernel == tx.KERNEL_DECODE_16BIT:
-        # the slice of 16 ceil(M / 16) rows x 64-column strips x 128-row K batches;
-        # strips x splits workgroups, at most one a CU (no split once the strips alone fill them)
+        # the slice of 16 ceil(M / 16) rows x strips of 64 columns (128 for slices of 32 .. 80
+        # rows, N >= 256) x 128-row K batches; strips x splits workgroups, at most one a CU (no
+        # split once the strips alone fill them)
         sr = 16 * -(-M // 16)
-        assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (sr, 64, 128)
-        strips = -(-N // 64)
+        w = 128 if 32 <= sr <= 80 and N >= 256 else 64
+        assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (sr, w, 128)
+        strips = -(-N // w)
         # (the largest split that keeps one workgroup a CU)
         assert p.grid_x == strips * p.split_k <= max(strips, 256) and p.block_threads == 256
         assert p.split_k == 1 if 2 * strips > 256 else 2 * strips * p.split_k > 256
-        # the 64 KiB counter region, then fp32 partials: [split][strip][sr x 64]
-        assert p.workspace_bytes == (65536 + p.split_k * strips * sr * 64 * 4
+        # the 64 KiB counter region, then fp32 partials: [split][strip][sr x w]
+        assert p.workspace_bytes == (65536 + p.split_k * strips * sr * w * 4
                                      if p.split_k > 1 else 0)
     assert (p.split_k & (p.split_k - 1)) == 0
 

@@ -1,7 +1,7 @@
 """The 16-bit decode kernel (decode16.h) against the oracle.
 
-bf16 / fp16 dots with M <= 96 stream B once on the decode kernel: 64-column
-strips, 128-row K batches, split-K with the fp32 partials summed in split
+bf16 / fp16 dots with M <= 96 stream B once on the decode kernel: strips of
+64 columns (128 for slices of 32 .. 80 rows), 128-row K batches, split-K with the fp32 partials summed in split
 order.  Parity is the north_star's fp bar: |d| <= 1e-3 + 1e-2 |ref| for inputs
 N(0,1)/sqrt(K), against the oracle at the plan's block; fp32 C is also held to
 the exact (float64) product within fp32 summation error.  Sums of fp32
@@ -232,3 +232,35 @@ def test_decode16_kmajor_b_accumulate_deterministic(gpu):
     assert np.abs(outs[0] - (exact(a, b, "bf16") + acc)).max() < 1e-5
     for o in outs[1:]:
         assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+
+
+@pytest.mark.parametrize("M,N,K,kind,out_kind,kmajor", [
+    (70, 1000, 3000, "bf16", "f32", False), (70, 1000, 3000, "f16", "f16", True),
+    (5, 136, 136, "bf16", "bf16", False), (33, 4104, 2056, "bf16", "f32", True),
+    (80, 8192, 8192, "f16", "f32", False), (64, 56, 304, "bf16", "f32", True),
+    (48, 200, 1000, "f16", "f32", False)])
+def test_decode16_strip_widths(gpu, M, N, K, kind, out_kind, kmajor):
+    """Strips of 64 and of 128 columns, named by explicit block, on ragged shapes (N past the
+    strip, K past the batch, rows past M), B row-major or K-major: each against the oracle and,
+    in fp32, against the exact product within fp32 summation error."""
+    import torch
+    say(f"decode16 strip widths {kind}->{out_kind} M={M} N={N} K={K} kmajor={kmajor}")
+    tdt = getattr(torch, TORCH_DT[kind])
+    odt = getattr(torch, TORCH_DT[out_kind])
+    a, b = operands(M, N, K, kind, 3 * M + N)
+    da = to_device(a, gpu).view(tdt)
+    db = (to_device(np.ascontiguousarray(b.T), gpu).view(tdt).t() if kmajor
+          else to_device(b, gpu).view(tdt))
+    sr = 16 * -(-M // 16)
+    for w in (64, 128):
+        c = tx.dot(da, db, out_dtype=odt, block=(sr, w, 128))
+        torch.cuda.synchronize()
+        p = tx.plan_for(da, db, tx.tx_type(c), block=(sr, w, 128), ldc=c.stride(0))
+        assert p.kernel == tx.KERNEL_DECODE_16BIT and p.desc.block_n == w
+        assert p.grid_x == -(-N // w) * p.split_k
+        got = from_device(c)
+        ref = as_f32(oracle_16bit(a, b, kind, out_kind, (sr, w, 128)), out_kind)
+        check_close(as_f32(got, out_kind), ref, atol=ATOL, rtol=RTOL,
+                    what=f"decode16 W={w} {M}x{N}x{K}")
+        if out_kind == "f32":
+            assert np.abs(got - exact(a, b, kind)).max() < 1e-5

@@ -236,6 +236,15 @@ const Decode16KernelFn kDecode16Kernels[2][2][kDec16MaxM / 16] = {
     {TX_D16_SLICES(false, false), TX_D16_SLICES(true, false)},
     {TX_D16_SLICES(false, true), TX_D16_SLICES(true, true)}};
 #undef TX_D16_SLICES
+// The same with strips of 128 columns, slices of 16 .. 80 rows.
+#define TX_D16W_SLICES(BF, BT)                                                                 \
+  {decode16_kernel<16, BF, BT, 128>, decode16_kernel<32, BF, BT, 128>,                         \
+   decode16_kernel<48, BF, BT, 128>, decode16_kernel<64, BF, BT, 128>,                         \
+   decode16_kernel<80, BF, BT, 128>}
+const Decode16KernelFn kDecode16WideKernels[2][2][kDec16WideMaxM / 16] = {
+    {TX_D16W_SLICES(false, false), TX_D16W_SLICES(true, false)},
+    {TX_D16W_SLICES(false, true), TX_D16W_SLICES(true, true)}};
+#undef TX_D16W_SLICES
 
 // MFMA format code of an MX operand type (-1 if it has none).
 int mxFormat(int32_t t) {
@@ -446,18 +455,19 @@ bool useDecode16(const tx_dot_desc &d) {
          d.M <= kDec16MaxM && cdiv(d.N, kDec16StripN) <= kDec16MaxStrips;
 }
 // Its tile as the arith_intensity pass names it: the slice (16 ceil(M / 16)
-// rows) x a 64-column strip x 128-row K batches.  (No 16-bit GEMM tile has
-// block_k 128.)
+// rows) x a strip of 64 columns (or of 128, for slices up to 80 rows) x
+// 128-row K batches.  (No 16-bit GEMM tile has block_k 128.)
 bool decode16Tile(const tx_dot_desc &d) {
-  return d.block_m == decode16Rows(d) && d.block_n == kDec16StripN &&
-         d.block_k == kDec16BatchK;
+  return d.block_m == decode16Rows(d) && d.block_k == kDec16BatchK &&
+         (d.block_n == kDec16StripN || (d.block_n == 128 && d.block_m <= kDec16WideMaxM));
 }
+int64_t decode16Strips(const tx_dot_desc &d) { return cdiv(d.N, d.block_n); }
 // Split-K factor: the largest power of two (<= kMaxSplit) with strips x
 // splits workgroups at most one per CU (one fits a CU's LDS; a second round
 // would run behind the first), each split with at least 4 batches of 128 K
 // rows, and every split owning one batch at least.
 int decode16Split(const tx_dot_desc &d) {
-  const int64_t strips = cdiv(d.N, kDec16StripN);
+  const int64_t strips = decode16Strips(d);
   const int64_t batches = cdiv(d.K, kDec16BatchK);
   int ks = 1;
   while (ks < (int)kMaxSplit && strips * ks * 2 <= 256 && batches / (ks * 2) >= 4)
@@ -470,7 +480,7 @@ int64_t decode16Workspace(const tx_dot_desc &d, int ksplit) {
   if (ksplit <= 1)
     return 0;
   return kDecodeCounterBytes +
-         ksplit * decode16_split_bytes(cdiv(d.N, kDec16StripN), decode16Rows(d));
+         ksplit * decode16_split_bytes(decode16Strips(d), decode16Rows(d), (int)d.block_n);
 }
 
 // The 8-bit ring decode kernel (decode_f8.h), B row-major or K-major: fp8 x
@@ -621,7 +631,7 @@ int txMi355xDotRun(tx_dot_plan *plan) {
     const int ks = decode16Split(d);
     plan->kernel = TX_KERNEL_DECODE_16BIT;
     plan->split_k = ks;
-    plan->grid_x = (int32_t)(cdiv(d.N, kDec16StripN) * ks);
+    plan->grid_x = (int32_t)(decode16Strips(d) * ks);
     plan->grid_y = plan->grid_z = 1;
     plan->block_threads = kDecodeWaves * 64;
     plan->workspace_bytes = decode16Workspace(d, ks);
@@ -1082,8 +1092,10 @@ int launchDecode16(const tx_dot_plan &plan, const void *A, const void *B, void *
   a.partials = need > 0 ? reinterpret_cast<float *>(static_cast<uint8_t *>(ws) +
                                                     kDecodeCounterBytes)
                         : nullptr;
-  const Decode16KernelFn fn = kDecode16Kernels[(d.flags & TX_FLAG_B_KMAJOR) != 0]
-                                               [d.a_type == TX_BF16][decode16Rows(d) / 16 - 1];
+  const int bt = (d.flags & TX_FLAG_B_KMAJOR) != 0, bf = d.a_type == TX_BF16,
+            slice = decode16Rows(d) / 16 - 1;
+  const Decode16KernelFn fn = d.block_n == 128 ? kDecode16WideKernels[bt][bf][slice]
+                                               : kDecode16Kernels[bt][bf][slice];
   hipLaunchKernelGGL(fn, dim3(plan.grid_x), dim3(plan.block_threads), 0, stream, a);
   TX_HIP_CHECK(hipGetLastError());
   return TX_OK;
@@ -1215,7 +1227,7 @@ int checkPlan(const tx_dot_plan &p) {
   if (p.kernel == TX_KERNEL_DECODE_16BIT) {
     const int sk = p.split_k;
     if (!useDecode16(d) || !decode16Tile(d) || sk < 1 || sk > (int)kMaxSplit ||
-        (sk & (sk - 1)) || p.grid_x != cdiv(d.N, kDec16StripN) * sk ||
+        (sk & (sk - 1)) || p.grid_x != decode16Strips(d) * sk ||
         p.block_threads != kDecodeWaves * 64 || p.workspace_bytes != decode16Workspace(d, sk))
       return fail(TX_ERR_INVALID, "the plan's decode launch does not follow from its descriptor");
     return TX_OK;

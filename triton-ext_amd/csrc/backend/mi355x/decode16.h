@@ -66,6 +66,7 @@ namespace txk {
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 
 constexpr int kDec16StripN = 64;                                   // columns: 128-byte rows
+constexpr int kDec16WideMaxM = 80; // strips of 128 columns: slices up to 80 rows (3 slots)
 constexpr int kDec16BatchK = 128;                                  // K rows a batch
 constexpr int kDec16MaxM = 96;                                     // one slice of 96 rows
 constexpr int64_t kDec16MaxStrips = kDecodeCounterBytes / 4;       // one counter per strip
@@ -85,14 +86,17 @@ struct Decode16Args {
   uint32_t *counters;     // [strips] arrival counters
 };
 
-// Bytes of one split's partials: every strip's SR x 64 fp32 sums.
-__host__ __device__ constexpr int64_t decode16_split_bytes(int64_t strips, int sr) {
-  return strips * sr * kDec16StripN * 4;
+// Bytes of one split's partials: every strip's SR x W fp32 sums.
+__host__ __device__ constexpr int64_t decode16_split_bytes(int64_t strips, int sr,
+                                                           int w = kDec16StripN) {
+  return strips * sr * w * 4;
 }
 
-template <int SR> struct Decode16Cfg {
+template <int SR, int W = kDec16StripN> struct Decode16Cfg {
+  static_assert(W == 64 || W == 128, "strips of 64 or 128 columns");
   static constexpr int T = SR / 16;                         // 16-row tiles
-  static constexpr int A_OFF = kDec16BatchK * 128;          // B's 16 KiB first
+  static constexpr int JB = W / 64;                         // 16-column blocks a wave
+  static constexpr int A_OFF = kDec16BatchK * 2 * W;        // B's batch first
   static constexpr int SLOT = A_OFF + SR * kDec16BatchK * 2; // then SR rows of 256 bytes
   static constexpr int S = 158 * 1024 / SLOT > 8 ? 8 : 158 * 1024 / SLOT;
   static constexpr int B_LOADS = A_OFF / 1024 / kDecodeWaves;                  // 4
@@ -260,10 +264,29 @@ __device__ __forceinline__ i32x4_t dec16_mask_k(const i32x4_t &v, int64_t k, int
   return i32x4_t{o[0], o[1], o[2], o[3]};
 }
 
-template <int SR, bool BF, bool BT = false>
+// B-only reads of two K steps for a wave's second column block (strips of
+// 128 columns): row-major, transposed reads at blo / bhi and +4 KiB;
+// K-major, ds_read_b128 at b0 / b1.
+__device__ __forceinline__ void dec16_read_b_pair(uint32_t blo, uint32_t bhi, v2i_t (&lo)[2],
+                                                  v2i_t (&hi)[2]) {
+  asm volatile("ds_read_b64_tr_b16 %0, %[blo]\n\tds_read_b64_tr_b16 %1, %[bhi]\n\t"
+               "ds_read_b64_tr_b16 %2, %[blo] offset:4096\n\t"
+               "ds_read_b64_tr_b16 %3, %[bhi] offset:4096\n\ts_waitcnt lgkmcnt(0)"
+               : "=&v"(lo[0]), "=&v"(hi[0]), "=&v"(lo[1]), "=&v"(hi[1])
+               : [blo] "v"(blo), [bhi] "v"(bhi)
+               : "memory");
+}
+__device__ __forceinline__ void dec16_read_bk_pair(uint32_t b0, uint32_t b1, i32x4_t (&bq)[2]) {
+  asm volatile("ds_read_b128 %0, %[b0]\n\tds_read_b128 %1, %[b1]\n\ts_waitcnt lgkmcnt(0)"
+               : "=&v"(bq[0]), "=&v"(bq[1])
+               : [b0] "v"(b0), [b1] "v"(b1)
+               : "memory");
+}
+
+template <int SR, bool BF, bool BT = false, int W = kDec16StripN>
 __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode16_kernel(Decode16Args p) {
-  typedef Decode16Cfg<SR> Cfg;
-  constexpr int S = Cfg::S, SLOT = Cfg::SLOT, T = Cfg::T;
+  typedef Decode16Cfg<SR, W> Cfg;
+  constexpr int S = Cfg::S, SLOT = Cfg::SLOT, T = Cfg::T, JB = Cfg::JB;
   __shared__ __attribute__((aligned(1024))) uint8_t ring[S * SLOT];
   __shared__ uint32_t last_flag;
 
@@ -273,10 +296,10 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode16_kernel(Decode16
   // Workgroup -> (strip, split): consecutive workgroups are adjacent strips
   // of one split, so the workgroups running at once read whole stretches of
   // B's rows.
-  const int strips = (p.N + kDec16StripN - 1) / kDec16StripN;
+  const int strips = (p.N + W - 1) / W;
   const int strip = blockIdx.x % strips, split = blockIdx.x / strips;
-  const int64_t n0 = (int64_t)strip * kDec16StripN;
-  const bool n_edge = n0 + kDec16StripN > p.N;
+  const int64_t n0 = (int64_t)strip * W;
+  const bool n_edge = n0 + W > p.N;
 
   const int total_batches = (p.K + kDec16BatchK - 1) / kDec16BatchK;
   const int b_begin = split * p.batches_per_split;
@@ -321,9 +344,11 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode16_kernel(Decode16
         if (mask && (!live || n >= p.N || k >= p.K))
           src = tx_zero_chunk;
       } else {
-        const int row = 8 * q + (lane >> 3);
+        // Strips of 128 columns: load q >= 16 fills the second 16 KiB, the
+        // batch's columns 64 .. 127 in the same layout.
+        const int row = 8 * (q & 15) + (lane >> 3);
         const int c = (lane & 7) ^ (row & 7);
-        const int64_t k = k0 + row, n = n0 + 8 * c;
+        const int64_t k = k0 + row, n = n0 + 64 * (q >> 4) + 8 * c;
         src = p.B + k * p.ldb + n;
         if (mask && (!live || k >= p.K || n >= p.N))
           src = tx_zero_chunk;
@@ -343,25 +368,37 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode16_kernel(Decode16
     }
   };
 
-  f32x4_t acc[T];
+  f32x4_t acc[JB][T]; // [column block][row tile]
 #pragma unroll
-  for (int t = 0; t < T; ++t)
-    acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int jj = 0; jj < JB; ++jj)
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      acc[jj][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // Per-lane LDS offsets within a slot.  B, K step ks: rows 32 ks + 8 G +
   // L / 4 (lo) and +4 (hi), columns 16 wave + 4 (L % 4) .. +3, i.e. chunk
   // 2 wave + (L % 4) / 2, byte 8 (L % 2); the swizzle takes row & 7, which
   // is L / 4 for lo and L / 4 + 4 for hi in every step, so a step is +4 KiB.
   // A, step ks, tile t: row 16 t + L, chunk (4 ks + G) ^ L: +4 KiB per tile.
-  const int cb = 2 * wave + ((L & 3) >> 1);
-  const uint32_t b_lo = (L >> 2) * 128 + ((cb ^ (L >> 2)) << 4) + 8 * (L & 1) + 8 * G * 128;
-  const uint32_t b_hi = b_lo + 4 * 128 - ((cb ^ (L >> 2)) << 4) + ((cb ^ ((L >> 2) + 4)) << 4);
-  // K-major B, step ks: storage row 16 wave + L, chunk (4 ks + G) ^ L.
-  uint32_t a_k[4], bk_k[4];
+  // Column block jj of the wave is block J = JB wave + jj of the strip: in
+  // row-major B, the 16 KiB half J / 4 and there block J % 4.
+  uint32_t b_lo[JB], b_hi[JB];
+#pragma unroll
+  for (int jj = 0; jj < JB; ++jj) {
+    const int J = JB * wave + jj;
+    const int cb = 2 * (J & 3) + ((L & 3) >> 1);
+    b_lo[jj] = (J >> 2) * 16384 + (L >> 2) * 128 + ((cb ^ (L >> 2)) << 4) + 8 * (L & 1) +
+               8 * G * 128;
+    b_hi[jj] = b_lo[jj] + 4 * 128 - ((cb ^ (L >> 2)) << 4) + ((cb ^ ((L >> 2) + 4)) << 4);
+  }
+  // K-major B, step ks: storage row 16 J + L, chunk (4 ks + G) ^ L.
+  uint32_t a_k[4], bk_k[JB][4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     a_k[ks] = Cfg::A_OFF + L * 256 + (((4 * ks + G) ^ L) << 4);
-    bk_k[ks] = (16 * wave + L) * 256 + (((4 * ks + G) ^ L) << 4);
+#pragma unroll
+    for (int jj = 0; jj < JB; ++jj)
+      bk_k[jj][ks] = (16 * (JB * wave + jj) + L) * 256 + (((4 * ks + G) ^ L) << 4);
   }
 
   auto consume = [&](const uint8_t *slot, int i) {
@@ -372,18 +409,25 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode16_kernel(Decode16
 #pragma unroll
     for (int pr = 0; pr < 2; ++pr) {
       constexpr int T4 = T < 4 ? T : 4; // tiles the first read block brings
-      i32x4_t bq[2];
+      i32x4_t bq[JB][2];
       i32x4_t a4[2][T4];
       if constexpr (BT) {
-        dec16_read_pair_kmajor<T4>(base + bk_k[2 * pr], base + bk_k[2 * pr + 1],
-                                   base + a_k[2 * pr], base + a_k[2 * pr + 1], bq, a4);
+        dec16_read_pair_kmajor<T4>(base + bk_k[0][2 * pr], base + bk_k[0][2 * pr + 1],
+                                   base + a_k[2 * pr], base + a_k[2 * pr + 1], bq[0], a4);
+        if constexpr (JB == 2)
+          dec16_read_bk_pair(base + bk_k[1][2 * pr], base + bk_k[1][2 * pr + 1], bq[1]);
       } else {
-        v2i_t lo[2], hi[2];
-        dec16_read_pair<T4>(base + b_lo + pr * 8192, base + b_hi + pr * 8192,
-                            base + a_k[2 * pr], base + a_k[2 * pr + 1], lo, hi, a4);
+        v2i_t lo[JB][2], hi[JB][2];
+        dec16_read_pair<T4>(base + b_lo[0] + pr * 8192, base + b_hi[0] + pr * 8192,
+                            base + a_k[2 * pr], base + a_k[2 * pr + 1], lo[0], hi[0], a4);
+        if constexpr (JB == 2)
+          dec16_read_b_pair(base + b_lo[1] + pr * 8192, base + b_hi[1] + pr * 8192, lo[1],
+                            hi[1]);
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-          bq[h] = i32x4_t{lo[h].x, lo[h].y, hi[h].x, hi[h].y};
+        for (int jj = 0; jj < JB; ++jj)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            bq[jj][h] = i32x4_t{lo[jj][h].x, lo[jj][h].y, hi[jj][h].x, hi[jj][h].y};
       }
       i32x4_t a[2][T];
 #pragma unroll
@@ -402,18 +446,26 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode16_kernel(Decode16
       }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        i32x4_t bf = bq[h];
+        i32x4_t bf[JB];
+#pragma unroll
+        for (int jj = 0; jj < JB; ++jj)
+          bf[jj] = bq[jj][h];
         if (tail) {
           const int64_t k = k0 + 32 * (2 * pr + h) + 8 * G;
 #pragma unroll
           for (int t = 0; t < T; ++t)
             a[h][t] = dec16_mask_k(a[h][t], k, p.K);
-          if constexpr (BT)
-            bf = dec16_mask_k(bf, k, p.K);
+          if constexpr (BT) {
+#pragma unroll
+            for (int jj = 0; jj < JB; ++jj)
+              bf[jj] = dec16_mask_k(bf[jj], k, p.K);
+          }
         }
 #pragma unroll
-        for (int t = 0; t < T; ++t)
-          acc[t] = mfma16x16x32<BF>(bf, a[h][t], acc[t]);
+        for (int jj = 0; jj < JB; ++jj)
+#pragma unroll
+          for (int t = 0; t < T; ++t)
+            acc[jj][t] = mfma16x16x32<BF>(bf[jj], a[h][t], acc[jj][t]);
       }
     }
   };
@@ -442,11 +494,11 @@ __global__ void __launch_bounds__(kDecodeWaves * 64, 1) decode16_kernel(Decode16
 k_loop_done:
   __builtin_amdgcn_s_waitcnt(0); // the zero-chunk loads past nb have landed
 
-  // C for this lane: row 16 t + L, columns n0 + 16 wave + 4 G .. +3 (one
-  // 8-byte store in 16-bit C, 16 bytes in fp32; single elements where the
-  // quad crosses N).
-  const int64_t col = n0 + 16 * wave + 4 * G;
-  auto epilogue = [&](const f32x4_t (&sum)[T]) {
+  // C for this lane and column block jj: row 16 t + L, columns
+  // n0 + 16 (JB wave + jj) + 4 G .. +3 (one 8-byte store in 16-bit C, 16
+  // bytes in fp32; single elements where the quad crosses N).
+  auto epilogue = [&](const f32x4_t (&sum)[T], int jj) {
+    const int64_t col = n0 + 16 * (JB * wave + jj) + 4 * G;
     if (col >= p.N)
       return;
 #pragma unroll
@@ -485,7 +537,9 @@ k_loop_done:
     }
   };
   if (p.ksplit == 1) {
-    epilogue(acc);
+#pragma unroll
+    for (int jj = 0; jj < JB; ++jj)
+      epilogue(acc[jj], jj);
     return;
   }
 
@@ -495,19 +549,23 @@ k_loop_done:
   // is acknowledged before the barrier that precedes the counter increment;
   // the last workgroup loads only after its increment has returned).
   constexpr int kSC1 = 16;
-  const int64_t split_bytes = decode16_split_bytes(strips, SR);
+  const int64_t split_bytes = decode16_split_bytes(strips, SR, W);
   auto part_rsrc = [&](int q) {
     return __builtin_amdgcn_make_buffer_rsrc(
         reinterpret_cast<uint8_t *>(p.partials) + (int64_t)q * split_bytes, 0, (int)split_bytes,
         0x00020000);
   };
-  const int blk0 = (strip * kDecodeWaves + wave) * T; // 1 KiB blocks, in lane order
+  // 1 KiB blocks in lane order: column block jj, row tile t at blk0 + jj T + t.
+  const int blk0 = (strip * kDecodeWaves + wave) * JB * T;
   {
     const auto mine = part_rsrc(split);
 #pragma unroll
-    for (int t = 0; t < T; ++t)
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i_t, acc[t]), mine,
-                                             ((blk0 + t) << 10) + 16 * lane, 0, kSC1);
+    for (int jj = 0; jj < JB; ++jj)
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i_t, acc[jj][t]), mine,
+                                               ((blk0 + jj * T + t) << 10) + 16 * lane, 0,
+                                               kSC1);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -525,30 +583,39 @@ k_loop_done:
     return;
   // Last arrival: sum = partial 0 + partial 1 + .. in split order, its own
   // from registers; NQ splits' loads in flight before any is used.
-  f32x4_t sum[T];
+  f32x4_t sum[JB][T];
 #pragma unroll
-  for (int t = 0; t < T; ++t)
-    sum[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  constexpr int NQ = 4;
+  for (int jj = 0; jj < JB; ++jj)
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      sum[jj][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  constexpr int NQ = 4 / JB;
   for (int q0 = 0; q0 < p.ksplit; q0 += NQ) {
-    v4i_t v[NQ][T];
+    v4i_t v[NQ][JB][T];
 #pragma unroll
     for (int qq = 0; qq < NQ; ++qq)
       if (q0 + qq < p.ksplit && q0 + qq != split) {
         const auto r = part_rsrc(q0 + qq);
 #pragma unroll
-        for (int t = 0; t < T; ++t)
-          v[qq][t] = __builtin_amdgcn_raw_buffer_load_b128(r, ((blk0 + t) << 10) + 16 * lane, 0,
-                                                           kSC1);
+        for (int jj = 0; jj < JB; ++jj)
+#pragma unroll
+          for (int t = 0; t < T; ++t)
+            v[qq][jj][t] = __builtin_amdgcn_raw_buffer_load_b128(
+                r, ((blk0 + jj * T + t) << 10) + 16 * lane, 0, kSC1);
       }
 #pragma unroll
     for (int qq = 0; qq < NQ; ++qq)
       if (q0 + qq < p.ksplit)
 #pragma unroll
-        for (int t = 0; t < T; ++t)
-          sum[t] += q0 + qq == split ? acc[t] : __builtin_bit_cast(f32x4_t, v[qq][t]);
+        for (int jj = 0; jj < JB; ++jj)
+#pragma unroll
+          for (int t = 0; t < T; ++t)
+            sum[jj][t] +=
+                q0 + qq == split ? acc[jj][t] : __builtin_bit_cast(f32x4_t, v[qq][jj][t]);
   }
-  epilogue(sum);
+#pragma unroll
+  for (int jj = 0; jj < JB; ++jj)
+    epilogue(sum[jj], jj);
 }
 
 } // namespace txk

@@ -252,8 +252,15 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
       t = ba == 4 ? kTileMx4 : kTileMx8;
     else if (decode_f8)
       t = Tile{(int32_t)(16 * cdiv(d->M > 0 ? d->M : 1, 16)), 128, 128, 1.0};
-    else if (decode16)
-      t = Tile{(int32_t)(16 * cdiv(d->M > 0 ? d->M : 1, 16)), 64, 128, 1.0};
+    else if (decode16) {
+      // Every strip reads all of A, so A's re-reads are M / W of B's bytes.
+      // Strips of W = 128 columns halve them: at N = K = 8192 bf16 M = 48 / 64
+      // / 80 32.0 / 35.2 / 38.9 us against 35.1 / 40.7 / 46.2 with 64 (B
+      // K-major: M = 32 28.2 against 31.8), equal at M = 16.  Their ring holds
+      // slices up to 80 rows.
+      const int32_t rows = (int32_t)(16 * cdiv(d->M > 0 ? d->M : 1, 16));
+      t = Tile{rows, rows >= 32 && rows <= 80 && d->N >= 256 ? 128 : 64, 128, 1.0};
+    }
     else if (sa == 2 && (d->flags & TX_FLAG_B_KMAJOR))
       t = kTiles16[0]; // the K-major B kernel exists for this tile only
     else if (sa == 2)
