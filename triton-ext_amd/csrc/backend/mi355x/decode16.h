@@ -55,6 +55,14 @@
 // A's.  Each strip starts its split's batches at its own batch (strip mod the
 // split's batch count), so its fp32 sums can differ from the row-major form's
 // in the last bits.
+//
+// W = 128: strips of 128 columns, for slices up to 80 rows (three slots of
+// 32 KiB of B and the slice's A rows fit the LDS).  Every strip reads all of
+// A, so A's re-reads are M / W of B's bytes, and wider strips halve them.
+// The batch's B is stored as two 64-column halves in the layout above, and
+// wave w owns 16-column blocks 2 w and 2 w + 1 (the second block's B
+// fragments read in a block of their own); in K-major B, storage rows
+// 32 w .. 32 w + 31.
 #pragma once
 
 #include <type_traits>
