@@ -61,7 +61,8 @@ def parse():
                          "K-major), w8a8_kmajor (or w8a8_kmajor_1, _16, _64, _256: W8A8 with the "
                          "weight kept [N][K]), bf16_decode (or bf16_decode_1, _16, _64, _96: "
                          "bf16 at N = K = 8192 on the 16-bit decode kernel; bf16_decode_kmajor, "
-                         "or _1, _16, _64, _96: the same with B K-major), mid_m (or mid_m_bf16_128, _256, "
+                         "or _1, _16, _64, _96: the same with B K-major), decode16_widths (not in the "
+                         "default run: bf16 M = 16 .. 80 with strips of 64 and of 128 columns), mid_m (or mid_m_bf16_128, _256, "
                          "_512, mid_m_fp8_256: a few hundred rows on the split-K tiles), fp8_decode (or "
                          "fp8_decode_1, _16, _64: block-scaled e4m3 at N = K = 7168 on the fp8 "
                          "decode kernel), int8, fp8 (fp8u: the unscaled 4096^3 line only), kmajor (bf16 "
@@ -418,6 +419,28 @@ def bench_mid_m(tx, dev, kind, M, N, K, flush, seed=7):
     return dict(workload=what + ", split-K", ms=ms, tflops=2.0 * M * N * K / ms / 1e9,
                 ms_vendor=vendor,
                 plan=plan_info(tx, p, split_k=p.split_k, grid=[p.grid_x, p.grid_y]))
+
+
+def bench_decode16_widths(tx, dev, flush, N=8192, K=8192, seed=7):
+    """The 16-bit decode kernel with strips of 64 and of 128 columns named by explicit block,
+    bf16, B row-major and K-major, M = 16 .. 80, cold in a stream."""
+    import torch
+    out = []
+    for kmajor in (False, True):
+        for M in (16, 32, 48, 64, 80):
+            a, b = bf16_inputs(M, N, K, dev, seed)
+            if kmajor:
+                b = b.t().contiguous().t()
+            c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            sr = 16 * -(-M // 16)
+            ms = {}
+            for w in (64, 128):
+                run = Launcher(tx, a, b, c, block=(sr, w, 128))
+                ms[w] = time_cold_in_stream(run, flush)
+            out.append(dict(workload=f"bf16 decode M={M} N={N} K={K}"
+                            + (", B K-major" if kmajor else "") + ", strips of 64 / 128 columns",
+                            ms_w64=ms[64], ms_w128=ms[128]))
+    return out
 
 
 def fp8_block_inputs_dev(M, N, K, dev, seed):
@@ -1216,6 +1239,11 @@ def main():
             print(f"# {r['workload']}: {r['ms'] * 1e3:.2f} us in stream, {r['gbps']:.0f} GB/s "
                   f"({100 * r['frac_hbm']:.1f}% HBM); isolated launch "
                   f"{r['ms_isolated'] * 1e3:.2f} us", file=sys.stderr, flush=True)
+    if only and "decode16_widths" in only:
+        for r in bench_decode16_widths(tx, dev, flush):
+            secondary.append(r)
+            print(f"# {r['workload']}: {r['ms_w64'] * 1e3:.1f} / {r['ms_w128'] * 1e3:.1f} us in "
+                  f"stream", file=sys.stderr, flush=True)
     for kind, m, n in (("bf16", 128, 8192), ("bf16", 256, 8192), ("bf16", 512, 8192),
                        ("fp8", 256, 7168)):
         if want("mid_m") or want(f"mid_m_{kind}_{m}"):

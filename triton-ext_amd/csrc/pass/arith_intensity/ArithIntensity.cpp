@@ -255,8 +255,8 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
     else if (decode16) {
       // Every strip reads all of A, so A's re-reads are M / W of B's bytes.
       // Strips of W = 128 columns halve them: at N = K = 8192 bf16 M = 48 / 64
-      // / 80 32.0 / 35.2 / 38.9 us against 35.1 / 40.7 / 46.2 with 64 (B
-      // K-major: M = 32 28.2 against 31.8), equal at M = 16.  Their ring holds
+      // / 80 31.6 / 34.2 / 37.8 us against 34.9 / 39.9 / 45.3 with 64 (B
+      // K-major: M = 32 28.0 against 31.8), equal at M = 16.  Their ring holds
       // slices up to 80 rows.
       const int32_t rows = (int32_t)(16 * cdiv(d->M > 0 ? d->M : 1, 16));
       t = Tile{rows, rows >= 32 && rows <= 80 && d->N >= 256 ? 128 : 64, 128, 1.0};
