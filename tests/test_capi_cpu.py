@@ -238,10 +238,10 @@ def test_kernel_choice(M, N, K, a, c, sm, kernel):
                                      if p.split_k > 1 else 0)
     if kernel == tx.KERNEL_DECODE_16BIT:
         # the slice of 16 ceil(M / 16) rows x strips of 64 columns (128 for slices of 32 .. 80
-        # rows, N >= 256) x 128-row K batches; strips x splits workgroups, at most one a CU (no
-        # split once the strips alone fill them)
+        # rows with N K >= 2^25) x 128-row K batches; strips x splits workgroups, at most one a
+        # CU (no split once the strips alone fill them)
         sr = 16 * -(-M // 16)
-        w = 128 if 32 <= sr <= 80 and N >= 256 else 64
+        w = 128 if 32 <= sr <= 80 and N * K >= 1 << 25 else 64
         assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (sr, w, 128)
         strips = -(-N // w)
         # (the largest split that keeps one workgroup a CU)
