@@ -62,7 +62,8 @@ def parse():
                          "weight kept [N][K]), bf16_decode (or bf16_decode_1, _16, _64, _96: "
                          "bf16 at N = K = 8192 on the 16-bit decode kernel; bf16_decode_kmajor, "
                          "or _1, _16, _64, _96: the same with B K-major), decode16_widths (not in the "
-                         "default run: bf16 M = 16 .. 80 with strips of 64 and of 128 columns), mid_m (or mid_m_bf16_128, _256, "
+                         "default run: bf16 with strips of 64 and of 128 columns, M = 16 .. 80 and a sweep "
+                         "of N and K at M = 64), mid_m (or mid_m_bf16_128, _256, "
                          "_512, mid_m_fp8_256: a few hundred rows on the split-K tiles), fp8_decode (or "
                          "fp8_decode_1, _16, _64: block-scaled e4m3 at N = K = 7168 on the fp8 "
                          "decode kernel), int8, fp8 (fp8u: the unscaled 4096^3 line only), kmajor (bf16 "
@@ -421,25 +422,29 @@ def bench_mid_m(tx, dev, kind, M, N, K, flush, seed=7):
                 plan=plan_info(tx, p, split_k=p.split_k, grid=[p.grid_x, p.grid_y]))
 
 
-def bench_decode16_widths(tx, dev, flush, N=8192, K=8192, seed=7):
+def bench_decode16_widths(tx, dev, flush, seed=7):
     """The 16-bit decode kernel with strips of 64 and of 128 columns named by explicit block,
-    bf16, B row-major and K-major, M = 16 .. 80, cold in a stream."""
+    bf16, cold in a stream: N = K = 8192 at M = 16 .. 80 with B row-major and K-major, then
+    M = 64 over B from 2^23 to 2^28 elements (B row-major)."""
     import torch
     out = []
-    for kmajor in (False, True):
-        for M in (16, 32, 48, 64, 80):
-            a, b = bf16_inputs(M, N, K, dev, seed)
-            if kmajor:
-                b = b.t().contiguous().t()
-            c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-            sr = 16 * -(-M // 16)
-            ms = {}
-            for w in (64, 128):
-                run = Launcher(tx, a, b, c, block=(sr, w, 128))
-                ms[w] = time_cold_in_stream(run, flush)
-            out.append(dict(workload=f"bf16 decode M={M} N={N} K={K}"
-                            + (", B K-major" if kmajor else "") + ", strips of 64 / 128 columns",
-                            ms_w64=ms[64], ms_w128=ms[128]))
+    cases = [(M, 8192, 8192, km) for km in (False, True) for M in (16, 32, 48, 64, 80)]
+    cases += [(64, n, k, False) for n, k in ((1024, 8192), (2048, 8192), (4096, 4096),
+                                             (8192, 2048), (4096, 8192), (16384, 8192),
+                                             (28672, 8192))]
+    for M, N, K, kmajor in cases:
+        a, b = bf16_inputs(M, N, K, dev, seed)
+        if kmajor:
+            b = b.t().contiguous().t()
+        c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        sr = 16 * -(-M // 16)
+        ms = {}
+        for w in (64, 128):
+            run = Launcher(tx, a, b, c, block=(sr, w, 128))
+            ms[w] = time_cold_in_stream(run, flush)
+        out.append(dict(workload=f"bf16 decode M={M} N={N} K={K}"
+                        + (", B K-major" if kmajor else "") + ", strips of 64 / 128 columns",
+                        ms_w64=ms[64], ms_w128=ms[128]))
     return out
 
 

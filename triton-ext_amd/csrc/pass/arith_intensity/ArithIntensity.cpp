@@ -255,12 +255,13 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
     else if (decode16) {
       // Every strip reads all of A, so A's re-reads are M / W of B's bytes.
       // Strips of W = 128 columns halve them: at N = K = 8192 bf16 M = 48 / 64
-      // / 80 31.6 / 34.2 / 37.8 us against 34.9 / 39.9 / 45.3 with 64 (B
-      // K-major: M = 32 28.0 against 31.8), equal at M = 16; M = 64 at
-      // N = 16384 / 28672 56.7 / 99.6 against 67.8 / 129.5.  With B under
-      // 2^25 elements the wider strips double the split (and its partials) and
-      // lose: M = 64 at N = K = 4096 17.8 against 16.1 us, at N = 2048 21.0
-      // against 17.1.  Their ring holds slices up to 80 rows.
+      // / 80 31.3 / 34.0 / 38.0 us against 35.0 / 39.6 / 45.3 with 64 (B
+      // K-major: M = 32 28.5 against 31.8), about equal at M = 16; M = 64 at
+      // N = 16384 / 28672 57.1 / 100.2 against 68.4 / 129.9.  With B under
+      // 2^25 elements the wider strips double the split (and its partials) or
+      // halve the workgroups, and lose: M = 64 at N = K = 4096 18.2 against
+      // 16.4 us, at N = 2048 22.0 against 17.9.  Their ring holds slices up
+      // to 80 rows.
       const int32_t rows = (int32_t)(16 * cdiv(d->M > 0 ? d->M : 1, 16));
       const bool wide = rows >= 32 && rows <= 80 && d->N * d->K >= ((int64_t)1 << 25);
       t = Tile{rows, wide ? 128 : 64, 128, 1.0};
