@@ -63,7 +63,7 @@ def parse():
                          "bf16 at N = K = 8192 on the 16-bit decode kernel; bf16_decode_kmajor, "
                          "or _1, _16, _64, _96: the same with B K-major), decode16_widths (not in the "
                          "default run: bf16 with strips of 64 and of 128 columns, M = 16 .. 80 and a sweep "
-                         "of N and K at M = 64), mid_m (or mid_m_bf16_128, _256, "
+                         "of N and K at M = 64 and 16), mid_m (or mid_m_bf16_128, _256, "
                          "_512, mid_m_fp8_256: a few hundred rows on the split-K tiles), fp8_decode (or "
                          "fp8_decode_1, _16, _64: block-scaled e4m3 at N = K = 7168 on the fp8 "
                          "decode kernel), int8, fp8 (fp8u: the unscaled 4096^3 line only), kmajor (bf16 "
@@ -425,13 +425,15 @@ def bench_mid_m(tx, dev, kind, M, N, K, flush, seed=7):
 def bench_decode16_widths(tx, dev, flush, seed=7):
     """The 16-bit decode kernel with strips of 64 and of 128 columns named by explicit block,
     bf16, cold in a stream: N = K = 8192 at M = 16 .. 80 with B row-major and K-major, then
-    M = 64 over B from 2^23 to 2^28 elements (B row-major)."""
+    M = 64 over B from 2^23 to 2^28 elements (B row-major), then M = 16 at N = 8192 .. 28672."""
     import torch
     out = []
     cases = [(M, 8192, 8192, km) for km in (False, True) for M in (16, 32, 48, 64, 80)]
     cases += [(64, n, k, False) for n, k in ((1024, 8192), (2048, 8192), (4096, 4096),
                                              (8192, 2048), (4096, 8192), (16384, 8192),
                                              (28672, 8192))]
+    cases += [(16, n, k, km) for n, k in ((8192, 8192), (16384, 4096), (28672, 8192))
+              for km in (False, True)]
     for M, N, K, kmajor in cases:
         a, b = bf16_inputs(M, N, K, dev, seed)
         if kmajor:

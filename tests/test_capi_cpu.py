@@ -199,6 +199,8 @@ def test_plan_validation():
     (16, 8192, 8192, tx.BF16, tx.F32, 0, tx.KERNEL_DECODE_16BIT),
     (64, 4096, 4096, tx.F16, tx.F16, 0, tx.KERNEL_DECODE_16BIT),
     (33, 28672, 8192, tx.F16, tx.F32, 0, tx.KERNEL_DECODE_16BIT),
+    (16, 28672, 8192, tx.BF16, tx.BF16, 0, tx.KERNEL_DECODE_16BIT),
+    (16, 28672, 1024, tx.BF16, tx.BF16, 0, tx.KERNEL_DECODE_16BIT),
     (80, 8192, 8192, tx.BF16, tx.BF16, 0, tx.KERNEL_DECODE_16BIT),
     (96, 4096, 4096, tx.F16, tx.F32, 0, tx.KERNEL_DECODE_16BIT),
     (97, 8192, 8192, tx.BF16, tx.BF16, 0, tx.KERNEL_GEMM_16BIT),
@@ -241,7 +243,8 @@ def test_kernel_choice(M, N, K, a, c, sm, kernel):
         # rows with N K >= 2^25) x 128-row K batches; strips x splits workgroups, at most one a
         # CU (no split once the strips alone fill them)
         sr = 16 * -(-M // 16)
-        w = 128 if 32 <= sr <= 80 and N * K >= 1 << 25 else 64
+        w = 128 if ((32 <= sr <= 80 and N * K >= 1 << 25)
+                    or (sr == 16 and N >= 16384 and N * K >= 1 << 26)) else 64
         assert (p.desc.block_m, p.desc.block_n, p.desc.block_k) == (sr, w, 128)
         strips = -(-N // w)
         # (the largest split that keeps one workgroup a CU)

@@ -56,7 +56,7 @@ def exact(a, b, kind):
 @pytest.mark.parametrize("M,N,K,kind,out_kind", [
     (1, 8192, 8192, "bf16", "bf16"), (16, 8192, 8192, "bf16", "f32"),
     (64, 4096, 4096, "f16", "f16"), (48, 2048, 8192, "bf16", "bf16"),
-    (16, 28672, 1024, "bf16", "bf16"),
+    (16, 28672, 1024, "bf16", "bf16"), (8, 16384, 4096, "f16", "f32"),
     # ragged: K and N that fill no 16-byte chunk, slices of 16 .. 64 rows, one split
     (33, 4100, 2050, "bf16", "bf16"), (7, 1000, 3000, "f16", "f32"), (3, 24, 64, "bf16", "f32"),
     (64, 61, 300, "f16", "f16"), (17, 130, 129, "bf16", "f32"), (50, 520, 127, "f16", "f32"),

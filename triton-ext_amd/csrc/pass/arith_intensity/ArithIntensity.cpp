@@ -261,9 +261,14 @@ extern "C" int tx_arith_intensity(const tx_dot_desc *d, tx_ai_report *out) {
       // 2^25 elements the wider strips double the split (and its partials) or
       // halve the workgroups, and lose: M = 64 at N = K = 4096 18.2 against
       // 16.4 us, at N = 2048 22.0 against 17.9.  Their ring holds slices up
-      // to 80 rows.
+      // to 80 rows.  Slices of 16 rows gain from them at N >= 16384, where 64
+      // columns make 256 strips or more: M = 16 at N = 28672, K = 8192 77.6
+      // against 93.0 us (B K-major 73.6 / 87.4), at N = 16384, K = 4096 26.6
+      // against 28.9 (K-major 29.3 / 37.0); at N = K = 8192 they tie.
       const int32_t rows = (int32_t)(16 * cdiv(d->M > 0 ? d->M : 1, 16));
-      const bool wide = rows >= 32 && rows <= 80 && d->N * d->K >= ((int64_t)1 << 25);
+      const int64_t nk = d->N * d->K;
+      const bool wide = (rows >= 32 && rows <= 80 && nk >= ((int64_t)1 << 25)) ||
+                        (rows == 16 && d->N >= 16384 && nk >= ((int64_t)1 << 26));
       t = Tile{rows, wide ? 128 : 64, 128, 1.0};
     }
     else if (sa == 2 && (d->flags & TX_FLAG_B_KMAJOR))
